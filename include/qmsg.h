@@ -1,0 +1,187 @@
+/* qmsg.h - MI355X (gfx950) Qwen3-MoE expert-FFN layer behind a plain C ABI.
+ *
+ * Drop-in for the reference engine's MoE layer with resident experts:
+ *   static int moe(QmsModel *m, int l, const float *xn, const float *h, int T, float *out)
+ *   (src/model.c:1032-1167), called once per layer by qms_forward (src/model.c:1284).
+ * The weights are the GGUF tensor bytes exactly as the reference holds them (stacked
+ * ffn_{gate,up,down}_exps [X][rows][cols] and the F32 ffn_gate_inp router,
+ * src/model.c:133-157, 359-362), copied once to HBM and never repacked.
+ *
+ * Conventions follow the reference: int status (0 ok, negative error, reason available from
+ * qmsg_last_error), no exceptions, no abort. A context is thread-compatible, not thread-safe:
+ * one host thread drives it, like the reference's moe() (src/model.c:329 shares m->eptr).
+ * Everything is enqueued on the context's own HIP stream. */
+#ifndef QMSG_H
+#define QMSG_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ------------------------------------------------------------------ status codes ---- */
+#define QMSG_OK 0
+#define QMSG_E_INVALID (-1)      /* bad argument or shape                                   */
+#define QMSG_E_UNSUPPORTED (-2)  /* outside the integer fast path (src/model.c:1090-1093)    */
+#define QMSG_E_NOMEM (-3)        /* device or host allocation failed                         */
+#define QMSG_E_DEVICE (-4)       /* HIP runtime error                                        */
+#define QMSG_E_RANGE (-5)        /* T above the context's max_tokens, or layer out of range  */
+
+/* GGUF tensor type ids (src/gguf.h:8-10). */
+enum {
+    QMSG_T_F32 = 0,
+    QMSG_T_F16 = 1,
+    QMSG_T_Q4_0 = 2,
+    QMSG_T_Q4_1 = 3,
+    QMSG_T_Q8_0 = 8,
+    QMSG_T_Q6_K = 14
+};
+
+/* A 2-D weight view, QmsMat (src/quant.h:11-16): row r starts at data + r*row_bytes. */
+typedef struct {
+    int type;
+    int64_t rows, cols;
+    uint64_t row_bytes;
+    const void *data;
+} qmsg_mat;
+
+/* n_expert stacked matrices, QmsExperts (src/model.h:31-35) for resident weights:
+ * m.data points at expert 0, expert e at m.data + e*expert_bytes. */
+typedef struct {
+    qmsg_mat m;
+    uint64_t expert_bytes;
+} qmsg_experts;
+
+/* The MoE part of QmsLayer (src/model.h:37-45): F32 router [n_expert][n_embd] and the
+ * stacked gate/up [n_expert][n_ff_exp][n_embd] and down [n_expert][n_embd][n_ff_exp]. */
+typedef struct {
+    qmsg_mat router;
+    qmsg_experts gate, up, down;
+} qmsg_layer;
+
+/* The hyper-parameters moe() reads from QmsCfg (src/model.h:24-29). */
+typedef struct {
+    int n_embd;    /* E */
+    int n_expert;  /* X */
+    int n_used;    /* K, top-k */
+    int n_ff_exp;  /* F */
+} qmsg_cfg;
+
+typedef struct qmsg_ctx qmsg_ctx;
+
+/* Which kernels run the expert products.
+ *   EXACT: per-row fp32 FMA chains in the reference's lane order; every intermediate
+ *          (int8 blocks, fp32 rows, outputs) is bit-identical to the reference's AVX path.
+ *   MFMA:  int8 MFMA grouped GEMM; int32 block dots are exact, fp32 rows are summed per
+ *          block in another order (outputs agree to ~1e-6 relative).
+ *   AUTO:  EXACT up to the context's exact-token limit, MFMA above it. */
+enum { QMSG_PATH_AUTO = 0, QMSG_PATH_EXACT = 1, QMSG_PATH_MFMA = 2 };
+
+/* ------------------------------------------------------------------ lifecycle ---- */
+
+/* No reference counterpart (the reference keeps this state in QmsModel, src/model.h:106-139):
+ * create a context on HIP device `device` for `n_layer` resident layers of shape `cfg`,
+ * with device scratch for up to `max_tokens` tokens per call. */
+int qmsg_create(qmsg_ctx **out, int device, const qmsg_cfg *cfg, int n_layer, int max_tokens);
+void qmsg_destroy(qmsg_ctx *ctx);
+
+/* Text of the last error on this context (or of the last qmsg_create failure when ctx is NULL). */
+const char *qmsg_last_error(const qmsg_ctx *ctx);
+
+/* The HIP stream (hipStream_t) all work of this context is enqueued on. */
+void *qmsg_stream(qmsg_ctx *ctx);
+
+/* Choose the expert-product kernels (QMSG_PATH_*); AUTO by default. */
+int qmsg_set_path(qmsg_ctx *ctx, int path);
+
+/* ------------------------------------------------------------------ weights ---- */
+
+/* Replaces load_experts/load_mat's resident read (src/model.c:133-157, 67-85): copy one
+ * layer's router and expert tensors (host memory, GGUF bytes) into HBM unchanged. Shapes
+ * and row_bytes are checked against cfg and qms_row_bytes (src/gguf.c:85-96). */
+int qmsg_layer_upload(qmsg_ctx *ctx, int layer, const qmsg_layer *host);
+
+/* No reference counterpart: fill a layer with the seeded synthetic weights described in
+ * large_model_amd/csrc/qmsg_synth.h, generated on the device (router F32 N(0, sigma), experts
+ * N(0, sigma) quantised to gate_type/up_type/down_type). If router_col0 is not NULL its
+ * n_expert floats replace column 0 of the router (a routing bias for skewed expert load). */
+int qmsg_layer_synth(qmsg_ctx *ctx, int layer, uint64_t seed, int gate_type, int up_type, int down_type,
+                     float sigma, const float *router_col0);
+
+/* No reference counterpart: copy a resident layer back to host memory (for checks). Any
+ * pointer may be NULL; sizes are X*E*4 for the router and X*expert_bytes for each tensor. */
+int qmsg_layer_download(qmsg_ctx *ctx, int layer, float *router, void *gate, void *up, void *down);
+
+/* ------------------------------------------------------------------ the layer ---- */
+
+/* moe(m, l, xn, h, T, out) (src/model.c:1032): out[T][E] = sum over the top-K experts of
+ * each token of wt * down(silu(gate xq) * up xq), with host buffers; blocks until done.
+ * h is accepted for signature parity and ignored (the reference only uses it to prefetch
+ * streamed experts, src/model.c:1118). T may be 0. */
+int qmsg_moe(qmsg_ctx *ctx, int layer, const float *xn, const float *h, int T, float *out);
+
+/* The same layer on device buffers (d_xn [T][E], d_out [T][E] fp32), enqueued on the
+ * context's stream without waiting. */
+int qmsg_moe_device(qmsg_ctx *ctx, int layer, const float *d_xn, int T, float *d_out);
+
+/* Wait for everything enqueued on the context's stream. */
+int qmsg_sync(qmsg_ctx *ctx);
+
+/* ------------------------------------------------------------------ device buffers ---- */
+
+/* No reference counterpart: device memory owned by the context (freed by qmsg_destroy). */
+void *qmsg_device_alloc(qmsg_ctx *ctx, size_t bytes);
+int qmsg_memcpy_h2d(qmsg_ctx *ctx, void *dst, const void *src, size_t bytes);
+int qmsg_memcpy_d2h(qmsg_ctx *ctx, void *dst, const void *src, size_t bytes);
+
+/* No reference counterpart: seeded synthetic layer inputs written to d_x [T][E] on the device
+ * (N(0, sigma), optionally RMS-normalised per row like src/model.c:403-409 with a unit weight,
+ * optionally with column 0 set to 1.0 to carry a router bias). */
+int qmsg_synth_input(qmsg_ctx *ctx, uint64_t seed, int layer, int T, float sigma, int rmsnorm, int bias_col0,
+                     float *d_x);
+
+/* ------------------------------------------------------------------ checks and timing ---- */
+
+/* Intermediates of one layer call for parity checks (no counterpart: the reference frees
+ * them inside moe()). Host buffers, each optional (NULL = skip). NS = T*K slots. */
+typedef struct {
+    float *logits;   /* [T][X]                                                    */
+    int32_t *sel;    /* [T][K] experts in selection order                         */
+    float *wt;       /* [T][K] renormalised routing weights                       */
+    int32_t *start;  /* [X+1]  slots of expert e are start[e] .. start[e+1]-1     */
+    int32_t *slot_t; /* [NS]   token of each slot                                 */
+    int32_t *slot_of;/* [T][K] slot of (token, selection)                         */
+    int32_t *active; /* [X]    active experts ascending; count in *n_active       */
+    int32_t *n_active;
+    void *xq;        /* [T][E/32]  QmsQ8 blocks, 44 bytes each (src/kernels.h:7-12) */
+    float *gu;       /* [NS][2F]   gate rows then up rows (EXACT path only)       */
+    float *act;      /* [NS][F]    silu(g)*u                                      */
+    void *aq;        /* [NS][F/32] QmsQ8 blocks                                   */
+    float *dn;       /* [NS][E]    per-slot expert outputs                        */
+} qmsg_debug;
+
+/* Run one layer like qmsg_moe and copy the requested intermediates back. */
+int qmsg_moe_debug(qmsg_ctx *ctx, int layer, const float *xn, int T, float *out, qmsg_debug *dbg);
+
+/* Exact signed int32 dot of one 32-element block of an expert row with a QmsQ8 block, as the
+ * device kernels form it: which = 0 gate, 1 up, 2 down; x is one 44-byte QmsQ8 block.
+ * Q4_0: sum (q-8)*x; Q6_K: sc_lo*sum_{l<16}(q-32)*x + sc_hi*sum_{l>=16}(q-32)*x. */
+int qmsg_block_dots(qmsg_ctx *ctx, int layer, int which, int n, const int32_t *expert, const int32_t *row,
+                    const int32_t *block, const void *xq_blocks, int32_t *out);
+
+/* Per-kernel timing with HIP events on the context's stream (off by default). While on,
+ * every kernel launch of the context is bracketed by an event pair. */
+int qmsg_profile(qmsg_ctx *ctx, int enable);
+/* Launch count and summed milliseconds of kernel `name` since profiling was enabled
+ * (synchronises the stream). Names: "route", "gateup", "down", and the MFMA-path kernels. */
+int qmsg_profile_read(qmsg_ctx *ctx, const char *name, int64_t *launches, double *total_ms);
+
+/* Device facts used by the roofline report: CU count, peak engine clock (kHz), HBM bytes. */
+int qmsg_device_info(qmsg_ctx *ctx, int *n_cu, int *clock_khz, uint64_t *hbm_bytes, char *arch, int arch_len);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* QMSG_H */

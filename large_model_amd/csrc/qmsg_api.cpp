@@ -1,0 +1,551 @@
+/* qmsg_api.cpp - the C ABI of libqmsg: contexts, resident weights, the layer entry points. */
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "../../include/qmsg.h"
+#include "qmsg_internal.h"
+#include "qmsg_synth.h"
+
+using namespace qmsg;
+
+namespace {
+
+struct LayerStore {
+    float *router = nullptr;
+    uint8_t *gate = nullptr, *up = nullptr, *down = nullptr;
+    int gate_type = -1, up_type = -1, down_type = -1;
+    bool ready = false;
+};
+
+struct ProfRec {
+    std::string name;
+    hipEvent_t a, b;
+};
+
+/* qms_row_bytes (src/gguf.c:85-96). */
+uint64_t row_bytes(int type, int64_t ne0)
+{
+    switch (type) {
+    case QMSG_T_F32: return (uint64_t)ne0 * 4;
+    case QMSG_T_F16: return (uint64_t)ne0 * 2;
+    case QMSG_T_Q4_0: return ne0 % 32 ? 0 : (uint64_t)ne0 / 32 * 18;
+    case QMSG_T_Q4_1: return ne0 % 32 ? 0 : (uint64_t)ne0 / 32 * 20;
+    case QMSG_T_Q8_0: return ne0 % 32 ? 0 : (uint64_t)ne0 / 32 * 34;
+    case QMSG_T_Q6_K: return ne0 % 256 ? 0 : (uint64_t)ne0 / 256 * 210;
+    default: return 0;
+    }
+}
+
+thread_local std::string g_create_error;
+
+}  // namespace
+
+struct qmsg_ctx {
+    int device = 0;
+    qmsg_cfg cfg{};
+    int n_layer = 0, max_tokens = 0, path = QMSG_PATH_AUTO;
+    hipStream_t stream = nullptr;
+    std::vector<LayerStore> layers;
+    Scratch S{};
+    std::vector<void *> scratch_allocs, user_allocs;
+    float *d_x = nullptr, *d_out = nullptr;
+    std::string err;
+    bool prof = false;
+    std::vector<ProfRec> prof_recs, prof_free;
+    struct Tot { std::string name; int64_t n; double ms; };
+    std::vector<Tot> prof_tot;
+};
+
+static int fail(qmsg_ctx *c, int code, const char *fmt, ...)
+{
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    if (c) c->err = buf;
+    else g_create_error = buf;
+    return code;
+}
+
+#define HIP_TRY(c, call)                                                                               \
+    do {                                                                                               \
+        hipError_t e_ = (call);                                                                        \
+        if (e_ != hipSuccess) return fail((c), QMSG_E_DEVICE, "%s: %s", #call, hipGetErrorString(e_)); \
+    } while (0)
+
+static int dev_alloc(qmsg_ctx *c, void **p, size_t bytes, std::vector<void *> &list)
+{
+    /* 256 bytes of tail padding: kernels may read one aligned word past a tensor's end. */
+    hipError_t e = hipMalloc(p, bytes + 256);
+    if (e != hipSuccess) return fail(c, QMSG_E_NOMEM, "hipMalloc(%zu): %s", bytes, hipGetErrorString(e));
+    list.push_back(*p);
+    return QMSG_OK;
+}
+
+static void prof_begin(qmsg_ctx *c, const char *name, ProfRec &r)
+{
+    if (!c->prof) return;
+    if (!c->prof_free.empty()) {
+        r = c->prof_free.back();
+        c->prof_free.pop_back();
+    } else {
+        hipEventCreate(&r.a);
+        hipEventCreate(&r.b);
+    }
+    r.name = name;
+    hipEventRecord(r.a, c->stream);
+}
+
+static void prof_end(qmsg_ctx *c, ProfRec &r)
+{
+    if (!c->prof) return;
+    hipEventRecord(r.b, c->stream);
+    c->prof_recs.push_back(r);
+}
+
+#define LAUNCH(c, name, expr)                                                                             \
+    do {                                                                                                  \
+        ProfRec pr_;                                                                                      \
+        prof_begin((c), (name), pr_);                                                                     \
+        hipError_t e_ = (expr);                                                                           \
+        prof_end((c), pr_);                                                                               \
+        if (e_ != hipSuccess) return fail((c), QMSG_E_DEVICE, "%s launch: %s", (name), hipGetErrorString(e_)); \
+    } while (0)
+
+extern "C" {
+
+int qmsg_create(qmsg_ctx **out, int device, const qmsg_cfg *cfg, int n_layer, int max_tokens)
+{
+    if (!out || !cfg) return fail(nullptr, QMSG_E_INVALID, "qmsg_create: null argument");
+    *out = nullptr;
+    const int E = cfg->n_embd, X = cfg->n_expert, K = cfg->n_used, F = cfg->n_ff_exp;
+    if (E <= 0 || X <= 0 || K <= 0 || F <= 0 || K > X || n_layer <= 0 || max_tokens <= 0)
+        return fail(nullptr, QMSG_E_INVALID, "qmsg_create: bad shape E=%d X=%d K=%d F=%d layers=%d T=%d", E, X, K, F,
+                    n_layer, max_tokens);
+    /* The reference's integer fast path needs E % 256 == 0 and F % 32 == 0
+     * (src/model.c:1090-1093). The kernels also pair 32-blocks (F % 64 == 0), run four router
+     * dots per wave (X % 4 == 0) and keep per-expert state in 256-entry LDS arrays (X <= 256). */
+    if (E % 256 || F % 64 || X % 4 || X > 256 || K > 64)
+        return fail(nullptr, QMSG_E_UNSUPPORTED, "qmsg_create: unsupported shape E=%d X=%d K=%d F=%d", E, X, K, F);
+    int ndev = 0;
+    if (hipGetDeviceCount(&ndev) != hipSuccess || device < 0 || device >= ndev)
+        return fail(nullptr, QMSG_E_DEVICE, "qmsg_create: HIP device %d not available (%d devices)", device, ndev);
+    qmsg_ctx *c = new qmsg_ctx;
+    c->device = device;
+    c->cfg = *cfg;
+    c->n_layer = n_layer;
+    c->max_tokens = max_tokens;
+    c->layers.resize((size_t)n_layer);
+    hipError_t e = hipSetDevice(device);
+    if (e == hipSuccess) e = hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking);
+    if (e != hipSuccess) {
+        fail(nullptr, QMSG_E_DEVICE, "qmsg_create: %s", hipGetErrorString(e));
+        delete c;
+        return QMSG_E_DEVICE;
+    }
+    const size_t Tm = (size_t)max_tokens, NS = Tm * K, nbE = E / 32, nbF = F / 32;
+    struct Item { void **p; size_t bytes; } items[] = {
+        { (void **)&c->S.logits, Tm * X * 4 },  { (void **)&c->S.sel, NS * 4 },
+        { (void **)&c->S.wt, NS * 4 },          { (void **)&c->S.slot_t, NS * 4 },
+        { (void **)&c->S.slot_of, NS * 4 },     { (void **)&c->S.start, (size_t)(X + 1) * 4 },
+        { (void **)&c->S.active, (size_t)X * 4 }, { (void **)&c->S.meta, 64 },
+        { (void **)&c->S.tok_cnt, Tm * 4 },     { (void **)&c->S.tile_cnt, (size_t)(E / 32) * 4 },
+        { (void **)&c->S.xq, Tm * nbE * sizeof(Q8) }, { (void **)&c->S.xqk, Tm * (nbE / 2) * kPairBytes },
+        { (void **)&c->S.gu, NS * 2 * F * 4 },  { (void **)&c->S.act, NS * F * 4 },
+        { (void **)&c->S.aq, NS * nbF * sizeof(Q8) }, { (void **)&c->S.aqk, NS * (nbF / 2) * kPairBytes },
+        { (void **)&c->S.dn, NS * E * 4 },      { (void **)&c->d_x, Tm * E * 4 },
+        { (void **)&c->d_out, Tm * E * 4 },
+    };
+    for (auto &it : items) {
+        if (dev_alloc(c, it.p, it.bytes, c->scratch_allocs) != QMSG_OK) {
+            g_create_error = c->err;
+            qmsg_destroy(c);
+            return QMSG_E_NOMEM;
+        }
+    }
+    /* counters start at zero; the kernels that use them leave them at zero */
+    e = hipMemset(c->S.meta, 0, 64);
+    if (e == hipSuccess) e = hipMemset(c->S.tok_cnt, 0, Tm * 4);
+    if (e == hipSuccess) e = hipMemset(c->S.tile_cnt, 0, (size_t)(E / 32) * 4);
+    if (e != hipSuccess) {
+        fail(nullptr, QMSG_E_DEVICE, "qmsg_create: %s", hipGetErrorString(e));
+        qmsg_destroy(c);
+        return QMSG_E_DEVICE;
+    }
+    *out = c;
+    return QMSG_OK;
+}
+
+void qmsg_destroy(qmsg_ctx *c)
+{
+    if (!c) return;
+    hipSetDevice(c->device);
+    if (c->stream) hipStreamSynchronize(c->stream);
+    for (auto &L : c->layers) {
+        hipFree(L.router);
+        hipFree(L.gate);
+        hipFree(L.up);
+        hipFree(L.down);
+    }
+    for (void *p : c->scratch_allocs) hipFree(p);
+    for (void *p : c->user_allocs) hipFree(p);
+    for (auto &r : c->prof_recs) { hipEventDestroy(r.a); hipEventDestroy(r.b); }
+    for (auto &r : c->prof_free) { hipEventDestroy(r.a); hipEventDestroy(r.b); }
+    if (c->stream) hipStreamDestroy(c->stream);
+    delete c;
+}
+
+const char *qmsg_last_error(const qmsg_ctx *c) { return c ? c->err.c_str() : g_create_error.c_str(); }
+
+void *qmsg_stream(qmsg_ctx *c) { return c ? (void *)c->stream : nullptr; }
+
+int qmsg_set_path(qmsg_ctx *c, int path)
+{
+    if (!c) return QMSG_E_INVALID;
+    if (path != QMSG_PATH_AUTO && path != QMSG_PATH_EXACT && path != QMSG_PATH_MFMA)
+        return fail(c, QMSG_E_INVALID, "qmsg_set_path: unknown path %d", path);
+    c->path = path;
+    return QMSG_OK;
+}
+
+static int check_layer_index(qmsg_ctx *c, int layer)
+{
+    if (layer < 0 || layer >= c->n_layer) return fail(c, QMSG_E_RANGE, "layer %d out of range [0, %d)", layer, c->n_layer);
+    return QMSG_OK;
+}
+
+/* Allocate a layer's four tensors (freeing an earlier set) for the given types. */
+static int layer_alloc(qmsg_ctx *c, LayerStore &L, int gt, int ut, int dt)
+{
+    const int64_t E = c->cfg.n_embd, X = c->cfg.n_expert, F = c->cfg.n_ff_exp;
+    if (gt != QMSG_T_Q4_0 || ut != QMSG_T_Q4_0 || (dt != QMSG_T_Q4_0 && dt != QMSG_T_Q6_K))
+        return fail(c, QMSG_E_UNSUPPORTED, "expert types gate=%d up=%d down=%d: kernels take Q4_0 gate/up and Q4_0 or Q6_K down",
+                    gt, ut, dt);
+    if (dt == QMSG_T_Q6_K && F % 256)
+        return fail(c, QMSG_E_UNSUPPORTED, "Q6_K down needs n_ff_exp %% 256 == 0 (got %lld)", (long long)F);
+    hipFree(L.router); hipFree(L.gate); hipFree(L.up); hipFree(L.down);
+    L = LayerStore{};
+    std::vector<void *> dummy;
+    const size_t gb = (size_t)row_bytes(gt, E) * F * X, ub = (size_t)row_bytes(ut, E) * F * X,
+                 db = (size_t)row_bytes(dt, F) * E * X;
+    int rc;
+    if ((rc = dev_alloc(c, (void **)&L.router, (size_t)X * E * 4, dummy)) ||
+        (rc = dev_alloc(c, (void **)&L.gate, gb, dummy)) || (rc = dev_alloc(c, (void **)&L.up, ub, dummy)) ||
+        (rc = dev_alloc(c, (void **)&L.down, db, dummy))) {
+        hipFree(L.router); hipFree(L.gate); hipFree(L.up); hipFree(L.down);
+        L = LayerStore{};
+        return rc;
+    }
+    L.gate_type = gt;
+    L.up_type = ut;
+    L.down_type = dt;
+    return QMSG_OK;
+}
+
+static LayerDev layer_dev(const qmsg_ctx *c, const LayerStore &L)
+{
+    const int64_t E = c->cfg.n_embd, F = c->cfg.n_ff_exp;
+    LayerDev d;
+    d.router = L.router;
+    d.gate = L.gate;
+    d.up = L.up;
+    d.down = L.down;
+    d.gate_type = L.gate_type;
+    d.up_type = L.up_type;
+    d.down_type = L.down_type;
+    d.gate_rb = row_bytes(L.gate_type, E);
+    d.up_rb = row_bytes(L.up_type, E);
+    d.down_rb = row_bytes(L.down_type, F);
+    d.gate_eb = d.gate_rb * F;
+    d.up_eb = d.up_rb * F;
+    d.down_eb = d.down_rb * E;
+    return d;
+}
+
+int qmsg_layer_upload(qmsg_ctx *c, int layer, const qmsg_layer *h)
+{
+    if (!c || !h) return QMSG_E_INVALID;
+    int rc = check_layer_index(c, layer);
+    if (rc) return rc;
+    const int64_t E = c->cfg.n_embd, X = c->cfg.n_expert, F = c->cfg.n_ff_exp;
+    if (h->router.type != QMSG_T_F32 || h->router.rows != X || h->router.cols != E ||
+        h->router.row_bytes != (uint64_t)E * 4 || !h->router.data)
+        return fail(c, QMSG_E_INVALID, "router must be F32 [%lld][%lld]", (long long)X, (long long)E);
+    const struct { const qmsg_experts *x; int64_t rows, cols; const char *name; } t[3] = {
+        { &h->gate, F, E, "gate" }, { &h->up, F, E, "up" }, { &h->down, E, F, "down" }
+    };
+    for (auto &k : t) {
+        const uint64_t rb = row_bytes(k.x->m.type, k.cols);
+        if (!rb || k.x->m.rows != k.rows || k.x->m.cols != k.cols || k.x->m.row_bytes != rb ||
+            k.x->expert_bytes != rb * (uint64_t)k.rows || !k.x->m.data)
+            return fail(c, QMSG_E_INVALID, "%s experts: expected [%lld x %lld] of type %d with row_bytes %llu", k.name,
+                        (long long)k.rows, (long long)k.cols, k.x->m.type, (unsigned long long)rb);
+    }
+    HIP_TRY(c, hipSetDevice(c->device));
+    LayerStore &L = c->layers[(size_t)layer];
+    if ((rc = layer_alloc(c, L, h->gate.m.type, h->up.m.type, h->down.m.type))) return rc;
+    HIP_TRY(c, hipMemcpy(L.router, h->router.data, (size_t)X * E * 4, hipMemcpyHostToDevice));
+    HIP_TRY(c, hipMemcpy(L.gate, h->gate.m.data, h->gate.expert_bytes * X, hipMemcpyHostToDevice));
+    HIP_TRY(c, hipMemcpy(L.up, h->up.m.data, h->up.expert_bytes * X, hipMemcpyHostToDevice));
+    HIP_TRY(c, hipMemcpy(L.down, h->down.m.data, h->down.expert_bytes * X, hipMemcpyHostToDevice));
+    L.ready = true;
+    return QMSG_OK;
+}
+
+int qmsg_layer_synth(qmsg_ctx *c, int layer, uint64_t seed, int gt, int ut, int dt, float sigma,
+                     const float *router_col0)
+{
+    if (!c) return QMSG_E_INVALID;
+    int rc = check_layer_index(c, layer);
+    if (rc) return rc;
+    const int64_t E = c->cfg.n_embd, X = c->cfg.n_expert, F = c->cfg.n_ff_exp;
+    HIP_TRY(c, hipSetDevice(c->device));
+    LayerStore &L = c->layers[(size_t)layer];
+    if ((rc = layer_alloc(c, L, gt, ut, dt))) return rc;
+    const uint64_t rkey = qmsg_tensor_key(seed, (uint32_t)layer, QMSG_KIND_ROUTER, 0);
+    HIP_TRY(c, launch_synth_f32(rkey, (uint64_t)X * E, sigma, L.router, c->stream));
+    if (router_col0) {
+        float *tmp = nullptr;
+        HIP_TRY(c, hipMalloc((void **)&tmp, (size_t)X * 4));
+        hipError_t e = hipMemcpyAsync(tmp, router_col0, (size_t)X * 4, hipMemcpyHostToDevice, c->stream);
+        if (e == hipSuccess) e = launch_set_col0(L.router, (int)X, (int)E, tmp, 0.0f, c->stream);
+        if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
+        hipFree(tmp);
+        if (e != hipSuccess) return fail(c, QMSG_E_DEVICE, "router bias: %s", hipGetErrorString(e));
+    }
+    HIP_TRY(c, launch_synth_experts(seed, (uint32_t)layer, QMSG_KIND_GATE, gt, F, E, (int)X, sigma, L.gate, c->stream));
+    HIP_TRY(c, launch_synth_experts(seed, (uint32_t)layer, QMSG_KIND_UP, ut, F, E, (int)X, sigma, L.up, c->stream));
+    HIP_TRY(c, launch_synth_experts(seed, (uint32_t)layer, QMSG_KIND_DOWN, dt, E, F, (int)X, sigma, L.down, c->stream));
+    HIP_TRY(c, hipStreamSynchronize(c->stream));
+    L.ready = true;
+    return QMSG_OK;
+}
+
+int qmsg_layer_download(qmsg_ctx *c, int layer, float *router, void *gate, void *up, void *down)
+{
+    if (!c) return QMSG_E_INVALID;
+    int rc = check_layer_index(c, layer);
+    if (rc) return rc;
+    const LayerStore &L = c->layers[(size_t)layer];
+    if (!L.ready) return fail(c, QMSG_E_INVALID, "layer %d has no weights", layer);
+    const LayerDev d = layer_dev(c, L);
+    const size_t X = (size_t)c->cfg.n_expert;
+    HIP_TRY(c, hipSetDevice(c->device));
+    HIP_TRY(c, hipStreamSynchronize(c->stream));
+    if (router) HIP_TRY(c, hipMemcpy(router, L.router, X * c->cfg.n_embd * 4, hipMemcpyDeviceToHost));
+    if (gate) HIP_TRY(c, hipMemcpy(gate, L.gate, X * d.gate_eb, hipMemcpyDeviceToHost));
+    if (up) HIP_TRY(c, hipMemcpy(up, L.up, X * d.up_eb, hipMemcpyDeviceToHost));
+    if (down) HIP_TRY(c, hipMemcpy(down, L.down, X * d.down_eb, hipMemcpyDeviceToHost));
+    return QMSG_OK;
+}
+
+static int run_layer(qmsg_ctx *c, int layer, const float *d_xn, int T, float *d_out, int debug)
+{
+    int rc = check_layer_index(c, layer);
+    if (rc) return rc;
+    if (T < 0 || T > c->max_tokens)
+        return fail(c, QMSG_E_RANGE, "T=%d outside [0, max_tokens=%d]", T, c->max_tokens);
+    const LayerStore &L = c->layers[(size_t)layer];
+    if (!L.ready) return fail(c, QMSG_E_INVALID, "layer %d has no weights", layer);
+    if (T == 0) return QMSG_OK;
+    if (((uintptr_t)d_xn & 15) || ((uintptr_t)d_out & 3))
+        return fail(c, QMSG_E_INVALID, "device buffers must be 16-byte aligned (xn) and 4-byte aligned (out)");
+    const Shape s{ c->cfg.n_embd, c->cfg.n_expert, c->cfg.n_used, c->cfg.n_ff_exp };
+    const LayerDev d = layer_dev(c, L);
+    LAUNCH(c, "route", launch_route(s, d, c->S, d_xn, T, c->stream));
+    LAUNCH(c, "gateup", launch_gateup_exact(s, d, c->S, T, debug, c->stream));
+    LAUNCH(c, "down", launch_down_exact(s, d, c->S, d_out, T, c->stream));
+    return QMSG_OK;
+}
+
+int qmsg_moe_device(qmsg_ctx *c, int layer, const float *d_xn, int T, float *d_out)
+{
+    if (!c) return QMSG_E_INVALID;
+    return run_layer(c, layer, d_xn, T, d_out, 0);
+}
+
+int qmsg_moe(qmsg_ctx *c, int layer, const float *xn, const float *h, int T, float *out)
+{
+    (void)h;
+    if (!c) return QMSG_E_INVALID;
+    if (T < 0 || T > c->max_tokens) return fail(c, QMSG_E_RANGE, "T=%d outside [0, max_tokens=%d]", T, c->max_tokens);
+    if (T == 0) return QMSG_OK;
+    if (!xn || !out) return fail(c, QMSG_E_INVALID, "qmsg_moe: null buffer");
+    const size_t bytes = (size_t)T * c->cfg.n_embd * 4;
+    HIP_TRY(c, hipSetDevice(c->device));
+    HIP_TRY(c, hipMemcpyAsync(c->d_x, xn, bytes, hipMemcpyHostToDevice, c->stream));
+    int rc = run_layer(c, layer, c->d_x, T, c->d_out, 0);
+    if (rc) return rc;
+    HIP_TRY(c, hipMemcpyAsync(out, c->d_out, bytes, hipMemcpyDeviceToHost, c->stream));
+    HIP_TRY(c, hipStreamSynchronize(c->stream));
+    return QMSG_OK;
+}
+
+int qmsg_sync(qmsg_ctx *c)
+{
+    if (!c) return QMSG_E_INVALID;
+    HIP_TRY(c, hipStreamSynchronize(c->stream));
+    return QMSG_OK;
+}
+
+void *qmsg_device_alloc(qmsg_ctx *c, size_t bytes)
+{
+    if (!c) return nullptr;
+    void *p = nullptr;
+    if (hipSetDevice(c->device) != hipSuccess) return nullptr;
+    if (dev_alloc(c, &p, bytes, c->user_allocs) != QMSG_OK) return nullptr;
+    return p;
+}
+
+int qmsg_memcpy_h2d(qmsg_ctx *c, void *dst, const void *src, size_t bytes)
+{
+    if (!c) return QMSG_E_INVALID;
+    HIP_TRY(c, hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, c->stream));
+    HIP_TRY(c, hipStreamSynchronize(c->stream));
+    return QMSG_OK;
+}
+
+int qmsg_memcpy_d2h(qmsg_ctx *c, void *dst, const void *src, size_t bytes)
+{
+    if (!c) return QMSG_E_INVALID;
+    HIP_TRY(c, hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, c->stream));
+    HIP_TRY(c, hipStreamSynchronize(c->stream));
+    return QMSG_OK;
+}
+
+int qmsg_synth_input(qmsg_ctx *c, uint64_t seed, int layer, int T, float sigma, int rmsnorm, int bias_col0, float *d_x)
+{
+    if (!c || !d_x || T < 0) return QMSG_E_INVALID;
+    const int E = c->cfg.n_embd;
+    const uint64_t key = qmsg_tensor_key(seed, (uint32_t)layer, QMSG_KIND_X, 0);
+    HIP_TRY(c, hipSetDevice(c->device));
+    HIP_TRY(c, launch_synth_f32(key, (uint64_t)T * E, sigma, d_x, c->stream));
+    if (rmsnorm) HIP_TRY(c, launch_rmsnorm_rows(d_x, T, E, 1e-6f, c->stream));
+    if (bias_col0) HIP_TRY(c, launch_set_col0(d_x, T, E, nullptr, 1.0f, c->stream));
+    HIP_TRY(c, hipStreamSynchronize(c->stream));
+    return QMSG_OK;
+}
+
+int qmsg_moe_debug(qmsg_ctx *c, int layer, const float *xn, int T, float *out, qmsg_debug *g)
+{
+    if (!c || !xn || !out) return QMSG_E_INVALID;
+    if (T <= 0 || T > c->max_tokens) return fail(c, QMSG_E_RANGE, "T=%d outside [1, max_tokens=%d]", T, c->max_tokens);
+    const size_t E = c->cfg.n_embd, X = c->cfg.n_expert, K = c->cfg.n_used, F = c->cfg.n_ff_exp, NS = (size_t)T * K;
+    HIP_TRY(c, hipSetDevice(c->device));
+    HIP_TRY(c, hipMemcpyAsync(c->d_x, xn, (size_t)T * E * 4, hipMemcpyHostToDevice, c->stream));
+    int rc = run_layer(c, layer, c->d_x, T, c->d_out, 1);
+    if (rc) return rc;
+    HIP_TRY(c, hipStreamSynchronize(c->stream));
+    HIP_TRY(c, hipMemcpy(out, c->d_out, (size_t)T * E * 4, hipMemcpyDeviceToHost));
+    if (!g) return QMSG_OK;
+    struct { void *dst; const void *src; size_t bytes; } cp[] = {
+        { g->logits, c->S.logits, (size_t)T * X * 4 }, { g->sel, c->S.sel, NS * 4 },
+        { g->wt, c->S.wt, NS * 4 },                    { g->start, c->S.start, (X + 1) * 4 },
+        { g->slot_t, c->S.slot_t, NS * 4 },            { g->slot_of, c->S.slot_of, NS * 4 },
+        { g->active, c->S.active, X * 4 },             { g->n_active, c->S.meta, 4 },
+        { g->xq, c->S.xq, (size_t)T * (E / 32) * sizeof(Q8) }, { g->gu, c->S.gu, NS * 2 * F * 4 },
+        { g->act, c->S.act, NS * F * 4 },              { g->aq, c->S.aq, NS * (F / 32) * sizeof(Q8) },
+        { g->dn, c->S.dn, NS * E * 4 },
+    };
+    for (auto &x : cp)
+        if (x.dst) HIP_TRY(c, hipMemcpy(x.dst, x.src, x.bytes, hipMemcpyDeviceToHost));
+    return QMSG_OK;
+}
+
+int qmsg_block_dots(qmsg_ctx *c, int layer, int which, int n, const int32_t *expert, const int32_t *row,
+                    const int32_t *block, const void *xq_blocks, int32_t *out)
+{
+    if (!c || n < 0 || which < 0 || which > 2) return QMSG_E_INVALID;
+    int rc = check_layer_index(c, layer);
+    if (rc) return rc;
+    if (n == 0) return QMSG_OK;
+    const LayerStore &L = c->layers[(size_t)layer];
+    if (!L.ready) return fail(c, QMSG_E_INVALID, "layer %d has no weights", layer);
+    const LayerDev d = layer_dev(c, L);
+    const uint8_t *base = which == 0 ? d.gate : (which == 1 ? d.up : d.down);
+    const int type = which == 0 ? d.gate_type : (which == 1 ? d.up_type : d.down_type);
+    const uint64_t rb = which == 0 ? d.gate_rb : (which == 1 ? d.up_rb : d.down_rb);
+    const uint64_t eb = which == 0 ? d.gate_eb : (which == 1 ? d.up_eb : d.down_eb);
+    const int64_t rows = which == 2 ? c->cfg.n_embd : c->cfg.n_ff_exp;
+    const int64_t nblk = (which == 2 ? c->cfg.n_ff_exp : c->cfg.n_embd) / 32;
+    for (int i = 0; i < n; i++)
+        if (expert[i] < 0 || expert[i] >= c->cfg.n_expert || row[i] < 0 || row[i] >= rows || block[i] < 0 ||
+            block[i] >= nblk)
+            return fail(c, QMSG_E_INVALID, "qmsg_block_dots: entry %d out of range", i);
+    HIP_TRY(c, hipSetDevice(c->device));
+    std::vector<void *> tmp;
+    int32_t *dbuf = nullptr;
+    Q8 *dx = nullptr;
+    const size_t ib = (size_t)n * 4;
+    if ((rc = dev_alloc(c, (void **)&dbuf, ib * 4, tmp))) return rc;
+    if ((rc = dev_alloc(c, (void **)&dx, (size_t)n * sizeof(Q8), tmp))) { hipFree(dbuf); return rc; }
+    hipError_t e = hipMemcpy(dbuf, expert, ib, hipMemcpyHostToDevice);
+    if (e == hipSuccess) e = hipMemcpy(dbuf + n, row, ib, hipMemcpyHostToDevice);
+    if (e == hipSuccess) e = hipMemcpy(dbuf + 2 * n, block, ib, hipMemcpyHostToDevice);
+    if (e == hipSuccess) e = hipMemcpy(dx, xq_blocks, (size_t)n * sizeof(Q8), hipMemcpyHostToDevice);
+    if (e == hipSuccess)
+        e = launch_block_dots(base, type, rb, eb, n, dbuf, dbuf + n, dbuf + 2 * n, dx, dbuf + 3 * n, c->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
+    if (e == hipSuccess) e = hipMemcpy(out, dbuf + 3 * n, ib, hipMemcpyDeviceToHost);
+    hipFree(dbuf);
+    hipFree(dx);
+    if (e != hipSuccess) return fail(c, QMSG_E_DEVICE, "qmsg_block_dots: %s", hipGetErrorString(e));
+    return QMSG_OK;
+}
+
+int qmsg_profile(qmsg_ctx *c, int enable)
+{
+    if (!c) return QMSG_E_INVALID;
+    HIP_TRY(c, hipStreamSynchronize(c->stream));
+    for (auto &r : c->prof_recs) c->prof_free.push_back(r);
+    c->prof_recs.clear();
+    c->prof_tot.clear();
+    c->prof = enable != 0;
+    return QMSG_OK;
+}
+
+int qmsg_profile_read(qmsg_ctx *c, const char *name, int64_t *launches, double *total_ms)
+{
+    if (!c || !name) return QMSG_E_INVALID;
+    HIP_TRY(c, hipStreamSynchronize(c->stream));
+    for (auto &r : c->prof_recs) {
+        float ms = 0.0f;
+        HIP_TRY(c, hipEventElapsedTime(&ms, r.a, r.b));
+        bool found = false;
+        for (auto &t : c->prof_tot)
+            if (t.name == r.name) { t.n++; t.ms += ms; found = true; break; }
+        if (!found) c->prof_tot.push_back({ r.name, 1, (double)ms });
+        c->prof_free.push_back(r);
+    }
+    c->prof_recs.clear();
+    int64_t n = 0;
+    double ms = 0.0;
+    for (auto &t : c->prof_tot)
+        if (t.name == name) { n = t.n; ms = t.ms; }
+    if (launches) *launches = n;
+    if (total_ms) *total_ms = ms;
+    return QMSG_OK;
+}
+
+int qmsg_device_info(qmsg_ctx *c, int *n_cu, int *clock_khz, uint64_t *hbm_bytes, char *arch, int arch_len)
+{
+    if (!c) return QMSG_E_INVALID;
+    hipDeviceProp_t p;
+    HIP_TRY(c, hipGetDeviceProperties(&p, c->device));
+    if (n_cu) *n_cu = p.multiProcessorCount;
+    if (clock_khz) *clock_khz = p.clockRate;
+    if (hbm_bytes) *hbm_bytes = (uint64_t)p.totalGlobalMem;
+    if (arch && arch_len > 0) {
+        strncpy(arch, p.gcnArchName, (size_t)arch_len - 1);
+        arch[arch_len - 1] = 0;
+    }
+    return QMSG_OK;
+}
+
+}  // extern "C"

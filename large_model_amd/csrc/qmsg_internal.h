@@ -1,0 +1,82 @@
+/* qmsg_internal.h - shapes and device pointers shared by the host API and the kernels. */
+#ifndef QMSG_INTERNAL_H
+#define QMSG_INTERNAL_H
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace qmsg {
+
+/* QmsQ8 (src/kernels.h:7-12): the reference's 44-byte int8 activation block. */
+struct Q8 {
+    float d;
+    float ds;
+    int16_t s16[2];
+    int8_t q[32];
+};
+static_assert(sizeof(Q8) == 44, "QmsQ8 is 44 bytes");
+
+/* Kernel-side copy of the same blocks, grouped by pairs of 32-blocks (b even, b+1) so one
+ * 16-byte LDS read gives a lane both of its code dwords for two blocks. 96 bytes per pair:
+ *   [16p .. 16p+15]  for lane p = 0..3: q[4p..4p+3] of b, q[16+4p..] of b,
+ *                                        q[4p..4p+3] of b+1, q[16+4p..] of b+1
+ *   [64 .. 79]       d(b), ds(b), d(b+1), ds(b+1)
+ *   [80 .. 87]       s16 pair of b, s16 pair of b+1 (low half = s16[0])
+ *   [88 .. 95]       zero */
+constexpr int kPairBytes = 96;
+
+/* Per-layer device weights: the GGUF bytes, unchanged, in one allocation per tensor. */
+struct LayerDev {
+    const float *router;    /* [X][E] */
+    const uint8_t *gate;    /* [X][F] rows of gate_rb bytes */
+    const uint8_t *up;      /* [X][F] rows of up_rb bytes   */
+    const uint8_t *down;    /* [X][E] rows of down_rb bytes */
+    int gate_type, up_type, down_type;
+    uint64_t gate_rb, up_rb, down_rb;
+    uint64_t gate_eb, up_eb, down_eb;
+};
+
+/* Device scratch of a context, sized for max_tokens. */
+struct Scratch {
+    float *logits;      /* [Tm][X]             */
+    int32_t *sel;       /* [Tm*K]              */
+    float *wt;          /* [Tm*K]              */
+    int32_t *slot_t;    /* [Tm*K]              */
+    int32_t *slot_of;   /* [Tm*K]              */
+    int32_t *start;     /* [X+1]               */
+    int32_t *active;    /* [X]                 */
+    int32_t *meta;      /* [0] n_active, [1] tokens finished, [2..] spare */
+    int32_t *tok_cnt;   /* [Tm] router WGs finished per token   */
+    int32_t *tile_cnt;  /* [E/32] down WGs finished per row tile */
+    Q8 *xq;             /* [Tm][E/32]          */
+    uint8_t *xqk;       /* [Tm][E/64][96]      */
+    float *gu;          /* [Tm*K][2F]          */
+    float *act;         /* [Tm*K][F]           */
+    Q8 *aq;             /* [Tm*K][F/32]        */
+    uint8_t *aqk;       /* [Tm*K][F/64][96]    */
+    float *dn;          /* [Tm*K][E]           */
+};
+
+struct Shape {
+    int E, X, K, F;
+};
+
+/* Launchers (qmsg_kernels.hip). Each returns hipSuccess or the launch error. */
+hipError_t launch_route(const Shape &s, const LayerDev &L, const Scratch &S, const float *xn, int T,
+                        hipStream_t st);
+hipError_t launch_gateup_exact(const Shape &s, const LayerDev &L, const Scratch &S, int T, int debug,
+                               hipStream_t st);
+hipError_t launch_down_exact(const Shape &s, const LayerDev &L, const Scratch &S, float *out, int T,
+                             hipStream_t st);
+hipError_t launch_synth_f32(uint64_t key, uint64_t n, float sigma, float *out, hipStream_t st);
+hipError_t launch_synth_experts(uint64_t seed, uint32_t layer, uint32_t kind, int type, int64_t rows,
+                                int64_t cols, int X, float sigma, uint8_t *base, hipStream_t st);
+hipError_t launch_rmsnorm_rows(float *x, int T, int E, float eps, hipStream_t st);
+hipError_t launch_set_col0(float *m, int rows, int stride, const float *vals, float fill, hipStream_t st);
+hipError_t launch_block_dots(const uint8_t *base, int type, uint64_t rb, uint64_t eb, int n, const int32_t *expert,
+                             const int32_t *row, const int32_t *block, const Q8 *xq, int32_t *out,
+                             hipStream_t st);
+
+}  // namespace qmsg
+
+#endif /* QMSG_INTERNAL_H */

@@ -1,0 +1,62 @@
+"""Layer parity on the GPU: libqmsg (HIP, gfx950) against the CPU oracle on identical seeded inputs.
+
+The exact path must reproduce every intermediate bit for bit: router logits, expert ids and
+weights, dispatch, the int8 input blocks (xq), gate/up rows, SwiGLU activations, the int8
+activation blocks (aq), per-slot down rows and the layer output.
+"""
+import numpy as np
+import pytest
+
+import oracle as orc
+
+pytestmark = pytest.mark.gpu
+
+CASES = [
+    # name, E, X, K, F, T, seed, down_type, rmsnorm
+    ("tiny_t1", 256, 16, 4, 128, 1, 0, orc.T_Q4_0, False),
+    ("tiny_t7", 256, 16, 4, 128, 7, 0, orc.T_Q4_0, False),
+    ("q30b_t1", 2048, 128, 8, 768, 1, 1, orc.T_Q4_0, True),
+    ("q235b_t1", 4096, 128, 8, 1536, 1, 2, orc.T_Q4_0, False),
+    ("q235b_t4", 4096, 128, 8, 1536, 4, 2, orc.T_Q4_0, False),
+    ("q235b_t16", 4096, 128, 8, 1536, 16, 2, orc.T_Q4_0, False),
+    ("q30b_q6k_t5", 2048, 128, 8, 768, 5, 3, orc.T_Q6_K, False),
+    ("q235b_q6k_t3", 4096, 128, 8, 1536, 3, 4, orc.T_Q6_K, False),
+]
+
+
+def _bits(a):
+    return np.ascontiguousarray(a).view(np.uint8)
+
+
+@pytest.fixture(scope="module")
+def qmsg():
+    from large_model_amd import qmsg as q
+    return q
+
+
+@pytest.mark.parametrize("name,E,X,K,F,T,seed,dt,rms", CASES, ids=[c[0] for c in CASES])
+def test_layer_exact(qmsg, name, E, X, K, F, T, seed, dt, rms):
+    print(f"[case] {name} E={E} X={X} K={K} F={F} T={T} seed={seed} down={dt}", flush=True)
+    x = orc.make_input(E, T, seed, rmsnorm=rms)
+    host = orc.Layer(E, X, K, F, seed, down_type=dt, experts=[])
+    ref_out, ref = host.moe(x, debug=True)
+    with qmsg.Context(E, X, K, F, n_layer=1, max_tokens=max(T, 1)) as ctx:
+        ctx.synth(0, seed, down_type=dt)
+        # the device generator wrote the same bytes as the host generator for the used experts
+        r, g, u, d = ctx.download(0)
+        assert np.array_equal(r, host.router)
+        for e in ref["active"]:
+            for dev, hst, eb in ((g, host.gate, host.eb[0]), (u, host.up, host.eb[1]), (d, host.down, host.eb[2])):
+                assert np.array_equal(dev[e * eb:(e + 1) * eb], hst[e * eb:(e + 1) * eb]), f"expert {e} bytes"
+        out, got = ctx.moe_debug(0, x)
+    assert np.array_equal(_bits(got["logits"]), _bits(ref["logits"])), "router logits"
+    assert np.array_equal(got["sel"], ref["sel"]), "expert ids"
+    assert np.array_equal(_bits(got["wt"]), _bits(ref["wt"])), "routing weights"
+    for k in ("start", "slot_t", "slot_of", "active"):
+        assert np.array_equal(got[k], ref[k]), k
+    assert np.array_equal(_bits(got["xq"]), _bits(ref["xq"])), "int8 input blocks"
+    assert np.array_equal(_bits(got["gu"]), _bits(ref["gu"])), "gate/up rows"
+    assert np.array_equal(_bits(got["act"]), _bits(ref["act"])), "swiglu"
+    assert np.array_equal(_bits(got["aq"]), _bits(ref["aq"])), "int8 activation blocks"
+    assert np.array_equal(_bits(got["dn"]), _bits(ref["dn"])), "down rows"
+    assert np.array_equal(_bits(out), _bits(ref_out)), "layer output"
