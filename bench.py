@@ -1,0 +1,246 @@
+#!/usr/bin/env python3
+"""bench.py - Qwen3-MoE expert-FFN layer throughput on one MI355X (libqmsg, gfx950).
+
+A step is one call of the MoE layer (router -> dispatch -> int8 quantise -> gate/up + SwiGLU
+-> down -> weighted combine) on one batch of T tokens. Weights (all 128 experts of each
+layer, GGUF Q4_0 bytes) and inputs are resident in HBM before timing. Consecutive steps use
+different resident layers and different tokens, so each step streams experts that are not in
+the 256 MB last-level cache.
+
+Prints one JSON line: tokens/s, ms per step, a roofline object for the dominant kernel
+(algorithmic bytes / its HIP-event-timed average duration, against 8 TB/s), and the
+reference's own CPU layer (its C sources built by oracle/Makefile, weights resident in host
+RAM) timed on this host's cores on a bounded sample of the same workload.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import subprocess
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+
+
+def physical_cores() -> int:
+    try:
+        out = subprocess.run(["lscpu", "-p=CORE,SOCKET"], capture_output=True, text=True, check=True).stdout
+        cores = {ln for ln in out.splitlines() if ln and not ln.startswith("#")}
+        return max(1, len(cores))
+    except Exception:
+        return os.cpu_count() or 1
+
+
+def cpu_model() -> str:
+    try:
+        for ln in subprocess.run(["lscpu"], capture_output=True, text=True, check=True).stdout.splitlines():
+            if ln.startswith("Model name"):
+                return ln.split(":", 1)[1].strip()
+    except Exception:
+        pass
+    return "unknown"
+
+
+# OpenMP reads its environment when libgomp loads: pin the CPU baseline to the physical
+# cores before anything that links it is imported.
+os.environ.setdefault("OMP_NUM_THREADS", str(physical_cores()))
+os.environ.setdefault("OMP_PROC_BIND", "close")
+os.environ.setdefault("OMP_PLACES", "cores")
+sys.path.insert(0, ROOT)
+
+import numpy as np  # noqa: E402
+
+from large_model_amd import qmsg  # noqa: E402
+from large_model_amd.workloads import HBM_PEAK_GBS, INT8_PEAK_TOPS, WORKLOADS, zipf_bias  # noqa: E402
+
+METRIC = "MoE-layer tokens/s + achieved HBM GB/s (decode), int8 MFMA util (prefill), 1 GPU"
+
+
+def log(msg: str):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def read_traffic(workload: str):
+    """HBM bytes per dominant-kernel launch measured by rocprofv3 --pmc (FETCH_SIZE, WRITE_SIZE),
+    as recorded in profiles/traffic_<kernel>_<workload>.txt; None when not measured."""
+    path = os.path.join(ROOT, "profiles", f"traffic_gateup_{workload}.txt")
+    if not os.path.exists(path):
+        return None
+    vals = {}
+    with open(path) as f:
+        for ln in f:
+            if "=" in ln and not ln.lstrip().startswith("#"):
+                k, v = ln.split("=", 1)
+                vals[k.strip()] = v.strip()
+    try:
+        return float(vals["hbm_bytes_per_launch"])
+    except (KeyError, ValueError):
+        return None
+
+
+def cpu_baseline(ctx, w, seconds: float):
+    """The reference's moe() (oracle/_ref build of its own sources) on this host, else the
+    oracle's restatement, over distinct seeded tokens of the same workload."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle as orc  # checker only: times the CPU path beside the GPU
+
+    R = orc.load_ref()
+    kind = "reference" if R is not None else "port"
+    host = orc.Layer(w.E, w.X, w.K, w.F, w.seed, layer=0, down_type=w.down_type, experts=[])
+    router, gate, up, down = ctx.download(0)
+    host.router[:] = router
+    host.gate, host.up, host.down = gate, up, down
+    host.have = set(range(w.X))
+    xs = [orc.make_input(w.E, w.T, 10_000 + i, rmsnorm=w.rmsnorm) for i in range(64)]
+    run = (lambda x: orc.ref_moe(R, host, x)) if R is not None else (lambda x: host.moe(x))
+    for x in xs[:2]:
+        run(x)
+    n, t0 = 0, time.perf_counter()
+    while True:
+        run(xs[n % len(xs)])
+        n += 1
+        el = time.perf_counter() - t0
+        if (el >= seconds and n >= 5) or el >= 3 * seconds:
+            break
+    threads = R.qref_max_threads() if R is not None else int(os.environ.get("OMP_NUM_THREADS", "1"))
+    isa = R.qref_isa().decode() if R is not None else "oracle restatement"
+    return {
+        "value": round(w.T * n / el, 3),
+        "unit": "tokens/s",
+        "cores": threads,
+        "kind": kind,
+        "sample": f"{n} calls of {'the reference moe() (its C sources, ' + isa + ' build)' if R else 'the oracle'}"
+                  f" on one {w.name} layer, T={w.T}, {len(xs)} distinct seeded inputs cycled, all experts resident"
+                  f" in host RAM; {el:.1f} s on {threads} OpenMP threads of {cpu_model()}",
+        "ms_per_layer": round(1e3 * el / n, 4),
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=500)
+    ap.add_argument("--warmup", type=int, default=50)
+    ap.add_argument("--workload", default="q235b_decode_t1", choices=sorted(WORKLOADS))
+    ap.add_argument("--layers", type=int, default=16, help="distinct resident layers cycled by the steps")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--path", choices=["auto", "exact", "mfma"], default="auto")
+    args = ap.parse_args()
+
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path (expert sharding is described in "
+              "DESIGN.md, not built). Run with --gpus 1.", file=sys.stderr)
+        sys.exit(2)
+
+    w = WORKLOADS[args.workload]
+    K_steps, W_steps, NL = args.steps, args.warmup, max(1, args.layers)
+    total = K_steps + W_steps
+    log(f"workload {w.name}: E={w.E} X={w.X} K={w.K} F={w.F} T={w.T}, {NL} resident layers")
+    ctx = qmsg.Context(w.E, w.X, w.K, w.F, n_layer=NL, max_tokens=w.T)
+    ctx.set_path({"auto": qmsg.PATH_AUTO, "exact": qmsg.PATH_EXACT, "mfma": qmsg.PATH_MFMA}[args.path])
+    bias = zipf_bias(w.X, w.K, w.T, w.E) if w.zipf else None
+    for l in range(NL):
+        ctx.synth(l, w.seed + 1000 * l, down_type=w.down_type, router_col0=bias)
+    log("weights generated in HBM")
+    row = w.T * w.E * 4
+    d_x = ctx.device_alloc(total * row)
+    d_out = ctx.device_alloc(total * row)
+    for s in range(total):
+        ctx.synth_input(w.seed + 7 + s, 0, w.T, d_x + s * row, rmsnorm=w.rmsnorm, bias_col0=w.zipf)
+    ctx.sync()
+
+    def step(s):
+        ctx.moe_device(s % NL, d_x + s * row, w.T, d_out + s * row)
+
+    for s in range(W_steps):
+        step(s)
+    ctx.sync()
+    t0 = time.perf_counter()
+    for s in range(W_steps, total):
+        step(s)
+    ctx.sync()
+    el = time.perf_counter() - t0
+    ms_step = 1e3 * el / K_steps
+    log(f"timed {K_steps} steps: {ms_step * 1e3:.2f} us/step")
+
+    # the same steps again with HIP events around every kernel, on the library's stream
+    ctx.profile(True)
+    for s in range(W_steps, total):
+        step(s)
+    ctx.sync()
+    kern = {}
+    for name in ("route", "select", "gateup", "down"):
+        n, ms = ctx.profile_read(name)
+        if n:
+            kern[name] = {"launches": n, "avg_us": round(1e3 * ms / n, 3)}
+    ctx.profile(False)
+
+    # distinct experts per call (8 at T=1); sampled through the debug entry for larger T
+    if w.T == 1:
+        d_active = w.K
+    else:
+        ds = []
+        for s in range(min(8, K_steps)):
+            x = ctx.d2h(d_x + (W_steps + s) * row, (w.T, w.E))
+            _, dbg = ctx.moe_debug((W_steps + s) % NL, x)
+            ds.append(len(dbg["active"]))
+        d_active = float(np.mean(ds))
+    gate_up_bytes = d_active * 2 * w.gate_bytes
+    layer_bytes = w.layer_bytes(0) + d_active * w.expert_bytes
+    g_us = kern.get("gateup", {}).get("avg_us")
+    achieved = gate_up_bytes / (g_us * 1e-6) / 1e9 if g_us else None
+    traffic = read_traffic(w.name)
+    result = {
+        "metric": METRIC,
+        "value": round(w.T * K_steps / el, 3),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": K_steps,
+        "warmup": W_steps,
+        "ms_per_step": round(ms_step, 6),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8",
+        "data": "synthetic",
+        "config": {
+            "workload": f"{w.name}: {w.note}",
+            "n_embd": w.E, "n_expert": w.X, "n_used": w.K, "n_ff_exp": w.F, "tokens_per_step": w.T,
+            "weights": "Q4_0 gate/up/" + ("Q6_K" if w.down_type == qmsg.QMSG_T_Q6_K else "Q4_0") + " down, F32 router",
+            "resident_layers_cycled": NL, "path": args.path,
+        },
+        "roofline": {
+            "kernel": "gateup (gate/up Q4_0 row dots + SwiGLU + int8 requantise)",
+            "bound": "hbm",
+            "achieved": round(achieved, 1) if achieved else None,
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4) if achieved else None,
+            "traffic": traffic,
+            "algorithmic_bytes_per_launch": int(gate_up_bytes),
+        },
+        "layer": {
+            "algorithmic_bytes": int(layer_bytes),
+            "distinct_experts": d_active,
+            "achieved_GBps": round(layer_bytes / (ms_step * 1e-3) / 1e9, 1),
+            "frac_of_hbm_peak": round(layer_bytes / (ms_step * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+            "int8_tops": round(w.int8_ops() / (ms_step * 1e-3) / 1e12, 3),
+            "int8_frac_of_peak": round(w.int8_ops() / (ms_step * 1e-3) / 1e12 / INT8_PEAK_TOPS, 5),
+        },
+        "kernels": kern,
+        "device": ctx.device_info(),
+        "cpu_baseline": None,
+    }
+    if not args.no_cpu:
+        log("timing the CPU baseline")
+        result["cpu_baseline"] = cpu_baseline(ctx, w, args.cpu_seconds)
+    ctx.close()
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -178,6 +178,10 @@ int qmsg_profile(qmsg_ctx *ctx, int enable);
  * (synchronises the stream). Names: "route", "gateup", "down", and the MFMA-path kernels. */
 int qmsg_profile_read(qmsg_ctx *ctx, const char *name, int64_t *launches, double *total_ms);
 
+/* No reference counterpart: a plain device copy of `bytes` (multiple of 16) with a simple
+ * coalesced kernel, used to calibrate HBM byte counters against a known transfer. */
+int qmsg_calibrate_copy(qmsg_ctx *ctx, void *d_dst, const void *d_src, size_t bytes);
+
 /* Device facts used by the roofline report: CU count, peak engine clock (kHz), HBM bytes. */
 int qmsg_device_info(qmsg_ctx *ctx, int *n_cu, int *clock_khz, uint64_t *hbm_bytes, char *arch, int arch_len);
 

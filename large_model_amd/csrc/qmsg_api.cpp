@@ -130,8 +130,9 @@ int qmsg_create(qmsg_ctx **out, int device, const qmsg_cfg *cfg, int n_layer, in
                     n_layer, max_tokens);
     /* The reference's integer fast path needs E % 256 == 0 and F % 32 == 0
      * (src/model.c:1090-1093). The kernels also pair 32-blocks (F % 64 == 0), run four router
-     * dots per wave (X % 4 == 0) and keep per-expert state in 256-entry LDS arrays (X <= 256). */
-    if (E % 256 || F % 64 || X % 4 || X > 256 || K > 64)
+     * dots in 16-expert tiles (X % 16 == 0) and keep per-expert state in 256-entry LDS arrays
+     * (X <= 256). */
+    if (E % 256 || F % 64 || X % 16 || X > kMaxExperts || K > 64)
         return fail(nullptr, QMSG_E_UNSUPPORTED, "qmsg_create: unsupported shape E=%d X=%d K=%d F=%d", E, X, K, F);
     int ndev = 0;
     if (hipGetDeviceCount(&ndev) != hipSuccess || device < 0 || device >= ndev)
@@ -155,7 +156,7 @@ int qmsg_create(qmsg_ctx **out, int device, const qmsg_cfg *cfg, int n_layer, in
         { (void **)&c->S.wt, NS * 4 },          { (void **)&c->S.slot_t, NS * 4 },
         { (void **)&c->S.slot_of, NS * 4 },     { (void **)&c->S.start, (size_t)(X + 1) * 4 },
         { (void **)&c->S.active, (size_t)X * 4 }, { (void **)&c->S.meta, 64 },
-        { (void **)&c->S.tok_cnt, Tm * 4 },     { (void **)&c->S.tile_cnt, (size_t)(E / 32) * 4 },
+        { (void **)&c->S.work, (size_t)X * 16 },
         { (void **)&c->S.xq, Tm * nbE * sizeof(Q8) }, { (void **)&c->S.xqk, Tm * (nbE / 2) * kPairBytes },
         { (void **)&c->S.gu, NS * 2 * F * 4 },  { (void **)&c->S.act, NS * F * 4 },
         { (void **)&c->S.aq, NS * nbF * sizeof(Q8) }, { (void **)&c->S.aqk, NS * (nbF / 2) * kPairBytes },
@@ -169,10 +170,7 @@ int qmsg_create(qmsg_ctx **out, int device, const qmsg_cfg *cfg, int n_layer, in
             return QMSG_E_NOMEM;
         }
     }
-    /* counters start at zero; the kernels that use them leave them at zero */
     e = hipMemset(c->S.meta, 0, 64);
-    if (e == hipSuccess) e = hipMemset(c->S.tok_cnt, 0, Tm * 4);
-    if (e == hipSuccess) e = hipMemset(c->S.tile_cnt, 0, (size_t)(E / 32) * 4);
     if (e != hipSuccess) {
         fail(nullptr, QMSG_E_DEVICE, "qmsg_create: %s", hipGetErrorString(e));
         qmsg_destroy(c);
@@ -359,6 +357,7 @@ static int run_layer(qmsg_ctx *c, int layer, const float *d_xn, int T, float *d_
     const Shape s{ c->cfg.n_embd, c->cfg.n_expert, c->cfg.n_used, c->cfg.n_ff_exp };
     const LayerDev d = layer_dev(c, L);
     LAUNCH(c, "route", launch_route(s, d, c->S, d_xn, T, c->stream));
+    LAUNCH(c, "select", launch_select(s, c->S, T, c->stream));
     LAUNCH(c, "gateup", launch_gateup_exact(s, d, c->S, T, debug, c->stream));
     LAUNCH(c, "down", launch_down_exact(s, d, c->S, d_out, T, c->stream));
     return QMSG_OK;
@@ -530,6 +529,14 @@ int qmsg_profile_read(qmsg_ctx *c, const char *name, int64_t *launches, double *
         if (t.name == name) { n = t.n; ms = t.ms; }
     if (launches) *launches = n;
     if (total_ms) *total_ms = ms;
+    return QMSG_OK;
+}
+
+int qmsg_calibrate_copy(qmsg_ctx *c, void *d_dst, const void *d_src, size_t bytes)
+{
+    if (!c || !d_dst || !d_src || bytes % 16) return QMSG_E_INVALID;
+    HIP_TRY(c, hipSetDevice(c->device));
+    LAUNCH(c, "copy", launch_copy(d_dst, d_src, bytes, c->stream));
     return QMSG_OK;
 }
 

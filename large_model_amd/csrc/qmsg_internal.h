@@ -25,6 +25,9 @@ static_assert(sizeof(Q8) == 44, "QmsQ8 is 44 bytes");
  *   [88 .. 95]       zero */
 constexpr int kPairBytes = 96;
 
+/* Static shape limits of the kernels. */
+constexpr int kMaxExperts = 256;
+
 /* Per-layer device weights: the GGUF bytes, unchanged, in one allocation per tensor. */
 struct LayerDev {
     const float *router;    /* [X][E] */
@@ -45,9 +48,8 @@ struct Scratch {
     int32_t *slot_of;   /* [Tm*K]              */
     int32_t *start;     /* [X+1]               */
     int32_t *active;    /* [X]                 */
-    int32_t *meta;      /* [0] n_active, [1] tokens finished, [2..] spare */
-    int32_t *tok_cnt;   /* [Tm] router WGs finished per token   */
-    int32_t *tile_cnt;  /* [E/32] down WGs finished per row tile */
+    int4 *work;         /* [X] per active expert: {expert, first slot, end slot, 0}; expert -1 after */
+    int32_t *meta;      /* [0] n_active */
     Q8 *xq;             /* [Tm][E/32]          */
     uint8_t *xqk;       /* [Tm][E/64][96]      */
     float *gu;          /* [Tm*K][2F]          */
@@ -64,6 +66,7 @@ struct Shape {
 /* Launchers (qmsg_kernels.hip). Each returns hipSuccess or the launch error. */
 hipError_t launch_route(const Shape &s, const LayerDev &L, const Scratch &S, const float *xn, int T,
                         hipStream_t st);
+hipError_t launch_select(const Shape &s, const Scratch &S, int T, hipStream_t st);
 hipError_t launch_gateup_exact(const Shape &s, const LayerDev &L, const Scratch &S, int T, int debug,
                                hipStream_t st);
 hipError_t launch_down_exact(const Shape &s, const LayerDev &L, const Scratch &S, float *out, int T,
@@ -73,6 +76,7 @@ hipError_t launch_synth_experts(uint64_t seed, uint32_t layer, uint32_t kind, in
                                 int64_t cols, int X, float sigma, uint8_t *base, hipStream_t st);
 hipError_t launch_rmsnorm_rows(float *x, int T, int E, float eps, hipStream_t st);
 hipError_t launch_set_col0(float *m, int rows, int stride, const float *vals, float fill, hipStream_t st);
+hipError_t launch_copy(void *dst, const void *src, size_t bytes, hipStream_t st);
 hipError_t launch_block_dots(const uint8_t *base, int type, uint64_t rb, uint64_t eb, int n, const int32_t *expert,
                              const int32_t *row, const int32_t *block, const Q8 *xq, int32_t *out,
                              hipStream_t st);

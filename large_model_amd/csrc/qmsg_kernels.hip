@@ -30,6 +30,17 @@ __device__ __forceinline__ float h2f(uint32_t bits16)
 
 __device__ __forceinline__ int sdot4(int a, int b) { return __builtin_amdgcn_sdot4(a, b, 0, false); }
 
+/* fp16 (low or high half of h) times an fp32, rounded once: the product of the exact fp32
+ * value of the half and f (the added zero cannot change a non-zero product). */
+template <int HI>
+__device__ __forceinline__ float mul_f16_f32(uint32_t h, float f)
+{
+    float r;
+    if (HI) asm volatile("v_fma_mix_f32 %0, %1, %2, 0 op_sel:[1,0,0] op_sel_hi:[1,0,0]" : "=v"(r) : "v"(h), "v"(f));
+    else asm volatile("v_fma_mix_f32 %0, %1, %2, 0 op_sel_hi:[1,0,0]" : "=v"(r) : "v"(h), "v"(f));
+    return r;
+}
+
 /* 2^(i/32) rounded to double, minus i << 47 (the exponent part added back at use). */
 __device__ const uint64_t kExp2fTab[32] = {
     0x3ff0000000000000ULL, 0x3fefd9b0d3158574ULL, 0x3fefb5586cf9890fULL, 0x3fef9301d0125b51ULL,
@@ -122,163 +133,176 @@ __device__ void quantize_block_store(const float *v, Q8 *dst, uint32_t *pair, in
     if (half == 0) { pair[22] = 0; pair[23] = 0; }
 }
 
+/* ------------------------------------------------------------------ wave primitives ---- */
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+/* LDS ordering between the lanes of one wave (its LDS operations complete in order). */
+__device__ __forceinline__ void wave_sync()
+{
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+}
+
+/* DPP lane moves (GFX9 encodings): row_shr:n = 0x110+n, row_bcast:15 = 0x142, row_bcast:31 = 0x143.
+ * Lanes without a valid source, or in rows outside ROWM, return `old`. */
+template <int CTRL, int ROWM = 0xf>
+__device__ __forceinline__ uint32_t dpp32(uint32_t old, uint32_t v)
+{
+    return (uint32_t)__builtin_amdgcn_update_dpp((int)old, (int)v, CTRL, ROWM, 0xf, false);
+}
+
+/* Inclusive prefix sum over the 64 lanes. */
+__device__ __forceinline__ int wave_scan_add(int v)
+{
+    v += (int)dpp32<0x111>(0u, (uint32_t)v);
+    v += (int)dpp32<0x112>(0u, (uint32_t)v);
+    v += (int)dpp32<0x114>(0u, (uint32_t)v);
+    v += (int)dpp32<0x118>(0u, (uint32_t)v);
+    v += (int)dpp32<0x142, 0xa>(0u, (uint32_t)v);
+    v += (int)dpp32<0x143, 0xc>(0u, (uint32_t)v);
+    return v;
+}
+
 /* ------------------------------------------------------------------ route ---- */
 
 struct RouteArgs {
     const float *router, *xn;
-    int E, X, K, T, n_dot_wg;
+    int E, X, K, T;
+    int n_route_wg;    /* blocks doing router dots; the blocks after them quantise the input */
     Scratch S;
 };
 
-/* Softmax over one token's logits in double, K rounds of argmax with ties to the lower
- * index, weights renormalised over the selection (src/model.c:1045-1064). One wave. */
-__device__ void topk_token(const RouteArgs &a, int t, double *P, int *taken)
+/* Blocks past the router blocks: one input 32-block per thread (src/kernels.c:34-53). */
+__device__ void route_quantize(const RouteArgs &a)
 {
-    const int X = a.X, K = a.K, lane = threadIdx.x;
-    const float *lt = a.S.logits + (size_t)t * a.X;
-    double mx = -__builtin_inf();
-    for (int e = lane; e < X; e += 64) {
-        const double v = (double)lt[e];
-        if (v > mx) mx = v;
+    const int nbE = a.E >> 5;
+    const int b = ((int)blockIdx.x - a.n_route_wg) * (int)blockDim.x + (int)threadIdx.x;
+    if (b >= a.T * nbE) return;
+    const int t = b / nbE, blk = b - t * nbE;
+    float v[32];
+    const float4 *src = (const float4 *)(a.xn + (size_t)t * a.E + (size_t)blk * 32);
+    for (int j = 0; j < 8; j++) {
+        const float4 f = src[j];
+        v[4 * j] = f.x; v[4 * j + 1] = f.y; v[4 * j + 2] = f.z; v[4 * j + 3] = f.w;
     }
-    for (int o = 32; o > 0; o >>= 1) {
-        const double v = __shfl_xor(mx, o);
-        if (v > mx) mx = v;
-    }
-    for (int e = lane; e < X; e += 64) {
-        P[e] = exp((double)lt[e] - mx);
-        taken[e] = 0;
-    }
-    __syncthreads();
-    double z = 0.0;
-    if (lane == 0)
-        for (int e = 0; e < X; e++) z += P[e];           /* sequential, as the reference */
-    z = __shfl(z, 0);
-    for (int e = lane; e < X; e += 64) P[e] /= z;
-    __syncthreads();
-    double wsum = 0.0;
-    int *sel = a.S.sel + (size_t)t * K;
-    for (int j = 0; j < K; j++) {
-        double bp = 0.0;
-        int be = -1;
-        for (int e = lane; e < X; e += 64)
-            if (!taken[e] && (be < 0 || P[e] > bp)) { bp = P[e]; be = e; }
-        for (int o = 32; o > 0; o >>= 1) {
-            const double op = __shfl_xor(bp, o);
-            const int oe = __shfl_xor(be, o);
-            if (oe >= 0 && (be < 0 || op > bp || (op == bp && oe < be))) { bp = op; be = oe; }
-        }
-        if (lane == 0) {
-            sel[j] = be;
-            taken[be] = 1;
-            wsum += P[be];
-        }
-        __syncthreads();
-    }
-    if (lane == 0)
-        for (int j = 0; j < K; j++) a.S.wt[(size_t)t * K + j] = (float)(P[sel[j]] / wsum);
+    uint32_t *pair = (uint32_t *)(a.S.xqk + ((size_t)t * (nbE >> 1) + (blk >> 1)) * kPairBytes);
+    quantize_block_store(v, a.S.xq + (size_t)t * nbE + blk, pair, blk & 1);
 }
 
-/* Counting sort of the T*K (token, selection) slots by expert, src/model.c:1066-1088:
- * slots of one expert are contiguous, experts ascend, and inside an expert slots follow
- * token order then selection order. One wave. */
-__device__ void dispatch_slots(const RouteArgs &a, int *cnt, int *cur)
+/* hsum of dot_f32 (src/kernels.c:211, 66-72) over the 16 chain lanes of a 16-lane group:
+ * v_j = a0_j + a1_j (chains j and j+8), s_j = v_j + v_{j+4}, (s0+s2)+(s1+s3). Lane 0 holds it. */
+__device__ __forceinline__ float chain16_sum(float acc)
 {
-    const int X = a.X, NS = a.T * a.K, lane = threadIdx.x;
-    for (int e = lane; e < X; e += 64) { cnt[e] = 0; cur[e] = 0; }
-    __syncthreads();
-    for (int i = lane; i < NS; i += 64) atomicAdd(&cnt[a.S.sel[i]], 1);
-    __syncthreads();
-    if (lane == 0) {
-        int acc = 0, na = 0;
-        a.S.start[0] = 0;
-        for (int e = 0; e < X; e++) {
-            const int c = cnt[e];
-            cnt[e] = acc;                    /* cnt now holds start[e] */
-            acc += c;
-            a.S.start[e + 1] = acc;
-            if (c) a.S.active[na++] = e;
-        }
-        a.S.meta[0] = na;
-    }
-    __syncthreads();
-    const unsigned long long below = (1ULL << lane) - 1ULL;
-    for (int base = 0; base < NS; base += 64) {
-        const int i = base + lane;
-        const int e = i < NS ? a.S.sel[i] : -1;
-        unsigned long long same = __ballot(i < NS);
-        for (int bit = 0; bit < 9; bit++) {
-            const unsigned long long b = __ballot(i < NS && ((e >> bit) & 1));
-            same &= ((e >> bit) & 1) ? b : ~b;
-        }
-        int s = 0;
-        if (i < NS) s = cnt[e] + cur[e] + __popcll(same & below);
-        __syncthreads();
-        if (i < NS) {
-            a.S.slot_t[s] = i / a.K;
-            a.S.slot_of[i] = s;
-            if ((same >> lane) == 1ULL) cur[e] += __popcll(same);   /* highest lane of the group */
-        }
-        __syncthreads();
-    }
+    acc += __shfl_down(acc, 8, 16);
+    acc += __shfl_down(acc, 4, 16);
+    acc += __shfl_down(acc, 2, 16);
+    acc += __shfl_down(acc, 1, 16);
+    return acc;
 }
 
-/* Router dots + input quantisation. Blocks [0, n_dot_wg): one wave, four (token, expert)
- * dots of 16 lanes each; lane c runs the reference's FMA chain over elements c, c+16, ...
- * (two 8-lane AVX registers = 16 chains), then the hsum256 tree over the 16 chain sums.
- * The last block to finish a token runs its top-K; the last token to finish runs the
- * counting sort. Remaining blocks quantise the input rows, one 32-block per thread. */
-__global__ __launch_bounds__(64) void route_kernel(RouteArgs a)
+/* Router for T <= 4: one block per expert, 256 threads. The expert's router row and the T
+ * input rows are staged into LDS with every load in flight; lane (t, c) of wave 0 then runs
+ * the reference's FMA chain c (elements c, c+16, ...) of token t (src/kernels.c:202-213). */
+__global__ __launch_bounds__(256) void route_small_kernel(RouteArgs a)
 {
-    __shared__ double P[256];
-    __shared__ int taken[256];
-    __shared__ int cnt[256], cur[256];
-    __shared__ int flag;
-    const int lane = threadIdx.x;
-    if ((int)blockIdx.x >= a.n_dot_wg) {
-        const int nbE = a.E >> 5;
-        const int b = ((int)blockIdx.x - a.n_dot_wg) * 64 + lane;
-        if (b >= a.T * nbE) return;
-        const int t = b / nbE, blk = b - t * nbE;
-        float v[32];
-        const float4 *src = (const float4 *)(a.xn + (size_t)t * a.E + (size_t)blk * 32);
-        for (int j = 0; j < 8; j++) {
-            const float4 f = src[j];
-            v[4 * j] = f.x; v[4 * j + 1] = f.y; v[4 * j + 2] = f.z; v[4 * j + 3] = f.w;
+    extern __shared__ __align__(16) uint8_t smem[];
+    if ((int)blockIdx.x >= a.n_route_wg) { route_quantize(a); return; }
+    const int tid = threadIdx.x, E = a.E, T = a.T, e = blockIdx.x;
+    const int XS = E + 16;                       /* padded x rows: lanes of different t hit other banks */
+    float *wrow = (float *)smem, *xr = wrow + E;
+    const int nw = E / 4, nslot = nw * (1 + T);
+    const u32x4 *wsrc = (const u32x4 *)(a.router + (size_t)e * E);
+    const u32x4 *xsrc = (const u32x4 *)a.xn;
+    for (int base = 0; base < nslot; base += 256 * 20) {
+        u32x4 v[20];
+#pragma unroll
+        for (int m = 0; m < 20; m++) {
+            const int i = min(base + tid + 256 * m, nslot - 1);
+            v[m] = i < nw ? wsrc[i] : xsrc[i - nw];
         }
-        uint32_t *pair = (uint32_t *)(a.S.xqk + ((size_t)t * (nbE >> 1) + (blk >> 1)) * kPairBytes);
-        quantize_block_store(v, a.S.xq + (size_t)t * nbE + blk, pair, blk & 1);
-        return;
+#pragma unroll
+        for (int m = 0; m < 20; m++) {
+            const int i = min(base + tid + 256 * m, nslot - 1);
+            float *dst = i < nw ? wrow + 4 * i : xr + ((i - nw) / nw) * XS + 4 * ((i - nw) % nw);
+            *(u32x4 *)dst = v[m];
+        }
     }
-    const int dot = (int)blockIdx.x * 4 + (lane >> 4), c = lane & 15;
-    const int t = dot / a.X, e = dot - t * a.X;
-    const float *w = a.router + (size_t)e * a.E, *x = a.xn + (size_t)t * a.E;
-    const int E16 = a.E & ~15;
-    float acc = 0.0f;
+    __syncthreads();
+    if (tid < 16 * T) {
+        const int t = tid >> 4, c = tid & 15, E16 = E & ~15;
+        const float *xrow = xr + t * XS;
+        float acc = 0.0f;
 #pragma unroll 16
-    for (int i = c; i < E16; i += 16) acc = __builtin_fmaf(w[i], x[i], acc);
-    acc += __shfl_down(acc, 8, 16);      /* v_j = a0_j + a1_j            */
-    acc += __shfl_down(acc, 4, 16);      /* s_j = v_j + v_{j+4}          */
-    acc += __shfl_down(acc, 2, 16);      /* (s0 + s2), (s1 + s3)         */
-    acc += __shfl_down(acc, 1, 16);      /* (s0 + s2) + (s1 + s3)        */
-    if (c == 0) {
-        for (int i = E16; i < a.E; i++) acc = __builtin_fmaf(w[i], x[i], acc);
-        a.S.logits[(size_t)t * a.X + e] = acc;
+        for (int i = c; i < E16; i += 16) acc = __builtin_fmaf(wrow[i], xrow[i], acc);
+        acc = chain16_sum(acc);
+        if (c == 0) {
+            for (int i = E16; i < E; i++) acc = __builtin_fmaf(wrow[i], xrow[i], acc);
+            a.S.logits[(size_t)t * a.X + e] = acc;
+        }
     }
-    __threadfence();
-    if (lane == 0) flag = atomicAdd(&a.S.tok_cnt[t], 1) == a.X / 4 - 1;
-    __syncthreads();
-    if (!flag) return;
-    __threadfence();
-    topk_token(a, t, P, taken);
-    if (lane == 0) a.S.tok_cnt[t] = 0;
-    __threadfence();
-    if (lane == 0) flag = atomicAdd(&a.S.meta[1], 1) == a.T - 1;
-    __syncthreads();
-    if (!flag) return;
-    __threadfence();
-    dispatch_slots(a, cnt, cur);
-    if (lane == 0) a.S.meta[1] = 0;
+}
+
+/* Router for T > 4: one block per 16 tokens x 16 experts, 256 threads. Thread (c, ea, tb)
+ * runs chain c of 4 experts x 4 tokens over 256-element chunks staged in LDS (register
+ * prefetch of the next chunk). */
+__global__ __launch_bounds__(256) void route_big_kernel(RouteArgs a)
+{
+    extern __shared__ __align__(16) uint8_t smem[];
+    if ((int)blockIdx.x >= a.n_route_wg) { route_quantize(a); return; }
+    constexpr int CH = 256, RS = CH + 4;          /* chunk elements, padded LDS row */
+    const int tid = threadIdx.x, E = a.E, T = a.T, X = a.X;
+    const int egs = X / 16, tg = (int)blockIdx.x / egs, eg = (int)blockIdx.x - tg * egs;
+    const int t0 = tg * 16, e0 = eg * 16;
+    const int c = tid & 15, ea = (tid >> 4) & 3, tb = tid >> 6;
+    float *W = (float *)smem, *Xt = W + 16 * RS;
+    float acc[4][4];
+    for (int j = 0; j < 4; j++) for (int k = 0; k < 4; k++) acc[j][k] = 0.0f;
+    u32x4 pw[4], px[4];
+    const int nch = E / CH;
+#define QMSG_RSRC(base, row, m, ch)                                                                  \
+    ((const u32x4 *)((base) + (size_t)(row) * E + (size_t)(ch) * CH + ((tid + 256 * (m)) & 63) * 4))
+#pragma unroll
+    for (int m = 0; m < 4; m++) {
+        const int r = (tid + 256 * m) >> 6;
+        pw[m] = *QMSG_RSRC(a.router, e0 + r, m, 0);
+        px[m] = *QMSG_RSRC(a.xn, min(t0 + r, T - 1), m, 0);
+    }
+    for (int ch = 0; ch < nch; ch++) {
+        __syncthreads();
+#pragma unroll
+        for (int m = 0; m < 4; m++) {
+            const int q = tid + 256 * m, r = q >> 6, col = (q & 63) * 4;
+            *(u32x4 *)(W + r * RS + col) = pw[m];
+            *(u32x4 *)(Xt + r * RS + col) = px[m];
+        }
+        __syncthreads();
+        if (ch + 1 < nch) {
+#pragma unroll
+            for (int m = 0; m < 4; m++) {
+                const int r = (tid + 256 * m) >> 6;
+                pw[m] = *QMSG_RSRC(a.router, e0 + r, m, ch + 1);
+                px[m] = *QMSG_RSRC(a.xn, min(t0 + r, T - 1), m, ch + 1);
+            }
+        }
+#pragma unroll
+        for (int s = 0; s < 16; s++) {
+            const int i = 16 * s + c;
+            float wv[4], xv[4];
+            for (int j = 0; j < 4; j++) wv[j] = W[(4 * ea + j) * RS + i];
+            for (int k = 0; k < 4; k++) xv[k] = Xt[(4 * tb + k) * RS + i];
+            for (int j = 0; j < 4; j++)
+                for (int k = 0; k < 4; k++) acc[j][k] = __builtin_fmaf(wv[j], xv[k], acc[j][k]);
+        }
+    }
+#undef QMSG_RSRC
+    for (int j = 0; j < 4; j++)
+        for (int k = 0; k < 4; k++) {
+            const float v = chain16_sum(acc[j][k]);
+            const int t = t0 + 4 * tb + k, e = e0 + 4 * ea + j;
+            if (c == 0 && t < T) a.S.logits[(size_t)t * X + e] = v;
+        }
 }
 
 hipError_t launch_route(const Shape &s, const LayerDev &L, const Scratch &S, const float *xn, int T, hipStream_t st)
@@ -290,10 +314,197 @@ hipError_t launch_route(const Shape &s, const LayerDev &L, const Scratch &S, con
     a.X = s.X;
     a.K = s.K;
     a.T = T;
-    a.n_dot_wg = T * s.X / 4;
     a.S = S;
-    const int nq = (T * (s.E / 32) + 63) / 64;
-    hipLaunchKernelGGL(route_kernel, dim3(a.n_dot_wg + nq), dim3(64), 0, st, a);
+    const int nq = (T * (s.E / 32) + 255) / 256;
+    if (T <= 4) {
+        a.n_route_wg = s.X;
+        const size_t lds = (size_t)(s.E + T * (s.E + 16)) * 4;
+        hipLaunchKernelGGL(route_small_kernel, dim3(a.n_route_wg + nq), dim3(256), lds, st, a);
+    } else {
+        a.n_route_wg = ((T + 15) / 16) * (s.X / 16);
+        const size_t lds = (size_t)2 * 16 * (256 + 4) * 4;
+        hipLaunchKernelGGL(route_big_kernel, dim3(a.n_route_wg + nq), dim3(256), lds, st, a);
+    }
+    return hipGetLastError();
+}
+
+/* ------------------------------------------------------------------ select + dispatch ---- */
+
+struct SelectArgs {
+    int X, K, T;
+    Scratch S;
+};
+
+/* Softmax over one token's logits in double, then the top K by (probability descending,
+ * index ascending) - the order K rounds of argmax with ties to the lower index produce -
+ * and weights renormalised over the selection (src/model.c:1045-1064). One block of 256
+ * threads per token: P[e] = exp(l_e - max) / z in LDS with z summed sequentially in expert
+ * order; two threads per expert count the experts that precede it; wsum is summed in
+ * selection order. */
+__device__ void topk_token(const SelectArgs &a, int t, double *P, int *part, int *selb)
+{
+    const int X = a.X, K = a.K, tid = threadIdx.x;
+    const float *lt = a.S.logits + (size_t)t * X;
+    __shared__ double red[4];
+    __shared__ double zs;
+    double mx = -__builtin_inf();
+    for (int e = tid; e < X; e += 256) {
+        const double v = (double)lt[e];
+        P[e] = v;
+        if (v > mx) mx = v;
+    }
+    for (int o = 32; o > 0; o >>= 1) {
+        const double v = __shfl_xor(mx, o);
+        if (v > mx) mx = v;
+    }
+    if ((tid & 63) == 0) red[tid >> 6] = mx;
+    __syncthreads();
+    mx = fmax(fmax(red[0], red[1]), fmax(red[2], red[3]));
+    for (int e = tid; e < X; e += 256) P[e] = exp(P[e] - mx);
+    __syncthreads();
+    if (tid == 0) {
+        double z = 0.0;
+#pragma unroll 16
+        for (int e = 0; e < X; e++) z += P[e];
+        zs = z;
+    }
+    __syncthreads();
+    const double z = zs;
+    for (int e = tid; e < X; e += 256) P[e] /= z;
+    __syncthreads();
+    /* rank(e) = #{e' : P[e'] > P[e]} + #{e' < e : P[e'] == P[e]}, split over two threads */
+    for (int w = tid; w < 2 * X; w += 256) {
+        const int e = w >> 1, half = w & 1;
+        const double pe = P[e];
+        const int lo = half ? X / 2 : 0, hi = half ? X : X / 2;
+        int r = 0;
+#pragma unroll 8
+        for (int f = lo; f < hi; f++) {
+            const double pf = P[f];
+            r += (pf > pe) | ((pf == pe) & (f < e));
+        }
+        part[w] = r;
+    }
+    __syncthreads();
+    for (int e = tid; e < X; e += 256) {
+        const int r = part[2 * e] + part[2 * e + 1];
+        if (r < K) selb[r] = e;
+    }
+    __syncthreads();
+    if (tid == 0) {
+        double wsum = 0.0;
+        for (int j = 0; j < K; j++) wsum += P[selb[j]];
+        zs = wsum;
+    }
+    __syncthreads();
+    if (tid < K) {
+        a.S.sel[(size_t)t * K + tid] = selb[tid];
+        a.S.wt[(size_t)t * K + tid] = (float)(P[selb[tid]] / zs);
+    }
+    __syncthreads();
+}
+
+/* Counting sort of the T*K (token, selection) slots by expert, src/model.c:1066-1088:
+ * slots of one expert are contiguous, experts ascend, and inside an expert slots follow
+ * token order then selection order. Also writes one work record per active expert
+ * (expert, first slot, end slot) for the expert kernels, and -1 records after them. One wave. */
+__device__ void dispatch_slots(const SelectArgs &a, int *cnt, int *cur, int *tok)
+{
+    constexpr int NPL = kMaxExperts / 64;
+    const int X = a.X, NS = a.T * a.K, lane = threadIdx.x & 63;
+    for (int e = lane; e < X; e += 64) { cnt[e] = 0; cur[e] = 0; tok[e] = 0; }
+    wave_sync();
+    for (int i = lane; i < NS; i += 64) atomicAdd(&cnt[a.S.sel[i]], 1);
+    wave_sync();
+    /* lane l owns experts l*NPL .. l*NPL+NPL-1 (contiguous, so a lane scan orders them) */
+    int c[NPL], tot = 0, act = 0;
+#pragma unroll
+    for (int i = 0; i < NPL; i++) {
+        const int e = lane * NPL + i;
+        c[i] = e < X ? cnt[e] : 0;
+        tot += c[i];
+        act += c[i] > 0;
+    }
+    const int incl = wave_scan_add(tot), incl_a = wave_scan_add(act);
+    int st = incl - tot, pos = incl_a - act;
+    const int na = __builtin_amdgcn_readlane(incl_a, 63);
+    wave_sync();
+#pragma unroll
+    for (int i = 0; i < NPL; i++) {
+        const int e = lane * NPL + i;
+        if (e < X) {
+            cnt[e] = st;                         /* cnt now holds start[e] */
+            a.S.start[e] = st;
+            if (c[i]) a.S.active[pos++] = e;
+            st += c[i];
+        }
+    }
+    if (lane == 63) a.S.start[X] = incl;
+    for (int i = na + lane; i < X; i += 64) a.S.work[i] = make_int4(-1, 0, 0, 0);
+    if (lane == 0) a.S.meta[0] = na;
+    wave_sync();
+    const unsigned long long below = (1ULL << lane) - 1ULL;
+    for (int base = 0; base < NS; base += 64) {
+        const int i = base + lane;
+        const int e = i < NS ? a.S.sel[i] : -1;
+        unsigned long long same = __ballot(i < NS);
+        for (int bit = 0; bit < 9; bit++) {
+            const unsigned long long b = __ballot(i < NS && ((e >> bit) & 1));
+            same &= ((e >> bit) & 1) ? b : ~b;
+        }
+        int s = 0;
+        if (i < NS) s = cnt[e] + cur[e] + __popcll(same & below);
+        wave_sync();
+        if (i < NS) {
+            const int t = i / a.K, k = s - cnt[e];
+            a.S.slot_t[s] = t;
+            a.S.slot_of[i] = s;
+            if (k < 4) atomicOr(&tok[e], (t & 0xff) << (8 * k));
+            if ((same >> lane) == 1ULL) cur[e] += __popcll(same);   /* highest lane of the group */
+        }
+        wave_sync();
+    }
+    /* one work record per active expert: {expert, first slot, end slot, tokens of its first
+     * four slots (one byte each)} */
+    int wpos = incl_a - act;
+#pragma unroll
+    for (int i = 0; i < NPL; i++) {
+        const int e = lane * NPL + i;
+        if (e < X && c[i]) {
+            a.S.work[wpos] = make_int4(e, cnt[e], cnt[e] + cur[e], tok[e]);
+            wpos++;
+        }
+    }
+}
+
+/* Top-K of one token per block; a single-block launch (T == 1) also sorts the slots. */
+__global__ __launch_bounds__(256) void select_kernel(SelectArgs a, int do_dispatch)
+{
+    __shared__ double P[kMaxExperts];
+    __shared__ int part[2 * kMaxExperts];
+    __shared__ int selb[64];
+    __shared__ int tok[kMaxExperts];
+    const int t = blockIdx.x;
+    if (t < a.T) topk_token(a, t, P, part, selb);
+    if (!do_dispatch) return;
+    if (threadIdx.x < 64) dispatch_slots(a, part, part + kMaxExperts, tok);
+}
+
+__global__ __launch_bounds__(64) void dispatch_kernel(SelectArgs a)
+{
+    __shared__ int cnt[kMaxExperts], cur[kMaxExperts], tok[kMaxExperts];
+    dispatch_slots(a, cnt, cur, tok);
+}
+
+hipError_t launch_select(const Shape &s, const Scratch &S, int T, hipStream_t st)
+{
+    SelectArgs a;
+    a.X = s.X;
+    a.K = s.K;
+    a.T = T;
+    a.S = S;
+    hipLaunchKernelGGL(select_kernel, dim3(T), dim3(256), 0, st, a, T == 1 ? 1 : 0);
+    if (T > 1) hipLaunchKernelGGL(dispatch_kernel, dim3(1), dim3(64), 0, st, a);
     return hipGetLastError();
 }
 
@@ -305,23 +516,55 @@ struct RowAcc {
     float lo, hi, corr;
 };
 
-/* One pair of Q4_0 blocks (36 bytes at W, 4-byte aligned) against one token's pair record.
- * src/kernels.c:87-93 for blocks b and b+1, lanes k = p and p + 4. */
-__device__ __forceinline__ void q4_0_pair(const uint32_t *W, int p, const uint8_t *xp, RowAcc &r)
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+/* The words one lane needs from a pair of Q4_0 blocks (36 bytes at W, 4-byte aligned): its
+ * code dword of each block (bytes 4p..4p+3 of qs) and both scales. */
+struct Q4Pair {
+    uint32_t c0, c1;
+    uint32_t w0, w4;      /* d of block b in the low half of w0, d of b+1 in the high half of w4 */
+};
+
+__device__ __forceinline__ Q4Pair q4_0_load(const uint32_t *W, int p)
 {
-    const uint32_t w0 = W[0], w4 = W[4], wa = W[p], wb = W[p + 1], wc = W[5 + p];
-    const uint32_t c0 = __builtin_amdgcn_alignbyte(wb, wa, 2);
-    const float d0 = h2f(w0 & 0xffffu), d1 = h2f(w4 >> 16);
-    const uint4 xv = *(const uint4 *)(xp + 16 * p);
-    const float4 dv = *(const float4 *)(xp + 64);
-    const float m0 = d0 * dv.x;
-    r.lo = __builtin_fmaf((float)sdot4((int)(c0 & 0x0f0f0f0fu), (int)xv.x), m0, r.lo);
-    r.hi = __builtin_fmaf((float)sdot4((int)((c0 >> 4) & 0x0f0f0f0fu), (int)xv.y), m0, r.hi);
-    r.corr = __builtin_fmaf(d0, dv.y, r.corr);
-    const float m1 = d1 * dv.z;
-    r.lo = __builtin_fmaf((float)sdot4((int)(wc & 0x0f0f0f0fu), (int)xv.z), m1, r.lo);
-    r.hi = __builtin_fmaf((float)sdot4((int)((wc >> 4) & 0x0f0f0f0fu), (int)xv.w), m1, r.hi);
-    r.corr = __builtin_fmaf(d1, dv.w, r.corr);
+    const uint32_t wa = W[p], wb = W[p + 1];
+    Q4Pair r;
+    r.w0 = W[0];
+    r.w4 = W[4];
+    r.c0 = __builtin_amdgcn_alignbyte(wb, wa, 2);
+    r.c1 = W[5 + p];
+    return r;
+}
+
+/* One token's part of a pair record for lane p: its q dwords of both blocks and d/ds. */
+struct XPair {
+    u32x4 q;
+    f32x4 d;
+};
+
+__device__ __forceinline__ XPair x_load(const uint8_t *xp, int p)
+{
+    XPair r;
+    r.q = *(const u32x4 *)(xp + 16 * p);
+    r.d = *(const f32x4 *)(xp + 64);
+    return r;
+}
+
+/* src/kernels.c:87-93 for blocks b and b+1, reference lanes k = p (low nibbles) and p + 4. */
+__device__ __forceinline__ void q4_0_math(const Q4Pair &w, const XPair &x, RowAcc &r)
+{
+    const int s0 = sdot4((int)(w.c0 & 0x0f0f0f0fu), (int)x.q.x);
+    const int s1 = sdot4((int)((w.c0 >> 4) & 0x0f0f0f0fu), (int)x.q.y);
+    const int s2 = sdot4((int)(w.c1 & 0x0f0f0f0fu), (int)x.q.z);
+    const int s3 = sdot4((int)((w.c1 >> 4) & 0x0f0f0f0fu), (int)x.q.w);
+    const float d0 = h2f(w.w0 & 0xffffu), d1 = h2f(w.w4 >> 16);
+    const float m0 = mul_f16_f32<0>(w.w0, x.d.x), m1 = mul_f16_f32<1>(w.w4, x.d.z);
+    r.lo = __builtin_fmaf((float)s0, m0, r.lo);
+    r.hi = __builtin_fmaf((float)s1, m0, r.hi);
+    r.corr = __builtin_fmaf(d0, x.d.y, r.corr);
+    r.lo = __builtin_fmaf((float)s2, m1, r.lo);
+    r.hi = __builtin_fmaf((float)s3, m1, r.hi);
+    r.corr = __builtin_fmaf(d1, x.d.w, r.corr);
 }
 
 /* One Q6_K 32-block (index g of half h of the super-block at byte sb of the LDS tile)
@@ -366,79 +609,114 @@ __device__ __forceinline__ float quad_finish(const RowAcc &r, float scale)
 struct GateUpArgs {
     const uint8_t *gate, *up;
     uint64_t rb, eb;
-    int E, F, CB, wstride, debug;
+    int E, F, debug;
     Scratch S;
 };
 
-/* One block: expert active[blockIdx.y], gate rows and up rows r0 .. r0+31 (r0 = 32*blockIdx.x),
- * for every slot of that expert, NT slots per pass. Rows 0-31 of the tile are gate, 32-63 up.
- * Epilogue: a = silu(g)*u (src/model.c:989-997), then one 32-block of int8 activations. */
-template <int NT>
+/* Pairs of one row for NT tokens, loads batched B pairs at a time so their latencies overlap. */
+template <int NT, int B>
+__device__ __forceinline__ void q4_0_rows(const uint32_t *Wrow, int p, const uint8_t *x0, size_t xrec, int q0, int nq,
+                                          int nt, RowAcc *acc)
+{
+    int q = 0;
+    for (; q + B <= nq; q += B) {
+        Q4Pair w[B];
+        XPair x[B][NT];
+#pragma unroll
+        for (int u = 0; u < B; u++) {
+            w[u] = q4_0_load(Wrow + (q + u) * 9, p);
+#pragma unroll
+            for (int n = 0; n < NT; n++)
+                if (n < nt) x[u][n] = x_load(x0 + n * xrec + (size_t)(q0 + q + u) * kPairBytes, p);
+        }
+#pragma unroll
+        for (int u = 0; u < B; u++)
+#pragma unroll
+            for (int n = 0; n < NT; n++)
+                if (n < nt) q4_0_math(w[u], x[u][n], acc[n]);
+    }
+    for (; q < nq; q++) {
+        const Q4Pair w = q4_0_load(Wrow + q * 9, p);
+#pragma unroll
+        for (int n = 0; n < NT; n++)
+            if (n < nt) q4_0_math(w, x_load(x0 + n * xrec + (size_t)(q0 + q) * kPairBytes, p), acc[n]);
+    }
+}
+
+/* One block: expert work[blockIdx.y].x, gate rows and up rows r0 .. r0+31 (r0 = 32*blockIdx.x),
+ * for every slot of the expert, NT slots per pass. Wave w owns gate rows r0+8w .. r0+8w+7
+ * (quads 0-7) and the same up rows (quads 8-15) and loads exactly those rows: G chunks of CB
+ * blocks have all their loads in flight, each chunk goes through the wave's own LDS buffer,
+ * and waves synchronise only with themselves, so a wave whose bytes land early computes
+ * while others still wait. The slots' int8 input records are requested before the weights
+ * (waiting on them never waits on the weights). Epilogue: a = silu(g)*u
+ * (src/model.c:989-997), then one int8 32-block of activations. */
+template <int NT, int CB, int G>
 __global__ __launch_bounds__(256) void gateup_exact_kernel(GateUpArgs a)
 {
     extern __shared__ __align__(16) uint8_t smem[];
-    const int nbE = a.E >> 5, nP = nbE >> 1, CB = a.CB, WS = a.wstride;
-    const int nchunk = nbE / CB, spr = CB * 18 / 16, nslot = 64 * spr;
-    uint8_t *wbuf = smem;
-    uint8_t *xbuf = smem + 64 * WS;
+    constexpr int SPR = CB * 18 / 16;                 /* 16-byte slots per row per chunk      */
+    constexpr int NSL = 16 * SPR;                     /* slots of one wave's chunk            */
+    constexpr int SPT = (NSL + 63) / 64;              /* slots per lane per chunk             */
+    constexpr int WS = CB * 18 + ((SPR & 1) ? 0 : 16);/* LDS row stride, odd in 16-byte units */
+    const int nbE = a.E >> 5, nP = nbE >> 1, nchunk = nbE / CB;
+    const int xsl = nP * 6;                           /* 16-byte slots of one token's records */
+    constexpr int XS = (NT * (4096 / 64) * 6 + 255) / 256;  /* x slots per thread (E <= 4096) */
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, qd = lane >> 2, p = lane & 3;
+    uint8_t *wbuf = smem + wave * 16 * WS;
+    uint8_t *xbuf = smem + 4 * 16 * WS;
     float *res = (float *)(xbuf + NT * nP * kPairBytes);
     int8_t *qb = (int8_t *)(res + NT * 64);
 
-    const int ai = blockIdx.y;
-    if (ai >= a.S.meta[0]) return;
-    const int e = a.S.active[ai];
-    const int s_begin = a.S.start[e], s_end = a.S.start[e + 1];
-    const int r0 = (int)blockIdx.x * 32;
-    const int tid = threadIdx.x, rho = tid >> 2, p = tid & 3;
-    const uint8_t *gbase = a.gate + (size_t)e * a.eb, *ubase = a.up + (size_t)e * a.eb;
+    const int4 wk = a.S.work[blockIdx.y];
+    if (wk.x < 0) return;
+    const int e = wk.x, s_begin = wk.y, s_end = wk.z;
+    const int r0 = (int)blockIdx.x * 32, rw = r0 + 8 * wave;     /* this wave's first row */
+    const uint8_t *gbase = a.gate + (size_t)e * a.eb + (size_t)rw * a.rb;
+    const uint8_t *ubase = a.up + (size_t)e * a.eb + (size_t)rw * a.rb;
     const int F = a.F, nbF = F >> 5;
+    const int rho = qd < 8 ? 8 * wave + qd : 32 + 8 * wave + (qd - 8);   /* tile row of this quad */
 
     for (int g0 = s_begin; g0 < s_end; g0 += NT) {
         const int nt = min(NT, s_end - g0);
-        for (int i = tid; i < nt * nP * 6; i += 256) {
-            const int n = i / (nP * 6), off = i - n * nP * 6;
-            const int tok = a.S.slot_t[g0 + n];
-            ((uint4 *)xbuf)[n * nP * 6 + off] = ((const uint4 *)(a.S.xqk + (size_t)tok * nP * kPairBytes))[off];
+        /* the nt slots' input records (tokens of the first four slots ride in work.w) */
+        u32x4 xv[XS];
+#pragma unroll
+        for (int m = 0; m < XS; m++) {
+            const int i = min(tid + 256 * m, nt * xsl - 1), n = i / xsl, off = i - n * xsl;
+            const int k = g0 - s_begin + n;
+            const int tok = k < 4 ? (wk.w >> (8 * k)) & 0xff : a.S.slot_t[g0 + n];
+            xv[m] = ((const u32x4 *)(a.S.xqk + (size_t)tok * nP * kPairBytes))[off];
         }
         RowAcc acc[NT];
         for (int n = 0; n < NT; n++) acc[n] = RowAcc{ 0.0f, 0.0f, 0.0f };
-        /* register double buffer: nine 16-byte slots per thread cover a 64 x 576-byte chunk */
-        uint4 p0, p1, p2, p3, p4, p5, p6, p7, p8;
-#define QMSG_SLOT_SRC(m, c)                                                                         \
-    ({                                                                                              \
-        const int i_ = min(tid + 256 * (m), nslot - 1);                                             \
-        const int row_ = i_ / spr, j_ = i_ - row_ * spr;                                            \
-        (const uint4 *)((row_ < 32 ? gbase + (size_t)(r0 + row_) * a.rb                              \
-                                   : ubase + (size_t)(r0 + row_ - 32) * a.rb) +                      \
-                        (size_t)(c) * CB * 18 + 16 * j_);                                           \
-    })
-#define QMSG_SLOT_DST(m)                                                                            \
-    ({                                                                                              \
-        const int i_ = min(tid + 256 * (m), nslot - 1);                                             \
-        const int row_ = i_ / spr, j_ = i_ - row_ * spr;                                            \
-        (uint4 *)(wbuf + row_ * WS + 16 * j_);                                                      \
-    })
-#define QMSG_LOAD_ALL(c)                                                                            \
-    p0 = *QMSG_SLOT_SRC(0, c); p1 = *QMSG_SLOT_SRC(1, c); p2 = *QMSG_SLOT_SRC(2, c);                \
-    p3 = *QMSG_SLOT_SRC(3, c); p4 = *QMSG_SLOT_SRC(4, c); p5 = *QMSG_SLOT_SRC(5, c);                \
-    p6 = *QMSG_SLOT_SRC(6, c); p7 = *QMSG_SLOT_SRC(7, c); p8 = *QMSG_SLOT_SRC(8, c);
-        QMSG_LOAD_ALL(0)
-        for (int c = 0; c < nchunk; c++) {
-            __syncthreads();
-            *QMSG_SLOT_DST(0) = p0; *QMSG_SLOT_DST(1) = p1; *QMSG_SLOT_DST(2) = p2;
-            *QMSG_SLOT_DST(3) = p3; *QMSG_SLOT_DST(4) = p4; *QMSG_SLOT_DST(5) = p5;
-            *QMSG_SLOT_DST(6) = p6; *QMSG_SLOT_DST(7) = p7; *QMSG_SLOT_DST(8) = p8;
-            __syncthreads();
-            if (c + 1 < nchunk) { QMSG_LOAD_ALL(c + 1) }
-#undef QMSG_LOAD_ALL
-#undef QMSG_SLOT_DST
-#undef QMSG_SLOT_SRC
-            const uint32_t *Wrow = (const uint32_t *)(wbuf + rho * WS);
-            for (int q = 0; q < CB / 2; q++) {
-                const int gp = c * (CB / 2) + q;
+        for (int cg = 0; cg < nchunk; cg += G) {
+            u32x4 wv[G][SPT];
 #pragma unroll
-                for (int n = 0; n < NT; n++)
-                    if (n < nt) q4_0_pair(Wrow + q * 9, p, xbuf + (size_t)(n * nP + gp) * kPairBytes, acc[n]);
+            for (int c = 0; c < G; c++)
+#pragma unroll
+                for (int m = 0; m < SPT; m++) {
+                    const int i = min(lane + 64 * m, NSL - 1), row = i / SPR, j = i - row * SPR;
+                    wv[c][m] = *(const u32x4 *)((row < 8 ? gbase + (size_t)row * a.rb : ubase + (size_t)(row - 8) * a.rb) +
+                                                (size_t)(cg + c) * CB * 18 + 16 * j);
+                }
+            if (cg == 0) {
+#pragma unroll
+                for (int m = 0; m < XS; m++) ((u32x4 *)xbuf)[min(tid + 256 * m, nt * xsl - 1)] = xv[m];
+                __syncthreads();
+            }
+#pragma unroll
+            for (int c = 0; c < G; c++) {
+                wave_sync();
+#pragma unroll
+                for (int m = 0; m < SPT; m++) {
+                    const int i = min(lane + 64 * m, NSL - 1), row = i / SPR, j = i - row * SPR;
+                    *(u32x4 *)(wbuf + row * WS + 16 * j) = wv[c][m];
+                }
+                wave_sync();
+                q4_0_rows<NT, (NT >= 4 ? 1 : (NT == 2 ? 2 : 4))>((const uint32_t *)(wbuf + qd * WS), p, xbuf,
+                                                                  (size_t)nP * kPairBytes, (cg + c) * (CB / 2), CB / 2,
+                                                                  nt, acc);
             }
         }
 #pragma unroll
@@ -469,9 +747,7 @@ __global__ __launch_bounds__(256) void gateup_exact_kernel(GateUpArgs a)
             for (int o = 8; o > 0; o >>= 1) sum += __shfl_xor(sum, o, 16);   /* lanes 0-15, 16-31 */
             const int s0 = __shfl(sum, 0), s1 = __shfl(sum, 16);
             if (l < 32) qb[n * 32 + l] = (int8_t)qi;
-            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-            __builtin_amdgcn_wave_barrier();
-            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+            wave_sync();
             const float ds = d * (float)(s0 + s1);
             const uint32_t s16 = (uint32_t)(uint16_t)(int16_t)s0 | ((uint32_t)(uint16_t)(int16_t)s1 << 16);
             const uint32_t *qw = (const uint32_t *)(qb + n * 32);
@@ -496,6 +772,16 @@ __global__ __launch_bounds__(256) void gateup_exact_kernel(GateUpArgs a)
     }
 }
 
+template <int NT>
+static void launch_gateup_nt(const GateUpArgs &a, int CB, int G, dim3 grid, size_t lds, hipStream_t st)
+{
+    if (CB == 32 && G == 4) hipLaunchKernelGGL((gateup_exact_kernel<NT, 32, 4>), grid, dim3(256), lds, st, a);
+    else if (CB == 32 && G == 2) hipLaunchKernelGGL((gateup_exact_kernel<NT, 32, 2>), grid, dim3(256), lds, st, a);
+    else if (CB == 32) hipLaunchKernelGGL((gateup_exact_kernel<NT, 32, 1>), grid, dim3(256), lds, st, a);
+    else if (CB == 16) hipLaunchKernelGGL((gateup_exact_kernel<NT, 16, 1>), grid, dim3(256), lds, st, a);
+    else hipLaunchKernelGGL((gateup_exact_kernel<NT, 8, 1>), grid, dim3(256), lds, st, a);
+}
+
 hipError_t launch_gateup_exact(const Shape &s, const LayerDev &L, const Scratch &S, int T, int debug, hipStream_t st)
 {
     GateUpArgs a;
@@ -505,20 +791,22 @@ hipError_t launch_gateup_exact(const Shape &s, const LayerDev &L, const Scratch 
     a.eb = L.gate_eb;
     a.E = s.E;
     a.F = s.F;
-    const int nbE = s.E / 32;
-    a.CB = nbE % 32 == 0 ? 32 : (nbE % 16 == 0 ? 16 : 8);
-    const int spr = a.CB * 18 / 16;
-    a.wstride = a.CB * 18 + ((spr & 1) ? 0 : 16);
     a.debug = debug;
     a.S = S;
-    const int nP = nbE / 2;
+    const int nbE = s.E / 32, nP = nbE / 2;
+    const int CB = nbE % 32 == 0 ? 32 : (nbE % 16 == 0 ? 16 : 8);
+    const int nchunk = nbE / CB;
+    const int NT = T >= 4 ? 4 : (T >= 2 ? 2 : 1);
+    /* chunks with loads in flight at once: as many as the registers allow at this NT */
+    const int G = CB != 32 ? 1 : (NT == 1 && nchunk % 4 == 0 ? 4 : (nchunk % 2 == 0 ? 2 : 1));
+    const int spr = CB * 18 / 16;
+    const int ws = CB * 18 + ((spr & 1) ? 0 : 16);
     const int maxact = s.X < T * s.K ? s.X : T * s.K;
     dim3 grid(s.F / 32, maxact);
-    const int NT = T >= 4 ? 4 : (T >= 2 ? 2 : 1);
-    const size_t lds = (size_t)64 * a.wstride + (size_t)NT * nP * kPairBytes + (size_t)NT * 64 * 4 + NT * 32;
-    if (NT == 4) hipLaunchKernelGGL(gateup_exact_kernel<4>, grid, dim3(256), lds, st, a);
-    else if (NT == 2) hipLaunchKernelGGL(gateup_exact_kernel<2>, grid, dim3(256), lds, st, a);
-    else hipLaunchKernelGGL(gateup_exact_kernel<1>, grid, dim3(256), lds, st, a);
+    const size_t lds = (size_t)64 * ws + (size_t)NT * nP * kPairBytes + (size_t)NT * 64 * 4 + NT * 32;
+    if (NT == 4) launch_gateup_nt<4>(a, CB, G, grid, lds, st);
+    else if (NT == 2) launch_gateup_nt<2>(a, CB, G, grid, lds, st);
+    else launch_gateup_nt<1>(a, CB, G, grid, lds, st);
     return hipGetLastError();
 }
 
@@ -527,101 +815,134 @@ hipError_t launch_gateup_exact(const Shape &s, const LayerDev &L, const Scratch 
 struct DownArgs {
     const uint8_t *down;
     uint64_t rb, eb;
-    int E, F, K, T, type;
+    int E, F, K, T, X;
+    int fuse;          /* 1: combine inside the block (dn of all slots fits in LDS) */
+    int lds_slots;     /* slots of a round whose int8 activations are staged in LDS */
     float *out;
     Scratch S;
 };
 
-/* One block: expert active[blockIdx.y], down rows r0 .. r0+ROWS-1 (one contiguous byte range,
- * staged whole into LDS), for every slot of that expert; dn[s][r] to HBM. The last block to
- * finish a row tile forms out[t][r] = sum_j wt[t][j] * dn[slot_of[t][j]][r] in selection
- * order (src/model.c:1152-1162). */
-template <int TYPE, int ROWS, int NT>
-__global__ __launch_bounds__(4 * ROWS) void down_exact_kernel(DownArgs a)
+/* One block: down rows r0 .. r0+RD-1 (RD = 8) of every active expert. Items (expert, row)
+ * are taken 64 at a time, one per lane quad; each round's 8 experts x 8 rows (8 contiguous
+ * byte ranges) are staged whole into LDS, the next round's loads in flight during the
+ * current round's dots. Each item writes dn[s][r] for every slot s of its expert. With
+ * `fuse`, the block then forms out[t][r] = sum_j wt[t][j] * dn[slot_of[t][j]][r] in selection
+ * order (src/model.c:1152-1162) from LDS copies of its own rows. */
+template <int TYPE, int NT>
+__global__ __launch_bounds__(256) void down_exact_kernel(DownArgs a)
 {
     extern __shared__ __align__(16) uint8_t smem[];
-    constexpr int NTH = 4 * ROWS;
-    const int nbF = a.F >> 5, nPF = nbF >> 1, E = a.E;
-    const int tile_bytes = (int)(ROWS * a.rb);
+    constexpr int RD = 8, EPR = 8, MAXS = TYPE == 2 ? 14 : 20;   /* rows, experts per round, slots */
+    const int tid = threadIdx.x, quad = tid >> 2, p = tid & 3;
+    const int r0 = (int)blockIdx.x * RD, E = a.E, nPF = a.F >> 6, K = a.K;
+    const int rbytes = (int)(RD * a.rb);                 /* one expert's RD rows */
+    const int spe = rbytes / 16, nslot = EPR * spe;
+    const int xrec = nPF * kPairBytes;                   /* one slot's int8 activations */
     uint8_t *tile = smem;
-    uint8_t *xbuf = smem + ((tile_bytes + 16 + 15) & ~15);
-    __shared__ int flag;
-    const int tid = threadIdx.x, rho = tid >> 2, p = tid & 3;
-    const int ai = blockIdx.y, r0 = (int)blockIdx.x * ROWS;
-    const int n_active = a.S.meta[0];
-    if (ai >= n_active) return;
-    const int e = a.S.active[ai];
-    const int s_begin = a.S.start[e], s_end = a.S.start[e + 1];
-
-    const uint4 *src = (const uint4 *)(a.down + (size_t)e * a.eb + (size_t)r0 * a.rb);
-    for (int i = tid; i < tile_bytes / 16; i += NTH) ((uint4 *)tile)[i] = src[i];
-
-    for (int g0 = s_begin; g0 < s_end; g0 += NT) {
-        const int nt = min(NT, s_end - g0);
-        __syncthreads();
-        for (int i = tid; i < nt * nPF * 6; i += NTH) {
-            const int n = i / (nPF * 6), off = i - n * nPF * 6;
-            ((uint4 *)xbuf)[n * nPF * 6 + off] = ((const uint4 *)(a.S.aqk + (size_t)(g0 + n) * nPF * kPairBytes))[off];
-        }
-        __syncthreads();
-        RowAcc acc[NT];
-        for (int n = 0; n < NT; n++) acc[n] = RowAcc{ 0.0f, 0.0f, 0.0f };
-        if (TYPE == 2) {    /* Q4_0: pairs of 18-byte blocks, 36-byte aligned within the row */
-            const uint32_t *Wrow = (const uint32_t *)(tile + (size_t)rho * a.rb);
-            for (int q = 0; q < nPF; q++) {
-#pragma unroll
-                for (int n = 0; n < NT; n++)
-                    if (n < nt) q4_0_pair(Wrow + q * 9, p, xbuf + (size_t)(n * nPF + q) * kPairBytes, acc[n]);
-            }
-        } else {            /* Q6_K: 210-byte super-blocks of 8 blocks */
-            const int nsb = a.F >> 8;
-            for (int sbi = 0; sbi < nsb; sbi++) {
-                const uint32_t sb = (uint32_t)(rho * a.rb + sbi * 210);
-                for (int h = 0; h < 2; h++)
-                    for (int g = 0; g < 4; g++) {
-                        const int blk = sbi * 8 + h * 4 + g;
-#pragma unroll
-                        for (int n = 0; n < NT; n++)
-                            if (n < nt)
-                                q6_k_block(tile, sb, h, g, p, xbuf + (size_t)(n * nPF + (blk >> 1)) * kPairBytes,
-                                           blk & 1, acc[n]);
-                    }
-            }
-        }
-#pragma unroll
-        for (int n = 0; n < NT; n++) {
-            const float v = quad_finish(acc[n], TYPE == 2 ? 8.0f : 32.0f);
-            if (p == 0 && n < nt) a.S.dn[(size_t)(g0 + n) * E + r0 + rho] = v;
-        }
+    uint8_t *xbuf = smem + ((EPR * rbytes + 16 + 15) & ~15);        /* up to a.lds_slots slots */
+    float *dnl = (float *)(xbuf + (size_t)a.lds_slots * xrec);      /* [NS][RD] when fused */
+    u32x4 v[MAXS];
+    int rnd = 0;
+    /* round rnd covers active experts rnd*EPR .. rnd*EPR+7; work[] ends with expert -1 */
+#define QMSG_DLOAD(R)                                                                                \
+    _Pragma("unroll") for (int m = 0; m < MAXS; m++) {                                               \
+        const int i_ = min(tid + 256 * m, nslot - 1), k_ = i_ / spe, j_ = i_ - k_ * spe;             \
+        const int e_ = max(a.S.work[min((R) * EPR + k_, a.X - 1)].x, 0);                             \
+        v[m] = ((const u32x4 *)(a.down + (size_t)e_ * a.eb + (size_t)r0 * a.rb))[j_];                 \
     }
-    __threadfence();
+    QMSG_DLOAD(0)
+    for (;; rnd++) {
+        /* this round's experts and their (contiguous) slot range */
+        __shared__ int4 rw[EPR];
+        __shared__ int srange[2];
+        __syncthreads();
+        if (tid < EPR) {
+            const int ai = rnd * EPR + tid;
+            rw[tid] = ai < a.X ? a.S.work[ai] : make_int4(-1, 0, 0, 0);
+        }
+        __syncthreads();
+        if (rw[0].x < 0) break;
+        if (tid == 0) {
+            int hi = rw[0].z;
+            for (int k = 1; k < EPR; k++) if (rw[k].x >= 0) hi = rw[k].z;
+            srange[0] = rw[0].y;
+            srange[1] = hi;
+        }
+#pragma unroll
+        for (int m = 0; m < MAXS; m++) ((u32x4 *)tile)[min(tid + 256 * m, nslot - 1)] = v[m];
+        __syncthreads();
+        const int s_lo = srange[0], s_hi = srange[1];
+        const bool in_lds = s_hi - s_lo <= a.lds_slots;
+        if (in_lds)
+            for (int i = tid; i < (s_hi - s_lo) * (xrec >> 4); i += 256)
+                ((u32x4 *)xbuf)[i] = ((const u32x4 *)(a.S.aqk + (size_t)s_lo * xrec))[i];
+        const bool more = rnd * EPR + EPR < a.X && a.S.work[min(rnd * EPR + EPR, a.X - 1)].x >= 0;
+        if (more) { QMSG_DLOAD(rnd + 1) }
+        __syncthreads();
+        const int k = quad >> 3, rr = quad & 7;
+        const int4 w = rw[k];
+        if (w.x >= 0) {
+            const uint8_t *row = tile + k * rbytes + rr * (int)a.rb;
+            const uint8_t *xs = in_lds ? xbuf + (size_t)(w.y - s_lo) * xrec : a.S.aqk + (size_t)w.y * xrec;
+            for (int g0 = w.y; g0 < w.z; g0 += NT) {
+                const int nt = min(NT, w.z - g0);
+                RowAcc acc[NT];
+                for (int n = 0; n < NT; n++) acc[n] = RowAcc{ 0.0f, 0.0f, 0.0f };
+                const uint8_t *xg = xs + (size_t)(g0 - w.y) * xrec;
+                if (TYPE == 2) {
+                    q4_0_rows<NT, (NT >= 4 ? 1 : (NT == 2 ? 2 : 4))>((const uint32_t *)row, p, xg, (size_t)xrec, 0, nPF, nt, acc);
+                } else {
+                    const int nsb = a.F >> 8;
+                    const uint32_t rowoff = (uint32_t)(row - tile);
+                    for (int sbi = 0; sbi < nsb; sbi++) {
+                        const uint32_t sb = rowoff + (uint32_t)(sbi * 210);
+#pragma unroll
+                        for (int h = 0; h < 2; h++)
+#pragma unroll
+                            for (int g = 0; g < 4; g++) {
+                                const int blk = sbi * 8 + h * 4 + g;
+#pragma unroll
+                                for (int n = 0; n < NT; n++)
+                                    if (n < nt)
+                                        q6_k_block(tile, sb, h, g, p, xg + (size_t)n * xrec + (size_t)(blk >> 1) * kPairBytes,
+                                                   blk & 1, acc[n]);
+                            }
+                    }
+                }
+#pragma unroll
+                for (int n = 0; n < NT; n++) {
+                    const float d = quad_finish(acc[n], TYPE == 2 ? 8.0f : 32.0f);
+                    if (p == 0 && n < nt) {
+                        a.S.dn[(size_t)(g0 + n) * E + r0 + rr] = d;
+                        if (a.fuse) dnl[(g0 + n) * RD + rr] = d;
+                    }
+                }
+            }
+        }
+        if (!more) break;
+    }
+#undef QMSG_DLOAD
+    if (!a.fuse) return;
     __syncthreads();
-    if (tid == 0) flag = atomicAdd(&a.S.tile_cnt[blockIdx.x], 1) == n_active - 1;
-    __syncthreads();
-    if (!flag) return;
-    __threadfence();
-    const int K = a.K;
-    for (int i = tid; i < a.T * ROWS; i += NTH) {
-        const int t = i / ROWS, r = r0 + (i - t * ROWS);
+    for (int i = tid; i < a.T * RD; i += 256) {
+        const int t = i / RD, rr = i - t * RD;
         float o = 0.0f;
         for (int j = 0; j < K; j++)
-            o = __builtin_fmaf(a.S.wt[(size_t)t * K + j], a.S.dn[(size_t)a.S.slot_of[(size_t)t * K + j] * E + r], o);
-        a.out[(size_t)t * E + r] = o;
+            o = __builtin_fmaf(a.S.wt[(size_t)t * K + j], dnl[a.S.slot_of[(size_t)t * K + j] * RD + rr], o);
+        a.out[(size_t)t * E + r0 + rr] = o;
     }
-    if (tid == 0) a.S.tile_cnt[blockIdx.x] = 0;
 }
 
-template <int TYPE, int ROWS>
-static hipError_t launch_down_t(const DownArgs &a, dim3 grid, int T, hipStream_t st)
+/* Weighted sum per token in selection order (src/model.c:1152-1162) when dn did not fit. */
+__global__ void combine_kernel(const Scratch S, int E, int K, int T, float *out)
 {
-    const int nPF = a.F / 64;
-    const int tile_bytes = (int)(ROWS * a.rb);
-    const int NT = T >= 4 ? 4 : (T >= 2 ? 2 : 1);
-    const size_t lds = (size_t)((tile_bytes + 16 + 15) & ~15) + (size_t)NT * nPF * kPairBytes;
-    if (NT == 4) hipLaunchKernelGGL((down_exact_kernel<TYPE, ROWS, 4>), grid, dim3(4 * ROWS), lds, st, a);
-    else if (NT == 2) hipLaunchKernelGGL((down_exact_kernel<TYPE, ROWS, 2>), grid, dim3(4 * ROWS), lds, st, a);
-    else hipLaunchKernelGGL((down_exact_kernel<TYPE, ROWS, 1>), grid, dim3(4 * ROWS), lds, st, a);
-    return hipGetLastError();
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= T * E) return;
+    const int t = i / E, r = i - t * E;
+    float o = 0.0f;
+    for (int j = 0; j < K; j++)
+        o = __builtin_fmaf(S.wt[(size_t)t * K + j], S.dn[(size_t)S.slot_of[(size_t)t * K + j] * E + r], o);
+    out[i] = o;
 }
 
 hipError_t launch_down_exact(const Shape &s, const LayerDev &L, const Scratch &S, float *out, int T, hipStream_t st)
@@ -634,12 +955,31 @@ hipError_t launch_down_exact(const Shape &s, const LayerDev &L, const Scratch &S
     a.F = s.F;
     a.K = s.K;
     a.T = T;
-    a.type = L.down_type;
+    a.X = s.X;
     a.out = out;
     a.S = S;
-    const int maxact = s.X < T * s.K ? s.X : T * s.K;
-    if (L.down_type == 2) return launch_down_t<2, 64>(a, dim3(s.E / 64, maxact), T, st);
-    return launch_down_t<14, 32>(a, dim3(s.E / 32, maxact), T, st);
+    const size_t tile = ((size_t)8 * 8 * L.down_rb + 16 + 15) & ~(size_t)15;
+    const size_t dnl = (size_t)T * s.K * 8 * 4;
+    const size_t xrec = (size_t)(s.F / 64) * kPairBytes;
+    a.lds_slots = T * s.K < 16 ? T * s.K : 16;
+    a.fuse = tile + a.lds_slots * xrec + dnl <= 120 * 1024;
+    const size_t lds = tile + a.lds_slots * xrec + (a.fuse ? dnl : 0);
+    const int NT = T >= 4 ? 4 : (T >= 2 ? 2 : 1);
+    const dim3 grid(s.E / 8);
+    if (L.down_type == 2) {
+        if (NT == 4) hipLaunchKernelGGL((down_exact_kernel<2, 4>), grid, dim3(256), lds, st, a);
+        else if (NT == 2) hipLaunchKernelGGL((down_exact_kernel<2, 2>), grid, dim3(256), lds, st, a);
+        else hipLaunchKernelGGL((down_exact_kernel<2, 1>), grid, dim3(256), lds, st, a);
+    } else {
+        if (NT == 4) hipLaunchKernelGGL((down_exact_kernel<14, 4>), grid, dim3(256), lds, st, a);
+        else if (NT == 2) hipLaunchKernelGGL((down_exact_kernel<14, 2>), grid, dim3(256), lds, st, a);
+        else hipLaunchKernelGGL((down_exact_kernel<14, 1>), grid, dim3(256), lds, st, a);
+    }
+    if (!a.fuse) {
+        const int n = T * s.E;
+        hipLaunchKernelGGL(combine_kernel, dim3((n + 255) / 256), dim3(256), 0, st, S, s.E, s.K, T, out);
+    }
+    return hipGetLastError();
 }
 
 /* ------------------------------------------------------------------ block dots (checks) ---- */
@@ -690,6 +1030,21 @@ hipError_t launch_block_dots(const uint8_t *base, int type, uint64_t rb, uint64_
     if (n <= 0) return hipSuccess;
     hipLaunchKernelGGL(block_dots_kernel, dim3((n + 255) / 256), dim3(256), 0, st, base, type, rb, eb, n, expert, row,
                        block, xq, out);
+    return hipGetLastError();
+}
+
+/* ------------------------------------------------------------------ calibration copy ---- */
+
+__global__ void copy_kernel(uint4 *dst, const uint4 *src, size_t n)
+{
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
+        dst[i] = src[i];
+}
+
+hipError_t launch_copy(void *dst, const void *src, size_t bytes, hipStream_t st)
+{
+    const size_t n = bytes / 16;
+    hipLaunchKernelGGL(copy_kernel, dim3(4096), dim3(256), 0, st, (uint4 *)dst, (const uint4 *)src, n);
     return hipGetLastError();
 }
 
