@@ -171,6 +171,10 @@ int qmsg_moe_debug(qmsg_ctx *ctx, int layer, const float *xn, int T, float *out,
 int qmsg_block_dots(qmsg_ctx *ctx, int layer, int which, int n, const int32_t *expert, const int32_t *row,
                     const int32_t *block, const void *xq_blocks, int32_t *out);
 
+/* No reference counterpart: SiLU as the device kernels evaluate it, a/(1+expf(-a)) with the
+ * kernels' expf (src/model.c:424), on n host floats; for checking against the C library. */
+int qmsg_eval_silu(qmsg_ctx *ctx, const float *x, int n, float *out);
+
 /* Per-kernel timing with HIP events on the context's stream (off by default). While on,
  * every kernel launch of the context is bracketed by an event pair. */
 int qmsg_profile(qmsg_ctx *ctx, int enable);

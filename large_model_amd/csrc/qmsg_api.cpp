@@ -532,6 +532,24 @@ int qmsg_profile_read(qmsg_ctx *c, const char *name, int64_t *launches, double *
     return QMSG_OK;
 }
 
+int qmsg_eval_silu(qmsg_ctx *c, const float *x, int n, float *out)
+{
+    if (!c || n < 0 || (n && (!x || !out))) return QMSG_E_INVALID;
+    if (n == 0) return QMSG_OK;
+    HIP_TRY(c, hipSetDevice(c->device));
+    std::vector<void *> tmp;
+    float *d = nullptr;
+    int rc = dev_alloc(c, (void **)&d, (size_t)n * 8, tmp);
+    if (rc) return rc;
+    hipError_t e = hipMemcpy(d, x, (size_t)n * 4, hipMemcpyHostToDevice);
+    if (e == hipSuccess) e = launch_silu(d, n, d + n, c->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
+    if (e == hipSuccess) e = hipMemcpy(out, d + n, (size_t)n * 4, hipMemcpyDeviceToHost);
+    hipFree(d);
+    if (e != hipSuccess) return fail(c, QMSG_E_DEVICE, "qmsg_eval_silu: %s", hipGetErrorString(e));
+    return QMSG_OK;
+}
+
 int qmsg_calibrate_copy(qmsg_ctx *c, void *d_dst, const void *d_src, size_t bytes)
 {
     if (!c || !d_dst || !d_src || bytes % 16) return QMSG_E_INVALID;

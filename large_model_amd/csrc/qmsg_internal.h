@@ -76,6 +76,7 @@ hipError_t launch_synth_experts(uint64_t seed, uint32_t layer, uint32_t kind, in
                                 int64_t cols, int X, float sigma, uint8_t *base, hipStream_t st);
 hipError_t launch_rmsnorm_rows(float *x, int T, int E, float eps, hipStream_t st);
 hipError_t launch_set_col0(float *m, int rows, int stride, const float *vals, float fill, hipStream_t st);
+hipError_t launch_silu(const float *x, int n, float *out, hipStream_t st);
 hipError_t launch_copy(void *dst, const void *src, size_t bytes, hipStream_t st);
 hipError_t launch_block_dots(const uint8_t *base, int type, uint64_t rb, uint64_t eb, int n, const int32_t *expert,
                              const int32_t *row, const int32_t *block, const Q8 *xq, int32_t *out,

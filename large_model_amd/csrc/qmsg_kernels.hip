@@ -1033,6 +1033,21 @@ hipError_t launch_block_dots(const uint8_t *base, int type, uint64_t rb, uint64_
     return hipGetLastError();
 }
 
+/* ------------------------------------------------------------------ SiLU check ---- */
+
+__global__ void silu_kernel(const float *x, int n, float *out)
+{
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) out[i] = silu_ref(x[i]);
+}
+
+hipError_t launch_silu(const float *x, int n, float *out, hipStream_t st)
+{
+    if (n <= 0) return hipSuccess;
+    hipLaunchKernelGGL(silu_kernel, dim3((n + 255) / 256), dim3(256), 0, st, x, n, out);
+    return hipGetLastError();
+}
+
 /* ------------------------------------------------------------------ calibration copy ---- */
 
 __global__ void copy_kernel(uint4 *dst, const uint4 *src, size_t n)

@@ -122,6 +122,11 @@ void orc_quantize_q8(const float *x, int64_t n, orc_q8 *out)
 /* hsum256 (src/kernels.c:66-72): lanes j and j+4 first, then (s0+s2)+(s1+s3). */
 static inline float hsum8(const float a[8])
 {
+    if (orc_mutation == ORC_MUT_HSUM_LINEAR) {
+        float s = 0.0f;
+        for (int k = 0; k < 8; k++) s += a[k];
+        return s;
+    }
     const float s0 = a[0] + a[4], s1 = a[1] + a[5], s2 = a[2] + a[6], s3 = a[3] + a[7];
     return (s0 + s2) + (s1 + s3);
 }
@@ -151,7 +156,7 @@ static float dot_q4_0(const uint8_t *w, const orc_q8 *x, int64_t nb)
         for (int k = 0; k < 8; k++) acc[k] = fmaf((float)lane_q4(w + 2, x[b].q, k), dd, acc[k]);
         corr = orc_mutation == ORC_MUT_CORR_UNFUSED ? corr + d * x[b].ds : fmaf(d, x[b].ds, corr);
     }
-    if (orc_mutation == ORC_MUT_FUSED_TAIL) return fmaf(-8.0f, corr, hsum8(acc));
+    /* 8*corr is exact, so fusing this subtraction (as -ffp-contract=fast may) changes nothing */
     return hsum8(acc) - 8.0f * corr;
 }
 

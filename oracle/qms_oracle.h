@@ -58,7 +58,7 @@ typedef struct {
 /* Planted mistakes (orc_mutation): each one is a plausible slip the golden vectors must catch. */
 enum {
     ORC_MUT_NONE = 0,
-    ORC_MUT_FUSED_TAIL = 1,     /* hsum - 8*corr as one fma                         */
+    ORC_MUT_HSUM_LINEAR = 1,    /* the eight dot lanes summed left to right         */
     ORC_MUT_CORR_UNFUSED = 2,   /* offset chain as mul + add                        */
     ORC_MUT_NIBBLE_ORDER = 3,   /* interleaved instead of low-then-high nibbles     */
     ORC_MUT_ROUTER_TREE = 4,    /* router dot reduced left to right                 */
