@@ -118,6 +118,22 @@ def cpu_baseline(ctx, w, seconds: float):
     }
 
 
+def copy_calibration(nbytes: int, steps: int):
+    """A plain device copy of nbytes, `steps` times: the known transfer against which
+    rocprofv3's FETCH_SIZE / WRITE_SIZE readings are scaled."""
+    nbytes -= nbytes % 16
+    ctx = qmsg.Context(256, 16, 4, 128)
+    src, dst = ctx.device_alloc(nbytes), ctx.device_alloc(nbytes)
+    ctx.profile(True)
+    for _ in range(steps):
+        ctx.calibrate_copy(dst, src, nbytes)
+    ctx.sync()
+    n, ms = ctx.profile_read("copy")
+    ctx.close()
+    print(json.dumps({"copy_bytes": nbytes, "launches": n, "avg_us": round(1e3 * ms / n, 3),
+                      "GBps_read_plus_write": round(2 * nbytes * n / (ms * 1e-3) / 1e9, 1)}), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -128,6 +144,9 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--path", choices=["auto", "exact", "mfma"], default="auto")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES",
+                    help="instead of the layer, run the plain copy kernel on BYTES (reference transfer "
+                         "for HBM byte counters) --steps times and exit")
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -135,6 +154,10 @@ def main():
         print("bench.py measures one GPU: this build has no multi-GPU path (expert sharding is described in "
               "DESIGN.md, not built). Run with --gpus 1.", file=sys.stderr)
         sys.exit(2)
+
+    if args.copy_calibration:
+        copy_calibration(args.copy_calibration, args.steps)
+        return
 
     w = WORKLOADS[args.workload]
     K_steps, W_steps, NL = args.steps, args.warmup, max(1, args.layers)
@@ -167,13 +190,16 @@ def main():
     ms_step = 1e3 * el / K_steps
     log(f"timed {K_steps} steps: {ms_step * 1e3:.2f} us/step")
 
-    # the same steps again with HIP events around every kernel, on the library's stream
+    # the same steps again, every dispatch stamping its own start/end into HIP events
+    # (hipExtLaunchKernel on the library's stream)
     ctx.profile(True)
+    t0 = time.perf_counter()
     for s in range(W_steps, total):
         step(s)
     ctx.sync()
+    log(f"with per-dispatch events: {1e6 * (time.perf_counter() - t0) / K_steps:.2f} us/step")
     kern = {}
-    for name in ("route", "select", "gateup", "down"):
+    for name in ("route", "select", "dispatch", "gateup", "down", "combine"):
         n, ms = ctx.profile_read(name)
         if n:
             kern[name] = {"launches": n, "avg_us": round(1e3 * ms / n, 3)}

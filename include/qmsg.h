@@ -74,9 +74,9 @@ typedef struct qmsg_ctx qmsg_ctx;
 /* Which kernels run the expert products.
  *   EXACT: per-row fp32 FMA chains in the reference's lane order; every intermediate
  *          (int8 blocks, fp32 rows, outputs) is bit-identical to the reference's AVX path.
- *   MFMA:  int8 MFMA grouped GEMM; int32 block dots are exact, fp32 rows are summed per
- *          block in another order (outputs agree to ~1e-6 relative).
- *   AUTO:  EXACT up to the context's exact-token limit, MFMA above it. */
+ *   MFMA:  int8 MFMA grouped GEMM for prefill-sized batches; int32 block dots exact, fp32 rows
+ *          summed per block in another order. Not available yet: QMSG_E_UNSUPPORTED.
+ *   AUTO:  the best available path (EXACT today). */
 enum { QMSG_PATH_AUTO = 0, QMSG_PATH_EXACT = 1, QMSG_PATH_MFMA = 2 };
 
 /* ------------------------------------------------------------------ lifecycle ---- */
@@ -174,6 +174,9 @@ int qmsg_block_dots(qmsg_ctx *ctx, int layer, int which, int n, const int32_t *e
 /* No reference counterpart: SiLU as the device kernels evaluate it, a/(1+expf(-a)) with the
  * kernels' expf (src/model.c:424), on n host floats; for checking against the C library. */
 int qmsg_eval_silu(qmsg_ctx *ctx, const float *x, int n, float *out);
+/* No reference counterpart: exp in double as the routing softmax evaluates it on the device
+ * (src/model.c:1049), on n host doubles; for checking against the C library. */
+int qmsg_eval_exp(qmsg_ctx *ctx, const double *x, int n, double *out);
 
 /* Per-kernel timing with HIP events on the context's stream (off by default). While on,
  * every kernel launch of the context is bracketed by an event pair. */

@@ -88,33 +88,29 @@ static int dev_alloc(qmsg_ctx *c, void **p, size_t bytes, std::vector<void *> &l
     return QMSG_OK;
 }
 
-static void prof_begin(qmsg_ctx *c, const char *name, ProfRec &r)
+/* Timing hook: hands out an event pair per kernel dispatch while profiling is on. */
+static void prof_events(void *vc, const char *kernel, hipEvent_t *start, hipEvent_t *stop)
 {
-    if (!c->prof) return;
+    qmsg_ctx *c = (qmsg_ctx *)vc;
+    ProfRec r;
     if (!c->prof_free.empty()) {
         r = c->prof_free.back();
         c->prof_free.pop_back();
-    } else {
-        hipEventCreate(&r.a);
-        hipEventCreate(&r.b);
+    } else if (hipEventCreate(&r.a) != hipSuccess || hipEventCreate(&r.b) != hipSuccess) {
+        return;  /* no events: the launch goes untimed */
     }
-    r.name = name;
-    hipEventRecord(r.a, c->stream);
-}
-
-static void prof_end(qmsg_ctx *c, ProfRec &r)
-{
-    if (!c->prof) return;
-    hipEventRecord(r.b, c->stream);
+    r.name = kernel;
     c->prof_recs.push_back(r);
+    *start = r.a;
+    *stop = r.b;
 }
 
 #define LAUNCH(c, name, expr)                                                                             \
     do {                                                                                                  \
-        ProfRec pr_;                                                                                      \
-        prof_begin((c), (name), pr_);                                                                     \
+        const LaunchTimer timer_{ (c), prof_events };                                                     \
+        g_launch_timer = (c)->prof ? &timer_ : nullptr;                                                   \
         hipError_t e_ = (expr);                                                                           \
-        prof_end((c), pr_);                                                                               \
+        g_launch_timer = nullptr;                                                                         \
         if (e_ != hipSuccess) return fail((c), QMSG_E_DEVICE, "%s launch: %s", (name), hipGetErrorString(e_)); \
     } while (0)
 
@@ -208,6 +204,7 @@ int qmsg_set_path(qmsg_ctx *c, int path)
     if (!c) return QMSG_E_INVALID;
     if (path != QMSG_PATH_AUTO && path != QMSG_PATH_EXACT && path != QMSG_PATH_MFMA)
         return fail(c, QMSG_E_INVALID, "qmsg_set_path: unknown path %d", path);
+    if (path == QMSG_PATH_MFMA) return fail(c, QMSG_E_UNSUPPORTED, "qmsg_set_path: the MFMA path is not built");
     c->path = path;
     return QMSG_OK;
 }
@@ -532,22 +529,42 @@ int qmsg_profile_read(qmsg_ctx *c, const char *name, int64_t *launches, double *
     return QMSG_OK;
 }
 
-int qmsg_eval_silu(qmsg_ctx *c, const float *x, int n, float *out)
+}  /* extern "C" */
+
+/* Run one of the element-wise check kernels on n host values of `esz` bytes each. */
+template <class F>
+static int eval_elementwise(qmsg_ctx *c, const char *what, const void *x, int n, void *out, size_t esz, F launch)
 {
     if (!c || n < 0 || (n && (!x || !out))) return QMSG_E_INVALID;
     if (n == 0) return QMSG_OK;
     HIP_TRY(c, hipSetDevice(c->device));
     std::vector<void *> tmp;
-    float *d = nullptr;
-    int rc = dev_alloc(c, (void **)&d, (size_t)n * 8, tmp);
+    uint8_t *d = nullptr;
+    int rc = dev_alloc(c, (void **)&d, (size_t)n * esz * 2, tmp);
     if (rc) return rc;
-    hipError_t e = hipMemcpy(d, x, (size_t)n * 4, hipMemcpyHostToDevice);
-    if (e == hipSuccess) e = launch_silu(d, n, d + n, c->stream);
+    hipError_t e = hipMemcpy(d, x, (size_t)n * esz, hipMemcpyHostToDevice);
+    if (e == hipSuccess) e = launch(d, d + (size_t)n * esz);
     if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
-    if (e == hipSuccess) e = hipMemcpy(out, d + n, (size_t)n * 4, hipMemcpyDeviceToHost);
+    if (e == hipSuccess) e = hipMemcpy(out, d + (size_t)n * esz, (size_t)n * esz, hipMemcpyDeviceToHost);
     hipFree(d);
-    if (e != hipSuccess) return fail(c, QMSG_E_DEVICE, "qmsg_eval_silu: %s", hipGetErrorString(e));
+    if (e != hipSuccess) return fail(c, QMSG_E_DEVICE, "%s: %s", what, hipGetErrorString(e));
     return QMSG_OK;
+}
+
+extern "C" {
+
+int qmsg_eval_silu(qmsg_ctx *c, const float *x, int n, float *out)
+{
+    return eval_elementwise(c, "qmsg_eval_silu", x, n, out, 4, [&](uint8_t *in, uint8_t *o) {
+        return launch_silu((const float *)in, n, (float *)o, c->stream);
+    });
+}
+
+int qmsg_eval_exp(qmsg_ctx *c, const double *x, int n, double *out)
+{
+    return eval_elementwise(c, "qmsg_eval_exp", x, n, out, 8, [&](uint8_t *in, uint8_t *o) {
+        return launch_exp((const double *)in, n, (double *)o, c->stream);
+    });
 }
 
 int qmsg_calibrate_copy(qmsg_ctx *c, void *d_dst, const void *d_src, size_t bytes)

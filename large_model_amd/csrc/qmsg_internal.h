@@ -25,6 +25,17 @@ static_assert(sizeof(Q8) == 44, "QmsQ8 is 44 bytes");
  *   [88 .. 95]       zero */
 constexpr int kPairBytes = 96;
 
+/* Optional per-dispatch timing. While a hook is installed on the calling thread, every kernel
+ * launch of the library asks it for an event pair and launches through hipExtLaunchKernel,
+ * which stamps the dispatch's own start and end into the events (no marker packets between
+ * kernels). `kernel` is the launch's short name: route, select, dispatch, gateup, down,
+ * combine, copy. */
+struct LaunchTimer {
+    void *ctx;
+    void (*events)(void *ctx, const char *kernel, hipEvent_t *start, hipEvent_t *stop);
+};
+extern thread_local const LaunchTimer *g_launch_timer;
+
 /* Static shape limits of the kernels. */
 constexpr int kMaxExperts = 256;
 
@@ -77,6 +88,7 @@ hipError_t launch_synth_experts(uint64_t seed, uint32_t layer, uint32_t kind, in
 hipError_t launch_rmsnorm_rows(float *x, int T, int E, float eps, hipStream_t st);
 hipError_t launch_set_col0(float *m, int rows, int stride, const float *vals, float fill, hipStream_t st);
 hipError_t launch_silu(const float *x, int n, float *out, hipStream_t st);
+hipError_t launch_exp(const double *x, int n, double *out, hipStream_t st);
 hipError_t launch_copy(void *dst, const void *src, size_t bytes, hipStream_t st);
 hipError_t launch_block_dots(const uint8_t *base, int type, uint64_t rb, uint64_t eb, int n, const int32_t *expert,
                              const int32_t *row, const int32_t *block, const Q8 *xq, int32_t *out,

@@ -15,9 +15,27 @@
  * activations sit in LDS in a pair-of-blocks layout so a lane gets its two code partners
  * with one 16-byte read. */
 #include <hip/hip_runtime.h>
+#include <hip/hip_ext.h>
 
 #include "qmsg_internal.h"
+#include "qmsg_libm.h"
 #include "qmsg_synth.h"
+
+namespace qmsg {
+thread_local const LaunchTimer *g_launch_timer = nullptr;
+}
+
+/* Launch `kern` on `st`; with a timing hook installed the dispatch stamps its own events. */
+#define QLAUNCH(name, kern, grid, block, lds, st, ...)                                          \
+    do {                                                                                       \
+        hipEvent_t qa_ = nullptr, qb_ = nullptr;                                               \
+        if (qmsg::g_launch_timer)                                                              \
+            qmsg::g_launch_timer->events(qmsg::g_launch_timer->ctx, (name), &qa_, &qb_);       \
+        if (qa_)                                                                               \
+            hipExtLaunchKernelGGL(kern, (grid), (block), (lds), (st), qa_, qb_, 0u, __VA_ARGS__); \
+        else                                                                                   \
+            hipLaunchKernelGGL(kern, (grid), (block), (lds), (st), __VA_ARGS__);              \
+    } while (0)
 
 namespace qmsg {
 
@@ -41,52 +59,8 @@ __device__ __forceinline__ float mul_f16_f32(uint32_t h, float f)
     return r;
 }
 
-/* 2^(i/32) rounded to double, minus i << 47 (the exponent part added back at use). */
-__device__ const uint64_t kExp2fTab[32] = {
-    0x3ff0000000000000ULL, 0x3fefd9b0d3158574ULL, 0x3fefb5586cf9890fULL, 0x3fef9301d0125b51ULL,
-    0x3fef72b83c7d517bULL, 0x3fef54873168b9aaULL, 0x3fef387a6e756238ULL, 0x3fef1e9df51fdee1ULL,
-    0x3fef06fe0a31b715ULL, 0x3feef1a7373aa9cbULL, 0x3feedea64c123422ULL, 0x3feece086061892dULL,
-    0x3feebfdad5362a27ULL, 0x3feeb42b569d4f82ULL, 0x3feeab07dd485429ULL, 0x3feea47eb03a5585ULL,
-    0x3feea09e667f3bcdULL, 0x3fee9f75e8ec5f74ULL, 0x3feea11473eb0187ULL, 0x3feea589994cce13ULL,
-    0x3feeace5422aa0dbULL, 0x3feeb737b0cdc5e5ULL, 0x3feec49182a3f090ULL, 0x3feed503b23e255dULL,
-    0x3feee89f995ad3adULL, 0x3feeff76f2fb5e47ULL, 0x3fef199bdd85529cULL, 0x3fef3720dcef9069ULL,
-    0x3fef5818dcfba487ULL, 0x3fef7c97337b9b5fULL, 0x3fefa4afa2a490daULL, 0x3fefd0765b6e4540ULL
-};
-
-/* expf with the same result bits as the host C library the reference links (glibc 2.35's
- * FMA variant on x86-64, which implements the ARM optimized-routines method: x*32/ln2 =
- * k + r with round-to-nearest via a 1.5*2^52 shift, 2^(k/32) from the table above, a cubic
- * in r, everything in double, one final rounding to float). Checked on all 2^32 inputs. */
-__device__ __forceinline__ float expf_ref(float x)
-{
-    const uint32_t ux = __float_as_uint(x);
-    const uint32_t abstop = (ux >> 20) & 0x7ffu;
-    if (abstop >= 0x42bu) {                     /* |x| >= 88, inf or nan */
-        if (ux == 0xff800000u) return 0.0f;
-        if (abstop >= 0x7f8u) return x + x;
-        if (x > 0x1.62e42ep6f) return __builtin_inff();
-        if (x < -0x1.9fe368p6f) return 0.0f;
-    }
-    const double InvLn2N = 0x1.71547652b82fep+0 * 32.0, Shift = 0x1.8p+52;
-    const double C0 = 0x1.c6af84b912394p-5 / 32768.0, C1 = 0x1.ebfce50fac4f3p-3 / 1024.0,
-                 C2 = 0x1.62e42ff0c52d6p-1 / 32.0;
-    const double xd = (double)x;
-    double kd = __builtin_fma(InvLn2N, xd, Shift);
-    const uint64_t ki = (uint64_t)__double_as_longlong(kd);
-    kd -= Shift;
-    const double r = __builtin_fma(InvLn2N, xd, -kd);
-    const uint64_t t = kExp2fTab[ki & 31u] + (ki << 47);
-    const double s = __longlong_as_double((long long)t);
-    const double z = __builtin_fma(C0, r, C1);
-    const double r2 = r * r;
-    double y = __builtin_fma(C2, r, 1.0);
-    y = __builtin_fma(z, r2, y);
-    y = y * s;
-    return (float)y;
-}
-
 /* src/model.c:424 */
-__device__ __forceinline__ float silu_ref(float a) { return a / (1.0f + expf_ref(-a)); }
+__device__ __forceinline__ float silu_ref(float a) { return a / (1.0f + qmsg_expf(-a)); }
 
 /* An unaligned 32-bit read from LDS at an even byte address (two aligned reads). */
 __device__ __forceinline__ uint32_t lds_u32(const uint8_t *base, uint32_t a)
@@ -319,11 +293,11 @@ hipError_t launch_route(const Shape &s, const LayerDev &L, const Scratch &S, con
     if (T <= 4) {
         a.n_route_wg = s.X;
         const size_t lds = (size_t)(s.E + T * (s.E + 16)) * 4;
-        hipLaunchKernelGGL(route_small_kernel, dim3(a.n_route_wg + nq), dim3(256), lds, st, a);
+        QLAUNCH("route", route_small_kernel, dim3(a.n_route_wg + nq), dim3(256), lds, st, a);
     } else {
         a.n_route_wg = ((T + 15) / 16) * (s.X / 16);
         const size_t lds = (size_t)2 * 16 * (256 + 4) * 4;
-        hipLaunchKernelGGL(route_big_kernel, dim3(a.n_route_wg + nq), dim3(256), lds, st, a);
+        QLAUNCH("route", route_big_kernel, dim3(a.n_route_wg + nq), dim3(256), lds, st, a);
     }
     return hipGetLastError();
 }
@@ -360,7 +334,7 @@ __device__ void topk_token(const SelectArgs &a, int t, double *P, int *part, int
     if ((tid & 63) == 0) red[tid >> 6] = mx;
     __syncthreads();
     mx = fmax(fmax(red[0], red[1]), fmax(red[2], red[3]));
-    for (int e = tid; e < X; e += 256) P[e] = exp(P[e] - mx);
+    for (int e = tid; e < X; e += 256) P[e] = qmsg_exp(P[e] - mx);
     __syncthreads();
     if (tid == 0) {
         double z = 0.0;
@@ -503,8 +477,8 @@ hipError_t launch_select(const Shape &s, const Scratch &S, int T, hipStream_t st
     a.K = s.K;
     a.T = T;
     a.S = S;
-    hipLaunchKernelGGL(select_kernel, dim3(T), dim3(256), 0, st, a, T == 1 ? 1 : 0);
-    if (T > 1) hipLaunchKernelGGL(dispatch_kernel, dim3(1), dim3(64), 0, st, a);
+    QLAUNCH("select", select_kernel, dim3(T), dim3(256), 0, st, a, T == 1 ? 1 : 0);
+    if (T > 1) QLAUNCH("dispatch", dispatch_kernel, dim3(1), dim3(64), 0, st, a);
     return hipGetLastError();
 }
 
@@ -775,11 +749,11 @@ __global__ __launch_bounds__(256) void gateup_exact_kernel(GateUpArgs a)
 template <int NT>
 static void launch_gateup_nt(const GateUpArgs &a, int CB, int G, dim3 grid, size_t lds, hipStream_t st)
 {
-    if (CB == 32 && G == 4) hipLaunchKernelGGL((gateup_exact_kernel<NT, 32, 4>), grid, dim3(256), lds, st, a);
-    else if (CB == 32 && G == 2) hipLaunchKernelGGL((gateup_exact_kernel<NT, 32, 2>), grid, dim3(256), lds, st, a);
-    else if (CB == 32) hipLaunchKernelGGL((gateup_exact_kernel<NT, 32, 1>), grid, dim3(256), lds, st, a);
-    else if (CB == 16) hipLaunchKernelGGL((gateup_exact_kernel<NT, 16, 1>), grid, dim3(256), lds, st, a);
-    else hipLaunchKernelGGL((gateup_exact_kernel<NT, 8, 1>), grid, dim3(256), lds, st, a);
+    if (CB == 32 && G == 4) QLAUNCH("gateup", (gateup_exact_kernel<NT, 32, 4>), grid, dim3(256), lds, st, a);
+    else if (CB == 32 && G == 2) QLAUNCH("gateup", (gateup_exact_kernel<NT, 32, 2>), grid, dim3(256), lds, st, a);
+    else if (CB == 32) QLAUNCH("gateup", (gateup_exact_kernel<NT, 32, 1>), grid, dim3(256), lds, st, a);
+    else if (CB == 16) QLAUNCH("gateup", (gateup_exact_kernel<NT, 16, 1>), grid, dim3(256), lds, st, a);
+    else QLAUNCH("gateup", (gateup_exact_kernel<NT, 8, 1>), grid, dim3(256), lds, st, a);
 }
 
 hipError_t launch_gateup_exact(const Shape &s, const LayerDev &L, const Scratch &S, int T, int debug, hipStream_t st)
@@ -967,17 +941,17 @@ hipError_t launch_down_exact(const Shape &s, const LayerDev &L, const Scratch &S
     const int NT = T >= 4 ? 4 : (T >= 2 ? 2 : 1);
     const dim3 grid(s.E / 8);
     if (L.down_type == 2) {
-        if (NT == 4) hipLaunchKernelGGL((down_exact_kernel<2, 4>), grid, dim3(256), lds, st, a);
-        else if (NT == 2) hipLaunchKernelGGL((down_exact_kernel<2, 2>), grid, dim3(256), lds, st, a);
-        else hipLaunchKernelGGL((down_exact_kernel<2, 1>), grid, dim3(256), lds, st, a);
+        if (NT == 4) QLAUNCH("down", (down_exact_kernel<2, 4>), grid, dim3(256), lds, st, a);
+        else if (NT == 2) QLAUNCH("down", (down_exact_kernel<2, 2>), grid, dim3(256), lds, st, a);
+        else QLAUNCH("down", (down_exact_kernel<2, 1>), grid, dim3(256), lds, st, a);
     } else {
-        if (NT == 4) hipLaunchKernelGGL((down_exact_kernel<14, 4>), grid, dim3(256), lds, st, a);
-        else if (NT == 2) hipLaunchKernelGGL((down_exact_kernel<14, 2>), grid, dim3(256), lds, st, a);
-        else hipLaunchKernelGGL((down_exact_kernel<14, 1>), grid, dim3(256), lds, st, a);
+        if (NT == 4) QLAUNCH("down", (down_exact_kernel<14, 4>), grid, dim3(256), lds, st, a);
+        else if (NT == 2) QLAUNCH("down", (down_exact_kernel<14, 2>), grid, dim3(256), lds, st, a);
+        else QLAUNCH("down", (down_exact_kernel<14, 1>), grid, dim3(256), lds, st, a);
     }
     if (!a.fuse) {
         const int n = T * s.E;
-        hipLaunchKernelGGL(combine_kernel, dim3((n + 255) / 256), dim3(256), 0, st, S, s.E, s.K, T, out);
+        QLAUNCH("combine", combine_kernel, dim3((n + 255) / 256), dim3(256), 0, st, S, s.E, s.K, T, out);
     }
     return hipGetLastError();
 }
@@ -1041,6 +1015,19 @@ __global__ void silu_kernel(const float *x, int n, float *out)
     if (i < n) out[i] = silu_ref(x[i]);
 }
 
+__global__ void exp_kernel(const double *x, int n, double *out)
+{
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) out[i] = qmsg_exp(x[i]);
+}
+
+hipError_t launch_exp(const double *x, int n, double *out, hipStream_t st)
+{
+    if (n <= 0) return hipSuccess;
+    hipLaunchKernelGGL(exp_kernel, dim3((n + 255) / 256), dim3(256), 0, st, x, n, out);
+    return hipGetLastError();
+}
+
 hipError_t launch_silu(const float *x, int n, float *out, hipStream_t st)
 {
     if (n <= 0) return hipSuccess;
@@ -1059,7 +1046,7 @@ __global__ void copy_kernel(uint4 *dst, const uint4 *src, size_t n)
 hipError_t launch_copy(void *dst, const void *src, size_t bytes, hipStream_t st)
 {
     const size_t n = bytes / 16;
-    hipLaunchKernelGGL(copy_kernel, dim3(4096), dim3(256), 0, st, (uint4 *)dst, (const uint4 *)src, n);
+    QLAUNCH("copy", copy_kernel, dim3(4096), dim3(256), 0, st, (uint4 *)dst, (const uint4 *)src, n);
     return hipGetLastError();
 }
 

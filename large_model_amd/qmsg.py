@@ -94,6 +94,7 @@ _SIGS = {
     "qmsg_profile_read": (_I, [_P, ctypes.c_char_p, ctypes.POINTER(ctypes.c_int64),
                                ctypes.POINTER(ctypes.c_double)]),
     "qmsg_eval_silu": (_I, [_P, _P, _I, _P]),
+    "qmsg_eval_exp": (_I, [_P, _P, _I, _P]),
     "qmsg_calibrate_copy": (_I, [_P, _P, _P, ctypes.c_size_t]),
     "qmsg_device_info": (_I, [_P, ctypes.POINTER(_I), ctypes.POINTER(_I), ctypes.POINTER(ctypes.c_uint64),
                               ctypes.c_char_p, _I]),
@@ -275,6 +276,12 @@ class Context:
         x = np.ascontiguousarray(x, np.float32).ravel()
         out = np.empty_like(x)
         self._check(lib.qmsg_eval_silu(self._h, _ptr(x), x.size, _ptr(out)))
+        return out
+
+    def eval_exp(self, x: np.ndarray) -> np.ndarray:
+        x = np.ascontiguousarray(x, np.float64).ravel()
+        out = np.empty_like(x)
+        self._check(lib.qmsg_eval_exp(self._h, _ptr(x), x.size, _ptr(out)))
         return out
 
     def calibrate_copy(self, d_dst: int, d_src: int, nbytes: int):

@@ -62,6 +62,11 @@ def _load_oracle():
     L.orc_synth_experts.argtypes = [ctypes.c_uint64, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_int, ctypes.c_int64,
                                     ctypes.c_int64, ctypes.c_int, ctypes.c_int, ctypes.c_float, _P]
     L.orc_rmsnorm_unit.argtypes = [_P, _P, ctypes.c_int, ctypes.c_float]
+    L.orc_rmsnorm.argtypes = [_P, _P, _P, ctypes.c_int, ctypes.c_float]
+    L.orc_expf_mismatches.restype = ctypes.c_uint64
+    L.orc_expf_mismatches.argtypes = [ctypes.c_uint64, ctypes.c_uint64]
+    L.orc_exp_mismatches.restype = ctypes.c_uint64
+    L.orc_exp_mismatches.argtypes = [ctypes.c_uint64, ctypes.c_int64]
     return L
 
 
@@ -108,6 +113,16 @@ def synth_f32(seed: int, layer: int, kind: int, expert: int, n: int, sigma: floa
     out = np.empty(n, np.float32)
     lib.orc_synth_f32(seed, layer, kind, expert, n, sigma, _ptr(out))
     return out
+
+
+def rmsnorm(x: np.ndarray, w: Optional[np.ndarray] = None, eps: float = 1e-6) -> np.ndarray:
+    """Row-wise rmsnorm (src/model.c:403-409); w = None is a unit weight."""
+    x = np.ascontiguousarray(x, np.float32).reshape(-1, x.shape[-1])
+    wp = None if w is None else np.ascontiguousarray(w, np.float32)
+    y = np.empty_like(x)
+    for t in range(x.shape[0]):
+        lib.orc_rmsnorm(_ptr(y[t]), _ptr(x[t]), _ptr(wp), x.shape[1], eps)
+    return y
 
 
 def rmsnorm_unit(x: np.ndarray, eps: float = 1e-6) -> np.ndarray:
@@ -243,6 +258,7 @@ def load_ref():
     R.qref_silu.restype = ctypes.c_float
     R.qref_silu.argtypes = [ctypes.c_float]
     R.qref_rmsnorm_unit.argtypes = [_P, _P, ctypes.c_int, ctypes.c_float]
+    R.qref_rmsnorm.argtypes = [_P, _P, _P, ctypes.c_int, ctypes.c_float]
     R.qref_isa.restype = ctypes.c_char_p
     R.qref_max_threads.restype = ctypes.c_int
     return R

@@ -462,12 +462,14 @@ void orc_synth_experts(uint64_t seed, uint32_t layer, uint32_t kind, int type, i
     }
 }
 
-/* src/model.c:403-409 with a unit weight vector: sum of squares as a double FMA chain
- * (contracted by the reference build), 1/sqrt in double, then (float)(x*inv) * 1.0f. */
-void orc_rmsnorm_unit(float *y, const float *x, int n, float eps)
+/* src/model.c:403-409: sum of squares as a double FMA chain (contracted by the reference
+ * build), 1/sqrt in double, then (float)(x*inv) * w in float; w = NULL is a unit weight. */
+void orc_rmsnorm(float *y, const float *x, const float *w, int n, float eps)
 {
     double ss = 0.0;
     for (int i = 0; i < n; i++) ss = fma((double)x[i], (double)x[i], ss);
     const double inv = 1.0 / sqrt(ss / n + (double)eps);
-    for (int i = 0; i < n; i++) y[i] = (float)((double)x[i] * inv) * 1.0f;
+    for (int i = 0; i < n; i++) y[i] = (float)((double)x[i] * inv) * (w ? w[i] : 1.0f);
 }
+
+void orc_rmsnorm_unit(float *y, const float *x, int n, float eps) { orc_rmsnorm(y, x, NULL, n, eps); }

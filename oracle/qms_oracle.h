@@ -91,6 +91,7 @@ void orc_synth_f32(uint64_t seed, uint32_t layer, uint32_t kind, uint32_t expert
                    float *out);
 void orc_synth_experts(uint64_t seed, uint32_t layer, uint32_t kind, int type, int64_t rows, int64_t cols,
                        int e0, int e1, float sigma, uint8_t *base);
+void orc_rmsnorm(float *y, const float *x, const float *w, int n, float eps);
 void orc_rmsnorm_unit(float *y, const float *x, int n, float eps);
 
 #ifdef __cplusplus

@@ -58,6 +58,9 @@ void qref_rmsnorm_unit(float *y, const float *x, int n, float eps)
     free(w);
 }
 
+/* The reference's rmsnorm (src/model.c:403-409) with a caller's weight vector. */
+void qref_rmsnorm(float *y, const float *x, const float *w, int n, float eps) { rmsnorm(y, x, w, n, eps); }
+
 /* silu as the reference defines it (src/model.c:424), for element-wise checks. */
 float qref_silu(float a) { return silu(a); }
 

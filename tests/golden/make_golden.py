@@ -126,6 +126,15 @@ def kat_kernels(R) -> dict:
         out[f"f{i}_x"] = x
         out[f"f{i}_dot"] = np.float32(R.qms_vec_dot_f32(ptr(w), ptr(x), n))
     out["n_f32_cases"] = np.int32(4)
+    # rmsnorm (src/model.c:403-409) around the layer: unit and random weights, varied scales
+    for i, (n, scale, unit) in enumerate(((2048, 1.0, True), (4096, 1.0, True), (4096, 37.0, False),
+                                           (256, 1e-3, False))):
+        x = (rng.standard_normal(n) * scale).astype(np.float32)
+        w = np.ones(n, np.float32) if unit else rng.uniform(0.2, 2.0, n).astype(np.float32)
+        y = np.empty(n, np.float32)
+        R.qref_rmsnorm(ptr(y), ptr(x), ptr(w), n, np.float32(1e-6))
+        out[f"r{i}_x"], out[f"r{i}_w"], out[f"r{i}_y"] = x, w, y
+    out["n_rms_cases"] = np.int32(4)
     return out
 
 

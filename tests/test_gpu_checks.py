@@ -123,6 +123,29 @@ def test_silu_matches_glibc(q):
     assert np.array_equal(got.view(np.uint32)[~nan], ref.view(np.uint32)[~nan])
 
 
+def test_exp_matches_libc(q):
+    """The softmax's device exp (double) equals the C library's exp bit for bit."""
+    libm = ctypes.CDLL("libm.so.6")
+    libm.exp.restype = ctypes.c_double
+    libm.exp.argtypes = [ctypes.c_double]
+    rng = np.random.default_rng(5)
+    a = rng.standard_normal(8192).astype(np.float32) * 3
+    b = rng.standard_normal(8192).astype(np.float32) * 3
+    x = np.concatenate([
+        -np.abs(a.astype(np.float64) - b.astype(np.float64)),
+        -rng.uniform(0, 800, 8192),
+        rng.integers(0, 1 << 63, 8192, dtype=np.int64).view(np.float64),
+        np.array([0.0, -0.0, -1e-300, -700.0, -708.4, -745.1, -746.0, 709.7, 710.0, -np.inf, np.inf])])
+    x = x[~np.isnan(x)]
+    got = None
+    with q.Context(256, 16, 4, 128) as ctx:
+        got = ctx.eval_exp(x)
+    ref = np.array([libm.exp(float(v)) for v in x], np.float64)
+    nan = np.isnan(ref)
+    assert np.array_equal(np.isnan(got), nan)
+    assert np.array_equal(got.view(np.uint64)[~nan], ref.view(np.uint64)[~nan])
+
+
 def test_generator_bytes_identical(q):
     E, X, K, F = 512, 16, 4, 256
     with q.Context(E, X, K, F) as ctx:
@@ -148,7 +171,7 @@ def test_arguments_and_repeated_calls(q):
         with pytest.raises(q.QmsgError):
             ctx.moe(2, np.zeros((1, E), np.float32))
         xs = [orc.make_input(E, t, 100 + t) for t in (1, 4, 2, 3, 1)]
-        refs = {l: orc.Layer(E, X, K, F, 3 + l) for l in (0, 1)}
+        refs = {l: orc.Layer(E, X, K, F, 3 + l, layer=l) for l in (0, 1)}   # the layer index keys the generator
         for i, x in enumerate(xs):
             l = i % 2
             out = ctx.moe(l, x)

@@ -155,6 +155,23 @@ def test_block_dot_brute_force(t, n):
         assert orc.block_dot(t, row, xq, blk) == brute_block_dot(t, row, xq, blk)
 
 
+def test_rmsnorm_matches_reference(kat):
+    for i in range(int(kat["n_rms_cases"])):
+        got = orc.rmsnorm(kat[f"r{i}_x"][None, :], kat[f"r{i}_w"])[0]
+        assert np.array_equal(got.view(np.uint32), kat[f"r{i}_y"].view(np.uint32)), i
+
+
+def test_device_expf_restatement_on_all_inputs():
+    """The kernels' expf (qmsg_libm.h, compiled here for the CPU) equals the C library's
+    expf on every one of the 2^32 float inputs."""
+    assert orc.lib.orc_expf_mismatches(0, 1 << 32) == 0
+
+
+def test_device_exp_restatement_sampled():
+    """The kernels' double exp equals the C library's exp on 2e8 seeded inputs."""
+    assert orc.lib.orc_exp_mismatches(2024, 200_000_000) == 0
+
+
 def test_vec_dot_f32_matches_reference(kat):
     for i in range(int(kat["n_f32_cases"])):
         got = orc.vec_dot_f32(kat[f"f{i}_w"], kat[f"f{i}_x"])
