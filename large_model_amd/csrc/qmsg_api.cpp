@@ -49,6 +49,7 @@ struct qmsg_ctx {
     int device = 0;
     qmsg_cfg cfg{};
     int n_layer = 0, max_tokens = 0, path = QMSG_PATH_AUTO;
+    int n_cu = 256;
     hipStream_t stream = nullptr;
     std::vector<LayerStore> layers;
     Scratch S{};
@@ -141,6 +142,7 @@ int qmsg_create(qmsg_ctx **out, int device, const qmsg_cfg *cfg, int n_layer, in
     c->layers.resize((size_t)n_layer);
     hipError_t e = hipSetDevice(device);
     if (e == hipSuccess) e = hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking);
+    if (e == hipSuccess) e = hipDeviceGetAttribute(&c->n_cu, hipDeviceAttributeMultiprocessorCount, device);
     if (e != hipSuccess) {
         fail(nullptr, QMSG_E_DEVICE, "qmsg_create: %s", hipGetErrorString(e));
         delete c;
@@ -355,7 +357,7 @@ static int run_layer(qmsg_ctx *c, int layer, const float *d_xn, int T, float *d_
     const LayerDev d = layer_dev(c, L);
     LAUNCH(c, "route", launch_route(s, d, c->S, d_xn, T, c->stream));
     LAUNCH(c, "select", launch_select(s, c->S, T, c->stream));
-    LAUNCH(c, "gateup", launch_gateup_exact(s, d, c->S, T, debug, c->stream));
+    LAUNCH(c, "gateup", launch_gateup_exact(s, d, c->S, T, debug, c->n_cu, c->stream));
     LAUNCH(c, "down", launch_down_exact(s, d, c->S, d_out, T, c->stream));
     return QMSG_OK;
 }

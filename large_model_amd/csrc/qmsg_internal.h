@@ -39,6 +39,10 @@ extern thread_local const LaunchTimer *g_launch_timer;
 /* Static shape limits of the kernels. */
 constexpr int kMaxExperts = 256;
 
+/* One-token batches (n_used <= 8) are routed inside the gate/up kernel instead of by a
+ * separate select launch. */
+inline int use_small_route(int T, int K) { return T == 1 && K <= 8; }
+
 /* Per-layer device weights: the GGUF bytes, unchanged, in one allocation per tensor. */
 struct LayerDev {
     const float *router;    /* [X][E] */
@@ -78,7 +82,7 @@ struct Shape {
 hipError_t launch_route(const Shape &s, const LayerDev &L, const Scratch &S, const float *xn, int T,
                         hipStream_t st);
 hipError_t launch_select(const Shape &s, const Scratch &S, int T, hipStream_t st);
-hipError_t launch_gateup_exact(const Shape &s, const LayerDev &L, const Scratch &S, int T, int debug,
+hipError_t launch_gateup_exact(const Shape &s, const LayerDev &L, const Scratch &S, int T, int debug, int n_cu,
                                hipStream_t st);
 hipError_t launch_down_exact(const Shape &s, const LayerDev &L, const Scratch &S, float *out, int T,
                              hipStream_t st);

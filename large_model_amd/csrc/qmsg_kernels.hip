@@ -77,12 +77,21 @@ __device__ __forceinline__ uint32_t pack4(const int8_t *q)
 
 /* Quantise 32 floats the way qms_quantize_q8 does (src/kernels.c:34-53) and store the block
  * in both layouts: the reference's 44-byte Q8 and half of a 96-byte pair record. */
-__device__ void quantize_block_store(const float *v, Q8 *dst, uint32_t *pair, int half)
+/* One 32-block of the int8 quantiser (src/kernels.c:34-53): d = amax/127, q = rint(x/d) with
+ * the reference's reciprocal, per-half code sums and ds = d*sum. */
+struct Q8Vals {
+    float d, ds;
+    uint32_t s16;
+    uint32_t qw[8];          /* q[4w .. 4w+3] packed little-endian */
+};
+
+__device__ Q8Vals quantize_block(const float *v)
 {
     float amax = 0.0f;
     for (int j = 0; j < 32; j++) amax = fmaxf(amax, fabsf(v[j]));
-    const float d = amax / 127.0f;
-    const float id = d > 0.0f ? 1.0f / d : 0.0f;
+    Q8Vals r;
+    r.d = amax / 127.0f;
+    const float id = r.d > 0.0f ? 1.0f / r.d : 0.0f;
     int8_t q[32];
     int s0 = 0, s1 = 0;
     for (int j = 0; j < 32; j++) {
@@ -90,21 +99,40 @@ __device__ void quantize_block_store(const float *v, Q8 *dst, uint32_t *pair, in
         q[j] = (int8_t)qi;
         if (j < 16) s0 += qi; else s1 += qi;
     }
-    const float ds = d * (float)(s0 + s1);
-    const uint32_t s16 = (uint32_t)(uint16_t)(int16_t)s0 | ((uint32_t)(uint16_t)(int16_t)s1 << 16);
+    r.ds = r.d * (float)(s0 + s1);
+    r.s16 = (uint32_t)(uint16_t)(int16_t)s0 | ((uint32_t)(uint16_t)(int16_t)s1 << 16);
+    for (int w = 0; w < 8; w++) r.qw[w] = pack4(q + 4 * w);
+    return r;
+}
+
+/* The 44-byte QmsQ8 record. */
+__device__ void store_q8(const Q8Vals &q, Q8 *dst)
+{
     uint32_t *o = (uint32_t *)dst;
-    o[0] = __float_as_uint(d);
-    o[1] = __float_as_uint(ds);
-    o[2] = s16;
-    for (int w = 0; w < 8; w++) o[3 + w] = pack4(q + 4 * w);
+    o[0] = __float_as_uint(q.d);
+    o[1] = __float_as_uint(q.ds);
+    o[2] = q.s16;
+    for (int w = 0; w < 8; w++) o[3 + w] = q.qw[w];
+}
+
+/* Block `half` (0: even, 1: odd) of a 96-byte pair record. */
+__device__ void store_pair_half(const Q8Vals &q, uint32_t *pair, int half)
+{
     for (int p = 0; p < 4; p++) {
-        pair[4 * p + 2 * half] = pack4(q + 4 * p);
-        pair[4 * p + 2 * half + 1] = pack4(q + 16 + 4 * p);
+        pair[4 * p + 2 * half] = q.qw[p];
+        pair[4 * p + 2 * half + 1] = q.qw[4 + p];
     }
-    pair[16 + 2 * half] = __float_as_uint(d);
-    pair[17 + 2 * half] = __float_as_uint(ds);
-    pair[20 + half] = s16;
+    pair[16 + 2 * half] = __float_as_uint(q.d);
+    pair[17 + 2 * half] = __float_as_uint(q.ds);
+    pair[20 + half] = q.s16;
     if (half == 0) { pair[22] = 0; pair[23] = 0; }
+}
+
+__device__ void quantize_block_store(const float *v, Q8 *dst, uint32_t *pair, int half)
+{
+    const Q8Vals q = quantize_block(v);
+    store_q8(q, dst);
+    store_pair_half(q, pair, half);
 }
 
 /* ------------------------------------------------------------------ wave primitives ---- */
@@ -477,6 +505,7 @@ hipError_t launch_select(const Shape &s, const Scratch &S, int T, hipStream_t st
     a.K = s.K;
     a.T = T;
     a.S = S;
+    if (use_small_route(T, s.K)) return hipSuccess;   /* the gate/up kernel routes the batch */
     QLAUNCH("select", select_kernel, dim3(T), dim3(256), 0, st, a, T == 1 ? 1 : 0);
     if (T > 1) QLAUNCH("dispatch", dispatch_kernel, dim3(1), dim3(64), 0, st, a);
     return hipGetLastError();
@@ -578,12 +607,177 @@ __device__ __forceinline__ float quad_finish(const RowAcc &r, float scale)
     return h - scale * r.corr;
 }
 
+/* ------------------------------------------------------------------ small-batch routing ---- */
+
+/* A one-token batch is routed inside the expert kernel: every block recomputes the softmax,
+ * top-K and slot order from the logits, which removes a launch and a round trip through
+ * memory between the router and the experts. */
+constexpr int kSelNS = 8;              /* slots of such a batch (n_used <= 8) */
+
+struct alignas(16) SmallRoute {
+    int4 work[kSelNS];                 /* per active expert, as Scratch::work */
+    int sel[kSelNS];
+    float wt[kSelNS];
+    int slot_t[kSelNS];
+    int slot_of[kSelNS];
+    int cand[kSelNS + 1];              /* the first K+1 experts of the logit order */
+    int na;
+    int pad[2];
+};
+
+/* Routing of a one-token batch inside each gate/up block (src/model.c:1045-1088).
+ *
+ * The softmax runs on wave 0: P_e = exp(l_e - max) in double, z summed in expert order, p_e =
+ * P_e / z. Meanwhile the other waves rank the float logits (descending, ties to the lower
+ * index). Since p is non-decreasing in l, the reference's top K (p descending, ties to the
+ * lower index) is the first K of that order whenever p strictly decreases along its first
+ * K+1 entries, except between equal logits, whose p are equal and whose order is by index in
+ * both rankings; this is checked, and if a rounding tie shows up (logits of different value
+ * with equal p), wave 0 ranks the p exactly instead. Weights are renormalised with wsum in
+ * selection order; the slots of the token are its experts in ascending order.
+ * Shared scratch (LDS): L[X] floats, P[X] doubles, rank[X], selidx[X], start[X+1]. Ends with
+ * a block barrier; block (0, 0) also publishes the result for the down kernel and the debug
+ * copy-back. */
+__device__ void route_one(const Scratch &S, int K, int X, SmallRoute *R, float *L, double *P, int *rank, int *selidx,
+                          int *start)
+{
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, nw = blockDim.x >> 6;
+    for (int e = tid; e < X; e += blockDim.x) {
+        L[e] = S.logits[e];
+        rank[e] = 0;
+        selidx[e] = -1;
+    }
+    __syncthreads();
+    if (wave == 0) {
+        constexpr int NPL = kMaxExperts / 64;
+        double v[NPL];
+        float mf = -__builtin_inff();
+#pragma unroll
+        for (int i = 0; i < NPL; i++) {
+            const int e = lane + 64 * i;
+            const float l = e < X ? L[e] : -__builtin_inff();
+            mf = l > mf ? l : mf;
+        }
+        for (int o = 32; o > 0; o >>= 1) {
+            const float w = __shfl_xor(mf, o);
+            mf = w > mf ? w : mf;
+        }
+        const double mx = (double)mf;
+#pragma unroll
+        for (int i = 0; i < NPL; i++) {
+            const int e = lane + 64 * i;
+            v[i] = e < X ? qmsg_exp((double)L[e] - mx) : 0.0;
+            if (e < X) P[e] = v[i];
+        }
+        wave_sync();
+        double z = 0.0;
+        const double2 *P2 = (const double2 *)P;
+#pragma unroll 16
+        for (int e2 = 0; e2 < (X >> 1); e2++) {
+            const double2 q = P2[e2];
+            z += q.x;
+            z += q.y;
+        }
+        if (X & 1) z += P[X - 1];
+        wave_sync();
+#pragma unroll
+        for (int i = 0; i < NPL; i++) {
+            const int e = lane + 64 * i;
+            if (e < X) P[e] = v[i] / z;
+        }
+    } else {
+        /* float ranks, item (e, part) over waves 1 .. nw-1 */
+        const int nth = blockDim.x - 64, t = tid - 64;
+        const int np = max(1, nth / X), len = (X + np - 1) / np;
+        for (int it = t; it < X * np; it += nth) {
+            const int part = it % np, e = it / np;
+            const float le = L[e];
+            const int f0 = part * len, f1 = min(X, f0 + len);
+            int r = 0;
+#pragma unroll 8
+            for (int f = f0; f < f1; f++) {
+                const float lf = L[f];
+                r += (lf > le) | ((lf == le) & (f < e));
+            }
+            if (r) atomicAdd(&rank[e], r);
+        }
+    }
+    __syncthreads();
+    if (wave == 0) {
+        int *cand = R->cand;
+        for (int e = lane; e < X; e += 64)
+            if (rank[e] <= K) cand[rank[e]] = e;
+        wave_sync();
+        bool ok = true;
+        if (lane < K) {
+            const int a = cand[lane], b = cand[lane + 1];
+            ok = P[a] > P[b] || L[a] == L[b];
+        }
+        if (__ballot(!ok) == 0ULL) {
+            if (lane < K) R->sel[lane] = cand[lane];
+        } else {
+            /* a rounding tie among the candidates: rank the p exactly */
+            for (int e = lane; e < X; e += 64) {
+                const double pe = P[e];
+                int r = 0;
+                for (int f = 0; f < X; f++) {
+                    const double pf = P[f];
+                    r += (pf > pe) | ((pf == pe) & (f < e));
+                }
+                if (r < K) R->sel[r] = e;
+            }
+        }
+        wave_sync();
+        const int sj = lane < K ? R->sel[lane] : 0;
+        const double pj = lane < K ? P[sj] : 0.0;
+        double wsum = 0.0;
+        for (int j = 0; j < K; j++) wsum += __shfl(pj, j);
+        if (lane < K) {
+            R->wt[lane] = (float)(pj / wsum);
+            selidx[sj] = lane;
+        }
+        wave_sync();
+        /* the token's slots are its experts in ascending order */
+        int below = 0;
+        for (int e0 = 0; e0 <= X; e0 += 64) {
+            const int e = e0 + lane;
+            const int j = e < X ? selidx[e] : -1;
+            const unsigned long long m = __ballot(j >= 0);
+            const int pos = below + __popcll(m & ((1ULL << lane) - 1ULL));
+            if (e <= X) start[e] = pos;
+            if (j >= 0) {
+                R->work[pos] = make_int4(e, pos, pos + 1, 0);
+                R->slot_of[j] = pos;
+            }
+            below += __popcll(m);
+        }
+        wave_sync();
+        if (lane < K) R->slot_t[lane] = 0;
+        if (lane == 0) R->na = K;
+    }
+    __syncthreads();
+    if (blockIdx.x == 0 && blockIdx.y == 0) {
+        for (int i = tid; i < K; i += blockDim.x) {
+            S.sel[i] = R->sel[i];
+            S.wt[i] = R->wt[i];
+            S.slot_t[i] = 0;
+            S.slot_of[i] = R->slot_of[i];
+        }
+        for (int e = tid; e <= X; e += blockDim.x) S.start[e] = start[e];
+        for (int i = tid; i < X; i += blockDim.x) {
+            S.work[i] = i < K ? R->work[i] : make_int4(-1, 0, 0, 0);
+            if (i < K) S.active[i] = R->work[i].x;
+        }
+        if (tid == 0) S.meta[0] = K;
+    }
+}
+
 /* ------------------------------------------------------------------ gate / up ---- */
 
 struct GateUpArgs {
     const uint8_t *gate, *up;
     uint64_t rb, eb;
-    int E, F, debug;
+    int E, F, K, X, T, debug;
     Scratch S;
 };
 
@@ -617,146 +811,173 @@ __device__ __forceinline__ void q4_0_rows(const uint32_t *Wrow, int p, const uin
     }
 }
 
-/* One block: expert work[blockIdx.y].x, gate rows and up rows r0 .. r0+31 (r0 = 32*blockIdx.x),
- * for every slot of the expert, NT slots per pass. Wave w owns gate rows r0+8w .. r0+8w+7
- * (quads 0-7) and the same up rows (quads 8-15) and loads exactly those rows: G chunks of CB
- * blocks have all their loads in flight, each chunk goes through the wave's own LDS buffer,
- * and waves synchronise only with themselves, so a wave whose bytes land early computes
- * while others still wait. The slots' int8 input records are requested before the weights
- * (waiting on them never waits on the weights). Epilogue: a = silu(g)*u
- * (src/model.c:989-997), then one int8 32-block of activations. */
-template <int NT, int CB, int G>
-__global__ __launch_bounds__(256) void gateup_exact_kernel(GateUpArgs a)
+/* LDS bytes of a gateup block (shared by the kernel's carve-up and the launcher). */
+__host__ __device__ constexpr size_t gateup_lds(int W, int NT, int CB, int nP, int sel)
+{
+    return (size_t)W * 16 * (CB * 18 + (((CB * 18 / 16) & 1) ? 0 : 16)) + (size_t)NT * nP * kPairBytes +
+           (size_t)NT * 2 * 8 * W * 4 +
+           (sel ? sizeof(SmallRoute) + (size_t)kMaxExperts * (8 + 4 + 4 + 4) + (kMaxExperts + 1) * 4 : 0);
+}
+
+/* One block of W waves: expert work[blockIdx.y].x, gate rows and up rows r0 .. r0+8W-1
+ * (r0 = 8W*blockIdx.x), for every slot of the expert, NT slots per pass. W is chosen so the
+ * grid spreads evenly over the CUs (48 row pairs of the 235B shape: 256 blocks, one per CU).
+ * Wave w owns gate rows r0+8w .. r0+8w+7 (quads 0-7) and the same up rows (quads 8-15) and
+ * streams exactly those rows in chunks of CB blocks, D chunks in flight: a chunk is copied
+ * into the wave's own LDS buffer, its registers are refilled with chunk c+D, then its dots
+ * run, so each wave computes while its later bytes are still on the way and waves never wait
+ * for each other. With SEL the block first routes the batch itself; a one-token batch
+ * requests its input records before that, so they arrive during the routing. Epilogue:
+ * a = silu(g)*u (src/model.c:989-997); the int8 requantisation of a happens where all 32 rows
+ * of a block are known (the down kernel). */
+template <int W, int NT, int CB, int D, int SEL>
+__global__ __launch_bounds__(64 * W) void gateup_kernel(GateUpArgs a)
 {
     extern __shared__ __align__(16) uint8_t smem[];
+    constexpr int NTH = 64 * W, R = 8 * W;
     constexpr int SPR = CB * 18 / 16;                 /* 16-byte slots per row per chunk      */
     constexpr int NSL = 16 * SPR;                     /* slots of one wave's chunk            */
     constexpr int SPT = (NSL + 63) / 64;              /* slots per lane per chunk             */
     constexpr int WS = CB * 18 + ((SPR & 1) ? 0 : 16);/* LDS row stride, odd in 16-byte units */
     const int nbE = a.E >> 5, nP = nbE >> 1, nchunk = nbE / CB;
     const int xsl = nP * 6;                           /* 16-byte slots of one token's records */
-    constexpr int XS = (NT * (4096 / 64) * 6 + 255) / 256;  /* x slots per thread (E <= 4096) */
+    constexpr int XS = (NT * (4096 / 64) * 6 + NTH - 1) / NTH;  /* x slots per thread (E <= 4096) */
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, qd = lane >> 2, p = lane & 3;
     uint8_t *wbuf = smem + wave * 16 * WS;
-    uint8_t *xbuf = smem + 4 * 16 * WS;
-    float *res = (float *)(xbuf + NT * nP * kPairBytes);
-    int8_t *qb = (int8_t *)(res + NT * 64);
+    uint8_t *xbuf = smem + W * 16 * WS;
+    float *res = (float *)(xbuf + NT * nP * kPairBytes);               /* [NT][2R] */
 
-    const int4 wk = a.S.work[blockIdx.y];
-    if (wk.x < 0) return;
+    /* a one-token batch: its only token's records can be requested before the routing */
+    u32x4 xv[XS];
+    if constexpr (NT == 1) {
+#pragma unroll
+        for (int m = 0; m < XS; m++) xv[m] = ((const u32x4 *)a.S.xqk)[min(tid + NTH * m, xsl - 1)];
+    }
+    int4 wk;
+    const int *slot_t = a.S.slot_t;
+    if constexpr (SEL) {
+        SmallRoute *sr = (SmallRoute *)(res + NT * 2 * R);
+        double *P = (double *)(sr + 1);
+        float *L = (float *)(P + kMaxExperts);
+        int *rank = (int *)(L + kMaxExperts);
+        route_one(a.S, a.K, a.X, sr, L, P, rank, rank + kMaxExperts, rank + 2 * kMaxExperts);
+        if ((int)blockIdx.y >= sr->na) return;
+        wk = sr->work[blockIdx.y];
+        slot_t = sr->slot_t;
+    } else {
+        wk = a.S.work[blockIdx.y];
+        if (wk.x < 0) return;
+    }
     const int e = wk.x, s_begin = wk.y, s_end = wk.z;
-    const int r0 = (int)blockIdx.x * 32, rw = r0 + 8 * wave;     /* this wave's first row */
+    const int r0 = (int)blockIdx.x * R, rw = r0 + 8 * wave;     /* this wave's first row */
     const uint8_t *gbase = a.gate + (size_t)e * a.eb + (size_t)rw * a.rb;
     const uint8_t *ubase = a.up + (size_t)e * a.eb + (size_t)rw * a.rb;
-    const int F = a.F, nbF = F >> 5;
-    const int rho = qd < 8 ? 8 * wave + qd : 32 + 8 * wave + (qd - 8);   /* tile row of this quad */
+    const int F = a.F;
+    const int rho = qd < 8 ? 8 * wave + qd : R + 8 * wave + (qd - 8);   /* tile row of this quad */
+    const bool tok_bytes = a.T <= 256;              /* work.w holds the first four tokens */
 
     for (int g0 = s_begin; g0 < s_end; g0 += NT) {
         const int nt = min(NT, s_end - g0);
-        /* the nt slots' input records (tokens of the first four slots ride in work.w) */
-        u32x4 xv[XS];
+        if constexpr (NT > 1) {
 #pragma unroll
-        for (int m = 0; m < XS; m++) {
-            const int i = min(tid + 256 * m, nt * xsl - 1), n = i / xsl, off = i - n * xsl;
-            const int k = g0 - s_begin + n;
-            const int tok = k < 4 ? (wk.w >> (8 * k)) & 0xff : a.S.slot_t[g0 + n];
-            xv[m] = ((const u32x4 *)(a.S.xqk + (size_t)tok * nP * kPairBytes))[off];
+            for (int m = 0; m < XS; m++) {
+                const int i = min(tid + NTH * m, nt * xsl - 1), n = i / xsl, off = i - n * xsl;
+                const int k = g0 - s_begin + n;
+                const int tok = (k < 4 && tok_bytes) ? (wk.w >> (8 * k)) & 0xff : slot_t[g0 + n];
+                xv[m] = ((const u32x4 *)(a.S.xqk + (size_t)tok * nP * kPairBytes))[off];
+            }
         }
+        if (NT > 1 || g0 == s_begin) {
+#pragma unroll
+            for (int m = 0; m < XS; m++) ((u32x4 *)xbuf)[min(tid + NTH * m, nt * xsl - 1)] = xv[m];
+        }
+        __syncthreads();
         RowAcc acc[NT];
         for (int n = 0; n < NT; n++) acc[n] = RowAcc{ 0.0f, 0.0f, 0.0f };
-        for (int cg = 0; cg < nchunk; cg += G) {
-            u32x4 wv[G][SPT];
+        u32x4 wv[D][SPT];
+        auto load_chunk = [&](int c, u32x4 *dst) {
 #pragma unroll
-            for (int c = 0; c < G; c++)
-#pragma unroll
-                for (int m = 0; m < SPT; m++) {
-                    const int i = min(lane + 64 * m, NSL - 1), row = i / SPR, j = i - row * SPR;
-                    wv[c][m] = *(const u32x4 *)((row < 8 ? gbase + (size_t)row * a.rb : ubase + (size_t)(row - 8) * a.rb) +
-                                                (size_t)(cg + c) * CB * 18 + 16 * j);
-                }
-            if (cg == 0) {
-#pragma unroll
-                for (int m = 0; m < XS; m++) ((u32x4 *)xbuf)[min(tid + 256 * m, nt * xsl - 1)] = xv[m];
-                __syncthreads();
+            for (int m = 0; m < SPT; m++) {
+                const int i = min(lane + 64 * m, NSL - 1), row = i / SPR, j = i - row * SPR;
+                dst[m] = *(const u32x4 *)((row < 8 ? gbase + (size_t)row * a.rb : ubase + (size_t)(row - 8) * a.rb) +
+                                          (size_t)c * CB * 18 + 16 * j);
             }
+        };
 #pragma unroll
-            for (int c = 0; c < G; c++) {
-                wave_sync();
+        for (int d = 0; d < D; d++)
+            if (d < nchunk) load_chunk(d, wv[d]);
+        for (int c0 = 0; c0 < nchunk; c0 += D) {
 #pragma unroll
-                for (int m = 0; m < SPT; m++) {
-                    const int i = min(lane + 64 * m, NSL - 1), row = i / SPR, j = i - row * SPR;
-                    *(u32x4 *)(wbuf + row * WS + 16 * j) = wv[c][m];
+            for (int d = 0; d < D; d++) {
+                const int c = c0 + d;
+                if (c < nchunk) {
+                    wave_sync();
+#pragma unroll
+                    for (int m = 0; m < SPT; m++) {
+                        const int i = min(lane + 64 * m, NSL - 1), row = i / SPR, j = i - row * SPR;
+                        *(u32x4 *)(wbuf + row * WS + 16 * j) = wv[d][m];
+                    }
+                    wave_sync();
+                    if (c + D < nchunk) load_chunk(c + D, wv[d]);
+                    q4_0_rows<NT, (NT >= 4 ? 1 : (NT == 2 ? 2 : 4))>((const uint32_t *)(wbuf + qd * WS), p, xbuf,
+                                                                      (size_t)nP * kPairBytes, c * (CB / 2), CB / 2,
+                                                                      nt, acc);
                 }
-                wave_sync();
-                q4_0_rows<NT, (NT >= 4 ? 1 : (NT == 2 ? 2 : 4))>((const uint32_t *)(wbuf + qd * WS), p, xbuf,
-                                                                  (size_t)nP * kPairBytes, (cg + c) * (CB / 2), CB / 2,
-                                                                  nt, acc);
             }
         }
 #pragma unroll
         for (int n = 0; n < NT; n++) {
             const float v = quad_finish(acc[n], 8.0f);
-            if (p == 0 && n < nt) res[n * 64 + rho] = v;
+            if (p == 0 && n < nt) res[n * 2 * R + rho] = v;
         }
         __syncthreads();
-        const int wave = tid >> 6, l = tid & 63;
-        for (int n = wave; n < nt; n += 4) {
-            const int s = g0 + n;
-            float av = 0.0f;
-            if (l < 32) {
-                const float g = res[n * 64 + l], u = res[n * 64 + 32 + l];
-                av = silu_ref(g) * u;
-                a.S.act[(size_t)s * F + r0 + l] = av;
-                if (a.debug) {
-                    a.S.gu[(size_t)s * 2 * F + r0 + l] = g;
-                    a.S.gu[(size_t)s * 2 * F + F + r0 + l] = u;
-                }
+        for (int i = tid; i < nt * R; i += NTH) {
+            const int n = i / R, l = i - n * R, s = g0 + n;
+            const float g = res[n * 2 * R + l], u = res[n * 2 * R + R + l];
+            a.S.act[(size_t)s * F + r0 + l] = silu_ref(g) * u;
+            if (a.debug) {
+                a.S.gu[(size_t)s * 2 * F + r0 + l] = g;
+                a.S.gu[(size_t)s * 2 * F + F + r0 + l] = u;
             }
-            float amax = l < 32 ? fabsf(av) : 0.0f;
-            for (int o = 16; o > 0; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 32));
-            const float d = amax / 127.0f;
-            const float id = d > 0.0f ? 1.0f / d : 0.0f;
-            const int qi = (int)rintf(av * id);
-            int sum = qi;
-            for (int o = 8; o > 0; o >>= 1) sum += __shfl_xor(sum, o, 16);   /* lanes 0-15, 16-31 */
-            const int s0 = __shfl(sum, 0), s1 = __shfl(sum, 16);
-            if (l < 32) qb[n * 32 + l] = (int8_t)qi;
-            wave_sync();
-            const float ds = d * (float)(s0 + s1);
-            const uint32_t s16 = (uint32_t)(uint16_t)(int16_t)s0 | ((uint32_t)(uint16_t)(int16_t)s1 << 16);
-            const uint32_t *qw = (const uint32_t *)(qb + n * 32);
-            uint32_t *o = (uint32_t *)(a.S.aq + (size_t)s * nbF + (r0 >> 5));
-            if (l == 0) o[0] = __float_as_uint(d);
-            if (l == 1) o[1] = __float_as_uint(ds);
-            if (l == 2) o[2] = s16;
-            if (l >= 3 && l < 11) o[l] = qw[l - 3];
-            const int tile = r0 >> 5, half = tile & 1;
-            uint32_t *pr = (uint32_t *)(a.S.aqk + ((size_t)s * (nbF >> 1) + (tile >> 1)) * kPairBytes);
-            if (l >= 16 && l < 20) {
-                const int pp = l - 16;
-                pr[4 * pp + 2 * half] = qw[pp];
-                pr[4 * pp + 2 * half + 1] = qw[4 + pp];
-            }
-            if (l == 20) pr[16 + 2 * half] = __float_as_uint(d);
-            if (l == 21) pr[17 + 2 * half] = __float_as_uint(ds);
-            if (l == 22) pr[20 + half] = s16;
-            if (l == 23 && half == 0) { pr[22] = 0; pr[23] = 0; }
         }
         __syncthreads();
     }
 }
 
-template <int NT>
-static void launch_gateup_nt(const GateUpArgs &a, int CB, int G, dim3 grid, size_t lds, hipStream_t st)
+template <int W, int NT, int SEL>
+static void launch_gateup_w(const GateUpArgs &a, int CB, dim3 grid, size_t lds, hipStream_t st)
 {
-    if (CB == 32 && G == 4) QLAUNCH("gateup", (gateup_exact_kernel<NT, 32, 4>), grid, dim3(256), lds, st, a);
-    else if (CB == 32 && G == 2) QLAUNCH("gateup", (gateup_exact_kernel<NT, 32, 2>), grid, dim3(256), lds, st, a);
-    else if (CB == 32) QLAUNCH("gateup", (gateup_exact_kernel<NT, 32, 1>), grid, dim3(256), lds, st, a);
-    else if (CB == 16) QLAUNCH("gateup", (gateup_exact_kernel<NT, 16, 1>), grid, dim3(256), lds, st, a);
-    else QLAUNCH("gateup", (gateup_exact_kernel<NT, 8, 1>), grid, dim3(256), lds, st, a);
+    if (CB == 32) QLAUNCH("gateup", (gateup_kernel<W, NT, 32, 2, SEL>), grid, dim3(64 * W), lds, st, a);
+    else if (CB == 16) QLAUNCH("gateup", (gateup_kernel<W, NT, 16, 2, SEL>), grid, dim3(64 * W), lds, st, a);
+    else QLAUNCH("gateup", (gateup_kernel<W, NT, 8, 1, SEL>), grid, dim3(64 * W), lds, st, a);
 }
 
-hipError_t launch_gateup_exact(const Shape &s, const LayerDev &L, const Scratch &S, int T, int debug, hipStream_t st)
+template <int NT, int SEL>
+static void launch_gateup_nt(const GateUpArgs &a, int W, int CB, dim3 grid, size_t lds, hipStream_t st)
+{
+    if (W == 6) launch_gateup_w<6, NT, SEL>(a, CB, grid, lds, st);
+    else if (W == 4) launch_gateup_w<4, NT, SEL>(a, CB, grid, lds, st);
+    else if (W == 3) launch_gateup_w<3, NT, SEL>(a, CB, grid, lds, st);
+    else launch_gateup_w<2, NT, SEL>(a, CB, grid, lds, st);
+}
+
+/* Waves per gateup block: the W (rows 8W per block) whose grid, at the largest possible
+ * number of active experts, puts the least work on the busiest CU (one block per CU per
+ * pass); ties go to the larger block. */
+int gateup_waves(int F, int max_active, int n_cu)
+{
+    int best = 0, best_cost = 0;
+    for (int W : { 6, 4, 3, 2 }) {
+        if (F % (8 * W)) continue;
+        const long nblk = (long)(F / (8 * W)) * max_active;
+        const long cost = ((nblk + n_cu - 1) / n_cu) * W;
+        if (!best || cost < best_cost) { best = W; best_cost = (int)cost; }
+    }
+    return best;
+}
+
+hipError_t launch_gateup_exact(const Shape &s, const LayerDev &L, const Scratch &S, int T, int debug, int n_cu,
+                               hipStream_t st)
 {
     GateUpArgs a;
     a.gate = L.gate;
@@ -765,22 +986,28 @@ hipError_t launch_gateup_exact(const Shape &s, const LayerDev &L, const Scratch 
     a.eb = L.gate_eb;
     a.E = s.E;
     a.F = s.F;
+    a.K = s.K;
+    a.X = s.X;
+    a.T = T;
     a.debug = debug;
     a.S = S;
     const int nbE = s.E / 32, nP = nbE / 2;
-    const int CB = nbE % 32 == 0 ? 32 : (nbE % 16 == 0 ? 16 : 8);
-    const int nchunk = nbE / CB;
+    /* chunk of CB blocks; the D = 2 chunks in flight need an even chunk count */
+    const int CB = nbE % 64 == 0 ? 32 : (nbE % 32 == 0 ? 16 : 8);
     const int NT = T >= 4 ? 4 : (T >= 2 ? 2 : 1);
-    /* chunks with loads in flight at once: as many as the registers allow at this NT */
-    const int G = CB != 32 ? 1 : (NT == 1 && nchunk % 4 == 0 ? 4 : (nchunk % 2 == 0 ? 2 : 1));
-    const int spr = CB * 18 / 16;
-    const int ws = CB * 18 + ((spr & 1) ? 0 : 16);
     const int maxact = s.X < T * s.K ? s.X : T * s.K;
-    dim3 grid(s.F / 32, maxact);
-    const size_t lds = (size_t)64 * ws + (size_t)NT * nP * kPairBytes + (size_t)NT * 64 * 4 + NT * 32;
-    if (NT == 4) launch_gateup_nt<4>(a, CB, G, grid, lds, st);
-    else if (NT == 2) launch_gateup_nt<2>(a, CB, G, grid, lds, st);
-    else launch_gateup_nt<1>(a, CB, G, grid, lds, st);
+    const int W = gateup_waves(s.F, maxact, n_cu);
+    if (!W) return hipErrorInvalidValue;
+    const int sel = use_small_route(T, s.K);
+    dim3 grid(s.F / (8 * W), maxact);
+    const size_t lds = gateup_lds(W, NT, CB, nP, sel);
+    if (sel) {
+        launch_gateup_nt<1, 1>(a, W, CB, grid, lds, st);     /* one token: NT == 1 */
+    } else {
+        if (NT == 4) launch_gateup_nt<4, 0>(a, W, CB, grid, lds, st);
+        else if (NT == 2) launch_gateup_nt<2, 0>(a, W, CB, grid, lds, st);
+        else launch_gateup_nt<1, 0>(a, W, CB, grid, lds, st);
+    }
     return hipGetLastError();
 }
 
@@ -792,6 +1019,7 @@ struct DownArgs {
     int E, F, K, T, X;
     int fuse;          /* 1: combine inside the block (dn of all slots fits in LDS) */
     int lds_slots;     /* slots of a round whose int8 activations are staged in LDS */
+    int qlds;          /* 1: quantise every slot's activations into LDS in the prologue */
     float *out;
     Scratch S;
 };
@@ -806,25 +1034,72 @@ template <int TYPE, int NT>
 __global__ __launch_bounds__(256) void down_exact_kernel(DownArgs a)
 {
     extern __shared__ __align__(16) uint8_t smem[];
-    constexpr int RD = 8, EPR = 8, MAXS = TYPE == 2 ? 14 : 20;   /* rows, experts per round, slots */
+    constexpr int RD = 8, EPR = 8;                       /* rows, experts per round */
+    constexpr int LPE = TYPE == 2 ? 2 : 3, MAXS = EPR * LPE;   /* 16-byte loads per expert per thread */
     const int tid = threadIdx.x, quad = tid >> 2, p = tid & 3;
     const int r0 = (int)blockIdx.x * RD, E = a.E, nPF = a.F >> 6, K = a.K;
     const int rbytes = (int)(RD * a.rb);                 /* one expert's RD rows */
-    const int spe = rbytes / 16, nslot = EPR * spe;
+    const int spe = rbytes / 16;                         /* 16-byte slots of one expert's rows */
     const int xrec = nPF * kPairBytes;                   /* one slot's int8 activations */
     uint8_t *tile = smem;
     uint8_t *xbuf = smem + ((EPR * rbytes + 16 + 15) & ~15);        /* up to a.lds_slots slots */
     float *dnl = (float *)(xbuf + (size_t)a.lds_slots * xrec);      /* [NS][RD] when fused */
     u32x4 v[MAXS];
     int rnd = 0;
-    /* round rnd covers active experts rnd*EPR .. rnd*EPR+7; work[] ends with expert -1 */
+    /* round rnd covers active experts rnd*EPR .. rnd*EPR+7; work[] ends with expert -1. Every
+     * load instruction reads one expert's rows (a uniform address base), LPE per expert. */
 #define QMSG_DLOAD(R)                                                                                \
-    _Pragma("unroll") for (int m = 0; m < MAXS; m++) {                                               \
-        const int i_ = min(tid + 256 * m, nslot - 1), k_ = i_ / spe, j_ = i_ - k_ * spe;             \
+    _Pragma("unroll") for (int k_ = 0; k_ < EPR; k_++) {                                             \
         const int e_ = max(a.S.work[min((R) * EPR + k_, a.X - 1)].x, 0);                             \
-        v[m] = ((const u32x4 *)(a.down + (size_t)e_ * a.eb + (size_t)r0 * a.rb))[j_];                 \
+        const u32x4 *src_ = (const u32x4 *)(a.down + (size_t)e_ * a.eb + (size_t)r0 * a.rb);         \
+        _Pragma("unroll") for (int j_ = 0; j_ < LPE; j_++) v[k_ * LPE + j_] = src_[min(tid + 256 * j_, spe - 1)]; \
     }
+    /* Each int8 block of activations spans rows of two gate/up blocks, so with qlds it is
+     * formed here, for every slot. The first QPRE blocks' inputs per thread are requested
+     * before the weights (waits are in issue order), so they are quantised while the
+     * weights are in flight. Block 0 also writes the blocks out for the debug copy-back. */
+    constexpr int QPRE = 2;
+    const int nqb = a.qlds ? a.T * K * (a.F >> 5) : 0, nbF = a.F >> 5;
+    float4 av[QPRE][8];
+#pragma unroll
+    for (int u = 0; u < QPRE; u++) {
+        const int b = min(tid + 256 * u, max(nqb - 1, 0));    /* in bounds even when unused */
+        const float4 *src = (const float4 *)(a.S.act + (size_t)b * 32);
+#pragma unroll
+        for (int j = 0; j < 8; j++) av[u][j] = src[j];
+    }
+    __builtin_amdgcn_sched_barrier(0);     /* keep these requests ahead of the weights' */
     QMSG_DLOAD(0)
+    auto quant_store = [&](int b, const float *v) {
+        const int s = b / nbF, blk = b - s * nbF;
+        const Q8Vals q = quantize_block(v);
+        store_pair_half(q, (uint32_t *)(xbuf + (size_t)s * xrec + (size_t)(blk >> 1) * kPairBytes), blk & 1);
+        if (blockIdx.x == 0) {
+            store_q8(q, a.S.aq + b);
+            store_pair_half(q, (uint32_t *)(a.S.aqk + ((size_t)s * (nbF >> 1) + (blk >> 1)) * kPairBytes), blk & 1);
+        }
+    };
+#pragma unroll
+    for (int u = 0; u < QPRE; u++) {
+        if (tid + 256 * u < nqb) {
+            float v[32];
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+                v[4 * j] = av[u][j].x; v[4 * j + 1] = av[u][j].y; v[4 * j + 2] = av[u][j].z; v[4 * j + 3] = av[u][j].w;
+            }
+            quant_store(tid + 256 * u, v);
+        }
+    }
+    for (int b = tid + 256 * QPRE; b < nqb; b += 256) {
+        float v[32];
+        const float4 *src = (const float4 *)(a.S.act + (size_t)b * 32);
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const float4 f = src[j];
+            v[4 * j] = f.x; v[4 * j + 1] = f.y; v[4 * j + 2] = f.z; v[4 * j + 3] = f.w;
+        }
+        quant_store(b, v);
+    }
     for (;; rnd++) {
         /* this round's experts and their (contiguous) slot range */
         __shared__ int4 rw[EPR];
@@ -843,10 +1118,13 @@ __global__ __launch_bounds__(256) void down_exact_kernel(DownArgs a)
             srange[1] = hi;
         }
 #pragma unroll
-        for (int m = 0; m < MAXS; m++) ((u32x4 *)tile)[min(tid + 256 * m, nslot - 1)] = v[m];
+        for (int k = 0; k < EPR; k++)
+#pragma unroll
+            for (int j = 0; j < LPE; j++)
+                if (tid + 256 * j < spe) ((u32x4 *)tile)[k * spe + tid + 256 * j] = v[k * LPE + j];
         __syncthreads();
         const int s_lo = srange[0], s_hi = srange[1];
-        const bool in_lds = s_hi - s_lo <= a.lds_slots;
+        const bool in_lds = !a.qlds && s_hi - s_lo <= a.lds_slots;
         if (in_lds)
             for (int i = tid; i < (s_hi - s_lo) * (xrec >> 4); i += 256)
                 ((u32x4 *)xbuf)[i] = ((const u32x4 *)(a.S.aqk + (size_t)s_lo * xrec))[i];
@@ -857,7 +1135,8 @@ __global__ __launch_bounds__(256) void down_exact_kernel(DownArgs a)
         const int4 w = rw[k];
         if (w.x >= 0) {
             const uint8_t *row = tile + k * rbytes + rr * (int)a.rb;
-            const uint8_t *xs = in_lds ? xbuf + (size_t)(w.y - s_lo) * xrec : a.S.aqk + (size_t)w.y * xrec;
+            const uint8_t *xs = a.qlds ? xbuf + (size_t)w.y * xrec
+                                       : (in_lds ? xbuf + (size_t)(w.y - s_lo) * xrec : a.S.aqk + (size_t)w.y * xrec);
             for (int g0 = w.y; g0 < w.z; g0 += NT) {
                 const int nt = min(NT, w.z - g0);
                 RowAcc acc[NT];
@@ -907,6 +1186,25 @@ __global__ __launch_bounds__(256) void down_exact_kernel(DownArgs a)
     }
 }
 
+/* The int8 blocks of every slot's activations (src/model.c:996-997) for batches whose
+ * records do not fit the down kernel's LDS: one thread per 32-block. */
+__global__ void act_quant_kernel(Scratch S, int F, int NS)
+{
+    const int nbF = F >> 5;
+    const int b = blockIdx.x * blockDim.x + threadIdx.x;
+    if (b >= NS * nbF) return;
+    const int s = b / nbF, blk = b - s * nbF;
+    float v[32];
+    const float4 *src = (const float4 *)(S.act + (size_t)s * F + (size_t)blk * 32);
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+        const float4 f = src[j];
+        v[4 * j] = f.x; v[4 * j + 1] = f.y; v[4 * j + 2] = f.z; v[4 * j + 3] = f.w;
+    }
+    quantize_block_store(v, S.aq + b, (uint32_t *)(S.aqk + ((size_t)s * (nbF >> 1) + (blk >> 1)) * kPairBytes),
+                         blk & 1);
+}
+
 /* Weighted sum per token in selection order (src/model.c:1152-1162) when dn did not fit. */
 __global__ void combine_kernel(const Scratch S, int E, int K, int T, float *out)
 {
@@ -933,10 +1231,21 @@ hipError_t launch_down_exact(const Shape &s, const LayerDev &L, const Scratch &S
     a.out = out;
     a.S = S;
     const size_t tile = ((size_t)8 * 8 * L.down_rb + 16 + 15) & ~(size_t)15;
-    const size_t dnl = (size_t)T * s.K * 8 * 4;
+    if ((size_t)8 * L.down_rb / 16 > (size_t)256 * (L.down_type == 2 ? 2 : 3)) return hipErrorInvalidValue;
+    const int NS = T * s.K;
+    const size_t dnl = (size_t)NS * 8 * 4;
     const size_t xrec = (size_t)(s.F / 64) * kPairBytes;
-    a.lds_slots = T * s.K < 16 ? T * s.K : 16;
-    a.fuse = tile + a.lds_slots * xrec + dnl <= 120 * 1024;
+    /* quantise in the prologue when every slot's records fit with two blocks per CU */
+    a.qlds = tile + (size_t)NS * xrec + dnl <= 80 * 1024;
+    if (a.qlds) {
+        a.lds_slots = NS;
+        a.fuse = 1;
+    } else {
+        a.lds_slots = NS < 16 ? NS : 16;
+        a.fuse = tile + a.lds_slots * xrec + dnl <= 120 * 1024;
+        const int nq = NS * (s.F / 32);
+        QLAUNCH("actq", act_quant_kernel, dim3((nq + 255) / 256), dim3(256), 0, st, S, s.F, NS);
+    }
     const size_t lds = tile + a.lds_slots * xrec + (a.fuse ? dnl : 0);
     const int NT = T >= 4 ? 4 : (T >= 2 ? 2 : 1);
     const dim3 grid(s.E / 8);
