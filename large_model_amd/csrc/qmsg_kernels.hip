@@ -992,8 +992,9 @@ hipError_t launch_gateup_exact(const Shape &s, const LayerDev &L, const Scratch 
     a.debug = debug;
     a.S = S;
     const int nbE = s.E / 32, nP = nbE / 2;
-    /* chunk of CB blocks; the D = 2 chunks in flight need an even chunk count */
-    const int CB = nbE % 64 == 0 ? 32 : (nbE % 32 == 0 ? 16 : 8);
+    /* chunks of CB blocks, two in flight per wave (16-block chunks measured fastest for the
+     * 4096-wide rows: less in flight per wave lets the first chunks land sooner) */
+    const int CB = nbE % 32 == 0 ? 16 : 8;
     const int NT = T >= 4 ? 4 : (T >= 2 ? 2 : 1);
     const int maxact = s.X < T * s.K ? s.X : T * s.K;
     const int W = gateup_waves(s.F, maxact, n_cu);
@@ -1048,12 +1049,13 @@ __global__ __launch_bounds__(256) void down_exact_kernel(DownArgs a)
     int rnd = 0;
     /* round rnd covers active experts rnd*EPR .. rnd*EPR+7; work[] ends with expert -1. Every
      * load instruction reads one expert's rows (a uniform address base), LPE per expert. */
-#define QMSG_DLOAD(R)                                                                                \
-    _Pragma("unroll") for (int k_ = 0; k_ < EPR; k_++) {                                             \
+#define QMSG_DLOAD_K(R, K0, K1)                                                                      \
+    _Pragma("unroll") for (int k_ = (K0); k_ < (K1); k_++) {                                         \
         const int e_ = max(a.S.work[min((R) * EPR + k_, a.X - 1)].x, 0);                             \
         const u32x4 *src_ = (const u32x4 *)(a.down + (size_t)e_ * a.eb + (size_t)r0 * a.rb);         \
         _Pragma("unroll") for (int j_ = 0; j_ < LPE; j_++) v[k_ * LPE + j_] = src_[min(tid + 256 * j_, spe - 1)]; \
     }
+#define QMSG_DLOAD(R) QMSG_DLOAD_K(R, 0, EPR)
     /* Each int8 block of activations spans rows of two gate/up blocks, so with qlds it is
      * formed here, for every slot. The first QPRE blocks' inputs per thread are requested
      * before the weights (waits are in issue order), so they are quantised while the
@@ -1175,6 +1177,7 @@ __global__ __launch_bounds__(256) void down_exact_kernel(DownArgs a)
         if (!more) break;
     }
 #undef QMSG_DLOAD
+#undef QMSG_DLOAD_K
     if (!a.fuse) return;
     __syncthreads();
     for (int i = tid; i < a.T * RD; i += 256) {
@@ -1183,6 +1186,114 @@ __global__ __launch_bounds__(256) void down_exact_kernel(DownArgs a)
         for (int j = 0; j < K; j++)
             o = __builtin_fmaf(a.S.wt[(size_t)t * K + j], dnl[a.S.slot_of[(size_t)t * K + j] * RD + rr], o);
         a.out[(size_t)t * E + r0 + rr] = o;
+    }
+}
+
+/* One-token batch, Q4_0 down weights (K <= 8 experts, one slot each, slot j = j-th active
+ * expert): one block per 8 output rows r0 .. r0+7. Wave w owns active experts 2w and 2w+1
+ * (16 rows, one per lane quad) and streams exactly those rows in chunks of CB blocks, D chunks
+ * in flight, through its own LDS buffer, so its dots start as soon as its first bytes land.
+ * The prologue requests the first chunks, then quantises the K activation rows into int8
+ * pair records in LDS (block 0 also writes them out for the debug copy-back). The block ends
+ * with the weighted combine of its 8 rows in selection order (src/model.c:1152-1162). */
+template <int CB, int D>
+__global__ __launch_bounds__(256) void down_t1_kernel(DownArgs a)
+{
+    extern __shared__ __align__(16) uint8_t smem[];
+    constexpr int RD = 8;
+    constexpr int SPR = CB * 18 / 16;                 /* 16-byte slots per row per chunk      */
+    constexpr int NSL = 16 * SPR;                     /* slots of one wave's chunk            */
+    constexpr int SPT = (NSL + 63) / 64;              /* slots per lane per chunk             */
+    constexpr int WS = CB * 18 + ((SPR & 1) ? 0 : 16);/* LDS row stride, odd in 16-byte units */
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, qd = lane >> 2, p = lane & 3;
+    const int r0 = (int)blockIdx.x * RD, E = a.E, K = a.K, nbF = a.F >> 5, nPF = a.F >> 6;
+    const int nchunk = nbF / CB, xrec = nPF * kPairBytes;
+    uint8_t *wbuf = smem + wave * 16 * WS;
+    uint8_t *xbuf = smem + 4 * 16 * WS;               /* [K][xrec]                            */
+    float *dnl = (float *)(xbuf + (size_t)K * xrec);  /* [K][RD]                              */
+
+    /* the activations to quantise: 32 floats per int8 block, up to two blocks per thread */
+    const int nqb = K * nbF;
+    float4 av[2][8];
+#pragma unroll
+    for (int u = 0; u < 2; u++) {
+        const float4 *src = (const float4 *)(a.S.act + (size_t)min(tid + 256 * u, nqb - 1) * 32);
+#pragma unroll
+        for (int j = 0; j < 8; j++) av[u][j] = src[j];
+    }
+    /* this wave's experts (uniform): j0 = 2w, j1 = 2w+1 */
+    const int j0 = 2 * wave, j1 = j0 + 1;
+    const int e0 = j0 < K ? a.S.work[j0].x : -1, e1 = j1 < K ? a.S.work[j1].x : -1;
+    const uint8_t *b0 = a.down + (size_t)max(e0, 0) * a.eb + (size_t)r0 * a.rb;
+    const uint8_t *b1 = a.down + (size_t)max(e1, 0) * a.eb + (size_t)r0 * a.rb;
+    __builtin_amdgcn_sched_barrier(0);
+    u32x4 wv[D][SPT];
+    auto load_chunk = [&](int c, u32x4 *dst) {
+#pragma unroll
+        for (int m = 0; m < SPT; m++) {
+            const int i = min(lane + 64 * m, NSL - 1), row = i / SPR, j = i - row * SPR;
+            dst[m] = *(const u32x4 *)((row < 8 ? b0 + (size_t)row * a.rb : b1 + (size_t)(row - 8) * a.rb) +
+                                      (size_t)c * CB * 18 + 16 * j);
+        }
+    };
+    const bool active = e0 >= 0;
+    if (active) {
+#pragma unroll
+        for (int d = 0; d < D; d++)
+            if (d < nchunk) load_chunk(d, wv[d]);
+    }
+#pragma unroll
+    for (int u = 0; u < 2; u++) {
+        const int b = tid + 256 * u;
+        if (b < nqb) {
+            float v[32];
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+                v[4 * j] = av[u][j].x; v[4 * j + 1] = av[u][j].y; v[4 * j + 2] = av[u][j].z; v[4 * j + 3] = av[u][j].w;
+            }
+            const int s = b / nbF, blk = b - s * nbF;
+            const Q8Vals q = quantize_block(v);
+            store_pair_half(q, (uint32_t *)(xbuf + (size_t)s * xrec + (size_t)(blk >> 1) * kPairBytes), blk & 1);
+            if (blockIdx.x == 0) {
+                store_q8(q, a.S.aq + b);
+                store_pair_half(q, (uint32_t *)(a.S.aqk + ((size_t)s * (nbF >> 1) + (blk >> 1)) * kPairBytes), blk & 1);
+            }
+        }
+    }
+    __syncthreads();
+    if (active) {
+        /* quad qd: expert j0 + qd/8, row r0 + qd%8; its slot is its active index */
+        const int jq = j0 + (qd >> 3), rr = qd & 7;
+        const uint8_t *xq = xbuf + (size_t)min(jq, K - 1) * xrec;
+        RowAcc acc[1] = { RowAcc{ 0.0f, 0.0f, 0.0f } };
+        for (int c0 = 0; c0 < nchunk; c0 += D) {
+#pragma unroll
+            for (int d = 0; d < D; d++) {
+                const int c = c0 + d;
+                if (c < nchunk) {
+                    wave_sync();
+#pragma unroll
+                    for (int m = 0; m < SPT; m++) {
+                        const int i = min(lane + 64 * m, NSL - 1), row = i / SPR, j = i - row * SPR;
+                        *(u32x4 *)(wbuf + row * WS + 16 * j) = wv[d][m];
+                    }
+                    wave_sync();
+                    if (c + D < nchunk) load_chunk(c + D, wv[d]);
+                    q4_0_rows<1, 4>((const uint32_t *)(wbuf + qd * WS), p, xq, (size_t)xrec, c * (CB / 2), CB / 2, 1, acc);
+                }
+            }
+        }
+        const float v = quad_finish(acc[0], 8.0f);
+        if (p == 0 && jq < K) {
+            a.S.dn[(size_t)jq * E + r0 + rr] = v;
+            dnl[jq * RD + rr] = v;
+        }
+    }
+    __syncthreads();
+    if (tid < RD) {
+        float o = 0.0f;
+        for (int j = 0; j < K; j++) o = __builtin_fmaf(a.S.wt[j], dnl[a.S.slot_of[j] * RD + tid], o);
+        a.out[r0 + tid] = o;
     }
 }
 
@@ -1230,6 +1341,16 @@ hipError_t launch_down_exact(const Shape &s, const LayerDev &L, const Scratch &S
     a.X = s.X;
     a.out = out;
     a.S = S;
+    if (T == 1 && s.K <= 8 && L.down_type == 2 && s.F % 256 == 0) {
+        /* one token: each wave streams its own two experts' rows (Q4_0) */
+        const int nbF = s.F / 32, CB = nbF % 16 == 0 ? 16 : 8;
+        const size_t xrec = (size_t)(s.F / 64) * kPairBytes;
+        const size_t ws = (size_t)CB * 18 + (((CB * 18 / 16) & 1) ? 0 : 16);
+        const size_t lds = 4 * 16 * ws + (size_t)s.K * xrec + (size_t)s.K * 8 * 4;
+        if (CB == 16) QLAUNCH("down", (down_t1_kernel<16, 2>), dim3(s.E / 8), dim3(256), lds, st, a);
+        else QLAUNCH("down", (down_t1_kernel<8, 2>), dim3(s.E / 8), dim3(256), lds, st, a);
+        return hipGetLastError();
+    }
     const size_t tile = ((size_t)8 * 8 * L.down_rb + 16 + 15) & ~(size_t)15;
     if ((size_t)8 * L.down_rb / 16 > (size_t)256 * (L.down_type == 2 ? 2 : 3)) return hipErrorInvalidValue;
     const int NS = T * s.K;
