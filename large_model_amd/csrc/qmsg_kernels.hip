@@ -635,13 +635,11 @@ struct alignas(16) SmallRoute {
  * both rankings; this is checked, and if a rounding tie shows up (logits of different value
  * with equal p), wave 0 ranks the p exactly instead. Weights are renormalised with wsum in
  * selection order; the slots of the token are its experts in ascending order.
- * Shared scratch (LDS): L[X] floats, P[X] doubles, rank[X], selidx[X], start[X+1]. Ends with
- * a block barrier; block (0, 0) also publishes the result for the down kernel and the debug
- * copy-back. */
-__device__ void route_one(const Scratch &S, int K, int X, SmallRoute *R, float *L, double *P, int *rank, int *selidx,
-                          int *start)
+ * Shared scratch (LDS): L[X] floats, P[X] doubles, rank[X], selidx[X], start[X+1]. This
+ * first half (softmax and logit ranks) ends with a block barrier. */
+__device__ void route_one_rank(const Scratch &S, int X, float *L, double *P, int *rank, int *selidx)
 {
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, nw = blockDim.x >> 6;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     for (int e = tid; e < X; e += blockDim.x) {
         L[e] = S.logits[e];
         rank[e] = 0;
@@ -703,6 +701,36 @@ __device__ void route_one(const Scratch &S, int K, int X, SmallRoute *R, float *
         }
     }
     __syncthreads();
+}
+
+/* The y-th smallest expert id among the K first of the logit order (every wave forms it):
+ * the expert a gate/up block of a one-token batch almost always gets, known before the
+ * exact selection is. */
+__device__ int spec_expert(const int *rank, int X, int K, int y)
+{
+    const int lane = threadIdx.x & 63;
+    int below = 0, found = 0;
+    for (int e0 = 0; e0 < X; e0 += 64) {
+        const int e = e0 + lane;
+        const unsigned long long m = __ballot(e < X && rank[e] < K);
+        const int c = __popcll(m);
+        if (y >= below && y < below + c) {
+            /* the (y - below)-th set bit of m */
+            const int pos = below + __popcll(m & ((1ULL << lane) - 1ULL));
+            const unsigned long long hit = __ballot(e < X && rank[e] < K && pos == y);
+            found = e0 + (int)__builtin_ctzll(hit);
+        }
+        below += c;
+    }
+    return found;
+}
+
+/* Second half of the one-token routing: the exact top K (with the rounding-tie check),
+ * weights, slots and the published scratch arrays; ends with a block barrier. */
+__device__ void route_one_select(const Scratch &S, int K, int X, SmallRoute *R, float *L, double *P, int *rank,
+                                 int *selidx, int *start)
+{
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     if (wave == 0) {
         int *cand = R->cand;
         for (int e = lane; e < X; e += 64)
@@ -853,25 +881,50 @@ __global__ __launch_bounds__(64 * W) void gateup_kernel(GateUpArgs a)
 #pragma unroll
         for (int m = 0; m < XS; m++) xv[m] = ((const u32x4 *)a.S.xqk)[min(tid + NTH * m, xsl - 1)];
     }
+    const int r0 = (int)blockIdx.x * R, rw = r0 + 8 * wave;     /* this wave's first row */
+    const uint8_t *gbase, *ubase;
+    u32x4 wv[D][SPT];
+    auto load_chunk = [&](int c, u32x4 *dst) {
+#pragma unroll
+        for (int m = 0; m < SPT; m++) {
+            const int i = min(lane + 64 * m, NSL - 1), row = i / SPR, j = i - row * SPR;
+            dst[m] = *(const u32x4 *)((row < 8 ? gbase + (size_t)row * a.rb : ubase + (size_t)(row - 8) * a.rb) +
+                                      (size_t)c * CB * 18 + 16 * j);
+        }
+    };
+    auto set_expert = [&](int ex) {
+        gbase = a.gate + (size_t)ex * a.eb + (size_t)rw * a.rb;
+        ubase = a.up + (size_t)ex * a.eb + (size_t)rw * a.rb;
+    };
     int4 wk;
     const int *slot_t = a.S.slot_t;
+    bool prefetched = false;
     if constexpr (SEL) {
         SmallRoute *sr = (SmallRoute *)(res + NT * 2 * R);
         double *P = (double *)(sr + 1);
         float *L = (float *)(P + kMaxExperts);
         int *rank = (int *)(L + kMaxExperts);
-        route_one(a.S, a.K, a.X, sr, L, P, rank, rank + kMaxExperts, rank + 2 * kMaxExperts);
+        route_one_rank(a.S, a.X, L, P, rank, rank + kMaxExperts);
+        /* start streaming the expert the logit order points at while the exact selection
+         * finishes; the rare block whose expert changes reloads below */
+        const int e_spec = spec_expert(rank, a.X, a.K, (int)blockIdx.y);
+        set_expert(e_spec);
+        if (wave > 0) {                    /* wave 0 finishes the selection first */
+#pragma unroll
+            for (int d = 0; d < D; d++)
+                if (d < nchunk) load_chunk(d, wv[d]);
+        }
+        route_one_select(a.S, a.K, a.X, sr, L, P, rank, rank + kMaxExperts, rank + 2 * kMaxExperts);
         if ((int)blockIdx.y >= sr->na) return;
         wk = sr->work[blockIdx.y];
         slot_t = sr->slot_t;
+        prefetched = wk.x == e_spec && wave > 0;
     } else {
         wk = a.S.work[blockIdx.y];
         if (wk.x < 0) return;
     }
     const int e = wk.x, s_begin = wk.y, s_end = wk.z;
-    const int r0 = (int)blockIdx.x * R, rw = r0 + 8 * wave;     /* this wave's first row */
-    const uint8_t *gbase = a.gate + (size_t)e * a.eb + (size_t)rw * a.rb;
-    const uint8_t *ubase = a.up + (size_t)e * a.eb + (size_t)rw * a.rb;
+    if (!prefetched) set_expert(e);
     const int F = a.F;
     const int rho = qd < 8 ? 8 * wave + qd : R + 8 * wave + (qd - 8);   /* tile row of this quad */
     const bool tok_bytes = a.T <= 256;              /* work.w holds the first four tokens */
@@ -894,18 +947,11 @@ __global__ __launch_bounds__(64 * W) void gateup_kernel(GateUpArgs a)
         __syncthreads();
         RowAcc acc[NT];
         for (int n = 0; n < NT; n++) acc[n] = RowAcc{ 0.0f, 0.0f, 0.0f };
-        u32x4 wv[D][SPT];
-        auto load_chunk = [&](int c, u32x4 *dst) {
+        if (!(prefetched && g0 == s_begin)) {
 #pragma unroll
-            for (int m = 0; m < SPT; m++) {
-                const int i = min(lane + 64 * m, NSL - 1), row = i / SPR, j = i - row * SPR;
-                dst[m] = *(const u32x4 *)((row < 8 ? gbase + (size_t)row * a.rb : ubase + (size_t)(row - 8) * a.rb) +
-                                          (size_t)c * CB * 18 + 16 * j);
-            }
-        };
-#pragma unroll
-        for (int d = 0; d < D; d++)
-            if (d < nchunk) load_chunk(d, wv[d]);
+            for (int d = 0; d < D; d++)
+                if (d < nchunk) load_chunk(d, wv[d]);
+        }
         for (int c0 = 0; c0 < nchunk; c0 += D) {
 #pragma unroll
             for (int d = 0; d < D; d++) {
