@@ -205,44 +205,54 @@ __device__ __forceinline__ float chain16_sum(float acc)
 }
 
 /* Router for T <= 4: one block per expert, 256 threads. The expert's router row and the T
- * input rows are staged into LDS with every load in flight; lane (t, c) of wave 0 then runs
- * the reference's FMA chain c (elements c, c+16, ...) of token t (src/kernels.c:202-213). */
+ * input rows are requested in four chunks, all in flight at once; as each chunk lands it is
+ * staged into LDS and lane (t, c) of wave 0 advances the reference's FMA chain c (elements c,
+ * c+16, ...) of token t over it (src/kernels.c:202-213), so the chains run while the later
+ * chunks are still arriving. */
+template <int T>
 __global__ __launch_bounds__(256) void route_small_kernel(RouteArgs a)
 {
     extern __shared__ __align__(16) uint8_t smem[];
     if ((int)blockIdx.x >= a.n_route_wg) { route_quantize(a); return; }
-    const int tid = threadIdx.x, E = a.E, T = a.T, e = blockIdx.x;
+    constexpr int NCH = 4, MPC = 1 + T;          /* chunks; loads per thread per chunk (E <= 4096) */
+    const int tid = threadIdx.x, E = a.E, e = blockIdx.x;
     const int XS = E + 16;                       /* padded x rows: lanes of different t hit other banks */
     float *wrow = (float *)smem, *xr = wrow + E;
-    const int nw = E / 4, nslot = nw * (1 + T);
+    const int cw = E / (4 * NCH);                /* 16-byte slots of one row per chunk */
+    const int sc = cw * (1 + T);                 /* slots of one chunk */
     const u32x4 *wsrc = (const u32x4 *)(a.router + (size_t)e * E);
     const u32x4 *xsrc = (const u32x4 *)a.xn;
-    for (int base = 0; base < nslot; base += 256 * 20) {
-        u32x4 v[20];
+    auto slot_src = [&](int c, int i) -> const u32x4 * {
+        const int r = i / cw, j = c * cw + (i - r * cw);       /* r = 0: router row, r >= 1: input t = r-1 */
+        return r == 0 ? wsrc + j : xsrc + (size_t)(r - 1) * (E / 4) + j;
+    };
+    auto slot_dst = [&](int c, int i) -> float * {
+        const int r = i / cw, j = c * cw + (i - r * cw);
+        return r == 0 ? wrow + 4 * j : xr + (r - 1) * XS + 4 * j;
+    };
+    u32x4 v[NCH][MPC];
 #pragma unroll
-        for (int m = 0; m < 20; m++) {
-            const int i = min(base + tid + 256 * m, nslot - 1);
-            v[m] = i < nw ? wsrc[i] : xsrc[i - nw];
-        }
+    for (int c = 0; c < NCH; c++)
 #pragma unroll
-        for (int m = 0; m < 20; m++) {
-            const int i = min(base + tid + 256 * m, nslot - 1);
-            float *dst = i < nw ? wrow + 4 * i : xr + ((i - nw) / nw) * XS + 4 * ((i - nw) % nw);
-            *(u32x4 *)dst = v[m];
+        for (int m = 0; m < MPC; m++) v[c][m] = *slot_src(c, min(tid + 256 * m, sc - 1));
+    const int t = tid >> 4, cc = tid & 15;
+    float acc = 0.0f;
+#pragma unroll
+    for (int c = 0; c < NCH; c++) {
+#pragma unroll
+        for (int m = 0; m < MPC; m++)
+            if (tid + 256 * m < sc) *(u32x4 *)slot_dst(c, tid + 256 * m) = v[c][m];
+        __syncthreads();
+        if (tid < 16 * T) {
+            const float *xrow = xr + t * XS;
+            const int i1 = (c + 1) * (E / NCH);
+#pragma unroll 16
+            for (int i = c * (E / NCH) + cc; i < i1; i += 16) acc = __builtin_fmaf(wrow[i], xrow[i], acc);
         }
     }
-    __syncthreads();
     if (tid < 16 * T) {
-        const int t = tid >> 4, c = tid & 15, E16 = E & ~15;
-        const float *xrow = xr + t * XS;
-        float acc = 0.0f;
-#pragma unroll 16
-        for (int i = c; i < E16; i += 16) acc = __builtin_fmaf(wrow[i], xrow[i], acc);
         acc = chain16_sum(acc);
-        if (c == 0) {
-            for (int i = E16; i < E; i++) acc = __builtin_fmaf(wrow[i], xrow[i], acc);
-            a.S.logits[(size_t)t * a.X + e] = acc;
-        }
+        if (cc == 0) a.S.logits[(size_t)t * a.X + e] = acc;
     }
 }
 
@@ -318,10 +328,14 @@ hipError_t launch_route(const Shape &s, const LayerDev &L, const Scratch &S, con
     a.T = T;
     a.S = S;
     const int nq = (T * (s.E / 32) + 255) / 256;
-    if (T <= 4) {
+    if (T <= 4 && s.E <= 4096) {
         a.n_route_wg = s.X;
         const size_t lds = (size_t)(s.E + T * (s.E + 16)) * 4;
-        QLAUNCH("route", route_small_kernel, dim3(a.n_route_wg + nq), dim3(256), lds, st, a);
+        const dim3 grid(a.n_route_wg + nq);
+        if (T == 1) QLAUNCH("route", route_small_kernel<1>, grid, dim3(256), lds, st, a);
+        else if (T == 2) QLAUNCH("route", route_small_kernel<2>, grid, dim3(256), lds, st, a);
+        else if (T == 3) QLAUNCH("route", route_small_kernel<3>, grid, dim3(256), lds, st, a);
+        else QLAUNCH("route", route_small_kernel<4>, grid, dim3(256), lds, st, a);
     } else {
         a.n_route_wg = ((T + 15) / 16) * (s.X / 16);
         const size_t lds = (size_t)2 * 16 * (256 + 4) * 4;
