@@ -199,7 +199,7 @@ def main():
     ctx.sync()
     log(f"with per-dispatch events: {1e6 * (time.perf_counter() - t0) / K_steps:.2f} us/step")
     kern = {}
-    for name in ("route", "select", "dispatch", "gateup", "down", "combine"):
+    for name in ("route", "select", "dispatch", "gateup", "actq", "down", "combine"):
         n, ms = ctx.profile_read(name)
         if n:
             kern[name] = {"launches": n, "avg_us": round(1e3 * ms / n, 3)}
@@ -240,7 +240,7 @@ def main():
             "resident_layers_cycled": NL, "path": args.path,
         },
         "roofline": {
-            "kernel": "gateup (gate/up Q4_0 row dots + SwiGLU + int8 requantise)",
+            "kernel": "gateup (routing of the token, gate/up Q4_0 row dots, SwiGLU)",
             "bound": "hbm",
             "achieved": round(achieved, 1) if achieved else None,
             "peak": HBM_PEAK_GBS,

@@ -21,8 +21,9 @@ import sys
 
 SHORT = (
     ("route_small_kernel", "route"), ("route_big_kernel", "route"), ("select_kernel", "select"),
-    ("dispatch_kernel", "dispatch"), ("gateup_exact_kernel", "gateup"), ("down_exact_kernel", "down"),
-    ("combine_kernel", "combine"), ("copy_kernel", "copy"),
+    ("dispatch_kernel", "dispatch"), ("gateup_kernel", "gateup"), ("down_exact_kernel", "down"),
+    ("down_t1_kernel", "down"), ("act_quant_kernel", "actq"), ("combine_kernel", "combine"),
+    ("copy_kernel", "copy"),
 )
 
 

@@ -36,7 +36,8 @@ def golden_input(d):
     return x
 
 
-DEVICE_GOLD = ["tiny_t1", "tiny_t7", "q30b_t1", "q235b_t1", "q235b_t4", "q235b_t16", "q235b_q6k_t64"]
+DEVICE_GOLD = ["tiny_t1", "tiny_t7", "q30b_t1", "q235b_t1", "q235b_t4", "q235b_t16", "q235b_q6k_t64",
+               "q235b_zipf_t512"]
 
 
 @pytest.mark.parametrize("name", DEVICE_GOLD)
@@ -46,9 +47,10 @@ def test_device_layer_equals_reference_output(q, name):
     E, X, K, F, T, seed, dt, rms = (int(v) for v in d["shape"])
     print(f"[case] golden {name} T={T}", flush=True)
     x = golden_input(d)
+    col0 = d.get("router_col0")
     with q.Context(E, X, K, F, n_layer=1, max_tokens=T) as ctx:
         ctx.set_path(q.PATH_EXACT)
-        ctx.synth(0, seed, down_type=dt)
+        ctx.synth(0, seed, down_type=dt, router_col0=col0)
         out = ctx.moe(0, x)
     assert sha(out) == bytes(d["out_sha"])
 
