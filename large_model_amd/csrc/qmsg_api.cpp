@@ -155,6 +155,7 @@ int qmsg_create(qmsg_ctx **out, int device, const qmsg_cfg *cfg, int n_layer, in
         { (void **)&c->S.slot_of, NS * 4 },     { (void **)&c->S.start, (size_t)(X + 1) * 4 },
         { (void **)&c->S.active, (size_t)X * 4 }, { (void **)&c->S.meta, 64 },
         { (void **)&c->S.work, (size_t)X * 16 },
+        { (void **)&c->S.tiles, ((size_t)X + NS / kTileN + 1) * 16 },
         { (void **)&c->S.xq, Tm * nbE * sizeof(Q8) }, { (void **)&c->S.xqk, Tm * (nbE / 2) * kPairBytes },
         { (void **)&c->S.gu, NS * 2 * F * 4 },  { (void **)&c->S.act, NS * F * 4 },
         { (void **)&c->S.aq, NS * nbF * sizeof(Q8) }, { (void **)&c->S.aqk, NS * (nbF / 2) * kPairBytes },
@@ -206,7 +207,6 @@ int qmsg_set_path(qmsg_ctx *c, int path)
     if (!c) return QMSG_E_INVALID;
     if (path != QMSG_PATH_AUTO && path != QMSG_PATH_EXACT && path != QMSG_PATH_MFMA)
         return fail(c, QMSG_E_INVALID, "qmsg_set_path: unknown path %d", path);
-    if (path == QMSG_PATH_MFMA) return fail(c, QMSG_E_UNSUPPORTED, "qmsg_set_path: the MFMA path is not built");
     c->path = path;
     return QMSG_OK;
 }
@@ -355,10 +355,18 @@ static int run_layer(qmsg_ctx *c, int layer, const float *d_xn, int T, float *d_
         return fail(c, QMSG_E_INVALID, "device buffers must be 16-byte aligned (xn) and 4-byte aligned (out)");
     const Shape s{ c->cfg.n_embd, c->cfg.n_expert, c->cfg.n_used, c->cfg.n_ff_exp };
     const LayerDev d = layer_dev(c, L);
+    /* the MFMA grouped GEMM takes Q4_0 gate/up weights and batches routed by the select kernel */
+    const bool mfma = d.gate_type == QMSG_T_Q4_0 && d.up_type == QMSG_T_Q4_0 && !use_small_route(T, s.K) &&
+                      s.E % 256 == 0 && s.F % 256 == 0 &&
+                      (c->path == QMSG_PATH_MFMA || (c->path == QMSG_PATH_AUTO && T >= kMfmaMinT));
     LAUNCH(c, "route", launch_route(s, d, c->S, d_xn, T, c->stream));
     LAUNCH(c, "select", launch_select(s, c->S, T, c->stream));
-    LAUNCH(c, "gateup", launch_gateup_exact(s, d, c->S, T, debug, c->n_cu, c->stream));
-    LAUNCH(c, "down", launch_down_exact(s, d, c->S, d_out, T, c->stream));
+    if (mfma) {
+        LAUNCH(c, "experts", launch_experts_mfma(s, d, c->S, d_out, T, debug, c->stream));
+    } else {
+        LAUNCH(c, "gateup", launch_gateup_exact(s, d, c->S, T, debug, c->n_cu, c->stream));
+        LAUNCH(c, "down", launch_down_exact(s, d, c->S, d_out, T, c->stream));
+    }
     return QMSG_OK;
 }
 

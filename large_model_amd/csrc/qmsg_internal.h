@@ -39,6 +39,11 @@ extern thread_local const LaunchTimer *g_launch_timer;
 /* Static shape limits of the kernels. */
 constexpr int kMaxExperts = 256;
 
+/* Slots (tokens of one expert) per tile of the MFMA grouped-GEMM kernels, and the batch size
+ * from which QMSG_PATH_AUTO takes them. */
+constexpr int kTileN = 32;
+constexpr int kMfmaMinT = 64;
+
 /* One-token batches (n_used <= 8) are routed inside the gate/up kernel instead of by a
  * separate select launch. */
 inline int use_small_route(int T, int K) { return T == 1 && K <= 8; }
@@ -64,7 +69,8 @@ struct Scratch {
     int32_t *start;     /* [X+1]               */
     int32_t *active;    /* [X]                 */
     int4 *work;         /* [X] per active expert: {expert, first slot, end slot, 0}; expert -1 after */
-    int32_t *meta;      /* [0] n_active */
+    int4 *tiles;        /* [X + Tm*K/kTileN + 1] slot tiles of the MFMA kernels: {expert, first, end, 0} */
+    int32_t *meta;      /* [0] n_active, [1] number of slot tiles */
     Q8 *xq;             /* [Tm][E/32]          */
     uint8_t *xqk;       /* [Tm][E/64][96]      */
     float *gu;          /* [Tm*K][2F]          */
@@ -83,6 +89,8 @@ hipError_t launch_route(const Shape &s, const LayerDev &L, const Scratch &S, con
                         hipStream_t st);
 hipError_t launch_select(const Shape &s, const Scratch &S, int T, hipStream_t st);
 hipError_t launch_gateup_exact(const Shape &s, const LayerDev &L, const Scratch &S, int T, int debug, int n_cu,
+                               hipStream_t st);
+hipError_t launch_experts_mfma(const Shape &s, const LayerDev &L, const Scratch &S, float *out, int T, int debug,
                                hipStream_t st);
 hipError_t launch_down_exact(const Shape &s, const LayerDev &L, const Scratch &S, float *out, int T,
                              hipStream_t st);

@@ -491,6 +491,20 @@ __device__ void dispatch_slots(const SelectArgs &a, int *cnt, int *cur, int *tok
             wpos++;
         }
     }
+    /* slot tiles of at most kTileN slots of one expert, experts ascending (MFMA kernels) */
+    int nt = 0;
+#pragma unroll
+    for (int i = 0; i < NPL; i++) nt += (c[i] + kTileN - 1) / kTileN;
+    const int incl_t = wave_scan_add(nt);
+    int tpos = incl_t - nt;
+#pragma unroll
+    for (int i = 0; i < NPL; i++) {
+        const int e = lane * NPL + i;
+        if (e < X)
+            for (int b = 0; b < c[i]; b += kTileN)
+                a.S.tiles[tpos++] = make_int4(e, cnt[e] + b, cnt[e] + min(c[i], b + kTileN), 0);
+    }
+    if (lane == 63) a.S.meta[1] = incl_t;
 }
 
 /* Top-K of one token per block; a single-block launch (T == 1) also sorts the slots. */
@@ -1444,6 +1458,243 @@ hipError_t launch_down_exact(const Shape &s, const LayerDev &L, const Scratch &S
         QLAUNCH("combine", combine_kernel, dim3((n + 255) / 256), dim3(256), 0, st, S, s.E, s.K, T, out);
     }
     return hipGetLastError();
+}
+
+/* ------------------------------------------------------------------ MFMA grouped GEMM ---- */
+
+/* Prefill-sized batches: the expert products as int8 MFMA tiles (v_mfma_i32_16x16x32_i8, one
+ * 32-block of K per instruction). Per 32-block the instruction gives the exact signed block
+ * dot D = sum (q - 8) * x (unsigned nibbles, then a second MFMA with a constant -8 operand
+ * adds -8 * sum x), and the fp32 row value accumulates D * d_w * d_x block by block. Block
+ * dots are bit-exact; the fp32 sums are in another order than the reference's per-lane chains
+ * (agreement to rounding), so this path trades the order-exact fp32 for MFMA throughput.
+ *
+ * A block computes 64 weight rows x kTileN slots of one expert; wave w owns tile rows
+ * 16w .. 16w+15 and both 16-slot halves. K is staged through LDS in chunks of kMKC blocks,
+ * double-buffered, the next chunk's loads in flight during the current chunk's MFMAs.
+ * Lane layout of the 16x16x32 i8 MFMA: A[row = l%16][k = 8(l/16) .. +7],
+ * B[k = 8(l/16) .. +7][col = l%16], C[row = 4(l/16) + i][col = l%16]. */
+typedef int v4i __attribute__((ext_vector_type(4)));
+constexpr int kMKC = 8;
+
+struct MfmaArgs {
+    const uint8_t *w0, *w1;     /* gate, up (gate/up kernel); down (down kernel, w1 unused) */
+    uint64_t rb, eb;
+    int E, F, K, X, debug;
+    Scratch S;
+};
+
+/* Eight bytes at an even LDS byte address (three aligned reads). */
+__device__ __forceinline__ uint64_t lds_u64_even(const uint8_t *base, uint32_t a)
+{
+    const uint32_t *w = (const uint32_t *)(base + (a & ~3u));
+    const uint32_t s = a & 3u, d0 = w[0], d1 = w[1], d2 = w[2];
+    return (uint64_t)__builtin_amdgcn_alignbyte(d1, d0, s) | ((uint64_t)__builtin_amdgcn_alignbyte(d2, d1, s) << 32);
+}
+
+/* The lane's A operand from a Q4_0 block in LDS (18 bytes at byte offset `off`): k-group g
+ * takes elements 8g .. 8g+7, i.e. low nibbles of qs[0..7] / qs[8..15] for g = 0 / 1 and the
+ * high nibbles of the same bytes for g = 2 / 3 (src/kernels.c:8-13). */
+__device__ __forceinline__ long q4_a_operand(const uint8_t *tile, uint32_t off, int g)
+{
+    const uint64_t w = lds_u64_even(tile, off + 2 + 8 * (g & 1));
+    const int sh = 4 * (g >> 1);
+    const uint32_t lo = ((uint32_t)w >> sh) & 0x0f0f0f0fu, hi = ((uint32_t)(w >> 32) >> sh) & 0x0f0f0f0fu;
+    return (long)((uint64_t)lo | ((uint64_t)hi << 32));
+}
+
+/* One 64-row x kTileN-slot tile over K = nb 32-blocks. A rows come from `arow(row)` (18-byte
+ * Q4_0 blocks), B from kTileN Q8 records per block found by `brec(slot)` (44 bytes each, the
+ * slot's block 0; records of one slot are contiguous). y[jt][i]: row 16w + 4g + i, slot
+ * 16jt + l%16 of the tile. */
+template <class ARow, class BRec>
+__device__ __forceinline__ void mfma_tile(int nb, ARow arow, BRec brec, uint8_t *As, uint8_t *Bs, float y[2][4])
+{
+    constexpr int AS = 64 * kMKC * 18 / 16, BS = kTileN * kMKC * 44 / 16;   /* 16-byte slots per chunk */
+    constexpr int AM = (AS + 255) / 256, BM = (BS + 255) / 256;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, g = lane >> 4, lr = lane & 15;
+    const int nch = nb / kMKC;
+    u32x4 va[AM], vb[BM];
+    auto load = [&](int c) {
+#pragma unroll
+        for (int m = 0; m < AM; m++) {
+            const int i = min(tid + 256 * m, AS - 1), row = i / (kMKC * 18 / 16), j = i - row * (kMKC * 18 / 16);
+            va[m] = *(const u32x4 *)(arow(row) + (size_t)c * kMKC * 18 + 16 * j);
+        }
+#pragma unroll
+        for (int m = 0; m < BM; m++) {
+            const int i = min(tid + 256 * m, BS - 1), sl = i / (kMKC * 44 / 16), j = i - sl * (kMKC * 44 / 16);
+            vb[m] = *(const u32x4 *)(brec(sl) + (size_t)c * kMKC * 44 + 16 * j);
+        }
+    };
+    auto store = [&](int buf) {
+#pragma unroll
+        for (int m = 0; m < AM; m++)
+            if (tid + 256 * m < AS) *(u32x4 *)(As + buf * AS * 16 + 16 * (tid + 256 * m)) = va[m];
+#pragma unroll
+        for (int m = 0; m < BM; m++)
+            if (tid + 256 * m < BS) *(u32x4 *)(Bs + buf * BS * 16 + 16 * (tid + 256 * m)) = vb[m];
+    };
+#pragma unroll
+    for (int jt = 0; jt < 2; jt++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) y[jt][i] = 0.0f;
+    const long m8 = (long)0xf8f8f8f8f8f8f8f8ULL;            /* -8 in every byte */
+    load(0);
+    store(0);
+    __syncthreads();
+    for (int c = 0; c < nch; c++) {
+        const int buf = c & 1;
+        if (c + 1 < nch) load(c + 1);
+        const uint8_t *A = As + buf * AS * 16, *B = Bs + buf * BS * 16;
+#pragma unroll 2
+        for (int b = 0; b < kMKC; b++) {
+            const long aop = q4_a_operand(A, (uint32_t)((16 * wave + lr) * kMKC * 18 + b * 18), g);
+            float dw[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+                dw[i] = h2f(*(const uint16_t *)(A + (16 * wave + 4 * g + i) * kMKC * 18 + b * 18));
+#pragma unroll
+            for (int jt = 0; jt < 2; jt++) {
+                const uint8_t *xr = B + (16 * jt + lr) * kMKC * 44 + b * 44;
+                const uint32_t *xq = (const uint32_t *)(xr + 12 + 8 * g);
+                const long bop = (long)((uint64_t)xq[0] | ((uint64_t)xq[1] << 32));
+                const float dx = *(const float *)xr;
+                v4i d = { 0, 0, 0, 0 };
+                d = __builtin_amdgcn_mfma_i32_16x16x32_i8(aop, bop, d, 0, 0, 0);
+                d = __builtin_amdgcn_mfma_i32_16x16x32_i8(m8, bop, d, 0, 0, 0);
+#pragma unroll
+                for (int i = 0; i < 4; i++) y[jt][i] = __builtin_fmaf((float)d[i], dw[i] * dx, y[jt][i]);
+            }
+        }
+        if (c + 1 < nch) store(buf ^ 1);
+        __syncthreads();
+    }
+}
+
+/* Gate/up of one slot tile: 32 gate rows (tile rows 0-31) and the same 32 up rows (32-63),
+ * then a = silu(g)*u and, since the 32 gate rows are one int8 block of the activations, the
+ * quantised block of each slot (src/model.c:989-997). */
+__global__ __launch_bounds__(256) void gateup_mfma_kernel(MfmaArgs a)
+{
+    __shared__ __align__(16) uint8_t As[2 * 64 * kMKC * 18 + 16];   /* +16: the A reads' 12-byte windows */
+    __shared__ __align__(16) uint8_t Bs[2 * kTileN * kMKC * 44];
+    __shared__ int toks[kTileN];
+    __shared__ float res[64][kTileN + 1];
+    if ((int)blockIdx.y >= a.S.meta[1]) return;
+    const int4 tl = a.S.tiles[blockIdx.y];
+    const int e = tl.x, s0 = tl.y, ns = tl.z - tl.y;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, g = lane >> 4, lr = lane & 15;
+    const int r0 = (int)blockIdx.x * 32, nbE = a.E >> 5, nbF = a.F >> 5, F = a.F;
+    if (tid < kTileN) toks[tid] = a.S.slot_t[s0 + min(tid, ns - 1)];
+    __syncthreads();
+    const uint8_t *g0 = a.w0 + (size_t)e * a.eb + (size_t)r0 * a.rb, *u0 = a.w1 + (size_t)e * a.eb + (size_t)r0 * a.rb;
+    const uint8_t *xq = (const uint8_t *)a.S.xq;
+    float y[2][4];
+    mfma_tile(nbE, [&](int row) { return (row < 32 ? g0 : u0) + (size_t)(row & 31) * a.rb; },
+              [&](int sl) { return xq + (size_t)toks[sl] * nbE * 44; }, As, Bs, y);
+#pragma unroll
+    for (int jt = 0; jt < 2; jt++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) res[16 * wave + 4 * g + i][16 * jt + lr] = y[jt][i];
+    __syncthreads();
+    /* half-wave per slot: lane r of the half holds row r0 + r */
+    const int hw = tid >> 5, r = tid & 31, hb = lane & 32;
+    const int blk = r0 >> 5, half = blk & 1;
+    for (int sl = hw; sl < ns; sl += 8) {
+        const int s = s0 + sl;
+        const float gv = res[r][sl], uv = res[32 + r][sl];
+        const float av = silu_ref(gv) * uv;
+        a.S.act[(size_t)s * F + r0 + r] = av;
+        if (a.debug) {
+            a.S.gu[(size_t)s * 2 * F + r0 + r] = gv;
+            a.S.gu[(size_t)s * 2 * F + F + r0 + r] = uv;
+        }
+        float amax = fabsf(av);
+        for (int o = 16; o > 0; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o));
+        const float d = amax / 127.0f;
+        const float id = d > 0.0f ? 1.0f / d : 0.0f;
+        const int qi = (int)rintf(av * id);
+        int sum = qi;
+        for (int o = 8; o > 0; o >>= 1) sum += __shfl_xor(sum, o);   /* 16-row halves */
+        const int sa = __shfl(sum, hb), sb = __shfl(sum, hb + 16);
+        const float ds = d * (float)(sa + sb);
+        const uint32_t s16 = (uint32_t)(uint16_t)(int16_t)sa | ((uint32_t)(uint16_t)(int16_t)sb << 16);
+        const uint32_t b0 = (uint32_t)(qi & 0xff);
+        const uint32_t w4 = b0 | ((uint32_t)(__shfl(qi, lane + 1) & 0xff) << 8) |
+                            ((uint32_t)(__shfl(qi, lane + 2) & 0xff) << 16) | ((uint32_t)(__shfl(qi, lane + 3) & 0xff) << 24);
+        uint32_t *o = (uint32_t *)(a.S.aq + (size_t)s * nbF + blk);
+        uint32_t *pr = (uint32_t *)(a.S.aqk + ((size_t)s * (nbF >> 1) + (blk >> 1)) * kPairBytes);
+        if (r == 0) { o[0] = __float_as_uint(d); o[1] = __float_as_uint(ds); o[2] = s16; }
+        if ((r & 3) == 0) {
+            o[3 + (r >> 2)] = w4;                                          /* q[r .. r+3] */
+            const int p = (r & 15) >> 2;
+            pr[4 * p + 2 * half + (r >> 4)] = w4;                          /* q[4p..] or q[16+4p..] */
+        }
+        if (r == 1) pr[16 + 2 * half] = __float_as_uint(d);
+        if (r == 2) pr[17 + 2 * half] = __float_as_uint(ds);
+        if (r == 3) pr[20 + half] = s16;
+        if (r == 5 && half == 0) { pr[22] = 0; pr[23] = 0; }
+    }
+}
+
+/* Down rows of one slot tile: 64 output rows (R0 = 64*blockIdx.x) of expert e against the
+ * tile's int8 activation blocks; writes dn[slot][row], combined afterwards in selection order. */
+__global__ __launch_bounds__(256) void down_mfma_kernel(MfmaArgs a)
+{
+    __shared__ __align__(16) uint8_t As[2 * 64 * kMKC * 18 + 16];
+    __shared__ __align__(16) uint8_t Bs[2 * kTileN * kMKC * 44];
+    if ((int)blockIdx.y >= a.S.meta[1]) return;
+    const int4 tl = a.S.tiles[blockIdx.y];
+    const int e = tl.x, s0 = tl.y, ns = tl.z - tl.y;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, g = lane >> 4, lr = lane & 15;
+    const int R0 = (int)blockIdx.x * 64, nbF = a.F >> 5, E = a.E;
+    const uint8_t *w = a.w0 + (size_t)e * a.eb + (size_t)R0 * a.rb;
+    const uint8_t *aq = (const uint8_t *)a.S.aq;
+    float y[2][4];
+    mfma_tile(nbF, [&](int row) { return w + (size_t)row * a.rb; },
+              [&](int sl) { return aq + (size_t)(s0 + min(sl, ns - 1)) * nbF * 44; }, As, Bs, y);
+#pragma unroll
+    for (int jt = 0; jt < 2; jt++) {
+        const int sl = 16 * jt + lr;
+        if (sl < ns)
+#pragma unroll
+            for (int i = 0; i < 4; i++) a.S.dn[(size_t)(s0 + sl) * E + R0 + 16 * wave + 4 * g + i] = y[jt][i];
+    }
+}
+
+hipError_t launch_experts_mfma(const Shape &s, const LayerDev &L, const Scratch &S, float *out, int T, int debug,
+                               hipStream_t st)
+{
+    const int NS = T * s.K, maxt = (s.X < NS ? s.X : NS) + NS / kTileN + 1;
+    if (s.E % (32 * kMKC) || s.F % (32 * kMKC) || s.F % 32 || s.E % 64 || L.gate_type != 2 || L.up_type != 2)
+        return hipErrorInvalidValue;
+    MfmaArgs a;
+    a.w0 = L.gate;
+    a.w1 = L.up;
+    a.rb = L.gate_rb;
+    a.eb = L.gate_eb;
+    a.E = s.E;
+    a.F = s.F;
+    a.K = s.K;
+    a.X = s.X;
+    a.debug = debug;
+    a.S = S;
+    QLAUNCH("gateup", gateup_mfma_kernel, dim3(s.F / 32, maxt), dim3(256), 0, st, a);
+    if (L.down_type == 2) {
+        a.w0 = L.down;
+        a.w1 = nullptr;
+        a.rb = L.down_rb;
+        a.eb = L.down_eb;
+        QLAUNCH("down", down_mfma_kernel, dim3(s.E / 64, maxt), dim3(256), 0, st, a);
+        const int n = T * s.E;
+        QLAUNCH("combine", combine_kernel, dim3((n + 255) / 256), dim3(256), 0, st, S, s.E, s.K, T, out);
+        return hipGetLastError();
+    }
+    /* Q6_K down: the exact down kernel on the int8 blocks written above */
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    return launch_down_exact(s, L, S, out, T, st);
 }
 
 /* ------------------------------------------------------------------ block dots (checks) ---- */
