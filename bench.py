@@ -134,11 +134,158 @@ def copy_calibration(nbytes: int, steps: int):
                       "GBps_read_plus_write": round(2 * nbytes * n / (ms * 1e-3) / 1e9, 1)}), flush=True)
 
 
+def cpu_baseline_stack(ctx, w, seconds: float, n_cpu_layers: int = 2):
+    """The reference's moe() with its rmsnorm and residual add (src/model.c:1283-1285) chained
+    over n_cpu_layers resident layers on the host, scaled to the full stack."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle as orc  # checker only: times the CPU path beside the GPU
+
+    R = orc.load_ref()
+    if R is None:
+        return None
+    layers = []
+    for l in range(n_cpu_layers):
+        host = orc.Layer(w.E, w.X, w.K, w.F, w.seed + 1000 * l, layer=l, down_type=w.down_type, experts=[])
+        router, gate, up, down = ctx.download(l)
+        host.router[:] = router
+        host.gate, host.up, host.down = gate, up, down
+        host.have = set(range(w.X))
+        layers.append(host)
+    ones = np.ones(w.E, np.float32)
+    xn = np.empty((w.T, w.E), np.float32)
+
+    def chain(h):
+        for host in layers:
+            for t in range(w.T):
+                R.qref_rmsnorm(xn[t].ctypes.data, h[t].ctypes.data, ones.ctypes.data, w.E, np.float32(1e-6))
+            h += orc.ref_moe(R, host, xn)
+
+    hs = [orc.make_input(w.E, w.T, 20_000 + i) for i in range(4)]
+    chain(hs[0].copy())
+    n, t0 = 0, time.perf_counter()
+    while True:
+        chain(hs[n % len(hs)].copy())
+        n += 1
+        el = time.perf_counter() - t0
+        if (el >= seconds and n >= 2) or el >= 3 * seconds:
+            break
+    per_layer = el / (n * n_cpu_layers)
+    threads = R.qref_max_threads()
+    return {
+        "value": round(w.T / (per_layer * w.layers), 3),
+        "unit": "tokens/s",
+        "cores": threads,
+        "kind": "reference",
+        "sample": f"{n} passes of the reference rmsnorm + moe() + residual add over {n_cpu_layers} resident layers "
+                  f"({R.qref_isa().decode()} build), T={w.T}; per-layer time x {w.layers} layers (the full "
+                  f"{w.layers}-layer stack does not fit the host sample budget); {el:.1f} s on {threads} OpenMP "
+                  f"threads of {cpu_model()}",
+        "ms_per_layer": round(1e3 * per_layer, 4),
+    }
+
+
+def run_stack(args, w):
+    """A step is the whole layer stack: h += moe(l, rmsnorm(h)) for every resident layer."""
+    K_steps, W_steps, NL = args.steps, args.warmup, w.layers
+    total = K_steps + W_steps
+    log(f"workload {w.name}: E={w.E} X={w.X} K={w.K} F={w.F} T={w.T}, {NL}-layer stack")
+    ctx = qmsg.Context(w.E, w.X, w.K, w.F, n_layer=NL, max_tokens=w.T)
+    ctx.set_path({"auto": qmsg.PATH_AUTO, "exact": qmsg.PATH_EXACT, "mfma": qmsg.PATH_MFMA}[args.path])
+    for l in range(NL):
+        ctx.synth(l, w.seed + 1000 * l, down_type=w.down_type)
+    ctx.sync()
+    log("weights generated in HBM")
+    row = w.T * w.E * 4
+    d_h = ctx.device_alloc(total * row)
+    for s in range(total):
+        ctx.synth_input(w.seed + 7 + s, 0, w.T, d_h + s * row)
+    ctx.sync()
+
+    def step(s):
+        ctx.moe_chain(0, NL, d_h + s * row, w.T)
+
+    for s in range(W_steps):
+        step(s)
+    ctx.sync()
+    t0 = time.perf_counter()
+    for s in range(W_steps, total):
+        step(s)
+    ctx.sync()
+    el = time.perf_counter() - t0
+    ms_step = 1e3 * el / K_steps
+    log(f"timed {K_steps} steps: {ms_step:.3f} ms/step ({1e3 * ms_step / NL:.1f} us/layer)")
+    ctx.profile(True)
+    for s in range(W_steps):                      # the warmup inputs again (unchanged by timing)
+        step(s)
+    ctx.sync()
+    kern = {}
+    for name in ("rmsnorm", "route", "select", "dispatch", "gateup", "actq", "down", "combine", "add"):
+        n, ms = ctx.profile_read(name)
+        if n:
+            kern[name] = {"launches": n, "avg_us": round(1e3 * ms / n, 3)}
+    ctx.profile(False)
+    # distinct experts of the first layer on a fresh input (the routing is near uniform)
+    x = ctx.d2h(d_h + W_steps * row, (w.T, w.E))
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle as orc  # checker only: host rmsnorm of the sample input
+    _, dbg = ctx.moe_debug(0, orc.rmsnorm(x))
+    d_active = len(dbg["active"])
+    step_bytes = NL * w.layer_bytes(d_active)
+    g_us = kern.get("gateup", {}).get("avg_us")
+    gate_up_bytes = d_active * 2 * w.gate_bytes
+    achieved = gate_up_bytes / (g_us * 1e-6) / 1e9 if g_us else None
+    result = {
+        "metric": METRIC,
+        "value": round(w.T * K_steps / el, 3),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": K_steps,
+        "warmup": W_steps,
+        "ms_per_step": round(ms_step, 6),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8",
+        "data": "synthetic",
+        "config": {
+            "workload": f"{w.name}: {w.note}",
+            "n_embd": w.E, "n_expert": w.X, "n_used": w.K, "n_ff_exp": w.F, "tokens_per_step": w.T,
+            "layers": NL, "weights": "Q4_0 gate/up/" + ("Q6_K" if w.down_type == qmsg.QMSG_T_Q6_K else "Q4_0") +
+            " down, F32 router", "path": args.path,
+        },
+        "roofline": {
+            "kernel": "gateup (gate/up row dots + SwiGLU), per layer",
+            "bound": "hbm",
+            "achieved": round(achieved, 1) if achieved else None,
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4) if achieved else None,
+            "traffic": None,
+            "algorithmic_bytes_per_launch": int(gate_up_bytes),
+        },
+        "layer": {
+            "algorithmic_bytes_per_step": int(step_bytes),
+            "distinct_experts_per_layer": d_active,
+            "achieved_GBps": round(step_bytes / (ms_step * 1e-3) / 1e9, 1),
+            "frac_of_hbm_peak": round(step_bytes / (ms_step * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+            "us_per_layer": round(1e3 * ms_step / NL, 2),
+        },
+        "kernels": kern,
+        "device": ctx.device_info(),
+        "cpu_baseline": None,
+    }
+    if not args.no_cpu:
+        log("timing the CPU baseline")
+        result["cpu_baseline"] = cpu_baseline_stack(ctx, w, args.cpu_seconds)
+    ctx.close()
+    print(json.dumps(result), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=500)
-    ap.add_argument("--warmup", type=int, default=50)
+    ap.add_argument("--steps", type=int, default=None, help="timed steps (default 500; 20 for a layer stack)")
+    ap.add_argument("--warmup", type=int, default=None, help="untimed steps (default 50; 3 for a layer stack)")
     ap.add_argument("--workload", default="q235b_decode_t1", choices=sorted(WORKLOADS))
     ap.add_argument("--layers", type=int, default=16, help="distinct resident layers cycled by the steps")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
@@ -160,6 +307,14 @@ def main():
         return
 
     w = WORKLOADS[args.workload]
+    stack = w.layers > 1
+    if args.steps is None:
+        args.steps = 20 if stack else 500
+    if args.warmup is None:
+        args.warmup = 3 if stack else 50
+    if stack:
+        run_stack(args, w)
+        return
     K_steps, W_steps, NL = args.steps, args.warmup, max(1, args.layers)
     total = K_steps + W_steps
     log(f"workload {w.name}: E={w.E} X={w.X} K={w.K} F={w.F} T={w.T}, {NL} resident layers")

@@ -74,9 +74,12 @@ typedef struct qmsg_ctx qmsg_ctx;
 /* Which kernels run the expert products.
  *   EXACT: per-row fp32 FMA chains in the reference's lane order; every intermediate
  *          (int8 blocks, fp32 rows, outputs) is bit-identical to the reference's AVX path.
- *   MFMA:  int8 MFMA grouped GEMM for prefill-sized batches; int32 block dots exact, fp32 rows
- *          summed per block in another order. Not available yet: QMSG_E_UNSUPPORTED.
- *   AUTO:  the best available path (EXACT today). */
+ *   MFMA:  int8 MFMA grouped GEMM for batches routed by the select kernel (T > 1), Q4_0
+ *          gate/up (Q4_0 down on MFMA too, Q6_K down on the exact kernel): int32 block dots
+ *          exact, fp32 rows summed per block in another order (about 1e-6 of a row's
+ *          magnitude), which moves an int8 activation code where a value sits on a rounding
+ *          boundary (a few per 1e5 codes). An opt-in for prefill throughput.
+ *   AUTO:  EXACT (the order-exact results are the contract). */
 enum { QMSG_PATH_AUTO = 0, QMSG_PATH_EXACT = 1, QMSG_PATH_MFMA = 2 };
 
 /* ------------------------------------------------------------------ lifecycle ---- */
@@ -125,6 +128,17 @@ int qmsg_moe(qmsg_ctx *ctx, int layer, const float *xn, const float *h, int T, f
 /* The same layer on device buffers (d_xn [T][E], d_out [T][E] fp32), enqueued on the
  * context's stream without waiting. */
 int qmsg_moe_device(qmsg_ctx *ctx, int layer, const float *d_xn, int T, float *d_out);
+
+/* The MoE half of qms_forward's layer loop (src/model.c:1283-1285) over the resident layers
+ * first .. first+n-1, on device rows d_h [T][E] updated in place: for each layer,
+ * xn = rmsnorm(h, ffn_norm) (src/model.c:403-409, eps as the model's rms_norm_eps) and
+ * h += moe(l, xn). The attention half of each layer is not part of this library. Enqueued
+ * without waiting. */
+int qmsg_moe_chain(qmsg_ctx *ctx, int first, int n, float *d_h, int T, float eps);
+
+/* A layer's ffn_norm weight vector (QmsLayer.ffn_norm, src/model.h:37-45), n_embd floats on
+ * the host, copied to HBM; NULL restores the default unit weights. */
+int qmsg_layer_norm(qmsg_ctx *ctx, int layer, const float *w);
 
 /* Wait for everything enqueued on the context's stream. */
 int qmsg_sync(qmsg_ctx *ctx);

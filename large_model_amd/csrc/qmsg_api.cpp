@@ -17,6 +17,7 @@ namespace {
 
 struct LayerStore {
     float *router = nullptr;
+    float *norm = nullptr;        /* ffn_norm [E], nullptr: unit weights */
     uint8_t *gate = nullptr, *up = nullptr, *down = nullptr;
     int gate_type = -1, up_type = -1, down_type = -1;
     bool ready = false;
@@ -186,6 +187,7 @@ void qmsg_destroy(qmsg_ctx *c)
     if (c->stream) hipStreamSynchronize(c->stream);
     for (auto &L : c->layers) {
         hipFree(L.router);
+        hipFree(L.norm);
         hipFree(L.gate);
         hipFree(L.up);
         hipFree(L.down);
@@ -356,9 +358,8 @@ static int run_layer(qmsg_ctx *c, int layer, const float *d_xn, int T, float *d_
     const Shape s{ c->cfg.n_embd, c->cfg.n_expert, c->cfg.n_used, c->cfg.n_ff_exp };
     const LayerDev d = layer_dev(c, L);
     /* the MFMA grouped GEMM takes Q4_0 gate/up weights and batches routed by the select kernel */
-    const bool mfma = d.gate_type == QMSG_T_Q4_0 && d.up_type == QMSG_T_Q4_0 && !use_small_route(T, s.K) &&
-                      s.E % 256 == 0 && s.F % 256 == 0 &&
-                      (c->path == QMSG_PATH_MFMA || (c->path == QMSG_PATH_AUTO && T >= kMfmaMinT));
+    const bool mfma = c->path == QMSG_PATH_MFMA && d.gate_type == QMSG_T_Q4_0 && d.up_type == QMSG_T_Q4_0 &&
+                      !use_small_route(T, s.K) && s.E % 256 == 0 && s.F % 256 == 0;
     LAUNCH(c, "route", launch_route(s, d, c->S, d_xn, T, c->stream));
     LAUNCH(c, "select", launch_select(s, c->S, T, c->stream));
     if (mfma) {
@@ -374,6 +375,47 @@ int qmsg_moe_device(qmsg_ctx *c, int layer, const float *d_xn, int T, float *d_o
 {
     if (!c) return QMSG_E_INVALID;
     return run_layer(c, layer, d_xn, T, d_out, 0);
+}
+
+int qmsg_layer_norm(qmsg_ctx *c, int layer, const float *w)
+{
+    if (!c) return QMSG_E_INVALID;
+    int rc = check_layer_index(c, layer);
+    if (rc) return rc;
+    HIP_TRY(c, hipSetDevice(c->device));
+    LayerStore &L = c->layers[(size_t)layer];
+    if (!w) {
+        hipFree(L.norm);
+        L.norm = nullptr;
+        return QMSG_OK;
+    }
+    const size_t bytes = (size_t)c->cfg.n_embd * 4;
+    if (!L.norm) {
+        std::vector<void *> tmp;
+        if ((rc = dev_alloc(c, (void **)&L.norm, bytes, tmp))) return rc;
+    }
+    HIP_TRY(c, hipMemcpy(L.norm, w, bytes, hipMemcpyHostToDevice));
+    return QMSG_OK;
+}
+
+int qmsg_moe_chain(qmsg_ctx *c, int first, int n, float *d_h, int T, float eps)
+{
+    if (!c || !d_h || n < 0) return QMSG_E_INVALID;
+    if (first < 0 || first + n > c->n_layer)
+        return fail(c, QMSG_E_RANGE, "layers %d .. %d outside [0, %d)", first, first + n - 1, c->n_layer);
+    if (T < 0 || T > c->max_tokens) return fail(c, QMSG_E_RANGE, "T=%d outside [0, max_tokens=%d]", T, c->max_tokens);
+    if (T == 0 || n == 0) return QMSG_OK;
+    if ((uintptr_t)d_h & 15) return fail(c, QMSG_E_INVALID, "qmsg_moe_chain: d_h must be 16-byte aligned");
+    HIP_TRY(c, hipSetDevice(c->device));
+    const int E = c->cfg.n_embd;
+    for (int l = first; l < first + n; l++) {
+        if (!c->layers[(size_t)l].ready) return fail(c, QMSG_E_INVALID, "layer %d has no weights", l);
+        LAUNCH(c, "rmsnorm", launch_rmsnorm(d_h, c->layers[(size_t)l].norm, c->d_x, T, E, eps, c->stream));
+        const int rc = run_layer(c, l, c->d_x, T, c->d_out, 0);
+        if (rc) return rc;
+        LAUNCH(c, "add", launch_add_rows(d_h, c->d_out, (size_t)T * E, c->stream));
+    }
+    return QMSG_OK;
 }
 
 int qmsg_moe(qmsg_ctx *c, int layer, const float *xn, const float *h, int T, float *out)

@@ -39,10 +39,8 @@ extern thread_local const LaunchTimer *g_launch_timer;
 /* Static shape limits of the kernels. */
 constexpr int kMaxExperts = 256;
 
-/* Slots (tokens of one expert) per tile of the MFMA grouped-GEMM kernels, and the batch size
- * from which QMSG_PATH_AUTO takes them. */
+/* Slots (tokens of one expert) per tile of the MFMA grouped-GEMM kernels. */
 constexpr int kTileN = 32;
-constexpr int kMfmaMinT = 64;
 
 /* One-token batches (n_used <= 8) are routed inside the gate/up kernel instead of by a
  * separate select launch. */
@@ -98,6 +96,8 @@ hipError_t launch_synth_f32(uint64_t key, uint64_t n, float sigma, float *out, h
 hipError_t launch_synth_experts(uint64_t seed, uint32_t layer, uint32_t kind, int type, int64_t rows,
                                 int64_t cols, int X, float sigma, uint8_t *base, hipStream_t st);
 hipError_t launch_rmsnorm_rows(float *x, int T, int E, float eps, hipStream_t st);
+hipError_t launch_rmsnorm(const float *x, const float *w, float *y, int T, int E, float eps, hipStream_t st);
+hipError_t launch_add_rows(float *h, const float *d, size_t n, hipStream_t st);
 hipError_t launch_set_col0(float *m, int rows, int stride, const float *vals, float fill, hipStream_t st);
 hipError_t launch_silu(const float *x, int n, float *out, hipStream_t st);
 hipError_t launch_exp(const double *x, int n, double *out, hipStream_t st);

@@ -1862,6 +1862,57 @@ hipError_t launch_rmsnorm_rows(float *x, int T, int E, float eps, hipStream_t st
     return hipGetLastError();
 }
 
+/* src/model.c:403-409 into another buffer, with a weight vector (nullptr: unit): each row
+ * staged in LDS, its sum of squares the reference's sequential double FMA chain (one lane),
+ * then y = (float)(x * inv) * w in float. */
+__global__ void rmsnorm_kernel(const float *x, const float *w, float *y, int E, float eps)
+{
+    extern __shared__ __align__(16) float xs[];
+    __shared__ double inv;
+    const float *row = x + (size_t)blockIdx.x * E;
+    for (int i = threadIdx.x; i < E / 4; i += blockDim.x) ((float4 *)xs)[i] = ((const float4 *)row)[i];
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        double ss = 0.0;
+#pragma unroll 16
+        for (int i = 0; i < E; i++) ss = __builtin_fma((double)xs[i], (double)xs[i], ss);
+        inv = 1.0 / sqrt(ss / E + (double)eps);
+    }
+    __syncthreads();
+    const double v = inv;
+    float *out = y + (size_t)blockIdx.x * E;
+    for (int i = threadIdx.x; i < E; i += blockDim.x) out[i] = (float)((double)xs[i] * v) * (w ? w[i] : 1.0f);
+}
+
+hipError_t launch_rmsnorm(const float *x, const float *w, float *y, int T, int E, float eps, hipStream_t st)
+{
+    if (T <= 0) return hipSuccess;
+    if (E % 4) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(rmsnorm_kernel, dim3(T), dim3(256), (size_t)E * 4, st, x, w, y, E, eps);
+    return hipGetLastError();
+}
+
+/* h += d (src/model.c:1285), float adds. */
+__global__ void add_rows_kernel(float4 *h, const float4 *d, size_t n4)
+{
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n4) {
+        float4 a = h[i];
+        const float4 b = d[i];
+        a.x += b.x; a.y += b.y; a.z += b.z; a.w += b.w;
+        h[i] = a;
+    }
+}
+
+hipError_t launch_add_rows(float *h, const float *d, size_t n, hipStream_t st)
+{
+    if (n % 4) return hipErrorInvalidValue;
+    const size_t n4 = n / 4;
+    if (n4) hipLaunchKernelGGL(add_rows_kernel, dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0, st, (float4 *)h,
+                               (const float4 *)d, n4);
+    return hipGetLastError();
+}
+
 __global__ void set_col0_kernel(float *m, int rows, int stride, const float *vals, float fill)
 {
     const int r = blockIdx.x * blockDim.x + threadIdx.x;

@@ -93,6 +93,8 @@ _SIGS = {
     "qmsg_profile": (_I, [_P, _I]),
     "qmsg_profile_read": (_I, [_P, ctypes.c_char_p, ctypes.POINTER(ctypes.c_int64),
                                ctypes.POINTER(ctypes.c_double)]),
+    "qmsg_moe_chain": (_I, [_P, _I, _I, _P, _I, ctypes.c_float]),
+    "qmsg_layer_norm": (_I, [_P, _I, _P]),
     "qmsg_eval_silu": (_I, [_P, _P, _I, _P]),
     "qmsg_eval_exp": (_I, [_P, _P, _I, _P]),
     "qmsg_calibrate_copy": (_I, [_P, _P, _P, ctypes.c_size_t]),
@@ -250,6 +252,14 @@ class Context:
 
     def moe_device(self, layer: int, d_xn: int, T: int, d_out: int):
         self._check(lib.qmsg_moe_device(self._h, layer, d_xn, T, d_out))
+
+    def moe_chain(self, first: int, n: int, d_h: int, T: int, eps: float = 1e-6):
+        """h += moe(l, rmsnorm(h, ffn_norm_l)) for layers first .. first+n-1 on device rows d_h."""
+        self._check(lib.qmsg_moe_chain(self._h, first, n, d_h, T, eps))
+
+    def layer_norm(self, layer: int, w: Optional[np.ndarray]):
+        wp = None if w is None else np.ascontiguousarray(w, np.float32)
+        self._check(lib.qmsg_layer_norm(self._h, layer, _ptr(wp)))
 
     def sync(self):
         self._check(lib.qmsg_sync(self._h))
