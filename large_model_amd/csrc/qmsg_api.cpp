@@ -366,7 +366,7 @@ static int run_layer(qmsg_ctx *c, int layer, const float *d_xn, int T, float *d_
         LAUNCH(c, "experts", launch_experts_mfma(s, d, c->S, d_out, T, debug, c->stream));
     } else {
         LAUNCH(c, "gateup", launch_gateup_exact(s, d, c->S, T, debug, c->n_cu, c->stream));
-        LAUNCH(c, "down", launch_down_exact(s, d, c->S, d_out, T, c->stream));
+        LAUNCH(c, "down", launch_down_exact(s, d, c->S, d_out, T, 1, c->stream));
     }
     return QMSG_OK;
 }

@@ -90,7 +90,7 @@ hipError_t launch_gateup_exact(const Shape &s, const LayerDev &L, const Scratch 
                                hipStream_t st);
 hipError_t launch_experts_mfma(const Shape &s, const LayerDev &L, const Scratch &S, float *out, int T, int debug,
                                hipStream_t st);
-hipError_t launch_down_exact(const Shape &s, const LayerDev &L, const Scratch &S, float *out, int T,
+hipError_t launch_down_exact(const Shape &s, const LayerDev &L, const Scratch &S, float *out, int T, int quant,
                              hipStream_t st);
 hipError_t launch_synth_f32(uint64_t key, uint64_t n, float sigma, float *out, hipStream_t st);
 hipError_t launch_synth_experts(uint64_t seed, uint32_t layer, uint32_t kind, int type, int64_t rows,

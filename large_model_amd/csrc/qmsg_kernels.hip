@@ -822,9 +822,15 @@ __device__ void route_one_select(const Scratch &S, int K, int X, SmallRoute *R, 
         for (int e = tid; e <= X; e += blockDim.x) S.start[e] = start[e];
         for (int i = tid; i < X; i += blockDim.x) {
             S.work[i] = i < K ? R->work[i] : make_int4(-1, 0, 0, 0);
-            if (i < K) S.active[i] = R->work[i].x;
+            if (i < K) {
+                S.active[i] = R->work[i].x;
+                S.tiles[i] = make_int4(R->work[i].x, i, i + 1, 0);   /* one slot per expert */
+            }
         }
-        if (tid == 0) S.meta[0] = K;
+        if (tid == 0) {
+            S.meta[0] = K;
+            S.meta[1] = K;
+        }
     }
 }
 
@@ -948,14 +954,14 @@ __global__ __launch_bounds__(64 * W) void gateup_kernel(GateUpArgs a)
         slot_t = sr->slot_t;
         prefetched = wk.x == e_spec && wave > 0;
     } else {
-        wk = a.S.work[blockIdx.y];
-        if (wk.x < 0) return;
+        if ((int)blockIdx.y >= a.S.meta[1]) return;
+        wk = a.S.tiles[blockIdx.y];                  /* at most kTileN slots of one expert */
     }
     const int e = wk.x, s_begin = wk.y, s_end = wk.z;
     if (!prefetched) set_expert(e);
     const int F = a.F;
     const int rho = qd < 8 ? 8 * wave + qd : R + 8 * wave + (qd - 8);   /* tile row of this quad */
-    const bool tok_bytes = a.T <= 256;              /* work.w holds the first four tokens */
+    const bool tok_bytes = SEL && a.T <= 256;       /* work.w holds the first four tokens */
 
     for (int g0 = s_begin; g0 < s_end; g0 += NT) {
         const int nt = min(NT, s_end - g0);
@@ -1071,10 +1077,11 @@ hipError_t launch_gateup_exact(const Shape &s, const LayerDev &L, const Scratch 
     const int CB = nbE % 32 == 0 ? 16 : 8;
     const int NT = T >= 4 ? 4 : (T >= 2 ? 2 : 1);
     const int maxact = s.X < T * s.K ? s.X : T * s.K;
-    const int W = gateup_waves(s.F, maxact, n_cu);
-    if (!W) return hipErrorInvalidValue;
     const int sel = use_small_route(T, s.K);
-    dim3 grid(s.F / (8 * W), maxact);
+    const int rows_y = sel ? maxact : maxact + T * s.K / kTileN + 1;   /* active experts, or slot tiles */
+    const int W = gateup_waves(s.F, rows_y, n_cu);
+    if (!W) return hipErrorInvalidValue;
+    dim3 grid(s.F / (8 * W), rows_y);
     const size_t lds = gateup_lds(W, NT, CB, nP, sel);
     if (sel) {
         launch_gateup_nt<1, 1>(a, W, CB, grid, lds, st);     /* one token: NT == 1 */
@@ -1099,167 +1106,65 @@ struct DownArgs {
     Scratch S;
 };
 
-/* One block: down rows r0 .. r0+RD-1 (RD = 8) of every active expert. Items (expert, row)
- * are taken 64 at a time, one per lane quad; each round's 8 experts x 8 rows (8 contiguous
- * byte ranges) are staged whole into LDS, the next round's loads in flight during the
- * current round's dots. Each item writes dn[s][r] for every slot s of its expert. With
- * `fuse`, the block then forms out[t][r] = sum_j wt[t][j] * dn[slot_of[t][j]][r] in selection
- * order (src/model.c:1152-1162) from LDS copies of its own rows. */
+/* Down rows of one slot tile (at most kTileN slots of one expert, from the dispatch's tile
+ * list): 64 output rows R0 .. R0+63 (one per lane quad), staged once in LDS, against the
+ * tile's int8 activation records, NT slots per pass. Writes dn[slot][row]; the combine runs
+ * afterwards in selection order. */
 template <int TYPE, int NT>
-__global__ __launch_bounds__(256) void down_exact_kernel(DownArgs a)
+__global__ __launch_bounds__(256) void down_tile_kernel(DownArgs a)
 {
     extern __shared__ __align__(16) uint8_t smem[];
-    constexpr int RD = 8, EPR = 8;                       /* rows, experts per round */
-    constexpr int LPE = TYPE == 2 ? 2 : 3, MAXS = EPR * LPE;   /* 16-byte loads per expert per thread */
+    if ((int)blockIdx.y >= a.S.meta[1]) return;
+    const int4 tl = a.S.tiles[blockIdx.y];
+    const int e = tl.x, s0 = tl.y, ns = tl.z - tl.y;
     const int tid = threadIdx.x, quad = tid >> 2, p = tid & 3;
-    const int r0 = (int)blockIdx.x * RD, E = a.E, nPF = a.F >> 6, K = a.K;
-    const int rbytes = (int)(RD * a.rb);                 /* one expert's RD rows */
-    const int spe = rbytes / 16;                         /* 16-byte slots of one expert's rows */
-    const int xrec = nPF * kPairBytes;                   /* one slot's int8 activations */
+    const int R0 = (int)blockIdx.x * 64, E = a.E, nPF = a.F >> 6, xrec = nPF * kPairBytes;
+    const int rb = (int)a.rb, n16 = 64 * rb / 16;
     uint8_t *tile = smem;
-    uint8_t *xbuf = smem + ((EPR * rbytes + 16 + 15) & ~15);        /* up to a.lds_slots slots */
-    float *dnl = (float *)(xbuf + (size_t)a.lds_slots * xrec);      /* [NS][RD] when fused */
-    u32x4 v[MAXS];
-    int rnd = 0;
-    /* round rnd covers active experts rnd*EPR .. rnd*EPR+7; work[] ends with expert -1. Every
-     * load instruction reads one expert's rows (a uniform address base), LPE per expert. */
-#define QMSG_DLOAD_K(R, K0, K1)                                                                      \
-    _Pragma("unroll") for (int k_ = (K0); k_ < (K1); k_++) {                                         \
-        const int e_ = max(a.S.work[min((R) * EPR + k_, a.X - 1)].x, 0);                             \
-        const u32x4 *src_ = (const u32x4 *)(a.down + (size_t)e_ * a.eb + (size_t)r0 * a.rb);         \
-        _Pragma("unroll") for (int j_ = 0; j_ < LPE; j_++) v[k_ * LPE + j_] = src_[min(tid + 256 * j_, spe - 1)]; \
+    uint8_t *xbuf = smem + ((64 * rb + 15) & ~15);            /* [NT][xrec] */
+    const u32x4 *wsrc = (const u32x4 *)(a.down + (size_t)e * a.eb + (size_t)R0 * a.rb);
+    for (int i0 = 0; i0 < n16; i0 += 256 * 8) {
+        u32x4 v[8];
+#pragma unroll
+        for (int m = 0; m < 8; m++) v[m] = wsrc[min(i0 + tid + 256 * m, n16 - 1)];
+#pragma unroll
+        for (int m = 0; m < 8; m++)
+            if (i0 + tid + 256 * m < n16) ((u32x4 *)tile)[i0 + tid + 256 * m] = v[m];
     }
-#define QMSG_DLOAD(R) QMSG_DLOAD_K(R, 0, EPR)
-    /* Each int8 block of activations spans rows of two gate/up blocks, so with qlds it is
-     * formed here, for every slot. The first QPRE blocks' inputs per thread are requested
-     * before the weights (waits are in issue order), so they are quantised while the
-     * weights are in flight. Block 0 also writes the blocks out for the debug copy-back. */
-    constexpr int QPRE = 2;
-    const int nqb = a.qlds ? a.T * K * (a.F >> 5) : 0, nbF = a.F >> 5;
-    float4 av[QPRE][8];
-#pragma unroll
-    for (int u = 0; u < QPRE; u++) {
-        const int b = min(tid + 256 * u, max(nqb - 1, 0));    /* in bounds even when unused */
-        const float4 *src = (const float4 *)(a.S.act + (size_t)b * 32);
-#pragma unroll
-        for (int j = 0; j < 8; j++) av[u][j] = src[j];
-    }
-    __builtin_amdgcn_sched_barrier(0);     /* keep these requests ahead of the weights' */
-    QMSG_DLOAD(0)
-    auto quant_store = [&](int b, const float *v) {
-        const int s = b / nbF, blk = b - s * nbF;
-        const Q8Vals q = quantize_block(v);
-        store_pair_half(q, (uint32_t *)(xbuf + (size_t)s * xrec + (size_t)(blk >> 1) * kPairBytes), blk & 1);
-        if (blockIdx.x == 0) {
-            store_q8(q, a.S.aq + b);
-            store_pair_half(q, (uint32_t *)(a.S.aqk + ((size_t)s * (nbF >> 1) + (blk >> 1)) * kPairBytes), blk & 1);
-        }
-    };
-#pragma unroll
-    for (int u = 0; u < QPRE; u++) {
-        if (tid + 256 * u < nqb) {
-            float v[32];
-#pragma unroll
-            for (int j = 0; j < 8; j++) {
-                v[4 * j] = av[u][j].x; v[4 * j + 1] = av[u][j].y; v[4 * j + 2] = av[u][j].z; v[4 * j + 3] = av[u][j].w;
-            }
-            quant_store(tid + 256 * u, v);
-        }
-    }
-    for (int b = tid + 256 * QPRE; b < nqb; b += 256) {
-        float v[32];
-        const float4 *src = (const float4 *)(a.S.act + (size_t)b * 32);
-#pragma unroll
-        for (int j = 0; j < 8; j++) {
-            const float4 f = src[j];
-            v[4 * j] = f.x; v[4 * j + 1] = f.y; v[4 * j + 2] = f.z; v[4 * j + 3] = f.w;
-        }
-        quant_store(b, v);
-    }
-    for (;; rnd++) {
-        /* this round's experts and their (contiguous) slot range */
-        __shared__ int4 rw[EPR];
-        __shared__ int srange[2];
+    const uint8_t *row = tile + quad * rb;
+    for (int g0 = 0; g0 < ns; g0 += NT) {
+        const int nt = min(NT, ns - g0);
+        __syncthreads();                                  /* the weights landed; xbuf is free */
+        for (int i = tid; i < nt * (xrec >> 4); i += 256)
+            ((u32x4 *)xbuf)[i] = ((const u32x4 *)(a.S.aqk + (size_t)(s0 + g0) * xrec))[i];
         __syncthreads();
-        if (tid < EPR) {
-            const int ai = rnd * EPR + tid;
-            rw[tid] = ai < a.X ? a.S.work[ai] : make_int4(-1, 0, 0, 0);
-        }
-        __syncthreads();
-        if (rw[0].x < 0) break;
-        if (tid == 0) {
-            int hi = rw[0].z;
-            for (int k = 1; k < EPR; k++) if (rw[k].x >= 0) hi = rw[k].z;
-            srange[0] = rw[0].y;
-            srange[1] = hi;
-        }
+        RowAcc acc[NT];
+        for (int n = 0; n < NT; n++) acc[n] = RowAcc{ 0.0f, 0.0f, 0.0f };
+        if (TYPE == 2) {
+            q4_0_rows<NT, (NT >= 4 ? 1 : (NT == 2 ? 2 : 4))>((const uint32_t *)row, p, xbuf, (size_t)xrec, 0, nPF, nt, acc);
+        } else {
+            const int nsb = a.F >> 8;
+            const uint32_t rowoff = (uint32_t)(row - tile);
+            for (int sbi = 0; sbi < nsb; sbi++) {
+                const uint32_t sb = rowoff + (uint32_t)(sbi * 210);
 #pragma unroll
-        for (int k = 0; k < EPR; k++)
+                for (int h = 0; h < 2; h++)
 #pragma unroll
-            for (int j = 0; j < LPE; j++)
-                if (tid + 256 * j < spe) ((u32x4 *)tile)[k * spe + tid + 256 * j] = v[k * LPE + j];
-        __syncthreads();
-        const int s_lo = srange[0], s_hi = srange[1];
-        const bool in_lds = !a.qlds && s_hi - s_lo <= a.lds_slots;
-        if (in_lds)
-            for (int i = tid; i < (s_hi - s_lo) * (xrec >> 4); i += 256)
-                ((u32x4 *)xbuf)[i] = ((const u32x4 *)(a.S.aqk + (size_t)s_lo * xrec))[i];
-        const bool more = rnd * EPR + EPR < a.X && a.S.work[min(rnd * EPR + EPR, a.X - 1)].x >= 0;
-        if (more) { QMSG_DLOAD(rnd + 1) }
-        __syncthreads();
-        const int k = quad >> 3, rr = quad & 7;
-        const int4 w = rw[k];
-        if (w.x >= 0) {
-            const uint8_t *row = tile + k * rbytes + rr * (int)a.rb;
-            const uint8_t *xs = a.qlds ? xbuf + (size_t)w.y * xrec
-                                       : (in_lds ? xbuf + (size_t)(w.y - s_lo) * xrec : a.S.aqk + (size_t)w.y * xrec);
-            for (int g0 = w.y; g0 < w.z; g0 += NT) {
-                const int nt = min(NT, w.z - g0);
-                RowAcc acc[NT];
-                for (int n = 0; n < NT; n++) acc[n] = RowAcc{ 0.0f, 0.0f, 0.0f };
-                const uint8_t *xg = xs + (size_t)(g0 - w.y) * xrec;
-                if (TYPE == 2) {
-                    q4_0_rows<NT, (NT >= 4 ? 1 : (NT == 2 ? 2 : 4))>((const uint32_t *)row, p, xg, (size_t)xrec, 0, nPF, nt, acc);
-                } else {
-                    const int nsb = a.F >> 8;
-                    const uint32_t rowoff = (uint32_t)(row - tile);
-                    for (int sbi = 0; sbi < nsb; sbi++) {
-                        const uint32_t sb = rowoff + (uint32_t)(sbi * 210);
+                    for (int g = 0; g < 4; g++) {
+                        const int blk = sbi * 8 + h * 4 + g;
 #pragma unroll
-                        for (int h = 0; h < 2; h++)
-#pragma unroll
-                            for (int g = 0; g < 4; g++) {
-                                const int blk = sbi * 8 + h * 4 + g;
-#pragma unroll
-                                for (int n = 0; n < NT; n++)
-                                    if (n < nt)
-                                        q6_k_block(tile, sb, h, g, p, xg + (size_t)n * xrec + (size_t)(blk >> 1) * kPairBytes,
-                                                   blk & 1, acc[n]);
-                            }
+                        for (int n = 0; n < NT; n++)
+                            if (n < nt)
+                                q6_k_block(tile, sb, h, g, p, xbuf + (size_t)n * xrec + (size_t)(blk >> 1) * kPairBytes,
+                                           blk & 1, acc[n]);
                     }
-                }
-#pragma unroll
-                for (int n = 0; n < NT; n++) {
-                    const float d = quad_finish(acc[n], TYPE == 2 ? 8.0f : 32.0f);
-                    if (p == 0 && n < nt) {
-                        a.S.dn[(size_t)(g0 + n) * E + r0 + rr] = d;
-                        if (a.fuse) dnl[(g0 + n) * RD + rr] = d;
-                    }
-                }
             }
         }
-        if (!more) break;
-    }
-#undef QMSG_DLOAD
-#undef QMSG_DLOAD_K
-    if (!a.fuse) return;
-    __syncthreads();
-    for (int i = tid; i < a.T * RD; i += 256) {
-        const int t = i / RD, rr = i - t * RD;
-        float o = 0.0f;
-        for (int j = 0; j < K; j++)
-            o = __builtin_fmaf(a.S.wt[(size_t)t * K + j], dnl[a.S.slot_of[(size_t)t * K + j] * RD + rr], o);
-        a.out[(size_t)t * E + r0 + rr] = o;
+#pragma unroll
+        for (int n = 0; n < NT; n++) {
+            const float d = quad_finish(acc[n], TYPE == 2 ? 8.0f : 32.0f);
+            if (p == 0 && n < nt) a.S.dn[(size_t)(s0 + g0 + n) * E + R0 + quad] = d;
+        }
     }
 }
 
@@ -1402,7 +1307,8 @@ __global__ void combine_kernel(const Scratch S, int E, int K, int T, float *out)
     out[i] = o;
 }
 
-hipError_t launch_down_exact(const Shape &s, const LayerDev &L, const Scratch &S, float *out, int T, hipStream_t st)
+hipError_t launch_down_exact(const Shape &s, const LayerDev &L, const Scratch &S, float *out, int T, int quant,
+                             hipStream_t st)
 {
     DownArgs a;
     a.down = L.down;
@@ -1425,38 +1331,28 @@ hipError_t launch_down_exact(const Shape &s, const LayerDev &L, const Scratch &S
         else QLAUNCH("down", (down_t1_kernel<8, 2>), dim3(s.E / 8), dim3(256), lds, st, a);
         return hipGetLastError();
     }
-    const size_t tile = ((size_t)8 * 8 * L.down_rb + 16 + 15) & ~(size_t)15;
-    if ((size_t)8 * L.down_rb / 16 > (size_t)256 * (L.down_type == 2 ? 2 : 3)) return hipErrorInvalidValue;
-    const int NS = T * s.K;
-    const size_t dnl = (size_t)NS * 8 * 4;
-    const size_t xrec = (size_t)(s.F / 64) * kPairBytes;
-    /* quantise in the prologue when every slot's records fit with two blocks per CU */
-    a.qlds = tile + (size_t)NS * xrec + dnl <= 80 * 1024;
-    if (a.qlds) {
-        a.lds_slots = NS;
-        a.fuse = 1;
-    } else {
-        a.lds_slots = NS < 16 ? NS : 16;
-        a.fuse = tile + a.lds_slots * xrec + dnl <= 120 * 1024;
+    /* slot tiles: the activations' int8 records first (unless the MFMA gate/up wrote them) */
+    const int NS = T * s.K, maxt = (s.X < NS ? s.X : NS) + NS / kTileN + 1;
+    if (quant) {
         const int nq = NS * (s.F / 32);
         QLAUNCH("actq", act_quant_kernel, dim3((nq + 255) / 256), dim3(256), 0, st, S, s.F, NS);
     }
-    const size_t lds = tile + a.lds_slots * xrec + (a.fuse ? dnl : 0);
     const int NT = T >= 4 ? 4 : (T >= 2 ? 2 : 1);
-    const dim3 grid(s.E / 8);
+    const size_t xrec = (size_t)(s.F / 64) * kPairBytes;
+    const size_t lds = ((64 * L.down_rb + 15) & ~(size_t)15) + (size_t)NT * xrec;
+    if (lds > 160 * 1024 || s.E % 64) return hipErrorInvalidValue;
+    const dim3 grid(s.E / 64, maxt);
     if (L.down_type == 2) {
-        if (NT == 4) QLAUNCH("down", (down_exact_kernel<2, 4>), grid, dim3(256), lds, st, a);
-        else if (NT == 2) QLAUNCH("down", (down_exact_kernel<2, 2>), grid, dim3(256), lds, st, a);
-        else QLAUNCH("down", (down_exact_kernel<2, 1>), grid, dim3(256), lds, st, a);
+        if (NT == 4) QLAUNCH("down", (down_tile_kernel<2, 4>), grid, dim3(256), lds, st, a);
+        else if (NT == 2) QLAUNCH("down", (down_tile_kernel<2, 2>), grid, dim3(256), lds, st, a);
+        else QLAUNCH("down", (down_tile_kernel<2, 1>), grid, dim3(256), lds, st, a);
     } else {
-        if (NT == 4) QLAUNCH("down", (down_exact_kernel<14, 4>), grid, dim3(256), lds, st, a);
-        else if (NT == 2) QLAUNCH("down", (down_exact_kernel<14, 2>), grid, dim3(256), lds, st, a);
-        else QLAUNCH("down", (down_exact_kernel<14, 1>), grid, dim3(256), lds, st, a);
+        if (NT == 4) QLAUNCH("down", (down_tile_kernel<14, 4>), grid, dim3(256), lds, st, a);
+        else if (NT == 2) QLAUNCH("down", (down_tile_kernel<14, 2>), grid, dim3(256), lds, st, a);
+        else QLAUNCH("down", (down_tile_kernel<14, 1>), grid, dim3(256), lds, st, a);
     }
-    if (!a.fuse) {
-        const int n = T * s.E;
-        QLAUNCH("combine", combine_kernel, dim3((n + 255) / 256), dim3(256), 0, st, S, s.E, s.K, T, out);
-    }
+    const int n = T * s.E;
+    QLAUNCH("combine", combine_kernel, dim3((n + 255) / 256), dim3(256), 0, st, S, s.E, s.K, T, out);
     return hipGetLastError();
 }
 
@@ -1694,7 +1590,7 @@ hipError_t launch_experts_mfma(const Shape &s, const LayerDev &L, const Scratch 
     /* Q6_K down: the exact down kernel on the int8 blocks written above */
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    return launch_down_exact(s, L, S, out, T, st);
+    return launch_down_exact(s, L, S, out, T, 0, st);
 }
 
 /* ------------------------------------------------------------------ block dots (checks) ---- */
