@@ -75,7 +75,7 @@ typedef struct qmsg_ctx qmsg_ctx;
  *   EXACT: per-row fp32 FMA chains in the reference's lane order; every intermediate
  *          (int8 blocks, fp32 rows, outputs) is bit-identical to the reference's AVX path.
  *   MFMA:  int8 MFMA grouped GEMM for batches routed by the select kernel (T > 1), Q4_0
- *          gate/up (Q4_0 down on MFMA too, Q6_K down on the exact kernel): int32 block dots
+ *          gate/up (Q4_0 down on MFMA too, Q4_1/Q6_K down on the exact kernel): int32 block dots
  *          exact, fp32 rows summed per block in another order (about 1e-6 of a row's
  *          magnitude), which moves an int8 activation code where a value sits on a rounding
  *          boundary (a few per 1e5 codes). An opt-in for prefill throughput.
@@ -181,7 +181,8 @@ int qmsg_moe_debug(qmsg_ctx *ctx, int layer, const float *xn, int T, float *out,
 
 /* Exact signed int32 dot of one 32-element block of an expert row with a QmsQ8 block, as the
  * device kernels form it: which = 0 gate, 1 up, 2 down; x is one 44-byte QmsQ8 block.
- * Q4_0: sum (q-8)*x; Q6_K: sc_lo*sum_{l<16}(q-32)*x + sc_hi*sum_{l>=16}(q-32)*x. */
+ * Q4_0: sum (q-8)*x; Q4_1: sum q*x (its m*ds offset is fp32, outside the block dot);
+ * Q6_K: sc_lo*sum_{l<16}(q-32)*x + sc_hi*sum_{l>=16}(q-32)*x. */
 int qmsg_block_dots(qmsg_ctx *ctx, int layer, int which, int n, const int32_t *expert, const int32_t *row,
                     const int32_t *block, const void *xq_blocks, int32_t *out);
 

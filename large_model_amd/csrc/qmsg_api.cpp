@@ -223,9 +223,10 @@ static int check_layer_index(qmsg_ctx *c, int layer)
 static int layer_alloc(qmsg_ctx *c, LayerStore &L, int gt, int ut, int dt)
 {
     const int64_t E = c->cfg.n_embd, X = c->cfg.n_expert, F = c->cfg.n_ff_exp;
-    if (gt != QMSG_T_Q4_0 || ut != QMSG_T_Q4_0 || (dt != QMSG_T_Q4_0 && dt != QMSG_T_Q6_K))
-        return fail(c, QMSG_E_UNSUPPORTED, "expert types gate=%d up=%d down=%d: kernels take Q4_0 gate/up and Q4_0 or Q6_K down",
-                    gt, ut, dt);
+    if (gt != QMSG_T_Q4_0 || ut != QMSG_T_Q4_0 || (dt != QMSG_T_Q4_0 && dt != QMSG_T_Q4_1 && dt != QMSG_T_Q6_K))
+        return fail(c, QMSG_E_UNSUPPORTED,
+                    "expert types gate=%d up=%d down=%d: kernels take Q4_0 gate/up and Q4_0, Q4_1 or Q6_K down", gt, ut,
+                    dt);
     if (dt == QMSG_T_Q6_K && F % 256)
         return fail(c, QMSG_E_UNSUPPORTED, "Q6_K down needs n_ff_exp %% 256 == 0 (got %lld)", (long long)F);
     hipFree(L.router); hipFree(L.gate); hipFree(L.up); hipFree(L.down);

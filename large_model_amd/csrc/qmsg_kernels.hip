@@ -598,6 +598,41 @@ __device__ __forceinline__ void q4_0_math(const Q4Pair &w, const XPair &x, RowAc
     r.corr = __builtin_fmaf(d1, x.d.w, r.corr);
 }
 
+/* The words one lane needs from a pair of Q4_1 blocks {f16 d; f16 m; u8 qs[16]} (40 bytes at
+ * W, 4-byte aligned): its code dword of each block and the d|m word of each. */
+struct Q41Pair {
+    uint32_t c0, c1;
+    uint32_t w0, w5;      /* d of block b in the low half of w0, m in its high half; w5 for b+1 */
+};
+
+__device__ __forceinline__ Q41Pair q4_1_load(const uint32_t *W, int p)
+{
+    Q41Pair r;
+    r.w0 = W[0];
+    r.c0 = W[1 + p];
+    r.w5 = W[5];
+    r.c1 = W[6 + p];
+    return r;
+}
+
+/* src/kernels.c:113-119 for blocks b and b+1: unsigned codes (no -8), lane sums scaled by
+ * fl(d*xd), and the offset chain off = fma(m, ds, off) kept in corr. */
+__device__ __forceinline__ void q4_1_math(const Q41Pair &w, const XPair &x, RowAcc &r)
+{
+    const int s0 = sdot4((int)(w.c0 & 0x0f0f0f0fu), (int)x.q.x);
+    const int s1 = sdot4((int)((w.c0 >> 4) & 0x0f0f0f0fu), (int)x.q.y);
+    const int s2 = sdot4((int)(w.c1 & 0x0f0f0f0fu), (int)x.q.z);
+    const int s3 = sdot4((int)((w.c1 >> 4) & 0x0f0f0f0fu), (int)x.q.w);
+    const float o0 = h2f(w.w0 >> 16), o1 = h2f(w.w5 >> 16);
+    const float m0 = mul_f16_f32<0>(w.w0, x.d.x), m1 = mul_f16_f32<0>(w.w5, x.d.z);
+    r.lo = __builtin_fmaf((float)s0, m0, r.lo);
+    r.hi = __builtin_fmaf((float)s1, m0, r.hi);
+    r.corr = __builtin_fmaf(o0, x.d.y, r.corr);
+    r.lo = __builtin_fmaf((float)s2, m1, r.lo);
+    r.hi = __builtin_fmaf((float)s3, m1, r.hi);
+    r.corr = __builtin_fmaf(o1, x.d.w, r.corr);
+}
+
 /* One Q6_K 32-block (index g of half h of the super-block at byte sb of the LDS tile)
  * against one token's block, src/kernels.c:148-167: lanes k < 4 use sc[2g], k >= 4 sc[2g+1]. */
 __device__ __forceinline__ void q6_k_block(const uint8_t *tile, uint32_t sb, int h, int g, int p, const uint8_t *xp,
@@ -626,7 +661,9 @@ __device__ __forceinline__ void q6_k_block(const uint8_t *tile, uint32_t sb, int
     r.corr = __builtin_fmaf(dd, (float)(sa * s16a + sbb * s16b), r.corr);
 }
 
-/* hsum256 over the quad, then the unfused offset subtraction. Valid on lane p == 0. */
+/* hsum256 over the quad, then the unfused offset term h - scale*corr: scale 8 (Q4_0), 32
+ * (Q6_K), or -1 for Q4_1's h + off (src/kernels.c:120; -1*off is exact, so h - (-off) is the
+ * reference's sum). Valid on lane p == 0. */
 __device__ __forceinline__ float quad_finish(const RowAcc &r, float scale)
 {
     const float s = r.lo + r.hi;                      /* s_p = acc_p + acc_{p+4}   */
@@ -872,6 +909,39 @@ __device__ __forceinline__ void q4_0_rows(const uint32_t *Wrow, int p, const uin
             if (n < nt) q4_0_math(w, x_load(x0 + n * xrec + (size_t)(q0 + q) * kPairBytes, p), acc[n]);
     }
 }
+
+/* The same for Q4_1 rows (40-byte block pairs). */
+template <int NT, int B>
+__device__ __forceinline__ void q4_1_rows(const uint32_t *Wrow, int p, const uint8_t *x0, size_t xrec, int q0, int nq,
+                                          int nt, RowAcc *acc)
+{
+    int q = 0;
+    for (; q + B <= nq; q += B) {
+        Q41Pair w[B];
+        XPair x[B][NT];
+#pragma unroll
+        for (int u = 0; u < B; u++) {
+            w[u] = q4_1_load(Wrow + (q + u) * 10, p);
+#pragma unroll
+            for (int n = 0; n < NT; n++)
+                if (n < nt) x[u][n] = x_load(x0 + n * xrec + (size_t)(q0 + q + u) * kPairBytes, p);
+        }
+#pragma unroll
+        for (int u = 0; u < B; u++)
+#pragma unroll
+            for (int n = 0; n < NT; n++)
+                if (n < nt) q4_1_math(w[u], x[u][n], acc[n]);
+    }
+    for (; q < nq; q++) {
+        const Q41Pair w = q4_1_load(Wrow + q * 10, p);
+#pragma unroll
+        for (int n = 0; n < NT; n++)
+            if (n < nt) q4_1_math(w, x_load(x0 + n * xrec + (size_t)(q0 + q) * kPairBytes, p), acc[n]);
+    }
+}
+
+/* Offset scale of quad_finish for a row type (Q4_0 8, Q4_1 -1, Q6_K 32). */
+__host__ __device__ constexpr float finish_scale(int type) { return type == 2 ? 8.0f : (type == 3 ? -1.0f : 32.0f); }
 
 /* LDS bytes of a gateup block (shared by the kernel's carve-up and the launcher). */
 __host__ __device__ constexpr size_t gateup_lds(int W, int NT, int CB, int nP, int sel)
@@ -1142,6 +1212,8 @@ __global__ __launch_bounds__(256) void down_tile_kernel(DownArgs a)
         for (int n = 0; n < NT; n++) acc[n] = RowAcc{ 0.0f, 0.0f, 0.0f };
         if (TYPE == 2) {
             q4_0_rows<NT, (NT >= 4 ? 1 : (NT == 2 ? 2 : 4))>((const uint32_t *)row, p, xbuf, (size_t)xrec, 0, nPF, nt, acc);
+        } else if (TYPE == 3) {
+            q4_1_rows<NT, (NT >= 4 ? 1 : (NT == 2 ? 2 : 4))>((const uint32_t *)row, p, xbuf, (size_t)xrec, 0, nPF, nt, acc);
         } else {
             const int nsb = a.F >> 8;
             const uint32_t rowoff = (uint32_t)(row - tile);
@@ -1162,28 +1234,29 @@ __global__ __launch_bounds__(256) void down_tile_kernel(DownArgs a)
         }
 #pragma unroll
         for (int n = 0; n < NT; n++) {
-            const float d = quad_finish(acc[n], TYPE == 2 ? 8.0f : 32.0f);
+            const float d = quad_finish(acc[n], finish_scale(TYPE));
             if (p == 0 && n < nt) a.S.dn[(size_t)(s0 + g0 + n) * E + R0 + quad] = d;
         }
     }
 }
 
-/* One-token batch, Q4_0 down weights (K <= 8 experts, one slot each, slot j = j-th active
+/* One-token batch, Q4_0 or Q4_1 down weights (K <= 8 experts, one slot each, slot j = j-th active
  * expert): one block per 8 output rows r0 .. r0+7. Wave w owns active experts 2w and 2w+1
  * (16 rows, one per lane quad) and streams exactly those rows in chunks of CB blocks, D chunks
  * in flight, through its own LDS buffer, so its dots start as soon as its first bytes land.
  * The prologue requests the first chunks, then quantises the K activation rows into int8
  * pair records in LDS (block 0 also writes them out for the debug copy-back). The block ends
  * with the weighted combine of its 8 rows in selection order (src/model.c:1152-1162). */
-template <int CB, int D>
+template <int TYPE, int CB, int D>
 __global__ __launch_bounds__(256) void down_t1_kernel(DownArgs a)
 {
     extern __shared__ __align__(16) uint8_t smem[];
     constexpr int RD = 8;
-    constexpr int SPR = CB * 18 / 16;                 /* 16-byte slots per row per chunk      */
+    constexpr int BB = TYPE == 3 ? 20 : 18;           /* bytes per 32-block                   */
+    constexpr int SPR = CB * BB / 16;                 /* 16-byte slots per row per chunk      */
     constexpr int NSL = 16 * SPR;                     /* slots of one wave's chunk            */
     constexpr int SPT = (NSL + 63) / 64;              /* slots per lane per chunk             */
-    constexpr int WS = CB * 18 + ((SPR & 1) ? 0 : 16);/* LDS row stride, odd in 16-byte units */
+    constexpr int WS = CB * BB + ((SPR & 1) ? 0 : 16);/* LDS row stride, odd in 16-byte units */
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, qd = lane >> 2, p = lane & 3;
     const int r0 = (int)blockIdx.x * RD, E = a.E, K = a.K, nbF = a.F >> 5, nPF = a.F >> 6;
     const int nchunk = nbF / CB, xrec = nPF * kPairBytes;
@@ -1212,7 +1285,7 @@ __global__ __launch_bounds__(256) void down_t1_kernel(DownArgs a)
         for (int m = 0; m < SPT; m++) {
             const int i = min(lane + 64 * m, NSL - 1), row = i / SPR, j = i - row * SPR;
             dst[m] = *(const u32x4 *)((row < 8 ? b0 + (size_t)row * a.rb : b1 + (size_t)(row - 8) * a.rb) +
-                                      (size_t)c * CB * 18 + 16 * j);
+                                      (size_t)c * CB * BB + 16 * j);
         }
     };
     const bool active = e0 >= 0;
@@ -1258,11 +1331,16 @@ __global__ __launch_bounds__(256) void down_t1_kernel(DownArgs a)
                     }
                     wave_sync();
                     if (c + D < nchunk) load_chunk(c + D, wv[d]);
-                    q4_0_rows<1, 4>((const uint32_t *)(wbuf + qd * WS), p, xq, (size_t)xrec, c * (CB / 2), CB / 2, 1, acc);
+                    if (TYPE == 3)
+                        q4_1_rows<1, 4>((const uint32_t *)(wbuf + qd * WS), p, xq, (size_t)xrec, c * (CB / 2), CB / 2,
+                                        1, acc);
+                    else
+                        q4_0_rows<1, 4>((const uint32_t *)(wbuf + qd * WS), p, xq, (size_t)xrec, c * (CB / 2), CB / 2,
+                                        1, acc);
                 }
             }
         }
-        const float v = quad_finish(acc[0], 8.0f);
+        const float v = quad_finish(acc[0], finish_scale(TYPE));
         if (p == 0 && jq < K) {
             a.S.dn[(size_t)jq * E + r0 + rr] = v;
             dnl[jq * RD + rr] = v;
@@ -1321,14 +1399,19 @@ hipError_t launch_down_exact(const Shape &s, const LayerDev &L, const Scratch &S
     a.X = s.X;
     a.out = out;
     a.S = S;
-    if (T == 1 && s.K <= 8 && L.down_type == 2 && s.F % 256 == 0) {
-        /* one token: each wave streams its own two experts' rows (Q4_0) */
-        const int nbF = s.F / 32, CB = nbF % 16 == 0 ? 16 : 8;
+    if (T == 1 && s.K <= 8 && (L.down_type == 2 || L.down_type == 3) && s.F % 256 == 0) {
+        /* one token: each wave streams its own two experts' rows (Q4_0 / Q4_1) */
+        const int nbF = s.F / 32, CB = nbF % 16 == 0 ? 16 : 8, bb = L.down_type == 3 ? 20 : 18;
         const size_t xrec = (size_t)(s.F / 64) * kPairBytes;
-        const size_t ws = (size_t)CB * 18 + (((CB * 18 / 16) & 1) ? 0 : 16);
+        const size_t ws = (size_t)CB * bb + (((CB * bb / 16) & 1) ? 0 : 16);
         const size_t lds = 4 * 16 * ws + (size_t)s.K * xrec + (size_t)s.K * 8 * 4;
-        if (CB == 16) QLAUNCH("down", (down_t1_kernel<16, 2>), dim3(s.E / 8), dim3(256), lds, st, a);
-        else QLAUNCH("down", (down_t1_kernel<8, 2>), dim3(s.E / 8), dim3(256), lds, st, a);
+        if (L.down_type == 3) {
+            if (CB == 16) QLAUNCH("down", (down_t1_kernel<3, 16, 2>), dim3(s.E / 8), dim3(256), lds, st, a);
+            else QLAUNCH("down", (down_t1_kernel<3, 8, 2>), dim3(s.E / 8), dim3(256), lds, st, a);
+        } else {
+            if (CB == 16) QLAUNCH("down", (down_t1_kernel<2, 16, 2>), dim3(s.E / 8), dim3(256), lds, st, a);
+            else QLAUNCH("down", (down_t1_kernel<2, 8, 2>), dim3(s.E / 8), dim3(256), lds, st, a);
+        }
         return hipGetLastError();
     }
     /* slot tiles: the activations' int8 records first (unless the MFMA gate/up wrote them) */
@@ -1346,6 +1429,10 @@ hipError_t launch_down_exact(const Shape &s, const LayerDev &L, const Scratch &S
         if (NT == 4) QLAUNCH("down", (down_tile_kernel<2, 4>), grid, dim3(256), lds, st, a);
         else if (NT == 2) QLAUNCH("down", (down_tile_kernel<2, 2>), grid, dim3(256), lds, st, a);
         else QLAUNCH("down", (down_tile_kernel<2, 1>), grid, dim3(256), lds, st, a);
+    } else if (L.down_type == 3) {
+        if (NT == 4) QLAUNCH("down", (down_tile_kernel<3, 4>), grid, dim3(256), lds, st, a);
+        else if (NT == 2) QLAUNCH("down", (down_tile_kernel<3, 2>), grid, dim3(256), lds, st, a);
+        else QLAUNCH("down", (down_tile_kernel<3, 1>), grid, dim3(256), lds, st, a);
     } else {
         if (NT == 4) QLAUNCH("down", (down_tile_kernel<14, 4>), grid, dim3(256), lds, st, a);
         else if (NT == 2) QLAUNCH("down", (down_tile_kernel<14, 2>), grid, dim3(256), lds, st, a);
@@ -1587,7 +1674,7 @@ hipError_t launch_experts_mfma(const Shape &s, const LayerDev &L, const Scratch 
         QLAUNCH("combine", combine_kernel, dim3((n + 255) / 256), dim3(256), 0, st, S, s.E, s.K, T, out);
         return hipGetLastError();
     }
-    /* Q6_K down: the exact down kernel on the int8 blocks written above */
+    /* Q4_1 / Q6_K down: the exact down kernel on the int8 blocks written above */
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     return launch_down_exact(s, L, S, out, T, 0, st);
@@ -1614,6 +1701,13 @@ __global__ void block_dots_kernel(const uint8_t *base, int type, uint64_t rb, ui
             s += sdot4((int)(c & 0x0f0f0f0fu), (int)xw[p]) + sdot4((int)((c >> 4) & 0x0f0f0f0fu), (int)xw[4 + p]);
         }
         s -= 8 * ((int)x.s16[0] + (int)x.s16[1]);
+    } else if (type == 3) {
+        const uint8_t *b = r + (size_t)blk[i] * 20 + 4;
+        for (int p = 0; p < 4; p++) {
+            const uint32_t c = (uint32_t)b[4 * p] | ((uint32_t)b[4 * p + 1] << 8) | ((uint32_t)b[4 * p + 2] << 16) |
+                               ((uint32_t)b[4 * p + 3] << 24);
+            s += sdot4((int)(c & 0x0f0f0f0fu), (int)xw[p]) + sdot4((int)((c >> 4) & 0x0f0f0f0fu), (int)xw[4 + p]);
+        }
     } else {
         const int b = blk[i], sbi = b >> 3, h = (b & 7) >> 2, g = b & 3;
         const uint8_t *sb = r + (size_t)sbi * 210;
@@ -1702,12 +1796,12 @@ hipError_t launch_synth_f32(uint64_t key, uint64_t n, float sigma, float *out, h
     return hipGetLastError();
 }
 
-/* One thread per Q4_0 block (or Q6_K super-block) of all X experts. */
+/* One thread per Q4_0 / Q4_1 block (or Q6_K super-block) of all X experts. */
 __global__ void synth_experts_kernel(uint64_t seed, uint32_t layer, uint32_t kind, int type, int64_t rows,
                                      int64_t cols, int X, float sigma, uint8_t *base)
 {
     const int64_t per_row = type == 14 ? cols / 256 : cols / 32;
-    const uint64_t rb = type == 14 ? (uint64_t)per_row * 210 : (uint64_t)per_row * 18;
+    const uint64_t rb = (uint64_t)per_row * (type == 14 ? 210 : (type == 3 ? 20 : 18));
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     const int64_t per_e = rows * per_row;
     if (i >= per_e * X) return;
@@ -1719,6 +1813,10 @@ __global__ void synth_experts_kernel(uint64_t seed, uint32_t layer, uint32_t kin
         uint8_t blk[210];
         qmsg_synth_q6_k_block(key, (uint64_t)r * (uint64_t)cols + (uint64_t)b * 256, sigma, blk);
         for (int k = 0; k < 210; k++) dst[(uint64_t)b * 210 + k] = blk[k];
+    } else if (type == 3) {
+        uint8_t blk[20];
+        qmsg_synth_q4_1_block(key, (uint64_t)cols, (uint64_t)r, (uint64_t)b, sigma, blk);
+        for (int k = 0; k < 20; k++) dst[(uint64_t)b * 20 + k] = blk[k];
     } else {
         uint8_t blk[18];
         qmsg_synth_q4_0_block(key, (uint64_t)cols, (uint64_t)r, (uint64_t)b, sigma, blk);

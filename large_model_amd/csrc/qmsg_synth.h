@@ -9,7 +9,7 @@
  * Normal samples: Irwin-Hall sum of twelve 16-bit uniforms (three 64-bit hashes), centred and
  * scaled by 2^-16, which is N(0,1) up to the Irwin-Hall approximation (support +-6).
  * Q4_0 blocks use the usual ggml rounding (scale = signed max / -8, codes (x/d + 8.5) truncated,
- * capped at 15). Q6_K super-blocks use per-16 scales (max|x|/31) requantised to int8 against
+ * capped at 15); Q4_1 blocks take the block's min as m and (max - min) / 15 as d. Q6_K super-blocks use per-16 scales (max|x|/31) requantised to int8 against
  * one fp16 super-scale; only the block format matters for the layer, not this rounding rule. */
 #ifndef QMSG_SYNTH_H
 #define QMSG_SYNTH_H
@@ -142,6 +142,41 @@ QMSG_HD static inline void qmsg_synth_q4_0_block(uint64_t key, uint64_t cols, ui
     const uint64_t i0 = r * cols + b * 32;
     for (int j = 0; j < 32; j++) v[j] = qmsg_normal(key, i0 + (uint64_t)j) * sigma;
     qmsg_quant_q4_0_block(v, out);
+}
+
+/* One Q4_1 block {f16 d; f16 m; u8 qs[16]} from 32 values, nibbles as in Q4_0; w = q * d + m
+ * with m = min, d = (max - min) / 15, codes (x - m) / d rounded half up, capped at 15. */
+QMSG_HD static inline void qmsg_quant_q4_1_block(const float *v, uint8_t *out)
+{
+    float lo = v[0], hi = v[0];
+    for (int j = 1; j < 32; j++) {
+        lo = v[j] < lo ? v[j] : lo;
+        hi = v[j] > hi ? v[j] : hi;
+    }
+    const float d = (hi - lo) / 15.0f;
+    const float id = d != 0.0f ? 1.0f / d : 0.0f;
+    const uint16_t dh = qmsg_f32_to_f16(d), mh = qmsg_f32_to_f16(lo);
+    out[0] = (uint8_t)(dh & 0xFF);
+    out[1] = (uint8_t)(dh >> 8);
+    out[2] = (uint8_t)(mh & 0xFF);
+    out[3] = (uint8_t)(mh >> 8);
+    for (int j = 0; j < 16; j++) {
+        const float x0 = (v[j] - lo) * id, x1 = (v[j + 16] - lo) * id;
+        int q0 = (int)(x0 + 0.5f), q1 = (int)(x1 + 0.5f);
+        q0 = q0 > 15 ? 15 : q0;
+        q1 = q1 > 15 ? 15 : q1;
+        out[4 + j] = (uint8_t)(q0 | (q1 << 4));
+    }
+}
+
+/* Q4_1 block b of row r of a [rows][cols] slice drawn from N(0, sigma). */
+QMSG_HD static inline void qmsg_synth_q4_1_block(uint64_t key, uint64_t cols, uint64_t r, uint64_t b,
+                                                 float sigma, uint8_t *out)
+{
+    float v[32];
+    const uint64_t i0 = r * cols + b * 32;
+    for (int j = 0; j < 32; j++) v[j] = qmsg_normal(key, i0 + (uint64_t)j) * sigma;
+    qmsg_quant_q4_1_block(v, out);
 }
 
 /* One Q6_K super-block {u8 ql[128]; u8 qh[64]; i8 sc[16]; f16 d} = 210 bytes for 256 values

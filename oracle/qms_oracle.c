@@ -455,6 +455,9 @@ void orc_synth_experts(uint64_t seed, uint32_t layer, uint32_t kind, int type, i
                 if (type == ORC_T_Q6_K)
                     qmsg_synth_q6_k_block(key, (uint64_t)r * cols + (uint64_t)b * 256, sigma,
                                           m + (uint64_t)r * rb + (uint64_t)b * 210);
+                else if (type == ORC_T_Q4_1)
+                    qmsg_synth_q4_1_block(key, (uint64_t)cols, (uint64_t)r, (uint64_t)b, sigma,
+                                          m + (uint64_t)r * rb + (uint64_t)b * 20);
                 else
                     qmsg_synth_q4_0_block(key, (uint64_t)cols, (uint64_t)r, (uint64_t)b, sigma,
                                           m + (uint64_t)r * rb + (uint64_t)b * 18);

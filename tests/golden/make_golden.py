@@ -151,6 +151,8 @@ LAYERS = {
     "q235b_t16": (4096, 128, 8, 1536, 16, 2, orc.T_Q4_0, False, None),
     "q235b_q6k_t64": (4096, 128, 8, 1536, 64, 6, orc.T_Q6_K, False, None),
     "q235b_zipf_t512": (4096, 128, 8, 1536, 512, 5, orc.T_Q4_0, False, "zipf"),
+    "q235b_q41_t1": (4096, 128, 8, 1536, 1, 7, orc.T_Q4_1, False, None),
+    "q235b_q41_t5": (4096, 128, 8, 1536, 5, 7, orc.T_Q4_1, True, None),
 }
 
 
@@ -211,8 +213,12 @@ def main():
         sys.exit("oracle/_ref is not built: run `make -C oracle` where the reference sources are present")
     R.qms_matmul.argtypes = [ctypes.POINTER(QmsMat), P, ctypes.c_int, P]
     print("reference build:", orc.ref_library_path(), R.qref_isa().decode())
-    np.savez_compressed(os.path.join(HERE, "kat_kernels.npz"), **kat_kernels(R))
+    only = sys.argv[1:]                     # optional: regenerate just these layer files
+    if not only:
+        np.savez_compressed(os.path.join(HERE, "kat_kernels.npz"), **kat_kernels(R))
     for name, cfg in LAYERS.items():
+        if only and name not in only:
+            continue
         d = layer_case(R, name, *cfg)
         np.savez_compressed(os.path.join(HERE, f"layer_{name}.npz"), **d)
         print("wrote", name, "experts", len(d["experts"]))

@@ -14,6 +14,7 @@ CASES = [
     ("tiny_q4_l3_t5", 256, 16, 4, 128, 5, 3, orc.T_Q4_0, False),
     ("q30b_q6k_l3_t4", 2048, 128, 8, 768, 4, 3, orc.T_Q6_K, True),
     ("q30b_q4_l2_t1", 2048, 128, 8, 768, 1, 2, orc.T_Q4_0, True),
+    ("q30b_q41_l2_t3", 2048, 128, 8, 768, 3, 2, orc.T_Q4_1, True),
 ]
 
 

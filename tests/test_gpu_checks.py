@@ -37,7 +37,7 @@ def golden_input(d):
 
 
 DEVICE_GOLD = ["tiny_t1", "tiny_t7", "q30b_t1", "q235b_t1", "q235b_t4", "q235b_t16", "q235b_q6k_t64",
-               "q235b_zipf_t512"]
+               "q235b_zipf_t512", "q235b_q41_t1", "q235b_q41_t5"]
 
 
 @pytest.mark.parametrize("name", DEVICE_GOLD)
@@ -76,22 +76,24 @@ def test_uploaded_edge_layers(q, name):
 
 def test_block_dots_exact(q):
     """Per-block int32 dots of the device kernels against the oracle's block_dot (Q4_0 gate
-    and up, Q6_K down), random rows/blocks and int8 blocks of widely varying scale."""
+    and up, Q6_K and Q4_1 down), random rows/blocks and int8 blocks of widely varying scale."""
     E, X, K, F = 2048, 16, 4, 768
     rng = np.random.default_rng(1)
-    with q.Context(E, X, K, F) as ctx:
+    with q.Context(E, X, K, F, n_layer=2) as ctx:
         ctx.synth(0, 21, down_type=q.QMSG_T_Q6_K)
+        ctx.synth(1, 22, down_type=q.QMSG_T_Q4_1)
         _, g, u, dn = ctx.download(0)
-        for which, buf, t, rows, n in ((0, g, orc.T_Q4_0, F, E), (1, u, orc.T_Q4_0, F, E),
-                                       (2, dn, orc.T_Q6_K, E, F)):
+        dn41 = ctx.download(1)[3]
+        for layer, which, buf, t, rows, n in ((0, 0, g, orc.T_Q4_0, F, E), (0, 1, u, orc.T_Q4_0, F, E),
+                                              (0, 2, dn, orc.T_Q6_K, E, F), (1, 2, dn41, orc.T_Q4_1, E, F)):
             m = 384
             ex = rng.integers(0, X, m).astype(np.int32)
             row = rng.integers(0, rows, m).astype(np.int32)
             blk = rng.integers(0, n // 32, m).astype(np.int32)
             x = rng.standard_normal((m, 32)).astype(np.float32) * rng.uniform(0.01, 50, (m, 1)).astype(np.float32)
             xq = np.concatenate([orc.quantize_q8(x[i]) for i in range(m)])
-            print(f"[case] block_dots which={which} m={m}", flush=True)
-            got = ctx.block_dots(0, which, ex, row, blk, xq)
+            print(f"[case] block_dots layer={layer} which={which} m={m}", flush=True)
+            got = ctx.block_dots(layer, which, ex, row, blk, xq)
             rb = orc.row_bytes(t, n)
             ref = np.empty(m, np.int32)
             xfull = np.zeros(n // 32, orc.Q8_DTYPE)
@@ -99,7 +101,7 @@ def test_block_dots_exact(q):
                 off = (int(ex[i]) * rows + int(row[i])) * rb
                 xfull[blk[i]] = xq[i]
                 ref[i] = orc.block_dot(t, buf[off:off + rb], xfull, int(blk[i]))
-            assert np.array_equal(got, ref), which
+            assert np.array_equal(got, ref), (layer, which)
 
 
 def test_silu_matches_glibc(q):
@@ -148,12 +150,13 @@ def test_exp_matches_libc(q):
     assert np.array_equal(got.view(np.uint64)[~nan], ref.view(np.uint64)[~nan])
 
 
-def test_generator_bytes_identical(q):
+@pytest.mark.parametrize("dt", [orc.T_Q6_K, orc.T_Q4_1])
+def test_generator_bytes_identical(q, dt):
     E, X, K, F = 512, 16, 4, 256
     with q.Context(E, X, K, F) as ctx:
-        ctx.synth(0, 77, down_type=q.QMSG_T_Q6_K)
+        ctx.synth(0, 77, down_type=dt)
         r, g, u, d = ctx.download(0)
-    L = orc.Layer(E, X, K, F, 77, down_type=orc.T_Q6_K)
+    L = orc.Layer(E, X, K, F, 77, down_type=dt)
     assert np.array_equal(r, L.router) and np.array_equal(g, L.gate)
     assert np.array_equal(u, L.up) and np.array_equal(d, L.down)
 

@@ -23,6 +23,7 @@ CASES = [
     ("q30b_t64", 2048, 128, 8, 768, 64, 1, orc.T_Q4_0, False),
     ("q235b_t64", 4096, 128, 8, 1536, 64, 2, orc.T_Q4_0, False),
     ("q235b_q6k_t64", 4096, 128, 8, 1536, 64, 6, orc.T_Q6_K, False),
+    ("q235b_q41_t64", 4096, 128, 8, 1536, 64, 7, orc.T_Q4_1, False),
     ("q235b_zipf_t512", 4096, 128, 8, 1536, 512, 5, orc.T_Q4_0, True),
 ]
 

@@ -135,6 +135,10 @@ def brute_block_dot(t, w_row, xq, blk):
         b = w_row[blk * 18 + 2: blk * 18 + 18].astype(np.int64)
         codes = np.concatenate([b & 15, b >> 4]) - 8
         return int((codes * q).sum())
+    if t == orc.T_Q4_1:
+        b = w_row[blk * 20 + 4: blk * 20 + 20].astype(np.int64)
+        codes = np.concatenate([b & 15, b >> 4])
+        return int((codes * q).sum())
     sb = w_row[(blk // 8) * 210:(blk // 8) * 210 + 210].astype(np.int64)
     half, g = (blk % 8) // 4, blk % 4
     ql, qh = sb[64 * half: 64 * half + 64], sb[128 + 32 * half: 128 + 32 * half + 32]
@@ -145,7 +149,7 @@ def brute_block_dot(t, w_row, xq, blk):
     return int(sc[2 * g] * (codes[:16] * q[:16]).sum() + sc[2 * g + 1] * (codes[16:] * q[16:]).sum())
 
 
-@pytest.mark.parametrize("t,n", [(orc.T_Q4_0, 1536), (orc.T_Q6_K, 1536)])
+@pytest.mark.parametrize("t,n", [(orc.T_Q4_0, 1536), (orc.T_Q4_1, 1536), (orc.T_Q6_K, 1536)])
 def test_block_dot_brute_force(t, n):
     L = orc.Layer(256, 16, 4, n, 9, down_type=t, experts=[3])
     x = np.random.default_rng(5).standard_normal(n).astype(np.float32)
