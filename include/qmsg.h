@@ -117,6 +117,61 @@ int qmsg_layer_synth(qmsg_ctx *ctx, int layer, uint64_t seed, int gate_type, int
  * pointer may be NULL; sizes are X*E*4 for the router and X*expert_bytes for each tensor. */
 int qmsg_layer_download(qmsg_ctx *ctx, int layer, float *router, void *gate, void *up, void *down);
 
+/* ------------------------------------------------------------------ GGUF files ---- */
+
+/* A parsed GGUF v3 model: the tensor table and the first shard's scalar metadata, QmsGguf
+ * (src/gguf.h:33-44). Parsing reads headers only and needs no GPU. */
+typedef struct qmsg_gguf qmsg_gguf;
+
+/* One tensor-table entry, QmsTensor (src/gguf.h:15-23): ne[0] is the contiguous dimension,
+ * unused ne are 1; off is the absolute byte offset in its shard file; nbytes is 0 for a type
+ * qms_row_bytes does not know. */
+typedef struct {
+    char name[96];
+    int type;
+    int n_dims;
+    int64_t ne[4];
+    int shard;
+    uint64_t off;
+    uint64_t nbytes;
+} qmsg_tensor;
+
+/* qms_gguf_open (src/gguf.c:222-241, 112-194): parse `path`, or every shard of a
+ * "<stem>-00001-of-0000N.gguf" set (src/gguf.c:198-219). Version 3 only; a tensor that runs
+ * past the end of its file, or a truncated header, is an error. On failure *out is NULL and
+ * qmsg_last_error(NULL) has the reason. */
+int qmsg_gguf_open(qmsg_gguf **out, const char *path);
+/* qms_gguf_close (src/gguf.c:243-253). */
+void qmsg_gguf_close(qmsg_gguf *g);
+
+/* Number of tensors, and entry i of the table (shard order, then file order). */
+int qmsg_gguf_n_tensors(const qmsg_gguf *g);
+int qmsg_gguf_tensor(const qmsg_gguf *g, int i, qmsg_tensor *out);
+/* qms_gguf_find (src/gguf.c:255-260): index of the tensor called `name`, or -1. */
+int qmsg_gguf_find(const qmsg_gguf *g, const char *name);
+/* qms_gguf_get_int / qms_gguf_get_float (src/gguf.c:269-283): a required numeric scalar of
+ * the first shard's metadata (any integer, float or bool type, converted as the reference
+ * does); QMSG_E_INVALID when the key is missing or holds a string. Arrays are not kept. */
+int qmsg_gguf_get_int(const qmsg_gguf *g, const char *key, int64_t *out);
+int qmsg_gguf_get_float(const qmsg_gguf *g, const char *key, double *out);
+/* A string scalar (such as general.architecture) into buf (truncated to n-1 bytes). */
+int qmsg_gguf_get_str(const qmsg_gguf *g, const char *key, char *buf, size_t n);
+
+/* The MoE half of read_cfg (src/model.c:278-310): general.architecture must be qwen3moe;
+ * qwen3moe.{embedding_length, expert_count, expert_used_count, expert_feed_forward_length}
+ * fill cfg, qwen3moe.block_count n_layer and qwen3moe.attention.layer_norm_rms_epsilon eps
+ * (either pointer may be NULL). */
+int qmsg_gguf_moe_cfg(const qmsg_gguf *g, qmsg_cfg *cfg, int *n_layer, float *eps);
+
+/* The MoE lines of qms_model_load (src/model.c:349, 359-362) for file layers first ..
+ * first+n-1 into the context's layers of the same index: blk.L.ffn_gate_inp.weight (F32
+ * [n_expert][n_embd]), blk.L.ffn_{gate,up}_exps.weight ([n_expert][n_ff_exp][n_embd]),
+ * blk.L.ffn_down_exps.weight ([n_expert][n_embd][n_ff_exp]) and blk.L.ffn_norm.weight (F32
+ * [n_embd]), shapes checked like load_mat / load_experts / load_f32_vec (src/model.c:52-85,
+ * 133-157). The bytes go from the file to HBM unchanged, through pinned staging buffers
+ * that several reader threads fill while the previous buffer is copied. */
+int qmsg_gguf_upload(qmsg_ctx *ctx, const qmsg_gguf *g, int first, int n);
+
 /* ------------------------------------------------------------------ the layer ---- */
 
 /* moe(m, l, xn, h, T, out) (src/model.c:1032): out[T][E] = sum over the top-K experts of

@@ -5,9 +5,11 @@
 #include <cstdio>
 #include <cstring>
 #include <string>
+#include <thread>
 #include <vector>
 
 #include "../../include/qmsg.h"
+#include "qmsg_gguf.h"
 #include "qmsg_internal.h"
 #include "qmsg_synth.h"
 
@@ -230,7 +232,9 @@ static int layer_alloc(qmsg_ctx *c, LayerStore &L, int gt, int ut, int dt)
     if (dt == QMSG_T_Q6_K && F % 256)
         return fail(c, QMSG_E_UNSUPPORTED, "Q6_K down needs n_ff_exp %% 256 == 0 (got %lld)", (long long)F);
     hipFree(L.router); hipFree(L.gate); hipFree(L.up); hipFree(L.down);
+    float *norm = L.norm;                     /* the ffn_norm weights stay with the layer */
     L = LayerStore{};
+    L.norm = norm;
     std::vector<void *> dummy;
     const size_t gb = (size_t)row_bytes(gt, E) * F * X, ub = (size_t)row_bytes(ut, E) * F * X,
                  db = (size_t)row_bytes(dt, F) * E * X;
@@ -240,6 +244,7 @@ static int layer_alloc(qmsg_ctx *c, LayerStore &L, int gt, int ut, int dt)
         (rc = dev_alloc(c, (void **)&L.down, db, dummy))) {
         hipFree(L.router); hipFree(L.gate); hipFree(L.up); hipFree(L.down);
         L = LayerStore{};
+        L.norm = norm;
         return rc;
     }
     L.gate_type = gt;
@@ -342,6 +347,175 @@ int qmsg_layer_download(qmsg_ctx *c, int layer, float *router, void *gate, void 
     if (gate) HIP_TRY(c, hipMemcpy(gate, L.gate, X * d.gate_eb, hipMemcpyDeviceToHost));
     if (up) HIP_TRY(c, hipMemcpy(up, L.up, X * d.up_eb, hipMemcpyDeviceToHost));
     if (down) HIP_TRY(c, hipMemcpy(down, L.down, X * d.down_eb, hipMemcpyDeviceToHost));
+    return QMSG_OK;
+}
+
+}  // extern "C"
+
+namespace {
+
+/* File -> HBM copies through two pinned staging buffers: while one buffer's bytes travel
+ * over PCIe (hipMemcpyAsync on the context's stream), reader threads fill the other with
+ * pread. A buffer is refilled only after the event recorded behind its last copy. */
+class Stager {
+public:
+    static constexpr size_t kCap = 64u << 20;        /* bytes per staging buffer            */
+    static constexpr size_t kPiece = 8u << 20;       /* bytes per reader thread and fill    */
+
+    explicit Stager(qmsg_ctx *c) : c_(c) {}
+    ~Stager()
+    {
+        for (int k = 0; k < 2; k++) {
+            if (ev_[k]) {
+                hipEventSynchronize(ev_[k]);
+                hipEventDestroy(ev_[k]);
+            }
+            if (buf_[k]) hipHostFree(buf_[k]);
+        }
+    }
+
+    int init()
+    {
+        for (int k = 0; k < 2; k++) {
+            if (hipHostMalloc(&buf_[k], kCap, hipHostMallocDefault) != hipSuccess) {
+                buf_[k] = nullptr;
+                return fail(c_, QMSG_E_NOMEM, "gguf upload: pinned staging buffer of %zu bytes", kCap);
+            }
+            HIP_TRY(c_, hipEventCreateWithFlags(&ev_[k], hipEventDisableTiming));
+        }
+        return QMSG_OK;
+    }
+
+    /* Tensor t of g (all its bytes) to device address dst. */
+    int copy(const qmsg_gguf *g, const qmsg_tensor &t, void *dst)
+    {
+        for (uint64_t done = 0; done < t.nbytes;) {
+            const size_t n = (size_t)(t.nbytes - done < kCap ? t.nbytes - done : kCap);
+            const int k = next_;
+            next_ ^= 1;
+            if (used_[k]) HIP_TRY(c_, hipEventSynchronize(ev_[k]));
+            if (read(g, t.shard, t.off + done, n, (uint8_t *)buf_[k]))
+                return fail(c_, QMSG_E_INVALID, "gguf upload: read failed for %s", t.name);
+            HIP_TRY(c_, hipMemcpyAsync((uint8_t *)dst + done, buf_[k], n, hipMemcpyHostToDevice, c_->stream));
+            HIP_TRY(c_, hipEventRecord(ev_[k], c_->stream));
+            used_[k] = true;
+            done += n;
+            bytes_ += n;
+        }
+        return QMSG_OK;
+    }
+
+    int finish()
+    {
+        HIP_TRY(c_, hipStreamSynchronize(c_->stream));
+        return QMSG_OK;
+    }
+
+private:
+    static int read(const qmsg_gguf *g, int shard, uint64_t off, size_t n, uint8_t *dst)
+    {
+        const size_t np = (n + kPiece - 1) / kPiece;
+        if (np <= 1) return gguf_pread(g, shard, off, n, dst);
+        std::vector<std::thread> th;
+        std::vector<int> rc(np, 0);
+        for (size_t p = 1; p < np; p++)
+            th.emplace_back([&, p] {
+                const size_t a = p * kPiece, m = n - a < kPiece ? n - a : kPiece;
+                rc[p] = gguf_pread(g, shard, off + a, m, dst + a);
+            });
+        rc[0] = gguf_pread(g, shard, off, kPiece, dst);
+        for (auto &x : th) x.join();
+        for (int v : rc)
+            if (v) return v;
+        return 0;
+    }
+
+    qmsg_ctx *c_;
+    void *buf_[2] = { nullptr, nullptr };
+    hipEvent_t ev_[2] = { nullptr, nullptr };
+    bool used_[2] = { false, false };
+    int next_ = 0;
+    uint64_t bytes_ = 0;
+};
+
+/* One layer's MoE tensors in the table, checked like load_mat / load_experts / load_f32_vec
+ * (src/model.c:52-85, 133-157). */
+struct LayerTensors {
+    const qmsg_tensor *router, *gate, *up, *down, *norm;
+};
+
+int find_layer(qmsg_ctx *c, const qmsg_gguf *g, int l, LayerTensors &out)
+{
+    const int64_t E = c->cfg.n_embd, X = c->cfg.n_expert, F = c->cfg.n_ff_exp;
+    auto need = [&](const char *what, const qmsg_tensor *&t) -> int {
+        char name[96];
+        snprintf(name, sizeof name, "blk.%d.%s.weight", l, what);
+        const int i = gguf_find(g, name);
+        if (i < 0) return fail(c, QMSG_E_INVALID, "model: missing tensor %s", name);
+        t = &g->tensors[(size_t)i];
+        return QMSG_OK;
+    };
+    int rc;
+    if ((rc = need("ffn_gate_inp", out.router)) || (rc = need("ffn_gate_exps", out.gate)) ||
+        (rc = need("ffn_up_exps", out.up)) || (rc = need("ffn_down_exps", out.down)) ||
+        (rc = need("ffn_norm", out.norm)))
+        return rc;
+    const qmsg_tensor *r = out.router;
+    if (r->ne[0] != E || r->ne[1] != X || r->ne[2] != 1 || !row_bytes(r->type, E))
+        return fail(c, QMSG_E_INVALID, "model: %s expected [%lld x %lld], got ne=[%lld,%lld,%lld]", r->name,
+                    (long long)X, (long long)E, (long long)r->ne[0], (long long)r->ne[1], (long long)r->ne[2]);
+    if (r->type != QMSG_T_F32)
+        return fail(c, QMSG_E_UNSUPPORTED, "%s: the router kernels take F32 (got type %d)", r->name, r->type);
+    const struct { const qmsg_tensor *t; int64_t rows, cols; } ex[3] = {
+        { out.gate, F, E }, { out.up, F, E }, { out.down, E, F }
+    };
+    for (const auto &k : ex)
+        if (k.t->ne[0] != k.cols || k.t->ne[1] != k.rows || k.t->ne[2] != X || !row_bytes(k.t->type, k.cols))
+            return fail(c, QMSG_E_INVALID, "model: %s expected [%lld x %lld x %lld], got ne=[%lld,%lld,%lld]", k.t->name,
+                        (long long)X, (long long)k.rows, (long long)k.cols, (long long)k.t->ne[0],
+                        (long long)k.t->ne[1], (long long)k.t->ne[2]);
+    if (out.norm->type != QMSG_T_F32 || out.norm->ne[0] != E)
+        return fail(c, QMSG_E_INVALID, "model: %s expected F32[%lld], got type %d [%lld]", out.norm->name,
+                    (long long)E, out.norm->type, (long long)out.norm->ne[0]);
+    return QMSG_OK;
+}
+
+}  // namespace
+
+namespace qmsg {
+void set_global_error(const char *msg) { g_create_error = msg; }
+}  // namespace qmsg
+
+extern "C" {
+
+int qmsg_gguf_upload(qmsg_ctx *c, const qmsg_gguf *g, int first, int n)
+{
+    if (!c || !g || n < 0) return QMSG_E_INVALID;
+    if (first < 0 || first + n > c->n_layer)
+        return fail(c, QMSG_E_RANGE, "layers %d .. %d outside [0, %d)", first, first + n - 1, c->n_layer);
+    /* every layer's tensors are checked before any device memory changes */
+    std::vector<LayerTensors> lt((size_t)n);
+    int rc;
+    for (int i = 0; i < n; i++)
+        if ((rc = find_layer(c, g, first + i, lt[(size_t)i]))) return rc;
+    HIP_TRY(c, hipSetDevice(c->device));
+    HIP_TRY(c, hipStreamSynchronize(c->stream));
+    Stager st(c);
+    if ((rc = st.init())) return rc;
+    for (int i = 0; i < n; i++) {
+        const LayerTensors &t = lt[(size_t)i];
+        LayerStore &L = c->layers[(size_t)(first + i)];
+        if ((rc = layer_alloc(c, L, t.gate->type, t.up->type, t.down->type))) return rc;
+        if (!L.norm) {
+            std::vector<void *> tmp;
+            if ((rc = dev_alloc(c, (void **)&L.norm, (size_t)c->cfg.n_embd * 4, tmp))) return rc;
+        }
+        if ((rc = st.copy(g, *t.router, L.router)) || (rc = st.copy(g, *t.gate, L.gate)) ||
+            (rc = st.copy(g, *t.up, L.up)) || (rc = st.copy(g, *t.down, L.down)) || (rc = st.copy(g, *t.norm, L.norm)))
+            return rc;
+    }
+    if ((rc = st.finish())) return rc;
+    for (int i = 0; i < n; i++) c->layers[(size_t)(first + i)].ready = true;
     return QMSG_OK;
 }
 

@@ -18,7 +18,7 @@ import numpy as np
 
 __all__ = [
     "QMSG_T_F32", "QMSG_T_Q4_0", "QMSG_T_Q4_1", "QMSG_T_Q6_K", "PATH_AUTO", "PATH_EXACT", "PATH_MFMA",
-    "Q8_DTYPE", "QmsgError", "Context", "row_bytes", "lib", "library_path",
+    "Q8_DTYPE", "QmsgError", "Context", "Gguf", "row_bytes", "lib", "library_path",
 ]
 
 QMSG_T_F32, QMSG_T_F16, QMSG_T_Q4_0, QMSG_T_Q4_1, QMSG_T_Q8_0, QMSG_T_Q6_K = 0, 1, 2, 3, 8, 14
@@ -64,6 +64,12 @@ class _Cfg(ctypes.Structure):
                 ("n_ff_exp", ctypes.c_int)]
 
 
+class _Tensor(ctypes.Structure):
+    _fields_ = [("name", ctypes.c_char * 96), ("type", ctypes.c_int), ("n_dims", ctypes.c_int),
+                ("ne", ctypes.c_int64 * 4), ("shard", ctypes.c_int), ("off", ctypes.c_uint64),
+                ("nbytes", ctypes.c_uint64)]
+
+
 class _Debug(ctypes.Structure):
     _fields_ = [(n, ctypes.c_void_p) for n in
                 ("logits", "sel", "wt", "start", "slot_t", "slot_of", "active", "n_active", "xq", "gu", "act",
@@ -98,6 +104,16 @@ _SIGS = {
     "qmsg_eval_silu": (_I, [_P, _P, _I, _P]),
     "qmsg_eval_exp": (_I, [_P, _P, _I, _P]),
     "qmsg_calibrate_copy": (_I, [_P, _P, _P, ctypes.c_size_t]),
+    "qmsg_gguf_open": (_I, [ctypes.POINTER(_P), ctypes.c_char_p]),
+    "qmsg_gguf_close": (None, [_P]),
+    "qmsg_gguf_n_tensors": (_I, [_P]),
+    "qmsg_gguf_tensor": (_I, [_P, _I, ctypes.POINTER(_Tensor)]),
+    "qmsg_gguf_find": (_I, [_P, ctypes.c_char_p]),
+    "qmsg_gguf_get_int": (_I, [_P, ctypes.c_char_p, ctypes.POINTER(ctypes.c_int64)]),
+    "qmsg_gguf_get_float": (_I, [_P, ctypes.c_char_p, ctypes.POINTER(ctypes.c_double)]),
+    "qmsg_gguf_get_str": (_I, [_P, ctypes.c_char_p, ctypes.c_char_p, ctypes.c_size_t]),
+    "qmsg_gguf_moe_cfg": (_I, [_P, ctypes.POINTER(_Cfg), ctypes.POINTER(_I), ctypes.POINTER(ctypes.c_float)]),
+    "qmsg_gguf_upload": (_I, [_P, _P, _I, _I]),
     "qmsg_device_info": (_I, [_P, ctypes.POINTER(_I), ctypes.POINTER(_I), ctypes.POINTER(ctypes.c_uint64),
                               ctypes.c_char_p, _I]),
 }
@@ -127,6 +143,82 @@ class QmsgError(RuntimeError):
 
 def _ptr(a: Optional[np.ndarray]):
     return None if a is None else a.ctypes.data_as(_P)
+
+
+class Gguf:
+    """A parsed GGUF v3 model (qms_gguf_open, src/gguf.c:222-241): tensor table and the first
+    shard's scalar metadata. Needs no GPU; ``Context.load_gguf`` moves its MoE tensors to HBM."""
+
+    def __init__(self, path: str):
+        h = _P()
+        st = lib.qmsg_gguf_open(ctypes.byref(h), os.fsencode(path))
+        if st != 0:
+            raise QmsgError(st, lib.qmsg_last_error(None).decode())
+        self._h = h
+        self.path = path
+
+    def close(self):
+        if getattr(self, "_h", None):
+            lib.qmsg_gguf_close(self._h)
+            self._h = None
+
+    def __del__(self):
+        self.close()
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *a):
+        self.close()
+
+    def _raise(self, st: int):
+        raise QmsgError(st, lib.qmsg_last_error(None).decode())
+
+    def tensors(self) -> list:
+        """The tensor table: dicts of name, type, n_dims, ne (4 ints), shard, off, nbytes."""
+        out = []
+        t = _Tensor()
+        for i in range(lib.qmsg_gguf_n_tensors(self._h)):
+            st = lib.qmsg_gguf_tensor(self._h, i, ctypes.byref(t))
+            if st != 0:
+                self._raise(st)
+            out.append({"name": t.name.decode(), "type": t.type, "n_dims": t.n_dims, "ne": list(t.ne),
+                        "shard": t.shard, "off": t.off, "nbytes": t.nbytes})
+        return out
+
+    def find(self, name: str) -> int:
+        return lib.qmsg_gguf_find(self._h, name.encode())
+
+    def get_int(self, key: str) -> int:
+        v = ctypes.c_int64()
+        st = lib.qmsg_gguf_get_int(self._h, key.encode(), ctypes.byref(v))
+        if st != 0:
+            self._raise(st)
+        return v.value
+
+    def get_float(self, key: str) -> float:
+        v = ctypes.c_double()
+        st = lib.qmsg_gguf_get_float(self._h, key.encode(), ctypes.byref(v))
+        if st != 0:
+            self._raise(st)
+        return v.value
+
+    def get_str(self, key: str) -> str:
+        buf = ctypes.create_string_buffer(512)
+        st = lib.qmsg_gguf_get_str(self._h, key.encode(), buf, len(buf))
+        if st != 0:
+            self._raise(st)
+        return buf.value.decode()
+
+    def moe_cfg(self) -> dict:
+        """read_cfg's MoE keys (src/model.c:278-310): n_embd, n_expert, n_used, n_ff_exp,
+        n_layer, eps."""
+        cfg, nl, eps = _Cfg(), _I(), ctypes.c_float()
+        st = lib.qmsg_gguf_moe_cfg(self._h, ctypes.byref(cfg), ctypes.byref(nl), ctypes.byref(eps))
+        if st != 0:
+            self._raise(st)
+        return {"n_embd": cfg.n_embd, "n_expert": cfg.n_expert, "n_used": cfg.n_used, "n_ff_exp": cfg.n_ff_exp,
+                "n_layer": nl.value, "eps": eps.value}
 
 
 class Context:
@@ -196,6 +288,30 @@ class Context:
         down = np.empty(X * E * row_bytes(dt, F), np.uint8)
         self._check(lib.qmsg_layer_download(self._h, layer, _ptr(router), _ptr(gate), _ptr(up), _ptr(down)))
         return router, gate, up, down
+
+    def load_gguf(self, g: Gguf, first: int = 0, n: Optional[int] = None):
+        """Copy file layers first .. first+n-1 (router, gate/up/down experts, ffn_norm) of a
+        parsed GGUF into the context's layers of the same index."""
+        n = self.n_layer - first if n is None else n
+        self._check(lib.qmsg_gguf_upload(self._h, g._h, first, n))
+        for t in g.tensors():
+            parts = t["name"].split(".")
+            if len(parts) == 4 and parts[0] == "blk" and parts[2] in ("ffn_gate_exps", "ffn_up_exps", "ffn_down_exps"):
+                layer = int(parts[1])
+                if first <= layer < first + n:
+                    types = list(self._types.get(layer, (QMSG_T_Q4_0,) * 3))
+                    types[("ffn_gate_exps", "ffn_up_exps", "ffn_down_exps").index(parts[2])] = t["type"]
+                    self._types[layer] = tuple(types)
+
+    @classmethod
+    def from_gguf(cls, g: Gguf, max_tokens: int = 16, device: int = 0) -> "Context":
+        """A context shaped by the file's MoE config with every layer loaded."""
+        c = g.moe_cfg()
+        ctx = cls(c["n_embd"], c["n_expert"], c["n_used"], c["n_ff_exp"], n_layer=c["n_layer"],
+                  max_tokens=max_tokens, device=device)
+        ctx.eps = c["eps"]
+        ctx.load_gguf(g, 0, c["n_layer"])
+        return ctx
 
     def set_path(self, path: int):
         self._check(lib.qmsg_set_path(self._h, path))

@@ -259,6 +259,9 @@ def load_ref():
     R.qref_silu.argtypes = [ctypes.c_float]
     R.qref_rmsnorm_unit.argtypes = [_P, _P, ctypes.c_int, ctypes.c_float]
     R.qref_rmsnorm.argtypes = [_P, _P, _P, ctypes.c_int, ctypes.c_float]
+    R.qref_gguf_table.argtypes = [ctypes.c_char_p, ctypes.c_int] + [_P] * 7
+    R.qref_gguf_value.argtypes = [ctypes.c_char_p, ctypes.c_char_p, _P, _P]
+    R.qref_gguf_moe.argtypes = [ctypes.c_char_p, ctypes.c_int, _P, ctypes.c_int, _P]
     R.qref_isa.restype = ctypes.c_char_p
     R.qref_max_threads.restype = ctypes.c_int
     return R

@@ -77,3 +77,56 @@ const char *qref_isa(void)
     return "scalar";
 #endif
 }
+
+/* The reference's GGUF reader (qms_gguf_open, src/gguf.c:222-241) on a file: the tensor
+ * table flattened into caller arrays (up to cap entries; names 96 bytes apart). Returns the
+ * number of tensors, or -1 where qms_gguf_open fails. */
+int qref_gguf_table(const char *path, int cap, char *names, int *type, int *n_dims, int64_t *ne, int *shard,
+                    uint64_t *off, uint64_t *nbytes)
+{
+    QmsGguf g;
+    if (qms_gguf_open(&g, path) != 0) return -1;
+    const int n = g.n_tensors;
+    for (int i = 0; i < n && i < cap; i++) {
+        const QmsTensor *t = &g.tensors[i];
+        memcpy(names + (size_t)i * QMS_MAX_NAME, t->name, QMS_MAX_NAME);
+        type[i] = t->type;
+        n_dims[i] = t->n_dims;
+        for (int d = 0; d < 4; d++) ne[4 * i + d] = t->ne[d];
+        shard[i] = t->shard;
+        off[i] = t->off;
+        nbytes[i] = t->nbytes;
+    }
+    qms_gguf_close(&g);
+    return n;
+}
+
+/* qms_gguf_get_int and qms_gguf_get_float of one key: bit 0 set when get_int failed, bit 1
+ * when get_float failed; -1 where the file does not open. */
+int qref_gguf_value(const char *path, const char *key, int64_t *i, double *f)
+{
+    QmsGguf g;
+    if (qms_gguf_open(&g, path) != 0) return -1;
+    int rc = 0;
+    if (qms_gguf_get_int(&g, key, i) != 0) rc |= 1;
+    if (qms_gguf_get_float(&g, key, f) != 0) rc |= 2;
+    qms_gguf_close(&g);
+    return rc;
+}
+
+/* A whole model file loaded by the reference (qms_model_load: resident weights, KV cache for
+ * 8 positions), then its moe() on layer l for caller rows xn [T][n_embd]. Returns -1 when the
+ * load fails, else moe()'s status. */
+int qref_gguf_moe(const char *path, int l, const float *xn, int T, float *out)
+{
+    QmsModel m;
+    QmsLoadOpts o;
+    memset(&o, 0, sizeof o);
+    o.ctx = 8;
+    o.force = 1;
+    o.pin_layers = -1;
+    if (qms_model_load(&m, path, &o) != 0) return -1;
+    const int rc = l >= 0 && l < m.c.n_layer ? moe(&m, l, xn, xn, T, out) : -1;
+    qms_model_free(&m);
+    return rc;
+}
