@@ -281,6 +281,55 @@ def run_stack(args, w):
     print(json.dumps(result), flush=True)
 
 
+def gguf_load(args):
+    """File -> HBM rate of qmsg_gguf_upload for n layers of the 235B shape (Q4_0 gate/up; down
+    Q4_0 and Q4_1 on alternate layers, as real files mix them), page cache warm: the file is
+    written first, then loaded --steps times; prints one JSON line with the best rate."""
+    import tempfile
+
+    from large_model_amd import gguf_writer as gw
+    E, X, K, F, NL = 4096, 128, 8, 1536, args.gguf_load
+    tensors = []
+    for l in range(NL):
+        dt = qmsg.QMSG_T_Q4_1 if l % 2 else qmsg.QMSG_T_Q4_0
+        b = f"blk.{l}."
+        tensors += [
+            (b + "ffn_norm.weight", qmsg.QMSG_T_F32, [E], np.ones(E, np.float32).tobytes()),
+            (b + "ffn_gate_inp.weight", qmsg.QMSG_T_F32, [E, X], np.zeros((X, E), np.float32).tobytes()),
+            (b + "ffn_gate_exps.weight", qmsg.QMSG_T_Q4_0, [E, F, X], qmsg.row_bytes(qmsg.QMSG_T_Q4_0, E) * F * X),
+            (b + "ffn_up_exps.weight", qmsg.QMSG_T_Q4_0, [E, F, X], qmsg.row_bytes(qmsg.QMSG_T_Q4_0, E) * F * X),
+            (b + "ffn_down_exps.weight", dt, [F, E, X], qmsg.row_bytes(dt, F) * E * X),
+        ]
+    nbytes = sum(t[3] if isinstance(t[3], int) else len(t[3]) for t in tensors)
+    d = tempfile.mkdtemp(prefix="qmsg_gguf_")
+    path = os.path.join(d, "moe.gguf")
+    try:
+        t0 = time.perf_counter()
+        gw.write_gguf(path, gw.moe_header(E, X, K, F, NL), tensors)
+        log(f"wrote {nbytes / 1e9:.2f} GB of MoE tensors ({NL} layers) in {time.perf_counter() - t0:.1f} s")
+        runs = []
+        with qmsg.Gguf(path) as g, qmsg.Context(E, X, K, F, n_layer=NL, max_tokens=1) as ctx:
+            for r in range(args.steps):
+                t0 = time.perf_counter()
+                ctx.load_gguf(g, 0, NL)
+                runs.append(time.perf_counter() - t0)
+                log(f"load {r}: {runs[-1]:.3f} s, {nbytes / runs[-1] / 1e9:.2f} GB/s")
+            dev = ctx.device_info()
+    finally:
+        if os.path.exists(path):
+            os.remove(path)
+        os.rmdir(d)
+    best = min(runs)
+    print(json.dumps({
+        "metric": "GGUF MoE tensors file -> HBM (qmsg_gguf_upload), page cache warm",
+        "value": round(nbytes / best / 1e9, 3), "unit": "GB/s", "higher_is_better": True, "n_gpus": 1,
+        "steps": args.steps, "bytes_per_load": nbytes, "seconds": [round(t, 4) for t in runs],
+        "config": {"workload": f"{NL} layers of the Qwen3-235B-A22B MoE shape (E=4096 X=128 F=1536)",
+                   "staging": "2 x 64 MiB pinned buffers, 8 MiB pread pieces on parallel threads"},
+        "host_cpu": cpu_model(), "device": dev,
+    }), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -294,6 +343,9 @@ def main():
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES",
                     help="instead of the layer, run the plain copy kernel on BYTES (reference transfer "
                          "for HBM byte counters) --steps times and exit")
+    ap.add_argument("--gguf-load", type=int, default=0, metavar="LAYERS",
+                    help="instead of the layer, time loading LAYERS 235B-shape MoE layers from a GGUF file "
+                         "into HBM (--steps loads, default 3) and exit")
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -304,6 +356,10 @@ def main():
 
     if args.copy_calibration:
         copy_calibration(args.copy_calibration, args.steps)
+        return
+    if args.gguf_load:
+        args.steps = args.steps or 3
+        gguf_load(args)
         return
 
     w = WORKLOADS[args.workload]
