@@ -172,6 +172,23 @@ int qmsg_gguf_moe_cfg(const qmsg_gguf *g, qmsg_cfg *cfg, int *n_layer, float *ep
  * that several reader threads fill while the previous buffer is copied. */
 int qmsg_gguf_upload(qmsg_ctx *ctx, const qmsg_gguf *g, int first, int n);
 
+/* ------------------------------------------------------------------ dense (trunk) products ---- */
+
+/* A dense weight matrix resident in HBM, a QmsMat (src/quant.h:11-16) loaded by load_mat
+ * (src/model.c:67-85): rows of row_bytes GGUF bytes, copied unchanged; *id names it in
+ * qmsg_matmul_n. Q4_0 and Q4_1 rows with cols % 256 == 0 (the trunk's attn_q/k/v/output). */
+int qmsg_mat_upload(qmsg_ctx *ctx, const qmsg_mat *host, int *id);
+/* The same from a parsed GGUF file, by tensor name (e.g. "blk.0.attn_q.weight"). */
+int qmsg_gguf_upload_mat(qmsg_ctx *ctx, const qmsg_gguf *g, const char *name, int *id);
+
+/* qms_matmul_n (src/quant.c:128-170) on resident matrices ids[0..nW-1] of equal cols C:
+ * every row of x [T][C] is quantised to int8 blocks (qms_quantize_q8) and ys[i][t][r] =
+ * qms_vec_dot_q8(row r of W_i, xq_t), bit-identical to the reference's fast path. Host
+ * buffers; blocks until done. The first call with a larger T*C allocates device buffers. */
+int qmsg_matmul_n(qmsg_ctx *ctx, const int *ids, int nW, const float *x, int T, float *const *ys);
+/* The same on device buffers (x 16-byte aligned), enqueued on the context's stream. */
+int qmsg_matmul_n_device(qmsg_ctx *ctx, const int *ids, int nW, const float *d_x, int T, float *const *d_ys);
+
 /* ------------------------------------------------------------------ the layer ---- */
 
 /* moe(m, l, xn, h, T, out) (src/model.c:1032): out[T][E] = sum over the top-K experts of

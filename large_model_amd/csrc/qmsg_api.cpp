@@ -25,6 +25,14 @@ struct LayerStore {
     bool ready = false;
 };
 
+/* A dense (trunk) matrix resident in HBM, QmsMat (src/quant.h:11-16) with device data. */
+struct DenseStore {
+    uint8_t *w = nullptr;
+    int type = -1;
+    int64_t rows = 0, cols = 0;
+    uint64_t rb = 0;
+};
+
 struct ProfRec {
     std::string name;
     hipEvent_t a, b;
@@ -58,6 +66,12 @@ struct qmsg_ctx {
     Scratch S{};
     std::vector<void *> scratch_allocs, user_allocs;
     float *d_x = nullptr, *d_out = nullptr;
+    std::vector<DenseStore> mats;
+    /* grow-on-demand buffers of the dense products: int8 records, host-call staging */
+    uint8_t *dense_xqk = nullptr;
+    size_t dense_xqk_bytes = 0;
+    void *dense_io = nullptr;
+    size_t dense_io_bytes = 0;
     std::string err;
     bool prof = false;
     std::vector<ProfRec> prof_recs, prof_free;
@@ -194,6 +208,9 @@ void qmsg_destroy(qmsg_ctx *c)
         hipFree(L.up);
         hipFree(L.down);
     }
+    for (auto &m : c->mats) hipFree(m.w);
+    hipFree(c->dense_xqk);
+    hipFree(c->dense_io);
     for (void *p : c->scratch_allocs) hipFree(p);
     for (void *p : c->user_allocs) hipFree(p);
     for (auto &r : c->prof_recs) { hipEventDestroy(r.a); hipEventDestroy(r.b); }
@@ -516,6 +533,154 @@ int qmsg_gguf_upload(qmsg_ctx *c, const qmsg_gguf *g, int first, int n)
     }
     if ((rc = st.finish())) return rc;
     for (int i = 0; i < n; i++) c->layers[(size_t)(first + i)].ready = true;
+    return QMSG_OK;
+}
+
+/* ------------------------------------------------------------------ dense (trunk) products ---- */
+
+static int dense_check(qmsg_ctx *c, int type, int64_t rows, int64_t cols, const char *what)
+{
+    if (type != QMSG_T_Q4_0 && type != QMSG_T_Q4_1)
+        return fail(c, QMSG_E_UNSUPPORTED, "%s: the dense kernels take Q4_0 and Q4_1 (got type %d)", what, type);
+    if (rows <= 0 || rows > (1 << 30) || cols <= 0 || cols % 256)
+        return fail(c, QMSG_E_UNSUPPORTED, "%s: needs rows > 0 and cols %% 256 == 0 (got %lld x %lld)", what,
+                    (long long)rows, (long long)cols);
+    return QMSG_OK;
+}
+
+/* A new resident matrix of the given shape; its bytes are written by the caller. */
+static int dense_new(qmsg_ctx *c, int type, int64_t rows, int64_t cols, int *id)
+{
+    DenseStore m;
+    m.type = type;
+    m.rows = rows;
+    m.cols = cols;
+    m.rb = row_bytes(type, cols);
+    std::vector<void *> tmp;
+    const int rc = dev_alloc(c, (void **)&m.w, m.rb * (uint64_t)rows, tmp);
+    if (rc) return rc;
+    c->mats.push_back(m);
+    *id = (int)c->mats.size() - 1;
+    return QMSG_OK;
+}
+
+int qmsg_mat_upload(qmsg_ctx *c, const qmsg_mat *h, int *id)
+{
+    if (!c || !h || !id || !h->data) return QMSG_E_INVALID;
+    int rc = dense_check(c, h->type, h->rows, h->cols, "qmsg_mat_upload");
+    if (rc) return rc;
+    if (h->row_bytes != row_bytes(h->type, h->cols))
+        return fail(c, QMSG_E_INVALID, "qmsg_mat_upload: row_bytes %llu, expected %llu",
+                    (unsigned long long)h->row_bytes, (unsigned long long)row_bytes(h->type, h->cols));
+    HIP_TRY(c, hipSetDevice(c->device));
+    if ((rc = dense_new(c, h->type, h->rows, h->cols, id))) return rc;
+    const DenseStore &m = c->mats[(size_t)*id];
+    HIP_TRY(c, hipMemcpy(m.w, h->data, m.rb * (uint64_t)m.rows, hipMemcpyHostToDevice));
+    return QMSG_OK;
+}
+
+int qmsg_gguf_upload_mat(qmsg_ctx *c, const qmsg_gguf *g, const char *name, int *id)
+{
+    if (!c || !g || !name || !id) return QMSG_E_INVALID;
+    const int i = gguf_find(g, name);
+    if (i < 0) return fail(c, QMSG_E_INVALID, "model: missing tensor %s", name);
+    const qmsg_tensor &t = g->tensors[(size_t)i];
+    if (t.ne[2] != 1 || t.ne[3] != 1)
+        return fail(c, QMSG_E_INVALID, "model: %s is not a 2-D matrix (ne=[%lld,%lld,%lld])", name, (long long)t.ne[0],
+                    (long long)t.ne[1], (long long)t.ne[2]);
+    int rc = dense_check(c, t.type, t.ne[1], t.ne[0], name);
+    if (rc) return rc;
+    HIP_TRY(c, hipSetDevice(c->device));
+    HIP_TRY(c, hipStreamSynchronize(c->stream));
+    int nid = -1;
+    if ((rc = dense_new(c, t.type, t.ne[1], t.ne[0], &nid))) return rc;
+    Stager st(c);
+    if ((rc = st.init()) || (rc = st.copy(g, t, c->mats[(size_t)nid].w)) || (rc = st.finish())) return rc;
+    *id = nid;
+    return QMSG_OK;
+}
+
+/* Device buffer *p of at least `bytes`, reallocated (after the stream drains) when smaller. */
+static int grow(qmsg_ctx *c, void **p, size_t *cap, size_t bytes)
+{
+    if (*cap >= bytes) return QMSG_OK;
+    HIP_TRY(c, hipStreamSynchronize(c->stream));
+    hipFree(*p);
+    *p = nullptr;
+    *cap = 0;
+    std::vector<void *> tmp;
+    const int rc = dev_alloc(c, p, bytes, tmp);
+    if (rc == QMSG_OK) *cap = bytes;
+    return rc;
+}
+
+int qmsg_matmul_n_device(qmsg_ctx *c, const int *ids, int nW, const float *d_x, int T, float *const *d_ys)
+{
+    if (!c || !ids || !d_ys || nW <= 0 || T < 0) return QMSG_E_INVALID;
+    int64_t C = -1;
+    for (int i = 0; i < nW; i++) {
+        if (ids[i] < 0 || ids[i] >= (int)c->mats.size())
+            return fail(c, QMSG_E_INVALID, "qmsg_matmul_n: matrix id %d unknown", ids[i]);
+        const DenseStore &m = c->mats[(size_t)ids[i]];
+        if (C >= 0 && m.cols != C) return fail(c, QMSG_E_INVALID, "qmsg_matmul_n: matrices differ in cols");
+        C = m.cols;
+        if (!d_ys[i] || ((uintptr_t)d_ys[i] & 3)) return fail(c, QMSG_E_INVALID, "qmsg_matmul_n: output %d", i);
+    }
+    if (T == 0) return QMSG_OK;
+    if (!d_x || ((uintptr_t)d_x & 15)) return fail(c, QMSG_E_INVALID, "qmsg_matmul_n: x must be 16-byte aligned");
+    HIP_TRY(c, hipSetDevice(c->device));
+    int rc = grow(c, (void **)&c->dense_xqk, &c->dense_xqk_bytes, (size_t)T * (size_t)(C / 64) * kPairBytes);
+    if (rc) return rc;
+    /* launches of up to kDenseMats matrices of one type, in argument order */
+    std::vector<bool> done((size_t)nW, false);
+    for (int i = 0; i < nW; i++) {
+        if (done[(size_t)i]) continue;
+        const int type = c->mats[(size_t)ids[i]].type;
+        DenseArgs a{};
+        a.rb = c->mats[(size_t)ids[i]].rb;
+        a.C = (int)C;
+        a.T = T;
+        for (int j = i; j < nW && a.nm < kDenseMats; j++) {
+            const DenseStore &m = c->mats[(size_t)ids[j]];
+            if (done[(size_t)j] || m.type != type) continue;
+            a.m[a.nm].w = m.w;
+            a.m[a.nm].y = d_ys[j];
+            a.m[a.nm].rows = (int)m.rows;
+            a.nm++;
+            done[(size_t)j] = true;
+        }
+        LAUNCH(c, "dense", launch_dense(a, type, d_x, c->dense_xqk, c->stream));
+    }
+    return QMSG_OK;
+}
+
+int qmsg_matmul_n(qmsg_ctx *c, const int *ids, int nW, const float *x, int T, float *const *ys)
+{
+    if (!c || !ids || !ys || nW <= 0 || T < 0) return QMSG_E_INVALID;
+    for (int i = 0; i < nW; i++)
+        if (ids[i] < 0 || ids[i] >= (int)c->mats.size())
+            return fail(c, QMSG_E_INVALID, "qmsg_matmul_n: matrix id %d unknown", ids[i]);
+    if (T == 0) return QMSG_OK;
+    if (!x) return QMSG_E_INVALID;
+    const int64_t C = c->mats[(size_t)ids[0]].cols;
+    size_t bytes = (size_t)T * (size_t)C * 4;
+    std::vector<size_t> off((size_t)nW);
+    for (int i = 0; i < nW; i++) {
+        off[(size_t)i] = bytes;
+        bytes += ((size_t)T * (size_t)c->mats[(size_t)ids[i]].rows * 4 + 255) & ~(size_t)255;
+    }
+    HIP_TRY(c, hipSetDevice(c->device));
+    int rc = grow(c, &c->dense_io, &c->dense_io_bytes, bytes);
+    if (rc) return rc;
+    uint8_t *io = (uint8_t *)c->dense_io;
+    std::vector<float *> dy((size_t)nW);
+    for (int i = 0; i < nW; i++) dy[(size_t)i] = (float *)(io + off[(size_t)i]);
+    HIP_TRY(c, hipMemcpyAsync(io, x, (size_t)T * (size_t)C * 4, hipMemcpyHostToDevice, c->stream));
+    if ((rc = qmsg_matmul_n_device(c, ids, nW, (const float *)io, T, dy.data()))) return rc;
+    for (int i = 0; i < nW; i++)
+        HIP_TRY(c, hipMemcpyAsync(ys[i], dy[(size_t)i], (size_t)T * (size_t)c->mats[(size_t)ids[i]].rows * 4,
+                                  hipMemcpyDeviceToHost, c->stream));
+    HIP_TRY(c, hipStreamSynchronize(c->stream));
     return QMSG_OK;
 }
 

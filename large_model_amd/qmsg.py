@@ -114,6 +114,10 @@ _SIGS = {
     "qmsg_gguf_get_str": (_I, [_P, ctypes.c_char_p, ctypes.c_char_p, ctypes.c_size_t]),
     "qmsg_gguf_moe_cfg": (_I, [_P, ctypes.POINTER(_Cfg), ctypes.POINTER(_I), ctypes.POINTER(ctypes.c_float)]),
     "qmsg_gguf_upload": (_I, [_P, _P, _I, _I]),
+    "qmsg_mat_upload": (_I, [_P, ctypes.POINTER(_Mat), ctypes.POINTER(_I)]),
+    "qmsg_gguf_upload_mat": (_I, [_P, _P, ctypes.c_char_p, ctypes.POINTER(_I)]),
+    "qmsg_matmul_n": (_I, [_P, _P, _I, _P, _I, _P]),
+    "qmsg_matmul_n_device": (_I, [_P, _P, _I, _P, _I, _P]),
     "qmsg_device_info": (_I, [_P, ctypes.POINTER(_I), ctypes.POINTER(_I), ctypes.POINTER(ctypes.c_uint64),
                               ctypes.c_char_p, _I]),
 }
@@ -312,6 +316,45 @@ class Context:
         ctx.eps = c["eps"]
         ctx.load_gguf(g, 0, c["n_layer"])
         return ctx
+
+    # ---------------------------------------------------------------- dense (trunk) products
+    def mat_upload(self, type_: int, data: np.ndarray, rows: int, cols: int) -> int:
+        """A dense matrix (GGUF rows, QmsMat) resident in HBM; returns its id."""
+        data = np.ascontiguousarray(data, np.uint8)
+        m = _Mat(type_, rows, cols, row_bytes(type_, cols), data.ctypes.data)
+        i = _I()
+        self._check(lib.qmsg_mat_upload(self._h, ctypes.byref(m), ctypes.byref(i)))
+        self._mats = getattr(self, "_mats", {})
+        self._mats[i.value] = (rows, cols)
+        return i.value
+
+    def gguf_upload_mat(self, g: "Gguf", name: str) -> int:
+        i = _I()
+        self._check(lib.qmsg_gguf_upload_mat(self._h, g._h, name.encode(), ctypes.byref(i)))
+        t = g.tensors()[g.find(name)]
+        self._mats = getattr(self, "_mats", {})
+        self._mats[i.value] = (t["ne"][1], t["ne"][0])
+        return i.value
+
+    def matmul_n(self, ids, x: np.ndarray) -> list:
+        """qms_matmul_n: [y_i [T][rows_i]] for resident matrices ids on host rows x [T][cols]."""
+        mats = getattr(self, "_mats", {})
+        if any(i not in mats for i in ids):         # let the library report the bad id
+            idv = (_I * len(ids))(*ids)
+            self._check(lib.qmsg_matmul_n(self._h, idv, len(ids), None, 0, (_P * len(ids))()))
+        cols = mats[ids[0]][1]
+        x = np.ascontiguousarray(x, np.float32).reshape(-1, cols)
+        T = x.shape[0]
+        ys = [np.empty((T, self._mats[i][0]), np.float32) for i in ids]
+        idv = (_I * len(ids))(*ids)
+        yp = (_P * len(ids))(*[y.ctypes.data for y in ys])
+        self._check(lib.qmsg_matmul_n(self._h, idv, len(ids), _ptr(x), T, yp))
+        return ys
+
+    def matmul_n_device(self, ids, d_x: int, T: int, d_ys):
+        idv = (_I * len(ids))(*ids)
+        yp = (_P * len(ids))(*d_ys)
+        self._check(lib.qmsg_matmul_n_device(self._h, idv, len(ids), d_x, T, yp))
 
     def set_path(self, path: int):
         self._check(lib.qmsg_set_path(self._h, path))

@@ -49,6 +49,7 @@ def _load_oracle():
     L.orc_vec_dot_f32.argtypes = [_P, _P, ctypes.c_int64]
     L.orc_block_dot.restype = ctypes.c_int32
     L.orc_block_dot.argtypes = [ctypes.c_int, _P, _P, ctypes.c_int64]
+    L.orc_matmul_q8.argtypes = [ctypes.c_int, _P, ctypes.c_int64, ctypes.c_int64, ctypes.c_uint64, _P, ctypes.c_int, _P]
     L.orc_dequant_row.argtypes = [ctypes.c_int, _P, _P, ctypes.c_int64]
     L.orc_silu.restype = ctypes.c_float
     L.orc_silu.argtypes = [ctypes.c_float]
@@ -97,6 +98,15 @@ def vec_dot_f32(w: np.ndarray, x: np.ndarray) -> float:
     w = np.ascontiguousarray(w, np.float32)
     x = np.ascontiguousarray(x, np.float32)
     return float(lib.orc_vec_dot_f32(_ptr(w), _ptr(x), w.size))
+
+
+def matmul_q8(t: int, w: np.ndarray, rows: int, cols: int, x: np.ndarray) -> np.ndarray:
+    """qms_matmul's fast path (src/quant.c:128-170) for one quantised matrix: y [T][rows]."""
+    x = np.ascontiguousarray(x, np.float32).reshape(-1, cols)
+    y = np.empty((x.shape[0], rows), np.float32)
+    assert lib.orc_matmul_q8(t, _ptr(np.ascontiguousarray(w, np.uint8)), rows, cols, row_bytes(t, cols), _ptr(x),
+                             x.shape[0], _ptr(y)) == 0
+    return y
 
 
 def block_dot(t: int, w_row: np.ndarray, xq: np.ndarray, blk: int) -> int:

@@ -430,6 +430,24 @@ int orc_moe(int E, int X, int K, int F, const orc_mat *router, const orc_mat *ga
     return 0;
 }
 
+/* The fast path of qms_matmul_n for one quantised matrix (src/quant.c:128-170): each row of
+ * x [T][cols] quantised to int8 blocks, then y[t][r] = vec_dot_q8(row r, xq_t). */
+int orc_matmul_q8(int type, const uint8_t *w, int64_t rows, int64_t cols, uint64_t row_bytes, const float *x, int T,
+                  float *y)
+{
+    if (cols % 32 || !orc_row_bytes(type, cols) || type == ORC_T_F32) return -1;
+    const int64_t nb = cols / 32;
+    orc_q8 *xq = (orc_q8 *)malloc((size_t)T * (size_t)nb * sizeof(orc_q8));
+    if (!xq) return -1;
+    for (int t = 0; t < T; t++) orc_quantize_q8(x + (size_t)t * cols, cols, xq + (size_t)t * nb);
+#pragma omp parallel for schedule(static)
+    for (int64_t r = 0; r < rows; r++)
+        for (int t = 0; t < T; t++)
+            y[(size_t)t * rows + r] = orc_vec_dot_q8(type, w + (uint64_t)r * row_bytes, xq + (size_t)t * nb, cols);
+    free(xq);
+    return 0;
+}
+
 /* ---------------------------------------------------------------- synthetic inputs ---- */
 
 void orc_synth_f32(uint64_t seed, uint32_t layer, uint32_t kind, uint32_t expert, uint64_t n, float sigma,

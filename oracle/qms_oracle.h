@@ -73,6 +73,8 @@ uint64_t orc_row_bytes(int type, int64_t ne0);
 int orc_dequant_row(int type, const void *src, float *dst, int64_t n);
 void orc_quantize_q8(const float *x, int64_t n, orc_q8 *out);
 float orc_vec_dot_q8(int type, const uint8_t *w, const orc_q8 *x, int64_t n);
+int orc_matmul_q8(int type, const uint8_t *w, int64_t rows, int64_t cols, uint64_t row_bytes, const float *x, int T,
+                  float *y);
 float orc_vec_dot_f32(const float *w, const float *x, int64_t n);
 int32_t orc_block_dot(int type, const uint8_t *w_row, const orc_q8 *x, int64_t blk);
 float orc_silu(float a);

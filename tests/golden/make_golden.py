@@ -12,6 +12,8 @@ Outputs (numpy .npz, no pickles):
                    results on the test_kernels.c-style cases, plus quantiser tie cases
   layer_*.npz      the reference moe() on whole layers: inputs' hashes, router logits
                    (qms_matmul), int8 input blocks (qms_quantize_q8) and the layer output
+  dense.npz        qms_matmul on quantised dense (trunk-shaped) matrices: inputs' hashes and
+                   outputs
 """
 import ctypes
 import hashlib
@@ -138,6 +140,34 @@ def kat_kernels(R) -> dict:
     return out
 
 
+# dense (trunk) matrices through qms_matmul: (type, rows, cols, T, seed)
+DENSE = [(orc.T_Q4_0, 512, 4096, 3, 1), (orc.T_Q4_1, 256, 2048, 2, 2), (orc.T_Q4_0, 100, 8192, 1, 3),
+         (orc.T_Q4_0, 64, 4096, 9, 4)]
+
+
+def dense_mat(t, rows, cols, seed):
+    """Seeded synthetic weight rows (the shared generator, one 'expert' of kind gate)."""
+    w = np.zeros(rows * orc.row_bytes(t, cols), np.uint8)
+    orc.lib.orc_synth_experts(seed, 0, orc.KIND_GATE, t, rows, cols, 0, 1, 0.02, w.ctypes.data)
+    return w
+
+
+def dense_cases(R) -> dict:
+    out = {}
+    for i, (t, rows, cols, T, seed) in enumerate(DENSE):
+        w = dense_mat(t, rows, cols, seed)
+        x = orc.make_input(cols, T, seed)
+        y = np.empty((T, rows), np.float32)
+        m = QmsMat(t, rows, cols, orc.row_bytes(t, cols), w.ctypes.data)
+        R.qms_matmul(ctypes.byref(m), ptr(x), T, ptr(y))
+        out[f"d{i}_shape"] = np.array([t, rows, cols, T, seed], np.int64)
+        out[f"d{i}_w_sha"] = np.frombuffer(bytes.fromhex(sha(w)), np.uint8)
+        out[f"d{i}_x_sha"] = np.frombuffer(bytes.fromhex(sha(x)), np.uint8)
+        out[f"d{i}_y"] = y
+    out["n_dense_cases"] = np.int32(len(DENSE))
+    return out
+
+
 # name: (E, X, K, F, T, seed, down_type, rmsnorm, special)
 LAYERS = {
     "tiny_t1": (256, 16, 4, 128, 1, 0, orc.T_Q4_0, False, None),
@@ -213,9 +243,12 @@ def main():
         sys.exit("oracle/_ref is not built: run `make -C oracle` where the reference sources are present")
     R.qms_matmul.argtypes = [ctypes.POINTER(QmsMat), P, ctypes.c_int, P]
     print("reference build:", orc.ref_library_path(), R.qref_isa().decode())
-    only = sys.argv[1:]                     # optional: regenerate just these layer files
+    only = sys.argv[1:]                     # optional: regenerate just these files ("dense", layer names)
     if not only:
         np.savez_compressed(os.path.join(HERE, "kat_kernels.npz"), **kat_kernels(R))
+    if not only or "dense" in only:
+        np.savez_compressed(os.path.join(HERE, "dense.npz"), **dense_cases(R))
+        print("wrote dense")
     for name, cfg in LAYERS.items():
         if only and name not in only:
             continue

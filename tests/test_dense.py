@@ -1,0 +1,70 @@
+"""Dense (trunk) products on the CPU: the oracle's qms_matmul restatement against the reference's
+own qms_matmul outputs (tests/golden/dense.npz) and, where the reference build is present,
+live on further shapes."""
+import ctypes
+import hashlib
+import os
+
+import numpy as np
+import pytest
+
+import oracle as orc
+
+GOLD = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+
+
+def sha(a) -> bytes:
+    return hashlib.sha256(np.ascontiguousarray(a).view(np.uint8).tobytes()).digest()
+
+
+def dense_mat(t, rows, cols, seed):
+    w = np.zeros(rows * orc.row_bytes(t, cols), np.uint8)
+    orc.lib.orc_synth_experts(seed, 0, orc.KIND_GATE, t, rows, cols, 0, 1, 0.02, w.ctypes.data)
+    return w
+
+
+def test_oracle_matmul_matches_reference_fixtures():
+    d = dict(np.load(os.path.join(GOLD, "dense.npz")))
+    for i in range(int(d["n_dense_cases"])):
+        t, rows, cols, T, seed = (int(v) for v in d[f"d{i}_shape"])
+        w = dense_mat(t, rows, cols, seed)
+        x = orc.make_input(cols, T, seed)
+        assert sha(w) == bytes(d[f"d{i}_w_sha"]) and sha(x) == bytes(d[f"d{i}_x_sha"]), i
+        y = orc.matmul_q8(t, w, rows, cols, x)
+        assert np.array_equal(y.view(np.uint32), d[f"d{i}_y"].view(np.uint32)), i
+
+
+def test_oracle_matmul_row_is_vec_dot():
+    """Each output is the vec_dot of its row with the token's int8 blocks (no cross-row mixing,
+    [T][rows] layout), and a planted row swap is seen."""
+    t, rows, cols, T = orc.T_Q4_1, 40, 512, 3
+    w = dense_mat(t, rows, cols, 9)
+    x = orc.make_input(cols, T, 9)
+    y = orc.matmul_q8(t, w, rows, cols, x)
+    rb = orc.row_bytes(t, cols)
+    for tt in range(T):
+        xq = orc.quantize_q8(x[tt])
+        for r in (0, 17, rows - 1):
+            assert np.float32(orc.vec_dot_q8(t, w[r * rb:(r + 1) * rb], xq, cols)) == y[tt, r]
+    w2 = w.copy()
+    w2[:rb], w2[rb:2 * rb] = w[rb:2 * rb], w[:rb]
+    assert not np.array_equal(orc.matmul_q8(t, w2, rows, cols, x), y)
+
+
+@pytest.mark.skipif(orc.load_ref() is None, reason="oracle/_ref (the reference build) is not built here")
+@pytest.mark.parametrize("t,rows,cols,T", [(orc.T_Q4_0, 96, 4096, 5), (orc.T_Q4_1, 33, 1024, 2),
+                                           (orc.T_Q6_K, 20, 2048, 3)])
+def test_oracle_matmul_matches_reference_live(t, rows, cols, T):
+    R = orc.load_ref()
+
+    class QmsMat(ctypes.Structure):   # src/quant.h:11-16
+        _fields_ = [("type", ctypes.c_int), ("rows", ctypes.c_int64), ("cols", ctypes.c_int64),
+                    ("row_bytes", ctypes.c_uint64), ("data", ctypes.c_void_p)]
+
+    R.qms_matmul.argtypes = [ctypes.POINTER(QmsMat), ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p]
+    w = dense_mat(t, rows, cols, 21)
+    x = orc.make_input(cols, T, 22) * np.float32(4.0)
+    y = np.empty((T, rows), np.float32)
+    m = QmsMat(t, rows, cols, orc.row_bytes(t, cols), w.ctypes.data)
+    R.qms_matmul(ctypes.byref(m), x.ctypes.data, T, y.ctypes.data)
+    assert np.array_equal(orc.matmul_q8(t, w, rows, cols, x).view(np.uint32), y.view(np.uint32))
