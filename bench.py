@@ -281,6 +281,114 @@ def run_stack(args, w):
     print(json.dumps(result), flush=True)
 
 
+def run_trunk(args):
+    """A step is the dense products of the 235B trunk for every resident layer (src/model.c:442,
+    494): q/k/v in one qms_matmul_n call ([8192 | 512 | 512] x 4096, Q4_0), then attn_output
+    (4096 x 8192, Q4_0), on T tokens. Attention itself is not part of this library."""
+    E, H, KV, NL, T = 4096, 8192, 512, args.trunk, args.tokens
+    K_steps, W_steps = args.steps, args.warmup
+    log(f"trunk q/k/v/o: {NL} resident layers, T={T}")
+    ctx = qmsg.Context(256, 16, 4, 128, max_tokens=1)
+    layers = []
+    for l in range(NL):
+        q = ctx.mat_synth(qmsg.QMSG_T_Q4_0, H, E, 100 + 4 * l)
+        k = ctx.mat_synth(qmsg.QMSG_T_Q4_0, KV, E, 101 + 4 * l)
+        v = ctx.mat_synth(qmsg.QMSG_T_Q4_0, KV, E, 102 + 4 * l)
+        o = ctx.mat_synth(qmsg.QMSG_T_Q4_0, E, H, 103 + 4 * l)
+        layers.append((q, k, v, o))
+    d_x = ctx.device_alloc(T * E * 4)
+    d_a = ctx.device_alloc(T * H * 4)
+    ctx.synth_input(7, 0, T, d_x)
+    d_y = [ctx.device_alloc(T * r * 4) for r in (H, KV, KV, E)]
+    ctx.sync()
+
+    def step():
+        for q, k, v, o in layers:
+            ctx.matmul_n_device([q, k, v], d_x, T, d_y[:3])
+            ctx.matmul_n_device([o], d_a, T, d_y[3:])
+
+    for _ in range(W_steps):
+        step()
+    ctx.sync()
+    t0 = time.perf_counter()
+    for _ in range(K_steps):
+        step()
+    ctx.sync()
+    el = time.perf_counter() - t0
+    ctx.profile(True)
+    step()
+    ctx.sync()
+    kern = {}
+    for name in ("dquant", "dense"):
+        n, ms = ctx.profile_read(name)
+        if n:
+            kern[name] = {"launches": n, "avg_us": round(1e3 * ms / n, 3)}
+    ctx.profile(False)
+    rb = qmsg.row_bytes(qmsg.QMSG_T_Q4_0, E)
+    layer_bytes = (H + 2 * KV) * rb + E * qmsg.row_bytes(qmsg.QMSG_T_Q4_0, H)
+    us_layer = 1e6 * el / K_steps / NL
+    d_us = kern["dense"]["avg_us"]
+    dense_bytes = layer_bytes / 2                     # per dense launch on average (q/k/v, then o)
+    achieved = dense_bytes / (d_us * 1e-6) / 1e9
+    result = {
+        "metric": "trunk q/k/v/o dense products: us per layer + achieved HBM GB/s",
+        "value": round(us_layer, 3), "unit": "us/layer", "higher_is_better": False, "n_gpus": 1,
+        "steps": K_steps, "warmup": W_steps, "dtype": "int8", "data": "synthetic",
+        "config": {"workload": f"Qwen3-235B-A22B trunk q/k/v/o shapes (Q4_0), {NL} resident layers", "T": T},
+        "layer_bytes": layer_bytes, "achieved_GBps_layer": round(layer_bytes / (us_layer * 1e-6) / 1e9, 1),
+        "roofline": {"kernel": "dense (row dots, average of the q/k/v and o launches)", "bound": "hbm",
+                     "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None},
+        "kernels": kern, "cpu_baseline": None,
+    }
+    if not args.no_cpu:
+        result["cpu_baseline"] = cpu_baseline_trunk(T, args.cpu_seconds)
+    ctx.close()
+    print(json.dumps(result), flush=True)
+
+
+def cpu_baseline_trunk(T: int, seconds: float):
+    """The reference's own qms_matmul_n (src/quant.c:128-170) on one layer's q/k/v and o."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import ctypes
+
+    import oracle as orc  # checker only: times the CPU path beside the GPU
+    R = orc.load_ref()
+    if R is None:
+        return None
+
+    class QmsMat(ctypes.Structure):   # src/quant.h:11-16
+        _fields_ = [("type", ctypes.c_int), ("rows", ctypes.c_int64), ("cols", ctypes.c_int64),
+                    ("row_bytes", ctypes.c_uint64), ("data", ctypes.c_void_p)]
+
+    E, H, KV = 4096, 8192, 512
+    bufs, mats = [], []
+    for rows, cols, seed in ((H, E, 1), (KV, E, 2), (KV, E, 3), (E, H, 4)):
+        w = np.zeros(rows * qmsg.row_bytes(qmsg.QMSG_T_Q4_0, cols), np.uint8)
+        orc.lib.orc_synth_experts(seed, 0, orc.KIND_GATE, qmsg.QMSG_T_Q4_0, rows, cols, 0, 1, 0.02, w.ctypes.data)
+        bufs.append(w)
+        mats.append(QmsMat(qmsg.QMSG_T_Q4_0, rows, cols, qmsg.row_bytes(qmsg.QMSG_T_Q4_0, cols), w.ctypes.data))
+    x = orc.make_input(E, T, 5)
+    a = orc.make_input(H, T, 6)
+    ys = [np.empty((T, m.rows), np.float32) for m in mats]
+    P = ctypes.POINTER(QmsMat)
+    qkv = (P * 3)(*[ctypes.pointer(m) for m in mats[:3]])
+    yqkv = (ctypes.c_void_p * 3)(*[y.ctypes.data for y in ys[:3]])
+    o = (P * 1)(ctypes.pointer(mats[3]))
+    yo = (ctypes.c_void_p * 1)(ys[3].ctypes.data)
+    R.qms_matmul_n.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p]
+    n, t0 = 0, time.perf_counter()
+    while True:
+        R.qms_matmul_n(qkv, 3, x.ctypes.data, T, yqkv)
+        R.qms_matmul_n(o, 1, a.ctypes.data, T, yo)
+        n += 1
+        if time.perf_counter() - t0 > min(seconds, 10.0):
+            break
+    el = time.perf_counter() - t0
+    return {"value": round(1e6 * el / n, 3), "unit": "us/layer", "cores": int(R.qref_max_threads()),
+            "kind": "reference", "sample": f"{n} layers of q/k/v + o qms_matmul_n at T={T} on the host"}
+
+
 def gguf_load(args):
     """File -> HBM rate of qmsg_gguf_upload for n layers of the 235B shape (Q4_0 gate/up; down
     Q4_0 and Q4_1 on alternate layers, as real files mix them), page cache warm: the file is
@@ -343,6 +451,10 @@ def main():
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES",
                     help="instead of the layer, run the plain copy kernel on BYTES (reference transfer "
                          "for HBM byte counters) --steps times and exit")
+    ap.add_argument("--trunk", type=int, default=0, metavar="LAYERS",
+                    help="instead of the MoE layer, time the trunk's q/k/v/o dense products over LAYERS "
+                         "resident layers and exit")
+    ap.add_argument("--tokens", type=int, default=1, help="tokens per step of --trunk")
     ap.add_argument("--gguf-load", type=int, default=0, metavar="LAYERS",
                     help="instead of the layer, time loading LAYERS 235B-shape MoE layers from a GGUF file "
                          "into HBM (--steps loads, default 3) and exit")
@@ -356,6 +468,11 @@ def main():
 
     if args.copy_calibration:
         copy_calibration(args.copy_calibration, args.steps)
+        return
+    if args.trunk:
+        args.steps = args.steps or 200
+        args.warmup = args.warmup if args.warmup is not None else 20
+        run_trunk(args)
         return
     if args.gguf_load:
         args.steps = args.steps or 3

@@ -180,6 +180,9 @@ int qmsg_gguf_upload(qmsg_ctx *ctx, const qmsg_gguf *g, int first, int n);
 int qmsg_mat_upload(qmsg_ctx *ctx, const qmsg_mat *host, int *id);
 /* The same from a parsed GGUF file, by tensor name (e.g. "blk.0.attn_q.weight"). */
 int qmsg_gguf_upload_mat(qmsg_ctx *ctx, const qmsg_gguf *g, const char *name, int *id);
+/* No reference counterpart: a resident matrix of seeded synthetic rows generated on the device
+ * (the generator of qmsg_layer_synth, one expert of kind gate, layer 0), for benchmarks. */
+int qmsg_mat_synth(qmsg_ctx *ctx, int type, int64_t rows, int64_t cols, uint64_t seed, float sigma, int *id);
 
 /* qms_matmul_n (src/quant.c:128-170) on resident matrices ids[0..nW-1] of equal cols C:
  * every row of x [T][C] is quantised to int8 blocks (qms_quantize_q8) and ys[i][t][r] =

@@ -67,9 +67,7 @@ struct qmsg_ctx {
     std::vector<void *> scratch_allocs, user_allocs;
     float *d_x = nullptr, *d_out = nullptr;
     std::vector<DenseStore> mats;
-    /* grow-on-demand buffers of the dense products: int8 records, host-call staging */
-    uint8_t *dense_xqk = nullptr;
-    size_t dense_xqk_bytes = 0;
+    /* grow-on-demand staging of qmsg_matmul_n's host buffers */
     void *dense_io = nullptr;
     size_t dense_io_bytes = 0;
     std::string err;
@@ -209,7 +207,6 @@ void qmsg_destroy(qmsg_ctx *c)
         hipFree(L.down);
     }
     for (auto &m : c->mats) hipFree(m.w);
-    hipFree(c->dense_xqk);
     hipFree(c->dense_io);
     for (void *p : c->scratch_allocs) hipFree(p);
     for (void *p : c->user_allocs) hipFree(p);
@@ -579,6 +576,19 @@ int qmsg_mat_upload(qmsg_ctx *c, const qmsg_mat *h, int *id)
     return QMSG_OK;
 }
 
+int qmsg_mat_synth(qmsg_ctx *c, int type, int64_t rows, int64_t cols, uint64_t seed, float sigma, int *id)
+{
+    if (!c || !id) return QMSG_E_INVALID;
+    int rc = dense_check(c, type, rows, cols, "qmsg_mat_synth");
+    if (rc) return rc;
+    HIP_TRY(c, hipSetDevice(c->device));
+    if ((rc = dense_new(c, type, rows, cols, id))) return rc;
+    /* the generator of the expert tensors with one "expert" of kind gate, layer 0 */
+    HIP_TRY(c, launch_synth_experts(seed, 0, QMSG_KIND_GATE, type, rows, cols, 1, sigma, c->mats[(size_t)*id].w,
+                                    c->stream));
+    return QMSG_OK;
+}
+
 int qmsg_gguf_upload_mat(qmsg_ctx *c, const qmsg_gguf *g, const char *name, int *id)
 {
     if (!c || !g || !name || !id) return QMSG_E_INVALID;
@@ -629,8 +639,6 @@ int qmsg_matmul_n_device(qmsg_ctx *c, const int *ids, int nW, const float *d_x, 
     if (T == 0) return QMSG_OK;
     if (!d_x || ((uintptr_t)d_x & 15)) return fail(c, QMSG_E_INVALID, "qmsg_matmul_n: x must be 16-byte aligned");
     HIP_TRY(c, hipSetDevice(c->device));
-    int rc = grow(c, (void **)&c->dense_xqk, &c->dense_xqk_bytes, (size_t)T * (size_t)(C / 64) * kPairBytes);
-    if (rc) return rc;
     /* launches of up to kDenseMats matrices of one type, in argument order */
     std::vector<bool> done((size_t)nW, false);
     for (int i = 0; i < nW; i++) {
@@ -640,6 +648,7 @@ int qmsg_matmul_n_device(qmsg_ctx *c, const int *ids, int nW, const float *d_x, 
         a.rb = c->mats[(size_t)ids[i]].rb;
         a.C = (int)C;
         a.T = T;
+        a.x = d_x;
         for (int j = i; j < nW && a.nm < kDenseMats; j++) {
             const DenseStore &m = c->mats[(size_t)ids[j]];
             if (done[(size_t)j] || m.type != type) continue;
@@ -649,7 +658,7 @@ int qmsg_matmul_n_device(qmsg_ctx *c, const int *ids, int nW, const float *d_x, 
             a.nm++;
             done[(size_t)j] = true;
         }
-        LAUNCH(c, "dense", launch_dense(a, type, d_x, c->dense_xqk, c->stream));
+        LAUNCH(c, "dense", launch_dense(a, type, c->stream));
     }
     return QMSG_OK;
 }

@@ -1682,30 +1682,14 @@ hipError_t launch_experts_mfma(const Shape &s, const LayerDev &L, const Scratch 
 
 /* ------------------------------------------------------------------ dense rows (trunk) ---- */
 
-/* The int8 pair records of T input rows of C floats (src/quant.c:151-154: qms_quantize_q8 of
- * every row): one thread per 32-block. */
-__global__ void dense_quant_kernel(const float *x, int C, int T, uint8_t *xqk)
-{
-    const int nb = C >> 5;
-    const int b = blockIdx.x * blockDim.x + threadIdx.x;
-    if (b >= T * nb) return;
-    const int t = b / nb, blk = b - t * nb;
-    float v[32];
-    const float4 *src = (const float4 *)(x + (size_t)t * C + (size_t)blk * 32);
-#pragma unroll
-    for (int j = 0; j < 8; j++) {
-        const float4 f = src[j];
-        v[4 * j] = f.x; v[4 * j + 1] = f.y; v[4 * j + 2] = f.z; v[4 * j + 3] = f.w;
-    }
-    store_pair_half(quantize_block(v), (uint32_t *)(xqk + ((size_t)t * (nb >> 1) + (blk >> 1)) * kPairBytes), blk & 1);
-}
-
-/* qms_matmul_n's fast loop (src/quant.c:156-169) over up to kDenseMats matrices of one type
- * sharing cols: y_i[t][r] = qms_vec_dot_q8(row r of W_i, xq_t). Block b covers rows
- * 16W*(b - first_i) .. +16W-1 of the matrix i whose block range holds b; wave w owns 16 of
- * them (one per lane quad) and streams exactly those rows in chunks of CB blocks, D chunks in
- * flight, through its own LDS buffer, as the expert kernels do, against NT tokens' records
- * per pass. Rows past the matrix's end load its last row and store nothing. */
+/* qms_matmul_n's fast loop (src/quant.c:151-169) over up to kDenseMats matrices of one type
+ * sharing cols: every input row quantised to int8 blocks (qms_quantize_q8), then y_i[t][r] =
+ * qms_vec_dot_q8(row r of W_i, xq_t). Block b covers rows 16W*(b - first_i) .. +16W-1 of the
+ * matrix i whose block range holds b; wave w owns 16 of them (one per lane quad) and streams
+ * exactly those rows in chunks of CB blocks, D chunks in flight, through its own LDS buffer,
+ * as the expert kernels do. The block quantises the input rows itself, NT tokens per pass,
+ * straight into LDS pair records while its first chunks are on the way (no separate launch).
+ * Rows past the matrix's end load its last row and store nothing. */
 template <int TYPE, int W, int NT, int CB, int D>
 __global__ __launch_bounds__(64 * W) void dense_kernel(DenseArgs a)
 {
@@ -1716,7 +1700,7 @@ __global__ __launch_bounds__(64 * W) void dense_kernel(DenseArgs a)
     constexpr int NSL = 16 * SPR;                     /* slots of one wave's chunk            */
     constexpr int SPT = (NSL + 63) / 64;              /* slots per lane per chunk             */
     constexpr int WS = CB * BB + ((SPR & 1) ? 0 : 16);/* LDS row stride, odd in 16-byte units */
-    const int nb = a.C >> 5, nP = nb >> 1, nchunk = nb / CB, xsl = nP * 6;
+    const int nb = a.C >> 5, nP = nb >> 1, nchunk = nb / CB;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, qd = lane >> 2, p = lane & 3;
     uint8_t *wbuf = smem + wave * 16 * WS;
     uint8_t *xbuf = smem + W * 16 * WS;
@@ -1740,12 +1724,21 @@ __global__ __launch_bounds__(64 * W) void dense_kernel(DenseArgs a)
     const int row = rw + qd;
     for (int t0 = 0; t0 < a.T; t0 += NT) {
         const int nt = min(NT, a.T - t0);
-        if (t0 > 0) __syncthreads();                  /* the previous pass is done with xbuf  */
-        for (int i = tid; i < nt * xsl; i += NTH)
-            ((u32x4 *)xbuf)[i] = ((const u32x4 *)(a.xqk + (size_t)t0 * nP * kPairBytes))[i];
 #pragma unroll
         for (int d = 0; d < D; d++)
             if (d < nchunk) load_chunk(d, wv[d]);
+        if (t0 > 0) __syncthreads();                  /* the previous pass is done with xbuf  */
+        for (int i = tid; i < nt * nb; i += NTH) {
+            const int n = i / nb, blk = i - n * nb;
+            float v[32];
+            const float4 *src = (const float4 *)(a.x + (size_t)(t0 + n) * a.C + (size_t)blk * 32);
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+                const float4 f = src[j];
+                v[4 * j] = f.x; v[4 * j + 1] = f.y; v[4 * j + 2] = f.z; v[4 * j + 3] = f.w;
+            }
+            store_pair_half(quantize_block(v), (uint32_t *)(xbuf + ((size_t)n * nP + (blk >> 1)) * kPairBytes), blk & 1);
+        }
         __syncthreads();
         RowAcc acc[NT];
         for (int n = 0; n < NT; n++) acc[n] = RowAcc{ 0.0f, 0.0f, 0.0f };
@@ -1781,19 +1774,24 @@ __global__ __launch_bounds__(64 * W) void dense_kernel(DenseArgs a)
     }
 }
 
-template <int TYPE, int NT>
-static void launch_dense_t(const DenseArgs &a, int CB, dim3 grid, size_t lds, hipStream_t st)
+template <int TYPE, int NT, int D>
+static void launch_dense_d(const DenseArgs &a, int CB, dim3 grid, size_t lds, hipStream_t st)
 {
-    if (CB == 16) QLAUNCH("dense", (dense_kernel<TYPE, 1, NT, 16, 2>), grid, dim3(64), lds, st, a);
-    else QLAUNCH("dense", (dense_kernel<TYPE, 1, NT, 8, 2>), grid, dim3(64), lds, st, a);
+    if (CB == 16) QLAUNCH("dense", (dense_kernel<TYPE, 1, NT, 16, D>), grid, dim3(64), lds, st, a);
+    else QLAUNCH("dense", (dense_kernel<TYPE, 1, NT, 8, D>), grid, dim3(64), lds, st, a);
 }
 
-hipError_t launch_dense(const DenseArgs &args, int type, const float *x, uint8_t *xqk, hipStream_t st)
+template <int TYPE, int NT>
+static void launch_dense_t(const DenseArgs &a, int CB, int D, dim3 grid, size_t lds, hipStream_t st)
+{
+    (void)D;
+    launch_dense_d<TYPE, NT, 2>(a, CB, grid, lds, st);
+}
+
+hipError_t launch_dense(const DenseArgs &args, int type, hipStream_t st)
 {
     DenseArgs a = args;
-    a.xqk = xqk;
     const int nb = a.C / 32;
-    QLAUNCH("dquant", dense_quant_kernel, dim3((a.T * nb + 255) / 256), dim3(256), 0, st, x, a.C, a.T, xqk);
     /* one wave per block, 16 rows each: the trunk's small matrices (attn_k/v: 512 rows) still
      * spread over 32 CUs, the large ones over every CU */
     int nblk = 0;
@@ -1803,19 +1801,20 @@ hipError_t launch_dense(const DenseArgs &args, int type, const float *x, uint8_t
     }
     const int NT = a.T >= 4 ? 4 : (a.T >= 2 ? 2 : 1);
     const int CB = nb % 16 == 0 ? 16 : 8;
+    const int D = 2;              /* chunks in flight per wave (2, 4 and 8 measured: 2 fastest) */
     const int bb = type == 3 ? 20 : 18;
     const size_t ws = (size_t)CB * bb + (((CB * bb / 16) & 1) ? 0 : 16);
     const size_t lds = 16 * ws + (size_t)NT * (nb / 2) * kPairBytes;
     if (lds > 160 * 1024) return hipErrorInvalidValue;
     const dim3 grid(nblk);
     if (type == 3) {
-        if (NT == 4) launch_dense_t<3, 4>(a, CB, grid, lds, st);
-        else if (NT == 2) launch_dense_t<3, 2>(a, CB, grid, lds, st);
-        else launch_dense_t<3, 1>(a, CB, grid, lds, st);
+        if (NT == 4) launch_dense_t<3, 4>(a, CB, D, grid, lds, st);
+        else if (NT == 2) launch_dense_t<3, 2>(a, CB, D, grid, lds, st);
+        else launch_dense_t<3, 1>(a, CB, D, grid, lds, st);
     } else {
-        if (NT == 4) launch_dense_t<2, 4>(a, CB, grid, lds, st);
-        else if (NT == 2) launch_dense_t<2, 2>(a, CB, grid, lds, st);
-        else launch_dense_t<2, 1>(a, CB, grid, lds, st);
+        if (NT == 4) launch_dense_t<2, 4>(a, CB, D, grid, lds, st);
+        else if (NT == 2) launch_dense_t<2, 2>(a, CB, D, grid, lds, st);
+        else launch_dense_t<2, 1>(a, CB, D, grid, lds, st);
     }
     return hipGetLastError();
 }

@@ -116,6 +116,8 @@ _SIGS = {
     "qmsg_gguf_upload": (_I, [_P, _P, _I, _I]),
     "qmsg_mat_upload": (_I, [_P, ctypes.POINTER(_Mat), ctypes.POINTER(_I)]),
     "qmsg_gguf_upload_mat": (_I, [_P, _P, ctypes.c_char_p, ctypes.POINTER(_I)]),
+    "qmsg_mat_synth": (_I, [_P, _I, ctypes.c_int64, ctypes.c_int64, ctypes.c_uint64, ctypes.c_float,
+                            ctypes.POINTER(_I)]),
     "qmsg_matmul_n": (_I, [_P, _P, _I, _P, _I, _P]),
     "qmsg_matmul_n_device": (_I, [_P, _P, _I, _P, _I, _P]),
     "qmsg_device_info": (_I, [_P, ctypes.POINTER(_I), ctypes.POINTER(_I), ctypes.POINTER(ctypes.c_uint64),
@@ -324,6 +326,14 @@ class Context:
         m = _Mat(type_, rows, cols, row_bytes(type_, cols), data.ctypes.data)
         i = _I()
         self._check(lib.qmsg_mat_upload(self._h, ctypes.byref(m), ctypes.byref(i)))
+        self._mats = getattr(self, "_mats", {})
+        self._mats[i.value] = (rows, cols)
+        return i.value
+
+    def mat_synth(self, type_: int, rows: int, cols: int, seed: int, sigma: float = 0.02) -> int:
+        """A resident matrix of seeded synthetic rows generated on the device; returns its id."""
+        i = _I()
+        self._check(lib.qmsg_mat_synth(self._h, type_, rows, cols, seed, sigma, ctypes.byref(i)))
         self._mats = getattr(self, "_mats", {})
         self._mats[i.value] = (rows, cols)
         return i.value
