@@ -1774,18 +1774,12 @@ __global__ __launch_bounds__(64 * W) void dense_kernel(DenseArgs a)
     }
 }
 
-template <int TYPE, int NT, int D>
-static void launch_dense_d(const DenseArgs &a, int CB, dim3 grid, size_t lds, hipStream_t st)
-{
-    if (CB == 16) QLAUNCH("dense", (dense_kernel<TYPE, 1, NT, 16, D>), grid, dim3(64), lds, st, a);
-    else QLAUNCH("dense", (dense_kernel<TYPE, 1, NT, 8, D>), grid, dim3(64), lds, st, a);
-}
-
+/* Two chunks in flight per wave (2, 4 and 8 were measured at the trunk's shapes: 2 fastest). */
 template <int TYPE, int NT>
-static void launch_dense_t(const DenseArgs &a, int CB, int D, dim3 grid, size_t lds, hipStream_t st)
+static void launch_dense_t(const DenseArgs &a, int CB, dim3 grid, size_t lds, hipStream_t st)
 {
-    (void)D;
-    launch_dense_d<TYPE, NT, 2>(a, CB, grid, lds, st);
+    if (CB == 16) QLAUNCH("dense", (dense_kernel<TYPE, 1, NT, 16, 2>), grid, dim3(64), lds, st, a);
+    else QLAUNCH("dense", (dense_kernel<TYPE, 1, NT, 8, 2>), grid, dim3(64), lds, st, a);
 }
 
 hipError_t launch_dense(const DenseArgs &args, int type, hipStream_t st)
@@ -1801,20 +1795,19 @@ hipError_t launch_dense(const DenseArgs &args, int type, hipStream_t st)
     }
     const int NT = a.T >= 4 ? 4 : (a.T >= 2 ? 2 : 1);
     const int CB = nb % 16 == 0 ? 16 : 8;
-    const int D = 2;              /* chunks in flight per wave (2, 4 and 8 measured: 2 fastest) */
     const int bb = type == 3 ? 20 : 18;
     const size_t ws = (size_t)CB * bb + (((CB * bb / 16) & 1) ? 0 : 16);
     const size_t lds = 16 * ws + (size_t)NT * (nb / 2) * kPairBytes;
     if (lds > 160 * 1024) return hipErrorInvalidValue;
     const dim3 grid(nblk);
     if (type == 3) {
-        if (NT == 4) launch_dense_t<3, 4>(a, CB, D, grid, lds, st);
-        else if (NT == 2) launch_dense_t<3, 2>(a, CB, D, grid, lds, st);
-        else launch_dense_t<3, 1>(a, CB, D, grid, lds, st);
+        if (NT == 4) launch_dense_t<3, 4>(a, CB, grid, lds, st);
+        else if (NT == 2) launch_dense_t<3, 2>(a, CB, grid, lds, st);
+        else launch_dense_t<3, 1>(a, CB, grid, lds, st);
     } else {
-        if (NT == 4) launch_dense_t<2, 4>(a, CB, D, grid, lds, st);
-        else if (NT == 2) launch_dense_t<2, 2>(a, CB, D, grid, lds, st);
-        else launch_dense_t<2, 1>(a, CB, D, grid, lds, st);
+        if (NT == 4) launch_dense_t<2, 4>(a, CB, grid, lds, st);
+        else if (NT == 2) launch_dense_t<2, 2>(a, CB, grid, lds, st);
+        else launch_dense_t<2, 1>(a, CB, grid, lds, st);
     }
     return hipGetLastError();
 }
