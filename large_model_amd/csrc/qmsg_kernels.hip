@@ -973,7 +973,7 @@ __global__ __launch_bounds__(64 * W) void gateup_kernel(GateUpArgs a)
     constexpr int WS = CB * 18 + ((SPR & 1) ? 0 : 16);/* LDS row stride, odd in 16-byte units */
     const int nbE = a.E >> 5, nP = nbE >> 1, nchunk = nbE / CB;
     const int xsl = nP * 6;                           /* 16-byte slots of one token's records */
-    constexpr int XS = (NT * (4096 / 64) * 6 + NTH - 1) / NTH;  /* x slots per thread (E <= 4096) */
+    constexpr int XS = (NT * (4096 / 64) * 6 + NTH - 1) / NTH;  /* x slots per thread in registers */
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, qd = lane >> 2, p = lane & 3;
     uint8_t *wbuf = smem + wave * 16 * WS;
     uint8_t *xbuf = smem + W * 16 * WS;
@@ -1047,6 +1047,12 @@ __global__ __launch_bounds__(64 * W) void gateup_kernel(GateUpArgs a)
         if (NT > 1 || g0 == s_begin) {
 #pragma unroll
             for (int m = 0; m < XS; m++) ((u32x4 *)xbuf)[min(tid + NTH * m, nt * xsl - 1)] = xv[m];
+            /* rows wider than 4096: the records past the register share */
+            for (int i = tid + NTH * XS; i < nt * xsl; i += NTH) {
+                const int n = i / xsl, off = i - n * xsl, k = g0 - s_begin + n;
+                const int tok = NT == 1 ? 0 : ((k < 4 && tok_bytes) ? (wk.w >> (8 * k)) & 0xff : slot_t[g0 + n]);
+                ((u32x4 *)xbuf)[i] = ((const u32x4 *)(a.S.xqk + (size_t)tok * nP * kPairBytes))[off];
+            }
         }
         __syncthreads();
         RowAcc acc[NT];
@@ -1241,17 +1247,20 @@ __global__ __launch_bounds__(256) void down_tile_kernel(DownArgs a)
 }
 
 /* One-token batch, Q4_0 or Q4_1 down weights (K <= 8 experts, one slot each, slot j = j-th active
- * expert): one block per 8 output rows r0 .. r0+7. Wave w owns active experts 2w and 2w+1
- * (16 rows, one per lane quad) and streams exactly those rows in chunks of CB blocks, D chunks
- * in flight, through its own LDS buffer, so its dots start as soon as its first bytes land.
- * The prologue requests the first chunks, then quantises the K activation rows into int8
- * pair records in LDS (block 0 also writes them out for the debug copy-back). The block ends
- * with the weighted combine of its 8 rows in selection order (src/model.c:1152-1162). */
-template <int TYPE, int CB, int D>
-__global__ __launch_bounds__(256) void down_t1_kernel(DownArgs a)
+ * expert): one block per RD output rows r0 .. r0+RD-1 and RD/2 waves. Wave w owns the 16/RD
+ * active experts 16w/RD .. (16 rows, one per lane quad) and streams exactly those rows in
+ * chunks of CB blocks, D chunks in flight, through its own LDS buffer, so its dots start as
+ * soon as its first bytes land. The prologue requests the first chunks, then quantises the K
+ * activation rows into int8 pair records in LDS (block 0 also writes them out for the debug
+ * copy-back). The block ends with the weighted combine of its RD rows in selection order
+ * (src/model.c:1152-1162). */
+template <int TYPE, int CB, int D, int RD>
+__global__ __launch_bounds__(32 * RD) void down_t1_kernel(DownArgs a)
 {
     extern __shared__ __align__(16) uint8_t smem[];
-    constexpr int RD = 8;
+    constexpr int NW = RD / 2, NTH = 64 * NW;         /* waves: 8 experts x RD rows / 16      */
+    constexpr int EPW = 16 / RD;                      /* experts per wave                     */
+    constexpr int QPT = (512 + NTH - 1) / NTH;        /* int8 blocks per thread in registers  */
     constexpr int BB = TYPE == 3 ? 20 : 18;           /* bytes per 32-block                   */
     constexpr int SPR = CB * BB / 16;                 /* 16-byte slots per row per chunk      */
     constexpr int NSL = 16 * SPR;                     /* slots of one wave's chunk            */
@@ -1261,20 +1270,20 @@ __global__ __launch_bounds__(256) void down_t1_kernel(DownArgs a)
     const int r0 = (int)blockIdx.x * RD, E = a.E, K = a.K, nbF = a.F >> 5, nPF = a.F >> 6;
     const int nchunk = nbF / CB, xrec = nPF * kPairBytes;
     uint8_t *wbuf = smem + wave * 16 * WS;
-    uint8_t *xbuf = smem + 4 * 16 * WS;               /* [K][xrec]                            */
+    uint8_t *xbuf = smem + NW * 16 * WS;              /* [K][xrec]                            */
     float *dnl = (float *)(xbuf + (size_t)K * xrec);  /* [K][RD]                              */
 
-    /* the activations to quantise: 32 floats per int8 block, up to two blocks per thread */
+    /* the activations to quantise: 32 floats per int8 block, the first QPT*NTH in registers */
     const int nqb = K * nbF;
-    float4 av[2][8];
+    float4 av[QPT][8];
 #pragma unroll
-    for (int u = 0; u < 2; u++) {
-        const float4 *src = (const float4 *)(a.S.act + (size_t)min(tid + 256 * u, nqb - 1) * 32);
+    for (int u = 0; u < QPT; u++) {
+        const float4 *src = (const float4 *)(a.S.act + (size_t)min(tid + NTH * u, nqb - 1) * 32);
 #pragma unroll
         for (int j = 0; j < 8; j++) av[u][j] = src[j];
     }
-    /* this wave's experts (uniform): j0 = 2w, j1 = 2w+1 */
-    const int j0 = 2 * wave, j1 = j0 + 1;
+    /* this wave's experts (uniform): j0 = EPW*w, and j0 + 1 when a wave holds two */
+    const int j0 = EPW * wave, j1 = j0 + EPW - 1;
     const int e0 = j0 < K ? a.S.work[j0].x : -1, e1 = j1 < K ? a.S.work[j1].x : -1;
     const uint8_t *b0 = a.down + (size_t)max(e0, 0) * a.eb + (size_t)r0 * a.rb;
     const uint8_t *b1 = a.down + (size_t)max(e1, 0) * a.eb + (size_t)r0 * a.rb;
@@ -1284,8 +1293,8 @@ __global__ __launch_bounds__(256) void down_t1_kernel(DownArgs a)
 #pragma unroll
         for (int m = 0; m < SPT; m++) {
             const int i = min(lane + 64 * m, NSL - 1), row = i / SPR, j = i - row * SPR;
-            dst[m] = *(const u32x4 *)((row < 8 ? b0 + (size_t)row * a.rb : b1 + (size_t)(row - 8) * a.rb) +
-                                      (size_t)c * CB * BB + 16 * j);
+            const uint8_t *rp = (EPW == 1 || row < RD) ? b0 + (size_t)row * a.rb : b1 + (size_t)(row - RD) * a.rb;
+            dst[m] = *(const u32x4 *)(rp + (size_t)c * CB * BB + 16 * j);
         }
     };
     const bool active = e0 >= 0;
@@ -1294,28 +1303,40 @@ __global__ __launch_bounds__(256) void down_t1_kernel(DownArgs a)
         for (int d = 0; d < D; d++)
             if (d < nchunk) load_chunk(d, wv[d]);
     }
+    auto quant = [&](int b, const float *v) {
+        const int s = b / nbF, blk = b - s * nbF;
+        const Q8Vals q = quantize_block(v);
+        store_pair_half(q, (uint32_t *)(xbuf + (size_t)s * xrec + (size_t)(blk >> 1) * kPairBytes), blk & 1);
+        if (blockIdx.x == 0) {
+            store_q8(q, a.S.aq + b);
+            store_pair_half(q, (uint32_t *)(a.S.aqk + ((size_t)s * (nbF >> 1) + (blk >> 1)) * kPairBytes), blk & 1);
+        }
+    };
 #pragma unroll
-    for (int u = 0; u < 2; u++) {
-        const int b = tid + 256 * u;
+    for (int u = 0; u < QPT; u++) {
+        const int b = tid + NTH * u;
         if (b < nqb) {
             float v[32];
 #pragma unroll
             for (int j = 0; j < 8; j++) {
                 v[4 * j] = av[u][j].x; v[4 * j + 1] = av[u][j].y; v[4 * j + 2] = av[u][j].z; v[4 * j + 3] = av[u][j].w;
             }
-            const int s = b / nbF, blk = b - s * nbF;
-            const Q8Vals q = quantize_block(v);
-            store_pair_half(q, (uint32_t *)(xbuf + (size_t)s * xrec + (size_t)(blk >> 1) * kPairBytes), blk & 1);
-            if (blockIdx.x == 0) {
-                store_q8(q, a.S.aq + b);
-                store_pair_half(q, (uint32_t *)(a.S.aqk + ((size_t)s * (nbF >> 1) + (blk >> 1)) * kPairBytes), blk & 1);
-            }
+            quant(b, v);
         }
+    }
+    for (int b = tid + NTH * QPT; b < nqb; b += NTH) {  /* rows longer than the register share */
+        float v[32];
+        const float4 *src = (const float4 *)(a.S.act + (size_t)b * 32);
+        for (int j = 0; j < 8; j++) {
+            const float4 f = src[j];
+            v[4 * j] = f.x; v[4 * j + 1] = f.y; v[4 * j + 2] = f.z; v[4 * j + 3] = f.w;
+        }
+        quant(b, v);
     }
     __syncthreads();
     if (active) {
-        /* quad qd: expert j0 + qd/8, row r0 + qd%8; its slot is its active index */
-        const int jq = j0 + (qd >> 3), rr = qd & 7;
+        /* quad qd: expert j0 + qd/RD, row r0 + qd%RD; its slot is its active index */
+        const int jq = j0 + qd / RD, rr = qd % RD;
         const uint8_t *xq = xbuf + (size_t)min(jq, K - 1) * xrec;
         RowAcc acc[1] = { RowAcc{ 0.0f, 0.0f, 0.0f } };
         for (int c0 = 0; c0 < nchunk; c0 += D) {
@@ -1385,6 +1406,10 @@ __global__ void combine_kernel(const Scratch S, int E, int K, int T, float *out)
     out[i] = o;
 }
 
+/* Output rows per block of the one-token down kernel (8: 512 blocks of 4 waves for E = 4096;
+ * 16: 256 blocks of 8 waves, half the activation reads). */
+constexpr int kDownT1Rows = 16;
+
 hipError_t launch_down_exact(const Shape &s, const LayerDev &L, const Scratch &S, float *out, int T, int quant,
                              hipStream_t st)
 {
@@ -1399,18 +1424,22 @@ hipError_t launch_down_exact(const Shape &s, const LayerDev &L, const Scratch &S
     a.X = s.X;
     a.out = out;
     a.S = S;
-    if (T == 1 && s.K <= 8 && (L.down_type == 2 || L.down_type == 3) && s.F % 256 == 0) {
-        /* one token: each wave streams its own two experts' rows (Q4_0 / Q4_1) */
-        const int nbF = s.F / 32, CB = nbF % 16 == 0 ? 16 : 8, bb = L.down_type == 3 ? 20 : 18;
-        const size_t xrec = (size_t)(s.F / 64) * kPairBytes;
-        const size_t ws = (size_t)CB * bb + (((CB * bb / 16) & 1) ? 0 : 16);
-        const size_t lds = 4 * 16 * ws + (size_t)s.K * xrec + (size_t)s.K * 8 * 4;
+    /* one token: each wave streams its own experts' rows (Q4_0 / Q4_1); RD output rows per
+     * block, RD/2 waves */
+    constexpr int RD = kDownT1Rows;
+    const int nbF = s.F / 32, CB = nbF % 16 == 0 ? 16 : 8, bb = L.down_type == 3 ? 20 : 18;
+    const size_t xrec = (size_t)(s.F / 64) * kPairBytes;
+    const size_t ws = (size_t)CB * bb + (((CB * bb / 16) & 1) ? 0 : 16);
+    const size_t lds_t1 = (size_t)(RD / 2) * 16 * ws + (size_t)s.K * xrec + (size_t)s.K * RD * 4;
+    if (T == 1 && s.K <= 8 && (L.down_type == 2 || L.down_type == 3) && s.F % 256 == 0 && s.E % RD == 0 &&
+        lds_t1 <= 160 * 1024) {
+        const dim3 grid(s.E / RD), block(32 * RD);
         if (L.down_type == 3) {
-            if (CB == 16) QLAUNCH("down", (down_t1_kernel<3, 16, 2>), dim3(s.E / 8), dim3(256), lds, st, a);
-            else QLAUNCH("down", (down_t1_kernel<3, 8, 2>), dim3(s.E / 8), dim3(256), lds, st, a);
+            if (CB == 16) QLAUNCH("down", (down_t1_kernel<3, 16, 2, RD>), grid, block, lds_t1, st, a);
+            else QLAUNCH("down", (down_t1_kernel<3, 8, 2, RD>), grid, block, lds_t1, st, a);
         } else {
-            if (CB == 16) QLAUNCH("down", (down_t1_kernel<2, 16, 2>), dim3(s.E / 8), dim3(256), lds, st, a);
-            else QLAUNCH("down", (down_t1_kernel<2, 8, 2>), dim3(s.E / 8), dim3(256), lds, st, a);
+            if (CB == 16) QLAUNCH("down", (down_t1_kernel<2, 16, 2, RD>), grid, block, lds_t1, st, a);
+            else QLAUNCH("down", (down_t1_kernel<2, 8, 2, RD>), grid, block, lds_t1, st, a);
         }
         return hipGetLastError();
     }
@@ -1421,7 +1450,6 @@ hipError_t launch_down_exact(const Shape &s, const LayerDev &L, const Scratch &S
         QLAUNCH("actq", act_quant_kernel, dim3((nq + 255) / 256), dim3(256), 0, st, S, s.F, NS);
     }
     const int NT = T >= 4 ? 4 : (T >= 2 ? 2 : 1);
-    const size_t xrec = (size_t)(s.F / 64) * kPairBytes;
     const size_t lds = ((64 * L.down_rb + 15) & ~(size_t)15) + (size_t)NT * xrec;
     if (lds > 160 * 1024 || s.E % 64) return hipErrorInvalidValue;
     const dim3 grid(s.E / 64, maxt);

@@ -183,6 +183,9 @@ LAYERS = {
     "q235b_zipf_t512": (4096, 128, 8, 1536, 512, 5, orc.T_Q4_0, False, "zipf"),
     "q235b_q41_t1": (4096, 128, 8, 1536, 1, 7, orc.T_Q4_1, False, None),
     "q235b_q41_t5": (4096, 128, 8, 1536, 5, 7, orc.T_Q4_1, True, None),
+    # the widest Qwen3-MoE shape (Qwen3-Coder-480B-A35B: n_embd 6144, 160 experts, n_ff_exp 2560)
+    "q480b_t1": (6144, 160, 8, 2560, 1, 12, orc.T_Q4_0, True, None),
+    "q480b_t2": (6144, 160, 8, 2560, 2, 13, orc.T_Q4_0, False, None),
 }
 
 

@@ -37,7 +37,7 @@ def golden_input(d):
 
 
 DEVICE_GOLD = ["tiny_t1", "tiny_t7", "q30b_t1", "q235b_t1", "q235b_t4", "q235b_t16", "q235b_q6k_t64",
-               "q235b_zipf_t512", "q235b_q41_t1", "q235b_q41_t5"]
+               "q235b_zipf_t512", "q235b_q41_t1", "q235b_q41_t5", "q480b_t1", "q480b_t2"]
 
 
 @pytest.mark.parametrize("name", DEVICE_GOLD)

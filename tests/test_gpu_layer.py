@@ -25,6 +25,9 @@ CASES = [
     ("q30b_q41_t1", 2048, 128, 8, 768, 1, 8, orc.T_Q4_1, True),
     ("q235b_q41_t1", 4096, 128, 8, 1536, 1, 7, orc.T_Q4_1, False),
     ("q235b_q41_t6", 4096, 128, 8, 1536, 6, 7, orc.T_Q4_1, False),
+    ("q480b_t1", 6144, 160, 8, 2560, 1, 14, orc.T_Q4_0, True),
+    ("q480b_q41_t1", 6144, 160, 8, 2560, 1, 15, orc.T_Q4_1, False),
+    ("q480b_t5", 6144, 160, 8, 2560, 5, 16, orc.T_Q4_0, False),
 ]
 
 
