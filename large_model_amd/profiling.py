@@ -22,8 +22,10 @@ import sys
 SHORT = (
     ("route_small_kernel", "route"), ("route_big_kernel", "route"), ("select_kernel", "select"),
     ("dispatch_kernel", "dispatch"), ("gateup_kernel", "gateup"), ("down_exact_kernel", "down"),
-    ("down_t1_kernel", "down"), ("act_quant_kernel", "actq"), ("combine_kernel", "combine"),
-    ("copy_kernel", "copy"),
+    ("down_t1_kernel", "down"), ("down_tile_kernel", "down"), ("act_quant_kernel", "actq"),
+    ("combine_kernel", "combine"), ("copy_kernel", "copy"), ("dense_kernel", "dense"),
+    ("gateup_mfma_kernel", "gateup"), ("down_mfma_kernel", "down"), ("rmsnorm_kernel", "rmsnorm"),
+    ("add_rows_kernel", "add"),
 )
 
 
