@@ -1175,9 +1175,6 @@ struct DownArgs {
     const uint8_t *down;
     uint64_t rb, eb;
     int E, F, K, T, X;
-    int fuse;          /* 1: combine inside the block (dn of all slots fits in LDS) */
-    int lds_slots;     /* slots of a round whose int8 activations are staged in LDS */
-    int qlds;          /* 1: quantise every slot's activations into LDS in the prologue */
     float *out;
     Scratch S;
 };
