@@ -256,66 +256,84 @@ __global__ __launch_bounds__(256) void route_small_kernel(RouteArgs a)
     }
 }
 
-/* Router for T > 4: one block per 16 tokens x 16 experts, 256 threads. Thread (c, ea, tb)
- * runs chain c of 4 experts x 4 tokens over 256-element chunks staged in LDS (register
- * prefetch of the next chunk). */
+/* Router for T > 4: one block per 4KT tokens x 4J experts, 256 threads. Thread (c, ea, tb)
+ * runs chain c of J experts x KT tokens over 256-element chunks staged in LDS, so each chain
+ * still walks its elements c, c+16, ... in order. The next P chunks are in flight in
+ * registers while one is consumed. Small blocks (J = KT = 1: 4 experts x 4 tokens) spread
+ * batches of up to 64 tokens over many CUs; larger batches take J = KT = 4 (16 x 16), which
+ * reads each router and input row fewer times. */
+template <int J, int KT, int P>
 __global__ __launch_bounds__(256) void route_big_kernel(RouteArgs a)
 {
     extern __shared__ __align__(16) uint8_t smem[];
     if ((int)blockIdx.x >= a.n_route_wg) { route_quantize(a); return; }
     constexpr int CH = 256, RS = CH + 4;          /* chunk elements, padded LDS row */
+    constexpr int EB = 4 * J;                     /* experts per block              */
     const int tid = threadIdx.x, E = a.E, T = a.T, X = a.X;
-    const int egs = X / 16, tg = (int)blockIdx.x / egs, eg = (int)blockIdx.x - tg * egs;
-    const int t0 = tg * 16, e0 = eg * 16;
+    constexpr int TB = 4 * KT;                    /* tokens per block               */
+    const int egs = X / EB, tg = (int)blockIdx.x / egs, eg = (int)blockIdx.x - tg * egs;
+    const int t0 = tg * TB, e0 = eg * EB;
     const int c = tid & 15, ea = (tid >> 4) & 3, tb = tid >> 6;
-    float *W = (float *)smem, *Xt = W + 16 * RS;
-    float acc[4][4];
-    for (int j = 0; j < 4; j++) for (int k = 0; k < 4; k++) acc[j][k] = 0.0f;
-    u32x4 pw[4], px[4];
+    float *W = (float *)smem, *Xt = W + EB * RS;
+    float acc[J][KT];
+    for (int j = 0; j < J; j++) for (int k = 0; k < KT; k++) acc[j][k] = 0.0f;
+    u32x4 pw[P][J], px[P][KT];
     const int nch = E / CH;
-#define QMSG_RSRC(base, row, m, ch)                                                                  \
-    ((const u32x4 *)((base) + (size_t)(row) * E + (size_t)(ch) * CH + ((tid + 256 * (m)) & 63) * 4))
+    auto load = [&](int ch, u32x4 *w, u32x4 *x) {
 #pragma unroll
-    for (int m = 0; m < 4; m++) {
-        const int r = (tid + 256 * m) >> 6;
-        pw[m] = *QMSG_RSRC(a.router, e0 + r, m, 0);
-        px[m] = *QMSG_RSRC(a.xn, min(t0 + r, T - 1), m, 0);
-    }
-    for (int ch = 0; ch < nch; ch++) {
-        __syncthreads();
-#pragma unroll
-        for (int m = 0; m < 4; m++) {
-            const int q = tid + 256 * m, r = q >> 6, col = (q & 63) * 4;
-            *(u32x4 *)(W + r * RS + col) = pw[m];
-            *(u32x4 *)(Xt + r * RS + col) = px[m];
+        for (int m = 0; m < J; m++) {
+            const int q = tid + 256 * m;
+            w[m] = *(const u32x4 *)(a.router + (size_t)(e0 + (q >> 6)) * E + (size_t)ch * CH + (q & 63) * 4);
         }
-        __syncthreads();
-        if (ch + 1 < nch) {
 #pragma unroll
-            for (int m = 0; m < 4; m++) {
-                const int r = (tid + 256 * m) >> 6;
-                pw[m] = *QMSG_RSRC(a.router, e0 + r, m, ch + 1);
-                px[m] = *QMSG_RSRC(a.xn, min(t0 + r, T - 1), m, ch + 1);
+        for (int m = 0; m < KT; m++) {
+            const int q = tid + 256 * m;
+            x[m] = *(const u32x4 *)(a.xn + (size_t)min(t0 + (q >> 6), T - 1) * E + (size_t)ch * CH + (q & 63) * 4);
+        }
+    };
+#pragma unroll
+    for (int d = 0; d < P; d++)
+        if (d < nch) load(d, pw[d], px[d]);
+    for (int ch0 = 0; ch0 < nch; ch0 += P) {
+#pragma unroll
+        for (int d = 0; d < P; d++) {
+            const int ch = ch0 + d;
+            if (ch < nch) {
+                __syncthreads();
+#pragma unroll
+                for (int m = 0; m < J; m++) {
+                    const int q = tid + 256 * m;
+                    *(u32x4 *)(W + (q >> 6) * RS + (q & 63) * 4) = pw[d][m];
+                }
+#pragma unroll
+                for (int m = 0; m < KT; m++) {
+                    const int q = tid + 256 * m;
+                    *(u32x4 *)(Xt + (q >> 6) * RS + (q & 63) * 4) = px[d][m];
+                }
+                __syncthreads();
+                if (ch + P < nch) load(ch + P, pw[d], px[d]);
+#pragma unroll
+                for (int s = 0; s < 16; s++) {
+                    const int i = 16 * s + c;
+                    float wv[J], xv[KT];
+                    for (int j = 0; j < J; j++) wv[j] = W[(J * ea + j) * RS + i];
+                    for (int k = 0; k < KT; k++) xv[k] = Xt[(KT * tb + k) * RS + i];
+                    for (int j = 0; j < J; j++)
+                        for (int k = 0; k < KT; k++) acc[j][k] = __builtin_fmaf(wv[j], xv[k], acc[j][k]);
+                }
             }
         }
-#pragma unroll
-        for (int s = 0; s < 16; s++) {
-            const int i = 16 * s + c;
-            float wv[4], xv[4];
-            for (int j = 0; j < 4; j++) wv[j] = W[(4 * ea + j) * RS + i];
-            for (int k = 0; k < 4; k++) xv[k] = Xt[(4 * tb + k) * RS + i];
-            for (int j = 0; j < 4; j++)
-                for (int k = 0; k < 4; k++) acc[j][k] = __builtin_fmaf(wv[j], xv[k], acc[j][k]);
-        }
     }
-#undef QMSG_RSRC
-    for (int j = 0; j < 4; j++)
-        for (int k = 0; k < 4; k++) {
+    for (int j = 0; j < J; j++)
+        for (int k = 0; k < KT; k++) {
             const float v = chain16_sum(acc[j][k]);
-            const int t = t0 + 4 * tb + k, e = e0 + 4 * ea + j;
+            const int t = t0 + KT * tb + k, e = e0 + J * ea + j;
             if (c == 0 && t < T) a.S.logits[(size_t)t * X + e] = v;
         }
 }
+
+/* Chunks in flight per thread of the T > 4 router. */
+constexpr int kRouteBigP = 4;
 
 hipError_t launch_route(const Shape &s, const LayerDev &L, const Scratch &S, const float *xn, int T, hipStream_t st)
 {
@@ -337,9 +355,11 @@ hipError_t launch_route(const Shape &s, const LayerDev &L, const Scratch &S, con
         else if (T == 3) QLAUNCH("route", route_small_kernel<3>, grid, dim3(256), lds, st, a);
         else QLAUNCH("route", route_small_kernel<4>, grid, dim3(256), lds, st, a);
     } else {
-        a.n_route_wg = ((T + 15) / 16) * (s.X / 16);
-        const size_t lds = (size_t)2 * 16 * (256 + 4) * 4;
-        QLAUNCH("route", route_big_kernel, dim3(a.n_route_wg + nq), dim3(256), lds, st, a);
+        const int J = T <= 64 ? 1 : 4;               /* experts and tokens per thread group */
+        a.n_route_wg = ((T + 4 * J - 1) / (4 * J)) * (s.X / (4 * J));
+        const size_t lds = (size_t)(8 * J) * (256 + 4) * 4;
+        if (J == 1) QLAUNCH("route", (route_big_kernel<1, 1, kRouteBigP>), dim3(a.n_route_wg + nq), dim3(256), lds, st, a);
+        else QLAUNCH("route", (route_big_kernel<4, 4, kRouteBigP>), dim3(a.n_route_wg + nq), dim3(256), lds, st, a);
     }
     return hipGetLastError();
 }
@@ -940,6 +960,26 @@ __device__ __forceinline__ void q4_1_rows(const uint32_t *Wrow, int p, const uin
     }
 }
 
+/* Row dots of one Q4_0 (TYPE 2) or Q4_1 (TYPE 3) row for nt <= NT tokens, batching as many
+ * pairs as nt allows: a kernel built for NT tokens per pass mostly serves one-token slot
+ * tiles at small batches, where NT-wide batching would leave each pair's LDS reads unhidden. */
+template <int TYPE, int NT>
+__device__ __forceinline__ void q4_rows_nt(const uint32_t *Wrow, int p, const uint8_t *x0, size_t xrec, int q0,
+                                           int nq, int nt, RowAcc *acc)
+{
+    constexpr int B = NT >= 4 ? 1 : (NT == 2 ? 2 : 4);
+    if (NT >= 2 && nt == 1) {
+        if (TYPE == 3) q4_1_rows<1, 4>(Wrow, p, x0, xrec, q0, nq, 1, acc);
+        else q4_0_rows<1, 4>(Wrow, p, x0, xrec, q0, nq, 1, acc);
+    } else if (NT >= 4 && nt == 2) {
+        if (TYPE == 3) q4_1_rows<2, 2>(Wrow, p, x0, xrec, q0, nq, 2, acc);
+        else q4_0_rows<2, 2>(Wrow, p, x0, xrec, q0, nq, 2, acc);
+    } else {
+        if (TYPE == 3) q4_1_rows<NT, B>(Wrow, p, x0, xrec, q0, nq, nt, acc);
+        else q4_0_rows<NT, B>(Wrow, p, x0, xrec, q0, nq, nt, acc);
+    }
+}
+
 /* Offset scale of quad_finish for a row type (Q4_0 8, Q4_1 -1, Q6_K 32). */
 __host__ __device__ constexpr float finish_scale(int type) { return type == 2 ? 8.0f : (type == 3 ? -1.0f : 32.0f); }
 
@@ -1075,9 +1115,8 @@ __global__ __launch_bounds__(64 * W) void gateup_kernel(GateUpArgs a)
                     }
                     wave_sync();
                     if (c + D < nchunk) load_chunk(c + D, wv[d]);
-                    q4_0_rows<NT, (NT >= 4 ? 1 : (NT == 2 ? 2 : 4))>((const uint32_t *)(wbuf + qd * WS), p, xbuf,
-                                                                      (size_t)nP * kPairBytes, c * (CB / 2), CB / 2,
-                                                                      nt, acc);
+                    q4_rows_nt<2, NT>((const uint32_t *)(wbuf + qd * WS), p, xbuf, (size_t)nP * kPairBytes,
+                                      c * (CB / 2), CB / 2, nt, acc);
                 }
             }
         }
@@ -1213,10 +1252,8 @@ __global__ __launch_bounds__(256) void down_tile_kernel(DownArgs a)
         __syncthreads();
         RowAcc acc[NT];
         for (int n = 0; n < NT; n++) acc[n] = RowAcc{ 0.0f, 0.0f, 0.0f };
-        if (TYPE == 2) {
-            q4_0_rows<NT, (NT >= 4 ? 1 : (NT == 2 ? 2 : 4))>((const uint32_t *)row, p, xbuf, (size_t)xrec, 0, nPF, nt, acc);
-        } else if (TYPE == 3) {
-            q4_1_rows<NT, (NT >= 4 ? 1 : (NT == 2 ? 2 : 4))>((const uint32_t *)row, p, xbuf, (size_t)xrec, 0, nPF, nt, acc);
+        if (TYPE == 2 || TYPE == 3) {
+            q4_rows_nt<TYPE, NT>((const uint32_t *)row, p, xbuf, (size_t)xrec, 0, nPF, nt, acc);
         } else {
             const int nsb = a.F >> 8;
             const uint32_t rowoff = (uint32_t)(row - tile);
@@ -1777,14 +1814,8 @@ __global__ __launch_bounds__(64 * W) void dense_kernel(DenseArgs a)
                     }
                     wave_sync();
                     if (c + D < nchunk) load_chunk(c + D, wv[d]);
-                    if (TYPE == 3)
-                        q4_1_rows<NT, (NT >= 4 ? 1 : (NT == 2 ? 2 : 4))>((const uint32_t *)(wbuf + qd * WS), p, xbuf,
-                                                                          (size_t)nP * kPairBytes, c * (CB / 2),
-                                                                          CB / 2, nt, acc);
-                    else
-                        q4_0_rows<NT, (NT >= 4 ? 1 : (NT == 2 ? 2 : 4))>((const uint32_t *)(wbuf + qd * WS), p, xbuf,
-                                                                          (size_t)nP * kPairBytes, c * (CB / 2),
-                                                                          CB / 2, nt, acc);
+                    q4_rows_nt<TYPE, NT>((const uint32_t *)(wbuf + qd * WS), p, xbuf, (size_t)nP * kPairBytes,
+                                         c * (CB / 2), CB / 2, nt, acc);
                 }
             }
         }
