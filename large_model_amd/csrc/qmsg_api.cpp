@@ -67,7 +67,9 @@ struct qmsg_ctx {
     std::vector<void *> scratch_allocs, user_allocs;
     float *d_x = nullptr, *d_out = nullptr;
     std::vector<DenseStore> mats;
-    /* grow-on-demand staging of qmsg_matmul_n's host buffers */
+    /* grow-on-demand buffers of the dense products: input records, host-call staging */
+    void *dense_xqk = nullptr;
+    size_t dense_xqk_bytes = 0;
     void *dense_io = nullptr;
     size_t dense_io_bytes = 0;
     std::string err;
@@ -207,6 +209,7 @@ void qmsg_destroy(qmsg_ctx *c)
         hipFree(L.down);
     }
     for (auto &m : c->mats) hipFree(m.w);
+    hipFree(c->dense_xqk);
     hipFree(c->dense_io);
     for (void *p : c->scratch_allocs) hipFree(p);
     for (void *p : c->user_allocs) hipFree(p);
@@ -639,6 +642,10 @@ int qmsg_matmul_n_device(qmsg_ctx *c, const int *ids, int nW, const float *d_x, 
     if (T == 0) return QMSG_OK;
     if (!d_x || ((uintptr_t)d_x & 15)) return fail(c, QMSG_E_INVALID, "qmsg_matmul_n: x must be 16-byte aligned");
     HIP_TRY(c, hipSetDevice(c->device));
+    if (T >= kDenseQuantT) {
+        const int rc = grow(c, &c->dense_xqk, &c->dense_xqk_bytes, (size_t)T * (size_t)(C / 64) * kPairBytes);
+        if (rc) return rc;
+    }
     /* launches of up to kDenseMats matrices of one type, in argument order */
     std::vector<bool> done((size_t)nW, false);
     for (int i = 0; i < nW; i++) {
@@ -658,7 +665,7 @@ int qmsg_matmul_n_device(qmsg_ctx *c, const int *ids, int nW, const float *d_x, 
             a.nm++;
             done[(size_t)j] = true;
         }
-        LAUNCH(c, "dense", launch_dense(a, type, c->stream));
+        LAUNCH(c, "dense", launch_dense(a, type, (uint8_t *)c->dense_xqk, c->stream));
     }
     return QMSG_OK;
 }

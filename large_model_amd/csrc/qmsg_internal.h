@@ -96,7 +96,12 @@ struct DenseArgs {
     uint64_t rb;
     int C, T;
     const float *x;         /* [T][C] input rows (16-byte aligned) */
+    const uint8_t *xqk;     /* [T][C/64] pair records, or NULL: the kernel quantises x */
 };
+
+/* Batches of at least this many rows are quantised once by a separate launch; smaller ones
+ * inside every dense block. */
+constexpr int kDenseQuantT = 8;
 
 /* Launchers (qmsg_kernels.hip). Each returns hipSuccess or the launch error. */
 hipError_t launch_route(const Shape &s, const LayerDev &L, const Scratch &S, const float *xn, int T,
@@ -118,8 +123,9 @@ hipError_t launch_set_col0(float *m, int rows, int stride, const float *vals, fl
 hipError_t launch_silu(const float *x, int n, float *out, hipStream_t st);
 hipError_t launch_exp(const double *x, int n, double *out, hipStream_t st);
 hipError_t launch_copy(void *dst, const void *src, size_t bytes, hipStream_t st);
-/* The dense rows kernel (quantises a.x itself). */
-hipError_t launch_dense(const DenseArgs &a, int type, hipStream_t st);
+/* The dense rows kernel; for T >= kDenseQuantT the input records are formed first into xqk
+ * (T*C/64 records of 96 bytes). */
+hipError_t launch_dense(const DenseArgs &a, int type, uint8_t *xqk, hipStream_t st);
 hipError_t launch_block_dots(const uint8_t *base, int type, uint64_t rb, uint64_t eb, int n, const int32_t *expert,
                              const int32_t *row, const int32_t *block, const Q8 *xq, int32_t *out,
                              hipStream_t st);

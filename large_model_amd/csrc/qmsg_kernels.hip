@@ -1741,13 +1741,34 @@ hipError_t launch_experts_mfma(const Shape &s, const LayerDev &L, const Scratch 
 
 /* ------------------------------------------------------------------ dense rows (trunk) ---- */
 
+/* The int8 pair records of T input rows of C floats (src/quant.c:151-154: qms_quantize_q8 of
+ * every row), once, for batches where every dense block forming them itself costs more than
+ * a launch: one thread per 32-block. */
+__global__ void dense_quant_kernel(const float *x, int C, int T, uint8_t *xqk)
+{
+    const int nb = C >> 5;
+    const int b = blockIdx.x * blockDim.x + threadIdx.x;
+    if (b >= T * nb) return;
+    const int t = b / nb, blk = b - t * nb;
+    float v[32];
+    const float4 *src = (const float4 *)(x + (size_t)t * C + (size_t)blk * 32);
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+        const float4 f = src[j];
+        v[4 * j] = f.x; v[4 * j + 1] = f.y; v[4 * j + 2] = f.z; v[4 * j + 3] = f.w;
+    }
+    store_pair_half(quantize_block(v), (uint32_t *)(xqk + ((size_t)t * (nb >> 1) + (blk >> 1)) * kPairBytes), blk & 1);
+}
+
 /* qms_matmul_n's fast loop (src/quant.c:151-169) over up to kDenseMats matrices of one type
  * sharing cols: every input row quantised to int8 blocks (qms_quantize_q8), then y_i[t][r] =
  * qms_vec_dot_q8(row r of W_i, xq_t). Block b covers rows 16W*(b - first_i) .. +16W-1 of the
  * matrix i whose block range holds b; wave w owns 16 of them (one per lane quad) and streams
  * exactly those rows in chunks of CB blocks, D chunks in flight, through its own LDS buffer,
- * as the expert kernels do. The block quantises the input rows itself, NT tokens per pass,
- * straight into LDS pair records while its first chunks are on the way (no separate launch).
+ * as the expert kernels do. With a.xqk NULL the block quantises the input rows itself, NT
+ * tokens per pass, straight into LDS pair records while its first chunks are on the way (no
+ * separate launch: the choice below kDenseQuantT tokens); otherwise it copies the records
+ * dense_quant_kernel formed.
  * Rows past the matrix's end load its last row and store nothing. */
 template <int TYPE, int W, int NT, int CB, int D>
 __global__ __launch_bounds__(64 * W) void dense_kernel(DenseArgs a)
@@ -1787,7 +1808,11 @@ __global__ __launch_bounds__(64 * W) void dense_kernel(DenseArgs a)
         for (int d = 0; d < D; d++)
             if (d < nchunk) load_chunk(d, wv[d]);
         if (t0 > 0) __syncthreads();                  /* the previous pass is done with xbuf  */
-        for (int i = tid; i < nt * nb; i += NTH) {
+        if (a.xqk) {                                  /* records formed by dense_quant_kernel */
+            for (int i = tid; i < nt * nP * 6; i += NTH)
+                ((u32x4 *)xbuf)[i] = ((const u32x4 *)(a.xqk + (size_t)t0 * nP * kPairBytes))[i];
+        }
+        for (int i = a.xqk ? nt * nb : tid; i < nt * nb; i += NTH) {
             const int n = i / nb, blk = i - n * nb;
             float v[32];
             const float4 *src = (const float4 *)(a.x + (size_t)(t0 + n) * a.C + (size_t)blk * 32);
@@ -1814,8 +1839,14 @@ __global__ __launch_bounds__(64 * W) void dense_kernel(DenseArgs a)
                     }
                     wave_sync();
                     if (c + D < nchunk) load_chunk(c + D, wv[d]);
-                    q4_rows_nt<TYPE, NT>((const uint32_t *)(wbuf + qd * WS), p, xbuf, (size_t)nP * kPairBytes,
-                                         c * (CB / 2), CB / 2, nt, acc);
+                    if (TYPE == 3)
+                        q4_1_rows<NT, (NT >= 4 ? 1 : (NT == 2 ? 2 : 4))>((const uint32_t *)(wbuf + qd * WS), p, xbuf,
+                                                                          (size_t)nP * kPairBytes, c * (CB / 2),
+                                                                          CB / 2, nt, acc);
+                    else
+                        q4_0_rows<NT, (NT >= 4 ? 1 : (NT == 2 ? 2 : 4))>((const uint32_t *)(wbuf + qd * WS), p, xbuf,
+                                                                          (size_t)nP * kPairBytes, c * (CB / 2),
+                                                                          CB / 2, nt, acc);
                 }
             }
         }
@@ -1835,10 +1866,15 @@ static void launch_dense_t(const DenseArgs &a, int CB, dim3 grid, size_t lds, hi
     else QLAUNCH("dense", (dense_kernel<TYPE, 1, NT, 8, 2>), grid, dim3(64), lds, st, a);
 }
 
-hipError_t launch_dense(const DenseArgs &args, int type, hipStream_t st)
+hipError_t launch_dense(const DenseArgs &args, int type, uint8_t *xqk, hipStream_t st)
 {
     DenseArgs a = args;
     const int nb = a.C / 32;
+    a.xqk = nullptr;
+    if (a.T >= kDenseQuantT && xqk) {
+        QLAUNCH("dquant", dense_quant_kernel, dim3((a.T * nb + 255) / 256), dim3(256), 0, st, a.x, a.C, a.T, xqk);
+        a.xqk = xqk;
+    }
     /* one wave per block, 16 rows each: the trunk's small matrices (attn_k/v: 512 rows) still
      * spread over 32 CUs, the large ones over every CU */
     int nblk = 0;
