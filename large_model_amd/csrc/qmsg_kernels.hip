@@ -653,32 +653,47 @@ __device__ __forceinline__ void q4_1_math(const Q41Pair &w, const XPair &x, RowA
     r.corr = __builtin_fmaf(o1, x.d.w, r.corr);
 }
 
-/* One Q6_K 32-block (index g of half h of the super-block at byte sb of the LDS tile)
- * against one token's block, src/kernels.c:148-167: lanes k < 4 use sc[2g], k >= 4 sc[2g+1]. */
-__device__ __forceinline__ void q6_k_block(const uint8_t *tile, uint32_t sb, int h, int g, int p, const uint8_t *xp,
-                                           int xhalf, RowAcc &r)
+/* The weight side of one Q6_K 32-block for lane p (src/kernels.c:148-160): its two 6-bit code
+ * dwords (elements 4p.. of the low 16 and of the high 16), the two sub-scales and d. Read once
+ * and used for every token of a pass. */
+struct Q6W {
+    uint32_t q6lo, q6hi;
+    int sa, sb;
+    float d;
+};
+
+__device__ __forceinline__ Q6W q6_k_weights(const uint8_t *tile, uint32_t sb, int h, int g, int p)
 {
     const uint32_t qlo = lds_u32(tile, sb + 64 * h + 32 * (g & 1) + 4 * p);
     const uint32_t qhi = lds_u32(tile, sb + 64 * h + 32 * (g & 1) + 16 + 4 * p);
     const uint32_t hlo = lds_u32(tile, sb + 128 + 32 * h + 4 * p);
     const uint32_t hhi = lds_u32(tile, sb + 128 + 32 * h + 16 + 4 * p);
     const uint32_t scw = lds_u32(tile, sb + 192 + 8 * h + 2 * g);
-    const float d = h2f(lds_u32(tile, sb + 208) & 0xffffu);
-    const int sa = (int)(int8_t)(scw & 0xff), sbb = (int)(int8_t)((scw >> 8) & 0xff);
     const int sh = 2 * g;
     const uint32_t nlo = g < 2 ? (qlo & 0x0f0f0f0fu) : ((qlo >> 4) & 0x0f0f0f0fu);
     const uint32_t nhi = g < 2 ? (qhi & 0x0f0f0f0fu) : ((qhi >> 4) & 0x0f0f0f0fu);
-    const uint32_t q6lo = nlo | (((hlo >> sh) & 0x03030303u) << 4);
-    const uint32_t q6hi = nhi | (((hhi >> sh) & 0x03030303u) << 4);
+    Q6W w;
+    w.q6lo = nlo | (((hlo >> sh) & 0x03030303u) << 4);
+    w.q6hi = nhi | (((hhi >> sh) & 0x03030303u) << 4);
+    w.sa = (int)(int8_t)(scw & 0xff);
+    w.sb = (int)(int8_t)((scw >> 8) & 0xff);
+    w.d = h2f(lds_u32(tile, sb + 208) & 0xffffu);
+    return w;
+}
+
+/* The token side of the same block against one token's pair record (lanes k < 4 use sc[2g],
+ * k >= 4 sc[2g+1]; src/kernels.c:161-167), on weights already read. */
+__device__ __forceinline__ void q6_k_token(const Q6W &w, const uint8_t *xp, int p, int xhalf, RowAcc &r)
+{
     const uint32_t xlo = *(const uint32_t *)(xp + 16 * p + 8 * xhalf);
     const uint32_t xhi = *(const uint32_t *)(xp + 16 * p + 8 * xhalf + 4);
     const float xd = *(const float *)(xp + 64 + 8 * xhalf);
     const uint32_t s16 = *(const uint32_t *)(xp + 80 + 4 * xhalf);
     const int s16a = (int)(int16_t)(s16 & 0xffffu), s16b = (int)(int16_t)(s16 >> 16);
-    const float dd = d * xd;
-    r.lo = __builtin_fmaf((float)(sdot4((int)q6lo, (int)xlo) * sa), dd, r.lo);
-    r.hi = __builtin_fmaf((float)(sdot4((int)q6hi, (int)xhi) * sbb), dd, r.hi);
-    r.corr = __builtin_fmaf(dd, (float)(sa * s16a + sbb * s16b), r.corr);
+    const float dd = w.d * xd;
+    r.lo = __builtin_fmaf((float)(sdot4((int)w.q6lo, (int)xlo) * w.sa), dd, r.lo);
+    r.hi = __builtin_fmaf((float)(sdot4((int)w.q6hi, (int)xhi) * w.sb), dd, r.hi);
+    r.corr = __builtin_fmaf(dd, (float)(w.sa * s16a + w.sb * s16b), r.corr);
 }
 
 /* hsum256 over the quad, then the unfused offset term h - scale*corr: scale 8 (Q4_0), 32
@@ -1264,11 +1279,12 @@ __global__ __launch_bounds__(256) void down_tile_kernel(DownArgs a)
 #pragma unroll
                     for (int g = 0; g < 4; g++) {
                         const int blk = sbi * 8 + h * 4 + g;
+                        const Q6W w = q6_k_weights(tile, sb, h, g, p);
 #pragma unroll
                         for (int n = 0; n < NT; n++)
                             if (n < nt)
-                                q6_k_block(tile, sb, h, g, p, xbuf + (size_t)n * xrec + (size_t)(blk >> 1) * kPairBytes,
-                                           blk & 1, acc[n]);
+                                q6_k_token(w, xbuf + (size_t)n * xrec + (size_t)(blk >> 1) * kPairBytes, p, blk & 1,
+                                           acc[n]);
                     }
             }
         }
