@@ -17,6 +17,8 @@
 #include <hip/hip_runtime.h>
 #include <hip/hip_ext.h>
 
+#include <type_traits>
+
 #include "qmsg_internal.h"
 #include "qmsg_libm.h"
 #include "qmsg_synth.h"
@@ -662,13 +664,23 @@ struct Q6W {
     float d;
 };
 
+template <bool AL>
+__device__ __forceinline__ uint32_t lds_word(const uint8_t *base, uint32_t a)
+{
+    if (AL) return *(const uint32_t *)(base + a);      /* a is a multiple of 4 */
+    return lds_u32(base, a);
+}
+
+/* AL: the super-block starts at a multiple of 4 bytes, so its code dwords are single reads. */
+template <bool AL>
 __device__ __forceinline__ Q6W q6_k_weights(const uint8_t *tile, uint32_t sb, int h, int g, int p)
 {
-    const uint32_t qlo = lds_u32(tile, sb + 64 * h + 32 * (g & 1) + 4 * p);
-    const uint32_t qhi = lds_u32(tile, sb + 64 * h + 32 * (g & 1) + 16 + 4 * p);
-    const uint32_t hlo = lds_u32(tile, sb + 128 + 32 * h + 4 * p);
-    const uint32_t hhi = lds_u32(tile, sb + 128 + 32 * h + 16 + 4 * p);
-    const uint32_t scw = lds_u32(tile, sb + 192 + 8 * h + 2 * g);
+    const uint32_t qlo = lds_word<AL>(tile, sb + 64 * h + 32 * (g & 1) + 4 * p);
+    const uint32_t qhi = lds_word<AL>(tile, sb + 64 * h + 32 * (g & 1) + 16 + 4 * p);
+    const uint32_t hlo = lds_word<AL>(tile, sb + 128 + 32 * h + 4 * p);
+    const uint32_t hhi = lds_word<AL>(tile, sb + 128 + 32 * h + 16 + 4 * p);
+    const uint32_t scw = AL ? (lds_word<true>(tile, sb + 192 + 8 * h + 4 * (g >> 1)) >> (16 * (g & 1)))
+                            : lds_u32(tile, sb + 192 + 8 * h + 2 * g);
     const int sh = 2 * g;
     const uint32_t nlo = g < 2 ? (qlo & 0x0f0f0f0fu) : ((qlo >> 4) & 0x0f0f0f0fu);
     const uint32_t nhi = g < 2 ? (qhi & 0x0f0f0f0fu) : ((qhi >> 4) & 0x0f0f0f0fu);
@@ -677,7 +689,7 @@ __device__ __forceinline__ Q6W q6_k_weights(const uint8_t *tile, uint32_t sb, in
     w.q6hi = nhi | (((hhi >> sh) & 0x03030303u) << 4);
     w.sa = (int)(int8_t)(scw & 0xff);
     w.sb = (int)(int8_t)((scw >> 8) & 0xff);
-    w.d = h2f(lds_u32(tile, sb + 208) & 0xffffu);
+    w.d = h2f(lds_word<AL>(tile, sb + 208) & 0xffffu);
     return w;
 }
 
@@ -1237,32 +1249,33 @@ struct DownArgs {
  * list): 64 output rows R0 .. R0+63 (one per lane quad), staged once in LDS, against the
  * tile's int8 activation records, NT slots per pass. Writes dn[slot][row]; the combine runs
  * afterwards in selection order. */
-template <int TYPE, int NT>
-__global__ __launch_bounds__(256) void down_tile_kernel(DownArgs a)
+template <int TYPE, int NT, int RT>
+__global__ __launch_bounds__(4 * RT) void down_tile_kernel(DownArgs a)
 {
     extern __shared__ __align__(16) uint8_t smem[];
+    constexpr int NTH = 4 * RT;
     if ((int)blockIdx.y >= a.S.meta[1]) return;
     const int4 tl = a.S.tiles[blockIdx.y];
     const int e = tl.x, s0 = tl.y, ns = tl.z - tl.y;
     const int tid = threadIdx.x, quad = tid >> 2, p = tid & 3;
-    const int R0 = (int)blockIdx.x * 64, E = a.E, nPF = a.F >> 6, xrec = nPF * kPairBytes;
-    const int rb = (int)a.rb, n16 = 64 * rb / 16;
+    const int R0 = (int)blockIdx.x * RT, E = a.E, nPF = a.F >> 6, xrec = nPF * kPairBytes;
+    const int rb = (int)a.rb, n16 = RT * rb / 16;
     uint8_t *tile = smem;
-    uint8_t *xbuf = smem + ((64 * rb + 15) & ~15);            /* [NT][xrec] */
+    uint8_t *xbuf = smem + ((RT * rb + 15) & ~15);            /* [NT][xrec] */
     const u32x4 *wsrc = (const u32x4 *)(a.down + (size_t)e * a.eb + (size_t)R0 * a.rb);
-    for (int i0 = 0; i0 < n16; i0 += 256 * 8) {
+    for (int i0 = 0; i0 < n16; i0 += NTH * 8) {
         u32x4 v[8];
 #pragma unroll
-        for (int m = 0; m < 8; m++) v[m] = wsrc[min(i0 + tid + 256 * m, n16 - 1)];
+        for (int m = 0; m < 8; m++) v[m] = wsrc[min(i0 + tid + NTH * m, n16 - 1)];
 #pragma unroll
         for (int m = 0; m < 8; m++)
-            if (i0 + tid + 256 * m < n16) ((u32x4 *)tile)[i0 + tid + 256 * m] = v[m];
+            if (i0 + tid + NTH * m < n16) ((u32x4 *)tile)[i0 + tid + NTH * m] = v[m];
     }
     const uint8_t *row = tile + quad * rb;
     for (int g0 = 0; g0 < ns; g0 += NT) {
         const int nt = min(NT, ns - g0);
         __syncthreads();                                  /* the weights landed; xbuf is free */
-        for (int i = tid; i < nt * (xrec >> 4); i += 256)
+        for (int i = tid; i < nt * (xrec >> 4); i += NTH)
             ((u32x4 *)xbuf)[i] = ((const u32x4 *)(a.S.aqk + (size_t)(s0 + g0) * xrec))[i];
         __syncthreads();
         RowAcc acc[NT];
@@ -1272,20 +1285,26 @@ __global__ __launch_bounds__(256) void down_tile_kernel(DownArgs a)
         } else {
             const int nsb = a.F >> 8;
             const uint32_t rowoff = (uint32_t)(row - tile);
-            for (int sbi = 0; sbi < nsb; sbi++) {
+            /* rows of a multiple of 4 bytes: even super-blocks start 4-aligned on every row */
+            const bool even_al = (rb & 3) == 0;
+            auto superblock = [&](auto al, int sbi) {
                 const uint32_t sb = rowoff + (uint32_t)(sbi * 210);
 #pragma unroll
                 for (int h = 0; h < 2; h++)
 #pragma unroll
                     for (int g = 0; g < 4; g++) {
                         const int blk = sbi * 8 + h * 4 + g;
-                        const Q6W w = q6_k_weights(tile, sb, h, g, p);
+                        const Q6W w = q6_k_weights<decltype(al)::value>(tile, sb, h, g, p);
 #pragma unroll
                         for (int n = 0; n < NT; n++)
                             if (n < nt)
                                 q6_k_token(w, xbuf + (size_t)n * xrec + (size_t)(blk >> 1) * kPairBytes, p, blk & 1,
                                            acc[n]);
                     }
+            };
+            for (int sbi = 0; sbi < nsb; sbi++) {
+                if (even_al && !(sbi & 1)) superblock(std::integral_constant<bool, true>(), sbi);
+                else superblock(std::integral_constant<bool, false>(), sbi);
             }
         }
 #pragma unroll
@@ -1456,6 +1475,18 @@ __global__ void combine_kernel(const Scratch S, int E, int K, int T, float *out)
     out[i] = o;
 }
 
+template <int TYPE, int RT>
+static void launch_down_tile(const DownArgs &a, int NT, dim3 grid, size_t lds, hipStream_t st)
+{
+    if (NT == 4) QLAUNCH("down", (down_tile_kernel<TYPE, 4, RT>), grid, dim3(4 * RT), lds, st, a);
+    else if (NT == 2) QLAUNCH("down", (down_tile_kernel<TYPE, 2, RT>), grid, dim3(4 * RT), lds, st, a);
+    else QLAUNCH("down", (down_tile_kernel<TYPE, 1, RT>), grid, dim3(4 * RT), lds, st, a);
+}
+
+/* Rows per block of the Q6_K slot-tile kernel (its 210-byte super-blocks make a 64-row tile
+ * 81 KB of LDS for n_ff_exp 1536, one block per CU). */
+constexpr int kDownTileRowsQ6K = 32;
+
 /* Output rows per block of the one-token down kernel (8: 512 blocks of 4 waves for E = 4096;
  * 16: 256 blocks of 8 waves, half the activation reads). */
 constexpr int kDownT1Rows = 16;
@@ -1497,22 +1528,13 @@ hipError_t launch_down_exact(const Shape &s, const LayerDev &L, const Scratch &S
         QLAUNCH("actq", act_quant_kernel, dim3((nq + 255) / 256), dim3(256), 0, st, S, s.F, NS);
     }
     const int NT = T >= 4 ? 4 : (T >= 2 ? 2 : 1);
-    const size_t lds = ((64 * L.down_rb + 15) & ~(size_t)15) + (size_t)NT * xrec;
-    if (lds > 160 * 1024 || s.E % 64) return hipErrorInvalidValue;
-    const dim3 grid(s.E / 64, maxt);
-    if (L.down_type == 2) {
-        if (NT == 4) QLAUNCH("down", (down_tile_kernel<2, 4>), grid, dim3(256), lds, st, a);
-        else if (NT == 2) QLAUNCH("down", (down_tile_kernel<2, 2>), grid, dim3(256), lds, st, a);
-        else QLAUNCH("down", (down_tile_kernel<2, 1>), grid, dim3(256), lds, st, a);
-    } else if (L.down_type == 3) {
-        if (NT == 4) QLAUNCH("down", (down_tile_kernel<3, 4>), grid, dim3(256), lds, st, a);
-        else if (NT == 2) QLAUNCH("down", (down_tile_kernel<3, 2>), grid, dim3(256), lds, st, a);
-        else QLAUNCH("down", (down_tile_kernel<3, 1>), grid, dim3(256), lds, st, a);
-    } else {
-        if (NT == 4) QLAUNCH("down", (down_tile_kernel<14, 4>), grid, dim3(256), lds, st, a);
-        else if (NT == 2) QLAUNCH("down", (down_tile_kernel<14, 2>), grid, dim3(256), lds, st, a);
-        else QLAUNCH("down", (down_tile_kernel<14, 1>), grid, dim3(256), lds, st, a);
-    }
+    const int RT = L.down_type == 14 ? kDownTileRowsQ6K : 64;
+    const size_t lds = ((RT * L.down_rb + 15) & ~(size_t)15) + (size_t)NT * xrec;
+    if (lds > 160 * 1024 || s.E % RT) return hipErrorInvalidValue;
+    const dim3 grid(s.E / RT, maxt);
+    if (L.down_type == 2) launch_down_tile<2, 64>(a, NT, grid, lds, st);
+    else if (L.down_type == 3) launch_down_tile<3, 64>(a, NT, grid, lds, st);
+    else launch_down_tile<14, kDownTileRowsQ6K>(a, NT, grid, lds, st);
     const int n = T * s.E;
     QLAUNCH("combine", combine_kernel, dim3((n + 255) / 256), dim3(256), 0, st, S, s.E, s.K, T, out);
     return hipGetLastError();
