@@ -89,18 +89,36 @@ struct Q8Vals {
 
 __device__ Q8Vals quantize_block(const float *v)
 {
-    float amax = 0.0f;
-    for (int j = 0; j < 32; j++) amax = fmaxf(amax, fabsf(v[j]));
+    /* the maximum and the integer sums as trees: both are exact in any order, and a tree has a
+     * dependency depth of 5 instead of 32 (the quantiser often runs one wave per SIMD, where
+     * every dependent step costs its full latency). fmaxf ignores NaN like the reference's
+     * running fmaxf from 0; the final fmaxf with 0 covers an all-NaN block. */
+    float m[16];
+#pragma unroll
+    for (int j = 0; j < 16; j++) m[j] = fmaxf(fabsf(v[j]), fabsf(v[j + 16]));
+#pragma unroll
+    for (int w = 8; w > 0; w >>= 1)
+#pragma unroll
+        for (int j = 0; j < w; j++) m[j] = fmaxf(m[j], m[j + w]);
+    const float amax = fmaxf(0.0f, m[0]);
     Q8Vals r;
     r.d = amax / 127.0f;
     const float id = r.d > 0.0f ? 1.0f / r.d : 0.0f;
     int8_t q[32];
-    int s0 = 0, s1 = 0;
+    int qs[32];
+#pragma unroll
     for (int j = 0; j < 32; j++) {
-        const int qi = (int)rintf(v[j] * id);
-        q[j] = (int8_t)qi;
-        if (j < 16) s0 += qi; else s1 += qi;
+        qs[j] = (int)rintf(v[j] * id);
+        q[j] = (int8_t)qs[j];
     }
+#pragma unroll
+    for (int w = 8; w > 0; w >>= 1)
+#pragma unroll
+        for (int j = 0; j < w; j++) {
+            qs[j] += qs[j + w];
+            qs[16 + j] += qs[16 + j + w];
+        }
+    const int s0 = qs[0], s1 = qs[16];
     r.ds = r.d * (float)(s0 + s1);
     r.s16 = (uint32_t)(uint16_t)(int16_t)s0 | ((uint32_t)(uint16_t)(int16_t)s1 << 16);
     for (int w = 0; w < 8; w++) r.qw[w] = pack4(q + 4 * w);
@@ -1896,6 +1914,150 @@ __global__ __launch_bounds__(64 * W) void dense_kernel(DenseArgs a)
     }
 }
 
+/* One block pair of a Q4_0 (TYPE 2) or Q4_1 (TYPE 3) row for lane k of an octet: the lane keeps
+ * the reference's FMA chain k (elements 4k..4k+3 of each block, src/kernels.c:82-94, 109-121)
+ * and the offset chain. */
+template <int TYPE>
+__device__ __forceinline__ void oct_pair(const uint32_t *W, int k, const uint8_t *xp, float &acc, float &corr)
+{
+    const int p = k & 3, hi = k >> 2;
+    const XPair x = x_load(xp, p);
+    const uint32_t xb = hi ? x.q.y : x.q.x, xb1 = hi ? x.q.w : x.q.z;
+    uint32_t c0, c1, wa, wb;
+    if (TYPE == 3) {
+        const Q41Pair w = q4_1_load(W, p);
+        c0 = w.c0; c1 = w.c1; wa = w.w0; wb = w.w5;
+    } else {
+        const Q4Pair w = q4_0_load(W, p);
+        c0 = w.c0; c1 = w.c1; wa = w.w0; wb = w.w4;
+    }
+    const uint32_t n0 = (hi ? c0 >> 4 : c0) & 0x0f0f0f0fu, n1 = (hi ? c1 >> 4 : c1) & 0x0f0f0f0fu;
+    const int s0 = sdot4((int)n0, (int)xb), s1 = sdot4((int)n1, (int)xb1);
+    float m0, m1, o0, o1;
+    if (TYPE == 3) {
+        m0 = mul_f16_f32<0>(wa, x.d.x);
+        m1 = mul_f16_f32<0>(wb, x.d.z);
+        o0 = h2f(wa >> 16);
+        o1 = h2f(wb >> 16);
+    } else {
+        m0 = mul_f16_f32<0>(wa, x.d.x);
+        m1 = mul_f16_f32<1>(wb, x.d.z);
+        o0 = h2f(wa & 0xffffu);
+        o1 = h2f(wb >> 16);
+    }
+    acc = __builtin_fmaf((float)s0, m0, acc);
+    corr = __builtin_fmaf(o0, x.d.y, corr);
+    acc = __builtin_fmaf((float)s1, m1, acc);
+    corr = __builtin_fmaf(o1, x.d.w, corr);
+}
+
+/* hsum256 over the octet (s_j = a_j + a_{j+4}, then (s0+s2)+(s1+s3)) and the unfused offset
+ * term, as quad_finish. Valid on lane k == 0. */
+__device__ __forceinline__ float oct_finish(float acc, float corr, float scale)
+{
+    const float s = acc + __shfl_down(acc, 4, 8);
+    const float t = s + __shfl_down(s, 2, 8);
+    const float h = t + __shfl_down(t, 1, 8);
+    return h - scale * corr;
+}
+
+/* One-token dense products: as dense_kernel, but eight lanes per row (one per reference lane
+ * chain), so a wave streams 8 rows and a launch has twice the waves, each with half the bytes.
+ * The trunk's one-token launches have few rows (attn_k/v: 512), and each wave's stream is a
+ * serial chain of chunk waits, so more and shorter streams finish sooner. */
+constexpr int kDenseOctXB = 4;     /* input 32-blocks per lane held in registers (cols <= 8192) */
+
+template <int TYPE, int CB, int D>
+__global__ __launch_bounds__(64) void dense_oct_kernel(DenseArgs a)
+{
+    extern __shared__ __align__(16) uint8_t smem[];
+    constexpr int BB = TYPE == 3 ? 20 : 18;           /* bytes per 32-block                   */
+    constexpr int SPR = CB * BB / 16;                 /* 16-byte slots per row per chunk      */
+    constexpr int NSL = 8 * SPR;                      /* slots of the wave's chunk            */
+    constexpr int SPT = (NSL + 63) / 64;              /* slots per lane per chunk             */
+    constexpr int WS = CB * BB + ((SPR & 1) ? 0 : 16);/* LDS row stride, odd in 16-byte units */
+    const int nb = a.C >> 5, nP = nb >> 1, nchunk = nb / CB;
+    const int lane = threadIdx.x, rr = lane >> 3, k = lane & 7;
+    uint8_t *wbuf = smem;
+    uint8_t *xbuf = smem + 8 * WS;
+
+    int mi = 0;
+#pragma unroll
+    for (int i = 1; i < kDenseMats; i++)
+        if (i < a.nm && (int)blockIdx.x >= a.m[i].first_block) mi = i;
+    const DenseMat M = a.m[mi];
+    const int rw = ((int)blockIdx.x - M.first_block) * 8;                 /* the wave's first row */
+    const uint8_t *wbase = M.w + (size_t)min(rw, M.rows - 1) * a.rb;
+    const int last = M.rows - 1 - min(rw, M.rows - 1);
+    u32x4 wv[D][SPT];
+    auto load_chunk = [&](int c, u32x4 *dst) {
+#pragma unroll
+        for (int m = 0; m < SPT; m++) {
+            const int i = min(lane + 64 * m, NSL - 1), row = i / SPR, j = i - row * SPR;
+            dst[m] = *(const u32x4 *)(wbase + (size_t)min(row, last) * a.rb + (size_t)c * CB * BB + 16 * j);
+        }
+    };
+    /* the input row first, then the weights: loads complete in order, so quantising the row
+     * waits only for its own bytes while the first chunks are still on the way */
+    constexpr int XB = kDenseOctXB;
+    float4 xr[XB][8];
+#pragma unroll
+    for (int u = 0; u < XB; u++) {
+        const float4 *src = (const float4 *)(a.x + (size_t)min(lane + 64 * u, nb - 1) * 32);
+#pragma unroll
+        for (int j = 0; j < 8; j++) xr[u][j] = src[j];
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int d = 0; d < D; d++)
+        if (d < nchunk) load_chunk(d, wv[d]);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int u = 0; u < XB; u++) {
+        const int b = lane + 64 * u;
+        if (b < nb) {
+            float v[32];
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+                v[4 * j] = xr[u][j].x; v[4 * j + 1] = xr[u][j].y; v[4 * j + 2] = xr[u][j].z; v[4 * j + 3] = xr[u][j].w;
+            }
+            store_pair_half(quantize_block(v), (uint32_t *)(xbuf + (size_t)(b >> 1) * kPairBytes), b & 1);
+        }
+    }
+    for (int b = lane + 64 * XB; b < nb; b += 64) {   /* rows longer than the register share */
+        float v[32];
+        const float4 *src = (const float4 *)(a.x + (size_t)b * 32);
+        for (int j = 0; j < 8; j++) {
+            const float4 f = src[j];
+            v[4 * j] = f.x; v[4 * j + 1] = f.y; v[4 * j + 2] = f.z; v[4 * j + 3] = f.w;
+        }
+        store_pair_half(quantize_block(v), (uint32_t *)(xbuf + (size_t)(b >> 1) * kPairBytes), b & 1);
+    }
+    float acc = 0.0f, corr = 0.0f;
+    for (int c0 = 0; c0 < nchunk; c0 += D) {
+#pragma unroll
+        for (int d = 0; d < D; d++) {
+            const int c = c0 + d;
+            if (c < nchunk) {
+                wave_sync();
+#pragma unroll
+                for (int m = 0; m < SPT; m++) {
+                    const int i = min(lane + 64 * m, NSL - 1), r = i / SPR, j = i - r * SPR;
+                    *(u32x4 *)(wbuf + r * WS + 16 * j) = wv[d][m];
+                }
+                wave_sync();
+                if (c + D < nchunk) load_chunk(c + D, wv[d]);
+                const uint32_t *Wrow = (const uint32_t *)(wbuf + rr * WS);
+#pragma unroll 4
+                for (int q = 0; q < CB / 2; q++)
+                    oct_pair<TYPE>(Wrow + q * (BB * 2 / 4), k, xbuf + (size_t)(c * (CB / 2) + q) * kPairBytes, acc, corr);
+            }
+        }
+    }
+    const float v = oct_finish(acc, corr, finish_scale(TYPE));
+    if (k == 0 && rw + rr < M.rows) M.y[rw + rr] = v;
+}
+
 /* Two chunks in flight per wave (2, 4 and 8 were measured at the trunk's shapes: 2 fastest). */
 template <int TYPE, int NT>
 static void launch_dense_t(const DenseArgs &a, int CB, dim3 grid, size_t lds, hipStream_t st)
@@ -1915,6 +2077,24 @@ hipError_t launch_dense(const DenseArgs &args, int type, uint8_t *xqk, hipStream
     }
     /* one wave per block, 16 rows each: the trunk's small matrices (attn_k/v: 512 rows) still
      * spread over 32 CUs, the large ones over every CU */
+    if (a.T == 1) {                                   /* eight lanes per row, 8 rows per wave */
+        int nb8 = 0;
+        for (int i = 0; i < a.nm; i++) {
+            a.m[i].first_block = nb8;
+            nb8 += (a.m[i].rows + 7) / 8;
+        }
+        const int CB = nb % 16 == 0 ? 16 : 8, bb = type == 3 ? 20 : 18;
+        const size_t ws = (size_t)CB * bb + (((CB * bb / 16) & 1) ? 0 : 16);
+        const size_t lds8 = 8 * ws + (size_t)(nb / 2) * kPairBytes;
+        if (type == 3) {
+            if (CB == 16) QLAUNCH("dense", (dense_oct_kernel<3, 16, 2>), dim3(nb8), dim3(64), lds8, st, a);
+            else QLAUNCH("dense", (dense_oct_kernel<3, 8, 2>), dim3(nb8), dim3(64), lds8, st, a);
+        } else {
+            if (CB == 16) QLAUNCH("dense", (dense_oct_kernel<2, 16, 2>), dim3(nb8), dim3(64), lds8, st, a);
+            else QLAUNCH("dense", (dense_oct_kernel<2, 8, 2>), dim3(nb8), dim3(64), lds8, st, a);
+        }
+        return hipGetLastError();
+    }
     int nblk = 0;
     for (int i = 0; i < a.nm; i++) {
         a.m[i].first_block = nblk;

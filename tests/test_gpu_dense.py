@@ -65,10 +65,12 @@ def test_dense_qkv_and_output_235b_shapes(q, T):
     assert np.array_equal(bits(yo), bits(orc.matmul_q8(orc.T_Q4_0, wo, E, H, a)))
 
 
-def test_dense_mixed_types_tails_and_device_buffers(q):
+@pytest.mark.parametrize("T", [1, 3])
+def test_dense_mixed_types_tails_and_device_buffers(q, T):
     """Q4_0 and Q4_1 matrices in one call (two launches), row counts that are not multiples
-    of 16, more than four matrices, and the device-buffer entry point."""
-    C, T = 2048, 3
+    of 8 or 16, more than four matrices, and the device-buffer entry point (one token: eight
+    lanes per row; three: four)."""
+    C = 2048
     shapes = [(orc.T_Q4_1, 1000), (orc.T_Q4_0, 17), (orc.T_Q4_1, 16), (orc.T_Q4_0, 1), (orc.T_Q4_0, 300),
               (orc.T_Q4_1, 65)]
     ws = [dense_mat(t, r, C, 30 + i) for i, (t, r) in enumerate(shapes)]
