@@ -28,6 +28,12 @@ CASES = [
     ("q480b_t1", 6144, 160, 8, 2560, 1, 14, orc.T_Q4_0, True),
     ("q480b_q41_t1", 6144, 160, 8, 2560, 1, 15, orc.T_Q4_1, False),
     ("q480b_t5", 6144, 160, 8, 2560, 5, 16, orc.T_Q4_0, False),
+    # limits and shapes off the common path
+    ("k16_t1", 512, 64, 16, 256, 1, 21, orc.T_Q4_0, False),      # n_used > 8: routed by select
+    ("k64_all_t2", 256, 64, 64, 128, 2, 22, orc.T_Q4_0, False),  # every expert used (QMS_MAX_USED)
+    ("x256_t3", 256, 256, 8, 128, 3, 23, orc.T_Q4_0, False),     # 256 experts (kernel maximum)
+    ("f64_t3", 256, 16, 4, 64, 3, 24, orc.T_Q4_1, False),        # smallest n_ff_exp
+    ("q6k_f768_t1", 2048, 128, 8, 768, 1, 25, orc.T_Q6_K, True),  # odd super-blocks per row
 ]
 
 
