@@ -79,8 +79,14 @@ typedef struct qmsg_ctx qmsg_ctx;
  *          exact, fp32 rows summed per block in another order (about 1e-6 of a row's
  *          magnitude), which moves an int8 activation code where a value sits on a rounding
  *          boundary (a few per 1e5 codes). An opt-in for prefill throughput.
- *   AUTO:  EXACT (the order-exact results are the contract). */
-enum { QMSG_PATH_AUTO = 0, QMSG_PATH_EXACT = 1, QMSG_PATH_MFMA = 2 };
+ *   AUTO:  EXACT (the order-exact results are the contract).
+ *   FP32:  the reference's --exact mode (qms_exact_math = 1, src/quant.c:95-115,
+ *          model.c:1009-1030): router, gate/up and down rows dequantised to fp32 and dotted in
+ *          one FMA chain per row (matmul_exact), fp32 activations, no int8 blocks; bit-identical
+ *          to the reference run with --exact. Takes Q4_0, Q4_1 or Q6_K for every expert tensor.
+ * The integer paths (AUTO, EXACT, MFMA) take Q4_0 gate/up; a layer with other gate/up types
+ * runs only with FP32. */
+enum { QMSG_PATH_AUTO = 0, QMSG_PATH_EXACT = 1, QMSG_PATH_MFMA = 2, QMSG_PATH_FP32 = 3 };
 
 /* ------------------------------------------------------------------ lifecycle ---- */
 

@@ -226,7 +226,7 @@ void *qmsg_stream(qmsg_ctx *c) { return c ? (void *)c->stream : nullptr; }
 int qmsg_set_path(qmsg_ctx *c, int path)
 {
     if (!c) return QMSG_E_INVALID;
-    if (path != QMSG_PATH_AUTO && path != QMSG_PATH_EXACT && path != QMSG_PATH_MFMA)
+    if (path != QMSG_PATH_AUTO && path != QMSG_PATH_EXACT && path != QMSG_PATH_MFMA && path != QMSG_PATH_FP32)
         return fail(c, QMSG_E_INVALID, "qmsg_set_path: unknown path %d", path);
     c->path = path;
     return QMSG_OK;
@@ -242,10 +242,10 @@ static int check_layer_index(qmsg_ctx *c, int layer)
 static int layer_alloc(qmsg_ctx *c, LayerStore &L, int gt, int ut, int dt)
 {
     const int64_t E = c->cfg.n_embd, X = c->cfg.n_expert, F = c->cfg.n_ff_exp;
-    if (gt != QMSG_T_Q4_0 || ut != QMSG_T_Q4_0 || (dt != QMSG_T_Q4_0 && dt != QMSG_T_Q4_1 && dt != QMSG_T_Q6_K))
-        return fail(c, QMSG_E_UNSUPPORTED,
-                    "expert types gate=%d up=%d down=%d: kernels take Q4_0 gate/up and Q4_0, Q4_1 or Q6_K down", gt, ut,
-                    dt);
+    auto known = [](int t) { return t == QMSG_T_Q4_0 || t == QMSG_T_Q4_1 || t == QMSG_T_Q6_K; };
+    if (!known(gt) || !known(ut) || !known(dt))
+        return fail(c, QMSG_E_UNSUPPORTED, "expert types gate=%d up=%d down=%d: kernels take Q4_0, Q4_1 and Q6_K", gt,
+                    ut, dt);
     if (dt == QMSG_T_Q6_K && F % 256)
         return fail(c, QMSG_E_UNSUPPORTED, "Q6_K down needs n_ff_exp %% 256 == 0 (got %lld)", (long long)F);
     hipFree(L.router); hipFree(L.gate); hipFree(L.up); hipFree(L.down);
@@ -713,6 +713,13 @@ static int run_layer(qmsg_ctx *c, int layer, const float *d_xn, int T, float *d_
         return fail(c, QMSG_E_INVALID, "device buffers must be 16-byte aligned (xn) and 4-byte aligned (out)");
     const Shape s{ c->cfg.n_embd, c->cfg.n_expert, c->cfg.n_used, c->cfg.n_ff_exp };
     const LayerDev d = layer_dev(c, L);
+    if (c->path == QMSG_PATH_FP32) {
+        LAUNCH(c, "layer", launch_layer_fp32(s, d, c->S, d_xn, d_out, T, c->stream));
+        return QMSG_OK;
+    }
+    if (d.gate_type != QMSG_T_Q4_0 || d.up_type != QMSG_T_Q4_0)
+        return fail(c, QMSG_E_UNSUPPORTED, "layer %d: the integer gate/up kernels take Q4_0 (types %d, %d); "
+                    "QMSG_PATH_FP32 takes any", layer, d.gate_type, d.up_type);
     /* the MFMA grouped GEMM takes Q4_0 gate/up weights and batches routed by the select kernel */
     const bool mfma = c->path == QMSG_PATH_MFMA && d.gate_type == QMSG_T_Q4_0 && d.up_type == QMSG_T_Q4_0 &&
                       !use_small_route(T, s.K) && s.E % 256 == 0 && s.F % 256 == 0;

@@ -113,6 +113,9 @@ hipError_t launch_experts_mfma(const Shape &s, const LayerDev &L, const Scratch 
                                hipStream_t st);
 hipError_t launch_down_exact(const Shape &s, const LayerDev &L, const Scratch &S, float *out, int T, int quant,
                              hipStream_t st);
+/* The whole layer in the reference's --exact mode (fp32 dequantised rows, fp32 activations). */
+hipError_t launch_layer_fp32(const Shape &s, const LayerDev &L, const Scratch &S, const float *xn, float *out, int T,
+                             hipStream_t st);
 hipError_t launch_synth_f32(uint64_t key, uint64_t n, float sigma, float *out, hipStream_t st);
 hipError_t launch_synth_experts(uint64_t seed, uint32_t layer, uint32_t kind, int type, int64_t rows,
                                 int64_t cols, int X, float sigma, uint8_t *base, hipStream_t st);

@@ -2119,6 +2119,170 @@ hipError_t launch_dense(const DenseArgs &args, int type, uint8_t *xqk, hipStream
     return hipGetLastError();
 }
 
+/* ------------------------------------------------------------------ fp32 mode (--exact) ---- */
+
+/* The reference's --exact mode (qms_exact_math = 1): every product is matmul_exact
+ * (src/quant.c:97-115), a row dequantised to fp32 (qms_dequant_row, src/quant.c:17-93) against
+ * fp32 inputs in one FMA chain in element order; the activations stay fp32. */
+
+/* Router logits: one lane per expert, token blockIdx.y; the token's row is staged in LDS. */
+__global__ __launch_bounds__(64) void route_exact_kernel(const float *router, const float *xn, int E, int X,
+                                                         float *logits)
+{
+    extern __shared__ __align__(16) uint8_t smem[];
+    float *xr = (float *)smem;
+    const int t = blockIdx.y, e = blockIdx.x * 64 + threadIdx.x;
+    for (int i = threadIdx.x; i < E / 4; i += 64) ((float4 *)xr)[i] = ((const float4 *)(xn + (size_t)t * E))[i];
+    __syncthreads();
+    if (e >= X) return;
+    const float4 *w = (const float4 *)(router + (size_t)e * E);
+    float acc = 0.0f;
+    for (int c = 0; c < E / 4; c++) {
+        const float4 v = w[c];
+        acc = __builtin_fmaf(v.x, xr[4 * c], acc);
+        acc = __builtin_fmaf(v.y, xr[4 * c + 1], acc);
+        acc = __builtin_fmaf(v.z, xr[4 * c + 2], acc);
+        acc = __builtin_fmaf(v.w, xr[4 * c + 3], acc);
+    }
+    logits[(size_t)t * X + e] = acc;
+}
+
+/* Dequantised 32-block b of a row (src/quant.c:17-79): Q4_0 (q-8)*d, Q4_1 q*d+m (fused like
+ * the reference build), Q6_K (d*sc)*q. */
+__device__ __forceinline__ void dequant_block(int type, const uint8_t *row, int b, float *w)
+{
+    if (type == 14) {
+        const uint8_t *sb = row + (size_t)(b >> 3) * 210;
+        const int h = (b & 7) >> 2, g = b & 3;
+        const float d = h2f((uint32_t)sb[208] | ((uint32_t)sb[209] << 8));
+        const float d0 = d * (float)(int8_t)sb[192 + 8 * h + 2 * g];
+        const float d1 = d * (float)(int8_t)sb[192 + 8 * h + 2 * g + 1];
+#pragma unroll
+        for (int l = 0; l < 32; l++) {
+            const int lo = sb[64 * h + 32 * (g & 1) + l];
+            const int q = ((g < 2 ? lo & 15 : lo >> 4) | (((sb[128 + 32 * h + l] >> (2 * g)) & 3) << 4)) - 32;
+            w[l] = (l < 16 ? d0 : d1) * (float)q;
+        }
+    } else if (type == 3) {
+        const uint8_t *bp = row + (size_t)b * 20;
+        const float d = h2f((uint32_t)bp[0] | ((uint32_t)bp[1] << 8)), m = h2f((uint32_t)bp[2] | ((uint32_t)bp[3] << 8));
+#pragma unroll
+        for (int j = 0; j < 16; j++) {
+            w[j] = __builtin_fmaf((float)(bp[4 + j] & 15), d, m);
+            w[j + 16] = __builtin_fmaf((float)(bp[4 + j] >> 4), d, m);
+        }
+    } else {
+        const uint8_t *bp = row + (size_t)b * 18;
+        const float d = h2f((uint32_t)bp[0] | ((uint32_t)bp[1] << 8));
+#pragma unroll
+        for (int j = 0; j < 16; j++) {
+            w[j] = (float)((int)(bp[2 + j] & 15) - 8) * d;
+            w[j + 16] = (float)((int)(bp[2 + j] >> 4) - 8) * d;
+        }
+    }
+}
+
+/* y = matmul_exact rows of each active expert's matrix for its slots: one lane per row
+ * (64 rows per block, blockIdx.y = active expert), up to 4 slots per pass with their input
+ * rows staged in LDS. Inputs: the slot's token row of xn (by_token) or its own row of x. */
+struct ExactArgs {
+    const uint8_t *w;
+    uint64_t rb, eb;
+    int type, rows, cols, by_token;
+    const float *x;
+    float *y;
+    int y_stride, y_off;
+    Scratch S;
+};
+
+__global__ __launch_bounds__(64) void exact_rows_kernel(ExactArgs a)
+{
+    extern __shared__ __align__(16) uint8_t smem[];
+    constexpr int NT = 4;
+    if ((int)blockIdx.y >= a.S.meta[0]) return;
+    const int4 wk = a.S.work[blockIdx.y];
+    const int e = wk.x, lane = threadIdx.x, r = blockIdx.x * 64 + lane, C = a.cols;
+    float *xr = (float *)smem;                                      /* [NT][C] */
+    const uint8_t *row = a.w + (size_t)e * a.eb + (size_t)min(r, a.rows - 1) * a.rb;
+    for (int s0 = wk.y; s0 < wk.z; s0 += NT) {
+        const int nt = min(NT, wk.z - s0);
+        __syncthreads();
+        for (int i = lane; i < nt * (C / 4); i += 64) {
+            const int n = i / (C / 4), j = i - n * (C / 4);
+            const size_t src = a.by_token ? (size_t)a.S.slot_t[s0 + n] : (size_t)(s0 + n);
+            ((float4 *)xr)[i] = ((const float4 *)(a.x + src * C))[j];
+        }
+        __syncthreads();
+        float acc[NT] = { 0.0f, 0.0f, 0.0f, 0.0f };
+        for (int b = 0; b < C / 32; b++) {
+            float w[32];
+            dequant_block(a.type, row, b, w);
+#pragma unroll
+            for (int n = 0; n < NT; n++)
+                if (n < nt)
+#pragma unroll
+                    for (int j = 0; j < 32; j++) acc[n] = __builtin_fmaf(w[j], xr[n * C + 32 * b + j], acc[n]);
+        }
+        if (r < a.rows)
+            for (int n = 0; n < nt; n++) a.y[(size_t)(s0 + n) * a.y_stride + a.y_off + r] = acc[n];
+    }
+}
+
+/* a = silu(g) * u per slot (src/model.c:1024-1025), fp32. */
+__global__ void swiglu_kernel(Scratch S, int F, int NS)
+{
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= NS * F) return;
+    const int s = i / F, j = i - s * F;
+    S.act[i] = silu_ref(S.gu[(size_t)s * 2 * F + j]) * S.gu[(size_t)s * 2 * F + F + j];
+}
+
+hipError_t launch_layer_fp32(const Shape &s, const LayerDev &L, const Scratch &S, const float *xn, float *out, int T,
+                             hipStream_t st)
+{
+    SelectArgs sa;
+    sa.X = s.X;
+    sa.K = s.K;
+    sa.T = T;
+    sa.S = S;
+    QLAUNCH("route", route_exact_kernel, dim3((s.X + 63) / 64, T), dim3(64), (size_t)s.E * 4, st, L.router, xn, s.E,
+            s.X, S.logits);
+    QLAUNCH("select", select_kernel, dim3(T), dim3(256), 0, st, sa, 0);
+    QLAUNCH("dispatch", dispatch_kernel, dim3(1), dim3(64), 0, st, sa);
+    const int maxact = s.X < T * s.K ? s.X : T * s.K;
+    ExactArgs a;
+    a.S = S;
+    const struct { const uint8_t *w; uint64_t rb, eb; int type, rows, cols, by_token; const float *x; float *y;
+                   int stride, off; } m[3] = {
+        { L.gate, L.gate_rb, L.gate_eb, L.gate_type, s.F, s.E, 1, xn, S.gu, 2 * s.F, 0 },
+        { L.up, L.up_rb, L.up_eb, L.up_type, s.F, s.E, 1, xn, S.gu, 2 * s.F, s.F },
+        { L.down, L.down_rb, L.down_eb, L.down_type, s.E, s.F, 0, S.act, S.dn, s.E, 0 },
+    };
+    for (int i = 0; i < 3; i++) {
+        a.w = m[i].w;
+        a.rb = m[i].rb;
+        a.eb = m[i].eb;
+        a.type = m[i].type;
+        a.rows = m[i].rows;
+        a.cols = m[i].cols;
+        a.by_token = m[i].by_token;
+        a.x = m[i].x;
+        a.y = m[i].y;
+        a.y_stride = m[i].stride;
+        a.y_off = m[i].off;
+        const size_t lds = (size_t)4 * m[i].cols * 4;
+        if (lds > 160 * 1024) return hipErrorInvalidValue;
+        if (i == 2) {
+            const int n = T * s.K * s.F;
+            QLAUNCH("swiglu", swiglu_kernel, dim3((n + 255) / 256), dim3(256), 0, st, S, s.F, T * s.K);
+        }
+        QLAUNCH(i == 2 ? "down" : "gateup", exact_rows_kernel, dim3((m[i].rows + 63) / 64, maxact), dim3(64), lds, st, a);
+    }
+    const int n = T * s.E;
+    QLAUNCH("combine", combine_kernel, dim3((n + 255) / 256), dim3(256), 0, st, S, s.E, s.K, T, out);
+    return hipGetLastError();
+}
+
 /* ------------------------------------------------------------------ block dots (checks) ---- */
 
 /* Exact signed int32 dot of one 32-block of a weight row with one Q8 block, formed with the

@@ -17,12 +17,12 @@ from typing import Optional
 import numpy as np
 
 __all__ = [
-    "QMSG_T_F32", "QMSG_T_Q4_0", "QMSG_T_Q4_1", "QMSG_T_Q6_K", "PATH_AUTO", "PATH_EXACT", "PATH_MFMA",
+    "QMSG_T_F32", "QMSG_T_Q4_0", "QMSG_T_Q4_1", "QMSG_T_Q6_K", "PATH_AUTO", "PATH_EXACT", "PATH_MFMA", "PATH_FP32",
     "Q8_DTYPE", "QmsgError", "Context", "Gguf", "row_bytes", "lib", "library_path",
 ]
 
 QMSG_T_F32, QMSG_T_F16, QMSG_T_Q4_0, QMSG_T_Q4_1, QMSG_T_Q8_0, QMSG_T_Q6_K = 0, 1, 2, 3, 8, 14
-PATH_AUTO, PATH_EXACT, PATH_MFMA = 0, 1, 2
+PATH_AUTO, PATH_EXACT, PATH_MFMA, PATH_FP32 = 0, 1, 2, 3
 
 #: QmsQ8 (src/kernels.h:7-12): one int8 activation block of 32 values, 44 bytes.
 Q8_DTYPE = np.dtype([("d", "<f4"), ("ds", "<f4"), ("s16", "<i2", (2,)), ("q", "i1", (32,))])

@@ -58,6 +58,10 @@ def _load_oracle():
     L.orc_route.argtypes = [ctypes.c_int] * 3 + [_P, _P, ctypes.c_int, _P, _P, _P]
     L.orc_moe.argtypes = [ctypes.c_int] * 4 + [ctypes.POINTER(OrcMat)] * 4 + [_P, ctypes.c_int, _P,
                                                                              ctypes.POINTER(OrcDbg)]
+    L.orc_moe_exact.argtypes = L.orc_moe.argtypes
+    L.orc_route_exact.argtypes = L.orc_route.argtypes
+    L.orc_matmul_exact.argtypes = [ctypes.c_int, _P, ctypes.c_int64, ctypes.c_int64, ctypes.c_uint64, _P,
+                                   ctypes.c_int, _P]
     L.orc_synth_f32.argtypes = [ctypes.c_uint64, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint64,
                                 ctypes.c_float, _P]
     L.orc_synth_experts.argtypes = [ctypes.c_uint64, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_int, ctypes.c_int64,
@@ -179,20 +183,22 @@ class Layer:
         d = OrcMat(self.types[2], E, F, self.rb[2], self.eb[2], self.down.ctypes.data)
         return r, g, u, d
 
-    def route(self, xn: np.ndarray):
+    def route(self, xn: np.ndarray, exact: bool = False):
         xn = np.ascontiguousarray(xn, np.float32)
         T = xn.shape[0]
         logits = np.empty((T, self.X), np.float32)
         sel = np.empty((T, self.K), np.int32)
         wt = np.empty((T, self.K), np.float32)
-        lib.orc_route(self.E, self.X, self.K, _ptr(self.router), _ptr(xn), T, _ptr(logits), _ptr(sel), _ptr(wt))
+        fn = lib.orc_route_exact if exact else lib.orc_route
+        fn(self.E, self.X, self.K, _ptr(self.router), _ptr(xn), T, _ptr(logits), _ptr(sel), _ptr(wt))
         return logits, sel, wt
 
-    def moe(self, xn: np.ndarray, debug: bool = False):
-        """The oracle layer; returns out, or (out, intermediates) with debug=True."""
+    def moe(self, xn: np.ndarray, debug: bool = False, exact: bool = False):
+        """The oracle layer; returns out, or (out, intermediates) with debug=True. exact: the
+        reference's --exact mode (fp32 dequantised rows, no int8)."""
         xn = np.ascontiguousarray(xn, np.float32)
         T = xn.shape[0]
-        _, sel, _ = self.route(xn)
+        _, sel, _ = self.route(xn, exact)
         self.ensure(np.unique(sel))
         E, X, K, F = self.E, self.X, self.K, self.F
         NS = T * K
@@ -209,8 +215,9 @@ class Layer:
                  "dn": np.empty((NS, E), np.float32)}
             dbg = OrcDbg(**{k: v.ctypes.data for k, v in d.items()})
         r, g, u, dm = self.mats()
-        rc = lib.orc_moe(E, X, K, F, ctypes.byref(r), ctypes.byref(g), ctypes.byref(u), ctypes.byref(dm), _ptr(xn), T,
-                         _ptr(out), ctypes.byref(dbg) if dbg is not None else None)
+        fn = lib.orc_moe_exact if exact else lib.orc_moe
+        rc = fn(E, X, K, F, ctypes.byref(r), ctypes.byref(g), ctypes.byref(u), ctypes.byref(dm), _ptr(xn), T,
+                _ptr(out), ctypes.byref(dbg) if dbg is not None else None)
         if rc != 0:
             raise RuntimeError(f"orc_moe failed ({rc})")
         if debug:
@@ -277,12 +284,18 @@ def load_ref():
     return R
 
 
-def ref_moe(R, layer: Layer, xn: np.ndarray) -> np.ndarray:
+def ref_moe(R, layer: Layer, xn: np.ndarray, exact: bool = False) -> np.ndarray:
+    """The reference's own moe() on the layer; exact sets its qms_exact_math (--exact) for the call."""
     xn = np.ascontiguousarray(xn, np.float32)
     T = xn.shape[0]
     out = np.empty((T, layer.E), np.float32)
-    rc = R.qref_moe(layer.E, layer.X, layer.K, layer.F, _ptr(layer.router), layer.types[0], _ptr(layer.gate),
-                    layer.types[1], _ptr(layer.up), layer.types[2], _ptr(layer.down), _ptr(xn), T, _ptr(out))
+    flag = ctypes.c_int.in_dll(R, "qms_exact_math")
+    flag.value = 1 if exact else 0
+    try:
+        rc = R.qref_moe(layer.E, layer.X, layer.K, layer.F, _ptr(layer.router), layer.types[0], _ptr(layer.gate),
+                        layer.types[1], _ptr(layer.up), layer.types[2], _ptr(layer.down), _ptr(xn), T, _ptr(out))
+    finally:
+        flag.value = 0
     if rc != 0:
         raise RuntimeError(f"reference moe() returned {rc}")
     return out

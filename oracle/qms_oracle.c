@@ -287,13 +287,10 @@ static inline const uint8_t *expert_row(const orc_mat *m, int e, int64_t r)
  * src/quant.c:128-170 -> dot_f32), then per token a double softmax, top-K by repeated argmax
  * with ties to the lower index, and weights renormalised over the selection
  * (src/model.c:1045-1064). */
-void orc_route(int E, int X, int K, const float *router, const float *xn, int T, float *logits, int *selv,
-               float *wtv)
+/* src/model.c:1045-1064 on given logits: softmax in double, top K (ties to the lower index),
+ * weights renormalised in selection order. */
+static void topk_all(int X, int K, const float *logits, int T, int *selv, float *wtv)
 {
-#pragma omp parallel for schedule(static) if ((int64_t)X * E * T >= (1 << 21))
-    for (int r = 0; r < X; r++)
-        for (int t = 0; t < T; t++)
-            logits[(size_t)t * X + r] = orc_vec_dot_f32(router + (size_t)r * E, xn + (size_t)t * E, E);
     double *prob = (double *)malloc((size_t)X * sizeof(double));
     for (int t = 0; t < T; t++) {
         const float *lt = logits + (size_t)t * X;
@@ -320,24 +317,86 @@ void orc_route(int E, int X, int K, const float *router, const float *xn, int T,
     free(prob);
 }
 
-/* src/model.c:1032-1167 with moe_group_fast (969-1007) for resident experts (one group). */
-int orc_moe(int E, int X, int K, int F, const orc_mat *router, const orc_mat *gate, const orc_mat *up,
-            const orc_mat *down, const float *xn, int T, float *out, orc_moe_dbg *dbg)
+void orc_route(int E, int X, int K, const float *router, const float *xn, int T, float *logits, int *selv,
+               float *wtv)
+{
+#pragma omp parallel for schedule(static) if ((int64_t)X * E * T >= (1 << 21))
+    for (int r = 0; r < X; r++)
+        for (int t = 0; t < T; t++)
+            logits[(size_t)t * X + r] = orc_vec_dot_f32(router + (size_t)r * E, xn + (size_t)t * E, E);
+    topk_all(X, K, logits, T, selv, wtv);
+}
+
+static float dot_exact(const float *row, const float *x, int64_t n);
+
+/* Routing of the reference's --exact mode: logits by matmul_exact on the F32 router. */
+void orc_route_exact(int E, int X, int K, const float *router, const float *xn, int T, float *logits, int *selv,
+                     float *wtv)
+{
+#pragma omp parallel for schedule(static) if ((int64_t)X * E * T >= (1 << 21))
+    for (int r = 0; r < X; r++)
+        for (int t = 0; t < T; t++)
+            logits[(size_t)t * X + r] = dot_exact(router + (size_t)r * E, xn + (size_t)t * E, E);
+    topk_all(X, K, logits, T, selv, wtv);
+}
+
+/* matmul_exact's dot (src/quant.c:97-115): a dequantised row against fp32 x, one FMA chain
+ * in element order (the reference build contracts acc += row*x). */
+static float dot_exact(const float *row, const float *x, int64_t n)
+{
+    float acc = 0.0f;
+    for (int64_t c = 0; c < n; c++) acc = fmaf(row[c], x[c], acc);
+    return acc;
+}
+
+/* qms_matmul with qms_exact_math set (src/quant.c:97-115, 128-139): every row dequantised to
+ * fp32 (qms_dequant_row), y[t][r] = dot_exact(row r, x_t). */
+int orc_matmul_exact(int type, const uint8_t *w, int64_t rows, int64_t cols, uint64_t row_bytes, const float *x,
+                     int T, float *y)
+{
+    if (!orc_row_bytes(type, cols)) return -1;
+    int bad = 0;
+#pragma omp parallel
+    {
+        float *row = (float *)malloc((size_t)cols * sizeof(float));
+#pragma omp for schedule(static)
+        for (int64_t r = 0; r < rows; r++) {
+            if (orc_dequant_row(type, w + (uint64_t)r * row_bytes, row, cols) != 0) { bad = 1; continue; }
+            for (int t = 0; t < T; t++) y[(size_t)t * rows + r] = dot_exact(row, x + (size_t)t * cols, cols);
+        }
+        free(row);
+    }
+    return bad ? -1 : 0;
+}
+
+/* src/model.c:1032-1167 for resident experts (one group): with exact = 0 the integer path,
+ * moe_group_fast (969-1007); with exact = 1 the reference's --exact mode (qms_exact_math),
+ * where the router and moe_group_exact (1010-1030) use matmul_exact and the activations stay
+ * fp32. */
+static int moe_common(int exact, int E, int X, int K, int F, const orc_mat *router, const orc_mat *gate,
+                      const orc_mat *up, const orc_mat *down, const float *xn, int T, float *out, orc_moe_dbg *dbg)
 {
     if (T < 0 || K <= 0 || K > X) return -1;
     if (router->type != ORC_T_F32 || router->cols != E || router->rows != X) return -1;
-    /* model.c:1090-1093: the integer path needs these; the reference otherwise falls back to
-     * its fp32 dequantising path, which the device library does not implement either. */
-    const int fast = orc_fast_supported(gate->type) && orc_fast_supported(up->type) &&
-                     orc_fast_supported(down->type) && gate->type != ORC_T_F32 &&
-                     up->type != ORC_T_F32 && down->type != ORC_T_F32 && E % 256 == 0 && F % 32 == 0;
-    if (!fast) return -1;
+    if (exact) {
+        if (!orc_row_bytes(gate->type, E) || !orc_row_bytes(up->type, E) || !orc_row_bytes(down->type, F)) return -1;
+    } else {
+        /* model.c:1090-1093: the integer path needs these */
+        const int fast = orc_fast_supported(gate->type) && orc_fast_supported(up->type) &&
+                         orc_fast_supported(down->type) && gate->type != ORC_T_F32 &&
+                         up->type != ORC_T_F32 && down->type != ORC_T_F32 && E % 256 == 0 && F % 32 == 0;
+        if (!fast) return -1;
+    }
     if (T == 0) return 0;
     const int NS = T * K, nbE = E / 32, nbF = F / 32;
     float *logits = (float *)malloc((size_t)T * X * sizeof(float));
     int *selv = (int *)malloc((size_t)NS * sizeof(int));
     float *wtv = (float *)malloc((size_t)NS * sizeof(float));
-    orc_route(E, X, K, (const float *)router->data, xn, T, logits, selv, wtv);
+    if (exact) {
+        orc_route_exact(E, X, K, (const float *)router->data, xn, T, logits, selv, wtv);
+    } else {
+        orc_route(E, X, K, (const float *)router->data, xn, T, logits, selv, wtv);
+    }
 
     /* counting sort of slots by expert: model.c:1066-1088 */
     int *start = (int *)calloc((size_t)X + 1, sizeof(int));
@@ -361,13 +420,46 @@ int orc_moe(int E, int X, int K, int F, const orc_mat *router, const orc_mat *ga
     free(cnt);
 
     /* model.c:1096-1097 */
-    orc_q8 *xq = (orc_q8 *)malloc((size_t)T * nbE * sizeof(orc_q8));
-    for (int t = 0; t < T; t++) orc_quantize_q8(xn + (size_t)t * E, E, xq + (size_t)t * nbE);
+    orc_q8 *xq = (orc_q8 *)calloc((size_t)T * nbE, sizeof(orc_q8));
+    if (!exact)
+        for (int t = 0; t < T; t++) orc_quantize_q8(xn + (size_t)t * E, E, xq + (size_t)t * nbE);
     float *gu = (float *)malloc((size_t)NS * 2 * F * sizeof(float));
     float *act = (float *)malloc((size_t)NS * F * sizeof(float));
-    orc_q8 *aq = (orc_q8 *)malloc((size_t)NS * nbF * sizeof(orc_q8));
+    orc_q8 *aq = (orc_q8 *)calloc((size_t)NS * nbF, sizeof(orc_q8));
     float *dn = (float *)malloc((size_t)NS * E * sizeof(float));
 
+    if (exact) {
+        /* moe_group_exact, model.c:1010-1030: per slot g, u by matmul_exact, a = silu(g)*u,
+         * dn = matmul_exact(down, a) */
+#pragma omp parallel
+        {
+            float *row = (float *)malloc((size_t)(E > F ? E : F) * sizeof(float));
+#pragma omp for schedule(static)
+            for (int64_t it = 0; it < (int64_t)na * 2 * F; it++) {
+                const int e = active[it / (2 * F)];
+                const int r = (int)(it % (2 * F));
+                const orc_mat *W = r < F ? gate : up;
+                orc_dequant_row(W->type, expert_row(W, e, r < F ? r : r - F), row, E);
+                for (int s = start[e]; s < start[e + 1]; s++)
+                    gu[(size_t)s * 2 * F + r] = dot_exact(row, xn + (size_t)slot_t[s] * E, E);
+            }
+#pragma omp for schedule(static)
+            for (int s = 0; s < NS; s++) {
+                const float *g = gu + (size_t)s * 2 * F;
+                float *a = act + (size_t)s * F;
+                for (int j = 0; j < F; j++) a[j] = orc_silu(g[j]) * g[F + j];
+            }
+#pragma omp for schedule(static)
+            for (int64_t it = 0; it < (int64_t)na * E; it++) {
+                const int e = active[it / E];
+                const int r = (int)(it % E);
+                orc_dequant_row(down->type, expert_row(down, e, r), row, F);
+                for (int s = start[e]; s < start[e + 1]; s++)
+                    dn[(size_t)s * E + r] = dot_exact(row, act + (size_t)s * F, F);
+            }
+            free(row);
+        }
+    } else {
     /* moe_group_fast, model.c:979-1005 */
 #pragma omp parallel
     {
@@ -395,6 +487,7 @@ int orc_moe(int E, int X, int K, int F, const orc_mat *router, const orc_mat *ga
             for (int s = start[e]; s < start[e + 1]; s++)
                 dn[(size_t)s * E + r] = orc_vec_dot_q8(down->type, row, aq + (size_t)s * nbF, F);
         }
+    }
     }
 
     /* weighted sum per token in selection order: model.c:1152-1162 */
@@ -428,6 +521,18 @@ int orc_moe(int E, int X, int K, int F, const orc_mat *router, const orc_mat *ga
     free(xq); free(gu); free(act); free(aq); free(dn);
     free(logits); free(selv); free(wtv);
     return 0;
+}
+
+int orc_moe(int E, int X, int K, int F, const orc_mat *router, const orc_mat *gate, const orc_mat *up,
+            const orc_mat *down, const float *xn, int T, float *out, orc_moe_dbg *dbg)
+{
+    return moe_common(0, E, X, K, F, router, gate, up, down, xn, T, out, dbg);
+}
+
+int orc_moe_exact(int E, int X, int K, int F, const orc_mat *router, const orc_mat *gate, const orc_mat *up,
+                  const orc_mat *down, const float *xn, int T, float *out, orc_moe_dbg *dbg)
+{
+    return moe_common(1, E, X, K, F, router, gate, up, down, xn, T, out, dbg);
 }
 
 /* The fast path of qms_matmul_n for one quantised matrix (src/quant.c:128-170): each row of

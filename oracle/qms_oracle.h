@@ -87,6 +87,13 @@ void orc_route(int E, int X, int K, const float *router, const float *xn, int T,
  * shapes or types are outside the reference's integer fast path. */
 int orc_moe(int E, int X, int K, int F, const orc_mat *router, const orc_mat *gate, const orc_mat *up,
             const orc_mat *down, const float *xn, int T, float *out, orc_moe_dbg *dbg);
+/* The reference's --exact mode (qms_exact_math): matmul_exact everywhere, fp32 activations. */
+void orc_route_exact(int E, int X, int K, const float *router, const float *xn, int T, float *logits, int *selv,
+                     float *wtv);
+int orc_moe_exact(int E, int X, int K, int F, const orc_mat *router, const orc_mat *gate, const orc_mat *up,
+                  const orc_mat *down, const float *xn, int T, float *out, orc_moe_dbg *dbg);
+int orc_matmul_exact(int type, const uint8_t *w, int64_t rows, int64_t cols, uint64_t row_bytes, const float *x,
+                     int T, float *y);
 
 /* Host copies of the synthetic generator (same source as the device kernels). */
 void orc_synth_f32(uint64_t seed, uint32_t layer, uint32_t kind, uint32_t expert, uint64_t n, float sigma,

@@ -186,6 +186,10 @@ LAYERS = {
     # the widest Qwen3-MoE shape (Qwen3-Coder-480B-A35B: n_embd 6144, 160 experts, n_ff_exp 2560)
     "q480b_t1": (6144, 160, 8, 2560, 1, 12, orc.T_Q4_0, True, None),
     "q480b_t2": (6144, 160, 8, 2560, 2, 13, orc.T_Q4_0, False, None),
+    # the reference's --exact mode (qms_exact_math = 1): fp32 dequantised rows, no int8
+    "tiny_exact_t3": (256, 16, 4, 128, 3, 30, orc.T_Q4_0, False, "exact"),
+    "q30b_exact_t2": (2048, 128, 8, 768, 2, 31, orc.T_Q4_1, True, "exact"),
+    "q235b_q6k_exact_t1": (4096, 128, 8, 1536, 1, 32, orc.T_Q6_K, False, "exact"),
 }
 
 
@@ -203,12 +207,16 @@ def layer_case(R, name, E, X, K, F, T, seed, dt, rms, special):
         x[1] = 0.0                         # all logits 0: experts 0..K-1, equal weights
     elif special == "large":
         x *= 300.0
-    logits, sel, wt = L.route(x)
+    exact = special == "exact"
+    logits, sel, wt = L.route(x, exact)
     L.ensure(np.unique(sel))
-    out = orc.ref_moe(R, L, x)
+    out = orc.ref_moe(R, L, x, exact=exact)
     qm = QmsMat(orc.T_F32, X, E, 4 * E, L.router.ctypes.data)
     ref_logits = np.empty((T, X), np.float32)
+    flag = ctypes.c_int.in_dll(R, "qms_exact_math")
+    flag.value = int(exact)
     R.qms_matmul(ctypes.byref(qm), ptr(x), T, ptr(ref_logits))
+    flag.value = 0
     xq = np.empty((T, E // 32), orc.Q8_DTYPE)
     for t in range(T):
         R.qms_quantize_q8(ptr(x[t]), E, ptr(xq[t]))

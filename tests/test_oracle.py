@@ -217,13 +217,14 @@ def check_layer(d, L, x, logits=True):
     """Raise AssertionError unless the oracle reproduces the reference's vectors."""
     assert sha(L.router) == bytes(d["router_sha"]), "router generator"
     assert sha(x) == bytes(d["x_sha"]), "input generator"
-    lg, sel, wt = L.route(x)
+    exact = str(d["special"]) == "exact"
+    lg, sel, wt = L.route(x, exact)
     if logits:
         assert sha(lg) == bytes(d["logits_sha"]), "router logits"
     xq = orc.quantize_q8(x).reshape(x.shape[0], -1)
     assert sha(xq) == bytes(d["xq_sha"]), "int8 input blocks"
     assert np.array_equal(np.unique(sel), d["experts"]), "expert ids"
-    out = L.moe(x)
+    out = L.moe(x, exact=exact)
     eb = L.eb
     assert sha(*[np.concatenate([L.gate[e * eb[0]:(e + 1) * eb[0]], L.up[e * eb[1]:(e + 1) * eb[1]],
                                  L.down[e * eb[2]:(e + 1) * eb[2]]]) for e in d["experts"]]) == bytes(d["experts_sha"]), \
