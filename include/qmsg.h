@@ -84,8 +84,9 @@ typedef struct qmsg_ctx qmsg_ctx;
  *          model.c:1009-1030): router, gate/up and down rows dequantised to fp32 and dotted in
  *          one FMA chain per row (matmul_exact), fp32 activations, no int8 blocks; bit-identical
  *          to the reference run with --exact. Takes Q4_0, Q4_1 or Q6_K for every expert tensor.
- * The integer paths (AUTO, EXACT, MFMA) take Q4_0 gate/up; a layer with other gate/up types
- * runs only with FP32. */
+ * Every path takes Q4_0, Q4_1 or Q6_K in each expert tensor (src/kernels.c:197-200). On the
+ * integer paths a layer whose gate or up is not Q4_0 runs its gate/up rows on the exact
+ * slot-tile kernel, also under MFMA. */
 enum { QMSG_PATH_AUTO = 0, QMSG_PATH_EXACT = 1, QMSG_PATH_MFMA = 2, QMSG_PATH_FP32 = 3 };
 
 /* ------------------------------------------------------------------ lifecycle ---- */

@@ -717,16 +717,18 @@ static int run_layer(qmsg_ctx *c, int layer, const float *d_xn, int T, float *d_
         LAUNCH(c, "layer", launch_layer_fp32(s, d, c->S, d_xn, d_out, T, c->stream));
         return QMSG_OK;
     }
-    if (d.gate_type != QMSG_T_Q4_0 || d.up_type != QMSG_T_Q4_0)
-        return fail(c, QMSG_E_UNSUPPORTED, "layer %d: the integer gate/up kernels take Q4_0 (types %d, %d); "
-                    "QMSG_PATH_FP32 takes any", layer, d.gate_type, d.up_type);
-    /* the MFMA grouped GEMM takes Q4_0 gate/up weights and batches routed by the select kernel */
-    const bool mfma = c->path == QMSG_PATH_MFMA && d.gate_type == QMSG_T_Q4_0 && d.up_type == QMSG_T_Q4_0 &&
-                      !use_small_route(T, s.K) && s.E % 256 == 0 && s.F % 256 == 0;
+    /* Q4_0 gate and up take the streaming gate/up kernel (which also routes one-token batches)
+     * or the MFMA grouped GEMM; other types take the slot-tile row kernel */
+    const bool q40 = d.gate_type == QMSG_T_Q4_0 && d.up_type == QMSG_T_Q4_0;
+    const bool mfma = c->path == QMSG_PATH_MFMA && q40 && !use_small_route(T, s.K) && s.E % 256 == 0 &&
+                      s.F % 256 == 0;
     LAUNCH(c, "route", launch_route(s, d, c->S, d_xn, T, c->stream));
-    LAUNCH(c, "select", launch_select(s, c->S, T, c->stream));
+    LAUNCH(c, "select", launch_select(s, c->S, T, q40 ? 1 : 0, c->stream));
     if (mfma) {
         LAUNCH(c, "experts", launch_experts_mfma(s, d, c->S, d_out, T, debug, c->stream));
+    } else if (!q40) {
+        LAUNCH(c, "gateup", launch_gateup_tiles(s, d, c->S, T, c->stream));
+        LAUNCH(c, "down", launch_down_exact(s, d, c->S, d_out, T, 1, c->stream));
     } else {
         LAUNCH(c, "gateup", launch_gateup_exact(s, d, c->S, T, debug, c->n_cu, c->stream));
         LAUNCH(c, "down", launch_down_exact(s, d, c->S, d_out, T, 1, c->stream));

@@ -106,11 +106,14 @@ constexpr int kDenseQuantT = 8;
 /* Launchers (qmsg_kernels.hip). Each returns hipSuccess or the launch error. */
 hipError_t launch_route(const Shape &s, const LayerDev &L, const Scratch &S, const float *xn, int T,
                         hipStream_t st);
-hipError_t launch_select(const Shape &s, const Scratch &S, int T, hipStream_t st);
+/* Top-K and dispatch; a one-token batch is left to the Q4_0 gate/up kernel when gateup_routes. */
+hipError_t launch_select(const Shape &s, const Scratch &S, int T, int gateup_routes, hipStream_t st);
 hipError_t launch_gateup_exact(const Shape &s, const LayerDev &L, const Scratch &S, int T, int debug, int n_cu,
                                hipStream_t st);
 hipError_t launch_experts_mfma(const Shape &s, const LayerDev &L, const Scratch &S, float *out, int T, int debug,
                                hipStream_t st);
+/* Gate/up rows of Q4_1 / Q6_K (or mixed) layers by slot tiles, then the SwiGLU. */
+hipError_t launch_gateup_tiles(const Shape &s, const LayerDev &L, const Scratch &S, int T, hipStream_t st);
 hipError_t launch_down_exact(const Shape &s, const LayerDev &L, const Scratch &S, float *out, int T, int quant,
                              hipStream_t st);
 /* The whole layer in the reference's --exact mode (fp32 dequantised rows, fp32 activations). */

@@ -566,14 +566,14 @@ __global__ __launch_bounds__(64) void dispatch_kernel(SelectArgs a)
     dispatch_slots(a, cnt, cur, tok);
 }
 
-hipError_t launch_select(const Shape &s, const Scratch &S, int T, hipStream_t st)
+hipError_t launch_select(const Shape &s, const Scratch &S, int T, int gateup_routes, hipStream_t st)
 {
     SelectArgs a;
     a.X = s.X;
     a.K = s.K;
     a.T = T;
     a.S = S;
-    if (use_small_route(T, s.K)) return hipSuccess;   /* the gate/up kernel routes the batch */
+    if (gateup_routes && use_small_route(T, s.K)) return hipSuccess;   /* the gate/up kernel routes the batch */
     QLAUNCH("select", select_kernel, dim3(T), dim3(256), 0, st, a, T == 1 ? 1 : 0);
     if (T > 1) QLAUNCH("dispatch", dispatch_kernel, dim3(1), dim3(64), 0, st, a);
     return hipGetLastError();
@@ -1263,12 +1263,23 @@ struct DownArgs {
     Scratch S;
 };
 
-/* Down rows of one slot tile (at most kTileN slots of one expert, from the dispatch's tile
- * list): 64 output rows R0 .. R0+63 (one per lane quad), staged once in LDS, against the
- * tile's int8 activation records, NT slots per pass. Writes dn[slot][row]; the combine runs
- * afterwards in selection order. */
-template <int TYPE, int NT, int RT>
-__global__ __launch_bounds__(4 * RT) void down_tile_kernel(DownArgs a)
+/* Rows of one expert's matrix against the int8 input records of one slot tile (at most kTileN
+ * slots of one expert, from the dispatch's tile list): RT rows R0 .. R0+RT-1 (one per lane
+ * quad), staged once in LDS, NT slots per pass. The records are the slot's own (down: the
+ * activations) or, with BT, those of the slot's token (gate / up: the layer input). Writes
+ * y[slot * y_stride + y_off + row]; for down the combine runs afterwards in selection order. */
+struct TileArgs {
+    const uint8_t *w;       /* expert 0's rows of rb bytes; expert e at w + e*eb */
+    uint64_t rb, eb;
+    int cols;               /* elements per row (a multiple of 64; 256 for Q6_K) */
+    const uint8_t *rec;     /* pair records, cols/64 per slot (or per token with BT) */
+    float *y;
+    int y_stride, y_off;
+    Scratch S;
+};
+
+template <int TYPE, int NT, int RT, int BT>
+__global__ __launch_bounds__(4 * RT) void tile_rows_kernel(TileArgs a)
 {
     extern __shared__ __align__(16) uint8_t smem[];
     constexpr int NTH = 4 * RT;
@@ -1276,11 +1287,11 @@ __global__ __launch_bounds__(4 * RT) void down_tile_kernel(DownArgs a)
     const int4 tl = a.S.tiles[blockIdx.y];
     const int e = tl.x, s0 = tl.y, ns = tl.z - tl.y;
     const int tid = threadIdx.x, quad = tid >> 2, p = tid & 3;
-    const int R0 = (int)blockIdx.x * RT, E = a.E, nPF = a.F >> 6, xrec = nPF * kPairBytes;
+    const int R0 = (int)blockIdx.x * RT, nPF = a.cols >> 6, xrec = nPF * kPairBytes, x16 = xrec >> 4;
     const int rb = (int)a.rb, n16 = RT * rb / 16;
     uint8_t *tile = smem;
     uint8_t *xbuf = smem + ((RT * rb + 15) & ~15);            /* [NT][xrec] */
-    const u32x4 *wsrc = (const u32x4 *)(a.down + (size_t)e * a.eb + (size_t)R0 * a.rb);
+    const u32x4 *wsrc = (const u32x4 *)(a.w + (size_t)e * a.eb + (size_t)R0 * a.rb);
     for (int i0 = 0; i0 < n16; i0 += NTH * 8) {
         u32x4 v[8];
 #pragma unroll
@@ -1293,15 +1304,22 @@ __global__ __launch_bounds__(4 * RT) void down_tile_kernel(DownArgs a)
     for (int g0 = 0; g0 < ns; g0 += NT) {
         const int nt = min(NT, ns - g0);
         __syncthreads();                                  /* the weights landed; xbuf is free */
-        for (int i = tid; i < nt * (xrec >> 4); i += NTH)
-            ((u32x4 *)xbuf)[i] = ((const u32x4 *)(a.S.aqk + (size_t)(s0 + g0) * xrec))[i];
+        for (int i = tid; i < nt * x16; i += NTH) {
+            if (BT) {
+                const int n = i / x16;
+                const u32x4 *src = (const u32x4 *)(a.rec + (size_t)a.S.slot_t[s0 + g0 + n] * xrec);
+                ((u32x4 *)xbuf)[i] = src[i - n * x16];
+            } else {
+                ((u32x4 *)xbuf)[i] = ((const u32x4 *)(a.rec + (size_t)(s0 + g0) * xrec))[i];
+            }
+        }
         __syncthreads();
         RowAcc acc[NT];
         for (int n = 0; n < NT; n++) acc[n] = RowAcc{ 0.0f, 0.0f, 0.0f };
         if (TYPE == 2 || TYPE == 3) {
             q4_rows_nt<TYPE, NT>((const uint32_t *)row, p, xbuf, (size_t)xrec, 0, nPF, nt, acc);
         } else {
-            const int nsb = a.F >> 8;
+            const int nsb = a.cols >> 8;
             const uint32_t rowoff = (uint32_t)(row - tile);
             /* rows of a multiple of 4 bytes: even super-blocks start 4-aligned on every row */
             const bool even_al = (rb & 3) == 0;
@@ -1328,7 +1346,7 @@ __global__ __launch_bounds__(4 * RT) void down_tile_kernel(DownArgs a)
 #pragma unroll
         for (int n = 0; n < NT; n++) {
             const float d = quad_finish(acc[n], finish_scale(TYPE));
-            if (p == 0 && n < nt) a.S.dn[(size_t)(s0 + g0 + n) * E + R0 + quad] = d;
+            if (p == 0 && n < nt) a.y[(size_t)(s0 + g0 + n) * a.y_stride + a.y_off + R0 + quad] = d;
         }
     }
 }
@@ -1494,11 +1512,11 @@ __global__ void combine_kernel(const Scratch S, int E, int K, int T, float *out)
 }
 
 template <int TYPE, int RT>
-static void launch_down_tile(const DownArgs &a, int NT, dim3 grid, size_t lds, hipStream_t st)
+static void launch_down_tile(const TileArgs &a, int NT, dim3 grid, size_t lds, hipStream_t st)
 {
-    if (NT == 4) QLAUNCH("down", (down_tile_kernel<TYPE, 4, RT>), grid, dim3(4 * RT), lds, st, a);
-    else if (NT == 2) QLAUNCH("down", (down_tile_kernel<TYPE, 2, RT>), grid, dim3(4 * RT), lds, st, a);
-    else QLAUNCH("down", (down_tile_kernel<TYPE, 1, RT>), grid, dim3(4 * RT), lds, st, a);
+    if (NT == 4) QLAUNCH("down", (tile_rows_kernel<TYPE, 4, RT, 0>), grid, dim3(4 * RT), lds, st, a);
+    else if (NT == 2) QLAUNCH("down", (tile_rows_kernel<TYPE, 2, RT, 0>), grid, dim3(4 * RT), lds, st, a);
+    else QLAUNCH("down", (tile_rows_kernel<TYPE, 1, RT, 0>), grid, dim3(4 * RT), lds, st, a);
 }
 
 /* Rows per block of the Q6_K slot-tile kernel (its 210-byte super-blocks make a 64-row tile
@@ -1550,11 +1568,70 @@ hipError_t launch_down_exact(const Shape &s, const LayerDev &L, const Scratch &S
     const size_t lds = ((RT * L.down_rb + 15) & ~(size_t)15) + (size_t)NT * xrec;
     if (lds > 160 * 1024 || s.E % RT) return hipErrorInvalidValue;
     const dim3 grid(s.E / RT, maxt);
-    if (L.down_type == 2) launch_down_tile<2, 64>(a, NT, grid, lds, st);
-    else if (L.down_type == 3) launch_down_tile<3, 64>(a, NT, grid, lds, st);
-    else launch_down_tile<14, kDownTileRowsQ6K>(a, NT, grid, lds, st);
+    TileArgs ta;
+    ta.w = L.down;
+    ta.rb = L.down_rb;
+    ta.eb = L.down_eb;
+    ta.cols = s.F;
+    ta.rec = S.aqk;
+    ta.y = S.dn;
+    ta.y_stride = s.E;
+    ta.y_off = 0;
+    ta.S = S;
+    if (L.down_type == 2) launch_down_tile<2, 64>(ta, NT, grid, lds, st);
+    else if (L.down_type == 3) launch_down_tile<3, 64>(ta, NT, grid, lds, st);
+    else launch_down_tile<14, kDownTileRowsQ6K>(ta, NT, grid, lds, st);
     const int n = T * s.E;
     QLAUNCH("combine", combine_kernel, dim3((n + 255) / 256), dim3(256), 0, st, S, s.E, s.K, T, out);
+    return hipGetLastError();
+}
+
+/* a = silu(g) * u per slot (src/model.c:994; in --exact mode 1024), fp32. */
+__global__ void swiglu_kernel(Scratch S, int F, int NS)
+{
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= NS * F) return;
+    const int s = i / F, j = i - s * F;
+    S.act[i] = silu_ref(S.gu[(size_t)s * 2 * F + j]) * S.gu[(size_t)s * 2 * F + F + j];
+}
+
+/* Gate and up rows of any of Q4_0 / Q4_1 / Q6_K (the reference's fast path takes each,
+ * src/kernels.c:197-200; src/model.c:979-988) by slot tiles against the tokens' int8 input
+ * records, then a = silu(g) * u. Layers whose gate and up are both Q4_0 take gateup_kernel. */
+template <int TYPE, int RT>
+static void launch_gu_tile(const TileArgs &a, dim3 grid, size_t lds, hipStream_t st)
+{
+    QLAUNCH("gateup", (tile_rows_kernel<TYPE, 4, RT, 1>), grid, dim3(4 * RT), lds, st, a);
+}
+
+hipError_t launch_gateup_tiles(const Shape &s, const LayerDev &L, const Scratch &S, int T, hipStream_t st)
+{
+    const int NS = T * s.K, maxt = (s.X < NS ? s.X : NS) + NS / kTileN + 1;
+    const size_t xrec = (size_t)(s.E / 64) * kPairBytes;
+    for (int i = 0; i < 2; i++) {
+        TileArgs a;
+        a.w = i ? L.up : L.gate;
+        a.rb = i ? L.up_rb : L.gate_rb;
+        a.eb = i ? L.up_eb : L.gate_eb;
+        a.cols = s.E;
+        a.rec = S.xqk;
+        a.y = S.gu;
+        a.y_stride = 2 * s.F;
+        a.y_off = i ? s.F : 0;
+        a.S = S;
+        const int type = i ? L.up_type : L.gate_type;
+        /* 32 rows per block where they fit in LDS with four slots' records, else 16 */
+        int RT = 32;
+        if (((RT * a.rb + 15) & ~(uint64_t)15) + 4 * xrec > 160 * 1024) RT = 16;
+        const size_t lds = ((RT * a.rb + 15) & ~(size_t)15) + 4 * xrec;
+        if (lds > 160 * 1024 || s.F % RT) return hipErrorInvalidValue;
+        const dim3 grid(s.F / RT, maxt);
+        if (type == 2) RT == 32 ? launch_gu_tile<2, 32>(a, grid, lds, st) : launch_gu_tile<2, 16>(a, grid, lds, st);
+        else if (type == 3) RT == 32 ? launch_gu_tile<3, 32>(a, grid, lds, st) : launch_gu_tile<3, 16>(a, grid, lds, st);
+        else RT == 32 ? launch_gu_tile<14, 32>(a, grid, lds, st) : launch_gu_tile<14, 16>(a, grid, lds, st);
+    }
+    const int n = NS * s.F;
+    QLAUNCH("swiglu", swiglu_kernel, dim3((n + 255) / 256), dim3(256), 0, st, S, s.F, NS);
     return hipGetLastError();
 }
 
@@ -2226,15 +2303,6 @@ __global__ __launch_bounds__(64) void exact_rows_kernel(ExactArgs a)
         if (r < a.rows)
             for (int n = 0; n < nt; n++) a.y[(size_t)(s0 + n) * a.y_stride + a.y_off + r] = acc[n];
     }
-}
-
-/* a = silu(g) * u per slot (src/model.c:1024-1025), fp32. */
-__global__ void swiglu_kernel(Scratch S, int F, int NS)
-{
-    const int i = blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= NS * F) return;
-    const int s = i / F, j = i - s * F;
-    S.act[i] = silu_ref(S.gu[(size_t)s * 2 * F + j]) * S.gu[(size_t)s * 2 * F + F + j];
 }
 
 hipError_t launch_layer_fp32(const Shape &s, const LayerDev &L, const Scratch &S, const float *xn, float *out, int T,

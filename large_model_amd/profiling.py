@@ -22,7 +22,8 @@ import sys
 SHORT = (
     ("route_small_kernel", "route"), ("route_big_kernel", "route"), ("select_kernel", "select"),
     ("dispatch_kernel", "dispatch"), ("gateup_kernel", "gateup"), ("down_exact_kernel", "down"),
-    ("down_t1_kernel", "down"), ("down_tile_kernel", "down"), ("act_quant_kernel", "actq"),
+    ("down_t1_kernel", "down"), ("act_quant_kernel", "actq"), ("swiglu_kernel", "swiglu"),
+    ("route_exact_kernel", "route"), ("exact_rows_kernel", "rows_f32"),
     ("combine_kernel", "combine"), ("copy_kernel", "copy"), ("dense_kernel", "dense"),
     ("gateup_mfma_kernel", "gateup"), ("down_mfma_kernel", "down"), ("rmsnorm_kernel", "rmsnorm"),
     ("add_rows_kernel", "add"),
@@ -30,6 +31,8 @@ SHORT = (
 
 
 def short_name(kernel: str) -> str:
+    if "tile_rows_kernel" in kernel:       # last template argument: 1 = gate/up rows, 0 = down rows
+        return "gateup" if kernel.replace(" ", "").split(">")[0].endswith(",1") else "down"
     for key, name in SHORT:
         if key in kernel:
             return name

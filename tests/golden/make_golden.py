@@ -190,6 +190,16 @@ LAYERS = {
     "tiny_exact_t3": (256, 16, 4, 128, 3, 30, orc.T_Q4_0, False, "exact"),
     "q30b_exact_t2": (2048, 128, 8, 768, 2, 31, orc.T_Q4_1, True, "exact"),
     "q235b_q6k_exact_t1": (4096, 128, 8, 1536, 1, 32, orc.T_Q6_K, False, "exact"),
+    # gate/up other than Q4_0 on the integer path (qms_fast_supported takes any of the three)
+    "q30b_gq41_t1": (2048, 128, 8, 768, 1, 33, orc.T_Q4_0, True, None),
+    "q235b_gq6k_t4": (4096, 128, 8, 1536, 4, 34, orc.T_Q6_K, False, None),
+    "tiny_gq6k_uq41_t7": (256, 16, 4, 128, 7, 35, orc.T_Q4_1, False, None),
+}
+# gate and up types of the layers above that are not Q4_0 / Q4_0 (stored as "gu_types")
+GATE_UP = {
+    "q30b_gq41_t1": (orc.T_Q4_1, orc.T_Q4_1),
+    "q235b_gq6k_t4": (orc.T_Q6_K, orc.T_Q6_K),
+    "tiny_gq6k_uq41_t7": (orc.T_Q6_K, orc.T_Q4_1),
 }
 
 
@@ -198,7 +208,8 @@ def layer_case(R, name, E, X, K, F, T, seed, dt, rms, special):
     if special == "zipf":
         from large_model_amd.workloads import zipf_bias
         col0 = zipf_bias(X, K, T, E)
-    L = orc.Layer(E, X, K, F, seed, down_type=dt, experts=[], router_col0=col0)
+    gt, ut = GATE_UP.get(name, (orc.T_Q4_0, orc.T_Q4_0))
+    L = orc.Layer(E, X, K, F, seed, gate_type=gt, up_type=ut, down_type=dt, experts=[], router_col0=col0)
     x = orc.make_input(E, T, seed, rmsnorm=rms, bias_col0=special == "zipf")
     if special == "ties":
         L.router[5] = L.router[2]          # experts 2 and 5 tie on every token
@@ -237,6 +248,8 @@ def layer_case(R, name, E, X, K, F, T, seed, dt, rms, special):
     }
     if special == "zipf":
         d["router_col0"] = col0
+    if name in GATE_UP:
+        d["gu_types"] = np.array([gt, ut], np.int64)
     if out.size <= 16384:
         d["out"] = out
         d["logits"] = ref_logits

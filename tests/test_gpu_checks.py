@@ -37,7 +37,8 @@ def golden_input(d):
 
 
 DEVICE_GOLD = ["tiny_t1", "tiny_t7", "q30b_t1", "q235b_t1", "q235b_t4", "q235b_t16", "q235b_q6k_t64",
-               "q235b_zipf_t512", "q235b_q41_t1", "q235b_q41_t5", "q480b_t1", "q480b_t2"]
+               "q235b_zipf_t512", "q235b_q41_t1", "q235b_q41_t5", "q480b_t1", "q480b_t2",
+               "q30b_gq41_t1", "q235b_gq6k_t4", "tiny_gq6k_uq41_t7"]
 
 
 @pytest.mark.parametrize("name", DEVICE_GOLD)
@@ -48,9 +49,10 @@ def test_device_layer_equals_reference_output(q, name):
     print(f"[case] golden {name} T={T}", flush=True)
     x = golden_input(d)
     col0 = d.get("router_col0")
+    gt, ut = (int(v) for v in d.get("gu_types", (q.QMSG_T_Q4_0, q.QMSG_T_Q4_0)))
     with q.Context(E, X, K, F, n_layer=1, max_tokens=T) as ctx:
         ctx.set_path(q.PATH_EXACT)
-        ctx.synth(0, seed, down_type=dt, router_col0=col0)
+        ctx.synth(0, seed, gate_type=gt, up_type=ut, down_type=dt, router_col0=col0)
         out = ctx.moe(0, x)
     assert sha(out) == bytes(d["out_sha"])
 

@@ -1,7 +1,7 @@
 """The reference's --exact mode on the GPU (QMSG_PATH_FP32): fp32 dequantised rows in one FMA
 chain per row, fp32 activations. Output hashed against the reference's own moe() run with
 qms_exact_math = 1 (tests/golden/layer_*exact*.npz), and every intermediate against the
-oracle, including expert types the integer kernels do not take."""
+oracle, with Q4_0, Q4_1 and Q6_K in every tensor, and switching between the paths."""
 import hashlib
 import os
 
@@ -58,12 +58,12 @@ def test_fp32_path_intermediates(q, name, E, X, K, F, T, seed, gt, ut, dt):
     ref_out, ref = host.moe(x, debug=True, exact=True)
     with q.Context(E, X, K, F, n_layer=1, max_tokens=T) as ctx:
         ctx.synth(0, seed, gate_type=gt, up_type=ut, down_type=dt)
-        if gt != orc.T_Q4_0:
-            with pytest.raises(q.QmsgError) as ei:      # the integer kernels take Q4_0 gate/up
-                ctx.moe(0, x)
-            assert ei.value.status == -2
+        fast = ctx.moe(0, x)                            # the default (integer) path on the same layer
         ctx.set_path(q.PATH_FP32)
         out, got = ctx.moe_debug(0, x)
+        ctx.set_path(q.PATH_AUTO)
+        fast_again = ctx.moe(0, x)
+    assert np.array_equal(bits(fast), bits(host.moe(x))) and np.array_equal(bits(fast_again), bits(fast))
     assert np.array_equal(bits(got["logits"]), bits(ref["logits"])), "router logits"
     assert np.array_equal(got["sel"], ref["sel"]) and np.array_equal(bits(got["wt"]), bits(ref["wt"]))
     for k in ("start", "slot_t", "slot_of", "active"):

@@ -73,3 +73,37 @@ def test_layer_exact(qmsg, name, E, X, K, F, T, seed, dt, rms):
     assert np.array_equal(_bits(got["aq"]), _bits(ref["aq"])), "int8 activation blocks"
     assert np.array_equal(_bits(got["dn"]), _bits(ref["dn"])), "down rows"
     assert np.array_equal(_bits(out), _bits(ref_out)), "layer output"
+
+
+GATE_UP_CASES = [
+    # name, E, X, K, F, T, seed, gate_type, up_type, down_type, rmsnorm
+    ("gq41_t1", 2048, 128, 8, 768, 1, 51, orc.T_Q4_1, orc.T_Q4_1, orc.T_Q4_0, True),
+    ("gq6k_t4", 4096, 128, 8, 1536, 4, 52, orc.T_Q6_K, orc.T_Q6_K, orc.T_Q6_K, False),
+    ("gq6k_uq41_t7", 256, 16, 4, 128, 7, 53, orc.T_Q6_K, orc.T_Q4_1, orc.T_Q4_1, False),
+    ("gq40_uq6k_t2", 2048, 128, 8, 768, 2, 54, orc.T_Q4_0, orc.T_Q6_K, orc.T_Q4_0, False),
+    ("q480b_gq6k_t3", 6144, 160, 8, 2560, 3, 55, orc.T_Q6_K, orc.T_Q6_K, orc.T_Q4_0, False),
+    ("k16_gq41_t1", 512, 64, 16, 256, 1, 56, orc.T_Q4_1, orc.T_Q4_1, orc.T_Q4_0, False),
+    ("tiny_gq41_t200", 256, 16, 4, 256, 200, 57, orc.T_Q4_1, orc.T_Q4_1, orc.T_Q6_K, False),
+]
+
+
+@pytest.mark.parametrize("name,E,X,K,F,T,seed,gt,ut,dt,rms", GATE_UP_CASES, ids=[c[0] for c in GATE_UP_CASES])
+def test_layer_gate_up_types(qmsg, name, E, X, K, F, T, seed, gt, ut, dt, rms):
+    """Gate and up rows of Q4_1 / Q6_K (and mixed with Q4_0), which the reference's fast path
+    takes as well (src/kernels.c:197-200): every intermediate bit for bit, on the default and
+    the MFMA path (which hands such layers to the same kernels)."""
+    print(f"[case] {name} E={E} X={X} K={K} F={F} T={T} types={gt},{ut},{dt}", flush=True)
+    x = orc.make_input(E, T, seed, rmsnorm=rms)
+    host = orc.Layer(E, X, K, F, seed, gate_type=gt, up_type=ut, down_type=dt, experts=[])
+    ref_out, ref = host.moe(x, debug=True)
+    with qmsg.Context(E, X, K, F, n_layer=1, max_tokens=T) as ctx:
+        ctx.synth(0, seed, gate_type=gt, up_type=ut, down_type=dt)
+        out, got = ctx.moe_debug(0, x)
+        ctx.set_path(qmsg.PATH_MFMA)
+        out_mfma = ctx.moe(0, x)
+    for k in ("sel", "start", "slot_t", "slot_of", "active"):
+        assert np.array_equal(got[k], ref[k]), k
+    for k in ("logits", "wt", "xq", "gu", "act", "aq", "dn"):
+        assert np.array_equal(_bits(got[k]), _bits(ref[k])), k
+    assert np.array_equal(_bits(out), _bits(ref_out)), "layer output"
+    assert np.array_equal(_bits(out_mfma), _bits(ref_out)), "layer output (MFMA path)"

@@ -201,7 +201,8 @@ def load_layer(path):
     E, X, K, F, T, seed, dt, rms = (int(v) for v in d["shape"])
     special = str(d["special"])
     col0 = d.get("router_col0")
-    L = orc.Layer(E, X, K, F, seed, down_type=dt, experts=[], router_col0=col0)
+    gt, ut = (int(v) for v in d.get("gu_types", (orc.T_Q4_0, orc.T_Q4_0)))
+    L = orc.Layer(E, X, K, F, seed, gate_type=gt, up_type=ut, down_type=dt, experts=[], router_col0=col0)
     x = orc.make_input(E, T, seed, rmsnorm=bool(rms), bias_col0=special == "zipf")
     if special == "ties":
         L.router[5] = L.router[2]
