@@ -27,6 +27,29 @@ namespace qmsg {
 thread_local const LaunchTimer *g_launch_timer = nullptr;
 }
 
+/* Phase stamps for development builds (-DQMSG_PHASE_TRACE): thread 0 of a block records the
+ * 100 MHz real-time counter at numbered points of a kernel into a device table of 8 stamps
+ * per block (route blocks from row 0, gate/up from 1024, down from 2048), read back with
+ * qmsg_phase_read. Compiled out otherwise. */
+#ifdef QMSG_PHASE_TRACE
+namespace qmsg {
+__device__ unsigned long long g_phase[4096 * 8];
+}
+#define PHASE(region, k)                                                                        \
+    do {                                                                                        \
+        if (threadIdx.x == 0) {                                                                 \
+            const unsigned b_ = (region) + blockIdx.y * gridDim.x + blockIdx.x;                 \
+            if (b_ < 4096) qmsg::g_phase[b_ * 8 + (k)] = __builtin_amdgcn_s_memrealtime();      \
+        }                                                                                       \
+    } while (0)
+extern "C" int qmsg_phase_read(void *dst, size_t bytes)
+{
+    return (int)hipMemcpyFromSymbol(dst, HIP_SYMBOL(qmsg::g_phase), bytes);
+}
+#else
+#define PHASE(region, k) ((void)0)
+#endif
+
 /* Launch `kern` on `st`; with a timing hook installed the dispatch stamps its own events. */
 #define QLAUNCH(name, kern, grid, block, lds, st, ...)                                          \
     do {                                                                                       \
@@ -224,52 +247,89 @@ __device__ __forceinline__ float chain16_sum(float acc)
     return acc;
 }
 
+/* Steps q0 .. q1-1 (16-byte groups of four) of one FMA chain over chain-major rows in LDS,
+ * B groups per batch: the batch's reads are all issued before its FMAs. */
+template <int B>
+__device__ __forceinline__ float chain_steps(const float4 *wr, const float4 *xr, int q0, int q1, float acc)
+{
+    for (int q = q0; q < q1; q += B) {
+        float4 w[B], x[B];
+#pragma unroll
+        for (int u = 0; u < B; u++) {
+            w[u] = wr[q + u];
+            x[u] = xr[q + u];
+        }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int u = 0; u < B; u++) {
+            acc = __builtin_fmaf(w[u].x, x[u].x, acc);
+            acc = __builtin_fmaf(w[u].y, x[u].y, acc);
+            acc = __builtin_fmaf(w[u].z, x[u].z, acc);
+            acc = __builtin_fmaf(w[u].w, x[u].w, acc);
+        }
+    }
+    return acc;
+}
+
 /* Router for T <= 4: one block per expert, 256 threads. The expert's router row and the T
- * input rows are requested in four chunks, all in flight at once; as each chunk lands it is
- * staged into LDS and lane (t, c) of wave 0 advances the reference's FMA chain c (elements c,
- * c+16, ...) of token t over it (src/kernels.c:202-213), so the chains run while the later
- * chunks are still arriving. */
+ * input rows are requested all at once, staged into LDS chain-major (chain c of a row holds
+ * elements c, c+16, ... contiguously, so one 16-byte read gives a lane four steps of its
+ * chain), and lane (t, c) of wave 0 then runs the reference's FMA chain c of token t
+ * (src/kernels.c:202-213) with its reads batched ahead of the FMAs: 256 dependent FMAs per
+ * chain for n_embd 4096. Chains advanced chunk by chunk as the data landed were slower (a
+ * block barrier per chunk). */
 template <int T>
 __global__ __launch_bounds__(256) void route_small_kernel(RouteArgs a)
 {
     extern __shared__ __align__(16) uint8_t smem[];
     if ((int)blockIdx.x >= a.n_route_wg) { route_quantize(a); return; }
+    PHASE(0, 0);
     constexpr int NCH = 4, MPC = 1 + T;          /* chunks; loads per thread per chunk (E <= 4096) */
     const int tid = threadIdx.x, E = a.E, e = blockIdx.x;
-    const int XS = E + 16;                       /* padded x rows: lanes of different t hit other banks */
-    float *wrow = (float *)smem, *xr = wrow + E;
+    const int CS = E / 16 + 4;                   /* floats per chain: E/16 steps, padded (16-byte rows) */
+    float *buf = (float *)smem;                  /* [1 + T rows][16 chains][CS]: row 0 router, 1.. inputs */
     const int cw = E / (4 * NCH);                /* 16-byte slots of one row per chunk */
     const int sc = cw * (1 + T);                 /* slots of one chunk */
     const u32x4 *wsrc = (const u32x4 *)(a.router + (size_t)e * E);
     const u32x4 *xsrc = (const u32x4 *)a.xn;
-    auto slot_src = [&](int c, int i) -> const u32x4 * {
-        const int r = i / cw, j = c * cw + (i - r * cw);       /* r = 0: router row, r >= 1: input t = r-1 */
-        return r == 0 ? wsrc + j : xsrc + (size_t)(r - 1) * (E / 4) + j;
-    };
-    auto slot_dst = [&](int c, int i) -> float * {
-        const int r = i / cw, j = c * cw + (i - r * cw);
-        return r == 0 ? wrow + 4 * j : xr + (r - 1) * XS + 4 * j;
-    };
     u32x4 v[NCH][MPC];
 #pragma unroll
     for (int c = 0; c < NCH; c++)
 #pragma unroll
-        for (int m = 0; m < MPC; m++) v[c][m] = *slot_src(c, min(tid + 256 * m, sc - 1));
+        for (int m = 0; m < MPC; m++) {
+            const int i = min(tid + 256 * m, sc - 1), r = i / cw, j = c * cw + (i - r * cw);
+            v[c][m] = r == 0 ? wsrc[j] : xsrc[(size_t)(r - 1) * (E / 4) + j];
+        }
     const int t = tid >> 4, cc = tid & 15;
+    const float4 *wr = (const float4 *)(buf + cc * CS);
+    const float4 *xr = (const float4 *)(buf + ((1 + t) * 16 + cc) * CS);
+    const int q4 = E / (16 * NCH * 4);           /* float4 steps of one chain per chunk */
     float acc = 0.0f;
 #pragma unroll
     for (int c = 0; c < NCH; c++) {
 #pragma unroll
-        for (int m = 0; m < MPC; m++)
-            if (tid + 256 * m < sc) *(u32x4 *)slot_dst(c, tid + 256 * m) = v[c][m];
-        __syncthreads();
-        if (tid < 16 * T) {
-            const float *xrow = xr + t * XS;
-            const int i1 = (c + 1) * (E / NCH);
-#pragma unroll 16
-            for (int i = c * (E / NCH) + cc; i < i1; i += 16) acc = __builtin_fmaf(wrow[i], xrow[i], acc);
+        for (int m = 0; m < MPC; m++) {
+            const int i = tid + 256 * m;
+            if (i < sc) {
+                /* slot j holds elements 4j .. 4j+3: chains 4(j%4) .. 4(j%4)+3, step j/4 */
+                const int r = i / cw, j = c * cw + (i - r * cw);
+                float *dst = buf + (r * 16 + 4 * (j & 3)) * CS + (j >> 2);
+                dst[0] = __uint_as_float(v[c][m].x);
+                dst[CS] = __uint_as_float(v[c][m].y);
+                dst[2 * CS] = __uint_as_float(v[c][m].z);
+                dst[3 * CS] = __uint_as_float(v[c][m].w);
+            }
         }
     }
+    __syncthreads();
+    PHASE(0, 1);
+    if (tid < 16 * T) {
+        const int q1 = NCH * q4;
+        if ((q1 & 7) == 0) acc = chain_steps<8>(wr, xr, 0, q1, acc);
+        else if ((q1 & 3) == 0) acc = chain_steps<4>(wr, xr, 0, q1, acc);
+        else acc = chain_steps<1>(wr, xr, 0, q1, acc);
+    }
+    PHASE(0, 2);
     if (tid < 16 * T) {
         acc = chain16_sum(acc);
         if (cc == 0) a.S.logits[(size_t)t * a.X + e] = acc;
@@ -368,7 +428,7 @@ hipError_t launch_route(const Shape &s, const LayerDev &L, const Scratch &S, con
     const int nq = (T * (s.E / 32) + 255) / 256;
     if (T <= 4 && s.E <= 4096) {
         a.n_route_wg = s.X;
-        const size_t lds = (size_t)(s.E + T * (s.E + 16)) * 4;
+        const size_t lds = (size_t)(1 + T) * 16 * (s.E / 16 + 4) * 4;
         const dim3 grid(a.n_route_wg + nq);
         if (T == 1) QLAUNCH("route", route_small_kernel<1>, grid, dim3(256), lds, st, a);
         else if (T == 2) QLAUNCH("route", route_small_kernel<2>, grid, dim3(256), lds, st, a);
@@ -1063,6 +1123,7 @@ __global__ __launch_bounds__(64 * W) void gateup_kernel(GateUpArgs a)
     uint8_t *wbuf = smem + wave * 16 * WS;
     uint8_t *xbuf = smem + W * 16 * WS;
     float *res = (float *)(xbuf + NT * nP * kPairBytes);               /* [NT][2R] */
+    PHASE(1024, 0);
 
     /* a one-token batch: its only token's records can be requested before the routing */
     u32x4 xv[XS];
@@ -1094,6 +1155,7 @@ __global__ __launch_bounds__(64 * W) void gateup_kernel(GateUpArgs a)
         float *L = (float *)(P + kMaxExperts);
         int *rank = (int *)(L + kMaxExperts);
         route_one_rank(a.S, a.X, L, P, rank, rank + kMaxExperts);
+        PHASE(1024, 1);
         /* start streaming the expert the logit order points at while the exact selection
          * finishes; the rare block whose expert changes reloads below */
         const int e_spec = spec_expert(rank, a.X, a.K, (int)blockIdx.y);
@@ -1104,6 +1166,7 @@ __global__ __launch_bounds__(64 * W) void gateup_kernel(GateUpArgs a)
                 if (d < nchunk) load_chunk(d, wv[d]);
         }
         route_one_select(a.S, a.K, a.X, sr, L, P, rank, rank + kMaxExperts, rank + 2 * kMaxExperts);
+        PHASE(1024, 2);
         if ((int)blockIdx.y >= sr->na) return;
         wk = sr->work[blockIdx.y];
         slot_t = sr->slot_t;
@@ -1162,9 +1225,11 @@ __global__ __launch_bounds__(64 * W) void gateup_kernel(GateUpArgs a)
                     if (c + D < nchunk) load_chunk(c + D, wv[d]);
                     q4_rows_nt<2, NT>((const uint32_t *)(wbuf + qd * WS), p, xbuf, (size_t)nP * kPairBytes,
                                       c * (CB / 2), CB / 2, nt, acc);
+                    if (c == 0 && g0 == s_begin) PHASE(1024, 3);
                 }
             }
         }
+        if (g0 == s_begin) PHASE(1024, 4);
 #pragma unroll
         for (int n = 0; n < NT; n++) {
             const float v = quad_finish(acc[n], 8.0f);
@@ -1182,6 +1247,7 @@ __global__ __launch_bounds__(64 * W) void gateup_kernel(GateUpArgs a)
         }
         __syncthreads();
     }
+    PHASE(1024, 5);
 }
 
 template <int W, int NT, int SEL>
@@ -1402,12 +1468,14 @@ __global__ __launch_bounds__(32 * RD) void down_t1_kernel(DownArgs a)
             dst[m] = *(const u32x4 *)(rp + (size_t)c * CB * BB + 16 * j);
         }
     };
+    PHASE(2048, 0);
     const bool active = e0 >= 0;
     if (active) {
 #pragma unroll
         for (int d = 0; d < D; d++)
             if (d < nchunk) load_chunk(d, wv[d]);
     }
+    PHASE(2048, 1);
     auto quant = [&](int b, const float *v) {
         const int s = b / nbF, blk = b - s * nbF;
         const Q8Vals q = quantize_block(v);
@@ -1439,6 +1507,7 @@ __global__ __launch_bounds__(32 * RD) void down_t1_kernel(DownArgs a)
         quant(b, v);
     }
     __syncthreads();
+    PHASE(2048, 2);
     if (active) {
         /* quad qd: expert j0 + qd/RD, row r0 + qd%RD; its slot is its active index */
         const int jq = j0 + qd / RD, rr = qd % RD;
@@ -1463,9 +1532,11 @@ __global__ __launch_bounds__(32 * RD) void down_t1_kernel(DownArgs a)
                     else
                         q4_0_rows<1, 4>((const uint32_t *)(wbuf + qd * WS), p, xq, (size_t)xrec, c * (CB / 2), CB / 2,
                                         1, acc);
+                    if (c == 0) PHASE(2048, 3);
                 }
             }
         }
+        PHASE(2048, 4);
         const float v = quad_finish(acc[0], finish_scale(TYPE));
         if (p == 0 && jq < K) {
             a.S.dn[(size_t)jq * E + r0 + rr] = v;
@@ -1478,6 +1549,7 @@ __global__ __launch_bounds__(32 * RD) void down_t1_kernel(DownArgs a)
         for (int j = 0; j < K; j++) o = __builtin_fmaf(a.S.wt[j], dnl[a.S.slot_of[j] * RD + tid], o);
         a.out[r0 + tid] = o;
     }
+    PHASE(2048, 5);
 }
 
 /* The int8 blocks of every slot's activations (src/model.c:996-997) for batches whose

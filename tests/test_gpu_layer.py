@@ -107,3 +107,24 @@ def test_layer_gate_up_types(qmsg, name, E, X, K, F, T, seed, gt, ut, dt, rms):
         assert np.array_equal(_bits(got[k]), _bits(ref[k])), k
     assert np.array_equal(_bits(out), _bits(ref_out)), "layer output"
     assert np.array_equal(_bits(out_mfma), _bits(ref_out)), "layer output (MFMA path)"
+
+
+@pytest.mark.parametrize("scale", [0.0, 1e-38, 1e-30, 300.0])
+def test_one_token_routing_ties(qmsg, scale):
+    """One-token batches route inside the gate/up kernel. Inputs scaled so every logit is 0,
+    or so small that exp(l - max) rounds to the same double for different logits (the exact
+    ranking of p then decides, lower index first), or large: selection and weights bit for
+    bit against the oracle."""
+    E, X, K, F, seed = 2048, 128, 8, 768, 61
+    print(f"[case] one-token routing scale={scale}", flush=True)
+    x = orc.make_input(E, 1, seed) * np.float32(scale)
+    host = orc.Layer(E, X, K, F, seed, experts=[])
+    ref_out, ref = host.moe(x, debug=True)
+    with qmsg.Context(E, X, K, F, n_layer=1, max_tokens=1) as ctx:
+        ctx.synth(0, seed)
+        out, got = ctx.moe_debug(0, x)
+    assert np.array_equal(got["sel"], ref["sel"]), (got["sel"], ref["sel"])
+    assert np.array_equal(_bits(got["wt"]), _bits(ref["wt"])), "routing weights"
+    for k in ("start", "slot_t", "slot_of", "active"):
+        assert np.array_equal(got[k], ref[k]), k
+    assert np.array_equal(_bits(out), _bits(ref_out)), "layer output"
