@@ -1437,12 +1437,26 @@ __global__ __launch_bounds__(32 * RD) void down_t1_kernel(DownArgs a)
     constexpr int NSL = 16 * SPR;                     /* slots of one wave's chunk            */
     constexpr int SPT = (NSL + 63) / 64;              /* slots per lane per chunk             */
     constexpr int WS = CB * BB + ((SPR & 1) ? 0 : 16);/* LDS row stride, odd in 16-byte units */
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, qd = lane >> 2, p = lane & 3;
+    const int tid = threadIdx.x, lane = tid & 63, qd = lane >> 2, p = lane & 3;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int r0 = (int)blockIdx.x * RD, E = a.E, K = a.K, nbF = a.F >> 5, nPF = a.F >> 6;
     const int nchunk = nbF / CB, xrec = nPF * kPairBytes;
     uint8_t *wbuf = smem + wave * 16 * WS;
     uint8_t *xbuf = smem + NW * 16 * WS;              /* [K][xrec]                            */
     float *dnl = (float *)(xbuf + (size_t)K * xrec);  /* [K][RD]                              */
+
+    /* this wave's experts, j0 = EPW*w and j0 + 1 when a wave holds two, and the combine's
+     * weights and slots: wave-uniform scalar loads, requested first, so that the weight rows
+     * are not requested behind the activation loads (vector loads complete in order) */
+    const int j0 = EPW * wave, j1 = j0 + EPW - 1;
+    const int e0 = j0 < K ? a.S.work[j0].x : -1, e1 = j1 < K ? a.S.work[j1].x : -1;
+    float wtk[kSelNS];
+    int sok[kSelNS];
+#pragma unroll
+    for (int j = 0; j < kSelNS; j++) {
+        wtk[j] = a.S.wt[min(j, K - 1)];
+        sok[j] = a.S.slot_of[min(j, K - 1)];
+    }
 
     /* the activations to quantise: 32 floats per int8 block, the first QPT*NTH in registers */
     const int nqb = K * nbF;
@@ -1453,9 +1467,6 @@ __global__ __launch_bounds__(32 * RD) void down_t1_kernel(DownArgs a)
 #pragma unroll
         for (int j = 0; j < 8; j++) av[u][j] = src[j];
     }
-    /* this wave's experts (uniform): j0 = EPW*w, and j0 + 1 when a wave holds two */
-    const int j0 = EPW * wave, j1 = j0 + EPW - 1;
-    const int e0 = j0 < K ? a.S.work[j0].x : -1, e1 = j1 < K ? a.S.work[j1].x : -1;
     const uint8_t *b0 = a.down + (size_t)max(e0, 0) * a.eb + (size_t)r0 * a.rb;
     const uint8_t *b1 = a.down + (size_t)max(e1, 0) * a.eb + (size_t)r0 * a.rb;
     __builtin_amdgcn_sched_barrier(0);
@@ -1546,7 +1557,9 @@ __global__ __launch_bounds__(32 * RD) void down_t1_kernel(DownArgs a)
     __syncthreads();
     if (tid < RD) {
         float o = 0.0f;
-        for (int j = 0; j < K; j++) o = __builtin_fmaf(a.S.wt[j], dnl[a.S.slot_of[j] * RD + tid], o);
+#pragma unroll
+        for (int j = 0; j < kSelNS; j++)
+            if (j < K) o = __builtin_fmaf(wtk[j], dnl[sok[j] * RD + tid], o);
         a.out[r0 + tid] = o;
     }
     PHASE(2048, 5);

@@ -128,3 +128,36 @@ def test_one_token_routing_ties(qmsg, scale):
     for k in ("start", "slot_t", "slot_of", "active"):
         assert np.array_equal(got[k], ref[k]), k
     assert np.array_equal(_bits(out), _bits(ref_out)), "layer output"
+
+
+
+ONE_TOKEN_CASES = [
+    # name, E, X, K, F, seed, down_type, rmsnorm
+    ("q235b", 4096, 128, 8, 1536, 71, orc.T_Q4_0, False),
+    ("q235b_q41", 4096, 128, 8, 1536, 72, orc.T_Q4_1, True),
+    ("q30b", 2048, 128, 8, 768, 73, orc.T_Q4_0, True),
+    ("k4_x64", 1024, 64, 4, 512, 74, orc.T_Q4_0, False),
+    ("x256", 2048, 256, 8, 256, 75, orc.T_Q4_1, False),
+]
+
+
+@pytest.mark.parametrize("name,E,X,K,F,seed,dt,rms", ONE_TOKEN_CASES, ids=[c[0] for c in ONE_TOKEN_CASES])
+def test_one_token_tokens_in_a_row(qmsg, name, E, X, K, F, seed, dt, rms):
+    """One-token batches, several tokens in a row on one context (the routing inside the
+    gate/up kernel, its published arrays and the down kernel's own quantisation are rewritten
+    every call), on the default and the EXACT path: every intermediate bit for bit."""
+    print(f"[case] one token {name}", flush=True)
+    host = orc.Layer(E, X, K, F, seed, down_type=dt, experts=[])
+    with qmsg.Context(E, X, K, F, n_layer=1, max_tokens=1) as ctx:
+        ctx.synth(0, seed, down_type=dt)
+        for t in range(3):
+            x = orc.make_input(E, 1, seed + 100 * t, rmsnorm=rms)
+            ref_out, ref = host.moe(x, debug=True)
+            for path in (qmsg.PATH_AUTO, qmsg.PATH_EXACT):
+                ctx.set_path(path)
+                out, got = ctx.moe_debug(0, x)
+                for k in ("sel", "start", "slot_t", "slot_of", "active"):
+                    assert np.array_equal(got[k], ref[k]), (path, t, k)
+                for k in ("logits", "wt", "xq", "gu", "act", "aq", "dn"):
+                    assert np.array_equal(_bits(got[k]), _bits(ref[k])), (path, t, k)
+                assert np.array_equal(_bits(out), _bits(ref_out)), (path, t, "layer output")
