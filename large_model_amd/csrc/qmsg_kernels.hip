@@ -1176,7 +1176,13 @@ __global__ __launch_bounds__(64 * W) void gateup_kernel(GateUpArgs a)
         wk = a.S.tiles[blockIdx.y];                  /* at most kTileN slots of one expert */
     }
     const int e = wk.x, s_begin = wk.y, s_end = wk.z;
-    if (!prefetched) set_expert(e);
+    if (!prefetched) {
+        /* the first pass's weight chunks go out before the token records are fetched */
+        set_expert(e);
+#pragma unroll
+        for (int d = 0; d < D; d++)
+            if (d < nchunk) load_chunk(d, wv[d]);
+    }
     const int F = a.F;
     const int rho = qd < 8 ? 8 * wave + qd : R + 8 * wave + (qd - 8);   /* tile row of this quad */
     const bool tok_bytes = SEL && a.T <= 256;       /* work.w holds the first four tokens */
@@ -1205,7 +1211,7 @@ __global__ __launch_bounds__(64 * W) void gateup_kernel(GateUpArgs a)
         __syncthreads();
         RowAcc acc[NT];
         for (int n = 0; n < NT; n++) acc[n] = RowAcc{ 0.0f, 0.0f, 0.0f };
-        if (!(prefetched && g0 == s_begin)) {
+        if (g0 != s_begin) {
 #pragma unroll
             for (int d = 0; d < D; d++)
                 if (d < nchunk) load_chunk(d, wv[d]);
