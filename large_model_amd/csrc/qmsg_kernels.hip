@@ -1364,27 +1364,41 @@ __global__ __launch_bounds__(4 * RT) void tile_rows_kernel(TileArgs a)
     uint8_t *tile = smem;
     uint8_t *xbuf = smem + ((RT * rb + 15) & ~15);            /* [NT][xrec] */
     const u32x4 *wsrc = (const u32x4 *)(a.w + (size_t)e * a.eb + (size_t)R0 * a.rb);
-    for (int i0 = 0; i0 < n16; i0 += NTH * 8) {
-        u32x4 v[8];
+    /* 16-byte slot i of pass g0's input records */
+    auto rec_slot = [&](int g0, int i) -> const u32x4 * {
+        const int n = i / x16;
+        const size_t src = BT ? (size_t)a.S.slot_t[s0 + g0 + n] : (size_t)(s0 + g0 + n);
+        return (const u32x4 *)(a.rec + src * xrec) + (i - n * x16);
+    };
+    /* the weight tile (up to WPT loads per thread) and the first pass's records (XPT per
+     * thread) are all requested before any of them is waited for */
+    constexpr int WPT = 16, XPT = 4;
+    const int nt0 = min(NT, ns), nx0 = nt0 * x16;
+    u32x4 xr[XPT];
+    for (int i0 = 0; i0 < n16; i0 += NTH * WPT) {
+        u32x4 v[WPT];
 #pragma unroll
-        for (int m = 0; m < 8; m++) v[m] = wsrc[min(i0 + tid + NTH * m, n16 - 1)];
+        for (int m = 0; m < WPT; m++) v[m] = wsrc[min(i0 + tid + NTH * m, n16 - 1)];
+        if (i0 == 0) {
 #pragma unroll
-        for (int m = 0; m < 8; m++)
+            for (int m = 0; m < XPT; m++) xr[m] = *rec_slot(0, min(tid + NTH * m, nx0 - 1));
+        }
+#pragma unroll
+        for (int m = 0; m < WPT; m++)
             if (i0 + tid + NTH * m < n16) ((u32x4 *)tile)[i0 + tid + NTH * m] = v[m];
     }
     const uint8_t *row = tile + quad * rb;
     for (int g0 = 0; g0 < ns; g0 += NT) {
         const int nt = min(NT, ns - g0);
         __syncthreads();                                  /* the weights landed; xbuf is free */
-        for (int i = tid; i < nt * x16; i += NTH) {
-            if (BT) {
-                const int n = i / x16;
-                const u32x4 *src = (const u32x4 *)(a.rec + (size_t)a.S.slot_t[s0 + g0 + n] * xrec);
-                ((u32x4 *)xbuf)[i] = src[i - n * x16];
-            } else {
-                ((u32x4 *)xbuf)[i] = ((const u32x4 *)(a.rec + (size_t)(s0 + g0) * xrec))[i];
-            }
+        int i = tid;
+        if (g0 == 0) {
+#pragma unroll
+            for (int m = 0; m < XPT; m++)
+                if (tid + NTH * m < nx0) ((u32x4 *)xbuf)[tid + NTH * m] = xr[m];
+            i = tid + NTH * XPT;
         }
+        for (; i < nt * x16; i += NTH) ((u32x4 *)xbuf)[i] = *rec_slot(g0, i);
         __syncthreads();
         RowAcc acc[NT];
         for (int n = 0; n < NT; n++) acc[n] = RowAcc{ 0.0f, 0.0f, 0.0f };
