@@ -524,13 +524,13 @@ __device__ void topk_token(const SelectArgs &a, int t, double *P, int *part, int
  * slots of one expert are contiguous, experts ascend, and inside an expert slots follow
  * token order then selection order. Also writes one work record per active expert
  * (expert, first slot, end slot) for the expert kernels, and -1 records after them. One wave. */
-__device__ void dispatch_slots(const SelectArgs &a, int *cnt, int *cur, int *tok)
+__device__ void dispatch_slots(const SelectArgs &a, const int *sel, int *cnt, int *cur, int *tok)
 {
     constexpr int NPL = kMaxExperts / 64;
     const int X = a.X, NS = a.T * a.K, lane = threadIdx.x & 63;
     for (int e = lane; e < X; e += 64) { cnt[e] = 0; cur[e] = 0; tok[e] = 0; }
     wave_sync();
-    for (int i = lane; i < NS; i += 64) atomicAdd(&cnt[a.S.sel[i]], 1);
+    for (int i = lane; i < NS; i += 64) atomicAdd(&cnt[sel[i]], 1);
     wave_sync();
     /* lane l owns experts l*NPL .. l*NPL+NPL-1 (contiguous, so a lane scan orders them) */
     int c[NPL], tot = 0, act = 0;
@@ -562,7 +562,7 @@ __device__ void dispatch_slots(const SelectArgs &a, int *cnt, int *cur, int *tok
     const unsigned long long below = (1ULL << lane) - 1ULL;
     for (int base = 0; base < NS; base += 64) {
         const int i = base + lane;
-        const int e = i < NS ? a.S.sel[i] : -1;
+        const int e = i < NS ? sel[i] : -1;
         unsigned long long same = __ballot(i < NS);
         for (int bit = 0; bit < 9; bit++) {
             const unsigned long long b = __ballot(i < NS && ((e >> bit) & 1));
@@ -607,23 +607,36 @@ __device__ void dispatch_slots(const SelectArgs &a, int *cnt, int *cur, int *tok
     if (lane == 63) a.S.meta[1] = incl_t;
 }
 
-/* Top-K of one token per block; a single-block launch (T == 1) also sorts the slots. */
+/* Top-K of one token per block. The block that finishes last sorts the slots: each block
+ * releases its selection (device-scope fence by the wave that wrote it) and takes a ticket
+ * from meta[4]; the last ticket acquires the others' selections, dispatches and resets the
+ * counter for the next launch. A one-block launch (T == 1) dispatches directly. */
 __global__ __launch_bounds__(256) void select_kernel(SelectArgs a, int do_dispatch)
 {
     __shared__ double P[kMaxExperts];
     __shared__ int part[2 * kMaxExperts];
     __shared__ int selb[64];
     __shared__ int tok[kMaxExperts];
+    __shared__ int last;
     const int t = blockIdx.x;
     if (t < a.T) topk_token(a, t, P, part, selb);
     if (!do_dispatch) return;
-    if (threadIdx.x < 64) dispatch_slots(a, part, part + kMaxExperts, tok);
+    if (gridDim.x > 1) {
+        if (threadIdx.x < 64) __threadfence();          /* sel/wt were written by wave 0 */
+        __syncthreads();
+        if (threadIdx.x == 0) last = atomicAdd(a.S.meta + 4, 1) == (int)gridDim.x - 1;
+        __syncthreads();
+        if (!last) return;
+        __threadfence();
+    }
+    if (threadIdx.x < 64) dispatch_slots(a, a.S.sel, part, part + kMaxExperts, tok);
+    if (gridDim.x > 1 && threadIdx.x == 0) __hip_atomic_store(a.S.meta + 4, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 __global__ __launch_bounds__(64) void dispatch_kernel(SelectArgs a)
 {
     __shared__ int cnt[kMaxExperts], cur[kMaxExperts], tok[kMaxExperts];
-    dispatch_slots(a, cnt, cur, tok);
+    dispatch_slots(a, a.S.sel, cnt, cur, tok);
 }
 
 hipError_t launch_select(const Shape &s, const Scratch &S, int T, int gateup_routes, hipStream_t st)
@@ -634,8 +647,10 @@ hipError_t launch_select(const Shape &s, const Scratch &S, int T, int gateup_rou
     a.T = T;
     a.S = S;
     if (gateup_routes && use_small_route(T, s.K)) return hipSuccess;   /* the gate/up kernel routes the batch */
-    QLAUNCH("select", select_kernel, dim3(T), dim3(256), 0, st, a, T == 1 ? 1 : 0);
-    if (T > 1) QLAUNCH("dispatch", dispatch_kernel, dim3(1), dim3(64), 0, st, a);
+    /* up to 64 tokens the last select block also dispatches; larger batches take a separate
+     * dispatch launch rather than hundreds of tickets on one counter */
+    QLAUNCH("select", select_kernel, dim3(T), dim3(256), 0, st, a, T <= 64 ? 1 : 0);
+    if (T > 64) QLAUNCH("dispatch", dispatch_kernel, dim3(1), dim3(64), 0, st, a);
     return hipGetLastError();
 }
 
@@ -1609,7 +1624,9 @@ __global__ void combine_kernel(const Scratch S, int E, int K, int T, float *out)
 {
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= T * E) return;
-    const int t = i / E, r = i - t * E;
+    /* n_embd is a multiple of the block size: the token is block-uniform, so its weights
+     * and slots are scalar loads */
+    const int t = (int)(blockIdx.x * blockDim.x) / E, r = i - t * E;
     float o = 0.0f;
     for (int j = 0; j < K; j++)
         o = __builtin_fmaf(S.wt[(size_t)t * K + j], S.dn[(size_t)S.slot_of[(size_t)t * K + j] * E + r], o);
