@@ -1365,7 +1365,7 @@ struct TileArgs {
     Scratch S;
 };
 
-template <int TYPE, int NT, int RT, int BT>
+template <int TYPE, int NT, int RT, int BT, int QA = 0>
 __global__ __launch_bounds__(4 * RT) void tile_rows_kernel(TileArgs a)
 {
     extern __shared__ __align__(16) uint8_t smem[];
@@ -1386,17 +1386,31 @@ __global__ __launch_bounds__(4 * RT) void tile_rows_kernel(TileArgs a)
         return (const u32x4 *)(a.rec + src * xrec) + (i - n * x16);
     };
     /* the weight tile (up to WPT loads per thread) and the first pass's records (XPT per
-     * thread) are all requested before any of them is waited for */
-    constexpr int WPT = 16, XPT = 4;
+     * thread; with QA the first activation block of this thread instead) are all requested
+     * before any of them is waited for */
+    constexpr int WPT = 16, XPT = QA ? 1 : 4;
     const int nt0 = min(NT, ns), nx0 = nt0 * x16;
+    const int nbF = a.cols >> 5, nq0 = nt0 * nbF;
     u32x4 xr[XPT];
+    float4 av[QA ? 8 : 1];
+    /* QA: activation block i of pass g0 (slot s0+g0+i/nbF, block i%nbF), 32 floats */
+    auto act_block = [&](int g0, int i) -> const float4 * {
+        const int n = i / nbF;
+        return (const float4 *)(a.S.act + (size_t)(s0 + g0 + n) * a.cols + (size_t)(i - n * nbF) * 32);
+    };
     for (int i0 = 0; i0 < n16; i0 += NTH * WPT) {
         u32x4 v[WPT];
 #pragma unroll
         for (int m = 0; m < WPT; m++) v[m] = wsrc[min(i0 + tid + NTH * m, n16 - 1)];
         if (i0 == 0) {
+            if (QA) {
+                const float4 *src = act_block(0, min(tid, nq0 - 1));
 #pragma unroll
-            for (int m = 0; m < XPT; m++) xr[m] = *rec_slot(0, min(tid + NTH * m, nx0 - 1));
+                for (int j = 0; j < (QA ? 8 : 1); j++) av[j] = src[j];
+            } else {
+#pragma unroll
+                for (int m = 0; m < XPT; m++) xr[m] = *rec_slot(0, min(tid + NTH * m, nx0 - 1));
+            }
         }
 #pragma unroll
         for (int m = 0; m < WPT; m++)
@@ -1406,14 +1420,45 @@ __global__ __launch_bounds__(4 * RT) void tile_rows_kernel(TileArgs a)
     for (int g0 = 0; g0 < ns; g0 += NT) {
         const int nt = min(NT, ns - g0);
         __syncthreads();                                  /* the weights landed; xbuf is free */
-        int i = tid;
-        if (g0 == 0) {
+        if (QA) {
+            /* the int8 records of this pass's slots, formed here (src/model.c:996-997); the
+             * first column of blocks also writes them out for the debug copy */
+            auto quant = [&](int i, const float4 *f) {
+                float v[32];
 #pragma unroll
-            for (int m = 0; m < XPT; m++)
-                if (tid + NTH * m < nx0) ((u32x4 *)xbuf)[tid + NTH * m] = xr[m];
-            i = tid + NTH * XPT;
+                for (int j = 0; j < 8; j++) {
+                    v[4 * j] = f[j].x; v[4 * j + 1] = f[j].y; v[4 * j + 2] = f[j].z; v[4 * j + 3] = f[j].w;
+                }
+                const int n = i / nbF, blk = i - n * nbF, slot = s0 + g0 + n;
+                const Q8Vals q = quantize_block(v);
+                store_pair_half(q, (uint32_t *)(xbuf + (size_t)n * xrec + (size_t)(blk >> 1) * kPairBytes), blk & 1);
+                if (blockIdx.x == 0) {
+                    store_q8(q, a.S.aq + (size_t)slot * nbF + blk);
+                    store_pair_half(q, (uint32_t *)(a.S.aqk + ((size_t)slot * nPF + (blk >> 1)) * kPairBytes), blk & 1);
+                }
+            };
+            int i = tid;
+            if (g0 == 0) {
+                if (tid < nq0) quant(tid, av);
+                i = tid + NTH;
+            }
+            for (; i < nt * nbF; i += NTH) {
+                float4 f[8];
+                const float4 *src = act_block(g0, i);
+#pragma unroll
+                for (int j = 0; j < 8; j++) f[j] = src[j];
+                quant(i, f);
+            }
+        } else {
+            int i = tid;
+            if (g0 == 0) {
+#pragma unroll
+                for (int m = 0; m < XPT; m++)
+                    if (tid + NTH * m < nx0) ((u32x4 *)xbuf)[tid + NTH * m] = xr[m];
+                i = tid + NTH * XPT;
+            }
+            for (; i < nt * x16; i += NTH) ((u32x4 *)xbuf)[i] = *rec_slot(g0, i);
         }
-        for (; i < nt * x16; i += NTH) ((u32x4 *)xbuf)[i] = *rec_slot(g0, i);
         __syncthreads();
         RowAcc acc[NT];
         for (int n = 0; n < NT; n++) acc[n] = RowAcc{ 0.0f, 0.0f, 0.0f };
@@ -1633,13 +1678,17 @@ __global__ void combine_kernel(const Scratch S, int E, int K, int T, float *out)
     out[i] = o;
 }
 
-template <int TYPE, int RT>
+template <int TYPE, int RT, int QA>
 static void launch_down_tile(const TileArgs &a, int NT, dim3 grid, size_t lds, hipStream_t st)
 {
-    if (NT == 4) QLAUNCH("down", (tile_rows_kernel<TYPE, 4, RT, 0>), grid, dim3(4 * RT), lds, st, a);
-    else if (NT == 2) QLAUNCH("down", (tile_rows_kernel<TYPE, 2, RT, 0>), grid, dim3(4 * RT), lds, st, a);
-    else QLAUNCH("down", (tile_rows_kernel<TYPE, 1, RT, 0>), grid, dim3(4 * RT), lds, st, a);
+    if (NT == 4) QLAUNCH("down", (tile_rows_kernel<TYPE, 4, RT, 0, QA>), grid, dim3(4 * RT), lds, st, a);
+    else if (NT == 2) QLAUNCH("down", (tile_rows_kernel<TYPE, 2, RT, 0, QA>), grid, dim3(4 * RT), lds, st, a);
+    else QLAUNCH("down", (tile_rows_kernel<TYPE, 1, RT, 0, QA>), grid, dim3(4 * RT), lds, st, a);
 }
+
+/* Batches up to this many tokens form the activation records inside the down tiles (each of
+ * a tile's row blocks quantises the tile's slots again) instead of in a separate launch. */
+constexpr int kTileQuantT = 8;
 
 /* Rows per block of the Q6_K slot-tile kernel (its 210-byte super-blocks make a 64-row tile
  * 81 KB of LDS for n_ff_exp 1536, one block per CU). */
@@ -1681,7 +1730,8 @@ hipError_t launch_down_exact(const Shape &s, const LayerDev &L, const Scratch &S
     }
     /* slot tiles: the activations' int8 records first (unless the MFMA gate/up wrote them) */
     const int NS = T * s.K, maxt = (s.X < NS ? s.X : NS) + NS / kTileN + 1;
-    if (quant) {
+    const bool qa = quant && T <= kTileQuantT;
+    if (quant && !qa) {
         const int nq = NS * (s.F / 32);
         QLAUNCH("actq", act_quant_kernel, dim3((nq + 255) / 256), dim3(256), 0, st, S, s.F, NS);
     }
@@ -1700,9 +1750,15 @@ hipError_t launch_down_exact(const Shape &s, const LayerDev &L, const Scratch &S
     ta.y_stride = s.E;
     ta.y_off = 0;
     ta.S = S;
-    if (L.down_type == 2) launch_down_tile<2, 64>(ta, NT, grid, lds, st);
-    else if (L.down_type == 3) launch_down_tile<3, 64>(ta, NT, grid, lds, st);
-    else launch_down_tile<14, kDownTileRowsQ6K>(ta, NT, grid, lds, st);
+    if (qa) {
+        if (L.down_type == 2) launch_down_tile<2, 64, 1>(ta, NT, grid, lds, st);
+        else if (L.down_type == 3) launch_down_tile<3, 64, 1>(ta, NT, grid, lds, st);
+        else launch_down_tile<14, kDownTileRowsQ6K, 1>(ta, NT, grid, lds, st);
+    } else {
+        if (L.down_type == 2) launch_down_tile<2, 64, 0>(ta, NT, grid, lds, st);
+        else if (L.down_type == 3) launch_down_tile<3, 64, 0>(ta, NT, grid, lds, st);
+        else launch_down_tile<14, kDownTileRowsQ6K, 0>(ta, NT, grid, lds, st);
+    }
     const int n = T * s.E;
     QLAUNCH("combine", combine_kernel, dim3((n + 255) / 256), dim3(256), 0, st, S, s.E, s.K, T, out);
     return hipGetLastError();
