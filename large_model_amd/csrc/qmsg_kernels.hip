@@ -2172,20 +2172,36 @@ __global__ __launch_bounds__(64 * W) void dense_kernel(DenseArgs a)
 /* One block pair of a Q4_0 (TYPE 2) or Q4_1 (TYPE 3) row for lane k of an octet: the lane keeps
  * the reference's FMA chain k (elements 4k..4k+3 of each block, src/kernels.c:82-94, 109-121)
  * and the offset chain. */
-template <int TYPE>
-__device__ __forceinline__ void oct_pair(const uint32_t *W, int k, const uint8_t *xp, float &acc, float &corr)
-{
-    const int p = k & 3, hi = k >> 2;
-    const XPair x = x_load(xp, p);
-    const uint32_t xb = hi ? x.q.y : x.q.x, xb1 = hi ? x.q.w : x.q.z;
+/* The LDS words one lane of an octet needs for a pair of 32-blocks, then its arithmetic:
+ * split so that a loop can request the next pairs before summing the current one. */
+struct OctIn {
+    XPair x;
     uint32_t c0, c1, wa, wb;
+};
+
+template <int TYPE>
+__device__ __forceinline__ OctIn oct_load(const uint32_t *W, int k, const uint8_t *xp)
+{
+    const int p = k & 3;
+    OctIn r;
+    r.x = x_load(xp, p);
     if (TYPE == 3) {
         const Q41Pair w = q4_1_load(W, p);
-        c0 = w.c0; c1 = w.c1; wa = w.w0; wb = w.w5;
+        r.c0 = w.c0; r.c1 = w.c1; r.wa = w.w0; r.wb = w.w5;
     } else {
         const Q4Pair w = q4_0_load(W, p);
-        c0 = w.c0; c1 = w.c1; wa = w.w0; wb = w.w4;
+        r.c0 = w.c0; r.c1 = w.c1; r.wa = w.w0; r.wb = w.w4;
     }
+    return r;
+}
+
+template <int TYPE>
+__device__ __forceinline__ void oct_math(const OctIn &in, int k, float &acc, float &corr)
+{
+    const int hi = k >> 2;
+    const XPair &x = in.x;
+    const uint32_t xb = hi ? x.q.y : x.q.x, xb1 = hi ? x.q.w : x.q.z;
+    const uint32_t c0 = in.c0, c1 = in.c1, wa = in.wa, wb = in.wb;
     const uint32_t n0 = (hi ? c0 >> 4 : c0) & 0x0f0f0f0fu, n1 = (hi ? c1 >> 4 : c1) & 0x0f0f0f0fu;
     const int s0 = sdot4((int)n0, (int)xb), s1 = sdot4((int)n1, (int)xb1);
     float m0, m1, o0, o1;
@@ -2206,6 +2222,12 @@ __device__ __forceinline__ void oct_pair(const uint32_t *W, int k, const uint8_t
     corr = __builtin_fmaf(o1, x.d.w, corr);
 }
 
+template <int TYPE>
+__device__ __forceinline__ void oct_pair(const uint32_t *W, int k, const uint8_t *xp, float &acc, float &corr)
+{
+    oct_math<TYPE>(oct_load<TYPE>(W, k, xp), k, acc, corr);
+}
+
 /* hsum256 over the octet (s_j = a_j + a_{j+4}, then (s0+s2)+(s1+s3)) and the unfused offset
  * term, as quad_finish. Valid on lane k == 0. */
 __device__ __forceinline__ float oct_finish(float acc, float corr, float scale)
@@ -2220,10 +2242,9 @@ __device__ __forceinline__ float oct_finish(float acc, float corr, float scale)
  * chain), so a wave streams 8 rows and a launch has twice the waves, each with half the bytes.
  * The trunk's one-token launches have few rows (attn_k/v: 512), and each wave's stream is a
  * serial chain of chunk waits, so more and shorter streams finish sooner. */
-constexpr int kDenseOctXB = 4;     /* input 32-blocks per lane held in registers (cols <= 8192) */
 
-template <int TYPE, int CB, int D>
-__global__ __launch_bounds__(64) void dense_oct_kernel(DenseArgs a)
+template <int TYPE, int CB, int D, int W>
+__global__ __launch_bounds__(64 * W) void dense_oct_kernel(DenseArgs a)
 {
     extern __shared__ __align__(16) uint8_t smem[];
     constexpr int BB = TYPE == 3 ? 20 : 18;           /* bytes per 32-block                   */
@@ -2231,17 +2252,19 @@ __global__ __launch_bounds__(64) void dense_oct_kernel(DenseArgs a)
     constexpr int NSL = 8 * SPR;                      /* slots of the wave's chunk            */
     constexpr int SPT = (NSL + 63) / 64;              /* slots per lane per chunk             */
     constexpr int WS = CB * BB + ((SPR & 1) ? 0 : 16);/* LDS row stride, odd in 16-byte units */
+    constexpr int NTH = 64 * W;
     const int nb = a.C >> 5, nP = nb >> 1, nchunk = nb / CB;
-    const int lane = threadIdx.x, rr = lane >> 3, k = lane & 7;
-    uint8_t *wbuf = smem;
-    uint8_t *xbuf = smem + 8 * WS;
+    const int tid = threadIdx.x, lane = tid & 63, rr = lane >> 3, k = lane & 7;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    uint8_t *wbuf = smem + wave * 8 * WS;
+    uint8_t *xbuf = smem + W * 8 * WS;
 
     int mi = 0;
 #pragma unroll
     for (int i = 1; i < kDenseMats; i++)
         if (i < a.nm && (int)blockIdx.x >= a.m[i].first_block) mi = i;
     const DenseMat M = a.m[mi];
-    const int rw = ((int)blockIdx.x - M.first_block) * 8;                 /* the wave's first row */
+    const int rw = ((int)blockIdx.x - M.first_block) * 8 * W + 8 * wave;   /* the wave's first row */
     const uint8_t *wbase = M.w + (size_t)min(rw, M.rows - 1) * a.rb;
     const int last = M.rows - 1 - min(rw, M.rows - 1);
     u32x4 wv[D][SPT];
@@ -2253,33 +2276,28 @@ __global__ __launch_bounds__(64) void dense_oct_kernel(DenseArgs a)
         }
     };
     /* the input row first, then the weights: loads complete in order, so quantising the row
-     * waits only for its own bytes while the first chunks are still on the way */
-    constexpr int XB = kDenseOctXB;
-    float4 xr[XB][8];
+     * waits only for its own bytes while the first chunks are still on the way. The block's
+     * W waves share one quantisation of the row (one 32-block per thread, then any rest). */
+    float4 xr[8];
+    {
+        const float4 *src = (const float4 *)(a.x + (size_t)min(tid, nb - 1) * 32);
 #pragma unroll
-    for (int u = 0; u < XB; u++) {
-        const float4 *src = (const float4 *)(a.x + (size_t)min(lane + 64 * u, nb - 1) * 32);
-#pragma unroll
-        for (int j = 0; j < 8; j++) xr[u][j] = src[j];
+        for (int j = 0; j < 8; j++) xr[j] = src[j];
     }
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int d = 0; d < D; d++)
         if (d < nchunk) load_chunk(d, wv[d]);
     __builtin_amdgcn_sched_barrier(0);
+    if (tid < nb) {
+        float v[32];
 #pragma unroll
-    for (int u = 0; u < XB; u++) {
-        const int b = lane + 64 * u;
-        if (b < nb) {
-            float v[32];
-#pragma unroll
-            for (int j = 0; j < 8; j++) {
-                v[4 * j] = xr[u][j].x; v[4 * j + 1] = xr[u][j].y; v[4 * j + 2] = xr[u][j].z; v[4 * j + 3] = xr[u][j].w;
-            }
-            store_pair_half(quantize_block(v), (uint32_t *)(xbuf + (size_t)(b >> 1) * kPairBytes), b & 1);
+        for (int j = 0; j < 8; j++) {
+            v[4 * j] = xr[j].x; v[4 * j + 1] = xr[j].y; v[4 * j + 2] = xr[j].z; v[4 * j + 3] = xr[j].w;
         }
+        store_pair_half(quantize_block(v), (uint32_t *)(xbuf + (size_t)(tid >> 1) * kPairBytes), tid & 1);
     }
-    for (int b = lane + 64 * XB; b < nb; b += 64) {   /* rows longer than the register share */
+    for (int b = tid + NTH; b < nb; b += NTH) {       /* rows longer than one block per thread */
         float v[32];
         const float4 *src = (const float4 *)(a.x + (size_t)b * 32);
         for (int j = 0; j < 8; j++) {
@@ -2288,6 +2306,8 @@ __global__ __launch_bounds__(64) void dense_oct_kernel(DenseArgs a)
         }
         store_pair_half(quantize_block(v), (uint32_t *)(xbuf + (size_t)(b >> 1) * kPairBytes), b & 1);
     }
+    if (W > 1) __syncthreads();
+    else wave_sync();
     float acc = 0.0f, corr = 0.0f;
     for (int c0 = 0; c0 < nchunk; c0 += D) {
 #pragma unroll
@@ -2303,9 +2323,20 @@ __global__ __launch_bounds__(64) void dense_oct_kernel(DenseArgs a)
                 wave_sync();
                 if (c + D < nchunk) load_chunk(c + D, wv[d]);
                 const uint32_t *Wrow = (const uint32_t *)(wbuf + rr * WS);
-#pragma unroll 4
-                for (int q = 0; q < CB / 2; q++)
-                    oct_pair<TYPE>(Wrow + q * (BB * 2 / 4), k, xbuf + (size_t)(c * (CB / 2) + q) * kPairBytes, acc, corr);
+                /* four pairs' LDS words requested before their arithmetic (one wave per SIMD
+                 * leaves each read's latency otherwise exposed) */
+                constexpr int PB = CB / 2 >= 4 ? 4 : CB / 2;
+#pragma unroll
+                for (int q0 = 0; q0 < CB / 2; q0 += PB) {
+                    OctIn in[PB];
+#pragma unroll
+                    for (int u = 0; u < PB; u++)
+                        in[u] = oct_load<TYPE>(Wrow + (q0 + u) * (BB * 2 / 4), k,
+                                               xbuf + (size_t)(c * (CB / 2) + q0 + u) * kPairBytes);
+                    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                    for (int u = 0; u < PB; u++) oct_math<TYPE>(in[u], k, acc, corr);
+                }
             }
         }
     }
@@ -2333,21 +2364,32 @@ hipError_t launch_dense(const DenseArgs &args, int type, uint8_t *xqk, hipStream
     /* one wave per block, 16 rows each: the trunk's small matrices (attn_k/v: 512 rows) still
      * spread over 32 CUs, the large ones over every CU */
     if (a.T == 1) {                                   /* eight lanes per row, 8 rows per wave */
-        int nb8 = 0;
+        /* W waves per block share the input row's quantisation: the most that still gives
+         * every CU a block */
+        int rows = 0;
+        for (int i = 0; i < a.nm; i++) rows += a.m[i].rows;
+        const int W = rows >= 256 * 32 ? 4 : (rows >= 256 * 16 ? 2 : 1);
+        int nbw = 0;
         for (int i = 0; i < a.nm; i++) {
-            a.m[i].first_block = nb8;
-            nb8 += (a.m[i].rows + 7) / 8;
+            a.m[i].first_block = nbw;
+            nbw += (a.m[i].rows + 8 * W - 1) / (8 * W);
         }
         const int CB = nb % 16 == 0 ? 16 : 8, bb = type == 3 ? 20 : 18;
         const size_t ws = (size_t)CB * bb + (((CB * bb / 16) & 1) ? 0 : 16);
-        const size_t lds8 = 8 * ws + (size_t)(nb / 2) * kPairBytes;
-        if (type == 3) {
-            if (CB == 16) QLAUNCH("dense", (dense_oct_kernel<3, 16, 2>), dim3(nb8), dim3(64), lds8, st, a);
-            else QLAUNCH("dense", (dense_oct_kernel<3, 8, 2>), dim3(nb8), dim3(64), lds8, st, a);
-        } else {
-            if (CB == 16) QLAUNCH("dense", (dense_oct_kernel<2, 16, 2>), dim3(nb8), dim3(64), lds8, st, a);
-            else QLAUNCH("dense", (dense_oct_kernel<2, 8, 2>), dim3(nb8), dim3(64), lds8, st, a);
-        }
+        const size_t lds8 = (size_t)W * 8 * ws + (size_t)(nb / 2) * kPairBytes;
+        auto go = [&](auto tw) {
+            constexpr int WW = decltype(tw)::value;
+            if (type == 3) {
+                if (CB == 16) QLAUNCH("dense", (dense_oct_kernel<3, 16, 2, WW>), dim3(nbw), dim3(64 * WW), lds8, st, a);
+                else QLAUNCH("dense", (dense_oct_kernel<3, 8, 2, WW>), dim3(nbw), dim3(64 * WW), lds8, st, a);
+            } else {
+                if (CB == 16) QLAUNCH("dense", (dense_oct_kernel<2, 16, 2, WW>), dim3(nbw), dim3(64 * WW), lds8, st, a);
+                else QLAUNCH("dense", (dense_oct_kernel<2, 8, 2, WW>), dim3(nbw), dim3(64 * WW), lds8, st, a);
+            }
+        };
+        if (W == 4) go(std::integral_constant<int, 4>());
+        else if (W == 2) go(std::integral_constant<int, 2>());
+        else go(std::integral_constant<int, 1>());
         return hipGetLastError();
     }
     int nblk = 0;
