@@ -2345,6 +2345,119 @@ __global__ __launch_bounds__(64 * W) void dense_oct_kernel(DenseArgs a)
 }
 
 /* Two chunks in flight per wave (2, 4 and 8 were measured at the trunk's shapes: 2 fastest). */
+/* Batches of two or more tokens: a block owns 16 rows (one per lane quad) and stages each
+ * chunk of them once into LDS for its W waves; wave w computes tokens w*NT .. w*NT+NT-1 of the
+ * pass (W*NT tokens per pass, the rows streamed once per pass). A block's waves thus share the
+ * weight bytes, and a launch has W times the waves of one wave doing every token, which keeps
+ * the per-lane reference chains (src/quant.c:151-169, qms_vec_dot_q8) spread over every SIMD.
+ * Chunk c sits in buffer c % D; one block barrier per chunk both publishes it and, with
+ * D >= 2, guarantees every wave is done with the chunk that last used that buffer. */
+template <int TYPE, int CB, int D, int W, int NT>
+__global__ __launch_bounds__(64 * W) void dense_tok_kernel(DenseArgs a)
+{
+    extern __shared__ __align__(16) uint8_t smem[];
+    constexpr int BB = TYPE == 3 ? 20 : 18;           /* bytes per 32-block                   */
+    constexpr int NTH = 64 * W, TP = W * NT;
+    constexpr int SPR = CB * BB / 16;                 /* 16-byte slots per row per chunk      */
+    constexpr int NSL = 16 * SPR;                     /* slots of one chunk (16 rows)         */
+    constexpr int SPT = (NSL + NTH - 1) / NTH;        /* slots per thread per chunk           */
+    constexpr int WS = CB * BB + ((SPR & 1) ? 0 : 16);/* LDS row stride, odd in 16-byte units */
+    const int nb = a.C >> 5, nP = nb >> 1, nchunk = nb / CB;
+    const int tid = threadIdx.x, lane = tid & 63, qd = lane >> 2, p = lane & 3;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    uint8_t *wbuf = smem;                             /* [D][16][WS]                          */
+    uint8_t *xbuf = smem + D * 16 * WS;               /* [TP][nP][96]                         */
+
+    int mi = 0;
+#pragma unroll
+    for (int i = 1; i < kDenseMats; i++)
+        if (i < a.nm && (int)blockIdx.x >= a.m[i].first_block) mi = i;
+    const DenseMat M = a.m[mi];
+    const int r0 = ((int)blockIdx.x - M.first_block) * 16;
+    const uint8_t *wbase = M.w + (size_t)min(r0, M.rows - 1) * a.rb;
+    const int last = M.rows - 1 - min(r0, M.rows - 1);
+    u32x4 wv[D][SPT];
+    auto load_chunk = [&](int c, u32x4 *dst) {
+#pragma unroll
+        for (int m = 0; m < SPT; m++) {
+            const int i = min(tid + NTH * m, NSL - 1), row = i / SPR, j = i - row * SPR;
+            dst[m] = *(const u32x4 *)(wbase + (size_t)min(row, last) * a.rb + (size_t)c * CB * BB + 16 * j);
+        }
+    };
+    const int row = r0 + qd, tw0 = wave * NT;
+    for (int t0 = 0; t0 < a.T; t0 += TP) {
+        const int ntp = min(TP, a.T - t0), ntw = max(0, min(NT, ntp - tw0));
+#pragma unroll
+        for (int d = 0; d < D; d++)
+            if (d < nchunk) load_chunk(d, wv[d]);
+        if (t0 > 0) __syncthreads();                  /* the previous pass is done with LDS   */
+        if (a.xqk) {                                  /* records formed by dense_quant_kernel */
+            for (int i = tid; i < ntp * nP * 6; i += NTH)
+                ((u32x4 *)xbuf)[i] = ((const u32x4 *)(a.xqk + (size_t)t0 * nP * kPairBytes))[i];
+        } else {
+            for (int i = tid; i < ntp * nb; i += NTH) {
+                const int n = i / nb, blk = i - n * nb;
+                float v[32];
+                const float4 *src = (const float4 *)(a.x + (size_t)(t0 + n) * a.C + (size_t)blk * 32);
+#pragma unroll
+                for (int j = 0; j < 8; j++) {
+                    const float4 f = src[j];
+                    v[4 * j] = f.x; v[4 * j + 1] = f.y; v[4 * j + 2] = f.z; v[4 * j + 3] = f.w;
+                }
+                store_pair_half(quantize_block(v), (uint32_t *)(xbuf + ((size_t)n * nP + (blk >> 1)) * kPairBytes),
+                                blk & 1);
+            }
+        }
+        RowAcc acc[NT];
+        for (int n = 0; n < NT; n++) acc[n] = RowAcc{ 0.0f, 0.0f, 0.0f };
+        for (int c0 = 0; c0 < nchunk; c0 += D) {
+#pragma unroll
+            for (int d = 0; d < D; d++) {
+                const int c = c0 + d;
+                if (c < nchunk) {
+                    uint8_t *cb = wbuf + d * 16 * WS;
+#pragma unroll
+                    for (int m = 0; m < SPT; m++) {
+                        const int i = tid + NTH * m;
+                        if (i < NSL) {
+                            const int r = i / SPR, j = i - r * SPR;
+                            *(u32x4 *)(cb + r * WS + 16 * j) = wv[d][m];
+                        }
+                    }
+                    __syncthreads();
+                    if (c + D < nchunk) load_chunk(c + D, wv[d]);
+                    if (ntw > 0) {
+                        if (TYPE == 3)
+                            q4_1_rows<NT, (NT >= 4 ? 1 : (NT == 2 ? 2 : 4))>((const uint32_t *)(cb + qd * WS), p,
+                                                                              xbuf + (size_t)tw0 * nP * kPairBytes,
+                                                                              (size_t)nP * kPairBytes, c * (CB / 2),
+                                                                              CB / 2, ntw, acc);
+                        else
+                            q4_0_rows<NT, (NT >= 4 ? 1 : (NT == 2 ? 2 : 4))>((const uint32_t *)(cb + qd * WS), p,
+                                                                              xbuf + (size_t)tw0 * nP * kPairBytes,
+                                                                              (size_t)nP * kPairBytes, c * (CB / 2),
+                                                                              CB / 2, ntw, acc);
+                    }
+                }
+            }
+        }
+#pragma unroll
+        for (int n = 0; n < NT; n++) {
+            const float v = quad_finish(acc[n], finish_scale(TYPE));
+            if (p == 0 && n < ntw && row < M.rows) M.y[(size_t)(t0 + tw0 + n) * M.rows + row] = v;
+        }
+    }
+}
+
+/* Tokens per wave of dense_tok_kernel's passes for a batch of T (four waves per block), and
+ * its LDS bytes. */
+constexpr int kDenseTokW = 4;
+static size_t dense_tok_lds(int NT, int CB, int bb, int nb)
+{
+    const size_t ws = (size_t)CB * bb + (((CB * bb / 16) & 1) ? 0 : 16);
+    return 2 * 16 * ws + (size_t)kDenseTokW * NT * (nb / 2) * kPairBytes;
+}
+
 template <int TYPE, int NT>
 static void launch_dense_t(const DenseArgs &a, int CB, dim3 grid, size_t lds, hipStream_t st)
 {
@@ -2396,6 +2509,30 @@ hipError_t launch_dense(const DenseArgs &args, int type, uint8_t *xqk, hipStream
     for (int i = 0; i < a.nm; i++) {
         a.m[i].first_block = nblk;
         nblk += (a.m[i].rows + 15) / 16;
+    }
+    {
+        /* four waves sharing each block's 16 rows, NT tokens each: the smallest NT whose pass
+         * covers the batch, as long as the records fit in LDS */
+        const int CB = nb % 16 == 0 ? 16 : 8, bb = type == 3 ? 20 : 18;
+        int NT = a.T <= kDenseTokW ? 1 : (a.T <= 2 * kDenseTokW ? 2 : 4);
+        while (NT > 1 && dense_tok_lds(NT, CB, bb, nb) > 160 * 1024) NT >>= 1;
+        const size_t lds = dense_tok_lds(NT, CB, bb, nb);
+        if (lds <= 160 * 1024) {
+            const dim3 grid(nblk), block(64 * kDenseTokW);
+            auto go = [&](auto ty, auto nt) {
+                constexpr int TY = decltype(ty)::value, N = decltype(nt)::value;
+                if (CB == 16) QLAUNCH("dense", (dense_tok_kernel<TY, 16, 2, kDenseTokW, N>), grid, block, lds, st, a);
+                else QLAUNCH("dense", (dense_tok_kernel<TY, 8, 2, kDenseTokW, N>), grid, block, lds, st, a);
+            };
+            auto by_nt = [&](auto ty) {
+                if (NT == 4) go(ty, std::integral_constant<int, 4>());
+                else if (NT == 2) go(ty, std::integral_constant<int, 2>());
+                else go(ty, std::integral_constant<int, 1>());
+            };
+            if (type == 3) by_nt(std::integral_constant<int, 3>());
+            else by_nt(std::integral_constant<int, 2>());
+            return hipGetLastError();
+        }
     }
     const int NT = a.T >= 4 ? 4 : (a.T >= 2 ? 2 : 1);
     const int CB = nb % 16 == 0 ? 16 : 8;
