@@ -281,20 +281,25 @@ def run_stack(args, w):
     print(json.dumps(result), flush=True)
 
 
+TRUNK_TYPES = {"f32": qmsg.QMSG_T_F32, "q4_0": qmsg.QMSG_T_Q4_0, "q4_1": qmsg.QMSG_T_Q4_1, "q6_k": qmsg.QMSG_T_Q6_K}
+
+
 def run_trunk(args):
     """A step is the dense products of the 235B trunk for every resident layer (src/model.c:442,
     494): q/k/v in one qms_matmul_n call ([8192 | 512 | 512] x 4096, Q4_0), then attn_output
-    (4096 x 8192, Q4_0), on T tokens. Attention itself is not part of this library."""
+    (4096 x 8192), on T tokens, all in one type (Q4_0 unless --trunk-type says otherwise).
+    Attention itself is not part of this library."""
     E, H, KV, NL, T = 4096, 8192, 512, args.trunk, args.tokens
+    TT = TRUNK_TYPES[args.trunk_type]
     K_steps, W_steps = args.steps, args.warmup
-    log(f"trunk q/k/v/o: {NL} resident layers, T={T}")
+    log(f"trunk q/k/v/o: {NL} resident layers, T={T}, {args.trunk_type}")
     ctx = qmsg.Context(256, 16, 4, 128, max_tokens=1)
     layers = []
     for l in range(NL):
-        q = ctx.mat_synth(qmsg.QMSG_T_Q4_0, H, E, 100 + 4 * l)
-        k = ctx.mat_synth(qmsg.QMSG_T_Q4_0, KV, E, 101 + 4 * l)
-        v = ctx.mat_synth(qmsg.QMSG_T_Q4_0, KV, E, 102 + 4 * l)
-        o = ctx.mat_synth(qmsg.QMSG_T_Q4_0, E, H, 103 + 4 * l)
+        q = ctx.mat_synth(TT, H, E, 100 + 4 * l)
+        k = ctx.mat_synth(TT, KV, E, 101 + 4 * l)
+        v = ctx.mat_synth(TT, KV, E, 102 + 4 * l)
+        o = ctx.mat_synth(TT, E, H, 103 + 4 * l)
         layers.append((q, k, v, o))
     d_x = ctx.device_alloc(T * E * 4)
     d_a = ctx.device_alloc(T * H * 4)
@@ -324,8 +329,8 @@ def run_trunk(args):
         if n:
             kern[name] = {"launches": n, "avg_us": round(1e3 * ms / n, 3)}
     ctx.profile(False)
-    rb = qmsg.row_bytes(qmsg.QMSG_T_Q4_0, E)
-    layer_bytes = (H + 2 * KV) * rb + E * qmsg.row_bytes(qmsg.QMSG_T_Q4_0, H)
+    rb = qmsg.row_bytes(TT, E)
+    layer_bytes = (H + 2 * KV) * rb + E * qmsg.row_bytes(TT, H)
     us_layer = 1e6 * el / K_steps / NL
     d_us = kern["dense"]["avg_us"]
     dense_bytes = layer_bytes / 2                     # per dense launch on average (q/k/v, then o)
@@ -333,8 +338,10 @@ def run_trunk(args):
     result = {
         "metric": "trunk q/k/v/o dense products: us per layer + achieved HBM GB/s",
         "value": round(us_layer, 3), "unit": "us/layer", "higher_is_better": False, "n_gpus": 1,
-        "steps": K_steps, "warmup": W_steps, "dtype": "int8", "data": "synthetic",
-        "config": {"workload": f"Qwen3-235B-A22B trunk q/k/v/o shapes (Q4_0), {NL} resident layers", "T": T},
+        "steps": K_steps, "warmup": W_steps, "dtype": "f32" if TT == qmsg.QMSG_T_F32 else "int8",
+        "data": "synthetic",
+        "config": {"workload": f"Qwen3-235B-A22B trunk q/k/v/o shapes ({args.trunk_type}), {NL} resident layers",
+                   "T": T},
         "layer_bytes": layer_bytes, "achieved_GBps_layer": round(layer_bytes / (us_layer * 1e-6) / 1e9, 1),
         "roofline": {"kernel": "dense (row dots, average of the q/k/v and o launches)", "bound": "hbm",
                      "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
@@ -342,12 +349,12 @@ def run_trunk(args):
         "kernels": kern, "cpu_baseline": None,
     }
     if not args.no_cpu:
-        result["cpu_baseline"] = cpu_baseline_trunk(T, args.cpu_seconds)
+        result["cpu_baseline"] = cpu_baseline_trunk(T, args.cpu_seconds, TT)
     ctx.close()
     print(json.dumps(result), flush=True)
 
 
-def cpu_baseline_trunk(T: int, seconds: float):
+def cpu_baseline_trunk(T: int, seconds: float, TT: int):
     """The reference's own qms_matmul_n (src/quant.c:128-170) on one layer's q/k/v and o."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import ctypes
@@ -364,10 +371,9 @@ def cpu_baseline_trunk(T: int, seconds: float):
     E, H, KV = 4096, 8192, 512
     bufs, mats = [], []
     for rows, cols, seed in ((H, E, 1), (KV, E, 2), (KV, E, 3), (E, H, 4)):
-        w = np.zeros(rows * qmsg.row_bytes(qmsg.QMSG_T_Q4_0, cols), np.uint8)
-        orc.lib.orc_synth_experts(seed, 0, orc.KIND_GATE, qmsg.QMSG_T_Q4_0, rows, cols, 0, 1, 0.02, w.ctypes.data)
+        w = orc.synth_mat(TT, rows, cols, seed)
         bufs.append(w)
-        mats.append(QmsMat(qmsg.QMSG_T_Q4_0, rows, cols, qmsg.row_bytes(qmsg.QMSG_T_Q4_0, cols), w.ctypes.data))
+        mats.append(QmsMat(TT, rows, cols, qmsg.row_bytes(TT, cols), w.ctypes.data))
     x = orc.make_input(E, T, 5)
     a = orc.make_input(H, T, 6)
     ys = [np.empty((T, m.rows), np.float32) for m in mats]
@@ -455,6 +461,7 @@ def main():
                     help="instead of the MoE layer, time the trunk's q/k/v/o dense products over LAYERS "
                          "resident layers and exit")
     ap.add_argument("--tokens", type=int, default=1, help="tokens per step of --trunk")
+    ap.add_argument("--trunk-type", default="q4_0", choices=sorted(TRUNK_TYPES), help="matrix type of --trunk")
     ap.add_argument("--gguf-load", type=int, default=0, metavar="LAYERS",
                     help="instead of the layer, time loading LAYERS 235B-shape MoE layers from a GGUF file "
                          "into HBM (--steps loads, default 3) and exit")

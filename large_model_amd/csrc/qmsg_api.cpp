@@ -540,11 +540,14 @@ int qmsg_gguf_upload(qmsg_ctx *c, const qmsg_gguf *g, int first, int n)
 
 static int dense_check(qmsg_ctx *c, int type, int64_t rows, int64_t cols, const char *what)
 {
-    if (type != QMSG_T_Q4_0 && type != QMSG_T_Q4_1)
-        return fail(c, QMSG_E_UNSUPPORTED, "%s: the dense kernels take Q4_0 and Q4_1 (got type %d)", what, type);
-    if (rows <= 0 || rows > (1 << 30) || cols <= 0 || cols % 256)
-        return fail(c, QMSG_E_UNSUPPORTED, "%s: needs rows > 0 and cols %% 256 == 0 (got %lld x %lld)", what,
-                    (long long)rows, (long long)cols);
+    /* the types of qms_matmul_n's fast path (src/quant.c:128-170, qms_fast_supported) */
+    if (type != QMSG_T_F32 && type != QMSG_T_Q4_0 && type != QMSG_T_Q4_1 && type != QMSG_T_Q6_K)
+        return fail(c, QMSG_E_UNSUPPORTED, "%s: the dense kernels take F32, Q4_0, Q4_1 and Q6_K (got type %d)", what,
+                    type);
+    const int64_t step = type == QMSG_T_Q6_K ? 2048 : 256;   /* Q6_K: whole chunks of 8 super-blocks */
+    if (rows <= 0 || rows > (1 << 30) || cols <= 0 || cols % step)
+        return fail(c, QMSG_E_UNSUPPORTED, "%s: needs rows > 0 and cols %% %lld == 0 (got %lld x %lld)", what,
+                    (long long)step, (long long)rows, (long long)cols);
     return QMSG_OK;
 }
 
@@ -586,9 +589,14 @@ int qmsg_mat_synth(qmsg_ctx *c, int type, int64_t rows, int64_t cols, uint64_t s
     if (rc) return rc;
     HIP_TRY(c, hipSetDevice(c->device));
     if ((rc = dense_new(c, type, rows, cols, id))) return rc;
-    /* the generator of the expert tensors with one "expert" of kind gate, layer 0 */
-    HIP_TRY(c, launch_synth_experts(seed, 0, QMSG_KIND_GATE, type, rows, cols, 1, sigma, c->mats[(size_t)*id].w,
-                                    c->stream));
+    /* the generator of the expert tensors with one "expert" of kind gate, layer 0 (F32: the
+     * generator's normal values) */
+    if (type == QMSG_T_F32)
+        HIP_TRY(c, launch_synth_f32(qmsg_tensor_key(seed, 0, QMSG_KIND_GATE, 0), (uint64_t)rows * (uint64_t)cols, sigma,
+                                    (float *)c->mats[(size_t)*id].w, c->stream));
+    else
+        HIP_TRY(c, launch_synth_experts(seed, 0, QMSG_KIND_GATE, type, rows, cols, 1, sigma, c->mats[(size_t)*id].w,
+                                        c->stream));
     return QMSG_OK;
 }
 
@@ -598,7 +606,7 @@ int qmsg_gguf_upload_mat(qmsg_ctx *c, const qmsg_gguf *g, const char *name, int 
     const int i = gguf_find(g, name);
     if (i < 0) return fail(c, QMSG_E_INVALID, "model: missing tensor %s", name);
     const qmsg_tensor &t = g->tensors[(size_t)i];
-    if (t.ne[2] != 1 || t.ne[3] != 1)
+    if (t.n_dims != 2 || t.ne[2] != 1 || t.ne[3] != 1)
         return fail(c, QMSG_E_INVALID, "model: %s is not a 2-D matrix (ne=[%lld,%lld,%lld])", name, (long long)t.ne[0],
                     (long long)t.ne[1], (long long)t.ne[2]);
     int rc = dense_check(c, t.type, t.ne[1], t.ne[0], name);

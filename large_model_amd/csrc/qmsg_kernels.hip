@@ -216,6 +216,8 @@ struct RouteArgs {
     const float *router, *xn;
     int E, X, K, T;
     int n_route_wg;    /* blocks doing router dots; the blocks after them quantise the input */
+    float *y;          /* logits: y[t * ystride + e] (the router: S.logits, stride X)        */
+    int ystride;
     Scratch S;
 };
 
@@ -332,7 +334,7 @@ __global__ __launch_bounds__(256) void route_small_kernel(RouteArgs a)
     PHASE(0, 2);
     if (tid < 16 * T) {
         acc = chain16_sum(acc);
-        if (cc == 0) a.S.logits[(size_t)t * a.X + e] = acc;
+        if (cc == 0) a.y[(size_t)t * a.ystride + e] = acc;
     }
 }
 
@@ -351,7 +353,7 @@ __global__ __launch_bounds__(256) void route_big_kernel(RouteArgs a)
     constexpr int EB = 4 * J;                     /* experts per block              */
     const int tid = threadIdx.x, E = a.E, T = a.T, X = a.X;
     constexpr int TB = 4 * KT;                    /* tokens per block               */
-    const int egs = X / EB, tg = (int)blockIdx.x / egs, eg = (int)blockIdx.x - tg * egs;
+    const int egs = (X + EB - 1) / EB, tg = (int)blockIdx.x / egs, eg = (int)blockIdx.x - tg * egs;
     const int t0 = tg * TB, e0 = eg * EB;
     const int c = tid & 15, ea = (tid >> 4) & 3, tb = tid >> 6;
     float *W = (float *)smem, *Xt = W + EB * RS;
@@ -363,7 +365,7 @@ __global__ __launch_bounds__(256) void route_big_kernel(RouteArgs a)
 #pragma unroll
         for (int m = 0; m < J; m++) {
             const int q = tid + 256 * m;
-            w[m] = *(const u32x4 *)(a.router + (size_t)(e0 + (q >> 6)) * E + (size_t)ch * CH + (q & 63) * 4);
+            w[m] = *(const u32x4 *)(a.router + (size_t)min(e0 + (q >> 6), X - 1) * E + (size_t)ch * CH + (q & 63) * 4);
         }
 #pragma unroll
         for (int m = 0; m < KT; m++) {
@@ -408,7 +410,7 @@ __global__ __launch_bounds__(256) void route_big_kernel(RouteArgs a)
         for (int k = 0; k < KT; k++) {
             const float v = chain16_sum(acc[j][k]);
             const int t = t0 + KT * tb + k, e = e0 + J * ea + j;
-            if (c == 0 && t < T) a.S.logits[(size_t)t * X + e] = v;
+            if (c == 0 && t < T && e < X) a.y[(size_t)t * a.ystride + e] = v;
         }
 }
 
@@ -424,6 +426,8 @@ hipError_t launch_route(const Shape &s, const LayerDev &L, const Scratch &S, con
     a.X = s.X;
     a.K = s.K;
     a.T = T;
+    a.y = S.logits;
+    a.ystride = s.X;
     a.S = S;
     const int nq = (T * (s.E / 32) + 255) / 256;
     if (T <= 4 && s.E <= 4096) {
@@ -436,7 +440,7 @@ hipError_t launch_route(const Shape &s, const LayerDev &L, const Scratch &S, con
         else QLAUNCH("route", route_small_kernel<4>, grid, dim3(256), lds, st, a);
     } else {
         const int J = T <= 64 ? 1 : 4;               /* experts and tokens per thread group */
-        a.n_route_wg = ((T + 4 * J - 1) / (4 * J)) * (s.X / (4 * J));
+        a.n_route_wg = ((T + 4 * J - 1) / (4 * J)) * ((s.X + 4 * J - 1) / (4 * J));
         const size_t lds = (size_t)(8 * J) * (256 + 4) * 4;
         if (J == 1) QLAUNCH("route", (route_big_kernel<1, 1, kRouteBigP>), dim3(a.n_route_wg + nq), dim3(256), lds, st, a);
         else QLAUNCH("route", (route_big_kernel<4, 4, kRouteBigP>), dim3(a.n_route_wg + nq), dim3(256), lds, st, a);
@@ -2243,15 +2247,63 @@ __device__ __forceinline__ float oct_finish(float acc, float corr, float scale)
  * The trunk's one-token launches have few rows (attn_k/v: 512), and each wave's stream is a
  * serial chain of chunk waits, so more and shorter streams finish sooner. */
 
+/* Q6_K super-block s of a row's chunk in LDS for octet lane k, against the chunk's pair
+ * records xc: the lane's chain of dot_q6_k (src/kernels.c:148-167) takes bytes 4k..4k+3 of
+ * each 32-block's codes with sub-scale sc[2g] (k < 4) or sc[2g+1] (k >= 4); the offset chain
+ * (corr) runs on every lane alike. A half's words are all requested before its arithmetic.
+ * AL: the super-block starts at a multiple of 4 bytes. */
+template <bool AL>
+__device__ __forceinline__ void q6_k_oct(const uint8_t *Wr, int s, int k, const uint8_t *xc, float &acc, float &corr)
+{
+    const int p = k & 3, hi = k >> 2;
+    const uint32_t sb = (uint32_t)(s * 210);
+    const float d = h2f(*(const uint16_t *)(Wr + sb + 208));
+#pragma unroll
+    for (int h = 0; h < 2; h++) {
+        const uint32_t ql0 = lds_word<AL>(Wr, sb + 64 * h + 4 * k), ql1 = lds_word<AL>(Wr, sb + 64 * h + 32 + 4 * k);
+        const uint32_t qh = lds_word<AL>(Wr, sb + 128 + 32 * h + 4 * k);
+        const uint32_t sc0 = lds_word<AL>(Wr, sb + 192 + 8 * h), sc1 = lds_word<AL>(Wr, sb + 196 + 8 * h);
+        const uint8_t *xp = xc + (size_t)(4 * s + 2 * h) * kPairBytes;   /* blocks 8s+4h .. +3 */
+        uint32_t xq[4];
+        float4 xd[2];
+        uint2 x16[2];
+#pragma unroll
+        for (int g = 0; g < 4; g++) xq[g] = *(const uint32_t *)(xp + (g >> 1) * kPairBytes + 16 * p + 8 * (g & 1) + 4 * hi);
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+            xd[j] = *(const float4 *)(xp + j * kPairBytes + 64);
+            x16[j] = *(const uint2 *)(xp + j * kPairBytes + 80);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int g = 0; g < 4; g++) {
+            const uint32_t ql = (g & 1) ? ql1 : ql0;
+            const uint32_t nib = g < 2 ? (ql & 0x0f0f0f0fu) : ((ql >> 4) & 0x0f0f0f0fu);
+            const uint32_t q6 = nib | (((qh >> (2 * g)) & 0x03030303u) << 4);
+            const uint32_t scw = (g < 2 ? sc0 : sc1) >> (16 * (g & 1));
+            const int sa = (int)(int8_t)(scw & 0xff), sbv = (int)(int8_t)((scw >> 8) & 0xff);
+            const float xdv = (g & 1) ? xd[g >> 1].z : xd[g >> 1].x;
+            const uint32_t s16 = (g & 1) ? x16[g >> 1].y : x16[g >> 1].x;
+            const int s16a = (int)(int16_t)(s16 & 0xffffu), s16b = (int)(int16_t)(s16 >> 16);
+            const float dd = d * xdv;
+            acc = __builtin_fmaf((float)(sdot4((int)q6, (int)xq[g]) * (hi ? sbv : sa)), dd, acc);
+            corr = __builtin_fmaf(dd, (float)(sa * s16a + sbv * s16b), corr);
+        }
+    }
+}
+
 template <int TYPE, int CB, int D, int W>
 __global__ __launch_bounds__(64 * W) void dense_oct_kernel(DenseArgs a)
 {
     extern __shared__ __align__(16) uint8_t smem[];
-    constexpr int BB = TYPE == 3 ? 20 : 18;           /* bytes per 32-block                   */
-    constexpr int SPR = CB * BB / 16;                 /* 16-byte slots per row per chunk      */
+    constexpr int BB = TYPE == 3 ? 20 : 18;           /* bytes per 32-block (Q4_0, Q4_1)      */
+    /* one row's chunk: CB 32-blocks (Q6_K: CB/8 super-blocks, CB = 64 keeps 16-byte slots) */
+    constexpr int RCB = TYPE == 14 ? CB / 8 * 210 : CB * BB;
+    constexpr int SPR = RCB / 16;                     /* 16-byte slots per row per chunk      */
+    static_assert(RCB % 16 == 0, "chunk rows are whole 16-byte slots");
     constexpr int NSL = 8 * SPR;                      /* slots of the wave's chunk            */
     constexpr int SPT = (NSL + 63) / 64;              /* slots per lane per chunk             */
-    constexpr int WS = CB * BB + ((SPR & 1) ? 0 : 16);/* LDS row stride, odd in 16-byte units */
+    constexpr int WS = RCB + ((SPR & 1) ? 0 : 16);    /* LDS row stride, odd in 16-byte units */
     constexpr int NTH = 64 * W;
     const int nb = a.C >> 5, nP = nb >> 1, nchunk = nb / CB;
     const int tid = threadIdx.x, lane = tid & 63, rr = lane >> 3, k = lane & 7;
@@ -2272,7 +2324,7 @@ __global__ __launch_bounds__(64 * W) void dense_oct_kernel(DenseArgs a)
 #pragma unroll
         for (int m = 0; m < SPT; m++) {
             const int i = min(lane + 64 * m, NSL - 1), row = i / SPR, j = i - row * SPR;
-            dst[m] = *(const u32x4 *)(wbase + (size_t)min(row, last) * a.rb + (size_t)c * CB * BB + 16 * j);
+            dst[m] = *(const u32x4 *)(wbase + (size_t)min(row, last) * a.rb + (size_t)c * RCB + 16 * j);
         }
     };
     /* the input row first, then the weights: loads complete in order, so quantising the row
@@ -2322,20 +2374,29 @@ __global__ __launch_bounds__(64 * W) void dense_oct_kernel(DenseArgs a)
                 }
                 wave_sync();
                 if (c + D < nchunk) load_chunk(c + D, wv[d]);
-                const uint32_t *Wrow = (const uint32_t *)(wbuf + rr * WS);
-                /* four pairs' LDS words requested before their arithmetic (one wave per SIMD
-                 * leaves each read's latency otherwise exposed) */
-                constexpr int PB = CB / 2 >= 4 ? 4 : CB / 2;
+                if constexpr (TYPE == 14) {
+                    const uint8_t *xc = xbuf + (size_t)c * (CB / 2) * kPairBytes;
+#pragma unroll 1
+                    for (int sbi = 0; sbi < CB / 8; sbi += 2) {   /* even super-blocks 4-aligned */
+                        q6_k_oct<true>(wbuf + rr * WS, sbi, k, xc, acc, corr);
+                        q6_k_oct<false>(wbuf + rr * WS, sbi + 1, k, xc, acc, corr);
+                    }
+                } else {
+                    const uint32_t *Wrow = (const uint32_t *)(wbuf + rr * WS);
+                    /* four pairs' LDS words requested before their arithmetic (one wave per
+                     * SIMD leaves each read's latency otherwise exposed) */
+                    constexpr int PB = CB / 2 >= 4 ? 4 : CB / 2;
 #pragma unroll
-                for (int q0 = 0; q0 < CB / 2; q0 += PB) {
-                    OctIn in[PB];
+                    for (int q0 = 0; q0 < CB / 2; q0 += PB) {
+                        OctIn in[PB];
 #pragma unroll
-                    for (int u = 0; u < PB; u++)
-                        in[u] = oct_load<TYPE>(Wrow + (q0 + u) * (BB * 2 / 4), k,
-                                               xbuf + (size_t)(c * (CB / 2) + q0 + u) * kPairBytes);
-                    __builtin_amdgcn_sched_barrier(0);
+                        for (int u = 0; u < PB; u++)
+                            in[u] = oct_load<TYPE>(Wrow + (q0 + u) * (BB * 2 / 4), k,
+                                                   xbuf + (size_t)(c * (CB / 2) + q0 + u) * kPairBytes);
+                        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-                    for (int u = 0; u < PB; u++) oct_math<TYPE>(in[u], k, acc, corr);
+                        for (int u = 0; u < PB; u++) oct_math<TYPE>(in[u], k, acc, corr);
+                    }
                 }
             }
         }
@@ -2356,12 +2417,16 @@ template <int TYPE, int CB, int D, int W, int NT>
 __global__ __launch_bounds__(64 * W) void dense_tok_kernel(DenseArgs a)
 {
     extern __shared__ __align__(16) uint8_t smem[];
-    constexpr int BB = TYPE == 3 ? 20 : 18;           /* bytes per 32-block                   */
+    constexpr int BB = TYPE == 3 ? 20 : 18;           /* bytes per 32-block (Q4_0, Q4_1)      */
+    /* one row's chunk: CB 32-blocks (Q6_K: CB/8 super-blocks of 210 bytes, CB = 64 keeps it a
+     * whole number of 16-byte slots) */
+    constexpr int RCB = TYPE == 14 ? CB / 8 * 210 : CB * BB;
     constexpr int NTH = 64 * W, TP = W * NT;
-    constexpr int SPR = CB * BB / 16;                 /* 16-byte slots per row per chunk      */
+    constexpr int SPR = RCB / 16;                     /* 16-byte slots per row per chunk      */
+    static_assert(RCB % 16 == 0, "chunk rows are whole 16-byte slots");
     constexpr int NSL = 16 * SPR;                     /* slots of one chunk (16 rows)         */
     constexpr int SPT = (NSL + NTH - 1) / NTH;        /* slots per thread per chunk           */
-    constexpr int WS = CB * BB + ((SPR & 1) ? 0 : 16);/* LDS row stride, odd in 16-byte units */
+    constexpr int WS = RCB + ((SPR & 1) ? 0 : 16);    /* LDS row stride, odd in 16-byte units */
     const int nb = a.C >> 5, nP = nb >> 1, nchunk = nb / CB;
     const int tid = threadIdx.x, lane = tid & 63, qd = lane >> 2, p = lane & 3;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -2381,7 +2446,7 @@ __global__ __launch_bounds__(64 * W) void dense_tok_kernel(DenseArgs a)
 #pragma unroll
         for (int m = 0; m < SPT; m++) {
             const int i = min(tid + NTH * m, NSL - 1), row = i / SPR, j = i - row * SPR;
-            dst[m] = *(const u32x4 *)(wbase + (size_t)min(row, last) * a.rb + (size_t)c * CB * BB + 16 * j);
+            dst[m] = *(const u32x4 *)(wbase + (size_t)min(row, last) * a.rb + (size_t)c * RCB + 16 * j);
         }
     };
     const int row = r0 + qd, tw0 = wave * NT;
@@ -2426,7 +2491,34 @@ __global__ __launch_bounds__(64 * W) void dense_tok_kernel(DenseArgs a)
                     }
                     __syncthreads();
                     if (c + D < nchunk) load_chunk(c + D, wv[d]);
-                    if (ntw > 0) {
+                    if (ntw > 0 && TYPE == 14) {
+                        /* super-block k of the chunk: Q6_K rows as the expert tile kernel
+                         * reads them (an even super-block starts 4-byte aligned: WS and 420
+                         * are multiples of 4) */
+                        const uint8_t *xw = xbuf + (size_t)tw0 * nP * kPairBytes;
+                        auto superblock = [&](auto al, int k) {
+                            const uint32_t sb = (uint32_t)(qd * WS + k * 210);
+#pragma unroll
+                            for (int h = 0; h < 2; h++)
+#pragma unroll
+                                for (int g = 0; g < 4; g++) {
+                                    const int blk = (c * (CB / 8) + k) * 8 + h * 4 + g;
+                                    const Q6W w6 = q6_k_weights<decltype(al)::value>(cb, sb, h, g, p);
+#pragma unroll
+                                    for (int n = 0; n < NT; n++)
+                                        if (n < ntw)
+                                            q6_k_token(w6, xw + (size_t)n * nP * kPairBytes +
+                                                               (size_t)(blk >> 1) * kPairBytes, p, blk & 1, acc[n]);
+                                }
+                        };
+                        /* two super-blocks per iteration: unrolling the chunk's eight
+                         * spilled the NT = 2, 4 variants */
+#pragma unroll 1
+                        for (int k = 0; k < CB / 8; k += 2) {
+                            superblock(std::integral_constant<bool, true>(), k);
+                            superblock(std::integral_constant<bool, false>(), k + 1);
+                        }
+                    } else if (ntw > 0) {
                         if (TYPE == 3)
                             q4_1_rows<NT, (NT >= 4 ? 1 : (NT == 2 ? 2 : 4))>((const uint32_t *)(cb + qd * WS), p,
                                                                               xbuf + (size_t)tw0 * nP * kPairBytes,
@@ -2452,9 +2544,10 @@ __global__ __launch_bounds__(64 * W) void dense_tok_kernel(DenseArgs a)
 /* Tokens per wave of dense_tok_kernel's passes for a batch of T (four waves per block), and
  * its LDS bytes. */
 constexpr int kDenseTokW = 4;
-static size_t dense_tok_lds(int NT, int CB, int bb, int nb)
+static size_t dense_tok_lds(int NT, int CB, int type, int nb)
 {
-    const size_t ws = (size_t)CB * bb + (((CB * bb / 16) & 1) ? 0 : 16);
+    const int rcb = type == 14 ? CB / 8 * 210 : CB * (type == 3 ? 20 : 18);
+    const size_t ws = (size_t)rcb + (((rcb / 16) & 1) ? 0 : 16);
     return 2 * 16 * ws + (size_t)kDenseTokW * NT * (nb / 2) * kPairBytes;
 }
 
@@ -2469,6 +2562,39 @@ hipError_t launch_dense(const DenseArgs &args, int type, uint8_t *xqk, hipStream
 {
     DenseArgs a = args;
     const int nb = a.C / 32;
+    if (type == 0) {
+        /* F32 rows: qms_vec_dot_f32 (src/quant.c:161-163, src/kernels.c:202-221), the router's
+         * arithmetic; one launch per matrix */
+        for (int i = 0; i < a.nm; i++) {
+            RouteArgs r;
+            r.router = (const float *)a.m[i].w;
+            r.xn = a.x;
+            r.E = a.C;
+            r.X = a.m[i].rows;
+            r.K = 0;
+            r.T = a.T;
+            r.y = a.m[i].y;
+            r.ystride = a.m[i].rows;
+            r.S = Scratch{};
+            /* one token: a block per row (rows up to 4096 wide) or 4 rows per block; more
+             * tokens: 16 rows x 16 tokens per block, so each row is read once per 16 tokens
+             * (a block per row and token group re-read the rows, measured 5x slower at 4) */
+            if (a.T == 1 && a.C <= 4096) {
+                r.n_route_wg = r.X;
+                const size_t lds = (size_t)2 * 16 * (a.C / 16 + 4) * 4;
+                QLAUNCH("dense", route_small_kernel<1>, dim3(r.X), dim3(256), lds, st, r);
+            } else if (a.T == 1) {
+                r.n_route_wg = (r.X + 3) / 4;
+                const size_t lds = (size_t)8 * (256 + 4) * 4;
+                QLAUNCH("dense", (route_big_kernel<1, 1, kRouteBigP>), dim3(r.n_route_wg), dim3(256), lds, st, r);
+            } else {
+                r.n_route_wg = ((a.T + 15) / 16) * ((r.X + 15) / 16);
+                const size_t lds = (size_t)32 * (256 + 4) * 4;
+                QLAUNCH("dense", (route_big_kernel<4, 4, kRouteBigP>), dim3(r.n_route_wg), dim3(256), lds, st, r);
+            }
+        }
+        return hipGetLastError();
+    }
     a.xqk = nullptr;
     if (a.T >= kDenseQuantT && xqk) {
         QLAUNCH("dquant", dense_quant_kernel, dim3((a.T * nb + 255) / 256), dim3(256), 0, st, a.x, a.C, a.T, xqk);
@@ -2476,7 +2602,7 @@ hipError_t launch_dense(const DenseArgs &args, int type, uint8_t *xqk, hipStream
     }
     /* one wave per block, 16 rows each: the trunk's small matrices (attn_k/v: 512 rows) still
      * spread over 32 CUs, the large ones over every CU */
-    if (a.T == 1) {                                   /* eight lanes per row, 8 rows per wave */
+    if (a.T == 1 && (type != 14 || nb % 64 == 0)) {  /* eight lanes per row, 8 rows per wave */
         /* W waves per block share the input row's quantisation: the most that still gives
          * every CU a block */
         int rows = 0;
@@ -2487,12 +2613,16 @@ hipError_t launch_dense(const DenseArgs &args, int type, uint8_t *xqk, hipStream
             a.m[i].first_block = nbw;
             nbw += (a.m[i].rows + 8 * W - 1) / (8 * W);
         }
-        const int CB = nb % 16 == 0 ? 16 : 8, bb = type == 3 ? 20 : 18;
-        const size_t ws = (size_t)CB * bb + (((CB * bb / 16) & 1) ? 0 : 16);
+        const int CB = type == 14 ? 64 : (nb % 16 == 0 ? 16 : 8);
+        const int rcb = type == 14 ? CB / 8 * 210 : CB * (type == 3 ? 20 : 18);
+        const size_t ws = (size_t)rcb + (((rcb / 16) & 1) ? 0 : 16);
         const size_t lds8 = (size_t)W * 8 * ws + (size_t)(nb / 2) * kPairBytes;
+        if (lds8 > 160 * 1024) return hipErrorInvalidValue;
         auto go = [&](auto tw) {
             constexpr int WW = decltype(tw)::value;
-            if (type == 3) {
+            if (type == 14) {
+                QLAUNCH("dense", (dense_oct_kernel<14, 64, 2, WW>), dim3(nbw), dim3(64 * WW), lds8, st, a);
+            } else if (type == 3) {
                 if (CB == 16) QLAUNCH("dense", (dense_oct_kernel<3, 16, 2, WW>), dim3(nbw), dim3(64 * WW), lds8, st, a);
                 else QLAUNCH("dense", (dense_oct_kernel<3, 8, 2, WW>), dim3(nbw), dim3(64 * WW), lds8, st, a);
             } else {
@@ -2513,27 +2643,34 @@ hipError_t launch_dense(const DenseArgs &args, int type, uint8_t *xqk, hipStream
     {
         /* four waves sharing each block's 16 rows, NT tokens each: the smallest NT whose pass
          * covers the batch, as long as the records fit in LDS */
-        const int CB = nb % 16 == 0 ? 16 : 8, bb = type == 3 ? 20 : 18;
+        const int CB = type == 14 ? 64 : (nb % 16 == 0 ? 16 : 8);
+        if (type == 14 && nb % 64) return hipErrorInvalidValue;     /* Q6_K: cols % 2048 */
         int NT = a.T <= kDenseTokW ? 1 : (a.T <= 2 * kDenseTokW ? 2 : 4);
-        while (NT > 1 && dense_tok_lds(NT, CB, bb, nb) > 160 * 1024) NT >>= 1;
-        const size_t lds = dense_tok_lds(NT, CB, bb, nb);
+        while (NT > 1 && dense_tok_lds(NT, CB, type, nb) > 160 * 1024) NT >>= 1;
+        const size_t lds = dense_tok_lds(NT, CB, type, nb);
         if (lds <= 160 * 1024) {
             const dim3 grid(nblk), block(64 * kDenseTokW);
             auto go = [&](auto ty, auto nt) {
                 constexpr int TY = decltype(ty)::value, N = decltype(nt)::value;
-                if (CB == 16) QLAUNCH("dense", (dense_tok_kernel<TY, 16, 2, kDenseTokW, N>), grid, block, lds, st, a);
-                else QLAUNCH("dense", (dense_tok_kernel<TY, 8, 2, kDenseTokW, N>), grid, block, lds, st, a);
+                if constexpr (TY == 14) {
+                    QLAUNCH("dense", (dense_tok_kernel<14, 64, 2, kDenseTokW, N>), grid, block, lds, st, a);
+                } else {
+                    if (CB == 16) QLAUNCH("dense", (dense_tok_kernel<TY, 16, 2, kDenseTokW, N>), grid, block, lds, st, a);
+                    else QLAUNCH("dense", (dense_tok_kernel<TY, 8, 2, kDenseTokW, N>), grid, block, lds, st, a);
+                }
             };
             auto by_nt = [&](auto ty) {
                 if (NT == 4) go(ty, std::integral_constant<int, 4>());
                 else if (NT == 2) go(ty, std::integral_constant<int, 2>());
                 else go(ty, std::integral_constant<int, 1>());
             };
-            if (type == 3) by_nt(std::integral_constant<int, 3>());
+            if (type == 14) by_nt(std::integral_constant<int, 14>());
+            else if (type == 3) by_nt(std::integral_constant<int, 3>());
             else by_nt(std::integral_constant<int, 2>());
             return hipGetLastError();
         }
     }
+    if (type == 14) return hipErrorInvalidValue;
     const int NT = a.T >= 4 ? 4 : (a.T >= 2 ? 2 : 1);
     const int CB = nb % 16 == 0 ? 16 : 8;
     const int bb = type == 3 ? 20 : 18;

@@ -321,8 +321,9 @@ class Context:
 
     # ---------------------------------------------------------------- dense (trunk) products
     def mat_upload(self, type_: int, data: np.ndarray, rows: int, cols: int) -> int:
-        """A dense matrix (GGUF rows, QmsMat) resident in HBM; returns its id."""
-        data = np.ascontiguousarray(data, np.uint8)
+        """A dense matrix (GGUF rows, QmsMat) resident in HBM; returns its id. data holds the
+        row bytes (F32 rows may be given as float32)."""
+        data = np.ascontiguousarray(data).reshape(-1).view(np.uint8)
         m = _Mat(type_, rows, cols, row_bytes(type_, cols), data.ctypes.data)
         i = _I()
         self._check(lib.qmsg_mat_upload(self._h, ctypes.byref(m), ctypes.byref(i)))

@@ -15,7 +15,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 ORACLE_SO = os.path.join(HERE, "liboracle.so")
 REF_DIR = os.path.join(HERE, "_ref")
 
-T_F32, T_Q4_0, T_Q4_1, T_Q6_K = 0, 2, 3, 14
+T_F32, T_Q4_0, T_Q4_1, T_Q8_0, T_Q6_K = 0, 2, 3, 8, 14
 KIND_X, KIND_ROUTER, KIND_GATE, KIND_UP, KIND_DOWN = 0, 1, 2, 3, 4
 Q8_DTYPE = np.dtype([("d", "<f4"), ("ds", "<f4"), ("s16", "<i2", (2,)), ("q", "i1", (32,))])
 
@@ -105,11 +105,13 @@ def vec_dot_f32(w: np.ndarray, x: np.ndarray) -> float:
 
 
 def matmul_q8(t: int, w: np.ndarray, rows: int, cols: int, x: np.ndarray) -> np.ndarray:
-    """qms_matmul's fast path (src/quant.c:128-170) for one quantised matrix: y [T][rows]."""
+    """qms_matmul's fast path (src/quant.c:128-170) for one matrix: y [T][rows]. w holds the
+    GGUF row bytes (any dtype; F32 rows may be passed as float32)."""
     x = np.ascontiguousarray(x, np.float32).reshape(-1, cols)
     y = np.empty((x.shape[0], rows), np.float32)
-    assert lib.orc_matmul_q8(t, _ptr(np.ascontiguousarray(w, np.uint8)), rows, cols, row_bytes(t, cols), _ptr(x),
-                             x.shape[0], _ptr(y)) == 0
+    wb = np.ascontiguousarray(w).reshape(-1).view(np.uint8)
+    assert wb.size == rows * row_bytes(t, cols)
+    assert lib.orc_matmul_q8(t, _ptr(wb), rows, cols, row_bytes(t, cols), _ptr(x), x.shape[0], _ptr(y)) == 0
     return y
 
 
@@ -127,6 +129,17 @@ def synth_f32(seed: int, layer: int, kind: int, expert: int, n: int, sigma: floa
     out = np.empty(n, np.float32)
     lib.orc_synth_f32(seed, layer, kind, expert, n, sigma, _ptr(out))
     return out
+
+
+def synth_mat(t: int, rows: int, cols: int, seed: int, sigma: float = 0.02) -> np.ndarray:
+    """The GGUF bytes of a seeded synthetic [rows][cols] matrix of type t, as qmsg_mat_synth
+    writes them: the expert generator's one 'expert' 0 of kind gate at layer 0 (F32: its normal
+    values times sigma)."""
+    if t == T_F32:
+        return synth_f32(seed, 0, KIND_GATE, 0, rows * cols, sigma).view(np.uint8)
+    w = np.zeros(rows * row_bytes(t, cols), np.uint8)
+    lib.orc_synth_experts(seed, 0, KIND_GATE, t, rows, cols, 0, 1, sigma, _ptr(w))
+    return w
 
 
 def rmsnorm(x: np.ndarray, w: Optional[np.ndarray] = None, eps: float = 1e-6) -> np.ndarray:

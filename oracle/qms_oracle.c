@@ -535,12 +535,21 @@ int orc_moe_exact(int E, int X, int K, int F, const orc_mat *router, const orc_m
     return moe_common(1, E, X, K, F, router, gate, up, down, xn, T, out, dbg);
 }
 
-/* The fast path of qms_matmul_n for one quantised matrix (src/quant.c:128-170): each row of
- * x [T][cols] quantised to int8 blocks, then y[t][r] = vec_dot_q8(row r, xq_t). */
+/* The fast path of qms_matmul_n for one matrix (src/quant.c:128-170): for a quantised type
+ * each row of x [T][cols] is quantised to int8 blocks and y[t][r] = vec_dot_q8(row r, xq_t);
+ * F32 rows take qms_vec_dot_f32 against x itself (src/quant.c:161-163). */
 int orc_matmul_q8(int type, const uint8_t *w, int64_t rows, int64_t cols, uint64_t row_bytes, const float *x, int T,
                   float *y)
 {
-    if (cols % 32 || !orc_row_bytes(type, cols) || type == ORC_T_F32) return -1;
+    if (cols % 32 || !orc_row_bytes(type, cols) || type == ORC_T_F16 || type == ORC_T_Q8_0) return -1;
+    if (type == ORC_T_F32) {
+#pragma omp parallel for schedule(static)
+        for (int64_t r = 0; r < rows; r++)
+            for (int t = 0; t < T; t++)
+                y[(size_t)t * rows + r] =
+                    orc_vec_dot_f32((const float *)(w + (uint64_t)r * row_bytes), x + (size_t)t * cols, cols);
+        return 0;
+    }
     const int64_t nb = cols / 32;
     orc_q8 *xq = (orc_q8 *)malloc((size_t)T * (size_t)nb * sizeof(orc_q8));
     if (!xq) return -1;

@@ -12,7 +12,7 @@ Outputs (numpy .npz, no pickles):
                    results on the test_kernels.c-style cases, plus quantiser tie cases
   layer_*.npz      the reference moe() on whole layers: inputs' hashes, router logits
                    (qms_matmul), int8 input blocks (qms_quantize_q8) and the layer output
-  dense.npz        qms_matmul on quantised dense (trunk-shaped) matrices: inputs' hashes and
+  dense.npz        qms_matmul on dense (trunk-shaped) matrices: inputs' hashes and
                    outputs
 """
 import ctypes
@@ -142,14 +142,12 @@ def kat_kernels(R) -> dict:
 
 # dense (trunk) matrices through qms_matmul: (type, rows, cols, T, seed)
 DENSE = [(orc.T_Q4_0, 512, 4096, 3, 1), (orc.T_Q4_1, 256, 2048, 2, 2), (orc.T_Q4_0, 100, 8192, 1, 3),
-         (orc.T_Q4_0, 64, 4096, 9, 4)]
+         (orc.T_Q4_0, 64, 4096, 9, 4), (orc.T_Q6_K, 96, 4096, 3, 5), (orc.T_Q6_K, 40, 2048, 9, 6),
+         (orc.T_F32, 64, 2048, 2, 7), (orc.T_F32, 40, 4096, 6, 8)]
 
 
 def dense_mat(t, rows, cols, seed):
-    """Seeded synthetic weight rows (the shared generator, one 'expert' of kind gate)."""
-    w = np.zeros(rows * orc.row_bytes(t, cols), np.uint8)
-    orc.lib.orc_synth_experts(seed, 0, orc.KIND_GATE, t, rows, cols, 0, 1, 0.02, w.ctypes.data)
-    return w
+    return orc.synth_mat(t, rows, cols, seed)
 
 
 def dense_cases(R) -> dict:

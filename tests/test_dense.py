@@ -18,9 +18,7 @@ def sha(a) -> bytes:
 
 
 def dense_mat(t, rows, cols, seed):
-    w = np.zeros(rows * orc.row_bytes(t, cols), np.uint8)
-    orc.lib.orc_synth_experts(seed, 0, orc.KIND_GATE, t, rows, cols, 0, 1, 0.02, w.ctypes.data)
-    return w
+    return orc.synth_mat(t, rows, cols, seed)
 
 
 def test_oracle_matmul_matches_reference_fixtures():
@@ -53,7 +51,8 @@ def test_oracle_matmul_row_is_vec_dot():
 
 @pytest.mark.skipif(orc.load_ref() is None, reason="oracle/_ref (the reference build) is not built here")
 @pytest.mark.parametrize("t,rows,cols,T", [(orc.T_Q4_0, 96, 4096, 5), (orc.T_Q4_1, 33, 1024, 2),
-                                           (orc.T_Q6_K, 20, 2048, 3)])
+                                           (orc.T_Q6_K, 20, 2048, 3), (orc.T_F32, 24, 1024, 3),
+                                           (orc.T_F32, 7, 4096, 1)])
 def test_oracle_matmul_matches_reference_live(t, rows, cols, T):
     R = orc.load_ref()
 

@@ -22,9 +22,7 @@ def q():
 
 
 def dense_mat(t, rows, cols, seed):
-    w = np.zeros(rows * orc.row_bytes(t, cols), np.uint8)
-    orc.lib.orc_synth_experts(seed, 0, orc.KIND_GATE, t, rows, cols, 0, 1, 0.02, w.ctypes.data)
-    return w
+    return orc.synth_mat(t, rows, cols, seed)
 
 
 def bits(a):
@@ -93,18 +91,25 @@ def test_dense_mixed_types_tails_and_device_buffers(q, T):
 def test_dense_from_gguf_and_errors(q, tmp_path):
     E, R = 1024, 256
     wq = dense_mat(orc.T_Q4_0, R, E, 11)
+    wk = orc.make_input(E, 64, 13)
     path = str(tmp_path / "trunk.gguf")
     gf.write_gguf(path, [("general.architecture", gf.STR, "qwen3moe")],
                   [("blk.0.attn_q.weight", orc.T_Q4_0, [E, R], wq.tobytes()),
                    ("blk.0.attn_norm.weight", orc.T_F32, [E], np.ones(E, np.float32).tobytes()),
-                   ("blk.0.attn_k.weight", orc.T_F32, [E, 64], np.zeros((64, E), np.float32).tobytes())])
+                   ("blk.0.attn_k.weight", orc.T_F32, [E, 64], wk.tobytes()),
+                   ("blk.0.attn_v.weight", orc.T_Q8_0, [E, 8], np.zeros(8 * 34 * E // 32, np.uint8).tobytes())])
     x = orc.make_input(E, 2, 12)
     with q.Gguf(path) as g, q.Context(256, 16, 4, 128, max_tokens=1) as ctx:
         mid = ctx.gguf_upload_mat(g, "blk.0.attn_q.weight")
         (y,) = ctx.matmul_n([mid], x)
         assert np.array_equal(bits(y), bits(orc.matmul_q8(orc.T_Q4_0, wq, R, E, x)))
+        kid = ctx.gguf_upload_mat(g, "blk.0.attn_k.weight")       # F32 rows
+        qid = ctx.gguf_upload_mat(g, "blk.0.attn_q.weight")
+        yk, yq = ctx.matmul_n([kid, qid], x)                       # F32 and Q4_0 in one call
+        assert np.array_equal(bits(yk), bits(orc.matmul_q8(orc.T_F32, wk, 64, E, x)))
+        assert np.array_equal(bits(yq), bits(y))
         with pytest.raises(q.QmsgError) as ei:
-            ctx.gguf_upload_mat(g, "blk.0.attn_k.weight")         # F32 rows: not a dense kernel type
+            ctx.gguf_upload_mat(g, "blk.0.attn_v.weight")         # Q8_0: not a dense kernel type
         assert ei.value.status == -2
         with pytest.raises(q.QmsgError):
             ctx.gguf_upload_mat(g, "blk.0.attn_norm.weight")      # 1-D
@@ -118,3 +123,37 @@ def test_dense_from_gguf_and_errors(q, tmp_path):
         with pytest.raises(q.QmsgError) as ei:
             ctx.mat_upload(orc.T_Q4_0, dense_mat(orc.T_Q4_0, 4, 96, 1), 4, 96)   # cols % 256
         assert ei.value.status == -2
+        with pytest.raises(q.QmsgError) as ei:
+            ctx.mat_synth(orc.T_Q6_K, 4, 1024, 1)                              # Q6_K: cols % 2048
+        assert ei.value.status == -2
+
+
+@pytest.mark.parametrize("T", [1, 2, 5, 9])
+def test_dense_q6k_and_f32_trunk_shapes(q, T):
+    """Q6_K and F32 rows (the other types of qms_matmul's fast path, src/quant.c:128-170): the
+    235B trunk's q/k/v shapes in Q6_K (super-blocks staged in chunks of eight), an F32 matrix
+    in the same call as a Q4_0 one, and an output-weight-like Q6_K matrix with a ragged row
+    count; device-generated matrices checked against the same generator on the host."""
+    E, H = 4096, 8192
+    print(f"[case] dense q6k/f32 T={T}", flush=True)
+    x = orc.make_input(E, T, 20 + T) * np.float32(3.0)
+    with q.Context(256, 16, 4, 128, max_tokens=1) as ctx:
+        specs = [(orc.T_Q6_K, H, E, 1), (orc.T_Q6_K, 512, E, 2), (orc.T_F32, 512, E, 3), (orc.T_Q4_0, 512, E, 4),
+                 (orc.T_Q6_K, 1000, E, 5), (orc.T_F32, 129, E, 6)]
+        ids = [ctx.mat_synth(t, r, c, s) for t, r, c, s in specs]
+        ys = ctx.matmul_n(ids, x)
+    for (t, r, c, s), y in zip(specs, ys):
+        ref = orc.matmul_q8(t, dense_mat(t, r, c, s), r, c, x)
+        assert np.array_equal(bits(y), bits(ref)), (t, r)
+
+
+@pytest.mark.parametrize("T", [1, 3, 6])
+def test_dense_f32_wide_rows(q, T):
+    """F32 rows of 8192 (attn_output's width: the many-chunk router path) and of 2048."""
+    print(f"[case] dense f32 wide T={T}", flush=True)
+    with q.Context(256, 16, 4, 128, max_tokens=1) as ctx:
+        for C, R in ((8192, 300), (2048, 77)):
+            x = orc.make_input(C, T, 40 + C)
+            mid = ctx.mat_synth(orc.T_F32, R, C, 9)
+            (y,) = ctx.matmul_n([mid], x)
+            assert np.array_equal(bits(y), bits(orc.matmul_q8(orc.T_F32, dense_mat(orc.T_F32, R, C, 9), R, C, x))), C
