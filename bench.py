@@ -332,9 +332,10 @@ def run_trunk(args):
     rb = qmsg.row_bytes(TT, E)
     layer_bytes = (H + 2 * KV) * rb + E * qmsg.row_bytes(TT, H)
     us_layer = 1e6 * el / K_steps / NL
-    d_us = kern["dense"]["avg_us"]
-    dense_bytes = layer_bytes / 2                     # per dense launch on average (q/k/v, then o)
-    achieved = dense_bytes / (d_us * 1e-6) / 1e9
+    # the layer's bytes over its dense launches' summed duration (q/k/v then o: two launches
+    # for a quantised type, four for F32, whose matrices launch one by one)
+    d_us_layer = kern["dense"]["avg_us"] * kern["dense"]["launches"] / NL
+    achieved = layer_bytes / (d_us_layer * 1e-6) / 1e9
     result = {
         "metric": "trunk q/k/v/o dense products: us per layer + achieved HBM GB/s",
         "value": round(us_layer, 3), "unit": "us/layer", "higher_is_better": False, "n_gpus": 1,
@@ -343,7 +344,7 @@ def run_trunk(args):
         "config": {"workload": f"Qwen3-235B-A22B trunk q/k/v/o shapes ({args.trunk_type}), {NL} resident layers",
                    "T": T},
         "layer_bytes": layer_bytes, "achieved_GBps_layer": round(layer_bytes / (us_layer * 1e-6) / 1e9, 1),
-        "roofline": {"kernel": "dense (row dots, average of the q/k/v and o launches)", "bound": "hbm",
+        "roofline": {"kernel": "dense (row dots over the layer's q/k/v and o launches)", "bound": "hbm",
                      "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None},
         "kernels": kern, "cpu_baseline": None,

@@ -183,7 +183,9 @@ int qmsg_gguf_upload(qmsg_ctx *ctx, const qmsg_gguf *g, int first, int n);
 
 /* A dense weight matrix resident in HBM, a QmsMat (src/quant.h:11-16) loaded by load_mat
  * (src/model.c:67-85): rows of row_bytes GGUF bytes, copied unchanged; *id names it in
- * qmsg_matmul_n. Q4_0 and Q4_1 rows with cols % 256 == 0 (the trunk's attn_q/k/v/output). */
+ * qmsg_matmul_n. The types of the reference's fast path (qms_fast_supported,
+ * src/kernels.c:197-200): F32, Q4_0 and Q4_1 rows with cols % 256 == 0, Q6_K rows with
+ * cols % 2048 == 0; QMSG_E_UNSUPPORTED otherwise (the reference would take matmul_exact). */
 int qmsg_mat_upload(qmsg_ctx *ctx, const qmsg_mat *host, int *id);
 /* The same from a parsed GGUF file, by tensor name (e.g. "blk.0.attn_q.weight"). */
 int qmsg_gguf_upload_mat(qmsg_ctx *ctx, const qmsg_gguf *g, const char *name, int *id);
@@ -191,9 +193,10 @@ int qmsg_gguf_upload_mat(qmsg_ctx *ctx, const qmsg_gguf *g, const char *name, in
  * (the generator of qmsg_layer_synth, one expert of kind gate, layer 0), for benchmarks. */
 int qmsg_mat_synth(qmsg_ctx *ctx, int type, int64_t rows, int64_t cols, uint64_t seed, float sigma, int *id);
 
-/* qms_matmul_n (src/quant.c:128-170) on resident matrices ids[0..nW-1] of equal cols C:
- * every row of x [T][C] is quantised to int8 blocks (qms_quantize_q8) and ys[i][t][r] =
- * qms_vec_dot_q8(row r of W_i, xq_t), bit-identical to the reference's fast path. Host
+/* qms_matmul_n (src/quant.c:128-170) on resident matrices ids[0..nW-1] of equal cols C
+ * (types may differ): for a quantised W_i every row of x [T][C] is quantised to int8 blocks
+ * (qms_quantize_q8) and ys[i][t][r] = qms_vec_dot_q8(row r of W_i, xq_t); for F32 rows
+ * ys[i][t][r] = qms_vec_dot_f32(row r, x_t). Bit-identical to the reference's fast path. Host
  * buffers; blocks until done. The first call with a larger T*C allocates device buffers. */
 int qmsg_matmul_n(qmsg_ctx *ctx, const int *ids, int nW, const float *x, int T, float *const *ys);
 /* The same on device buffers (x 16-byte aligned), enqueued on the context's stream. */
