@@ -25,6 +25,7 @@ SHORT = (
     ("down_t1_kernel", "down"), ("act_quant_kernel", "actq"), ("swiglu_kernel", "swiglu"),
     ("route_exact_kernel", "route"), ("exact_rows_kernel", "rows_f32"),
     ("combine_kernel", "combine"), ("copy_kernel", "copy"), ("dense_kernel", "dense"),
+    ("dense_oct_kernel", "dense"), ("dense_tok_kernel", "dense"), ("dense_quant_kernel", "dquant"),
     ("gateup_mfma_kernel", "gateup"), ("down_mfma_kernel", "down"), ("rmsnorm_kernel", "rmsnorm"),
     ("add_rows_kernel", "add"),
 )
