@@ -1649,6 +1649,156 @@ __global__ __launch_bounds__(32 * RD) void down_t1_kernel(DownArgs a)
     PHASE(2048, 5);
 }
 
+/* Slots of the batches the small-batch down kernel takes (two to four tokens). */
+constexpr int kSmallDownNS = 32;
+
+/* Two to four tokens, Q4_0 or Q4_1 down weights (at most kSmallDownNS slots): the layout of
+ * down_t1_kernel, one block per RD output rows and RD/2 waves, but wave w streams the active
+ * experts w, w + RD/2, ... one after another, each against its one to four slots, and
+ * requests the next expert's first chunks while it consumes the current one's last. The block
+ * first quantises every slot's activations into LDS pair records and ends with the weighted
+ * combine of its rows for every token, in selection order (src/model.c:998-1005, 1152-1162). */
+template <int TYPE, int CB, int D, int RD>
+__global__ __launch_bounds__(32 * RD) void down_small_kernel(DownArgs a)
+{
+    extern __shared__ __align__(16) uint8_t smem[];
+    constexpr int NW = RD / 2, NTH = 64 * NW, NT = 4;
+    constexpr int QPT = 2;                            /* int8 blocks per thread in registers  */
+    constexpr int BB = TYPE == 3 ? 20 : 18;           /* bytes per 32-block                   */
+    constexpr int SPR = CB * BB / 16;                 /* 16-byte slots per row per chunk      */
+    constexpr int NSL = RD * SPR;                     /* slots of one wave's chunk            */
+    constexpr int SPT = (NSL + 63) / 64;              /* slots per lane per chunk             */
+    constexpr int WS = CB * BB + ((SPR & 1) ? 0 : 16);/* LDS row stride, odd in 16-byte units */
+    static_assert(RD == 16, "a lane quad per row of the wave's 16");
+    const int tid = threadIdx.x, lane = tid & 63, qd = lane >> 2, p = lane & 3;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int r0 = (int)blockIdx.x * RD, E = a.E, K = a.K, T = a.T, NS = T * K;
+    const int nbF = a.F >> 5, nPF = a.F >> 6, nchunk = nbF / CB, xrec = nPF * kPairBytes;
+    uint8_t *wbuf = smem + wave * 16 * WS;
+    uint8_t *xbuf = smem + NW * 16 * WS;              /* [NS][xrec]                           */
+    float *dnl = (float *)(xbuf + (size_t)NS * xrec); /* [NS][RD]                             */
+
+    /* the wave's first expert (wave-uniform scalar loads first, as in the one-token kernel) */
+    const int na = a.S.meta[0];
+    int j = wave;
+    int4 wk = j < na ? a.S.work[j] : make_int4(-1, 0, 0, 0);
+    const int nqb = NS * nbF;
+    float4 av[QPT][8];
+#pragma unroll
+    for (int u = 0; u < QPT; u++) {
+        const float4 *src = (const float4 *)(a.S.act + (size_t)min(tid + NTH * u, nqb - 1) * 32);
+#pragma unroll
+        for (int q = 0; q < 8; q++) av[u][q] = src[q];
+    }
+    const uint8_t *b = a.down + (size_t)max(wk.x, 0) * a.eb + (size_t)r0 * a.rb;
+    __builtin_amdgcn_sched_barrier(0);
+    u32x4 wv[D][SPT];
+    auto load_chunk = [&](int c, u32x4 *dst) {
+#pragma unroll
+        for (int m = 0; m < SPT; m++) {
+            const int i = min(lane + 64 * m, NSL - 1), row = i / SPR, q = i - row * SPR;
+            dst[m] = *(const u32x4 *)(b + (size_t)row * a.rb + (size_t)c * CB * BB + 16 * q);
+        }
+    };
+    if (wk.x >= 0) {
+#pragma unroll
+        for (int d = 0; d < D; d++)
+            if (d < nchunk) load_chunk(d, wv[d]);
+    }
+    auto quant = [&](int qb, const float *v) {
+        const int sl = qb / nbF, blk = qb - sl * nbF;
+        const Q8Vals q = quantize_block(v);
+        store_pair_half(q, (uint32_t *)(xbuf + (size_t)sl * xrec + (size_t)(blk >> 1) * kPairBytes), blk & 1);
+        if (blockIdx.x == 0) {
+            store_q8(q, a.S.aq + qb);
+            store_pair_half(q, (uint32_t *)(a.S.aqk + ((size_t)sl * (nbF >> 1) + (blk >> 1)) * kPairBytes), blk & 1);
+        }
+    };
+#pragma unroll
+    for (int u = 0; u < QPT; u++) {
+        const int qb = tid + NTH * u;
+        if (qb < nqb) {
+            float v[32];
+#pragma unroll
+            for (int q = 0; q < 8; q++) {
+                v[4 * q] = av[u][q].x; v[4 * q + 1] = av[u][q].y; v[4 * q + 2] = av[u][q].z; v[4 * q + 3] = av[u][q].w;
+            }
+            quant(qb, v);
+        }
+    }
+    for (int qb = tid + NTH * QPT; qb < nqb; qb += NTH) {   /* past the register share */
+        float v[32];
+        const float4 *src = (const float4 *)(a.S.act + (size_t)qb * 32);
+        for (int q = 0; q < 8; q++) {
+            const float4 f = src[q];
+            v[4 * q] = f.x; v[4 * q + 1] = f.y; v[4 * q + 2] = f.z; v[4 * q + 3] = f.w;
+        }
+        quant(qb, v);
+    }
+    __syncthreads();
+    const bool can_pre = nchunk % D == 0;             /* chunk c + D - nchunk lands in c's registers */
+    while (wk.x >= 0) {
+        const int jn = j + NW;
+        const int4 wn = jn < na ? a.S.work[jn] : make_int4(-1, 0, 0, 0);
+        const bool pre = can_pre && wn.x >= 0;
+        bool switched = false;
+        const int s0 = wk.y, nt = wk.z - wk.y;        /* one slot per token of the expert: nt <= T */
+        const uint8_t *xq = xbuf + (size_t)s0 * xrec;
+        RowAcc acc[NT];
+        for (int n = 0; n < NT; n++) acc[n] = RowAcc{ 0.0f, 0.0f, 0.0f };
+        for (int c0 = 0; c0 < nchunk; c0 += D) {
+#pragma unroll
+            for (int d = 0; d < D; d++) {
+                const int c = c0 + d;
+                if (c < nchunk) {
+                    wave_sync();
+#pragma unroll
+                    for (int m = 0; m < SPT; m++) {
+                        const int i = min(lane + 64 * m, NSL - 1), row = i / SPR, q = i - row * SPR;
+                        *(u32x4 *)(wbuf + row * WS + 16 * q) = wv[d][m];
+                    }
+                    wave_sync();
+                    if (c + D < nchunk) {
+                        load_chunk(c + D, wv[d]);
+                    } else if (pre && c + D - nchunk < nchunk) {
+                        if (!switched) {                 /* every chunk of this expert is requested */
+                            b = a.down + (size_t)wn.x * a.eb + (size_t)r0 * a.rb;
+                            switched = true;
+                        }
+                        load_chunk(c + D - nchunk, wv[d]);
+                    }
+                    q4_rows_nt<TYPE, NT>((const uint32_t *)(wbuf + qd * WS), p, xq, (size_t)xrec, c * (CB / 2),
+                                         CB / 2, nt, acc);
+                }
+            }
+        }
+#pragma unroll
+        for (int n = 0; n < NT; n++) {
+            const float v = quad_finish(acc[n], finish_scale(TYPE));
+            if (p == 0 && n < nt) {
+                a.S.dn[(size_t)(s0 + n) * E + r0 + qd] = v;
+                dnl[(s0 + n) * RD + qd] = v;
+            }
+        }
+        j = jn;
+        wk = wn;
+        if (wk.x >= 0 && !pre) {
+            b = a.down + (size_t)wk.x * a.eb + (size_t)r0 * a.rb;
+#pragma unroll
+            for (int d = 0; d < D; d++)
+                if (d < nchunk) load_chunk(d, wv[d]);
+        }
+    }
+    __syncthreads();
+    for (int i = tid; i < T * RD; i += NTH) {
+        const int t = i / RD, r = i - t * RD;
+        float o = 0.0f;
+        for (int jj = 0; jj < K; jj++)
+            o = __builtin_fmaf(a.S.wt[t * K + jj], dnl[a.S.slot_of[t * K + jj] * RD + r], o);
+        a.out[(size_t)t * E + r0 + r] = o;
+    }
+}
+
 /* The int8 blocks of every slot's activations (src/model.c:996-997) for batches whose
  * records do not fit the down kernel's LDS: one thread per 32-block. */
 __global__ void act_quant_kernel(Scratch S, int F, int NS)
@@ -1730,6 +1880,15 @@ hipError_t launch_down_exact(const Shape &s, const LayerDev &L, const Scratch &S
         const dim3 grid(s.E / RD), block(32 * RD);
         if (L.down_type == 3) QLAUNCH("down", (down_t1_kernel<3, CB, 3, RD>), grid, block, lds_t1, st, a);
         else QLAUNCH("down", (down_t1_kernel<2, CB, 3, RD>), grid, block, lds_t1, st, a);
+        return hipGetLastError();
+    }
+    /* two to four tokens: the same layout, each wave streaming several experts */
+    const size_t lds_s = (size_t)(RD / 2) * 16 * ws + (size_t)T * s.K * (xrec + RD * 4);
+    if (T >= 2 && T <= 4 && T * s.K <= kSmallDownNS && quant && (L.down_type == 2 || L.down_type == 3) &&
+        s.F % 256 == 0 && s.E % RD == 0 && lds_s <= 160 * 1024) {
+        const dim3 grid(s.E / RD), block(32 * RD);
+        if (L.down_type == 3) QLAUNCH("down", (down_small_kernel<3, CB, 3, RD>), grid, block, lds_s, st, a);
+        else QLAUNCH("down", (down_small_kernel<2, CB, 3, RD>), grid, block, lds_s, st, a);
         return hipGetLastError();
     }
     /* slot tiles: the activations' int8 records first (unless the MFMA gate/up wrote them) */
