@@ -22,7 +22,7 @@ import sys
 SHORT = (
     ("route_small_kernel", "route"), ("route_big_kernel", "route"), ("select_kernel", "select"),
     ("dispatch_kernel", "dispatch"), ("gateup_kernel", "gateup"), ("down_exact_kernel", "down"),
-    ("down_t1_kernel", "down"), ("act_quant_kernel", "actq"), ("swiglu_kernel", "swiglu"),
+    ("down_t1_kernel", "down"), ("down_small_kernel", "down"), ("act_quant_kernel", "actq"), ("swiglu_kernel", "swiglu"),
     ("route_exact_kernel", "route"), ("exact_rows_kernel", "rows_f32"),
     ("combine_kernel", "combine"), ("copy_kernel", "copy"), ("dense_kernel", "dense"),
     ("dense_oct_kernel", "dense"), ("dense_tok_kernel", "dense"), ("dense_quant_kernel", "dquant"),
