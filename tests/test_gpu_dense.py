@@ -157,3 +157,18 @@ def test_dense_f32_wide_rows(q, T):
             mid = ctx.mat_synth(orc.T_F32, R, C, 9)
             (y,) = ctx.matmul_n([mid], x)
             assert np.array_equal(bits(y), bits(orc.matmul_q8(orc.T_F32, dense_mat(orc.T_F32, R, C, 9), R, C, x))), C
+
+
+def test_dense_many_tokens_every_type(q):
+    """37 tokens: three 16-token passes of the batch kernel (with the separate input
+    quantisation) for Q4_0, Q4_1 and Q6_K, three 16-token groups for F32; and T = 0."""
+    C, T = 4096, 37
+    print(f"[case] dense all types T={T}", flush=True)
+    x = orc.make_input(C, T, 50) * np.float32(2.0)
+    specs = [(orc.T_Q4_0, 300, 1), (orc.T_Q4_1, 129, 2), (orc.T_Q6_K, 200, 3), (orc.T_F32, 70, 4)]
+    with q.Context(256, 16, 4, 128, max_tokens=1) as ctx:
+        ids = [ctx.mat_synth(t, r, C, s) for t, r, s in specs]
+        ys = ctx.matmul_n(ids, x)
+        assert all(y.shape == (0, r) for y, (_, r, _) in zip(ctx.matmul_n(ids, x[:0]), specs))
+    for (t, r, s), y in zip(specs, ys):
+        assert np.array_equal(bits(y), bits(orc.matmul_q8(t, dense_mat(t, r, C, s), r, C, x))), t
