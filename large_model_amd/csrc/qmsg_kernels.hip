@@ -1326,7 +1326,10 @@ hipError_t launch_gateup_exact(const Shape &s, const LayerDev &L, const Scratch 
     /* chunks of CB blocks, two in flight per wave (16-block chunks measured fastest for the
      * 4096-wide rows: less in flight per wave lets the first chunks land sooner) */
     const int CB = nbE % 32 == 0 ? 16 : 8;
-    const int NT = T >= 4 ? 4 : (T >= 2 ? 2 : 1);
+    /* two slots per pass for every batch: measured faster than four at T = 4, 16, 64 and 512
+     * (fewer registers and a smaller record buffer let more blocks share a CU; most
+     * decode tiles hold one or two slots) and than one */
+    const int NT = T >= 2 ? 2 : 1;
     const int maxact = s.X < T * s.K ? s.X : T * s.K;
     const int sel = use_small_route(T, s.K);
     const int rows_y = sel ? maxact : maxact + T * s.K / kTileN + 1;   /* active experts, or slot tiles */
@@ -1337,8 +1340,7 @@ hipError_t launch_gateup_exact(const Shape &s, const LayerDev &L, const Scratch 
     if (sel) {
         launch_gateup_nt<1, 1>(a, W, CB, grid, lds, st);     /* one token: NT == 1 */
     } else {
-        if (NT == 4) launch_gateup_nt<4, 0>(a, W, CB, grid, lds, st);
-        else if (NT == 2) launch_gateup_nt<2, 0>(a, W, CB, grid, lds, st);
+        if (NT == 2) launch_gateup_nt<2, 0>(a, W, CB, grid, lds, st);
         else launch_gateup_nt<1, 0>(a, W, CB, grid, lds, st);
     }
     return hipGetLastError();
