@@ -1294,12 +1294,13 @@ static void launch_gateup_nt(const GateUpArgs &a, int W, int CB, dim3 grid, size
 
 /* Waves per gateup block: the W (rows 8W per block) whose grid, at the largest possible
  * number of active experts, puts the least work on the busiest CU (one block per CU per
- * pass); ties go to the larger block. */
-int gateup_waves(int F, int max_active, int n_cu)
+ * pass); ties go to the larger block. Slot-tile grids (batch) leave out W = 6, measured
+ * 20-60 % slower there at the 235B shape (W = 2, 3, 4 within 2 % of each other). */
+int gateup_waves(int F, int max_active, int n_cu, int batch)
 {
     int best = 0, best_cost = 0;
     for (int W : { 6, 4, 3, 2 }) {
-        if (F % (8 * W)) continue;
+        if (F % (8 * W) || (batch && W == 6)) continue;
         const long nblk = (long)(F / (8 * W)) * max_active;
         const long cost = ((nblk + n_cu - 1) / n_cu) * W;
         if (!best || cost < best_cost) { best = W; best_cost = (int)cost; }
@@ -1333,7 +1334,7 @@ hipError_t launch_gateup_exact(const Shape &s, const LayerDev &L, const Scratch 
     const int maxact = s.X < T * s.K ? s.X : T * s.K;
     const int sel = use_small_route(T, s.K);
     const int rows_y = sel ? maxact : maxact + T * s.K / kTileN + 1;   /* active experts, or slot tiles */
-    const int W = gateup_waves(s.F, rows_y, n_cu);
+    const int W = gateup_waves(s.F, rows_y, n_cu, !sel);
     if (!W) return hipErrorInvalidValue;
     dim3 grid(s.F / (8 * W), rows_y);
     const size_t lds = gateup_lds(W, NT, CB, nP, sel);
