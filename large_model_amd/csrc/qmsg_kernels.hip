@@ -2807,7 +2807,11 @@ hipError_t launch_dense(const DenseArgs &args, int type, uint8_t *xqk, hipStream
          * covers the batch, as long as the records fit in LDS */
         const int CB = type == 14 ? 64 : (nb % 16 == 0 ? 16 : 8);
         if (type == 14 && nb % 64) return hipErrorInvalidValue;     /* Q6_K: cols % 2048 */
-        int NT = a.T <= kDenseTokW ? 1 : (a.T <= 2 * kDenseTokW ? 2 : 4);
+        /* Q4_0 / Q4_1: at most two tokens per wave and pass, although the rows are then
+         * streamed once per 8 tokens instead of 16 (T = 16 154.7 -> 128.3 us per trunk layer,
+         * T = 32 294 -> 242: half the record buffer lets two blocks share a CU); Q6_K, whose
+         * per-token work is heavier, measured 1-2 % slower that way and keeps four */
+        int NT = a.T <= kDenseTokW ? 1 : ((type == 14 && a.T > 2 * kDenseTokW) ? 4 : 2);
         while (NT > 1 && dense_tok_lds(NT, CB, type, nb) > 160 * 1024) NT >>= 1;
         const size_t lds = dense_tok_lds(NT, CB, type, nb);
         if (lds <= 160 * 1024) {
