@@ -2412,10 +2412,12 @@ __device__ __forceinline__ float oct_finish(float acc, float corr, float scale)
 /* Q6_K super-block s of a row's chunk in LDS for octet lane k, against the chunk's pair
  * records xc: the lane's chain of dot_q6_k (src/kernels.c:148-167) takes bytes 4k..4k+3 of
  * each 32-block's codes with sub-scale sc[2g] (k < 4) or sc[2g+1] (k >= 4); the offset chain
- * (corr) runs on every lane alike. A half's words are all requested before its arithmetic.
+ * (corr) runs on every lane alike. For each of the nt <= NT tokens (records xs bytes apart)
+ * a half's words are all requested before its arithmetic; the weight words are read once.
  * AL: the super-block starts at a multiple of 4 bytes. */
-template <bool AL>
-__device__ __forceinline__ void q6_k_oct(const uint8_t *Wr, int s, int k, const uint8_t *xc, float &acc, float &corr)
+template <bool AL, int NT>
+__device__ __forceinline__ void q6_k_oct(const uint8_t *Wr, int s, int k, const uint8_t *xc, size_t xs, int nt,
+                                         float *acc, float *corr)
 {
     const int p = k & 3, hi = k >> 2;
     const uint32_t sb = (uint32_t)(s * 210);
@@ -2425,38 +2427,44 @@ __device__ __forceinline__ void q6_k_oct(const uint8_t *Wr, int s, int k, const 
         const uint32_t ql0 = lds_word<AL>(Wr, sb + 64 * h + 4 * k), ql1 = lds_word<AL>(Wr, sb + 64 * h + 32 + 4 * k);
         const uint32_t qh = lds_word<AL>(Wr, sb + 128 + 32 * h + 4 * k);
         const uint32_t sc0 = lds_word<AL>(Wr, sb + 192 + 8 * h), sc1 = lds_word<AL>(Wr, sb + 196 + 8 * h);
-        const uint8_t *xp = xc + (size_t)(4 * s + 2 * h) * kPairBytes;   /* blocks 8s+4h .. +3 */
-        uint32_t xq[4];
-        float4 xd[2];
-        uint2 x16[2];
 #pragma unroll
-        for (int g = 0; g < 4; g++) xq[g] = *(const uint32_t *)(xp + (g >> 1) * kPairBytes + 16 * p + 8 * (g & 1) + 4 * hi);
+        for (int n = 0; n < NT; n++) {
+            if (n >= nt) break;
+            const uint8_t *xp = xc + n * xs + (size_t)(4 * s + 2 * h) * kPairBytes;   /* blocks 8s+4h .. +3 */
+            uint32_t xq[4];
+            float4 xd[2];
+            uint2 x16[2];
 #pragma unroll
-        for (int j = 0; j < 2; j++) {
-            xd[j] = *(const float4 *)(xp + j * kPairBytes + 64);
-            x16[j] = *(const uint2 *)(xp + j * kPairBytes + 80);
-        }
-        __builtin_amdgcn_sched_barrier(0);
+            for (int g = 0; g < 4; g++)
+                xq[g] = *(const uint32_t *)(xp + (g >> 1) * kPairBytes + 16 * p + 8 * (g & 1) + 4 * hi);
 #pragma unroll
-        for (int g = 0; g < 4; g++) {
-            const uint32_t ql = (g & 1) ? ql1 : ql0;
-            const uint32_t nib = g < 2 ? (ql & 0x0f0f0f0fu) : ((ql >> 4) & 0x0f0f0f0fu);
-            const uint32_t q6 = nib | (((qh >> (2 * g)) & 0x03030303u) << 4);
-            const uint32_t scw = (g < 2 ? sc0 : sc1) >> (16 * (g & 1));
-            const int sa = (int)(int8_t)(scw & 0xff), sbv = (int)(int8_t)((scw >> 8) & 0xff);
-            const float xdv = (g & 1) ? xd[g >> 1].z : xd[g >> 1].x;
-            const uint32_t s16 = (g & 1) ? x16[g >> 1].y : x16[g >> 1].x;
-            const int s16a = (int)(int16_t)(s16 & 0xffffu), s16b = (int)(int16_t)(s16 >> 16);
-            const float dd = d * xdv;
-            acc = __builtin_fmaf((float)(sdot4((int)q6, (int)xq[g]) * (hi ? sbv : sa)), dd, acc);
-            corr = __builtin_fmaf(dd, (float)(sa * s16a + sbv * s16b), corr);
+            for (int j = 0; j < 2; j++) {
+                xd[j] = *(const float4 *)(xp + j * kPairBytes + 64);
+                x16[j] = *(const uint2 *)(xp + j * kPairBytes + 80);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int g = 0; g < 4; g++) {
+                const uint32_t ql = (g & 1) ? ql1 : ql0;
+                const uint32_t nib = g < 2 ? (ql & 0x0f0f0f0fu) : ((ql >> 4) & 0x0f0f0f0fu);
+                const uint32_t q6 = nib | (((qh >> (2 * g)) & 0x03030303u) << 4);
+                const uint32_t scw = (g < 2 ? sc0 : sc1) >> (16 * (g & 1));
+                const int sa = (int)(int8_t)(scw & 0xff), sbv = (int)(int8_t)((scw >> 8) & 0xff);
+                const float xdv = (g & 1) ? xd[g >> 1].z : xd[g >> 1].x;
+                const uint32_t s16 = (g & 1) ? x16[g >> 1].y : x16[g >> 1].x;
+                const int s16a = (int)(int16_t)(s16 & 0xffffu), s16b = (int)(int16_t)(s16 >> 16);
+                const float dd = d * xdv;
+                acc[n] = __builtin_fmaf((float)(sdot4((int)q6, (int)xq[g]) * (hi ? sbv : sa)), dd, acc[n]);
+                corr[n] = __builtin_fmaf(dd, (float)(sa * s16a + sbv * s16b), corr[n]);
+            }
         }
     }
 }
 
-template <int TYPE, int CB, int D, int W>
+template <int TYPE, int CB, int D, int W, int NT = 1>
 __global__ __launch_bounds__(64 * W) void dense_oct_kernel(DenseArgs a)
 {
+    static_assert(NT == 1 || TYPE == 14, "several tokens only for Q6_K rows");
     extern __shared__ __align__(16) uint8_t smem[];
     constexpr int BB = TYPE == 3 ? 20 : 18;           /* bytes per 32-block (Q4_0, Q4_1)      */
     /* one row's chunk: CB 32-blocks (Q6_K: CB/8 super-blocks, CB = 64 keeps 16-byte slots) */
@@ -2471,7 +2479,8 @@ __global__ __launch_bounds__(64 * W) void dense_oct_kernel(DenseArgs a)
     const int tid = threadIdx.x, lane = tid & 63, rr = lane >> 3, k = lane & 7;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     uint8_t *wbuf = smem + wave * 8 * WS;
-    uint8_t *xbuf = smem + W * 8 * WS;
+    uint8_t *xbuf = smem + W * 8 * WS;                /* [a.T][nP][96]                        */
+    const int nqb = a.T * nb;                         /* input 32-blocks of every token       */
 
     int mi = 0;
 #pragma unroll
@@ -2494,7 +2503,7 @@ __global__ __launch_bounds__(64 * W) void dense_oct_kernel(DenseArgs a)
      * W waves share one quantisation of the row (one 32-block per thread, then any rest). */
     float4 xr[8];
     {
-        const float4 *src = (const float4 *)(a.x + (size_t)min(tid, nb - 1) * 32);
+        const float4 *src = (const float4 *)(a.x + (size_t)min(tid, nqb - 1) * 32);
 #pragma unroll
         for (int j = 0; j < 8; j++) xr[j] = src[j];
     }
@@ -2503,26 +2512,30 @@ __global__ __launch_bounds__(64 * W) void dense_oct_kernel(DenseArgs a)
     for (int d = 0; d < D; d++)
         if (d < nchunk) load_chunk(d, wv[d]);
     __builtin_amdgcn_sched_barrier(0);
-    if (tid < nb) {
+    if (tid < nqb) {
         float v[32];
 #pragma unroll
         for (int j = 0; j < 8; j++) {
             v[4 * j] = xr[j].x; v[4 * j + 1] = xr[j].y; v[4 * j + 2] = xr[j].z; v[4 * j + 3] = xr[j].w;
         }
-        store_pair_half(quantize_block(v), (uint32_t *)(xbuf + (size_t)(tid >> 1) * kPairBytes), tid & 1);
+        const int n = tid / nb, blk = tid - n * nb;
+        store_pair_half(quantize_block(v), (uint32_t *)(xbuf + ((size_t)n * nP + (blk >> 1)) * kPairBytes), blk & 1);
     }
-    for (int b = tid + NTH; b < nb; b += NTH) {       /* rows longer than one block per thread */
+    for (int b = tid + NTH; b < nqb; b += NTH) {      /* rows longer than one block per thread */
         float v[32];
         const float4 *src = (const float4 *)(a.x + (size_t)b * 32);
         for (int j = 0; j < 8; j++) {
             const float4 f = src[j];
             v[4 * j] = f.x; v[4 * j + 1] = f.y; v[4 * j + 2] = f.z; v[4 * j + 3] = f.w;
         }
-        store_pair_half(quantize_block(v), (uint32_t *)(xbuf + (size_t)(b >> 1) * kPairBytes), b & 1);
+        const int n = b / nb, blk = b - n * nb;
+        store_pair_half(quantize_block(v), (uint32_t *)(xbuf + ((size_t)n * nP + (blk >> 1)) * kPairBytes), blk & 1);
     }
     if (W > 1) __syncthreads();
     else wave_sync();
-    float acc = 0.0f, corr = 0.0f;
+    float acc[NT], corr[NT];
+#pragma unroll
+    for (int n = 0; n < NT; n++) acc[n] = corr[n] = 0.0f;
     for (int c0 = 0; c0 < nchunk; c0 += D) {
 #pragma unroll
         for (int d = 0; d < D; d++) {
@@ -2540,8 +2553,9 @@ __global__ __launch_bounds__(64 * W) void dense_oct_kernel(DenseArgs a)
                     const uint8_t *xc = xbuf + (size_t)c * (CB / 2) * kPairBytes;
 #pragma unroll 1
                     for (int sbi = 0; sbi < CB / 8; sbi += 2) {   /* even super-blocks 4-aligned */
-                        q6_k_oct<true>(wbuf + rr * WS, sbi, k, xc, acc, corr);
-                        q6_k_oct<false>(wbuf + rr * WS, sbi + 1, k, xc, acc, corr);
+                        q6_k_oct<true, NT>(wbuf + rr * WS, sbi, k, xc, (size_t)nP * kPairBytes, a.T, acc, corr);
+                        q6_k_oct<false, NT>(wbuf + rr * WS, sbi + 1, k, xc, (size_t)nP * kPairBytes, a.T, acc,
+                                            corr);
                     }
                 } else {
                     const uint32_t *Wrow = (const uint32_t *)(wbuf + rr * WS);
@@ -2557,14 +2571,17 @@ __global__ __launch_bounds__(64 * W) void dense_oct_kernel(DenseArgs a)
                                                    xbuf + (size_t)(c * (CB / 2) + q0 + u) * kPairBytes);
                         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-                        for (int u = 0; u < PB; u++) oct_math<TYPE>(in[u], k, acc, corr);
+                        for (int u = 0; u < PB; u++) oct_math<TYPE>(in[u], k, acc[0], corr[0]);
                     }
                 }
             }
         }
     }
-    const float v = oct_finish(acc, corr, finish_scale(TYPE));
-    if (k == 0 && rw + rr < M.rows) M.y[rw + rr] = v;
+#pragma unroll
+    for (int n = 0; n < NT; n++) {
+        const float v = oct_finish(acc[n], corr[n], finish_scale(TYPE));
+        if (k == 0 && n < a.T && rw + rr < M.rows) M.y[(size_t)n * M.rows + rw + rr] = v;
+    }
 }
 
 /* Two chunks in flight per wave (2, 4 and 8 were measured at the trunk's shapes: 2 fastest). */
@@ -2764,7 +2781,11 @@ hipError_t launch_dense(const DenseArgs &args, int type, uint8_t *xqk, hipStream
     }
     /* one wave per block, 16 rows each: the trunk's small matrices (attn_k/v: 512 rows) still
      * spread over 32 CUs, the large ones over every CU */
-    if (a.T == 1 && (type != 14 || nb % 64 == 0)) {  /* eight lanes per row, 8 rows per wave */
+    /* eight lanes per row, 8 rows per wave: one token, or Q6_K rows for two or three (each
+     * super-block's weight words read once for all of them: trunk layer 81.9 -> 56.3 us at
+     * T = 2, 85.4 -> 74.6 at T = 3; at T = 4 the token-parallel kernel is faster, 85.6
+     * against 90.6) */
+    if ((a.T == 1 && (type != 14 || nb % 64 == 0)) || (type == 14 && a.T <= 3 && nb % 64 == 0)) {
         /* W waves per block share the input row's quantisation: the most that still gives
          * every CU a block */
         int rows = 0;
@@ -2778,12 +2799,15 @@ hipError_t launch_dense(const DenseArgs &args, int type, uint8_t *xqk, hipStream
         const int CB = type == 14 ? 64 : (nb % 16 == 0 ? 16 : 8);
         const int rcb = type == 14 ? CB / 8 * 210 : CB * (type == 3 ? 20 : 18);
         const size_t ws = (size_t)rcb + (((rcb / 16) & 1) ? 0 : 16);
-        const size_t lds8 = (size_t)W * 8 * ws + (size_t)(nb / 2) * kPairBytes;
+        const size_t lds8 = (size_t)W * 8 * ws + (size_t)a.T * (nb / 2) * kPairBytes;
         if (lds8 > 160 * 1024) return hipErrorInvalidValue;
         auto go = [&](auto tw) {
             constexpr int WW = decltype(tw)::value;
             if (type == 14) {
-                QLAUNCH("dense", (dense_oct_kernel<14, 64, 2, WW>), dim3(nbw), dim3(64 * WW), lds8, st, a);
+                if (a.T == 1) QLAUNCH("dense", (dense_oct_kernel<14, 64, 2, WW>), dim3(nbw), dim3(64 * WW), lds8, st, a);
+                else if (a.T == 2)
+                    QLAUNCH("dense", (dense_oct_kernel<14, 64, 2, WW, 2>), dim3(nbw), dim3(64 * WW), lds8, st, a);
+                else QLAUNCH("dense", (dense_oct_kernel<14, 64, 2, WW, 4>), dim3(nbw), dim3(64 * WW), lds8, st, a);
             } else if (type == 3) {
                 if (CB == 16) QLAUNCH("dense", (dense_oct_kernel<3, 16, 2, WW>), dim3(nbw), dim3(64 * WW), lds8, st, a);
                 else QLAUNCH("dense", (dense_oct_kernel<3, 8, 2, WW>), dim3(nbw), dim3(64 * WW), lds8, st, a);

@@ -128,7 +128,7 @@ def test_dense_from_gguf_and_errors(q, tmp_path):
         assert ei.value.status == -2
 
 
-@pytest.mark.parametrize("T", [1, 2, 5, 9])
+@pytest.mark.parametrize("T", [1, 2, 3, 4, 5, 9])
 def test_dense_q6k_and_f32_trunk_shapes(q, T):
     """Q6_K and F32 rows (the other types of qms_matmul's fast path, src/quant.c:128-170): the
     235B trunk's q/k/v shapes in Q6_K (super-blocks staged in chunks of eight), an F32 matrix
