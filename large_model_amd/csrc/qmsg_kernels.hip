@@ -492,8 +492,11 @@ __device__ void topk_token(const SelectArgs &a, int t, double *P, int *part, int
     const double z = zs;
     for (int e = tid; e < X; e += 256) P[e] /= z;
     __syncthreads();
-    /* rank(e) = #{e' : P[e'] > P[e]} + #{e' < e : P[e'] == P[e]}, split over two threads */
-    for (int w = tid; w < 2 * X; w += 256) {
+    /* rank(e) = #{e' : P[e'] > P[e]} + #{e' < e : P[e'] == P[e]}, split over two threads.
+     * A NaN or infinite logit makes z and every p NaN: no p then compares greater, so the
+     * reference's argmax rounds take experts 0 .. K-1 in order (src/model.c:1053-1062). */
+    const bool nan_p = z != z;
+    for (int w = tid; w < 2 * X && !nan_p; w += 256) {
         const int e = w >> 1, half = w & 1;
         const double pe = P[e];
         const int lo = half ? X / 2 : 0, hi = half ? X : X / 2;
@@ -506,9 +509,13 @@ __device__ void topk_token(const SelectArgs &a, int t, double *P, int *part, int
         part[w] = r;
     }
     __syncthreads();
-    for (int e = tid; e < X; e += 256) {
-        const int r = part[2 * e] + part[2 * e + 1];
-        if (r < K) selb[r] = e;
+    if (nan_p) {
+        if (tid < K) selb[tid] = tid;
+    } else {
+        for (int e = tid; e < X; e += 256) {
+            const int r = part[2 * e] + part[2 * e + 1];
+            if (r < K) selb[r] = e;
+        }
     }
     __syncthreads();
     if (tid == 0) {
@@ -942,15 +949,27 @@ __device__ void route_one_select(const Scratch &S, int K, int X, SmallRoute *R, 
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     if (wave == 0) {
         int *cand = R->cand;
-        for (int e = lane; e < X; e += 64)
-            if (rank[e] <= K) cand[rank[e]] = e;
+        /* A NaN or infinite logit makes z and every p NaN (p is finite otherwise): no p then
+         * compares greater, so the reference's argmax rounds take experts 0 .. K-1 in order
+         * (src/model.c:1053-1062). The logit ranks are no permutation then and stay unused. */
+        const bool nan_p = P[0] != P[0];
+        if (!nan_p)
+            for (int e = lane; e < X; e += 64)
+                if (rank[e] <= K) cand[rank[e]] = e;
         wave_sync();
+        /* Equal logits have equal p and sort by index in both orders. A p tie between logits
+         * of different value sorts by logit here but by index in the reference, so every
+         * adjacent pair must have strictly decreasing p or equal logits; across the boundary
+         * (K-1, K) the p must decrease strictly, since an equal-p run may continue past K with
+         * a lower logit and a lower index. */
         bool ok = true;
-        if (lane < K) {
+        if (lane < K && !nan_p) {
             const int a = cand[lane], b = cand[lane + 1];
-            ok = P[a] > P[b] || L[a] == L[b];
+            ok = P[a] > P[b] || (lane < K - 1 && L[a] == L[b]);
         }
-        if (__ballot(!ok) == 0ULL) {
+        if (nan_p) {
+            if (lane < K) R->sel[lane] = lane;
+        } else if (__ballot(!ok) == 0ULL) {
             if (lane < K) R->sel[lane] = cand[lane];
         } else {
             /* a rounding tie among the candidates: rank the p exactly */

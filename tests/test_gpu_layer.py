@@ -165,3 +165,44 @@ def test_one_token_tokens_in_a_row(qmsg, name, E, X, K, F, seed, dt, rms):
                 for k in ("logits", "wt", "xq", "gu", "act", "aq", "dn"):
                     assert np.array_equal(_bits(got[k]), _bits(ref[k])), (path, t, k)
                 assert np.array_equal(_bits(out), _bits(ref_out)), (path, t, "layer output")
+
+
+EDGE_CASES = [
+    # name, tokens of the case's input, path
+    ("nonfinite", (0, 1), "auto"),         # batch: the select kernel
+    ("nonfinite", (1,), "auto"),           # one token routed inside the gate/up kernel, every p NaN
+    ("nonfinite", (0,), "auto"),           # one token, p = 1 and fifteen p = 0
+    ("boundary_underflow", (0,), "auto"),  # logit tie at the top-K boundary, underflowed p
+    ("boundary_underflow", (0, 0), "auto"),
+    ("nonfinite", (0, 1), "fp32"),         # the --exact mode's routing
+]
+
+
+@pytest.mark.parametrize("name,toks,path", EDGE_CASES, ids=[f"{c[0]}_t{''.join(map(str, c[1]))}_{c[2]}" for c in EDGE_CASES])
+def test_routing_edge_cases(qmsg, name, toks, path):
+    """A non-finite logit (every p NaN: the reference takes experts 0 .. K-1 with NaN weights)
+    and an exact logit tie at the top-K boundary with underflowed p (the lowest untaken index
+    wins): expert ids, dispatch and every finite intermediate bit for bit against the oracle,
+    NaN weights and outputs in the same places."""
+    import routing_cases as rc
+    seed = 81 if name == "nonfinite" else 82
+    col0, x_all, expect = rc.CASES[name](seed)
+    x = np.ascontiguousarray(x_all[list(toks)])
+    print(f"[case] routing edge {name} tokens={toks} path={path}", flush=True)
+    host = rc.layer(col0, seed)
+    exact = path == "fp32"
+    ref_out, ref = host.moe(x, debug=True, exact=exact)
+    assert np.array_equal(ref["sel"], expect[list(toks)])
+    with qmsg.Context(rc.E, rc.X, rc.K, rc.F, n_layer=1, max_tokens=len(toks)) as ctx:
+        ctx.synth(0, seed, router_col0=col0)
+        if exact:
+            ctx.set_path(qmsg.PATH_FP32)
+        out, got = ctx.moe_debug(0, x)
+    for k in ("sel", "start", "slot_t", "slot_of", "active"):
+        assert np.array_equal(got[k], ref[k]), (k, got[k], ref[k])
+    assert np.array_equal(_bits(got["logits"]), _bits(ref["logits"])), "router logits"
+    assert rc.same_bits_or_both_nan(got["wt"], ref["wt"]), (got["wt"], ref["wt"])
+    keys = ("gu", "act", "dn") if exact else ("xq", "gu", "act", "aq", "dn")
+    for k in keys:
+        assert np.array_equal(_bits(got[k]), _bits(ref[k])), k
+    assert rc.same_bits_or_both_nan(out, ref_out), "layer output"

@@ -13,6 +13,7 @@ import numpy as np
 import pytest
 
 import oracle as orc
+import routing_cases as rc
 
 GOLD = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
 
@@ -262,6 +263,31 @@ def test_tied_experts_keep_lower_index_first():
         s = list(sel[t])
         picked = [e for e in s if e in (2, 5, 9)]
         assert picked == sorted(picked)
+
+
+@pytest.mark.parametrize("name", sorted(rc.CASES))
+def test_routing_edge_cases(name):
+    """A non-finite logit (every p NaN: experts 0 .. K-1, NaN weights) and an exact logit tie
+    at the top-K boundary whose p underflow to 0 (the lowest untaken index wins): the oracle's
+    selection equals the hand-derived argmax rounds, and its layer output equals the
+    reference build's moe() bit for bit, NaN in the same places."""
+    seed = 81 if name == "nonfinite" else 82
+    col0, x, expect_sel = rc.CASES[name](seed)
+    L = rc.layer(col0, seed)
+    lg, sel, wt = L.route(x)
+    assert np.array_equal(sel, expect_sel), sel
+    if name == "nonfinite":
+        assert np.isposinf(lg[1, 5]) and np.isfinite(lg[0]).all()
+        assert np.isnan(wt[1]).all() and np.array_equal(wt[0], np.float32([1, 0, 0, 0]))
+    else:
+        assert np.array_equal(lg[0], col0)
+        assert wt[0, 3] == 0.0 and np.isfinite(wt).all()
+    out = L.moe(x)
+    assert np.isnan(out[1]).all() if name == "nonfinite" else np.isfinite(out).all()
+    R = orc.load_ref()
+    if R is None:
+        pytest.skip("reference build (oracle/_ref) not present")
+    assert rc.same_bits_or_both_nan(orc.ref_moe(R, L, x), out)
 
 
 # ------------------------------------------------------------------ planted mistakes
