@@ -214,6 +214,16 @@ int qmsg_moe(qmsg_ctx *ctx, int layer, const float *xn, const float *h, int T, f
  * context's stream without waiting. */
 int qmsg_moe_device(qmsg_ctx *ctx, int layer, const float *d_xn, int T, float *d_out);
 
+/* No counterpart in the reference: for callers that cannot allocate device memory (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). The same layer as
+ * qmsg_moe_device, with the same results, but its scratch arrays come from a static 32 MiB
+ * device array of the library (one per GPU, held until the process ends) instead of the
+ * context's, and it calls no hipMalloc, hipFree or other allocating routine. T is not bound
+ * by max_tokens; a T whose scratch exceeds 32 MiB (above about 100 tokens at the 235B shape)
+ * returns QMSG_E_RANGE. Every call on one GPU shares that array: calls that overlap on one
+ * GPU (two streams, or two contexts on one device) race and must be serialised. */
+int qmsg_moe_device_noalloc(qmsg_ctx *ctx, int layer, const float *d_xn, int T, float *d_out);
+
 /* The MoE half of qms_forward's layer loop (src/model.c:1283-1285) over the resident layers
  * first .. first+n-1, on device rows d_h [T][E] updated in place: for each layer,
  * xn = rmsnorm(h, ffn_norm) (src/model.c:403-409, eps as the model's rms_norm_eps) and

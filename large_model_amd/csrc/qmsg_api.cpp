@@ -4,6 +4,7 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <mutex>
 #include <string>
 #include <thread>
 #include <vector>
@@ -53,6 +54,72 @@ uint64_t row_bytes(int type, int64_t ne0)
 }
 
 thread_local std::string g_create_error;
+
+/* The device scratch arrays of one layer call for T tokens: where each pointer of S goes and
+ * how many bytes it needs. */
+struct ScratchItem {
+    void **p;
+    size_t bytes;
+};
+
+std::vector<ScratchItem> scratch_items(const qmsg_cfg &cfg, size_t T, Scratch *S)
+{
+    const size_t E = (size_t)cfg.n_embd, X = (size_t)cfg.n_expert, F = (size_t)cfg.n_ff_exp;
+    const size_t NS = T * (size_t)cfg.n_used, nbE = E / 32, nbF = F / 32;
+    return {
+        { (void **)&S->logits, T * X * 4 },     { (void **)&S->sel, NS * 4 },
+        { (void **)&S->wt, NS * 4 },            { (void **)&S->slot_t, NS * 4 },
+        { (void **)&S->slot_of, NS * 4 },       { (void **)&S->start, (X + 1) * 4 },
+        { (void **)&S->active, X * 4 },         { (void **)&S->meta, 64 },
+        { (void **)&S->work, X * 16 },          { (void **)&S->tiles, (X + NS / kTileN + 1) * 16 },
+        { (void **)&S->xq, T * nbE * sizeof(Q8) }, { (void **)&S->xqk, T * (nbE / 2) * kPairBytes },
+        { (void **)&S->gu, NS * 2 * F * 4 },    { (void **)&S->act, NS * F * 4 },
+        { (void **)&S->aq, NS * nbF * sizeof(Q8) }, { (void **)&S->aqk, NS * (nbF / 2) * kPairBytes },
+        { (void **)&S->dn, NS * E * 4 },
+    };
+}
+
+/* ---- the allocation-free layer call (qmsg_moe_device_noalloc) ----
+ * Its scratch arrays live in this file-scope device array, one copy per GPU, held until the
+ * process ends. Host code never passes `scratch` itself (in host code the name is only a
+ * stand-in): each device's address comes from hipGetSymbolAddress, taken once per device
+ * with that device current (in qmsg_create), and only that address is used. */
+constexpr size_t kNoAllocScratchBytes = (size_t)32 << 20;
+constexpr int kMaxDevices = 64;
+__device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
+
+std::mutex g_noalloc_mu;
+void *g_noalloc_ptr[kMaxDevices];
+hipError_t g_noalloc_err[kMaxDevices];
+
+/* The device's address of `scratch`; the calling thread has `device` current. */
+hipError_t noalloc_scratch_setup(int device)
+{
+    if (device < 0 || device >= kMaxDevices) return hipErrorInvalidDevice;
+    std::lock_guard<std::mutex> lock(g_noalloc_mu);
+    if (g_noalloc_ptr[device]) return hipSuccess;
+    void *ptr = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    g_noalloc_err[device] = e;
+    if (e == hipSuccess) g_noalloc_ptr[device] = ptr;
+    return e;
+}
+
+/* Carve the scratch of a T-token call out of [base, base + cap): every array 256-byte aligned
+ * and followed by 256 bytes, as dev_alloc pads (kernels may read one aligned word past an
+ * array's end). Returns the bytes needed; S is filled only when they fit. */
+size_t scratch_carve(const qmsg_cfg &cfg, size_t T, uint8_t *base, size_t cap, Scratch *S)
+{
+    Scratch tmp{};
+    size_t off = 0;
+    std::vector<ScratchItem> items = scratch_items(cfg, T, &tmp);
+    for (auto &it : items) {
+        *it.p = base + off;
+        off += ((it.bytes + 255) & ~(size_t)255) + 256;
+    }
+    if (off <= cap) *S = tmp;
+    return off;
+}
 
 }  // namespace
 
@@ -165,20 +232,15 @@ int qmsg_create(qmsg_ctx **out, int device, const qmsg_cfg *cfg, int n_layer, in
         delete c;
         return QMSG_E_DEVICE;
     }
-    const size_t Tm = (size_t)max_tokens, NS = Tm * K, nbE = E / 32, nbF = F / 32;
-    struct Item { void **p; size_t bytes; } items[] = {
-        { (void **)&c->S.logits, Tm * X * 4 },  { (void **)&c->S.sel, NS * 4 },
-        { (void **)&c->S.wt, NS * 4 },          { (void **)&c->S.slot_t, NS * 4 },
-        { (void **)&c->S.slot_of, NS * 4 },     { (void **)&c->S.start, (size_t)(X + 1) * 4 },
-        { (void **)&c->S.active, (size_t)X * 4 }, { (void **)&c->S.meta, 64 },
-        { (void **)&c->S.work, (size_t)X * 16 },
-        { (void **)&c->S.tiles, ((size_t)X + NS / kTileN + 1) * 16 },
-        { (void **)&c->S.xq, Tm * nbE * sizeof(Q8) }, { (void **)&c->S.xqk, Tm * (nbE / 2) * kPairBytes },
-        { (void **)&c->S.gu, NS * 2 * F * 4 },  { (void **)&c->S.act, NS * F * 4 },
-        { (void **)&c->S.aq, NS * nbF * sizeof(Q8) }, { (void **)&c->S.aqk, NS * (nbF / 2) * kPairBytes },
-        { (void **)&c->S.dn, NS * E * 4 },      { (void **)&c->d_x, Tm * E * 4 },
-        { (void **)&c->d_out, Tm * E * 4 },
-    };
+    if (noalloc_scratch_setup(device) != hipSuccess) {
+        fail(nullptr, QMSG_E_DEVICE, "qmsg_create: static scratch of device %d: %s", device,
+             hipGetErrorString(g_noalloc_err[device]));
+        delete c;
+        return QMSG_E_DEVICE;
+    }
+    std::vector<ScratchItem> items = scratch_items(*cfg, (size_t)max_tokens, &c->S);
+    items.push_back({ (void **)&c->d_x, (size_t)max_tokens * E * 4 });
+    items.push_back({ (void **)&c->d_out, (size_t)max_tokens * E * 4 });
     for (auto &it : items) {
         if (dev_alloc(c, it.p, it.bytes, c->scratch_allocs) != QMSG_OK) {
             g_create_error = c->err;
@@ -708,12 +770,12 @@ int qmsg_matmul_n(qmsg_ctx *c, const int *ids, int nW, const float *x, int T, fl
     return QMSG_OK;
 }
 
-static int run_layer(qmsg_ctx *c, int layer, const float *d_xn, int T, float *d_out, int debug)
+/* One layer on device buffers with the scratch arrays S (the context's, or carved from the
+ * library's static array by qmsg_moe_device_noalloc). */
+static int run_layer_s(qmsg_ctx *c, const Scratch &S, int layer, const float *d_xn, int T, float *d_out, int debug)
 {
     int rc = check_layer_index(c, layer);
     if (rc) return rc;
-    if (T < 0 || T > c->max_tokens)
-        return fail(c, QMSG_E_RANGE, "T=%d outside [0, max_tokens=%d]", T, c->max_tokens);
     const LayerStore &L = c->layers[(size_t)layer];
     if (!L.ready) return fail(c, QMSG_E_INVALID, "layer %d has no weights", layer);
     if (T == 0) return QMSG_OK;
@@ -722,7 +784,7 @@ static int run_layer(qmsg_ctx *c, int layer, const float *d_xn, int T, float *d_
     const Shape s{ c->cfg.n_embd, c->cfg.n_expert, c->cfg.n_used, c->cfg.n_ff_exp };
     const LayerDev d = layer_dev(c, L);
     if (c->path == QMSG_PATH_FP32) {
-        LAUNCH(c, "layer", launch_layer_fp32(s, d, c->S, d_xn, d_out, T, c->stream));
+        LAUNCH(c, "layer", launch_layer_fp32(s, d, S, d_xn, d_out, T, c->stream));
         return QMSG_OK;
     }
     /* Q4_0 gate and up take the streaming gate/up kernel (which also routes one-token batches)
@@ -730,24 +792,51 @@ static int run_layer(qmsg_ctx *c, int layer, const float *d_xn, int T, float *d_
     const bool q40 = d.gate_type == QMSG_T_Q4_0 && d.up_type == QMSG_T_Q4_0;
     const bool mfma = c->path == QMSG_PATH_MFMA && q40 && !use_small_route(T, s.K) && s.E % 256 == 0 &&
                       s.F % 256 == 0;
-    LAUNCH(c, "route", launch_route(s, d, c->S, d_xn, T, c->stream));
-    LAUNCH(c, "select", launch_select(s, c->S, T, q40 ? 1 : 0, c->stream));
+    LAUNCH(c, "route", launch_route(s, d, S, d_xn, T, c->stream));
+    LAUNCH(c, "select", launch_select(s, S, T, q40 ? 1 : 0, c->stream));
     if (mfma) {
-        LAUNCH(c, "experts", launch_experts_mfma(s, d, c->S, d_out, T, debug, c->stream));
+        LAUNCH(c, "experts", launch_experts_mfma(s, d, S, d_out, T, debug, c->stream));
     } else if (!q40) {
-        LAUNCH(c, "gateup", launch_gateup_tiles(s, d, c->S, T, c->stream));
-        LAUNCH(c, "down", launch_down_exact(s, d, c->S, d_out, T, 1, c->stream));
+        LAUNCH(c, "gateup", launch_gateup_tiles(s, d, S, T, c->stream));
+        LAUNCH(c, "down", launch_down_exact(s, d, S, d_out, T, 1, c->stream));
     } else {
-        LAUNCH(c, "gateup", launch_gateup_exact(s, d, c->S, T, debug, c->n_cu, c->stream));
-        LAUNCH(c, "down", launch_down_exact(s, d, c->S, d_out, T, 1, c->stream));
+        LAUNCH(c, "gateup", launch_gateup_exact(s, d, S, T, debug, c->n_cu, c->stream));
+        LAUNCH(c, "down", launch_down_exact(s, d, S, d_out, T, 1, c->stream));
     }
     return QMSG_OK;
+}
+
+static int run_layer(qmsg_ctx *c, int layer, const float *d_xn, int T, float *d_out, int debug)
+{
+    if (T < 0 || T > c->max_tokens)
+        return fail(c, QMSG_E_RANGE, "T=%d outside [0, max_tokens=%d]", T, c->max_tokens);
+    return run_layer_s(c, c->S, layer, d_xn, T, d_out, debug);
 }
 
 int qmsg_moe_device(qmsg_ctx *c, int layer, const float *d_xn, int T, float *d_out)
 {
     if (!c) return QMSG_E_INVALID;
     return run_layer(c, layer, d_xn, T, d_out, 0);
+}
+
+int qmsg_moe_device_noalloc(qmsg_ctx *c, int layer, const float *d_xn, int T, float *d_out)
+{
+    if (!c) return QMSG_E_INVALID;
+    if (T < 0) return fail(c, QMSG_E_RANGE, "T=%d is negative", T);
+    if (c->device < 0 || c->device >= kMaxDevices || !g_noalloc_ptr[c->device])
+        return fail(c, QMSG_E_DEVICE, "qmsg_moe_device_noalloc: no static scratch on device %d", c->device);
+    Scratch S{};
+    const size_t need = scratch_carve(c->cfg, (size_t)T, (uint8_t *)g_noalloc_ptr[c->device], kNoAllocScratchBytes, &S);
+    if (need > kNoAllocScratchBytes)
+        return fail(c, QMSG_E_RANGE,
+                    "qmsg_moe_device_noalloc: T=%d needs %zu bytes of scratch, above the static maximum of %zu", T,
+                    need, kNoAllocScratchBytes);
+    if (T == 0) return run_layer_s(c, S, layer, d_xn, T, d_out, 0);
+    HIP_TRY(c, hipSetDevice(c->device));
+    /* the select kernel's ticket counter (meta[4]) must start at zero; a fill kernel rather
+     * than a memset node, so the call can be captured into a graph */
+    LAUNCH(c, "fill", launch_fill_u32((uint32_t *)S.meta, 0u, 16, c->stream));
+    return run_layer_s(c, S, layer, d_xn, T, d_out, 0);
 }
 
 int qmsg_layer_norm(qmsg_ctx *c, int layer, const float *w)

@@ -3155,6 +3155,19 @@ hipError_t launch_copy(void *dst, const void *src, size_t bytes, hipStream_t st)
     return hipGetLastError();
 }
 
+__global__ void fill_u32_kernel(uint32_t *p, uint32_t v, size_t n)
+{
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
+        p[i] = v;
+}
+
+hipError_t launch_fill_u32(uint32_t *p, uint32_t v, size_t n, hipStream_t st)
+{
+    const size_t blocks = n / 256 + 1;
+    QLAUNCH("fill", fill_u32_kernel, dim3(blocks < 1024 ? (unsigned)blocks : 1024u), dim3(256), 0, st, p, v, n);
+    return hipGetLastError();
+}
+
 /* ------------------------------------------------------------------ synthetic data ---- */
 
 __global__ void synth_f32_kernel(uint64_t key, uint64_t n, float sigma, float *out)

@@ -89,6 +89,7 @@ _SIGS = {
     "qmsg_layer_download": (_I, [_P, _I, _P, _P, _P, _P]),
     "qmsg_moe": (_I, [_P, _I, _P, _P, _I, _P]),
     "qmsg_moe_device": (_I, [_P, _I, _P, _I, _P]),
+    "qmsg_moe_device_noalloc": (_I, [_P, _I, _P, _I, _P]),
     "qmsg_sync": (_I, [_P]),
     "qmsg_device_alloc": (_P, [_P, ctypes.c_size_t]),
     "qmsg_memcpy_h2d": (_I, [_P, _P, _P, ctypes.c_size_t]),
@@ -422,6 +423,10 @@ class Context:
 
     def moe_device(self, layer: int, d_xn: int, T: int, d_out: int):
         self._check(lib.qmsg_moe_device(self._h, layer, d_xn, T, d_out))
+
+    def moe_device_noalloc(self, layer: int, d_xn: int, T: int, d_out: int):
+        """The same layer with the library's static scratch (allocates nothing)."""
+        self._check(lib.qmsg_moe_device_noalloc(self._h, layer, d_xn, T, d_out))
 
     def moe_chain(self, first: int, n: int, d_h: int, T: int, eps: float = 1e-6):
         """h += moe(l, rmsnorm(h, ffn_norm_l)) for layers first .. first+n-1 on device rows d_h."""
