@@ -76,6 +76,7 @@ std::vector<ScratchItem> scratch_items(const qmsg_cfg &cfg, size_t T, Scratch *S
         { (void **)&S->gu, NS * 2 * F * 4 },    { (void **)&S->act, NS * F * 4 },
         { (void **)&S->aq, NS * nbF * sizeof(Q8) }, { (void **)&S->aqk, NS * (nbF / 2) * kPairBytes },
         { (void **)&S->dn, NS * E * 4 },
+        { (void **)&S->mxx, T * nbE * 128 },    { (void **)&S->mxa, NS * nbF * 128 },
     };
 }
 
@@ -788,14 +789,15 @@ static int run_layer_s(qmsg_ctx *c, const Scratch &S, int layer, const float *d_
         return QMSG_OK;
     }
     /* Q4_0 gate and up take the streaming gate/up kernel (which also routes one-token batches)
-     * or the MFMA grouped GEMM; other types take the slot-tile row kernel */
+     * or, for batches with several slots per expert, the MFMA kernels; other types take the
+     * slot-tile row kernel */
     const bool q40 = d.gate_type == QMSG_T_Q4_0 && d.up_type == QMSG_T_Q4_0;
-    const bool mfma = c->path == QMSG_PATH_MFMA && q40 && !use_small_route(T, s.K) && s.E % 256 == 0 &&
-                      s.F % 256 == 0;
+    const bool mx_ok = q40 && !use_small_route(T, s.K) && mx_supported(s, d, nullptr);
+    const bool mfma = mx_ok && (c->path == QMSG_PATH_MFMA || (c->path == QMSG_PATH_AUTO && T >= kMxAutoT));
     LAUNCH(c, "route", launch_route(s, d, S, d_xn, T, c->stream));
     LAUNCH(c, "select", launch_select(s, S, T, q40 ? 1 : 0, c->stream));
     if (mfma) {
-        LAUNCH(c, "experts", launch_experts_mfma(s, d, S, d_out, T, debug, c->stream));
+        LAUNCH(c, "experts", launch_experts_mx(s, d, S, d_out, T, debug, c->stream));
     } else if (!q40) {
         LAUNCH(c, "gateup", launch_gateup_tiles(s, d, S, T, c->stream));
         LAUNCH(c, "down", launch_down_exact(s, d, S, d_out, T, 1, c->stream));

@@ -39,8 +39,11 @@ extern thread_local const LaunchTimer *g_launch_timer;
 /* Static shape limits of the kernels. */
 constexpr int kMaxExperts = 256;
 
-/* Slots (tokens of one expert) per tile of the MFMA grouped-GEMM kernels. */
+/* Slots (tokens of one expert) per slot tile of the batch kernels (dispatch's tile list). */
 constexpr int kTileN = 32;
+
+/* Batches of at least this many tokens take the MFMA expert kernels on the default path. */
+constexpr int kMxAutoT = 32;
 
 /* One-token batches (n_used <= 8) are routed inside the gate/up kernel instead of by a
  * separate select launch. */
@@ -76,6 +79,8 @@ struct Scratch {
     Q8 *aq;             /* [Tm*K][F/32]        */
     uint8_t *aqk;       /* [Tm*K][F/64][96]    */
     float *dn;          /* [Tm*K][E]           */
+    uint8_t *mxx;       /* [Tm][E/32][128] MFMA records of the layer input */
+    uint8_t *mxa;       /* [Tm*K][F/32][128] MFMA records of the activations */
 };
 
 struct Shape {
@@ -110,8 +115,12 @@ hipError_t launch_route(const Shape &s, const LayerDev &L, const Scratch &S, con
 hipError_t launch_select(const Shape &s, const Scratch &S, int T, int gateup_routes, hipStream_t st);
 hipError_t launch_gateup_exact(const Shape &s, const LayerDev &L, const Scratch &S, int T, int debug, int n_cu,
                                hipStream_t st);
-hipError_t launch_experts_mfma(const Shape &s, const LayerDev &L, const Scratch &S, float *out, int T, int debug,
-                               hipStream_t st);
+/* The expert products on the matrix cores (order-exact): gate/up, then down and the combine.
+ * mx_supported: whether the layer's types and shape fit the MFMA kernels (Q4_0 gate and up;
+ * *down_mx: whether down runs on them too, else on the exact down kernel). */
+bool mx_supported(const Shape &s, const LayerDev &L, int *down_mx);
+hipError_t launch_experts_mx(const Shape &s, const LayerDev &L, const Scratch &S, float *out, int T, int debug,
+                             hipStream_t st);
 /* Gate/up rows of Q4_1 / Q6_K (or mixed) layers by slot tiles, then the SwiGLU. */
 hipError_t launch_gateup_tiles(const Shape &s, const LayerDev &L, const Scratch &S, int T, hipStream_t st);
 hipError_t launch_down_exact(const Shape &s, const LayerDev &L, const Scratch &S, float *out, int T, int quant,

@@ -1998,241 +1998,454 @@ hipError_t launch_gateup_tiles(const Shape &s, const LayerDev &L, const Scratch 
     return hipGetLastError();
 }
 
-/* ------------------------------------------------------------------ MFMA grouped GEMM ---- */
+/* ------------------------------------------------------------------ MFMA expert products ---- */
 
-/* Prefill-sized batches: the expert products as int8 MFMA tiles (v_mfma_i32_16x16x32_i8, one
- * 32-block of K per instruction). Per 32-block the instruction gives the exact signed block
- * dot D = sum (q - 8) * x (unsigned nibbles, then a second MFMA with a constant -8 operand
- * adds -8 * sum x), and the fp32 row value accumulates D * d_w * d_x block by block. Block
- * dots are bit-exact; the fp32 sums are in another order than the reference's per-lane chains
- * (agreement to rounding), so this path trades the order-exact fp32 for MFMA throughput.
+/* Batches with several slots per expert: the expert products on the matrix cores, order-exact.
  *
- * A block computes 64 weight rows x kTileN slots of one expert; wave w owns tile rows
- * 16w .. 16w+15 and both 16-slot halves. K is staged through LDS in chunks of kMKC blocks,
- * double-buffered, the next chunk's loads in flight during the current chunk's MFMAs.
- * Lane layout of the 16x16x32 i8 MFMA: A[row = l%16][k = 8(l/16) .. +7],
- * B[k = 8(l/16) .. +7][col = l%16], C[row = 4(l/16) + i][col = l%16]. */
-typedef int v4i __attribute__((ext_vector_type(4)));
-constexpr int kMKC = 8;
+ * For a weight row, a slot's int8 block x and a 32-block b, the reference's AVX2 dot forms
+ * eight int32 lane sums S_k = sum_{i in 4k..4k+3} u_i x_i (u the unsigned weight code, lanes
+ * 0-3 over the low nibbles) and folds each into its own fp32 chain
+ * acc_k = fma((float)S_k, fl(d_w d_x), acc_k) (src/kernels.c:85-94, 113-119, 145-166). One
+ * v_mfma_f32_16x16x32_f16 returns those eight S_k for 16 weight rows and 2 slots:
+ *   - B holds the codes of 16 rows, biased by 1024 (0x6400 | u is the f16 1024 + u, exact);
+ *   - A is block-diagonal over the lane groups: its row (slot j, lane k) holds x_j only at the
+ *     four K positions of group k, so D-row (j, k) of column r sums group k only;
+ *   - the C input is -1024 * sum_{group k} x_j, which cancels the bias.
+ * Every partial sum is an integer below 2^24, so the f32 accumulation inside the MFMA is exact
+ * in any order and D equals S_k. The VALU then runs the reference's chains: acc_k =
+ * fma(S_k, fl(d_w d_x), acc_k) per block, the offset chain, and at the end the hsum256 tree and
+ * the unfused final term. Q6_K scales S_k by its int8 sub-scale first (exact in f32).
+ *
+ * Operand layout of the 16x16x32 f16 MFMA (checked on the device): lane l supplies
+ * A[l%16][8(l/16) + e] and B[8(l/16) + e][l%16] for e = 0..7 and receives D[4(l/16) + v][l%16].
+ * K position 8g + e of lane group g is block element pi(8g + e) =
+ * 4g, 4g+2, 4g+1, 4g+3, 16+4g, 16+4g+2, 16+4g+1, 16+4g+3: the first four are reference lane
+ * k = g, the last four lane k = g + 4, and both come from one code dword (Q4) of the block
+ * with four shift-and-or steps. D-row 4(l/16) + v is slot j = l/32 of the pair and lane
+ * k = 4((l/16)&1) + v, so a lane holds four chains of one (row, slot): one fl(d_w d_x) product
+ * serves its four FMAs.
+ *
+ * Activation records (kMxRec bytes per slot, or per token, and 32-block) carry x in that
+ * order as f16, the C input, d, ds and the half sums; the lanes of A outside their group read
+ * the record's zero words. Gate/up writes the records of the activations it quantises, so the
+ * down products read them directly.
+ *
+ * A block of 8 waves computes 512/WSG weight rows x 8*WSG slots of one expert's slot tile:
+ * wave (wr, ws) owns 64 rows (four 16-row MFMA tiles) and 8 slots (four pairs). For gate/up the
+ * 64 rows are 32 gate rows and the same 32 up rows, so SwiGLU and the int8 requantisation of
+ * whole 32-blocks happen in the block. K is staged through LDS in chunks of kMxC blocks,
+ * double-buffered: the next chunk's loads are in flight while the current one computes. */
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
-struct MfmaArgs {
-    const uint8_t *w0, *w1;     /* gate, up (gate/up kernel); down (down kernel, w1 unused) */
+constexpr int kMxRec = 128;      /* bytes of one activation record */
+constexpr int kMxC = 8;          /* 32-blocks per staged chunk (one Q6_K super-block) */
+constexpr int kMxZero = 112;     /* offset of the record's zero words */
+constexpr bool kMxQ6K = false;   /* Q6_K down rows on the MFMA kernel */
+
+/* One int8 block as an activation record (layout above). */
+__device__ void mx_store_record(const Q8Vals &q, uint8_t *rec)
+{
+    u32x4 w[8];
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+        const uint32_t c = q.qw[k];
+        const int x0 = (int)(int8_t)(c & 0xffu), x1 = (int)(int8_t)((c >> 8) & 0xffu);
+        const int x2 = (int)(int8_t)((c >> 16) & 0xffu), x3 = (int)(int8_t)(c >> 24);
+        auto h = [](int x) { return (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)(float)x); };
+        w[k >> 1][2 * (k & 1)] = h(x0) | (h(x2) << 16);
+        w[k >> 1][2 * (k & 1) + 1] = h(x1) | (h(x3) << 16);
+        ((float *)&w[4])[k] = -1024.0f * (float)(x0 + x1 + x2 + x3);
+    }
+    w[6] = u32x4{ __float_as_uint(q.d), __float_as_uint(q.ds), q.s16, 0u };
+    w[7] = u32x4{ 0u, 0u, 0u, 0u };
+#pragma unroll
+    for (int i = 0; i < 8; i++) ((u32x4 *)rec)[i] = w[i];
+}
+
+/* The layer input's records from its int8 blocks (one thread per block). */
+__global__ void mx_input_kernel(const Q8 *xq, int n, uint8_t *rec)
+{
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    const uint32_t *s = (const uint32_t *)(xq + i);
+    Q8Vals q;
+    q.d = __uint_as_float(s[0]);
+    q.ds = __uint_as_float(s[1]);
+    q.s16 = s[2];
+#pragma unroll
+    for (int w = 0; w < 8; w++) q.qw[w] = s[3 + w];
+    mx_store_record(q, rec + (size_t)i * kMxRec);
+}
+
+struct MxArgs {
+    const uint8_t *w0, *w1;      /* gate and up (gate/up kernel); down (down kernel) */
     uint64_t rb, eb;
-    int E, F, K, X, debug;
+    int E, F, debug;
+    const uint8_t *rec;          /* input records: [token][E/32] (gate/up) or [slot][F/32] (down) */
+    uint8_t *rec_out;            /* gate/up: the activation records [slot][F/32] */
     Scratch S;
 };
 
-/* Eight bytes at an even LDS byte address (three aligned reads). */
-__device__ __forceinline__ uint64_t lds_u64_even(const uint8_t *base, uint32_t a)
+/* LDS bytes of one staged weight row (kMxC blocks): Q4_0 144, Q4_1 160, Q6_K one super-block
+ * copied from the 4-byte boundary below it (216 bytes) in a 224-byte slot. */
+__host__ __device__ constexpr int mx_wstride(int type) { return type == 14 ? 224 : (type == 3 ? 160 : 144); }
+
+__host__ __device__ constexpr int mx_buf_bytes(int type, int wsg)
 {
-    const uint32_t *w = (const uint32_t *)(base + (a & ~3u));
-    const uint32_t s = a & 3u, d0 = w[0], d1 = w[1], d2 = w[2];
-    return (uint64_t)__builtin_amdgcn_alignbyte(d1, d0, s) | ((uint64_t)__builtin_amdgcn_alignbyte(d2, d1, s) << 32);
+    return (512 / wsg) * mx_wstride(type) + 8 * wsg * kMxC * kMxRec;
 }
 
-/* The lane's A operand from a Q4_0 block in LDS (18 bytes at byte offset `off`): k-group g
- * takes elements 8g .. 8g+7, i.e. low nibbles of qs[0..7] / qs[8..15] for g = 0 / 1 and the
- * high nibbles of the same bytes for g = 2 / 3 (src/kernels.c:8-13). */
-__device__ __forceinline__ long q4_a_operand(const uint8_t *tile, uint32_t off, int g)
+/* Two aligned LDS reads for a word at an even offset O (mod 4) known at compile time. */
+template <int O>
+__device__ __forceinline__ uint32_t lds_word_at(const uint8_t *base, uint32_t a)
 {
-    const uint64_t w = lds_u64_even(tile, off + 2 + 8 * (g & 1));
-    const int sh = 4 * (g >> 1);
-    const uint32_t lo = ((uint32_t)w >> sh) & 0x0f0f0f0fu, hi = ((uint32_t)(w >> 32) >> sh) & 0x0f0f0f0fu;
-    return (long)((uint64_t)lo | ((uint64_t)hi << 32));
+    if constexpr (O == 0) return *(const uint32_t *)(base + a);
+    else return lds_u32(base, a);
 }
 
-/* One 64-row x kTileN-slot tile over K = nb 32-blocks. A rows come from `arow(row)` (18-byte
- * Q4_0 blocks), B from kTileN Q8 records per block found by `brec(slot)` (44 bytes each, the
- * slot's block 0; records of one slot are contiguous). y[jt][i]: row 16w + 4g + i, slot
- * 16jt + l%16 of the tile. */
-template <class ARow, class BRec>
-__device__ __forceinline__ void mfma_tile(int nb, ARow arow, BRec brec, uint8_t *As, uint8_t *Bs, float y[2][4])
+/* The B operand of one 16-row tile for 32-block b of the staged chunk (row = this lane's row
+ * in LDS) and the scale words the chains need. */
+struct MxB {
+    f16x8 op;
+    uint32_t dw;      /* Q4_0: d (low half); Q4_1: d | m << 16; Q6_K: d (low half) */
+    float sc;         /* Q6_K: the lane's sub-scale (k < 4: sc[2g], k >= 4: sc[2g+1]) */
+    int sa, sb;       /* Q6_K: both sub-scales of the block */
+};
+
+__device__ __forceinline__ f16x8 mx_pack_codes(uint32_t b0, uint32_t b1, uint32_t b2, uint32_t b3)
 {
-    constexpr int AS = 64 * kMKC * 18 / 16, BS = kTileN * kMKC * 44 / 16;   /* 16-byte slots per chunk */
-    constexpr int AM = (AS + 255) / 256, BM = (BS + 255) / 256;
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, g = lane >> 4, lr = lane & 15;
-    const int nch = nb / kMKC;
-    u32x4 va[AM], vb[BM];
+    return __builtin_bit_cast(f16x8, u32x4{ b0, b1, b2, b3 });
+}
+
+template <int TYPE, int O>
+__device__ __forceinline__ MxB mx_weights(const uint8_t *row, int b, int lg, int kh)
+{
+    constexpr uint32_t bias = 0x64006400u;
+    MxB w;
+    if constexpr (TYPE == 14) {
+        const uint8_t *sb = row + O;
+        const int h = b >> 2, g = b & 3;
+        const uint32_t qlA = lds_word_at<O>(sb, 64 * h + 32 * (g & 1) + 4 * lg);
+        const uint32_t qlB = lds_word_at<O>(sb, 64 * h + 32 * (g & 1) + 16 + 4 * lg);
+        const uint32_t qhA = lds_word_at<O>(sb, 128 + 32 * h + 4 * lg);
+        const uint32_t qhB = lds_word_at<O>(sb, 128 + 32 * h + 16 + 4 * lg);
+        const int ns = 4 * (g >> 1), hs = 2 * g;
+        const uint32_t cA = ((qlA >> ns) & 0x0f0f0f0fu) | (((qhA >> hs) & 0x03030303u) << 4);
+        const uint32_t cB = ((qlB >> ns) & 0x0f0f0f0fu) | (((qhB >> hs) & 0x03030303u) << 4);
+        w.op = mx_pack_codes((cA & 0x00ff00ffu) | bias, ((cA >> 8) & 0x00ff00ffu) | bias, (cB & 0x00ff00ffu) | bias,
+                             ((cB >> 8) & 0x00ff00ffu) | bias);
+        const uint32_t scw = *(const uint16_t *)(sb + 192 + 8 * h + 2 * g);
+        w.sa = (int)(int8_t)(scw & 0xffu);
+        w.sb = (int)(int8_t)(scw >> 8);
+        w.sc = (float)(kh ? w.sb : w.sa);
+        w.dw = *(const uint16_t *)(sb + 208);
+    } else {
+        constexpr int BB = TYPE == 3 ? 20 : 18, QO = TYPE == 3 ? 4 : 2;
+        uint32_t v;
+        if (TYPE == 3 || (b & 1)) v = *(const uint32_t *)(row + BB * b + QO + 4 * lg);
+        else v = lds_u32(row, BB * b + QO + 4 * lg);
+        w.op = mx_pack_codes((v & 0x000f000fu) | bias, ((v >> 8) & 0x000f000fu) | bias, ((v >> 4) & 0x000f000fu) | bias,
+                             ((v >> 12) & 0x000f000fu) | bias);
+        w.dw = TYPE == 3 ? *(const uint32_t *)(row + BB * b) : (uint32_t) * (const uint16_t *)(row + BB * b);
+        w.sc = 0.0f;
+        w.sa = w.sb = 0;
+    }
+    return w;
+}
+
+/* fl(h * f) for the f16 in the low half of h (v_fma_mix, one rounding; the added zero cannot
+ * change a non-zero product). */
+__device__ __forceinline__ float mix_mul(uint32_t h, float f)
+{
+    float r;
+    asm("v_fma_mix_f32 %0, %1, %2, 0 op_sel_hi:[1,0,0]" : "=v"(r) : "v"(h), "v"(f));
+    return r;
+}
+
+/* fma(f16 low half of h, f, c) in one rounding. */
+__device__ __forceinline__ float mix_fma_lo(uint32_t h, float f, float c)
+{
+    float r;
+    asm("v_fma_mix_f32 %0, %1, %2, %3 op_sel_hi:[1,0,0]" : "=v"(r) : "v"(h), "v"(f), "v"(c));
+    return r;
+}
+
+/* fma(f16 high half of h, f, c) in one rounding. */
+__device__ __forceinline__ float mix_fma_hi(uint32_t h, float f, float c)
+{
+    float r;
+    asm("v_fma_mix_f32 %0, %1, %2, %3 op_sel:[1,0,0] op_sel_hi:[1,0,0]" : "=v"(r) : "v"(h), "v"(f), "v"(c));
+    return r;
+}
+
+template <int TYPE, int WSG, int GU, int O>
+__device__ __forceinline__ void mx_chunk(const uint8_t *W, const uint8_t *R, int np, int lr, int lg, int kh, int jd,
+                                         int offa_lo, int offa_hi, f32x4 (&acc)[4][4], float (&cr)[4][4])
+{
+#pragma unroll
+    for (int b = 0; b < kMxC; b++) {
+        MxB w[4];
+#pragma unroll
+        for (int t = 0; t < 4; t++) w[t] = mx_weights<TYPE, O>(W + (16 * t + lr) * mx_wstride(TYPE), b, lg, kh);
+#pragma unroll
+        for (int p = 0; p < 4; p++) {
+            if (p < np) {
+                const uint8_t *rp = R + ((2 * p) * kMxC + b) * kMxRec;
+                const u32x2 lo = *(const u32x2 *)(rp + offa_lo);
+                const u32x2 hi = *(const u32x2 *)(rp + offa_hi);
+                const f16x8 aop = __builtin_bit_cast(f16x8, u32x4{ lo.x, lo.y, hi.x, hi.y });
+                const uint8_t *rd = rp + jd * kMxC * kMxRec;
+                const f32x4 cin = *(const f32x4 *)(rd + 64 + 16 * kh);
+                const u32x4 dx = *(const u32x4 *)(rd + 96);       /* d, ds, s16 pair, 0 */
+                const float xd = __uint_as_float(dx.x), xds = __uint_as_float(dx.y);
+#pragma unroll
+                for (int t = 0; t < 4; t++) {
+                    const f32x4 S = __builtin_amdgcn_mfma_f32_16x16x32_f16(aop, w[t].op, cin, 0, 0, 0);
+                    const float dd = mix_mul(w[t].dw, xd);
+                    if constexpr (TYPE == 14) {
+#pragma unroll
+                        for (int v = 0; v < 4; v++) acc[t][p][v] = __builtin_fmaf(S[v] * w[t].sc, dd, acc[t][p][v]);
+                        const int s0 = (int)(int16_t)(dx.z & 0xffffu), s1 = (int)(int16_t)(dx.z >> 16);
+                        cr[t][p] = __builtin_fmaf(dd, (float)(w[t].sa * s0 + w[t].sb * s1), cr[t][p]);
+                    } else {
+#pragma unroll
+                        for (int v = 0; v < 4; v++) acc[t][p][v] = __builtin_fmaf(S[v], dd, acc[t][p][v]);
+                        if constexpr (TYPE == 3) cr[t][p] = mix_fma_hi(w[t].dw, xds, cr[t][p]);   /* off += m*ds */
+                        else cr[t][p] = mix_fma_lo(w[t].dw, xds, cr[t][p]);                     /* corr += d*ds */
+                    }
+                }
+            }
+        }
+    }
+}
+
+/* Gate/up (GU = 1: gate rows against the token's input records, the same up rows, SwiGLU, the
+ * int8 activation blocks and their records) or down (GU = 0: dn rows) of one slot tile. */
+template <int TYPE, int WSG, int GU>
+__global__ __launch_bounds__(512) void mx_kernel(MxArgs a)
+{
+    extern __shared__ __align__(16) uint8_t smem[];
+    constexpr int RWG = 512 / WSG, SWG = 8 * WSG, WS = mx_wstride(TYPE);
+    constexpr int WBYTES = RWG * WS, BUF = mx_buf_bytes(TYPE, WSG);
+    constexpr int WU = TYPE == 14 ? 4 : 16;                                   /* bytes per copy unit  */
+    constexpr int WUR = TYPE == 14 ? 54 : kMxC * (TYPE == 3 ? 20 : 18) / 16;  /* units per row      */
+    constexpr int WPT = (RWG * WUR + 511) / 512, RU = SWG * kMxC * kMxRec / 16, RPT = (RU + 511) / 512;
+    if ((int)blockIdx.y >= a.S.meta[1]) return;
+    const int4 tl = a.S.tiles[blockIdx.y];
+    const int e = tl.x, s0 = tl.y + (int)blockIdx.z * SWG, ns = min(SWG, tl.z - s0);
+    if (ns <= 0) return;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, lr = lane & 15, lg = lane >> 4;
+    const int wr = wave / WSG, ws = wave % WSG, kh = lg & 1, jd = lg >> 1;
+    const int nb = (GU ? a.E : a.F) >> 5, nch = nb / kMxC;
+    const int R0 = (int)blockIdx.x * (GU ? RWG / 2 : RWG);
+
+    /* row i of the staged tile: for gate/up, row group g = i / 64 holds gate rows
+     * R0 + 32g .. R0 + 32g + 31 and then the same up rows */
+    auto row_ptr = [&](int i) -> const uint8_t * {
+        if (GU) {
+            const int g = i >> 6, within = i & 63;
+            return (within < 32 ? a.w0 : a.w1) + (size_t)e * a.eb + (size_t)(R0 + 32 * g + (within & 31)) * a.rb;
+        }
+        return a.w0 + (size_t)e * a.eb + (size_t)(R0 + i) * a.rb;
+    };
+    /* slot i's records (slots past the tile repeat its last slot) */
+    auto rec_ptr = [&](int i) -> const uint8_t * {
+        const int s = s0 + min(i, ns - 1);
+        return a.rec + (size_t)(GU ? a.S.slot_t[s] : s) * nb * kMxRec;
+    };
+    uint32_t wv[WPT][WU / 4];
+    u32x4 rv[RPT];
     auto load = [&](int c) {
 #pragma unroll
-        for (int m = 0; m < AM; m++) {
-            const int i = min(tid + 256 * m, AS - 1), row = i / (kMKC * 18 / 16), j = i - row * (kMKC * 18 / 16);
-            va[m] = *(const u32x4 *)(arow(row) + (size_t)c * kMKC * 18 + 16 * j);
+        for (int m = 0; m < WPT; m++) {
+            const int idx = min(tid + 512 * m, RWG * WUR - 1), i = idx / WUR, u = idx - i * WUR;
+            if constexpr (TYPE == 14) {
+                /* the super-block starts 2 bytes past a 4-byte boundary on odd chunks */
+                wv[m][0] = ((const uint32_t *)(row_ptr(i) + (size_t)c * 210 - 2 * (c & 1)))[u];
+            } else {
+                *(u32x4 *)wv[m] = *(const u32x4 *)(row_ptr(i) + (size_t)c * (WUR * 16) + 16 * u);
+            }
         }
 #pragma unroll
-        for (int m = 0; m < BM; m++) {
-            const int i = min(tid + 256 * m, BS - 1), sl = i / (kMKC * 44 / 16), j = i - sl * (kMKC * 44 / 16);
-            vb[m] = *(const u32x4 *)(brec(sl) + (size_t)c * kMKC * 44 + 16 * j);
+        for (int m = 0; m < RPT; m++) {
+            const int idx = min(tid + 512 * m, RU - 1), i = idx / (kMxC * kMxRec / 16), u = idx - i * (kMxC * kMxRec / 16);
+            rv[m] = ((const u32x4 *)(rec_ptr(i) + (size_t)c * kMxC * kMxRec))[u];
         }
     };
     auto store = [&](int buf) {
+        uint8_t *Wl = smem + buf * BUF, *Rl = Wl + WBYTES;
 #pragma unroll
-        for (int m = 0; m < AM; m++)
-            if (tid + 256 * m < AS) *(u32x4 *)(As + buf * AS * 16 + 16 * (tid + 256 * m)) = va[m];
+        for (int m = 0; m < WPT; m++) {
+            const int idx = tid + 512 * m;
+            if (idx < RWG * WUR) {
+                const int i = idx / WUR, u = idx - i * WUR;
+                if constexpr (TYPE == 14) *(uint32_t *)(Wl + i * WS + 4 * u) = wv[m][0];
+                else *(u32x4 *)(Wl + i * WS + 16 * u) = *(const u32x4 *)wv[m];
+            }
+        }
 #pragma unroll
-        for (int m = 0; m < BM; m++)
-            if (tid + 256 * m < BS) *(u32x4 *)(Bs + buf * BS * 16 + 16 * (tid + 256 * m)) = vb[m];
+        for (int m = 0; m < RPT; m++)
+            if (tid + 512 * m < RU) ((u32x4 *)Rl)[tid + 512 * m] = rv[m];
     };
+
+    /* A reads: D... lane row lr is slot ja = lr/8 of the pair, reference lane ka = lr%8; it
+     * holds x only if ka%4 == lg, in the low half of its 8 K positions for ka < 4 */
+    const int ja = lr >> 3, ka = lr & 7;
+    const bool nz = (ka & 3) == lg;
+    const int offa_lo = ja * kMxC * kMxRec + ((nz && ka < 4) ? 8 * ka : kMxZero);
+    const int offa_hi = ja * kMxC * kMxRec + ((nz && ka >= 4) ? 8 * ka : kMxZero);
+    const int nw = min(max(ns - 8 * ws, 0), 8), np = (nw + 1) >> 1;      /* this wave's slot pairs */
+
+    f32x4 acc[4][4];
+    float cr[4][4];
 #pragma unroll
-    for (int jt = 0; jt < 2; jt++)
+    for (int t = 0; t < 4; t++)
 #pragma unroll
-        for (int i = 0; i < 4; i++) y[jt][i] = 0.0f;
-    const long m8 = (long)0xf8f8f8f8f8f8f8f8ULL;            /* -8 in every byte */
+        for (int p = 0; p < 4; p++) {
+            acc[t][p] = f32x4{ 0.0f, 0.0f, 0.0f, 0.0f };
+            cr[t][p] = 0.0f;
+        }
+
     load(0);
     store(0);
     __syncthreads();
     for (int c = 0; c < nch; c++) {
         const int buf = c & 1;
         if (c + 1 < nch) load(c + 1);
-        const uint8_t *A = As + buf * AS * 16, *B = Bs + buf * BS * 16;
-#pragma unroll 2
-        for (int b = 0; b < kMKC; b++) {
-            const long aop = q4_a_operand(A, (uint32_t)((16 * wave + lr) * kMKC * 18 + b * 18), g);
-            float dw[4];
-#pragma unroll
-            for (int i = 0; i < 4; i++)
-                dw[i] = h2f(*(const uint16_t *)(A + (16 * wave + 4 * g + i) * kMKC * 18 + b * 18));
-#pragma unroll
-            for (int jt = 0; jt < 2; jt++) {
-                const uint8_t *xr = B + (16 * jt + lr) * kMKC * 44 + b * 44;
-                const uint32_t *xq = (const uint32_t *)(xr + 12 + 8 * g);
-                const long bop = (long)((uint64_t)xq[0] | ((uint64_t)xq[1] << 32));
-                const float dx = *(const float *)xr;
-                v4i d = { 0, 0, 0, 0 };
-                d = __builtin_amdgcn_mfma_i32_16x16x32_i8(aop, bop, d, 0, 0, 0);
-                d = __builtin_amdgcn_mfma_i32_16x16x32_i8(m8, bop, d, 0, 0, 0);
-#pragma unroll
-                for (int i = 0; i < 4; i++) y[jt][i] = __builtin_fmaf((float)d[i], dw[i] * dx, y[jt][i]);
-            }
-        }
+        const uint8_t *Wl = smem + buf * BUF + (64 * wr) * WS;
+        const uint8_t *Rl = smem + buf * BUF + WBYTES + (8 * ws) * kMxC * kMxRec;
+        if (TYPE == 14 && (c & 1))
+            mx_chunk<TYPE, WSG, GU, 2>(Wl, Rl, np, lr, lg, kh, jd, offa_lo, offa_hi, acc, cr);
+        else
+            mx_chunk<TYPE, WSG, GU, 0>(Wl, Rl, np, lr, lg, kh, jd, offa_lo, offa_hi, acc, cr);
         if (c + 1 < nch) store(buf ^ 1);
         __syncthreads();
     }
-}
 
-/* Gate/up of one slot tile: 32 gate rows (tile rows 0-31) and the same 32 up rows (32-63),
- * then a = silu(g)*u and, since the 32 gate rows are one int8 block of the activations, the
- * quantised block of each slot (src/model.c:989-997). */
-__global__ __launch_bounds__(256) void gateup_mfma_kernel(MfmaArgs a)
-{
-    __shared__ __align__(16) uint8_t As[2 * 64 * kMKC * 18 + 16];   /* +16: the A reads' 12-byte windows */
-    __shared__ __align__(16) uint8_t Bs[2 * kTileN * kMKC * 44];
-    __shared__ int toks[kTileN];
-    __shared__ float res[64][kTileN + 1];
-    if ((int)blockIdx.y >= a.S.meta[1]) return;
-    const int4 tl = a.S.tiles[blockIdx.y];
-    const int e = tl.x, s0 = tl.y, ns = tl.z - tl.y;
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, g = lane >> 4, lr = lane & 15;
-    const int r0 = (int)blockIdx.x * 32, nbE = a.E >> 5, nbF = a.F >> 5, F = a.F;
-    if (tid < kTileN) toks[tid] = a.S.slot_t[s0 + min(tid, ns - 1)];
-    __syncthreads();
-    const uint8_t *g0 = a.w0 + (size_t)e * a.eb + (size_t)r0 * a.rb, *u0 = a.w1 + (size_t)e * a.eb + (size_t)r0 * a.rb;
-    const uint8_t *xq = (const uint8_t *)a.S.xq;
-    float y[2][4];
-    mfma_tile(nbE, [&](int row) { return (row < 32 ? g0 : u0) + (size_t)(row & 31) * a.rb; },
-              [&](int sl) { return xq + (size_t)toks[sl] * nbE * 44; }, As, Bs, y);
+    /* hsum256 per (row, slot): lanes of k-half 0 take the partner lane's k + 4 chains */
+    constexpr float scale = finish_scale(TYPE);
+    float *res = (float *)smem;                                   /* [RWG][SWG + 1] */
 #pragma unroll
-    for (int jt = 0; jt < 2; jt++)
+    for (int t = 0; t < 4; t++)
 #pragma unroll
-        for (int i = 0; i < 4; i++) res[16 * wave + 4 * g + i][16 * jt + lr] = y[jt][i];
+        for (int p = 0; p < 4; p++) {
+            f32x4 o;
+#pragma unroll
+            for (int v = 0; v < 4; v++) o[v] = __shfl_xor(acc[t][p][v], 16);
+            if (p < np && kh == 0) {
+                const f32x4 &q = acc[t][p];
+                const float h = ((q[0] + o[0]) + (q[2] + o[2])) + ((q[1] + o[1]) + (q[3] + o[3]));
+                const float val = h - scale * cr[t][p];
+                const int row = 64 * wr + 16 * t + lr, sl = 8 * ws + 2 * p + jd;
+                if (GU) res[row * (SWG + 1) + sl] = val;
+                else if (sl < ns) a.S.dn[(size_t)(s0 + sl) * a.E + R0 + row] = val;
+            }
+        }
+    if (!GU) return;
     __syncthreads();
-    /* half-wave per slot: lane r of the half holds row r0 + r */
-    const int hw = tid >> 5, r = tid & 31, hb = lane & 32;
-    const int blk = r0 >> 5, half = blk & 1;
-    for (int sl = hw; sl < ns; sl += 8) {
-        const int s = s0 + sl;
-        const float gv = res[r][sl], uv = res[32 + r][sl];
+    /* a = silu(g) * u (src/model.c:989-994) into the gate half of res, then the int8 blocks
+     * of whole 32-row blocks (src/model.c:996-997) and their records */
+    const int F = a.F, nbF = F >> 5;
+    for (int i = tid; i < (RWG / 2) * SWG; i += 512) {
+        const int fr = i / SWG, sl = i - fr * SWG, g = fr >> 5, j = fr & 31;
+        if (sl >= ns) continue;
+        const float gv = res[(64 * g + j) * (SWG + 1) + sl], uv = res[(64 * g + 32 + j) * (SWG + 1) + sl];
         const float av = silu_ref(gv) * uv;
-        a.S.act[(size_t)s * F + r0 + r] = av;
+        res[(64 * g + j) * (SWG + 1) + sl] = av;
         if (a.debug) {
-            a.S.gu[(size_t)s * 2 * F + r0 + r] = gv;
-            a.S.gu[(size_t)s * 2 * F + F + r0 + r] = uv;
+            const size_t s = (size_t)(s0 + sl);
+            a.S.gu[s * 2 * F + R0 + fr] = gv;
+            a.S.gu[s * 2 * F + F + R0 + fr] = uv;
+            a.S.act[s * F + R0 + fr] = av;
         }
-        float amax = fabsf(av);
-        for (int o = 16; o > 0; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o));
-        const float d = amax / 127.0f;
-        const float id = d > 0.0f ? 1.0f / d : 0.0f;
-        const int qi = (int)rintf(av * id);
-        int sum = qi;
-        for (int o = 8; o > 0; o >>= 1) sum += __shfl_xor(sum, o);   /* 16-row halves */
-        const int sa = __shfl(sum, hb), sb = __shfl(sum, hb + 16);
-        const float ds = d * (float)(sa + sb);
-        const uint32_t s16 = (uint32_t)(uint16_t)(int16_t)sa | ((uint32_t)(uint16_t)(int16_t)sb << 16);
-        const uint32_t b0 = (uint32_t)(qi & 0xff);
-        const uint32_t w4 = b0 | ((uint32_t)(__shfl(qi, lane + 1) & 0xff) << 8) |
-                            ((uint32_t)(__shfl(qi, lane + 2) & 0xff) << 16) | ((uint32_t)(__shfl(qi, lane + 3) & 0xff) << 24);
-        uint32_t *o = (uint32_t *)(a.S.aq + (size_t)s * nbF + blk);
-        uint32_t *pr = (uint32_t *)(a.S.aqk + ((size_t)s * (nbF >> 1) + (blk >> 1)) * kPairBytes);
-        if (r == 0) { o[0] = __float_as_uint(d); o[1] = __float_as_uint(ds); o[2] = s16; }
-        if ((r & 3) == 0) {
-            o[3 + (r >> 2)] = w4;                                          /* q[r .. r+3] */
-            const int p = (r & 15) >> 2;
-            pr[4 * p + 2 * half + (r >> 4)] = w4;                          /* q[4p..] or q[16+4p..] */
-        }
-        if (r == 1) pr[16 + 2 * half] = __float_as_uint(d);
-        if (r == 2) pr[17 + 2 * half] = __float_as_uint(ds);
-        if (r == 3) pr[20 + half] = s16;
-        if (r == 5 && half == 0) { pr[22] = 0; pr[23] = 0; }
+    }
+    __syncthreads();
+    constexpr int NFB = RWG / 64;                                  /* activation blocks per slot */
+    for (int i = tid; i < SWG * NFB; i += 512) {
+        const int sl = i / NFB, g = i - sl * NFB;
+        if (sl >= ns) continue;
+        float v[32];
+#pragma unroll
+        for (int j = 0; j < 32; j++) v[j] = res[(64 * g + j) * (SWG + 1) + sl];
+        const Q8Vals q = quantize_block(v);
+        const int s = s0 + sl, blk = (R0 >> 5) + g;
+        store_q8(q, a.S.aq + (size_t)s * nbF + blk);
+        store_pair_half(q, (uint32_t *)(a.S.aqk + ((size_t)s * (nbF >> 1) + (blk >> 1)) * kPairBytes), blk & 1);
+        mx_store_record(q, a.rec_out + ((size_t)s * nbF + blk) * kMxRec);
     }
 }
 
-/* Down rows of one slot tile: 64 output rows (R0 = 64*blockIdx.x) of expert e against the
- * tile's int8 activation blocks; writes dn[slot][row], combined afterwards in selection order. */
-__global__ __launch_bounds__(256) void down_mfma_kernel(MfmaArgs a)
+template <int TYPE, int GU>
+static void launch_mx(const MxArgs &a, int wsg, int rows, int maxt, hipStream_t st)
 {
-    __shared__ __align__(16) uint8_t As[2 * 64 * kMKC * 18 + 16];
-    __shared__ __align__(16) uint8_t Bs[2 * kTileN * kMKC * 44];
-    if ((int)blockIdx.y >= a.S.meta[1]) return;
-    const int4 tl = a.S.tiles[blockIdx.y];
-    const int e = tl.x, s0 = tl.y, ns = tl.z - tl.y;
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, g = lane >> 4, lr = lane & 15;
-    const int R0 = (int)blockIdx.x * 64, nbF = a.F >> 5, E = a.E;
-    const uint8_t *w = a.w0 + (size_t)e * a.eb + (size_t)R0 * a.rb;
-    const uint8_t *aq = (const uint8_t *)a.S.aq;
-    float y[2][4];
-    mfma_tile(nbF, [&](int row) { return w + (size_t)row * a.rb; },
-              [&](int sl) { return aq + (size_t)(s0 + min(sl, ns - 1)) * nbF * 44; }, As, Bs, y);
-#pragma unroll
-    for (int jt = 0; jt < 2; jt++) {
-        const int sl = 16 * jt + lr;
-        if (sl < ns)
-#pragma unroll
-            for (int i = 0; i < 4; i++) a.S.dn[(size_t)(s0 + sl) * E + R0 + 16 * wave + 4 * g + i] = y[jt][i];
-    }
+    const size_t lds = 2 * (size_t)mx_buf_bytes(TYPE, wsg);
+    if (wsg == 4)
+        QLAUNCH(GU ? "gateup" : "down", (mx_kernel<TYPE, 4, GU>), dim3(rows / (GU ? 64 : 128), maxt, kTileN / 32),
+                dim3(512), lds, st, a);
+    else
+        QLAUNCH(GU ? "gateup" : "down", (mx_kernel<TYPE, 2, GU>), dim3(rows / (GU ? 128 : 256), maxt, kTileN / 16),
+                dim3(512), lds, st, a);
 }
 
-hipError_t launch_experts_mfma(const Shape &s, const LayerDev &L, const Scratch &S, float *out, int T, int debug,
-                               hipStream_t st)
+/* Whether the MFMA kernels take this layer: Q4_0 gate and up; Q4_0, Q4_1 or Q6_K down (Q6_K
+ * rows a multiple of 4 bytes long); 32-blocks in whole chunks; rows in whole tiles. */
+bool mx_supported(const Shape &s, const LayerDev &L, int *down_mx)
 {
-    const int NS = T * s.K, maxt = (s.X < NS ? s.X : NS) + NS / kTileN + 1;
-    if (s.E % (32 * kMKC) || s.F % (32 * kMKC) || s.F % 32 || s.E % 64 || L.gate_type != 2 || L.up_type != 2)
-        return hipErrorInvalidValue;
-    MfmaArgs a;
+    const int nbE = s.E / 32, nbF = s.F / 32;
+    const bool gu = L.gate_type == 2 && L.up_type == 2 && nbE % kMxC == 0 && s.F % 128 == 0;
+    /* Q6_K down: its kernel spills registers with the register-staged copy; the exact kernel
+     * takes it for now */
+    const bool dn = (L.down_type == 2 || L.down_type == 3 || (L.down_type == 14 && L.down_rb % 4 == 0 && kMxQ6K)) &&
+                    nbF % kMxC == 0 && s.E % 256 == 0;
+    if (down_mx) *down_mx = dn;
+    return gu;
+}
+
+/* Slots per block: 32 when the batch averages at least 24 slots per active expert, else 16. */
+static int mx_wsg(const Shape &s, int T)
+{
+    const int NS = T * s.K, act = s.X < NS ? s.X : NS;
+    return NS >= 24 * act ? 4 : 2;
+}
+
+hipError_t launch_experts_mx(const Shape &s, const LayerDev &L, const Scratch &S, float *out, int T, int debug,
+                             hipStream_t st)
+{
+    int down_mx = 0;
+    if (!mx_supported(s, L, &down_mx)) return hipErrorInvalidValue;
+    const int NS = T * s.K, maxt = (s.X < NS ? s.X : NS) + NS / kTileN + 1, wsg = mx_wsg(s, T);
+    const int nx = T * (s.E / 32);
+    QLAUNCH("mxin", mx_input_kernel, dim3((nx + 255) / 256), dim3(256), 0, st, S.xq, nx, S.mxx);
+    MxArgs a;
     a.w0 = L.gate;
     a.w1 = L.up;
     a.rb = L.gate_rb;
     a.eb = L.gate_eb;
     a.E = s.E;
     a.F = s.F;
-    a.K = s.K;
-    a.X = s.X;
     a.debug = debug;
+    a.rec = S.mxx;
+    a.rec_out = S.mxa;
     a.S = S;
-    QLAUNCH("gateup", gateup_mfma_kernel, dim3(s.F / 32, maxt), dim3(256), 0, st, a);
-    if (L.down_type == 2) {
-        a.w0 = L.down;
-        a.w1 = nullptr;
-        a.rb = L.down_rb;
-        a.eb = L.down_eb;
-        QLAUNCH("down", down_mfma_kernel, dim3(s.E / 64, maxt), dim3(256), 0, st, a);
-        const int n = T * s.E;
-        QLAUNCH("combine", combine_kernel, dim3((n + 255) / 256), dim3(256), 0, st, S, s.E, s.K, T, out);
-        return hipGetLastError();
+    launch_mx<2, 1>(a, wsg, s.F, maxt, st);
+    if (!down_mx) {
+        const hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+        return launch_down_exact(s, L, S, out, T, 0, st);    /* on the aqk records written above */
     }
-    /* Q4_1 / Q6_K down: the exact down kernel on the int8 blocks written above */
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return e;
-    return launch_down_exact(s, L, S, out, T, 0, st);
+    a.w0 = L.down;
+    a.w1 = nullptr;
+    a.rb = L.down_rb;
+    a.eb = L.down_eb;
+    a.rec = S.mxa;
+    a.rec_out = nullptr;
+    if (L.down_type == 14) launch_mx<14, 0>(a, wsg, s.E, maxt, st);
+    else if (L.down_type == 3) launch_mx<3, 0>(a, wsg, s.E, maxt, st);
+    else launch_mx<2, 0>(a, wsg, s.E, maxt, st);
+    const int n = T * s.E;
+    QLAUNCH("combine", combine_kernel, dim3((n + 255) / 256), dim3(256), 0, st, S, s.E, s.K, T, out);
+    return hipGetLastError();
 }
 
 /* ------------------------------------------------------------------ dense rows (trunk) ---- */
