@@ -535,7 +535,7 @@ def main():
     ctx.sync()
     log(f"with per-dispatch events: {1e6 * (time.perf_counter() - t0) / K_steps:.2f} us/step")
     kern = {}
-    for name in ("route", "select", "dispatch", "gateup", "actq", "down", "combine"):
+    for name in ("route", "select", "dispatch", "mxin", "gateup", "actq", "down", "combine"):
         n, ms = ctx.profile_read(name)
         if n:
             kern[name] = {"launches": n, "avg_us": round(1e3 * ms / n, 3)}

@@ -71,22 +71,21 @@ typedef struct {
 
 typedef struct qmsg_ctx qmsg_ctx;
 
-/* Which kernels run the expert products.
- *   EXACT: per-row fp32 FMA chains in the reference's lane order; every intermediate
- *          (int8 blocks, fp32 rows, outputs) is bit-identical to the reference's AVX path.
- *   MFMA:  int8 MFMA grouped GEMM for batches routed by the select kernel (T > 1), Q4_0
- *          gate/up (Q4_0 down on MFMA too, Q4_1/Q6_K down on the exact kernel): int32 block dots
- *          exact, fp32 rows summed per block in another order (about 1e-6 of a row's
- *          magnitude), which moves an int8 activation code where a value sits on a rounding
- *          boundary (a few per 1e5 codes). An opt-in for prefill throughput.
- *   AUTO:  EXACT (the order-exact results are the contract).
+/* Which kernels run the expert products. Every integer path gives the same bits: the int8
+ * blocks, the per-block int32 dots and the fp32 rows follow the reference's AVX path exactly.
+ *   EXACT: per-row VALU kernels (integer dot4 lane sums, the reference's fp32 lane chains).
+ *   MFMA:  the lane sums of 16 rows x 2 slots per f16 MFMA (exact small integers), the same
+ *          fp32 chains on the VALU; for batches of two or more tokens with Q4_0 gate and up
+ *          (down Q4_0, Q4_1 or Q6_K; other down rows on the EXACT kernel).
+ *   AUTO:  MFMA for batches averaging at least 12 slots per active expert (prefill), EXACT
+ *          otherwise.
  *   FP32:  the reference's --exact mode (qms_exact_math = 1, src/quant.c:95-115,
  *          model.c:1009-1030): router, gate/up and down rows dequantised to fp32 and dotted in
  *          one FMA chain per row (matmul_exact), fp32 activations, no int8 blocks; bit-identical
  *          to the reference run with --exact. Takes Q4_0, Q4_1 or Q6_K for every expert tensor.
  * Every path takes Q4_0, Q4_1 or Q6_K in each expert tensor (src/kernels.c:197-200). On the
  * integer paths a layer whose gate or up is not Q4_0 runs its gate/up rows on the exact
- * slot-tile kernel, also under MFMA. */
+ * slot-tile kernel. */
 enum { QMSG_PATH_AUTO = 0, QMSG_PATH_EXACT = 1, QMSG_PATH_MFMA = 2, QMSG_PATH_FP32 = 3 };
 
 /* ------------------------------------------------------------------ lifecycle ---- */
@@ -219,7 +218,7 @@ int qmsg_moe_device(qmsg_ctx *ctx, int layer, const float *d_xn, int T, float *d
  * qmsg_moe_device, with the same results, but its scratch arrays come from a static 32 MiB
  * device array of the library (one per GPU, held until the process ends) instead of the
  * context's, and it calls no hipMalloc, hipFree or other allocating routine. T is not bound
- * by max_tokens; a T whose scratch exceeds 32 MiB (above about 100 tokens at the 235B shape)
+ * by max_tokens; a T whose scratch exceeds 32 MiB (above about 80 tokens at the 235B shape)
  * returns QMSG_E_RANGE. Every call on one GPU shares that array: calls that overlap on one
  * GPU (two streams, or two contexts on one device) race and must be serialised. */
 int qmsg_moe_device_noalloc(qmsg_ctx *ctx, int layer, const float *d_xn, int T, float *d_out);

@@ -793,7 +793,7 @@ static int run_layer_s(qmsg_ctx *c, const Scratch &S, int layer, const float *d_
      * slot-tile row kernel */
     const bool q40 = d.gate_type == QMSG_T_Q4_0 && d.up_type == QMSG_T_Q4_0;
     const bool mx_ok = q40 && !use_small_route(T, s.K) && mx_supported(s, d, nullptr);
-    const bool mfma = mx_ok && (c->path == QMSG_PATH_MFMA || (c->path == QMSG_PATH_AUTO && T >= kMxAutoT));
+    const bool mfma = mx_ok && (c->path == QMSG_PATH_MFMA || (c->path == QMSG_PATH_AUTO && mx_auto(T, s.K, s.X)));
     LAUNCH(c, "route", launch_route(s, d, S, d_xn, T, c->stream));
     LAUNCH(c, "select", launch_select(s, S, T, q40 ? 1 : 0, c->stream));
     if (mfma) {

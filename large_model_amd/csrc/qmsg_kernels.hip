@@ -1,19 +1,22 @@
-/* qmsg_kernels.hip - gfx950 kernels for the Qwen3-MoE expert-FFN layer (exact path).
+/* qmsg_kernels.hip - gfx950 kernels for the Qwen3-MoE expert-FFN layer.
  *
- * Layer = route (router dots + int8 input blocks + softmax/top-K + counting sort, one launch)
- *       -> gateup (gate/up row dots over Q4_0, SwiGLU, int8 activation blocks, one launch)
- *       -> down   (down row dots over Q4_0/Q6_K, weighted combine, one launch).
+ * Layer = route (router dots + int8 input blocks; one-token batches also take their softmax and
+ *         top-K inside the gate/up kernel, larger ones a select launch with the counting sort)
+ *       -> gateup (gate/up row dots over Q4_0, SwiGLU)
+ *       -> down   (int8 activation blocks, down row dots over Q4_0/Q4_1/Q6_K, weighted combine).
+ * Prefill-sized batches run gate/up and down on the MFMA kernels instead (section "MFMA expert
+ * products"), which fuse SwiGLU and the activation blocks into gate/up.
  *
  * Every fp32 operation reproduces the reference's AVX2 order (src/kernels.c, src/model.c):
  * each row's dot is eight 4-element int32 lanes per 32-block, a per-lane fp32 FMA chain
  * over blocks, an FMA chain for the offset term, the hsum256 tree and an unfused final
  * subtraction. Build with -ffp-contract=off: every fused multiply-add here is explicit.
  *
- * Work mapping (64-wide waves): one quad of lanes per weight row; lane p of the quad owns
- * the reference lanes k = p (low nibbles) and k = p + 4 (high nibbles), which read the same
- * code dword. Weight tiles stream from HBM with 16-byte coalesced loads into LDS; the int8
- * activations sit in LDS in a pair-of-blocks layout so a lane gets its two code partners
- * with one 16-byte read. */
+ * Work mapping of the row kernels (64-wide waves): one quad of lanes per weight row; lane p of
+ * the quad owns the reference lanes k = p (low nibbles) and k = p + 4 (high nibbles), which
+ * read the same code dword. Weight tiles stream from HBM with 16-byte coalesced loads into LDS;
+ * the int8 activations sit in LDS in a pair-of-blocks layout so a lane gets its two code
+ * partners with one 16-byte read. */
 #include <hip/hip_runtime.h>
 #include <hip/hip_ext.h>
 
@@ -2037,11 +2040,11 @@ hipError_t launch_gateup_tiles(const Shape &s, const LayerDev &L, const Scratch 
  * double-buffered: the next chunk's loads are in flight while the current one computes. */
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef short short2_t __attribute__((ext_vector_type(2)));
 
 constexpr int kMxRec = 128;      /* bytes of one activation record */
 constexpr int kMxC = 8;          /* 32-blocks per staged chunk (one Q6_K super-block) */
 constexpr int kMxZero = 112;     /* offset of the record's zero words */
-constexpr bool kMxQ6K = false;   /* Q6_K down rows on the MFMA kernel */
 
 /* One int8 block as an activation record (layout above). */
 __device__ void mx_store_record(const Q8Vals &q, uint8_t *rec)
@@ -2091,65 +2094,97 @@ struct MxArgs {
  * copied from the 4-byte boundary below it (216 bytes) in a 224-byte slot. */
 __host__ __device__ constexpr int mx_wstride(int type) { return type == 14 ? 224 : (type == 3 ? 160 : 144); }
 
-__host__ __device__ constexpr int mx_buf_bytes(int type, int wsg)
+/* Staged chunk layout of a block of 8 waves: (8/WSG) row groups of 32 weight rows, WSG slot
+ * groups of 8 slots; the weight rows, then each slot's kMxC records at a stride of kMxRStride
+ * bytes (64 bytes past the records, so the two slots of a pair sit 16 LDS banks apart). Every
+ * piece is copied by the LDS DMA (global_load_lds): a wave instruction moves 64 lanes x 16 bytes
+ * (Q6_K weights: x 4 bytes) to consecutive LDS bytes. Two buffers: the next chunk's copy is in
+ * flight while the current one computes. */
+constexpr int kMxRStride = kMxC * kMxRec + 64;
+
+template <int TYPE, int WSG>
+struct MxLayout {
+    static constexpr int RWG = 256 / WSG, SWG = 8 * WSG, WS = mx_wstride(TYPE);
+    static constexpr int WBYTES = RWG * WS, BUF = WBYTES + SWG * kMxRStride;
+    static constexpr int WUNIT = TYPE == 14 ? 4 : 16;                 /* bytes per lane per DMA   */
+    static constexpr int WUR = WS / WUNIT;                             /* DMA units per row        */
+    static constexpr int WUSED = TYPE == 14 ? 54 : WUR;                /* units holding row bytes  */
+    static constexpr int WINSTR = (RWG * WUR + 63) / 64;               /* weight DMA instructions  */
+};
+
+__host__ __device__ constexpr int mx_lds_bytes(int type, int wsg)
 {
-    return (512 / wsg) * mx_wstride(type) + 8 * wsg * kMxC * kMxRec;
+    return 2 * ((256 / wsg) * mx_wstride(type) + 8 * wsg * kMxRStride);
 }
 
-/* Two aligned LDS reads for a word at an even offset O (mod 4) known at compile time. */
-template <int O>
-__device__ __forceinline__ uint32_t lds_word_at(const uint8_t *base, uint32_t a)
+/* (x & m) | c in one instruction; m and c in registers (no literal operands in VOP3 here). */
+__device__ __forceinline__ uint32_t and_or(uint32_t x, uint32_t m, uint32_t c)
 {
-    if constexpr (O == 0) return *(const uint32_t *)(base + a);
-    else return lds_u32(base, a);
+    uint32_t r;
+    asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(x), "v"(m), "v"(c));
+    return r;
 }
 
-/* The B operand of one 16-row tile for 32-block b of the staged chunk (row = this lane's row
- * in LDS) and the scale words the chains need. */
+/* Four words of biased codes (f16 1024 + u, from 0x6400 | u) to the f16 codes u: one packed f16
+ * subtraction per word, exact (both terms and the difference are small integers). */
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ f16x8 mx_pack_codes(uint32_t b0, uint32_t b1, uint32_t b2, uint32_t b3)
+{
+    const f16x2 k = { (_Float16)1024.0f, (_Float16)1024.0f };
+    const f16x2 c0 = __builtin_bit_cast(f16x2, b0) - k, c1 = __builtin_bit_cast(f16x2, b1) - k;
+    const f16x2 c2 = __builtin_bit_cast(f16x2, b2) - k, c3 = __builtin_bit_cast(f16x2, b3) - k;
+    return f16x8{ c0.x, c0.y, c1.x, c1.y, c2.x, c2.y, c3.x, c3.y };
+}
+
+/* The B operand of one 16-row tile for 32-block b of the staged chunk (row = this lane's row in
+ * LDS) and the scale words the chains need. */
 struct MxB {
     f16x8 op;
     uint32_t dw;      /* Q4_0: d (low half); Q4_1: d | m << 16; Q6_K: d (low half) */
     float sc;         /* Q6_K: the lane's sub-scale (k < 4: sc[2g], k >= 4: sc[2g+1]) */
-    int sa, sb;       /* Q6_K: both sub-scales of the block */
+    uint32_t sab;     /* Q6_K: both sub-scales as int16 pair (sc[2g] low) */
 };
 
-__device__ __forceinline__ f16x8 mx_pack_codes(uint32_t b0, uint32_t b1, uint32_t b2, uint32_t b3)
+/* The word at base + O + a (base 4-byte aligned, a a multiple of 4): one aligned read for
+ * O == 0, two and a byte alignment for O == 2. */
+template <int O>
+__device__ __forceinline__ uint32_t lds_word_at(const uint8_t *base, uint32_t a)
 {
-    return __builtin_bit_cast(f16x8, u32x4{ b0, b1, b2, b3 });
+    if constexpr (O == 0) return *(const uint32_t *)(base + a);
+    else return lds_u32(base, O + a);
 }
 
-template <int TYPE, int O>
+template <int TYPE, int O, int PAR>
 __device__ __forceinline__ MxB mx_weights(const uint8_t *row, int b, int lg, int kh)
 {
-    constexpr uint32_t bias = 0x64006400u;
+    const uint32_t m4 = 0x000f000fu, m8 = 0x00ff00ffu, bias = 0x64006400u;
     MxB w;
     if constexpr (TYPE == 14) {
-        const uint8_t *sb = row + O;
         const int h = b >> 2, g = b & 3;
-        const uint32_t qlA = lds_word_at<O>(sb, 64 * h + 32 * (g & 1) + 4 * lg);
-        const uint32_t qlB = lds_word_at<O>(sb, 64 * h + 32 * (g & 1) + 16 + 4 * lg);
-        const uint32_t qhA = lds_word_at<O>(sb, 128 + 32 * h + 4 * lg);
-        const uint32_t qhB = lds_word_at<O>(sb, 128 + 32 * h + 16 + 4 * lg);
+        const uint32_t qlA = lds_word_at<O>(row, 64 * h + 32 * (g & 1) + 4 * lg);
+        const uint32_t qlB = lds_word_at<O>(row, 64 * h + 32 * (g & 1) + 16 + 4 * lg);
+        const uint32_t qhA = lds_word_at<O>(row, 128 + 32 * h + 4 * lg);
+        const uint32_t qhB = lds_word_at<O>(row, 128 + 32 * h + 16 + 4 * lg);
         const int ns = 4 * (g >> 1), hs = 2 * g;
         const uint32_t cA = ((qlA >> ns) & 0x0f0f0f0fu) | (((qhA >> hs) & 0x03030303u) << 4);
         const uint32_t cB = ((qlB >> ns) & 0x0f0f0f0fu) | (((qhB >> hs) & 0x03030303u) << 4);
-        w.op = mx_pack_codes((cA & 0x00ff00ffu) | bias, ((cA >> 8) & 0x00ff00ffu) | bias, (cB & 0x00ff00ffu) | bias,
-                             ((cB >> 8) & 0x00ff00ffu) | bias);
-        const uint32_t scw = *(const uint16_t *)(sb + 192 + 8 * h + 2 * g);
-        w.sa = (int)(int8_t)(scw & 0xffu);
-        w.sb = (int)(int8_t)(scw >> 8);
-        w.sc = (float)(kh ? w.sb : w.sa);
-        w.dw = *(const uint16_t *)(sb + 208);
+        w.op = mx_pack_codes(and_or(cA, m8, bias), and_or(cA >> 8, m8, bias), and_or(cB, m8, bias),
+                             and_or(cB >> 8, m8, bias));
+        const uint32_t scw = *(const uint16_t *)(row + O + 192 + 8 * h + 2 * g);
+        const int sa = (int)(int8_t)(scw & 0xffu), sbv = (int)(int8_t)(scw >> 8);
+        w.sab = ((uint32_t)sa & 0xffffu) | ((uint32_t)sbv << 16);
+        w.sc = (float)(kh ? sbv : sa);
+        w.dw = *(const uint16_t *)(row + O + 208);
     } else {
         constexpr int BB = TYPE == 3 ? 20 : 18, QO = TYPE == 3 ? 4 : 2;
         uint32_t v;
-        if (TYPE == 3 || (b & 1)) v = *(const uint32_t *)(row + BB * b + QO + 4 * lg);
-        else v = lds_u32(row, BB * b + QO + 4 * lg);
-        w.op = mx_pack_codes((v & 0x000f000fu) | bias, ((v >> 8) & 0x000f000fu) | bias, ((v >> 4) & 0x000f000fu) | bias,
-                             ((v >> 12) & 0x000f000fu) | bias);
+        if (TYPE == 3 || PAR) v = *(const uint32_t *)(row + BB * b + QO + 4 * lg);
+        else v = lds_u32(row, BB * b + QO + 4 * lg);      /* even blocks: 2 mod 4 */
+        w.op = mx_pack_codes(and_or(v, m4, bias), and_or(v >> 8, m4, bias), and_or(v >> 4, m4, bias),
+                             and_or(v >> 12, m4, bias));
         w.dw = TYPE == 3 ? *(const uint32_t *)(row + BB * b) : (uint32_t) * (const uint16_t *)(row + BB * b);
         w.sc = 0.0f;
-        w.sa = w.sb = 0;
+        w.sab = 0u;
     }
     return w;
 }
@@ -2179,155 +2214,192 @@ __device__ __forceinline__ float mix_fma_hi(uint32_t h, float f, float c)
     return r;
 }
 
-template <int TYPE, int WSG, int GU, int O>
-__device__ __forceinline__ void mx_chunk(const uint8_t *W, const uint8_t *R, int np, int lr, int lg, int kh, int jd,
-                                         int offa_lo, int offa_hi, f32x4 (&acc)[4][4], float (&cr)[4][4])
+/* One block b (parity PAR) of the staged chunk: NP slot pairs of this wave against its two
+ * 16-row tiles. */
+template <int TYPE, int NP, int O, int PAR>
+__device__ __forceinline__ void mx_block(int b, const uint8_t *W, const uint8_t *R, int lr, int lg, int kh, int jd,
+                                         int offa_lo, int offa_hi, f32x4 (&acc)[2][4], float (&cr)[2][4])
 {
+    constexpr int WS = mx_wstride(TYPE);
+    MxB w[2];
 #pragma unroll
-    for (int b = 0; b < kMxC; b++) {
-        MxB w[4];
+    for (int t = 0; t < 2; t++) w[t] = mx_weights<TYPE, O, PAR>(W + (16 * t + lr) * WS, b, lg, kh);
 #pragma unroll
-        for (int t = 0; t < 4; t++) w[t] = mx_weights<TYPE, O>(W + (16 * t + lr) * mx_wstride(TYPE), b, lg, kh);
+    for (int p = 0; p < NP; p++) {
+        const uint8_t *rp = R + (2 * p) * kMxRStride + b * kMxRec;
+        const u32x2 lo = *(const u32x2 *)(rp + offa_lo), hi = *(const u32x2 *)(rp + offa_hi);
+        const f16x8 aop = __builtin_bit_cast(f16x8, u32x4{ lo.x, lo.y, hi.x, hi.y });
+        const uint8_t *rd = rp + jd * kMxRStride;
+        u32x4 dx;
+        if constexpr (TYPE == 14) dx = *(const u32x4 *)(rd + 96);        /* d, ds, s16 pair, 0 */
+        else {
+            const u32x2 d2 = *(const u32x2 *)(rd + 96);                   /* d, ds */
+            dx = u32x4{ d2.x, d2.y, 0u, 0u };
+        }
+        const float xd = __uint_as_float(dx.x), xds = __uint_as_float(dx.y);
 #pragma unroll
-        for (int p = 0; p < 4; p++) {
-            if (p < np) {
-                const uint8_t *rp = R + ((2 * p) * kMxC + b) * kMxRec;
-                const u32x2 lo = *(const u32x2 *)(rp + offa_lo);
-                const u32x2 hi = *(const u32x2 *)(rp + offa_hi);
-                const f16x8 aop = __builtin_bit_cast(f16x8, u32x4{ lo.x, lo.y, hi.x, hi.y });
-                const uint8_t *rd = rp + jd * kMxC * kMxRec;
-                const f32x4 cin = *(const f32x4 *)(rd + 64 + 16 * kh);
-                const u32x4 dx = *(const u32x4 *)(rd + 96);       /* d, ds, s16 pair, 0 */
-                const float xd = __uint_as_float(dx.x), xds = __uint_as_float(dx.y);
+        for (int t = 0; t < 2; t++) {
+            const f32x4 S =
+                __builtin_amdgcn_mfma_f32_16x16x32_f16(aop, w[t].op, f32x4{ 0.0f, 0.0f, 0.0f, 0.0f }, 0, 0, 0);
+            const float dd = mix_mul(w[t].dw, xd);
+            if constexpr (TYPE == 14) {
 #pragma unroll
-                for (int t = 0; t < 4; t++) {
-                    const f32x4 S = __builtin_amdgcn_mfma_f32_16x16x32_f16(aop, w[t].op, cin, 0, 0, 0);
-                    const float dd = mix_mul(w[t].dw, xd);
-                    if constexpr (TYPE == 14) {
+                for (int v = 0; v < 4; v++) acc[t][p][v] = __builtin_fmaf(S[v] * w[t].sc, dd, acc[t][p][v]);
+                /* sc[2g]*s16[0] + sc[2g+1]*s16[1] in one packed int16 dot */
+                const uint32_t s16p = dx.z;       /* (bit_cast of a vector element itself reads .x) */
+                const int ssum = __builtin_amdgcn_sdot2(__builtin_bit_cast(short2_t, w[t].sab),
+                                                        __builtin_bit_cast(short2_t, s16p), 0, false);
+                cr[t][p] = __builtin_fmaf(dd, (float)ssum, cr[t][p]);
+            } else {
 #pragma unroll
-                        for (int v = 0; v < 4; v++) acc[t][p][v] = __builtin_fmaf(S[v] * w[t].sc, dd, acc[t][p][v]);
-                        const int s0 = (int)(int16_t)(dx.z & 0xffffu), s1 = (int)(int16_t)(dx.z >> 16);
-                        cr[t][p] = __builtin_fmaf(dd, (float)(w[t].sa * s0 + w[t].sb * s1), cr[t][p]);
-                    } else {
-#pragma unroll
-                        for (int v = 0; v < 4; v++) acc[t][p][v] = __builtin_fmaf(S[v], dd, acc[t][p][v]);
-                        if constexpr (TYPE == 3) cr[t][p] = mix_fma_hi(w[t].dw, xds, cr[t][p]);   /* off += m*ds */
-                        else cr[t][p] = mix_fma_lo(w[t].dw, xds, cr[t][p]);                     /* corr += d*ds */
-                    }
-                }
+                for (int v = 0; v < 4; v++) acc[t][p][v] = __builtin_fmaf(S[v], dd, acc[t][p][v]);
+                if constexpr (TYPE == 3) cr[t][p] = mix_fma_hi(w[t].dw, xds, cr[t][p]);   /* off += m*ds */
+                else cr[t][p] = mix_fma_lo(w[t].dw, xds, cr[t][p]);                     /* corr += d*ds */
             }
         }
     }
 }
 
+/* One staged chunk (kMxC blocks), two blocks per loop trip. A lane's A words are its x words
+ * where it holds x, else the record's zero words. */
+template <int TYPE, int NP, int O>
+__device__ __forceinline__ void mx_chunk(const uint8_t *W, const uint8_t *R, int lr, int lg, int kh, int jd,
+                                         int offa_lo, int offa_hi, f32x4 (&acc)[2][4], float (&cr)[2][4])
+{
+#pragma unroll 1
+    for (int b = 0; b < kMxC; b += 2) {
+        mx_block<TYPE, NP, O, 0>(b, W, R, lr, lg, kh, jd, offa_lo, offa_hi, acc, cr);
+        mx_block<TYPE, NP, O, 1>(b + 1, W, R, lr, lg, kh, jd, offa_lo, offa_hi, acc, cr);
+    }
+}
+
+template <int TYPE, int O>
+__device__ __forceinline__ void mx_chunk_np(int np, const uint8_t *W, const uint8_t *R, int lr, int lg, int kh, int jd,
+                                            int offa_lo, int offa_hi, f32x4 (&acc)[2][4], float (&cr)[2][4])
+{
+    if (np == 4) mx_chunk<TYPE, 4, O>(W, R, lr, lg, kh, jd, offa_lo, offa_hi, acc, cr);
+    else if (np == 3) mx_chunk<TYPE, 3, O>(W, R, lr, lg, kh, jd, offa_lo, offa_hi, acc, cr);
+    else if (np == 2) mx_chunk<TYPE, 2, O>(W, R, lr, lg, kh, jd, offa_lo, offa_hi, acc, cr);
+    else if (np == 1) mx_chunk<TYPE, 1, O>(W, R, lr, lg, kh, jd, offa_lo, offa_hi, acc, cr);
+}
+
+/* The LDS DMA: `bytes` (4 or 16) from src of every active lane to dst + lane * bytes. */
+template <int BYTES>
+__device__ __forceinline__ void dma_to_lds(const void *src, uint8_t *dst)
+{
+    if constexpr (BYTES == 4) __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void *)dst, 4, 0, 0);
+    else __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void *)dst, 16, 0, 0);
+}
+
+/* Wait for all of this wave's vector memory instructions (its LDS DMA included) and LDS
+ * accesses, then the block barrier. The memory clobber keeps the compiler from moving LDS
+ * accesses across it. */
+__device__ __forceinline__ void mx_wait_barrier()
+{
+    asm volatile("s_waitcnt vmcnt(0)\n\ts_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
 /* Gate/up (GU = 1: gate rows against the token's input records, the same up rows, SwiGLU, the
- * int8 activation blocks and their records) or down (GU = 0: dn rows) of one slot tile. */
+ * int8 activation blocks and their records) or down (GU = 0: dn rows) of one slot tile. Two
+ * blocks share a CU (16 waves, four per SIMD), which hides the LDS and memory latency. */
 template <int TYPE, int WSG, int GU>
-__global__ __launch_bounds__(512) void mx_kernel(MxArgs a)
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4, 4))) void mx_kernel(MxArgs a)
 {
     extern __shared__ __align__(16) uint8_t smem[];
-    constexpr int RWG = 512 / WSG, SWG = 8 * WSG, WS = mx_wstride(TYPE);
-    constexpr int WBYTES = RWG * WS, BUF = mx_buf_bytes(TYPE, WSG);
-    constexpr int WU = TYPE == 14 ? 4 : 16;                                   /* bytes per copy unit  */
-    constexpr int WUR = TYPE == 14 ? 54 : kMxC * (TYPE == 3 ? 20 : 18) / 16;  /* units per row      */
-    constexpr int WPT = (RWG * WUR + 511) / 512, RU = SWG * kMxC * kMxRec / 16, RPT = (RU + 511) / 512;
+    using Lay = MxLayout<TYPE, WSG>;
+    constexpr int RWG = Lay::RWG, SWG = Lay::SWG, WS = Lay::WS, BUF = Lay::BUF;
     if ((int)blockIdx.y >= a.S.meta[1]) return;
     const int4 tl = a.S.tiles[blockIdx.y];
     const int e = tl.x, s0 = tl.y + (int)blockIdx.z * SWG, ns = min(SWG, tl.z - s0);
     if (ns <= 0) return;
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, lr = lane & 15, lg = lane >> 4;
+    const int tid = threadIdx.x, lane = tid & 63, lr = lane & 15, lg = lane >> 4;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);          /* wave-uniform */
     const int wr = wave / WSG, ws = wave % WSG, kh = lg & 1, jd = lg >> 1;
     const int nb = (GU ? a.E : a.F) >> 5, nch = nb / kMxC;
     const int R0 = (int)blockIdx.x * (GU ? RWG / 2 : RWG);
 
-    /* row i of the staged tile: for gate/up, row group g = i / 64 holds gate rows
-     * R0 + 32g .. R0 + 32g + 31 and then the same up rows */
-    auto row_ptr = [&](int i) -> const uint8_t * {
+    /* row i of the staged tile: for gate/up, row group g = i / 32 holds gate rows
+     * R0 + 16g .. R0 + 16g + 15 and then the same up rows. Byte offsets inside one expert's
+     * matrix fit 32 bits; the expert bases are wave-uniform. */
+    const uint8_t *wb0 = a.w0 + (size_t)e * a.eb, *wb1 = GU ? a.w1 + (size_t)e * a.eb : wb0;
+    const uint32_t rb = (uint32_t)a.rb;
+    auto row_src = [&](int i, uint32_t off) -> const uint8_t * {
         if (GU) {
-            const int g = i >> 6, within = i & 63;
-            return (within < 32 ? a.w0 : a.w1) + (size_t)e * a.eb + (size_t)(R0 + 32 * g + (within & 31)) * a.rb;
+            const int g = i >> 5, within = i & 31;
+            return (within < 16 ? wb0 : wb1) + ((uint32_t)(R0 + 16 * g + (within & 15)) * rb + off);
         }
-        return a.w0 + (size_t)e * a.eb + (size_t)(R0 + i) * a.rb;
+        return wb0 + ((uint32_t)(R0 + i) * rb + off);
     };
     /* slot i's records (slots past the tile repeat its last slot) */
     auto rec_ptr = [&](int i) -> const uint8_t * {
         const int s = s0 + min(i, ns - 1);
         return a.rec + (size_t)(GU ? a.S.slot_t[s] : s) * nb * kMxRec;
     };
-    uint32_t wv[WPT][WU / 4];
-    u32x4 rv[RPT];
-    auto load = [&](int c) {
+    /* the DMA of chunk c into buffer k: weight instruction q goes to wave q % 8, the records of
+     * slot i (one instruction) to wave i % 8, their source fixed per block */
+    constexpr int RPW = SWG / 8;                      /* slots whose records one wave copies */
+    const uint8_t *rsrc[RPW];
 #pragma unroll
-        for (int m = 0; m < WPT; m++) {
-            const int idx = min(tid + 512 * m, RWG * WUR - 1), i = idx / WUR, u = idx - i * WUR;
-            if constexpr (TYPE == 14) {
-                /* the super-block starts 2 bytes past a 4-byte boundary on odd chunks */
-                wv[m][0] = ((const uint32_t *)(row_ptr(i) + (size_t)c * 210 - 2 * (c & 1)))[u];
-            } else {
-                *(u32x4 *)wv[m] = *(const u32x4 *)(row_ptr(i) + (size_t)c * (WUR * 16) + 16 * u);
+    for (int j = 0; j < RPW; j++) rsrc[j] = rec_ptr(wave + 8 * j);
+    auto issue = [&](int c, int k) {
+        uint8_t *base = smem + k * BUF;
+        for (int q = wave; q < Lay::WINSTR; q += 8) {
+            const int n = 64 * q + lane;
+            if (n < RWG * Lay::WUR) {
+                const int i = n / Lay::WUR, u = n - i * Lay::WUR;
+                if constexpr (TYPE == 14) {
+                    /* the super-block starts 2 bytes past a 4-byte boundary on odd chunks; the
+                     * two padding words of the slot repeat the last one */
+                    dma_to_lds<4>(row_src(i, (uint32_t)(c * 210 - 2 * (c & 1) + 4 * min(u, Lay::WUSED - 1))),
+                                  base + 256 * q);
+                } else {
+                    dma_to_lds<16>(row_src(i, (uint32_t)(c * (kMxC * (TYPE == 3 ? 20 : 18)) + 16 * u)), base + 1024 * q);
+                }
             }
         }
 #pragma unroll
-        for (int m = 0; m < RPT; m++) {
-            const int idx = min(tid + 512 * m, RU - 1), i = idx / (kMxC * kMxRec / 16), u = idx - i * (kMxC * kMxRec / 16);
-            rv[m] = ((const u32x4 *)(rec_ptr(i) + (size_t)c * kMxC * kMxRec))[u];
-        }
-    };
-    auto store = [&](int buf) {
-        uint8_t *Wl = smem + buf * BUF, *Rl = Wl + WBYTES;
-#pragma unroll
-        for (int m = 0; m < WPT; m++) {
-            const int idx = tid + 512 * m;
-            if (idx < RWG * WUR) {
-                const int i = idx / WUR, u = idx - i * WUR;
-                if constexpr (TYPE == 14) *(uint32_t *)(Wl + i * WS + 4 * u) = wv[m][0];
-                else *(u32x4 *)(Wl + i * WS + 16 * u) = *(const u32x4 *)wv[m];
-            }
-        }
-#pragma unroll
-        for (int m = 0; m < RPT; m++)
-            if (tid + 512 * m < RU) ((u32x4 *)Rl)[tid + 512 * m] = rv[m];
+        for (int j = 0; j < RPW; j++)
+            dma_to_lds<16>(rsrc[j] + (size_t)c * kMxC * kMxRec + 16 * lane,
+                           base + Lay::WBYTES + (wave + 8 * j) * kMxRStride);
     };
 
-    /* A reads: D... lane row lr is slot ja = lr/8 of the pair, reference lane ka = lr%8; it
-     * holds x only if ka%4 == lg, in the low half of its 8 K positions for ka < 4 */
+    /* A reads: lane row lr is slot ja = lr/8 of the pair, reference lane ka = lr%8; it holds x
+     * only if ka%4 == lg, in the low half of its 8 K positions for ka < 4 */
     const int ja = lr >> 3, ka = lr & 7;
     const bool nz = (ka & 3) == lg;
-    const int offa_lo = ja * kMxC * kMxRec + ((nz && ka < 4) ? 8 * ka : kMxZero);
-    const int offa_hi = ja * kMxC * kMxRec + ((nz && ka >= 4) ? 8 * ka : kMxZero);
+    const int offa_lo = ja * kMxRStride + ((nz && ka < 4) ? 8 * ka : kMxZero);
+    const int offa_hi = ja * kMxRStride + ((nz && ka >= 4) ? 8 * ka : kMxZero);
     const int nw = min(max(ns - 8 * ws, 0), 8), np = (nw + 1) >> 1;      /* this wave's slot pairs */
 
-    f32x4 acc[4][4];
-    float cr[4][4];
+    f32x4 acc[2][4];
+    float cr[2][4];
 #pragma unroll
-    for (int t = 0; t < 4; t++)
+    for (int t = 0; t < 2; t++)
 #pragma unroll
         for (int p = 0; p < 4; p++) {
             acc[t][p] = f32x4{ 0.0f, 0.0f, 0.0f, 0.0f };
             cr[t][p] = 0.0f;
         }
 
-    load(0);
-    store(0);
-    __syncthreads();
+    issue(0, 0);
+    mx_wait_barrier();
     for (int c = 0; c < nch; c++) {
         const int buf = c & 1;
-        if (c + 1 < nch) load(c + 1);
-        const uint8_t *Wl = smem + buf * BUF + (64 * wr) * WS;
-        const uint8_t *Rl = smem + buf * BUF + WBYTES + (8 * ws) * kMxC * kMxRec;
+        if (c + 1 < nch) issue(c + 1, buf ^ 1);
+        const uint8_t *Wl = smem + buf * BUF + (32 * wr) * WS;
+        const uint8_t *Rl = smem + buf * BUF + Lay::WBYTES + (8 * ws) * kMxRStride;
         if (TYPE == 14 && (c & 1))
-            mx_chunk<TYPE, WSG, GU, 2>(Wl, Rl, np, lr, lg, kh, jd, offa_lo, offa_hi, acc, cr);
+            mx_chunk_np<TYPE, 2>(np, Wl, Rl, lr, lg, kh, jd, offa_lo, offa_hi, acc, cr);
         else
-            mx_chunk<TYPE, WSG, GU, 0>(Wl, Rl, np, lr, lg, kh, jd, offa_lo, offa_hi, acc, cr);
-        if (c + 1 < nch) store(buf ^ 1);
-        __syncthreads();
+            mx_chunk_np<TYPE, 0>(np, Wl, Rl, lr, lg, kh, jd, offa_lo, offa_hi, acc, cr);
+        mx_wait_barrier();           /* chunk c+1 has landed; buffer c is free for chunk c+2 */
     }
 
     /* hsum256 per (row, slot): lanes of k-half 0 take the partner lane's k + 4 chains */
     constexpr float scale = finish_scale(TYPE);
     float *res = (float *)smem;                                   /* [RWG][SWG + 1] */
 #pragma unroll
-    for (int t = 0; t < 4; t++)
+    for (int t = 0; t < 2; t++)
 #pragma unroll
         for (int p = 0; p < 4; p++) {
             f32x4 o;
@@ -2337,22 +2409,24 @@ __global__ __launch_bounds__(512) void mx_kernel(MxArgs a)
                 const f32x4 &q = acc[t][p];
                 const float h = ((q[0] + o[0]) + (q[2] + o[2])) + ((q[1] + o[1]) + (q[3] + o[3]));
                 const float val = h - scale * cr[t][p];
-                const int row = 64 * wr + 16 * t + lr, sl = 8 * ws + 2 * p + jd;
+                const int row = 32 * wr + 16 * t + lr, sl = 8 * ws + 2 * p + jd;
                 if (GU) res[row * (SWG + 1) + sl] = val;
                 else if (sl < ns) a.S.dn[(size_t)(s0 + sl) * a.E + R0 + row] = val;
             }
         }
     if (!GU) return;
     __syncthreads();
-    /* a = silu(g) * u (src/model.c:989-994) into the gate half of res, then the int8 blocks
-     * of whole 32-row blocks (src/model.c:996-997) and their records */
+    /* a = silu(g) * u (src/model.c:989-994) into the gate rows of res, then the int8 blocks of
+     * whole 32-row blocks (src/model.c:996-997) and their records. F-row fr sits in row group
+     * fr / 16: gate at res row 32 (fr / 16) + fr % 16, up 16 rows further. */
     const int F = a.F, nbF = F >> 5;
+    auto gate_row = [](int fr) { return 32 * (fr >> 4) + (fr & 15); };
     for (int i = tid; i < (RWG / 2) * SWG; i += 512) {
-        const int fr = i / SWG, sl = i - fr * SWG, g = fr >> 5, j = fr & 31;
+        const int fr = i / SWG, sl = i - fr * SWG;
         if (sl >= ns) continue;
-        const float gv = res[(64 * g + j) * (SWG + 1) + sl], uv = res[(64 * g + 32 + j) * (SWG + 1) + sl];
+        const float gv = res[gate_row(fr) * (SWG + 1) + sl], uv = res[(gate_row(fr) + 16) * (SWG + 1) + sl];
         const float av = silu_ref(gv) * uv;
-        res[(64 * g + j) * (SWG + 1) + sl] = av;
+        res[gate_row(fr) * (SWG + 1) + sl] = av;
         if (a.debug) {
             const size_t s = (size_t)(s0 + sl);
             a.S.gu[s * 2 * F + R0 + fr] = gv;
@@ -2367,7 +2441,7 @@ __global__ __launch_bounds__(512) void mx_kernel(MxArgs a)
         if (sl >= ns) continue;
         float v[32];
 #pragma unroll
-        for (int j = 0; j < 32; j++) v[j] = res[(64 * g + j) * (SWG + 1) + sl];
+        for (int j = 0; j < 32; j++) v[j] = res[gate_row(32 * g + j) * (SWG + 1) + sl];
         const Q8Vals q = quantize_block(v);
         const int s = s0 + sl, blk = (R0 >> 5) + g;
         store_q8(q, a.S.aq + (size_t)s * nbF + blk);
@@ -2379,34 +2453,33 @@ __global__ __launch_bounds__(512) void mx_kernel(MxArgs a)
 template <int TYPE, int GU>
 static void launch_mx(const MxArgs &a, int wsg, int rows, int maxt, hipStream_t st)
 {
-    const size_t lds = 2 * (size_t)mx_buf_bytes(TYPE, wsg);
-    if (wsg == 4)
-        QLAUNCH(GU ? "gateup" : "down", (mx_kernel<TYPE, 4, GU>), dim3(rows / (GU ? 64 : 128), maxt, kTileN / 32),
+    const size_t lds = (size_t)mx_lds_bytes(TYPE, wsg);
+    const int rwg = 256 / wsg;
+    if (wsg == 2)
+        QLAUNCH(GU ? "gateup" : "down", (mx_kernel<TYPE, 2, GU>), dim3(rows / (GU ? rwg / 2 : rwg), maxt, kTileN / 16),
                 dim3(512), lds, st, a);
     else
-        QLAUNCH(GU ? "gateup" : "down", (mx_kernel<TYPE, 2, GU>), dim3(rows / (GU ? 128 : 256), maxt, kTileN / 16),
+        QLAUNCH(GU ? "gateup" : "down", (mx_kernel<TYPE, 1, GU>), dim3(rows / (GU ? rwg / 2 : rwg), maxt, kTileN / 8),
                 dim3(512), lds, st, a);
 }
 
 /* Whether the MFMA kernels take this layer: Q4_0 gate and up; Q4_0, Q4_1 or Q6_K down (Q6_K
- * rows a multiple of 4 bytes long); 32-blocks in whole chunks; rows in whole tiles. */
+ * rows a multiple of 4 bytes long); 32-blocks in whole chunks; rows in whole blocks' tiles. */
 bool mx_supported(const Shape &s, const LayerDev &L, int *down_mx)
 {
     const int nbE = s.E / 32, nbF = s.F / 32;
     const bool gu = L.gate_type == 2 && L.up_type == 2 && nbE % kMxC == 0 && s.F % 128 == 0;
-    /* Q6_K down: its kernel spills registers with the register-staged copy; the exact kernel
-     * takes it for now */
-    const bool dn = (L.down_type == 2 || L.down_type == 3 || (L.down_type == 14 && L.down_rb % 4 == 0 && kMxQ6K)) &&
+    const bool dn = (L.down_type == 2 || L.down_type == 3 || (L.down_type == 14 && L.down_rb % 4 == 0)) &&
                     nbF % kMxC == 0 && s.E % 256 == 0;
     if (down_mx) *down_mx = dn;
     return gu;
 }
 
-/* Slots per block: 32 when the batch averages at least 24 slots per active expert, else 16. */
+/* Slots per block: 16 when the batch averages at least 12 slots per active expert, else 8. */
 static int mx_wsg(const Shape &s, int T)
 {
     const int NS = T * s.K, act = s.X < NS ? s.X : NS;
-    return NS >= 24 * act ? 4 : 2;
+    return NS >= 12 * act ? 2 : 1;
 }
 
 hipError_t launch_experts_mx(const Shape &s, const LayerDev &L, const Scratch &S, float *out, int T, int debug,
