@@ -281,6 +281,112 @@ def run_stack(args, w):
     print(json.dumps(result), flush=True)
 
 
+def extra_prefill(steps: int = 10, warmup: int = 2, NL: int = 4):
+    """The 512-token Zipf prefill of the 235B shape (the prefill half of the metric), bounded to
+    a few seconds: ms per layer, distinct experts, int8 op/s against the MFMA peak, per-kernel
+    times. Cycles NL resident layers."""
+    w = WORKLOADS["q235b_prefill_t512"]
+    ctx = qmsg.Context(w.E, w.X, w.K, w.F, n_layer=NL, max_tokens=w.T)
+    bias = zipf_bias(w.X, w.K, w.T, w.E)
+    for l in range(NL):
+        ctx.synth(l, w.seed + 1000 * l, router_col0=bias)
+    row = w.T * w.E * 4
+    total = steps + warmup
+    d_x = ctx.device_alloc(total * row)
+    d_out = ctx.device_alloc(total * row)
+    for s in range(total):
+        ctx.synth_input(w.seed + 7 + s, 0, w.T, d_x + s * row, bias_col0=True)
+    ctx.sync()
+    for s in range(warmup):
+        ctx.moe_device(s % NL, d_x + s * row, w.T, d_out + s * row)
+    ctx.sync()
+    t0 = time.perf_counter()
+    for s in range(warmup, total):
+        ctx.moe_device(s % NL, d_x + s * row, w.T, d_out + s * row)
+    ctx.sync()
+    el = time.perf_counter() - t0
+    ms = 1e3 * el / steps
+    ctx.profile(True)
+    for s in range(warmup, total):
+        ctx.moe_device(s % NL, d_x + s * row, w.T, d_out + s * row)
+    ctx.sync()
+    kern = {}
+    for name in ("route", "select", "dispatch", "mxin", "gateup", "actq", "down", "combine"):
+        n, kms = ctx.profile_read(name)
+        if n:
+            kern[name] = {"launches": n, "avg_us": round(1e3 * kms / n, 3)}
+    ctx.profile(False)
+    x = ctx.d2h(d_x + warmup * row, (w.T, w.E))
+    _, dbg = ctx.moe_debug(warmup % NL, x)
+    d_active = len(dbg["active"])
+    ctx.close()
+    ops = w.int8_ops()
+    nbytes = w.layer_bytes(d_active)
+    mfma_us = ops / (INT8_PEAK_TOPS * 1e12) * 1e6
+    hbm_us = nbytes / (HBM_PEAK_GBS * 1e9) * 1e6
+    return {
+        "workload": f"{w.name}: {w.note}, {NL} resident layers cycled",
+        "ms_per_layer": round(ms, 4), "tokens_per_s": round(w.T / (ms * 1e-3), 1),
+        "distinct_experts": d_active, "int8_ops": ops,
+        "int8_tops": round(ops / (ms * 1e-3) / 1e12, 3),
+        "int8_frac_of_peak": round(ops / (ms * 1e-3) / 1e12 / INT8_PEAK_TOPS, 5),
+        "algorithmic_bytes": nbytes, "achieved_GBps": round(nbytes / (ms * 1e-3) / 1e9, 1),
+        "bound_us": {"mfma_at_peak": round(mfma_us, 1), "hbm_at_peak": round(hbm_us, 1)},
+        "path": "auto (MFMA expert kernels at this batch)", "kernels": kern,
+    }
+
+
+def extra_stack_layer(steps: int = 4, warmup: int = 1, NL: int = 8):
+    """Per-layer figures of the 94-layer stack shape (Q6_K down): h += moe(l, rmsnorm(h)) over NL
+    resident layers (each layer's 1.57 GB exceeds the last-level cache, so NL distinct layers
+    stream as the full stack does), at its 64-token batch and at batch 1 inside the chain."""
+    w = WORKLOADS["q235b_stack_t64"]
+    ctx = qmsg.Context(w.E, w.X, w.K, w.F, n_layer=NL, max_tokens=w.T)
+    for l in range(NL):
+        ctx.synth(l, w.seed + 1000 * l, down_type=w.down_type)
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle as orc  # checker only: host rmsnorm of the sample input
+    out = {"workload": f"{w.name}: {w.note}; {NL} resident layers chained, per-layer figures"}
+    for T in (w.T, 1):
+        row = T * w.E * 4
+        total = steps + warmup
+        d_h = ctx.device_alloc(total * row)
+        for s in range(total):
+            ctx.synth_input(w.seed + 7 + s, 0, T, d_h + s * row)
+        ctx.sync()
+        for s in range(warmup):
+            ctx.moe_chain(0, NL, d_h + s * row, T)
+        ctx.sync()
+        t0 = time.perf_counter()
+        for s in range(warmup, total):
+            ctx.moe_chain(0, NL, d_h + s * row, T)
+        ctx.sync()
+        el = time.perf_counter() - t0
+        us_layer = 1e6 * el / (steps * NL)
+        ctx.profile(True)
+        ctx.moe_chain(0, NL, d_h, T)
+        ctx.sync()
+        kern = {}
+        for name in ("rmsnorm", "route", "select", "dispatch", "gateup", "actq", "down", "combine", "add"):
+            n, kms = ctx.profile_read(name)
+            if n:
+                kern[name] = {"launches": n, "avg_us": round(1e3 * kms / n, 3)}
+        ctx.profile(False)
+        x = ctx.d2h(d_h + warmup * row, (T, w.E))
+        _, dbg = ctx.moe_debug(0, orc.rmsnorm(x))
+        d_active = len(dbg["active"])
+        nbytes = 4 * w.X * w.E + d_active * w.expert_bytes + 8 * T * w.E
+        out[f"t{T}"] = {
+            "us_per_layer": round(us_layer, 2), "projected_94_layer_ms": round(us_layer * w.layers / 1e3, 3),
+            "tokens_per_s_94_layers": round(T / (us_layer * w.layers * 1e-6), 2),
+            "distinct_experts_per_layer": d_active, "algorithmic_bytes_per_layer": nbytes,
+            "achieved_GBps": round(nbytes / (us_layer * 1e-6) / 1e9, 1),
+            "frac_of_hbm_peak": round(nbytes / (us_layer * 1e-6) / 1e9 / HBM_PEAK_GBS, 4), "kernels": kern,
+        }
+    ctx.close()
+    return out
+
+
 TRUNK_TYPES = {"f32": qmsg.QMSG_T_F32, "q4_0": qmsg.QMSG_T_Q4_0, "q4_1": qmsg.QMSG_T_Q4_1, "q6_k": qmsg.QMSG_T_Q6_K}
 
 
@@ -454,6 +560,8 @@ def main():
     ap.add_argument("--layers", type=int, default=16, help="distinct resident layers cycled by the steps")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-extras", action="store_true",
+                    help="skip the prefill and stack-layer figures the default decode run also reports")
     ap.add_argument("--path", choices=["auto", "exact", "mfma"], default="auto")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES",
                     help="instead of the layer, run the plain copy kernel on BYTES (reference transfer "
@@ -601,6 +709,11 @@ def main():
         log("timing the CPU baseline")
         result["cpu_baseline"] = cpu_baseline(ctx, w, args.cpu_seconds)
     ctx.close()
+    if w.name == "q235b_decode_t1" and not args.no_extras:
+        log("prefill extra: 512-token Zipf prefill")
+        result["prefill_t512"] = extra_prefill()
+        log("stack extra: per-layer figure of the 94-layer stack shape")
+        result["stack_t64_layer"] = extra_stack_layer()
     print(json.dumps(result), flush=True)
 
 
