@@ -144,7 +144,8 @@ typedef struct {
 
 /* qms_gguf_open (src/gguf.c:222-241, 112-194): parse `path`, or every shard of a
  * "<stem>-00001-of-0000N.gguf" set (src/gguf.c:198-219). Version 3 only; a tensor that runs
- * past the end of its file, or a truncated header, is an error. On failure *out is NULL and
+ * past the end of its file (its extent computed without wrapping), a truncated header or an
+ * unknown value type is an error. On failure *out is NULL and
  * qmsg_last_error(NULL) has the reason. */
 int qmsg_gguf_open(qmsg_gguf **out, const char *path);
 /* qms_gguf_close (src/gguf.c:243-253). */

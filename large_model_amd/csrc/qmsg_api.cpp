@@ -608,9 +608,10 @@ static int dense_check(qmsg_ctx *c, int type, int64_t rows, int64_t cols, const 
         return fail(c, QMSG_E_UNSUPPORTED, "%s: the dense kernels take F32, Q4_0, Q4_1 and Q6_K (got type %d)", what,
                     type);
     const int64_t step = type == QMSG_T_Q6_K ? 2048 : 256;   /* Q6_K: whole chunks of 8 super-blocks */
-    if (rows <= 0 || rows > (1 << 30) || cols <= 0 || cols % step)
-        return fail(c, QMSG_E_UNSUPPORTED, "%s: needs rows > 0 and cols %% %lld == 0 (got %lld x %lld)", what,
-                    (long long)step, (long long)rows, (long long)cols);
+    /* both bounded by 2^30: rows x row bytes stays far inside 64 bits and cols fits an int */
+    if (rows <= 0 || rows > (1 << 30) || cols <= 0 || cols > (1 << 30) || cols % step)
+        return fail(c, QMSG_E_UNSUPPORTED, "%s: needs 0 < rows, cols <= 2^30 and cols %% %lld == 0 (got %lld x %lld)",
+                    what, (long long)step, (long long)rows, (long long)cols);
     return QMSG_OK;
 }
 

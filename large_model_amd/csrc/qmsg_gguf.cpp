@@ -1,248 +1,372 @@
-/* qmsg_gguf.cpp - GGUF v3 header reader: scalar metadata of the first shard and the tensor
- * table of every shard (the reference's qms_gguf_open, src/gguf.c:112-241). Only headers are
- * read here; tensor bytes are fetched by the upload with gguf_pread. No GPU calls. */
+/* qmsg_gguf.cpp - GGUF v3 header reader for the upload into HBM. Behaviour follows the reference's
+ * qms_gguf_open / qms_gguf_get_* (src/gguf.c:112-283): the scalar metadata of the first shard, the
+ * tensor table of every shard with absolute offsets, the same refusals. The layout is read from the
+ * GGUF v3 format itself:
+ *
+ *   "GGUF" u32:version u64:n_tensors u64:n_kv
+ *   n_kv    x { string key, u32 value_type, value }
+ *   n_tensors x { string name, u32 n_dims, u64 ne[n_dims], u32 ggml_type, u64 offset }
+ *   padding to general.alignment (default 32), then the tensor data; offsets are relative to it.
+ *   string = u64 length + bytes; array value = u32 element_type + u64 count + elements.
+ *
+ * Each shard's header is parsed from a read-only mapping of the file with bounds-checked field
+ * reads; the mapping is dropped once the table is built and tensor bytes are fetched later with
+ * pread (gguf_pread). Sizes taken from the file are combined with overflow-checked arithmetic.
+ * No GPU calls. */
 #include <fcntl.h>
+#include <sys/mman.h>
 #include <sys/stat.h>
 #include <unistd.h>
 
 #include <cerrno>
+#include <cmath>
 #include <cstdarg>
 #include <cstdio>
-#include <cstdlib>
 #include <cstring>
+#include <string_view>
 
 #include "qmsg_gguf.h"
 
 namespace {
 
-/* GGUF metadata value types (GGUF v3 specification). */
-enum { V_U8, V_I8, V_U16, V_I16, V_U32, V_I32, V_F32, V_BOOL, V_STR, V_ARR, V_U64, V_I64, V_F64 };
-constexpr int kValueBytes[] = { 1, 1, 2, 2, 4, 4, 4, 1, 0, 0, 8, 8, 8 };
+/* How each GGUF value type is stored: payload bytes and how its scalar views derive. */
+enum class Kind : uint8_t { Unsigned, Signed, Real, Text, List, None };
+struct TypeInfo {
+    uint8_t bytes;
+    Kind kind;
+};
+constexpr uint32_t kTypeStr = 8, kTypeArr = 9, kNumTypes = 13;
+constexpr TypeInfo kTypeInfo[kNumTypes] = {
+    { 1, Kind::Unsigned }, { 1, Kind::Signed }, { 2, Kind::Unsigned }, { 2, Kind::Signed },  /* u8 i8 u16 i16 */
+    { 4, Kind::Unsigned }, { 4, Kind::Signed }, { 4, Kind::Real },                         /* u32 i32 f32    */
+    { 1, Kind::Unsigned },                                                                   /* bool           */
+    { 0, Kind::Text },     { 0, Kind::List },                                                /* string array   */
+    { 8, Kind::Unsigned }, { 8, Kind::Signed }, { 8, Kind::Real },                         /* u64 i64 f64    */
+};
+inline TypeInfo type_info(uint32_t t) { return t < kNumTypes ? kTypeInfo[t] : TypeInfo{ 0, Kind::None }; }
 
-constexpr size_t kKeyCap = 96, kStrCap = 256, kNameCap = sizeof(((qmsg_tensor *)nullptr)->name);
+/* Kept lengths of the reference's fixed-size fields (QmsKV.key[96], QmsKV.str[256],
+ * QmsTensor.name[96]): longer keys, strings and names are cut, the rest of the bytes skipped. */
+constexpr size_t kKeyKeep = 95, kTextKeep = 255, kNameKeep = sizeof(((qmsg_tensor *)nullptr)->name) - 1;
 constexpr int kMaxShards = 256;
+constexpr int kMaxNesting = 16;          /* arrays of arrays deeper than this are refused */
 
-int fail_open(const char *fmt, ...)
+int refuse(const char *fmt, ...)
 {
-    char buf[640];
+    char msg[640];
     va_list ap;
     va_start(ap, fmt);
-    vsnprintf(buf, sizeof buf, fmt, ap);
+    vsnprintf(msg, sizeof msg, fmt, ap);
     va_end(ap);
-    qmsg::set_global_error(buf);
+    qmsg::set_global_error(msg);
     return QMSG_E_INVALID;
 }
 
-int pread_all(int fd, void *dst, uint64_t n, uint64_t off)
-{
-    uint8_t *d = (uint8_t *)dst;
-    while (n > 0) {
-        const size_t want = n > (1ull << 30) ? (size_t)(1ull << 30) : (size_t)n;
-        const ssize_t got = ::pread(fd, d, want, (off_t)off);
-        if (got < 0 && errno == EINTR) continue;
-        if (got <= 0) return -1;
-        d += got;
-        off += (uint64_t)got;
-        n -= (uint64_t)got;
+/* Bounds-checked little-endian fields of a mapped header. Any read past the end clears ok()
+ * and yields zeros; callers check ok() at the points where a refusal is reported. */
+class FieldReader {
+public:
+    FieldReader(const uint8_t *base, uint64_t size) : base_(base), size_(size) {}
+
+    bool ok() const { return ok_; }
+    uint64_t offset() const { return at_; }
+
+    /* Advance over n bytes; returns where they start, or nullptr past the end. */
+    const uint8_t *advance(uint64_t n)
+    {
+        if (!ok_ || n > size_ - at_) {
+            ok_ = false;
+            return nullptr;
+        }
+        const uint8_t *p = base_ + at_;
+        at_ += n;
+        return p;
     }
+    template <class T>
+    T field()
+    {
+        T v{};
+        if (const uint8_t *p = advance(sizeof(T))) memcpy(&v, p, sizeof(T));
+        return v;
+    }
+    /* A GGUF string; the view spans all of its bytes. */
+    std::string_view text()
+    {
+        const uint64_t n = field<uint64_t>();
+        const uint8_t *p = advance(n);
+        return p ? std::string_view((const char *)p, (size_t)n) : std::string_view();
+    }
+    void fail() { ok_ = false; }
+
+private:
+    const uint8_t *base_;
+    uint64_t size_, at_ = 0;
+    bool ok_ = true;
+};
+
+std::string cut(std::string_view s, size_t keep) { return std::string(s.substr(0, keep)); }
+
+/* Step over one value of type t (arrays: every element, nested arrays included). */
+void pass_value(FieldReader &rd, uint32_t t, int depth)
+{
+    const TypeInfo ti = type_info(t);
+    switch (ti.kind) {
+    case Kind::Text: (void)rd.text(); return;
+    case Kind::List: {
+        const uint32_t et = rd.field<uint32_t>();
+        const uint64_t count = rd.field<uint64_t>();
+        const TypeInfo ei = type_info(et);
+        if (ei.kind == Kind::None || depth >= kMaxNesting) return rd.fail();
+        if (ei.bytes) {
+            uint64_t span = 0;
+            if (__builtin_mul_overflow(count, (uint64_t)ei.bytes, &span)) return rd.fail();
+            (void)rd.advance(span);
+            return;
+        }
+        for (uint64_t k = 0; k < count && rd.ok(); k++) pass_value(rd, et, depth + 1);
+        return;
+    }
+    case Kind::None: return rd.fail();
+    default: (void)rd.advance(ti.bytes); return;
+    }
+}
+
+/* A scalar's payload: raw little-endian bits (integers, sign-extended for signed types) or the
+ * value as a double (f32 / f64). */
+void read_scalar(FieldReader &rd, const TypeInfo &ti, qmsg_gguf::Scalar &s)
+{
+    const uint8_t *p = rd.advance(ti.bytes);
+    if (!p) return;
+    uint64_t raw = 0;
+    memcpy(&raw, p, ti.bytes);
+    if (ti.kind == Kind::Signed && ti.bytes < 8) {
+        const int sh = 64 - 8 * ti.bytes;
+        raw = (uint64_t)((int64_t)(raw << sh) >> sh);
+    }
+    if (ti.kind == Kind::Real) {
+        if (ti.bytes == 4) {
+            float f;
+            memcpy(&f, p, 4);
+            s.real = f;
+        } else {
+            memcpy(&s.real, p, 8);
+        }
+    } else {
+        s.bits = raw;
+    }
+}
+
+/* Bytes of one row of ne0 elements, 0 where the type is not one the upload knows or ne0 is not a
+ * whole number of its blocks (src/gguf.c:85-96: those tensors keep nbytes 0). */
+uint64_t bytes_per_row(int type, int64_t ne0)
+{
+    if (ne0 < 0) return 0;
+    struct Blk { int type, elems, bytes; };
+    static constexpr Blk kBlk[] = { { QMSG_T_F32, 1, 4 },    { QMSG_T_F16, 1, 2 },   { QMSG_T_Q4_0, 32, 18 },
+                                    { QMSG_T_Q4_1, 32, 20 }, { QMSG_T_Q8_0, 32, 34 }, { QMSG_T_Q6_K, 256, 210 } };
+    for (const Blk &b : kBlk)
+        if (b.type == type) return ne0 % b.elems ? 0 : (uint64_t)(ne0 / b.elems) * (uint64_t)b.bytes;
     return 0;
 }
 
-/* Sequential reader over a file with a 1 MiB window; any short read latches `bad`. */
-class Cursor {
-public:
-    Cursor(int fd, uint64_t size) : fd_(fd), size_(size), win_(1u << 20) {}
-
-    bool bad() const { return bad_; }
-    uint64_t tell() const { return base_ + at_; }
-
-    void bytes(void *dst, uint64_t n)
+/* A file mapped read-only for the duration of its header parse. */
+struct HeaderMap {
+    const uint8_t *p = nullptr;
+    uint64_t n = 0;
+    HeaderMap(int fd, uint64_t size)
     {
-        uint8_t *d = (uint8_t *)dst;
-        while (n > 0 && !bad_) {
-            if (at_ == len_ && !refill()) return;
-            const uint64_t k = len_ - at_ < n ? len_ - at_ : n;
-            if (d) {
-                memcpy(d, win_.data() + at_, (size_t)k);
-                d += k;
-            }
-            at_ += (size_t)k;
-            n -= k;
+        void *m = mmap(nullptr, (size_t)size, PROT_READ, MAP_PRIVATE, fd, 0);
+        if (m != MAP_FAILED) {
+            p = (const uint8_t *)m;
+            n = size;
         }
     }
-    void skip(uint64_t n) { bytes(nullptr, n); }
-    uint32_t u32() { uint32_t v = 0; bytes(&v, 4); return v; }
-    uint64_t u64() { uint64_t v = 0; bytes(&v, 8); return v; }
-
-    /* A GGUF string (u64 length + bytes); keeps at most cap-1 bytes, consumes all of it. */
-    std::string str(size_t cap)
+    ~HeaderMap()
     {
-        const uint64_t n = u64();
-        if (bad_ || n > (1ull << 32)) { bad_ = true; return std::string(); }
-        const uint64_t keep = n < cap - 1 ? n : cap - 1;
-        std::string s((size_t)keep, '\0');
-        bytes(&s[0], keep);
-        skip(n - keep);
-        return s;
+        if (p) munmap((void *)p, (size_t)n);
     }
-
-    /* Skip one value of type t (nested arrays included). */
-    void skip_value(uint32_t t)
-    {
-        if (t == V_STR) { (void)str(1); return; }
-        if (t == V_ARR) {
-            const uint32_t et = u32();
-            const uint64_t n = u64();
-            if (et > V_F64) { bad_ = true; return; }
-            if (et == V_STR || et == V_ARR) {
-                for (uint64_t k = 0; k < n && !bad_; k++) skip_value(et);
-                return;
-            }
-            skip(n * (uint64_t)kValueBytes[et]);
-            return;
-        }
-        if (t > V_F64) { bad_ = true; return; }
-        skip((uint64_t)kValueBytes[t]);
-    }
-
-private:
-    bool refill()
-    {
-        base_ += at_;
-        at_ = 0;
-        const uint64_t left = size_ > base_ ? size_ - base_ : 0;
-        len_ = left < win_.size() ? (size_t)left : win_.size();
-        if (len_ == 0 || pread_all(fd_, win_.data(), len_, base_) != 0) {
-            bad_ = true;
-            len_ = 0;
-            return false;
-        }
-        return true;
-    }
-
-    int fd_;
-    uint64_t size_, base_ = 0;
-    std::vector<uint8_t> win_;
-    size_t len_ = 0, at_ = 0;
-    bool bad_ = false;
+    HeaderMap(const HeaderMap &) = delete;
+    HeaderMap &operator=(const HeaderMap &) = delete;
 };
 
-uint64_t row_bytes_of(int type, int64_t ne0)
+/* Metadata section of one shard. Scalars go to g->meta when keep is set (first shard); the
+ * shard's own general.alignment is returned through align. */
+int read_metadata(FieldReader &rd, uint64_t n_kv, bool keep, qmsg_gguf *g, uint64_t *align, const char *path)
 {
-    switch (type) {
-    case QMSG_T_F32: return (uint64_t)ne0 * 4;
-    case QMSG_T_F16: return (uint64_t)ne0 * 2;
-    case QMSG_T_Q4_0: return ne0 % 32 ? 0 : (uint64_t)ne0 / 32 * 18;
-    case QMSG_T_Q4_1: return ne0 % 32 ? 0 : (uint64_t)ne0 / 32 * 20;
-    case QMSG_T_Q8_0: return ne0 % 32 ? 0 : (uint64_t)ne0 / 32 * 34;
-    case QMSG_T_Q6_K: return ne0 % 256 ? 0 : (uint64_t)ne0 / 256 * 210;
-    default: return 0;
+    for (uint64_t k = 0; k < n_kv && rd.ok(); k++) {
+        qmsg_gguf::Scalar s;
+        s.key = cut(rd.text(), kKeyKeep);
+        s.type = rd.field<uint32_t>();
+        const TypeInfo ti = type_info(s.type);
+        if (!rd.ok()) break;
+        switch (ti.kind) {
+        case Kind::Unsigned:
+        case Kind::Signed:
+        case Kind::Real: read_scalar(rd, ti, s); break;
+        case Kind::Text: s.text = cut(rd.text(), kTextKeep); break;
+        default: pass_value(rd, s.type, 0); break;       /* arrays (tokenizer tables) are not kept */
+        }
+        if (!rd.ok()) break;
+        if (s.key == "general.alignment") *align = g->unsigned_view(s);
+        if (keep && ti.kind != Kind::List) g->meta.push_back(std::move(s));
     }
+    if (!rd.ok()) return refuse("gguf %s: metadata is cut short or holds a value of unknown type", path);
+    return QMSG_OK;
 }
 
-/* One shard: header, metadata (kept for the first shard only), tensor table; offsets made
- * absolute against the aligned start of the data section. */
-int parse_shard(qmsg_gguf *g, int si)
+/* Tensor table of one shard, appended to g->tensors with offsets made absolute. */
+int read_tensors(FieldReader &rd, uint64_t n_tensors, int shard, uint64_t align, qmsg_gguf *g, const char *path)
 {
-    const char *path = g->paths[(size_t)si].c_str();
-    Cursor r(g->fds[(size_t)si], g->sizes[(size_t)si]);
-    char magic[4] = { 0 };
-    r.bytes(magic, 4);
-    if (r.bad() || memcmp(magic, "GGUF", 4) != 0) return fail_open("gguf: %s is not a GGUF file", path);
-    const uint32_t version = r.u32();
-    if (r.bad() || version != 3) return fail_open("gguf: %s version %u unsupported", path, version);
-    const uint64_t n_tensors = r.u64(), n_kv = r.u64();
-    uint64_t alignment = 32;
-    for (uint64_t k = 0; k < n_kv && !r.bad(); k++) {
-        qmsg_gguf::KV kv;
-        kv.key = r.str(kKeyCap);
-        const uint32_t t = r.u32();
-        kv.vtype = (int)t;
-        bool keep = si == 0;
-        switch (t) {
-        case V_U8: { uint8_t v = 0; r.bytes(&v, 1); kv.u = v; kv.i = v; kv.f = v; break; }
-        case V_I8: { int8_t v = 0; r.bytes(&v, 1); kv.i = v; kv.u = (uint64_t)v; kv.f = v; break; }
-        case V_U16: { uint16_t v = 0; r.bytes(&v, 2); kv.u = v; kv.i = v; kv.f = v; break; }
-        case V_I16: { int16_t v = 0; r.bytes(&v, 2); kv.i = v; kv.u = (uint64_t)v; kv.f = v; break; }
-        case V_U32: { uint32_t v = 0; r.bytes(&v, 4); kv.u = v; kv.i = v; kv.f = v; break; }
-        case V_I32: { int32_t v = 0; r.bytes(&v, 4); kv.i = v; kv.u = (uint64_t)v; kv.f = v; break; }
-        case V_F32: { float v = 0; r.bytes(&v, 4); kv.f = v; kv.i = (int64_t)v; break; }
-        case V_BOOL: { uint8_t v = 0; r.bytes(&v, 1); kv.u = v; kv.i = v; kv.f = v; break; }
-        case V_U64: { uint64_t v = 0; r.bytes(&v, 8); kv.u = v; kv.i = (int64_t)v; kv.f = (double)v; break; }
-        case V_I64: { int64_t v = 0; r.bytes(&v, 8); kv.i = v; kv.u = (uint64_t)v; kv.f = (double)v; break; }
-        case V_F64: { double v = 0; r.bytes(&v, 8); kv.f = v; kv.i = (int64_t)v; break; }
-        case V_STR: kv.str = r.str(kStrCap); break;
-        default: r.skip_value(t); keep = false; break;      /* arrays (tokenizer tables) */
-        }
-        if (kv.key == "general.alignment") alignment = kv.u;
-        if (keep && !r.bad()) g->kv.push_back(std::move(kv));
-    }
-    if (r.bad()) return fail_open("gguf: truncated metadata in %s", path);
-    if (alignment == 0) return fail_open("gguf: %s has general.alignment 0", path);
-
     const size_t first = g->tensors.size();
-    for (uint64_t k = 0; k < n_tensors && !r.bad(); k++) {
+    for (uint64_t k = 0; k < n_tensors; k++) {
         qmsg_tensor t;
         memset(&t, 0, sizeof t);
-        const std::string name = r.str(kNameCap);
+        const std::string name = cut(rd.text(), kNameKeep);
         memcpy(t.name, name.data(), name.size());
-        t.n_dims = (int)r.u32();
-        if (r.bad() || t.n_dims < 1 || t.n_dims > 4)
-            return fail_open("gguf: truncated tensor table in %s", path);
-        for (int d = 0; d < 4; d++) t.ne[d] = 1;
-        for (int d = 0; d < t.n_dims; d++) t.ne[d] = (int64_t)r.u64();
-        t.type = (int)r.u32();
-        t.off = r.u64();                                   /* relative to the data section */
-        t.shard = si;
+        const uint32_t dims = rd.field<uint32_t>();
+        if (!rd.ok() || dims < 1 || dims > 4)
+            return refuse("gguf %s: tensor table cut short or a tensor with %u dimensions (1 to 4 allowed)", path,
+                          dims);
+        t.n_dims = (int)dims;
+        for (int d = 0; d < 4; d++) t.ne[d] = d < t.n_dims ? (int64_t)rd.field<uint64_t>() : 1;
+        t.type = (int)rd.field<uint32_t>();
+        t.off = rd.field<uint64_t>();
+        t.shard = shard;
+        if (!rd.ok()) return refuse("gguf %s: tensor table cut short at entry %llu", path, (unsigned long long)k);
         g->tensors.push_back(t);
     }
-    if (r.bad()) return fail_open("gguf: truncated tensor table in %s", path);
-
-    const uint64_t data_start = (r.tell() + alignment - 1) / alignment * alignment;
+    if (align == 0) return refuse("gguf %s: general.alignment is 0", path);
+    uint64_t data = 0;
+    if (__builtin_add_overflow(rd.offset(), align - 1, &data))
+        return refuse("gguf %s: general.alignment %llu is too large", path, (unsigned long long)align);
+    data -= data % align;
+    const uint64_t fsize = g->shards[(size_t)shard].size;
     for (size_t k = first; k < g->tensors.size(); k++) {
         qmsg_tensor &t = g->tensors[k];
-        const uint64_t rb = row_bytes_of(t.type, t.ne[0]);
-        t.nbytes = rb * (uint64_t)(t.ne[1] * t.ne[2] * t.ne[3]);
-        t.off += data_start;
-        if (rb && t.off + t.nbytes > g->sizes[(size_t)si])
-            return fail_open("gguf: tensor %s runs past end of %s", t.name, path);
+        const uint64_t rb = bytes_per_row(t.type, t.ne[0]);
+        uint64_t rows = 1, nb = 0, end = 0;
+        bool bad = __builtin_add_overflow(t.off, data, &t.off);
+        if (rb) {
+            for (int d = 1; d < 4; d++)
+                bad = bad || t.ne[d] < 0 || __builtin_mul_overflow(rows, (uint64_t)t.ne[d], &rows);
+            bad = bad || __builtin_mul_overflow(rb, rows, &nb) || __builtin_add_overflow(t.off, nb, &end);
+            if (bad || end > fsize)
+                return refuse("gguf %s: tensor %s (%lld x %lld x %lld x %lld, type %d) does not fit in the file's "
+                              "%llu bytes", path, t.name, (long long)t.ne[0], (long long)t.ne[1], (long long)t.ne[2],
+                              (long long)t.ne[3], t.type, (unsigned long long)fsize);
+        } else if (bad) {
+            return refuse("gguf %s: tensor %s has an offset past 2^64", path, t.name);
+        }
+        t.nbytes = nb;
     }
     return QMSG_OK;
 }
 
-/* "<stem>-00001-of-0000N.gguf" names every shard of the set; any other path is one file. */
-int shard_paths(const char *path, std::vector<std::string> &out)
+int read_shard(qmsg_gguf *g, int shard)
 {
-    const size_t n = strlen(path), tl = strlen("-00001-of-00000.gguf");
-    if (n > tl && strncmp(path + n - tl, "-00001-of-", 10) == 0) {
-        const int count = atoi(path + n - tl + 10);
-        if (count < 1 || count > kMaxShards) return -1;
-        for (int i = 0; i < count; i++) {
-            char buf[32];
-            snprintf(buf, sizeof buf, "-%05d-of-%05d.gguf", i + 1, count);
-            out.push_back(std::string(path, n - tl) + buf);
+    const qmsg_gguf::Shard &sh = g->shards[(size_t)shard];
+    const char *path = sh.path.c_str();
+    HeaderMap map(sh.fd, sh.size);
+    if (!map.p) return refuse("gguf %s: cannot map the header (%s)", path, strerror(errno));
+    FieldReader rd(map.p, map.n);
+    const uint8_t *magic = rd.advance(4);
+    if (!magic || memcmp(magic, "GGUF", 4) != 0) return refuse("gguf %s: no GGUF magic at offset 0", path);
+    const uint32_t version = rd.field<uint32_t>();
+    if (!rd.ok() || version != 3) return refuse("gguf %s: format version %u, this reader takes version 3", path, version);
+    const uint64_t n_tensors = rd.field<uint64_t>(), n_kv = rd.field<uint64_t>();
+    uint64_t align = 32;
+    int rc = read_metadata(rd, n_kv, shard == 0, g, &align, path);
+    if (rc == QMSG_OK) rc = read_tensors(rd, n_tensors, shard, align, g, path);
+    return rc;
+}
+
+/* Files of a set: a path ending "-00001-of-NNNNN.gguf" (first shard of N) names N files with
+ * the index field counted up; any other path is a single file. */
+int expand_set(const std::string &path, std::vector<std::string> &files)
+{
+    constexpr size_t kTail = sizeof("-00001-of-00000.gguf") - 1;
+    auto digits = [](const char *s, int *v) {
+        *v = 0;
+        for (int i = 0; i < 5; i++) {
+            if (s[i] < '0' || s[i] > '9') return false;
+            *v = 10 * *v + (s[i] - '0');
         }
-    } else {
-        out.push_back(path);
+        return true;
+    };
+    const size_t n = path.size();
+    int first = 0, count = 0;
+    const char *tail = path.c_str() + (n > kTail ? n - kTail : 0);
+    const bool is_set = n > kTail && tail[0] == '-' && digits(tail + 1, &first) && first == 1 &&
+                        memcmp(tail + 6, "-of-", 4) == 0;
+    if (!is_set) {
+        files.push_back(path);
+        return QMSG_OK;
+    }
+    if (!digits(tail + 10, &count) || memcmp(tail + 15, ".gguf", 5) != 0 || count < 1 || count > kMaxShards)
+        return refuse("gguf %s: a shard set needs 1 to %d files", path.c_str(), kMaxShards);
+    const std::string stem = path.substr(0, n - kTail);
+    for (int i = 1; i <= count; i++) {
+        char idx[kTail + 1];
+        snprintf(idx, sizeof idx, "-%05d-of-%05d.gguf", i, count);
+        files.push_back(stem + idx);
+    }
+    return QMSG_OK;
+}
+
+int read_fully(int fd, void *dst, uint64_t n, uint64_t off)
+{
+    uint8_t *d = (uint8_t *)dst;
+    for (uint64_t done = 0; done < n;) {
+        const uint64_t ask = n - done < (1ull << 30) ? n - done : (1ull << 30);
+        const ssize_t got = ::pread(fd, d + done, (size_t)ask, (off_t)(off + done));
+        if (got > 0) done += (uint64_t)got;
+        else if (!(got < 0 && errno == EINTR)) return -1;
     }
     return 0;
 }
 
-const qmsg_gguf::KV *find_kv(const qmsg_gguf *g, const char *key)
+}  // namespace
+
+uint64_t qmsg_gguf::unsigned_view(const Scalar &s) const
 {
-    for (const auto &kv : g->kv)
-        if (kv.key == key) return &kv;
-    return nullptr;
+    const Kind k = type_info(s.type).kind;
+    return k == Kind::Unsigned || k == Kind::Signed ? s.bits : 0;
 }
 
-}  // namespace
+bool qmsg_gguf::numeric(const Scalar &s, int64_t *i, double *f) const
+{
+    /* the reference's three views (src/gguf.c:143-153): integers as themselves, reals truncated
+     * toward zero for the integer view (x86 conversion: INT64_MIN where the value has no int64) */
+    switch (type_info(s.type).kind) {
+    case Kind::Unsigned:
+        *i = (int64_t)s.bits;
+        *f = (double)s.bits;
+        return true;
+    case Kind::Signed:
+        *i = (int64_t)s.bits;
+        *f = (double)(int64_t)s.bits;
+        return true;
+    case Kind::Real:
+        *i = s.real >= -0x1p63 && s.real < 0x1p63 ? (int64_t)s.real : INT64_MIN;
+        *f = s.real;
+        return true;
+    default: return false;
+    }
+}
+
+const qmsg_gguf::Scalar *qmsg_gguf::scalar(const char *key) const
+{
+    for (const Scalar &s : meta)
+        if (s.key == key) return &s;
+    return nullptr;
+}
 
 namespace qmsg {
 
 int gguf_pread(const qmsg_gguf *g, int shard, uint64_t off, uint64_t n, void *dst)
 {
-    if (shard < 0 || shard >= (int)g->fds.size()) return -1;
-    return pread_all(g->fds[(size_t)shard], dst, n, off);
+    if (shard < 0 || shard >= (int)g->shards.size()) return -1;
+    return read_fully(g->shards[(size_t)shard].fd, dst, n, off);
 }
 
 int gguf_find(const qmsg_gguf *g, const char *name)
@@ -259,36 +383,34 @@ extern "C" {
 void qmsg_gguf_close(qmsg_gguf *g)
 {
     if (!g) return;
-    for (int fd : g->fds)
-        if (fd >= 0) ::close(fd);
+    for (const qmsg_gguf::Shard &s : g->shards)
+        if (s.fd >= 0) ::close(s.fd);
     delete g;
 }
 
 int qmsg_gguf_open(qmsg_gguf **out, const char *path)
 {
-    if (!out || !path) return fail_open("qmsg_gguf_open: null argument");
+    if (!out || !path) return refuse("qmsg_gguf_open: out and path must not be NULL");
     *out = nullptr;
+    std::vector<std::string> files;
+    int rc = expand_set(path, files);
+    if (rc) return rc;
     qmsg_gguf *g = new qmsg_gguf;
-    if (shard_paths(path, g->paths) != 0) {
-        delete g;
-        return fail_open("gguf: bad shard name %s", path);
-    }
-    for (size_t i = 0; i < g->paths.size(); i++) {
-        const int fd = ::open(g->paths[i].c_str(), O_RDONLY | O_CLOEXEC);
+    for (size_t i = 0; i < files.size() && rc == QMSG_OK; i++) {
+        qmsg_gguf::Shard s;
+        s.path = files[i];
+        s.fd = ::open(s.path.c_str(), O_RDONLY | O_CLOEXEC);
         struct stat st;
-        if (fd < 0 || fstat(fd, &st) != 0 || st.st_size <= 0) {
-            if (fd >= 0) ::close(fd);
-            const int rc = fail_open("gguf: cannot open %s", g->paths[i].c_str());
-            qmsg_gguf_close(g);
-            return rc;
-        }
-        g->fds.push_back(fd);
-        g->sizes.push_back((uint64_t)st.st_size);
-        const int rc = parse_shard(g, (int)i);
-        if (rc != QMSG_OK) {
-            qmsg_gguf_close(g);
-            return rc;
-        }
+        const bool usable = s.fd >= 0 && fstat(s.fd, &st) == 0 && S_ISREG(st.st_mode) && st.st_size > 0;
+        if (usable) s.size = (uint64_t)st.st_size;
+        g->shards.push_back(s);
+        rc = usable ? read_shard(g, (int)i)
+                    : refuse("gguf %s: not a readable, non-empty regular file (%s)", s.path.c_str(),
+                             s.fd < 0 ? strerror(errno) : "empty or special");
+    }
+    if (rc != QMSG_OK) {
+        qmsg_gguf_close(g);
+        return rc;
     }
     *out = g;
     return QMSG_OK;
@@ -312,59 +434,62 @@ int qmsg_gguf_find(const qmsg_gguf *g, const char *name)
 int qmsg_gguf_get_int(const qmsg_gguf *g, const char *key, int64_t *out)
 {
     if (!g || !key || !out) return QMSG_E_INVALID;
-    const qmsg_gguf::KV *kv = find_kv(g, key);
-    if (!kv || kv->vtype == V_STR) return fail_open("gguf: missing required key %s", key);
-    *out = kv->i;
+    const qmsg_gguf::Scalar *s = g->scalar(key);
+    double f;
+    if (!s || !g->numeric(*s, out, &f)) return refuse("gguf: no numeric scalar %s in the metadata", key);
     return QMSG_OK;
 }
 
 int qmsg_gguf_get_float(const qmsg_gguf *g, const char *key, double *out)
 {
     if (!g || !key || !out) return QMSG_E_INVALID;
-    const qmsg_gguf::KV *kv = find_kv(g, key);
-    if (!kv || kv->vtype == V_STR) return fail_open("gguf: missing required key %s", key);
-    *out = kv->f;
+    const qmsg_gguf::Scalar *s = g->scalar(key);
+    int64_t i;
+    if (!s || !g->numeric(*s, &i, out)) return refuse("gguf: no numeric scalar %s in the metadata", key);
     return QMSG_OK;
 }
 
 int qmsg_gguf_get_str(const qmsg_gguf *g, const char *key, char *buf, size_t n)
 {
     if (!g || !key || !buf || n == 0) return QMSG_E_INVALID;
-    const qmsg_gguf::KV *kv = find_kv(g, key);
-    if (!kv || kv->vtype != V_STR) return fail_open("gguf: missing string key %s", key);
-    const size_t k = kv->str.size() < n - 1 ? kv->str.size() : n - 1;
-    memcpy(buf, kv->str.data(), k);
+    const qmsg_gguf::Scalar *s = g->scalar(key);
+    if (!s || s->type != kTypeStr) return refuse("gguf: no string scalar %s in the metadata", key);
+    const size_t k = s->text.size() < n - 1 ? s->text.size() : n - 1;
+    memcpy(buf, s->text.data(), k);
     buf[k] = '\0';
     return QMSG_OK;
 }
 
 int qmsg_gguf_moe_cfg(const qmsg_gguf *g, qmsg_cfg *cfg, int *n_layer, float *eps)
 {
+    /* the keys the reference's read_cfg takes for the expert layers (src/model.c:275-300) */
     if (!g) return QMSG_E_INVALID;
-    const qmsg_gguf::KV *arch = find_kv(g, "general.architecture");
-    if (!arch || arch->vtype != V_STR || arch->str != "qwen3moe")
-        return fail_open("model: architecture %s is not qwen3moe",
-                         arch && arch->vtype == V_STR ? arch->str.c_str() : "(missing)");
-    struct { const char *key; int64_t v; } k[5] = {
-        { "qwen3moe.block_count", 0 }, { "qwen3moe.embedding_length", 0 }, { "qwen3moe.expert_count", 0 },
-        { "qwen3moe.expert_used_count", 0 }, { "qwen3moe.expert_feed_forward_length", 0 },
-    };
-    for (auto &e : k) {
-        const int rc = qmsg_gguf_get_int(g, e.key, &e.v);
+    const qmsg_gguf::Scalar *arch = g->scalar("general.architecture");
+    if (!arch || arch->type != kTypeStr || arch->text != "qwen3moe")
+        return refuse("qmsg_gguf_moe_cfg: general.architecture is %s%s%s, not qwen3moe", arch ? "\"" : "",
+                      arch ? arch->text.c_str() : "absent", arch ? "\"" : "");
+    const char *names[5] = { "qwen3moe.block_count", "qwen3moe.embedding_length", "qwen3moe.expert_count",
+                             "qwen3moe.expert_used_count", "qwen3moe.expert_feed_forward_length" };
+    int64_t v[5];
+    for (int k = 0; k < 5; k++) {
+        const int rc = qmsg_gguf_get_int(g, names[k], &v[k]);
         if (rc) return rc;
-        if (e.v <= 0 || e.v > (1 << 30)) return fail_open("model: %s = %lld is out of range", e.key, (long long)e.v);
+        if (v[k] <= 0 || v[k] > (1 << 30))
+            return refuse("qmsg_gguf_moe_cfg: %s = %lld is outside 1 .. 2^30", names[k], (long long)v[k]);
     }
     double f = 0.0;
     const int rc = qmsg_gguf_get_float(g, "qwen3moe.attention.layer_norm_rms_epsilon", &f);
     if (rc) return rc;
-    if (k[3].v > k[2].v) return fail_open("model: inconsistent config (expert_used_count > expert_count)");
+    if (v[3] > v[2])
+        return refuse("qmsg_gguf_moe_cfg: expert_used_count %lld exceeds expert_count %lld", (long long)v[3],
+                      (long long)v[2]);
     if (cfg) {
-        cfg->n_embd = (int)k[1].v;
-        cfg->n_expert = (int)k[2].v;
-        cfg->n_used = (int)k[3].v;
-        cfg->n_ff_exp = (int)k[4].v;
+        cfg->n_embd = (int)v[1];
+        cfg->n_expert = (int)v[2];
+        cfg->n_used = (int)v[3];
+        cfg->n_ff_exp = (int)v[4];
     }
-    if (n_layer) *n_layer = (int)k[0].v;
+    if (n_layer) *n_layer = (int)v[0];
     if (eps) *eps = (float)f;
     return QMSG_OK;
 }

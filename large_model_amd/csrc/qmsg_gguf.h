@@ -10,20 +10,29 @@
 #include "../../include/qmsg.h"
 
 struct qmsg_gguf {
-    /* one scalar of the first shard's metadata; every numeric view filled as it is read */
-    struct KV {
-        std::string key;   /* at most 95 bytes, like QmsKV.key */
-        int vtype = 0;
-        uint64_t u = 0;
-        int64_t i = 0;
-        double f = 0.0;
-        std::string str;   /* string values, at most 255 bytes */
+    /* one open file of the set */
+    struct Shard {
+        std::string path;
+        int fd = -1;
+        uint64_t size = 0;
     };
-    std::vector<std::string> paths;
-    std::vector<int> fds;
-    std::vector<uint64_t> sizes;
+    /* one scalar of the first shard's metadata: its GGUF value type and payload */
+    struct Scalar {
+        std::string key;       /* cut to 95 bytes */
+        uint32_t type = 0;
+        uint64_t bits = 0;     /* integers and bool; signed types sign-extended */
+        double real = 0.0;     /* f32 / f64 */
+        std::string text;      /* strings, cut to 255 bytes */
+    };
+    std::vector<Shard> shards;
     std::vector<qmsg_tensor> tensors;
-    std::vector<KV> kv;
+    std::vector<Scalar> meta;
+
+    const Scalar *scalar(const char *key) const;
+    /* integer and real views of a numeric scalar; false for strings */
+    bool numeric(const Scalar &s, int64_t *i, double *f) const;
+    /* the unsigned view (general.alignment): integer bits, 0 for reals and strings */
+    uint64_t unsigned_view(const Scalar &s) const;
 };
 
 namespace qmsg {

@@ -148,6 +148,44 @@ def test_bad_files_are_refused(q, tmp_path):
             assert ref_table(path) is None, name
 
 
+def _nested(depth):
+    """An array value nested `depth` levels deep around one i8 array."""
+    v = (gf.I8, [1, 2])
+    for _ in range(depth - 1):
+        v = (gf.ARR, [v])
+    return v
+
+
+def test_hostile_sizes_are_refused(q, tmp_path):
+    """Sizes from the file that wrap 64-bit arithmetic or recurse without end are refused (the
+    reader's own checks: the reference multiplies the tensor extent unchecked)."""
+    cases = {
+        "extent wraps": [("t", gf.T_F32, [2 ** 33, 2 ** 33], bytes(16))],
+        "negative dim": [("t", gf.T_F32, [4, 2 ** 63 + 1], bytes(16))],
+        "rows wrap": [("t", gf.T_Q4_0, [32, 2 ** 62, 4, 2], bytes(18))],
+    }
+    for name, ts in cases.items():
+        p = str(tmp_path / (name.replace(" ", "_") + ".gguf"))
+        gf.write_gguf(p, [], ts)
+        with pytest.raises(q.QmsgError, match="does not fit") as ei:
+            q.Gguf(p)
+        assert ei.value.status == -1, name
+    p = str(tmp_path / "deep.gguf")
+    gf.write_gguf(p, [("deep", gf.ARR, _nested(20))], [("t", gf.T_F32, [4], bytes(16))])
+    with pytest.raises(q.QmsgError, match="metadata"):
+        q.Gguf(p)
+    p = str(tmp_path / "shallow.gguf")
+    gf.write_gguf(p, [("deep", gf.ARR, _nested(8)), ("k", gf.U8, 3)], [("t", gf.T_F32, [4], bytes(16))])
+    with q.Gguf(p) as g:
+        assert g.get_int("k") == 3
+    p = str(tmp_path / "count_wraps.gguf")
+    with open(p, "wb") as f:     # one metadata entry "a": an u32 array of 2^62 + 1 elements
+        f.write(b"GGUF" + struct.pack("<IQQ", 3, 0, 1) + struct.pack("<Q", 1) + b"a" +
+                struct.pack("<IIQ", gf.ARR, gf.U32, 2 ** 62 + 1) + bytes(16))
+    with pytest.raises(q.QmsgError, match="metadata"):
+        q.Gguf(p)
+
+
 def test_moe_cfg(q, tmp_path):
     lays = small_layers()
     path, _ = gf.moe_model(str(tmp_path / "m.gguf"), lays, eps=1e-5)
@@ -162,7 +200,7 @@ def test_moe_cfg(q, tmp_path):
     p = str(tmp_path / "nokey.gguf")
     gf.write_gguf(p, [("general.architecture", gf.STR, "qwen3moe"), ("qwen3moe.block_count", gf.U32, 2)],
                   [("t", gf.T_F32, [4], bytes(16))])
-    with q.Gguf(p) as g, pytest.raises(q.QmsgError, match="missing required key"):
+    with q.Gguf(p) as g, pytest.raises(q.QmsgError, match="no numeric scalar"):
         g.moe_cfg()
 
 

@@ -126,6 +126,9 @@ def test_dense_from_gguf_and_errors(q, tmp_path):
         with pytest.raises(q.QmsgError) as ei:
             ctx.mat_synth(orc.T_Q6_K, 4, 1024, 1)                              # Q6_K: cols % 2048
         assert ei.value.status == -2
+        with pytest.raises(q.QmsgError, match="2\\^30") as ei:
+            ctx.mat_synth(orc.T_Q4_0, 1, 2 ** 31, 1)                           # cols beyond 2^30
+        assert ei.value.status == -2
 
 
 @pytest.mark.parametrize("T", [1, 2, 3, 4, 5, 9])
