@@ -49,6 +49,8 @@ def _load_oracle():
     L.orc_vec_dot_f32.argtypes = [_P, _P, ctypes.c_int64]
     L.orc_block_dot.restype = ctypes.c_int32
     L.orc_block_dot.argtypes = [ctypes.c_int, _P, _P, ctypes.c_int64]
+    L.orc_block_dots_at.argtypes = [ctypes.c_int, _P, ctypes.c_uint64, ctypes.c_uint64, ctypes.c_int64, _P, _P, _P, _P,
+                                    _P, _P]
     L.orc_matmul_q8.argtypes = [ctypes.c_int, _P, ctypes.c_int64, ctypes.c_int64, ctypes.c_uint64, _P, ctypes.c_int, _P]
     L.orc_dequant_row.argtypes = [ctypes.c_int, _P, _P, ctypes.c_int64]
     L.orc_silu.restype = ctypes.c_float
@@ -117,6 +119,19 @@ def matmul_q8(t: int, w: np.ndarray, rows: int, cols: int, x: np.ndarray) -> np.
 
 def block_dot(t: int, w_row: np.ndarray, xq: np.ndarray, blk: int) -> int:
     return int(lib.orc_block_dot(t, _ptr(np.ascontiguousarray(w_row, np.uint8)), _ptr(xq), blk))
+
+
+def block_dots_at(t: int, w: np.ndarray, rb: int, eb: int, ex, row, blk, xq: np.ndarray, xrow) -> np.ndarray:
+    """block_dot of stacked expert tensor w at each (expert, row, block) against Q8 row xrow of
+    xq (xrow counts Q8 blocks from the start of xq)."""
+    ex, row, blk = (np.ascontiguousarray(v, np.int32) for v in (ex, row, blk))
+    xrow = np.ascontiguousarray(xrow, np.int64)
+    xq = np.ascontiguousarray(xq).reshape(-1)
+    assert xq.dtype == Q8_DTYPE and ex.shape == row.shape == blk.shape == xrow.shape
+    out = np.empty(ex.shape[0], np.int32)
+    lib.orc_block_dots_at(t, _ptr(w), rb, eb, ex.shape[0], _ptr(ex), _ptr(row), _ptr(blk), _ptr(xq), _ptr(xrow),
+                          _ptr(out))
+    return out
 
 
 def dequant_row(t: int, w: np.ndarray, n: int) -> np.ndarray:

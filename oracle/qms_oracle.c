@@ -273,6 +273,17 @@ int32_t orc_block_dot(int type, const uint8_t *w, const orc_q8 *x, int64_t blk)
     return 0;
 }
 
+/* orc_block_dot over n (expert, row, block) triples of one stacked expert tensor, each against
+ * the Q8 row starting at block xrow[i] of x (test driver of the row above, no reference code). */
+void orc_block_dots_at(int type, const uint8_t *w, uint64_t row_bytes, uint64_t expert_bytes, int64_t n,
+                       const int32_t *ex, const int32_t *row, const int32_t *blk, const orc_q8 *x,
+                       const int64_t *xrow, int32_t *out)
+{
+    for (int64_t i = 0; i < n; i++)
+        out[i] = orc_block_dot(type, w + (uint64_t)ex[i] * expert_bytes + (uint64_t)row[i] * row_bytes,
+                               x + xrow[i], blk[i]);
+}
+
 /* src/model.c:424 (glibc expf). */
 float orc_silu(float a) { return a / (1.0f + expf(-a)); }
 

@@ -77,6 +77,9 @@ int orc_matmul_q8(int type, const uint8_t *w, int64_t rows, int64_t cols, uint64
                   float *y);
 float orc_vec_dot_f32(const float *w, const float *x, int64_t n);
 int32_t orc_block_dot(int type, const uint8_t *w_row, const orc_q8 *x, int64_t blk);
+void orc_block_dots_at(int type, const uint8_t *w, uint64_t row_bytes, uint64_t expert_bytes, int64_t n,
+                       const int32_t *ex, const int32_t *row, const int32_t *blk, const orc_q8 *x,
+                       const int64_t *xrow, int32_t *out);
 float orc_silu(float a);
 int orc_fast_supported(int type);
 
