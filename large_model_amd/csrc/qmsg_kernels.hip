@@ -2145,6 +2145,10 @@ struct MxB {
     uint32_t sab;     /* Q6_K: both sub-scales as int16 pair (sc[2g] low) */
 };
 
+typedef __attribute__((address_space(3))) const uint8_t *LdsPtr;
+typedef __attribute__((address_space(3))) const u32x2 LdsU32x2;
+typedef __attribute__((address_space(3))) const u32x4 LdsU32x4;
+
 /* The word at base + O + a (base 4-byte aligned, a a multiple of 4): one aligned read for
  * O == 0, two and a byte alignment for O == 2. */
 template <int O>
@@ -2189,6 +2193,32 @@ __device__ __forceinline__ MxB mx_weights(const uint8_t *row, int b, int lg, int
     return w;
 }
 
+/* The same for Q4_0 / Q4_1 from two per-block LDS pointers: pq at the lane's code word of the
+ * block in tile row lr (Q4_0 even blocks: 2 bytes past a word boundary), pd at the block's
+ * scale word; tile t is an immediate offset. */
+template <int TYPE, int PAR>
+__device__ __forceinline__ MxB mx_weights_q4(LdsPtr pq, LdsPtr pd, int t)
+{
+    constexpr int WS = mx_wstride(TYPE);
+    const uint32_t m4 = 0x000f000fu, bias = 0x64006400u;
+    MxB w;
+    uint32_t v;
+    if constexpr (TYPE == 3 || PAR) {
+        v = *(const __attribute__((address_space(3))) uint32_t *)(pq + 16 * t * WS);
+    } else {
+        const uint32_t a0 = *(const __attribute__((address_space(3))) uint32_t *)(pq + 16 * t * WS - 2);
+        const uint32_t a1 = *(const __attribute__((address_space(3))) uint32_t *)(pq + 16 * t * WS + 2);
+        v = __builtin_amdgcn_alignbyte(a1, a0, 2);
+    }
+    w.op = mx_pack_codes(and_or(v, m4, bias), and_or(v >> 8, m4, bias), and_or(v >> 4, m4, bias),
+                         and_or(v >> 12, m4, bias));
+    if constexpr (TYPE == 3) w.dw = *(const __attribute__((address_space(3))) uint32_t *)(pd + 16 * t * WS);
+    else w.dw = *(const __attribute__((address_space(3))) uint16_t *)(pd + 16 * t * WS);
+    w.sc = 0.0f;
+    w.sab = 0u;
+    return w;
+}
+
 /* fl(h * f) for the f16 in the low half of h (v_fma_mix, one rounding; the added zero cannot
  * change a non-zero product). */
 __device__ __forceinline__ float mix_mul(uint32_t h, float f)
@@ -2216,24 +2246,47 @@ __device__ __forceinline__ float mix_fma_hi(uint32_t h, float f, float c)
 
 /* One block b (parity PAR) of the staged chunk: NP slot pairs of this wave against its two
  * 16-row tiles. */
+/* A lane's LDS read streams over a staged chunk, each one register: A low and high words and
+ * the slot's d/ds words (at the trip's first block; the pair p adds 2p record strides), and for
+ * Q4_0 / Q4_1 the code word and the scale word of tile row lr (the tile t adds 16t rows). One
+ * trip covers two blocks; the second block and the pairs and tiles are immediate offsets. */
+struct MxStreams {
+    LdsPtr alo, ahi, d, q, dw;
+};
+
+/* The empty asm keeps each stream a single register: otherwise every (pair, stream) address
+ * becomes a loop variable of its own and the registers run out. */
+__device__ __forceinline__ void mx_opaque(MxStreams &st)
+{
+    asm("" : "+v"(st.alo), "+v"(st.ahi), "+v"(st.d), "+v"(st.q), "+v"(st.dw));
+}
+
+/* One block b (parity PAR within the trip) of the staged chunk: NP slot pairs of this wave
+ * against its two 16-row tiles. */
 template <int TYPE, int NP, int O, int PAR>
-__device__ __forceinline__ void mx_block(int b, const uint8_t *W, const uint8_t *R, int lr, int lg, int kh, int jd,
-                                         int offa_lo, int offa_hi, f32x4 (&acc)[2][4], float (&cr)[2][4])
+__device__ __forceinline__ void mx_block(int b, const MxStreams &st, const uint8_t *W, int lr, int lg, int kh,
+                                         f32x4 (&acc)[2][4], float (&cr)[2][4])
 {
     constexpr int WS = mx_wstride(TYPE);
     MxB w[2];
+    if constexpr (TYPE == 14) {
 #pragma unroll
-    for (int t = 0; t < 2; t++) w[t] = mx_weights<TYPE, O, PAR>(W + (16 * t + lr) * WS, b, lg, kh);
+        for (int t = 0; t < 2; t++) w[t] = mx_weights<TYPE, O, PAR>(W + (16 * t + lr) * WS, b, lg, kh);
+    } else {
+        constexpr int BB = TYPE == 3 ? 20 : 18;
+#pragma unroll
+        for (int t = 0; t < 2; t++) w[t] = mx_weights_q4<TYPE, PAR>(st.q + PAR * BB, st.dw + PAR * BB, t);
+    }
 #pragma unroll
     for (int p = 0; p < NP; p++) {
-        const uint8_t *rp = R + (2 * p) * kMxRStride + b * kMxRec;
-        const u32x2 lo = *(const u32x2 *)(rp + offa_lo), hi = *(const u32x2 *)(rp + offa_hi);
+        constexpr int RB = PAR * kMxRec;
+        const u32x2 lo = *(const LdsU32x2 *)(st.alo + RB + 2 * p * kMxRStride);
+        const u32x2 hi = *(const LdsU32x2 *)(st.ahi + RB + 2 * p * kMxRStride);
         const f16x8 aop = __builtin_bit_cast(f16x8, u32x4{ lo.x, lo.y, hi.x, hi.y });
-        const uint8_t *rd = rp + jd * kMxRStride;
         u32x4 dx;
-        if constexpr (TYPE == 14) dx = *(const u32x4 *)(rd + 96);        /* d, ds, s16 pair, 0 */
+        if constexpr (TYPE == 14) dx = *(const LdsU32x4 *)(st.d + RB + 2 * p * kMxRStride);   /* d, ds, s16 pair, 0 */
         else {
-            const u32x2 d2 = *(const u32x2 *)(rd + 96);                   /* d, ds */
+            const u32x2 d2 = *(const LdsU32x2 *)(st.d + RB + 2 * p * kMxRStride);            /* d, ds */
             dx = u32x4{ d2.x, d2.y, 0u, 0u };
         }
         const float xd = __uint_as_float(dx.x), xds = __uint_as_float(dx.y);
@@ -2266,10 +2319,24 @@ template <int TYPE, int NP, int O>
 __device__ __forceinline__ void mx_chunk(const uint8_t *W, const uint8_t *R, int lr, int lg, int kh, int jd,
                                          int offa_lo, int offa_hi, f32x4 (&acc)[2][4], float (&cr)[2][4])
 {
+    constexpr int WS = mx_wstride(TYPE), BB = TYPE == 3 ? 20 : 18, QO = TYPE == 3 ? 4 : 2;
+    MxStreams st;
+    st.alo = (LdsPtr)(R + offa_lo);
+    st.ahi = (LdsPtr)(R + offa_hi);
+    st.d = (LdsPtr)(R + jd * kMxRStride + 96);
+    st.q = (LdsPtr)(W + lr * WS + QO + 4 * lg);
+    st.dw = (LdsPtr)(W + lr * WS);
 #pragma unroll 1
     for (int b = 0; b < kMxC; b += 2) {
-        mx_block<TYPE, NP, O, 0>(b, W, R, lr, lg, kh, jd, offa_lo, offa_hi, acc, cr);
-        mx_block<TYPE, NP, O, 1>(b + 1, W, R, lr, lg, kh, jd, offa_lo, offa_hi, acc, cr);
+        mx_opaque(st);
+        mx_block<TYPE, NP, O, 0>(b, st, W, lr, lg, kh, acc, cr);
+        __builtin_amdgcn_sched_barrier(0);      /* one block's operands in registers at a time */
+        mx_block<TYPE, NP, O, 1>(b + 1, st, W, lr, lg, kh, acc, cr);
+        st.alo += 2 * kMxRec;
+        st.ahi += 2 * kMxRec;
+        st.d += 2 * kMxRec;
+        st.q += 2 * BB;
+        st.dw += 2 * BB;
     }
 }
 
