@@ -2340,16 +2340,6 @@ __device__ __forceinline__ void mx_chunk(const uint8_t *W, const uint8_t *R, int
     }
 }
 
-template <int TYPE, int O>
-__device__ __forceinline__ void mx_chunk_np(int np, const uint8_t *W, const uint8_t *R, int lr, int lg, int kh, int jd,
-                                            int offa_lo, int offa_hi, f32x4 (&acc)[2][4], float (&cr)[2][4])
-{
-    if (np == 4) mx_chunk<TYPE, 4, O>(W, R, lr, lg, kh, jd, offa_lo, offa_hi, acc, cr);
-    else if (np == 3) mx_chunk<TYPE, 3, O>(W, R, lr, lg, kh, jd, offa_lo, offa_hi, acc, cr);
-    else if (np == 2) mx_chunk<TYPE, 2, O>(W, R, lr, lg, kh, jd, offa_lo, offa_hi, acc, cr);
-    else if (np == 1) mx_chunk<TYPE, 1, O>(W, R, lr, lg, kh, jd, offa_lo, offa_hi, acc, cr);
-}
-
 /* The LDS DMA: `bytes` (4 or 16) from src of every active lane to dst + lane * bytes. */
 template <int BYTES>
 __device__ __forceinline__ void dma_to_lds(const void *src, uint8_t *dst)
@@ -2438,49 +2428,60 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4, 4))) voi
     const int offa_hi = ja * kMxRStride + ((nz && ka >= 4) ? 8 * ka : kMxZero);
     const int nw = min(max(ns - 8 * ws, 0), 8), np = (nw + 1) >> 1;      /* this wave's slot pairs */
 
-    f32x4 acc[2][4];
-    float cr[2][4];
-#pragma unroll
-    for (int t = 0; t < 2; t++)
-#pragma unroll
-        for (int p = 0; p < 4; p++) {
-            acc[t][p] = f32x4{ 0.0f, 0.0f, 0.0f, 0.0f };
-            cr[t][p] = 0.0f;
-        }
-
-    issue(0, 0);
-    mx_wait_barrier();
-    for (int c = 0; c < nch; c++) {
-        const int buf = c & 1;
-        if (c + 1 < nch) issue(c + 1, buf ^ 1);
-        const uint8_t *Wl = smem + buf * BUF + (32 * wr) * WS;
-        const uint8_t *Rl = smem + buf * BUF + Lay::WBYTES + (8 * ws) * kMxRStride;
-        if (TYPE == 14 && (c & 1))
-            mx_chunk_np<TYPE, 2>(np, Wl, Rl, lr, lg, kh, jd, offa_lo, offa_hi, acc, cr);
-        else
-            mx_chunk_np<TYPE, 0>(np, Wl, Rl, lr, lg, kh, jd, offa_lo, offa_hi, acc, cr);
-        mx_wait_barrier();           /* chunk c+1 has landed; buffer c is free for chunk c+2 */
-    }
-
-    /* hsum256 per (row, slot): lanes of k-half 0 take the partner lane's k + 4 chains */
+    /* The whole chunk loop and the row sums for one slot-pair count NP, chosen once per wave,
+     * so the accumulators keep their registers from the first chunk to the last. Every wave
+     * issues its share of the DMA and meets every barrier, whatever its NP (0 included). */
     constexpr float scale = finish_scale(TYPE);
-    float *res = (float *)smem;                                   /* [RWG][SWG + 1] */
+    float *res = (float *)smem;                                   /* [RWG][SWG + 1], after the loop */
+    auto run = [&](auto npc) {
+        constexpr int NP = decltype(npc)::value;
+        f32x4 acc[2][4];
+        float cr[2][4];
 #pragma unroll
-    for (int t = 0; t < 2; t++)
+        for (int t = 0; t < 2; t++)
 #pragma unroll
-        for (int p = 0; p < 4; p++) {
-            f32x4 o;
-#pragma unroll
-            for (int v = 0; v < 4; v++) o[v] = __shfl_xor(acc[t][p][v], 16);
-            if (p < np && kh == 0) {
-                const f32x4 &q = acc[t][p];
-                const float h = ((q[0] + o[0]) + (q[2] + o[2])) + ((q[1] + o[1]) + (q[3] + o[3]));
-                const float val = h - scale * cr[t][p];
-                const int row = 32 * wr + 16 * t + lr, sl = 8 * ws + 2 * p + jd;
-                if (GU) res[row * (SWG + 1) + sl] = val;
-                else if (sl < ns) a.S.dn[(size_t)(s0 + sl) * a.E + R0 + row] = val;
+            for (int p = 0; p < 4; p++) {
+                acc[t][p] = f32x4{ 0.0f, 0.0f, 0.0f, 0.0f };
+                cr[t][p] = 0.0f;
             }
+        issue(0, 0);
+        mx_wait_barrier();
+        for (int c = 0; c < nch; c++) {
+            const int buf = c & 1;
+            if (c + 1 < nch) issue(c + 1, buf ^ 1);
+            if constexpr (NP > 0) {
+                const uint8_t *Wl = smem + buf * BUF + (32 * wr) * WS;
+                const uint8_t *Rl = smem + buf * BUF + Lay::WBYTES + (8 * ws) * kMxRStride;
+                if (TYPE == 14 && (c & 1))
+                    mx_chunk<TYPE, NP, 2>(Wl, Rl, lr, lg, kh, jd, offa_lo, offa_hi, acc, cr);
+                else
+                    mx_chunk<TYPE, NP, 0>(Wl, Rl, lr, lg, kh, jd, offa_lo, offa_hi, acc, cr);
+            }
+            mx_wait_barrier();       /* chunk c+1 has landed; buffer c is free for chunk c+2 */
         }
+        /* hsum256 per (row, slot): lanes of k-half 0 take the partner lane's k + 4 chains */
+#pragma unroll
+        for (int t = 0; t < 2; t++)
+#pragma unroll
+            for (int p = 0; p < NP; p++) {
+                f32x4 o;
+#pragma unroll
+                for (int v = 0; v < 4; v++) o[v] = __shfl_xor(acc[t][p][v], 16);
+                if (kh == 0) {
+                    const f32x4 &q = acc[t][p];
+                    const float h = ((q[0] + o[0]) + (q[2] + o[2])) + ((q[1] + o[1]) + (q[3] + o[3]));
+                    const float val = h - scale * cr[t][p];
+                    const int row = 32 * wr + 16 * t + lr, sl = 8 * ws + 2 * p + jd;
+                    if (GU) res[row * (SWG + 1) + sl] = val;
+                    else if (sl < ns) a.S.dn[(size_t)(s0 + sl) * a.E + R0 + row] = val;
+                }
+            }
+    };
+    if (np == 4) run(std::integral_constant<int, 4>{});
+    else if (np == 3) run(std::integral_constant<int, 3>{});
+    else if (np == 2) run(std::integral_constant<int, 2>{});
+    else if (np == 1) run(std::integral_constant<int, 1>{});
+    else run(std::integral_constant<int, 0>{});
     if (!GU) return;
     __syncthreads();
     /* a = silu(g) * u (src/model.c:989-994) into the gate rows of res, then the int8 blocks of
