@@ -793,19 +793,22 @@ static int run_layer_s(qmsg_ctx *c, const Scratch &S, int layer, const float *d_
      * or, for batches with several slots per expert, the MFMA kernels; other types take the
      * slot-tile row kernel */
     const bool q40 = d.gate_type == QMSG_T_Q4_0 && d.up_type == QMSG_T_Q4_0;
-    const bool mx_ok = q40 && !use_small_route(T, s.K) && mx_supported(s, d, nullptr);
-    const bool mfma = mx_ok && (c->path == QMSG_PATH_MFMA || (c->path == QMSG_PATH_AUTO && mx_auto(T, s.K, s.X)));
+    int dn_ok = 0;
+    const bool many = !use_small_route(T, s.K);
+    const bool gu_ok = mx_supported(s, d, &dn_ok) && q40 && many;
+    const bool forced = c->path == QMSG_PATH_MFMA, autop = c->path == QMSG_PATH_AUTO;
+    const bool gu_mx = gu_ok && (forced || (autop && mx_auto(T, s.K, s.X)));
+    const bool dn_mx = dn_ok && many && (forced || (autop && mx_auto_down(T, s.K, s.X)));
     LAUNCH(c, "route", launch_route(s, d, S, d_xn, T, c->stream));
     LAUNCH(c, "select", launch_select(s, S, T, q40 ? 1 : 0, c->stream));
-    if (mfma) {
+    if (gu_mx) {
         LAUNCH(c, "experts", launch_experts_mx(s, d, S, d_out, T, debug, c->stream));
-    } else if (!q40) {
-        LAUNCH(c, "gateup", launch_gateup_tiles(s, d, S, T, c->stream));
-        LAUNCH(c, "down", launch_down_exact(s, d, S, d_out, T, 1, c->stream));
-    } else {
-        LAUNCH(c, "gateup", launch_gateup_exact(s, d, S, T, debug, c->n_cu, c->stream));
-        LAUNCH(c, "down", launch_down_exact(s, d, S, d_out, T, 1, c->stream));
+        return QMSG_OK;
     }
+    if (!q40) LAUNCH(c, "gateup", launch_gateup_tiles(s, d, S, T, c->stream));
+    else LAUNCH(c, "gateup", launch_gateup_exact(s, d, S, T, debug, c->n_cu, c->stream));
+    if (dn_mx) LAUNCH(c, "down", launch_down_mx(s, d, S, d_out, T, c->stream));
+    else LAUNCH(c, "down", launch_down_exact(s, d, S, d_out, T, 1, c->stream));
     return QMSG_OK;
 }
 

@@ -42,14 +42,22 @@ constexpr int kMaxExperts = 256;
 /* Slots (tokens of one expert) per slot tile of the batch kernels (dispatch's tile list). */
 constexpr int kTileN = 32;
 
-/* The default path takes the MFMA expert kernels for batches averaging at least this many
- * slots per active expert (measured: 32 per expert at 512 tokens 3.3 against 4.3 ms per layer
- * for the 235B shape; 4 per expert, the 64-token stack, slower than the row kernels). */
-constexpr int kMxAutoSlots = 12;
+/* The default path takes the MFMA kernels for gate/up from kMxAutoSlots slots per active
+ * expert on average, and for down from kMxDownSlots (235B shape, Q4_0 down, per layer: gate/up
+ * on MFMA against the row kernels 573 / 553 us at 6 slots per expert, 616 / 734 at 8, 709 /
+ * 1080 at 12, 1545 / 2697 at 32 (the Zipf prefill); down 158 / 182 at 3 slots per expert,
+ * 139 / 134 at 2; Q6_K down 410 / 500 at 4). */
+constexpr int kMxAutoSlots = 7;
+constexpr int kMxDownSlots = 3;
 inline bool mx_auto(int T, int K, int X)
 {
     const long NS = (long)T * K, act = X < NS ? X : NS;
     return NS >= (long)kMxAutoSlots * act;
+}
+inline bool mx_auto_down(int T, int K, int X)
+{
+    const long NS = (long)T * K, act = X < NS ? X : NS;
+    return NS >= (long)kMxDownSlots * act;
 }
 
 /* One-token batches (n_used <= 8) are routed inside the gate/up kernel instead of by a
@@ -128,6 +136,9 @@ hipError_t launch_gateup_exact(const Shape &s, const LayerDev &L, const Scratch 
 bool mx_supported(const Shape &s, const LayerDev &L, int *down_mx);
 hipError_t launch_experts_mx(const Shape &s, const LayerDev &L, const Scratch &S, float *out, int T, int debug,
                              hipStream_t st);
+/* Down alone on the MFMA kernels after a row-kernel gate/up: activation blocks and records from
+ * act, the down tiles, the combine (needs *down_mx of mx_supported). */
+hipError_t launch_down_mx(const Shape &s, const LayerDev &L, const Scratch &S, float *out, int T, hipStream_t st);
 /* Gate/up rows of Q4_1 / Q6_K (or mixed) layers by slot tiles, then the SwiGLU. */
 hipError_t launch_gateup_tiles(const Shape &s, const LayerDev &L, const Scratch &S, int T, hipStream_t st);
 hipError_t launch_down_exact(const Shape &s, const LayerDev &L, const Scratch &S, float *out, int T, int quant,

@@ -1826,7 +1826,11 @@ __global__ __launch_bounds__(32 * RD) void down_small_kernel(DownArgs a)
 
 /* The int8 blocks of every slot's activations (src/model.c:996-997) for batches whose
  * records do not fit the down kernel's LDS: one thread per 32-block. */
-__global__ void act_quant_kernel(Scratch S, int F, int NS)
+__device__ void mx_store_record(const Q8Vals &q, uint8_t *rec);
+
+/* The int8 activation blocks of every slot (src/model.c:996-997) from act: QmsQ8 blocks, pair
+ * records, and, when mxrec is set, the MFMA kernels' records too. */
+__global__ void act_quant_kernel(Scratch S, int F, int NS, uint8_t *mxrec)
 {
     const int nbF = F >> 5;
     const int b = blockIdx.x * blockDim.x + threadIdx.x;
@@ -1839,8 +1843,10 @@ __global__ void act_quant_kernel(Scratch S, int F, int NS)
         const float4 f = src[j];
         v[4 * j] = f.x; v[4 * j + 1] = f.y; v[4 * j + 2] = f.z; v[4 * j + 3] = f.w;
     }
-    quantize_block_store(v, S.aq + b, (uint32_t *)(S.aqk + ((size_t)s * (nbF >> 1) + (blk >> 1)) * kPairBytes),
-                         blk & 1);
+    const Q8Vals q = quantize_block(v);
+    store_q8(q, S.aq + b);
+    store_pair_half(q, (uint32_t *)(S.aqk + ((size_t)s * (nbF >> 1) + (blk >> 1)) * kPairBytes), blk & 1);
+    if (mxrec) mx_store_record(q, mxrec + (size_t)b * 128);
 }
 
 /* Weighted sum per token in selection order (src/model.c:1152-1162) when dn did not fit. */
@@ -1921,7 +1927,7 @@ hipError_t launch_down_exact(const Shape &s, const LayerDev &L, const Scratch &S
     const bool qa = quant && T <= kTileQuantT;
     if (quant && !qa) {
         const int nq = NS * (s.F / 32);
-        QLAUNCH("actq", act_quant_kernel, dim3((nq + 255) / 256), dim3(256), 0, st, S, s.F, NS);
+        QLAUNCH("actq", act_quant_kernel, dim3((nq + 255) / 256), dim3(256), 0, st, S, s.F, NS, (uint8_t *)nullptr);
     }
     const int NT = T >= 4 ? 4 : (T >= 2 ? 2 : 1);
     const int RT = L.down_type == 14 ? kDownTileRowsQ6K : 64;
@@ -2518,17 +2524,22 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4, 4))) voi
     }
 }
 
+/* Slot groups per block: 2 (16 slots, 128 rows) for Q4_0 / Q4_1, whose 72-89 KB of LDS let
+ * two blocks share a CU; measured faster than 8-slot blocks at every batch from 3 slots per
+ * expert up (235B shape, 48 to 192 tokens). Q6_K rows need 224 LDS bytes a chunk, so a block
+ * has a CU to itself either way, and 8-slot blocks of 256 rows run faster (64 tokens: 413
+ * against 625 us). */
+template <int TYPE>
+constexpr int mx_wsg() { return TYPE == 14 ? 1 : 2; }
+
 template <int TYPE, int GU>
-static void launch_mx(const MxArgs &a, int wsg, int rows, int maxt, hipStream_t st)
+static void launch_mx(const MxArgs &a, int rows, int maxt, hipStream_t st)
 {
-    const size_t lds = (size_t)mx_lds_bytes(TYPE, wsg);
-    const int rwg = 256 / wsg;
-    if (wsg == 2)
-        QLAUNCH(GU ? "gateup" : "down", (mx_kernel<TYPE, 2, GU>), dim3(rows / (GU ? rwg / 2 : rwg), maxt, kTileN / 16),
-                dim3(512), lds, st, a);
-    else
-        QLAUNCH(GU ? "gateup" : "down", (mx_kernel<TYPE, 1, GU>), dim3(rows / (GU ? rwg / 2 : rwg), maxt, kTileN / 8),
-                dim3(512), lds, st, a);
+    constexpr int W = mx_wsg<TYPE>();
+    using Lay = MxLayout<TYPE, W>;
+    const size_t lds = (size_t)mx_lds_bytes(TYPE, W);
+    QLAUNCH(GU ? "gateup" : "down", (mx_kernel<TYPE, W, GU>),
+            dim3(rows / (GU ? Lay::RWG / 2 : Lay::RWG), maxt, kTileN / Lay::SWG), dim3(512), lds, st, a);
 }
 
 /* Whether the MFMA kernels take this layer: Q4_0 gate and up; Q4_0, Q4_1 or Q6_K down (Q6_K
@@ -2543,19 +2554,12 @@ bool mx_supported(const Shape &s, const LayerDev &L, int *down_mx)
     return gu;
 }
 
-/* Slots per block: 16 when the batch averages at least 12 slots per active expert, else 8. */
-static int mx_wsg(const Shape &s, int T)
-{
-    const int NS = T * s.K, act = s.X < NS ? s.X : NS;
-    return NS >= 12 * act ? 2 : 1;
-}
-
 hipError_t launch_experts_mx(const Shape &s, const LayerDev &L, const Scratch &S, float *out, int T, int debug,
                              hipStream_t st)
 {
     int down_mx = 0;
     if (!mx_supported(s, L, &down_mx)) return hipErrorInvalidValue;
-    const int NS = T * s.K, maxt = (s.X < NS ? s.X : NS) + NS / kTileN + 1, wsg = mx_wsg(s, T);
+    const int NS = T * s.K, maxt = (s.X < NS ? s.X : NS) + NS / kTileN + 1;
     const int nx = T * (s.E / 32);
     QLAUNCH("mxin", mx_input_kernel, dim3((nx + 255) / 256), dim3(256), 0, st, S.xq, nx, S.mxx);
     MxArgs a;
@@ -2569,7 +2573,7 @@ hipError_t launch_experts_mx(const Shape &s, const LayerDev &L, const Scratch &S
     a.rec = S.mxx;
     a.rec_out = S.mxa;
     a.S = S;
-    launch_mx<2, 1>(a, wsg, s.F, maxt, st);
+    launch_mx<2, 1>(a, s.F, maxt, st);
     if (!down_mx) {
         const hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
@@ -2581,9 +2585,38 @@ hipError_t launch_experts_mx(const Shape &s, const LayerDev &L, const Scratch &S
     a.eb = L.down_eb;
     a.rec = S.mxa;
     a.rec_out = nullptr;
-    if (L.down_type == 14) launch_mx<14, 0>(a, wsg, s.E, maxt, st);
-    else if (L.down_type == 3) launch_mx<3, 0>(a, wsg, s.E, maxt, st);
-    else launch_mx<2, 0>(a, wsg, s.E, maxt, st);
+    if (L.down_type == 14) launch_mx<14, 0>(a, s.E, maxt, st);
+    else if (L.down_type == 3) launch_mx<3, 0>(a, s.E, maxt, st);
+    else launch_mx<2, 0>(a, s.E, maxt, st);
+    const int n = T * s.E;
+    QLAUNCH("combine", combine_kernel, dim3((n + 255) / 256), dim3(256), 0, st, S, s.E, s.K, T, out);
+    return hipGetLastError();
+}
+
+/* Down on the MFMA kernels after the row kernels' gate/up (which leave act in scratch): the
+ * activation blocks and their MFMA records in one pass, the down tiles, the combine. */
+hipError_t launch_down_mx(const Shape &s, const LayerDev &L, const Scratch &S, float *out, int T, hipStream_t st)
+{
+    int down_mx = 0;
+    (void)mx_supported(s, L, &down_mx);
+    if (!down_mx) return hipErrorInvalidValue;
+    const int NS = T * s.K, maxt = (s.X < NS ? s.X : NS) + NS / kTileN + 1;
+    const int nq = NS * (s.F / 32);
+    QLAUNCH("actq", act_quant_kernel, dim3((nq + 255) / 256), dim3(256), 0, st, S, s.F, NS, S.mxa);
+    MxArgs a;
+    a.w0 = L.down;
+    a.w1 = nullptr;
+    a.rb = L.down_rb;
+    a.eb = L.down_eb;
+    a.E = s.E;
+    a.F = s.F;
+    a.debug = 0;
+    a.rec = S.mxa;
+    a.rec_out = nullptr;
+    a.S = S;
+    if (L.down_type == 14) launch_mx<14, 0>(a, s.E, maxt, st);
+    else if (L.down_type == 3) launch_mx<3, 0>(a, s.E, maxt, st);
+    else launch_mx<2, 0>(a, s.E, maxt, st);
     const int n = T * s.E;
     QLAUNCH("combine", combine_kernel, dim3((n + 255) / 256), dim3(256), 0, st, S, s.E, s.K, T, out);
     return hipGetLastError();

@@ -1,11 +1,13 @@
 """The MFMA expert kernels (f16 MFMA lane sums + the reference's fp32 chains on the VALU) on the
 GPU: every intermediate bit for bit against the oracle, like the exact path.
 
-The MFMA path runs for QMSG_PATH_MFMA at any batch of two or more tokens and for the default
-path from 32 tokens on. Cases cover Q4_0 / Q4_1 / Q6_K down rows, 16- and 32-slot blocks
-(average slots per expert below and above 24), odd slot counts per expert, the Zipf-skewed
-512-token prefill, shapes whose down rows fall back to the exact kernel (F/32 not a whole number
-of 8-block chunks), and batches of alternating sizes on one context."""
+The MFMA kernels run for QMSG_PATH_MFMA at any batch of two or more tokens; the default path
+takes them for gate/up from 7 slots per active expert and for down from 3, so the 64-token
+cases also run the row-kernel gate/up followed by the MFMA down. Cases cover Q4_0 / Q4_1 /
+Q6_K down rows, tiles of up to 32 slots run as 16-slot blocks, odd slot
+counts per expert, the Zipf-skewed 512-token prefill, shapes whose down rows fall back to the
+exact kernel (F/32 not a whole number of 8-block chunks), and batches of alternating sizes on
+one context."""
 import numpy as np
 import pytest
 
@@ -16,6 +18,7 @@ pytestmark = pytest.mark.gpu
 CASES = [
     # name, E, X, K, F, T, seed, down_type, zipf
     ("q30b_t64", 2048, 128, 8, 768, 64, 1, orc.T_Q4_0, False),
+    ("q30b_t128", 2048, 128, 8, 768, 128, 11, orc.T_Q4_0, False),    # 8 slots per expert: both on MFMA
     ("q235b_t64", 4096, 128, 8, 1536, 64, 2, orc.T_Q4_0, False),
     ("q235b_t33", 4096, 128, 8, 1536, 33, 3, orc.T_Q4_0, False),
     ("q235b_q6k_t64", 4096, 128, 8, 1536, 64, 6, orc.T_Q6_K, False),
@@ -49,14 +52,14 @@ def test_mfma_bit_exact(q, name, E, X, K, F, T, seed, dt, zipf):
         ctx.synth(0, seed, down_type=dt, router_col0=col0)
         ctx.set_path(q.PATH_MFMA)
         out, got = ctx.moe_debug(0, x)
-        ctx.set_path(q.PATH_AUTO)
-        out_auto = ctx.moe(0, x)
-    for k in ("sel", "start", "slot_t", "slot_of", "active"):
-        assert np.array_equal(got[k], ref[k]), k
-    for k in ("logits", "wt", "xq", "gu", "act", "aq", "dn"):
-        assert np.array_equal(_bits(got[k]), _bits(ref[k])), k
-    assert np.array_equal(_bits(out), _bits(ref_out)), "layer output"
-    assert np.array_equal(_bits(out_auto), _bits(ref_out)), "layer output (default path)"
+        ctx.set_path(q.PATH_AUTO)        # below 7 slots per expert: row-kernel gate/up, MFMA down
+        out_auto, got_auto = ctx.moe_debug(0, x)
+    for path, o, g in (("mfma", out, got), ("default", out_auto, got_auto)):
+        for k in ("sel", "start", "slot_t", "slot_of", "active"):
+            assert np.array_equal(g[k], ref[k]), (path, k)
+        for k in ("logits", "wt", "xq", "gu", "act", "aq", "dn"):
+            assert np.array_equal(_bits(g[k]), _bits(ref[k])), (path, k)
+        assert np.array_equal(_bits(o), _bits(ref_out)), (path, "layer output")
 
 
 def test_mfma_repeated_calls_and_sizes(q):
