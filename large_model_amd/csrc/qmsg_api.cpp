@@ -76,7 +76,7 @@ std::vector<ScratchItem> scratch_items(const qmsg_cfg &cfg, size_t T, Scratch *S
         { (void **)&S->gu, NS * 2 * F * 4 },    { (void **)&S->act, NS * F * 4 },
         { (void **)&S->aq, NS * nbF * sizeof(Q8) }, { (void **)&S->aqk, NS * (nbF / 2) * kPairBytes },
         { (void **)&S->dn, NS * E * 4 },
-        { (void **)&S->mxx, T * nbE * 128 },    { (void **)&S->mxa, NS * nbF * 128 },
+        { (void **)&S->mxx, T * nbE * kMxRec },  { (void **)&S->mxa, NS * nbF * kMxRec },
     };
 }
 

@@ -1846,7 +1846,7 @@ __global__ void act_quant_kernel(Scratch S, int F, int NS, uint8_t *mxrec)
     const Q8Vals q = quantize_block(v);
     store_q8(q, S.aq + b);
     store_pair_half(q, (uint32_t *)(S.aqk + ((size_t)s * (nbF >> 1) + (blk >> 1)) * kPairBytes), blk & 1);
-    if (mxrec) mx_store_record(q, mxrec + (size_t)b * 128);
+    if (mxrec) mx_store_record(q, mxrec + (size_t)b * kMxRec);
 }
 
 /* Weighted sum per token in selection order (src/model.c:1152-1162) when dn did not fit. */
@@ -2035,8 +2035,8 @@ hipError_t launch_gateup_tiles(const Shape &s, const LayerDev &L, const Scratch 
  * serves its four FMAs.
  *
  * Activation records (kMxRec bytes per slot, or per token, and 32-block) carry x in that
- * order as f16, the C input, d, ds and the half sums; the lanes of A outside their group read
- * the record's zero words. Gate/up writes the records of the activations it quantises, so the
+ * order as f16 (64 bytes), then d, ds and the half sums (16 bytes), then 16 zero bytes, which
+ * the lanes of A outside their group read. Gate/up writes the records of the activations it quantises, so the
  * down products read them directly.
  *
  * A block of 8 waves computes 512/WSG weight rows x 8*WSG slots of one expert's slot tile:
@@ -2048,14 +2048,15 @@ typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef short short2_t __attribute__((ext_vector_type(2)));
 
-constexpr int kMxRec = 128;      /* bytes of one activation record */
 constexpr int kMxC = 8;          /* 32-blocks per staged chunk (one Q6_K super-block) */
-constexpr int kMxZero = 112;     /* offset of the record's zero words */
+constexpr int kMxDx = 64;        /* offset of the record's d, ds, half sums */
+constexpr int kMxZero = 80;      /* offset of the record's zero words */
+static_assert(kMxRec == 96, "record layout: 64 bytes of codes, 16 of scales, 16 of zeros");
 
 /* One int8 block as an activation record (layout above). */
 __device__ void mx_store_record(const Q8Vals &q, uint8_t *rec)
 {
-    u32x4 w[8];
+    u32x4 w[6];
 #pragma unroll
     for (int k = 0; k < 8; k++) {
         const uint32_t c = q.qw[k];
@@ -2064,12 +2065,11 @@ __device__ void mx_store_record(const Q8Vals &q, uint8_t *rec)
         auto h = [](int x) { return (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)(float)x); };
         w[k >> 1][2 * (k & 1)] = h(x0) | (h(x2) << 16);
         w[k >> 1][2 * (k & 1) + 1] = h(x1) | (h(x3) << 16);
-        ((float *)&w[4])[k] = -1024.0f * (float)(x0 + x1 + x2 + x3);
     }
-    w[6] = u32x4{ __float_as_uint(q.d), __float_as_uint(q.ds), q.s16, 0u };
-    w[7] = u32x4{ 0u, 0u, 0u, 0u };
+    w[4] = u32x4{ __float_as_uint(q.d), __float_as_uint(q.ds), q.s16, 0u };
+    w[5] = u32x4{ 0u, 0u, 0u, 0u };
 #pragma unroll
-    for (int i = 0; i < 8; i++) ((u32x4 *)rec)[i] = w[i];
+    for (int i = 0; i < 6; i++) ((u32x4 *)rec)[i] = w[i];
 }
 
 /* The layer input's records from its int8 blocks (one thread per block). */
@@ -2097,30 +2097,33 @@ struct MxArgs {
 };
 
 /* LDS bytes of one staged weight row (kMxC blocks): Q4_0 144, Q4_1 160, Q6_K one super-block
- * copied from the 4-byte boundary below it (216 bytes) in a 224-byte slot. */
-__host__ __device__ constexpr int mx_wstride(int type) { return type == 14 ? 224 : (type == 3 ? 160 : 144); }
+ * copied from the 4-byte boundary below it (216 bytes, 54 words). */
+__host__ __device__ constexpr int mx_wstride(int type) { return type == 14 ? 216 : (type == 3 ? 160 : 144); }
 
 /* Staged chunk layout of a block of 8 waves: (8/WSG) row groups of 32 weight rows, WSG slot
- * groups of 8 slots; the weight rows, then each slot's kMxC records at a stride of kMxRStride
- * bytes (64 bytes past the records, so the two slots of a pair sit 16 LDS banks apart). Every
+ * groups of 8 slots; the weight rows, then each slot's kMxC records at a stride of
+ * mx_rstride bytes: 64 bytes past the records for Q6_K (two 80 KB blocks fill a CU's LDS), 320
+ * for the Q4 types, so that two pairs' records lie more than 2040 bytes apart and every A read
+ * stays a single read straight into the MFMA operand (closer records get merged into paired
+ * reads plus register moves); either way the two slots of a pair sit 16 LDS banks apart. Every
  * piece is copied by the LDS DMA (global_load_lds): a wave instruction moves 64 lanes x 16 bytes
  * (Q6_K weights: x 4 bytes) to consecutive LDS bytes. Two buffers: the next chunk's copy is in
  * flight while the current one computes. */
-constexpr int kMxRStride = kMxC * kMxRec + 64;
+__host__ __device__ constexpr int mx_rstride(int type) { return kMxC * kMxRec + (type == 14 ? 64 : 320); }
 
 template <int TYPE, int WSG>
 struct MxLayout {
     static constexpr int RWG = 256 / WSG, SWG = 8 * WSG, WS = mx_wstride(TYPE);
-    static constexpr int WBYTES = RWG * WS, BUF = WBYTES + SWG * kMxRStride;
+    static constexpr int RS = mx_rstride(TYPE);
+    static constexpr int WBYTES = RWG * WS, BUF = WBYTES + SWG * RS;
     static constexpr int WUNIT = TYPE == 14 ? 4 : 16;                 /* bytes per lane per DMA   */
     static constexpr int WUR = WS / WUNIT;                             /* DMA units per row        */
-    static constexpr int WUSED = TYPE == 14 ? 54 : WUR;                /* units holding row bytes  */
     static constexpr int WINSTR = (RWG * WUR + 63) / 64;               /* weight DMA instructions  */
 };
 
 __host__ __device__ constexpr int mx_lds_bytes(int type, int wsg)
 {
-    return 2 * ((256 / wsg) * mx_wstride(type) + 8 * wsg * kMxRStride);
+    return 2 * ((256 / wsg) * mx_wstride(type) + 8 * wsg * mx_rstride(type));
 }
 
 /* (x & m) | c in one instruction; m and c in registers (no literal operands in VOP3 here). */
@@ -2285,14 +2288,14 @@ __device__ __forceinline__ void mx_block(int b, const MxStreams &st, const uint8
     }
 #pragma unroll
     for (int p = 0; p < NP; p++) {
-        constexpr int RB = PAR * kMxRec;
-        const u32x2 lo = *(const LdsU32x2 *)(st.alo + RB + 2 * p * kMxRStride);
-        const u32x2 hi = *(const LdsU32x2 *)(st.ahi + RB + 2 * p * kMxRStride);
+        constexpr int RB = PAR * kMxRec, RS = mx_rstride(TYPE);
+        const u32x2 lo = *(const LdsU32x2 *)(st.alo + RB + 2 * p * RS);
+        const u32x2 hi = *(const LdsU32x2 *)(st.ahi + RB + 2 * p * RS);
         const f16x8 aop = __builtin_bit_cast(f16x8, u32x4{ lo.x, lo.y, hi.x, hi.y });
         u32x4 dx;
-        if constexpr (TYPE == 14) dx = *(const LdsU32x4 *)(st.d + RB + 2 * p * kMxRStride);   /* d, ds, s16 pair, 0 */
+        if constexpr (TYPE == 14) dx = *(const LdsU32x4 *)(st.d + RB + 2 * p * RS);   /* d, ds, s16 pair, 0 */
         else {
-            const u32x2 d2 = *(const LdsU32x2 *)(st.d + RB + 2 * p * kMxRStride);            /* d, ds */
+            const u32x2 d2 = *(const LdsU32x2 *)(st.d + RB + 2 * p * RS);            /* d, ds */
             dx = u32x4{ d2.x, d2.y, 0u, 0u };
         }
         const float xd = __uint_as_float(dx.x), xds = __uint_as_float(dx.y);
@@ -2329,7 +2332,7 @@ __device__ __forceinline__ void mx_chunk(const uint8_t *W, const uint8_t *R, int
     MxStreams st;
     st.alo = (LdsPtr)(R + offa_lo);
     st.ahi = (LdsPtr)(R + offa_hi);
-    st.d = (LdsPtr)(R + jd * kMxRStride + 96);
+    st.d = (LdsPtr)(R + jd * mx_rstride(TYPE) + kMxDx);
     st.q = (LdsPtr)(W + lr * WS + QO + 4 * lg);
     st.dw = (LdsPtr)(W + lr * WS);
 #pragma unroll 1
@@ -2344,6 +2347,109 @@ __device__ __forceinline__ void mx_chunk(const uint8_t *W, const uint8_t *R, int
         st.q += 2 * BB;
         st.dw += 2 * BB;
     }
+}
+
+/* A word of a staged Q6_K row at byte off past the row's 4-byte-aligned LDS base (O = 2: the
+ * super-block sits 2 bytes in, so the word straddles two aligned words). */
+template <int O>
+__device__ __forceinline__ uint32_t q6_word(LdsPtr base, int off)
+{
+    typedef __attribute__((address_space(3))) const uint32_t LdsU32;
+    if constexpr (O == 0) return *(LdsU32 *)(base + off);
+    else return __builtin_amdgcn_alignbyte(*(LdsU32 *)(base + off + 2), *(LdsU32 *)(base + off - 2), 2);
+}
+
+/* The B operand and scales of 32-block B (0..7) of the staged Q6_K super-block for tile t:
+ * q points at the lane's code words (row base + 4*lg), rb at the row base. Every offset and
+ * shift is a constant. The 6-bit code dword is the low nibbles (shifted down for the upper
+ * two blocks of a half) with the two high bits of qh moved to bits 4-5 (src/kernels.c:148-160). */
+template <int O, int B>
+__device__ __forceinline__ MxB mx_weights_q6(LdsPtr q, LdsPtr rb, int t, int kh)
+{
+    constexpr int WS = mx_wstride(14), h = B >> 2, g = B & 3, ns = 4 * (g >> 1), hs = 2 * g;
+    constexpr int oql = O + 64 * h + 32 * (g & 1), oqh = O + 128 + 32 * h;
+    const uint32_t m8 = 0x00ff00ffu, bias = 0x64006400u, lo4 = 0x0f0f0f0fu;
+    auto code = [&](int dq) {
+        const uint32_t ql = q6_word<O>(q, 16 * t * WS + oql + dq), qh = q6_word<O>(q, 16 * t * WS + oqh + dq);
+        uint32_t hi;
+        if constexpr (hs < 4) hi = (qh << (4 - hs)) & 0x30303030u;
+        else if constexpr (hs == 4) hi = qh & 0x30303030u;
+        else hi = (qh >> (hs - 4)) & 0x30303030u;
+        return and_or(ns ? (ql >> ns) : ql, lo4, hi);
+    };
+    const uint32_t cA = code(0), cB = code(16);
+    MxB w;
+    w.op = mx_pack_codes(and_or(cA, m8, bias), and_or(cA >> 8, m8, bias), and_or(cB, m8, bias),
+                         and_or(cB >> 8, m8, bias));
+    const uint32_t scw = *(const __attribute__((address_space(3))) uint16_t *)(rb + 16 * t * WS + O + 192 + 8 * h + 2 * g);
+    const int sa = (int)(int8_t)(scw & 0xffu), sbv = (int)(int8_t)(scw >> 8);
+    w.sab = ((uint32_t)sa & 0xffffu) | ((uint32_t)sbv << 16);
+    w.sc = (float)(kh ? sbv : sa);
+    w.dw = *(const __attribute__((address_space(3))) uint16_t *)(rb + 16 * t * WS + O + 208);
+    return w;
+}
+
+/* One Q6_K block B of the staged chunk: NP slot pairs against the wave's two 16-row tiles. */
+template <int NP, int O, int B>
+__device__ __forceinline__ void mx_block_q6(const MxStreams &st, int kh, f32x4 (&acc)[2][4], float (&cr)[2][4])
+{
+    constexpr int RS = mx_rstride(14), RB = B * kMxRec;
+    MxB w[2];
+#pragma unroll
+    for (int t = 0; t < 2; t++) w[t] = mx_weights_q6<O, B>(st.q, st.dw, t, kh);
+#pragma unroll
+    for (int p = 0; p < NP; p++) {
+        /* volatile: keeps each A read a single read into the MFMA operand (records 832 bytes
+         * apart would otherwise be merged into paired reads plus register moves) */
+        const u32x2 lo = *(const volatile LdsU32x2 *)(st.alo + RB + 2 * p * RS);
+        const u32x2 hi = *(const volatile LdsU32x2 *)(st.ahi + RB + 2 * p * RS);
+        const f16x8 aop = __builtin_bit_cast(f16x8, u32x4{ lo.x, lo.y, hi.x, hi.y });
+        const u32x4 dx = *(const LdsU32x4 *)(st.d + RB + 2 * p * RS);          /* d, ds, s16 pair, 0 */
+        const float xd = __uint_as_float(dx.x);
+        const uint32_t s16p = dx.z;           /* (bit_cast of a vector element itself reads .x) */
+#pragma unroll
+        for (int t = 0; t < 2; t++) {
+            const f32x4 S =
+                __builtin_amdgcn_mfma_f32_16x16x32_f16(aop, w[t].op, f32x4{ 0.0f, 0.0f, 0.0f, 0.0f }, 0, 0, 0);
+            const float dd = mix_mul(w[t].dw, xd);
+#pragma unroll
+            for (int v = 0; v < 4; v++) acc[t][p][v] = __builtin_fmaf(S[v] * w[t].sc, dd, acc[t][p][v]);
+            /* sc[2g]*s16[0] + sc[2g+1]*s16[1] in one packed int16 dot */
+            const int ssum = __builtin_amdgcn_sdot2(__builtin_bit_cast(short2_t, w[t].sab),
+                                                    __builtin_bit_cast(short2_t, s16p), 0, false);
+            cr[t][p] = __builtin_fmaf(dd, (float)ssum, cr[t][p]);
+        }
+    }
+}
+
+/* A staged Q6_K super-block, its 8 blocks unrolled (offsets and shifts depend on the block). */
+template <int NP, int O>
+__device__ __forceinline__ void mx_chunk_q6(const uint8_t *W, const uint8_t *R, int lr, int lg, int kh, int jd,
+                                            int offa_lo, int offa_hi, f32x4 (&acc)[2][4], float (&cr)[2][4])
+{
+    constexpr int WS = mx_wstride(14);
+    MxStreams st;
+    st.alo = (LdsPtr)(R + offa_lo);
+    st.ahi = (LdsPtr)(R + offa_hi);
+    st.d = (LdsPtr)(R + jd * mx_rstride(14) + kMxDx);
+    st.q = (LdsPtr)(W + lr * WS + 4 * lg);
+    st.dw = (LdsPtr)(W + lr * WS);
+    mx_opaque(st);
+    mx_block_q6<NP, O, 0>(st, kh, acc, cr);
+    __builtin_amdgcn_sched_barrier(0);
+    mx_block_q6<NP, O, 1>(st, kh, acc, cr);
+    __builtin_amdgcn_sched_barrier(0);
+    mx_block_q6<NP, O, 2>(st, kh, acc, cr);
+    __builtin_amdgcn_sched_barrier(0);
+    mx_block_q6<NP, O, 3>(st, kh, acc, cr);
+    __builtin_amdgcn_sched_barrier(0);
+    mx_block_q6<NP, O, 4>(st, kh, acc, cr);
+    __builtin_amdgcn_sched_barrier(0);
+    mx_block_q6<NP, O, 5>(st, kh, acc, cr);
+    __builtin_amdgcn_sched_barrier(0);
+    mx_block_q6<NP, O, 6>(st, kh, acc, cr);
+    __builtin_amdgcn_sched_barrier(0);
+    mx_block_q6<NP, O, 7>(st, kh, acc, cr);
 }
 
 /* The LDS DMA: `bytes` (4 or 16) from src of every active lane to dst + lane * bytes. */
@@ -2411,27 +2517,28 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4, 4))) voi
             if (n < RWG * Lay::WUR) {
                 const int i = n / Lay::WUR, u = n - i * Lay::WUR;
                 if constexpr (TYPE == 14) {
-                    /* the super-block starts 2 bytes past a 4-byte boundary on odd chunks; the
-                     * two padding words of the slot repeat the last one */
-                    dma_to_lds<4>(row_src(i, (uint32_t)(c * 210 - 2 * (c & 1) + 4 * min(u, Lay::WUSED - 1))),
-                                  base + 256 * q);
+                    /* the super-block starts 2 bytes past a 4-byte boundary on odd chunks */
+                    dma_to_lds<4>(row_src(i, (uint32_t)(c * 210 - 2 * (c & 1) + 4 * u)), base + 256 * q);
                 } else {
                     dma_to_lds<16>(row_src(i, (uint32_t)(c * (kMxC * (TYPE == 3 ? 20 : 18)) + 16 * u)), base + 1024 * q);
                 }
             }
         }
+        /* a slot's kMxC records: 48 lanes x 16 bytes */
+        if (lane < kMxC * kMxRec / 16) {
 #pragma unroll
-        for (int j = 0; j < RPW; j++)
-            dma_to_lds<16>(rsrc[j] + (size_t)c * kMxC * kMxRec + 16 * lane,
-                           base + Lay::WBYTES + (wave + 8 * j) * kMxRStride);
+            for (int j = 0; j < RPW; j++)
+                dma_to_lds<16>(rsrc[j] + (size_t)c * kMxC * kMxRec + 16 * lane,
+                               base + Lay::WBYTES + (wave + 8 * j) * Lay::RS);
+        }
     };
 
     /* A reads: lane row lr is slot ja = lr/8 of the pair, reference lane ka = lr%8; it holds x
      * only if ka%4 == lg, in the low half of its 8 K positions for ka < 4 */
     const int ja = lr >> 3, ka = lr & 7;
     const bool nz = (ka & 3) == lg;
-    const int offa_lo = ja * kMxRStride + ((nz && ka < 4) ? 8 * ka : kMxZero);
-    const int offa_hi = ja * kMxRStride + ((nz && ka >= 4) ? 8 * ka : kMxZero);
+    const int offa_lo = ja * Lay::RS + ((nz && ka < 4) ? 8 * ka : kMxZero);
+    const int offa_hi = ja * Lay::RS + ((nz && ka >= 4) ? 8 * ka : kMxZero);
     const int nw = min(max(ns - 8 * ws, 0), 8), np = (nw + 1) >> 1;      /* this wave's slot pairs */
 
     /* The whole chunk loop and the row sums for one slot-pair count NP, chosen once per wave,
@@ -2457,11 +2564,13 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4, 4))) voi
             if (c + 1 < nch) issue(c + 1, buf ^ 1);
             if constexpr (NP > 0) {
                 const uint8_t *Wl = smem + buf * BUF + (32 * wr) * WS;
-                const uint8_t *Rl = smem + buf * BUF + Lay::WBYTES + (8 * ws) * kMxRStride;
-                if (TYPE == 14 && (c & 1))
-                    mx_chunk<TYPE, NP, 2>(Wl, Rl, lr, lg, kh, jd, offa_lo, offa_hi, acc, cr);
-                else
+                const uint8_t *Rl = smem + buf * BUF + Lay::WBYTES + (8 * ws) * Lay::RS;
+                if constexpr (TYPE == 14) {
+                    if (c & 1) mx_chunk_q6<NP, 2>(Wl, Rl, lr, lg, kh, jd, offa_lo, offa_hi, acc, cr);
+                    else mx_chunk_q6<NP, 0>(Wl, Rl, lr, lg, kh, jd, offa_lo, offa_hi, acc, cr);
+                } else {
                     mx_chunk<TYPE, NP, 0>(Wl, Rl, lr, lg, kh, jd, offa_lo, offa_hi, acc, cr);
+                }
             }
             mx_wait_barrier();       /* chunk c+1 has landed; buffer c is free for chunk c+2 */
         }
@@ -2524,13 +2633,13 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4, 4))) voi
     }
 }
 
-/* Slot groups per block: 2 (16 slots, 128 rows) for Q4_0 / Q4_1, whose 72-89 KB of LDS let
- * two blocks share a CU; measured faster than 8-slot blocks at every batch from 3 slots per
- * expert up (235B shape, 48 to 192 tokens). Q6_K rows need 224 LDS bytes a chunk, so a block
- * has a CU to itself either way, and 8-slot blocks of 256 rows run faster (64 tokens: 413
- * against 625 us). */
+/* Slot groups per block: 2 (16 slots, 128 rows), so two blocks share a CU (Q4_0 62 KB of LDS,
+ * Q4_1 66 KB, Q6_K 80 KB); measured faster than 8-slot blocks of 256 rows at every batch from 3
+ * slots per expert up (235B shape, 48 to 192 tokens; Q6_K down at 64 tokens 329 against
+ * 405 us). */
 template <int TYPE>
-constexpr int mx_wsg() { return TYPE == 14 ? 1 : 2; }
+constexpr int mx_wsg() { return 2; }
+static_assert(2 * mx_lds_bytes(14, 2) <= 160 * 1024, "two Q6_K blocks per CU");
 
 template <int TYPE, int GU>
 static void launch_mx(const MxArgs &a, int rows, int maxt, hipStream_t st)
