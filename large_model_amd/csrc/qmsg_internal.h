@@ -47,10 +47,10 @@ constexpr int kMxRec = 96;
 /* The default path takes the MFMA kernels for gate/up from kMxAutoSlots slots per active
  * expert on average, and for down from kMxDownSlots (235B shape, Q4_0 down, per layer: gate/up
  * on MFMA against the row kernels 573 / 553 us at 6 slots per expert, 616 / 734 at 8, 709 /
- * 1080 at 12, 1545 / 2697 at 32 (the Zipf prefill); down 158 / 182 at 3 slots per expert,
- * 139 / 134 at 2; Q6_K down 410 / 500 at 4). */
+ * 1080 at 12, 1545 / 2697 at 32 (the Zipf prefill); down 158 / 184 at 3 slots per expert,
+ * 133 / 133 at 2; Q6_K down 248 / 300 at 2, 336 / 500 at 4). */
 constexpr int kMxAutoSlots = 7;
-constexpr int kMxDownSlots = 3;
+constexpr int kMxDownSlots = 2;
 inline bool mx_auto(int T, int K, int X)
 {
     const long NS = (long)T * K, act = X < NS ? X : NS;

@@ -2158,53 +2158,10 @@ typedef __attribute__((address_space(3))) const uint8_t *LdsPtr;
 typedef __attribute__((address_space(3))) const u32x2 LdsU32x2;
 typedef __attribute__((address_space(3))) const u32x4 LdsU32x4;
 
-/* The word at base + O + a (base 4-byte aligned, a a multiple of 4): one aligned read for
- * O == 0, two and a byte alignment for O == 2. */
-template <int O>
-__device__ __forceinline__ uint32_t lds_word_at(const uint8_t *base, uint32_t a)
-{
-    if constexpr (O == 0) return *(const uint32_t *)(base + a);
-    else return lds_u32(base, O + a);
-}
-
-template <int TYPE, int O, int PAR>
-__device__ __forceinline__ MxB mx_weights(const uint8_t *row, int b, int lg, int kh)
-{
-    const uint32_t m4 = 0x000f000fu, m8 = 0x00ff00ffu, bias = 0x64006400u;
-    MxB w;
-    if constexpr (TYPE == 14) {
-        const int h = b >> 2, g = b & 3;
-        const uint32_t qlA = lds_word_at<O>(row, 64 * h + 32 * (g & 1) + 4 * lg);
-        const uint32_t qlB = lds_word_at<O>(row, 64 * h + 32 * (g & 1) + 16 + 4 * lg);
-        const uint32_t qhA = lds_word_at<O>(row, 128 + 32 * h + 4 * lg);
-        const uint32_t qhB = lds_word_at<O>(row, 128 + 32 * h + 16 + 4 * lg);
-        const int ns = 4 * (g >> 1), hs = 2 * g;
-        const uint32_t cA = ((qlA >> ns) & 0x0f0f0f0fu) | (((qhA >> hs) & 0x03030303u) << 4);
-        const uint32_t cB = ((qlB >> ns) & 0x0f0f0f0fu) | (((qhB >> hs) & 0x03030303u) << 4);
-        w.op = mx_pack_codes(and_or(cA, m8, bias), and_or(cA >> 8, m8, bias), and_or(cB, m8, bias),
-                             and_or(cB >> 8, m8, bias));
-        const uint32_t scw = *(const uint16_t *)(row + O + 192 + 8 * h + 2 * g);
-        const int sa = (int)(int8_t)(scw & 0xffu), sbv = (int)(int8_t)(scw >> 8);
-        w.sab = ((uint32_t)sa & 0xffffu) | ((uint32_t)sbv << 16);
-        w.sc = (float)(kh ? sbv : sa);
-        w.dw = *(const uint16_t *)(row + O + 208);
-    } else {
-        constexpr int BB = TYPE == 3 ? 20 : 18, QO = TYPE == 3 ? 4 : 2;
-        uint32_t v;
-        if (TYPE == 3 || PAR) v = *(const uint32_t *)(row + BB * b + QO + 4 * lg);
-        else v = lds_u32(row, BB * b + QO + 4 * lg);      /* even blocks: 2 mod 4 */
-        w.op = mx_pack_codes(and_or(v, m4, bias), and_or(v >> 8, m4, bias), and_or(v >> 4, m4, bias),
-                             and_or(v >> 12, m4, bias));
-        w.dw = TYPE == 3 ? *(const uint32_t *)(row + BB * b) : (uint32_t) * (const uint16_t *)(row + BB * b);
-        w.sc = 0.0f;
-        w.sab = 0u;
-    }
-    return w;
-}
-
-/* The same for Q4_0 / Q4_1 from two per-block LDS pointers: pq at the lane's code word of the
- * block in tile row lr (Q4_0 even blocks: 2 bytes past a word boundary), pd at the block's
- * scale word; tile t is an immediate offset. */
+/* The B operand of one 16-row tile for a Q4_0 / Q4_1 block of the staged chunk, and its scale
+ * word, from two LDS pointers: pq at the lane's code word of the block in tile row lr (Q4_0
+ * even blocks: 2 bytes past a word boundary), pd at the block's scale word; tile t is an
+ * immediate offset. */
 template <int TYPE, int PAR>
 __device__ __forceinline__ MxB mx_weights_q4(LdsPtr pq, LdsPtr pd, int t)
 {
@@ -2276,48 +2233,38 @@ template <int TYPE, int NP, int O, int PAR>
 __device__ __forceinline__ void mx_block(int b, const MxStreams &st, const uint8_t *W, int lr, int lg, int kh,
                                          f32x4 (&acc)[2][4], float (&cr)[2][4])
 {
-    constexpr int WS = mx_wstride(TYPE);
+    static_assert(TYPE == 2 || TYPE == 3, "Q6_K chunks take mx_chunk_q6");
+    constexpr int BB = TYPE == 3 ? 20 : 18, RB = PAR * kMxRec, RS = mx_rstride(TYPE);
     MxB w[2];
-    if constexpr (TYPE == 14) {
 #pragma unroll
-        for (int t = 0; t < 2; t++) w[t] = mx_weights<TYPE, O, PAR>(W + (16 * t + lr) * WS, b, lg, kh);
-    } else {
-        constexpr int BB = TYPE == 3 ? 20 : 18;
-#pragma unroll
-        for (int t = 0; t < 2; t++) w[t] = mx_weights_q4<TYPE, PAR>(st.q + PAR * BB, st.dw + PAR * BB, t);
-    }
-#pragma unroll
-    for (int p = 0; p < NP; p++) {
-        constexpr int RB = PAR * kMxRec, RS = mx_rstride(TYPE);
+    for (int t = 0; t < 2; t++) w[t] = mx_weights_q4<TYPE, PAR>(st.q + PAR * BB, st.dw + PAR * BB, t);
+    /* pair p's two MFMAs are issued before pair p-1's results are used, so the chains of one
+     * pair run while the matrix core works on the next */
+    f32x4 S[2][2];
+    float xd[2], xds[2];
+    auto issue = [&](int p, int k) {
         const u32x2 lo = *(const LdsU32x2 *)(st.alo + RB + 2 * p * RS);
         const u32x2 hi = *(const LdsU32x2 *)(st.ahi + RB + 2 * p * RS);
+        const u32x2 d2 = *(const LdsU32x2 *)(st.d + RB + 2 * p * RS);          /* d, ds */
         const f16x8 aop = __builtin_bit_cast(f16x8, u32x4{ lo.x, lo.y, hi.x, hi.y });
-        u32x4 dx;
-        if constexpr (TYPE == 14) dx = *(const LdsU32x4 *)(st.d + RB + 2 * p * RS);   /* d, ds, s16 pair, 0 */
-        else {
-            const u32x2 d2 = *(const LdsU32x2 *)(st.d + RB + 2 * p * RS);            /* d, ds */
-            dx = u32x4{ d2.x, d2.y, 0u, 0u };
-        }
-        const float xd = __uint_as_float(dx.x), xds = __uint_as_float(dx.y);
+        xd[k] = __uint_as_float(d2.x);
+        xds[k] = __uint_as_float(d2.y);
+#pragma unroll
+        for (int t = 0; t < 2; t++)
+            S[k][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(aop, w[t].op, f32x4{ 0.0f, 0.0f, 0.0f, 0.0f }, 0, 0, 0);
+    };
+    issue(0, 0);
+#pragma unroll
+    for (int p = 0; p < NP; p++) {
+        const int k = p & 1;
+        if (p + 1 < NP) issue(p + 1, k ^ 1);
 #pragma unroll
         for (int t = 0; t < 2; t++) {
-            const f32x4 S =
-                __builtin_amdgcn_mfma_f32_16x16x32_f16(aop, w[t].op, f32x4{ 0.0f, 0.0f, 0.0f, 0.0f }, 0, 0, 0);
-            const float dd = mix_mul(w[t].dw, xd);
-            if constexpr (TYPE == 14) {
+            const float dd = mix_mul(w[t].dw, xd[k]);
 #pragma unroll
-                for (int v = 0; v < 4; v++) acc[t][p][v] = __builtin_fmaf(S[v] * w[t].sc, dd, acc[t][p][v]);
-                /* sc[2g]*s16[0] + sc[2g+1]*s16[1] in one packed int16 dot */
-                const uint32_t s16p = dx.z;       /* (bit_cast of a vector element itself reads .x) */
-                const int ssum = __builtin_amdgcn_sdot2(__builtin_bit_cast(short2_t, w[t].sab),
-                                                        __builtin_bit_cast(short2_t, s16p), 0, false);
-                cr[t][p] = __builtin_fmaf(dd, (float)ssum, cr[t][p]);
-            } else {
-#pragma unroll
-                for (int v = 0; v < 4; v++) acc[t][p][v] = __builtin_fmaf(S[v], dd, acc[t][p][v]);
-                if constexpr (TYPE == 3) cr[t][p] = mix_fma_hi(w[t].dw, xds, cr[t][p]);   /* off += m*ds */
-                else cr[t][p] = mix_fma_lo(w[t].dw, xds, cr[t][p]);                     /* corr += d*ds */
-            }
+            for (int v = 0; v < 4; v++) acc[t][p][v] = __builtin_fmaf(S[k][t][v], dd, acc[t][p][v]);
+            if constexpr (TYPE == 3) cr[t][p] = mix_fma_hi(w[t].dw, xds[k], cr[t][p]);   /* off += m*ds */
+            else cr[t][p] = mix_fma_lo(w[t].dw, xds[k], cr[t][p]);                     /* corr += d*ds */
         }
     }
 }

@@ -2,7 +2,7 @@
 GPU: every intermediate bit for bit against the oracle, like the exact path.
 
 The MFMA kernels run for QMSG_PATH_MFMA at any batch of two or more tokens; the default path
-takes them for gate/up from 7 slots per active expert and for down from 3, so the 64-token
+takes them for gate/up from 7 slots per active expert and for down from 2, so the 33- to 64-token
 cases also run the row-kernel gate/up followed by the MFMA down. Cases cover Q4_0 / Q4_1 /
 Q6_K down rows, tiles of up to 32 slots run as 16-slot blocks, odd slot
 counts per expert, the Zipf-skewed 512-token prefill, shapes whose down rows fall back to the
