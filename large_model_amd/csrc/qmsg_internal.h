@@ -96,8 +96,8 @@ struct Scratch {
     Q8 *aq;             /* [Tm*K][F/32]        */
     uint8_t *aqk;       /* [Tm*K][F/64][96]    */
     float *dn;          /* [Tm*K][E]           */
-    uint8_t *mxx;       /* [Tm][E/32][128] MFMA records of the layer input */
-    uint8_t *mxa;       /* [Tm*K][F/32][128] MFMA records of the activations */
+    uint8_t *mxx;       /* [Tm][E/32][kMxRec] MFMA records of the layer input */
+    uint8_t *mxa;       /* [Tm*K][F/32][kMxRec] MFMA records of the activations */
 };
 
 struct Shape {

@@ -653,6 +653,106 @@ __global__ __launch_bounds__(64) void dispatch_kernel(SelectArgs a)
     dispatch_slots(a, a.S.sel, cnt, cur, tok);
 }
 
+/* Inclusive sum over the block's first kMaxExperts threads (4 waves); others return 0. */
+__device__ __forceinline__ int experts_scan(int v, int *wsum)
+{
+    const int tid = threadIdx.x, lane = tid & 63;
+    int incl = 0;
+    if (tid < kMaxExperts) {
+        incl = wave_scan_add(v);
+        if (lane == 63) wsum[tid >> 6] = incl;
+    }
+    __syncthreads();
+    if (tid < kMaxExperts)
+        for (int j = 0; j < (tid >> 6); j++) incl += wsum[j];
+    __syncthreads();
+    return incl;
+}
+
+/* The same counting sort as dispatch_slots for large batches, on 16 waves: wave w owns a
+ * contiguous run of the (token, selection) entries; the per-wave expert counts and their
+ * prefix (experts ascending, then waves in entry order) give every slot its position, so the
+ * order inside an expert is still token order then selection order (src/model.c:1066-1088). */
+constexpr int kDispWaves = 16;
+__global__ __launch_bounds__(64 * kDispWaves) void dispatch_wide_kernel(SelectArgs a)
+{
+    __shared__ int cw[kDispWaves][kMaxExperts];       /* per-wave counts, then next positions */
+    __shared__ int start[kMaxExperts], tok[kMaxExperts], wsum[4], n_active;
+    const int X = a.X, K = a.K, NS = a.T * K, tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int per = (NS + kDispWaves - 1) / kDispWaves, lo = min(w * per, NS), hi = min(lo + per, NS);
+    for (int i = tid; i < kDispWaves * kMaxExperts; i += 64 * kDispWaves) (&cw[0][0])[i] = 0;
+    for (int e = tid; e < kMaxExperts; e += 64 * kDispWaves) tok[e] = 0;
+    __syncthreads();
+    const unsigned long long below = (1ULL << lane) - 1ULL;
+    /* lanes of this 64-entry chunk with the same expert as this lane's entry */
+    auto group = [&](int i, int e) {
+        unsigned long long same = __ballot(i < hi);
+        for (int bit = 0; bit < 9; bit++) {
+            const unsigned long long b = __ballot(i < hi && ((e >> bit) & 1));
+            same &= ((e >> bit) & 1) ? b : ~b;
+        }
+        return same;
+    };
+    for (int base = lo; base < hi; base += 64) {
+        const int i = base + lane, e = i < hi ? a.S.sel[i] : -1;
+        const unsigned long long same = group(i, e);
+        if (i < hi && (same >> lane) == 1ULL) cw[w][e] += __popcll(same);   /* highest lane of the group */
+        wave_sync();
+    }
+    __syncthreads();
+    /* thread e: the expert's total, start, active index and tile count; per-wave first slots */
+    int tot = 0;
+    if (tid < kMaxExperts && tid < X)
+        for (int v = 0; v < kDispWaves; v++) tot += cw[v][tid];
+    const int incl = experts_scan(tot, wsum);
+    const int act = tot > 0 ? 1 : 0, incl_a = experts_scan(act, wsum);
+    const int nt = (tot + kTileN - 1) / kTileN, incl_t = experts_scan(nt, wsum);
+    if (tid < X) {
+        int run = incl - tot;
+        start[tid] = run;
+        a.S.start[tid] = run;
+        if (act) a.S.active[incl_a - 1] = tid;
+        for (int v = 0; v < kDispWaves; v++) {
+            const int c = cw[v][tid];
+            cw[v][tid] = run;
+            run += c;
+        }
+        if (tid == X - 1) {
+            a.S.start[X] = incl;
+            a.S.meta[0] = incl_a;
+            a.S.meta[1] = incl_t;
+            n_active = incl_a;
+        }
+    }
+    __syncthreads();
+    for (int base = lo; base < hi; base += 64) {
+        const int i = base + lane, e = i < hi ? a.S.sel[i] : -1;
+        const unsigned long long same = group(i, e);
+        int s = 0;
+        if (i < hi) s = cw[w][e] + __popcll(same & below);
+        wave_sync();
+        if (i < hi) {
+            const int t = i / K, k = s - start[e];
+            a.S.slot_t[s] = t;
+            a.S.slot_of[i] = s;
+            if (k < 4) atomicOr(&tok[e], (t & 0xff) << (8 * k));
+            if ((same >> lane) == 1ULL) cw[w][e] += __popcll(same);
+        }
+        wave_sync();
+    }
+    __syncthreads();
+    /* work records per active expert {expert, first slot, end slot, tokens of its first four
+     * slots}, -1 records after them; slot tiles of at most kTileN slots, experts ascending */
+    const int na = n_active;
+    if (tid < X) {
+        if (act) a.S.work[incl_a - 1] = make_int4(tid, start[tid], start[tid] + tot, tok[tid]);
+        if (tid >= na) a.S.work[tid] = make_int4(-1, 0, 0, 0);
+        int tpos = incl_t - nt;
+        for (int b = 0; b < tot; b += kTileN)
+            a.S.tiles[tpos++] = make_int4(tid, start[tid] + b, start[tid] + min(tot, b + kTileN), 0);
+    }
+}
+
 hipError_t launch_select(const Shape &s, const Scratch &S, int T, int gateup_routes, hipStream_t st)
 {
     SelectArgs a;
@@ -664,7 +764,7 @@ hipError_t launch_select(const Shape &s, const Scratch &S, int T, int gateup_rou
     /* up to 64 tokens the last select block also dispatches; larger batches take a separate
      * dispatch launch rather than hundreds of tickets on one counter */
     QLAUNCH("select", select_kernel, dim3(T), dim3(256), 0, st, a, T <= 64 ? 1 : 0);
-    if (T > 64) QLAUNCH("dispatch", dispatch_kernel, dim3(1), dim3(64), 0, st, a);
+    if (T > 64) QLAUNCH("dispatch", dispatch_wide_kernel, dim3(1), dim3(64 * kDispWaves), 0, st, a);
     return hipGetLastError();
 }
 
@@ -2111,9 +2211,9 @@ __host__ __device__ constexpr int mx_wstride(int type) { return type == 14 ? 216
  * flight while the current one computes. */
 __host__ __device__ constexpr int mx_rstride(int type) { return kMxC * kMxRec + (type == 14 ? 64 : 320); }
 
-template <int TYPE, int WSG>
+template <int TYPE, int WSG, int PPW = 4>
 struct MxLayout {
-    static constexpr int RWG = 256 / WSG, SWG = 8 * WSG, WS = mx_wstride(TYPE);
+    static constexpr int RWG = 256 / WSG, SWG = 2 * PPW * WSG, WS = mx_wstride(TYPE);
     static constexpr int RS = mx_rstride(TYPE);
     static constexpr int WBYTES = RWG * WS, BUF = WBYTES + SWG * RS;
     static constexpr int WUNIT = TYPE == 14 ? 4 : 16;                 /* bytes per lane per DMA   */
@@ -2121,9 +2221,9 @@ struct MxLayout {
     static constexpr int WINSTR = (RWG * WUR + 63) / 64;               /* weight DMA instructions  */
 };
 
-__host__ __device__ constexpr int mx_lds_bytes(int type, int wsg)
+__host__ __device__ constexpr int mx_lds_bytes(int type, int wsg, int ppw = 4)
 {
-    return 2 * ((256 / wsg) * mx_wstride(type) + 8 * wsg * mx_rstride(type));
+    return 2 * ((256 / wsg) * mx_wstride(type) + 2 * ppw * wsg * mx_rstride(type));
 }
 
 /* (x & m) | c in one instruction; m and c in registers (no literal operands in VOP3 here). */
@@ -2418,11 +2518,18 @@ __device__ __forceinline__ void mx_wait_barrier()
 /* Gate/up (GU = 1: gate rows against the token's input records, the same up rows, SwiGLU, the
  * int8 activation blocks and their records) or down (GU = 0: dn rows) of one slot tile. Two
  * blocks share a CU (16 waves, four per SIMD), which hides the LDS and memory latency. */
-template <int TYPE, int WSG, int GU>
-__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4, 4))) void mx_kernel(MxArgs a)
+/* Waves per SIMD the MFMA kernel is built for: six where three blocks' LDS fits a CU, else four
+ * (the register budget follows: 80 or 128 VGPRs). */
+template <int TYPE, int WSG, int PPW>
+constexpr int mx_waves() { return 3 * mx_lds_bytes(TYPE, WSG, PPW) <= 160 * 1024 ? 6 : 4; }
+
+template <int TYPE, int WSG, int GU, int PPW>
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(mx_waves<TYPE, WSG, PPW>(),
+                                                                     mx_waves<TYPE, WSG, PPW>())))
+void mx_kernel(MxArgs a)
 {
     extern __shared__ __align__(16) uint8_t smem[];
-    using Lay = MxLayout<TYPE, WSG>;
+    using Lay = MxLayout<TYPE, WSG, PPW>;
     constexpr int RWG = Lay::RWG, SWG = Lay::SWG, WS = Lay::WS, BUF = Lay::BUF;
     if ((int)blockIdx.y >= a.S.meta[1]) return;
     const int4 tl = a.S.tiles[blockIdx.y];
@@ -2486,7 +2593,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4, 4))) voi
     const bool nz = (ka & 3) == lg;
     const int offa_lo = ja * Lay::RS + ((nz && ka < 4) ? 8 * ka : kMxZero);
     const int offa_hi = ja * Lay::RS + ((nz && ka >= 4) ? 8 * ka : kMxZero);
-    const int nw = min(max(ns - 8 * ws, 0), 8), np = (nw + 1) >> 1;      /* this wave's slot pairs */
+    const int nw = min(max(ns - 2 * PPW * ws, 0), 2 * PPW), np = (nw + 1) >> 1;   /* this wave's slot pairs */
 
     /* The whole chunk loop and the row sums for one slot-pair count NP, chosen once per wave,
      * so the accumulators keep their registers from the first chunk to the last. Every wave
@@ -2511,7 +2618,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4, 4))) voi
             if (c + 1 < nch) issue(c + 1, buf ^ 1);
             if constexpr (NP > 0) {
                 const uint8_t *Wl = smem + buf * BUF + (32 * wr) * WS;
-                const uint8_t *Rl = smem + buf * BUF + Lay::WBYTES + (8 * ws) * Lay::RS;
+                const uint8_t *Rl = smem + buf * BUF + Lay::WBYTES + (2 * PPW * ws) * Lay::RS;
                 if constexpr (TYPE == 14) {
                     if (c & 1) mx_chunk_q6<NP, 2>(Wl, Rl, lr, lg, kh, jd, offa_lo, offa_hi, acc, cr);
                     else mx_chunk_q6<NP, 0>(Wl, Rl, lr, lg, kh, jd, offa_lo, offa_hi, acc, cr);
@@ -2533,14 +2640,14 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4, 4))) voi
                     const f32x4 &q = acc[t][p];
                     const float h = ((q[0] + o[0]) + (q[2] + o[2])) + ((q[1] + o[1]) + (q[3] + o[3]));
                     const float val = h - scale * cr[t][p];
-                    const int row = 32 * wr + 16 * t + lr, sl = 8 * ws + 2 * p + jd;
+                    const int row = 32 * wr + 16 * t + lr, sl = 2 * PPW * ws + 2 * p + jd;
                     if (GU) res[row * (SWG + 1) + sl] = val;
                     else if (sl < ns) a.S.dn[(size_t)(s0 + sl) * a.E + R0 + row] = val;
                 }
             }
     };
-    if (np == 4) run(std::integral_constant<int, 4>{});
-    else if (np == 3) run(std::integral_constant<int, 3>{});
+    if (PPW == 4 && np == 4) run(std::integral_constant<int, PPW == 4 ? 4 : 0>{});
+    else if (PPW == 4 && np == 3) run(std::integral_constant<int, PPW == 4 ? 3 : 0>{});
     else if (np == 2) run(std::integral_constant<int, 2>{});
     else if (np == 1) run(std::integral_constant<int, 1>{});
     else run(std::integral_constant<int, 0>{});
@@ -2588,14 +2695,32 @@ template <int TYPE>
 constexpr int mx_wsg() { return 2; }
 static_assert(2 * mx_lds_bytes(14, 2) <= 160 * 1024, "two Q6_K blocks per CU");
 
-template <int TYPE, int GU>
-static void launch_mx(const MxArgs &a, int rows, int maxt, hipStream_t st)
+/* Slot pairs per wave: 4 (16-slot blocks) once the batch averages kMxWidePairs slots per active
+ * expert, else 2 (8-slot blocks, up to three per CU), so that sparse tiles leave fewer waves
+ * without slots. */
+constexpr int kMxWideSlots = 8;
+
+template <int TYPE, int GU, int PPW>
+static void launch_mx_ppw(const MxArgs &a, int rows, int maxt, hipStream_t st)
 {
     constexpr int W = mx_wsg<TYPE>();
-    using Lay = MxLayout<TYPE, W>;
-    const size_t lds = (size_t)mx_lds_bytes(TYPE, W);
-    QLAUNCH(GU ? "gateup" : "down", (mx_kernel<TYPE, W, GU>),
+    using Lay = MxLayout<TYPE, W, PPW>;
+    const size_t lds = (size_t)mx_lds_bytes(TYPE, W, PPW);
+    QLAUNCH(GU ? "gateup" : "down", (mx_kernel<TYPE, W, GU, PPW>),
             dim3(rows / (GU ? Lay::RWG / 2 : Lay::RWG), maxt, kTileN / Lay::SWG), dim3(512), lds, st, a);
+}
+
+template <int TYPE, int GU>
+static void launch_mx(const MxArgs &a, int rows, int maxt, int wide, hipStream_t st)
+{
+    if (wide) launch_mx_ppw<TYPE, GU, 4>(a, rows, maxt, st);
+    else launch_mx_ppw<TYPE, GU, 2>(a, rows, maxt, st);
+}
+
+static int mx_wide(const Shape &s, int T)
+{
+    const int NS = T * s.K, act = s.X < NS ? s.X : NS;
+    return NS >= kMxWideSlots * act;
 }
 
 /* Whether the MFMA kernels take this layer: Q4_0 gate and up; Q4_0, Q4_1 or Q6_K down (Q6_K
@@ -2629,7 +2754,7 @@ hipError_t launch_experts_mx(const Shape &s, const LayerDev &L, const Scratch &S
     a.rec = S.mxx;
     a.rec_out = S.mxa;
     a.S = S;
-    launch_mx<2, 1>(a, s.F, maxt, st);
+    launch_mx<2, 1>(a, s.F, maxt, mx_wide(s, T), st);
     if (!down_mx) {
         const hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
@@ -2641,9 +2766,9 @@ hipError_t launch_experts_mx(const Shape &s, const LayerDev &L, const Scratch &S
     a.eb = L.down_eb;
     a.rec = S.mxa;
     a.rec_out = nullptr;
-    if (L.down_type == 14) launch_mx<14, 0>(a, s.E, maxt, st);
-    else if (L.down_type == 3) launch_mx<3, 0>(a, s.E, maxt, st);
-    else launch_mx<2, 0>(a, s.E, maxt, st);
+    if (L.down_type == 14) launch_mx<14, 0>(a, s.E, maxt, mx_wide(s, T), st);
+    else if (L.down_type == 3) launch_mx<3, 0>(a, s.E, maxt, mx_wide(s, T), st);
+    else launch_mx<2, 0>(a, s.E, maxt, mx_wide(s, T), st);
     const int n = T * s.E;
     QLAUNCH("combine", combine_kernel, dim3((n + 255) / 256), dim3(256), 0, st, S, s.E, s.K, T, out);
     return hipGetLastError();
@@ -2670,9 +2795,9 @@ hipError_t launch_down_mx(const Shape &s, const LayerDev &L, const Scratch &S, f
     a.rec = S.mxa;
     a.rec_out = nullptr;
     a.S = S;
-    if (L.down_type == 14) launch_mx<14, 0>(a, s.E, maxt, st);
-    else if (L.down_type == 3) launch_mx<3, 0>(a, s.E, maxt, st);
-    else launch_mx<2, 0>(a, s.E, maxt, st);
+    if (L.down_type == 14) launch_mx<14, 0>(a, s.E, maxt, mx_wide(s, T), st);
+    else if (L.down_type == 3) launch_mx<3, 0>(a, s.E, maxt, mx_wide(s, T), st);
+    else launch_mx<2, 0>(a, s.E, maxt, mx_wide(s, T), st);
     const int n = T * s.E;
     QLAUNCH("combine", combine_kernel, dim3((n + 255) / 256), dim3(256), 0, st, S, s.E, s.K, T, out);
     return hipGetLastError();
