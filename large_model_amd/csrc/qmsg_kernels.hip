@@ -2543,16 +2543,9 @@ void mx_kernel(MxArgs a)
 
     /* row i of the staged tile: for gate/up, row group g = i / 32 holds gate rows
      * R0 + 16g .. R0 + 16g + 15 and then the same up rows. Byte offsets inside one expert's
-     * matrix fit 32 bits; the expert bases are wave-uniform. */
+     * matrix fit 31 bits (mx_supported); the expert bases are wave-uniform. */
     const uint8_t *wb0 = a.w0 + (size_t)e * a.eb, *wb1 = GU ? a.w1 + (size_t)e * a.eb : wb0;
     const uint32_t rb = (uint32_t)a.rb;
-    auto row_src = [&](int i, uint32_t off) -> const uint8_t * {
-        if (GU) {
-            const int g = i >> 5, within = i & 31;
-            return (within < 16 ? wb0 : wb1) + ((uint32_t)(R0 + 16 * g + (within & 15)) * rb + off);
-        }
-        return wb0 + ((uint32_t)(R0 + i) * rb + off);
-    };
     /* slot i's records (slots past the tile repeat its last slot) */
     auto rec_ptr = [&](int i) -> const uint8_t * {
         const int s = s0 + min(i, ns - 1);
@@ -2564,17 +2557,56 @@ void mx_kernel(MxArgs a)
     const uint8_t *rsrc[RPW];
 #pragma unroll
     for (int j = 0; j < RPW; j++) rsrc[j] = rec_ptr(wave + 8 * j);
+    /* Each lane's weight DMA sources, computed once: unit n = 64q + lane of the staged tile
+     * (row n / WUR, unit n % WUR) for this wave's instructions q = wave, wave + 8, ... Q4 types:
+     * the offset inside the expert's matrix per instruction (bit 31: an up row); Q6_K (down
+     * rows, whose 108 instructions per chunk would take too many registers): the first one,
+     * stepped by 512 units per instruction. */
+    static_assert(RWG * Lay::WUR % 64 == 0, "whole DMA instructions per chunk");
+    constexpr int NQ = (Lay::WINSTR + 7) / 8;
+    uint32_t qoff[TYPE == 14 ? 1 : NQ];
+    int qu = 0;
+    auto unit_off = [&](int n, int *u_out) -> uint32_t {
+        const int i = n / Lay::WUR, u = n - i * Lay::WUR;
+        *u_out = u;
+        const int row = GU ? R0 + 16 * (i >> 5) + (i & 15) : R0 + i;
+        const uint32_t up = GU && (i & 31) >= 16 ? 0x80000000u : 0u;
+        return ((uint32_t)row * rb + (uint32_t)(Lay::WUNIT * u)) | up;
+    };
+    if constexpr (TYPE == 14) {
+        qoff[0] = unit_off(64 * wave + lane, &qu);
+    } else {
+#pragma unroll
+        for (int j = 0; j < NQ; j++) {
+            int u;
+            qoff[j] = unit_off(min(64 * (wave + 8 * j) + lane, RWG * Lay::WUR - 1), &u);
+        }
+    }
     auto issue = [&](int c, int k) {
         uint8_t *base = smem + k * BUF;
-        for (int q = wave; q < Lay::WINSTR; q += 8) {
-            const int n = 64 * q + lane;
-            if (n < RWG * Lay::WUR) {
-                const int i = n / Lay::WUR, u = n - i * Lay::WUR;
-                if constexpr (TYPE == 14) {
-                    /* the super-block starts 2 bytes past a 4-byte boundary on odd chunks */
-                    dma_to_lds<4>(row_src(i, (uint32_t)(c * 210 - 2 * (c & 1) + 4 * u)), base + 256 * q);
-                } else {
-                    dma_to_lds<16>(row_src(i, (uint32_t)(c * (kMxC * (TYPE == 3 ? 20 : 18)) + 16 * u)), base + 1024 * q);
+        if constexpr (TYPE == 14) {
+            /* the super-block starts 2 bytes past a 4-byte boundary on odd chunks */
+            const uint32_t cb = (uint32_t)(c * 210 - 2 * (c & 1));
+            uint32_t o = qoff[0];
+            int u = qu;
+            for (int q = wave; q < Lay::WINSTR; q += 8) {
+                dma_to_lds<4>(wb0 + (o + cb), base + 256 * q);
+                /* 512 units on: 9 rows and 26 units, one row more where the units wrap */
+                u += 512 - 9 * Lay::WUR;
+                o += 9 * rb + 4 * (512 - 9 * Lay::WUR);
+                if (u >= Lay::WUR) {
+                    u -= Lay::WUR;
+                    o += rb - 4 * Lay::WUR;
+                }
+            }
+        } else {
+            const uint32_t cb = (uint32_t)(c * (kMxC * (TYPE == 3 ? 20 : 18)));
+#pragma unroll
+            for (int j = 0; j < NQ; j++) {
+                const int q = wave + 8 * j;
+                if (q < Lay::WINSTR) {
+                    const uint32_t o = qoff[j];
+                    dma_to_lds<16>(((o >> 31) ? wb1 : wb0) + ((o & 0x7fffffffu) + cb), base + 1024 * q);
                 }
             }
         }
@@ -2728,9 +2760,10 @@ static int mx_wide(const Shape &s, int T)
 bool mx_supported(const Shape &s, const LayerDev &L, int *down_mx)
 {
     const int nbE = s.E / 32, nbF = s.F / 32;
-    const bool gu = L.gate_type == 2 && L.up_type == 2 && nbE % kMxC == 0 && s.F % 128 == 0;
+    const bool gu = L.gate_type == 2 && L.up_type == 2 && nbE % kMxC == 0 && s.F % 128 == 0 &&
+                    (uint64_t)s.F * L.gate_rb < (1ull << 31);
     const bool dn = (L.down_type == 2 || L.down_type == 3 || (L.down_type == 14 && L.down_rb % 4 == 0)) &&
-                    nbF % kMxC == 0 && s.E % 256 == 0;
+                    nbF % kMxC == 0 && s.E % 256 == 0 && (uint64_t)s.E * L.down_rb < (1ull << 31);
     if (down_mx) *down_mx = dn;
     return gu;
 }
