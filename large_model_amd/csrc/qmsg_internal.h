@@ -41,8 +41,9 @@ constexpr int kMaxExperts = 256;
 
 /* Slots (tokens of one expert) per slot tile of the batch kernels (dispatch's tile list). */
 constexpr int kTileN = 32;
-/* Bytes of one activation record of the MFMA kernels (one int8 block as f16 codes and scales). */
-constexpr int kMxRec = 96;
+/* Bytes of one activation record of the MFMA kernels (one int8 block as f16 codes, its scales
+ * and the MFMA accumulator inputs). */
+constexpr int kMxRec = 128;
 
 /* The default path takes the MFMA kernels for gate/up from kMxAutoSlots slots per active
  * expert on average, and for down from kMxDownSlots (235B shape, Q4_0 down, per layer: gate/up

@@ -2136,7 +2136,10 @@ hipError_t launch_gateup_tiles(const Shape &s, const LayerDev &L, const Scratch 
  *
  * Activation records (kMxRec bytes per slot, or per token, and 32-block) carry x in that
  * order as f16 (64 bytes), then d, ds and the half sums (16 bytes), then 16 zero bytes, which
- * the lanes of A outside their group read. Gate/up writes the records of the activations it quantises, so the
+ * the lanes of A outside their group read, then -1024 x (the sum of lane k's four codes) for
+ * k = 0..7 (32 bytes): the Q4 kernels feed the B operand as f16 1024 + code and start the MFMA
+ * from those sums, so the result is the lane sums themselves. Q6_K kernels stage the first 96
+ * bytes of each record and subtract 1024 from B instead. Gate/up writes the records of the activations it quantises, so the
  * down products read them directly.
  *
  * A block of 8 waves computes 512/WSG weight rows x 8*WSG slots of one expert's slot tile:
@@ -2151,12 +2154,15 @@ typedef short short2_t __attribute__((ext_vector_type(2)));
 constexpr int kMxC = 8;          /* 32-blocks per staged chunk (one Q6_K super-block) */
 constexpr int kMxDx = 64;        /* offset of the record's d, ds, half sums */
 constexpr int kMxZero = 80;      /* offset of the record's zero words */
-static_assert(kMxRec == 96, "record layout: 64 bytes of codes, 16 of scales, 16 of zeros");
+constexpr int kMxAcc = 96;       /* offset of the record's MFMA accumulator inputs */
+static_assert(kMxRec == 128, "record layout: 64 bytes of codes, 16 of scales, 16 of zeros, 32 of sums");
+/* bytes of one record in LDS: whole for the Q4 kernels, without the sums for Q6_K */
+__host__ __device__ constexpr int mx_recl(int type) { return type == 14 ? 96 : kMxRec; }
 
 /* One int8 block as an activation record (layout above). */
 __device__ void mx_store_record(const Q8Vals &q, uint8_t *rec)
 {
-    u32x4 w[6];
+    u32x4 w[8];
 #pragma unroll
     for (int k = 0; k < 8; k++) {
         const uint32_t c = q.qw[k];
@@ -2165,11 +2171,12 @@ __device__ void mx_store_record(const Q8Vals &q, uint8_t *rec)
         auto h = [](int x) { return (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)(float)x); };
         w[k >> 1][2 * (k & 1)] = h(x0) | (h(x2) << 16);
         w[k >> 1][2 * (k & 1) + 1] = h(x1) | (h(x3) << 16);
+        w[6 + (k >> 2)][k & 3] = __float_as_uint(-1024.0f * (float)(x0 + x1 + x2 + x3));
     }
     w[4] = u32x4{ __float_as_uint(q.d), __float_as_uint(q.ds), q.s16, 0u };
     w[5] = u32x4{ 0u, 0u, 0u, 0u };
 #pragma unroll
-    for (int i = 0; i < 6; i++) ((u32x4 *)rec)[i] = w[i];
+    for (int i = 0; i < 8; i++) ((u32x4 *)rec)[i] = w[i];
 }
 
 /* The layer input's records from its int8 blocks (one thread per block). */
@@ -2209,7 +2216,7 @@ __host__ __device__ constexpr int mx_wstride(int type) { return type == 14 ? 216
  * piece is copied by the LDS DMA (global_load_lds): a wave instruction moves 64 lanes x 16 bytes
  * (Q6_K weights: x 4 bytes) to consecutive LDS bytes. Two buffers: the next chunk's copy is in
  * flight while the current one computes. */
-__host__ __device__ constexpr int mx_rstride(int type) { return kMxC * kMxRec + (type == 14 ? 64 : 320); }
+__host__ __device__ constexpr int mx_rstride(int type) { return kMxC * mx_recl(type) + 64; }
 
 template <int TYPE, int WSG, int PPW = 4>
 struct MxLayout {
@@ -2262,7 +2269,7 @@ typedef __attribute__((address_space(3))) const u32x4 LdsU32x4;
  * word, from two LDS pointers: pq at the lane's code word of the block in tile row lr (Q4_0
  * even blocks: 2 bytes past a word boundary), pd at the block's scale word; tile t is an
  * immediate offset. */
-template <int TYPE, int PAR>
+template <int TYPE, int PAR, int USEC>
 __device__ __forceinline__ MxB mx_weights_q4(LdsPtr pq, LdsPtr pd, int t)
 {
     constexpr int WS = mx_wstride(TYPE);
@@ -2276,8 +2283,12 @@ __device__ __forceinline__ MxB mx_weights_q4(LdsPtr pq, LdsPtr pd, int t)
         const uint32_t a1 = *(const __attribute__((address_space(3))) uint32_t *)(pq + 16 * t * WS + 2);
         v = __builtin_amdgcn_alignbyte(a1, a0, 2);
     }
-    w.op = mx_pack_codes(and_or(v, m4, bias), and_or(v >> 8, m4, bias), and_or(v >> 4, m4, bias),
-                         and_or(v >> 12, m4, bias));
+    /* f16 1024 + code; USEC: the MFMA starts from -1024 x the lane's code sum (the record's
+     * sums), else the 1024 is subtracted here */
+    const uint32_t b0 = and_or(v, m4, bias), b1 = and_or(v >> 8, m4, bias), b2 = and_or(v >> 4, m4, bias),
+                   b3 = and_or(v >> 12, m4, bias);
+    if constexpr (USEC) w.op = __builtin_bit_cast(f16x8, u32x4{ b0, b1, b2, b3 });
+    else w.op = mx_pack_codes(b0, b1, b2, b3);
     if constexpr (TYPE == 3) w.dw = *(const __attribute__((address_space(3))) uint32_t *)(pd + 16 * t * WS);
     else w.dw = *(const __attribute__((address_space(3))) uint16_t *)(pd + 16 * t * WS);
     w.sc = 0.0f;
@@ -2317,27 +2328,27 @@ __device__ __forceinline__ float mix_fma_hi(uint32_t h, float f, float c)
  * Q4_0 / Q4_1 the code word and the scale word of tile row lr (the tile t adds 16t rows). One
  * trip covers two blocks; the second block and the pairs and tiles are immediate offsets. */
 struct MxStreams {
-    LdsPtr alo, ahi, d, q, dw;
+    LdsPtr alo, ahi, d, q, dw, acc;
 };
 
 /* The empty asm keeps each stream a single register: otherwise every (pair, stream) address
  * becomes a loop variable of its own and the registers run out. */
 __device__ __forceinline__ void mx_opaque(MxStreams &st)
 {
-    asm("" : "+v"(st.alo), "+v"(st.ahi), "+v"(st.d), "+v"(st.q), "+v"(st.dw));
+    asm("" : "+v"(st.alo), "+v"(st.ahi), "+v"(st.d), "+v"(st.q), "+v"(st.dw), "+v"(st.acc));
 }
 
 /* One block b (parity PAR within the trip) of the staged chunk: NP slot pairs of this wave
  * against its two 16-row tiles. */
-template <int TYPE, int NP, int O, int PAR>
+template <int TYPE, int NP, int O, int PAR, int USEC>
 __device__ __forceinline__ void mx_block(int b, const MxStreams &st, const uint8_t *W, int lr, int lg, int kh,
                                          f32x4 (&acc)[2][4], float (&cr)[2][4])
 {
     static_assert(TYPE == 2 || TYPE == 3, "Q6_K chunks take mx_chunk_q6");
-    constexpr int BB = TYPE == 3 ? 20 : 18, RB = PAR * kMxRec, RS = mx_rstride(TYPE);
+    constexpr int BB = TYPE == 3 ? 20 : 18, RB = PAR * mx_recl(TYPE), RS = mx_rstride(TYPE);
     MxB w[2];
 #pragma unroll
-    for (int t = 0; t < 2; t++) w[t] = mx_weights_q4<TYPE, PAR>(st.q + PAR * BB, st.dw + PAR * BB, t);
+    for (int t = 0; t < 2; t++) w[t] = mx_weights_q4<TYPE, PAR, USEC>(st.q + PAR * BB, st.dw + PAR * BB, t);
     /* pair p's two MFMAs are issued before pair p-1's results are used, so the chains of one
      * pair run while the matrix core works on the next */
     f32x4 S[2][2];
@@ -2346,12 +2357,13 @@ __device__ __forceinline__ void mx_block(int b, const MxStreams &st, const uint8
         const u32x2 lo = *(const LdsU32x2 *)(st.alo + RB + 2 * p * RS);
         const u32x2 hi = *(const LdsU32x2 *)(st.ahi + RB + 2 * p * RS);
         const u32x2 d2 = *(const LdsU32x2 *)(st.d + RB + 2 * p * RS);          /* d, ds */
+        f32x4 c0 = f32x4{ 0.0f, 0.0f, 0.0f, 0.0f };
+        if constexpr (USEC) c0 = *(const __attribute__((address_space(3))) f32x4 *)(st.acc + RB + 2 * p * RS);
         const f16x8 aop = __builtin_bit_cast(f16x8, u32x4{ lo.x, lo.y, hi.x, hi.y });
         xd[k] = __uint_as_float(d2.x);
         xds[k] = __uint_as_float(d2.y);
 #pragma unroll
-        for (int t = 0; t < 2; t++)
-            S[k][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(aop, w[t].op, f32x4{ 0.0f, 0.0f, 0.0f, 0.0f }, 0, 0, 0);
+        for (int t = 0; t < 2; t++) S[k][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(aop, w[t].op, c0, 0, 0, 0);
     };
     issue(0, 0);
 #pragma unroll
@@ -2371,7 +2383,7 @@ __device__ __forceinline__ void mx_block(int b, const MxStreams &st, const uint8
 
 /* One staged chunk (kMxC blocks), two blocks per loop trip. A lane's A words are its x words
  * where it holds x, else the record's zero words. */
-template <int TYPE, int NP, int O>
+template <int TYPE, int NP, int O, int USEC>
 __device__ __forceinline__ void mx_chunk(const uint8_t *W, const uint8_t *R, int lr, int lg, int kh, int jd,
                                          int offa_lo, int offa_hi, f32x4 (&acc)[2][4], float (&cr)[2][4])
 {
@@ -2382,15 +2394,17 @@ __device__ __forceinline__ void mx_chunk(const uint8_t *W, const uint8_t *R, int
     st.d = (LdsPtr)(R + jd * mx_rstride(TYPE) + kMxDx);
     st.q = (LdsPtr)(W + lr * WS + QO + 4 * lg);
     st.dw = (LdsPtr)(W + lr * WS);
+    st.acc = (LdsPtr)(R + jd * mx_rstride(TYPE) + kMxAcc + 16 * kh);   /* -1024 x sums of lanes 4kh.. */
 #pragma unroll 1
     for (int b = 0; b < kMxC; b += 2) {
         mx_opaque(st);
-        mx_block<TYPE, NP, O, 0>(b, st, W, lr, lg, kh, acc, cr);
+        mx_block<TYPE, NP, O, 0, USEC>(b, st, W, lr, lg, kh, acc, cr);
         __builtin_amdgcn_sched_barrier(0);      /* one block's operands in registers at a time */
-        mx_block<TYPE, NP, O, 1>(b + 1, st, W, lr, lg, kh, acc, cr);
-        st.alo += 2 * kMxRec;
-        st.ahi += 2 * kMxRec;
-        st.d += 2 * kMxRec;
+        mx_block<TYPE, NP, O, 1, USEC>(b + 1, st, W, lr, lg, kh, acc, cr);
+        st.alo += 2 * mx_recl(TYPE);
+        st.ahi += 2 * mx_recl(TYPE);
+        st.d += 2 * mx_recl(TYPE);
+        st.acc += 2 * mx_recl(TYPE);
         st.q += 2 * BB;
         st.dw += 2 * BB;
     }
@@ -2440,7 +2454,7 @@ __device__ __forceinline__ MxB mx_weights_q6(LdsPtr q, LdsPtr rb, int t, int kh)
 template <int NP, int O, int B>
 __device__ __forceinline__ void mx_block_q6(const MxStreams &st, int kh, f32x4 (&acc)[2][4], float (&cr)[2][4])
 {
-    constexpr int RS = mx_rstride(14), RB = B * kMxRec;
+    constexpr int RS = mx_rstride(14), RB = B * mx_recl(14);
     MxB w[2];
 #pragma unroll
     for (int t = 0; t < 2; t++) w[t] = mx_weights_q6<O, B>(st.q, st.dw, t, kh);
@@ -2481,6 +2495,7 @@ __device__ __forceinline__ void mx_chunk_q6(const uint8_t *W, const uint8_t *R, 
     st.d = (LdsPtr)(R + jd * mx_rstride(14) + kMxDx);
     st.q = (LdsPtr)(W + lr * WS + 4 * lg);
     st.dw = (LdsPtr)(W + lr * WS);
+    st.acc = st.d;                          /* (Q6_K starts its MFMAs from zero) */
     mx_opaque(st);
     mx_block_q6<NP, O, 0>(st, kh, acc, cr);
     __builtin_amdgcn_sched_barrier(0);
@@ -2611,10 +2626,12 @@ void mx_kernel(MxArgs a)
             }
         }
         /* a slot's kMxC records: 48 lanes x 16 bytes */
-        if (lane < kMxC * kMxRec / 16) {
+        if (lane < kMxC * mx_recl(TYPE) / 16) {
+            /* Q4: whole records, 64 lanes; Q6_K: the first 96 bytes of each, 48 lanes */
+            const uint32_t src = TYPE == 14 ? (uint32_t)((lane / 6) * kMxRec + 16 * (lane % 6)) : (uint32_t)(16 * lane);
 #pragma unroll
             for (int j = 0; j < RPW; j++)
-                dma_to_lds<16>(rsrc[j] + (size_t)c * kMxC * kMxRec + 16 * lane,
+                dma_to_lds<16>(rsrc[j] + (size_t)c * kMxC * kMxRec + src,
                                base + Lay::WBYTES + (wave + 8 * j) * Lay::RS);
         }
     };
@@ -2655,7 +2672,9 @@ void mx_kernel(MxArgs a)
                     if (c & 1) mx_chunk_q6<NP, 2>(Wl, Rl, lr, lg, kh, jd, offa_lo, offa_hi, acc, cr);
                     else mx_chunk_q6<NP, 0>(Wl, Rl, lr, lg, kh, jd, offa_lo, offa_hi, acc, cr);
                 } else {
-                    mx_chunk<TYPE, NP, 0>(Wl, Rl, lr, lg, kh, jd, offa_lo, offa_hi, acc, cr);
+                    /* gate/up starts its MFMAs from the records' sums; down, whose registers
+                     * are tighter, subtracts the bias from B (measured both ways) */
+                    mx_chunk<TYPE, NP, 0, GU>(Wl, Rl, lr, lg, kh, jd, offa_lo, offa_hi, acc, cr);
                 }
             }
             mx_wait_barrier();       /* chunk c+1 has landed; buffer c is free for chunk c+2 */
