@@ -3863,20 +3863,57 @@ hipError_t launch_rmsnorm_rows(float *x, int T, int E, float eps, hipStream_t st
     return hipGetLastError();
 }
 
-/* src/model.c:403-409 into another buffer, with a weight vector (nullptr: unit): each row
- * staged in LDS, its sum of squares the reference's sequential double FMA chain (one lane),
- * then y = (float)(x * inv) * w in float. */
+/* Sum of q[0..n) in index order, one double add after another (n a multiple of 32); the next
+ * 16 terms are read from LDS while the current 16 are added, so only the adds' latency is on
+ * the chain. */
+__device__ __forceinline__ double ordered_sum(const double *q, int n)
+{
+    double ss = 0.0, a[16], b[16];
+#pragma unroll
+    for (int j = 0; j < 16; j++) a[j] = q[j];
+    for (int base = 0; base < n; base += 32) {
+#pragma unroll
+        for (int j = 0; j < 16; j++) b[j] = q[base + 16 + j];
+#pragma unroll
+        for (int j = 0; j < 16; j++) ss += a[j];
+        if (base + 32 < n) {
+#pragma unroll
+            for (int j = 0; j < 16; j++) a[j] = q[base + 32 + j];
+        }
+#pragma unroll
+        for (int j = 0; j < 16; j++) ss += b[j];
+    }
+    return ss;
+}
+
+/* rmsnorm of one row per block into another buffer, with a weight vector (nullptr: unit)
+ * (src/model.c:403-409): y = (float)(x * inv) * w. ss accumulates (double)x*(double)x in index
+ * order; each square is exact in double (48 significant bits), so the reference's
+ * fma(x, x, ss) equals ss + x*x with the square formed first: every thread forms squares into
+ * LDS, and one lane runs the ordered sum. */
 __global__ void rmsnorm_kernel(const float *x, const float *w, float *y, int E, float eps)
 {
-    extern __shared__ __align__(16) float xs[];
+    extern __shared__ __align__(16) float xs[];      /* [E] x, then [E] squares as double */
     __shared__ double inv;
     const float *row = x + (size_t)blockIdx.x * E;
-    for (int i = threadIdx.x; i < E / 4; i += blockDim.x) ((float4 *)xs)[i] = ((const float4 *)row)[i];
+    double *q = (double *)(xs + E + (E & 1));
+    for (int i = threadIdx.x; i < E / 4; i += blockDim.x) {
+        const float4 v = ((const float4 *)row)[i];
+        ((float4 *)xs)[i] = v;
+        q[4 * i] = (double)v.x * (double)v.x;
+        q[4 * i + 1] = (double)v.y * (double)v.y;
+        q[4 * i + 2] = (double)v.z * (double)v.z;
+        q[4 * i + 3] = (double)v.w * (double)v.w;
+    }
     __syncthreads();
     if (threadIdx.x == 0) {
-        double ss = 0.0;
-#pragma unroll 16
-        for (int i = 0; i < E; i++) ss = __builtin_fma((double)xs[i], (double)xs[i], ss);
+        double ss;
+        if (E % 32 == 0) {
+            ss = ordered_sum(q, E);
+        } else {
+            ss = 0.0;
+            for (int i = 0; i < E; i++) ss += q[i];
+        }
         inv = 1.0 / sqrt(ss / E + (double)eps);
     }
     __syncthreads();
@@ -3889,7 +3926,7 @@ hipError_t launch_rmsnorm(const float *x, const float *w, float *y, int T, int E
 {
     if (T <= 0) return hipSuccess;
     if (E % 4) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(rmsnorm_kernel, dim3(T), dim3(256), (size_t)E * 4, st, x, w, y, E, eps);
+    hipLaunchKernelGGL(rmsnorm_kernel, dim3(T), dim3(256), (size_t)E * 4 + 4 + (size_t)E * 8, st, x, w, y, E, eps);
     return hipGetLastError();
 }
 
