@@ -2218,9 +2218,9 @@ __host__ __device__ constexpr int mx_wstride(int type) { return type == 14 ? 216
  * flight while the current one computes. */
 __host__ __device__ constexpr int mx_rstride(int type) { return kMxC * mx_recl(type) + 64; }
 
-template <int TYPE, int WSG, int PPW = 4>
+template <int TYPE, int WSG, int PPW = 4, int NW = 8>
 struct MxLayout {
-    static constexpr int RWG = 256 / WSG, SWG = 2 * PPW * WSG, WS = mx_wstride(TYPE);
+    static constexpr int RWG = 32 * NW / WSG, SWG = 2 * PPW * WSG, WS = mx_wstride(TYPE);
     static constexpr int RS = mx_rstride(TYPE);
     static constexpr int WBYTES = RWG * WS, BUF = WBYTES + SWG * RS;
     static constexpr int WUNIT = TYPE == 14 ? 4 : 16;                 /* bytes per lane per DMA   */
@@ -2228,9 +2228,9 @@ struct MxLayout {
     static constexpr int WINSTR = (RWG * WUR + 63) / 64;               /* weight DMA instructions  */
 };
 
-__host__ __device__ constexpr int mx_lds_bytes(int type, int wsg, int ppw = 4)
+__host__ __device__ constexpr int mx_lds_bytes(int type, int wsg, int ppw = 4, int nw = 8)
 {
-    return 2 * ((256 / wsg) * mx_wstride(type) + 2 * ppw * wsg * mx_rstride(type));
+    return 2 * ((32 * nw / wsg) * mx_wstride(type) + 2 * ppw * wsg * mx_rstride(type));
 }
 
 /* (x & m) | c in one instruction; m and c in registers (no literal operands in VOP3 here). */
@@ -2535,16 +2535,16 @@ __device__ __forceinline__ void mx_wait_barrier()
  * blocks share a CU (16 waves, four per SIMD), which hides the LDS and memory latency. */
 /* Waves per SIMD the MFMA kernel is built for: six where three blocks' LDS fits a CU, else four
  * (the register budget follows: 80 or 128 VGPRs). */
-template <int TYPE, int WSG, int PPW>
-constexpr int mx_waves() { return 3 * mx_lds_bytes(TYPE, WSG, PPW) <= 160 * 1024 ? 6 : 4; }
+template <int TYPE, int WSG, int PPW, int NW>
+constexpr int mx_waves() { return (160 * 1024 / mx_lds_bytes(TYPE, WSG, PPW, NW)) * NW / 4 >= 6 ? 6 : 4; }
 
-template <int TYPE, int WSG, int GU, int PPW>
-__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(mx_waves<TYPE, WSG, PPW>(),
-                                                                     mx_waves<TYPE, WSG, PPW>())))
+template <int TYPE, int WSG, int GU, int PPW, int NW>
+__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(mx_waves<TYPE, WSG, PPW, NW>(),
+                                                                         mx_waves<TYPE, WSG, PPW, NW>())))
 void mx_kernel(MxArgs a)
 {
     extern __shared__ __align__(16) uint8_t smem[];
-    using Lay = MxLayout<TYPE, WSG, PPW>;
+    using Lay = MxLayout<TYPE, WSG, PPW, NW>;
     constexpr int RWG = Lay::RWG, SWG = Lay::SWG, WS = Lay::WS, BUF = Lay::BUF;
     if ((int)blockIdx.y >= a.S.meta[1]) return;
     const int4 tl = a.S.tiles[blockIdx.y];
@@ -2568,17 +2568,18 @@ void mx_kernel(MxArgs a)
     };
     /* the DMA of chunk c into buffer k: weight instruction q goes to wave q % 8, the records of
      * slot i (one instruction) to wave i % 8, their source fixed per block */
-    constexpr int RPW = SWG / 8;                      /* slots whose records one wave copies */
+    constexpr int RPW = SWG / NW;                     /* slots whose records one wave copies */
+    static_assert(RPW >= 1 && SWG % NW == 0, "every slot's records copied by one wave");
     const uint8_t *rsrc[RPW];
 #pragma unroll
-    for (int j = 0; j < RPW; j++) rsrc[j] = rec_ptr(wave + 8 * j);
+    for (int j = 0; j < RPW; j++) rsrc[j] = rec_ptr(wave + NW * j);
     /* Each lane's weight DMA sources, computed once: unit n = 64q + lane of the staged tile
      * (row n / WUR, unit n % WUR) for this wave's instructions q = wave, wave + 8, ... Q4 types:
      * the offset inside the expert's matrix per instruction (bit 31: an up row); Q6_K (down
      * rows, whose 108 instructions per chunk would take too many registers): the first one,
      * stepped by 512 units per instruction. */
     static_assert(RWG * Lay::WUR % 64 == 0, "whole DMA instructions per chunk");
-    constexpr int NQ = (Lay::WINSTR + 7) / 8;
+    constexpr int NQ = (Lay::WINSTR + NW - 1) / NW;
     uint32_t qoff[TYPE == 14 ? 1 : NQ];
     int qu = 0;
     auto unit_off = [&](int n, int *u_out) -> uint32_t {
@@ -2594,7 +2595,7 @@ void mx_kernel(MxArgs a)
 #pragma unroll
         for (int j = 0; j < NQ; j++) {
             int u;
-            qoff[j] = unit_off(min(64 * (wave + 8 * j) + lane, RWG * Lay::WUR - 1), &u);
+            qoff[j] = unit_off(min(64 * (wave + NW * j) + lane, RWG * Lay::WUR - 1), &u);
         }
     }
     auto issue = [&](int c, int k) {
@@ -2604,11 +2605,13 @@ void mx_kernel(MxArgs a)
             const uint32_t cb = (uint32_t)(c * 210 - 2 * (c & 1));
             uint32_t o = qoff[0];
             int u = qu;
-            for (int q = wave; q < Lay::WINSTR; q += 8) {
+            /* 64 NW units on: STEP / WUR rows and STEP % WUR units, one row more where the
+             * units wrap */
+            constexpr int STEP = 64 * NW, SR = STEP / Lay::WUR, SU = STEP % Lay::WUR;
+            for (int q = wave; q < Lay::WINSTR; q += NW) {
                 dma_to_lds<4>(wb0 + (o + cb), base + 256 * q);
-                /* 512 units on: 9 rows and 26 units, one row more where the units wrap */
-                u += 512 - 9 * Lay::WUR;
-                o += 9 * rb + 4 * (512 - 9 * Lay::WUR);
+                u += SU;
+                o += SR * rb + 4 * SU;
                 if (u >= Lay::WUR) {
                     u -= Lay::WUR;
                     o += rb - 4 * Lay::WUR;
@@ -2618,7 +2621,7 @@ void mx_kernel(MxArgs a)
             const uint32_t cb = (uint32_t)(c * (kMxC * (TYPE == 3 ? 20 : 18)));
 #pragma unroll
             for (int j = 0; j < NQ; j++) {
-                const int q = wave + 8 * j;
+                const int q = wave + NW * j;
                 if (q < Lay::WINSTR) {
                     const uint32_t o = qoff[j];
                     dma_to_lds<16>(((o >> 31) ? wb1 : wb0) + ((o & 0x7fffffffu) + cb), base + 1024 * q);
@@ -2632,7 +2635,7 @@ void mx_kernel(MxArgs a)
 #pragma unroll
             for (int j = 0; j < RPW; j++)
                 dma_to_lds<16>(rsrc[j] + (size_t)c * kMxC * kMxRec + src,
-                               base + Lay::WBYTES + (wave + 8 * j) * Lay::RS);
+                               base + Lay::WBYTES + (wave + NW * j) * Lay::RS);
         }
     };
 
@@ -2709,7 +2712,7 @@ void mx_kernel(MxArgs a)
      * fr / 16: gate at res row 32 (fr / 16) + fr % 16, up 16 rows further. */
     const int F = a.F, nbF = F >> 5;
     auto gate_row = [](int fr) { return 32 * (fr >> 4) + (fr & 15); };
-    for (int i = tid; i < (RWG / 2) * SWG; i += 512) {
+    for (int i = tid; i < (RWG / 2) * SWG; i += 64 * NW) {
         const int fr = i / SWG, sl = i - fr * SWG;
         if (sl >= ns) continue;
         const float gv = res[gate_row(fr) * (SWG + 1) + sl], uv = res[(gate_row(fr) + 16) * (SWG + 1) + sl];
@@ -2724,7 +2727,7 @@ void mx_kernel(MxArgs a)
     }
     __syncthreads();
     constexpr int NFB = RWG / 64;                                  /* activation blocks per slot */
-    for (int i = tid; i < SWG * NFB; i += 512) {
+    for (int i = tid; i < SWG * NFB; i += 64 * NW) {
         const int sl = i / NFB, g = i - sl * NFB;
         if (sl >= ns) continue;
         float v[32];
@@ -2746,26 +2749,29 @@ template <int TYPE>
 constexpr int mx_wsg() { return 2; }
 static_assert(2 * mx_lds_bytes(14, 2) <= 160 * 1024, "two Q6_K blocks per CU");
 
-/* Slot pairs per wave: 4 (16-slot blocks) once the batch averages kMxWidePairs slots per active
+/* Slot pairs per wave: 4 (16-slot blocks) once the batch averages kMxWideSlots slots per active
  * expert, else 2 (8-slot blocks, up to three per CU), so that sparse tiles leave fewer waves
  * without slots. */
 constexpr int kMxWideSlots = 8;
 
-template <int TYPE, int GU, int PPW>
-static void launch_mx_ppw(const MxArgs &a, int rows, int maxt, hipStream_t st)
+template <int TYPE, int GU, int WSG, int PPW, int NW>
+static void launch_mx_shape(const MxArgs &a, int rows, int maxt, hipStream_t st)
 {
-    constexpr int W = mx_wsg<TYPE>();
-    using Lay = MxLayout<TYPE, W, PPW>;
-    const size_t lds = (size_t)mx_lds_bytes(TYPE, W, PPW);
-    QLAUNCH(GU ? "gateup" : "down", (mx_kernel<TYPE, W, GU, PPW>),
-            dim3(rows / (GU ? Lay::RWG / 2 : Lay::RWG), maxt, kTileN / Lay::SWG), dim3(512), lds, st, a);
+    using Lay = MxLayout<TYPE, WSG, PPW, NW>;
+    const size_t lds = (size_t)mx_lds_bytes(TYPE, WSG, PPW, NW);
+    QLAUNCH(GU ? "gateup" : "down", (mx_kernel<TYPE, WSG, GU, PPW, NW>),
+            dim3(rows / (GU ? Lay::RWG / 2 : Lay::RWG), maxt, kTileN / Lay::SWG), dim3(64 * NW), lds, st, a);
 }
 
+/* Blocks of 8 waves and 128 rows: 16 slots (wide) or 8. Measured at the 512-token prefill
+ * against other shapes of the same kernel: 32-slot blocks of 16 waves (one per CU) 1.76 ms for
+ * gate/up, 64-row blocks of 4 waves (three per CU) 1.25, 128-row 8-slot blocks of 4 waves 1.80,
+ * against 1.24 here. */
 template <int TYPE, int GU>
 static void launch_mx(const MxArgs &a, int rows, int maxt, int wide, hipStream_t st)
 {
-    if (wide) launch_mx_ppw<TYPE, GU, 4>(a, rows, maxt, st);
-    else launch_mx_ppw<TYPE, GU, 2>(a, rows, maxt, st);
+    if (wide) launch_mx_shape<TYPE, GU, 2, 4, 8>(a, rows, maxt, st);
+    else launch_mx_shape<TYPE, GU, 2, 2, 8>(a, rows, maxt, st);
 }
 
 static int mx_wide(const Shape &s, int T)
