@@ -20,6 +20,7 @@ CASES = [
     ("q30b_t64", 2048, 128, 8, 768, 64, 1, orc.T_Q4_0, False),
     ("q30b_t128", 2048, 128, 8, 768, 128, 11, orc.T_Q4_0, False),    # 8 slots per expert: both on MFMA
     ("q235b_t64", 4096, 128, 8, 1536, 64, 2, orc.T_Q4_0, False),
+    ("q235b_t16", 4096, 128, 8, 1536, 16, 12, orc.T_Q4_0, False),    # about one slot per expert
     ("q235b_t33", 4096, 128, 8, 1536, 33, 3, orc.T_Q4_0, False),
     ("q235b_q6k_t64", 4096, 128, 8, 1536, 64, 6, orc.T_Q6_K, False),
     ("q235b_q41_t64", 4096, 128, 8, 1536, 64, 7, orc.T_Q4_1, False),
