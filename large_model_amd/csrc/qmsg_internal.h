@@ -45,20 +45,22 @@ constexpr int kTileN = 32;
  * and the MFMA accumulator inputs). */
 constexpr int kMxRec = 128;
 
-/* The default path takes the MFMA kernels for gate/up from kMxAutoSlots slots per active
- * expert on average, and for down from kMxDownSlots (235B shape, Q4_0 down, per layer: gate/up
- * on MFMA against the row kernels 573 / 553 us at 6 slots per expert, 616 / 734 at 8, 709 /
- * 1080 at 12, 1545 / 2697 at 32 (the Zipf prefill); down 158 / 184 at 3 slots per expert,
- * 133 / 133 at 2; Q6_K down 248 / 300 at 2, 336 / 500 at 4). */
-constexpr int kMxAutoSlots = 7;
+/* The default path takes the MFMA kernels for gate/up once a batch averages kMxAutoQuarters / 4
+ * slots per active expert, for Q4_0 / Q4_1 down from kMxDownSlots, and for Q6_K down at every batch
+ * they take (235B shape, per layer, MFMA against the row kernels: gate/up 221 / 216 us at 2 slots
+ * per expert (32 tokens), 236 / 240 at 2.25, 298 / 380 at 4, 364 / 550 at 6; Q4_0 down 86 / 79 at
+ * 1 slot, 105 / 105 at 1.5, 121 / 131 at 2; Q4_1 down 89 / 84 at 1, 124 / 137 at 2; Q6_K down
+ * 37.4 / 37.8 at 2 tokens, 103 / 114 at 8, 306 / 501 at 64). */
+constexpr int kMxAutoQuarters = 9;
 constexpr int kMxDownSlots = 2;
 inline bool mx_auto(int T, int K, int X)
 {
     const long NS = (long)T * K, act = X < NS ? X : NS;
-    return NS >= (long)kMxAutoSlots * act;
+    return 4 * NS >= (long)kMxAutoQuarters * act;
 }
-inline bool mx_auto_down(int T, int K, int X)
+inline bool mx_auto_down(int T, int K, int X, int down_type)
 {
+    if (down_type == 14) return true;
     const long NS = (long)T * K, act = X < NS ? X : NS;
     return NS >= (long)kMxDownSlots * act;
 }

@@ -2,8 +2,9 @@
 GPU: every intermediate bit for bit against the oracle, like the exact path.
 
 The MFMA kernels run for QMSG_PATH_MFMA at any batch of two or more tokens; the default path
-takes them for gate/up from 7 slots per active expert and for down from 2, so the 33- to 64-token
-cases also run the row-kernel gate/up followed by the MFMA down. Cases cover Q4_0 / Q4_1 /
+takes them for gate/up from 2.25 slots per active expert, for Q4_0 / Q4_1 down from 2 and for
+Q6_K down at every batch of two or more tokens, so the 33-token and the 8-token Q6_K cases also
+run the row-kernel gate/up followed by the MFMA down. Cases cover Q4_0 / Q4_1 /
 Q6_K down rows, tiles of up to 32 slots run as 16-slot blocks, odd slot
 counts per expert, the Zipf-skewed 512-token prefill, shapes whose down rows fall back to the
 exact kernel (F/32 not a whole number of 8-block chunks), and batches of alternating sizes on
@@ -23,6 +24,7 @@ CASES = [
     ("q235b_t16", 4096, 128, 8, 1536, 16, 12, orc.T_Q4_0, False),    # about one slot per expert
     ("q235b_t33", 4096, 128, 8, 1536, 33, 3, orc.T_Q4_0, False),
     ("q235b_q6k_t64", 4096, 128, 8, 1536, 64, 6, orc.T_Q6_K, False),
+    ("q235b_q6k_t8", 4096, 128, 8, 1536, 8, 13, orc.T_Q6_K, False),   # Q6_K down on MFMA below one slot
     ("q235b_q41_t64", 4096, 128, 8, 1536, 64, 7, orc.T_Q4_1, False),
     ("q480b_t48", 6144, 160, 8, 2560, 48, 8, orc.T_Q4_0, False),
     ("tiny_t40", 256, 16, 4, 128, 40, 9, orc.T_Q4_0, False),         # down on the exact kernel
@@ -53,7 +55,7 @@ def test_mfma_bit_exact(q, name, E, X, K, F, T, seed, dt, zipf):
         ctx.synth(0, seed, down_type=dt, router_col0=col0)
         ctx.set_path(q.PATH_MFMA)
         out, got = ctx.moe_debug(0, x)
-        ctx.set_path(q.PATH_AUTO)        # below 7 slots per expert: row-kernel gate/up, MFMA down
+        ctx.set_path(q.PATH_AUTO)        # per stage: row kernels or MFMA by slots per expert
         out_auto, got_auto = ctx.moe_debug(0, x)
     for path, o, g in (("mfma", out, got), ("default", out_auto, got_auto)):
         for k in ("sel", "start", "slot_t", "slot_of", "active"):
