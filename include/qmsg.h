@@ -77,9 +77,9 @@ typedef struct qmsg_ctx qmsg_ctx;
  *   MFMA:  the lane sums of 16 rows x 2 slots per f16 MFMA (exact small integers), the same
  *          fp32 chains on the VALU; for batches of two or more tokens with Q4_0 gate and up
  *          (down Q4_0, Q4_1 or Q6_K; other down rows on the EXACT kernel).
- *   AUTO:  per stage: gate/up on MFMA for batches averaging at least 2.25 slots per active
- *          expert, Q4_0 / Q4_1 down from 2, Q6_K down at every batch of two or more tokens,
- *          EXACT otherwise.
+ *   AUTO:  per stage: gate/up on MFMA for batches averaging at least 1.25 slots per active
+ *          expert, down on MFMA for batches of at least 32 slots (tokens x n_used), EXACT
+ *          otherwise.
  *   FP32:  the reference's --exact mode (qms_exact_math = 1, src/quant.c:95-115,
  *          model.c:1009-1030): router, gate/up and down rows dequantised to fp32 and dotted in
  *          one FMA chain per row (matmul_exact), fp32 activations, no int8 blocks; bit-identical

@@ -46,24 +46,19 @@ constexpr int kTileN = 32;
 constexpr int kMxRec = 128;
 
 /* The default path takes the MFMA kernels for gate/up once a batch averages kMxAutoQuarters / 4
- * slots per active expert, for Q4_0 / Q4_1 down from kMxDownSlots, and for Q6_K down at every batch
- * they take (235B shape, per layer, MFMA against the row kernels: gate/up 221 / 216 us at 2 slots
- * per expert (32 tokens), 236 / 240 at 2.25, 298 / 380 at 4, 364 / 550 at 6; Q4_0 down 86 / 79 at
- * 1 slot, 105 / 105 at 1.5, 121 / 131 at 2; Q4_1 down 89 / 84 at 1, 124 / 137 at 2; Q6_K down
- * 37.4 / 37.8 at 2 tokens, 103 / 114 at 8, 306 / 501 at 64). */
-constexpr int kMxAutoQuarters = 9;
-constexpr int kMxDownSlots = 2;
+ * slots per active expert, and for down from kMxDownMinSlots slots. Measured per layer at the
+ * 235B shape, MFMA against the row kernels (us): gate/up with the records each needs 227.5 /
+ * 229.7 at 20 tokens (1.25 slots per expert), 132.6 / 129.6 at 16; down with the combine,
+ * Q4_0 20.8 / 19.0 at 2 tokens, 33.9 / 34.1 at 4, 40.8 / 44.1 at 6, 45.0 / 49.7 at 8; Q6_K
+ * 35.7 / 37.0 at 2, 55.2 / 49.5 at 3, 61.9 / 67.6 at 4, 101 / 114 at 8. */
+constexpr int kMxAutoQuarters = 5;
+constexpr int kMxDownMinSlots = 32;
 inline bool mx_auto(int T, int K, int X)
 {
     const long NS = (long)T * K, act = X < NS ? X : NS;
     return 4 * NS >= (long)kMxAutoQuarters * act;
 }
-inline bool mx_auto_down(int T, int K, int X, int down_type)
-{
-    if (down_type == 14) return true;
-    const long NS = (long)T * K, act = X < NS ? X : NS;
-    return NS >= (long)kMxDownSlots * act;
-}
+inline bool mx_auto_down(int T, int K) { return (long)T * K >= kMxDownMinSlots; }
 
 /* One-token batches (n_used <= 8) are routed inside the gate/up kernel instead of by a
  * separate select launch. */

@@ -761,10 +761,10 @@ hipError_t launch_select(const Shape &s, const Scratch &S, int T, int gateup_rou
     a.T = T;
     a.S = S;
     if (gateup_routes && use_small_route(T, s.K)) return hipSuccess;   /* the gate/up kernel routes the batch */
-    /* up to 64 tokens the last select block also dispatches; larger batches take a separate
-     * dispatch launch rather than hundreds of tickets on one counter */
-    QLAUNCH("select", select_kernel, dim3(T), dim3(256), 0, st, a, T <= 64 ? 1 : 0);
-    if (T > 64) QLAUNCH("dispatch", dispatch_wide_kernel, dim3(1), dim3(64 * kDispWaves), 0, st, a);
+    /* up to 16 tokens the last select block also dispatches (one wave); larger batches take the
+     * 16-wave dispatch launch (measured 5 us less per layer at 48 and 64 tokens) */
+    QLAUNCH("select", select_kernel, dim3(T), dim3(256), 0, st, a, T <= 16 ? 1 : 0);
+    if (T > 16) QLAUNCH("dispatch", dispatch_wide_kernel, dim3(1), dim3(64 * kDispWaves), 0, st, a);
     return hipGetLastError();
 }
 
@@ -2741,18 +2741,33 @@ void mx_kernel(MxArgs a)
     }
 }
 
-/* Slot groups per block: 2 (16 slots, 128 rows), so two blocks share a CU (Q4_0 62 KB of LDS,
- * Q4_1 66 KB, Q6_K 80 KB); measured faster than 8-slot blocks of 256 rows at every batch from 3
- * slots per expert up (235B shape, 48 to 192 tokens; Q6_K down at 64 tokens 329 against
- * 405 us). */
-template <int TYPE>
-constexpr int mx_wsg() { return 2; }
+/* Two 80 KB Q6_K blocks (16-slot, 128 rows) share a CU. */
 static_assert(2 * mx_lds_bytes(14, 2) <= 160 * 1024, "two Q6_K blocks per CU");
 
-/* Slot pairs per wave: 4 (16-slot blocks) once the batch averages kMxWideSlots slots per active
- * expert, else 2 (8-slot blocks, up to three per CU), so that sparse tiles leave fewer waves
- * without slots. */
+/* Block shapes, chosen per kernel by the batch's slots per active expert r (the more slots a
+ * block takes, the more of them are padding on sparse tiles; the fewer, the fewer MFMAs each
+ * staged weight row feeds). A block's waves form row groups of 32 rows x slot groups:
+ *   wide   (r >= kMxWideSlots): 8 waves, 4 row groups x 2 slot groups of 4 pairs: 128 rows x
+ *          16 slots;
+ *   mid:   gate/up 8 waves, 4 row groups x 2 slot groups of 2 pairs (128 rows x 8 slots); down
+ *          4 waves, 4 row groups x 1 slot group of 4 pairs (128 rows x 8 slots);
+ *   narrow (gate/up r < 4.5, Q4_0 / Q4_1 down r < 3.5, Q6_K down r < 2.5): 4 waves, 4 row
+ *          groups x 1 slot group of 2 pairs (128 rows x 4 slots), three blocks per CU.
+ * Measured per layer at the 235B shape, narrow against mid (us): gate/up 167 / 194 at r = 1.5,
+ * 238 / 266 at 3, 296 / 300 at 4, 395 / 385 at 6; Q4_0 down 89 / 100 at 1.5, 124 / 133 at 3,
+ * 154 / 150 at 4, 206 / 183 at 6; Q6_K down 198 / 200 at 1.5, 223 / 223 at 2, 288 / 271 at 3,
+ * 356 / 303 at 4. At r = 8 the wide blocks lead every kernel (gate/up 460 against 514 narrow;
+ * Q6_K down 466 against 495 for 4-wave 8-slot blocks and 618 narrow). */
 constexpr int kMxWideSlots = 8;
+enum MxShape { kMxNarrow, kMxMid, kMxWide };
+
+static MxShape mx_shape(const Shape &s, int T, int gu, int type)
+{
+    const long NS = (long)T * s.K, act = s.X < NS ? s.X : NS;
+    if (NS >= (long)kMxWideSlots * act) return kMxWide;
+    const long narrow_quarters = gu ? 18 : (type == 14 ? 10 : 14);
+    return 4 * NS < narrow_quarters * act ? kMxNarrow : kMxMid;
+}
 
 template <int TYPE, int GU, int WSG, int PPW, int NW>
 static void launch_mx_shape(const MxArgs &a, int rows, int maxt, hipStream_t st)
@@ -2763,21 +2778,16 @@ static void launch_mx_shape(const MxArgs &a, int rows, int maxt, hipStream_t st)
             dim3(rows / (GU ? Lay::RWG / 2 : Lay::RWG), maxt, kTileN / Lay::SWG), dim3(64 * NW), lds, st, a);
 }
 
-/* Blocks of 8 waves and 128 rows: 16 slots (wide) or 8. Measured at the 512-token prefill
- * against other shapes of the same kernel: 32-slot blocks of 16 waves (one per CU) 1.76 ms for
- * gate/up, 64-row blocks of 4 waves (three per CU) 1.25, 128-row 8-slot blocks of 4 waves 1.80,
- * against 1.24 here. */
+/* Other shapes of the same kernel measured at the 512-token prefill: 32-slot blocks of 16
+ * waves (one per CU) 1.76 ms for gate/up, 64-row blocks of 4 waves (three per CU) 1.25,
+ * against 1.24 for the wide blocks. */
 template <int TYPE, int GU>
-static void launch_mx(const MxArgs &a, int rows, int maxt, int wide, hipStream_t st)
+static void launch_mx(const MxArgs &a, int rows, int maxt, MxShape shape, hipStream_t st)
 {
-    if (wide) launch_mx_shape<TYPE, GU, 2, 4, 8>(a, rows, maxt, st);
-    else launch_mx_shape<TYPE, GU, 2, 2, 8>(a, rows, maxt, st);
-}
-
-static int mx_wide(const Shape &s, int T)
-{
-    const int NS = T * s.K, act = s.X < NS ? s.X : NS;
-    return NS >= kMxWideSlots * act;
+    if (shape == kMxWide) launch_mx_shape<TYPE, GU, 2, 4, 8>(a, rows, maxt, st);
+    else if (shape == kMxNarrow) launch_mx_shape<TYPE, GU, 1, 2, 4>(a, rows, maxt, st);
+    else if constexpr (GU) launch_mx_shape<TYPE, GU, 2, 2, 8>(a, rows, maxt, st);
+    else launch_mx_shape<TYPE, GU, 1, 4, 4>(a, rows, maxt, st);
 }
 
 /* Whether the MFMA kernels take this layer: Q4_0 gate and up; Q4_0, Q4_1 or Q6_K down (Q6_K
@@ -2812,7 +2822,7 @@ hipError_t launch_experts_mx(const Shape &s, const LayerDev &L, const Scratch &S
     a.rec = S.mxx;
     a.rec_out = S.mxa;
     a.S = S;
-    launch_mx<2, 1>(a, s.F, maxt, mx_wide(s, T), st);
+    launch_mx<2, 1>(a, s.F, maxt, mx_shape(s, T, 1, 2), st);
     if (!down_mx) {
         const hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
@@ -2824,9 +2834,9 @@ hipError_t launch_experts_mx(const Shape &s, const LayerDev &L, const Scratch &S
     a.eb = L.down_eb;
     a.rec = S.mxa;
     a.rec_out = nullptr;
-    if (L.down_type == 14) launch_mx<14, 0>(a, s.E, maxt, mx_wide(s, T), st);
-    else if (L.down_type == 3) launch_mx<3, 0>(a, s.E, maxt, mx_wide(s, T), st);
-    else launch_mx<2, 0>(a, s.E, maxt, mx_wide(s, T), st);
+    if (L.down_type == 14) launch_mx<14, 0>(a, s.E, maxt, mx_shape(s, T, 0, 14), st);
+    else if (L.down_type == 3) launch_mx<3, 0>(a, s.E, maxt, mx_shape(s, T, 0, 3), st);
+    else launch_mx<2, 0>(a, s.E, maxt, mx_shape(s, T, 0, 2), st);
     const int n = T * s.E;
     QLAUNCH("combine", combine_kernel, dim3((n + 255) / 256), dim3(256), 0, st, S, s.E, s.K, T, out);
     return hipGetLastError();
@@ -2853,9 +2863,9 @@ hipError_t launch_down_mx(const Shape &s, const LayerDev &L, const Scratch &S, f
     a.rec = S.mxa;
     a.rec_out = nullptr;
     a.S = S;
-    if (L.down_type == 14) launch_mx<14, 0>(a, s.E, maxt, mx_wide(s, T), st);
-    else if (L.down_type == 3) launch_mx<3, 0>(a, s.E, maxt, mx_wide(s, T), st);
-    else launch_mx<2, 0>(a, s.E, maxt, mx_wide(s, T), st);
+    if (L.down_type == 14) launch_mx<14, 0>(a, s.E, maxt, mx_shape(s, T, 0, 14), st);
+    else if (L.down_type == 3) launch_mx<3, 0>(a, s.E, maxt, mx_shape(s, T, 0, 3), st);
+    else launch_mx<2, 0>(a, s.E, maxt, mx_shape(s, T, 0, 2), st);
     const int n = T * s.E;
     QLAUNCH("combine", combine_kernel, dim3((n + 255) / 256), dim3(256), 0, st, S, s.E, s.K, T, out);
     return hipGetLastError();

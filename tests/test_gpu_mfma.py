@@ -2,9 +2,10 @@
 GPU: every intermediate bit for bit against the oracle, like the exact path.
 
 The MFMA kernels run for QMSG_PATH_MFMA at any batch of two or more tokens; the default path
-takes them for gate/up from 2.25 slots per active expert, for Q4_0 / Q4_1 down from 2 and for
-Q6_K down at every batch of two or more tokens, so the 33-token and the 8-token Q6_K cases also
-run the row-kernel gate/up followed by the MFMA down. Cases cover Q4_0 / Q4_1 /
+takes them for gate/up from 1.25 slots per active expert and for down from 32 slots, so the
+16-token and the 8-token Q6_K cases also run the row-kernel gate/up followed by the MFMA down.
+The block shapes (4-, 8- and 16-slot blocks, chosen per kernel by slots per expert) are all
+covered. Cases cover Q4_0 / Q4_1 /
 Q6_K down rows, tiles of up to 32 slots run as 16-slot blocks, odd slot
 counts per expert, the Zipf-skewed 512-token prefill, shapes whose down rows fall back to the
 exact kernel (F/32 not a whole number of 8-block chunks), and batches of alternating sizes on
@@ -26,6 +27,7 @@ CASES = [
     ("q235b_q6k_t64", 4096, 128, 8, 1536, 64, 6, orc.T_Q6_K, False),
     ("q235b_q6k_t8", 4096, 128, 8, 1536, 8, 13, orc.T_Q6_K, False),   # Q6_K down on MFMA below one slot
     ("q235b_q41_t64", 4096, 128, 8, 1536, 64, 7, orc.T_Q4_1, False),
+    ("q235b_q41_t24", 4096, 128, 8, 1536, 24, 14, orc.T_Q4_1, False),  # 4-slot blocks, Q4_1 down
     ("q480b_t48", 6144, 160, 8, 2560, 48, 8, orc.T_Q4_0, False),
     ("tiny_t40", 256, 16, 4, 128, 40, 9, orc.T_Q4_0, False),         # down on the exact kernel
     ("tiny_q6k_t200", 256, 16, 4, 256, 200, 10, orc.T_Q6_K, False),  # 50 slots per expert: 32-slot blocks
