@@ -232,6 +232,12 @@ int qmsg_moe_device_noalloc(qmsg_ctx *ctx, int layer, const float *d_xn, int T, 
  * without waiting. */
 int qmsg_moe_chain(qmsg_ctx *ctx, int first, int n, float *d_h, int T, float eps);
 
+/* rmsnorm (src/model.c:403-409) of rows device rows of n floats (n % 4 == 0; d_x, d_y and d_w
+ * 16-byte aligned): d_y[r] = (float)(x * inv) * w with inv = 1 / sqrt(ss / n + eps) in double
+ * and ss the sequential double sum of the squares, bit for bit; d_w is n device floats or NULL
+ * (unit weights). d_y may equal d_x. Enqueued without waiting. */
+int qmsg_rmsnorm_device(qmsg_ctx *ctx, float *d_y, const float *d_x, const float *d_w, int rows, int n, float eps);
+
 /* A layer's ffn_norm weight vector (QmsLayer.ffn_norm, src/model.h:37-45), n_embd floats on
  * the host, copied to HBM; NULL restores the default unit weights. */
 int qmsg_layer_norm(qmsg_ctx *ctx, int layer, const float *w);

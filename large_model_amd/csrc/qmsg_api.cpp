@@ -886,6 +886,21 @@ int qmsg_moe_chain(qmsg_ctx *c, int first, int n, float *d_h, int T, float eps)
     return QMSG_OK;
 }
 
+int qmsg_rmsnorm_device(qmsg_ctx *c, float *d_y, const float *d_x, const float *d_w, int rows, int n, float eps)
+{
+    if (!c) return QMSG_E_INVALID;
+    if (rows < 0 || n <= 0 || n % 4) return fail(c, QMSG_E_INVALID, "qmsg_rmsnorm_device: rows=%d n=%d (n a positive multiple of 4)", rows, n);
+    if (rmsnorm_lds_bytes(n) > 160 * 1024)
+        return fail(c, QMSG_E_UNSUPPORTED, "qmsg_rmsnorm_device: rows of %d floats exceed the kernel's LDS", n);
+    if (rows == 0) return QMSG_OK;
+    if (!d_x || !d_y) return fail(c, QMSG_E_INVALID, "qmsg_rmsnorm_device: null buffer");
+    if (((uintptr_t)d_x | (uintptr_t)d_y | (uintptr_t)d_w) & 15)
+        return fail(c, QMSG_E_INVALID, "qmsg_rmsnorm_device: d_x, d_y and d_w must be 16-byte aligned");
+    HIP_TRY(c, hipSetDevice(c->device));
+    LAUNCH(c, "rmsnorm", launch_rmsnorm(d_x, d_w, d_y, rows, n, eps, c->stream));
+    return QMSG_OK;
+}
+
 int qmsg_moe(qmsg_ctx *c, int layer, const float *xn, const float *h, int T, float *out)
 {
     (void)h;

@@ -150,6 +150,12 @@ hipError_t launch_synth_f32(uint64_t key, uint64_t n, float sigma, float *out, h
 hipError_t launch_synth_experts(uint64_t seed, uint32_t layer, uint32_t kind, int type, int64_t rows,
                                 int64_t cols, int X, float sigma, uint8_t *base, hipStream_t st);
 hipError_t launch_rmsnorm_rows(float *x, int T, int E, float eps, hipStream_t st);
+/* LDS bytes of the rmsnorm kernel for rows of E floats (at most 160 KiB is launchable). */
+inline size_t rmsnorm_lds_bytes(int E)
+{
+    const size_t sq = E % 512 == 0 ? (size_t)(E / 64) * 65 : (size_t)E;      /* squares, in doubles */
+    return sq * 8;
+}
 hipError_t launch_rmsnorm(const float *x, const float *w, float *y, int T, int E, float eps, hipStream_t st);
 hipError_t launch_add_rows(float *h, const float *d, size_t n, hipStream_t st);
 hipError_t launch_set_col0(float *m, int rows, int stride, const float *vals, float fill, hipStream_t st);

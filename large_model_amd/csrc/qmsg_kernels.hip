@@ -3879,70 +3879,219 @@ hipError_t launch_rmsnorm_rows(float *x, int T, int E, float eps, hipStream_t st
     return hipGetLastError();
 }
 
-/* Sum of q[0..n) in index order, one double add after another (n a multiple of 32); the next
- * 16 terms are read from LDS while the current 16 are added, so only the adds' latency is on
- * the chain. */
-__device__ __forceinline__ double ordered_sum(const double *q, int n)
+/* Biased exponent field of a double. */
+__device__ __forceinline__ int dexp(double v) { return (int)((__double_as_longlong(v) >> 52) & 0x7ff); }
+
+/* Pitch (in doubles) of a term row of the chunked layout: term i of lane j's chunk at
+ * qt[i * kSumPitch + j], so the 64 lanes read 64 consecutive doubles per step. */
+constexpr int kSumPitch = 65;
+
+/* NR sequential sums over the column col of qt (C terms, C % 8 == 0), chain r starting from
+ * s[r]: every term is added to every chain in order; the next 8 terms are read while the
+ * current 8 are added, so only the adds' latency is on the chains. */
+template <int NR>
+__device__ __forceinline__ void column_run(const double *qt, int col, int C, double (&s)[NR])
 {
-    double ss = 0.0, a[16], b[16];
+    double a[8], b[8];
 #pragma unroll
-    for (int j = 0; j < 16; j++) a[j] = q[j];
-    for (int base = 0; base < n; base += 32) {
+    for (int k = 0; k < 8; k++) a[k] = qt[k * kSumPitch + col];
+    for (int i = 0; i < C; i += 16) {
+        if (i + 8 < C) {
 #pragma unroll
-        for (int j = 0; j < 16; j++) b[j] = q[base + 16 + j];
-#pragma unroll
-        for (int j = 0; j < 16; j++) ss += a[j];
-        if (base + 32 < n) {
-#pragma unroll
-            for (int j = 0; j < 16; j++) a[j] = q[base + 32 + j];
+            for (int k = 0; k < 8; k++) b[k] = qt[(i + 8 + k) * kSumPitch + col];
         }
 #pragma unroll
-        for (int j = 0; j < 16; j++) ss += b[j];
+        for (int k = 0; k < 8; k++)
+#pragma unroll
+            for (int r = 0; r < NR; r++) s[r] += a[k];
+        if (i + 8 >= C) break;
+        if (i + 16 < C) {
+#pragma unroll
+            for (int k = 0; k < 8; k++) a[k] = qt[(i + 16 + k) * kSumPitch + col];
+        }
+#pragma unroll
+        for (int k = 0; k < 8; k++)
+#pragma unroll
+            for (int r = 0; r < NR; r++) s[r] += b[k];
     }
-    return ss;
+}
+
+/* A 64-bit value of lane l (l wave-uniform), as a wave-uniform value. */
+__device__ __forceinline__ uint64_t readlane_u64(uint64_t v, int l)
+{
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)v, l);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(v >> 32), l);
+    return ((uint64_t)hi << 32) | lo;
+}
+
+__device__ __forceinline__ uint64_t dbits(double v) { return (uint64_t)__double_as_longlong(v); }
+
+/* The sequential sum s_{i+1} = fl(s_i + q_i), s_0 = 0, of n = 64 C terms q_i >= 0 (C % 8 == 0),
+ * bit for bit, by one wave (all 64 lanes, the result in every lane); lane j's chunk is terms
+ * jC .. jC + C - 1, stored at qt[i * kSumPitch + j].
+ *  1. Approximate chunk starts P_j: every chunk summed in any order, an exclusive lane scan.
+ *  2. Every lane runs its chunk term by term from P_j and from P_j + u, u = 2^(e - 52) for
+ *     P_j in the binade [2^e, 2^(e+1)): ends G0_j and G1_j.
+ *  3. A walk over the chunks with the true sum s, the same on every lane: if s == P_j the chunk
+ *     ends at G0_j; else if s, P_j, P_j + u, G0_j and G1_j all lie in P_j's binade, r is the
+ *     parity of (s - P_j) / u and s + (G_r - P_r) (P_1 = P_j + u) lies in it too, the chunk ends
+ *     there; otherwise the chunk is added to s term by term.
+ * Why the second case is exact: inside one binade the doubles are the multiples of u, and for
+ * such an a, fl(a + q) = a + (q rounded to a multiple of u); the increment depends on a only in
+ * a tie (q/u with fraction 1/2 exactly), through the parity of a/u, which picks the even
+ * multiple. Runs from starts equal modulo 2u take the same increments while both stay in the
+ * binade; the run from s does, since it ends below 2^(e+1) and never decreases (q_i >= 0); and
+ * the differences and the final sum are multiples of u below 2^(e+1), so exact. A chunk whose
+ * sum crosses a power of two takes the term-by-term case. Non-finite sums take it everywhere.
+ * Inside one binade the bit pattern of a non-negative double is its value in units of u plus a
+ * constant, so the walk runs on bit patterns in integer (scalar) arithmetic: (s - P_j) / u is
+ * bits(s) - bits(P_j), and adding G_r - P_r adds bits(G_r) - bits(P_r). */
+__device__ double ordered_sum_chunked(const double *qt, int C)
+{
+    const int j = threadIdx.x & 63;
+    /* 1 */
+    double c0 = 0.0, c1 = 0.0, c2 = 0.0, c3 = 0.0;
+    for (int i = 0; i < C; i += 4) {
+        c0 += qt[i * kSumPitch + j];
+        c1 += qt[(i + 1) * kSumPitch + j];
+        c2 += qt[(i + 2) * kSumPitch + j];
+        c3 += qt[(i + 3) * kSumPitch + j];
+    }
+    double inc = (c0 + c1) + (c2 + c3);
+    if (!__all(__builtin_isfinite(inc))) {
+        /* an infinite or NaN term: term by term throughout */
+        double s[1] = { 0.0 };
+        for (int k = 0; k < 64; k++) column_run<1>(qt, k, C, s);
+        return s[0];
+    }
+    for (int d = 1; d < 64; d <<= 1) {
+        const double t = __shfl_up(inc, d);
+        if (j >= d) inc += t;
+    }
+    double P = __shfl_up(inc, 1);
+    if (j == 0) P = 0.0;
+    /* 2 */
+    const int e = dexp(P);
+    const bool normal = e > 52;                        /* u = 2^(e - 52) a normal double too */
+    const double P1 = P + __longlong_as_double((long long)(normal ? e - 52 : 1) << 52);
+    double g[2] = { P, P1 };
+    column_run<2>(qt, j, C, g);
+    const uint64_t pb = dbits(P);
+    const uint64_t d0 = dbits(g[0]) - pb, d1 = dbits(g[1]) - (pb + 1);
+    const int ex = normal && dexp(P1) == e && dexp(g[0]) == e && dexp(g[1]) == e ? e : -1;
+    /* 3 */
+    uint64_t sb = 0;                                   /* bits of s = +0.0 */
+    for (int k0 = 0; k0 < 64; k0 += 8) {
+        /* eight chunks' values in scalar registers ahead of the walk through them */
+        uint64_t Pk[8], D0[8], D1[8];
+        int ek[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            Pk[u] = readlane_u64(pb, k0 + u);
+            D0[u] = readlane_u64(d0, k0 + u);
+            D1[u] = readlane_u64(d1, k0 + u);
+            ek[u] = __builtin_amdgcn_readlane(ex, k0 + u);
+        }
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            /* selects, not branches, on the common paths */
+            const bool same = sb == Pk[u];
+            const uint64_t nx = sb + (((sb - Pk[u]) & 1) ? D1[u] : D0[u]);
+            const bool fast = ek[u] >= 0 && (int)(sb >> 52) == ek[u] && (int)(nx >> 52) == ek[u];
+            const bool slow = !same && !fast;
+            const uint64_t s0 = sb;
+            sb = same ? Pk[u] + D0[u] : nx;
+            if (slow) {
+                double t[1] = { __longlong_as_double((long long)s0) };
+                column_run<1>(qt, k0 + u, C, t);
+                sb = readlane_u64(dbits(t[0]), 0);
+            }
+        }
+    }
+    return __longlong_as_double((long long)sb);
 }
 
 /* rmsnorm of one row per block into another buffer, with a weight vector (nullptr: unit)
  * (src/model.c:403-409): y = (float)(x * inv) * w. ss accumulates (double)x*(double)x in index
  * order; each square is exact in double (48 significant bits), so the reference's
  * fma(x, x, ss) equals ss + x*x with the square formed first: every thread forms squares into
- * LDS, and one lane runs the ordered sum. */
-__global__ void rmsnorm_kernel(const float *x, const float *w, float *y, int E, float eps)
+ * LDS, and wave 0 forms their sequential sum (ordered_sum_chunked for E a multiple of 512, else
+ * one lane term by term). Rows of up to kNormVec * 1024 floats stay in registers, with their
+ * weights, loaded before the sum; longer rows are read again for the output. */
+constexpr int kNormVec = 8;
+__global__ __launch_bounds__(256) void rmsnorm_kernel(const float *x, const float *w, float *y, int E, float eps)
 {
-    extern __shared__ __align__(16) float xs[];      /* [E] x, then [E] squares as double */
+    extern __shared__ __align__(16) double q[];      /* the squares */
     __shared__ double inv;
-    const float *row = x + (size_t)blockIdx.x * E;
-    double *q = (double *)(xs + E + (E & 1));
-    for (int i = threadIdx.x; i < E / 4; i += blockDim.x) {
-        const float4 v = ((const float4 *)row)[i];
-        ((float4 *)xs)[i] = v;
-        q[4 * i] = (double)v.x * (double)v.x;
-        q[4 * i + 1] = (double)v.y * (double)v.y;
-        q[4 * i + 2] = (double)v.z * (double)v.z;
-        q[4 * i + 3] = (double)v.w * (double)v.w;
+    const float4 *row = (const float4 *)(x + (size_t)blockIdx.x * E);
+    const float4 *w4 = (const float4 *)w;
+    float4 *out = (float4 *)(y + (size_t)blockIdx.x * E);
+    const int n4 = E >> 2, tid = threadIdx.x;
+    const bool chunked = E % 512 == 0, held = n4 <= 256 * kNormVec;
+    const int C = E >> 6;                            /* terms per lane (chunked: C % 8 == 0) */
+    const float4 one = make_float4(1.0f, 1.0f, 1.0f, 1.0f);
+    float4 xv[kNormVec], wv[kNormVec];
+    for (int base = 0; base < n4; base += 256 * kNormVec) {
+#pragma unroll
+        for (int m = 0; m < kNormVec; m++) {
+            const int i = base + tid + 256 * m;
+            if (i < n4) {
+                xv[m] = row[i];
+                wv[m] = w ? w4[i] : one;
+            }
+        }
+#pragma unroll
+        for (int m = 0; m < kNormVec; m++) {
+            const int i = base + tid + 256 * m;
+            if (i >= n4) continue;
+            const float4 v = xv[m];
+            const double sq[4] = { (double)v.x * (double)v.x, (double)v.y * (double)v.y,
+                                   (double)v.z * (double)v.z, (double)v.w * (double)v.w };
+            /* element 4i + k: lane (4i + k) / C, term (4i + k) % C of its chunk */
+            const int lj = chunked ? (4 * i) / C : 0, ti = 4 * i - lj * C;
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                if (chunked) q[(ti + k) * kSumPitch + lj] = sq[k];
+                else q[4 * i + k] = sq[k];
+            }
+        }
     }
     __syncthreads();
-    if (threadIdx.x == 0) {
+    if (tid < 64) {
         double ss;
-        if (E % 32 == 0) {
-            ss = ordered_sum(q, E);
+        if (chunked) {
+            ss = ordered_sum_chunked(q, C);
         } else {
             ss = 0.0;
-            for (int i = 0; i < E; i++) ss += q[i];
+            if (tid == 0)
+                for (int i = 0; i < E; i++) ss += q[i];
         }
-        inv = 1.0 / sqrt(ss / E + (double)eps);
+        if (tid == 0) inv = 1.0 / sqrt(ss / E + (double)eps);
     }
     __syncthreads();
     const double v = inv;
-    float *out = y + (size_t)blockIdx.x * E;
-    for (int i = threadIdx.x; i < E; i += blockDim.x) out[i] = (float)((double)xs[i] * v) * (w ? w[i] : 1.0f);
+    auto norm = [&](float4 a, float4 b) {
+        return make_float4((float)((double)a.x * v) * b.x, (float)((double)a.y * v) * b.y,
+                           (float)((double)a.z * v) * b.z, (float)((double)a.w * v) * b.w);
+    };
+    if (held) {
+#pragma unroll
+        for (int m = 0; m < kNormVec; m++) {
+            const int i = tid + 256 * m;
+            if (i < n4) out[i] = norm(xv[m], wv[m]);
+        }
+    } else {
+        for (int i = tid; i < n4; i += 256) out[i] = norm(row[i], w ? w4[i] : one);
+    }
 }
 
 hipError_t launch_rmsnorm(const float *x, const float *w, float *y, int T, int E, float eps, hipStream_t st)
 {
     if (T <= 0) return hipSuccess;
     if (E % 4) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(rmsnorm_kernel, dim3(T), dim3(256), (size_t)E * 4 + 4 + (size_t)E * 8, st, x, w, y, E, eps);
+    static_assert(kSumPitch == 65, "rmsnorm_lds_bytes assumes the pitch");
+    if (rmsnorm_lds_bytes(E) > 160 * 1024) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(rmsnorm_kernel, dim3(T), dim3(256), rmsnorm_lds_bytes(E), st, x, w, y, E, eps);
     return hipGetLastError();
 }
 

@@ -101,6 +101,7 @@ _SIGS = {
     "qmsg_profile_read": (_I, [_P, ctypes.c_char_p, ctypes.POINTER(ctypes.c_int64),
                                ctypes.POINTER(ctypes.c_double)]),
     "qmsg_moe_chain": (_I, [_P, _I, _I, _P, _I, ctypes.c_float]),
+    "qmsg_rmsnorm_device": (_I, [_P, _P, _P, _P, _I, _I, ctypes.c_float]),
     "qmsg_layer_norm": (_I, [_P, _I, _P]),
     "qmsg_eval_silu": (_I, [_P, _P, _I, _P]),
     "qmsg_eval_exp": (_I, [_P, _P, _I, _P]),
@@ -431,6 +432,24 @@ class Context:
     def moe_chain(self, first: int, n: int, d_h: int, T: int, eps: float = 1e-6):
         """h += moe(l, rmsnorm(h, ffn_norm_l)) for layers first .. first+n-1 on device rows d_h."""
         self._check(lib.qmsg_moe_chain(self._h, first, n, d_h, T, eps))
+
+    def rmsnorm_device(self, d_y: int, d_x: int, d_w: Optional[int], rows: int, n: int, eps: float = 1e-6):
+        """d_y = rmsnorm(d_x, d_w) row by row on device buffers (d_w None: unit weights)."""
+        self._check(lib.qmsg_rmsnorm_device(self._h, d_y, d_x, d_w, rows, n, eps))
+
+    def rmsnorm(self, x: np.ndarray, w: Optional[np.ndarray] = None, eps: float = 1e-6) -> np.ndarray:
+        """rmsnorm of host rows x [rows][n] on the device (src/model.c:403-409); returns y."""
+        x = np.ascontiguousarray(x, np.float32)
+        rows, n = x.shape
+        d_x = self.device_alloc(max(x.nbytes, 16))
+        d_w = None
+        self.h2d(d_x, x)
+        if w is not None:
+            d_w = self.device_alloc(n * 4)
+            self.h2d(d_w, np.ascontiguousarray(w, np.float32))
+        self.rmsnorm_device(d_x, d_x, d_w, rows, n, eps)
+        self.sync()
+        return self.d2h(d_x, (rows, n))
 
     def layer_norm(self, layer: int, w: Optional[np.ndarray]):
         wp = None if w is None else np.ascontiguousarray(w, np.float32)

@@ -1,0 +1,83 @@
+"""rmsnorm (src/model.c:403-409) on the GPU through qmsg_rmsnorm_device, bit for bit against the
+oracle's sequential double chain, on rows chosen to stress the chunked ordered sum: wide
+dynamic range, small integers and powers of two (many exact sums and rounding ties), leading
+zeros, few mantissa bits, spikes, random exponents; rows whose length is a multiple of 512 take
+the chunked sum, others (256, 132) the term-by-term one."""
+import numpy as np
+import pytest
+
+import oracle as orc
+
+pytestmark = pytest.mark.gpu
+
+
+def rows_of_kind(kind: int, n: int, count: int, rng) -> np.ndarray:
+    shape = (count, n)
+    if kind == 0:
+        return rng.standard_normal(shape).astype(np.float32)
+    if kind == 1:
+        return (rng.standard_normal(shape) * np.exp(3.0 * rng.standard_normal(shape))).astype(np.float32)
+    if kind == 2:
+        return rng.integers(-3, 4, size=shape).astype(np.float32)
+    if kind == 3:
+        return (np.ldexp(1.0, rng.integers(-20, 20, size=shape)) * rng.choice([-1.0, 1.0], size=shape)).astype(np.float32)
+    if kind == 4:
+        x = rng.standard_normal(shape).astype(np.float32)
+        x[:, : n // 2] = 0.0
+        return x
+    if kind == 5:
+        return np.ldexp(1.0 + rng.integers(0, 8, size=shape) / 8.0, rng.integers(0, 6, size=shape)).astype(np.float32)
+    if kind == 6:
+        x = (1e-3 * rng.standard_normal(shape)).astype(np.float32)
+        x[:, ::97] = (1e3 * rng.standard_normal((count, len(range(0, n, 97))))).astype(np.float32)
+        return x
+    bits = rng.integers(0, 2 ** 32, size=shape, dtype=np.uint64).astype(np.uint32)
+    bits = (bits & np.uint32(0x807FFFFF)) | (rng.integers(100, 160, size=shape).astype(np.uint32) << np.uint32(23))
+    return bits.view(np.float32)
+
+
+@pytest.fixture(scope="module")
+def ctx():
+    from large_model_amd import qmsg
+    with qmsg.Context(256, 16, 4, 128, n_layer=1, max_tokens=1) as c:
+        yield c
+
+
+@pytest.mark.parametrize("n", [256, 2048, 4096, 6144, 7168, 132])
+def test_rmsnorm_rows_bit_exact(ctx, n):
+    print(f"[case] rmsnorm n={n}", flush=True)
+    rng = np.random.default_rng(n)
+    x = np.concatenate([rows_of_kind(k, n, 24, rng) for k in range(8)])
+    w = rng.uniform(0.5, 1.5, n).astype(np.float32)
+    for weights in (None, w):
+        got = ctx.rmsnorm(x, weights, eps=1e-6)
+        ref = orc.rmsnorm(x, weights, eps=1e-6)
+        assert np.array_equal(got.view(np.uint32), ref.view(np.uint32)), (n, weights is None)
+
+
+def test_rmsnorm_non_finite_rows(ctx):
+    """An infinite or NaN element makes the sum non-finite: the kernel then adds term by term
+    and matches the oracle's values (NaN where it has NaN)."""
+    print("[case] rmsnorm non-finite", flush=True)
+    rng = np.random.default_rng(5)
+    x = rng.standard_normal((4, 4096)).astype(np.float32)
+    x[0, 1000] = np.inf
+    x[1, 3000] = np.nan
+    x[2, 5] = -np.inf
+    got, ref = ctx.rmsnorm(x), orc.rmsnorm(x)
+    assert np.array_equal(np.isnan(got), np.isnan(ref))
+    fin = ~np.isnan(ref)
+    assert np.array_equal(got[fin].view(np.uint32), ref[fin].view(np.uint32))
+
+
+def test_rmsnorm_arguments(ctx):
+    from large_model_amd import qmsg
+    d = ctx.device_alloc(4096)
+    with pytest.raises(qmsg.QmsgError):
+        ctx.rmsnorm_device(d, d, None, 1, 6, 1e-6)            # n % 4
+    with pytest.raises(qmsg.QmsgError):
+        ctx.rmsnorm_device(d, d + 4, None, 1, 8, 1e-6)        # unaligned input
+    with pytest.raises(qmsg.QmsgError) as ei:
+        ctx.rmsnorm_device(d, d, None, 1, 1 << 16, 1e-6)      # too long for the kernel's LDS
+    assert ei.value.status == -2
+    ctx.rmsnorm_device(d, d, None, 0, 256, 1e-6)              # no rows: nothing to do
