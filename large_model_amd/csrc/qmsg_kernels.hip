@@ -2228,9 +2228,9 @@ struct MxLayout {
     static constexpr int WINSTR = (RWG * WUR + 63) / 64;               /* weight DMA instructions  */
 };
 
-__host__ __device__ constexpr int mx_lds_bytes(int type, int wsg, int ppw = 4, int nw = 8)
+__host__ __device__ constexpr int mx_lds_bytes(int type, int wsg, int ppw = 4, int nw = 8, int nb = 2)
 {
-    return 2 * ((32 * nw / wsg) * mx_wstride(type) + 2 * ppw * wsg * mx_rstride(type));
+    return nb * ((32 * nw / wsg) * mx_wstride(type) + 2 * ppw * wsg * mx_rstride(type));
 }
 
 /* (x & m) | c in one instruction; m and c in registers (no literal operands in VOP3 here). */
@@ -2530,17 +2530,22 @@ __device__ __forceinline__ void mx_wait_barrier()
     asm volatile("s_waitcnt vmcnt(0)\n\ts_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
 
-/* Gate/up (GU = 1: gate rows against the token's input records, the same up rows, SwiGLU, the
- * int8 activation blocks and their records) or down (GU = 0: dn rows) of one slot tile. Two
- * blocks share a CU (16 waves, four per SIMD), which hides the LDS and memory latency. */
-/* Waves per SIMD the MFMA kernel is built for: six where three blocks' LDS fits a CU, else four
- * (the register budget follows: 80 or 128 VGPRs). */
-template <int TYPE, int WSG, int PPW, int NW>
-constexpr int mx_waves() { return (160 * 1024 / mx_lds_bytes(TYPE, WSG, PPW, NW)) * NW / 4 >= 6 ? 6 : 4; }
+/* Waves per SIMD the MFMA kernel is built for: six where three double-buffered blocks' LDS
+ * fits a CU, else four (the register budget follows: 80 or 128 VGPRs). */
+template <int TYPE, int WSG, int PPW, int NW, int NB>
+constexpr int mx_waves()
+{
+    return NB == 1 ? 4 : (160 * 1024 / mx_lds_bytes(TYPE, WSG, PPW, NW, NB)) * NW / 4 >= 6 ? 6 : 4;
+}
 
-template <int TYPE, int WSG, int GU, int PPW, int NW>
-__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(mx_waves<TYPE, WSG, PPW, NW>(),
-                                                                         mx_waves<TYPE, WSG, PPW, NW>())))
+/* Gate/up (GU = 1: gate rows against the token's input records, the same up rows, SwiGLU, the
+ * int8 activation blocks and their records) or down (GU = 0: dn rows) of one slot tile, with NB
+ * staging buffers: 2 (the next chunk's copy in flight while this one computes) or 1 (copy, wait,
+ * compute; the other blocks on the CU hide the copy). Several blocks share a CU, which hides the
+ * LDS and memory latency. */
+template <int TYPE, int WSG, int GU, int PPW, int NW, int NB>
+__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(mx_waves<TYPE, WSG, PPW, NW, NB>(),
+                                                                         mx_waves<TYPE, WSG, PPW, NW, NB>())))
 void mx_kernel(MxArgs a)
 {
     extern __shared__ __align__(16) uint8_t smem[];
@@ -2663,11 +2668,18 @@ void mx_kernel(MxArgs a)
                 acc[t][p] = f32x4{ 0.0f, 0.0f, 0.0f, 0.0f };
                 cr[t][p] = 0.0f;
             }
-        issue(0, 0);
-        mx_wait_barrier();
+        if (NB == 2) {
+            issue(0, 0);
+            mx_wait_barrier();
+        }
         for (int c = 0; c < nch; c++) {
-            const int buf = c & 1;
-            if (c + 1 < nch) issue(c + 1, buf ^ 1);
+            const int buf = NB == 2 ? c & 1 : 0;
+            if (NB == 1) {
+                issue(c, 0);
+                mx_wait_barrier();
+            } else if (c + 1 < nch) {
+                issue(c + 1, buf ^ 1);
+            }
             if constexpr (NP > 0) {
                 const uint8_t *Wl = smem + buf * BUF + (32 * wr) * WS;
                 const uint8_t *Rl = smem + buf * BUF + Lay::WBYTES + (2 * PPW * ws) * Lay::RS;
@@ -2680,7 +2692,8 @@ void mx_kernel(MxArgs a)
                     mx_chunk<TYPE, NP, 0, GU>(Wl, Rl, lr, lg, kh, jd, offa_lo, offa_hi, acc, cr);
                 }
             }
-            mx_wait_barrier();       /* chunk c+1 has landed; buffer c is free for chunk c+2 */
+            /* chunk c+1 has landed; buffer c is free for chunk c+2 (one buffer: it is free) */
+            mx_wait_barrier();
         }
         /* hsum256 per (row, slot): lanes of k-half 0 take the partner lane's k + 4 chains */
 #pragma unroll
@@ -2769,25 +2782,31 @@ static MxShape mx_shape(const Shape &s, int T, int gu, int type)
     return 4 * NS < narrow_quarters * act ? kMxNarrow : kMxMid;
 }
 
-template <int TYPE, int GU, int WSG, int PPW, int NW>
+template <int TYPE, int GU, int WSG, int PPW, int NW, int NB = 2>
 static void launch_mx_shape(const MxArgs &a, int rows, int maxt, hipStream_t st)
 {
     using Lay = MxLayout<TYPE, WSG, PPW, NW>;
-    const size_t lds = (size_t)mx_lds_bytes(TYPE, WSG, PPW, NW);
-    QLAUNCH(GU ? "gateup" : "down", (mx_kernel<TYPE, WSG, GU, PPW, NW>),
+    const size_t lds = (size_t)mx_lds_bytes(TYPE, WSG, PPW, NW, NB);
+    QLAUNCH(GU ? "gateup" : "down", (mx_kernel<TYPE, WSG, GU, PPW, NW, NB>),
             dim3(rows / (GU ? Lay::RWG / 2 : Lay::RWG), maxt, kTileN / Lay::SWG), dim3(64 * NW), lds, st, a);
 }
 
 /* Other shapes of the same kernel measured at the 512-token prefill: 32-slot blocks of 16
  * waves (one per CU) 1.76 ms for gate/up, 64-row blocks of 4 waves (three per CU) 1.25,
- * against 1.24 for the wide blocks. */
+ * against 1.24 for the wide blocks.
+ * Staging buffers: the 4-wave down blocks of 8 slots, and of 4 for Q6_K, stage one chunk at a
+ * time (half the LDS, so four blocks share a CU instead of two or three: the waves of other
+ * blocks cover each block's copy); every other shape double-buffers. Measured at the 235B
+ * shape, one buffer against two: Q6_K down 236 / 303 us at 4 slots per expert, 124 / 154 at
+ * 1 slot; Q4_0 down 129 / 148 at 4 slots, 72.5 / 70.6 at 1 slot; gate/up 297 / 287 at 4
+ * slots; the wide blocks 481 / 463 (Q6_K down) and 510 / 455 (gate/up) at 8 slots. */
 template <int TYPE, int GU>
 static void launch_mx(const MxArgs &a, int rows, int maxt, MxShape shape, hipStream_t st)
 {
     if (shape == kMxWide) launch_mx_shape<TYPE, GU, 2, 4, 8>(a, rows, maxt, st);
-    else if (shape == kMxNarrow) launch_mx_shape<TYPE, GU, 1, 2, 4>(a, rows, maxt, st);
+    else if (shape == kMxNarrow) launch_mx_shape<TYPE, GU, 1, 2, 4, (!GU && TYPE == 14) ? 1 : 2>(a, rows, maxt, st);
     else if constexpr (GU) launch_mx_shape<TYPE, GU, 2, 2, 8>(a, rows, maxt, st);
-    else launch_mx_shape<TYPE, GU, 1, 4, 4>(a, rows, maxt, st);
+    else launch_mx_shape<TYPE, GU, 1, 4, 4, 1>(a, rows, maxt, st);
 }
 
 /* Whether the MFMA kernels take this layer: Q4_0 gate and up; Q4_0, Q4_1 or Q6_K down (Q6_K
