@@ -798,7 +798,7 @@ static int run_layer_s(qmsg_ctx *c, const Scratch &S, int layer, const float *d_
     const bool gu_ok = mx_supported(s, d, &dn_ok) && q40 && many;
     const bool forced = c->path == QMSG_PATH_MFMA, autop = c->path == QMSG_PATH_AUTO;
     const bool gu_mx = gu_ok && (forced || (autop && mx_auto(T, s.K, s.X)));
-    const bool dn_mx = dn_ok && many && (forced || (autop && mx_auto_down(T, s.K)));
+    const bool dn_mx = dn_ok && many && (forced || (autop && mx_auto_down(T, s.K, d.down_type)));
     LAUNCH(c, "route", launch_route(s, d, S, d_xn, T, c->stream));
     LAUNCH(c, "select", launch_select(s, S, T, q40 ? 1 : 0, c->stream));
     if (gu_mx) {

@@ -46,19 +46,24 @@ constexpr int kTileN = 32;
 constexpr int kMxRec = 128;
 
 /* The default path takes the MFMA kernels for gate/up once a batch averages kMxAutoQuarters / 4
- * slots per active expert, and for down from kMxDownMinSlots slots. Measured per layer at the
- * 235B shape, MFMA against the row kernels (us): gate/up with the records each needs 227.5 /
- * 229.7 at 20 tokens (1.25 slots per expert), 132.6 / 129.6 at 16; down with the combine,
- * Q4_0 20.8 / 19.0 at 2 tokens, 33.9 / 34.1 at 4, 40.8 / 44.1 at 6, 45.0 / 49.7 at 8; Q6_K
- * 35.7 / 37.0 at 2, 55.2 / 49.5 at 3, 61.9 / 67.6 at 4, 101 / 114 at 8. */
+ * slots per active expert, and for down from kMxDownMinSlotsQ4 slots (Q4_0 / Q4_1 rows) or
+ * kMxDownMinSlotsQ6 (Q6_K rows). Measured per layer at the 235B shape, MFMA against the row
+ * kernels (us): gate/up with the records each needs 227.5 / 229.7 at 20 tokens (1.25 slots per
+ * expert), 132.6 / 129.6 at 16; down after row-kernel gate/up, with the activation records it
+ * needs and the combine: Q4_0 37.9 / 34.1 at 4 tokens, 44.9 / 44.1 at 6, 53.2 / 53.8 at 8, 64.4 /
+ * 69.3 at 12; Q6_K 39.8 / 41.0 at 2, 59.2 / 53.6 at 3, 66.0 / 71.6 at 4, 105 / 118 at 8. */
 constexpr int kMxAutoQuarters = 5;
-constexpr int kMxDownMinSlots = 32;
+constexpr int kMxDownMinSlotsQ4 = 72;
+constexpr int kMxDownMinSlotsQ6 = 32;
 inline bool mx_auto(int T, int K, int X)
 {
     const long NS = (long)T * K, act = X < NS ? X : NS;
     return 4 * NS >= (long)kMxAutoQuarters * act;
 }
-inline bool mx_auto_down(int T, int K) { return (long)T * K >= kMxDownMinSlots; }
+inline bool mx_auto_down(int T, int K, int down_type)
+{
+    return (long)T * K >= (down_type == 14 ? kMxDownMinSlotsQ6 : kMxDownMinSlotsQ4);
+}
 
 /* One-token batches (n_used <= 8) are routed inside the gate/up kernel instead of by a
  * separate select launch. */
