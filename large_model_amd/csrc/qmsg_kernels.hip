@@ -2760,25 +2760,28 @@ static_assert(2 * mx_lds_bytes(14, 2) <= 160 * 1024, "two Q6_K blocks per CU");
 /* Block shapes, chosen per kernel by the batch's slots per active expert r (the more slots a
  * block takes, the more of them are padding on sparse tiles; the fewer, the fewer MFMAs each
  * staged weight row feeds). A block's waves form row groups of 32 rows x slot groups:
- *   wide   (r >= kMxWideSlots): 8 waves, 4 row groups x 2 slot groups of 4 pairs: 128 rows x
- *          16 slots;
- *   mid:   gate/up 8 waves, 4 row groups x 2 slot groups of 2 pairs (128 rows x 8 slots); down
- *          4 waves, 4 row groups x 1 slot group of 4 pairs (128 rows x 8 slots);
- *   narrow (gate/up r < 4.5, Q4_0 / Q4_1 down r < 3.5, Q6_K down r < 2.5): 4 waves, 4 row
- *          groups x 1 slot group of 2 pairs (128 rows x 4 slots), three blocks per CU.
- * Measured per layer at the 235B shape, narrow against mid (us): gate/up 167 / 194 at r = 1.5,
- * 238 / 266 at 3, 296 / 300 at 4, 395 / 385 at 6; Q4_0 down 89 / 100 at 1.5, 124 / 133 at 3,
- * 154 / 150 at 4, 206 / 183 at 6; Q6_K down 198 / 200 at 1.5, 223 / 223 at 2, 288 / 271 at 3,
- * 356 / 303 at 4. At r = 8 the wide blocks lead every kernel (gate/up 460 against 514 narrow;
- * Q6_K down 466 against 495 for 4-wave 8-slot blocks and 618 narrow). */
-constexpr int kMxWideSlots = 8;
+ *   wide   (gate/up r >= 12, down r >= 16): 8 waves, 4 row groups x 2 slot groups of 4 pairs:
+ *          128 rows x 16 slots, two staging buffers;
+ *   mid:   4 waves, 4 row groups x 1 slot group of 4 pairs: 128 rows x 8 slots, one staging
+ *          buffer (four blocks per CU);
+ *   narrow (gate/up r < 3, Q4_0 / Q4_1 down r < 3.5, Q6_K down r < 2.5): 4 waves, 4 row
+ *          groups x 1 slot group of 2 pairs (128 rows x 4 slots), two buffers (Q6_K: one).
+ * Measured per layer at the 235B shape (us): gate/up narrow / mid 166 / 178 at r = 1.5, 187 /
+ * 199 at 2, 236 / 237 at 3, 287 / 269 at 4; mid / 8-slot blocks of 8 waves 317-325 / 364-378 at
+ * 6; mid / wide 407-416 / 460-467 at 8, 571-620 / 581-593 at 12 (run to run), 765-786 / 723-751
+ * at 16. Down narrow / mid: Q4_0 89 / 100 at 1.5, 124 / 133 at 3, 154 / 150 at 4; Q6_K 198 /
+ * 200 at 1.5, 223 / 223 at 2, 288 / 271 at 3. Down mid / wide: Q4_0 193 / 229 at 8, 271 / 288 at
+ * 12, 373 / 375 at 16; Q6_K 362 / 460 at 8, 496 / 549 at 12, 701 / 719 at 16. */
+constexpr int kMxWideSlots = 16;
+constexpr int kMxWideSlotsGateUp = 12;
 enum MxShape { kMxNarrow, kMxMid, kMxWide };
 
 static MxShape mx_shape(const Shape &s, int T, int gu, int type)
 {
     const long NS = (long)T * s.K, act = s.X < NS ? s.X : NS;
-    if (NS >= (long)kMxWideSlots * act) return kMxWide;
-    const long narrow_quarters = gu ? 18 : (type == 14 ? 10 : 14);
+    const long wide_slots = gu ? kMxWideSlotsGateUp : kMxWideSlots;
+    if (NS >= wide_slots * act) return kMxWide;
+    const long narrow_quarters = gu ? 12 : (type == 14 ? 10 : 14);
     return 4 * NS < narrow_quarters * act ? kMxNarrow : kMxMid;
 }
 
@@ -2794,18 +2797,17 @@ static void launch_mx_shape(const MxArgs &a, int rows, int maxt, hipStream_t st)
 /* Other shapes of the same kernel measured at the 512-token prefill: 32-slot blocks of 16
  * waves (one per CU) 1.76 ms for gate/up, 64-row blocks of 4 waves (three per CU) 1.25,
  * against 1.24 for the wide blocks.
- * Staging buffers: the 4-wave down blocks of 8 slots, and of 4 for Q6_K, stage one chunk at a
- * time (half the LDS, so four blocks share a CU instead of two or three: the waves of other
- * blocks cover each block's copy); every other shape double-buffers. Measured at the 235B
- * shape, one buffer against two: Q6_K down 236 / 303 us at 4 slots per expert, 124 / 154 at
- * 1 slot; Q4_0 down 129 / 148 at 4 slots, 72.5 / 70.6 at 1 slot; gate/up 297 / 287 at 4
- * slots; the wide blocks 481 / 463 (Q6_K down) and 510 / 455 (gate/up) at 8 slots. */
+ * Staging buffers: the 8-slot blocks of 4 waves, and the 4-slot Q6_K down blocks, stage one
+ * chunk at a time (half the LDS, so four blocks share a CU instead of two or three: the waves of
+ * other blocks cover each block's copy); the others double-buffer. Measured at the 235B shape,
+ * one buffer against two: Q6_K down 236 / 303 us at 4 slots per expert, 124 / 154 at 1 slot;
+ * Q4_0 down 129 / 148 at 4 slots, 72.5 / 70.6 at 1 slot; the 4-slot gate/up blocks 297 / 287 at
+ * 4 slots; the wide blocks 481 / 463 (Q6_K down) and 510 / 455 (gate/up) at 8 slots. */
 template <int TYPE, int GU>
 static void launch_mx(const MxArgs &a, int rows, int maxt, MxShape shape, hipStream_t st)
 {
     if (shape == kMxWide) launch_mx_shape<TYPE, GU, 2, 4, 8>(a, rows, maxt, st);
     else if (shape == kMxNarrow) launch_mx_shape<TYPE, GU, 1, 2, 4, (!GU && TYPE == 14) ? 1 : 2>(a, rows, maxt, st);
-    else if constexpr (GU) launch_mx_shape<TYPE, GU, 2, 2, 8>(a, rows, maxt, st);
     else launch_mx_shape<TYPE, GU, 1, 4, 4, 1>(a, rows, maxt, st);
 }
 

@@ -21,7 +21,7 @@ pytestmark = pytest.mark.gpu
 CASES = [
     # name, E, X, K, F, T, seed, down_type, zipf
     ("q30b_t64", 2048, 128, 8, 768, 64, 1, orc.T_Q4_0, False),
-    ("q30b_t128", 2048, 128, 8, 768, 128, 11, orc.T_Q4_0, False),    # 8 slots per expert: both on MFMA
+    ("q30b_t128", 2048, 128, 8, 768, 128, 11, orc.T_Q4_0, False),    # 8 slots per expert: 8-slot blocks
     ("q235b_t64", 4096, 128, 8, 1536, 64, 2, orc.T_Q4_0, False),
     ("q235b_t16", 4096, 128, 8, 1536, 16, 12, orc.T_Q4_0, False),    # about one slot per expert
     ("q235b_t33", 4096, 128, 8, 1536, 33, 3, orc.T_Q4_0, False),
@@ -31,7 +31,8 @@ CASES = [
     ("q235b_q41_t24", 4096, 128, 8, 1536, 24, 14, orc.T_Q4_1, False),  # 4-slot blocks, Q4_1 down
     ("q480b_t48", 6144, 160, 8, 2560, 48, 8, orc.T_Q4_0, False),
     ("tiny_t40", 256, 16, 4, 128, 40, 9, orc.T_Q4_0, False),         # down on the exact kernel
-    ("tiny_q6k_t200", 256, 16, 4, 256, 200, 10, orc.T_Q6_K, False),  # 50 slots per expert: 32-slot blocks
+    ("tiny_q6k_t200", 256, 16, 4, 256, 200, 10, orc.T_Q6_K, False),  # 50 slots per expert: 16-slot blocks
+    ("q30b_q41_t256", 2048, 128, 8, 768, 256, 15, orc.T_Q4_1, False),  # 16 slots per expert: wide Q4_1 down
     ("q235b_zipf_t512", 4096, 128, 8, 1536, 512, 5, orc.T_Q4_0, True),
 ]
 
