@@ -1626,11 +1626,13 @@ __global__ __launch_bounds__(4 * RT) void tile_rows_kernel(TileArgs a)
     }
 }
 
-/* One-token batch, Q4_0 or Q4_1 down weights (K <= 8 experts, one slot each, slot j = j-th active
- * expert): one block per RD output rows r0 .. r0+RD-1 and RD/2 waves. Wave w owns the 16/RD
- * active experts 16w/RD .. (16 rows, one per lane quad) and streams exactly those rows in
+/* One-token batch, Q4_0, Q4_1 or Q6_K down weights (K <= 8 experts, one slot each, slot j = j-th
+ * active expert): one block per RD output rows r0 .. r0+RD-1 and RD/2 waves. Wave w owns the
+ * 16/RD active experts 16w/RD .. (16 rows, one per lane quad) and streams exactly those rows in
  * chunks of CB blocks, D chunks in flight, through its own LDS buffer, so its dots start as
- * soon as its first bytes land. The prologue requests the first chunks, then quantises the K
+ * soon as its first bytes land. Q6_K rows go a super-block per chunk (CB = 8), 216 bytes from
+ * the 4-byte boundary below it in 4-byte units (row bytes a multiple of 4; tensors carry 256
+ * bytes of tail padding). The prologue requests the first chunks, then quantises the K
  * activation rows into int8 pair records in LDS (block 0 also writes them out for the debug
  * copy-back). The block ends with the weighted combine of its RD rows in selection order
  * (src/model.c:1152-1162). */
@@ -1638,14 +1640,19 @@ template <int TYPE, int CB, int D, int RD>
 __global__ __launch_bounds__(32 * RD) void down_t1_kernel(DownArgs a)
 {
     extern __shared__ __align__(16) uint8_t smem[];
+    constexpr bool Q6 = TYPE == 14;
+    static_assert(!Q6 || CB == 8, "a Q6_K chunk is one super-block");
     constexpr int NW = RD / 2, NTH = 64 * NW;         /* waves: 8 experts x RD rows / 16      */
     constexpr int EPW = 16 / RD;                      /* experts per wave                     */
     constexpr int QPT = (512 + NTH - 1) / NTH;        /* int8 blocks per thread in registers  */
-    constexpr int BB = TYPE == 3 ? 20 : 18;           /* bytes per 32-block                   */
-    constexpr int SPR = CB * BB / 16;                 /* 16-byte slots per row per chunk      */
-    constexpr int NSL = 16 * SPR;                     /* slots of one wave's chunk            */
-    constexpr int SPT = (NSL + 63) / 64;              /* slots per lane per chunk             */
-    constexpr int WS = CB * BB + ((SPR & 1) ? 0 : 16);/* LDS row stride, odd in 16-byte units */
+    constexpr int BB = TYPE == 3 ? 20 : 18;           /* bytes per 32-block (Q4 types)        */
+    constexpr int UNIT = Q6 ? 4 : 16;                 /* bytes per load                       */
+    constexpr int SPR = Q6 ? 54 : CB * BB / 16;       /* loads per row per chunk              */
+    constexpr int NSL = 16 * SPR;                     /* loads of one wave's chunk            */
+    constexpr int SPT = (NSL + 63) / 64;              /* loads per lane per chunk             */
+    /* LDS row stride, odd in 16-byte units (Q6_K: in 4-byte units) */
+    constexpr int WS = Q6 ? 220 : CB * BB + ((SPR & 1) ? 0 : 16);
+    typedef typename std::conditional<Q6, uint32_t, u32x4>::type Unit;
     const int tid = threadIdx.x, lane = tid & 63, qd = lane >> 2, p = lane & 3;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int r0 = (int)blockIdx.x * RD, E = a.E, K = a.K, nbF = a.F >> 5, nPF = a.F >> 6;
@@ -1679,13 +1686,16 @@ __global__ __launch_bounds__(32 * RD) void down_t1_kernel(DownArgs a)
     const uint8_t *b0 = a.down + (size_t)max(e0, 0) * a.eb + (size_t)r0 * a.rb;
     const uint8_t *b1 = a.down + (size_t)max(e1, 0) * a.eb + (size_t)r0 * a.rb;
     __builtin_amdgcn_sched_barrier(0);
-    u32x4 wv[D][SPT];
-    auto load_chunk = [&](int c, u32x4 *dst) {
+    Unit wv[D][SPT];
+    auto load_chunk = [&](int c, Unit *dst) {
 #pragma unroll
         for (int m = 0; m < SPT; m++) {
             const int i = min(lane + 64 * m, NSL - 1), row = i / SPR, j = i - row * SPR;
             const uint8_t *rp = (EPW == 1 || row < RD) ? b0 + (size_t)row * a.rb : b1 + (size_t)(row - RD) * a.rb;
-            dst[m] = *(const u32x4 *)(rp + (size_t)c * CB * BB + 16 * j);
+            if constexpr (Q6)     /* the super-block starts 2 bytes past a 4-byte boundary on odd chunks */
+                dst[m] = *(const uint32_t *)(rp + (size_t)(c * 210 - 2 * (c & 1)) + 4 * j);
+            else
+                dst[m] = *(const u32x4 *)(rp + (size_t)c * CB * BB + 16 * j);
         }
     };
     PHASE(2048, 0);
@@ -1742,16 +1752,31 @@ __global__ __launch_bounds__(32 * RD) void down_t1_kernel(DownArgs a)
 #pragma unroll
                     for (int m = 0; m < SPT; m++) {
                         const int i = min(lane + 64 * m, NSL - 1), row = i / SPR, j = i - row * SPR;
-                        *(u32x4 *)(wbuf + row * WS + 16 * j) = wv[d][m];
+                        *(Unit *)(wbuf + row * WS + UNIT * j) = wv[d][m];
                     }
                     wave_sync();
                     if (c + D < nchunk) load_chunk(c + D, wv[d]);
-                    if (TYPE == 3)
+                    if constexpr (Q6) {
+                        /* the 8 blocks of super-block c (src/kernels.c:142-170) */
+                        auto superblock = [&](auto al) {
+#pragma unroll
+                            for (int h = 0; h < 2; h++)
+#pragma unroll
+                                for (int g = 0; g < 4; g++) {
+                                    const int blk = c * 8 + h * 4 + g;
+                                    const Q6W w = q6_k_weights<decltype(al)::value>(wbuf + qd * WS, al ? 0 : 2, h, g, p);
+                                    q6_k_token(w, xq + (size_t)(blk >> 1) * kPairBytes, p, blk & 1, acc[0]);
+                                }
+                        };
+                        if (c & 1) superblock(std::integral_constant<bool, false>());
+                        else superblock(std::integral_constant<bool, true>());
+                    } else if (TYPE == 3) {
                         q4_1_rows<1, 4>((const uint32_t *)(wbuf + qd * WS), p, xq, (size_t)xrec, c * (CB / 2), CB / 2,
                                         1, acc);
-                    else
+                    } else {
                         q4_0_rows<1, 4>((const uint32_t *)(wbuf + qd * WS), p, xq, (size_t)xrec, c * (CB / 2), CB / 2,
                                         1, acc);
+                    }
                     if (c == 0) PHASE(2048, 3);
                 }
             }
@@ -2004,12 +2029,13 @@ hipError_t launch_down_exact(const Shape &s, const LayerDev &L, const Scratch &S
     constexpr int RD = kDownT1Rows, CB = 8;
     const int bb = L.down_type == 3 ? 20 : 18;
     const size_t xrec = (size_t)(s.F / 64) * kPairBytes;
-    const size_t ws = (size_t)CB * bb + (((CB * bb / 16) & 1) ? 0 : 16);
+    const size_t ws = L.down_type == 14 ? 220 : (size_t)CB * bb + (((CB * bb / 16) & 1) ? 0 : 16);
     const size_t lds_t1 = (size_t)(RD / 2) * 16 * ws + (size_t)s.K * xrec + (size_t)s.K * RD * 4;
-    if (T == 1 && s.K <= 8 && (L.down_type == 2 || L.down_type == 3) && s.F % 256 == 0 && s.E % RD == 0 &&
-        lds_t1 <= 160 * 1024) {
+    const bool t1_type = L.down_type == 2 || L.down_type == 3 || (L.down_type == 14 && L.down_rb % 4 == 0);
+    if (T == 1 && s.K <= 8 && t1_type && s.F % 256 == 0 && s.E % RD == 0 && lds_t1 <= 160 * 1024) {
         const dim3 grid(s.E / RD), block(32 * RD);
-        if (L.down_type == 3) QLAUNCH("down", (down_t1_kernel<3, CB, 3, RD>), grid, block, lds_t1, st, a);
+        if (L.down_type == 14) QLAUNCH("down", (down_t1_kernel<14, CB, 3, RD>), grid, block, lds_t1, st, a);
+        else if (L.down_type == 3) QLAUNCH("down", (down_t1_kernel<3, CB, 3, RD>), grid, block, lds_t1, st, a);
         else QLAUNCH("down", (down_t1_kernel<2, CB, 3, RD>), grid, block, lds_t1, st, a);
         return hipGetLastError();
     }

@@ -34,6 +34,8 @@ CASES = [
     ("x256_t3", 256, 256, 8, 128, 3, 23, orc.T_Q4_0, False),     # 256 experts (kernel maximum)
     ("f64_t3", 256, 16, 4, 64, 3, 24, orc.T_Q4_1, False),        # smallest n_ff_exp
     ("q6k_f768_t1", 2048, 128, 8, 768, 1, 25, orc.T_Q6_K, True),  # odd super-blocks per row
+    ("q235b_q6k_t1", 4096, 128, 8, 1536, 1, 29, orc.T_Q6_K, False),  # one-token down kernel, Q6_K rows
+    ("q480b_q6k_t1", 6144, 160, 8, 2560, 1, 30, orc.T_Q6_K, True),
     # two to four tokens: the small-batch down kernel (several experts per wave, fused combine)
     ("q235b_q41_t3", 4096, 128, 8, 1536, 3, 26, orc.T_Q4_1, False),
     ("q30b_t2", 2048, 128, 8, 768, 2, 27, orc.T_Q4_0, True),
