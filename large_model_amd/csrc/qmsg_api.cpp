@@ -876,13 +876,16 @@ int qmsg_moe_chain(qmsg_ctx *c, int first, int n, float *d_h, int T, float eps)
     if ((uintptr_t)d_h & 15) return fail(c, QMSG_E_INVALID, "qmsg_moe_chain: d_h must be 16-byte aligned");
     HIP_TRY(c, hipSetDevice(c->device));
     const int E = c->cfg.n_embd;
-    for (int l = first; l < first + n; l++) {
+    for (int l = first; l < first + n; l++)
         if (!c->layers[(size_t)l].ready) return fail(c, QMSG_E_INVALID, "layer %d has no weights", l);
-        LAUNCH(c, "rmsnorm", launch_rmsnorm(d_h, c->layers[(size_t)l].norm, c->d_x, T, E, eps, c->stream));
+    /* each layer's residual add h += out rides in the next layer's rmsnorm launch */
+    for (int l = first; l < first + n; l++) {
+        const float *pending = l > first ? c->d_out : nullptr;
+        LAUNCH(c, "rmsnorm", launch_rmsnorm(d_h, pending, c->layers[(size_t)l].norm, c->d_x, T, E, eps, c->stream));
         const int rc = run_layer(c, l, c->d_x, T, c->d_out, 0);
         if (rc) return rc;
-        LAUNCH(c, "add", launch_add_rows(d_h, c->d_out, (size_t)T * E, c->stream));
     }
+    LAUNCH(c, "add", launch_add_rows(d_h, c->d_out, (size_t)T * E, c->stream));
     return QMSG_OK;
 }
 
@@ -897,7 +900,7 @@ int qmsg_rmsnorm_device(qmsg_ctx *c, float *d_y, const float *d_x, const float *
     if (((uintptr_t)d_x | (uintptr_t)d_y | (uintptr_t)d_w) & 15)
         return fail(c, QMSG_E_INVALID, "qmsg_rmsnorm_device: d_x, d_y and d_w must be 16-byte aligned");
     HIP_TRY(c, hipSetDevice(c->device));
-    LAUNCH(c, "rmsnorm", launch_rmsnorm(d_x, d_w, d_y, rows, n, eps, c->stream));
+    LAUNCH(c, "rmsnorm", launch_rmsnorm(const_cast<float *>(d_x), nullptr, d_w, d_y, rows, n, eps, c->stream));
     return QMSG_OK;
 }
 

@@ -161,7 +161,9 @@ inline size_t rmsnorm_lds_bytes(int E)
     const size_t sq = E % 512 == 0 ? (size_t)(E / 64) * 65 : (size_t)E;      /* squares, in doubles */
     return sq * 8;
 }
-hipError_t launch_rmsnorm(const float *x, const float *w, float *y, int T, int E, float eps, hipStream_t st);
+/* y = rmsnorm(x) * w per row of E floats; with add (not NULL) x += add first, stored back. */
+hipError_t launch_rmsnorm(float *x, const float *add, const float *w, float *y, int T, int E, float eps,
+                          hipStream_t st);
 hipError_t launch_add_rows(float *h, const float *d, size_t n, hipStream_t st);
 hipError_t launch_set_col0(float *m, int rows, int stride, const float *vals, float fill, hipStream_t st);
 hipError_t launch_silu(const float *x, int n, float *out, hipStream_t st);

@@ -4064,13 +4064,18 @@ __device__ double ordered_sum_chunked(const double *qt, int C)
  * fma(x, x, ss) equals ss + x*x with the square formed first: every thread forms squares into
  * LDS, and wave 0 forms their sequential sum (ordered_sum_chunked for E a multiple of 512, else
  * one lane term by term). Rows of up to kNormVec * 1024 floats stay in registers, with their
- * weights, loaded before the sum; longer rows are read again for the output. */
+ * weights, loaded before the sum; longer rows are read again for the output. With add, the row
+ * is first x + add in float (the residual add h += out of the previous layer,
+ * src/model.c:1285), stored back to x, and normalised. */
 constexpr int kNormVec = 8;
-__global__ __launch_bounds__(256) void rmsnorm_kernel(const float *x, const float *w, float *y, int E, float eps)
+__global__ __launch_bounds__(256) void rmsnorm_kernel(float *x, const float *add, const float *w, float *y, int E,
+                                                      float eps)
 {
     extern __shared__ __align__(16) double q[];      /* the squares */
     __shared__ double inv;
-    const float4 *row = (const float4 *)(x + (size_t)blockIdx.x * E);
+    float4 *xrow = (float4 *)(x + (size_t)blockIdx.x * E);
+    const float4 *arow = add ? (const float4 *)(add + (size_t)blockIdx.x * E) : nullptr;
+    const float4 *row = xrow;
     const float4 *w4 = (const float4 *)w;
     float4 *out = (float4 *)(y + (size_t)blockIdx.x * E);
     const int n4 = E >> 2, tid = threadIdx.x;
@@ -4085,6 +4090,17 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const float *x, const floa
             if (i < n4) {
                 xv[m] = row[i];
                 wv[m] = w ? w4[i] : one;
+            }
+        }
+        if (arow) {
+#pragma unroll
+            for (int m = 0; m < kNormVec; m++) {
+                const int i = base + tid + 256 * m;
+                if (i < n4) {
+                    const float4 d = arow[i];
+                    xv[m] = make_float4(xv[m].x + d.x, xv[m].y + d.y, xv[m].z + d.z, xv[m].w + d.w);
+                    xrow[i] = xv[m];
+                }
             }
         }
 #pragma unroll
@@ -4132,13 +4148,14 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const float *x, const floa
     }
 }
 
-hipError_t launch_rmsnorm(const float *x, const float *w, float *y, int T, int E, float eps, hipStream_t st)
+hipError_t launch_rmsnorm(float *x, const float *add, const float *w, float *y, int T, int E, float eps,
+                          hipStream_t st)
 {
     if (T <= 0) return hipSuccess;
     if (E % 4) return hipErrorInvalidValue;
     static_assert(kSumPitch == 65, "rmsnorm_lds_bytes assumes the pitch");
     if (rmsnorm_lds_bytes(E) > 160 * 1024) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(rmsnorm_kernel, dim3(T), dim3(256), rmsnorm_lds_bytes(E), st, x, w, y, E, eps);
+    hipLaunchKernelGGL(rmsnorm_kernel, dim3(T), dim3(256), rmsnorm_lds_bytes(E), st, x, add, w, y, E, eps);
     return hipGetLastError();
 }
 
