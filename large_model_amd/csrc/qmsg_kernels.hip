@@ -2837,13 +2837,13 @@ static void launch_mx(const MxArgs &a, int rows, int maxt, MxShape shape, hipStr
     else launch_mx_shape<TYPE, GU, 1, 4, 4, 1>(a, rows, maxt, st);
 }
 
-/* Whether the MFMA kernels take this layer: Q4_0 gate and up; Q4_0, Q4_1 or Q6_K down (Q6_K
+/* Whether the MFMA kernels take this layer: gate and up both Q4_0 or both Q4_1; Q4_0, Q4_1 or Q6_K down (Q6_K
  * rows a multiple of 4 bytes long); 32-blocks in whole chunks; rows in whole blocks' tiles. */
 bool mx_supported(const Shape &s, const LayerDev &L, int *down_mx)
 {
     const int nbE = s.E / 32, nbF = s.F / 32;
-    const bool gu = L.gate_type == 2 && L.up_type == 2 && nbE % kMxC == 0 && s.F % 128 == 0 &&
-                    (uint64_t)s.F * L.gate_rb < (1ull << 31);
+    const bool gu = L.gate_type == L.up_type && (L.gate_type == 2 || L.gate_type == 3) && nbE % kMxC == 0 &&
+                    s.F % 128 == 0 && (uint64_t)s.F * L.gate_rb < (1ull << 31);
     const bool dn = (L.down_type == 2 || L.down_type == 3 || (L.down_type == 14 && L.down_rb % 4 == 0)) &&
                     nbF % kMxC == 0 && s.E % 256 == 0 && (uint64_t)s.E * L.down_rb < (1ull << 31);
     if (down_mx) *down_mx = dn;
@@ -2869,7 +2869,8 @@ hipError_t launch_experts_mx(const Shape &s, const LayerDev &L, const Scratch &S
     a.rec = S.mxx;
     a.rec_out = S.mxa;
     a.S = S;
-    launch_mx<2, 1>(a, s.F, maxt, mx_shape(s, T, 1, 2), st);
+    if (L.gate_type == 3) launch_mx<3, 1>(a, s.F, maxt, mx_shape(s, T, 1, 3), st);
+    else launch_mx<2, 1>(a, s.F, maxt, mx_shape(s, T, 1, 2), st);
     if (!down_mx) {
         const hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;

@@ -82,3 +82,33 @@ def test_mfma_repeated_calls_and_sizes(q):
             ctx.set_path(q.PATH_MFMA)
             out = ctx.moe(0, x)
             assert np.array_equal(_bits(out), _bits(ref)), T
+
+
+GATE_UP_CASES = [
+    # name, E, X, K, F, T, seed, gate/up type, down type
+    ("q235b_gq41_t24", 4096, 128, 8, 1536, 24, 31, orc.T_Q4_1, orc.T_Q4_0),     # 4-slot blocks
+    ("q235b_gq41_t64", 4096, 128, 8, 1536, 64, 32, orc.T_Q4_1, orc.T_Q6_K),     # 8-slot blocks
+    ("q30b_gq41_t256", 2048, 128, 8, 768, 256, 33, orc.T_Q4_1, orc.T_Q4_1),     # 16-slot blocks
+]
+
+
+@pytest.mark.parametrize("name,E,X,K,F,T,seed,gt,dt", GATE_UP_CASES, ids=[c[0] for c in GATE_UP_CASES])
+def test_mfma_q41_gateup_bit_exact(q, name, E, X, K, F, T, seed, gt, dt):
+    """Q4_1 gate and up rows on the MFMA kernels (unsigned codes, the offset chain
+    off = fma(m, ds, off), src/kernels.c:113-120): every intermediate against the oracle."""
+    print(f"[case] mfma gate/up {name} T={T}", flush=True)
+    x = orc.make_input(E, T, seed)
+    host = orc.Layer(E, X, K, F, seed, gate_type=gt, up_type=gt, down_type=dt, experts=[])
+    ref_out, ref = host.moe(x, debug=True)
+    with q.Context(E, X, K, F, n_layer=1, max_tokens=T) as ctx:
+        ctx.synth(0, seed, gate_type=gt, up_type=gt, down_type=dt)
+        results = []
+        for path in (q.PATH_MFMA, q.PATH_AUTO):
+            ctx.set_path(path)
+            results.append(ctx.moe_debug(0, x))
+    for o, g in results:
+        for k in ("sel", "start", "slot_t", "slot_of", "active"):
+            assert np.array_equal(g[k], ref[k]), k
+        for k in ("logits", "wt", "xq", "gu", "act", "aq", "dn"):
+            assert np.array_equal(_bits(g[k]), _bits(ref[k])), k
+        assert np.array_equal(_bits(o), _bits(ref_out)), "layer output"
