@@ -75,10 +75,10 @@ typedef struct qmsg_ctx qmsg_ctx;
  * blocks, the per-block int32 dots and the fp32 rows follow the reference's AVX path exactly.
  *   EXACT: per-row VALU kernels (integer dot4 lane sums, the reference's fp32 lane chains).
  *   MFMA:  the lane sums of 16 rows x 2 slots per f16 MFMA (exact small integers), the same
- *          fp32 chains on the VALU; for batches of two or more tokens with gate and up both
- *          Q4_0 or both Q4_1 (down Q4_0, Q4_1 or Q6_K; other down rows on the EXACT kernel).
+ *          fp32 chains on the VALU; for batches of two or more tokens with gate and up of one
+ *          type (down Q4_0, Q4_1 or Q6_K; other down rows on the EXACT kernel).
  *   AUTO:  per stage: Q4_0 gate/up on MFMA for batches averaging at least 1.25 slots per
- *          active expert, Q4_1 gate/up at every batch of two or more tokens, down on MFMA for
+ *          active expert, Q4_1 / Q6_K gate/up at every batch of two or more tokens, down on MFMA for
  *          batches of at least 72 slots (tokens x n_used; Q6_K down rows: 32), EXACT
  *          otherwise.
  *   FP32:  the reference's --exact mode (qms_exact_math = 1, src/quant.c:95-115,

@@ -791,14 +791,14 @@ static int run_layer_s(qmsg_ctx *c, const Scratch &S, int layer, const float *d_
     }
     /* Q4_0 gate and up take the streaming gate/up kernel (which also routes one-token batches),
      * other types the slot-tile row kernel; batches with several slots per expert take the
-     * MFMA kernels when gate and up are both Q4_0 or both Q4_1 */
+     * MFMA kernels when gate and up share a type */
     const bool q40 = d.gate_type == QMSG_T_Q4_0 && d.up_type == QMSG_T_Q4_0;
     int dn_ok = 0;
     const bool many = !use_small_route(T, s.K);
-    const bool gu_ok = mx_supported(s, d, &dn_ok) && many;   /* Q4_0 or Q4_1 gate and up */
+    const bool gu_ok = mx_supported(s, d, &dn_ok) && many;   /* gate and up of one type */
     const bool forced = c->path == QMSG_PATH_MFMA, autop = c->path == QMSG_PATH_AUTO;
-    /* Q4_1 gate/up has only the slot-tile row kernel besides, which the MFMA kernels beat at every
-     * batch (235B shape: 89 / 258 us at 8 tokens, 320 / 1548 at 64) */
+    /* Q4_1 and Q6_K gate/up have only the slot-tile row kernel besides, which the MFMA kernels
+     * beat at every batch (235B shape, Q4_1: 89 / 258 us at 8 tokens, 320 / 1548 at 64) */
     const bool gu_mx = gu_ok && (forced || (autop && (!q40 || mx_auto(T, s.K, s.X))));
     const bool dn_mx = dn_ok && many && (forced || (autop && mx_auto_down(T, s.K, d.down_type)));
     LAUNCH(c, "route", launch_route(s, d, S, d_xn, T, c->stream));

@@ -136,8 +136,8 @@ hipError_t launch_select(const Shape &s, const Scratch &S, int T, int gateup_rou
 hipError_t launch_gateup_exact(const Shape &s, const LayerDev &L, const Scratch &S, int T, int debug, int n_cu,
                                hipStream_t st);
 /* The expert products on the matrix cores (order-exact): gate/up, then down and the combine.
- * mx_supported: whether the layer's types and shape fit the MFMA kernels (gate and up both Q4_0
- * or both Q4_1;
+ * mx_supported: whether the layer's types and shape fit the MFMA kernels (gate and up of one
+ * type: Q4_0, Q4_1 or Q6_K;
  * *down_mx: whether down runs on them too, else on the exact down kernel). */
 bool mx_supported(const Shape &s, const LayerDev &L, int *down_mx);
 hipError_t launch_experts_mx(const Shape &s, const LayerDev &L, const Scratch &S, float *out, int T, int debug,

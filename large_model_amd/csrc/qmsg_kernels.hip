@@ -2450,14 +2450,14 @@ __device__ __forceinline__ uint32_t q6_word(LdsPtr base, int off)
  * q points at the lane's code words (row base + 4*lg), rb at the row base. Every offset and
  * shift is a constant. The 6-bit code dword is the low nibbles (shifted down for the upper
  * two blocks of a half) with the two high bits of qh moved to bits 4-5 (src/kernels.c:148-160). */
-template <int O, int B>
+template <int O, int B, int TS>
 __device__ __forceinline__ MxB mx_weights_q6(LdsPtr q, LdsPtr rb, int t, int kh)
 {
     constexpr int WS = mx_wstride(14), h = B >> 2, g = B & 3, ns = 4 * (g >> 1), hs = 2 * g;
     constexpr int oql = O + 64 * h + 32 * (g & 1), oqh = O + 128 + 32 * h;
     const uint32_t m8 = 0x00ff00ffu, bias = 0x64006400u, lo4 = 0x0f0f0f0fu;
     auto code = [&](int dq) {
-        const uint32_t ql = q6_word<O>(q, 16 * t * WS + oql + dq), qh = q6_word<O>(q, 16 * t * WS + oqh + dq);
+        const uint32_t ql = q6_word<O>(q, TS * t * WS + oql + dq), qh = q6_word<O>(q, TS * t * WS + oqh + dq);
         uint32_t hi;
         if constexpr (hs < 4) hi = (qh << (4 - hs)) & 0x30303030u;
         else if constexpr (hs == 4) hi = qh & 0x30303030u;
@@ -2468,22 +2468,22 @@ __device__ __forceinline__ MxB mx_weights_q6(LdsPtr q, LdsPtr rb, int t, int kh)
     MxB w;
     w.op = mx_pack_codes(and_or(cA, m8, bias), and_or(cA >> 8, m8, bias), and_or(cB, m8, bias),
                          and_or(cB >> 8, m8, bias));
-    const uint32_t scw = *(const __attribute__((address_space(3))) uint16_t *)(rb + 16 * t * WS + O + 192 + 8 * h + 2 * g);
+    const uint32_t scw = *(const __attribute__((address_space(3))) uint16_t *)(rb + TS * t * WS + O + 192 + 8 * h + 2 * g);
     const int sa = (int)(int8_t)(scw & 0xffu), sbv = (int)(int8_t)(scw >> 8);
     w.sab = ((uint32_t)sa & 0xffffu) | ((uint32_t)sbv << 16);
     w.sc = (float)(kh ? sbv : sa);
-    w.dw = *(const __attribute__((address_space(3))) uint16_t *)(rb + 16 * t * WS + O + 208);
+    w.dw = *(const __attribute__((address_space(3))) uint16_t *)(rb + TS * t * WS + O + 208);
     return w;
 }
 
 /* One Q6_K block B of the staged chunk: NP slot pairs against the wave's two 16-row tiles. */
-template <int NP, int O, int B>
+template <int NP, int O, int B, int TS>
 __device__ __forceinline__ void mx_block_q6(const MxStreams &st, int kh, f32x4 (&acc)[2][4], float (&cr)[2][4])
 {
     constexpr int RS = mx_rstride(14), RB = B * mx_recl(14);
     MxB w[2];
 #pragma unroll
-    for (int t = 0; t < 2; t++) w[t] = mx_weights_q6<O, B>(st.q, st.dw, t, kh);
+    for (int t = 0; t < 2; t++) w[t] = mx_weights_q6<O, B, TS>(st.q, st.dw, t, kh);
 #pragma unroll
     for (int p = 0; p < NP; p++) {
         /* volatile: keeps each A read a single read into the MFMA operand (records 832 bytes
@@ -2509,8 +2509,9 @@ __device__ __forceinline__ void mx_block_q6(const MxStreams &st, int kh, f32x4 (
     }
 }
 
-/* A staged Q6_K super-block, its 8 blocks unrolled (offsets and shifts depend on the block). */
-template <int NP, int O>
+/* A staged Q6_K super-block, its 8 blocks unrolled (offsets and shifts depend on the block);
+ * the wave's two tiles TS staged rows apart. */
+template <int NP, int O, int TS>
 __device__ __forceinline__ void mx_chunk_q6(const uint8_t *W, const uint8_t *R, int lr, int lg, int kh, int jd,
                                             int offa_lo, int offa_hi, f32x4 (&acc)[2][4], float (&cr)[2][4])
 {
@@ -2523,21 +2524,21 @@ __device__ __forceinline__ void mx_chunk_q6(const uint8_t *W, const uint8_t *R, 
     st.dw = (LdsPtr)(W + lr * WS);
     st.acc = st.d;                          /* (Q6_K starts its MFMAs from zero) */
     mx_opaque(st);
-    mx_block_q6<NP, O, 0>(st, kh, acc, cr);
+    mx_block_q6<NP, O, 0, TS>(st, kh, acc, cr);
     __builtin_amdgcn_sched_barrier(0);
-    mx_block_q6<NP, O, 1>(st, kh, acc, cr);
+    mx_block_q6<NP, O, 1, TS>(st, kh, acc, cr);
     __builtin_amdgcn_sched_barrier(0);
-    mx_block_q6<NP, O, 2>(st, kh, acc, cr);
+    mx_block_q6<NP, O, 2, TS>(st, kh, acc, cr);
     __builtin_amdgcn_sched_barrier(0);
-    mx_block_q6<NP, O, 3>(st, kh, acc, cr);
+    mx_block_q6<NP, O, 3, TS>(st, kh, acc, cr);
     __builtin_amdgcn_sched_barrier(0);
-    mx_block_q6<NP, O, 4>(st, kh, acc, cr);
+    mx_block_q6<NP, O, 4, TS>(st, kh, acc, cr);
     __builtin_amdgcn_sched_barrier(0);
-    mx_block_q6<NP, O, 5>(st, kh, acc, cr);
+    mx_block_q6<NP, O, 5, TS>(st, kh, acc, cr);
     __builtin_amdgcn_sched_barrier(0);
-    mx_block_q6<NP, O, 6>(st, kh, acc, cr);
+    mx_block_q6<NP, O, 6, TS>(st, kh, acc, cr);
     __builtin_amdgcn_sched_barrier(0);
-    mx_block_q6<NP, O, 7>(st, kh, acc, cr);
+    mx_block_q6<NP, O, 7, TS>(st, kh, acc, cr);
 }
 
 /* The LDS DMA: `bytes` (4 or 16) from src of every active lane to dst + lane * bytes. */
@@ -2576,6 +2577,9 @@ void mx_kernel(MxArgs a)
 {
     extern __shared__ __align__(16) uint8_t smem[];
     using Lay = MxLayout<TYPE, WSG, PPW, NW>;
+    /* Q6_K gate/up stages its gate rows, then its up rows (so the DMA steps through one matrix
+     * at a time); the Q4 kernels interleave them by 16-row groups */
+    constexpr bool QS6 = GU && TYPE == 14;
     constexpr int RWG = Lay::RWG, SWG = Lay::SWG, WS = Lay::WS, BUF = Lay::BUF;
     if ((int)blockIdx.y >= a.S.meta[1]) return;
     const int4 tl = a.S.tiles[blockIdx.y];
@@ -2610,18 +2614,26 @@ void mx_kernel(MxArgs a)
      * rows, whose 108 instructions per chunk would take too many registers): the first one,
      * stepped by 512 units per instruction. */
     static_assert(RWG * Lay::WUR % 64 == 0, "whole DMA instructions per chunk");
+    static_assert(!QS6 || (RWG / 2) * Lay::WUR % 64 == 0, "gate rows in whole DMA instructions");
     constexpr int NQ = (Lay::WINSTR + NW - 1) / NW;
     uint32_t qoff[TYPE == 14 ? 1 : NQ];
     int qu = 0;
     auto unit_off = [&](int n, int *u_out) -> uint32_t {
         const int i = n / Lay::WUR, u = n - i * Lay::WUR;
         *u_out = u;
-        const int row = GU ? R0 + 16 * (i >> 5) + (i & 15) : R0 + i;
-        const uint32_t up = GU && (i & 31) >= 16 ? 0x80000000u : 0u;
+        /* Q6_K gate/up: gate rows first, up rows from staged row RWG/2 on (QS6) */
+        const int row = QS6 ? R0 + (i % (RWG / 2)) : (GU ? R0 + 16 * (i >> 5) + (i & 15) : R0 + i);
+        const uint32_t up = GU && !QS6 && (i & 31) >= 16 ? 0x80000000u : 0u;
         return ((uint32_t)row * rb + (uint32_t)(Lay::WUNIT * u)) | up;
     };
+    /* Q6_K gate/up: the first instruction of this wave in the up half, and its source */
+    constexpr int HALF = Lay::WINSTR / 2;
+    const int q_up = wave + NW * ((HALF - wave + NW - 1) / NW);
+    uint32_t qoff_up = 0;
+    int qu_up = 0;
     if constexpr (TYPE == 14) {
         qoff[0] = unit_off(64 * wave + lane, &qu);
+        if constexpr (QS6) qoff_up = unit_off(64 * (q_up - HALF) + lane, &qu_up);
     } else {
 #pragma unroll
         for (int j = 0; j < NQ; j++) {
@@ -2636,11 +2648,17 @@ void mx_kernel(MxArgs a)
             const uint32_t cb = (uint32_t)(c * 210 - 2 * (c & 1));
             uint32_t o = qoff[0];
             int u = qu;
+            const uint8_t *wq = wb0;
             /* 64 NW units on: STEP / WUR rows and STEP % WUR units, one row more where the
              * units wrap */
             constexpr int STEP = 64 * NW, SR = STEP / Lay::WUR, SU = STEP % Lay::WUR;
             for (int q = wave; q < Lay::WINSTR; q += NW) {
-                dma_to_lds<4>(wb0 + (o + cb), base + 256 * q);
+                if (QS6 && q == q_up) {        /* into the up half: the up matrix from its row R0 */
+                    o = qoff_up;
+                    u = qu_up;
+                    wq = wb1;
+                }
+                dma_to_lds<4>(wq + (o + cb), base + 256 * q);
                 u += SU;
                 o += SR * rb + 4 * SU;
                 if (u >= Lay::WUR) {
@@ -2707,11 +2725,12 @@ void mx_kernel(MxArgs a)
                 issue(c + 1, buf ^ 1);
             }
             if constexpr (NP > 0) {
-                const uint8_t *Wl = smem + buf * BUF + (32 * wr) * WS;
+                const uint8_t *Wl = smem + buf * BUF + ((QS6 ? 16 : 32) * wr) * WS;
                 const uint8_t *Rl = smem + buf * BUF + Lay::WBYTES + (2 * PPW * ws) * Lay::RS;
                 if constexpr (TYPE == 14) {
-                    if (c & 1) mx_chunk_q6<NP, 2>(Wl, Rl, lr, lg, kh, jd, offa_lo, offa_hi, acc, cr);
-                    else mx_chunk_q6<NP, 0>(Wl, Rl, lr, lg, kh, jd, offa_lo, offa_hi, acc, cr);
+                    constexpr int TS6 = QS6 ? RWG / 2 : 16;
+                    if (c & 1) mx_chunk_q6<NP, 2, TS6>(Wl, Rl, lr, lg, kh, jd, offa_lo, offa_hi, acc, cr);
+                    else mx_chunk_q6<NP, 0, TS6>(Wl, Rl, lr, lg, kh, jd, offa_lo, offa_hi, acc, cr);
                 } else {
                     /* gate/up starts its MFMAs from the records' sums; down, whose registers
                      * are tighter, subtracts the bias from B (measured both ways) */
@@ -2837,13 +2856,15 @@ static void launch_mx(const MxArgs &a, int rows, int maxt, MxShape shape, hipStr
     else launch_mx_shape<TYPE, GU, 1, 4, 4, 1>(a, rows, maxt, st);
 }
 
-/* Whether the MFMA kernels take this layer: gate and up both Q4_0 or both Q4_1; Q4_0, Q4_1 or Q6_K down (Q6_K
+/* Whether the MFMA kernels take this layer: gate and up of one type (Q4_0, Q4_1, or Q6_K with
+ * rows a multiple of 4 bytes long); Q4_0, Q4_1 or Q6_K down (Q6_K
  * rows a multiple of 4 bytes long); 32-blocks in whole chunks; rows in whole blocks' tiles. */
 bool mx_supported(const Shape &s, const LayerDev &L, int *down_mx)
 {
     const int nbE = s.E / 32, nbF = s.F / 32;
-    const bool gu = L.gate_type == L.up_type && (L.gate_type == 2 || L.gate_type == 3) && nbE % kMxC == 0 &&
-                    s.F % 128 == 0 && (uint64_t)s.F * L.gate_rb < (1ull << 31);
+    const bool gu = L.gate_type == L.up_type &&
+                    (L.gate_type == 2 || L.gate_type == 3 || (L.gate_type == 14 && L.gate_rb % 4 == 0)) &&
+                    nbE % kMxC == 0 && s.F % 128 == 0 && (uint64_t)s.F * L.gate_rb < (1ull << 31);
     const bool dn = (L.down_type == 2 || L.down_type == 3 || (L.down_type == 14 && L.down_rb % 4 == 0)) &&
                     nbF % kMxC == 0 && s.E % 256 == 0 && (uint64_t)s.E * L.down_rb < (1ull << 31);
     if (down_mx) *down_mx = dn;
@@ -2869,7 +2890,8 @@ hipError_t launch_experts_mx(const Shape &s, const LayerDev &L, const Scratch &S
     a.rec = S.mxx;
     a.rec_out = S.mxa;
     a.S = S;
-    if (L.gate_type == 3) launch_mx<3, 1>(a, s.F, maxt, mx_shape(s, T, 1, 3), st);
+    if (L.gate_type == 14) launch_mx<14, 1>(a, s.F, maxt, mx_shape(s, T, 1, 14), st);
+    else if (L.gate_type == 3) launch_mx<3, 1>(a, s.F, maxt, mx_shape(s, T, 1, 3), st);
     else launch_mx<2, 1>(a, s.F, maxt, mx_shape(s, T, 1, 2), st);
     if (!down_mx) {
         const hipError_t e = hipGetLastError();

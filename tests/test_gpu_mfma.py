@@ -89,13 +89,17 @@ GATE_UP_CASES = [
     ("q235b_gq41_t24", 4096, 128, 8, 1536, 24, 31, orc.T_Q4_1, orc.T_Q4_0),     # 4-slot blocks
     ("q235b_gq41_t64", 4096, 128, 8, 1536, 64, 32, orc.T_Q4_1, orc.T_Q6_K),     # 8-slot blocks
     ("q30b_gq41_t256", 2048, 128, 8, 768, 256, 33, orc.T_Q4_1, orc.T_Q4_1),     # 16-slot blocks
+    ("q235b_gq6k_t24", 4096, 128, 8, 1536, 24, 34, orc.T_Q6_K, orc.T_Q4_0),     # Q6_K gate/up, 4-slot
+    ("q235b_gq6k_t64", 4096, 128, 8, 1536, 64, 35, orc.T_Q6_K, orc.T_Q6_K),     # 8-slot blocks
+    ("q30b_gq6k_t256", 2048, 128, 8, 768, 256, 36, orc.T_Q6_K, orc.T_Q4_1),     # 16-slot blocks
 ]
 
 
 @pytest.mark.parametrize("name,E,X,K,F,T,seed,gt,dt", GATE_UP_CASES, ids=[c[0] for c in GATE_UP_CASES])
-def test_mfma_q41_gateup_bit_exact(q, name, E, X, K, F, T, seed, gt, dt):
+def test_mfma_gateup_types_bit_exact(q, name, E, X, K, F, T, seed, gt, dt):
     """Q4_1 gate and up rows on the MFMA kernels (unsigned codes, the offset chain
-    off = fma(m, ds, off), src/kernels.c:113-120): every intermediate against the oracle."""
+    off = fma(m, ds, off), src/kernels.c:113-120) and Q6_K ones (6-bit codes, sub-scales, the
+    32-scaled offset chain, src/kernels.c:142-170): every intermediate against the oracle."""
     print(f"[case] mfma gate/up {name} T={T}", flush=True)
     x = orc.make_input(E, T, seed)
     host = orc.Layer(E, X, K, F, seed, gate_type=gt, up_type=gt, down_type=dt, experts=[])
