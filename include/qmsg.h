@@ -77,8 +77,8 @@ typedef struct qmsg_ctx qmsg_ctx;
  *   MFMA:  the lane sums of 16 rows x 2 slots per f16 MFMA (exact small integers), the same
  *          fp32 chains on the VALU; for batches of two or more tokens with gate and up of one
  *          type (down Q4_0, Q4_1 or Q6_K; other down rows on the EXACT kernel).
- *   AUTO:  per stage: Q4_0 gate/up on MFMA for batches averaging at least 1.25 slots per
- *          active expert, Q4_1 / Q6_K gate/up at every batch of two or more tokens, down on MFMA for
+ *   AUTO:  per stage: Q4_0 / Q4_1 gate/up on MFMA for batches averaging at least 1.25 slots
+ *          per active expert, Q6_K gate/up from 2.5, down on MFMA for
  *          batches of at least 72 slots (tokens x n_used; Q6_K down rows: 32), EXACT
  *          otherwise.
  *   FP32:  the reference's --exact mode (qms_exact_math = 1, src/quant.c:95-115,

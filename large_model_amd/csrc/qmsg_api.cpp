@@ -789,25 +789,25 @@ static int run_layer_s(qmsg_ctx *c, const Scratch &S, int layer, const float *d_
         LAUNCH(c, "layer", launch_layer_fp32(s, d, S, d_xn, d_out, T, c->stream));
         return QMSG_OK;
     }
-    /* Q4_0 gate and up take the streaming gate/up kernel (which also routes one-token batches),
-     * other types the slot-tile row kernel; batches with several slots per expert take the
-     * MFMA kernels when gate and up share a type */
-    const bool q40 = d.gate_type == QMSG_T_Q4_0 && d.up_type == QMSG_T_Q4_0;
+    /* gate and up of one type take the streaming gate/up kernel (which also routes one-token
+     * batches), mixed types the slot-tile row kernel; batches with several slots per expert
+     * take the MFMA kernels when gate and up share a type */
+    const bool q4 = gateup_streams(d);      /* the streaming gate/up kernel takes gate and up */
     int dn_ok = 0;
     const bool many = !use_small_route(T, s.K);
     const bool gu_ok = mx_supported(s, d, &dn_ok) && many;   /* gate and up of one type */
     const bool forced = c->path == QMSG_PATH_MFMA, autop = c->path == QMSG_PATH_AUTO;
-    /* Q4_1 and Q6_K gate/up have only the slot-tile row kernel besides, which the MFMA kernels
-     * beat at every batch (235B shape, Q4_1: 89 / 258 us at 8 tokens, 320 / 1548 at 64) */
-    const bool gu_mx = gu_ok && (forced || (autop && (!q40 || mx_auto(T, s.K, s.X))));
+    /* against the streaming kernel the MFMA kernels win from 1.25 slots per expert (Q4_1:
+     * 139.7 / 128.2 us at 16 tokens, 173.8 / 174.0 at 24, 196.3 / 216.6 at 32), or 2.5 for Q6_K */
+    const bool gu_mx = gu_ok && (forced || (autop && mx_auto(T, s.K, s.X, d.gate_type)));
     const bool dn_mx = dn_ok && many && (forced || (autop && mx_auto_down(T, s.K, d.down_type)));
     LAUNCH(c, "route", launch_route(s, d, S, d_xn, T, c->stream));
-    LAUNCH(c, "select", launch_select(s, S, T, q40 ? 1 : 0, c->stream));
+    LAUNCH(c, "select", launch_select(s, S, T, q4 ? 1 : 0, c->stream));
     if (gu_mx) {
         LAUNCH(c, "experts", launch_experts_mx(s, d, S, d_out, T, debug, c->stream));
         return QMSG_OK;
     }
-    if (!q40) LAUNCH(c, "gateup", launch_gateup_tiles(s, d, S, T, c->stream));
+    if (!q4) LAUNCH(c, "gateup", launch_gateup_tiles(s, d, S, T, c->stream));
     else LAUNCH(c, "gateup", launch_gateup_exact(s, d, S, T, debug, c->n_cu, c->stream));
     if (dn_mx) LAUNCH(c, "down", launch_down_mx(s, d, S, d_out, T, c->stream));
     else LAUNCH(c, "down", launch_down_exact(s, d, S, d_out, T, 1, c->stream));

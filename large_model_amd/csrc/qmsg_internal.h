@@ -53,12 +53,15 @@ constexpr int kMxRec = 128;
  * needs and the combine: Q4_0 37.9 / 34.1 at 4 tokens, 44.9 / 44.1 at 6, 53.2 / 53.8 at 8, 64.4 /
  * 69.3 at 12; Q6_K 39.8 / 41.0 at 2, 59.2 / 53.6 at 3, 66.0 / 71.6 at 4, 105 / 118 at 8. */
 constexpr int kMxAutoQuarters = 5;
+/* Q6_K gate/up (its MFMA kernel unpacks 6-bit codes): from 2.5 slots per expert (streaming /
+ * MFMA us: 442 / 487 at 32 tokens, 618 / 435 at 48) */
+constexpr int kMxAutoQuartersQ6 = 10;
 constexpr int kMxDownMinSlotsQ4 = 72;
 constexpr int kMxDownMinSlotsQ6 = 32;
-inline bool mx_auto(int T, int K, int X)
+inline bool mx_auto(int T, int K, int X, int gate_type)
 {
     const long NS = (long)T * K, act = X < NS ? X : NS;
-    return 4 * NS >= (long)kMxAutoQuarters * act;
+    return 4 * NS >= (long)(gate_type == 14 ? kMxAutoQuartersQ6 : kMxAutoQuarters) * act;
 }
 inline bool mx_auto_down(int T, int K, int down_type)
 {
@@ -133,6 +136,9 @@ hipError_t launch_route(const Shape &s, const LayerDev &L, const Scratch &S, con
                         hipStream_t st);
 /* Top-K and dispatch; a one-token batch is left to the Q4_0 gate/up kernel when gateup_routes. */
 hipError_t launch_select(const Shape &s, const Scratch &S, int T, int gateup_routes, hipStream_t st);
+/* Whether gate and up take the streaming gate/up kernel (launch_gateup_exact): one type, Q4_0,
+ * Q4_1, or Q6_K with rows a multiple of 4 bytes long. */
+bool gateup_streams(const LayerDev &L);
 hipError_t launch_gateup_exact(const Shape &s, const LayerDev &L, const Scratch &S, int T, int debug, int n_cu,
                                hipStream_t st);
 /* The expert products on the matrix cores (order-exact): gate/up, then down and the combine.

@@ -1230,9 +1230,16 @@ __device__ __forceinline__ void q4_rows_nt(const uint32_t *Wrow, int p, const ui
 __host__ __device__ constexpr float finish_scale(int type) { return type == 2 ? 8.0f : (type == 3 ? -1.0f : 32.0f); }
 
 /* LDS bytes of a gateup block (shared by the kernel's carve-up and the launcher). */
-__host__ __device__ constexpr size_t gateup_lds(int W, int NT, int CB, int nP, int sel)
+/* LDS row stride of the gate/up kernel's staged rows (bytes; odd in 16-byte units, Q6_K in
+ * 4-byte units: a super-block from the 4-byte boundary below it, 216 bytes). */
+__host__ __device__ constexpr int gateup_ws(int type, int CB)
 {
-    return (size_t)W * 16 * (CB * 18 + (((CB * 18 / 16) & 1) ? 0 : 16)) + (size_t)NT * nP * kPairBytes +
+    return type == 14 ? 220 : CB * (type == 3 ? 20 : 18) + (((CB * (type == 3 ? 20 : 18) / 16) & 1) ? 0 : 16);
+}
+
+__host__ __device__ constexpr size_t gateup_lds(int W, int NT, int CB, int nP, int sel, int type = 2)
+{
+    return (size_t)W * 16 * gateup_ws(type, CB) + (size_t)NT * nP * kPairBytes +
            (size_t)NT * 2 * 8 * W * 4 +
            (sel ? sizeof(SmallRoute) + (size_t)kMaxExperts * (8 + 4 + 4 + 4) + (kMaxExperts + 1) * 4 : 0);
 }
@@ -1248,15 +1255,20 @@ __host__ __device__ constexpr size_t gateup_lds(int W, int NT, int CB, int nP, i
  * requests its input records before that, so they arrive during the routing. Epilogue:
  * a = silu(g)*u (src/model.c:989-997); the int8 requantisation of a happens where all 32 rows
  * of a block are known (the down kernel). */
-template <int W, int NT, int CB, int D, int SEL>
+template <int TYPE, int W, int NT, int CB, int D, int SEL>
 __global__ __launch_bounds__(64 * W) void gateup_kernel(GateUpArgs a)
 {
     extern __shared__ __align__(16) uint8_t smem[];
+    constexpr bool Q6 = TYPE == 14;
+    static_assert(TYPE == 2 || TYPE == 3 || (Q6 && CB == 8), "Q4_0 / Q4_1 rows, or Q6_K super-blocks");
     constexpr int NTH = 64 * W, R = 8 * W;
-    constexpr int SPR = CB * 18 / 16;                 /* 16-byte slots per row per chunk      */
-    constexpr int NSL = 16 * SPR;                     /* slots of one wave's chunk            */
-    constexpr int SPT = (NSL + 63) / 64;              /* slots per lane per chunk             */
-    constexpr int WS = CB * 18 + ((SPR & 1) ? 0 : 16);/* LDS row stride, odd in 16-byte units */
+    constexpr int BB = TYPE == 3 ? 20 : 18;           /* bytes per 32-block (Q4 types)        */
+    constexpr int UNIT = Q6 ? 4 : 16;                 /* bytes per load                       */
+    constexpr int SPR = Q6 ? 54 : CB * BB / 16;       /* loads per row per chunk              */
+    constexpr int NSL = 16 * SPR;                     /* loads of one wave's chunk            */
+    constexpr int SPT = (NSL + 63) / 64;              /* loads per lane per chunk             */
+    constexpr int WS = gateup_ws(TYPE, CB);           /* LDS row stride                       */
+    typedef typename std::conditional<Q6, uint32_t, u32x4>::type Unit;
     const int nbE = a.E >> 5, nP = nbE >> 1, nchunk = nbE / CB;
     const int xsl = nP * 6;                           /* 16-byte slots of one token's records */
     constexpr int XS = (NT * (4096 / 64) * 6 + NTH - 1) / NTH;  /* x slots per thread in registers */
@@ -1274,13 +1286,16 @@ __global__ __launch_bounds__(64 * W) void gateup_kernel(GateUpArgs a)
     }
     const int r0 = (int)blockIdx.x * R, rw = r0 + 8 * wave;     /* this wave's first row */
     const uint8_t *gbase, *ubase;
-    u32x4 wv[D][SPT];
-    auto load_chunk = [&](int c, u32x4 *dst) {
+    Unit wv[D][SPT];
+    auto load_chunk = [&](int c, Unit *dst) {
 #pragma unroll
         for (int m = 0; m < SPT; m++) {
             const int i = min(lane + 64 * m, NSL - 1), row = i / SPR, j = i - row * SPR;
-            dst[m] = *(const u32x4 *)((row < 8 ? gbase + (size_t)row * a.rb : ubase + (size_t)(row - 8) * a.rb) +
-                                      (size_t)c * CB * 18 + 16 * j);
+            const uint8_t *rp = row < 8 ? gbase + (size_t)row * a.rb : ubase + (size_t)(row - 8) * a.rb;
+            if constexpr (Q6)     /* the super-block starts 2 bytes past a 4-byte boundary on odd chunks */
+                dst[m] = *(const uint32_t *)(rp + (size_t)(c * 210 - 2 * (c & 1)) + 4 * j);
+            else
+                dst[m] = *(const u32x4 *)(rp + (size_t)c * CB * BB + 16 * j);
         }
     };
     auto set_expert = [&](int ex) {
@@ -1366,12 +1381,32 @@ __global__ __launch_bounds__(64 * W) void gateup_kernel(GateUpArgs a)
 #pragma unroll
                     for (int m = 0; m < SPT; m++) {
                         const int i = min(lane + 64 * m, NSL - 1), row = i / SPR, j = i - row * SPR;
-                        *(u32x4 *)(wbuf + row * WS + 16 * j) = wv[d][m];
+                        *(Unit *)(wbuf + row * WS + UNIT * j) = wv[d][m];
                     }
                     wave_sync();
                     if (c + D < nchunk) load_chunk(c + D, wv[d]);
-                    q4_rows_nt<2, NT>((const uint32_t *)(wbuf + qd * WS), p, xbuf, (size_t)nP * kPairBytes,
-                                      c * (CB / 2), CB / 2, nt, acc);
+                    if constexpr (Q6) {
+                        /* the 8 blocks of super-block c (src/kernels.c:142-170) for every slot */
+                        auto superblock = [&](auto al) {
+#pragma unroll
+                            for (int h = 0; h < 2; h++)
+#pragma unroll
+                                for (int g = 0; g < 4; g++) {
+                                    const int blk = c * 8 + h * 4 + g;
+                                    const Q6W w = q6_k_weights<decltype(al)::value>(wbuf + qd * WS, al ? 0 : 2, h, g, p);
+#pragma unroll
+                                    for (int n = 0; n < NT; n++)
+                                        if (n < nt)
+                                            q6_k_token(w, xbuf + (size_t)n * nP * kPairBytes + (size_t)(blk >> 1) * kPairBytes,
+                                                       p, blk & 1, acc[n]);
+                                }
+                        };
+                        if (c & 1) superblock(std::integral_constant<bool, false>());
+                        else superblock(std::integral_constant<bool, true>());
+                    } else {
+                        q4_rows_nt<TYPE, NT>((const uint32_t *)(wbuf + qd * WS), p, xbuf, (size_t)nP * kPairBytes,
+                                             c * (CB / 2), CB / 2, nt, acc);
+                    }
                     if (c == 0 && g0 == s_begin) PHASE(1024, 3);
                 }
             }
@@ -1379,7 +1414,7 @@ __global__ __launch_bounds__(64 * W) void gateup_kernel(GateUpArgs a)
         if (g0 == s_begin) PHASE(1024, 4);
 #pragma unroll
         for (int n = 0; n < NT; n++) {
-            const float v = quad_finish(acc[n], 8.0f);
+            const float v = quad_finish(acc[n], finish_scale(TYPE));
             if (p == 0 && n < nt) res[n * 2 * R + rho] = v;
         }
         __syncthreads();
@@ -1397,21 +1432,31 @@ __global__ __launch_bounds__(64 * W) void gateup_kernel(GateUpArgs a)
     PHASE(1024, 5);
 }
 
-template <int W, int NT, int SEL>
+template <int TYPE, int W, int NT, int SEL>
 static void launch_gateup_w(const GateUpArgs &a, int CB, dim3 grid, size_t lds, hipStream_t st)
 {
-    if (CB == 32) QLAUNCH("gateup", (gateup_kernel<W, NT, 32, 2, SEL>), grid, dim3(64 * W), lds, st, a);
-    else if (CB == 16) QLAUNCH("gateup", (gateup_kernel<W, NT, 16, 2, SEL>), grid, dim3(64 * W), lds, st, a);
-    else QLAUNCH("gateup", (gateup_kernel<W, NT, 8, 1, SEL>), grid, dim3(64 * W), lds, st, a);
+    if constexpr (TYPE == 14)      /* a super-block per chunk, three in flight */
+        QLAUNCH("gateup", (gateup_kernel<TYPE, W, NT, 8, 3, SEL>), grid, dim3(64 * W), lds, st, a);
+    else if (CB == 16) QLAUNCH("gateup", (gateup_kernel<TYPE, W, NT, 16, 2, SEL>), grid, dim3(64 * W), lds, st, a);
+    else QLAUNCH("gateup", (gateup_kernel<TYPE, W, NT, 8, 1, SEL>), grid, dim3(64 * W), lds, st, a);
 }
 
-template <int NT, int SEL>
+template <int TYPE, int NT, int SEL>
 static void launch_gateup_nt(const GateUpArgs &a, int W, int CB, dim3 grid, size_t lds, hipStream_t st)
 {
-    if (W == 6) launch_gateup_w<6, NT, SEL>(a, CB, grid, lds, st);
-    else if (W == 4) launch_gateup_w<4, NT, SEL>(a, CB, grid, lds, st);
-    else if (W == 3) launch_gateup_w<3, NT, SEL>(a, CB, grid, lds, st);
-    else launch_gateup_w<2, NT, SEL>(a, CB, grid, lds, st);
+    if (W == 6) launch_gateup_w<TYPE, 6, NT, SEL>(a, CB, grid, lds, st);
+    else if (W == 4) launch_gateup_w<TYPE, 4, NT, SEL>(a, CB, grid, lds, st);
+    else if (W == 3) launch_gateup_w<TYPE, 3, NT, SEL>(a, CB, grid, lds, st);
+    else launch_gateup_w<TYPE, 2, NT, SEL>(a, CB, grid, lds, st);
+}
+
+template <int TYPE>
+static void launch_gateup_type(const GateUpArgs &a, int sel, int NT, int W, int CB, dim3 grid, size_t lds,
+                               hipStream_t st)
+{
+    if (sel) launch_gateup_nt<TYPE, 1, 1>(a, W, CB, grid, lds, st);     /* one token: NT == 1 */
+    else if (NT == 2) launch_gateup_nt<TYPE, 2, 0>(a, W, CB, grid, lds, st);
+    else launch_gateup_nt<TYPE, 1, 0>(a, W, CB, grid, lds, st);
 }
 
 /* Waves per gateup block: the W (rows 8W per block) whose grid, at the largest possible
@@ -1428,6 +1473,12 @@ int gateup_waves(int F, int max_active, int n_cu, int batch)
         if (!best || cost < best_cost) { best = W; best_cost = (int)cost; }
     }
     return best;
+}
+
+bool gateup_streams(const LayerDev &L)
+{
+    return L.gate_type == L.up_type &&
+           (L.gate_type == 2 || L.gate_type == 3 || (L.gate_type == 14 && L.gate_rb % 4 == 0));
 }
 
 hipError_t launch_gateup_exact(const Shape &s, const LayerDev &L, const Scratch &S, int T, int debug, int n_cu,
@@ -1459,13 +1510,13 @@ hipError_t launch_gateup_exact(const Shape &s, const LayerDev &L, const Scratch 
     const int W = gateup_waves(s.F, rows_y, n_cu, !sel);
     if (!W) return hipErrorInvalidValue;
     dim3 grid(s.F / (8 * W), rows_y);
-    const size_t lds = gateup_lds(W, NT, CB, nP, sel);
-    if (sel) {
-        launch_gateup_nt<1, 1>(a, W, CB, grid, lds, st);     /* one token: NT == 1 */
-    } else {
-        if (NT == 2) launch_gateup_nt<2, 0>(a, W, CB, grid, lds, st);
-        else launch_gateup_nt<1, 0>(a, W, CB, grid, lds, st);
-    }
+    if (!gateup_streams(L)) return hipErrorInvalidValue;
+    const int cb = L.gate_type == 14 ? 8 : CB;
+    const size_t lds = gateup_lds(W, NT, cb, nP, sel, L.gate_type);
+    if (lds > 160 * 1024) return hipErrorInvalidValue;
+    if (L.gate_type == 14) launch_gateup_type<14>(a, sel, NT, W, cb, grid, lds, st);
+    else if (L.gate_type == 3) launch_gateup_type<3>(a, sel, NT, W, cb, grid, lds, st);
+    else launch_gateup_type<2>(a, sel, NT, W, cb, grid, lds, st);
     return hipGetLastError();
 }
 

@@ -27,6 +27,8 @@ CASES = [
     ("tiny_q41_q6k_t40", 256, 16, 4, 256, 40, orc.T_Q4_1, orc.T_Q6_K, orc.T_Q4_1, "auto", False),
     ("q235b_gq41_t16", 4096, 128, 8, 1536, 16, orc.T_Q4_1, orc.T_Q4_1, orc.T_Q4_0, "auto", False),
     ("q235b_gq6k_t16", 4096, 128, 8, 1536, 16, orc.T_Q6_K, orc.T_Q6_K, orc.T_Q4_0, "auto", False),
+    ("q235b_gq6k_t1", 4096, 128, 8, 1536, 1, orc.T_Q6_K, orc.T_Q6_K, orc.T_Q4_0, "auto", False),
+    ("q235b_gq41_t1", 4096, 128, 8, 1536, 1, orc.T_Q4_1, orc.T_Q4_1, orc.T_Q4_0, "auto", False),
     ("q235b_zipf_t512", 4096, 128, 8, 1536, 512, orc.T_Q4_0, orc.T_Q4_0, orc.T_Q4_0, "auto", True),
 ]
 

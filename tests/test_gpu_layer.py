@@ -90,6 +90,9 @@ GATE_UP_CASES = [
     ("q480b_gq6k_t3", 6144, 160, 8, 2560, 3, 55, orc.T_Q6_K, orc.T_Q6_K, orc.T_Q4_0, False),
     ("k16_gq41_t1", 512, 64, 16, 256, 1, 56, orc.T_Q4_1, orc.T_Q4_1, orc.T_Q4_0, False),
     ("tiny_gq41_t200", 256, 16, 4, 256, 200, 57, orc.T_Q4_1, orc.T_Q4_1, orc.T_Q6_K, False),
+    ("gq6k_t1", 4096, 128, 8, 1536, 1, 58, orc.T_Q6_K, orc.T_Q6_K, orc.T_Q4_0, False),   # streaming Q6_K gate/up
+    ("q30b_gq6k_t1", 2048, 128, 8, 768, 1, 59, orc.T_Q6_K, orc.T_Q6_K, orc.T_Q6_K, True),
+    ("gq41_t2", 4096, 128, 8, 1536, 2, 60, orc.T_Q4_1, orc.T_Q4_1, orc.T_Q4_1, False),   # streaming Q4_1, two tokens
 ]
 
 
