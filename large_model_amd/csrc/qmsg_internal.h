@@ -51,7 +51,7 @@ constexpr int kMxRec = 128;
  * kernels (us): gate/up with the records each needs 227.5 / 229.7 at 20 tokens (1.25 slots per
  * expert), 132.6 / 129.6 at 16; down after row-kernel gate/up, with the activation records it
  * needs and the combine: Q4_0 37.9 / 34.1 at 4 tokens, 44.9 / 44.1 at 6, 53.2 / 53.8 at 8, 64.4 /
- * 69.3 at 12; Q6_K 39.8 / 41.0 at 2, 59.2 / 53.6 at 3, 66.0 / 71.6 at 4, 105 / 118 at 8. */
+ * 69.3 at 12; Q6_K 41.6 / 32.9 at 2, 49.4 / 46.2 at 3, 58.2 / 58.2 at 4, 105 / 118 at 8. */
 constexpr int kMxAutoQuarters = 5;
 /* Q6_K gate/up (its MFMA kernel unpacks 6-bit codes): from 2.5 slots per expert (streaming /
  * MFMA us: 442 / 487 at 32 tokens, 618 / 435 at 48) */

@@ -1853,8 +1853,9 @@ __global__ __launch_bounds__(32 * RD) void down_t1_kernel(DownArgs a)
 /* Slots of the batches the small-batch down kernel takes (two to four tokens). */
 constexpr int kSmallDownNS = 32;
 
-/* Two to four tokens, Q4_0 or Q4_1 down weights (at most kSmallDownNS slots): the layout of
- * down_t1_kernel, one block per RD output rows and RD/2 waves, but wave w streams the active
+/* Two to four tokens, Q4_0, Q4_1 or Q6_K down weights (at most kSmallDownNS slots; Q6_K a
+ * super-block per chunk, as in down_t1_kernel): the layout of down_t1_kernel, one block per RD
+ * output rows and RD/2 waves, but wave w streams the active
  * experts w, w + RD/2, ... one after another, each against its one to four slots, and
  * requests the next expert's first chunks while it consumes the current one's last. The block
  * first quantises every slot's activations into LDS pair records and ends with the weighted
@@ -1863,13 +1864,17 @@ template <int TYPE, int CB, int D, int RD>
 __global__ __launch_bounds__(32 * RD) void down_small_kernel(DownArgs a)
 {
     extern __shared__ __align__(16) uint8_t smem[];
+    constexpr bool Q6 = TYPE == 14;
+    static_assert(!Q6 || CB == 8, "a Q6_K chunk is one super-block");
     constexpr int NW = RD / 2, NTH = 64 * NW, NT = 4;
     constexpr int QPT = 2;                            /* int8 blocks per thread in registers  */
-    constexpr int BB = TYPE == 3 ? 20 : 18;           /* bytes per 32-block                   */
-    constexpr int SPR = CB * BB / 16;                 /* 16-byte slots per row per chunk      */
-    constexpr int NSL = RD * SPR;                     /* slots of one wave's chunk            */
-    constexpr int SPT = (NSL + 63) / 64;              /* slots per lane per chunk             */
-    constexpr int WS = CB * BB + ((SPR & 1) ? 0 : 16);/* LDS row stride, odd in 16-byte units */
+    constexpr int BB = TYPE == 3 ? 20 : 18;           /* bytes per 32-block (Q4 types)        */
+    constexpr int UNIT = Q6 ? 4 : 16;                 /* bytes per load                       */
+    constexpr int SPR = Q6 ? 54 : CB * BB / 16;       /* loads per row per chunk              */
+    constexpr int NSL = RD * SPR;                     /* loads of one wave's chunk            */
+    constexpr int SPT = (NSL + 63) / 64;              /* loads per lane per chunk             */
+    constexpr int WS = Q6 ? 220 : CB * BB + ((SPR & 1) ? 0 : 16);   /* LDS row stride        */
+    typedef typename std::conditional<Q6, uint32_t, u32x4>::type Unit;
     static_assert(RD == 16, "a lane quad per row of the wave's 16");
     const int tid = threadIdx.x, lane = tid & 63, qd = lane >> 2, p = lane & 3;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -1893,12 +1898,15 @@ __global__ __launch_bounds__(32 * RD) void down_small_kernel(DownArgs a)
     }
     const uint8_t *b = a.down + (size_t)max(wk.x, 0) * a.eb + (size_t)r0 * a.rb;
     __builtin_amdgcn_sched_barrier(0);
-    u32x4 wv[D][SPT];
-    auto load_chunk = [&](int c, u32x4 *dst) {
+    Unit wv[D][SPT];
+    auto load_chunk = [&](int c, Unit *dst) {
 #pragma unroll
         for (int m = 0; m < SPT; m++) {
             const int i = min(lane + 64 * m, NSL - 1), row = i / SPR, q = i - row * SPR;
-            dst[m] = *(const u32x4 *)(b + (size_t)row * a.rb + (size_t)c * CB * BB + 16 * q);
+            if constexpr (Q6)     /* the super-block starts 2 bytes past a 4-byte boundary on odd chunks */
+                dst[m] = *(const uint32_t *)(b + (size_t)row * a.rb + (size_t)(c * 210 - 2 * (c & 1)) + 4 * q);
+            else
+                dst[m] = *(const u32x4 *)(b + (size_t)row * a.rb + (size_t)c * CB * BB + 16 * q);
         }
     };
     if (wk.x >= 0) {
@@ -1956,7 +1964,7 @@ __global__ __launch_bounds__(32 * RD) void down_small_kernel(DownArgs a)
 #pragma unroll
                     for (int m = 0; m < SPT; m++) {
                         const int i = min(lane + 64 * m, NSL - 1), row = i / SPR, q = i - row * SPR;
-                        *(u32x4 *)(wbuf + row * WS + 16 * q) = wv[d][m];
+                        *(Unit *)(wbuf + row * WS + UNIT * q) = wv[d][m];
                     }
                     wave_sync();
                     if (c + D < nchunk) {
@@ -1968,8 +1976,28 @@ __global__ __launch_bounds__(32 * RD) void down_small_kernel(DownArgs a)
                         }
                         load_chunk(c + D - nchunk, wv[d]);
                     }
-                    q4_rows_nt<TYPE, NT>((const uint32_t *)(wbuf + qd * WS), p, xq, (size_t)xrec, c * (CB / 2),
-                                         CB / 2, nt, acc);
+                    if constexpr (Q6) {
+                        /* the 8 blocks of super-block c (src/kernels.c:142-170) for every slot */
+                        auto superblock = [&](auto al) {
+#pragma unroll
+                            for (int h = 0; h < 2; h++)
+#pragma unroll
+                                for (int g = 0; g < 4; g++) {
+                                    const int blk = c * 8 + h * 4 + g;
+                                    const Q6W w = q6_k_weights<decltype(al)::value>(wbuf + qd * WS, al ? 0 : 2, h, g, p);
+#pragma unroll
+                                    for (int n = 0; n < NT; n++)
+                                        if (n < nt)
+                                            q6_k_token(w, xq + (size_t)n * xrec + (size_t)(blk >> 1) * kPairBytes, p,
+                                                       blk & 1, acc[n]);
+                                }
+                        };
+                        if (c & 1) superblock(std::integral_constant<bool, false>());
+                        else superblock(std::integral_constant<bool, true>());
+                    } else {
+                        q4_rows_nt<TYPE, NT>((const uint32_t *)(wbuf + qd * WS), p, xq, (size_t)xrec, c * (CB / 2),
+                                             CB / 2, nt, acc);
+                    }
                 }
             }
         }
@@ -2092,10 +2120,11 @@ hipError_t launch_down_exact(const Shape &s, const LayerDev &L, const Scratch &S
     }
     /* two to four tokens: the same layout, each wave streaming several experts */
     const size_t lds_s = (size_t)(RD / 2) * 16 * ws + (size_t)T * s.K * (xrec + RD * 4);
-    if (T >= 2 && T <= 4 && T * s.K <= kSmallDownNS && quant && (L.down_type == 2 || L.down_type == 3) &&
-        s.F % 256 == 0 && s.E % RD == 0 && lds_s <= 160 * 1024) {
+    if (T >= 2 && T <= 4 && T * s.K <= kSmallDownNS && quant && t1_type && s.F % 256 == 0 && s.E % RD == 0 &&
+        lds_s <= 160 * 1024) {
         const dim3 grid(s.E / RD), block(32 * RD);
-        if (L.down_type == 3) QLAUNCH("down", (down_small_kernel<3, CB, 3, RD>), grid, block, lds_s, st, a);
+        if (L.down_type == 14) QLAUNCH("down", (down_small_kernel<14, CB, 3, RD>), grid, block, lds_s, st, a);
+        else if (L.down_type == 3) QLAUNCH("down", (down_small_kernel<3, CB, 3, RD>), grid, block, lds_s, st, a);
         else QLAUNCH("down", (down_small_kernel<2, CB, 3, RD>), grid, block, lds_s, st, a);
         return hipGetLastError();
     }

@@ -24,6 +24,7 @@ CASES = [
     ("q235b_q6k_t64_mfma", 4096, 128, 8, 1536, 64, orc.T_Q4_0, orc.T_Q4_0, orc.T_Q6_K, "mfma", False),
     ("q235b_q41_t1", 4096, 128, 8, 1536, 1, orc.T_Q4_0, orc.T_Q4_0, orc.T_Q4_1, "auto", False),
     ("q235b_q6k_t1", 4096, 128, 8, 1536, 1, orc.T_Q4_0, orc.T_Q4_0, orc.T_Q6_K, "auto", False),
+    ("q235b_q6k_t3", 4096, 128, 8, 1536, 3, orc.T_Q4_0, orc.T_Q4_0, orc.T_Q6_K, "auto", False),
     ("tiny_q41_q6k_t40", 256, 16, 4, 256, 40, orc.T_Q4_1, orc.T_Q6_K, orc.T_Q4_1, "auto", False),
     ("q235b_gq41_t16", 4096, 128, 8, 1536, 16, orc.T_Q4_1, orc.T_Q4_1, orc.T_Q4_0, "auto", False),
     ("q235b_gq6k_t16", 4096, 128, 8, 1536, 16, orc.T_Q6_K, orc.T_Q6_K, orc.T_Q4_0, "auto", False),

@@ -21,6 +21,7 @@ CASES = [
     ("q235b_t16", 4096, 128, 8, 1536, 16, 2, orc.T_Q4_0, False),
     ("q30b_q6k_t5", 2048, 128, 8, 768, 5, 3, orc.T_Q6_K, False),
     ("q235b_q6k_t3", 4096, 128, 8, 1536, 3, 4, orc.T_Q6_K, False),
+    ("q235b_q6k_t2", 4096, 128, 8, 1536, 2, 31, orc.T_Q6_K, True),   # small-batch down kernel, Q6_K rows
     ("tiny_q41_t3", 256, 16, 4, 128, 3, 9, orc.T_Q4_1, False),
     ("q30b_q41_t1", 2048, 128, 8, 768, 1, 8, orc.T_Q4_1, True),
     ("q235b_q41_t1", 4096, 128, 8, 1536, 1, 7, orc.T_Q4_1, False),
