@@ -4,6 +4,7 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <atomic>
 #include <mutex>
 #include <string>
 #include <thread>
@@ -77,6 +78,7 @@ std::vector<ScratchItem> scratch_items(const qmsg_cfg &cfg, size_t T, Scratch *S
         { (void **)&S->aq, NS * nbF * sizeof(Q8) }, { (void **)&S->aqk, NS * (nbF / 2) * kPairBytes },
         { (void **)&S->dn, NS * E * 4 },
         { (void **)&S->mxx, T * nbE * kMxRec },  { (void **)&S->mxa, NS * nbF * kMxRec },
+        { (void **)&S->mxflag, 16 },
     };
 }
 
@@ -774,8 +776,13 @@ int qmsg_matmul_n(qmsg_ctx *c, const int *ids, int nW, const float *x, int T, fl
 
 /* One layer on device buffers with the scratch arrays S (the context's, or carved from the
  * library's static array by qmsg_moe_device_noalloc). */
-static int run_layer_s(qmsg_ctx *c, const Scratch &S, int layer, const float *d_xn, int T, float *d_out, int debug)
+static int run_layer_s(qmsg_ctx *c, const Scratch &S0, int layer, const float *d_xn, int T, float *d_out, int debug)
 {
+    /* every layer call gets an epoch of its own: record producers store it in S.mxflag when a
+     * record falls outside the MFMA kernels' scaled range, and the consumers compare */
+    static std::atomic<uint64_t> epochs{ 0 };
+    Scratch S = S0;
+    S.epoch = ++epochs;
     int rc = check_layer_index(c, layer);
     if (rc) return rc;
     const LayerStore &L = c->layers[(size_t)layer];

@@ -104,6 +104,9 @@ struct Scratch {
     float *dn;          /* [Tm*K][E]           */
     uint8_t *mxx;       /* [Tm][E/32][kMxRec] MFMA records of the layer input */
     uint8_t *mxa;       /* [Tm*K][F/32][kMxRec] MFMA records of the activations */
+    uint64_t *mxflag;   /* [2] the epoch of the last call whose input (0) / activation (1) records
+                         * hold a d_x outside the MFMA kernels' scaled range */
+    uint64_t epoch;     /* this call's epoch (unique per layer call in the process) */
 };
 
 struct Shape {

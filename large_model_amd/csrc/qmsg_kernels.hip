@@ -134,18 +134,22 @@ __device__ Q8Vals quantize_block(const float *v)
     int qs[32];
 #pragma unroll
     for (int j = 0; j < 32; j++) {
-        qs[j] = (int)rintf(v[j] * id);
+        /* the reference's (int)nearbyintf compiles to x86's conversion, which gives INT_MIN
+         * for a NaN or a value outside int's range (id = +inf when d is below 2^-128, or an
+         * infinite input); v_cvt_i32_f32 would clamp, so that case is chosen here */
+        const float r = rintf(v[j] * id);
+        qs[j] = fabsf(r) < 0x1p31f ? (int)r : (int)0x80000000u;
         q[j] = (int8_t)qs[j];
     }
 #pragma unroll
     for (int w = 8; w > 0; w >>= 1)
 #pragma unroll
         for (int j = 0; j < w; j++) {
-            qs[j] += qs[j + w];
-            qs[16 + j] += qs[16 + j + w];
+            qs[j] = (int)((uint32_t)qs[j] + (uint32_t)qs[j + w]);      /* wrapping, as the reference's */
+            qs[16 + j] = (int)((uint32_t)qs[16 + j] + (uint32_t)qs[16 + j + w]);
         }
     const int s0 = qs[0], s1 = qs[16];
-    r.ds = r.d * (float)(s0 + s1);
+    r.ds = r.d * (float)(int)((uint32_t)s0 + (uint32_t)s1);
     r.s16 = (uint32_t)(uint16_t)(int16_t)s0 | ((uint32_t)(uint16_t)(int16_t)s1 << 16);
     for (int w = 0; w < 8; w++) r.qw[w] = pack4(q + 4 * w);
     return r;
@@ -2030,7 +2034,7 @@ __global__ __launch_bounds__(32 * RD) void down_small_kernel(DownArgs a)
 
 /* The int8 blocks of every slot's activations (src/model.c:996-997) for batches whose
  * records do not fit the down kernel's LDS: one thread per 32-block. */
-__device__ void mx_store_record(const Q8Vals &q, uint8_t *rec);
+__device__ bool mx_store_record(const Q8Vals &q, uint8_t *rec);
 
 /* The int8 activation blocks of every slot (src/model.c:996-997) from act: QmsQ8 blocks, pair
  * records, and, when mxrec is set, the MFMA kernels' records too. */
@@ -2050,7 +2054,7 @@ __global__ void act_quant_kernel(Scratch S, int F, int NS, uint8_t *mxrec)
     const Q8Vals q = quantize_block(v);
     store_q8(q, S.aq + b);
     store_pair_half(q, (uint32_t *)(S.aqk + ((size_t)s * (nbF >> 1) + (blk >> 1)) * kPairBytes), blk & 1);
-    if (mxrec) mx_store_record(q, mxrec + (size_t)b * kMxRec);
+    if (mxrec && !mx_store_record(q, mxrec + (size_t)b * kMxRec)) S.mxflag[1] = S.epoch;
 }
 
 /* Weighted sum per token in selection order (src/model.c:1152-1162) when dn did not fit. */
@@ -2221,15 +2225,21 @@ hipError_t launch_gateup_tiles(const Shape &s, const LayerDev &L, const Scratch 
  * eight int32 lane sums S_k = sum_{i in 4k..4k+3} u_i x_i (u the unsigned weight code, lanes
  * 0-3 over the low nibbles) and folds each into its own fp32 chain
  * acc_k = fma((float)S_k, fl(d_w d_x), acc_k) (src/kernels.c:85-94, 113-119, 145-166). One
- * v_mfma_f32_16x16x32_f16 returns those eight S_k for 16 weight rows and 2 slots:
- *   - B holds the codes of 16 rows, biased by 1024 (0x6400 | u is the f16 1024 + u, exact);
+ * v_mfma_f32_16x16x32_f16 returns those eight S_k, scaled by 2^-24, for 16 weight rows and 2
+ * slots:
+ *   - B holds the codes of 16 rows as f16 subnormals: the bits of code u are the f16 u 2^-24,
+ *     so a mask unpacks them (the matrix cores keep subnormal inputs; checked on the device);
  *   - A is block-diagonal over the lane groups: its row (slot j, lane k) holds x_j only at the
- *     four K positions of group k, so D-row (j, k) of column r sums group k only;
- *   - the C input is -1024 * sum_{group k} x_j, which cancels the bias.
- * Every partial sum is an integer below 2^24, so the f32 accumulation inside the MFMA is exact
- * in any order and D equals S_k. The VALU then runs the reference's chains: acc_k =
- * fma(S_k, fl(d_w d_x), acc_k) per block, the offset chain, and at the end the hsum256 tree and
- * the unfused final term. Q6_K scales S_k by its int8 sub-scale first (exact in f32).
+ *     four K positions of group k, so D-row (j, k) of column r sums group k only.
+ * Every product and partial sum is an integer multiple of 2^-24 below 1, so the f32
+ * accumulation inside the MFMA is exact in any order and D equals S_k 2^-24. The VALU then runs
+ * the reference's chains, acc_k = fma(S_k, fl(d_w d_x), acc_k) per block, as
+ * fma(D, fl(d_w d_x 2^24), acc_k): the record carries d_x 2^24, and for d_x in [2^-102, 2^88]
+ * (or 0) fl(d_w d_x 2^24) = fl(d_w d_x) 2^24 for every f16 d_w (no subnormal or overflowing
+ * product), so the FMA sees the reference's exact product. A chunk with a d_x outside that
+ * range (the record's scaled word is then a NaN) runs fma(D 2^24, fl(d_w d_x), acc_k) instead.
+ * Then the offset chain, and at the end the hsum256 tree and the unfused final term. Q6_K
+ * multiplies D by its int8 sub-scale times 2^24 first (exact), which needs no range.
  *
  * Operand layout of the 16x16x32 f16 MFMA (checked on the device): lane l supplies
  * A[l%16][8(l/16) + e] and B[8(l/16) + e][l%16] for e = 0..7 and receives D[4(l/16) + v][l%16].
@@ -2241,12 +2251,11 @@ hipError_t launch_gateup_tiles(const Shape &s, const LayerDev &L, const Scratch 
  * serves its four FMAs.
  *
  * Activation records (kMxRec bytes per slot, or per token, and 32-block) carry x in that
- * order as f16 (64 bytes), then d, ds and the half sums (16 bytes), then 16 zero bytes, which
- * the lanes of A outside their group read, then -1024 x (the sum of lane k's four codes) for
- * k = 0..7 (32 bytes): the Q4 kernels feed the B operand as f16 1024 + code and start the MFMA
- * from those sums, so the result is the lane sums themselves. Q6_K kernels stage the first 96
- * bytes of each record and subtract 1024 from B instead. Gate/up writes the records of the activations it quantises, so the
- * down products read them directly.
+ * order as f16 (64 bytes), then d 2^24 (or the NaN that sends the chunk to the unscaled
+ * chains), ds, the half sums and d (16 bytes), then 16 zero bytes, which the lanes of A
+ * outside their group read; the kernels stage those first 96 bytes of each record. Gate/up
+ * writes the records of the activations it quantises, so the down products read them
+ * directly.
  *
  * A block of 8 waves computes 512/WSG weight rows x 8*WSG slots of one expert's slot tile:
  * wave (wr, ws) owns 64 rows (four 16-row MFMA tiles) and 8 slots (four pairs). For gate/up the
@@ -2258,17 +2267,24 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef short short2_t __attribute__((ext_vector_type(2)));
 
 constexpr int kMxC = 8;          /* 32-blocks per staged chunk (one Q6_K super-block) */
-constexpr int kMxDx = 64;        /* offset of the record's d, ds, half sums */
+constexpr int kMxDx = 64;        /* offset of the record's d 2^24, ds, half sums, d */
 constexpr int kMxZero = 80;      /* offset of the record's zero words */
-constexpr int kMxAcc = 96;       /* offset of the record's MFMA accumulator inputs */
-static_assert(kMxRec == 128, "record layout: 64 bytes of codes, 16 of scales, 16 of zeros, 32 of sums");
-/* bytes of one record in LDS: whole for the Q4 kernels, without the sums for Q6_K */
-__host__ __device__ constexpr int mx_recl(int type) { return type == 14 ? 96 : kMxRec; }
+static_assert(kMxRec == 128, "record layout: 64 bytes of codes, 16 of scales, 16 of zeros (32 unused)");
+/* bytes of one record in LDS */
+__host__ __device__ constexpr int mx_recl(int) { return 96; }
 
-/* One int8 block as an activation record (layout above). */
-__device__ void mx_store_record(const Q8Vals &q, uint8_t *rec)
+/* d 2^24 where fl(d_w d 2^24) = fl(d_w d) 2^24 for every f16 d_w, else a NaN. */
+__device__ __forceinline__ float mx_scaled_d(float d)
 {
-    u32x4 w[8];
+    const bool ok = d == 0.0f || (d >= 0x1p-102f && d <= 0x1p88f);
+    return ok ? d * 0x1p24f : __builtin_nanf("");
+}
+
+/* One int8 block as an activation record (layout above); false when its d_x 2^24 word is the
+ * NaN (d_x outside the scaled range). */
+__device__ bool mx_store_record(const Q8Vals &q, uint8_t *rec)
+{
+    u32x4 w[6];
 #pragma unroll
     for (int k = 0; k < 8; k++) {
         const uint32_t c = q.qw[k];
@@ -2277,16 +2293,17 @@ __device__ void mx_store_record(const Q8Vals &q, uint8_t *rec)
         auto h = [](int x) { return (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)(float)x); };
         w[k >> 1][2 * (k & 1)] = h(x0) | (h(x2) << 16);
         w[k >> 1][2 * (k & 1) + 1] = h(x1) | (h(x3) << 16);
-        w[6 + (k >> 2)][k & 3] = __float_as_uint(-1024.0f * (float)(x0 + x1 + x2 + x3));
     }
-    w[4] = u32x4{ __float_as_uint(q.d), __float_as_uint(q.ds), q.s16, 0u };
+    const float dsc = mx_scaled_d(q.d);
+    w[4] = u32x4{ __float_as_uint(dsc), __float_as_uint(q.ds), q.s16, __float_as_uint(q.d) };
     w[5] = u32x4{ 0u, 0u, 0u, 0u };
 #pragma unroll
-    for (int i = 0; i < 8; i++) ((u32x4 *)rec)[i] = w[i];
+    for (int i = 0; i < 6; i++) ((u32x4 *)rec)[i] = w[i];
+    return dsc == dsc;
 }
 
 /* The layer input's records from its int8 blocks (one thread per block). */
-__global__ void mx_input_kernel(const Q8 *xq, int n, uint8_t *rec)
+__global__ void mx_input_kernel(const Q8 *xq, int n, uint8_t *rec, uint64_t *flag, uint64_t epoch)
 {
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= n) return;
@@ -2297,7 +2314,7 @@ __global__ void mx_input_kernel(const Q8 *xq, int n, uint8_t *rec)
     q.s16 = s[2];
 #pragma unroll
     for (int w = 0; w < 8; w++) q.qw[w] = s[3 + w];
-    mx_store_record(q, rec + (size_t)i * kMxRec);
+    if (!mx_store_record(q, rec + (size_t)i * kMxRec)) *flag = epoch;
 }
 
 struct MxArgs {
@@ -2322,7 +2339,7 @@ __host__ __device__ constexpr int mx_wstride(int type) { return type == 14 ? 216
  * piece is copied by the LDS DMA (global_load_lds): a wave instruction moves 64 lanes x 16 bytes
  * (Q6_K weights: x 4 bytes) to consecutive LDS bytes. Two buffers: the next chunk's copy is in
  * flight while the current one computes. */
-__host__ __device__ constexpr int mx_rstride(int type) { return kMxC * mx_recl(type) + 64; }
+__host__ __device__ constexpr int mx_rstride(int type) { return kMxC * mx_recl(type) + (type == 14 ? 64 : 320); }
 
 template <int TYPE, int WSG, int PPW = 4, int NW = 8>
 struct MxLayout {
@@ -2347,23 +2364,12 @@ __device__ __forceinline__ uint32_t and_or(uint32_t x, uint32_t m, uint32_t c)
     return r;
 }
 
-/* Four words of biased codes (f16 1024 + u, from 0x6400 | u) to the f16 codes u: one packed f16
- * subtraction per word, exact (both terms and the difference are small integers). */
-typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
-__device__ __forceinline__ f16x8 mx_pack_codes(uint32_t b0, uint32_t b1, uint32_t b2, uint32_t b3)
-{
-    const f16x2 k = { (_Float16)1024.0f, (_Float16)1024.0f };
-    const f16x2 c0 = __builtin_bit_cast(f16x2, b0) - k, c1 = __builtin_bit_cast(f16x2, b1) - k;
-    const f16x2 c2 = __builtin_bit_cast(f16x2, b2) - k, c3 = __builtin_bit_cast(f16x2, b3) - k;
-    return f16x8{ c0.x, c0.y, c1.x, c1.y, c2.x, c2.y, c3.x, c3.y };
-}
-
 /* The B operand of one 16-row tile for 32-block b of the staged chunk (row = this lane's row in
  * LDS) and the scale words the chains need. */
 struct MxB {
     f16x8 op;
     uint32_t dw;      /* Q4_0: d (low half); Q4_1: d | m << 16; Q6_K: d (low half) */
-    float sc;         /* Q6_K: the lane's sub-scale (k < 4: sc[2g], k >= 4: sc[2g+1]) */
+    float sc;         /* Q6_K: the lane's sub-scale times 2^24 (k < 4: sc[2g], k >= 4: sc[2g+1]) */
     uint32_t sab;     /* Q6_K: both sub-scales as int16 pair (sc[2g] low) */
 };
 
@@ -2375,11 +2381,11 @@ typedef __attribute__((address_space(3))) const u32x4 LdsU32x4;
  * word, from two LDS pointers: pq at the lane's code word of the block in tile row lr (Q4_0
  * even blocks: 2 bytes past a word boundary), pd at the block's scale word; tile t is an
  * immediate offset. */
-template <int TYPE, int PAR, int USEC>
+template <int TYPE, int PAR, bool SC>
 __device__ __forceinline__ MxB mx_weights_q4(LdsPtr pq, LdsPtr pd, int t)
 {
     constexpr int WS = mx_wstride(TYPE);
-    const uint32_t m4 = 0x000f000fu, bias = 0x64006400u;
+    const uint32_t m4 = 0x000f000fu;
     MxB w;
     uint32_t v;
     if constexpr (TYPE == 3 || PAR) {
@@ -2389,12 +2395,20 @@ __device__ __forceinline__ MxB mx_weights_q4(LdsPtr pq, LdsPtr pd, int t)
         const uint32_t a1 = *(const __attribute__((address_space(3))) uint32_t *)(pq + 16 * t * WS + 2);
         v = __builtin_amdgcn_alignbyte(a1, a0, 2);
     }
-    /* f16 1024 + code; USEC: the MFMA starts from -1024 x the lane's code sum (the record's
-     * sums), else the 1024 is subtracted here */
-    const uint32_t b0 = and_or(v, m4, bias), b1 = and_or(v >> 8, m4, bias), b2 = and_or(v >> 4, m4, bias),
-                   b3 = and_or(v >> 12, m4, bias);
-    if constexpr (USEC) w.op = __builtin_bit_cast(f16x8, u32x4{ b0, b1, b2, b3 });
-    else w.op = mx_pack_codes(b0, b1, b2, b3);
+    if constexpr (SC) {
+        /* the f16 subnormals code 2^-24 */
+        w.op = __builtin_bit_cast(f16x8, u32x4{ v & m4, (v >> 8) & m4, (v >> 4) & m4, (v >> 12) & m4 });
+    } else {
+        /* the codes themselves: f16 1024 + code (0x6400 | code) minus 1024, exact */
+        const uint32_t bias = 0x64006400u;
+        typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+        const f16x2 k = { (_Float16)1024.0f, (_Float16)1024.0f };
+        const f16x2 c0 = __builtin_bit_cast(f16x2, and_or(v, m4, bias)) - k;
+        const f16x2 c1 = __builtin_bit_cast(f16x2, and_or(v >> 8, m4, bias)) - k;
+        const f16x2 c2 = __builtin_bit_cast(f16x2, and_or(v >> 4, m4, bias)) - k;
+        const f16x2 c3 = __builtin_bit_cast(f16x2, and_or(v >> 12, m4, bias)) - k;
+        w.op = f16x8{ c0.x, c0.y, c1.x, c1.y, c2.x, c2.y, c3.x, c3.y };
+    }
     if constexpr (TYPE == 3) w.dw = *(const __attribute__((address_space(3))) uint32_t *)(pd + 16 * t * WS);
     else w.dw = *(const __attribute__((address_space(3))) uint16_t *)(pd + 16 * t * WS);
     w.sc = 0.0f;
@@ -2434,27 +2448,27 @@ __device__ __forceinline__ float mix_fma_hi(uint32_t h, float f, float c)
  * Q4_0 / Q4_1 the code word and the scale word of tile row lr (the tile t adds 16t rows). One
  * trip covers two blocks; the second block and the pairs and tiles are immediate offsets. */
 struct MxStreams {
-    LdsPtr alo, ahi, d, q, dw, acc;
+    LdsPtr alo, ahi, d, q, dw;
 };
 
 /* The empty asm keeps each stream a single register: otherwise every (pair, stream) address
  * becomes a loop variable of its own and the registers run out. */
 __device__ __forceinline__ void mx_opaque(MxStreams &st)
 {
-    asm("" : "+v"(st.alo), "+v"(st.ahi), "+v"(st.d), "+v"(st.q), "+v"(st.dw), "+v"(st.acc));
+    asm("" : "+v"(st.alo), "+v"(st.ahi), "+v"(st.d), "+v"(st.q), "+v"(st.dw));
 }
 
 /* One block b (parity PAR within the trip) of the staged chunk: NP slot pairs of this wave
- * against its two 16-row tiles. */
-template <int TYPE, int NP, int O, int PAR, int USEC>
-__device__ __forceinline__ void mx_block(int b, const MxStreams &st, const uint8_t *W, int lr, int lg, int kh,
-                                         f32x4 (&acc)[2][4], float (&cr)[2][4])
+ * against its two 16-row tiles. SC: the chunk's records all carry d_x 2^24 and B holds the
+ * codes 2^-24; else B holds the codes themselves and the chains take d_x unscaled. */
+template <int TYPE, int NP, int PAR, bool SC>
+__device__ __forceinline__ void mx_block(const MxStreams &st, f32x4 (&acc)[2][4], float (&cr)[2][4])
 {
     static_assert(TYPE == 2 || TYPE == 3, "Q6_K chunks take mx_chunk_q6");
     constexpr int BB = TYPE == 3 ? 20 : 18, RB = PAR * mx_recl(TYPE), RS = mx_rstride(TYPE);
     MxB w[2];
 #pragma unroll
-    for (int t = 0; t < 2; t++) w[t] = mx_weights_q4<TYPE, PAR, USEC>(st.q + PAR * BB, st.dw + PAR * BB, t);
+    for (int t = 0; t < 2; t++) w[t] = mx_weights_q4<TYPE, PAR, SC>(st.q + PAR * BB, st.dw + PAR * BB, t);
     /* pair p's two MFMAs are issued before pair p-1's results are used, so the chains of one
      * pair run while the matrix core works on the next */
     f32x4 S[2][2];
@@ -2462,14 +2476,19 @@ __device__ __forceinline__ void mx_block(int b, const MxStreams &st, const uint8
     auto issue = [&](int p, int k) {
         const u32x2 lo = *(const LdsU32x2 *)(st.alo + RB + 2 * p * RS);
         const u32x2 hi = *(const LdsU32x2 *)(st.ahi + RB + 2 * p * RS);
-        const u32x2 d2 = *(const LdsU32x2 *)(st.d + RB + 2 * p * RS);          /* d, ds */
-        f32x4 c0 = f32x4{ 0.0f, 0.0f, 0.0f, 0.0f };
-        if constexpr (USEC) c0 = *(const __attribute__((address_space(3))) f32x4 *)(st.acc + RB + 2 * p * RS);
+        if constexpr (SC) {
+            const u32x2 d2 = *(const LdsU32x2 *)(st.d + RB + 2 * p * RS);      /* d 2^24, ds */
+            xd[k] = __uint_as_float(d2.x);
+            xds[k] = __uint_as_float(d2.y);
+        } else {
+            typedef __attribute__((address_space(3))) const float LdsF32;
+            xd[k] = *(LdsF32 *)(st.d + RB + 2 * p * RS + 12);                     /* d */
+            xds[k] = *(LdsF32 *)(st.d + RB + 2 * p * RS + 4);                     /* ds */
+        }
         const f16x8 aop = __builtin_bit_cast(f16x8, u32x4{ lo.x, lo.y, hi.x, hi.y });
-        xd[k] = __uint_as_float(d2.x);
-        xds[k] = __uint_as_float(d2.y);
 #pragma unroll
-        for (int t = 0; t < 2; t++) S[k][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(aop, w[t].op, c0, 0, 0, 0);
+        for (int t = 0; t < 2; t++)
+            S[k][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(aop, w[t].op, f32x4{ 0.0f, 0.0f, 0.0f, 0.0f }, 0, 0, 0);
     };
     issue(0, 0);
 #pragma unroll
@@ -2480,7 +2499,8 @@ __device__ __forceinline__ void mx_block(int b, const MxStreams &st, const uint8
         for (int t = 0; t < 2; t++) {
             const float dd = mix_mul(w[t].dw, xd[k]);
 #pragma unroll
-            for (int v = 0; v < 4; v++) acc[t][p][v] = __builtin_fmaf(S[k][t][v], dd, acc[t][p][v]);
+            for (int v = 0; v < 4; v++)
+                acc[t][p][v] = __builtin_fmaf(S[k][t][v], dd, acc[t][p][v]);
             if constexpr (TYPE == 3) cr[t][p] = mix_fma_hi(w[t].dw, xds[k], cr[t][p]);   /* off += m*ds */
             else cr[t][p] = mix_fma_lo(w[t].dw, xds[k], cr[t][p]);                     /* corr += d*ds */
         }
@@ -2489,9 +2509,9 @@ __device__ __forceinline__ void mx_block(int b, const MxStreams &st, const uint8
 
 /* One staged chunk (kMxC blocks), two blocks per loop trip. A lane's A words are its x words
  * where it holds x, else the record's zero words. */
-template <int TYPE, int NP, int O, int USEC>
-__device__ __forceinline__ void mx_chunk(const uint8_t *W, const uint8_t *R, int lr, int lg, int kh, int jd,
-                                         int offa_lo, int offa_hi, f32x4 (&acc)[2][4], float (&cr)[2][4])
+template <int TYPE, int NP, bool SC>
+__device__ __forceinline__ void mx_chunk(const uint8_t *W, const uint8_t *R, int lr, int lg, int jd, int offa_lo,
+                                         int offa_hi, f32x4 (&acc)[2][4], float (&cr)[2][4])
 {
     constexpr int WS = mx_wstride(TYPE), BB = TYPE == 3 ? 20 : 18, QO = TYPE == 3 ? 4 : 2;
     MxStreams st;
@@ -2500,17 +2520,15 @@ __device__ __forceinline__ void mx_chunk(const uint8_t *W, const uint8_t *R, int
     st.d = (LdsPtr)(R + jd * mx_rstride(TYPE) + kMxDx);
     st.q = (LdsPtr)(W + lr * WS + QO + 4 * lg);
     st.dw = (LdsPtr)(W + lr * WS);
-    st.acc = (LdsPtr)(R + jd * mx_rstride(TYPE) + kMxAcc + 16 * kh);   /* -1024 x sums of lanes 4kh.. */
 #pragma unroll 1
     for (int b = 0; b < kMxC; b += 2) {
         mx_opaque(st);
-        mx_block<TYPE, NP, O, 0, USEC>(b, st, W, lr, lg, kh, acc, cr);
+        mx_block<TYPE, NP, 0, SC>(st, acc, cr);
         __builtin_amdgcn_sched_barrier(0);      /* one block's operands in registers at a time */
-        mx_block<TYPE, NP, O, 1, USEC>(b + 1, st, W, lr, lg, kh, acc, cr);
+        mx_block<TYPE, NP, 1, SC>(st, acc, cr);
         st.alo += 2 * mx_recl(TYPE);
         st.ahi += 2 * mx_recl(TYPE);
         st.d += 2 * mx_recl(TYPE);
-        st.acc += 2 * mx_recl(TYPE);
         st.q += 2 * BB;
         st.dw += 2 * BB;
     }
@@ -2535,7 +2553,7 @@ __device__ __forceinline__ MxB mx_weights_q6(LdsPtr q, LdsPtr rb, int t, int kh)
 {
     constexpr int WS = mx_wstride(14), h = B >> 2, g = B & 3, ns = 4 * (g >> 1), hs = 2 * g;
     constexpr int oql = O + 64 * h + 32 * (g & 1), oqh = O + 128 + 32 * h;
-    const uint32_t m8 = 0x00ff00ffu, bias = 0x64006400u, lo4 = 0x0f0f0f0fu;
+    const uint32_t m8 = 0x00ff00ffu, lo4 = 0x0f0f0f0fu;
     auto code = [&](int dq) {
         const uint32_t ql = q6_word<O>(q, TS * t * WS + oql + dq), qh = q6_word<O>(q, TS * t * WS + oqh + dq);
         uint32_t hi;
@@ -2546,12 +2564,12 @@ __device__ __forceinline__ MxB mx_weights_q6(LdsPtr q, LdsPtr rb, int t, int kh)
     };
     const uint32_t cA = code(0), cB = code(16);
     MxB w;
-    w.op = mx_pack_codes(and_or(cA, m8, bias), and_or(cA >> 8, m8, bias), and_or(cB, m8, bias),
-                         and_or(cB >> 8, m8, bias));
+    /* the f16 subnormals code 2^-24 */
+    w.op = __builtin_bit_cast(f16x8, u32x4{ cA & m8, (cA >> 8) & m8, cB & m8, (cB >> 8) & m8 });
     const uint32_t scw = *(const __attribute__((address_space(3))) uint16_t *)(rb + TS * t * WS + O + 192 + 8 * h + 2 * g);
     const int sa = (int)(int8_t)(scw & 0xffu), sbv = (int)(int8_t)(scw >> 8);
     w.sab = ((uint32_t)sa & 0xffffu) | ((uint32_t)sbv << 16);
-    w.sc = (float)(kh ? sbv : sa);
+    w.sc = (float)((kh ? sbv : sa) * 16777216);         /* exact: at most 8 significant bits */
     w.dw = *(const __attribute__((address_space(3))) uint16_t *)(rb + TS * t * WS + O + 208);
     return w;
 }
@@ -2571,8 +2589,8 @@ __device__ __forceinline__ void mx_block_q6(const MxStreams &st, int kh, f32x4 (
         const u32x2 lo = *(const volatile LdsU32x2 *)(st.alo + RB + 2 * p * RS);
         const u32x2 hi = *(const volatile LdsU32x2 *)(st.ahi + RB + 2 * p * RS);
         const f16x8 aop = __builtin_bit_cast(f16x8, u32x4{ lo.x, lo.y, hi.x, hi.y });
-        const u32x4 dx = *(const LdsU32x4 *)(st.d + RB + 2 * p * RS);          /* d, ds, s16 pair, 0 */
-        const float xd = __uint_as_float(dx.x);
+        const u32x4 dx = *(const LdsU32x4 *)(st.d + RB + 2 * p * RS);          /* -, ds, s16 pair, d */
+        const float xd = __uint_as_float(dx.w);
         const uint32_t s16p = dx.z;           /* (bit_cast of a vector element itself reads .x) */
 #pragma unroll
         for (int t = 0; t < 2; t++) {
@@ -2602,7 +2620,6 @@ __device__ __forceinline__ void mx_chunk_q6(const uint8_t *W, const uint8_t *R, 
     st.d = (LdsPtr)(R + jd * mx_rstride(14) + kMxDx);
     st.q = (LdsPtr)(W + lr * WS + 4 * lg);
     st.dw = (LdsPtr)(W + lr * WS);
-    st.acc = st.d;                          /* (Q6_K starts its MFMAs from zero) */
     mx_opaque(st);
     mx_block_q6<NP, O, 0, TS>(st, kh, acc, cr);
     __builtin_amdgcn_sched_barrier(0);
@@ -2757,10 +2774,9 @@ void mx_kernel(MxArgs a)
                 }
             }
         }
-        /* a slot's kMxC records: 48 lanes x 16 bytes */
+        /* a slot's kMxC records, the first 96 bytes of each: 48 lanes x 16 bytes */
         if (lane < kMxC * mx_recl(TYPE) / 16) {
-            /* Q4: whole records, 64 lanes; Q6_K: the first 96 bytes of each, 48 lanes */
-            const uint32_t src = TYPE == 14 ? (uint32_t)((lane / 6) * kMxRec + 16 * (lane % 6)) : (uint32_t)(16 * lane);
+            const uint32_t src = (uint32_t)((lane / 6) * kMxRec + 16 * (lane % 6));
 #pragma unroll
             for (int j = 0; j < RPW; j++)
                 dma_to_lds<16>(rsrc[j] + (size_t)c * kMxC * kMxRec + src,
@@ -2781,8 +2797,9 @@ void mx_kernel(MxArgs a)
      * issues its share of the DMA and meets every barrier, whatever its NP (0 included). */
     constexpr float scale = finish_scale(TYPE);
     float *res = (float *)smem;                                   /* [RWG][SWG + 1], after the loop */
-    auto run = [&](auto npc) {
+    auto run = [&](auto npc, auto scc) {
         constexpr int NP = decltype(npc)::value;
+        constexpr bool SC = decltype(scc)::value;
         f32x4 acc[2][4];
         float cr[2][4];
 #pragma unroll
@@ -2812,9 +2829,7 @@ void mx_kernel(MxArgs a)
                     if (c & 1) mx_chunk_q6<NP, 2, TS6>(Wl, Rl, lr, lg, kh, jd, offa_lo, offa_hi, acc, cr);
                     else mx_chunk_q6<NP, 0, TS6>(Wl, Rl, lr, lg, kh, jd, offa_lo, offa_hi, acc, cr);
                 } else {
-                    /* gate/up starts its MFMAs from the records' sums; down, whose registers
-                     * are tighter, subtracts the bias from B (measured both ways) */
-                    mx_chunk<TYPE, NP, 0, GU>(Wl, Rl, lr, lg, kh, jd, offa_lo, offa_hi, acc, cr);
+                    mx_chunk<TYPE, NP, SC>(Wl, Rl, lr, lg, jd, offa_lo, offa_hi, acc, cr);
                 }
             }
             /* chunk c+1 has landed; buffer c is free for chunk c+2 (one buffer: it is free) */
@@ -2838,11 +2853,19 @@ void mx_kernel(MxArgs a)
                 }
             }
     };
-    if (PPW == 4 && np == 4) run(std::integral_constant<int, PPW == 4 ? 4 : 0>{});
-    else if (PPW == 4 && np == 3) run(std::integral_constant<int, PPW == 4 ? 3 : 0>{});
-    else if (np == 2) run(std::integral_constant<int, 2>{});
-    else if (np == 1) run(std::integral_constant<int, 1>{});
-    else run(std::integral_constant<int, 0>{});
+    auto by_pairs = [&](auto scc) {
+        if (PPW == 4 && np == 4) run(std::integral_constant<int, PPW == 4 ? 4 : 0>{}, scc);
+        else if (PPW == 4 && np == 3) run(std::integral_constant<int, PPW == 4 ? 3 : 0>{}, scc);
+        else if (np == 2) run(std::integral_constant<int, 2>{}, scc);
+        else if (np == 1) run(std::integral_constant<int, 1>{}, scc);
+        else run(std::integral_constant<int, 0>{}, scc);
+    };
+    /* Q4 types: whether every record this launch reads carries d_x 2^24 (their producers
+     * stored this call's epoch in the flag otherwise); both loops are whole, so neither's
+     * registers depend on the other */
+    if constexpr (TYPE == 14) by_pairs(std::true_type{});
+    else if (a.S.mxflag[GU ? 0 : 1] != a.S.epoch) by_pairs(std::true_type{});
+    else by_pairs(std::false_type{});
     if (!GU) return;
     __syncthreads();
     /* a = silu(g) * u (src/model.c:989-994) into the gate rows of res, then the int8 blocks of
@@ -2875,7 +2898,7 @@ void mx_kernel(MxArgs a)
         const int s = s0 + sl, blk = (R0 >> 5) + g;
         store_q8(q, a.S.aq + (size_t)s * nbF + blk);
         store_pair_half(q, (uint32_t *)(a.S.aqk + ((size_t)s * (nbF >> 1) + (blk >> 1)) * kPairBytes), blk & 1);
-        mx_store_record(q, a.rec_out + ((size_t)s * nbF + blk) * kMxRec);
+        if (!mx_store_record(q, a.rec_out + ((size_t)s * nbF + blk) * kMxRec)) a.S.mxflag[1] = a.S.epoch;
     }
 }
 
@@ -2958,7 +2981,7 @@ hipError_t launch_experts_mx(const Shape &s, const LayerDev &L, const Scratch &S
     if (!mx_supported(s, L, &down_mx)) return hipErrorInvalidValue;
     const int NS = T * s.K, maxt = (s.X < NS ? s.X : NS) + NS / kTileN + 1;
     const int nx = T * (s.E / 32);
-    QLAUNCH("mxin", mx_input_kernel, dim3((nx + 255) / 256), dim3(256), 0, st, S.xq, nx, S.mxx);
+    QLAUNCH("mxin", mx_input_kernel, dim3((nx + 255) / 256), dim3(256), 0, st, S.xq, nx, S.mxx, S.mxflag, S.epoch);
     MxArgs a;
     a.w0 = L.gate;
     a.w1 = L.up;

@@ -4,6 +4,10 @@
         per-kernel launches / average / min / max duration from rocprofv3 --kernel-trace --stats
         CSV output under DIR (its *kernel_stats.csv), short names for the library's kernels.
 
+    python -m large_model_amd.profiling counters DIR [DIR ...] [--command "..."]
+        per kernel, the mean per dispatch of every counter in the rocprofv3 --pmc CSV output
+        under the DIRs (a dispatch's rows summed over the device), one pass per DIR.
+
     python -m large_model_amd.profiling traffic --kernel gateup --fetch DIR --write DIR
         --copy-fetch DIR --copy-write DIR --copy-bytes N [--algorithmic-bytes B] [--command "..."]
         HBM bytes per dispatch of one kernel from rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE runs
@@ -69,6 +73,30 @@ def counter_values(d: str, counter: str, kernel: str) -> list[float]:
     return vals
 
 
+def counters(dirs: list[str]) -> list[str]:
+    per_kernel: dict[str, dict[str, list[float]]] = {}
+    for d in dirs:
+        files = glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True)
+        if not files:
+            sys.exit(f"no *counter_collection.csv under {d}")
+        for f in files:
+            per_dispatch: dict[tuple[str, str], dict[str, float]] = {}
+            for r in csv.DictReader(open(f)):
+                key = (r["Kernel_Name"], r["Dispatch_Id"])
+                c = per_dispatch.setdefault(key, {})
+                c[r["Counter_Name"]] = c.get(r["Counter_Name"], 0.0) + float(r["Counter_Value"])
+            for (k, _), cs in per_dispatch.items():
+                for c, v in cs.items():
+                    per_kernel.setdefault(k, {}).setdefault(c, []).append(v)
+    out = []
+    for k in sorted(per_kernel):
+        cs = per_kernel[k]
+        out.append(f"{k.split('(')[0]}  [{max(len(v) for v in cs.values())} dispatches]")
+        for c in sorted(cs):
+            out.append(f"   {c:32s} {sum(cs[c]) / len(cs[c]):18.0f}")
+    return out
+
+
 def traffic(a) -> list[str]:
     f = counter_values(a.fetch, "FETCH_SIZE", a.kernel)
     w = counter_values(a.write, "WRITE_SIZE", a.kernel)
@@ -105,6 +133,9 @@ def main():
     s = sub.add_parser("stats")
     s.add_argument("dir")
     s.add_argument("--command", default="")
+    c = sub.add_parser("counters")
+    c.add_argument("dirs", nargs="+")
+    c.add_argument("--command", default="")
     t = sub.add_parser("traffic")
     for k in ("fetch", "write", "copy_fetch", "copy_write"):
         t.add_argument("--" + k.replace("_", "-"), dest=k, required=True)
@@ -113,7 +144,12 @@ def main():
     t.add_argument("--algorithmic-bytes", type=int, default=0)
     t.add_argument("--command", default="")
     a = ap.parse_args()
-    lines = stats(a.dir) if a.mode == "stats" else traffic(a)
+    if a.mode == "stats":
+        lines = stats(a.dir)
+    elif a.mode == "counters":
+        lines = counters(a.dirs)
+    else:
+        lines = traffic(a)
     if a.command:
         print("# " + a.command.replace("\n", "\n# "))
     print("\n".join(lines))

@@ -10,6 +10,7 @@
 #include "qms_oracle.h"
 #include "qmsg_synth.h"
 
+#include <limits.h>
 #include <math.h>
 #include <stdlib.h>
 #include <string.h>
@@ -105,15 +106,20 @@ void orc_quantize_q8(const float *x, int64_t n, orc_q8 *out)
         const float id = d > 0.0f ? 1.0f / d : 0.0f;
         int s0 = 0, s1 = 0;
         for (int j = 0; j < 32; j++) {
-            const int q = orc_mutation == ORC_MUT_ROUND_AWAY ? (int)roundf(xb[j] * id)
-                                                             : (int)nearbyintf(xb[j] * id);
+            /* (int) of a value outside int's range, or of a NaN, is undefined in C; the x86
+             * conversion the reference compiles to gives INT_MIN (the "integer indefinite").
+             * That happens when id is +inf (d below 2^-128) or xb[j] is NaN or infinite. */
+            const float r = orc_mutation == ORC_MUT_ROUND_AWAY ? roundf(xb[j] * id) : nearbyintf(xb[j] * id);
+            const int q = fabsf(r) < 2147483648.0f ? (int)r : INT_MIN;
             out[b].q[j] = (int8_t)q;
-            if (j < 16) s0 += q; else s1 += q;
+            /* wrapping sums (several INT_MIN codes overflow int; the reference's adds wrap) */
+            if (j < 16) s0 = (int)((unsigned)s0 + (unsigned)q);
+            else s1 = (int)((unsigned)s1 + (unsigned)q);
         }
         out[b].d = d;
         out[b].s16[0] = (int16_t)s0;
         out[b].s16[1] = (int16_t)s1;
-        out[b].ds = d * (float)(s0 + s1);
+        out[b].ds = d * (float)(int)((unsigned)s0 + (unsigned)s1);
     }
 }
 

@@ -137,6 +137,8 @@ def test_one_token_routing_ties(qmsg, scale):
     assert np.array_equal(_bits(got["wt"]), _bits(ref["wt"])), "routing weights"
     for k in ("start", "slot_t", "slot_of", "active"):
         assert np.array_equal(got[k], ref[k]), k
+    # 1e-38: every block's d is below 2^-128, so 1/d is +inf and the codes convert from inf
+    assert np.array_equal(_bits(got["xq"]), _bits(ref["xq"])), "int8 input blocks"
     assert np.array_equal(_bits(out), _bits(ref_out)), "layer output"
 
 

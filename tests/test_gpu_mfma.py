@@ -116,3 +116,47 @@ def test_mfma_gateup_types_bit_exact(q, name, E, X, K, F, T, seed, gt, dt):
         for k in ("logits", "wt", "xq", "gu", "act", "aq", "dn"):
             assert np.array_equal(_bits(g[k]), _bits(ref[k])), k
         assert np.array_equal(_bits(o), _bits(ref_out)), "layer output"
+
+
+SCALE_CASES = [
+    # name, scale of every other token, gate/up type, down type
+    ("acts_subnormal_q4_0", 1e-20, orc.T_Q4_0, orc.T_Q4_0),   # activation blocks' d ~1e-43
+    ("input_tiny_q4_0", 1e-36, orc.T_Q4_0, orc.T_Q4_0),       # input blocks' d ~1e-38
+    ("acts_subnormal_q4_1", 1e-20, orc.T_Q4_1, orc.T_Q4_1),
+    ("input_tiny_q4_1", 1e-36, orc.T_Q4_1, orc.T_Q6_K),
+    ("input_tiny_q6_k", 1e-36, orc.T_Q6_K, orc.T_Q6_K),
+]
+
+
+@pytest.mark.parametrize("name,scale,gt,dt", SCALE_CASES, ids=[c[0] for c in SCALE_CASES])
+def test_mfma_scale_ranges(q, name, scale, gt, dt):
+    """Blocks whose d_x lies outside [2^-102, 2^88], where fl(d_w d_x 2^24) can differ from
+    fl(d_w d_x) 2^24 (subnormal products): the Q4 MFMA kernels must take their unscaled loop
+    for such launches, Q6_K needs no range. Every other token is scaled down, so a launch mixes
+    in-range and out-of-range records. Checked: the case does put records out of range."""
+    E, X, K, F, T, seed = 2048, 128, 8, 768, 64, 41
+    print(f"[case] mfma scale range {name}", flush=True)
+    x = orc.make_input(E, T, seed)
+    x[1::2] *= np.float32(scale)
+    host = orc.Layer(E, X, K, F, seed, gate_type=gt, up_type=gt, down_type=dt, experts=[])
+    ref_out, ref = host.moe(x, debug=True)
+    d = np.concatenate([ref["xq"]["d"].ravel(), ref["aq"]["d"].ravel()])
+    assert ((d != 0) & ((d < 2.0 ** -102) | (d > 2.0 ** 88))).any(), "no record outside the range"
+    with q.Context(E, X, K, F, n_layer=1, max_tokens=T) as ctx:
+        ctx.synth(0, seed, gate_type=gt, up_type=gt, down_type=dt)
+        results = []
+        for path in (q.PATH_MFMA, q.PATH_AUTO):
+            ctx.set_path(path)
+            results.append(ctx.moe_debug(0, x))
+        # the same context on in-range inputs next: no flag of this call may linger
+        x2 = orc.make_input(E, T, seed + 1)
+        ref2 = host.moe(x2)
+        ctx.set_path(q.PATH_MFMA)
+        out2 = ctx.moe(0, x2)
+    for o, g in results:
+        for k in ("sel", "start", "slot_t", "slot_of", "active"):
+            assert np.array_equal(g[k], ref[k]), k
+        for k in ("logits", "wt", "xq", "gu", "act", "aq", "dn"):
+            assert np.array_equal(_bits(g[k]), _bits(ref[k])), k
+        assert np.array_equal(_bits(o), _bits(ref_out)), "layer output"
+    assert np.array_equal(_bits(out2), _bits(ref2)), "in-range call after"

@@ -91,6 +91,50 @@ def test_quantize_q8_closed_form():
         assert np.abs(q).max() == 127
 
 
+def test_quantize_q8_codes_outside_int():
+    """Blocks whose scaled values leave int's range: d below 2^-128 (1/d = +inf), NaN and
+    infinite inputs. The reference's (int)nearbyintf is x86's conversion, INT_MIN for those,
+    so each such code is 0 as int8 and adds INT_MIN to its half sum (mod 2^32). Closed form
+    here; bit for bit against the reference build where it is present."""
+    rng = np.random.default_rng(5)
+    x = rng.standard_normal((6, 32)).astype(np.float32)
+    x[0] *= np.float32(1e-39)            # d below 2^-128: id = +inf
+    x[1] *= np.float32(1e-44)            # subnormal inputs, the same
+    x[2, 3] = np.inf                     # d = +inf, id = 0: inf * 0 is NaN
+    x[3, 7] = np.nan                     # amax ignores the NaN
+    x[4, :] = np.nan                     # all NaN: d = 0, every code from NaN * 0
+    x[5, ::3] = -np.inf
+    got = orc.quantize_q8(x.ravel())
+    imin = -2 ** 31
+    for b in range(6):
+        xb = x[b]
+        with np.errstate(all="ignore"):
+            amax = np.float32(0)
+            for v in xb:                 # fmaxf from 0, NaN ignored
+                if not np.isnan(v):
+                    amax = max(amax, np.float32(abs(v)))
+            d = amax / np.float32(127)
+            idv = np.float32(1) / d if d > 0 else np.float32(0)
+            r = np.rint(xb * idv)
+        q = np.array([int(v) if abs(v) < 2.0 ** 31 else imin for v in r], np.int64)
+        assert np.array_equal(got["q"][b].astype(np.int64), ((q + 128) % 256) - 128), b
+        wrap = lambda v: ((int(v) + 2 ** 31) % 2 ** 32) - 2 ** 31
+        s0, s1 = wrap(q[:16].sum()), wrap(q[16:].sum())
+        assert got["s16"][b][0] == ((s0 + 2 ** 15) % 2 ** 16) - 2 ** 15, b
+        assert got["s16"][b][1] == ((s1 + 2 ** 15) % 2 ** 16) - 2 ** 15, b
+        with np.errstate(all="ignore"):
+            ds = np.float32(d) * np.float32(wrap(s0 + s1))
+        assert f32_bits(got["ds"][b]) == f32_bits(ds) or (np.isnan(got["ds"][b]) and np.isnan(ds)), b
+    assert not got["q"][0].any() and not got["q"][1].any()
+    R = orc.load_ref()
+    if R is None:
+        pytest.skip("reference build (oracle/_ref) not present")
+    ref = np.zeros_like(got)
+    xs = np.ascontiguousarray(x.ravel())
+    R.qms_quantize_q8(xs.ctypes.data, xs.size, ref.ctypes.data)
+    assert np.array_equal(ref.view(np.uint8), got.view(np.uint8))
+
+
 def test_vec_dot_q8_matches_reference(kat):
     for t, w, x, xq, dot, _ in kernel_cases(kat):
         n = x.size
