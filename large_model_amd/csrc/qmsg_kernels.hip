@@ -2034,11 +2034,11 @@ __global__ __launch_bounds__(32 * RD) void down_small_kernel(DownArgs a)
 
 /* The int8 blocks of every slot's activations (src/model.c:996-997) for batches whose
  * records do not fit the down kernel's LDS: one thread per 32-block. */
-__device__ bool mx_store_record(const Q8Vals &q, uint8_t *rec);
+__device__ bool mx_store_record(const Q8Vals &q, uint8_t *rec, bool hi16);
 
 /* The int8 activation blocks of every slot (src/model.c:996-997) from act: QmsQ8 blocks, pair
  * records, and, when mxrec is set, the MFMA kernels' records too. */
-__global__ void act_quant_kernel(Scratch S, int F, int NS, uint8_t *mxrec)
+__global__ void act_quant_kernel(Scratch S, int F, int NS, uint8_t *mxrec, int hi16)
 {
     const int nbF = F >> 5;
     const int b = blockIdx.x * blockDim.x + threadIdx.x;
@@ -2054,7 +2054,7 @@ __global__ void act_quant_kernel(Scratch S, int F, int NS, uint8_t *mxrec)
     const Q8Vals q = quantize_block(v);
     store_q8(q, S.aq + b);
     store_pair_half(q, (uint32_t *)(S.aqk + ((size_t)s * (nbF >> 1) + (blk >> 1)) * kPairBytes), blk & 1);
-    if (mxrec && !mx_store_record(q, mxrec + (size_t)b * kMxRec)) S.mxflag[1] = S.epoch;
+    if (mxrec && !mx_store_record(q, mxrec + (size_t)b * kMxRec, hi16)) S.mxflag[1] = S.epoch;
 }
 
 /* Weighted sum per token in selection order (src/model.c:1152-1162) when dn did not fit. */
@@ -2137,7 +2137,7 @@ hipError_t launch_down_exact(const Shape &s, const LayerDev &L, const Scratch &S
     const bool qa = quant && T <= kTileQuantT;
     if (quant && !qa) {
         const int nq = NS * (s.F / 32);
-        QLAUNCH("actq", act_quant_kernel, dim3((nq + 255) / 256), dim3(256), 0, st, S, s.F, NS, (uint8_t *)nullptr);
+        QLAUNCH("actq", act_quant_kernel, dim3((nq + 255) / 256), dim3(256), 0, st, S, s.F, NS, (uint8_t *)nullptr, 0);
     }
     const int NT = T >= 4 ? 4 : (T >= 2 ? 2 : 1);
     const int RT = L.down_type == 14 ? kDownTileRowsQ6K : 64;
@@ -2246,12 +2246,13 @@ hipError_t launch_gateup_tiles(const Shape &s, const LayerDev &L, const Scratch 
  * K position 8g + e of lane group g is block element pi(8g + e) =
  * 4g, 4g+2, 4g+1, 4g+3, 16+4g, 16+4g+2, 16+4g+1, 16+4g+3: the first four are reference lane
  * k = g, the last four lane k = g + 4, and both come from one code dword (Q4) of the block
- * with four shift-and-or steps. D-row 4(l/16) + v is slot j = l/32 of the pair and lane
+ * with one shift and four masks: the high nibbles stay in place as 16 x code, against x / 16
+ * in the records' lanes 4-7 (the product is the same). D-row 4(l/16) + v is slot j = l/32 of the pair and lane
  * k = 4((l/16)&1) + v, so a lane holds four chains of one (row, slot): one fl(d_w d_x) product
  * serves its four FMAs.
  *
  * Activation records (kMxRec bytes per slot, or per token, and 32-block) carry x in that
- * order as f16 (64 bytes), then d 2^24 (or the NaN that sends the chunk to the unscaled
+ * order as f16 (64 bytes; for Q4 rows lanes 4-7 hold x / 16), then d 2^24 (or the NaN that sends the chunk to the unscaled
  * chains), ds, the half sums and d (16 bytes), then 16 zero bytes, which the lanes of A
  * outside their group read; the kernels stage those first 96 bytes of each record. Gate/up
  * writes the records of the activations it quantises, so the down products read them
@@ -2281,8 +2282,9 @@ __device__ __forceinline__ float mx_scaled_d(float d)
 }
 
 /* One int8 block as an activation record (layout above); false when its d_x 2^24 word is the
- * NaN (d_x outside the scaled range). */
-__device__ bool mx_store_record(const Q8Vals &q, uint8_t *rec)
+ * NaN (d_x outside the scaled range). hi16: for Q4_0 / Q4_1 rows, whose B operand takes the
+ * high nibbles in place (code 16 2^-24), lanes 4-7 carry x / 16 (exact in f16). */
+__device__ bool mx_store_record(const Q8Vals &q, uint8_t *rec, bool hi16)
 {
     u32x4 w[6];
 #pragma unroll
@@ -2290,7 +2292,8 @@ __device__ bool mx_store_record(const Q8Vals &q, uint8_t *rec)
         const uint32_t c = q.qw[k];
         const int x0 = (int)(int8_t)(c & 0xffu), x1 = (int)(int8_t)((c >> 8) & 0xffu);
         const int x2 = (int)(int8_t)((c >> 16) & 0xffu), x3 = (int)(int8_t)(c >> 24);
-        auto h = [](int x) { return (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)(float)x); };
+        const float sc = (hi16 && k >= 4) ? 0.0625f : 1.0f;
+        auto h = [sc](int x) { return (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)((float)x * sc)); };
         w[k >> 1][2 * (k & 1)] = h(x0) | (h(x2) << 16);
         w[k >> 1][2 * (k & 1) + 1] = h(x1) | (h(x3) << 16);
     }
@@ -2303,7 +2306,7 @@ __device__ bool mx_store_record(const Q8Vals &q, uint8_t *rec)
 }
 
 /* The layer input's records from its int8 blocks (one thread per block). */
-__global__ void mx_input_kernel(const Q8 *xq, int n, uint8_t *rec, uint64_t *flag, uint64_t epoch)
+__global__ void mx_input_kernel(const Q8 *xq, int n, uint8_t *rec, uint64_t *flag, uint64_t epoch, int hi16)
 {
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= n) return;
@@ -2314,7 +2317,7 @@ __global__ void mx_input_kernel(const Q8 *xq, int n, uint8_t *rec, uint64_t *fla
     q.s16 = s[2];
 #pragma unroll
     for (int w = 0; w < 8; w++) q.qw[w] = s[3 + w];
-    if (!mx_store_record(q, rec + (size_t)i * kMxRec)) *flag = epoch;
+    if (!mx_store_record(q, rec + (size_t)i * kMxRec, hi16)) *flag = epoch;
 }
 
 struct MxArgs {
@@ -2323,6 +2326,7 @@ struct MxArgs {
     int E, F, debug;
     const uint8_t *rec;          /* input records: [token][E/32] (gate/up) or [slot][F/32] (down) */
     uint8_t *rec_out;            /* gate/up: the activation records [slot][F/32] */
+    int rec_out_hi16;            /* gate/up: the down rows are Q4_0 / Q4_1 (records' lanes 4-7 x / 16) */
     Scratch S;
 };
 
@@ -2395,18 +2399,20 @@ __device__ __forceinline__ MxB mx_weights_q4(LdsPtr pq, LdsPtr pd, int t)
         const uint32_t a1 = *(const __attribute__((address_space(3))) uint32_t *)(pq + 16 * t * WS + 2);
         v = __builtin_amdgcn_alignbyte(a1, a0, 2);
     }
+    /* the high nibbles stay in place, as 16 x code (the records' lanes 4-7 carry x / 16) */
+    const uint32_t mh = 0x00f000f0u, v8 = v >> 8;
     if constexpr (SC) {
-        /* the f16 subnormals code 2^-24 */
-        w.op = __builtin_bit_cast(f16x8, u32x4{ v & m4, (v >> 8) & m4, (v >> 4) & m4, (v >> 12) & m4 });
+        /* the f16 subnormals code 2^-24 (high nibbles 16 code 2^-24) */
+        w.op = __builtin_bit_cast(f16x8, u32x4{ v & m4, v8 & m4, v & mh, v8 & mh });
     } else {
-        /* the codes themselves: f16 1024 + code (0x6400 | code) minus 1024, exact */
+        /* the codes themselves: f16 1024 + c (0x6400 | c) minus 1024, exact */
         const uint32_t bias = 0x64006400u;
         typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
         const f16x2 k = { (_Float16)1024.0f, (_Float16)1024.0f };
         const f16x2 c0 = __builtin_bit_cast(f16x2, and_or(v, m4, bias)) - k;
-        const f16x2 c1 = __builtin_bit_cast(f16x2, and_or(v >> 8, m4, bias)) - k;
-        const f16x2 c2 = __builtin_bit_cast(f16x2, and_or(v >> 4, m4, bias)) - k;
-        const f16x2 c3 = __builtin_bit_cast(f16x2, and_or(v >> 12, m4, bias)) - k;
+        const f16x2 c1 = __builtin_bit_cast(f16x2, and_or(v8, m4, bias)) - k;
+        const f16x2 c2 = __builtin_bit_cast(f16x2, and_or(v, mh, bias)) - k;
+        const f16x2 c3 = __builtin_bit_cast(f16x2, and_or(v8, mh, bias)) - k;
         w.op = f16x8{ c0.x, c0.y, c1.x, c1.y, c2.x, c2.y, c3.x, c3.y };
     }
     if constexpr (TYPE == 3) w.dw = *(const __attribute__((address_space(3))) uint32_t *)(pd + 16 * t * WS);
@@ -2898,7 +2904,8 @@ void mx_kernel(MxArgs a)
         const int s = s0 + sl, blk = (R0 >> 5) + g;
         store_q8(q, a.S.aq + (size_t)s * nbF + blk);
         store_pair_half(q, (uint32_t *)(a.S.aqk + ((size_t)s * (nbF >> 1) + (blk >> 1)) * kPairBytes), blk & 1);
-        if (!mx_store_record(q, a.rec_out + ((size_t)s * nbF + blk) * kMxRec)) a.S.mxflag[1] = a.S.epoch;
+        if (!mx_store_record(q, a.rec_out + ((size_t)s * nbF + blk) * kMxRec, a.rec_out_hi16))
+            a.S.mxflag[1] = a.S.epoch;
     }
 }
 
@@ -2981,7 +2988,8 @@ hipError_t launch_experts_mx(const Shape &s, const LayerDev &L, const Scratch &S
     if (!mx_supported(s, L, &down_mx)) return hipErrorInvalidValue;
     const int NS = T * s.K, maxt = (s.X < NS ? s.X : NS) + NS / kTileN + 1;
     const int nx = T * (s.E / 32);
-    QLAUNCH("mxin", mx_input_kernel, dim3((nx + 255) / 256), dim3(256), 0, st, S.xq, nx, S.mxx, S.mxflag, S.epoch);
+    QLAUNCH("mxin", mx_input_kernel, dim3((nx + 255) / 256), dim3(256), 0, st, S.xq, nx, S.mxx, S.mxflag, S.epoch,
+            L.gate_type != 14 ? 1 : 0);
     MxArgs a;
     a.w0 = L.gate;
     a.w1 = L.up;
@@ -2992,6 +3000,7 @@ hipError_t launch_experts_mx(const Shape &s, const LayerDev &L, const Scratch &S
     a.debug = debug;
     a.rec = S.mxx;
     a.rec_out = S.mxa;
+    a.rec_out_hi16 = L.down_type != 14 ? 1 : 0;
     a.S = S;
     if (L.gate_type == 14) launch_mx<14, 1>(a, s.F, maxt, mx_shape(s, T, 1, 14), st);
     else if (L.gate_type == 3) launch_mx<3, 1>(a, s.F, maxt, mx_shape(s, T, 1, 3), st);
@@ -3007,6 +3016,7 @@ hipError_t launch_experts_mx(const Shape &s, const LayerDev &L, const Scratch &S
     a.eb = L.down_eb;
     a.rec = S.mxa;
     a.rec_out = nullptr;
+    a.rec_out_hi16 = 0;
     if (L.down_type == 14) launch_mx<14, 0>(a, s.E, maxt, mx_shape(s, T, 0, 14), st);
     else if (L.down_type == 3) launch_mx<3, 0>(a, s.E, maxt, mx_shape(s, T, 0, 3), st);
     else launch_mx<2, 0>(a, s.E, maxt, mx_shape(s, T, 0, 2), st);
@@ -3024,7 +3034,8 @@ hipError_t launch_down_mx(const Shape &s, const LayerDev &L, const Scratch &S, f
     if (!down_mx) return hipErrorInvalidValue;
     const int NS = T * s.K, maxt = (s.X < NS ? s.X : NS) + NS / kTileN + 1;
     const int nq = NS * (s.F / 32);
-    QLAUNCH("actq", act_quant_kernel, dim3((nq + 255) / 256), dim3(256), 0, st, S, s.F, NS, S.mxa);
+    QLAUNCH("actq", act_quant_kernel, dim3((nq + 255) / 256), dim3(256), 0, st, S, s.F, NS, S.mxa,
+            L.down_type != 14 ? 1 : 0);
     MxArgs a;
     a.w0 = L.down;
     a.w1 = nullptr;
@@ -3035,6 +3046,7 @@ hipError_t launch_down_mx(const Shape &s, const LayerDev &L, const Scratch &S, f
     a.debug = 0;
     a.rec = S.mxa;
     a.rec_out = nullptr;
+    a.rec_out_hi16 = 0;
     a.S = S;
     if (L.down_type == 14) launch_mx<14, 0>(a, s.E, maxt, mx_shape(s, T, 0, 14), st);
     else if (L.down_type == 3) launch_mx<3, 0>(a, s.E, maxt, mx_shape(s, T, 0, 3), st);
