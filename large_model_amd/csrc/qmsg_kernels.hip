@@ -2468,13 +2468,16 @@ __device__ __forceinline__ void mx_opaque(MxStreams &st)
  * against its two 16-row tiles. SC: the chunk's records all carry d_x 2^24 and B holds the
  * codes 2^-24; else B holds the codes themselves and the chains take d_x unscaled. */
 template <int TYPE, int NP, int PAR, bool SC>
-__device__ __forceinline__ void mx_block(const MxStreams &st, f32x4 (&acc)[2][4], float (&cr)[2][4])
+__device__ __forceinline__ void mx_block(const MxStreams &st, bool kh, f32x4 (&acc)[2][4], float (&cr)[2][4])
 {
     static_assert(TYPE == 2 || TYPE == 3, "Q6_K chunks take mx_chunk_q6");
     constexpr int BB = TYPE == 3 ? 20 : 18, RB = PAR * mx_recl(TYPE), RS = mx_rstride(TYPE);
     MxB w[2];
 #pragma unroll
     for (int t = 0; t < 2; t++) w[t] = mx_weights_q4<TYPE, PAR, SC>(st.q + PAR * BB, st.dw + PAR * BB, t);
+    /* the two lanes of a (row, slot) share its offset chain: the k-half-0 lane runs tile 0's,
+     * the other tile 1's (cr[0][p]; the epilogue fetches the partner's) */
+    const uint32_t dwc = kh ? w[1].dw : w[0].dw;
     /* pair p's two MFMAs are issued before pair p-1's results are used, so the chains of one
      * pair run while the matrix core works on the next */
     f32x4 S[2][2];
@@ -2507,17 +2510,17 @@ __device__ __forceinline__ void mx_block(const MxStreams &st, f32x4 (&acc)[2][4]
 #pragma unroll
             for (int v = 0; v < 4; v++)
                 acc[t][p][v] = __builtin_fmaf(S[k][t][v], dd, acc[t][p][v]);
-            if constexpr (TYPE == 3) cr[t][p] = mix_fma_hi(w[t].dw, xds[k], cr[t][p]);   /* off += m*ds */
-            else cr[t][p] = mix_fma_lo(w[t].dw, xds[k], cr[t][p]);                     /* corr += d*ds */
         }
+        if constexpr (TYPE == 3) cr[0][p] = mix_fma_hi(dwc, xds[k], cr[0][p]);   /* off += m*ds */
+        else cr[0][p] = mix_fma_lo(dwc, xds[k], cr[0][p]);                     /* corr += d*ds */
     }
 }
 
 /* One staged chunk (kMxC blocks), two blocks per loop trip. A lane's A words are its x words
  * where it holds x, else the record's zero words. */
 template <int TYPE, int NP, bool SC>
-__device__ __forceinline__ void mx_chunk(const uint8_t *W, const uint8_t *R, int lr, int lg, int jd, int offa_lo,
-                                         int offa_hi, f32x4 (&acc)[2][4], float (&cr)[2][4])
+__device__ __forceinline__ void mx_chunk(const uint8_t *W, const uint8_t *R, int lr, int lg, int jd, bool kh,
+                                         int offa_lo, int offa_hi, f32x4 (&acc)[2][4], float (&cr)[2][4])
 {
     constexpr int WS = mx_wstride(TYPE), BB = TYPE == 3 ? 20 : 18, QO = TYPE == 3 ? 4 : 2;
     MxStreams st;
@@ -2529,9 +2532,9 @@ __device__ __forceinline__ void mx_chunk(const uint8_t *W, const uint8_t *R, int
 #pragma unroll 1
     for (int b = 0; b < kMxC; b += 2) {
         mx_opaque(st);
-        mx_block<TYPE, NP, 0, SC>(st, acc, cr);
+        mx_block<TYPE, NP, 0, SC>(st, kh, acc, cr);
         __builtin_amdgcn_sched_barrier(0);      /* one block's operands in registers at a time */
-        mx_block<TYPE, NP, 1, SC>(st, acc, cr);
+        mx_block<TYPE, NP, 1, SC>(st, kh, acc, cr);
         st.alo += 2 * mx_recl(TYPE);
         st.ahi += 2 * mx_recl(TYPE);
         st.d += 2 * mx_recl(TYPE);
@@ -2835,13 +2838,14 @@ void mx_kernel(MxArgs a)
                     if (c & 1) mx_chunk_q6<NP, 2, TS6>(Wl, Rl, lr, lg, kh, jd, offa_lo, offa_hi, acc, cr);
                     else mx_chunk_q6<NP, 0, TS6>(Wl, Rl, lr, lg, kh, jd, offa_lo, offa_hi, acc, cr);
                 } else {
-                    mx_chunk<TYPE, NP, SC>(Wl, Rl, lr, lg, jd, offa_lo, offa_hi, acc, cr);
+                    mx_chunk<TYPE, NP, SC>(Wl, Rl, lr, lg, jd, kh != 0, offa_lo, offa_hi, acc, cr);
                 }
             }
             /* chunk c+1 has landed; buffer c is free for chunk c+2 (one buffer: it is free) */
             mx_wait_barrier();
         }
-        /* hsum256 per (row, slot): lanes of k-half 0 take the partner lane's k + 4 chains */
+        /* hsum256 per (row, slot): lanes of k-half 0 take the partner lane's k + 4 chains (Q4
+         * types: and, for tile 1, the partner's offset chain) */
 #pragma unroll
         for (int t = 0; t < 2; t++)
 #pragma unroll
@@ -2849,10 +2853,15 @@ void mx_kernel(MxArgs a)
                 f32x4 o;
 #pragma unroll
                 for (int v = 0; v < 4; v++) o[v] = __shfl_xor(acc[t][p][v], 16);
+                float crv = cr[t][p];
+                if constexpr (TYPE != 14) {
+                    const float other = __shfl_xor(cr[0][p], 16);
+                    crv = t == 0 ? cr[0][p] : other;
+                }
                 if (kh == 0) {
                     const f32x4 &q = acc[t][p];
                     const float h = ((q[0] + o[0]) + (q[2] + o[2])) + ((q[1] + o[1]) + (q[3] + o[3]));
-                    const float val = h - scale * cr[t][p];
+                    const float val = h - scale * crv;
                     const int row = 32 * wr + 16 * t + lr, sl = 2 * PPW * ws + 2 * p + jd;
                     if (GU) res[row * (SWG + 1) + sl] = val;
                     else if (sl < ns) a.S.dn[(size_t)(s0 + sl) * a.E + R0 + row] = val;
