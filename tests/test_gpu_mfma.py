@@ -160,3 +160,43 @@ def test_mfma_scale_ranges(q, name, scale, gt, dt):
             assert np.array_equal(_bits(g[k]), _bits(ref[k])), k
         assert np.array_equal(_bits(o), _bits(ref_out)), "layer output"
     assert np.array_equal(_bits(out2), _bits(ref2)), "in-range call after"
+
+
+def _sweep_cases(n=12, seed=2026):
+    """Seeded random layers for the MFMA kernels: widths, batch sizes and tensor types drawn
+    from a fixed generator, so the list is the same on every run."""
+    rng = np.random.default_rng(seed)
+    types = [orc.T_Q4_0, orc.T_Q4_1, orc.T_Q6_K]
+    out = []
+    for i in range(n):
+        E, F = [(2048, 768), (4096, 1536), (1024, 512)][int(rng.integers(0, 3))]
+        T = int(rng.integers(5, 150))
+        gt = types[int(rng.integers(0, 3))]
+        dt = types[int(rng.integers(0, 3))]
+        out.append((f"sweep{i}_E{E}_T{T}_g{gt}_d{dt}", E, 128, 8, F, T, 100 + i, gt, dt))
+    return out
+
+
+SWEEP = _sweep_cases()
+
+
+@pytest.mark.parametrize("name,E,X,K,F,T,seed,gt,dt", SWEEP, ids=[c[0] for c in SWEEP])
+def test_mfma_sweep(q, name, E, X, K, F, T, seed, gt, dt):
+    """Seeded random shapes, batch sizes and tensor types on the forced MFMA path and the
+    default path: every intermediate bit for bit against the oracle."""
+    print(f"[case] mfma sweep {name}", flush=True)
+    x = orc.make_input(E, T, seed)
+    host = orc.Layer(E, X, K, F, seed, gate_type=gt, up_type=gt, down_type=dt, experts=[])
+    ref_out, ref = host.moe(x, debug=True)
+    with q.Context(E, X, K, F, n_layer=1, max_tokens=T) as ctx:
+        ctx.synth(0, seed, gate_type=gt, up_type=gt, down_type=dt)
+        results = []
+        for path in (q.PATH_MFMA, q.PATH_AUTO):
+            ctx.set_path(path)
+            results.append(ctx.moe_debug(0, x))
+    for o, g in results:
+        for k in ("sel", "start", "slot_t", "slot_of", "active"):
+            assert np.array_equal(g[k], ref[k]), k
+        for k in ("logits", "wt", "xq", "gu", "act", "aq", "dn"):
+            assert np.array_equal(_bits(g[k]), _bits(ref[k])), k
+        assert np.array_equal(_bits(o), _bits(ref_out)), "layer output"
