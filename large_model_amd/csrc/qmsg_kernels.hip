@@ -4152,6 +4152,7 @@ __device__ double ordered_sum_chunked(const double *qt, int C)
         c3 += qt[(i + 3) * kSumPitch + j];
     }
     double inc = (c0 + c1) + (c2 + c3);
+    PHASE(3072, 3);
     if (!__all(__builtin_isfinite(inc))) {
         /* an infinite or NaN term: term by term throughout */
         double s[1] = { 0.0 };
@@ -4170,38 +4171,77 @@ __device__ double ordered_sum_chunked(const double *qt, int C)
     const double P1 = P + __longlong_as_double((long long)(normal ? e - 52 : 1) << 52);
     double g[2] = { P, P1 };
     column_run<2>(qt, j, C, g);
+    PHASE(3072, 4);
     const uint64_t pb = dbits(P);
     const uint64_t d0 = dbits(g[0]) - pb, d1 = dbits(g[1]) - (pb + 1);
     const int ex = normal && dexp(P1) == e && dexp(g[0]) == e && dexp(g[1]) == e ? e : -1;
-    /* 3 */
+    /* 3. In bit patterns, an in-binade chunk maps s to s + a[s & 1] (a: the deltas by the parity
+     * of s itself, a[r ^ (P & 1)] = D_r). Such maps compose (f then g: s + f[p] + g[(p + f[p]) & 1]
+     * for p = s & 1), so a run of in-binade chunks is walked at once: a prefix over its lanes
+     * gives every chunk's start from the run's, each lane checks that its start and end stay in
+     * its binade (or that its start is its P), and the run ends at its last chunk's end; a
+     * chunk that fails the check, or one outside the rule, is added term by term. */
+    const uint64_t a0 = (pb & 1) ? d1 : d0, a1 = (pb & 1) ? d0 : d1;
+    const uint64_t outside = __ballot(ex < 0);
+    auto shfl_up_u64 = [](uint64_t v, int d) {
+        const uint32_t lo = (uint32_t)__shfl_up((int)(uint32_t)v, d), hi = (uint32_t)__shfl_up((int)(uint32_t)(v >> 32), d);
+        return ((uint64_t)hi << 32) | lo;
+    };
     uint64_t sb = 0;                                   /* bits of s = +0.0 */
-    for (int k0 = 0; k0 < 64; k0 += 8) {
-        /* eight chunks' values in scalar registers ahead of the walk through them */
-        uint64_t Pk[8], D0[8], D1[8];
-        int ek[8];
-#pragma unroll
-        for (int u = 0; u < 8; u++) {
-            Pk[u] = readlane_u64(pb, k0 + u);
-            D0[u] = readlane_u64(d0, k0 + u);
-            D1[u] = readlane_u64(d1, k0 + u);
-            ek[u] = __builtin_amdgcn_readlane(ex, k0 + u);
+#ifdef QMSG_PHASE_TRACE
+    int nslow = 0;
+    unsigned long long tslow = 0;
+#endif
+    auto term_by_term = [&](int k, uint64_t from) {
+#ifdef QMSG_PHASE_TRACE
+        const unsigned long long ts0 = __builtin_amdgcn_s_memrealtime();
+#endif
+        double t[1] = { __longlong_as_double((long long)from) };
+        column_run<1>(qt, k, C, t);
+#ifdef QMSG_PHASE_TRACE
+        nslow++;
+        tslow += __builtin_amdgcn_s_memrealtime() - ts0;
+#endif
+        return readlane_u64(dbits(t[0]), 0);
+    };
+    int k = 0;
+    while (k < 64) {
+        if ((outside >> k) & 1) {
+            const uint64_t pk = readlane_u64(pb, k);
+            sb = sb == pk ? pk + readlane_u64(d0, k) : term_by_term(k, sb);
+            k++;
+            continue;
         }
-#pragma unroll
-        for (int u = 0; u < 8; u++) {
-            /* selects, not branches, on the common paths */
-            const bool same = sb == Pk[u];
-            const uint64_t nx = sb + (((sb - Pk[u]) & 1) ? D1[u] : D0[u]);
-            const bool fast = ek[u] >= 0 && (int)(sb >> 52) == ek[u] && (int)(nx >> 52) == ek[u];
-            const bool slow = !same && !fast;
-            const uint64_t s0 = sb;
-            sb = same ? Pk[u] + D0[u] : nx;
-            if (slow) {
-                double t[1] = { __longlong_as_double((long long)s0) };
-                column_run<1>(qt, k0 + u, C, t);
-                sb = readlane_u64(dbits(t[0]), 0);
+        const uint64_t later = outside >> k;
+        const int r = later ? k + __builtin_ctzll(later) : 64;     /* the run is chunks k .. r-1 */
+        const bool in = j >= k && j < r;
+        uint64_t i0 = a0, i1 = a1;                     /* the maps of chunks k .. j composed */
+        for (int d = 1; d < 64; d <<= 1) {
+            const uint64_t p0 = shfl_up_u64(i0, d), p1 = shfl_up_u64(i1, d);
+            if (in && j - d >= k) {
+                const uint64_t n0 = p0 + ((p0 & 1) ? i1 : i0), n1 = p1 + ((p1 & 1) ? i0 : i1);
+                i0 = n0;
+                i1 = n1;
             }
         }
+        uint64_t e0 = shfl_up_u64(i0, 1), e1 = shfl_up_u64(i1, 1);
+        if (j == k) e0 = e1 = 0;
+        const uint64_t sj = sb + ((sb & 1) ? e1 : e0);  /* chunk j's start */
+        const uint64_t nj = sj + ((sj & 1) ? a1 : a0);
+        const bool ok = sj == pb || ((int)(sj >> 52) == ex && (int)(nj >> 52) == ex);
+        const uint64_t bad = __ballot(in && !ok);
+        if (!bad) {
+            sb = readlane_u64(nj, r - 1);
+            k = r;
+        } else {
+            const int b = __builtin_ctzll(bad);
+            sb = term_by_term(b, readlane_u64(sj, b));
+            k = b + 1;
+        }
     }
+#ifdef QMSG_PHASE_TRACE
+    if (threadIdx.x == 0 && blockIdx.x < 1024) qmsg::g_phase[(3072 + blockIdx.x) * 8 + 7] = (unsigned long long)nslow | (tslow << 8);
+#endif
     return __longlong_as_double((long long)sb);
 }
 
@@ -4220,6 +4260,7 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(float *x, const float *add
 {
     extern __shared__ __align__(16) double q[];      /* the squares */
     __shared__ double inv;
+    PHASE(3072, 0);
     float4 *xrow = (float4 *)(x + (size_t)blockIdx.x * E);
     const float4 *arow = add ? (const float4 *)(add + (size_t)blockIdx.x * E) : nullptr;
     const float4 *row = xrow;
@@ -4266,11 +4307,14 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(float *x, const float *add
             }
         }
     }
+    PHASE(3072, 1);
     __syncthreads();
+    PHASE(3072, 2);
     if (tid < 64) {
         double ss;
         if (chunked) {
             ss = ordered_sum_chunked(q, C);
+            PHASE(3072, 5);
         } else {
             ss = 0.0;
             if (tid == 0)
@@ -4279,6 +4323,7 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(float *x, const float *add
         if (tid == 0) inv = 1.0 / sqrt(ss / E + (double)eps);
     }
     __syncthreads();
+    PHASE(3072, 6);
     const double v = inv;
     auto norm = [&](float4 a, float4 b) {
         return make_float4((float)((double)a.x * v) * b.x, (float)((double)a.y * v) * b.y,
