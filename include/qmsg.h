@@ -74,12 +74,14 @@ typedef struct qmsg_ctx qmsg_ctx;
 /* Which kernels run the expert products. Every integer path gives the same bits: the int8
  * blocks, the per-block int32 dots and the fp32 rows follow the reference's AVX path exactly.
  *   EXACT: per-row VALU kernels (integer dot4 lane sums, the reference's fp32 lane chains).
- *   MFMA:  the lane sums of 16 rows x 2 slots per f16 MFMA (exact small integers), the same
- *          fp32 chains on the VALU; for batches of two or more tokens with gate and up of one
- *          type (down Q4_0, Q4_1 or Q6_K; other down rows on the EXACT kernel).
+ *   MFMA:  the lane sums on f16 MFMAs (exact small integers: 16 rows x 4 slots x half a
+ *          block per instruction for Q4_0 / Q4_1 rows, 16 rows x 2 slots for Q6_K rows and
+ *          waves of one or two slots), the same fp32 chains on the VALU; for batches of two or
+ *          more tokens with gate and up of one type (down Q4_0, Q4_1 or Q6_K; other down rows
+ *          on the EXACT kernel).
  *   AUTO:  per stage: Q4_0 / Q4_1 gate/up on MFMA for batches averaging at least 1.25 slots
  *          per active expert, Q6_K gate/up from 2.5, down on MFMA for
- *          batches of at least 72 slots (tokens x n_used; Q6_K down rows: 32), EXACT
+ *          batches of at least 64 slots (tokens x n_used; Q6_K down rows: 32), EXACT
  *          otherwise.
  *   FP32:  the reference's --exact mode (qms_exact_math = 1, src/quant.c:95-115,
  *          model.c:1009-1030): router, gate/up and down rows dequantised to fp32 and dotted in

@@ -48,15 +48,16 @@ constexpr int kMxRec = 128;
 /* The default path takes the MFMA kernels for gate/up once a batch averages kMxAutoQuarters / 4
  * slots per active expert, and for down from kMxDownMinSlotsQ4 slots (Q4_0 / Q4_1 rows) or
  * kMxDownMinSlotsQ6 (Q6_K rows). Measured per layer at the 235B shape, MFMA against the row
- * kernels (us): gate/up with the records each needs 227.5 / 229.7 at 20 tokens (1.25 slots per
- * expert), 132.6 / 129.6 at 16; down after row-kernel gate/up, with the activation records it
- * needs and the combine: Q4_0 37.9 / 34.1 at 4 tokens, 44.9 / 44.1 at 6, 53.2 / 53.8 at 8, 64.4 /
- * 69.3 at 12; Q6_K 41.6 / 32.9 at 2, 49.4 / 46.2 at 3, 58.2 / 58.2 at 4, 105 / 118 at 8. */
+ * kernels (us; Q4 MFMA kernels on the 16x16x16 instructions): gate/up with the records each
+ * needs 132.2 / 130.1 at 16 tokens, 114.2 / 107.1 at 12, and from 20 tokens (1.25 slots per
+ * expert) 149.6 / 154.8; Q4_0 down after row-kernel gate/up, with the activation records it
+ * needs: 41.3 / 41.5 at 6 tokens, 49.6 / 51.6 at 8, 55.8 / 62.1 at 12; Q6_K 41.6 / 32.9 at 2,
+ * 49.4 / 46.2 at 3, 58.2 / 58.2 at 4, 105 / 118 at 8. */
 constexpr int kMxAutoQuarters = 5;
 /* Q6_K gate/up (its MFMA kernel unpacks 6-bit codes): from 2.5 slots per expert (streaming /
  * MFMA us: 442 / 487 at 32 tokens, 618 / 435 at 48) */
 constexpr int kMxAutoQuartersQ6 = 10;
-constexpr int kMxDownMinSlotsQ4 = 72;
+constexpr int kMxDownMinSlotsQ4 = 64;
 constexpr int kMxDownMinSlotsQ6 = 32;
 inline bool mx_auto(int T, int K, int X, int gate_type)
 {

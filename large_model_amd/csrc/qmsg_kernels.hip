@@ -2543,6 +2543,103 @@ __device__ __forceinline__ void mx_chunk(const uint8_t *W, const uint8_t *R, int
     }
 }
 
+/* Q4_0 / Q4_1 lane sums on v_mfma_f32_16x16x16_f16, four slots per instruction. A row i of an
+ * instruction is (slot i / 4 of the quad, reference lane ka = i % 4 + 4h) for half h of the
+ * 32-block (h = 0: the low nibbles, reference lanes 0-3; h = 1: the high nibbles, lanes 4-7);
+ * K group lg of a lane holds reference lane lg + 4h, so A row i is non-zero only in the lane
+ * with lg == i % 4, and every other lane reads the records' zero words at one shared address.
+ * The lane (row lr, K group lg) of the result holds all eight chains of (tile row lr, slot
+ * 4q + lg): the two halves' four values each. One d_w d_x product and one offset-chain step per
+ * (tile, quad, block) serve both halves. */
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+
+template <int TYPE, int NQ, int PAR, bool SC>
+__device__ __forceinline__ void mx_block16(const MxStreams &st, f32x4 (&acc)[2][4], float (&cr)[2][4])
+{
+    static_assert(TYPE == 2 || TYPE == 3, "Q4_0 / Q4_1 rows");
+    constexpr int BB = TYPE == 3 ? 20 : 18, RB = PAR * mx_recl(TYPE), RS = mx_rstride(TYPE);
+    MxB w[2];
+    f16x4 b[2][2];
+#pragma unroll
+    for (int t = 0; t < 2; t++) {
+        w[t] = mx_weights_q4<TYPE, PAR, SC>(st.q + PAR * BB, st.dw + PAR * BB, t);
+        b[t][0] = __builtin_shufflevector(w[t].op, w[t].op, 0, 1, 2, 3);
+        b[t][1] = __builtin_shufflevector(w[t].op, w[t].op, 4, 5, 6, 7);
+    }
+    /* unit u = (quad u / 2, half u % 2); unit u + 1's two MFMAs are issued before unit u's
+     * results are used */
+    f32x4 S[2][2];
+    float xd[NQ], xds[NQ], dd[2];
+    auto issue = [&](int u, int k) {
+        const int q = u >> 1, h = u & 1;
+        const u32x2 av = *(const LdsU32x2 *)((h ? st.ahi : st.alo) + RB + 4 * q * RS);
+        if (h == 0) {
+            if constexpr (SC) {
+                const u32x2 d2 = *(const LdsU32x2 *)(st.d + RB + 4 * q * RS);      /* d 2^24, ds */
+                xd[q] = __uint_as_float(d2.x);
+                xds[q] = __uint_as_float(d2.y);
+            } else {
+                typedef __attribute__((address_space(3))) const float LdsF32;
+                xd[q] = *(LdsF32 *)(st.d + RB + 4 * q * RS + 12);                   /* d */
+                xds[q] = *(LdsF32 *)(st.d + RB + 4 * q * RS + 4);                   /* ds */
+            }
+        }
+        const f16x4 aop = __builtin_bit_cast(f16x4, av);
+#pragma unroll
+        for (int t = 0; t < 2; t++)
+            S[k][t] = __builtin_amdgcn_mfma_f32_16x16x16f16(aop, b[t][h], f32x4{ 0.0f, 0.0f, 0.0f, 0.0f }, 0, 0, 0);
+    };
+    issue(0, 0);
+#pragma unroll
+    for (int u = 0; u < 2 * NQ; u++) {
+        const int k = u & 1, q = u >> 1, h = u & 1;
+        if (u + 1 < 2 * NQ) issue(u + 1, k ^ 1);
+        if (h == 0) {
+#pragma unroll
+            for (int t = 0; t < 2; t++) dd[t] = mix_mul(w[t].dw, xd[q]);
+        }
+#pragma unroll
+        for (int t = 0; t < 2; t++)
+#pragma unroll
+            for (int v = 0; v < 4; v++)
+                acc[t][2 * q + h][v] = __builtin_fmaf(S[k][t][v], dd[t], acc[t][2 * q + h][v]);
+        if (h == 1) {
+#pragma unroll
+            for (int t = 0; t < 2; t++) {
+                if constexpr (TYPE == 3) cr[t][q] = mix_fma_hi(w[t].dw, xds[q], cr[t][q]);   /* off += m*ds */
+                else cr[t][q] = mix_fma_lo(w[t].dw, xds[q], cr[t][q]);                     /* corr += d*ds */
+            }
+        }
+    }
+}
+
+/* One staged chunk on the 16x16x16 instructions, two blocks per loop trip; offa_lo / offa_hi
+ * are the lane's A words of the low and high halves (or the shared zero words). */
+template <int TYPE, int NQ, bool SC>
+__device__ __forceinline__ void mx_chunk16(const uint8_t *W, const uint8_t *R, int lr, int lg, int offa_lo,
+                                           int offa_hi, f32x4 (&acc)[2][4], float (&cr)[2][4])
+{
+    constexpr int WS = mx_wstride(TYPE), BB = TYPE == 3 ? 20 : 18, QO = TYPE == 3 ? 4 : 2;
+    MxStreams st;
+    st.alo = (LdsPtr)(R + offa_lo);
+    st.ahi = (LdsPtr)(R + offa_hi);
+    st.d = (LdsPtr)(R + lg * mx_rstride(TYPE) + kMxDx);
+    st.q = (LdsPtr)(W + lr * WS + QO + 4 * lg);
+    st.dw = (LdsPtr)(W + lr * WS);
+#pragma unroll 1
+    for (int b = 0; b < kMxC; b += 2) {
+        mx_opaque(st);
+        mx_block16<TYPE, NQ, 0, SC>(st, acc, cr);
+        __builtin_amdgcn_sched_barrier(0);      /* one block's operands in registers at a time */
+        mx_block16<TYPE, NQ, 1, SC>(st, acc, cr);
+        st.alo += 2 * mx_recl(TYPE);
+        st.ahi += 2 * mx_recl(TYPE);
+        st.d += 2 * mx_recl(TYPE);
+        st.q += 2 * BB;
+        st.dw += 2 * BB;
+    }
+}
+
 /* A word of a staged Q6_K row at byte off past the row's 4-byte-aligned LDS base (O = 2: the
  * super-block sits 2 bytes in, so the word straddles two aligned words). */
 template <int O>
@@ -2686,6 +2783,11 @@ void mx_kernel(MxArgs a)
     /* Q6_K gate/up stages its gate rows, then its up rows (so the DMA steps through one matrix
      * at a time); the Q4 kernels interleave them by 16-row groups */
     constexpr bool QS6 = GU && TYPE == 14;
+#ifdef QMSG_MX_X32
+    constexpr bool X16Q = false;
+#else
+    constexpr bool X16Q = TYPE != 14;          /* Q4 lane sums on the 16x16x16 instructions */
+#endif
     constexpr int RWG = Lay::RWG, SWG = Lay::SWG, WS = Lay::WS, BUF = Lay::BUF;
     if ((int)blockIdx.y >= a.S.meta[1]) return;
     const int4 tl = a.S.tiles[blockIdx.y];
@@ -2799,6 +2901,11 @@ void mx_kernel(MxArgs a)
     const bool nz = (ka & 3) == lg;
     const int offa_lo = ja * Lay::RS + ((nz && ka < 4) ? 8 * ka : kMxZero);
     const int offa_hi = ja * Lay::RS + ((nz && ka >= 4) ? 8 * ka : kMxZero);
+    /* 16x16x16 instructions: lane row lr is slot lr / 4 of the quad, reference lane lr % 4 (+4 in
+     * the high half); it holds x only if lr % 4 == lg */
+    const bool nz4 = (lr & 3) == lg;
+    const int offq_lo = nz4 ? (lr >> 2) * Lay::RS + 8 * lg : kMxZero;
+    const int offq_hi = nz4 ? (lr >> 2) * Lay::RS + 8 * (lg + 4) : kMxZero;
     const int nw = min(max(ns - 2 * PPW * ws, 0), 2 * PPW), np = (nw + 1) >> 1;   /* this wave's slot pairs */
 
     /* The whole chunk loop and the row sums for one slot-pair count NP, chosen once per wave,
@@ -2806,9 +2913,10 @@ void mx_kernel(MxArgs a)
      * issues its share of the DMA and meets every barrier, whatever its NP (0 included). */
     constexpr float scale = finish_scale(TYPE);
     float *res = (float *)smem;                                   /* [RWG][SWG + 1], after the loop */
-    auto run = [&](auto npc, auto scc) {
+    auto run = [&](auto npc, auto scc, auto x16c) {
         constexpr int NP = decltype(npc)::value;
         constexpr bool SC = decltype(scc)::value;
+        constexpr bool X16 = decltype(x16c)::value;     /* NP / 2 quads on 16x16x16, else NP pairs */
         f32x4 acc[2][4];
         float cr[2][4];
 #pragma unroll
@@ -2837,12 +2945,30 @@ void mx_kernel(MxArgs a)
                     constexpr int TS6 = QS6 ? RWG / 2 : 16;
                     if (c & 1) mx_chunk_q6<NP, 2, TS6>(Wl, Rl, lr, lg, kh, jd, offa_lo, offa_hi, acc, cr);
                     else mx_chunk_q6<NP, 0, TS6>(Wl, Rl, lr, lg, kh, jd, offa_lo, offa_hi, acc, cr);
+                } else if constexpr (X16) {
+                    mx_chunk16<TYPE, NP / 2, SC>(Wl, Rl, lr, lg, offq_lo, offq_hi, acc, cr);
                 } else {
                     mx_chunk<TYPE, NP, SC>(Wl, Rl, lr, lg, jd, kh != 0, offa_lo, offa_hi, acc, cr);
                 }
             }
             /* chunk c+1 has landed; buffer c is free for chunk c+2 (one buffer: it is free) */
             mx_wait_barrier();
+        }
+        if constexpr (X16) {
+            /* hsum256 per (row, slot), all eight chains in the lane: acc[t][2q] lanes 0-3,
+             * acc[t][2q + 1] lanes 4-7 */
+#pragma unroll
+            for (int t = 0; t < 2; t++)
+#pragma unroll
+                for (int q = 0; q < NP / 2; q++) {
+                    const f32x4 &lo = acc[t][2 * q], &hi = acc[t][2 * q + 1];
+                    const float h = ((lo[0] + hi[0]) + (lo[2] + hi[2])) + ((lo[1] + hi[1]) + (lo[3] + hi[3]));
+                    const float val = h - scale * cr[t][q];
+                    const int row = 32 * wr + 16 * t + lr, sl = 2 * PPW * ws + 4 * q + lg;
+                    if (GU) res[row * (SWG + 1) + sl] = val;
+                    else if (sl < ns) a.S.dn[(size_t)(s0 + sl) * a.E + R0 + row] = val;
+                }
+            return;
         }
         /* hsum256 per (row, slot): lanes of k-half 0 take the partner lane's k + 4 chains (Q4
          * types: and, for tile 1, the partner's offset chain) */
@@ -2869,11 +2995,23 @@ void mx_kernel(MxArgs a)
             }
     };
     auto by_pairs = [&](auto scc) {
-        if (PPW == 4 && np == 4) run(std::integral_constant<int, PPW == 4 ? 4 : 0>{}, scc);
-        else if (PPW == 4 && np == 3) run(std::integral_constant<int, PPW == 4 ? 3 : 0>{}, scc);
-        else if (np == 2) run(std::integral_constant<int, 2>{}, scc);
-        else if (np == 1) run(std::integral_constant<int, 1>{}, scc);
-        else run(std::integral_constant<int, 0>{}, scc);
+        using Q = std::integral_constant<bool, X16Q>;
+        using P = std::false_type;
+        if constexpr (X16Q) {
+            /* quads of slots (NP = 2 x quads); a wave of one or two slots keeps the pair
+             * instructions, on which a quad's padding would double its work */
+            const int nq = (nw + 3) >> 2;
+            if (PPW == 4 && nq == 2) run(std::integral_constant<int, PPW == 4 ? 4 : 0>{}, scc, Q{});
+            else if (nw > 2) run(std::integral_constant<int, 2>{}, scc, Q{});
+            else if (nw > 0) run(std::integral_constant<int, 1>{}, scc, P{});
+            else run(std::integral_constant<int, 0>{}, scc, P{});
+        } else {
+            if (PPW == 4 && np == 4) run(std::integral_constant<int, PPW == 4 ? 4 : 0>{}, scc, P{});
+            else if (PPW == 4 && np == 3) run(std::integral_constant<int, PPW == 4 ? 3 : 0>{}, scc, P{});
+            else if (np == 2) run(std::integral_constant<int, 2>{}, scc, P{});
+            else if (np == 1) run(std::integral_constant<int, 1>{}, scc, P{});
+            else run(std::integral_constant<int, 0>{}, scc, P{});
+        }
     };
     /* Q4 types: whether every record this launch reads carries d_x 2^24 (their producers
      * stored this call's epoch in the flag otherwise); both loops are whole, so neither's

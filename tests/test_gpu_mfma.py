@@ -2,7 +2,7 @@
 GPU: every intermediate bit for bit against the oracle, like the exact path.
 
 The MFMA kernels run for QMSG_PATH_MFMA at any batch of two or more tokens; the default path
-takes them for gate/up from 1.25 slots per active expert and for down from 72 slots (Q6_K
+takes them for gate/up from 1.25 slots per active expert and for down from 64 slots (Q6_K
 down rows: 32), so the 16-token and the 8-token Q6_K cases also run the row-kernel gate/up
 followed by the MFMA down.
 The block shapes (4-, 8- and 16-slot blocks, chosen per kernel by slots per expert) are all
