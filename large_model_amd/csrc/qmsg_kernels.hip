@@ -2553,16 +2553,17 @@ __device__ __forceinline__ void mx_chunk(const uint8_t *W, const uint8_t *R, int
  * (tile, quad, block) serve both halves. */
 typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 
-template <int TYPE, int NQ, int PAR, bool SC>
+template <int TYPE, int NQ, int BI, bool SC>
 __device__ __forceinline__ void mx_block16(const MxStreams &st, f32x4 (&acc)[2][4], float (&cr)[2][4])
 {
     static_assert(TYPE == 2 || TYPE == 3, "Q4_0 / Q4_1 rows");
-    constexpr int BB = TYPE == 3 ? 20 : 18, RB = PAR * mx_recl(TYPE), RS = mx_rstride(TYPE);
+    /* block BI of the staged chunk: every stream offset an immediate */
+    constexpr int BB = TYPE == 3 ? 20 : 18, RB = BI * mx_recl(TYPE), RS = mx_rstride(TYPE), PAR = BI & 1;
     MxB w[2];
     f16x4 b[2][2];
 #pragma unroll
     for (int t = 0; t < 2; t++) {
-        w[t] = mx_weights_q4<TYPE, PAR, SC>(st.q + PAR * BB, st.dw + PAR * BB, t);
+        w[t] = mx_weights_q4<TYPE, PAR, SC>(st.q + BI * BB, st.dw + BI * BB, t);
         b[t][0] = __builtin_shufflevector(w[t].op, w[t].op, 0, 1, 2, 3);
         b[t][1] = __builtin_shufflevector(w[t].op, w[t].op, 4, 5, 6, 7);
     }
@@ -2613,31 +2614,37 @@ __device__ __forceinline__ void mx_block16(const MxStreams &st, f32x4 (&acc)[2][
     }
 }
 
-/* One staged chunk on the 16x16x16 instructions, two blocks per loop trip; offa_lo / offa_hi
- * are the lane's A words of the low and high halves (or the shared zero words). */
+/* One staged chunk on the 16x16x16 instructions, its 8 blocks unrolled; offa_lo / offa_hi are
+ * the lane's A words of the low and high halves (or the shared zero words). */
 template <int TYPE, int NQ, bool SC>
 __device__ __forceinline__ void mx_chunk16(const uint8_t *W, const uint8_t *R, int lr, int lg, int offa_lo,
                                            int offa_hi, f32x4 (&acc)[2][4], float (&cr)[2][4])
 {
-    constexpr int WS = mx_wstride(TYPE), BB = TYPE == 3 ? 20 : 18, QO = TYPE == 3 ? 4 : 2;
+    static_assert(kMxC == 8, "eight blocks per staged chunk");
+    constexpr int WS = mx_wstride(TYPE), QO = TYPE == 3 ? 4 : 2;
     MxStreams st;
     st.alo = (LdsPtr)(R + offa_lo);
     st.ahi = (LdsPtr)(R + offa_hi);
     st.d = (LdsPtr)(R + lg * mx_rstride(TYPE) + kMxDx);
     st.q = (LdsPtr)(W + lr * WS + QO + 4 * lg);
     st.dw = (LdsPtr)(W + lr * WS);
-#pragma unroll 1
-    for (int b = 0; b < kMxC; b += 2) {
-        mx_opaque(st);
-        mx_block16<TYPE, NQ, 0, SC>(st, acc, cr);
-        __builtin_amdgcn_sched_barrier(0);      /* one block's operands in registers at a time */
-        mx_block16<TYPE, NQ, 1, SC>(st, acc, cr);
-        st.alo += 2 * mx_recl(TYPE);
-        st.ahi += 2 * mx_recl(TYPE);
-        st.d += 2 * mx_recl(TYPE);
-        st.q += 2 * BB;
-        st.dw += 2 * BB;
-    }
+    mx_opaque(st);
+    /* one block's operands in registers at a time */
+    mx_block16<TYPE, NQ, 0, SC>(st, acc, cr);
+    __builtin_amdgcn_sched_barrier(0);
+    mx_block16<TYPE, NQ, 1, SC>(st, acc, cr);
+    __builtin_amdgcn_sched_barrier(0);
+    mx_block16<TYPE, NQ, 2, SC>(st, acc, cr);
+    __builtin_amdgcn_sched_barrier(0);
+    mx_block16<TYPE, NQ, 3, SC>(st, acc, cr);
+    __builtin_amdgcn_sched_barrier(0);
+    mx_block16<TYPE, NQ, 4, SC>(st, acc, cr);
+    __builtin_amdgcn_sched_barrier(0);
+    mx_block16<TYPE, NQ, 5, SC>(st, acc, cr);
+    __builtin_amdgcn_sched_barrier(0);
+    mx_block16<TYPE, NQ, 6, SC>(st, acc, cr);
+    __builtin_amdgcn_sched_barrier(0);
+    mx_block16<TYPE, NQ, 7, SC>(st, acc, cr);
 }
 
 /* A word of a staged Q6_K row at byte off past the row's 4-byte-aligned LDS base (O = 2: the
