@@ -75,8 +75,8 @@ typedef struct qmsg_ctx qmsg_ctx;
  * blocks, the per-block int32 dots and the fp32 rows follow the reference's AVX path exactly.
  *   EXACT: per-row VALU kernels (integer dot4 lane sums, the reference's fp32 lane chains).
  *   MFMA:  the lane sums on f16 MFMAs (exact small integers: 16 rows x 4 slots x half a
- *          block per instruction for Q4_0 / Q4_1 rows, 16 rows x 2 slots for Q6_K rows and
- *          waves of one or two slots), the same fp32 chains on the VALU; for batches of two or
+ *          block per instruction, 16 rows x 2 slots x a block for waves of one or two
+ *          slots), the same fp32 chains on the VALU; for batches of two or
  *          more tokens with gate and up of one type (down Q4_0, Q4_1 or Q6_K; other down rows
  *          on the EXACT kernel).
  *   AUTO:  per stage: Q4_0 / Q4_1 gate/up on MFMA for batches averaging at least 1.25 slots

@@ -2751,6 +2751,96 @@ __device__ __forceinline__ void mx_chunk_q6(const uint8_t *W, const uint8_t *R, 
     mx_block_q6<NP, O, 7, TS>(st, kh, acc, cr);
 }
 
+/* One Q6_K block B of the staged chunk on the 16x16x16 instructions (the layout of mx_block16):
+ * half h of the 32-block is sub-block 2g + h, so each instruction's lane sums share one
+ * sub-scale per row; one d_w d_x product and one half-sum offset step per (tile, quad, block). */
+template <int NQ, int O, int B, int TS>
+__device__ __forceinline__ void mx_block16_q6(const MxStreams &st, f32x4 (&acc)[2][4], float (&cr)[2][4])
+{
+    constexpr int RS = mx_rstride(14), RB = B * mx_recl(14);
+    MxB w[2];
+    f16x4 b[2][2];
+    float sc[2][2];
+#pragma unroll
+    for (int t = 0; t < 2; t++) {
+        w[t] = mx_weights_q6<O, B, TS>(st.q, st.dw, t, 0);
+        b[t][0] = __builtin_shufflevector(w[t].op, w[t].op, 0, 1, 2, 3);
+        b[t][1] = __builtin_shufflevector(w[t].op, w[t].op, 4, 5, 6, 7);
+        sc[t][0] = w[t].sc;                                              /* sc[2g] 2^24 */
+        sc[t][1] = (float)(((int)w[t].sab >> 16) * 16777216);           /* sc[2g+1] 2^24, exact */
+    }
+    f32x4 S[2][2];
+    float xd[NQ], dd[2];
+    uint32_t s16p[NQ];
+    auto issue = [&](int u, int k) {
+        const int q = u >> 1, h = u & 1;
+        const u32x2 av = *(const LdsU32x2 *)((h ? st.ahi : st.alo) + RB + 4 * q * RS);
+        if (h == 0) {
+            const u32x4 dx = *(const LdsU32x4 *)(st.d + RB + 4 * q * RS);    /* -, ds, s16 pair, d */
+            xd[q] = __uint_as_float(dx.w);
+            s16p[q] = dx.z;
+        }
+        const f16x4 aop = __builtin_bit_cast(f16x4, av);
+#pragma unroll
+        for (int t = 0; t < 2; t++)
+            S[k][t] = __builtin_amdgcn_mfma_f32_16x16x16f16(aop, b[t][h], f32x4{ 0.0f, 0.0f, 0.0f, 0.0f }, 0, 0, 0);
+    };
+    issue(0, 0);
+#pragma unroll
+    for (int u = 0; u < 2 * NQ; u++) {
+        const int k = u & 1, q = u >> 1, h = u & 1;
+        if (u + 1 < 2 * NQ) issue(u + 1, k ^ 1);
+        if (h == 0) {
+#pragma unroll
+            for (int t = 0; t < 2; t++) dd[t] = mix_mul(w[t].dw, xd[q]);
+        }
+#pragma unroll
+        for (int t = 0; t < 2; t++)
+#pragma unroll
+            for (int v = 0; v < 4; v++)
+                acc[t][2 * q + h][v] = __builtin_fmaf(S[k][t][v] * sc[t][h], dd[t], acc[t][2 * q + h][v]);
+        if (h == 1) {
+#pragma unroll
+            for (int t = 0; t < 2; t++) {
+                /* sc[2g]*s16[0] + sc[2g+1]*s16[1] in one packed int16 dot */
+                const int ssum = __builtin_amdgcn_sdot2(__builtin_bit_cast(short2_t, w[t].sab),
+                                                        __builtin_bit_cast(short2_t, s16p[q]), 0, false);
+                cr[t][q] = __builtin_fmaf(dd[t], (float)ssum, cr[t][q]);
+            }
+        }
+    }
+}
+
+/* A staged Q6_K super-block on the 16x16x16 instructions, its 8 blocks unrolled. */
+template <int NQ, int O, int TS>
+__device__ __forceinline__ void mx_chunk16_q6(const uint8_t *W, const uint8_t *R, int lr, int lg, int offa_lo,
+                                              int offa_hi, f32x4 (&acc)[2][4], float (&cr)[2][4])
+{
+    constexpr int WS = mx_wstride(14);
+    MxStreams st;
+    st.alo = (LdsPtr)(R + offa_lo);
+    st.ahi = (LdsPtr)(R + offa_hi);
+    st.d = (LdsPtr)(R + lg * mx_rstride(14) + kMxDx);
+    st.q = (LdsPtr)(W + lr * WS + 4 * lg);
+    st.dw = (LdsPtr)(W + lr * WS);
+    mx_opaque(st);
+    mx_block16_q6<NQ, O, 0, TS>(st, acc, cr);
+    __builtin_amdgcn_sched_barrier(0);
+    mx_block16_q6<NQ, O, 1, TS>(st, acc, cr);
+    __builtin_amdgcn_sched_barrier(0);
+    mx_block16_q6<NQ, O, 2, TS>(st, acc, cr);
+    __builtin_amdgcn_sched_barrier(0);
+    mx_block16_q6<NQ, O, 3, TS>(st, acc, cr);
+    __builtin_amdgcn_sched_barrier(0);
+    mx_block16_q6<NQ, O, 4, TS>(st, acc, cr);
+    __builtin_amdgcn_sched_barrier(0);
+    mx_block16_q6<NQ, O, 5, TS>(st, acc, cr);
+    __builtin_amdgcn_sched_barrier(0);
+    mx_block16_q6<NQ, O, 6, TS>(st, acc, cr);
+    __builtin_amdgcn_sched_barrier(0);
+    mx_block16_q6<NQ, O, 7, TS>(st, acc, cr);
+}
+
 /* The LDS DMA: `bytes` (4 or 16) from src of every active lane to dst + lane * bytes. */
 template <int BYTES>
 __device__ __forceinline__ void dma_to_lds(const void *src, uint8_t *dst)
@@ -2792,8 +2882,10 @@ void mx_kernel(MxArgs a)
     constexpr bool QS6 = GU && TYPE == 14;
 #ifdef QMSG_MX_X32
     constexpr bool X16Q = false;
+#elif defined(QMSG_MX_Q6_PAIRS)
+    constexpr bool X16Q = TYPE != 14;
 #else
-    constexpr bool X16Q = TYPE != 14;          /* Q4 lane sums on the 16x16x16 instructions */
+    constexpr bool X16Q = true;                /* lane sums on the 16x16x16 instructions (waves of 3+ slots) */
 #endif
     constexpr int RWG = Lay::RWG, SWG = Lay::SWG, WS = Lay::WS, BUF = Lay::BUF;
     if ((int)blockIdx.y >= a.S.meta[1]) return;
@@ -2948,7 +3040,11 @@ void mx_kernel(MxArgs a)
             if constexpr (NP > 0) {
                 const uint8_t *Wl = smem + buf * BUF + ((QS6 ? 16 : 32) * wr) * WS;
                 const uint8_t *Rl = smem + buf * BUF + Lay::WBYTES + (2 * PPW * ws) * Lay::RS;
-                if constexpr (TYPE == 14) {
+                if constexpr (TYPE == 14 && X16) {
+                    constexpr int TS6 = QS6 ? RWG / 2 : 16;
+                    if (c & 1) mx_chunk16_q6<NP / 2, 2, TS6>(Wl, Rl, lr, lg, offq_lo, offq_hi, acc, cr);
+                    else mx_chunk16_q6<NP / 2, 0, TS6>(Wl, Rl, lr, lg, offq_lo, offq_hi, acc, cr);
+                } else if constexpr (TYPE == 14) {
                     constexpr int TS6 = QS6 ? RWG / 2 : 16;
                     if (c & 1) mx_chunk_q6<NP, 2, TS6>(Wl, Rl, lr, lg, kh, jd, offa_lo, offa_hi, acc, cr);
                     else mx_chunk_q6<NP, 0, TS6>(Wl, Rl, lr, lg, kh, jd, offa_lo, offa_hi, acc, cr);
