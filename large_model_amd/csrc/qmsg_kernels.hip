@@ -2058,17 +2058,33 @@ __global__ void act_quant_kernel(Scratch S, int F, int NS, uint8_t *mxrec, int h
 }
 
 /* Weighted sum per token in selection order (src/model.c:1152-1162) when dn did not fit. */
+/* Threads per combine block: 4 x threads divides n_embd (a multiple of 256), so a block never
+ * straddles two tokens. */
+static inline int combine_threads(int E) { return (E / 4) % 256 == 0 ? 256 : ((E / 4) % 128 == 0 ? 128 : 64); }
+
 __global__ void combine_kernel(const Scratch S, int E, int K, int T, float *out)
 {
-    const int i = blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= T * E) return;
-    /* n_embd is a multiple of the block size: the token is block-uniform, so its weights
-     * and slots are scalar loads */
-    const int t = (int)(blockIdx.x * blockDim.x) / E, r = i - t * E;
-    float o = 0.0f;
-    for (int j = 0; j < K; j++)
-        o = __builtin_fmaf(S.wt[(size_t)t * K + j], S.dn[(size_t)S.slot_of[(size_t)t * K + j] * E + r], o);
-    out[i] = o;
+    /* four output elements per thread, 16-byte reads of the dn rows; n_embd is a multiple of
+     * 4 x the block size (combine_threads), so the token is block-uniform and its weights and
+     * slots are scalar loads. Each element's sum runs over j in order (src/model.c:1152-1162). */
+    const int i4 = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i4 * 4 >= T * E) return;
+    const int t = (int)(blockIdx.x * blockDim.x * 4) / E, r = 4 * i4 - t * E;
+    float4 o = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    for (int j = 0; j < K; j++) {
+        const float w = S.wt[(size_t)t * K + j];
+        const float4 d = *(const float4 *)(S.dn + (size_t)S.slot_of[(size_t)t * K + j] * E + r);
+        o.x = __builtin_fmaf(w, d.x, o.x);
+        o.y = __builtin_fmaf(w, d.y, o.y);
+        o.z = __builtin_fmaf(w, d.z, o.z);
+        o.w = __builtin_fmaf(w, d.w, o.w);
+    }
+    /* out need only be 4-byte aligned */
+    float *dst = out + 4 * (size_t)i4;
+    dst[0] = o.x;
+    dst[1] = o.y;
+    dst[2] = o.z;
+    dst[3] = o.w;
 }
 
 template <int TYPE, int RT, int QA>
@@ -2164,7 +2180,7 @@ hipError_t launch_down_exact(const Shape &s, const LayerDev &L, const Scratch &S
         else launch_down_tile<14, kDownTileRowsQ6K, 0>(ta, NT, grid, lds, st);
     }
     const int n = T * s.E;
-    QLAUNCH("combine", combine_kernel, dim3((n + 255) / 256), dim3(256), 0, st, S, s.E, s.K, T, out);
+    QLAUNCH("combine", combine_kernel, dim3(n / (4 * combine_threads(s.E))), dim3(combine_threads(s.E)), 0, st, S, s.E, s.K, T, out);
     return hipGetLastError();
 }
 
@@ -3271,7 +3287,7 @@ hipError_t launch_experts_mx(const Shape &s, const LayerDev &L, const Scratch &S
     else if (L.down_type == 3) launch_mx<3, 0>(a, s.E, maxt, mx_shape(s, T, 0, 3), st);
     else launch_mx<2, 0>(a, s.E, maxt, mx_shape(s, T, 0, 2), st);
     const int n = T * s.E;
-    QLAUNCH("combine", combine_kernel, dim3((n + 255) / 256), dim3(256), 0, st, S, s.E, s.K, T, out);
+    QLAUNCH("combine", combine_kernel, dim3(n / (4 * combine_threads(s.E))), dim3(combine_threads(s.E)), 0, st, S, s.E, s.K, T, out);
     return hipGetLastError();
 }
 
@@ -3302,7 +3318,7 @@ hipError_t launch_down_mx(const Shape &s, const LayerDev &L, const Scratch &S, f
     else if (L.down_type == 3) launch_mx<3, 0>(a, s.E, maxt, mx_shape(s, T, 0, 3), st);
     else launch_mx<2, 0>(a, s.E, maxt, mx_shape(s, T, 0, 2), st);
     const int n = T * s.E;
-    QLAUNCH("combine", combine_kernel, dim3((n + 255) / 256), dim3(256), 0, st, S, s.E, s.K, T, out);
+    QLAUNCH("combine", combine_kernel, dim3(n / (4 * combine_threads(s.E))), dim3(combine_threads(s.E)), 0, st, S, s.E, s.K, T, out);
     return hipGetLastError();
 }
 
@@ -4121,7 +4137,7 @@ hipError_t launch_layer_fp32(const Shape &s, const LayerDev &L, const Scratch &S
         QLAUNCH(i == 2 ? "down" : "gateup", exact_rows_kernel, dim3((m[i].rows + 63) / 64, maxact), dim3(64), lds, st, a);
     }
     const int n = T * s.E;
-    QLAUNCH("combine", combine_kernel, dim3((n + 255) / 256), dim3(256), 0, st, S, s.E, s.K, T, out);
+    QLAUNCH("combine", combine_kernel, dim3(n / (4 * combine_threads(s.E))), dim3(combine_threads(s.E)), 0, st, S, s.E, s.K, T, out);
     return hipGetLastError();
 }
 
