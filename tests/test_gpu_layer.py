@@ -20,6 +20,7 @@ CASES = [
     ("q235b_t4", 4096, 128, 8, 1536, 4, 2, orc.T_Q4_0, False),
     ("q235b_t16", 4096, 128, 8, 1536, 16, 2, orc.T_Q4_0, False),
     ("q235b_t8", 4096, 128, 8, 1536, 8, 32, orc.T_Q4_0, False),     # 64 slots: the default path's MFMA down
+    ("e768_t9", 768, 32, 4, 256, 9, 33, orc.T_Q4_0, False),         # combine: three 64-thread blocks per token
     ("q30b_q6k_t5", 2048, 128, 8, 768, 5, 3, orc.T_Q6_K, False),
     ("q235b_q6k_t3", 4096, 128, 8, 1536, 3, 4, orc.T_Q6_K, False),
     ("q235b_q6k_t2", 4096, 128, 8, 1536, 2, 31, orc.T_Q6_K, True),   # small-batch down kernel, Q6_K rows
