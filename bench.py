@@ -56,6 +56,19 @@ from large_model_amd import qmsg  # noqa: E402
 from large_model_amd.workloads import HBM_PEAK_GBS, INT8_PEAK_TOPS, WORKLOADS, zipf_bias  # noqa: E402
 
 METRIC = "MoE-layer tokens/s + achieved HBM GB/s (decode), int8 MFMA util (prefill), 1 GPU"
+# every launch name the library's per-dispatch events report (QLAUNCH names in csrc)
+KERNEL_NAMES = ("fill", "rmsnorm", "route", "select", "dispatch", "mxin", "layer", "gateup", "swiglu", "actq",
+                "down", "combine", "add", "dquant", "dense")
+
+
+def kernel_times(ctx):
+    """Launch count and average duration per kernel name from the per-dispatch events."""
+    kern = {}
+    for name in KERNEL_NAMES:
+        n, ms = ctx.profile_read(name)
+        if n:
+            kern[name] = {"launches": n, "avg_us": round(1e3 * ms / n, 3)}
+    return kern
 
 
 def log(msg: str):
@@ -218,11 +231,7 @@ def run_stack(args, w):
     for s in range(W_steps):                      # the warmup inputs again (unchanged by timing)
         step(s)
     ctx.sync()
-    kern = {}
-    for name in ("rmsnorm", "route", "select", "dispatch", "gateup", "actq", "down", "combine", "add"):
-        n, ms = ctx.profile_read(name)
-        if n:
-            kern[name] = {"launches": n, "avg_us": round(1e3 * ms / n, 3)}
+    kern = kernel_times(ctx)
     ctx.profile(False)
     # distinct experts of the first layer on a fresh input (the routing is near uniform)
     x = ctx.d2h(d_h + W_steps * row, (w.T, w.E))
@@ -310,11 +319,7 @@ def extra_prefill(steps: int = 10, warmup: int = 2, NL: int = 4):
     for s in range(warmup, total):
         ctx.moe_device(s % NL, d_x + s * row, w.T, d_out + s * row)
     ctx.sync()
-    kern = {}
-    for name in ("route", "select", "dispatch", "mxin", "gateup", "actq", "down", "combine"):
-        n, kms = ctx.profile_read(name)
-        if n:
-            kern[name] = {"launches": n, "avg_us": round(1e3 * kms / n, 3)}
+    kern = kernel_times(ctx)
     ctx.profile(False)
     x = ctx.d2h(d_x + warmup * row, (w.T, w.E))
     _, dbg = ctx.moe_debug(warmup % NL, x)
@@ -354,6 +359,8 @@ def extra_stack_layer(steps: int = 4, warmup: int = 1, NL: int = 8):
         for s in range(total):
             ctx.synth_input(w.seed + 7 + s, 0, T, d_h + s * row)
         ctx.sync()
+        # the first timed step's input as generated: the chain overwrites it in place
+        x0 = ctx.d2h(d_h + warmup * row, (T, w.E))
         for s in range(warmup):
             ctx.moe_chain(0, NL, d_h + s * row, T)
         ctx.sync()
@@ -366,25 +373,71 @@ def extra_stack_layer(steps: int = 4, warmup: int = 1, NL: int = 8):
         ctx.profile(True)
         ctx.moe_chain(0, NL, d_h, T)
         ctx.sync()
-        kern = {}
-        for name in ("rmsnorm", "route", "select", "dispatch", "gateup", "actq", "down", "combine", "add"):
-            n, kms = ctx.profile_read(name)
-            if n:
-                kern[name] = {"launches": n, "avg_us": round(1e3 * kms / n, 3)}
+        kern = kernel_times(ctx)
         ctx.profile(False)
-        x = ctx.d2h(d_h + warmup * row, (T, w.E))
-        _, dbg = ctx.moe_debug(0, orc.rmsnorm(x))
+        # distinct experts of layer 0 on that untouched input (the byte count assumes every
+        # layer touches as many; at T = 64 nearly all 128 are, at T = 1 exactly K)
+        _, dbg = ctx.moe_debug(0, orc.rmsnorm(x0))
         d_active = len(dbg["active"])
         nbytes = 4 * w.X * w.E + d_active * w.expert_bytes + 8 * T * w.E
         out[f"t{T}"] = {
             "us_per_layer": round(us_layer, 2), "projected_94_layer_ms": round(us_layer * w.layers / 1e3, 3),
             "tokens_per_s_94_layers": round(T / (us_layer * w.layers * 1e-6), 2),
-            "distinct_experts_per_layer": d_active, "algorithmic_bytes_per_layer": nbytes,
+            "distinct_experts_per_layer": d_active, "distinct_experts_source": "layer 0 on the first timed input",
+            "algorithmic_bytes_per_layer": nbytes,
             "achieved_GBps": round(nbytes / (us_layer * 1e-6) / 1e9, 1),
             "frac_of_hbm_peak": round(nbytes / (us_layer * 1e-6) / 1e9 / HBM_PEAK_GBS, 4), "kernels": kern,
         }
     ctx.close()
     return out
+
+
+def extra_decode(name: str, steps: int = 200, warmup: int = 20, NL: int = 16):
+    """A decode configuration beside the headline, bounded to a second or two: us per layer,
+    tokens/s, distinct experts, the layer's algorithmic bytes against the HBM peak and per-kernel
+    times. Cycles NL resident layers, different tokens per step, as the headline does."""
+    w = WORKLOADS[name]
+    ctx = qmsg.Context(w.E, w.X, w.K, w.F, n_layer=NL, max_tokens=w.T)
+    for l in range(NL):
+        ctx.synth(l, w.seed + 1000 * l, down_type=w.down_type)
+    row = w.T * w.E * 4
+    total = steps + warmup
+    d_x = ctx.device_alloc(total * row)
+    d_out = ctx.device_alloc(total * row)
+    for s in range(total):
+        ctx.synth_input(w.seed + 7 + s, 0, w.T, d_x + s * row, rmsnorm=w.rmsnorm)
+    ctx.sync()
+    for s in range(warmup):
+        ctx.moe_device(s % NL, d_x + s * row, w.T, d_out + s * row)
+    ctx.sync()
+    t0 = time.perf_counter()
+    for s in range(warmup, total):
+        ctx.moe_device(s % NL, d_x + s * row, w.T, d_out + s * row)
+    ctx.sync()
+    el = time.perf_counter() - t0
+    us = 1e6 * el / steps
+    ctx.profile(True)
+    for s in range(warmup, total):
+        ctx.moe_device(s % NL, d_x + s * row, w.T, d_out + s * row)
+    ctx.sync()
+    kern = kernel_times(ctx)
+    ctx.profile(False)
+    ds = []
+    for s in range(min(8, steps)):
+        x = ctx.d2h(d_x + (warmup + s) * row, (w.T, w.E))
+        _, dbg = ctx.moe_debug((warmup + s) % NL, x)
+        ds.append(len(dbg["active"]))
+    ctx.close()
+    d_active = float(np.mean(ds))
+    nbytes = w.layer_bytes(0) + d_active * w.expert_bytes
+    return {
+        "workload": f"{w.name}: {w.note}, {NL} resident layers cycled, {steps} timed steps",
+        "n_embd": w.E, "n_expert": w.X, "n_used": w.K, "n_ff_exp": w.F, "tokens_per_step": w.T,
+        "us_per_layer": round(us, 3), "tokens_per_s": round(w.T / (us * 1e-6), 1),
+        "distinct_experts": d_active, "algorithmic_bytes": int(nbytes),
+        "achieved_GBps": round(nbytes / (us * 1e-6) / 1e9, 1),
+        "frac_of_hbm_peak": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4), "kernels": kern,
+    }
 
 
 TRUNK_TYPES = {"f32": qmsg.QMSG_T_F32, "q4_0": qmsg.QMSG_T_Q4_0, "q4_1": qmsg.QMSG_T_Q4_1, "q6_k": qmsg.QMSG_T_Q6_K}
@@ -429,11 +482,7 @@ def run_trunk(args):
     ctx.profile(True)
     step()
     ctx.sync()
-    kern = {}
-    for name in ("dquant", "dense"):
-        n, ms = ctx.profile_read(name)
-        if n:
-            kern[name] = {"launches": n, "avg_us": round(1e3 * ms / n, 3)}
+    kern = kernel_times(ctx)
     ctx.profile(False)
     rb = qmsg.row_bytes(TT, E)
     layer_bytes = (H + 2 * KV) * rb + E * qmsg.row_bytes(TT, H)
@@ -642,11 +691,7 @@ def main():
         step(s)
     ctx.sync()
     log(f"with per-dispatch events: {1e6 * (time.perf_counter() - t0) / K_steps:.2f} us/step")
-    kern = {}
-    for name in ("route", "select", "dispatch", "mxin", "gateup", "actq", "down", "combine"):
-        n, ms = ctx.profile_read(name)
-        if n:
-            kern[name] = {"launches": n, "avg_us": round(1e3 * ms / n, 3)}
+    kern = kernel_times(ctx)
     ctx.profile(False)
 
     # distinct experts per call (8 at T=1); sampled through the debug entry for larger T
@@ -710,6 +755,10 @@ def main():
         result["cpu_baseline"] = cpu_baseline(ctx, w, args.cpu_seconds)
     ctx.close()
     if w.name == "q235b_decode_t1" and not args.no_extras:
+        for key, name in (("tiny_t1", "tiny"), ("q30b_decode_t1", "q30b_decode_t1"),
+                          ("q235b_decode_t4", "q235b_decode_t4"), ("q235b_decode_t16", "q235b_decode_t16")):
+            log(f"decode extra: {name}")
+            result[key] = extra_decode(name)
         log("prefill extra: 512-token Zipf prefill")
         result["prefill_t512"] = extra_prefill()
         log("stack extra: per-layer figure of the 94-layer stack shape")

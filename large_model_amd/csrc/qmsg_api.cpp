@@ -93,7 +93,6 @@ __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
 
 std::mutex g_noalloc_mu;
 void *g_noalloc_ptr[kMaxDevices];
-hipError_t g_noalloc_err[kMaxDevices];
 
 /* The device's address of `scratch`; the calling thread has `device` current. */
 hipError_t noalloc_scratch_setup(int device)
@@ -103,7 +102,6 @@ hipError_t noalloc_scratch_setup(int device)
     if (g_noalloc_ptr[device]) return hipSuccess;
     void *ptr = nullptr;
     const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
-    g_noalloc_err[device] = e;
     if (e == hipSuccess) g_noalloc_ptr[device] = ptr;
     return e;
 }
@@ -235,10 +233,10 @@ int qmsg_create(qmsg_ctx **out, int device, const qmsg_cfg *cfg, int n_layer, in
         delete c;
         return QMSG_E_DEVICE;
     }
-    if (noalloc_scratch_setup(device) != hipSuccess) {
-        fail(nullptr, QMSG_E_DEVICE, "qmsg_create: static scratch of device %d: %s", device,
-             hipGetErrorString(g_noalloc_err[device]));
-        delete c;
+    e = noalloc_scratch_setup(device);
+    if (e != hipSuccess) {
+        fail(nullptr, QMSG_E_DEVICE, "qmsg_create: static scratch of device %d: %s", device, hipGetErrorString(e));
+        qmsg_destroy(c);    /* releases the stream */
         return QMSG_E_DEVICE;
     }
     std::vector<ScratchItem> items = scratch_items(*cfg, (size_t)max_tokens, &c->S);
@@ -848,9 +846,9 @@ int qmsg_moe_device_noalloc(qmsg_ctx *c, int layer, const float *d_xn, int T, fl
                     need, kNoAllocScratchBytes);
     if (T == 0) return run_layer_s(c, S, layer, d_xn, T, d_out, 0);
     HIP_TRY(c, hipSetDevice(c->device));
-    /* the select kernel's ticket counter (meta[4]) must start at zero; a fill kernel rather
-     * than a memset node, so the call can be captured into a graph */
-    LAUNCH(c, "fill", launch_fill_u32((uint32_t *)S.meta, 0u, 16, c->stream));
+    /* the select kernel's ticket counter (meta[4]) must start at zero, and the record-range
+     * flags are cleared so a replay of a captured call does not inherit an earlier replay's */
+    LAUNCH(c, "fill", launch_call_reset(S, c->stream));
     return run_layer_s(c, S, layer, d_xn, T, d_out, 0);
 }
 

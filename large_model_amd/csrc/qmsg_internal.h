@@ -181,7 +181,7 @@ hipError_t launch_silu(const float *x, int n, float *out, hipStream_t st);
 hipError_t launch_exp(const double *x, int n, double *out, hipStream_t st);
 hipError_t launch_copy(void *dst, const void *src, size_t bytes, hipStream_t st);
 /* p[0 .. n-1] = v (a kernel, not a memset node: safe inside a captured graph). */
-hipError_t launch_fill_u32(uint32_t *p, uint32_t v, size_t n, hipStream_t st);
+hipError_t launch_call_reset(const Scratch &S, hipStream_t st);
 /* The dense rows kernel; for T >= kDenseQuantT the input records are formed first into xqk
  * (T*C/64 records of 96 bytes). */
 hipError_t launch_dense(const DenseArgs &a, int type, uint8_t *xqk, hipStream_t st);

@@ -4242,16 +4242,19 @@ hipError_t launch_copy(void *dst, const void *src, size_t bytes, hipStream_t st)
     return hipGetLastError();
 }
 
-__global__ void fill_u32_kernel(uint32_t *p, uint32_t v, size_t n)
+/* Clears the per-call state of a scratch set: the 16 meta words (the select kernel's ticket
+ * counter among them) and the two record-range flags, whose epoch would otherwise stay set
+ * across replays of a captured call. A kernel rather than a memset node, so the call can be
+ * captured into a graph. */
+__global__ void call_reset_kernel(uint32_t *meta, uint64_t *mxflag)
 {
-    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
-        p[i] = v;
+    if (threadIdx.x < 16) meta[threadIdx.x] = 0u;
+    if (threadIdx.x < 2) mxflag[threadIdx.x] = 0ull;
 }
 
-hipError_t launch_fill_u32(uint32_t *p, uint32_t v, size_t n, hipStream_t st)
+hipError_t launch_call_reset(const Scratch &S, hipStream_t st)
 {
-    const size_t blocks = n / 256 + 1;
-    QLAUNCH("fill", fill_u32_kernel, dim3(blocks < 1024 ? (unsigned)blocks : 1024u), dim3(256), 0, st, p, v, n);
+    QLAUNCH("fill", call_reset_kernel, dim3(1), dim3(64), 0, st, (uint32_t *)S.meta, S.mxflag);
     return hipGetLastError();
 }
 
@@ -4604,7 +4607,7 @@ hipError_t launch_rmsnorm(float *x, const float *add, const float *w, float *y, 
     if (E % 4) return hipErrorInvalidValue;
     static_assert(kSumPitch == 65, "rmsnorm_lds_bytes assumes the pitch");
     if (rmsnorm_lds_bytes(E) > 160 * 1024) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(rmsnorm_kernel, dim3(T), dim3(256), rmsnorm_lds_bytes(E), st, x, add, w, y, E, eps);
+    QLAUNCH("rmsnorm", rmsnorm_kernel, dim3(T), dim3(256), rmsnorm_lds_bytes(E), st, x, add, w, y, E, eps);
     return hipGetLastError();
 }
 
@@ -4624,8 +4627,8 @@ hipError_t launch_add_rows(float *h, const float *d, size_t n, hipStream_t st)
 {
     if (n % 4) return hipErrorInvalidValue;
     const size_t n4 = n / 4;
-    if (n4) hipLaunchKernelGGL(add_rows_kernel, dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0, st, (float4 *)h,
-                               (const float4 *)d, n4);
+    if (n4) QLAUNCH("add", add_rows_kernel, dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0, st, (float4 *)h,
+                    (const float4 *)d, n4);
     return hipGetLastError();
 }
 

@@ -437,19 +437,24 @@ class Context:
         """d_y = rmsnorm(d_x, d_w) row by row on device buffers (d_w None: unit weights)."""
         self._check(lib.qmsg_rmsnorm_device(self._h, d_y, d_x, d_w, rows, n, eps))
 
-    def rmsnorm(self, x: np.ndarray, w: Optional[np.ndarray] = None, eps: float = 1e-6) -> np.ndarray:
-        """rmsnorm of host rows x [rows][n] on the device (src/model.c:403-409); returns y."""
+    def rmsnorm(self, x: np.ndarray, w: Optional[np.ndarray] = None, eps: float = 1e-6,
+                inplace: bool = True) -> np.ndarray:
+        """rmsnorm of host rows x [rows][n] on the device (src/model.c:403-409); returns y.
+        inplace=False writes y to a buffer of its own and checks that x is left as it was."""
         x = np.ascontiguousarray(x, np.float32)
         rows, n = x.shape
         d_x = self.device_alloc(max(x.nbytes, 16))
+        d_y = d_x if inplace else self.device_alloc(max(x.nbytes, 16))
         d_w = None
         self.h2d(d_x, x)
         if w is not None:
             d_w = self.device_alloc(n * 4)
             self.h2d(d_w, np.ascontiguousarray(w, np.float32))
-        self.rmsnorm_device(d_x, d_x, d_w, rows, n, eps)
+        self.rmsnorm_device(d_y, d_x, d_w, rows, n, eps)
         self.sync()
-        return self.d2h(d_x, (rows, n))
+        if not inplace and not np.array_equal(self.d2h(d_x, (rows, n)).view(np.uint32), x.view(np.uint32)):
+            raise QmsgError(-4, "rmsnorm: the input rows changed")
+        return self.d2h(d_y, (rows, n))
 
     def layer_norm(self, layer: int, w: Optional[np.ndarray]):
         wp = None if w is None else np.ascontiguousarray(w, np.float32)

@@ -49,7 +49,7 @@ def test_oracle_matmul_row_is_vec_dot():
     assert not np.array_equal(orc.matmul_q8(t, w2, rows, cols, x), y)
 
 
-@pytest.mark.skipif(orc.load_ref() is None, reason="oracle/_ref (the reference build) is not built here")
+@pytest.mark.skipif(orc.ref_library_path() is None, reason="oracle/_ref (the reference build) is not built here")
 @pytest.mark.parametrize("t,rows,cols,T", [(orc.T_Q4_0, 96, 4096, 5), (orc.T_Q4_1, 33, 1024, 2),
                                            (orc.T_Q6_K, 20, 2048, 3), (orc.T_F32, 24, 1024, 3),
                                            (orc.T_F32, 7, 4096, 1)])

@@ -2,6 +2,7 @@
 (oracle/_ref, compiled from src/gguf.c) on files written by tests/gguf_file.py, plus the
 files' MoE layers through the reference's qms_model_load + moe() against the oracle."""
 import ctypes
+import functools
 import os
 import struct
 
@@ -11,8 +12,14 @@ import pytest
 import gguf_file as gf
 import oracle as orc
 
-R = orc.load_ref()
-need_ref = pytest.mark.skipif(R is None, reason="oracle/_ref (the reference build) is not built here")
+# the reference build is loaded on first use, not at import: collecting this module under
+# -m gpu must not map it into the GPU test process
+need_ref = pytest.mark.skipif(orc.ref_library_path() is None, reason="oracle/_ref (the reference build) is not built here")
+
+
+@functools.lru_cache(maxsize=None)
+def ref_lib():
+    return orc.load_ref()
 
 
 @pytest.fixture(scope="module")
@@ -31,7 +38,7 @@ def ref_table(path, cap=256):
     ne = np.zeros(4 * cap, np.int64)
     off = np.zeros(cap, np.uint64)
     nb = np.zeros(cap, np.uint64)
-    n = R.qref_gguf_table(os.fsencode(path), cap, names, a["type"].ctypes.data, a["n_dims"].ctypes.data,
+    n = ref_lib().qref_gguf_table(os.fsencode(path), cap, names, a["type"].ctypes.data, a["n_dims"].ctypes.data,
                           ne.ctypes.data, a["shard"].ctypes.data, off.ctypes.data, nb.ctypes.data)
     if n < 0:
         return None
@@ -76,7 +83,7 @@ def test_table_and_values_match_reference(q, tmp_path, shards):
                     "qwen3moe.attention.layer_norm_rms_epsilon", "qwen3moe.rope.freq_base", "general.alignment",
                     "general.architecture", "tokenizer.ggml.tokens", "no.such.key"):
             ri, rf = ctypes.c_int64(), ctypes.c_double()
-            rc = R.qref_gguf_value(os.fsencode(path), key.encode(), ctypes.byref(ri), ctypes.byref(rf))
+            rc = ref_lib().qref_gguf_value(os.fsencode(path), key.encode(), ctypes.byref(ri), ctypes.byref(rf))
             for bit, get, rv in ((1, g.get_int, ri), (2, g.get_float, rf)):
                 if rc & bit:
                     with pytest.raises(q.QmsgError):
@@ -97,7 +104,7 @@ def test_scalar_conversions_match_reference(q, tmp_path):
     with q.Gguf(path) as g:
         for key, _, _ in kvs:
             ri, rf = ctypes.c_int64(), ctypes.c_double()
-            rc = R.qref_gguf_value(os.fsencode(path), key.encode(), ctypes.byref(ri), ctypes.byref(rf))
+            rc = ref_lib().qref_gguf_value(os.fsencode(path), key.encode(), ctypes.byref(ri), ctypes.byref(rf))
             assert rc >= 0
             for bit, get, rv in ((1, g.get_int, ri), (2, g.get_float, rf)):
                 if rc & bit:
@@ -144,7 +151,7 @@ def test_bad_files_are_refused(q, tmp_path):
         with pytest.raises(q.QmsgError) as ei:
             q.Gguf(path)
         assert ei.value.status == -1, name
-        if R is not None:
+        if ref_lib() is not None:
             assert ref_table(path) is None, name
 
 
@@ -213,5 +220,5 @@ def test_reference_loader_moe_equals_oracle(tmp_path):
     x = orc.make_input(256, 3, 5)
     for l, lay in enumerate(lays):
         out = np.empty_like(x)
-        assert R.qref_gguf_moe(os.fsencode(path), l, x.ctypes.data, 3, out.ctypes.data) == 0
+        assert ref_lib().qref_gguf_moe(os.fsencode(path), l, x.ctypes.data, 3, out.ctypes.data) == 0
         assert np.array_equal(out.view(np.uint32), lay.moe(x).view(np.uint32)), l

@@ -15,6 +15,9 @@ CASES = [
     ("q30b_q6k_l3_t4", 2048, 128, 8, 768, 4, 3, orc.T_Q6_K, True),
     ("q30b_q4_l2_t1", 2048, 128, 8, 768, 1, 2, orc.T_Q4_0, True),
     ("q30b_q41_l2_t3", 2048, 128, 8, 768, 3, 2, orc.T_Q4_1, True),
+    # the 94-layer stack's shape and batch: MFMA gate/up and Q6_K down between rmsnorm and the
+    # residual add
+    ("q235b_q6k_l2_t64", 4096, 128, 8, 1536, 64, 2, orc.T_Q6_K, True),
 ]
 
 

@@ -41,17 +41,20 @@ DEVICE_GOLD = ["tiny_t1", "tiny_t7", "q30b_t1", "q235b_t1", "q235b_t4", "q235b_t
                "q30b_gq41_t1", "q235b_gq6k_t4", "tiny_gq6k_uq41_t7"]
 
 
+@pytest.mark.parametrize("path", ["exact", "auto"])
 @pytest.mark.parametrize("name", DEVICE_GOLD)
-def test_device_layer_equals_reference_output(q, name):
-    """Weights generated on the device, output hashed against the reference moe()'s output."""
+def test_device_layer_equals_reference_output(q, name, path):
+    """Weights generated on the device, output hashed against the reference moe()'s output, on
+    the row kernels (exact) and on the default path, which takes the MFMA kernels for the
+    16-, 64- and 512-token layers."""
     d = dict(np.load(os.path.join(GOLD, f"layer_{name}.npz")))
     E, X, K, F, T, seed, dt, rms = (int(v) for v in d["shape"])
-    print(f"[case] golden {name} T={T}", flush=True)
+    print(f"[case] golden {name} T={T} path={path}", flush=True)
     x = golden_input(d)
     col0 = d.get("router_col0")
     gt, ut = (int(v) for v in d.get("gu_types", (q.QMSG_T_Q4_0, q.QMSG_T_Q4_0)))
     with q.Context(E, X, K, F, n_layer=1, max_tokens=T) as ctx:
-        ctx.set_path(q.PATH_EXACT)
+        ctx.set_path(q.PATH_EXACT if path == "exact" else q.PATH_AUTO)
         ctx.synth(0, seed, gate_type=gt, up_type=ut, down_type=dt, router_col0=col0)
         out = ctx.moe(0, x)
     assert sha(out) == bytes(d["out_sha"])

@@ -119,17 +119,21 @@ def test_mfma_gateup_types_bit_exact(q, name, E, X, K, F, T, seed, gt, dt):
 
 
 SCALE_CASES = [
-    # name, scale of every other token, gate/up type, down type
-    ("acts_subnormal_q4_0", 1e-20, orc.T_Q4_0, orc.T_Q4_0),   # activation blocks' d ~1e-43
-    ("input_tiny_q4_0", 1e-36, orc.T_Q4_0, orc.T_Q4_0),       # input blocks' d ~1e-38
-    ("acts_subnormal_q4_1", 1e-20, orc.T_Q4_1, orc.T_Q4_1),
-    ("input_tiny_q4_1", 1e-36, orc.T_Q4_1, orc.T_Q6_K),
-    ("input_tiny_q6_k", 1e-36, orc.T_Q6_K, orc.T_Q6_K),
+    # name, scale of every other token, gate type, up type, down type
+    ("acts_subnormal_q4_0", 1e-20, orc.T_Q4_0, orc.T_Q4_0, orc.T_Q4_0),   # activation blocks' d ~1e-43
+    ("input_tiny_q4_0", 1e-36, orc.T_Q4_0, orc.T_Q4_0, orc.T_Q4_0),       # input blocks' d ~1e-38
+    ("acts_subnormal_q4_1", 1e-20, orc.T_Q4_1, orc.T_Q4_1, orc.T_Q4_1),
+    ("input_tiny_q4_1", 1e-36, orc.T_Q4_1, orc.T_Q4_1, orc.T_Q6_K),
+    ("input_tiny_q6_k", 1e-36, orc.T_Q6_K, orc.T_Q6_K, orc.T_Q6_K),
+    # gate and up of different types take the row kernels, so the MFMA down kernel's records
+    # come from act_quant_kernel, which must flag the out-of-range ones itself
+    ("acts_subnormal_rowgu_q4_0", 1e-20, orc.T_Q4_1, orc.T_Q4_0, orc.T_Q4_0),
+    ("acts_subnormal_rowgu_q4_1", 1e-20, orc.T_Q4_0, orc.T_Q4_1, orc.T_Q4_1),
 ]
 
 
-@pytest.mark.parametrize("name,scale,gt,dt", SCALE_CASES, ids=[c[0] for c in SCALE_CASES])
-def test_mfma_scale_ranges(q, name, scale, gt, dt):
+@pytest.mark.parametrize("name,scale,gt,ut,dt", SCALE_CASES, ids=[c[0] for c in SCALE_CASES])
+def test_mfma_scale_ranges(q, name, scale, gt, ut, dt):
     """Blocks whose d_x lies outside [2^-102, 2^88], where fl(d_w d_x 2^24) can differ from
     fl(d_w d_x) 2^24 (subnormal products): the Q4 MFMA kernels must take their unscaled loop
     for such launches, Q6_K needs no range. Every other token is scaled down, so a launch mixes
@@ -138,12 +142,15 @@ def test_mfma_scale_ranges(q, name, scale, gt, dt):
     print(f"[case] mfma scale range {name}", flush=True)
     x = orc.make_input(E, T, seed)
     x[1::2] *= np.float32(scale)
-    host = orc.Layer(E, X, K, F, seed, gate_type=gt, up_type=gt, down_type=dt, experts=[])
+    host = orc.Layer(E, X, K, F, seed, gate_type=gt, up_type=ut, down_type=dt, experts=[])
     ref_out, ref = host.moe(x, debug=True)
     d = np.concatenate([ref["xq"]["d"].ravel(), ref["aq"]["d"].ravel()])
     assert ((d != 0) & ((d < 2.0 ** -102) | (d > 2.0 ** 88))).any(), "no record outside the range"
+    if gt != ut:
+        da = ref["aq"]["d"].ravel()
+        assert ((da != 0) & (da < 2.0 ** -102)).any(), "no activation record outside the range"
     with q.Context(E, X, K, F, n_layer=1, max_tokens=T) as ctx:
-        ctx.synth(0, seed, gate_type=gt, up_type=gt, down_type=dt)
+        ctx.synth(0, seed, gate_type=gt, up_type=ut, down_type=dt)
         results = []
         for path in (q.PATH_MFMA, q.PATH_AUTO):
             ctx.set_path(path)

@@ -43,16 +43,20 @@ def ctx():
         yield c
 
 
-@pytest.mark.parametrize("n", [256, 2048, 4096, 6144, 7168, 132])
+# 512-multiples take the chunked sum: up to 8192 floats the row stays held in registers, above
+# that (12288, 16384) the kernel loops over several bases and rereads the row for the output,
+# and 16384 has 256 chunks per row. 132, 256 and 9004 take the term-by-term sum.
+@pytest.mark.parametrize("n", [256, 2048, 4096, 6144, 7168, 12288, 16384, 132, 9004])
 def test_rmsnorm_rows_bit_exact(ctx, n):
     print(f"[case] rmsnorm n={n}", flush=True)
     rng = np.random.default_rng(n)
     x = np.concatenate([rows_of_kind(k, n, 24, rng) for k in range(8)])
     w = rng.uniform(0.5, 1.5, n).astype(np.float32)
     for weights in (None, w):
-        got = ctx.rmsnorm(x, weights, eps=1e-6)
         ref = orc.rmsnorm(x, weights, eps=1e-6)
-        assert np.array_equal(got.view(np.uint32), ref.view(np.uint32)), (n, weights is None)
+        for inplace in (True, False):
+            got = ctx.rmsnorm(x, weights, eps=1e-6, inplace=inplace)
+            assert np.array_equal(got.view(np.uint32), ref.view(np.uint32)), (n, weights is None, inplace)
 
 
 def test_rmsnorm_non_finite_rows(ctx):

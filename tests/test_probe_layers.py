@@ -8,7 +8,6 @@ import pytest
 import oracle as orc
 import probe_layers as pl
 
-R = orc.load_ref()
 SMALL = dict(E=256, X=16, K=4, F=256)
 
 
@@ -25,6 +24,7 @@ def test_gateup_probe_rows_are_block_dots(types):
     exp = pl.expected_gateup(L, bg, bu, d)
     assert np.array_equal(_bits(d["gu"]), _bits(exp))
     assert np.count_nonzero(exp) > 0.9 * exp.size                  # the dots are not trivially 0
+    R = orc.load_ref()
     if R is not None:
         assert np.array_equal(_bits(orc.ref_moe(R, L, x)), _bits(out))
 
@@ -41,6 +41,7 @@ def test_down_probe_rows_are_block_dots(dt):
     exp = pl.expected_down(L, bd, d)
     assert np.array_equal(_bits(d["dn"]), _bits(exp))
     assert np.count_nonzero(exp) > 0.9 * exp.size
+    R = orc.load_ref()
     if R is not None:
         assert np.array_equal(_bits(orc.ref_moe(R, L, x)), _bits(out))
 
