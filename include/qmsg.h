@@ -241,6 +241,15 @@ int qmsg_moe_chain(qmsg_ctx *ctx, int first, int n, float *d_h, int T, float eps
  * (unit weights). d_y may equal d_x. Enqueued without waiting. */
 int qmsg_rmsnorm_device(qmsg_ctx *ctx, float *d_y, const float *d_x, const float *d_w, int rows, int n, float eps);
 
+/* How this context's rmsnorm launches (qmsg_moe_chain, qmsg_rmsnorm_device) form ss; the result
+ * is the same bits either way. always_walk 0 (the default): a parallel sum brackets ss, and the
+ * sum is formed in the reference's order only for rows where some output float differs between
+ * the bracket's ends; 1: every row forms it in order. *walked (if not NULL) receives the number
+ * of rows that formed it in order since the previous such read, after the stream has drained;
+ * the count restarts at 0. No counterpart in the reference (its rmsnorm, src/model.c:403-409,
+ * has one order only): for tests and measurement. */
+int qmsg_rmsnorm_mode(qmsg_ctx *ctx, int always_walk, int64_t *walked);
+
 /* A layer's ffn_norm weight vector (QmsLayer.ffn_norm, src/model.h:37-45), n_embd floats on
  * the host, copied to HBM; NULL restores the default unit weights. */
 int qmsg_layer_norm(qmsg_ctx *ctx, int layer, const float *w);

@@ -128,6 +128,9 @@ struct qmsg_ctx {
     int device = 0;
     qmsg_cfg cfg{};
     int n_layer = 0, max_tokens = 0, path = QMSG_PATH_AUTO;
+    int norm_walk = 0;                      /* rmsnorm: form every row's sum in order */
+    unsigned long long *d_walked = nullptr; /* rmsnorm: rows that formed it in order */
+    float *d_hb = nullptr;                  /* the one-token chain's second row of h */
     int n_cu = 256;
     hipStream_t stream = nullptr;
     std::vector<LayerStore> layers;
@@ -242,6 +245,8 @@ int qmsg_create(qmsg_ctx **out, int device, const qmsg_cfg *cfg, int n_layer, in
     std::vector<ScratchItem> items = scratch_items(*cfg, (size_t)max_tokens, &c->S);
     items.push_back({ (void **)&c->d_x, (size_t)max_tokens * E * 4 });
     items.push_back({ (void **)&c->d_out, (size_t)max_tokens * E * 4 });
+    items.push_back({ (void **)&c->d_walked, 8 });
+    items.push_back({ (void **)&c->d_hb, (size_t)E * 4 });
     for (auto &it : items) {
         if (dev_alloc(c, it.p, it.bytes, c->scratch_allocs) != QMSG_OK) {
             g_create_error = c->err;
@@ -250,6 +255,7 @@ int qmsg_create(qmsg_ctx **out, int device, const qmsg_cfg *cfg, int n_layer, in
         }
     }
     e = hipMemset(c->S.meta, 0, 64);
+    if (e == hipSuccess) e = hipMemset(c->d_walked, 0, 8);
     if (e != hipSuccess) {
         fail(nullptr, QMSG_E_DEVICE, "qmsg_create: %s", hipGetErrorString(e));
         qmsg_destroy(c);
@@ -773,8 +779,11 @@ int qmsg_matmul_n(qmsg_ctx *c, const int *ids, int nW, const float *x, int T, fl
 }
 
 /* One layer on device buffers with the scratch arrays S (the context's, or carved from the
- * library's static array by qmsg_moe_device_noalloc). */
-static int run_layer_s(qmsg_ctx *c, const Scratch &S0, int layer, const float *d_xn, int T, float *d_out, int debug)
+ * library's static array by qmsg_moe_device_noalloc). With ni (one token, rows route_norm_fits
+ * takes, not the fp32 path) the router launch forms xn = ni's rmsnorm itself and stores it to
+ * d_xn (= ni->xn_out) for the launches after it. */
+static int run_layer_s(qmsg_ctx *c, const Scratch &S0, int layer, const float *d_xn, int T, float *d_out, int debug,
+                       const NormIn *ni = nullptr)
 {
     /* every layer call gets an epoch of its own: record producers store it in S.mxflag when a
      * record falls outside the MFMA kernels' scaled range, and the consumers compare */
@@ -790,6 +799,8 @@ static int run_layer_s(qmsg_ctx *c, const Scratch &S0, int layer, const float *d
         return fail(c, QMSG_E_INVALID, "device buffers must be 16-byte aligned (xn) and 4-byte aligned (out)");
     const Shape s{ c->cfg.n_embd, c->cfg.n_expert, c->cfg.n_used, c->cfg.n_ff_exp };
     const LayerDev d = layer_dev(c, L);
+    if (ni && (T != 1 || c->path == QMSG_PATH_FP32 || !route_norm_fits(s.E) || ni->xn_out != d_xn))
+        return fail(c, QMSG_E_INVALID, "run_layer_s: the fused rmsnorm takes one token on the integer paths");
     if (c->path == QMSG_PATH_FP32) {
         LAUNCH(c, "layer", launch_layer_fp32(s, d, S, d_xn, d_out, T, c->stream));
         return QMSG_OK;
@@ -806,7 +817,8 @@ static int run_layer_s(qmsg_ctx *c, const Scratch &S0, int layer, const float *d
      * 139.7 / 128.2 us at 16 tokens, 173.8 / 174.0 at 24, 196.3 / 216.6 at 32), or 2.5 for Q6_K */
     const bool gu_mx = gu_ok && (forced || (autop && mx_auto(T, s.K, s.X, d.gate_type)));
     const bool dn_mx = dn_ok && many && (forced || (autop && mx_auto_down(T, s.K, d.down_type)));
-    LAUNCH(c, "route", launch_route(s, d, S, d_xn, T, c->stream));
+    if (ni) LAUNCH(c, "route", launch_route_norm(s, d, S, *ni, c->stream));
+    else LAUNCH(c, "route", launch_route(s, d, S, d_xn, T, c->stream));
     LAUNCH(c, "select", launch_select(s, S, T, q4 ? 1 : 0, c->stream));
     if (gu_mx) {
         LAUNCH(c, "experts", launch_experts_mx(s, d, S, d_out, T, debug, c->stream));
@@ -885,10 +897,28 @@ int qmsg_moe_chain(qmsg_ctx *c, int first, int n, float *d_h, int T, float eps)
     const int E = c->cfg.n_embd;
     for (int l = first; l < first + n; l++)
         if (!c->layers[(size_t)l].ready) return fail(c, QMSG_E_INVALID, "layer %d has no weights", l);
+    if (T == 1 && c->path != QMSG_PATH_FP32 && route_norm_fits(E)) {
+        /* One token: each layer's router launch forms the rmsnorm itself, every block from h
+         * and the previous layer's output, so h + out goes to the other of two rows (d_h and
+         * d_hb, in turn) while the blocks still read the first. */
+        float *cur = d_h;
+        for (int l = first; l < first + n; l++) {
+            const float *pending = l > first ? c->d_out : nullptr;
+            float *next = pending ? (cur == d_h ? c->d_hb : d_h) : cur;
+            const NormIn ni{ cur, pending, c->layers[(size_t)l].norm, pending ? next : nullptr, c->d_x, eps,
+                             c->norm_walk, c->d_walked };
+            const int rc = run_layer_s(c, c->S, l, c->d_x, T, c->d_out, 0, &ni);
+            if (rc) return rc;
+            cur = next;
+        }
+        LAUNCH(c, "add", launch_add_rows_to(d_h, cur, c->d_out, (size_t)E, c->stream));
+        return QMSG_OK;
+    }
     /* each layer's residual add h += out rides in the next layer's rmsnorm launch */
     for (int l = first; l < first + n; l++) {
         const float *pending = l > first ? c->d_out : nullptr;
-        LAUNCH(c, "rmsnorm", launch_rmsnorm(d_h, pending, c->layers[(size_t)l].norm, c->d_x, T, E, eps, c->stream));
+        LAUNCH(c, "rmsnorm", launch_rmsnorm(d_h, pending, c->layers[(size_t)l].norm, c->d_x, T, E, eps, c->norm_walk,
+                                             c->d_walked, c->stream));
         const int rc = run_layer(c, l, c->d_x, T, c->d_out, 0);
         if (rc) return rc;
     }
@@ -907,7 +937,25 @@ int qmsg_rmsnorm_device(qmsg_ctx *c, float *d_y, const float *d_x, const float *
     if (((uintptr_t)d_x | (uintptr_t)d_y | (uintptr_t)d_w) & 15)
         return fail(c, QMSG_E_INVALID, "qmsg_rmsnorm_device: d_x, d_y and d_w must be 16-byte aligned");
     HIP_TRY(c, hipSetDevice(c->device));
-    LAUNCH(c, "rmsnorm", launch_rmsnorm(const_cast<float *>(d_x), nullptr, d_w, d_y, rows, n, eps, c->stream));
+    LAUNCH(c, "rmsnorm", launch_rmsnorm(const_cast<float *>(d_x), nullptr, d_w, d_y, rows, n, eps, c->norm_walk,
+                                         c->d_walked, c->stream));
+    return QMSG_OK;
+}
+
+int qmsg_rmsnorm_mode(qmsg_ctx *c, int always_walk, int64_t *walked)
+{
+    if (!c) return QMSG_E_INVALID;
+    if (always_walk != 0 && always_walk != 1) return fail(c, QMSG_E_INVALID, "qmsg_rmsnorm_mode: always_walk=%d", always_walk);
+    HIP_TRY(c, hipSetDevice(c->device));
+    if (walked) {
+        unsigned long long n = 0;
+        const unsigned long long zero = 0;
+        HIP_TRY(c, hipStreamSynchronize(c->stream));
+        HIP_TRY(c, hipMemcpy(&n, c->d_walked, 8, hipMemcpyDeviceToHost));
+        HIP_TRY(c, hipMemcpy(c->d_walked, &zero, 8, hipMemcpyHostToDevice));
+        *walked = (int64_t)n;
+    }
+    c->norm_walk = always_walk;
     return QMSG_OK;
 }
 

@@ -172,10 +172,29 @@ inline size_t rmsnorm_lds_bytes(int E)
     const size_t sq = E % 512 == 0 ? (size_t)(E / 64) * 65 : (size_t)E;      /* squares, in doubles */
     return sq * 8;
 }
-/* y = rmsnorm(x) * w per row of E floats; with add (not NULL) x += add first, stored back. */
+/* y = rmsnorm(x) * w per row of E floats; with add (not NULL) x += add first, stored back.
+ * walk: form every row's sum in order (else only rows the bracket leaves open); rows that do
+ * are counted into *walked when it is not NULL. */
 hipError_t launch_rmsnorm(float *x, const float *add, const float *w, float *y, int T, int E, float eps,
-                          hipStream_t st);
+                          int walk, unsigned long long *walked, hipStream_t st);
 hipError_t launch_add_rows(float *h, const float *d, size_t n, hipStream_t st);
+/* dst = h + d over n floats (dst may be h). */
+hipError_t launch_add_rows_to(float *dst, const float *h, const float *d, size_t n, hipStream_t st);
+
+/* The rmsnorm of the one-token router launch (launch_route_norm): xn = rmsnorm(h + add) * w
+ * (add and w may be null), stored to xn_out; h + add stored to h_out when add is not null
+ * (h_out must then differ from h). */
+struct NormIn {
+    const float *h, *add, *w;
+    float *h_out, *xn_out;
+    float eps;
+    int walk;
+    unsigned long long *walked;
+};
+/* Row widths the fused launch takes. */
+inline bool route_norm_fits(int E) { return E % 512 == 0 && E <= 4096; }
+/* launch_route for one token with the rmsnorm in front (route_norm_kernel). */
+hipError_t launch_route_norm(const Shape &s, const LayerDev &L, const Scratch &S, const NormIn &n, hipStream_t st);
 hipError_t launch_set_col0(float *m, int rows, int stride, const float *vals, float fill, hipStream_t st);
 hipError_t launch_silu(const float *x, int n, float *out, hipStream_t st);
 hipError_t launch_exp(const double *x, int n, double *out, hipStream_t st);

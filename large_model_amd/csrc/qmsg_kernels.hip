@@ -4400,7 +4400,7 @@ __device__ __forceinline__ uint64_t dbits(double v) { return (uint64_t)__double_
  * Inside one binade the bit pattern of a non-negative double is its value in units of u plus a
  * constant, so the walk runs on bit patterns in integer (scalar) arithmetic: (s - P_j) / u is
  * bits(s) - bits(P_j), and adding G_r - P_r adds bits(G_r) - bits(P_r). */
-__device__ double ordered_sum_chunked(const double *qt, int C)
+__device__ __forceinline__ double ordered_sum_chunked(const double *qt, int C)
 {
     const int j = threadIdx.x & 63;
     /* 1 */
@@ -4506,20 +4506,157 @@ __device__ double ordered_sum_chunked(const double *qt, int C)
 }
 
 /* rmsnorm of one row per block into another buffer, with a weight vector (nullptr: unit)
- * (src/model.c:403-409): y = (float)(x * inv) * w. ss accumulates (double)x*(double)x in index
- * order; each square is exact in double (48 significant bits), so the reference's
- * fma(x, x, ss) equals ss + x*x with the square formed first: every thread forms squares into
- * LDS, and wave 0 forms their sequential sum (ordered_sum_chunked for E a multiple of 512, else
- * one lane term by term). Rows of up to kNormVec * 1024 floats stay in registers, with their
- * weights, loaded before the sum; longer rows are read again for the output. With add, the row
- * is first x + add in float (the residual add h += out of the previous layer,
- * src/model.c:1285), stored back to x, and normalised. */
+ * (src/model.c:403-409): y = (float)(x * inv) * w, inv = 1 / sqrt(ss / E + eps). ss accumulates
+ * (double)x*(double)x in index order; each square is exact in double (48 significant bits), so
+ * the reference's fma(x, x, ss) equals ss + x*x with the square formed first.
+ * The output needs ss only through the floats (float)(x * inv), so the kernel first brackets
+ * ss: S = the squares summed in any order, and the sequential sum's distance from the exact one
+ * is at most u * sum_k s_{k+1} (u = 2^-53, s the running sums, each step's rounding at most u
+ * times its result), with s_{k+1} <= (1 + u)^k times the exact partial sum, so at most
+ * u (1 + 2^-20) W, W = sum_j q_j (E - j) (q_j the square of element j); S's own distance from
+ * the exact sum is at most (E / 256 + 16) 2^-52 S (the depth of the parallel sum, with room
+ * for the rounding of the bracket's own operations). inv is monotone in ss (every rounded
+ * operation is), and so is (float)(x * inv) in inv: when every element gives the same float
+ * at both ends of the bracket, every ss inside gives it too, and the row is written from one
+ * end. Otherwise (about one 4096-wide row in 200 on normal data: an element within 1e-13 of a
+ * float rounding boundary), or for a non-finite sum, or with walk set, the sum is formed in
+ * order: every thread has put its squares into LDS, and wave 0 forms their sequential sum
+ * (ordered_sum_chunked for E a multiple of 512, else one lane term by term); a row that does
+ * so is counted into *walked (if not null). Rows of up to kNormVec * 1024 floats stay in
+ * registers, with their weights, loaded before the sum; longer rows are read again for the
+ * check and the output. With add, the row is first x + add in float (the residual add
+ * h += out of the previous layer, src/model.c:1285), stored back to x, and normalised. */
 constexpr int kNormVec = 8;
+
+template <int CTRL>
+__device__ __forceinline__ double dpp_f64(double x)
+{
+    const uint64_t b = dbits(x);
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)b, CTRL, 0xF, 0xF, false);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)(b >> 32), CTRL, 0xF, 0xF, false);
+    return __longlong_as_double((long long)(((uint64_t)hi << 32) | lo));
+}
+
+/* A sum of a double over the 64 lanes of a wave, in some fixed order, in every lane: the
+ * quads, halves of rows and rows by lane permutations, then the four rows' sums read out. */
+__device__ __forceinline__ double wave_sum_any(double v)
+{
+    v += dpp_f64<0xB1>(v);      /* quad_perm 1, 0, 3, 2 */
+    v += dpp_f64<0x4E>(v);      /* quad_perm 2, 3, 0, 1 */
+    v += dpp_f64<0x141>(v);     /* row_half_mirror      */
+    v += dpp_f64<0x140>(v);     /* row_mirror           */
+    const double r0 = __longlong_as_double((long long)readlane_u64(dbits(v), 0));
+    const double r1 = __longlong_as_double((long long)readlane_u64(dbits(v), 16));
+    const double r2 = __longlong_as_double((long long)readlane_u64(dbits(v), 32));
+    const double r3 = __longlong_as_double((long long)readlane_u64(dbits(v), 48));
+    return (r0 + r1) + (r2 + r3);
+}
+
+/* The inverse norm inv = 1 / sqrt(ss / E + eps) of one row (rmsnorm_kernel describes the
+ * bracket) from this thread's partial sums of the squares (sum_s) and of the squares weighted
+ * by E - j (sum_w); same(lo, hi) tells whether every element this thread holds gives one
+ * float (float)(x * inv) at inv = lo and at inv = hi, and fill() stores this thread's squares
+ * into LDS at q in the layout the ordered sum reads (norm_store), called only when the sum is
+ * formed in order. All 256 threads of the block call it, with the same E, eps and walk; part
+ * is 8 doubles of LDS and inv_sh one. A row that forms its sum in order is counted into
+ * *walked when walked is not null. */
+template <class Same, class Fill>
+__device__ double norm_inv(double sum_s, double sum_w, const double *q, int E, float eps, int walk,
+                           unsigned long long *walked, Same same, Fill fill, double *part, double *inv_sh)
+{
+    const int tid = threadIdx.x;
+    sum_s = wave_sum_any(sum_s);
+    sum_w = wave_sum_any(sum_w);
+    if ((tid & 63) == 0) {
+        part[tid >> 6] = sum_s;
+        part[4 + (tid >> 6)] = sum_w;
+    }
+    PHASE(3072, 1);
+    __syncthreads();
+    PHASE(3072, 2);
+    /* the same operations in the same order on every thread: S, W and the verdict are uniform */
+    const double S = (part[0] + part[1]) + (part[2] + part[3]);
+    const double W = (part[4] + part[5]) + (part[6] + part[7]);
+    bool open = walk || !__builtin_isfinite(S) || !__builtin_isfinite(W);
+    double inv_lo = 0.0;
+    if (!open) {
+        const double err = W * 0x1.00001p-53 + S * ((double)(E / 256 + 16) * 0x1p-52);
+        inv_lo = 1.0 / sqrt((S + err) / E + (double)eps);
+        const double inv_hi = 1.0 / sqrt((S - err) / E + (double)eps);
+        open = __syncthreads_or(!same(inv_lo, inv_hi));
+    }
+    if (!open) return inv_lo;
+    fill();
+    __syncthreads();
+    if (tid < 64) {
+        double ss;
+        if (E % 512 == 0) {
+            ss = ordered_sum_chunked(q, E >> 6);
+            PHASE(3072, 5);
+        } else {
+            ss = 0.0;
+            if (tid == 0)
+                for (int i = 0; i < E; i++) ss += q[i];
+        }
+        if (tid == 0) {
+            *inv_sh = 1.0 / sqrt(ss / E + (double)eps);
+            if (walked) atomicAdd(walked, 1ull);
+        }
+    }
+    __syncthreads();
+    return *inv_sh;
+}
+
+/* Whether a float4 of x gives the same (float)(x * inv) at inv = lo and inv = hi. */
+__device__ __forceinline__ bool same_at_both(float4 a, double lo, double hi)
+{
+    return (float)((double)a.x * lo) == (float)((double)a.x * hi) &&
+           (float)((double)a.y * lo) == (float)((double)a.y * hi) &&
+           (float)((double)a.z * lo) == (float)((double)a.z * hi) &&
+           (float)((double)a.w * lo) == (float)((double)a.w * hi);
+}
+
+/* y = (float)(x * inv) * w for a float4. */
+__device__ __forceinline__ float4 norm_apply(float4 a, float4 b, double v)
+{
+    return make_float4((float)((double)a.x * v) * b.x, (float)((double)a.y * v) * b.y,
+                       (float)((double)a.z * v) * b.z, (float)((double)a.w * v) * b.w);
+}
+
+/* The squares of a float4 of x at float4 index i of the row into the partial sums: sum_s of
+ * the squares, sum_w of the squares weighted by E - j (j the element's index). */
+__device__ __forceinline__ void norm_partials(float4 v, int i, int E, double &sum_s, double &sum_w)
+{
+    const double sq[4] = { (double)v.x * (double)v.x, (double)v.y * (double)v.y,
+                           (double)v.z * (double)v.z, (double)v.w * (double)v.w };
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        sum_s += sq[k];
+        sum_w += sq[k] * (double)(E - (4 * i + k));
+    }
+}
+
+/* The squares of a float4 of x at float4 index i of the row into q in the ordered sum's layout:
+ * for chunked rows element 4i + k at lane (4i + k) / C, term (4i + k) % C of its chunk. */
+__device__ __forceinline__ void norm_store(float4 v, int i, int E, double *q)
+{
+    const bool chunked = E % 512 == 0;
+    const int C = E >> 6;
+    const double sq[4] = { (double)v.x * (double)v.x, (double)v.y * (double)v.y,
+                           (double)v.z * (double)v.z, (double)v.w * (double)v.w };
+    const int lj = chunked ? (4 * i) / C : 0, ti = 4 * i - lj * C;
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        if (chunked) q[(ti + k) * kSumPitch + lj] = sq[k];
+        else q[4 * i + k] = sq[k];
+    }
+}
+
 __global__ __launch_bounds__(256) void rmsnorm_kernel(float *x, const float *add, const float *w, float *y, int E,
-                                                      float eps)
+                                                      float eps, int walk, unsigned long long *walked)
 {
     extern __shared__ __align__(16) double q[];      /* the squares */
-    __shared__ double inv;
+    __shared__ double inv_sh, part[8];
     PHASE(3072, 0);
     float4 *xrow = (float4 *)(x + (size_t)blockIdx.x * E);
     const float4 *arow = add ? (const float4 *)(add + (size_t)blockIdx.x * E) : nullptr;
@@ -4527,10 +4664,10 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(float *x, const float *add
     const float4 *w4 = (const float4 *)w;
     float4 *out = (float4 *)(y + (size_t)blockIdx.x * E);
     const int n4 = E >> 2, tid = threadIdx.x;
-    const bool chunked = E % 512 == 0, held = n4 <= 256 * kNormVec;
-    const int C = E >> 6;                            /* terms per lane (chunked: C % 8 == 0) */
+    const bool held = n4 <= 256 * kNormVec;
     const float4 one = make_float4(1.0f, 1.0f, 1.0f, 1.0f);
     float4 xv[kNormVec], wv[kNormVec];
+    double sum_s = 0.0, sum_w = 0.0;
     for (int base = 0; base < n4; base += 256 * kNormVec) {
 #pragma unroll
         for (int m = 0; m < kNormVec; m++) {
@@ -4554,82 +4691,212 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(float *x, const float *add
 #pragma unroll
         for (int m = 0; m < kNormVec; m++) {
             const int i = base + tid + 256 * m;
-            if (i >= n4) continue;
-            const float4 v = xv[m];
-            const double sq[4] = { (double)v.x * (double)v.x, (double)v.y * (double)v.y,
-                                   (double)v.z * (double)v.z, (double)v.w * (double)v.w };
-            /* element 4i + k: lane (4i + k) / C, term (4i + k) % C of its chunk */
-            const int lj = chunked ? (4 * i) / C : 0, ti = 4 * i - lj * C;
+            if (i < n4) norm_partials(xv[m], i, E, sum_s, sum_w);
+        }
+    }
+    auto same = [&](double lo, double hi) {
+        bool ok = true;
+        if (held) {
 #pragma unroll
-            for (int k = 0; k < 4; k++) {
-                if (chunked) q[(ti + k) * kSumPitch + lj] = sq[k];
-                else q[4 * i + k] = sq[k];
+            for (int m = 0; m < kNormVec; m++) {
+                const int i = tid + 256 * m;
+                if (i < n4 && !same_at_both(xv[m], lo, hi)) ok = false;
             }
-        }
-    }
-    PHASE(3072, 1);
-    __syncthreads();
-    PHASE(3072, 2);
-    if (tid < 64) {
-        double ss;
-        if (chunked) {
-            ss = ordered_sum_chunked(q, C);
-            PHASE(3072, 5);
         } else {
-            ss = 0.0;
-            if (tid == 0)
-                for (int i = 0; i < E; i++) ss += q[i];
+            for (int i = tid; i < n4; i += 256)
+                if (!same_at_both(row[i], lo, hi)) ok = false;
         }
-        if (tid == 0) inv = 1.0 / sqrt(ss / E + (double)eps);
-    }
-    __syncthreads();
-    PHASE(3072, 6);
-    const double v = inv;
-    auto norm = [&](float4 a, float4 b) {
-        return make_float4((float)((double)a.x * v) * b.x, (float)((double)a.y * v) * b.y,
-                           (float)((double)a.z * v) * b.z, (float)((double)a.w * v) * b.w);
+        return ok;
     };
+    auto fill = [&]() {
+        if (held) {
+#pragma unroll
+            for (int m = 0; m < kNormVec; m++) {
+                const int i = tid + 256 * m;
+                if (i < n4) norm_store(xv[m], i, E, q);
+            }
+        } else {
+            for (int i = tid; i < n4; i += 256) norm_store(row[i], i, E, q);
+        }
+    };
+    const double v = norm_inv(sum_s, sum_w, q, E, eps, walk, walked, same, fill, part, &inv_sh);
+    PHASE(3072, 6);
     if (held) {
 #pragma unroll
         for (int m = 0; m < kNormVec; m++) {
             const int i = tid + 256 * m;
-            if (i < n4) out[i] = norm(xv[m], wv[m]);
+            if (i < n4) out[i] = norm_apply(xv[m], wv[m], v);
         }
     } else {
-        for (int i = tid; i < n4; i += 256) out[i] = norm(row[i], w ? w4[i] : one);
+        for (int i = tid; i < n4; i += 256) out[i] = norm_apply(row[i], w ? w4[i] : one, v);
+    }
+    PHASE(3072, 3);
+}
+
+/* rmsnorm fused ahead of the one-token router, for the layer chain (src/model.c:1283-1284, then
+ * the router of src/model.c:1032-1167 as route_small_kernel<1> runs it): every block forms
+ * x = h + add (float) and xn = rmsnorm(x) * w itself, bit for bit as rmsnorm_kernel does (the
+ * bracket, and the ordered sum where it is open); router blocks, one per expert, then run the
+ * expert's 16 FMA chains over xn staged chain-major in LDS, and the last block stores x to
+ * h_out (when add is not null), xn to xn_out and the int8 input blocks of xn. h_out is not h,
+ * which every block reads. E a multiple of 512, at most 4096. */
+__global__ __launch_bounds__(256) void route_norm_kernel(RouteArgs a, NormIn n)
+{
+    extern __shared__ __align__(16) uint8_t smem[];
+    __shared__ double inv_sh, part[8];
+    constexpr int NV = 4;                            /* float4s i = tid + 256 m, E <= 4096 */
+    const int tid = threadIdx.x, E = a.E, n4 = E >> 2, e = blockIdx.x;
+    const bool router = e < a.n_route_wg;
+    const int C = E >> 6, CS = E / 16 + 4;
+    double *q = (double *)smem;                      /* the squares: C * kSumPitch doubles */
+    float *buf = (float *)(smem + (size_t)C * kSumPitch * 8);   /* [2 rows][16 chains][CS] */
+    const float4 *h4 = (const float4 *)n.h, *a4 = (const float4 *)n.add, *w4 = (const float4 *)n.w;
+    const float4 *r4 = (const float4 *)(a.router + (size_t)(router ? e : 0) * E);
+    const float4 one = make_float4(1.0f, 1.0f, 1.0f, 1.0f);
+    float4 xv[NV], wv[NV], rv[NV];
+#pragma unroll
+    for (int m = 0; m < NV; m++) {
+        const int i = tid + 256 * m;
+        if (i < n4) {
+            if (router) rv[m] = r4[i];
+            xv[m] = h4[i];
+            wv[m] = w4 ? w4[i] : one;
+            if (a4) {
+                const float4 d = a4[i];
+                xv[m] = make_float4(xv[m].x + d.x, xv[m].y + d.y, xv[m].z + d.z, xv[m].w + d.w);
+            }
+        }
+    }
+    double sum_s = 0.0, sum_w = 0.0;
+#pragma unroll
+    for (int m = 0; m < NV; m++) {
+        const int i = tid + 256 * m;
+        if (i < n4) norm_partials(xv[m], i, E, sum_s, sum_w);
+    }
+    auto same = [&](double lo, double hi) {
+        bool ok = true;
+#pragma unroll
+        for (int m = 0; m < NV; m++) {
+            const int i = tid + 256 * m;
+            if (i < n4 && !same_at_both(xv[m], lo, hi)) ok = false;
+        }
+        return ok;
+    };
+    auto fill = [&]() {
+#pragma unroll
+        for (int m = 0; m < NV; m++) {
+            const int i = tid + 256 * m;
+            if (i < n4) norm_store(xv[m], i, E, q);
+        }
+    };
+    const double v = norm_inv(sum_s, sum_w, q, E, n.eps, n.walk, router ? nullptr : n.walked, same, fill, part,
+                              &inv_sh);
+    float4 xn[NV];
+#pragma unroll
+    for (int m = 0; m < NV; m++) xn[m] = norm_apply(xv[m], wv[m], v);
+    if (router) {
+        /* float4 j holds elements 4j .. 4j+3: chains 4(j%4) .. 4(j%4)+3, step j/4 */
+#pragma unroll
+        for (int m = 0; m < NV; m++) {
+            const int j = tid + 256 * m;
+            if (j < n4) {
+                float *dw = buf + (4 * (j & 3)) * CS + (j >> 2), *dx = dw + 16 * CS;
+                dw[0] = rv[m].x; dw[CS] = rv[m].y; dw[2 * CS] = rv[m].z; dw[3 * CS] = rv[m].w;
+                dx[0] = xn[m].x; dx[CS] = xn[m].y; dx[2 * CS] = xn[m].z; dx[3 * CS] = xn[m].w;
+            }
+        }
+        __syncthreads();
+        if (tid < 16) {
+            const float4 *wr = (const float4 *)(buf + tid * CS), *xr = (const float4 *)(buf + (16 + tid) * CS);
+            const int q1 = E / 64;                   /* float4 steps of one chain */
+            float acc = 0.0f;
+            if ((q1 & 7) == 0) acc = chain_steps<8>(wr, xr, 0, q1, acc);
+            else acc = chain_steps<1>(wr, xr, 0, q1, acc);
+            acc = chain16_sum(acc);
+            if (tid == 0) a.y[e] = acc;
+        }
+        return;
+    }
+    float4 *lin = (float4 *)buf;
+#pragma unroll
+    for (int m = 0; m < NV; m++) {
+        const int i = tid + 256 * m;
+        if (i < n4) {
+            if (a4) ((float4 *)n.h_out)[i] = xv[m];
+            ((float4 *)n.xn_out)[i] = xn[m];
+            lin[i] = xn[m];
+        }
+    }
+    __syncthreads();
+    const int nbE = E >> 5;
+    if (tid < nbE) {
+        float vb[32];
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const float4 f = lin[8 * tid + j];
+            vb[4 * j] = f.x; vb[4 * j + 1] = f.y; vb[4 * j + 2] = f.z; vb[4 * j + 3] = f.w;
+        }
+        uint32_t *pair = (uint32_t *)(a.S.xqk + (size_t)(tid >> 1) * kPairBytes);
+        quantize_block_store(vb, a.S.xq + tid, pair, tid & 1);
     }
 }
 
+hipError_t launch_route_norm(const Shape &s, const LayerDev &L, const Scratch &S, const NormIn &n, hipStream_t st)
+{
+    if (!route_norm_fits(s.E) || !n.h || !n.xn_out || (n.add && (!n.h_out || n.h_out == n.h)))
+        return hipErrorInvalidValue;
+    RouteArgs a;
+    a.router = L.router;
+    a.xn = n.xn_out;
+    a.E = s.E;
+    a.X = s.X;
+    a.K = s.K;
+    a.T = 1;
+    a.y = S.logits;
+    a.ystride = s.X;
+    a.S = S;
+    a.n_route_wg = s.X;
+    const size_t lds = (size_t)(s.E / 64) * kSumPitch * 8 + (size_t)2 * 16 * (s.E / 16 + 4) * 4;
+    QLAUNCH("route", route_norm_kernel, dim3(s.X + 1), dim3(256), lds, st, a, n);
+    return hipGetLastError();
+}
+
 hipError_t launch_rmsnorm(float *x, const float *add, const float *w, float *y, int T, int E, float eps,
-                          hipStream_t st)
+                          int walk, unsigned long long *walked, hipStream_t st)
 {
     if (T <= 0) return hipSuccess;
     if (E % 4) return hipErrorInvalidValue;
     static_assert(kSumPitch == 65, "rmsnorm_lds_bytes assumes the pitch");
     if (rmsnorm_lds_bytes(E) > 160 * 1024) return hipErrorInvalidValue;
-    QLAUNCH("rmsnorm", rmsnorm_kernel, dim3(T), dim3(256), rmsnorm_lds_bytes(E), st, x, add, w, y, E, eps);
+    QLAUNCH("rmsnorm", rmsnorm_kernel, dim3(T), dim3(256), rmsnorm_lds_bytes(E), st, x, add, w, y, E, eps, walk,
+            walked);
     return hipGetLastError();
 }
 
-/* h += d (src/model.c:1285), float adds. */
-__global__ void add_rows_kernel(float4 *h, const float4 *d, size_t n4)
+/* dst = h + d (src/model.c:1285), float adds; dst may be h. */
+__global__ void add_rows_kernel(float4 *dst, const float4 *h, const float4 *d, size_t n4)
 {
     const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i < n4) {
         float4 a = h[i];
         const float4 b = d[i];
         a.x += b.x; a.y += b.y; a.z += b.z; a.w += b.w;
-        h[i] = a;
+        dst[i] = a;
     }
+}
+
+hipError_t launch_add_rows_to(float *dst, const float *h, const float *d, size_t n, hipStream_t st)
+{
+    if (n % 4) return hipErrorInvalidValue;
+    const size_t n4 = n / 4;
+    if (n4) QLAUNCH("add", add_rows_kernel, dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0, st, (float4 *)dst,
+                    (const float4 *)h, (const float4 *)d, n4);
+    return hipGetLastError();
 }
 
 hipError_t launch_add_rows(float *h, const float *d, size_t n, hipStream_t st)
 {
-    if (n % 4) return hipErrorInvalidValue;
-    const size_t n4 = n / 4;
-    if (n4) QLAUNCH("add", add_rows_kernel, dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0, st, (float4 *)h,
-                    (const float4 *)d, n4);
-    return hipGetLastError();
+    return launch_add_rows_to(h, h, d, n, st);
 }
 
 __global__ void set_col0_kernel(float *m, int rows, int stride, const float *vals, float fill)

@@ -102,6 +102,7 @@ _SIGS = {
                                ctypes.POINTER(ctypes.c_double)]),
     "qmsg_moe_chain": (_I, [_P, _I, _I, _P, _I, ctypes.c_float]),
     "qmsg_rmsnorm_device": (_I, [_P, _P, _P, _P, _I, _I, ctypes.c_float]),
+    "qmsg_rmsnorm_mode": (_I, [_P, _I, ctypes.POINTER(ctypes.c_int64)]),
     "qmsg_layer_norm": (_I, [_P, _I, _P]),
     "qmsg_eval_silu": (_I, [_P, _P, _I, _P]),
     "qmsg_eval_exp": (_I, [_P, _P, _I, _P]),
@@ -455,6 +456,14 @@ class Context:
         if not inplace and not np.array_equal(self.d2h(d_x, (rows, n)).view(np.uint32), x.view(np.uint32)):
             raise QmsgError(-4, "rmsnorm: the input rows changed")
         return self.d2h(d_y, (rows, n))
+
+    def rmsnorm_mode(self, always_walk: bool) -> int:
+        """Set how rmsnorm forms its sum (True: in order for every row; False: only for rows the
+        parallel bracket leaves open); returns the rows that formed it in order since the last
+        call."""
+        n = ctypes.c_int64(0)
+        self._check(lib.qmsg_rmsnorm_mode(self._h, int(always_walk), ctypes.byref(n)))
+        return int(n.value)
 
     def layer_norm(self, layer: int, w: Optional[np.ndarray]):
         wp = None if w is None else np.ascontiguousarray(w, np.float32)
