@@ -2284,6 +2284,7 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef short short2_t __attribute__((ext_vector_type(2)));
 
 constexpr int kMxC = 8;          /* 32-blocks per staged chunk (one Q6_K super-block) */
+constexpr int kMxNA = 8;         /* accumulator tiles per 16-row tile: 4 pairs, or 4 quads x 2 halves */
 constexpr int kMxDx = 64;        /* offset of the record's d 2^24, ds, half sums, d */
 constexpr int kMxZero = 80;      /* offset of the record's zero words */
 static_assert(kMxRec == 128, "record layout: 64 bytes of codes, 16 of scales, 16 of zeros (32 unused)");
@@ -2359,11 +2360,14 @@ __host__ __device__ constexpr int mx_wstride(int type) { return type == 14 ? 216
  * piece is copied by the LDS DMA (global_load_lds): a wave instruction moves 64 lanes x 16 bytes
  * (Q6_K weights: x 4 bytes) to consecutive LDS bytes. Two buffers: the next chunk's copy is in
  * flight while the current one computes. */
-__host__ __device__ constexpr int mx_rstride(int type) { return kMxC * mx_recl(type) + (type == 14 ? 64 : 320); }
+#ifndef QMSG_MX_RPAD
+#define QMSG_MX_RPAD 32
+#endif
+__host__ __device__ constexpr int mx_rstride(int type) { return kMxC * mx_recl(type) + QMSG_MX_RPAD; }
 
-template <int TYPE, int WSG, int PPW = 4, int NW = 8>
+template <int TYPE, int WSG, int PPW = 4, int NW = 8, int NT = 2>
 struct MxLayout {
-    static constexpr int RWG = 32 * NW / WSG, SWG = 2 * PPW * WSG, WS = mx_wstride(TYPE);
+    static constexpr int RWG = 16 * NT * NW / WSG, SWG = 2 * PPW * WSG, WS = mx_wstride(TYPE);
     static constexpr int RS = mx_rstride(TYPE);
     static constexpr int WBYTES = RWG * WS, BUF = WBYTES + SWG * RS;
     static constexpr int WUNIT = TYPE == 14 ? 4 : 16;                 /* bytes per lane per DMA   */
@@ -2371,9 +2375,9 @@ struct MxLayout {
     static constexpr int WINSTR = (RWG * WUR + 63) / 64;               /* weight DMA instructions  */
 };
 
-__host__ __device__ constexpr int mx_lds_bytes(int type, int wsg, int ppw = 4, int nw = 8, int nb = 2)
+__host__ __device__ constexpr int mx_lds_bytes(int type, int wsg, int ppw = 4, int nw = 8, int nb = 2, int nt = 2)
 {
-    return nb * ((32 * nw / wsg) * mx_wstride(type) + 2 * ppw * wsg * mx_rstride(type));
+    return nb * ((16 * nt * nw / wsg) * mx_wstride(type) + 2 * ppw * wsg * mx_rstride(type));
 }
 
 /* (x & m) | c in one instruction; m and c in registers (no literal operands in VOP3 here). */
@@ -2484,7 +2488,7 @@ __device__ __forceinline__ void mx_opaque(MxStreams &st)
  * against its two 16-row tiles. SC: the chunk's records all carry d_x 2^24 and B holds the
  * codes 2^-24; else B holds the codes themselves and the chains take d_x unscaled. */
 template <int TYPE, int NP, int PAR, bool SC>
-__device__ __forceinline__ void mx_block(const MxStreams &st, bool kh, f32x4 (&acc)[2][4], float (&cr)[2][4])
+__device__ __forceinline__ void mx_block(const MxStreams &st, bool kh, f32x4 (&acc)[2][kMxNA], float (&cr)[2][4])
 {
     static_assert(TYPE == 2 || TYPE == 3, "Q6_K chunks take mx_chunk_q6");
     constexpr int BB = TYPE == 3 ? 20 : 18, RB = PAR * mx_recl(TYPE), RS = mx_rstride(TYPE);
@@ -2536,7 +2540,7 @@ __device__ __forceinline__ void mx_block(const MxStreams &st, bool kh, f32x4 (&a
  * where it holds x, else the record's zero words. */
 template <int TYPE, int NP, bool SC>
 __device__ __forceinline__ void mx_chunk(const uint8_t *W, const uint8_t *R, int lr, int lg, int jd, bool kh,
-                                         int offa_lo, int offa_hi, f32x4 (&acc)[2][4], float (&cr)[2][4])
+                                         int offa_lo, int offa_hi, f32x4 (&acc)[2][kMxNA], float (&cr)[2][4])
 {
     constexpr int WS = mx_wstride(TYPE), BB = TYPE == 3 ? 20 : 18, QO = TYPE == 3 ? 4 : 2;
     MxStreams st;
@@ -2569,8 +2573,8 @@ __device__ __forceinline__ void mx_chunk(const uint8_t *W, const uint8_t *R, int
  * (tile, quad, block) serve both halves. */
 typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 
-template <int TYPE, int NQ, int BI, bool SC>
-__device__ __forceinline__ void mx_block16(const MxStreams &st, f32x4 (&acc)[2][4], float (&cr)[2][4])
+template <int TYPE, int NQ, int BI, bool SC, int NT>
+__device__ __forceinline__ void mx_block16(const MxStreams &st, f32x4 (&acc)[2][kMxNA], float (&cr)[2][4])
 {
     static_assert(TYPE == 2 || TYPE == 3, "Q4_0 / Q4_1 rows");
     /* block BI of the staged chunk: every stream offset an immediate */
@@ -2578,7 +2582,7 @@ __device__ __forceinline__ void mx_block16(const MxStreams &st, f32x4 (&acc)[2][
     MxB w[2];
     f16x4 b[2][2];
 #pragma unroll
-    for (int t = 0; t < 2; t++) {
+    for (int t = 0; t < NT; t++) {
         w[t] = mx_weights_q4<TYPE, PAR, SC>(st.q + BI * BB, st.dw + BI * BB, t);
         b[t][0] = __builtin_shufflevector(w[t].op, w[t].op, 0, 1, 2, 3);
         b[t][1] = __builtin_shufflevector(w[t].op, w[t].op, 4, 5, 6, 7);
@@ -2603,7 +2607,7 @@ __device__ __forceinline__ void mx_block16(const MxStreams &st, f32x4 (&acc)[2][
         }
         const f16x4 aop = __builtin_bit_cast(f16x4, av);
 #pragma unroll
-        for (int t = 0; t < 2; t++)
+        for (int t = 0; t < NT; t++)
             S[k][t] = __builtin_amdgcn_mfma_f32_16x16x16f16(aop, b[t][h], f32x4{ 0.0f, 0.0f, 0.0f, 0.0f }, 0, 0, 0);
     };
     issue(0, 0);
@@ -2613,16 +2617,16 @@ __device__ __forceinline__ void mx_block16(const MxStreams &st, f32x4 (&acc)[2][
         if (u + 1 < 2 * NQ) issue(u + 1, k ^ 1);
         if (h == 0) {
 #pragma unroll
-            for (int t = 0; t < 2; t++) dd[t] = mix_mul(w[t].dw, xd[q]);
+            for (int t = 0; t < NT; t++) dd[t] = mix_mul(w[t].dw, xd[q]);
         }
 #pragma unroll
-        for (int t = 0; t < 2; t++)
+        for (int t = 0; t < NT; t++)
 #pragma unroll
             for (int v = 0; v < 4; v++)
                 acc[t][2 * q + h][v] = __builtin_fmaf(S[k][t][v], dd[t], acc[t][2 * q + h][v]);
         if (h == 1) {
 #pragma unroll
-            for (int t = 0; t < 2; t++) {
+            for (int t = 0; t < NT; t++) {
                 if constexpr (TYPE == 3) cr[t][q] = mix_fma_hi(w[t].dw, xds[q], cr[t][q]);   /* off += m*ds */
                 else cr[t][q] = mix_fma_lo(w[t].dw, xds[q], cr[t][q]);                     /* corr += d*ds */
             }
@@ -2632,9 +2636,9 @@ __device__ __forceinline__ void mx_block16(const MxStreams &st, f32x4 (&acc)[2][
 
 /* One staged chunk on the 16x16x16 instructions, its 8 blocks unrolled; offa_lo / offa_hi are
  * the lane's A words of the low and high halves (or the shared zero words). */
-template <int TYPE, int NQ, bool SC>
+template <int TYPE, int NQ, bool SC, int NT>
 __device__ __forceinline__ void mx_chunk16(const uint8_t *W, const uint8_t *R, int lr, int lg, int offa_lo,
-                                           int offa_hi, f32x4 (&acc)[2][4], float (&cr)[2][4])
+                                           int offa_hi, f32x4 (&acc)[2][kMxNA], float (&cr)[2][4])
 {
     static_assert(kMxC == 8, "eight blocks per staged chunk");
     constexpr int WS = mx_wstride(TYPE), QO = TYPE == 3 ? 4 : 2;
@@ -2646,21 +2650,21 @@ __device__ __forceinline__ void mx_chunk16(const uint8_t *W, const uint8_t *R, i
     st.dw = (LdsPtr)(W + lr * WS);
     mx_opaque(st);
     /* one block's operands in registers at a time */
-    mx_block16<TYPE, NQ, 0, SC>(st, acc, cr);
+    mx_block16<TYPE, NQ, 0, SC, NT>(st, acc, cr);
     __builtin_amdgcn_sched_barrier(0);
-    mx_block16<TYPE, NQ, 1, SC>(st, acc, cr);
+    mx_block16<TYPE, NQ, 1, SC, NT>(st, acc, cr);
     __builtin_amdgcn_sched_barrier(0);
-    mx_block16<TYPE, NQ, 2, SC>(st, acc, cr);
+    mx_block16<TYPE, NQ, 2, SC, NT>(st, acc, cr);
     __builtin_amdgcn_sched_barrier(0);
-    mx_block16<TYPE, NQ, 3, SC>(st, acc, cr);
+    mx_block16<TYPE, NQ, 3, SC, NT>(st, acc, cr);
     __builtin_amdgcn_sched_barrier(0);
-    mx_block16<TYPE, NQ, 4, SC>(st, acc, cr);
+    mx_block16<TYPE, NQ, 4, SC, NT>(st, acc, cr);
     __builtin_amdgcn_sched_barrier(0);
-    mx_block16<TYPE, NQ, 5, SC>(st, acc, cr);
+    mx_block16<TYPE, NQ, 5, SC, NT>(st, acc, cr);
     __builtin_amdgcn_sched_barrier(0);
-    mx_block16<TYPE, NQ, 6, SC>(st, acc, cr);
+    mx_block16<TYPE, NQ, 6, SC, NT>(st, acc, cr);
     __builtin_amdgcn_sched_barrier(0);
-    mx_block16<TYPE, NQ, 7, SC>(st, acc, cr);
+    mx_block16<TYPE, NQ, 7, SC, NT>(st, acc, cr);
 }
 
 /* A word of a staged Q6_K row at byte off past the row's 4-byte-aligned LDS base (O = 2: the
@@ -2705,7 +2709,7 @@ __device__ __forceinline__ MxB mx_weights_q6(LdsPtr q, LdsPtr rb, int t, int kh)
 
 /* One Q6_K block B of the staged chunk: NP slot pairs against the wave's two 16-row tiles. */
 template <int NP, int O, int B, int TS>
-__device__ __forceinline__ void mx_block_q6(const MxStreams &st, int kh, f32x4 (&acc)[2][4], float (&cr)[2][4])
+__device__ __forceinline__ void mx_block_q6(const MxStreams &st, int kh, f32x4 (&acc)[2][kMxNA], float (&cr)[2][4])
 {
     constexpr int RS = mx_rstride(14), RB = B * mx_recl(14);
     MxB w[2];
@@ -2740,7 +2744,7 @@ __device__ __forceinline__ void mx_block_q6(const MxStreams &st, int kh, f32x4 (
  * the wave's two tiles TS staged rows apart. */
 template <int NP, int O, int TS>
 __device__ __forceinline__ void mx_chunk_q6(const uint8_t *W, const uint8_t *R, int lr, int lg, int kh, int jd,
-                                            int offa_lo, int offa_hi, f32x4 (&acc)[2][4], float (&cr)[2][4])
+                                            int offa_lo, int offa_hi, f32x4 (&acc)[2][kMxNA], float (&cr)[2][4])
 {
     constexpr int WS = mx_wstride(14);
     MxStreams st;
@@ -2771,7 +2775,7 @@ __device__ __forceinline__ void mx_chunk_q6(const uint8_t *W, const uint8_t *R, 
  * half h of the 32-block is sub-block 2g + h, so each instruction's lane sums share one
  * sub-scale per row; one d_w d_x product and one half-sum offset step per (tile, quad, block). */
 template <int NQ, int O, int B, int TS>
-__device__ __forceinline__ void mx_block16_q6(const MxStreams &st, f32x4 (&acc)[2][4], float (&cr)[2][4])
+__device__ __forceinline__ void mx_block16_q6(const MxStreams &st, f32x4 (&acc)[2][kMxNA], float (&cr)[2][4])
 {
     constexpr int RS = mx_rstride(14), RB = B * mx_recl(14);
     MxB w[2];
@@ -2830,7 +2834,7 @@ __device__ __forceinline__ void mx_block16_q6(const MxStreams &st, f32x4 (&acc)[
 /* A staged Q6_K super-block on the 16x16x16 instructions, its 8 blocks unrolled. */
 template <int NQ, int O, int TS>
 __device__ __forceinline__ void mx_chunk16_q6(const uint8_t *W, const uint8_t *R, int lr, int lg, int offa_lo,
-                                              int offa_hi, f32x4 (&acc)[2][4], float (&cr)[2][4])
+                                              int offa_hi, f32x4 (&acc)[2][kMxNA], float (&cr)[2][4])
 {
     constexpr int WS = mx_wstride(14);
     MxStreams st;
@@ -2873,12 +2877,28 @@ __device__ __forceinline__ void mx_wait_barrier()
     asm volatile("s_waitcnt vmcnt(0)\n\ts_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
 
+#ifndef QMSG_MX_WIDE16_SLOTS
+#define QMSG_MX_WIDE16_SLOTS 16
+#endif
+#ifndef QMSG_MX_WIDE16_NB
+#define QMSG_MX_WIDE16_NB 1
+#endif
+#ifndef QMSG_MX_WIDE16_NT
+#define QMSG_MX_WIDE16_NT 2
+#endif
+#ifndef QMSG_MX_WIDE16_NW
+#define QMSG_MX_WIDE16_NW 8
+#endif
+#ifndef QMSG_MX_WIDE16_WAVES
+#define QMSG_MX_WIDE16_WAVES (QMSG_MX_WIDE16_NB == 2 ? 2 : 3)
+#endif
 /* Waves per SIMD the MFMA kernel is built for: six where three double-buffered blocks' LDS
  * fits a CU, else four (the register budget follows: 80 or 128 VGPRs). */
-template <int TYPE, int WSG, int PPW, int NW, int NB>
+template <int TYPE, int WSG, int PPW, int NW, int NB, int NT>
 constexpr int mx_waves()
 {
-    return NB == 1 ? 4 : (160 * 1024 / mx_lds_bytes(TYPE, WSG, PPW, NW, NB)) * NW / 4 >= 6 ? 6 : 4;
+    if (PPW == 8 && NT == 2) return QMSG_MX_WIDE16_WAVES;    /* two tiles x 16 slots per wave: 168 VGPRs */
+    return NB == 1 ? 4 : (160 * 1024 / mx_lds_bytes(TYPE, WSG, PPW, NW, NB, NT)) * NW / 4 >= 6 ? 6 : 4;
 }
 
 /* Gate/up (GU = 1: gate rows against the token's input records, the same up rows, SwiGLU, the
@@ -2886,13 +2906,14 @@ constexpr int mx_waves()
  * staging buffers: 2 (the next chunk's copy in flight while this one computes) or 1 (copy, wait,
  * compute; the other blocks on the CU hide the copy). Several blocks share a CU, which hides the
  * LDS and memory latency. */
-template <int TYPE, int WSG, int GU, int PPW, int NW, int NB>
-__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(mx_waves<TYPE, WSG, PPW, NW, NB>(),
-                                                                         mx_waves<TYPE, WSG, PPW, NW, NB>())))
+template <int TYPE, int WSG, int GU, int PPW, int NW, int NB, int NT>
+__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(mx_waves<TYPE, WSG, PPW, NW, NB, NT>(),
+                                                                         mx_waves<TYPE, WSG, PPW, NW, NB, NT>())))
 void mx_kernel(MxArgs a)
 {
     extern __shared__ __align__(16) uint8_t smem[];
-    using Lay = MxLayout<TYPE, WSG, PPW, NW>;
+    using Lay = MxLayout<TYPE, WSG, PPW, NW, NT>;
+    static_assert(NT == 2 || (NT == 1 && TYPE != 14), "one-tile waves take Q4_0 / Q4_1 rows");
     /* Q6_K gate/up stages its gate rows, then its up rows (so the DMA steps through one matrix
      * at a time); the Q4 kernels interleave them by 16-row groups */
     constexpr bool QS6 = GU && TYPE == 14;
@@ -2904,6 +2925,7 @@ void mx_kernel(MxArgs a)
     constexpr bool X16Q = true;                /* lane sums on the 16x16x16 instructions (waves of 3+ slots) */
 #endif
     constexpr int RWG = Lay::RWG, SWG = Lay::SWG, WS = Lay::WS, BUF = Lay::BUF;
+    static_assert(PPW <= 4 || X16Q, "waves of more than 8 slots take the 16x16x16 quads");
     if ((int)blockIdx.y >= a.S.meta[1]) return;
     const int4 tl = a.S.tiles[blockIdx.y];
     const int e = tl.x, s0 = tl.y + (int)blockIdx.z * SWG, ns = min(SWG, tl.z - s0);
@@ -3017,10 +3039,13 @@ void mx_kernel(MxArgs a)
     const int offa_lo = ja * Lay::RS + ((nz && ka < 4) ? 8 * ka : kMxZero);
     const int offa_hi = ja * Lay::RS + ((nz && ka >= 4) ? 8 * ka : kMxZero);
     /* 16x16x16 instructions: lane row lr is slot lr / 4 of the quad, reference lane lr % 4 (+4 in
-     * the high half); it holds x only if lr % 4 == lg */
+     * the high half); it holds x only if lr % 4 == lg. The other lanes read the zero words of
+     * the quad's slot 3 (one address: a broadcast), whose LDS banks (word mod 64) the lanes
+     * holding x leave free at the 200-word record stride: their words sit at s * RS + 2 lg
+     * (+ 8 in the high half), the zero words at 3 RS + 20. */
     const bool nz4 = (lr & 3) == lg;
-    const int offq_lo = nz4 ? (lr >> 2) * Lay::RS + 8 * lg : kMxZero;
-    const int offq_hi = nz4 ? (lr >> 2) * Lay::RS + 8 * (lg + 4) : kMxZero;
+    const int offq_lo = nz4 ? (lr >> 2) * Lay::RS + 8 * lg : 3 * Lay::RS + kMxZero;
+    const int offq_hi = nz4 ? (lr >> 2) * Lay::RS + 8 * (lg + 4) : 3 * Lay::RS + kMxZero;
     const int nw = min(max(ns - 2 * PPW * ws, 0), 2 * PPW), np = (nw + 1) >> 1;   /* this wave's slot pairs */
 
     /* The whole chunk loop and the row sums for one slot-pair count NP, chosen once per wave,
@@ -3032,15 +3057,15 @@ void mx_kernel(MxArgs a)
         constexpr int NP = decltype(npc)::value;
         constexpr bool SC = decltype(scc)::value;
         constexpr bool X16 = decltype(x16c)::value;     /* NP / 2 quads on 16x16x16, else NP pairs */
-        f32x4 acc[2][4];
+        f32x4 acc[2][kMxNA];
         float cr[2][4];
 #pragma unroll
-        for (int t = 0; t < 2; t++)
+        for (int t = 0; t < 2; t++) {
 #pragma unroll
-            for (int p = 0; p < 4; p++) {
-                acc[t][p] = f32x4{ 0.0f, 0.0f, 0.0f, 0.0f };
-                cr[t][p] = 0.0f;
-            }
+            for (int p = 0; p < kMxNA; p++) acc[t][p] = f32x4{ 0.0f, 0.0f, 0.0f, 0.0f };
+#pragma unroll
+            for (int p = 0; p < 4; p++) cr[t][p] = 0.0f;
+        }
         if (NB == 2) {
             issue(0, 0);
             mx_wait_barrier();
@@ -3054,7 +3079,7 @@ void mx_kernel(MxArgs a)
                 issue(c + 1, buf ^ 1);
             }
             if constexpr (NP > 0) {
-                const uint8_t *Wl = smem + buf * BUF + ((QS6 ? 16 : 32) * wr) * WS;
+                const uint8_t *Wl = smem + buf * BUF + ((QS6 ? 16 : 16 * NT) * wr) * WS;
                 const uint8_t *Rl = smem + buf * BUF + Lay::WBYTES + (2 * PPW * ws) * Lay::RS;
                 if constexpr (TYPE == 14 && X16) {
                     constexpr int TS6 = QS6 ? RWG / 2 : 16;
@@ -3065,7 +3090,7 @@ void mx_kernel(MxArgs a)
                     if (c & 1) mx_chunk_q6<NP, 2, TS6>(Wl, Rl, lr, lg, kh, jd, offa_lo, offa_hi, acc, cr);
                     else mx_chunk_q6<NP, 0, TS6>(Wl, Rl, lr, lg, kh, jd, offa_lo, offa_hi, acc, cr);
                 } else if constexpr (X16) {
-                    mx_chunk16<TYPE, NP / 2, SC>(Wl, Rl, lr, lg, offq_lo, offq_hi, acc, cr);
+                    mx_chunk16<TYPE, NP / 2, SC, NT>(Wl, Rl, lr, lg, offq_lo, offq_hi, acc, cr);
                 } else {
                     mx_chunk<TYPE, NP, SC>(Wl, Rl, lr, lg, jd, kh != 0, offa_lo, offa_hi, acc, cr);
                 }
@@ -3077,20 +3102,21 @@ void mx_kernel(MxArgs a)
             /* hsum256 per (row, slot), all eight chains in the lane: acc[t][2q] lanes 0-3,
              * acc[t][2q + 1] lanes 4-7 */
 #pragma unroll
-            for (int t = 0; t < 2; t++)
+            for (int t = 0; t < NT; t++)
 #pragma unroll
                 for (int q = 0; q < NP / 2; q++) {
                     const f32x4 &lo = acc[t][2 * q], &hi = acc[t][2 * q + 1];
                     const float h = ((lo[0] + hi[0]) + (lo[2] + hi[2])) + ((lo[1] + hi[1]) + (lo[3] + hi[3]));
                     const float val = h - scale * cr[t][q];
-                    const int row = 32 * wr + 16 * t + lr, sl = 2 * PPW * ws + 4 * q + lg;
+                    const int row = 16 * NT * wr + 16 * t + lr, sl = 2 * PPW * ws + 4 * q + lg;
                     if (GU) res[row * (SWG + 1) + sl] = val;
                     else if (sl < ns) a.S.dn[(size_t)(s0 + sl) * a.E + R0 + row] = val;
                 }
             return;
         }
         /* hsum256 per (row, slot): lanes of k-half 0 take the partner lane's k + 4 chains (Q4
-         * types: and, for tile 1, the partner's offset chain) */
+         * types: and, for tile 1, the partner's offset chain); two-tile waves only */
+        static_assert(NT == 2 || X16 || NP == 0, "one-tile waves run quads only");
 #pragma unroll
         for (int t = 0; t < 2; t++)
 #pragma unroll
@@ -3120,9 +3146,11 @@ void mx_kernel(MxArgs a)
             /* quads of slots (NP = 2 x quads); a wave of one or two slots keeps the pair
              * instructions, on which a quad's padding would double its work */
             const int nq = (nw + 3) >> 2;
-            if (PPW == 4 && nq == 2) run(std::integral_constant<int, PPW == 4 ? 4 : 0>{}, scc, Q{});
-            else if (nw > 2) run(std::integral_constant<int, 2>{}, scc, Q{});
-            else if (nw > 0) run(std::integral_constant<int, 1>{}, scc, P{});
+            if (PPW == 8 && nq == 4) run(std::integral_constant<int, PPW == 8 ? 8 : 0>{}, scc, Q{});
+            else if (PPW == 8 && nq == 3) run(std::integral_constant<int, PPW == 8 ? 6 : 0>{}, scc, Q{});
+            else if (PPW >= 4 && nq == 2) run(std::integral_constant<int, PPW >= 4 ? 4 : 0>{}, scc, Q{});
+            else if (nw > 2 || (NT == 1 && nw > 0)) run(std::integral_constant<int, 2>{}, scc, Q{});
+            else if (nw > 0) run(std::integral_constant<int, NT == 2 ? 1 : 0>{}, scc, P{});
             else run(std::integral_constant<int, 0>{}, scc, P{});
         } else {
             if (PPW == 4 && np == 4) run(std::integral_constant<int, PPW == 4 ? 4 : 0>{}, scc, P{});
@@ -3195,23 +3223,24 @@ static_assert(2 * mx_lds_bytes(14, 2) <= 160 * 1024, "two Q6_K blocks per CU");
  * 12, 373 / 375 at 16; Q6_K 362 / 460 at 8, 496 / 549 at 12, 701 / 719 at 16. */
 constexpr int kMxWideSlots = 16;
 constexpr int kMxWideSlotsGateUp = 12;
-enum MxShape { kMxNarrow, kMxMid, kMxWide };
+enum MxShape { kMxNarrow, kMxMid, kMxWide, kMxWide16 };
 
 static MxShape mx_shape(const Shape &s, int T, int gu, int type)
 {
     const long NS = (long)T * s.K, act = s.X < NS ? s.X : NS;
     const long wide_slots = gu ? kMxWideSlotsGateUp : kMxWideSlots;
+    if (type != 14 && QMSG_MX_WIDE16_SLOTS > 0 && NS >= QMSG_MX_WIDE16_SLOTS * act) return kMxWide16;
     if (NS >= wide_slots * act) return kMxWide;
     const long narrow_quarters = gu ? 12 : (type == 14 ? 10 : 14);
     return 4 * NS < narrow_quarters * act ? kMxNarrow : kMxMid;
 }
 
-template <int TYPE, int GU, int WSG, int PPW, int NW, int NB = 2>
+template <int TYPE, int GU, int WSG, int PPW, int NW, int NB = 2, int NT = 2>
 static void launch_mx_shape(const MxArgs &a, int rows, int maxt, hipStream_t st)
 {
-    using Lay = MxLayout<TYPE, WSG, PPW, NW>;
-    const size_t lds = (size_t)mx_lds_bytes(TYPE, WSG, PPW, NW, NB);
-    QLAUNCH(GU ? "gateup" : "down", (mx_kernel<TYPE, WSG, GU, PPW, NW, NB>),
+    using Lay = MxLayout<TYPE, WSG, PPW, NW, NT>;
+    const size_t lds = (size_t)mx_lds_bytes(TYPE, WSG, PPW, NW, NB, NT);
+    QLAUNCH(GU ? "gateup" : "down", (mx_kernel<TYPE, WSG, GU, PPW, NW, NB, NT>),
             dim3(rows / (GU ? Lay::RWG / 2 : Lay::RWG), maxt, kTileN / Lay::SWG), dim3(64 * NW), lds, st, a);
 }
 
@@ -3228,6 +3257,13 @@ template <int TYPE, int GU>
 static void launch_mx(const MxArgs &a, int rows, int maxt, MxShape shape, hipStream_t st)
 {
     if (shape == kMxWide) launch_mx_shape<TYPE, GU, 2, 4, 8>(a, rows, maxt, st);
+    else if (shape == kMxWide16) {
+        /* Q4_0 / Q4_1 only (mx_shape) */
+        if constexpr (TYPE != 14 && QMSG_MX_WIDE16_NT == 1)
+            launch_mx_shape<TYPE, GU, 1, 8, QMSG_MX_WIDE16_NW, QMSG_MX_WIDE16_NB, 1>(a, rows, maxt, st);
+        else if constexpr (TYPE != 14)
+            launch_mx_shape<TYPE, GU, 1, 8, 4, QMSG_MX_WIDE16_NB>(a, rows, maxt, st);
+    }
     else if (shape == kMxNarrow) launch_mx_shape<TYPE, GU, 1, 2, 4, (!GU && TYPE == 14) ? 1 : 2>(a, rows, maxt, st);
     else launch_mx_shape<TYPE, GU, 1, 4, 4, 1>(a, rows, maxt, st);
 }
