@@ -143,8 +143,10 @@ hipError_t launch_select(const Shape &s, const Scratch &S, int T, int gateup_rou
 /* Whether gate and up take the streaming gate/up kernel (launch_gateup_exact): one type, Q4_0,
  * Q4_1, or Q6_K with rows a multiple of 4 bytes long. */
 bool gateup_streams(const LayerDev &L);
+/* quant_act: batches (not the one-token routing kernel) in blocks of 32 rows that also store
+ * the activations' int8 blocks (aq, aqk) for the down kernel. */
 hipError_t launch_gateup_exact(const Shape &s, const LayerDev &L, const Scratch &S, int T, int debug, int n_cu,
-                               hipStream_t st);
+                               int quant_act, hipStream_t st);
 /* The expert products on the matrix cores (order-exact): gate/up, then down and the combine.
  * mx_supported: whether the layer's types and shape fit the MFMA kernels (gate and up of one
  * type: Q4_0, Q4_1 or Q6_K;
@@ -157,6 +159,10 @@ hipError_t launch_experts_mx(const Shape &s, const LayerDev &L, const Scratch &S
 hipError_t launch_down_mx(const Shape &s, const LayerDev &L, const Scratch &S, float *out, int T, hipStream_t st);
 /* Gate/up rows of Q4_1 / Q6_K (or mixed) layers by slot tiles, then the SwiGLU. */
 hipError_t launch_gateup_tiles(const Shape &s, const LayerDev &L, const Scratch &S, int T, hipStream_t st);
+/* Whether two to four tokens take the small-batch down kernel. */
+bool down_small_fits(const Shape &s, const LayerDev &L, int T);
+/* quant: the activations' int8 blocks are formed here (else read from aqk, where gate/up or the
+ * MFMA gate/up stored them). */
 hipError_t launch_down_exact(const Shape &s, const LayerDev &L, const Scratch &S, float *out, int T, int quant,
                              hipStream_t st);
 /* The whole layer in the reference's --exact mode (fp32 dequantised rows, fp32 activations). */

@@ -217,6 +217,14 @@ __device__ __forceinline__ int wave_scan_add(int v)
     return v;
 }
 
+/* A 64-bit value of lane l (l wave-uniform), as a wave-uniform value. */
+__device__ __forceinline__ uint64_t readlane_u64(uint64_t v, int l)
+{
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)v, l);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(v >> 32), l);
+    return ((uint64_t)hi << 32) | lo;
+}
+
 /* ------------------------------------------------------------------ route ---- */
 
 struct RouteArgs {
@@ -468,12 +476,11 @@ struct SelectArgs {
  * threads per token: P[e] = exp(l_e - max) / z in LDS with z summed sequentially in expert
  * order; two threads per expert count the experts that precede it; wsum is summed in
  * selection order. */
-__device__ void topk_token(const SelectArgs &a, int t, double *P, int *part, int *selb)
+__device__ void topk_token(const SelectArgs &a, int t, int tid, double *P, int *part, int *selb, double *sh)
 {
-    const int X = a.X, K = a.K, tid = threadIdx.x;
+    const int X = a.X, K = a.K;
     const float *lt = a.S.logits + (size_t)t * X;
-    __shared__ double red[4];
-    __shared__ double zs;
+    double *red = sh, &zs = sh[4];                   /* LDS: 4 wave maxima, then z and wsum */
     double mx = -__builtin_inf();
     for (int e = tid; e < X; e += 256) {
         const double v = (double)lt[e];
@@ -486,9 +493,11 @@ __device__ void topk_token(const SelectArgs &a, int t, double *P, int *part, int
     }
     if ((tid & 63) == 0) red[tid >> 6] = mx;
     __syncthreads();
+    PHASE(0, 1);
     mx = fmax(fmax(red[0], red[1]), fmax(red[2], red[3]));
     for (int e = tid; e < X; e += 256) P[e] = qmsg_exp(P[e] - mx);
     __syncthreads();
+    PHASE(0, 2);
     if (tid == 0) {
         double z = 0.0;
 #pragma unroll 16
@@ -497,6 +506,7 @@ __device__ void topk_token(const SelectArgs &a, int t, double *P, int *part, int
     }
     __syncthreads();
     const double z = zs;
+    PHASE(0, 3);
     for (int e = tid; e < X; e += 256) P[e] /= z;
     __syncthreads();
     /* rank(e) = #{e' : P[e'] > P[e]} + #{e' < e : P[e'] == P[e]}, split over two threads.
@@ -516,6 +526,7 @@ __device__ void topk_token(const SelectArgs &a, int t, double *P, int *part, int
         part[w] = r;
     }
     __syncthreads();
+    PHASE(0, 4);
     if (nan_p) {
         if (tid < K) selb[tid] = tid;
     } else {
@@ -636,8 +647,11 @@ __global__ __launch_bounds__(256) void select_kernel(SelectArgs a, int do_dispat
     __shared__ int selb[64];
     __shared__ int tok[kMaxExperts];
     __shared__ int last;
+    __shared__ double sh[5];
     const int t = blockIdx.x;
-    if (t < a.T) topk_token(a, t, P, part, selb);
+    PHASE(0, 0);
+    if (t < a.T) topk_token(a, t, threadIdx.x, P, part, selb, sh);
+    PHASE(0, 5);
     if (!do_dispatch) return;
     if (gridDim.x > 1) {
         if (threadIdx.x < 64) __threadfence();          /* sel/wt were written by wave 0 */
@@ -647,8 +661,10 @@ __global__ __launch_bounds__(256) void select_kernel(SelectArgs a, int do_dispat
         if (!last) return;
         __threadfence();
     }
+    PHASE(0, 6);
     if (threadIdx.x < 64) dispatch_slots(a, a.S.sel, part, part + kMaxExperts, tok);
     if (gridDim.x > 1 && threadIdx.x == 0) __hip_atomic_store(a.S.meta + 4, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    PHASE(0, 7);
 }
 
 __global__ __launch_bounds__(64) void dispatch_kernel(SelectArgs a)
@@ -1147,6 +1163,7 @@ struct GateUpArgs {
     const uint8_t *gate, *up;
     uint64_t rb, eb;
     int E, F, K, X, T, debug;
+    int quant_act;     /* blocks of 32 rows also store the int8 activation blocks (aq, aqk) */
     Scratch S;
 };
 
@@ -1425,13 +1442,33 @@ __global__ __launch_bounds__(64 * W) void gateup_kernel(GateUpArgs a)
         for (int i = tid; i < nt * R; i += NTH) {
             const int n = i / R, l = i - n * R, s = g0 + n;
             const float g = res[n * 2 * R + l], u = res[n * 2 * R + R + l];
-            a.S.act[(size_t)s * F + r0 + l] = silu_ref(g) * u;
+            const float av = silu_ref(g) * u;
+            a.S.act[(size_t)s * F + r0 + l] = av;
             if (a.debug) {
                 a.S.gu[(size_t)s * 2 * F + r0 + l] = g;
                 a.S.gu[(size_t)s * 2 * F + F + r0 + l] = u;
             }
+            if (R % 32 == 0 && a.quant_act) res[n * 2 * R + l] = av;
         }
         __syncthreads();
+        if constexpr (R % 32 == 0 && !SEL) {
+            /* the int8 blocks of the block's whole 32-row groups (src/model.c:996-997), as
+             * act_quant_kernel forms them */
+            if (a.quant_act) {
+                const int nbF = F >> 5;
+                for (int i = tid; i < nt * (R / 32); i += NTH) {
+                    const int n = i / (R / 32), g = i - n * (R / 32), s = g0 + n, blk = (r0 >> 5) + g;
+                    float v[32];
+#pragma unroll
+                    for (int j = 0; j < 32; j++) v[j] = res[n * 2 * R + 32 * g + j];
+                    const Q8Vals q = quantize_block(v);
+                    store_q8(q, a.S.aq + (size_t)s * nbF + blk);
+                    store_pair_half(q, (uint32_t *)(a.S.aqk + ((size_t)s * (nbF >> 1) + (blk >> 1)) * kPairBytes),
+                                    blk & 1);
+                }
+                __syncthreads();
+            }
+        }
     }
     PHASE(1024, 5);
 }
@@ -1467,11 +1504,11 @@ static void launch_gateup_type(const GateUpArgs &a, int sel, int NT, int W, int 
  * number of active experts, puts the least work on the busiest CU (one block per CU per
  * pass); ties go to the larger block. Slot-tile grids (batch) leave out W = 6, measured
  * 20-60 % slower there at the 235B shape (W = 2, 3, 4 within 2 % of each other). */
-int gateup_waves(int F, int max_active, int n_cu, int batch)
+int gateup_waves(int F, int max_active, int n_cu, int batch, int rows32)
 {
     int best = 0, best_cost = 0;
     for (int W : { 6, 4, 3, 2 }) {
-        if (F % (8 * W) || (batch && W == 6)) continue;
+        if (F % (8 * W) || (batch && W == 6) || (rows32 && (8 * W) % 32)) continue;
         const long nblk = (long)(F / (8 * W)) * max_active;
         const long cost = ((nblk + n_cu - 1) / n_cu) * W;
         if (!best || cost < best_cost) { best = W; best_cost = (int)cost; }
@@ -1486,9 +1523,10 @@ bool gateup_streams(const LayerDev &L)
 }
 
 hipError_t launch_gateup_exact(const Shape &s, const LayerDev &L, const Scratch &S, int T, int debug, int n_cu,
-                               hipStream_t st)
+                               int quant_act, hipStream_t st)
 {
     GateUpArgs a;
+    a.quant_act = quant_act;
     a.gate = L.gate;
     a.up = L.up;
     a.rb = L.gate_rb;
@@ -1511,7 +1549,7 @@ hipError_t launch_gateup_exact(const Shape &s, const LayerDev &L, const Scratch 
     const int maxact = s.X < T * s.K ? s.X : T * s.K;
     const int sel = use_small_route(T, s.K);
     const int rows_y = sel ? maxact : maxact + T * s.K / kTileN + 1;   /* active experts, or slot tiles */
-    const int W = gateup_waves(s.F, rows_y, n_cu, !sel);
+    const int W = gateup_waves(s.F, rows_y, n_cu, !sel, quant_act);
     if (!W) return hipErrorInvalidValue;
     dim3 grid(s.F / (8 * W), rows_y);
     if (!gateup_streams(L)) return hipErrorInvalidValue;
@@ -1530,6 +1568,7 @@ struct DownArgs {
     const uint8_t *down;
     uint64_t rb, eb;
     int E, F, K, T, X;
+    int quant;         /* the kernel forms the activations' int8 blocks (else they are in aqk) */
     float *out;
     Scratch S;
 };
@@ -1887,18 +1926,22 @@ __global__ __launch_bounds__(32 * RD) void down_small_kernel(DownArgs a)
     uint8_t *wbuf = smem + wave * 16 * WS;
     uint8_t *xbuf = smem + NW * 16 * WS;              /* [NS][xrec]                           */
     float *dnl = (float *)(xbuf + (size_t)NS * xrec); /* [NS][RD]                             */
+    PHASE(2048, 0);
 
     /* the wave's first expert (wave-uniform scalar loads first, as in the one-token kernel) */
     const int na = a.S.meta[0];
     int j = wave;
     int4 wk = j < na ? a.S.work[j] : make_int4(-1, 0, 0, 0);
     const int nqb = NS * nbF;
+    const bool quant = a.quant != 0;
     float4 av[QPT][8];
+    if (quant) {
 #pragma unroll
-    for (int u = 0; u < QPT; u++) {
-        const float4 *src = (const float4 *)(a.S.act + (size_t)min(tid + NTH * u, nqb - 1) * 32);
+        for (int u = 0; u < QPT; u++) {
+            const float4 *src = (const float4 *)(a.S.act + (size_t)min(tid + NTH * u, nqb - 1) * 32);
 #pragma unroll
-        for (int q = 0; q < 8; q++) av[u][q] = src[q];
+            for (int q = 0; q < 8; q++) av[u][q] = src[q];
+        }
     }
     const uint8_t *b = a.down + (size_t)max(wk.x, 0) * a.eb + (size_t)r0 * a.rb;
     __builtin_amdgcn_sched_barrier(0);
@@ -1918,7 +1961,7 @@ __global__ __launch_bounds__(32 * RD) void down_small_kernel(DownArgs a)
         for (int d = 0; d < D; d++)
             if (d < nchunk) load_chunk(d, wv[d]);
     }
-    auto quant = [&](int qb, const float *v) {
+    auto quant_blk = [&](int qb, const float *v) {
         const int sl = qb / nbF, blk = qb - sl * nbF;
         const Q8Vals q = quantize_block(v);
         store_pair_half(q, (uint32_t *)(xbuf + (size_t)sl * xrec + (size_t)(blk >> 1) * kPairBytes), blk & 1);
@@ -1927,28 +1970,35 @@ __global__ __launch_bounds__(32 * RD) void down_small_kernel(DownArgs a)
             store_pair_half(q, (uint32_t *)(a.S.aqk + ((size_t)sl * (nbF >> 1) + (blk >> 1)) * kPairBytes), blk & 1);
         }
     };
+    if (quant) {
 #pragma unroll
-    for (int u = 0; u < QPT; u++) {
-        const int qb = tid + NTH * u;
-        if (qb < nqb) {
-            float v[32];
+        for (int u = 0; u < QPT; u++) {
+            const int qb = tid + NTH * u;
+            if (qb < nqb) {
+                float v[32];
 #pragma unroll
-            for (int q = 0; q < 8; q++) {
-                v[4 * q] = av[u][q].x; v[4 * q + 1] = av[u][q].y; v[4 * q + 2] = av[u][q].z; v[4 * q + 3] = av[u][q].w;
+                for (int q = 0; q < 8; q++) {
+                    v[4 * q] = av[u][q].x; v[4 * q + 1] = av[u][q].y; v[4 * q + 2] = av[u][q].z; v[4 * q + 3] = av[u][q].w;
+                }
+                quant_blk(qb, v);
             }
-            quant(qb, v);
         }
-    }
-    for (int qb = tid + NTH * QPT; qb < nqb; qb += NTH) {   /* past the register share */
-        float v[32];
-        const float4 *src = (const float4 *)(a.S.act + (size_t)qb * 32);
-        for (int q = 0; q < 8; q++) {
-            const float4 f = src[q];
-            v[4 * q] = f.x; v[4 * q + 1] = f.y; v[4 * q + 2] = f.z; v[4 * q + 3] = f.w;
+        for (int qb = tid + NTH * QPT; qb < nqb; qb += NTH) {   /* past the register share */
+            float v[32];
+            const float4 *src = (const float4 *)(a.S.act + (size_t)qb * 32);
+            for (int q = 0; q < 8; q++) {
+                const float4 f = src[q];
+                v[4 * q] = f.x; v[4 * q + 1] = f.y; v[4 * q + 2] = f.z; v[4 * q + 3] = f.w;
+            }
+            quant_blk(qb, v);
         }
-        quant(qb, v);
+    } else {
+        /* the pair records gate/up stored: [slot][F/64] in both places */
+        const int n16 = (int)((size_t)NS * xrec / 16);
+        for (int i = tid; i < n16; i += NTH) ((u32x4 *)xbuf)[i] = ((const u32x4 *)a.S.aqk)[i];
     }
     __syncthreads();
+    PHASE(2048, 1);
     const bool can_pre = nchunk % D == 0;             /* chunk c + D - nchunk lands in c's registers */
     while (wk.x >= 0) {
         const int jn = j + NW;
@@ -2022,7 +2072,9 @@ __global__ __launch_bounds__(32 * RD) void down_small_kernel(DownArgs a)
                 if (d < nchunk) load_chunk(d, wv[d]);
         }
     }
+    PHASE(2048, 2);
     __syncthreads();
+    PHASE(2048, 3);
     for (int i = tid; i < T * RD; i += NTH) {
         const int t = i / RD, r = i - t * RD;
         float o = 0.0f;
@@ -2107,6 +2159,21 @@ constexpr int kDownTileRowsQ6K = 32;
  * 16: 256 blocks of 8 waves, half the activation reads). */
 constexpr int kDownT1Rows = 16;
 
+#ifndef QMSG_DOWN_SMALL_D
+#define QMSG_DOWN_SMALL_D 3
+#endif
+bool down_small_fits(const Shape &s, const LayerDev &L, int T)
+{
+    constexpr int RD = kDownT1Rows, CB = 8;
+    const int bb = L.down_type == 3 ? 20 : 18;
+    const size_t xrec = (size_t)(s.F / 64) * kPairBytes;
+    const size_t ws = L.down_type == 14 ? 220 : (size_t)CB * bb + (((CB * bb / 16) & 1) ? 0 : 16);
+    const size_t lds_s = (size_t)(RD / 2) * 16 * ws + (size_t)T * s.K * (xrec + RD * 4);
+    const bool t1_type = L.down_type == 2 || L.down_type == 3 || (L.down_type == 14 && L.down_rb % 4 == 0);
+    return T >= 2 && T <= 4 && T * s.K <= kSmallDownNS && t1_type && s.F % 256 == 0 && s.E % RD == 0 &&
+           lds_s <= 160 * 1024;
+}
+
 hipError_t launch_down_exact(const Shape &s, const LayerDev &L, const Scratch &S, float *out, int T, int quant,
                              hipStream_t st)
 {
@@ -2120,6 +2187,7 @@ hipError_t launch_down_exact(const Shape &s, const LayerDev &L, const Scratch &S
     a.T = T;
     a.X = s.X;
     a.out = out;
+    a.quant = quant;
     a.S = S;
     /* one token: each wave streams its own experts' rows (Q4_0 / Q4_1); RD output rows per
      * block, RD/2 waves */
@@ -2138,14 +2206,14 @@ hipError_t launch_down_exact(const Shape &s, const LayerDev &L, const Scratch &S
         else QLAUNCH("down", (down_t1_kernel<2, CB, 3, RD>), grid, block, lds_t1, st, a);
         return hipGetLastError();
     }
-    /* two to four tokens: the same layout, each wave streaming several experts */
-    const size_t lds_s = (size_t)(RD / 2) * 16 * ws + (size_t)T * s.K * (xrec + RD * 4);
-    if (T >= 2 && T <= 4 && T * s.K <= kSmallDownNS && quant && t1_type && s.F % 256 == 0 && s.E % RD == 0 &&
-        lds_s <= 160 * 1024) {
+    /* two to four tokens: the same layout, each wave streaming several experts (the
+     * activations' records formed in the kernel, or read from aqk) */
+    if (down_small_fits(s, L, T)) {
+        const size_t lds_s = (size_t)(RD / 2) * 16 * ws + (size_t)T * s.K * (xrec + RD * 4);
         const dim3 grid(s.E / RD), block(32 * RD);
         if (L.down_type == 14) QLAUNCH("down", (down_small_kernel<14, CB, 3, RD>), grid, block, lds_s, st, a);
-        else if (L.down_type == 3) QLAUNCH("down", (down_small_kernel<3, CB, 3, RD>), grid, block, lds_s, st, a);
-        else QLAUNCH("down", (down_small_kernel<2, CB, 3, RD>), grid, block, lds_s, st, a);
+        else if (L.down_type == 3) QLAUNCH("down", (down_small_kernel<3, CB, QMSG_DOWN_SMALL_D, RD>), grid, block, lds_s, st, a);
+        else QLAUNCH("down", (down_small_kernel<2, CB, QMSG_DOWN_SMALL_D, RD>), grid, block, lds_s, st, a);
         return hipGetLastError();
     }
     /* slot tiles: the activations' int8 records first (unless the MFMA gate/up wrote them) */
@@ -4406,13 +4474,6 @@ __device__ __forceinline__ void column_run(const double *qt, int col, int C, dou
     }
 }
 
-/* A 64-bit value of lane l (l wave-uniform), as a wave-uniform value. */
-__device__ __forceinline__ uint64_t readlane_u64(uint64_t v, int l)
-{
-    const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)v, l);
-    const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(v >> 32), l);
-    return ((uint64_t)hi << 32) | lo;
-}
 
 __device__ __forceinline__ uint64_t dbits(double v) { return (uint64_t)__double_as_longlong(v); }
 
