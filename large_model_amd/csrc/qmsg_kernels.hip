@@ -4654,12 +4654,15 @@ __device__ __forceinline__ double wave_sum_any(double v)
  * by E - j (sum_w); same(lo, hi) tells whether every element this thread holds gives one
  * float (float)(x * inv) at inv = lo and at inv = hi, and fill() stores this thread's squares
  * into LDS at q in the layout the ordered sum reads (norm_store), called only when the sum is
- * formed in order. All 256 threads of the block call it, with the same E, eps and walk; part
- * is 8 doubles of LDS and inv_sh one. A row that forms its sum in order is counted into
- * *walked when walked is not null. */
-template <class Same, class Fill>
+ * formed in order. stage(v) runs with the bracket's end before the block's vote on it (its
+ * LDS writes are visible to the block after the call when *open_out is false); when the vote
+ * opens the row, the caller stages again with the returned inv. All 256 threads of the block
+ * call it, with the same E, eps and walk; part is 8 doubles of LDS and inv_sh one. A row that
+ * forms its sum in order is counted into *walked when walked is not null. */
+template <class Same, class Fill, class Stage>
 __device__ double norm_inv(double sum_s, double sum_w, const double *q, int E, float eps, int walk,
-                           unsigned long long *walked, Same same, Fill fill, double *part, double *inv_sh)
+                           unsigned long long *walked, Same same, Fill fill, double *part, double *inv_sh,
+                           Stage stage, bool &open_out)
 {
     const int tid = threadIdx.x;
     sum_s = wave_sum_any(sum_s);
@@ -4680,8 +4683,11 @@ __device__ double norm_inv(double sum_s, double sum_w, const double *q, int E, f
         const double err = W * 0x1.00001p-53 + S * ((double)(E / 256 + 16) * 0x1p-52);
         inv_lo = 1.0 / sqrt((S + err) / E + (double)eps);
         const double inv_hi = 1.0 / sqrt((S - err) / E + (double)eps);
-        open = __syncthreads_or(!same(inv_lo, inv_hi));
+        const bool differ = !same(inv_lo, inv_hi);
+        stage(inv_lo);                 /* the caller's use of the bracket's answer, before the vote */
+        open = __syncthreads_or(differ);
     }
+    open_out = open;
     if (!open) return inv_lo;
     fill();
     __syncthreads();
@@ -4816,7 +4822,9 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(float *x, const float *add
             for (int i = tid; i < n4; i += 256) norm_store(row[i], i, E, q);
         }
     };
-    const double v = norm_inv(sum_s, sum_w, q, E, eps, walk, walked, same, fill, part, &inv_sh);
+    bool open;
+    const double v = norm_inv(sum_s, sum_w, q, E, eps, walk, walked, same, fill, part, &inv_sh, [](double) {},
+                              open);
     PHASE(3072, 6);
     if (held) {
 #pragma unroll
@@ -4886,23 +4894,33 @@ __global__ __launch_bounds__(256) void route_norm_kernel(RouteArgs a, NormIn n)
             if (i < n4) norm_store(xv[m], i, E, q);
         }
     };
-    const double v = norm_inv(sum_s, sum_w, q, E, n.eps, n.walk, router ? nullptr : n.walked, same, fill, part,
-                              &inv_sh);
     float4 xn[NV];
-#pragma unroll
-    for (int m = 0; m < NV; m++) xn[m] = norm_apply(xv[m], wv[m], v);
-    if (router) {
-        /* float4 j holds elements 4j .. 4j+3: chains 4(j%4) .. 4(j%4)+3, step j/4 */
+    float4 *lin = (float4 *)buf;
+    /* router blocks: the router row and xn chain-major (float4 j holds elements 4j .. 4j+3:
+     * chains 4(j%4) .. 4(j%4)+3, step j/4); the quantiser block: xn in order */
+    auto stage = [&](double v) {
 #pragma unroll
         for (int m = 0; m < NV; m++) {
             const int j = tid + 256 * m;
-            if (j < n4) {
+            if (j >= n4) continue;
+            xn[m] = norm_apply(xv[m], wv[m], v);
+            if (router) {
                 float *dw = buf + (4 * (j & 3)) * CS + (j >> 2), *dx = dw + 16 * CS;
                 dw[0] = rv[m].x; dw[CS] = rv[m].y; dw[2 * CS] = rv[m].z; dw[3 * CS] = rv[m].w;
                 dx[0] = xn[m].x; dx[CS] = xn[m].y; dx[2 * CS] = xn[m].z; dx[3 * CS] = xn[m].w;
+            } else {
+                lin[j] = xn[m];
             }
         }
+    };
+    bool open;
+    const double v = norm_inv(sum_s, sum_w, q, E, n.eps, n.walk, router ? nullptr : n.walked, same, fill, part,
+                              &inv_sh, stage, open);
+    if (open) {
+        stage(v);
         __syncthreads();
+    }
+    if (router) {
         if (tid < 16) {
             const float4 *wr = (const float4 *)(buf + tid * CS), *xr = (const float4 *)(buf + (16 + tid) * CS);
             const int q1 = E / 64;                   /* float4 steps of one chain */
@@ -4914,17 +4932,14 @@ __global__ __launch_bounds__(256) void route_norm_kernel(RouteArgs a, NormIn n)
         }
         return;
     }
-    float4 *lin = (float4 *)buf;
 #pragma unroll
     for (int m = 0; m < NV; m++) {
         const int i = tid + 256 * m;
         if (i < n4) {
             if (a4) ((float4 *)n.h_out)[i] = xv[m];
             ((float4 *)n.xn_out)[i] = xn[m];
-            lin[i] = xn[m];
         }
     }
-    __syncthreads();
     const int nbE = E >> 5;
     if (tid < nbE) {
         float vb[32];
