@@ -2946,7 +2946,7 @@ __device__ __forceinline__ void mx_wait_barrier()
 }
 
 #ifndef QMSG_MX_WIDE16_SLOTS
-#define QMSG_MX_WIDE16_SLOTS 16
+#define QMSG_MX_WIDE16_SLOTS 8
 #endif
 #ifndef QMSG_MX_WIDE16_NB
 #define QMSG_MX_WIDE16_NB 1
@@ -3277,7 +3277,13 @@ static_assert(2 * mx_lds_bytes(14, 2) <= 160 * 1024, "two Q6_K blocks per CU");
 /* Block shapes, chosen per kernel by the batch's slots per active expert r (the more slots a
  * block takes, the more of them are padding on sparse tiles; the fewer, the fewer MFMAs each
  * staged weight row feeds). A block's waves form row groups of 32 rows x slot groups:
- *   wide   (gate/up r >= 12, down r >= 16): 8 waves, 4 row groups x 2 slot groups of 4 pairs:
+ *   wide16 (Q4_0 / Q4_1, r >= 8): 4 waves, 4 row groups of 8 pairs: 128 rows x 16 slots, each
+ *          wave's unpacked weight tiles feeding four quads; one staging buffer, three waves
+ *          per SIMD. Against the shapes below at the 235B shape (us, gate/up / down): 321 / 155
+ *          against 350 / 158 at r = 8, 353 / 171 against 422 / 196 at 10, 384 / 186 against
+ *          403 / 213 at 12, 719 / 348 against 734 / 364 at 24; 286 / 138 against 275 / 128 at
+ *          6 and 262 / 125 against 239 / 114 at 4, where it is not taken;
+ *   wide   (other types: gate/up r >= 12, down r >= 16): 8 waves, 4 row groups x 2 slot groups of 4 pairs:
  *          128 rows x 16 slots, two staging buffers;
  *   mid:   4 waves, 4 row groups x 1 slot group of 4 pairs: 128 rows x 8 slots, one staging
  *          buffer (four blocks per CU);

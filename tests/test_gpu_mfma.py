@@ -5,8 +5,8 @@ The MFMA kernels run for QMSG_PATH_MFMA at any batch of two or more tokens; the 
 takes them for gate/up from 1.25 slots per active expert and for down from 64 slots (Q6_K
 down rows: 32), so the 16-token and the 8-token Q6_K cases also run the row-kernel gate/up
 followed by the MFMA down.
-The block shapes (4-, 8- and 16-slot blocks, chosen per kernel by slots per expert) are all
-covered. Cases cover Q4_0 / Q4_1 /
+The block shapes (4-, 8- and 16-slot blocks, and the Q4 waves of 16 slots from 8 slots per
+expert, chosen per kernel by slots per expert) are all covered. Cases cover Q4_0 / Q4_1 /
 Q6_K down rows, tiles of up to 32 slots run as 16-slot blocks, odd slot
 counts per expert, the Zipf-skewed 512-token prefill, shapes whose down rows fall back to the
 exact kernel (F/32 not a whole number of 8-block chunks), and batches of alternating sizes on
@@ -21,7 +21,7 @@ pytestmark = pytest.mark.gpu
 CASES = [
     # name, E, X, K, F, T, seed, down_type, zipf
     ("q30b_t64", 2048, 128, 8, 768, 64, 1, orc.T_Q4_0, False),
-    ("q30b_t128", 2048, 128, 8, 768, 128, 11, orc.T_Q4_0, False),    # 8 slots per expert: 8-slot blocks
+    ("q30b_t128", 2048, 128, 8, 768, 128, 11, orc.T_Q4_0, False),    # 8 slots per expert: 16-slot waves from here
     ("q235b_t64", 4096, 128, 8, 1536, 64, 2, orc.T_Q4_0, False),
     ("q235b_t16", 4096, 128, 8, 1536, 16, 12, orc.T_Q4_0, False),    # about one slot per expert
     ("q235b_t33", 4096, 128, 8, 1536, 33, 3, orc.T_Q4_0, False),
