@@ -214,10 +214,9 @@ int qmsg_create(qmsg_ctx **out, int device, const qmsg_cfg *cfg, int n_layer, in
         return fail(nullptr, QMSG_E_INVALID, "qmsg_create: bad shape E=%d X=%d K=%d F=%d layers=%d T=%d", E, X, K, F,
                     n_layer, max_tokens);
     /* The reference's integer fast path needs E % 256 == 0 and F % 32 == 0
-     * (src/model.c:1090-1093). The kernels also pair 32-blocks (F % 64 == 0), run four router
-     * dots in 16-expert tiles (X % 16 == 0) and keep per-expert state in 256-entry LDS arrays
-     * (X <= 256). */
-    if (E % 256 || F % 64 || X % 16 || X > kMaxExperts || K > 64)
+     * (src/model.c:1090-1093). The kernels also pair 32-blocks (F % 64 == 0) and keep
+     * per-expert state in 256-entry LDS arrays (X <= 256). */
+    if (E % 256 || F % 64 || X > kMaxExperts || K > 64)
         return fail(nullptr, QMSG_E_UNSUPPORTED, "qmsg_create: unsupported shape E=%d X=%d K=%d F=%d", E, X, K, F);
     int ndev = 0;
     if (hipGetDeviceCount(&ndev) != hipSuccess || device < 0 || device >= ndev)
@@ -816,7 +815,10 @@ static int run_layer_s(qmsg_ctx *c, const Scratch &S0, int layer, const float *d
     /* against the streaming kernel the MFMA kernels win from 1.25 slots per expert (Q4_1:
      * 139.7 / 128.2 us at 16 tokens, 173.8 / 174.0 at 24, 196.3 / 216.6 at 32), or 2.5 for Q6_K */
     const bool gu_mx = gu_ok && (forced || (autop && mx_auto(T, s.K, s.X, d.gate_type)));
-    const bool dn_mx = dn_ok && many && (forced || (autop && mx_auto_down(T, s.K, d.down_type)));
+    /* rows too long for every exact down kernel's LDS (n_ff_exp 14336: 8 KB per Q4_0 row) take
+     * the MFMA down kernel on any path that allows it */
+    const bool dn_long = dn_ok && T >= 2 && c->path != QMSG_PATH_EXACT && !down_exact_fits(s, d, T);
+    const bool dn_mx = dn_ok && (dn_long || (many && (forced || (autop && mx_auto_down(T, s.K, d.down_type)))));
     if (ni) LAUNCH(c, "route", launch_route_norm(s, d, S, *ni, c->stream));
     else LAUNCH(c, "route", launch_route(s, d, S, d_xn, T, c->stream));
     LAUNCH(c, "select", launch_select(s, S, T, q4 ? 1 : 0, c->stream));

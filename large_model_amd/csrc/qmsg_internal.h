@@ -161,6 +161,9 @@ hipError_t launch_down_mx(const Shape &s, const LayerDev &L, const Scratch &S, f
 hipError_t launch_gateup_tiles(const Shape &s, const LayerDev &L, const Scratch &S, int T, hipStream_t st);
 /* Whether two to four tokens take the small-batch down kernel. */
 bool down_small_fits(const Shape &s, const LayerDev &L, int T);
+/* Whether one of the exact down kernels (one-token, small-batch, slot tiles) holds this shape
+ * in LDS; rows too long for all of them take the MFMA down kernel, which stages them in chunks. */
+bool down_exact_fits(const Shape &s, const LayerDev &L, int T);
 /* quant: the activations' int8 blocks are formed here (else read from aqk, where gate/up or the
  * MFMA gate/up stored them). */
 hipError_t launch_down_exact(const Shape &s, const LayerDev &L, const Scratch &S, float *out, int T, int quant,

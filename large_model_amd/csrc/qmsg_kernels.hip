@@ -2174,6 +2174,34 @@ bool down_small_fits(const Shape &s, const LayerDev &L, int T)
            lds_s <= 160 * 1024;
 }
 
+/* LDS bytes of the one-token down kernel, and of the slot-tile down kernel at NT slots per pass. */
+static size_t down_t1_lds(const Shape &s, const LayerDev &L)
+{
+    constexpr int RD = kDownT1Rows, CB = 8;
+    const int bb = L.down_type == 3 ? 20 : 18;
+    const size_t xrec = (size_t)(s.F / 64) * kPairBytes;
+    const size_t ws = L.down_type == 14 ? 220 : (size_t)CB * bb + (((CB * bb / 16) & 1) ? 0 : 16);
+    return (size_t)(RD / 2) * 16 * ws + (size_t)s.K * xrec + (size_t)s.K * RD * 4;
+}
+
+static size_t down_tile_lds(const Shape &s, const LayerDev &L, int T)
+{
+    const size_t xrec = (size_t)(s.F / 64) * kPairBytes;
+    const int NT = T >= 4 ? 4 : (T >= 2 ? 2 : 1);
+    const int RT = L.down_type == 14 ? kDownTileRowsQ6K : 64;
+    return ((RT * L.down_rb + 15) & ~(size_t)15) + (size_t)NT * xrec;
+}
+
+bool down_exact_fits(const Shape &s, const LayerDev &L, int T)
+{
+    const bool t1_type = L.down_type == 2 || L.down_type == 3 || (L.down_type == 14 && L.down_rb % 4 == 0);
+    if (T == 1 && s.K <= 8 && t1_type && s.F % 256 == 0 && s.E % kDownT1Rows == 0 && down_t1_lds(s, L) <= 160 * 1024)
+        return true;
+    if (down_small_fits(s, L, T)) return true;
+    const int RT = L.down_type == 14 ? kDownTileRowsQ6K : 64;
+    return down_tile_lds(s, L, T) <= 160 * 1024 && s.E % RT == 0;
+}
+
 hipError_t launch_down_exact(const Shape &s, const LayerDev &L, const Scratch &S, float *out, int T, int quant,
                              hipStream_t st)
 {
@@ -2197,7 +2225,7 @@ hipError_t launch_down_exact(const Shape &s, const LayerDev &L, const Scratch &S
     const int bb = L.down_type == 3 ? 20 : 18;
     const size_t xrec = (size_t)(s.F / 64) * kPairBytes;
     const size_t ws = L.down_type == 14 ? 220 : (size_t)CB * bb + (((CB * bb / 16) & 1) ? 0 : 16);
-    const size_t lds_t1 = (size_t)(RD / 2) * 16 * ws + (size_t)s.K * xrec + (size_t)s.K * RD * 4;
+    const size_t lds_t1 = down_t1_lds(s, L);
     const bool t1_type = L.down_type == 2 || L.down_type == 3 || (L.down_type == 14 && L.down_rb % 4 == 0);
     if (T == 1 && s.K <= 8 && t1_type && s.F % 256 == 0 && s.E % RD == 0 && lds_t1 <= 160 * 1024) {
         const dim3 grid(s.E / RD), block(32 * RD);
@@ -2225,7 +2253,7 @@ hipError_t launch_down_exact(const Shape &s, const LayerDev &L, const Scratch &S
     }
     const int NT = T >= 4 ? 4 : (T >= 2 ? 2 : 1);
     const int RT = L.down_type == 14 ? kDownTileRowsQ6K : 64;
-    const size_t lds = ((RT * L.down_rb + 15) & ~(size_t)15) + (size_t)NT * xrec;
+    const size_t lds = down_tile_lds(s, L, T);
     if (lds > 160 * 1024 || s.E % RT) return hipErrorInvalidValue;
     const dim3 grid(s.E / RT, maxt);
     TileArgs ta;

@@ -1,0 +1,68 @@
+"""Expert counts that are not a multiple of 16 on the GPU: a Mixtral-like layer (8 experts, top 2,
+n_ff_exp 14336), a small 8-expert layer and a 60-expert one, each at one token (routing inside
+the gate/up kernel), two to four tokens (select, the small-batch down kernel), a batch on the
+MFMA kernels, and the fp32 path. Every intermediate bit for bit against the oracle, as in
+test_gpu_layer.py; the reference's fast path has no condition on the expert count
+(src/model.c:1090-1093)."""
+import numpy as np
+import pytest
+
+import oracle as orc
+
+pytestmark = pytest.mark.gpu
+
+CASES = [
+    # name, E, X, K, F, T, seed, down type, path
+    ("x8_k2_t1", 256, 8, 2, 128, 1, 101, orc.T_Q4_0, "auto"),
+    ("x8_k2_t3", 256, 8, 2, 128, 3, 102, orc.T_Q4_0, "auto"),
+    ("x8_k2_t40_mfma", 256, 8, 2, 256, 40, 103, orc.T_Q4_1, "auto"),
+    ("x60_k4_t1", 1024, 60, 4, 256, 1, 104, orc.T_Q4_0, "auto"),
+    ("x60_k4_t4", 1024, 60, 4, 256, 4, 105, orc.T_Q6_K, "auto"),
+    ("x60_k4_t64", 1024, 60, 4, 256, 64, 106, orc.T_Q4_0, "auto"),
+    ("x60_k4_t5_exact", 1024, 60, 4, 256, 5, 107, orc.T_Q4_0, "exact"),
+    ("mixtral_t1", 4096, 8, 2, 14336, 1, 108, orc.T_Q4_0, "auto"),
+    ("mixtral_t4", 4096, 8, 2, 14336, 4, 109, orc.T_Q4_0, "auto"),
+]
+
+
+def _bits(a):
+    return np.ascontiguousarray(a).view(np.uint8)
+
+
+@pytest.fixture(scope="module")
+def q():
+    from large_model_amd import qmsg
+    return qmsg
+
+
+@pytest.mark.parametrize("name,E,X,K,F,T,seed,dt,path", CASES, ids=[c[0] for c in CASES])
+def test_expert_counts(q, name, E, X, K, F, T, seed, dt, path):
+    print(f"[case] shapes {name} E={E} X={X} K={K} F={F} T={T} path={path}", flush=True)
+    x = orc.make_input(E, T, seed, rmsnorm=True)
+    host = orc.Layer(E, X, K, F, seed, down_type=dt, experts=[])
+    ref_out, ref = host.moe(x, debug=True)
+    with q.Context(E, X, K, F, n_layer=1, max_tokens=T) as ctx:
+        ctx.synth(0, seed, down_type=dt)
+        ctx.set_path(q.PATH_EXACT if path == "exact" else q.PATH_AUTO)
+        out, got = ctx.moe_debug(0, x)
+        out2 = ctx.moe(0, x)
+    for k in ("sel", "start", "slot_t", "slot_of", "active"):
+        assert np.array_equal(got[k], ref[k]), k
+    for k in ("logits", "wt", "xq", "gu", "act", "aq", "dn"):
+        assert np.array_equal(_bits(got[k]), _bits(ref[k])), k
+    assert np.array_equal(_bits(out), _bits(ref_out)), "layer output"
+    assert np.array_equal(_bits(out2), _bits(ref_out)), "second call"
+
+
+@pytest.mark.parametrize("E,X,K,F,T,seed", [(256, 8, 2, 128, 3, 111), (1024, 60, 4, 256, 2, 112)])
+def test_expert_counts_fp32_path(q, E, X, K, F, T, seed):
+    """The --exact mode at the same expert counts."""
+    print(f"[case] shapes fp32 X={X} T={T}", flush=True)
+    x = orc.make_input(E, T, seed)
+    host = orc.Layer(E, X, K, F, seed, experts=[])
+    ref_out = host.moe(x, exact=True)
+    with q.Context(E, X, K, F, n_layer=1, max_tokens=T) as ctx:
+        ctx.synth(0, seed)
+        ctx.set_path(q.PATH_FP32)
+        out = ctx.moe(0, x)
+    assert np.array_equal(_bits(out), _bits(ref_out))
