@@ -61,6 +61,13 @@ KERNEL_NAMES = ("fill", "rmsnorm", "route", "select", "dispatch", "mxin", "layer
                 "down", "combine", "add", "dquant", "dense")
 
 
+# What int8_tops / int8_frac_of_peak measure: the layer's algorithmic int8 multiply-adds (the
+# reference's int8 dots) per second against 5 POPS of dense int8 MFMA. The kernels do not issue
+# int8 MFMAs: the prefill's lane sums come from f16 MFMAs on exact integer codes.
+INT8_BASIS = ("algorithmic int8 multiply-adds of the reference's dots per second / 5 POPS dense int8; "
+              "the kernels issue f16 MFMAs (block-diagonal, exact integer codes), not int8 ones")
+
+
 def kernel_times(ctx):
     """Launch count and average duration per kernel name from the per-dispatch events."""
     kern = {}
@@ -335,6 +342,7 @@ def extra_prefill(steps: int = 10, warmup: int = 2, NL: int = 4):
         "distinct_experts": d_active, "int8_ops": ops,
         "int8_tops": round(ops / (ms * 1e-3) / 1e12, 3),
         "int8_frac_of_peak": round(ops / (ms * 1e-3) / 1e12 / INT8_PEAK_TOPS, 5),
+        "int8_basis": INT8_BASIS,
         "algorithmic_bytes": nbytes, "achieved_GBps": round(nbytes / (ms * 1e-3) / 1e9, 1),
         "bound_us": {"mfma_at_peak": round(mfma_us, 1), "hbm_at_peak": round(hbm_us, 1)},
         "path": "auto (MFMA expert kernels at this batch)", "kernels": kern,
@@ -745,6 +753,7 @@ def main():
             "frac_of_hbm_peak": round(layer_bytes / (ms_step * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
             "int8_tops": round(w.int8_ops() / (ms_step * 1e-3) / 1e12, 3),
             "int8_frac_of_peak": round(w.int8_ops() / (ms_step * 1e-3) / 1e12 / INT8_PEAK_TOPS, 5),
+            "int8_basis": INT8_BASIS,
         },
         "kernels": kern,
         "device": ctx.device_info(),
