@@ -2976,6 +2976,9 @@ __device__ __forceinline__ void mx_wait_barrier()
 #ifndef QMSG_MX_WIDE16_SLOTS
 #define QMSG_MX_WIDE16_SLOTS 8
 #endif
+#ifndef QMSG_MX_MID_NB
+#define QMSG_MX_MID_NB 2
+#endif
 #ifndef QMSG_MX_WIDE16_NB
 #define QMSG_MX_WIDE16_NB 1
 #endif
@@ -3313,8 +3316,9 @@ static_assert(2 * mx_lds_bytes(14, 2) <= 160 * 1024, "two Q6_K blocks per CU");
  *          6 and 262 / 125 against 239 / 114 at 4, where it is not taken;
  *   wide   (other types: gate/up r >= 12, down r >= 16): 8 waves, 4 row groups x 2 slot groups of 4 pairs:
  *          128 rows x 16 slots, two staging buffers;
- *   mid:   4 waves, 4 row groups x 1 slot group of 4 pairs: 128 rows x 8 slots, one staging
- *          buffer (four blocks per CU);
+ *   mid:   4 waves, 4 row groups x 1 slot group of 4 pairs: 128 rows x 8 slots; Q4_0 / Q4_1
+ *          two staging buffers (three blocks per CU: the 64-token stack's gate/up 231-233 us
+ *          against 235-242 with one), Q6_K one (four blocks per CU);
  *   narrow (gate/up r < 3, Q4_0 / Q4_1 down r < 3.5, Q6_K down r < 2.5): 4 waves, 4 row
  *          groups x 1 slot group of 2 pairs (128 rows x 4 slots), two buffers (Q6_K: one).
  * Measured per layer at the 235B shape (us): gate/up narrow / mid 166 / 178 at r = 1.5, 187 /
@@ -3367,7 +3371,7 @@ static void launch_mx(const MxArgs &a, int rows, int maxt, MxShape shape, hipStr
             launch_mx_shape<TYPE, GU, 1, 8, 4, QMSG_MX_WIDE16_NB>(a, rows, maxt, st);
     }
     else if (shape == kMxNarrow) launch_mx_shape<TYPE, GU, 1, 2, 4, (!GU && TYPE == 14) ? 1 : 2>(a, rows, maxt, st);
-    else launch_mx_shape<TYPE, GU, 1, 4, 4, 1>(a, rows, maxt, st);
+    else launch_mx_shape<TYPE, GU, 1, 4, 4, TYPE == 14 ? 1 : QMSG_MX_MID_NB>(a, rows, maxt, st);
 }
 
 /* Whether the MFMA kernels take this layer: gate and up of one type (Q4_0, Q4_1, or Q6_K with
