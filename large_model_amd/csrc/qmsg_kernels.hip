@@ -2976,6 +2976,12 @@ __device__ __forceinline__ void mx_wait_barrier()
 #ifndef QMSG_MX_WIDE16_SLOTS
 #define QMSG_MX_WIDE16_SLOTS 8
 #endif
+#ifndef QMSG_MX_NARROW_GU
+#define QMSG_MX_NARROW_GU 8
+#endif
+#ifndef QMSG_MX_NARROW_DN
+#define QMSG_MX_NARROW_DN 8
+#endif
 #ifndef QMSG_MX_MID_NB
 #define QMSG_MX_MID_NB 2
 #endif
@@ -3319,9 +3325,12 @@ static_assert(2 * mx_lds_bytes(14, 2) <= 160 * 1024, "two Q6_K blocks per CU");
  *   mid:   4 waves, 4 row groups x 1 slot group of 4 pairs: 128 rows x 8 slots; Q4_0 / Q4_1
  *          two staging buffers (three blocks per CU: the 64-token stack's gate/up 231-233 us
  *          against 235-242 with one), Q6_K one (four blocks per CU);
- *   narrow (gate/up r < 3, Q4_0 / Q4_1 down r < 3.5, Q6_K down r < 2.5): 4 waves, 4 row
- *          groups x 1 slot group of 2 pairs (128 rows x 4 slots), two buffers (Q6_K: one).
- * Measured per layer at the 235B shape (us): gate/up narrow / mid 166 / 178 at r = 1.5, 187 /
+ *   narrow (Q4_0 / Q4_1 gate/up and down r < 2, Q6_K gate/up r < 3, Q6_K down r < 2.5): 4 waves,
+ *          4 row groups x 1 slot group of 2 pairs (128 rows x 4 slots), two buffers (Q6_K down:
+ *          one). With the double-buffered mid blocks, Q4_0 narrow / mid (us, gate/up, down):
+ *          126-131 / 133, 64-66 / 67 at r = 1; 165 / 165-166, 82 / 82 at 1.5; 188 / 186-187,
+ *          92 / 91 at 2; 207-208 / 201-202, 100.5 / 97 at 2.5.
+ * Measured per layer at the 235B shape with one-buffer mid blocks (us): gate/up narrow / mid 166 / 178 at r = 1.5, 187 /
  * 199 at 2, 236 / 237 at 3, 287 / 269 at 4; mid / 8-slot blocks of 8 waves 317-325 / 364-378 at
  * 6; mid / wide 407-416 / 460-467 at 8, 571-620 / 581-593 at 12 (run to run), 765-786 / 723-751
  * at 16. Down narrow / mid: Q4_0 89 / 100 at 1.5, 124 / 133 at 3, 154 / 150 at 4; Q6_K 198 /
@@ -3337,7 +3346,7 @@ static MxShape mx_shape(const Shape &s, int T, int gu, int type)
     const long wide_slots = gu ? kMxWideSlotsGateUp : kMxWideSlots;
     if (type != 14 && QMSG_MX_WIDE16_SLOTS > 0 && NS >= QMSG_MX_WIDE16_SLOTS * act) return kMxWide16;
     if (NS >= wide_slots * act) return kMxWide;
-    const long narrow_quarters = gu ? 12 : (type == 14 ? 10 : 14);
+    const long narrow_quarters = type == 14 ? (gu ? 12 : 10) : (gu ? QMSG_MX_NARROW_GU : QMSG_MX_NARROW_DN);
     return 4 * NS < narrow_quarters * act ? kMxNarrow : kMxMid;
 }
 
