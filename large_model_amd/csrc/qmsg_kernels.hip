@@ -1740,13 +1740,15 @@ __global__ __launch_bounds__(32 * RD) void down_t1_kernel(DownArgs a)
     constexpr int EPW = 16 / RD;                      /* experts per wave                     */
     constexpr int QPT = (512 + NTH - 1) / NTH;        /* int8 blocks per thread in registers  */
     constexpr int BB = TYPE == 3 ? 20 : 18;           /* bytes per 32-block (Q4 types)        */
-    constexpr int UNIT = Q6 ? 4 : 16;                 /* bytes per load                       */
-    constexpr int SPR = Q6 ? 54 : CB * BB / 16;       /* loads per row per chunk              */
+    constexpr int UNIT = 16;                          /* bytes per load                       */
+    /* loads per row per chunk; a Q6_K super-block (210 bytes, 2-byte aligned) is read as the
+     * 14 16-byte units from the 16-byte boundary below it, and found at that row's offset */
+    constexpr int SPR = Q6 ? 14 : CB * BB / 16;
     constexpr int NSL = 16 * SPR;                     /* loads of one wave's chunk            */
     constexpr int SPT = (NSL + 63) / 64;              /* loads per lane per chunk             */
-    /* LDS row stride, odd in 16-byte units (Q6_K: in 4-byte units) */
-    constexpr int WS = Q6 ? 220 : CB * BB + ((SPR & 1) ? 0 : 16);
-    typedef typename std::conditional<Q6, uint32_t, u32x4>::type Unit;
+    /* LDS row stride, odd in 16-byte units */
+    constexpr int WS = Q6 ? 240 : CB * BB + ((SPR & 1) ? 0 : 16);
+    typedef u32x4 Unit;
     const int tid = threadIdx.x, lane = tid & 63, qd = lane >> 2, p = lane & 3;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int r0 = (int)blockIdx.x * RD, E = a.E, K = a.K, nbF = a.F >> 5, nPF = a.F >> 6;
@@ -1786,8 +1788,8 @@ __global__ __launch_bounds__(32 * RD) void down_t1_kernel(DownArgs a)
         for (int m = 0; m < SPT; m++) {
             const int i = min(lane + 64 * m, NSL - 1), row = i / SPR, j = i - row * SPR;
             const uint8_t *rp = (EPW == 1 || row < RD) ? b0 + (size_t)row * a.rb : b1 + (size_t)(row - RD) * a.rb;
-            if constexpr (Q6)     /* the super-block starts 2 bytes past a 4-byte boundary on odd chunks */
-                dst[m] = *(const uint32_t *)(rp + (size_t)(c * 210 - 2 * (c & 1)) + 4 * j);
+            if constexpr (Q6)     /* up to 14 bytes past the super-block: within the tensor's tail padding */
+                dst[m] = *(const u32x4 *)(((uintptr_t)(rp + (size_t)c * 210) & ~(uintptr_t)15) + 16 * j);
             else
                 dst[m] = *(const u32x4 *)(rp + (size_t)c * CB * BB + 16 * j);
         }
@@ -1836,6 +1838,7 @@ __global__ __launch_bounds__(32 * RD) void down_t1_kernel(DownArgs a)
         /* quad qd: expert j0 + qd/RD, row r0 + qd%RD; its slot is its active index */
         const int jq = j0 + qd / RD, rr = qd % RD;
         const uint8_t *xq = xbuf + (size_t)min(jq, K - 1) * xrec;
+        const uint8_t *rq = (EPW == 1 || qd < RD ? b0 : b1) + (size_t)rr * a.rb;   /* this quad's row */
         RowAcc acc[1] = { RowAcc{ 0.0f, 0.0f, 0.0f } };
         for (int c0 = 0; c0 < nchunk; c0 += D) {
 #pragma unroll
@@ -1851,6 +1854,9 @@ __global__ __launch_bounds__(32 * RD) void down_t1_kernel(DownArgs a)
                     wave_sync();
                     if (c + D < nchunk) load_chunk(c + D, wv[d]);
                     if constexpr (Q6) {
+                        /* the super-block's offset in the row's staged units; a multiple of 4
+                         * on even chunks (rows are 4-byte aligned), 2 past one on odd ones */
+                        const uint32_t sbo = (uint32_t)((uintptr_t)(rq + (size_t)c * 210) & 15);
                         /* the 8 blocks of super-block c (src/kernels.c:142-170) */
                         auto superblock = [&](auto al) {
 #pragma unroll
@@ -1858,7 +1864,7 @@ __global__ __launch_bounds__(32 * RD) void down_t1_kernel(DownArgs a)
 #pragma unroll
                                 for (int g = 0; g < 4; g++) {
                                     const int blk = c * 8 + h * 4 + g;
-                                    const Q6W w = q6_k_weights<decltype(al)::value>(wbuf + qd * WS, al ? 0 : 2, h, g, p);
+                                    const Q6W w = q6_k_weights<decltype(al)::value>(wbuf + qd * WS, sbo, h, g, p);
                                     q6_k_token(w, xq + (size_t)(blk >> 1) * kPairBytes, p, blk & 1, acc[0]);
                                 }
                         };
@@ -1912,12 +1918,14 @@ __global__ __launch_bounds__(32 * RD) void down_small_kernel(DownArgs a)
     constexpr int NW = RD / 2, NTH = 64 * NW, NT = 4;
     constexpr int QPT = 2;                            /* int8 blocks per thread in registers  */
     constexpr int BB = TYPE == 3 ? 20 : 18;           /* bytes per 32-block (Q4 types)        */
-    constexpr int UNIT = Q6 ? 4 : 16;                 /* bytes per load                       */
-    constexpr int SPR = Q6 ? 54 : CB * BB / 16;       /* loads per row per chunk              */
+    constexpr int UNIT = 16;                          /* bytes per load                       */
+    /* loads per row per chunk (a Q6_K super-block: the 14 16-byte units from the 16-byte
+     * boundary below it, as in down_t1_kernel) */
+    constexpr int SPR = Q6 ? 14 : CB * BB / 16;
     constexpr int NSL = RD * SPR;                     /* loads of one wave's chunk            */
     constexpr int SPT = (NSL + 63) / 64;              /* loads per lane per chunk             */
-    constexpr int WS = Q6 ? 220 : CB * BB + ((SPR & 1) ? 0 : 16);   /* LDS row stride        */
-    typedef typename std::conditional<Q6, uint32_t, u32x4>::type Unit;
+    constexpr int WS = Q6 ? 240 : CB * BB + ((SPR & 1) ? 0 : 16);   /* LDS row stride        */
+    typedef u32x4 Unit;
     static_assert(RD == 16, "a lane quad per row of the wave's 16");
     const int tid = threadIdx.x, lane = tid & 63, qd = lane >> 2, p = lane & 3;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -1950,8 +1958,9 @@ __global__ __launch_bounds__(32 * RD) void down_small_kernel(DownArgs a)
 #pragma unroll
         for (int m = 0; m < SPT; m++) {
             const int i = min(lane + 64 * m, NSL - 1), row = i / SPR, q = i - row * SPR;
-            if constexpr (Q6)     /* the super-block starts 2 bytes past a 4-byte boundary on odd chunks */
-                dst[m] = *(const uint32_t *)(b + (size_t)row * a.rb + (size_t)(c * 210 - 2 * (c & 1)) + 4 * q);
+            if constexpr (Q6)     /* up to 14 bytes past the super-block: within the tensor's tail padding */
+                dst[m] = *(const u32x4 *)(((uintptr_t)(b + (size_t)row * a.rb + (size_t)c * 210) & ~(uintptr_t)15) +
+                                          16 * q);
             else
                 dst[m] = *(const u32x4 *)(b + (size_t)row * a.rb + (size_t)c * CB * BB + 16 * q);
         }
@@ -2006,6 +2015,7 @@ __global__ __launch_bounds__(32 * RD) void down_small_kernel(DownArgs a)
         const bool pre = can_pre && wn.x >= 0;
         bool switched = false;
         const int s0 = wk.y, nt = wk.z - wk.y;        /* one slot per token of the expert: nt <= T */
+        const uint8_t *cb = a.down + (size_t)wk.x * a.eb + (size_t)r0 * a.rb;    /* its rows (b may move on) */
         const uint8_t *xq = xbuf + (size_t)s0 * xrec;
         RowAcc acc[NT];
         for (int n = 0; n < NT; n++) acc[n] = RowAcc{ 0.0f, 0.0f, 0.0f };
@@ -2031,6 +2041,9 @@ __global__ __launch_bounds__(32 * RD) void down_small_kernel(DownArgs a)
                         load_chunk(c + D - nchunk, wv[d]);
                     }
                     if constexpr (Q6) {
+                        /* the super-block's offset in this quad's staged row (b: the expert
+                         * whose rows this chunk holds) */
+                        const uint32_t sbo = (uint32_t)((uintptr_t)(cb + (size_t)qd * a.rb + (size_t)c * 210) & 15);
                         /* the 8 blocks of super-block c (src/kernels.c:142-170) for every slot */
                         auto superblock = [&](auto al) {
 #pragma unroll
@@ -2038,7 +2051,7 @@ __global__ __launch_bounds__(32 * RD) void down_small_kernel(DownArgs a)
 #pragma unroll
                                 for (int g = 0; g < 4; g++) {
                                     const int blk = c * 8 + h * 4 + g;
-                                    const Q6W w = q6_k_weights<decltype(al)::value>(wbuf + qd * WS, al ? 0 : 2, h, g, p);
+                                    const Q6W w = q6_k_weights<decltype(al)::value>(wbuf + qd * WS, sbo, h, g, p);
 #pragma unroll
                                     for (int n = 0; n < NT; n++)
                                         if (n < nt)
@@ -2167,7 +2180,7 @@ bool down_small_fits(const Shape &s, const LayerDev &L, int T)
     constexpr int RD = kDownT1Rows, CB = 8;
     const int bb = L.down_type == 3 ? 20 : 18;
     const size_t xrec = (size_t)(s.F / 64) * kPairBytes;
-    const size_t ws = L.down_type == 14 ? 220 : (size_t)CB * bb + (((CB * bb / 16) & 1) ? 0 : 16);
+    const size_t ws = L.down_type == 14 ? 240 : (size_t)CB * bb + (((CB * bb / 16) & 1) ? 0 : 16);
     const size_t lds_s = (size_t)(RD / 2) * 16 * ws + (size_t)T * s.K * (xrec + RD * 4);
     const bool t1_type = L.down_type == 2 || L.down_type == 3 || (L.down_type == 14 && L.down_rb % 4 == 0);
     return T >= 2 && T <= 4 && T * s.K <= kSmallDownNS && t1_type && s.F % 256 == 0 && s.E % RD == 0 &&
@@ -2180,7 +2193,7 @@ static size_t down_t1_lds(const Shape &s, const LayerDev &L)
     constexpr int RD = kDownT1Rows, CB = 8;
     const int bb = L.down_type == 3 ? 20 : 18;
     const size_t xrec = (size_t)(s.F / 64) * kPairBytes;
-    const size_t ws = L.down_type == 14 ? 220 : (size_t)CB * bb + (((CB * bb / 16) & 1) ? 0 : 16);
+    const size_t ws = L.down_type == 14 ? 240 : (size_t)CB * bb + (((CB * bb / 16) & 1) ? 0 : 16);
     return (size_t)(RD / 2) * 16 * ws + (size_t)s.K * xrec + (size_t)s.K * RD * 4;
 }
 
@@ -2224,7 +2237,7 @@ hipError_t launch_down_exact(const Shape &s, const LayerDev &L, const Scratch &S
     constexpr int RD = kDownT1Rows, CB = 8;
     const int bb = L.down_type == 3 ? 20 : 18;
     const size_t xrec = (size_t)(s.F / 64) * kPairBytes;
-    const size_t ws = L.down_type == 14 ? 220 : (size_t)CB * bb + (((CB * bb / 16) & 1) ? 0 : 16);
+    const size_t ws = L.down_type == 14 ? 240 : (size_t)CB * bb + (((CB * bb / 16) & 1) ? 0 : 16);
     const size_t lds_t1 = down_t1_lds(s, L);
     const bool t1_type = L.down_type == 2 || L.down_type == 3 || (L.down_type == 14 && L.down_rb % 4 == 0);
     if (T == 1 && s.K <= 8 && t1_type && s.F % 256 == 0 && s.E % RD == 0 && lds_t1 <= 160 * 1024) {
