@@ -2504,7 +2504,17 @@ struct MxB {
     uint32_t dw;      /* Q4_0: d (low half); Q4_1: d | m << 16; Q6_K: d (low half) */
     float sc;         /* Q6_K: the lane's sub-scale times 2^24 (k < 4: sc[2g], k >= 4: sc[2g+1]) */
     uint32_t sab;     /* Q6_K: both sub-scales as int16 pair (sc[2g] low) */
+    float sc1;        /* Q6_K: sc[2g+1] times 2^24 */
 };
+
+/* a.lo*b.lo + a.hi*b.hi over int16 halves (v_dot2_i32_i16 with a zero addend: no register to
+ * clear first, as the accumulating form needs). */
+__device__ __forceinline__ int sdot2_i16(uint32_t a, uint32_t b)
+{
+    int r;
+    asm("v_dot2_i32_i16 %0, %1, %2, 0" : "=v"(r) : "v"(a), "v"(b));
+    return r;
+}
 
 typedef __attribute__((address_space(3))) const uint8_t *LdsPtr;
 typedef __attribute__((address_space(3))) const u32x2 LdsU32x2;
@@ -2548,6 +2558,7 @@ __device__ __forceinline__ MxB mx_weights_q4(LdsPtr pq, LdsPtr pd, int t)
     else w.dw = *(const __attribute__((address_space(3))) uint16_t *)(pd + 16 * t * WS);
     w.sc = 0.0f;
     w.sab = 0u;
+    w.sc1 = 0.0f;
     return w;
 }
 
@@ -2795,7 +2806,7 @@ __device__ __forceinline__ MxB mx_weights_q6(LdsPtr q, LdsPtr rb, int t, int kh)
 {
     constexpr int WS = mx_wstride(14), h = B >> 2, g = B & 3, ns = 4 * (g >> 1), hs = 2 * g;
     constexpr int oql = O + 64 * h + 32 * (g & 1), oqh = O + 128 + 32 * h;
-    const uint32_t m8 = 0x00ff00ffu, lo4 = 0x0f0f0f0fu;
+    const uint32_t lo4 = 0x0f0f0f0fu;
     auto code = [&](int dq) {
         const uint32_t ql = q6_word<O>(q, TS * t * WS + oql + dq), qh = q6_word<O>(q, TS * t * WS + oqh + dq);
         uint32_t hi;
@@ -2806,12 +2817,20 @@ __device__ __forceinline__ MxB mx_weights_q6(LdsPtr q, LdsPtr rb, int t, int kh)
     };
     const uint32_t cA = code(0), cB = code(16);
     MxB w;
-    /* the f16 subnormals code 2^-24 */
-    w.op = __builtin_bit_cast(f16x8, u32x4{ cA & m8, (cA >> 8) & m8, cB & m8, (cB >> 8) & m8 });
+    /* the f16 subnormals code 2^-24: bytes 0 and 2, then 1 and 3, of each code dword into the
+     * low bytes of its halves (one byte permute each) */
+    w.op = __builtin_bit_cast(f16x8, u32x4{ __builtin_amdgcn_perm(cA, cA, 0x0c020c00u), __builtin_amdgcn_perm(cA, cA, 0x0c030c01u),
+                                            __builtin_amdgcn_perm(cB, cB, 0x0c020c00u), __builtin_amdgcn_perm(cB, cB, 0x0c030c01u) });
     const uint32_t scw = *(const __attribute__((address_space(3))) uint16_t *)(rb + TS * t * WS + O + 192 + 8 * h + 2 * g);
-    const int sa = (int)(int8_t)(scw & 0xffu), sbv = (int)(int8_t)(scw >> 8);
-    w.sab = ((uint32_t)sa & 0xffffu) | ((uint32_t)sbv << 16);
-    w.sc = (float)((kh ? sbv : sa) * 16777216);         /* exact: at most 8 significant bits */
+    /* the int16 pair {sc[2g], sc[2g+1]}: byte permute with sign fills (selector 10: the sign of
+     * byte 1 of the first source, scw << 8, i.e. of sc[2g]; selector 8: of byte 1 of scw) */
+    w.sab = __builtin_amdgcn_perm(scw << 8, scw, 0x08010a00u);
+    /* sc * 2^24 = (u - 128) * 2^24 for the byte u = sc ^ 0x80, exact in one fma */
+    const uint32_t sx = scw ^ 0x8080u;
+    const float s0 = __builtin_fmaf((float)(sx & 0xffu), 16777216.0f, -2147483648.0f);
+    const float s1 = __builtin_fmaf((float)((sx >> 8) & 0xffu), 16777216.0f, -2147483648.0f);
+    w.sc = kh ? s1 : s0;
+    w.sc1 = s1;
     w.dw = *(const __attribute__((address_space(3))) uint16_t *)(rb + TS * t * WS + O + 208);
     return w;
 }
@@ -2842,8 +2861,7 @@ __device__ __forceinline__ void mx_block_q6(const MxStreams &st, int kh, f32x4 (
 #pragma unroll
             for (int v = 0; v < 4; v++) acc[t][p][v] = __builtin_fmaf(S[v] * w[t].sc, dd, acc[t][p][v]);
             /* sc[2g]*s16[0] + sc[2g+1]*s16[1] in one packed int16 dot */
-            const int ssum = __builtin_amdgcn_sdot2(__builtin_bit_cast(short2_t, w[t].sab),
-                                                    __builtin_bit_cast(short2_t, s16p), 0, false);
+            const int ssum = sdot2_i16(w[t].sab, s16p);
             cr[t][p] = __builtin_fmaf(dd, (float)ssum, cr[t][p]);
         }
     }
@@ -2896,7 +2914,7 @@ __device__ __forceinline__ void mx_block16_q6(const MxStreams &st, f32x4 (&acc)[
         b[t][0] = __builtin_shufflevector(w[t].op, w[t].op, 0, 1, 2, 3);
         b[t][1] = __builtin_shufflevector(w[t].op, w[t].op, 4, 5, 6, 7);
         sc[t][0] = w[t].sc;                                              /* sc[2g] 2^24 */
-        sc[t][1] = (float)(((int)w[t].sab >> 16) * 16777216);           /* sc[2g+1] 2^24, exact */
+        sc[t][1] = w[t].sc1;                                             /* sc[2g+1] 2^24 */
     }
     f32x4 S[2][2];
     float xd[NQ], dd[2];
@@ -2932,8 +2950,7 @@ __device__ __forceinline__ void mx_block16_q6(const MxStreams &st, f32x4 (&acc)[
 #pragma unroll
             for (int t = 0; t < 2; t++) {
                 /* sc[2g]*s16[0] + sc[2g+1]*s16[1] in one packed int16 dot */
-                const int ssum = __builtin_amdgcn_sdot2(__builtin_bit_cast(short2_t, w[t].sab),
-                                                        __builtin_bit_cast(short2_t, s16p[q]), 0, false);
+                const int ssum = sdot2_i16(w[t].sab, s16p[q]);
                 cr[t][q] = __builtin_fmaf(dd[t], (float)ssum, cr[t][q]);
             }
         }
