@@ -470,82 +470,37 @@ struct SelectArgs {
     Scratch S;
 };
 
-/* Softmax over one token's logits in double, then the top K by (probability descending,
- * index ascending) - the order K rounds of argmax with ties to the lower index produce -
- * and weights renormalised over the selection (src/model.c:1045-1064). One block of 256
- * threads per token: P[e] = exp(l_e - max) / z in LDS with z summed sequentially in expert
- * order; two threads per expert count the experts that precede it; wsum is summed in
- * selection order. */
+__device__ void route_one_rank(const float *logits, int X, float *L, double *P, int *rank, int *selidx);
+__device__ void topk_from_ranks(int K, int X, const float *L, const double *P, const int *rank, int *cand, int *sel);
+
+/* Softmax over one token's logits in double, the top K by (probability descending, index
+ * ascending) - the order K rounds of argmax with ties to the lower index produce - and the
+ * weights renormalised over the selection (src/model.c:1045-1064). One block of 256 threads
+ * per token, as the one-token routing does it: wave 0 runs the softmax while waves 1-3 rank
+ * the float logits (p is non-decreasing in the logit), then wave 0 takes the first K of that
+ * order after checking it for rounding ties (else it ranks the p exactly) and forms the
+ * weights, wsum summed in selection order. LDS: P[X] doubles, part[] the float logits and
+ * their ranks, selb[0 .. 63] the selection and selb[64 ..] K + 1 candidates. */
 __device__ void topk_token(const SelectArgs &a, int t, int tid, double *P, int *part, int *selb, double *sh)
 {
+    (void)sh;
     const int X = a.X, K = a.K;
-    const float *lt = a.S.logits + (size_t)t * X;
-    double *red = sh, &zs = sh[4];                   /* LDS: 4 wave maxima, then z and wsum */
-    double mx = -__builtin_inf();
-    for (int e = tid; e < X; e += 256) {
-        const double v = (double)lt[e];
-        P[e] = v;
-        if (v > mx) mx = v;
-    }
-    for (int o = 32; o > 0; o >>= 1) {
-        const double v = __shfl_xor(mx, o);
-        if (v > mx) mx = v;
-    }
-    if ((tid & 63) == 0) red[tid >> 6] = mx;
-    __syncthreads();
+    float *L = (float *)part;
+    int *rank = part + kMaxExperts;
+    route_one_rank(a.S.logits + (size_t)t * X, X, L, P, rank, nullptr);
     PHASE(0, 1);
-    mx = fmax(fmax(red[0], red[1]), fmax(red[2], red[3]));
-    for (int e = tid; e < X; e += 256) P[e] = qmsg_exp(P[e] - mx);
-    __syncthreads();
-    PHASE(0, 2);
-    if (tid == 0) {
-        double z = 0.0;
-#pragma unroll 16
-        for (int e = 0; e < X; e++) z += P[e];
-        zs = z;
-    }
-    __syncthreads();
-    const double z = zs;
-    PHASE(0, 3);
-    for (int e = tid; e < X; e += 256) P[e] /= z;
-    __syncthreads();
-    /* rank(e) = #{e' : P[e'] > P[e]} + #{e' < e : P[e'] == P[e]}, split over two threads.
-     * A NaN or infinite logit makes z and every p NaN: no p then compares greater, so the
-     * reference's argmax rounds take experts 0 .. K-1 in order (src/model.c:1053-1062). */
-    const bool nan_p = z != z;
-    for (int w = tid; w < 2 * X && !nan_p; w += 256) {
-        const int e = w >> 1, half = w & 1;
-        const double pe = P[e];
-        const int lo = half ? X / 2 : 0, hi = half ? X : X / 2;
-        int r = 0;
-#pragma unroll 8
-        for (int f = lo; f < hi; f++) {
-            const double pf = P[f];
-            r += (pf > pe) | ((pf == pe) & (f < e));
-        }
-        part[w] = r;
-    }
-    __syncthreads();
-    PHASE(0, 4);
-    if (nan_p) {
-        if (tid < K) selb[tid] = tid;
-    } else {
-        for (int e = tid; e < X; e += 256) {
-            const int r = part[2 * e] + part[2 * e + 1];
-            if (r < K) selb[r] = e;
-        }
-    }
-    __syncthreads();
-    if (tid == 0) {
+    if (tid < 64) {
+        topk_from_ranks(K, X, L, P, rank, selb + 64, selb);
+        const int sj = tid < K ? selb[tid] : 0;
+        const double pj = tid < K ? P[sj] : 0.0;
         double wsum = 0.0;
-        for (int j = 0; j < K; j++) wsum += P[selb[j]];
-        zs = wsum;
+        for (int j = 0; j < K; j++) wsum += __shfl(pj, j);
+        if (tid < K) {
+            a.S.sel[(size_t)t * K + tid] = sj;
+            a.S.wt[(size_t)t * K + tid] = (float)(pj / wsum);
+        }
     }
-    __syncthreads();
-    if (tid < K) {
-        a.S.sel[(size_t)t * K + tid] = selb[tid];
-        a.S.wt[(size_t)t * K + tid] = (float)(P[selb[tid]] / zs);
-    }
+    PHASE(0, 4);
     __syncthreads();
 }
 
@@ -643,8 +598,8 @@ __device__ void dispatch_slots(const SelectArgs &a, const int *sel, int *cnt, in
 __global__ __launch_bounds__(256) void select_kernel(SelectArgs a, int do_dispatch)
 {
     __shared__ double P[kMaxExperts];
-    __shared__ int part[2 * kMaxExperts];
-    __shared__ int selb[64];
+    __shared__ __align__(16) int part[2 * kMaxExperts];   /* float logits (16-byte reads), then ranks */
+    __shared__ int selb[64 + 65];                /* the selection, then K + 1 candidates */
     __shared__ int tok[kMaxExperts];
     __shared__ int last;
     __shared__ double sh[5];
@@ -974,15 +929,18 @@ struct alignas(16) SmallRoute {
  * both rankings; this is checked, and if a rounding tie shows up (logits of different value
  * with equal p), wave 0 ranks the p exactly instead. Weights are renormalised with wsum in
  * selection order; the slots of the token are its experts in ascending order.
- * Shared scratch (LDS): L[X] floats, P[X] doubles, rank[X], selidx[X], start[X+1]. This
- * first half (softmax and logit ranks) ends with a block barrier. */
-__device__ void route_one_rank(const Scratch &S, int X, float *L, double *P, int *rank, int *selidx)
+ * Shared scratch (LDS): L[X rounded up to 4] floats (16-byte aligned), P[X] doubles,
+ * rank[X], selidx[X] (may be null), start[X+1]. This first half (softmax and logit ranks)
+ * ends with a block barrier. */
+__device__ void route_one_rank(const float *logits, int X, float *L, double *P, int *rank, int *selidx)
 {
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    for (int e = tid; e < X; e += blockDim.x) {
-        L[e] = S.logits[e];
-        rank[e] = 0;
-        selidx[e] = -1;
+    for (int e = tid; e < ((X + 3) & ~3); e += blockDim.x) {
+        L[e] = e < X ? logits[e] : -__builtin_inff();
+        if (e < X) {
+            rank[e] = 0;
+            if (selidx) selidx[e] = -1;
+        }
     }
     __syncthreads();
     if (wave == 0) {
@@ -1023,18 +981,22 @@ __device__ void route_one_rank(const Scratch &S, int X, float *L, double *P, int
             if (e < X) P[e] = v[i] / z;
         }
     } else {
-        /* float ranks, item (e, part) over waves 1 .. nw-1 */
-        const int nth = blockDim.x - 64, t = tid - 64;
-        const int np = max(1, nth / X), len = (X + np - 1) / np;
+        /* float ranks, item (e, part) over waves 1 .. nw-1, four logits per LDS read (the
+         * entries past X hold -inf and never count) */
+        const int nth = blockDim.x - 64, t = tid - 64, X4 = (X + 3) & ~3;
+        const int np = max(1, nth / X), len = ((X4 + np - 1) / np + 3) & ~3;
         for (int it = t; it < X * np; it += nth) {
             const int part = it % np, e = it / np;
             const float le = L[e];
-            const int f0 = part * len, f1 = min(X, f0 + len);
+            const int f0 = part * len, f1 = min(X4, f0 + len);
             int r = 0;
-#pragma unroll 8
-            for (int f = f0; f < f1; f++) {
-                const float lf = L[f];
-                r += (lf > le) | ((lf == le) & (f < e));
+#pragma unroll 4
+            for (int f = f0; f < f1; f += 4) {
+                const float4 lf = *(const float4 *)(L + f);
+                r += (lf.x > le) | ((lf.x == le) & (f < e));
+                r += (lf.y > le) | ((lf.y == le) & (f + 1 < e));
+                r += (lf.z > le) | ((lf.z == le) & (f + 2 < e));
+                r += (lf.w > le) | ((lf.w == le) & (f + 3 < e));
             }
             if (r) atomicAdd(&rank[e], r);
         }
@@ -1064,6 +1026,48 @@ __device__ int spec_expert(const int *rank, int X, int K, int y)
     return found;
 }
 
+/* The reference's top K (src/model.c:1053-1062) from route_one_rank's softmax and logit
+ * ranks, on one wave: sel[0 .. K-1] in selection order. cand holds K + 1 ints. */
+__device__ void topk_from_ranks(int K, int X, const float *L, const double *P, const int *rank, int *cand, int *sel)
+{
+    const int lane = threadIdx.x & 63;
+    /* A NaN or infinite logit makes z and every p NaN (p is finite otherwise): no p then
+     * compares greater, so the reference's argmax rounds take experts 0 .. K-1 in order. The
+     * logit ranks are no permutation then and stay unused. */
+    const bool nan_p = P[0] != P[0];
+    if (!nan_p)
+        for (int e = lane; e < X; e += 64)
+            if (rank[e] <= K) cand[rank[e]] = e;
+    wave_sync();
+    /* Equal logits have equal p and sort by index in both orders. A p tie between logits of
+     * different value sorts by logit here but by index in the reference, so every adjacent
+     * pair must have strictly decreasing p or equal logits; across the boundary (K-1, K) the p
+     * must decrease strictly, since an equal-p run may continue past K with a lower logit and
+     * a lower index. With K == X there is no expert past the boundary. */
+    bool ok = true;
+    if (lane < K && lane + 1 < X && !nan_p) {
+        const int a = cand[lane], b = cand[lane + 1];
+        ok = P[a] > P[b] || (lane < K - 1 && L[a] == L[b]);
+    }
+    if (nan_p) {
+        if (lane < K) sel[lane] = lane;
+    } else if (__ballot(!ok) == 0ULL) {
+        if (lane < K) sel[lane] = cand[lane];
+    } else {
+        /* a rounding tie among the candidates: rank the p exactly */
+        for (int e = lane; e < X; e += 64) {
+            const double pe = P[e];
+            int r = 0;
+            for (int f = 0; f < X; f++) {
+                const double pf = P[f];
+                r += (pf > pe) | ((pf == pe) & (f < e));
+            }
+            if (r < K) sel[r] = e;
+        }
+    }
+    wave_sync();
+}
+
 /* Second half of the one-token routing: the exact top K (with the rounding-tie check),
  * weights, slots and the published scratch arrays; ends with a block barrier. */
 __device__ void route_one_select(const Scratch &S, int K, int X, SmallRoute *R, float *L, double *P, int *rank,
@@ -1071,42 +1075,7 @@ __device__ void route_one_select(const Scratch &S, int K, int X, SmallRoute *R, 
 {
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     if (wave == 0) {
-        int *cand = R->cand;
-        /* A NaN or infinite logit makes z and every p NaN (p is finite otherwise): no p then
-         * compares greater, so the reference's argmax rounds take experts 0 .. K-1 in order
-         * (src/model.c:1053-1062). The logit ranks are no permutation then and stay unused. */
-        const bool nan_p = P[0] != P[0];
-        if (!nan_p)
-            for (int e = lane; e < X; e += 64)
-                if (rank[e] <= K) cand[rank[e]] = e;
-        wave_sync();
-        /* Equal logits have equal p and sort by index in both orders. A p tie between logits
-         * of different value sorts by logit here but by index in the reference, so every
-         * adjacent pair must have strictly decreasing p or equal logits; across the boundary
-         * (K-1, K) the p must decrease strictly, since an equal-p run may continue past K with
-         * a lower logit and a lower index. */
-        bool ok = true;
-        if (lane < K && !nan_p) {
-            const int a = cand[lane], b = cand[lane + 1];
-            ok = P[a] > P[b] || (lane < K - 1 && L[a] == L[b]);
-        }
-        if (nan_p) {
-            if (lane < K) R->sel[lane] = lane;
-        } else if (__ballot(!ok) == 0ULL) {
-            if (lane < K) R->sel[lane] = cand[lane];
-        } else {
-            /* a rounding tie among the candidates: rank the p exactly */
-            for (int e = lane; e < X; e += 64) {
-                const double pe = P[e];
-                int r = 0;
-                for (int f = 0; f < X; f++) {
-                    const double pf = P[f];
-                    r += (pf > pe) | ((pf == pe) & (f < e));
-                }
-                if (r < K) R->sel[r] = e;
-            }
-        }
-        wave_sync();
+        topk_from_ranks(K, X, L, P, rank, R->cand, R->sel);
         const int sj = lane < K ? R->sel[lane] : 0;
         const double pj = lane < K ? P[sj] : 0.0;
         double wsum = 0.0;
@@ -1331,7 +1300,7 @@ __global__ __launch_bounds__(64 * W) void gateup_kernel(GateUpArgs a)
         double *P = (double *)(sr + 1);
         float *L = (float *)(P + kMaxExperts);
         int *rank = (int *)(L + kMaxExperts);
-        route_one_rank(a.S, a.X, L, P, rank, rank + kMaxExperts);
+        route_one_rank(a.S.logits, a.X, L, P, rank, rank + kMaxExperts);
         PHASE(1024, 1);
         /* start streaming the expert the logit order points at while the exact selection
          * finishes; the rare block whose expert changes reloads below */

@@ -1,11 +1,12 @@
 """Expert counts and top-k widths away from the 128 / 8 of the benchmark shapes on the GPU: a
 Mixtral-like layer (8 experts, top 2, n_ff_exp 14336), a small 8-expert layer, a 60-expert one,
 the largest count taken (256: four logits per lane of the one-token routing), 200 experts (a
-partly filled last group of 64), top 1, and top 16 / 64 (past the one-token and small-batch
-kernels' eight selections per token), each at one token (routing inside the gate/up kernel),
-two to four tokens (select, the small-batch down kernel), a batch on the MFMA kernels, and the
-fp32 path. Every intermediate bit for bit against the oracle, as in test_gpu_layer.py; the
-reference's fast path has no condition on the expert count (src/model.c:1090-1093)."""
+partly filled last group of 64), top 1, top 16 / 64 (past the one-token and small-batch
+kernels' eight selections per token) and top 8 of 8 (no expert past the top-K boundary), each
+at one token (routing inside the gate/up kernel), two to four tokens (select, the small-batch
+down kernel), a batch on the MFMA kernels, and the fp32 path. Every intermediate bit for bit
+against the oracle, as in test_gpu_layer.py; the reference's fast path has no condition on the
+expert count (src/model.c:1090-1093)."""
 import numpy as np
 import pytest
 
@@ -37,6 +38,8 @@ CASES = [
     ("x256_k16_t2", 1024, 256, 16, 256, 2, 131, orc.T_Q4_0, "auto"),
     ("x256_k64_t1", 1024, 256, 64, 256, 1, 132, orc.T_Q4_0, "auto"),
     ("x256_k64_t3", 1024, 256, 64, 256, 3, 133, orc.T_Q4_1, "auto"),
+    ("x8_k8_t1", 256, 8, 8, 128, 1, 134, orc.T_Q4_0, "auto"),      # every expert selected
+    ("x8_k8_t2", 256, 8, 8, 128, 2, 135, orc.T_Q4_0, "auto"),
 ]
 
 
