@@ -1,6 +1,9 @@
 """qmsg_moe_device_noalloc (the allocation-free layer call, scratch in the library's static
 device array) against qmsg_moe_device on the same device buffers: bit for bit, on calls in a
-row whose second input is smaller, on several shapes and paths, and its size limit."""
+row whose second input is smaller, on several shapes and paths, and its size limit; and the
+same calls captured into a HIP graph and replayed."""
+import ctypes
+
 import numpy as np
 import pytest
 
@@ -66,3 +69,62 @@ def test_noalloc_limits(qmsg):
         x = orc.make_input(E, 4, 95)
         want = orc.Layer(E, X, K, F, 95, experts=[]).moe(x)
         assert np.array_equal(ctx.d2h(d_out, (4, E)).view(np.uint32), want.view(np.uint32))
+
+
+def test_noalloc_graph_replay(qmsg):
+    """The calls the allocation-free entry point exists for: a sequence of layer calls (one token,
+    then three, then one, on two layers) captured on the context's stream into a HIP graph and
+    replayed three times. Between replays an eager call of another batch overwrites the shared
+    static scratch and the outputs are cleared, so each replay must reset what it needs (the
+    select launch's ticket counter, the record-range flags) itself. Every replay equals the
+    eager run of the same calls bit for bit."""
+    print("[case] noalloc graph replay", flush=True)
+    hip = ctypes.CDLL("libamdhip64.so")
+    vp = ctypes.c_void_p
+    hip.hipStreamBeginCapture.argtypes = [vp, ctypes.c_int]
+    hip.hipStreamEndCapture.argtypes = [vp, ctypes.POINTER(vp)]
+    hip.hipGraphInstantiate.argtypes = [ctypes.POINTER(vp), vp, vp, vp, ctypes.c_size_t]
+    hip.hipGraphLaunch.argtypes = [vp, vp]
+    hip.hipStreamSynchronize.argtypes = [vp]
+    hip.hipMemsetAsync.argtypes = [vp, ctypes.c_int, ctypes.c_size_t, vp]
+    hip.hipGraphExecDestroy.argtypes = [vp]
+    hip.hipGraphDestroy.argtypes = [vp]
+    E, X, K, F, seed = 1024, 64, 8, 256, 97
+    calls = [(0, 1), (1, 3), (0, 1)]            # (layer, tokens)
+    row = E * 4
+    with qmsg.Context(E, X, K, F, n_layer=2, max_tokens=4) as ctx:
+        ctx.synth(0, seed)
+        ctx.synth(1, seed + 1)
+        st = vp(qmsg.lib.qmsg_stream(ctx._h))
+        d_x = ctx.device_alloc(len(calls) * 4 * row)
+        d_ref = ctx.device_alloc(len(calls) * 4 * row)
+        d_got = ctx.device_alloc(len(calls) * 4 * row)
+        for i, (_, T) in enumerate(calls):
+            ctx.synth_input(seed + 10 + i, 0, T, d_x + i * 4 * row)
+        d_other, d_other_out = ctx.device_alloc(4 * row), ctx.device_alloc(4 * row)
+        ctx.synth_input(seed + 20, 0, 4, d_other)
+
+        def run(dst):
+            for i, (layer, T) in enumerate(calls):
+                ctx.moe_device_noalloc(layer, d_x + i * 4 * row, T, dst + i * 4 * row)
+
+        run(d_ref)
+        ctx.sync()
+        ref = [ctx.d2h(d_ref + i * 4 * row, (T, E)) for i, (_, T) in enumerate(calls)]
+        graph, exe = vp(), vp()
+        assert hip.hipStreamBeginCapture(st, 2) == 0          # relaxed capture mode
+        run(d_got)
+        assert hip.hipStreamEndCapture(st, ctypes.byref(graph)) == 0
+        assert hip.hipGraphInstantiate(ctypes.byref(exe), graph, None, None, 0) == 0
+        try:
+            for rep in range(3):
+                ctx.moe_device_noalloc(1, d_other, 4, d_other_out)  # eager work on the same scratch
+                assert hip.hipMemsetAsync(vp(d_got), 0xff, len(calls) * 4 * row, st) == 0
+                assert hip.hipGraphLaunch(exe, st) == 0
+                assert hip.hipStreamSynchronize(st) == 0
+                for i, (_, T) in enumerate(calls):
+                    got = ctx.d2h(d_got + i * 4 * row, (T, E))
+                    assert np.array_equal(got.view(np.uint32), ref[i].view(np.uint32)), (rep, i)
+        finally:
+            hip.hipGraphExecDestroy(exe)
+            hip.hipGraphDestroy(graph)
