@@ -2453,9 +2453,11 @@ struct MxLayout {
     static constexpr int WINSTR = (RWG * WUR + 63) / 64;               /* weight DMA instructions  */
 };
 
+/* nb: staging buffers, 1 or 2 of weights and records; 3: two of weights, one of records. */
 __host__ __device__ constexpr int mx_lds_bytes(int type, int wsg, int ppw = 4, int nw = 8, int nb = 2, int nt = 2)
 {
-    return nb * ((16 * nt * nw / wsg) * mx_wstride(type) + 2 * ppw * wsg * mx_rstride(type));
+    return nb == 3 ? 2 * ((16 * nt * nw / wsg) * mx_wstride(type)) + 2 * ppw * wsg * mx_rstride(type)
+                   : nb * ((16 * nt * nw / wsg) * mx_wstride(type) + 2 * ppw * wsg * mx_rstride(type));
 }
 
 /* (x & m) | c in one instruction; m and c in registers (no literal operands in VOP3 here). */
@@ -2972,6 +2974,12 @@ __device__ __forceinline__ void mx_wait_barrier()
     asm volatile("s_waitcnt vmcnt(0)\n\ts_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
 
+/* Wait for this wave's LDS accesses only (DMA still in flight), then the block barrier. */
+__device__ __forceinline__ void mx_lds_barrier()
+{
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
 #ifndef QMSG_MX_WIDE16_SLOTS
 #define QMSG_MX_WIDE16_SLOTS 8
 #endif
@@ -2984,8 +2992,16 @@ __device__ __forceinline__ void mx_wait_barrier()
 #ifndef QMSG_MX_MID_NB
 #define QMSG_MX_MID_NB 2
 #endif
-#ifndef QMSG_MX_WIDE16_NB
-#define QMSG_MX_WIDE16_NB 1
+#ifndef QMSG_MX_MID_NB_Q6
+#define QMSG_MX_MID_NB_Q6 1
+#endif
+/* staging of the 16-slot blocks: gate/up one buffer; down the weights in two, the records
+ * in one (mx_lds_bytes nb 3) */
+#ifndef QMSG_MX_WIDE16_NB_GU
+#define QMSG_MX_WIDE16_NB_GU 1
+#endif
+#ifndef QMSG_MX_WIDE16_NB_DN
+#define QMSG_MX_WIDE16_NB_DN 3
 #endif
 #ifndef QMSG_MX_WIDE16_NT
 #define QMSG_MX_WIDE16_NT 2
@@ -2993,15 +3009,12 @@ __device__ __forceinline__ void mx_wait_barrier()
 #ifndef QMSG_MX_WIDE16_NW
 #define QMSG_MX_WIDE16_NW 8
 #endif
-#ifndef QMSG_MX_WIDE16_WAVES
-#define QMSG_MX_WIDE16_WAVES (QMSG_MX_WIDE16_NB == 2 ? 2 : 3)
-#endif
 /* Waves per SIMD the MFMA kernel is built for: six where three double-buffered blocks' LDS
  * fits a CU, else four (the register budget follows: 80 or 128 VGPRs). */
 template <int TYPE, int WSG, int PPW, int NW, int NB, int NT>
 constexpr int mx_waves()
 {
-    if (PPW == 8 && NT == 2) return QMSG_MX_WIDE16_WAVES;    /* two tiles x 16 slots per wave: 168 VGPRs */
+    if (PPW == 8 && NT == 2) return NB == 2 ? 2 : 3;    /* two tiles x 16 slots per wave: 168 VGPRs */
     return NB == 1 ? 4 : (160 * 1024 / mx_lds_bytes(TYPE, WSG, PPW, NW, NB, NT)) * NW / 4 >= 6 ? 6 : 4;
 }
 
@@ -3090,8 +3103,9 @@ void mx_kernel(MxArgs a)
             qoff[j] = unit_off(min(64 * (wave + NW * j) + lane, RWG * Lay::WUR - 1), &u);
         }
     }
-    auto issue = [&](int c, int k) {
-        uint8_t *base = smem + k * BUF;
+    /* chunk c's weight rows into the weight area at base, its records into the record area
+     * at rbase */
+    auto issue_w = [&](int c, uint8_t *base) {
         if constexpr (TYPE == 14) {
             /* the super-block starts 2 bytes past a 4-byte boundary on odd chunks */
             const uint32_t cb = (uint32_t)(c * 210 - 2 * (c & 1));
@@ -3126,15 +3140,22 @@ void mx_kernel(MxArgs a)
                 }
             }
         }
+    };
+    auto issue_r = [&](int c, uint8_t *rbase) {
         /* a slot's kMxC records, the first 96 bytes of each: 48 lanes x 16 bytes */
         if (lane < kMxC * mx_recl(TYPE) / 16) {
             const uint32_t src = (uint32_t)((lane / 6) * kMxRec + 16 * (lane % 6));
 #pragma unroll
             for (int j = 0; j < RPW; j++)
-                dma_to_lds<16>(rsrc[j] + (size_t)c * kMxC * kMxRec + src,
-                               base + Lay::WBYTES + (wave + NW * j) * Lay::RS);
+                dma_to_lds<16>(rsrc[j] + (size_t)c * kMxC * kMxRec + src, rbase + (wave + NW * j) * Lay::RS);
         }
     };
+    auto issue = [&](int c, int k) {
+        issue_w(c, smem + k * BUF);
+        issue_r(c, smem + k * BUF + Lay::WBYTES);
+    };
+    /* NB == 3: weights in two buffers (W0, W1), records in one after them */
+    uint8_t *const rarea = smem + 2 * Lay::WBYTES;
 
     /* A reads: lane row lr is slot ja = lr/8 of the pair, reference lane ka = lr%8; it holds x
      * only if ka%4 == lg, in the low half of its 8 K positions for ka < 4 */
@@ -3173,18 +3194,32 @@ void mx_kernel(MxArgs a)
         if (NB == 2) {
             issue(0, 0);
             mx_wait_barrier();
+        } else if (NB == 3) {
+            issue_w(0, smem);
+            issue_r(0, rarea);
+            mx_wait_barrier();
         }
         for (int c = 0; c < nch; c++) {
-            const int buf = NB == 2 ? c & 1 : 0;
+            const int buf = NB >= 2 ? c & 1 : 0;
             if (NB == 1) {
                 issue(c, 0);
                 mx_wait_barrier();
-            } else if (c + 1 < nch) {
-                issue(c + 1, buf ^ 1);
+            } else if (NB == 2) {
+                if (c + 1 < nch) issue(c + 1, buf ^ 1);
+            } else {
+                if (c > 0) {
+                    /* this chunk's records (every wave is past its reads of the last ones),
+                     * then its weights, requested a chunk ago, and they */
+                    issue_r(c, rarea);
+                    mx_wait_barrier();
+                }
+                /* the next chunk's weights stream in while this one computes */
+                if (c + 1 < nch) issue_w(c + 1, smem + (buf ^ 1) * Lay::WBYTES);
             }
             if constexpr (NP > 0) {
-                const uint8_t *Wl = smem + buf * BUF + ((QS6 ? 16 : 16 * NT) * wr) * WS;
-                const uint8_t *Rl = smem + buf * BUF + Lay::WBYTES + (2 * PPW * ws) * Lay::RS;
+                const uint8_t *Wl = (NB == 3 ? smem + buf * Lay::WBYTES : smem + buf * BUF) +
+                                    ((QS6 ? 16 : 16 * NT) * wr) * WS;
+                const uint8_t *Rl = (NB == 3 ? rarea : smem + buf * BUF + Lay::WBYTES) + (2 * PPW * ws) * Lay::RS;
                 if constexpr (TYPE == 14 && X16) {
                     constexpr int TS6 = QS6 ? RWG / 2 : 16;
                     if (c & 1) mx_chunk16_q6<NP / 2, 2, TS6>(Wl, Rl, lr, lg, offq_lo, offq_hi, acc, cr);
@@ -3199,9 +3234,15 @@ void mx_kernel(MxArgs a)
                     mx_chunk<TYPE, NP, SC>(Wl, Rl, lr, lg, jd, kh != 0, offa_lo, offa_hi, acc, cr);
                 }
             }
-            /* chunk c+1 has landed; buffer c is free for chunk c+2 (one buffer: it is free) */
-            mx_wait_barrier();
+            if (NB == 3) {
+                /* every wave's record and weight reads of chunk c are done */
+                mx_lds_barrier();
+            } else {
+                /* chunk c+1 has landed; buffer c is free for chunk c+2 (one buffer: it is free) */
+                mx_wait_barrier();
+            }
         }
+        if (NB == 3) mx_wait_barrier();
         if constexpr (X16) {
             /* hsum256 per (row, slot), all eight chains in the lane: acc[t][2q] lanes 0-3,
              * acc[t][2q + 1] lanes 4-7 */
@@ -3314,8 +3355,11 @@ static_assert(2 * mx_lds_bytes(14, 2) <= 160 * 1024, "two Q6_K blocks per CU");
  * block takes, the more of them are padding on sparse tiles; the fewer, the fewer MFMAs each
  * staged weight row feeds). A block's waves form row groups of 32 rows x slot groups:
  *   wide16 (Q4_0 / Q4_1, r >= 8): 4 waves, 4 row groups of 8 pairs: 128 rows x 16 slots, each
- *          wave's unpacked weight tiles feeding four quads; one staging buffer, three waves
- *          per SIMD. Against the shapes below at the 235B shape (us, gate/up / down): 321 / 155
+ *          wave's unpacked weight tiles feeding four quads, three waves per SIMD. Gate/up
+ *          stages a chunk in one buffer; down keeps its weights in two buffers and its records
+ *          in one (49 KB, still three blocks per CU), the next chunk's weights streaming in
+ *          while one computes: at the 512-token prefill down 384 against 407 us; gate/up
+ *          that way spills (970 against 845 us). Against the shapes below at the 235B shape (us, gate/up / down): 321 / 155
  *          against 350 / 158 at r = 8, 353 / 171 against 422 / 196 at 10, 384 / 186 against
  *          403 / 213 at 12, 719 / 348 against 734 / 364 at 24; 286 / 138 against 275 / 128 at
  *          6 and 262 / 125 against 239 / 114 at 4, where it is not taken;
@@ -3374,12 +3418,13 @@ static void launch_mx(const MxArgs &a, int rows, int maxt, MxShape shape, hipStr
     else if (shape == kMxWide16) {
         /* Q4_0 / Q4_1 only (mx_shape) */
         if constexpr (TYPE != 14 && QMSG_MX_WIDE16_NT == 1)
-            launch_mx_shape<TYPE, GU, 1, 8, QMSG_MX_WIDE16_NW, QMSG_MX_WIDE16_NB, 1>(a, rows, maxt, st);
+            launch_mx_shape<TYPE, GU, 1, 8, QMSG_MX_WIDE16_NW, GU ? QMSG_MX_WIDE16_NB_GU : QMSG_MX_WIDE16_NB_DN, 1>(
+                a, rows, maxt, st);
         else if constexpr (TYPE != 14)
-            launch_mx_shape<TYPE, GU, 1, 8, 4, QMSG_MX_WIDE16_NB>(a, rows, maxt, st);
+            launch_mx_shape<TYPE, GU, 1, 8, 4, GU ? QMSG_MX_WIDE16_NB_GU : QMSG_MX_WIDE16_NB_DN>(a, rows, maxt, st);
     }
     else if (shape == kMxNarrow) launch_mx_shape<TYPE, GU, 1, 2, 4, (!GU && TYPE == 14) ? 1 : 2>(a, rows, maxt, st);
-    else launch_mx_shape<TYPE, GU, 1, 4, 4, TYPE == 14 ? 1 : QMSG_MX_MID_NB>(a, rows, maxt, st);
+    else launch_mx_shape<TYPE, GU, 1, 4, 4, TYPE == 14 ? QMSG_MX_MID_NB_Q6 : QMSG_MX_MID_NB>(a, rows, maxt, st);
 }
 
 /* Whether the MFMA kernels take this layer: gate and up of one type (Q4_0, Q4_1, or Q6_K with
