@@ -2495,7 +2495,7 @@ typedef __attribute__((address_space(3))) const u32x4 LdsU32x4;
  * word, from two LDS pointers: pq at the lane's code word of the block in tile row lr (Q4_0
  * even blocks: 2 bytes past a word boundary), pd at the block's scale word; tile t is an
  * immediate offset. */
-template <int TYPE, int PAR, bool SC>
+template <int TYPE, int PAR, bool SC, int TS = 16>
 __device__ __forceinline__ MxB mx_weights_q4(LdsPtr pq, LdsPtr pd, int t)
 {
     constexpr int WS = mx_wstride(TYPE);
@@ -2503,10 +2503,10 @@ __device__ __forceinline__ MxB mx_weights_q4(LdsPtr pq, LdsPtr pd, int t)
     MxB w;
     uint32_t v;
     if constexpr (TYPE == 3 || PAR) {
-        v = *(const __attribute__((address_space(3))) uint32_t *)(pq + 16 * t * WS);
+        v = *(const __attribute__((address_space(3))) uint32_t *)(pq + TS * t * WS);
     } else {
-        const uint32_t a0 = *(const __attribute__((address_space(3))) uint32_t *)(pq + 16 * t * WS - 2);
-        const uint32_t a1 = *(const __attribute__((address_space(3))) uint32_t *)(pq + 16 * t * WS + 2);
+        const uint32_t a0 = *(const __attribute__((address_space(3))) uint32_t *)(pq + TS * t * WS - 2);
+        const uint32_t a1 = *(const __attribute__((address_space(3))) uint32_t *)(pq + TS * t * WS + 2);
         v = __builtin_amdgcn_alignbyte(a1, a0, 2);
     }
     /* the high nibbles stay in place, as 16 x code (the records' lanes 4-7 carry x / 16) */
@@ -2525,8 +2525,8 @@ __device__ __forceinline__ MxB mx_weights_q4(LdsPtr pq, LdsPtr pd, int t)
         const f16x2 c3 = __builtin_bit_cast(f16x2, and_or(v8, mh, bias)) - k;
         w.op = f16x8{ c0.x, c0.y, c1.x, c1.y, c2.x, c2.y, c3.x, c3.y };
     }
-    if constexpr (TYPE == 3) w.dw = *(const __attribute__((address_space(3))) uint32_t *)(pd + 16 * t * WS);
-    else w.dw = *(const __attribute__((address_space(3))) uint16_t *)(pd + 16 * t * WS);
+    if constexpr (TYPE == 3) w.dw = *(const __attribute__((address_space(3))) uint32_t *)(pd + TS * t * WS);
+    else w.dw = *(const __attribute__((address_space(3))) uint16_t *)(pd + TS * t * WS);
     w.sc = 0.0f;
     w.sab = 0u;
     w.sc1 = 0.0f;
@@ -2578,14 +2578,14 @@ __device__ __forceinline__ void mx_opaque(MxStreams &st)
 /* One block b (parity PAR within the trip) of the staged chunk: NP slot pairs of this wave
  * against its two 16-row tiles. SC: the chunk's records all carry d_x 2^24 and B holds the
  * codes 2^-24; else B holds the codes themselves and the chains take d_x unscaled. */
-template <int TYPE, int NP, int PAR, bool SC>
+template <int TYPE, int NP, int PAR, bool SC, int TS>
 __device__ __forceinline__ void mx_block(const MxStreams &st, bool kh, f32x4 (&acc)[2][kMxNA], float (&cr)[2][4])
 {
     static_assert(TYPE == 2 || TYPE == 3, "Q6_K chunks take mx_chunk_q6");
     constexpr int BB = TYPE == 3 ? 20 : 18, RB = PAR * mx_recl(TYPE), RS = mx_rstride(TYPE);
     MxB w[2];
 #pragma unroll
-    for (int t = 0; t < 2; t++) w[t] = mx_weights_q4<TYPE, PAR, SC>(st.q + PAR * BB, st.dw + PAR * BB, t);
+    for (int t = 0; t < 2; t++) w[t] = mx_weights_q4<TYPE, PAR, SC, TS>(st.q + PAR * BB, st.dw + PAR * BB, t);
     /* the two lanes of a (row, slot) share its offset chain: the k-half-0 lane runs tile 0's,
      * the other tile 1's (cr[0][p]; the epilogue fetches the partner's) */
     const uint32_t dwc = kh ? w[1].dw : w[0].dw;
@@ -2629,7 +2629,7 @@ __device__ __forceinline__ void mx_block(const MxStreams &st, bool kh, f32x4 (&a
 
 /* One staged chunk (kMxC blocks), two blocks per loop trip. A lane's A words are its x words
  * where it holds x, else the record's zero words. */
-template <int TYPE, int NP, bool SC>
+template <int TYPE, int NP, bool SC, int TS>
 __device__ __forceinline__ void mx_chunk(const uint8_t *W, const uint8_t *R, int lr, int lg, int jd, bool kh,
                                          int offa_lo, int offa_hi, f32x4 (&acc)[2][kMxNA], float (&cr)[2][4])
 {
@@ -2643,9 +2643,9 @@ __device__ __forceinline__ void mx_chunk(const uint8_t *W, const uint8_t *R, int
 #pragma unroll 1
     for (int b = 0; b < kMxC; b += 2) {
         mx_opaque(st);
-        mx_block<TYPE, NP, 0, SC>(st, kh, acc, cr);
+        mx_block<TYPE, NP, 0, SC, TS>(st, kh, acc, cr);
         __builtin_amdgcn_sched_barrier(0);      /* one block's operands in registers at a time */
-        mx_block<TYPE, NP, 1, SC>(st, kh, acc, cr);
+        mx_block<TYPE, NP, 1, SC, TS>(st, kh, acc, cr);
         st.alo += 2 * mx_recl(TYPE);
         st.ahi += 2 * mx_recl(TYPE);
         st.d += 2 * mx_recl(TYPE);
@@ -2664,7 +2664,7 @@ __device__ __forceinline__ void mx_chunk(const uint8_t *W, const uint8_t *R, int
  * (tile, quad, block) serve both halves. */
 typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 
-template <int TYPE, int NQ, int BI, bool SC, int NT>
+template <int TYPE, int NQ, int BI, bool SC, int NT, int TS>
 __device__ __forceinline__ void mx_block16(const MxStreams &st, f32x4 (&acc)[2][kMxNA], float (&cr)[2][4])
 {
     static_assert(TYPE == 2 || TYPE == 3, "Q4_0 / Q4_1 rows");
@@ -2674,7 +2674,7 @@ __device__ __forceinline__ void mx_block16(const MxStreams &st, f32x4 (&acc)[2][
     f16x4 b[2][2];
 #pragma unroll
     for (int t = 0; t < NT; t++) {
-        w[t] = mx_weights_q4<TYPE, PAR, SC>(st.q + BI * BB, st.dw + BI * BB, t);
+        w[t] = mx_weights_q4<TYPE, PAR, SC, TS>(st.q + BI * BB, st.dw + BI * BB, t);
         b[t][0] = __builtin_shufflevector(w[t].op, w[t].op, 0, 1, 2, 3);
         b[t][1] = __builtin_shufflevector(w[t].op, w[t].op, 4, 5, 6, 7);
     }
@@ -2727,7 +2727,7 @@ __device__ __forceinline__ void mx_block16(const MxStreams &st, f32x4 (&acc)[2][
 
 /* One staged chunk on the 16x16x16 instructions, its 8 blocks unrolled; offa_lo / offa_hi are
  * the lane's A words of the low and high halves (or the shared zero words). */
-template <int TYPE, int NQ, bool SC, int NT>
+template <int TYPE, int NQ, bool SC, int NT, int TS>
 __device__ __forceinline__ void mx_chunk16(const uint8_t *W, const uint8_t *R, int lr, int lg, int offa_lo,
                                            int offa_hi, f32x4 (&acc)[2][kMxNA], float (&cr)[2][4])
 {
@@ -2741,21 +2741,21 @@ __device__ __forceinline__ void mx_chunk16(const uint8_t *W, const uint8_t *R, i
     st.dw = (LdsPtr)(W + lr * WS);
     mx_opaque(st);
     /* one block's operands in registers at a time */
-    mx_block16<TYPE, NQ, 0, SC, NT>(st, acc, cr);
+    mx_block16<TYPE, NQ, 0, SC, NT, TS>(st, acc, cr);
     __builtin_amdgcn_sched_barrier(0);
-    mx_block16<TYPE, NQ, 1, SC, NT>(st, acc, cr);
+    mx_block16<TYPE, NQ, 1, SC, NT, TS>(st, acc, cr);
     __builtin_amdgcn_sched_barrier(0);
-    mx_block16<TYPE, NQ, 2, SC, NT>(st, acc, cr);
+    mx_block16<TYPE, NQ, 2, SC, NT, TS>(st, acc, cr);
     __builtin_amdgcn_sched_barrier(0);
-    mx_block16<TYPE, NQ, 3, SC, NT>(st, acc, cr);
+    mx_block16<TYPE, NQ, 3, SC, NT, TS>(st, acc, cr);
     __builtin_amdgcn_sched_barrier(0);
-    mx_block16<TYPE, NQ, 4, SC, NT>(st, acc, cr);
+    mx_block16<TYPE, NQ, 4, SC, NT, TS>(st, acc, cr);
     __builtin_amdgcn_sched_barrier(0);
-    mx_block16<TYPE, NQ, 5, SC, NT>(st, acc, cr);
+    mx_block16<TYPE, NQ, 5, SC, NT, TS>(st, acc, cr);
     __builtin_amdgcn_sched_barrier(0);
-    mx_block16<TYPE, NQ, 6, SC, NT>(st, acc, cr);
+    mx_block16<TYPE, NQ, 6, SC, NT, TS>(st, acc, cr);
     __builtin_amdgcn_sched_barrier(0);
-    mx_block16<TYPE, NQ, 7, SC, NT>(st, acc, cr);
+    mx_block16<TYPE, NQ, 7, SC, NT, TS>(st, acc, cr);
 }
 
 /* A word of a staged Q6_K row at byte off past the row's 4-byte-aligned LDS base (O = 2: the
@@ -2995,10 +2995,10 @@ __device__ __forceinline__ void mx_lds_barrier()
 #ifndef QMSG_MX_MID_NB_Q6
 #define QMSG_MX_MID_NB_Q6 1
 #endif
-/* staging of the 16-slot blocks: gate/up one buffer; down the weights in two, the records
- * in one (mx_lds_bytes nb 3) */
+/* staging of the 16-slot blocks: the weights in two buffers, the records in one
+ * (mx_lds_bytes nb 3) */
 #ifndef QMSG_MX_WIDE16_NB_GU
-#define QMSG_MX_WIDE16_NB_GU 1
+#define QMSG_MX_WIDE16_NB_GU 3
 #endif
 #ifndef QMSG_MX_WIDE16_NB_DN
 #define QMSG_MX_WIDE16_NB_DN 3
@@ -3031,9 +3031,12 @@ void mx_kernel(MxArgs a)
     extern __shared__ __align__(16) uint8_t smem[];
     using Lay = MxLayout<TYPE, WSG, PPW, NW, NT>;
     static_assert(NT == 2 || (NT == 1 && TYPE != 14), "one-tile waves take Q4_0 / Q4_1 rows");
-    /* Q6_K gate/up stages its gate rows, then its up rows (so the DMA steps through one matrix
-     * at a time); the Q4 kernels interleave them by 16-row groups */
+    /* Q6_K gate/up (4-byte DMA units) steps through its gate rows, then its up rows */
     constexpr bool QS6 = GU && TYPE == 14;
+    /* gate/up on two-tile waves: the RWG/2 gate rows staged first, then the same up rows, so
+     * each DMA instruction reads one matrix (a wave-uniform base) and a wave's two tiles (its
+     * gate and up rows) lie RWG/2 rows apart */
+    constexpr bool GSEP = GU && NT == 2;
 #ifdef QMSG_MX_X32
     constexpr bool X16Q = false;
 #elif defined(QMSG_MX_Q6_PAIRS)
@@ -3053,7 +3056,8 @@ void mx_kernel(MxArgs a)
     const int nb = (GU ? a.E : a.F) >> 5, nch = nb / kMxC;
     const int R0 = (int)blockIdx.x * (GU ? RWG / 2 : RWG);
 
-    /* row i of the staged tile: for gate/up, row group g = i / 32 holds gate rows
+    /* row i of the staged tile: for gate/up on two-tile waves gate row R0 + i below RWG/2 and
+     * up row R0 + i - RWG/2 above; on one-tile waves row group g = i / 32 holds gate rows
      * R0 + 16g .. R0 + 16g + 15 and then the same up rows. Byte offsets inside one expert's
      * matrix fit 31 bits (mx_supported); the expert bases are wave-uniform. */
     const uint8_t *wb0 = a.w0 + (size_t)e * a.eb, *wb1 = GU ? a.w1 + (size_t)e * a.eb : wb0;
@@ -3076,16 +3080,17 @@ void mx_kernel(MxArgs a)
      * rows, whose 108 instructions per chunk would take too many registers): the first one,
      * stepped by 512 units per instruction. */
     static_assert(RWG * Lay::WUR % 64 == 0, "whole DMA instructions per chunk");
-    static_assert(!QS6 || (RWG / 2) * Lay::WUR % 64 == 0, "gate rows in whole DMA instructions");
+    static_assert(!GSEP || (RWG / 2) * Lay::WUR % 64 == 0, "gate rows in whole DMA instructions");
     constexpr int NQ = (Lay::WINSTR + NW - 1) / NW;
     uint32_t qoff[TYPE == 14 ? 1 : NQ];
     int qu = 0;
     auto unit_off = [&](int n, int *u_out) -> uint32_t {
         const int i = n / Lay::WUR, u = n - i * Lay::WUR;
         *u_out = u;
-        /* Q6_K gate/up: gate rows first, up rows from staged row RWG/2 on (QS6) */
-        const int row = QS6 ? R0 + (i % (RWG / 2)) : (GU ? R0 + 16 * (i >> 5) + (i & 15) : R0 + i);
-        const uint32_t up = GU && !QS6 && (i & 31) >= 16 ? 0x80000000u : 0u;
+        /* two-tile gate/up: gate rows first, up rows from staged row RWG/2 on (GSEP); one-tile
+         * gate/up: 16 gate rows, then the same up rows (bit 31 of the offset: an up row) */
+        const int row = GSEP ? R0 + (i % (RWG / 2)) : (GU ? R0 + 16 * (i >> 5) + (i & 15) : R0 + i);
+        const uint32_t up = GU && !GSEP && (i & 31) >= 16 ? 0x80000000u : 0u;
         return ((uint32_t)row * rb + (uint32_t)(Lay::WUNIT * u)) | up;
     };
     /* Q6_K gate/up: the first instruction of this wave in the up half, and its source */
@@ -3136,7 +3141,10 @@ void mx_kernel(MxArgs a)
                 const int q = wave + NW * j;
                 if (q < Lay::WINSTR) {
                     const uint32_t o = qoff[j];
-                    dma_to_lds<16>(((o >> 31) ? wb1 : wb0) + ((o & 0x7fffffffu) + cb), base + 1024 * q);
+                    if constexpr (GSEP)   /* instructions 0 .. HALF-1 read gate rows, the rest up rows */
+                        dma_to_lds<16>((q >= HALF ? wb1 : wb0) + (o + cb), base + 1024 * q);
+                    else
+                        dma_to_lds<16>(((o >> 31) ? wb1 : wb0) + ((o & 0x7fffffffu) + cb), base + 1024 * q);
                 }
             }
         }
@@ -3218,7 +3226,7 @@ void mx_kernel(MxArgs a)
             }
             if constexpr (NP > 0) {
                 const uint8_t *Wl = (NB == 3 ? smem + buf * Lay::WBYTES : smem + buf * BUF) +
-                                    ((QS6 ? 16 : 16 * NT) * wr) * WS;
+                                    ((GSEP ? 16 : 16 * NT) * wr) * WS;
                 const uint8_t *Rl = (NB == 3 ? rarea : smem + buf * BUF + Lay::WBYTES) + (2 * PPW * ws) * Lay::RS;
                 if constexpr (TYPE == 14 && X16) {
                     constexpr int TS6 = QS6 ? RWG / 2 : 16;
@@ -3229,9 +3237,9 @@ void mx_kernel(MxArgs a)
                     if (c & 1) mx_chunk_q6<NP, 2, TS6>(Wl, Rl, lr, lg, kh, jd, offa_lo, offa_hi, acc, cr);
                     else mx_chunk_q6<NP, 0, TS6>(Wl, Rl, lr, lg, kh, jd, offa_lo, offa_hi, acc, cr);
                 } else if constexpr (X16) {
-                    mx_chunk16<TYPE, NP / 2, SC, NT>(Wl, Rl, lr, lg, offq_lo, offq_hi, acc, cr);
+                    mx_chunk16<TYPE, NP / 2, SC, NT, GSEP ? RWG / 2 : 16>(Wl, Rl, lr, lg, offq_lo, offq_hi, acc, cr);
                 } else {
-                    mx_chunk<TYPE, NP, SC>(Wl, Rl, lr, lg, jd, kh != 0, offa_lo, offa_hi, acc, cr);
+                    mx_chunk<TYPE, NP, SC, GSEP ? RWG / 2 : 16>(Wl, Rl, lr, lg, jd, kh != 0, offa_lo, offa_hi, acc, cr);
                 }
             }
             if (NB == 3) {
@@ -3355,11 +3363,14 @@ static_assert(2 * mx_lds_bytes(14, 2) <= 160 * 1024, "two Q6_K blocks per CU");
  * block takes, the more of them are padding on sparse tiles; the fewer, the fewer MFMAs each
  * staged weight row feeds). A block's waves form row groups of 32 rows x slot groups:
  *   wide16 (Q4_0 / Q4_1, r >= 8): 4 waves, 4 row groups of 8 pairs: 128 rows x 16 slots, each
- *          wave's unpacked weight tiles feeding four quads, three waves per SIMD. Gate/up
- *          stages a chunk in one buffer; down keeps its weights in two buffers and its records
- *          in one (49 KB, still three blocks per CU), the next chunk's weights streaming in
- *          while one computes: at the 512-token prefill down 384 against 407 us; gate/up
- *          that way spills (970 against 845 us). Against the shapes below at the 235B shape (us, gate/up / down): 321 / 155
+ *          wave's unpacked weight tiles feeding four quads, three waves per SIMD. The weights
+ *          sit in two buffers and the records in one (49 KB, still three blocks per CU), the
+ *          next chunk's weights streaming in while one computes: at the 512-token prefill
+ *          gate/up 794-820 against 850 us with one buffer, down 384 against 407; gate/up at
+ *          128 / 192 / 256 tokens 295 / 363 / 483 against 324 / 391 / 525. Gate/up stages
+ *          its gate rows, then its up rows, so each DMA instruction reads one matrix from a
+ *          wave-uniform base (with 16-row groups interleaved it spilled 20 registers this
+ *          way and ran 970 us). Against the shapes below at the 235B shape (us, gate/up / down): 321 / 155
  *          against 350 / 158 at r = 8, 353 / 171 against 422 / 196 at 10, 384 / 186 against
  *          403 / 213 at 12, 719 / 348 against 734 / 364 at 24; 286 / 138 against 275 / 128 at
  *          6 and 262 / 125 against 239 / 114 at 4, where it is not taken;
