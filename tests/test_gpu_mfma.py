@@ -33,6 +33,11 @@ CASES = [
     ("tiny_t40", 256, 16, 4, 128, 40, 9, orc.T_Q4_0, False),         # down on the exact kernel
     ("tiny_q6k_t200", 256, 16, 4, 256, 200, 10, orc.T_Q6_K, False),  # 50 slots per expert: 16-slot blocks
     ("q30b_q41_t256", 2048, 128, 8, 768, 256, 15, orc.T_Q4_1, False),  # 16 slots per expert: wide Q4_1 down
+    # 16-slot blocks on one, two and three staged chunks (n_embd / 256 for gate/up, n_ff_exp / 256
+    # for down): the double-buffered weights' first and last chunks
+    ("tiny_t200", 256, 16, 4, 256, 200, 16, orc.T_Q4_0, False),
+    ("small_t160", 512, 16, 4, 512, 160, 17, orc.T_Q4_1, False),
+    ("small_t96", 768, 16, 4, 768, 96, 18, orc.T_Q4_0, False),
     ("q235b_zipf_t512", 4096, 128, 8, 1536, 512, 5, orc.T_Q4_0, True),
 ]
 
