@@ -354,24 +354,29 @@ __global__ __launch_bounds__(256) void route_small_kernel(RouteArgs a)
 }
 
 /* Router for T > 4: one block per 4KT tokens x 4J experts, 256 threads. Thread (c, ea, tb)
- * runs chain c of J experts x KT tokens over 256-element chunks staged in LDS, so each chain
- * still walks its elements c, c+16, ... in order. The next P chunks are in flight in
- * registers while one is consumed. Small blocks (J = KT = 1: 4 experts x 4 tokens) spread
- * batches of up to 64 tokens over many CUs; larger batches take J = KT = 4 (16 x 16), which
- * reads each router and input row fewer times. */
+ * runs chain c of J experts x KT tokens over 256-element chunks staged in LDS chain-major (as
+ * route_small_kernel does: chain c of a row holds its 16 elements c, c+16, ... of the chunk
+ * contiguously, padded to CSC floats, so one 16-byte read gives a lane four steps of its
+ * chain), so each chain still walks its elements c, c+16, ... in order. The next P chunks are
+ * in flight in registers while one is consumed. Small blocks (J = KT = 1: 4 experts x 4
+ * tokens) spread batches of up to 64 tokens over many CUs; larger batches take J = KT = 4
+ * (16 x 16), which reads each router and input row fewer times. */
+constexpr int kRouteBigCSC = 20;                  /* floats per chain and chunk in LDS (16 + pad) */
+/* LDS bytes of route_big_kernel<J, J, P>: 4J expert rows and 4J token rows of 16 chains. */
+constexpr size_t route_big_lds(int J) { return (size_t)(8 * J) * 16 * kRouteBigCSC * 4; }
 template <int J, int KT, int P>
 __global__ __launch_bounds__(256) void route_big_kernel(RouteArgs a)
 {
     extern __shared__ __align__(16) uint8_t smem[];
     if ((int)blockIdx.x >= a.n_route_wg) { route_quantize(a); return; }
-    constexpr int CH = 256, RS = CH + 4;          /* chunk elements, padded LDS row */
+    constexpr int CH = 256, CSC = kRouteBigCSC, RSC = 16 * CSC;   /* chunk elements, chain and row strides */
     constexpr int EB = 4 * J;                     /* experts per block              */
     const int tid = threadIdx.x, E = a.E, T = a.T, X = a.X;
     constexpr int TB = 4 * KT;                    /* tokens per block               */
     const int egs = (X + EB - 1) / EB, tg = (int)blockIdx.x / egs, eg = (int)blockIdx.x - tg * egs;
     const int t0 = tg * TB, e0 = eg * EB;
     const int c = tid & 15, ea = (tid >> 4) & 3, tb = tid >> 6;
-    float *W = (float *)smem, *Xt = W + EB * RS;
+    float *W = (float *)smem, *Xt = W + EB * RSC;
     float acc[J][KT];
     for (int j = 0; j < J; j++) for (int k = 0; k < KT; k++) acc[j][k] = 0.0f;
     u32x4 pw[P][J], px[P][KT];
@@ -388,6 +393,15 @@ __global__ __launch_bounds__(256) void route_big_kernel(RouteArgs a)
             x[m] = *(const u32x4 *)(a.xn + (size_t)min(t0 + (q >> 6), T - 1) * E + (size_t)ch * CH + (q & 63) * 4);
         }
     };
+    /* the 16-byte slot q4 of a row's chunk holds elements 4 q4 .. 4 q4 + 3: step q4 / 4 of chains
+     * 4 (q4 % 4) .. 4 (q4 % 4) + 3 */
+    auto stage = [&](float *rowbase, int q4, const u32x4 &v) {
+        float *dst = rowbase + (4 * (q4 & 3)) * CSC + (q4 >> 2);
+        dst[0] = __uint_as_float(v.x);
+        dst[CSC] = __uint_as_float(v.y);
+        dst[2 * CSC] = __uint_as_float(v.z);
+        dst[3 * CSC] = __uint_as_float(v.w);
+    };
 #pragma unroll
     for (int d = 0; d < P; d++)
         if (d < nch) load(d, pw[d], px[d]);
@@ -400,23 +414,27 @@ __global__ __launch_bounds__(256) void route_big_kernel(RouteArgs a)
 #pragma unroll
                 for (int m = 0; m < J; m++) {
                     const int q = tid + 256 * m;
-                    *(u32x4 *)(W + (q >> 6) * RS + (q & 63) * 4) = pw[d][m];
+                    stage(W + (q >> 6) * RSC, q & 63, pw[d][m]);
                 }
 #pragma unroll
                 for (int m = 0; m < KT; m++) {
                     const int q = tid + 256 * m;
-                    *(u32x4 *)(Xt + (q >> 6) * RS + (q & 63) * 4) = px[d][m];
+                    stage(Xt + (q >> 6) * RSC, q & 63, px[d][m]);
                 }
                 __syncthreads();
                 if (ch + P < nch) load(ch + P, pw[d], px[d]);
 #pragma unroll
-                for (int s = 0; s < 16; s++) {
-                    const int i = 16 * s + c;
-                    float wv[J], xv[KT];
-                    for (int j = 0; j < J; j++) wv[j] = W[(J * ea + j) * RS + i];
-                    for (int k = 0; k < KT; k++) xv[k] = Xt[(KT * tb + k) * RS + i];
+                for (int s0 = 0; s0 < 16; s0 += 4) {
+                    float4 wv[J], xv[KT];
+                    for (int j = 0; j < J; j++) wv[j] = *(const float4 *)(W + (J * ea + j) * RSC + c * CSC + s0);
+                    for (int k = 0; k < KT; k++) xv[k] = *(const float4 *)(Xt + (KT * tb + k) * RSC + c * CSC + s0);
                     for (int j = 0; j < J; j++)
-                        for (int k = 0; k < KT; k++) acc[j][k] = __builtin_fmaf(wv[j], xv[k], acc[j][k]);
+                        for (int k = 0; k < KT; k++) {
+                            acc[j][k] = __builtin_fmaf(wv[j].x, xv[k].x, acc[j][k]);
+                            acc[j][k] = __builtin_fmaf(wv[j].y, xv[k].y, acc[j][k]);
+                            acc[j][k] = __builtin_fmaf(wv[j].z, xv[k].z, acc[j][k]);
+                            acc[j][k] = __builtin_fmaf(wv[j].w, xv[k].w, acc[j][k]);
+                        }
                 }
             }
         }
@@ -456,7 +474,7 @@ hipError_t launch_route(const Shape &s, const LayerDev &L, const Scratch &S, con
     } else {
         const int J = T <= 64 ? 1 : 4;               /* experts and tokens per thread group */
         a.n_route_wg = ((T + 4 * J - 1) / (4 * J)) * ((s.X + 4 * J - 1) / (4 * J));
-        const size_t lds = (size_t)(8 * J) * (256 + 4) * 4;
+        const size_t lds = route_big_lds(J);
         if (J == 1) QLAUNCH("route", (route_big_kernel<1, 1, kRouteBigP>), dim3(a.n_route_wg + nq), dim3(256), lds, st, a);
         else QLAUNCH("route", (route_big_kernel<4, 4, kRouteBigP>), dim3(a.n_route_wg + nq), dim3(256), lds, st, a);
     }
@@ -4076,12 +4094,10 @@ hipError_t launch_dense(const DenseArgs &args, int type, uint8_t *xqk, hipStream
                 QLAUNCH("dense", route_small_kernel<1>, dim3(r.X), dim3(256), lds, st, r);
             } else if (a.T == 1) {
                 r.n_route_wg = (r.X + 3) / 4;
-                const size_t lds = (size_t)8 * (256 + 4) * 4;
-                QLAUNCH("dense", (route_big_kernel<1, 1, kRouteBigP>), dim3(r.n_route_wg), dim3(256), lds, st, r);
+                QLAUNCH("dense", (route_big_kernel<1, 1, kRouteBigP>), dim3(r.n_route_wg), dim3(256), route_big_lds(1), st, r);
             } else {
                 r.n_route_wg = ((a.T + 15) / 16) * ((r.X + 15) / 16);
-                const size_t lds = (size_t)32 * (256 + 4) * 4;
-                QLAUNCH("dense", (route_big_kernel<4, 4, kRouteBigP>), dim3(r.n_route_wg), dim3(256), lds, st, r);
+                QLAUNCH("dense", (route_big_kernel<4, 4, kRouteBigP>), dim3(r.n_route_wg), dim3(256), route_big_lds(4), st, r);
             }
         }
         return hipGetLastError();
