@@ -499,9 +499,8 @@ __device__ void topk_from_ranks(int K, int X, const float *L, const double *P, c
  * order after checking it for rounding ties (else it ranks the p exactly) and forms the
  * weights, wsum summed in selection order. LDS: P[X] doubles, part[] the float logits and
  * their ranks, selb[0 .. 63] the selection and selb[64 ..] K + 1 candidates. */
-__device__ void topk_token(const SelectArgs &a, int t, int tid, double *P, int *part, int *selb, double *sh)
+__device__ void topk_token(const SelectArgs &a, int t, int tid, double *P, int *part, int *selb)
 {
-    (void)sh;
     const int X = a.X, K = a.K;
     float *L = (float *)part;
     int *rank = part + kMaxExperts;
@@ -620,10 +619,9 @@ __global__ __launch_bounds__(256) void select_kernel(SelectArgs a, int do_dispat
     __shared__ int selb[64 + 65];                /* the selection, then K + 1 candidates */
     __shared__ int tok[kMaxExperts];
     __shared__ int last;
-    __shared__ double sh[5];
     const int t = blockIdx.x;
     PHASE(0, 0);
-    if (t < a.T) topk_token(a, t, threadIdx.x, P, part, selb, sh);
+    if (t < a.T) topk_token(a, t, threadIdx.x, P, part, selb);
     PHASE(0, 5);
     if (!do_dispatch) return;
     if (gridDim.x > 1) {
