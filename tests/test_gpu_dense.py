@@ -175,3 +175,27 @@ def test_dense_many_tokens_every_type(q):
         assert all(y.shape == (0, r) for y, (_, r, _) in zip(ctx.matmul_n(ids, x[:0]), specs))
     for (t, r, s), y in zip(specs, ys):
         assert np.array_equal(bits(y), bits(orc.matmul_q8(t, dense_mat(t, r, C, s), r, C, x))), t
+
+
+DENSE_TYPES = (orc.T_F32, orc.T_Q4_0, orc.T_Q4_1, orc.T_Q6_K)
+
+
+@pytest.mark.parametrize("seed", range(40))
+def test_dense_random_calls(q, seed):
+    """Seeded random calls: one to five matrices of random types (F32, Q4_0, Q4_1, and Q6_K
+    where the width is a multiple of 2048) and row counts sharing a width of 256-8192 columns,
+    1-40 tokens; every product bit for bit against the oracle's qms_matmul."""
+    rng = np.random.default_rng(7000 + seed)
+    C = int(rng.choice([256, 512, 768, 1024, 2048, 4096, 6144, 8192]))
+    T = int(rng.choice([1, 1, 2, 3, 4, 5, 8, 16, 17, 40]))
+    nm = int(rng.integers(1, 6))
+    types = DENSE_TYPES if C % 2048 == 0 else DENSE_TYPES[:3]
+    specs = [(int(rng.choice(types)), int(rng.integers(1, 1200))) for _ in range(nm)]
+    print(f"[case] dense random seed {seed}: C={C} T={T} {specs}", flush=True)
+    ws = [dense_mat(t, r, C, 500 + 10 * seed + i) for i, (t, r) in enumerate(specs)]
+    x = orc.make_input(C, T, 900 + seed)
+    with q.Context(256, 16, 4, 128, max_tokens=1) as ctx:
+        ids = [ctx.mat_upload(t, w, r, C) for (t, r), w in zip(specs, ws)]
+        ys = ctx.matmul_n(ids, x)
+    for (t, r), w, y in zip(specs, ws, ys):
+        assert np.array_equal(bits(y), bits(orc.matmul_q8(t, w, r, C, x))), (t, r)
