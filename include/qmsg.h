@@ -190,11 +190,11 @@ int qmsg_gguf_upload(qmsg_ctx *ctx, const qmsg_gguf *g, int first, int n);
 /* A dense weight matrix resident in HBM, a QmsMat (src/quant.h:11-16) loaded by load_mat
  * (src/model.c:67-85): rows of row_bytes GGUF bytes, copied unchanged; *id names it in
  * qmsg_matmul_n. The types of the reference's fast path (qms_fast_supported,
- * src/kernels.c:197-200): F32, Q4_0 and Q4_1 rows with cols % 256 == 0, Q6_K rows with
- * cols % 2048 == 0; QMSG_E_UNSUPPORTED otherwise. The reference's fast path is wider: Q4
- * rows with cols % 32 == 0 and Q6_K rows with cols % 256 == 0 (src/quant.c:134-136), any
- * other width going to its matmul_exact; no Qwen3-MoE trunk matrix has a width outside both
- * rules (2048, 4096, 6144 and 8192 columns). */
+ * src/kernels.c:197-200) at the widths it admits (src/quant.c:134-136): F32, Q4_0 and Q4_1
+ * rows with cols % 32 == 0, Q6_K rows with cols % 256 == 0; QMSG_E_UNSUPPORTED otherwise
+ * (the reference would take matmul_exact). Widths off the chunked kernels' grid (cols % 256,
+ * Q6_K cols % 2048; no Qwen3-MoE trunk matrix has one) take a direct-read kernel, which
+ * bounds quantised rows to cols <= 109,216 there. */
 int qmsg_mat_upload(qmsg_ctx *ctx, const qmsg_mat *host, int *id);
 /* The same from a parsed GGUF file, by tensor name (e.g. "blk.0.attn_q.weight"). */
 int qmsg_gguf_upload_mat(qmsg_ctx *ctx, const qmsg_gguf *g, const char *name, int *id);

@@ -612,11 +612,17 @@ static int dense_check(qmsg_ctx *c, int type, int64_t rows, int64_t cols, const 
     if (type != QMSG_T_F32 && type != QMSG_T_Q4_0 && type != QMSG_T_Q4_1 && type != QMSG_T_Q6_K)
         return fail(c, QMSG_E_UNSUPPORTED, "%s: the dense kernels take F32, Q4_0, Q4_1 and Q6_K (got type %d)", what,
                     type);
-    const int64_t step = type == QMSG_T_Q6_K ? 2048 : 256;   /* Q6_K: whole chunks of 8 super-blocks */
+    const int64_t step = type == QMSG_T_Q6_K ? 256 : 32;     /* src/quant.c:135-136 */
     /* both bounded by 2^30: rows x row bytes stays far inside 64 bits and cols fits an int */
     if (rows <= 0 || rows > (1 << 30) || cols <= 0 || cols > (1 << 30) || cols % step)
         return fail(c, QMSG_E_UNSUPPORTED, "%s: needs 0 < rows, cols <= 2^30 and cols %% %lld == 0 (got %lld x %lld)",
                     what, (long long)step, (long long)rows, (long long)cols);
+    /* widths off the chunked kernels' grid (cols % 256, Q6_K cols % 2048) take the direct-read
+     * kernel, whose quantised input row must fit in LDS: 48 bytes per 32-block, 160 KiB */
+    const bool direct = cols % (type == QMSG_T_Q6_K ? 2048 : 256) != 0;
+    if (direct && type != QMSG_T_F32 && cols / 32 * 48 > 160 * 1024)
+        return fail(c, QMSG_E_UNSUPPORTED, "%s: cols %lld is not a multiple of %d and above %d", what, (long long)cols,
+                    type == QMSG_T_Q6_K ? 2048 : 256, 160 * 1024 / 48 * 32);
     return QMSG_OK;
 }
 

@@ -4048,6 +4048,148 @@ __global__ __launch_bounds__(64 * W) void dense_tok_kernel(DenseArgs a)
     }
 }
 
+/* qms_matmul_n's fast loop (src/quant.c:134-169) for the row widths the chunked kernels above
+ * do not take: F32, Q4_0 and Q4_1 rows with cols % 256 != 0 and Q6_K rows with
+ * cols % 2048 != 0, which the reference's fast path still admits (cols % 32; Q6_K cols % 256).
+ * A lane group per row reads the row's words straight from memory: eight lanes per quantised
+ * row, lane k keeping the reference's FMA chain k (elements 4k..4k+3 of every 32-block) and
+ * the offset chain; sixteen lanes per F32 row, lane c keeping chain c of dot_f32 (elements
+ * c, c+16, ...; src/kernels.c:202-213). Up to NT tokens share a pass: their int8 blocks
+ * (qms_quantize_q8) sit in LDS as 48-byte records {q[32], d, ds, s16[2], pad}; F32 passes
+ * read the inputs from memory. Rows past a matrix's end read its last row and store nothing.
+ * No Qwen3-MoE trunk matrix has such a width; this path is for completeness, not speed. */
+constexpr int kDenseAnyRec = 48;
+
+__device__ __forceinline__ uint32_t ld_u32_a2(const uint8_t *p)   /* p a multiple of 2 */
+{
+    const uint16_t *h = (const uint16_t *)p;
+    return (uint32_t)h[0] | ((uint32_t)h[1] << 16);
+}
+
+template <int TYPE, int NT>
+__global__ __launch_bounds__(256) void dense_any_kernel(DenseArgs a)
+{
+    extern __shared__ __align__(16) uint8_t smem[];
+    constexpr int RPW = TYPE == 0 ? 4 : 8;            /* rows per wave  */
+    constexpr int LPR = 64 / RPW;                     /* lanes per row  */
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, k = lane % LPR;
+    int mi = 0;
+#pragma unroll
+    for (int i = 1; i < kDenseMats; i++)
+        if (i < a.nm && (int)blockIdx.x >= a.m[i].first_block) mi = i;
+    const DenseMat M = a.m[mi];
+    const int row = ((int)blockIdx.x - M.first_block) * 4 * RPW + wave * RPW + lane / LPR;
+    const uint8_t *wr = M.w + (size_t)min(row, M.rows - 1) * a.rb;
+    const int C = a.C, nb = C >> 5;
+    for (int t0 = 0; t0 < a.T; t0 += NT) {
+        const int nt = min(NT, a.T - t0);
+        float acc[NT], corr[NT];
+#pragma unroll
+        for (int n = 0; n < NT; n++) { acc[n] = 0.0f; corr[n] = 0.0f; }
+        if constexpr (TYPE == 0) {
+            const float *w = (const float *)wr, *x = a.x + (size_t)t0 * C;
+            for (int i = k; i < C; i += 16) {
+                const float wv = w[i];
+#pragma unroll
+                for (int n = 0; n < NT; n++)
+                    if (n < nt) acc[n] = __builtin_fmaf(wv, x[(size_t)n * C + i], acc[n]);
+            }
+        } else {
+            if (t0 > 0) __syncthreads();              /* the previous pass is done with the records */
+            for (int i = tid; i < nt * nb; i += 256) {
+                const int n = i / nb, blk = i - n * nb;
+                float v[32];
+                const float4 *src = (const float4 *)(a.x + (size_t)(t0 + n) * C + (size_t)blk * 32);
+#pragma unroll
+                for (int j = 0; j < 8; j++) {
+                    const float4 f = src[j];
+                    v[4 * j] = f.x; v[4 * j + 1] = f.y; v[4 * j + 2] = f.z; v[4 * j + 3] = f.w;
+                }
+                const Q8Vals q = quantize_block(v);
+                uint32_t *o = (uint32_t *)(smem + (size_t)i * kDenseAnyRec);
+#pragma unroll
+                for (int j = 0; j < 8; j++) o[j] = q.qw[j];
+                o[8] = __float_as_uint(q.d);
+                o[9] = __float_as_uint(q.ds);
+                o[10] = q.s16;
+                o[11] = 0;
+            }
+            __syncthreads();
+            auto rec = [&](int n, int blk) { return smem + ((size_t)n * nb + blk) * kDenseAnyRec; };
+            if constexpr (TYPE == 14) {
+                const int hi = k >> 2;
+                for (int s = 0; s < nb / 8; s++) {
+                    const uint8_t *sp = wr + (size_t)s * 210;
+                    const float d = h2f(*(const uint16_t *)(sp + 208));
+#pragma unroll
+                    for (int h = 0; h < 2; h++) {
+                        const uint32_t ql0 = ld_u32_a2(sp + 64 * h + 4 * k), ql1 = ld_u32_a2(sp + 64 * h + 32 + 4 * k);
+                        const uint32_t qh = ld_u32_a2(sp + 128 + 32 * h + 4 * k);
+                        const uint32_t sc0 = ld_u32_a2(sp + 192 + 8 * h), sc1 = ld_u32_a2(sp + 196 + 8 * h);
+#pragma unroll
+                        for (int g = 0; g < 4; g++) {
+                            const uint32_t ql = (g & 1) ? ql1 : ql0;
+                            const uint32_t nib = g < 2 ? (ql & 0x0f0f0f0fu) : ((ql >> 4) & 0x0f0f0f0fu);
+                            const uint32_t q6 = nib | (((qh >> (2 * g)) & 0x03030303u) << 4);
+                            const uint32_t scw = (g < 2 ? sc0 : sc1) >> (16 * (g & 1));
+                            const int sa = (int)(int8_t)(scw & 0xff), sbv = (int)(int8_t)((scw >> 8) & 0xff);
+#pragma unroll
+                            for (int n = 0; n < NT; n++) {
+                                if (n >= nt) break;
+                                const uint32_t *xr = (const uint32_t *)rec(n, 8 * s + 4 * h + g);
+                                const float dd = d * __uint_as_float(xr[8]);
+                                const int s16a = (int)(int16_t)(xr[10] & 0xffffu), s16b = (int)(int16_t)(xr[10] >> 16);
+                                acc[n] = __builtin_fmaf((float)(sdot4((int)q6, (int)xr[k]) * (hi ? sbv : sa)), dd, acc[n]);
+                                corr[n] = __builtin_fmaf(dd, (float)(sa * s16a + sbv * s16b), corr[n]);
+                            }
+                        }
+                    }
+                }
+            } else {
+                constexpr int BB = TYPE == 3 ? 20 : 18;
+                for (int b = 0; b < nb; b++) {
+                    const uint8_t *bp = wr + (size_t)b * BB;
+                    float d, o;
+                    uint32_t c;
+                    if (TYPE == 3) {
+                        const uint32_t dm = *(const uint32_t *)bp;      /* 20-byte blocks: 4-byte aligned */
+                        d = h2f(dm & 0xffffu);
+                        o = h2f(dm >> 16);
+                        c = *(const uint32_t *)(bp + 4 + 4 * (k & 3));
+                    } else {
+                        d = h2f(*(const uint16_t *)bp);
+                        o = d;
+                        c = ld_u32_a2(bp + 2 + 4 * (k & 3));
+                    }
+                    const uint32_t nib = (k < 4 ? c : c >> 4) & 0x0f0f0f0fu;
+#pragma unroll
+                    for (int n = 0; n < NT; n++) {
+                        if (n >= nt) break;
+                        const uint32_t *xr = (const uint32_t *)rec(n, b);
+                        acc[n] = __builtin_fmaf((float)sdot4((int)nib, (int)xr[k]), d * __uint_as_float(xr[8]), acc[n]);
+                        corr[n] = __builtin_fmaf(o, __uint_as_float(xr[9]), corr[n]);
+                    }
+                }
+            }
+        }
+#pragma unroll
+        for (int n = 0; n < NT; n++) {
+            const float v = TYPE == 0 ? chain16_sum(acc[n]) : oct_finish(acc[n], corr[n], finish_scale(TYPE));
+            if (k == 0 && n < nt && row < M.rows) M.y[(size_t)(t0 + n) * M.rows + row] = v;
+        }
+    }
+}
+
+/* Tokens per pass of dense_any_kernel for a batch of T and nb 32-blocks per row: the fewest
+ * passes whose records fit 64 KiB of LDS (0: one token's do not fit at all). */
+static int dense_any_nt(int type, int T, int nb)
+{
+    int nt = T <= 1 ? 1 : (T <= 2 ? 2 : (T <= 4 ? 4 : 8));
+    if (type == 0) return nt;
+    while (nt > 1 && (size_t)nt * nb * kDenseAnyRec > 64 * 1024) nt >>= 1;
+    return (size_t)nb * kDenseAnyRec <= 160 * 1024 ? nt : 0;
+}
+
 /* Tokens per wave of dense_tok_kernel's passes for a batch of T (four waves per block), and
  * its LDS bytes. */
 constexpr int kDenseTokW = 4;
@@ -4069,6 +4211,30 @@ hipError_t launch_dense(const DenseArgs &args, int type, uint8_t *xqk, hipStream
 {
     DenseArgs a = args;
     const int nb = a.C / 32;
+    if (type == 14 ? nb % 64 != 0 : nb % 8 != 0) {
+        /* widths the chunked kernels do not take: one direct-read pass per NT tokens */
+        const int NT = dense_any_nt(type, a.T, nb);
+        if (!NT) return hipErrorInvalidValue;
+        const int rpb = type == 0 ? 16 : 32;
+        int nblk = 0;
+        for (int i = 0; i < a.nm; i++) {
+            a.m[i].first_block = nblk;
+            nblk += (a.m[i].rows + rpb - 1) / rpb;
+        }
+        const size_t lds = type == 0 ? 0 : (size_t)NT * nb * kDenseAnyRec;
+        auto go = [&](auto ty) {
+            constexpr int TY = decltype(ty)::value;
+            if (NT == 8) QLAUNCH("dense", (dense_any_kernel<TY, 8>), dim3(nblk), dim3(256), lds, st, a);
+            else if (NT == 4) QLAUNCH("dense", (dense_any_kernel<TY, 4>), dim3(nblk), dim3(256), lds, st, a);
+            else if (NT == 2) QLAUNCH("dense", (dense_any_kernel<TY, 2>), dim3(nblk), dim3(256), lds, st, a);
+            else QLAUNCH("dense", (dense_any_kernel<TY, 1>), dim3(nblk), dim3(256), lds, st, a);
+        };
+        if (type == 0) go(std::integral_constant<int, 0>());
+        else if (type == 14) go(std::integral_constant<int, 14>());
+        else if (type == 3) go(std::integral_constant<int, 3>());
+        else go(std::integral_constant<int, 2>());
+        return hipGetLastError();
+    }
     if (type == 0) {
         /* F32 rows: qms_vec_dot_f32 (src/quant.c:161-163, src/kernels.c:202-221), the router's
          * arithmetic; one launch per matrix */

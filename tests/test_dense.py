@@ -52,7 +52,9 @@ def test_oracle_matmul_row_is_vec_dot():
 @pytest.mark.skipif(orc.ref_library_path() is None, reason="oracle/_ref (the reference build) is not built here")
 @pytest.mark.parametrize("t,rows,cols,T", [(orc.T_Q4_0, 96, 4096, 5), (orc.T_Q4_1, 33, 1024, 2),
                                            (orc.T_Q6_K, 20, 2048, 3), (orc.T_F32, 24, 1024, 3),
-                                           (orc.T_F32, 7, 4096, 1)])
+                                           (orc.T_F32, 7, 4096, 1), (orc.T_Q4_0, 17, 96, 3),
+                                           (orc.T_Q4_1, 9, 800, 2), (orc.T_Q6_K, 11, 768, 4),
+                                           (orc.T_F32, 5, 4128, 2), (orc.T_Q6_K, 3, 256, 1)])
 def test_oracle_matmul_matches_reference_live(t, rows, cols, T):
     R = orc.load_ref()
 

@@ -121,10 +121,13 @@ def test_dense_from_gguf_and_errors(q, tmp_path):
         with pytest.raises(q.QmsgError):
             ctx.matmul_n([mid + 5], x)                             # unknown id
         with pytest.raises(q.QmsgError) as ei:
-            ctx.mat_upload(orc.T_Q4_0, dense_mat(orc.T_Q4_0, 4, 96, 1), 4, 96)   # cols % 256
+            ctx.mat_synth(orc.T_F32, 4, 80, 1)                                 # cols % 32
         assert ei.value.status == -2
         with pytest.raises(q.QmsgError) as ei:
-            ctx.mat_synth(orc.T_Q6_K, 4, 1024, 1)                              # Q6_K: cols % 2048
+            ctx.mat_synth(orc.T_Q6_K, 4, 640, 1)                               # Q6_K: cols % 256
+        assert ei.value.status == -2
+        with pytest.raises(q.QmsgError, match="109216") as ei:
+            ctx.mat_synth(orc.T_Q4_1, 4, 109248, 1)                            # direct-read kernel's bound
         assert ei.value.status == -2
         with pytest.raises(q.QmsgError, match="2\\^30") as ei:
             ctx.mat_synth(orc.T_Q4_0, 1, 2 ** 31, 1)                           # cols beyond 2^30
@@ -148,6 +151,38 @@ def test_dense_q6k_and_f32_trunk_shapes(q, T):
     for (t, r, c, s), y in zip(specs, ys):
         ref = orc.matmul_q8(t, dense_mat(t, r, c, s), r, c, x)
         assert np.array_equal(bits(y), bits(ref)), (t, r)
+
+
+@pytest.mark.parametrize("T", [1, 2, 3, 5, 9, 20])
+def test_dense_odd_widths(q, T):
+    """Widths the reference's fast path admits (src/quant.c:134-136) off the chunked kernels'
+    grid, on the direct-read kernel: F32 / Q4_0 / Q4_1 rows of 96, 800 and 4128 columns (not
+    multiples of 256), Q6_K rows of 256, 768 and 4352 (not multiples of 2048) beside Q4 and F32
+    rows of the same width on the chunked kernels, ragged row counts, four types in a call."""
+    for C in (96, 256, 768, 800, 4128, 4352):
+        print(f"[case] dense odd width C={C} T={T}", flush=True)
+        x = orc.make_input(C, T, 60 + C) * np.float32(2.0)
+        types = [orc.T_Q4_0, orc.T_Q4_1, orc.T_F32] + ([orc.T_Q6_K] if C % 256 == 0 else [])
+        specs = [(t, 33 + 17 * i, 70 + i) for i, t in enumerate(types)]
+        with q.Context(256, 16, 4, 128, max_tokens=1) as ctx:
+            ids = [ctx.mat_synth(t, r, C, s) for t, r, s in specs]
+            ys = ctx.matmul_n(ids, x)
+        for (t, r, s), y in zip(specs, ys):
+            assert np.array_equal(bits(y), bits(orc.matmul_q8(t, dense_mat(t, r, C, s), r, C, x))), (C, t)
+
+
+def test_dense_direct_read_widest(q):
+    """The widest row the direct-read kernel takes (109,216 columns: one token's 3,413 int8
+    blocks fill 160 KiB of LDS), Q4_0 and Q4_1, two tokens in two passes."""
+    C, T = 109216, 2
+    print(f"[case] dense direct-read widest C={C}", flush=True)
+    x = orc.make_input(C, T, 61)
+    specs = [(orc.T_Q4_0, 7, 81), (orc.T_Q4_1, 5, 82)]
+    with q.Context(256, 16, 4, 128, max_tokens=1) as ctx:
+        ids = [ctx.mat_synth(t, r, C, s) for t, r, s in specs]
+        ys = ctx.matmul_n(ids, x)
+    for (t, r, s), y in zip(specs, ys):
+        assert np.array_equal(bits(y), bits(orc.matmul_q8(t, dense_mat(t, r, C, s), r, C, x))), t
 
 
 @pytest.mark.parametrize("T", [1, 3, 6])
@@ -183,13 +218,13 @@ DENSE_TYPES = (orc.T_F32, orc.T_Q4_0, orc.T_Q4_1, orc.T_Q6_K)
 @pytest.mark.parametrize("seed", range(40))
 def test_dense_random_calls(q, seed):
     """Seeded random calls: one to five matrices of random types (F32, Q4_0, Q4_1, and Q6_K
-    where the width is a multiple of 2048) and row counts sharing a width of 256-8192 columns,
+    where the width is a multiple of 256) and row counts sharing a width of 96-8192 columns,
     1-40 tokens; every product bit for bit against the oracle's qms_matmul."""
     rng = np.random.default_rng(7000 + seed)
-    C = int(rng.choice([256, 512, 768, 1024, 2048, 4096, 6144, 8192]))
+    C = int(rng.choice([96, 256, 512, 768, 800, 1024, 2048, 4096, 4128, 4352, 6144, 8192]))
     T = int(rng.choice([1, 1, 2, 3, 4, 5, 8, 16, 17, 40]))
     nm = int(rng.integers(1, 6))
-    types = DENSE_TYPES if C % 2048 == 0 else DENSE_TYPES[:3]
+    types = DENSE_TYPES if C % 256 == 0 else DENSE_TYPES[:3]
     specs = [(int(rng.choice(types)), int(rng.integers(1, 1200))) for _ in range(nm)]
     print(f"[case] dense random seed {seed}: C={C} T={T} {specs}", flush=True)
     ws = [dense_mat(t, r, C, 500 + 10 * seed + i) for i, (t, r) in enumerate(specs)]
