@@ -96,9 +96,12 @@ enum { QMSG_PATH_AUTO = 0, QMSG_PATH_EXACT = 1, QMSG_PATH_MFMA = 2, QMSG_PATH_FP
 
 /* No reference counterpart (the reference keeps this state in QmsModel, src/model.h:106-139):
  * create a context on HIP device `device` for `n_layer` resident layers of shape `cfg`,
- * with device scratch for up to `max_tokens` tokens per call. Shapes: n_embd % 256 == 0 (the
- * reference's fast-path condition, src/model.c:1090-1093), n_ff_exp % 64 == 0, n_expert <= 256
- * (any count), n_used <= min(n_expert, 64); QMSG_E_UNSUPPORTED otherwise. */
+ * with device scratch for up to `max_tokens` tokens per call. Shapes: n_embd % 32 == 0 and
+ * n_ff_exp % 32 == 0 (rows of whole 32-blocks, which the reference's qms_matmul needs for its
+ * int8 path, src/quant.c:134-136), n_expert <= 256 (any count), n_used <= min(n_expert, 64);
+ * QMSG_E_UNSUPPORTED otherwise. Layers with n_embd % 256 != 0 (past the reference's fast gate,
+ * src/model.c:1090-1093, where it runs moe_group_exact) or n_ff_exp % 64 != 0 run slot by slot
+ * with the same int8 arithmetic. */
 int qmsg_create(qmsg_ctx **out, int device, const qmsg_cfg *cfg, int n_layer, int max_tokens);
 void qmsg_destroy(qmsg_ctx *ctx);
 

@@ -213,10 +213,12 @@ int qmsg_create(qmsg_ctx **out, int device, const qmsg_cfg *cfg, int n_layer, in
     if (E <= 0 || X <= 0 || K <= 0 || F <= 0 || K > X || n_layer <= 0 || max_tokens <= 0)
         return fail(nullptr, QMSG_E_INVALID, "qmsg_create: bad shape E=%d X=%d K=%d F=%d layers=%d T=%d", E, X, K, F,
                     n_layer, max_tokens);
-    /* The reference's integer fast path needs E % 256 == 0 and F % 32 == 0
-     * (src/model.c:1090-1093). The kernels also pair 32-blocks (F % 64 == 0) and keep
-     * per-expert state in 256-entry LDS arrays (X <= 256). */
-    if (E % 256 || F % 64 || X > kMaxExperts || K > 64)
+    /* Rows of whole 32-blocks (E % 32 == 0, F % 32 == 0): what the reference's qms_matmul needs
+     * for its int8 path (src/quant.c:134-136) on every row the layer has. Shapes off the integer
+     * kernels' grid (integer_grid_shape: E % 256, F % 64) run slot by slot, as the reference's
+     * moe_group_exact does past its fast gate (src/model.c:1090-1093). The routing keeps
+     * per-expert state in 256-entry LDS arrays (X <= 256, K <= 64). */
+    if (E % 32 || F % 32 || X > kMaxExperts || K > 64)
         return fail(nullptr, QMSG_E_UNSUPPORTED, "qmsg_create: unsupported shape E=%d X=%d K=%d F=%d", E, X, K, F);
     int ndev = 0;
     if (hipGetDeviceCount(&ndev) != hipSuccess || device < 0 || device >= ndev)
@@ -316,6 +318,8 @@ static int layer_alloc(qmsg_ctx *c, LayerStore &L, int gt, int ut, int dt)
                     ut, dt);
     if (dt == QMSG_T_Q6_K && F % 256)
         return fail(c, QMSG_E_UNSUPPORTED, "Q6_K down needs n_ff_exp %% 256 == 0 (got %lld)", (long long)F);
+    if ((gt == QMSG_T_Q6_K || ut == QMSG_T_Q6_K) && E % 256)
+        return fail(c, QMSG_E_UNSUPPORTED, "Q6_K gate/up needs n_embd %% 256 == 0 (got %lld)", (long long)E);
     hipFree(L.router); hipFree(L.gate); hipFree(L.up); hipFree(L.down);
     float *norm = L.norm;                     /* the ffn_norm weights stay with the layer */
     L = LayerStore{};
@@ -804,10 +808,12 @@ static int run_layer_s(qmsg_ctx *c, const Scratch &S0, int layer, const float *d
         return fail(c, QMSG_E_INVALID, "device buffers must be 16-byte aligned (xn) and 4-byte aligned (out)");
     const Shape s{ c->cfg.n_embd, c->cfg.n_expert, c->cfg.n_used, c->cfg.n_ff_exp };
     const LayerDev d = layer_dev(c, L);
-    if (ni && (T != 1 || c->path == QMSG_PATH_FP32 || !route_norm_fits(s.E) || ni->xn_out != d_xn))
+    if (ni && (T != 1 || c->path == QMSG_PATH_FP32 || !route_norm_fits(s.E) || !integer_grid_shape(s.E, s.F) ||
+               ni->xn_out != d_xn))
         return fail(c, QMSG_E_INVALID, "run_layer_s: the fused rmsnorm takes one token on the integer paths");
-    if (c->path == QMSG_PATH_FP32) {
-        LAUNCH(c, "layer", launch_layer_fp32(s, d, S, d_xn, d_out, T, c->stream));
+    if (c->path == QMSG_PATH_FP32 || !integer_grid_shape(s.E, s.F)) {
+        LAUNCH(c, "layer", launch_layer_slots(s, d, S, d_xn, d_out, T, c->path == QMSG_PATH_FP32 ? 1 : 0, debug,
+                                              c->stream));
         return QMSG_OK;
     }
     /* gate and up of one type take the streaming gate/up kernel (which also routes one-token
@@ -909,7 +915,7 @@ int qmsg_moe_chain(qmsg_ctx *c, int first, int n, float *d_h, int T, float eps)
     const int E = c->cfg.n_embd;
     for (int l = first; l < first + n; l++)
         if (!c->layers[(size_t)l].ready) return fail(c, QMSG_E_INVALID, "layer %d has no weights", l);
-    if (T == 1 && c->path != QMSG_PATH_FP32 && route_norm_fits(E)) {
+    if (T == 1 && c->path != QMSG_PATH_FP32 && route_norm_fits(E) && integer_grid_shape(E, c->cfg.n_ff_exp)) {
         /* One token: each layer's router launch forms the rmsnorm itself, every block from h
          * and the previous layer's output, so h + out goes to the other of two rows (d_h and
          * d_hb, in turn) while the blocks still read the first. */

@@ -168,9 +168,15 @@ bool down_exact_fits(const Shape &s, const LayerDev &L, int T);
  * MFMA gate/up stored them). */
 hipError_t launch_down_exact(const Shape &s, const LayerDev &L, const Scratch &S, float *out, int T, int quant,
                              hipStream_t st);
-/* The whole layer in the reference's --exact mode (fp32 dequantised rows, fp32 activations). */
-hipError_t launch_layer_fp32(const Shape &s, const LayerDev &L, const Scratch &S, const float *xn, float *out, int T,
-                             hipStream_t st);
+/* The whole layer slot by slot, as the reference's moe_group_exact (src/model.c:1009-1030): with
+ * exact its --exact mode (fp32 dequantised rows, fp32 activations), else each qms_matmul on its
+ * int8 path, for shapes off the integer kernels' grid (integer_grid_shape). debug also stores
+ * the int8 blocks of the inputs and activations (xq, aq) that the slot kernels keep in LDS. */
+hipError_t launch_layer_slots(const Shape &s, const LayerDev &L, const Scratch &S, const float *xn, float *out, int T,
+                              int exact, int debug, hipStream_t st);
+/* The shapes the integer kernels take: n_embd % 256 == 0 (the reference's fast gate,
+ * src/model.c:1090-1093) and n_ff_exp % 64 == 0 (they pair 32-blocks). */
+inline bool integer_grid_shape(int E, int F) { return E % 256 == 0 && F % 64 == 0; }
 hipError_t launch_synth_f32(uint64_t key, uint64_t n, float sigma, float *out, hipStream_t st);
 hipError_t launch_synth_experts(uint64_t seed, uint32_t layer, uint32_t kind, int type, int64_t rows,
                                 int64_t cols, int X, float sigma, uint8_t *base, hipStream_t st);

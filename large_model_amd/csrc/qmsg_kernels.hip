@@ -4066,6 +4066,108 @@ __device__ __forceinline__ uint32_t ld_u32_a2(const uint8_t *p)   /* p a multipl
     return (uint32_t)h[0] | ((uint32_t)h[1] << 16);
 }
 
+/* One pass of a lane group's row (bytes wr, C columns) against nt <= NT input rows, xrow(n)
+ * giving row n's C floats (16-byte aligned); res[n] holds the product on lane k == 0 of the
+ * group. Every thread of the block calls it (the quantised records are formed block-wide). */
+template <int TYPE, int NT, typename XRow>
+__device__ __forceinline__ void any_rows_pass(const uint8_t *wr, int C, int nt, int k, XRow xrow, uint8_t *smem,
+                                              float *res)
+{
+    const int tid = threadIdx.x, nb = C >> 5;
+    float acc[NT], corr[NT];
+#pragma unroll
+    for (int n = 0; n < NT; n++) { acc[n] = 0.0f; corr[n] = 0.0f; }
+    if constexpr (TYPE == 0) {
+        const float *w = (const float *)wr;
+        for (int i = k; i < C; i += 16) {
+            const float wv = w[i];
+#pragma unroll
+            for (int n = 0; n < NT; n++)
+                if (n < nt) acc[n] = __builtin_fmaf(wv, xrow(n)[i], acc[n]);
+        }
+    } else {
+        __syncthreads();                              /* an earlier pass is done with the records */
+        for (int i = tid; i < nt * nb; i += blockDim.x) {
+            const int n = i / nb, blk = i - n * nb;
+            float v[32];
+            const float4 *src = (const float4 *)(xrow(n) + (size_t)blk * 32);
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+                const float4 f = src[j];
+                v[4 * j] = f.x; v[4 * j + 1] = f.y; v[4 * j + 2] = f.z; v[4 * j + 3] = f.w;
+            }
+            const Q8Vals q = quantize_block(v);
+            uint32_t *o = (uint32_t *)(smem + (size_t)i * kDenseAnyRec);
+#pragma unroll
+            for (int j = 0; j < 8; j++) o[j] = q.qw[j];
+            o[8] = __float_as_uint(q.d);
+            o[9] = __float_as_uint(q.ds);
+            o[10] = q.s16;
+            o[11] = 0;
+        }
+        __syncthreads();
+        auto rec = [&](int n, int blk) { return smem + ((size_t)n * nb + blk) * kDenseAnyRec; };
+        if constexpr (TYPE == 14) {
+            const int hi = k >> 2;
+            for (int s = 0; s < nb / 8; s++) {
+                const uint8_t *sp = wr + (size_t)s * 210;
+                const float d = h2f(*(const uint16_t *)(sp + 208));
+#pragma unroll
+                for (int h = 0; h < 2; h++) {
+                    const uint32_t ql0 = ld_u32_a2(sp + 64 * h + 4 * k), ql1 = ld_u32_a2(sp + 64 * h + 32 + 4 * k);
+                    const uint32_t qh = ld_u32_a2(sp + 128 + 32 * h + 4 * k);
+                    const uint32_t sc0 = ld_u32_a2(sp + 192 + 8 * h), sc1 = ld_u32_a2(sp + 196 + 8 * h);
+#pragma unroll
+                    for (int g = 0; g < 4; g++) {
+                        const uint32_t ql = (g & 1) ? ql1 : ql0;
+                        const uint32_t nib = g < 2 ? (ql & 0x0f0f0f0fu) : ((ql >> 4) & 0x0f0f0f0fu);
+                        const uint32_t q6 = nib | (((qh >> (2 * g)) & 0x03030303u) << 4);
+                        const uint32_t scw = (g < 2 ? sc0 : sc1) >> (16 * (g & 1));
+                        const int sa = (int)(int8_t)(scw & 0xff), sbv = (int)(int8_t)((scw >> 8) & 0xff);
+#pragma unroll
+                        for (int n = 0; n < NT; n++) {
+                            if (n >= nt) break;
+                            const uint32_t *xr = (const uint32_t *)rec(n, 8 * s + 4 * h + g);
+                            const float dd = d * __uint_as_float(xr[8]);
+                            const int s16a = (int)(int16_t)(xr[10] & 0xffffu), s16b = (int)(int16_t)(xr[10] >> 16);
+                            acc[n] = __builtin_fmaf((float)(sdot4((int)q6, (int)xr[k]) * (hi ? sbv : sa)), dd, acc[n]);
+                            corr[n] = __builtin_fmaf(dd, (float)(sa * s16a + sbv * s16b), corr[n]);
+                        }
+                    }
+                }
+            }
+        } else {
+            constexpr int BB = TYPE == 3 ? 20 : 18;
+            for (int b = 0; b < nb; b++) {
+                const uint8_t *bp = wr + (size_t)b * BB;
+                float d, o;
+                uint32_t c;
+                if (TYPE == 3) {
+                    const uint32_t dm = *(const uint32_t *)bp;      /* 20-byte blocks: 4-byte aligned */
+                    d = h2f(dm & 0xffffu);
+                    o = h2f(dm >> 16);
+                    c = *(const uint32_t *)(bp + 4 + 4 * (k & 3));
+                } else {
+                    d = h2f(*(const uint16_t *)bp);
+                    o = d;
+                    c = ld_u32_a2(bp + 2 + 4 * (k & 3));
+                }
+                const uint32_t nib = (k < 4 ? c : c >> 4) & 0x0f0f0f0fu;
+#pragma unroll
+                for (int n = 0; n < NT; n++) {
+                    if (n >= nt) break;
+                    const uint32_t *xr = (const uint32_t *)rec(n, b);
+                    acc[n] = __builtin_fmaf((float)sdot4((int)nib, (int)xr[k]), d * __uint_as_float(xr[8]), acc[n]);
+                    corr[n] = __builtin_fmaf(o, __uint_as_float(xr[9]), corr[n]);
+                }
+            }
+        }
+    }
+#pragma unroll
+    for (int n = 0; n < NT; n++)
+        res[n] = TYPE == 0 ? chain16_sum(acc[n]) : oct_finish(acc[n], corr[n], finish_scale(TYPE));
+}
+
 template <int TYPE, int NT>
 __global__ __launch_bounds__(256) void dense_any_kernel(DenseArgs a)
 {
@@ -4080,104 +4182,82 @@ __global__ __launch_bounds__(256) void dense_any_kernel(DenseArgs a)
     const DenseMat M = a.m[mi];
     const int row = ((int)blockIdx.x - M.first_block) * 4 * RPW + wave * RPW + lane / LPR;
     const uint8_t *wr = M.w + (size_t)min(row, M.rows - 1) * a.rb;
-    const int C = a.C, nb = C >> 5;
+    const int C = a.C;
     for (int t0 = 0; t0 < a.T; t0 += NT) {
         const int nt = min(NT, a.T - t0);
-        float acc[NT], corr[NT];
+        float res[NT];
+        any_rows_pass<TYPE, NT>(wr, C, nt, k, [&](int n) { return a.x + (size_t)(t0 + n) * C; }, smem, res);
 #pragma unroll
-        for (int n = 0; n < NT; n++) { acc[n] = 0.0f; corr[n] = 0.0f; }
-        if constexpr (TYPE == 0) {
-            const float *w = (const float *)wr, *x = a.x + (size_t)t0 * C;
-            for (int i = k; i < C; i += 16) {
-                const float wv = w[i];
-#pragma unroll
-                for (int n = 0; n < NT; n++)
-                    if (n < nt) acc[n] = __builtin_fmaf(wv, x[(size_t)n * C + i], acc[n]);
-            }
-        } else {
-            if (t0 > 0) __syncthreads();              /* the previous pass is done with the records */
-            for (int i = tid; i < nt * nb; i += 256) {
-                const int n = i / nb, blk = i - n * nb;
-                float v[32];
-                const float4 *src = (const float4 *)(a.x + (size_t)(t0 + n) * C + (size_t)blk * 32);
-#pragma unroll
-                for (int j = 0; j < 8; j++) {
-                    const float4 f = src[j];
-                    v[4 * j] = f.x; v[4 * j + 1] = f.y; v[4 * j + 2] = f.z; v[4 * j + 3] = f.w;
-                }
-                const Q8Vals q = quantize_block(v);
-                uint32_t *o = (uint32_t *)(smem + (size_t)i * kDenseAnyRec);
-#pragma unroll
-                for (int j = 0; j < 8; j++) o[j] = q.qw[j];
-                o[8] = __float_as_uint(q.d);
-                o[9] = __float_as_uint(q.ds);
-                o[10] = q.s16;
-                o[11] = 0;
-            }
-            __syncthreads();
-            auto rec = [&](int n, int blk) { return smem + ((size_t)n * nb + blk) * kDenseAnyRec; };
-            if constexpr (TYPE == 14) {
-                const int hi = k >> 2;
-                for (int s = 0; s < nb / 8; s++) {
-                    const uint8_t *sp = wr + (size_t)s * 210;
-                    const float d = h2f(*(const uint16_t *)(sp + 208));
-#pragma unroll
-                    for (int h = 0; h < 2; h++) {
-                        const uint32_t ql0 = ld_u32_a2(sp + 64 * h + 4 * k), ql1 = ld_u32_a2(sp + 64 * h + 32 + 4 * k);
-                        const uint32_t qh = ld_u32_a2(sp + 128 + 32 * h + 4 * k);
-                        const uint32_t sc0 = ld_u32_a2(sp + 192 + 8 * h), sc1 = ld_u32_a2(sp + 196 + 8 * h);
-#pragma unroll
-                        for (int g = 0; g < 4; g++) {
-                            const uint32_t ql = (g & 1) ? ql1 : ql0;
-                            const uint32_t nib = g < 2 ? (ql & 0x0f0f0f0fu) : ((ql >> 4) & 0x0f0f0f0fu);
-                            const uint32_t q6 = nib | (((qh >> (2 * g)) & 0x03030303u) << 4);
-                            const uint32_t scw = (g < 2 ? sc0 : sc1) >> (16 * (g & 1));
-                            const int sa = (int)(int8_t)(scw & 0xff), sbv = (int)(int8_t)((scw >> 8) & 0xff);
-#pragma unroll
-                            for (int n = 0; n < NT; n++) {
-                                if (n >= nt) break;
-                                const uint32_t *xr = (const uint32_t *)rec(n, 8 * s + 4 * h + g);
-                                const float dd = d * __uint_as_float(xr[8]);
-                                const int s16a = (int)(int16_t)(xr[10] & 0xffffu), s16b = (int)(int16_t)(xr[10] >> 16);
-                                acc[n] = __builtin_fmaf((float)(sdot4((int)q6, (int)xr[k]) * (hi ? sbv : sa)), dd, acc[n]);
-                                corr[n] = __builtin_fmaf(dd, (float)(sa * s16a + sbv * s16b), corr[n]);
-                            }
-                        }
-                    }
-                }
-            } else {
-                constexpr int BB = TYPE == 3 ? 20 : 18;
-                for (int b = 0; b < nb; b++) {
-                    const uint8_t *bp = wr + (size_t)b * BB;
-                    float d, o;
-                    uint32_t c;
-                    if (TYPE == 3) {
-                        const uint32_t dm = *(const uint32_t *)bp;      /* 20-byte blocks: 4-byte aligned */
-                        d = h2f(dm & 0xffffu);
-                        o = h2f(dm >> 16);
-                        c = *(const uint32_t *)(bp + 4 + 4 * (k & 3));
-                    } else {
-                        d = h2f(*(const uint16_t *)bp);
-                        o = d;
-                        c = ld_u32_a2(bp + 2 + 4 * (k & 3));
-                    }
-                    const uint32_t nib = (k < 4 ? c : c >> 4) & 0x0f0f0f0fu;
-#pragma unroll
-                    for (int n = 0; n < NT; n++) {
-                        if (n >= nt) break;
-                        const uint32_t *xr = (const uint32_t *)rec(n, b);
-                        acc[n] = __builtin_fmaf((float)sdot4((int)nib, (int)xr[k]), d * __uint_as_float(xr[8]), acc[n]);
-                        corr[n] = __builtin_fmaf(o, __uint_as_float(xr[9]), corr[n]);
-                    }
-                }
-            }
-        }
-#pragma unroll
-        for (int n = 0; n < NT; n++) {
-            const float v = TYPE == 0 ? chain16_sum(acc[n]) : oct_finish(acc[n], corr[n], finish_scale(TYPE));
-            if (k == 0 && n < nt && row < M.rows) M.y[(size_t)(t0 + n) * M.rows + row] = v;
-        }
+        for (int n = 0; n < NT; n++)
+            if (k == 0 && n < nt && row < M.rows) M.y[(size_t)(t0 + n) * M.rows + row] = res[n];
     }
+}
+
+/* The same products per slot for the MoE layer at shapes off the integer kernels' grid
+ * (n_embd % 256 != 0 or n_ff_exp % 64 != 0): the reference then runs moe_group_exact, whose
+ * qms_matmul of each slot's gate, up and down rows takes this int8 path (src/model.c:1009-1030,
+ * src/quant.c:134-136; with n_embd % 256 == 0 its moe_group_fast gives the same numbers,
+ * src/model.c:969-1006). Block (row group, active expert blockIdx.y) as exact_rows_kernel;
+ * the input of slot s is row slot_t[s] of x (by_token) or row s. */
+struct SlotAnyArgs {
+    const uint8_t *w;
+    uint64_t rb, eb;
+    int rows, cols, by_token;
+    const float *x;
+    float *y;
+    int y_stride, y_off;
+    Scratch S;
+};
+
+template <int TYPE, int NT>
+__global__ __launch_bounds__(256) void slot_any_kernel(SlotAnyArgs a)
+{
+    extern __shared__ __align__(16) uint8_t smem[];
+    if ((int)blockIdx.y >= a.S.meta[0]) return;       /* block-uniform */
+    const int4 wk = a.S.work[blockIdx.y];
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, k = lane & 7;
+    const int row = (int)blockIdx.x * 32 + wave * 8 + (lane >> 3), C = a.cols;
+    const uint8_t *wr = a.w + (size_t)wk.x * a.eb + (size_t)min(row, a.rows - 1) * a.rb;
+    for (int s0 = wk.y; s0 < wk.z; s0 += NT) {
+        const int nt = min(NT, wk.z - s0);
+        float res[NT];
+        any_rows_pass<TYPE, NT>(wr, C, nt, k, [&](int n) {
+            const size_t src = a.by_token ? (size_t)a.S.slot_t[s0 + n] : (size_t)(s0 + n);
+            return a.x + src * C;
+        }, smem, res);
+#pragma unroll
+        for (int n = 0; n < NT; n++)
+            if (k == 0 && n < nt && row < a.rows) a.y[(size_t)(s0 + n) * a.y_stride + a.y_off + row] = res[n];
+    }
+}
+
+/* The weighted sum of combine_kernel for any n_embd: one thread per output element. */
+__global__ void combine_any_kernel(const Scratch S, int E, int K, int T, float *out)
+{
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (size_t)T * E) return;
+    const int t = (int)(i / E), r = (int)(i - (size_t)t * E);
+    float o = 0.0f;
+    for (int j = 0; j < K; j++)
+        o = __builtin_fmaf(S.wt[(size_t)t * K + j], S.dn[(size_t)S.slot_of[(size_t)t * K + j] * E + r], o);
+    out[i] = o;
+}
+
+/* The 44-byte Q8 records of rows of C floats (qms_quantize_q8): the debug copies of the
+ * inputs' and activations' int8 blocks where the slot kernels keep theirs in LDS only. */
+__global__ void quant_rows_kernel(const float *x, int C, int rows, Q8 *dst)
+{
+    const int nb = C >> 5;
+    const int b = blockIdx.x * blockDim.x + threadIdx.x;
+    if (b >= rows * nb) return;
+    float v[32];
+    const float4 *src = (const float4 *)(x + (size_t)b * 32);
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+        const float4 f = src[j];
+        v[4 * j] = f.x; v[4 * j + 1] = f.y; v[4 * j + 2] = f.z; v[4 * j + 3] = f.w;
+    }
+    store_q8(quantize_block(v), dst + b);
 }
 
 /* Tokens per pass of dense_any_kernel for a batch of T and nb 32-blocks per row: the fewest
@@ -4481,21 +4561,40 @@ __global__ __launch_bounds__(64) void exact_rows_kernel(ExactArgs a)
     }
 }
 
-hipError_t launch_layer_fp32(const Shape &s, const LayerDev &L, const Scratch &S, const float *xn, float *out, int T,
-                             hipStream_t st)
+hipError_t launch_layer_slots(const Shape &s, const LayerDev &L, const Scratch &S, const float *xn, float *out, int T,
+                              int exact, int debug, hipStream_t st)
 {
     SelectArgs sa;
     sa.X = s.X;
     sa.K = s.K;
     sa.T = T;
     sa.S = S;
-    QLAUNCH("route", route_exact_kernel, dim3((s.X + 63) / 64, T), dim3(64), (size_t)s.E * 4, st, L.router, xn, s.E,
-            s.X, S.logits);
+    if (exact) {
+        QLAUNCH("route", route_exact_kernel, dim3((s.X + 63) / 64, T), dim3(64), (size_t)s.E * 4, st, L.router, xn,
+                s.E, s.X, S.logits);
+    } else {
+        /* qms_matmul of the F32 router (src/model.c:1043): dot_f32's sixteen chains */
+        DenseArgs r{};
+        r.m[0].w = (const uint8_t *)L.router;
+        r.m[0].y = S.logits;
+        r.m[0].rows = s.X;
+        r.m[0].first_block = 0;
+        r.nm = 1;
+        r.rb = (uint64_t)s.E * 4;
+        r.C = s.E;
+        r.T = T;
+        r.x = xn;
+        r.xqk = nullptr;
+        const int NT = dense_any_nt(0, T, s.E / 32);
+        const dim3 grid((s.X + 15) / 16);
+        if (NT == 8) QLAUNCH("route", (dense_any_kernel<0, 8>), grid, dim3(256), 0, st, r);
+        else if (NT == 4) QLAUNCH("route", (dense_any_kernel<0, 4>), grid, dim3(256), 0, st, r);
+        else if (NT == 2) QLAUNCH("route", (dense_any_kernel<0, 2>), grid, dim3(256), 0, st, r);
+        else QLAUNCH("route", (dense_any_kernel<0, 1>), grid, dim3(256), 0, st, r);
+    }
     QLAUNCH("select", select_kernel, dim3(T), dim3(256), 0, st, sa, 0);
     QLAUNCH("dispatch", dispatch_kernel, dim3(1), dim3(64), 0, st, sa);
     const int maxact = s.X < T * s.K ? s.X : T * s.K;
-    ExactArgs a;
-    a.S = S;
     const struct { const uint8_t *w; uint64_t rb, eb; int type, rows, cols, by_token; const float *x; float *y;
                    int stride, off; } m[3] = {
         { L.gate, L.gate_rb, L.gate_eb, L.gate_type, s.F, s.E, 1, xn, S.gu, 2 * s.F, 0 },
@@ -4503,10 +4602,35 @@ hipError_t launch_layer_fp32(const Shape &s, const LayerDev &L, const Scratch &S
         { L.down, L.down_rb, L.down_eb, L.down_type, s.E, s.F, 0, S.act, S.dn, s.E, 0 },
     };
     for (int i = 0; i < 3; i++) {
+        if (i == 2) {
+            const int n = T * s.K * s.F;
+            QLAUNCH("swiglu", swiglu_kernel, dim3((n + 255) / 256), dim3(256), 0, st, S, s.F, T * s.K);
+        }
+        const char *name = i == 2 ? "down" : "gateup";
+        if (exact) {
+            ExactArgs a;
+            a.S = S;
+            a.w = m[i].w;
+            a.rb = m[i].rb;
+            a.eb = m[i].eb;
+            a.type = m[i].type;
+            a.rows = m[i].rows;
+            a.cols = m[i].cols;
+            a.by_token = m[i].by_token;
+            a.x = m[i].x;
+            a.y = m[i].y;
+            a.y_stride = m[i].stride;
+            a.y_off = m[i].off;
+            const size_t lds = (size_t)4 * m[i].cols * 4;
+            if (lds > 160 * 1024) return hipErrorInvalidValue;
+            QLAUNCH(name, exact_rows_kernel, dim3((m[i].rows + 63) / 64, maxact), dim3(64), lds, st, a);
+            continue;
+        }
+        SlotAnyArgs a;
+        a.S = S;
         a.w = m[i].w;
         a.rb = m[i].rb;
         a.eb = m[i].eb;
-        a.type = m[i].type;
         a.rows = m[i].rows;
         a.cols = m[i].cols;
         a.by_token = m[i].by_token;
@@ -4514,16 +4638,32 @@ hipError_t launch_layer_fp32(const Shape &s, const LayerDev &L, const Scratch &S
         a.y = m[i].y;
         a.y_stride = m[i].stride;
         a.y_off = m[i].off;
-        const size_t lds = (size_t)4 * m[i].cols * 4;
-        if (lds > 160 * 1024) return hipErrorInvalidValue;
-        if (i == 2) {
-            const int n = T * s.K * s.F;
-            QLAUNCH("swiglu", swiglu_kernel, dim3((n + 255) / 256), dim3(256), 0, st, S, s.F, T * s.K);
-        }
-        QLAUNCH(i == 2 ? "down" : "gateup", exact_rows_kernel, dim3((m[i].rows + 63) / 64, maxact), dim3(64), lds, st, a);
+        const int nb = m[i].cols / 32, NT = dense_any_nt(m[i].type, T, nb);
+        if (!NT) return hipErrorInvalidValue;
+        const size_t lds = (size_t)NT * nb * kDenseAnyRec;
+        const dim3 grid((m[i].rows + 31) / 32, maxact);
+        auto go = [&](auto ty) {
+            constexpr int TY = decltype(ty)::value;
+            if (NT == 8) QLAUNCH(name, (slot_any_kernel<TY, 8>), grid, dim3(256), lds, st, a);
+            else if (NT == 4) QLAUNCH(name, (slot_any_kernel<TY, 4>), grid, dim3(256), lds, st, a);
+            else if (NT == 2) QLAUNCH(name, (slot_any_kernel<TY, 2>), grid, dim3(256), lds, st, a);
+            else QLAUNCH(name, (slot_any_kernel<TY, 1>), grid, dim3(256), lds, st, a);
+        };
+        if (m[i].type == 14) go(std::integral_constant<int, 14>());
+        else if (m[i].type == 3) go(std::integral_constant<int, 3>());
+        else go(std::integral_constant<int, 2>());
+    }
+    if (debug && !exact) {
+        /* the int8 blocks the slot kernels formed in LDS, for the debug copies */
+        const int nx = T * (s.E / 32), na = T * s.K * (s.F / 32);
+        QLAUNCH("debug", quant_rows_kernel, dim3((nx + 255) / 256), dim3(256), 0, st, xn, s.E, T, S.xq);
+        QLAUNCH("debug", quant_rows_kernel, dim3((na + 255) / 256), dim3(256), 0, st, S.act, s.F, T * s.K, S.aq);
     }
     const int n = T * s.E;
-    QLAUNCH("combine", combine_kernel, dim3(n / (4 * combine_threads(s.E))), dim3(combine_threads(s.E)), 0, st, S, s.E, s.K, T, out);
+    if (s.E % 256 == 0)
+        QLAUNCH("combine", combine_kernel, dim3(n / (4 * combine_threads(s.E))), dim3(combine_threads(s.E)), 0, st, S,
+                s.E, s.K, T, out);
+    else QLAUNCH("combine", combine_any_kernel, dim3((n + 255) / 256), dim3(256), 0, st, S, s.E, s.K, T, out);
     return hipGetLastError();
 }
 

@@ -389,7 +389,11 @@ int orc_matmul_exact(int type, const uint8_t *w, int64_t rows, int64_t cols, uin
 /* src/model.c:1032-1167 for resident experts (one group): with exact = 0 the integer path,
  * moe_group_fast (969-1007); with exact = 1 the reference's --exact mode (qms_exact_math),
  * where the router and moe_group_exact (1010-1030) use matmul_exact and the activations stay
- * fp32. */
+ * fp32. Past moe()'s fast gate (n_embd % 256 != 0 or n_ff_exp % 32 != 0; 1090-1093) without
+ * --exact, the reference runs moe_group_exact, whose per-slot qms_matmul calls take the int8
+ * path of src/quant.c:134-169 for quantised rows of whole blocks: the input row quantised, the
+ * gate and up dots, silu(g)*u, the activation row quantised, the down dots. Those are the
+ * integer branch's steps, so it serves that case too (rows of whole 32-blocks, any n_embd). */
 static int moe_common(int exact, int E, int X, int K, int F, const orc_mat *router, const orc_mat *gate,
                       const orc_mat *up, const orc_mat *down, const float *xn, int T, float *out, orc_moe_dbg *dbg)
 {
@@ -398,10 +402,11 @@ static int moe_common(int exact, int E, int X, int K, int F, const orc_mat *rout
     if (exact) {
         if (!orc_row_bytes(gate->type, E) || !orc_row_bytes(up->type, E) || !orc_row_bytes(down->type, F)) return -1;
     } else {
-        /* model.c:1090-1093: the integer path needs these */
+        /* model.c:1090-1093 (or, for n_embd % 256 != 0, the int8 qms_matmul of every slot) */
         const int fast = orc_fast_supported(gate->type) && orc_fast_supported(up->type) &&
                          orc_fast_supported(down->type) && gate->type != ORC_T_F32 &&
-                         up->type != ORC_T_F32 && down->type != ORC_T_F32 && E % 256 == 0 && F % 32 == 0;
+                         up->type != ORC_T_F32 && down->type != ORC_T_F32 && E % 32 == 0 && F % 32 == 0 &&
+                         orc_row_bytes(gate->type, E) && orc_row_bytes(up->type, E) && orc_row_bytes(down->type, F);
         if (!fast) return -1;
     }
     if (T == 0) return 0;

@@ -46,18 +46,20 @@ def test_create_rejects_bad_shapes(q, shape):
     assert st == -1 and not h.value and "bad shape" in msg
 
 
-@pytest.mark.parametrize("shape", [(300, 16, 4, 128), (256, 16, 4, 96), (256, 512, 8, 128)])
-def test_create_reports_shapes_outside_the_fast_path(q, shape):
-    """E % 256 and F % 32 are the reference's own fast-path conditions (src/model.c:1090-1093);
-    F % 64 and at most 256 experts are this library's."""
+@pytest.mark.parametrize("shape", [(300, 16, 4, 128), (256, 16, 4, 80), (256, 512, 8, 128), (256, 80, 72, 128)])
+def test_create_reports_unsupported_shapes(q, shape):
+    """Rows that are not whole 32-blocks (n_embd 300, n_ff_exp 80: no qms_matmul int8 path,
+    src/quant.c:134-136), more than 256 experts or more than 64 of them per token."""
     st, h, msg = create(q, *shape)
     assert st == -2 and not h.value and "unsupported" in msg
 
 
-@pytest.mark.parametrize("shape", [(256, 8, 2, 128), (256, 20, 4, 128), (1024, 60, 4, 256)])
+@pytest.mark.parametrize("shape", [(256, 8, 2, 128), (256, 20, 4, 128), (1024, 60, 4, 256), (96, 8, 2, 96),
+                                   (256, 16, 4, 96), (2080, 64, 8, 352)])
 def test_create_takes_any_expert_count(q, shape):
-    """Expert counts that are not a multiple of 16 (Mixtral's 8, 60) pass the shape gate; here,
-    without a device, creation then fails on the device, not on the shape."""
+    """Expert counts that are not a multiple of 16 (Mixtral's 8, 60) and rows of whole 32-blocks
+    off the integer kernels' grid (n_embd % 256 != 0, n_ff_exp = 32 x odd) pass the shape gate;
+    here, without a device, creation then fails on the device, not on the shape."""
     st, h, msg = create(q, *shape)
     assert st != -2 and "unsupported" not in msg
     if st == 0:

@@ -334,6 +334,45 @@ def test_routing_edge_cases(name):
     assert rc.same_bits_or_both_nan(orc.ref_moe(R, L, x), out)
 
 
+# ------------------------------------------------------------------ shapes off the integer kernels' grid
+
+OFF_GRID = [   # E, X, K, F, T, gate, up, down types
+    (96, 8, 2, 96, 3, orc.T_Q4_0, orc.T_Q4_0, orc.T_Q4_0),
+    (288, 12, 3, 160, 5, orc.T_Q4_1, orc.T_Q4_0, orc.T_Q4_1),
+    (256, 16, 4, 96, 4, orc.T_Q6_K, orc.T_Q6_K, orc.T_Q4_0),
+    (512, 8, 2, 32, 2, orc.T_Q4_0, orc.T_Q4_1, orc.T_Q4_0),
+    (800, 10, 4, 256, 1, orc.T_Q4_0, orc.T_Q4_0, orc.T_Q6_K),
+]
+
+
+@pytest.mark.parametrize("E,X,K,F,T,gt,ut,dt", OFF_GRID, ids=[f"e{c[0]}_f{c[3]}" for c in OFF_GRID])
+def test_off_grid_shapes(E, X, K, F, T, gt, ut, dt):
+    """n_embd % 256 != 0 (the reference's moe() then runs moe_group_exact, whose qms_matmul of
+    each slot takes the int8 path, src/model.c:1009-1030) and n_ff_exp = 32 x odd (its fast
+    path): every slot's gate/up and down rows of the oracle's layer equal the oracle's
+    qms_matmul restatement (pinned by the reference's dense fixtures) on that slot's input and
+    activation row, and the layer equals the reference build's moe() bit for bit, with and
+    without --exact."""
+    seed = 90 + E % 97
+    L = orc.Layer(E, X, K, F, seed, gate_type=gt, up_type=ut, down_type=dt, experts=[])
+    x = orc.make_input(E, T, seed, rmsnorm=True)
+    out, d = L.moe(x, debug=True)
+    rb, eb = L.rb, L.eb
+    for e in range(X):
+        for s in range(int(d["start"][e]), int(d["start"][e + 1])):
+            xt = x[d["slot_t"][s]][None]
+            g = orc.matmul_q8(gt, L.gate[e * eb[0]:(e + 1) * eb[0]], F, E, xt)
+            u = orc.matmul_q8(ut, L.up[e * eb[1]:(e + 1) * eb[1]], F, E, xt)
+            assert np.array_equal(d["gu"][s].view(np.uint32), np.concatenate([g[0], u[0]]).view(np.uint32))
+            dn = orc.matmul_q8(dt, L.down[e * eb[2]:(e + 1) * eb[2]], E, F, d["act"][s][None])
+            assert np.array_equal(d["dn"][s].view(np.uint32), dn[0].view(np.uint32))
+    R = orc.load_ref()
+    if R is None:
+        pytest.skip("reference build (oracle/_ref) not present")
+    assert np.array_equal(orc.ref_moe(R, L, x).view(np.uint32), out.view(np.uint32))
+    assert np.array_equal(orc.ref_moe(R, L, x, exact=True).view(np.uint32), L.moe(x, exact=True).view(np.uint32))
+
+
 # ------------------------------------------------------------------ planted mistakes
 
 MUTATIONS = ["HSUM_LINEAR", "CORR_UNFUSED", "NIBBLE_ORDER", "ROUTER_TREE", "ROUND_AWAY", "TIE_HIGH",
