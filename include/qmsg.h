@@ -118,12 +118,16 @@ int qmsg_set_path(qmsg_ctx *ctx, int path);
 
 /* Replaces load_experts/load_mat's resident read (src/model.c:133-157, 67-85): copy one
  * layer's router and expert tensors (host memory, GGUF bytes) into HBM unchanged. Shapes
- * and row_bytes are checked against cfg and qms_row_bytes (src/gguf.c:85-96). */
+ * and row_bytes are checked against cfg and qms_row_bytes (src/gguf.c:85-96). Expert types:
+ * Q4_0, Q4_1, Q6_K (the integer kernels), and Q8_0, F16, F32, whose layers run slot by slot
+ * as the reference's moe_group_exact does (src/model.c:1009-1030); F32 up rows with
+ * quantised gate and down at n_embd % 256 == 0 are QMSG_E_UNSUPPORTED (the reference's fast
+ * path has no F32 dot for them, src/kernels.c:223-231). */
 int qmsg_layer_upload(qmsg_ctx *ctx, int layer, const qmsg_layer *host);
 
 /* No reference counterpart: fill a layer with the seeded synthetic weights described in
  * large_model_amd/csrc/qmsg_synth.h, generated on the device (router F32 N(0, sigma), experts
- * N(0, sigma) quantised to gate_type/up_type/down_type). If router_col0 is not NULL its
+ * N(0, sigma) quantised to gate_type/up_type/down_type: Q4_0, Q4_1 or Q6_K). If router_col0 is not NULL its
  * n_expert floats replace column 0 of the router (a routing bias for skewed expert load). */
 int qmsg_layer_synth(qmsg_ctx *ctx, int layer, uint64_t seed, int gate_type, int up_type, int down_type,
                      float sigma, const float *router_col0);

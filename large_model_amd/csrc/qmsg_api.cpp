@@ -312,10 +312,21 @@ static int check_layer_index(qmsg_ctx *c, int layer)
 static int layer_alloc(qmsg_ctx *c, LayerStore &L, int gt, int ut, int dt)
 {
     const int64_t E = c->cfg.n_embd, X = c->cfg.n_expert, F = c->cfg.n_ff_exp;
-    auto known = [](int t) { return t == QMSG_T_Q4_0 || t == QMSG_T_Q4_1 || t == QMSG_T_Q6_K; };
+    auto known = [](int t) {
+        return t == QMSG_T_Q4_0 || t == QMSG_T_Q4_1 || t == QMSG_T_Q6_K || t == QMSG_T_Q8_0 || t == QMSG_T_F16 ||
+               t == QMSG_T_F32;
+    };
     if (!known(gt) || !known(ut) || !known(dt))
-        return fail(c, QMSG_E_UNSUPPORTED, "expert types gate=%d up=%d down=%d: kernels take Q4_0, Q4_1 and Q6_K", gt,
-                    ut, dt);
+        return fail(c, QMSG_E_UNSUPPORTED,
+                    "expert types gate=%d up=%d down=%d: kernels take Q4_0, Q4_1, Q6_K, Q8_0, F16 and F32", gt, ut, dt);
+    /* The reference's fast gate (src/model.c:1090-1093) checks gate and down for F32 but not up,
+     * and its qms_vec_dot_q8 has no F32 case (src/kernels.c:223-231): such a layer's up rows
+     * come out NaN there, its quantiser makes the activation blocks zero, and the layer's
+     * output is zero. Refused rather than reproduced. */
+    auto fast = [](int t) { return t == QMSG_T_Q4_0 || t == QMSG_T_Q4_1 || t == QMSG_T_Q6_K || t == QMSG_T_F32; };
+    if (ut == QMSG_T_F32 && fast(gt) && fast(dt) && gt != QMSG_T_F32 && dt != QMSG_T_F32 && E % 256 == 0)
+        return fail(c, QMSG_E_UNSUPPORTED,
+                    "F32 up experts with quantised gate and down: the reference's fast path has no F32 dot for them");
     if (dt == QMSG_T_Q6_K && F % 256)
         return fail(c, QMSG_E_UNSUPPORTED, "Q6_K down needs n_ff_exp %% 256 == 0 (got %lld)", (long long)F);
     if ((gt == QMSG_T_Q6_K || ut == QMSG_T_Q6_K) && E % 256)
@@ -399,6 +410,8 @@ int qmsg_layer_synth(qmsg_ctx *c, int layer, uint64_t seed, int gt, int ut, int 
     int rc = check_layer_index(c, layer);
     if (rc) return rc;
     const int64_t E = c->cfg.n_embd, X = c->cfg.n_expert, F = c->cfg.n_ff_exp;
+    if (!integer_expert_types(gt, ut, dt))
+        return fail(c, QMSG_E_UNSUPPORTED, "qmsg_layer_synth: the generator writes Q4_0, Q4_1 and Q6_K experts");
     HIP_TRY(c, hipSetDevice(c->device));
     LayerStore &L = c->layers[(size_t)layer];
     if ((rc = layer_alloc(c, L, gt, ut, dt))) return rc;
@@ -808,10 +821,10 @@ static int run_layer_s(qmsg_ctx *c, const Scratch &S0, int layer, const float *d
         return fail(c, QMSG_E_INVALID, "device buffers must be 16-byte aligned (xn) and 4-byte aligned (out)");
     const Shape s{ c->cfg.n_embd, c->cfg.n_expert, c->cfg.n_used, c->cfg.n_ff_exp };
     const LayerDev d = layer_dev(c, L);
-    if (ni && (T != 1 || c->path == QMSG_PATH_FP32 || !route_norm_fits(s.E) || !integer_grid_shape(s.E, s.F) ||
-               ni->xn_out != d_xn))
+    const bool integer = integer_grid_shape(s.E, s.F) && integer_expert_types(d.gate_type, d.up_type, d.down_type);
+    if (ni && (T != 1 || c->path == QMSG_PATH_FP32 || !route_norm_fits(s.E) || !integer || ni->xn_out != d_xn))
         return fail(c, QMSG_E_INVALID, "run_layer_s: the fused rmsnorm takes one token on the integer paths");
-    if (c->path == QMSG_PATH_FP32 || !integer_grid_shape(s.E, s.F)) {
+    if (c->path == QMSG_PATH_FP32 || !integer) {
         LAUNCH(c, "layer", launch_layer_slots(s, d, S, d_xn, d_out, T, c->path == QMSG_PATH_FP32 ? 1 : 0, debug,
                                               c->stream));
         return QMSG_OK;
@@ -913,9 +926,13 @@ int qmsg_moe_chain(qmsg_ctx *c, int first, int n, float *d_h, int T, float eps)
     if ((uintptr_t)d_h & 15) return fail(c, QMSG_E_INVALID, "qmsg_moe_chain: d_h must be 16-byte aligned");
     HIP_TRY(c, hipSetDevice(c->device));
     const int E = c->cfg.n_embd;
-    for (int l = first; l < first + n; l++)
-        if (!c->layers[(size_t)l].ready) return fail(c, QMSG_E_INVALID, "layer %d has no weights", l);
-    if (T == 1 && c->path != QMSG_PATH_FP32 && route_norm_fits(E) && integer_grid_shape(E, c->cfg.n_ff_exp)) {
+    bool integer = integer_grid_shape(E, c->cfg.n_ff_exp);
+    for (int l = first; l < first + n; l++) {
+        const LayerStore &L = c->layers[(size_t)l];
+        if (!L.ready) return fail(c, QMSG_E_INVALID, "layer %d has no weights", l);
+        integer = integer && integer_expert_types(L.gate_type, L.up_type, L.down_type);
+    }
+    if (T == 1 && c->path != QMSG_PATH_FP32 && route_norm_fits(E) && integer) {
         /* One token: each layer's router launch forms the rmsnorm itself, every block from h
          * and the previous layer's output, so h + out goes to the other of two rows (d_h and
          * d_hb, in turn) while the blocks still read the first. */
@@ -1077,6 +1094,9 @@ int qmsg_block_dots(qmsg_ctx *c, int layer, int which, int n, const int32_t *exp
     const LayerDev d = layer_dev(c, L);
     const uint8_t *base = which == 0 ? d.gate : (which == 1 ? d.up : d.down);
     const int type = which == 0 ? d.gate_type : (which == 1 ? d.up_type : d.down_type);
+    if (type != QMSG_T_Q4_0 && type != QMSG_T_Q4_1 && type != QMSG_T_Q6_K)
+        return fail(c, QMSG_E_UNSUPPORTED, "qmsg_block_dots: int8 block dots take Q4_0, Q4_1 and Q6_K rows (type %d)",
+                    type);
     const uint64_t rb = which == 0 ? d.gate_rb : (which == 1 ? d.up_rb : d.down_rb);
     const uint64_t eb = which == 0 ? d.gate_eb : (which == 1 ? d.up_eb : d.down_eb);
     const int64_t rows = which == 2 ? c->cfg.n_embd : c->cfg.n_ff_exp;

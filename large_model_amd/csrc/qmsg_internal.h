@@ -177,6 +177,13 @@ hipError_t launch_layer_slots(const Shape &s, const LayerDev &L, const Scratch &
 /* The shapes the integer kernels take: n_embd % 256 == 0 (the reference's fast gate,
  * src/model.c:1090-1093) and n_ff_exp % 64 == 0 (they pair 32-blocks). */
 inline bool integer_grid_shape(int E, int F) { return E % 256 == 0 && F % 64 == 0; }
+/* Expert types the integer kernels take (the quantised types of qms_fast_supported); layers
+ * with F32, F16 or Q8_0 expert tensors run slot by slot. */
+inline bool integer_expert_types(int gt, int ut, int dt)
+{
+    auto q = [](int t) { return t == 2 || t == 3 || t == 14; };
+    return q(gt) && q(ut) && q(dt);
+}
 hipError_t launch_synth_f32(uint64_t key, uint64_t n, float sigma, float *out, hipStream_t st);
 hipError_t launch_synth_experts(uint64_t seed, uint32_t layer, uint32_t kind, int type, int64_t rows,
                                 int64_t cols, int X, float sigma, uint8_t *base, hipStream_t st);

@@ -4193,12 +4193,13 @@ __global__ __launch_bounds__(256) void dense_any_kernel(DenseArgs a)
     }
 }
 
-/* The same products per slot for the MoE layer at shapes off the integer kernels' grid
- * (n_embd % 256 != 0 or n_ff_exp % 64 != 0): the reference then runs moe_group_exact, whose
- * qms_matmul of each slot's gate, up and down rows takes this int8 path (src/model.c:1009-1030,
- * src/quant.c:134-136; with n_embd % 256 == 0 its moe_group_fast gives the same numbers,
- * src/model.c:969-1006). Block (row group, active expert blockIdx.y) as exact_rows_kernel;
- * the input of slot s is row slot_t[s] of x (by_token) or row s. */
+/* The same products per slot for MoE layers the integer kernels do not take: shapes off their
+ * grid (n_embd % 256 != 0 or n_ff_exp % 64 != 0) and expert tensors of other types. The
+ * reference then runs moe_group_exact, whose qms_matmul of each slot's gate, up and down rows
+ * takes this int8 path for Q4_0 / Q4_1 / Q6_K rows and dot_f32 for F32 rows (src/model.c:
+ * 1009-1030, src/quant.c:134-169; with n_embd % 256 == 0 its moe_group_fast gives the same
+ * numbers, src/model.c:969-1006). Block (32 rows, or 16 F32 rows; active expert blockIdx.y) as
+ * exact_rows_kernel; the input of slot s is row slot_t[s] of x (by_token) or row s. */
 struct SlotAnyArgs {
     const uint8_t *w;
     uint64_t rb, eb;
@@ -4214,9 +4215,11 @@ __global__ __launch_bounds__(256) void slot_any_kernel(SlotAnyArgs a)
 {
     extern __shared__ __align__(16) uint8_t smem[];
     if ((int)blockIdx.y >= a.S.meta[0]) return;       /* block-uniform */
+    constexpr int RPW = TYPE == 0 ? 4 : 8;            /* rows per wave  */
+    constexpr int LPR = 64 / RPW;                     /* lanes per row  */
     const int4 wk = a.S.work[blockIdx.y];
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, k = lane & 7;
-    const int row = (int)blockIdx.x * 32 + wave * 8 + (lane >> 3), C = a.cols;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, k = lane % LPR;
+    const int row = (int)blockIdx.x * 4 * RPW + wave * RPW + lane / LPR, C = a.cols;
     const uint8_t *wr = a.w + (size_t)wk.x * a.eb + (size_t)min(row, a.rows - 1) * a.rb;
     for (int s0 = wk.y; s0 < wk.z; s0 += NT) {
         const int nt = min(NT, wk.z - s0);
@@ -4480,11 +4483,24 @@ __global__ __launch_bounds__(64) void route_exact_kernel(const float *router, co
     logits[(size_t)t * X + e] = acc;
 }
 
-/* Dequantised 32-block b of a row (src/quant.c:17-79): Q4_0 (q-8)*d, Q4_1 q*d+m (fused like
- * the reference build), Q6_K (d*sc)*q. */
+/* Dequantised 32-block b of a row (src/quant.c:17-93): Q4_0 (q-8)*d, Q4_1 q*d+m (fused like
+ * the reference build), Q8_0 q*d, Q6_K (d*sc)*q, F16 and F32 as they are. */
 __device__ __forceinline__ void dequant_block(int type, const uint8_t *row, int b, float *w)
 {
-    if (type == 14) {
+    if (type == 0) {
+        const float *p = (const float *)(row + (size_t)b * 128);
+#pragma unroll
+        for (int j = 0; j < 32; j++) w[j] = p[j];
+    } else if (type == 1) {
+        const uint16_t *p = (const uint16_t *)(row + (size_t)b * 64);
+#pragma unroll
+        for (int j = 0; j < 32; j++) w[j] = h2f(p[j]);
+    } else if (type == 8) {
+        const uint8_t *bp = row + (size_t)b * 34;
+        const float d = h2f((uint32_t)bp[0] | ((uint32_t)bp[1] << 8));
+#pragma unroll
+        for (int j = 0; j < 32; j++) w[j] = (float)(int8_t)bp[2 + j] * d;
+    } else if (type == 14) {
         const uint8_t *sb = row + (size_t)(b >> 3) * 210;
         const int h = (b & 7) >> 2, g = b & 3;
         const float d = h2f((uint32_t)sb[208] | ((uint32_t)sb[209] << 8));
@@ -4607,7 +4623,9 @@ hipError_t launch_layer_slots(const Shape &s, const LayerDev &L, const Scratch &
             QLAUNCH("swiglu", swiglu_kernel, dim3((n + 255) / 256), dim3(256), 0, st, S, s.F, T * s.K);
         }
         const char *name = i == 2 ? "down" : "gateup";
-        if (exact) {
+        /* --exact, and F16 / Q8_0 rows at any setting (outside qms_fast_supported, so the
+         * reference's qms_matmul takes matmul_exact for them): the fp32 chain */
+        if (exact || m[i].type == 1 || m[i].type == 8) {
             ExactArgs a;
             a.S = S;
             a.w = m[i].w;
@@ -4640,8 +4658,9 @@ hipError_t launch_layer_slots(const Shape &s, const LayerDev &L, const Scratch &
         a.y_off = m[i].off;
         const int nb = m[i].cols / 32, NT = dense_any_nt(m[i].type, T, nb);
         if (!NT) return hipErrorInvalidValue;
-        const size_t lds = (size_t)NT * nb * kDenseAnyRec;
-        const dim3 grid((m[i].rows + 31) / 32, maxact);
+        const size_t lds = m[i].type == 0 ? 0 : (size_t)NT * nb * kDenseAnyRec;
+        const int rpb = m[i].type == 0 ? 16 : 32;
+        const dim3 grid((m[i].rows + rpb - 1) / rpb, maxact);
         auto go = [&](auto ty) {
             constexpr int TY = decltype(ty)::value;
             if (NT == 8) QLAUNCH(name, (slot_any_kernel<TY, 8>), grid, dim3(256), lds, st, a);
@@ -4651,6 +4670,7 @@ hipError_t launch_layer_slots(const Shape &s, const LayerDev &L, const Scratch &
         };
         if (m[i].type == 14) go(std::integral_constant<int, 14>());
         else if (m[i].type == 3) go(std::integral_constant<int, 3>());
+        else if (m[i].type == 0) go(std::integral_constant<int, 0>());
         else go(std::integral_constant<int, 2>());
     }
     if (debug && !exact) {

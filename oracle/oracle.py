@@ -15,7 +15,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 ORACLE_SO = os.path.join(HERE, "liboracle.so")
 REF_DIR = os.path.join(HERE, "_ref")
 
-T_F32, T_Q4_0, T_Q4_1, T_Q8_0, T_Q6_K = 0, 2, 3, 8, 14
+T_F32, T_F16, T_Q4_0, T_Q4_1, T_Q8_0, T_Q6_K = 0, 1, 2, 3, 8, 14
 KIND_X, KIND_ROUTER, KIND_GATE, KIND_UP, KIND_DOWN = 0, 1, 2, 3, 4
 Q8_DTYPE = np.dtype([("d", "<f4"), ("ds", "<f4"), ("s16", "<i2", (2,)), ("q", "i1", (32,))])
 

@@ -366,6 +366,18 @@ static float dot_exact(const float *row, const float *x, int64_t n)
     return acc;
 }
 
+/* One product of moe_group_exact's per-slot qms_matmul with qms_exact_math = 0 (src/quant.c:
+ * 128-170, model.c:1024-1027): int8 blocks (xq, the row x quantised) for the quantised types of
+ * the fast path, dot_f32 on x for F32 rows of whole 32-blocks, and otherwise (F16, Q8_0) the
+ * fp32 chain of matmul_exact on the dequantised row (tmp: n floats). */
+static float slot_dot(int type, const uint8_t *w, const orc_q8 *xq, const float *x, int64_t n, float *tmp)
+{
+    if (type == ORC_T_Q4_0 || type == ORC_T_Q4_1 || type == ORC_T_Q6_K) return orc_vec_dot_q8(type, w, xq, n);
+    if (type == ORC_T_F32 && n % 32 == 0) return orc_vec_dot_f32((const float *)w, x, n);
+    orc_dequant_row(type, w, tmp, n);
+    return dot_exact(tmp, x, n);
+}
+
 /* qms_matmul with qms_exact_math set (src/quant.c:97-115, 128-139): every row dequantised to
  * fp32 (qms_dequant_row), y[t][r] = dot_exact(row r, x_t). */
 int orc_matmul_exact(int type, const uint8_t *w, int64_t rows, int64_t cols, uint64_t row_bytes, const float *x,
@@ -402,12 +414,16 @@ static int moe_common(int exact, int E, int X, int K, int F, const orc_mat *rout
     if (exact) {
         if (!orc_row_bytes(gate->type, E) || !orc_row_bytes(up->type, E) || !orc_row_bytes(down->type, F)) return -1;
     } else {
-        /* model.c:1090-1093 (or, for n_embd % 256 != 0, the int8 qms_matmul of every slot) */
+        /* model.c:1090-1093: moe_group_fast, or moe_group_exact whose per-slot qms_matmul picks
+         * each matrix's dot by its type (slot_dot). Rows of whole 32-blocks here. Not modelled:
+         * the fast gate with F32 up rows, which it sends to qms_vec_dot_q8 (no F32 case there:
+         * NaN, src/kernels.c:223-231). */
         const int fast = orc_fast_supported(gate->type) && orc_fast_supported(up->type) &&
                          orc_fast_supported(down->type) && gate->type != ORC_T_F32 &&
-                         up->type != ORC_T_F32 && down->type != ORC_T_F32 && E % 32 == 0 && F % 32 == 0 &&
-                         orc_row_bytes(gate->type, E) && orc_row_bytes(up->type, E) && orc_row_bytes(down->type, F);
-        if (!fast) return -1;
+                         down->type != ORC_T_F32 && E % 256 == 0 && F % 32 == 0;
+        if (E % 32 || F % 32 || !orc_row_bytes(gate->type, E) || !orc_row_bytes(up->type, E) ||
+            !orc_row_bytes(down->type, F) || (fast && up->type == ORC_T_F32))
+            return -1;
     }
     if (T == 0) return 0;
     const int NS = T * K, nbE = E / 32, nbF = F / 32;
@@ -482,9 +498,11 @@ static int moe_common(int exact, int E, int X, int K, int F, const orc_mat *rout
             free(row);
         }
     } else {
-    /* moe_group_fast, model.c:979-1005 */
+    /* moe_group_fast, model.c:979-1005; with every matrix quantised moe_group_exact's steps are
+     * the same, and slot_dot picks the dot of its other types */
 #pragma omp parallel
     {
+        float *tmp = (float *)malloc((size_t)(E > F ? E : F) * sizeof(float));
 #pragma omp for schedule(static)
         for (int64_t it = 0; it < (int64_t)na * 2 * F; it++) {
             const int e = active[it / (2 * F)];
@@ -492,7 +510,8 @@ static int moe_common(int exact, int E, int X, int K, int F, const orc_mat *rout
             const orc_mat *W = r < F ? gate : up;
             const uint8_t *row = expert_row(W, e, r < F ? r : r - F);
             for (int s = start[e]; s < start[e + 1]; s++)
-                gu[(size_t)s * 2 * F + r] = orc_vec_dot_q8(W->type, row, xq + (size_t)slot_t[s] * nbE, E);
+                gu[(size_t)s * 2 * F + r] = slot_dot(W->type, row, xq + (size_t)slot_t[s] * nbE,
+                                                     xn + (size_t)slot_t[s] * E, E, tmp);
         }
 #pragma omp for schedule(static)
         for (int s = 0; s < NS; s++) {
@@ -507,8 +526,9 @@ static int moe_common(int exact, int E, int X, int K, int F, const orc_mat *rout
             const int r = (int)(it % E);
             const uint8_t *row = expert_row(down, e, r);
             for (int s = start[e]; s < start[e + 1]; s++)
-                dn[(size_t)s * E + r] = orc_vec_dot_q8(down->type, row, aq + (size_t)s * nbF, F);
+                dn[(size_t)s * E + r] = slot_dot(down->type, row, aq + (size_t)s * nbF, act + (size_t)s * F, F, tmp);
         }
+        free(tmp);
     }
     }
 

@@ -373,6 +373,77 @@ def test_off_grid_shapes(E, X, K, F, T, gt, ut, dt):
     assert np.array_equal(orc.ref_moe(R, L, x, exact=True).view(np.uint32), L.moe(x, exact=True).view(np.uint32))
 
 
+# ------------------------------------------------------------------ expert tensors of other types
+
+Q40, Q41, Q6K, Q80, F16, F32 = orc.T_Q4_0, orc.T_Q4_1, orc.T_Q6_K, orc.T_Q8_0, orc.T_F16, orc.T_F32
+TYPED = [   # E, X, K, F, T, (gate, up, down)
+    (256, 16, 4, 128, 3, (Q80, Q80, Q80)),
+    (256, 16, 4, 128, 1, (F16, F16, F16)),
+    (256, 16, 4, 128, 4, (F32, Q40, F32)),
+    (512, 8, 2, 256, 5, (Q40, Q80, Q6K)),
+    (96, 8, 2, 96, 2, (Q80, Q41, F16)),
+    (288, 12, 3, 96, 3, (Q40, F32, Q40)),
+]
+
+
+def _slot_dot_ok(t, row, x, xq, y):
+    """y is row . x as the reference's qms_matmul takes it for type t: int8 blocks or dot_f32
+    exactly (the dense restatement, pinned by the reference's fixtures); for F16 / Q8_0 rows
+    (matmul_exact's fp32 chain) within the chain's rounding bound of the float64 dot."""
+    n = x.size
+    if t in (Q40, Q41, Q6K, F32):
+        return np.float32(y).view(np.uint32) == orc.matmul_q8(t, row, 1, n, x[None])[0, 0].view(np.uint32)
+    w = orc.dequant_row(t, row, n).astype(np.float64)
+    exact = float(np.dot(w, x.astype(np.float64)))
+    return abs(float(y) - exact) <= n * 2.0 ** -23 * float(np.abs(w * x).sum()) + 1e-30
+
+
+@pytest.mark.parametrize("E,X,K,F,T,types", TYPED, ids=["_".join(map(str, c[5])) + f"_e{c[0]}" for c in TYPED])
+def test_expert_types(E, X, K, F, T, types):
+    """Q8_0, F16 and F32 expert tensors (the reference's loader takes any type; outside its fast
+    gate moe_group_exact's qms_matmul picks each matrix's dot by type, src/model.c:1009-1030,
+    src/quant.c:128-170): the oracle's per-slot rows follow that choice, and its layer equals
+    the reference build's moe() bit for bit, with and without --exact."""
+    import expert_types as et
+    seed = 120 + E % 89 + T
+    L = et.typed_layer(E, X, K, F, types, seed)
+    x = orc.make_input(E, T, seed, rmsnorm=True)
+    out, d = L.moe(x, debug=True)
+    gt, ut, dt = types
+    rb, eb = L.rb, L.eb
+    for e in d["active"]:
+        for s in range(int(d["start"][e]), int(d["start"][e + 1])):
+            tk = int(d["slot_t"][s])
+            for r in (0, F // 2, F - 1):
+                assert _slot_dot_ok(gt, L.gate[e * eb[0] + r * rb[0]:e * eb[0] + (r + 1) * rb[0]], x[tk], None,
+                                    d["gu"][s, r])
+                assert _slot_dot_ok(ut, L.up[e * eb[1] + r * rb[1]:e * eb[1] + (r + 1) * rb[1]], x[tk], None,
+                                    d["gu"][s, F + r])
+            for r in (0, E - 1):
+                assert _slot_dot_ok(dt, L.down[e * eb[2] + r * rb[2]:e * eb[2] + (r + 1) * rb[2]], d["act"][s], None,
+                                    d["dn"][s, r])
+    R = orc.load_ref()
+    if R is None:
+        pytest.skip("reference build (oracle/_ref) not present")
+    assert np.array_equal(orc.ref_moe(R, L, x).view(np.uint32), out.view(np.uint32))
+    assert np.array_equal(orc.ref_moe(R, L, x, exact=True).view(np.uint32), L.moe(x, exact=True).view(np.uint32))
+
+
+def test_f32_up_behind_the_fast_gate_is_not_modelled():
+    """Quantised gate and down with F32 up at n_embd % 256 == 0 pass the reference's fast gate,
+    which sends the up rows to qms_vec_dot_q8 (no F32 case: NaN, src/kernels.c:223-231); its
+    quantiser turns the NaN activations into zero blocks (d = 0), so the layer's output is all
+    zeros there. The oracle refuses the layer, and the library refuses it at upload."""
+    import expert_types as et
+    L = et.typed_layer(256, 16, 4, 128, (Q40, F32, Q40), 77)
+    x = orc.make_input(256, 2, 77, rmsnorm=True)
+    with pytest.raises(RuntimeError):
+        L.moe(x)
+    R = orc.load_ref()
+    if R is not None:
+        assert not np.any(orc.ref_moe(R, L, x))
+
+
 # ------------------------------------------------------------------ planted mistakes
 
 MUTATIONS = ["HSUM_LINEAR", "CORR_UNFUSED", "NIBBLE_ORDER", "ROUTER_TREE", "ROUND_AWAY", "TIE_HIGH",
