@@ -224,6 +224,23 @@ def test_reference_loader_moe_equals_oracle(tmp_path):
         assert np.array_equal(out.view(np.uint32), lay.moe(x).view(np.uint32)), l
 
 
+@need_ref
+def test_reference_loader_typed_experts_off_grid(tmp_path):
+    """The same for Q8_0, F16 and F32 expert tensors at an n_embd off the integer kernels' grid
+    (the layers the slot kernels run)."""
+    import expert_types as et
+    E, X, K, F, T = 288, 12, 3, 160, 4
+    lays = [et.typed_layer(E, X, K, F, types, 70 + 10 * l)
+            for l, types in enumerate(((orc.T_Q8_0, orc.T_Q8_0, orc.T_Q8_0),
+                                       (orc.T_F16, orc.T_Q8_0, orc.T_F32)))]
+    path, _ = gf.moe_model(str(tmp_path / "q8.gguf"), lays)
+    x = orc.make_input(E, T, 5, rmsnorm=True)
+    for l, lay in enumerate(lays):
+        out = np.empty_like(x)
+        assert ref_lib().qref_gguf_moe(os.fsencode(path), l, x.ctypes.data, T, out.ctypes.data) == 0
+        assert np.array_equal(out.view(np.uint32), lay.moe(x).view(np.uint32)), l
+
+
 def test_mutated_files_under_sanitizers(tmp_path):
     """The reader on 2,000 mutations of a valid model file (bit flips, bytes set to boundary
     integers, truncations; mostly in the header and tables), built from its own source with

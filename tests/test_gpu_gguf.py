@@ -86,3 +86,31 @@ def test_gguf_upload_checks_shapes_and_range(q, tmp_path):
     with q.Gguf(path) as g, q.Context(E, X, K, F + 64, n_layer=2, max_tokens=2) as ctx:
         with pytest.raises(q.QmsgError):
             ctx.load_gguf(g, 0, 1)               # the file's n_ff_exp differs from the context's
+
+
+def test_gguf_q8_0_f16_experts_off_grid(q, tmp_path):
+    """A written file with Q8_0 and F16 / F32 expert tensors (Q8_0 GGUF files carry them) at an
+    n_embd off the integer kernels' grid: loaded, bit for bit per layer and over the chain."""
+    import expert_types as et
+    E, X, K, F, T = 288, 12, 3, 160, 4
+    lays = [et.typed_layer(E, X, K, F, types, 70 + 10 * l)
+            for l, types in enumerate(((orc.T_Q8_0, orc.T_Q8_0, orc.T_Q8_0),
+                                       (orc.T_F16, orc.T_Q8_0, orc.T_F32)))]
+    path, norms = gf.moe_model(str(tmp_path / "q8.gguf"), lays, eps=1e-6)
+    print(f"[case] gguf q8_0/f16 E={E} F={F} T={T}", flush=True)
+    x = orc.make_input(E, T, 5, rmsnorm=True)
+    h0 = orc.make_input(E, T, 6) * np.float32(3.0)
+    with q.Gguf(path) as g, q.Context.from_gguf(g, max_tokens=T) as ctx:
+        for l, lay in enumerate(lays):
+            r, gate, up, down = ctx.download(l)
+            assert np.array_equal(gate, lay.gate) and np.array_equal(up, lay.up) and np.array_equal(down, lay.down)
+            assert np.array_equal(ctx.moe(l, x).view(np.uint32), lay.moe(x).view(np.uint32)), l
+        h = h0.copy()
+        for l, lay in enumerate(lays):
+            h = h + lay.moe(orc.rmsnorm(h, norms[l], eps=ctx.eps))
+        d_h = ctx.device_alloc(h0.nbytes)
+        ctx.h2d(d_h, h0)
+        ctx.moe_chain(0, 2, d_h, T, eps=ctx.eps)
+        ctx.sync()
+        got = ctx.d2h(d_h, (T, E))
+    assert np.array_equal(got.view(np.uint32), h.view(np.uint32))
