@@ -198,10 +198,12 @@ int qmsg_gguf_upload(qmsg_ctx *ctx, const qmsg_gguf *g, int first, int n);
  * (src/model.c:67-85): rows of row_bytes GGUF bytes, copied unchanged; *id names it in
  * qmsg_matmul_n. The types of the reference's fast path (qms_fast_supported,
  * src/kernels.c:197-200) at the widths it admits (src/quant.c:134-136): F32, Q4_0 and Q4_1
- * rows with cols % 32 == 0, Q6_K rows with cols % 256 == 0; QMSG_E_UNSUPPORTED otherwise
- * (the reference would take matmul_exact). Widths off the chunked kernels' grid (cols % 256,
- * Q6_K cols % 2048; no Qwen3-MoE trunk matrix has one) take a direct-read kernel, which
- * bounds quantised rows to cols <= 109,216 there. */
+ * rows with cols % 32 == 0, Q6_K rows with cols % 256 == 0. Widths off the chunked kernels'
+ * grid (cols % 256, Q6_K cols % 2048; no Qwen3-MoE trunk matrix has one) take a direct-read
+ * kernel, which bounds quantised rows to cols <= 109,216 there. F16 and Q8_0 rows (cols % 32,
+ * cols <= 40,960) are taken too: as in the reference, a call holding one of them, and every
+ * call on a QMSG_PATH_FP32 context, runs matmul_exact's fp32 chains for all its matrices
+ * (src/quant.c:97-115, 131-141). Other types: QMSG_E_UNSUPPORTED. */
 int qmsg_mat_upload(qmsg_ctx *ctx, const qmsg_mat *host, int *id);
 /* The same from a parsed GGUF file, by tensor name (e.g. "blk.0.attn_q.weight"). */
 int qmsg_gguf_upload_mat(qmsg_ctx *ctx, const qmsg_gguf *g, const char *name, int *id);

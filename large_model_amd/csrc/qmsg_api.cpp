@@ -625,10 +625,12 @@ int qmsg_gguf_upload(qmsg_ctx *c, const qmsg_gguf *g, int first, int n)
 
 static int dense_check(qmsg_ctx *c, int type, int64_t rows, int64_t cols, const char *what)
 {
-    /* the types of qms_matmul_n's fast path (src/quant.c:128-170, qms_fast_supported) */
-    if (type != QMSG_T_F32 && type != QMSG_T_Q4_0 && type != QMSG_T_Q4_1 && type != QMSG_T_Q6_K)
-        return fail(c, QMSG_E_UNSUPPORTED, "%s: the dense kernels take F32, Q4_0, Q4_1 and Q6_K (got type %d)", what,
-                    type);
+    /* the types of qms_matmul_n's fast path (src/quant.c:128-170, qms_fast_supported), and F16
+     * and Q8_0, which it (and so every matrix of a call holding one) sends to matmul_exact */
+    if (type != QMSG_T_F32 && type != QMSG_T_Q4_0 && type != QMSG_T_Q4_1 && type != QMSG_T_Q6_K &&
+        type != QMSG_T_F16 && type != QMSG_T_Q8_0)
+        return fail(c, QMSG_E_UNSUPPORTED,
+                    "%s: the dense kernels take F32, F16, Q4_0, Q4_1, Q8_0 and Q6_K (got type %d)", what, type);
     const int64_t step = type == QMSG_T_Q6_K ? 256 : 32;     /* src/quant.c:135-136 */
     /* both bounded by 2^30: rows x row bytes stays far inside 64 bits and cols fits an int */
     if (rows <= 0 || rows > (1 << 30) || cols <= 0 || cols > (1 << 30) || cols % step)
@@ -637,9 +639,13 @@ static int dense_check(qmsg_ctx *c, int type, int64_t rows, int64_t cols, const 
     /* widths off the chunked kernels' grid (cols % 256, Q6_K cols % 2048) take the direct-read
      * kernel, whose quantised input row must fit in LDS: 48 bytes per 32-block, 160 KiB */
     const bool direct = cols % (type == QMSG_T_Q6_K ? 2048 : 256) != 0;
-    if (direct && type != QMSG_T_F32 && cols / 32 * 48 > 160 * 1024)
+    const bool exact_only = type == QMSG_T_F16 || type == QMSG_T_Q8_0;
+    if (direct && !exact_only && type != QMSG_T_F32 && cols / 32 * 48 > 160 * 1024)
         return fail(c, QMSG_E_UNSUPPORTED, "%s: cols %lld is not a multiple of %d and above %d", what, (long long)cols,
                     type == QMSG_T_Q6_K ? 2048 : 256, 160 * 1024 / 48 * 32);
+    /* the fp32-chain kernel stages one input row of cols floats in LDS */
+    if (exact_only && cols * 4 > 160 * 1024)
+        return fail(c, QMSG_E_UNSUPPORTED, "%s: F16 / Q8_0 rows above %d columns", what, 160 * 1024 / 4);
     return QMSG_OK;
 }
 
@@ -679,6 +685,8 @@ int qmsg_mat_synth(qmsg_ctx *c, int type, int64_t rows, int64_t cols, uint64_t s
     if (!c || !id) return QMSG_E_INVALID;
     int rc = dense_check(c, type, rows, cols, "qmsg_mat_synth");
     if (rc) return rc;
+    if (type == QMSG_T_F16 || type == QMSG_T_Q8_0)
+        return fail(c, QMSG_E_UNSUPPORTED, "qmsg_mat_synth: the generator writes F32, Q4_0, Q4_1 and Q6_K");
     HIP_TRY(c, hipSetDevice(c->device));
     if ((rc = dense_new(c, type, rows, cols, id))) return rc;
     /* the generator of the expert tensors with one "expert" of kind gate, layer 0 (F32: the
@@ -746,6 +754,15 @@ int qmsg_matmul_n_device(qmsg_ctx *c, const int *ids, int nW, const float *d_x, 
         const int rc = grow(c, &c->dense_xqk, &c->dense_xqk_bytes, (size_t)T * (size_t)(C / 64) * kPairBytes);
         if (rc) return rc;
     }
+    /* qms_matmul_n's choice for the whole call (src/quant.c:131-141): the fast loop, or
+     * matmul_exact for every matrix when --exact is set or one of them is F16 / Q8_0 */
+    bool exact = c->path == QMSG_PATH_FP32;
+    for (int i = 0; i < nW; i++) {
+        const int t = c->mats[(size_t)ids[i]].type;
+        exact = exact || t == QMSG_T_F16 || t == QMSG_T_Q8_0;
+    }
+    if (exact && C * 4 > 160 * 1024)
+        return fail(c, QMSG_E_UNSUPPORTED, "qmsg_matmul_n: fp32-chain rows above %d columns", 160 * 1024 / 4);
     /* launches of up to kDenseMats matrices of one type, in argument order */
     std::vector<bool> done((size_t)nW, false);
     for (int i = 0; i < nW; i++) {
@@ -765,7 +782,8 @@ int qmsg_matmul_n_device(qmsg_ctx *c, const int *ids, int nW, const float *d_x, 
             a.nm++;
             done[(size_t)j] = true;
         }
-        LAUNCH(c, "dense", launch_dense(a, type, (uint8_t *)c->dense_xqk, c->stream));
+        if (exact) LAUNCH(c, "dense", launch_dense_exact(a, type, c->stream));
+        else LAUNCH(c, "dense", launch_dense(a, type, (uint8_t *)c->dense_xqk, c->stream));
     }
     return QMSG_OK;
 }

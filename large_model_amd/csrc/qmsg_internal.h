@@ -226,6 +226,8 @@ hipError_t launch_call_reset(const Scratch &S, hipStream_t st);
 /* The dense rows kernel; for T >= kDenseQuantT the input records are formed first into xqk
  * (T*C/64 records of 96 bytes). */
 hipError_t launch_dense(const DenseArgs &a, int type, uint8_t *xqk, hipStream_t st);
+/* matmul_exact for every matrix of a call (--exact, or an F16 / Q8_0 matrix in the call). */
+hipError_t launch_dense_exact(const DenseArgs &args, int type, hipStream_t st);
 hipError_t launch_block_dots(const uint8_t *base, int type, uint64_t rb, uint64_t eb, int n, const int32_t *expert,
                              const int32_t *row, const int32_t *block, const Q8 *xq, int32_t *out,
                              hipStream_t st);

@@ -4687,6 +4687,68 @@ hipError_t launch_layer_slots(const Shape &s, const LayerDev &L, const Scratch &
     return hipGetLastError();
 }
 
+/* ------------------------------------------------------------------ dense rows, fp32 chains ---- */
+
+/* qms_matmul_n's matmul_exact (src/quant.c:97-115) for calls the fast loop does not take: the
+ * --exact mode, or any matrix of a type outside qms_fast_supported (F16, Q8_0) in the call,
+ * which sends every matrix of it there (src/quant.c:131-141). One lane per row of the call's
+ * matrices (one type per launch), its dequantised 32-blocks against up to NT tokens staged in
+ * LDS, acc = fma(w, x, acc) in element order. Rows past a matrix's end read its last row and
+ * store nothing. */
+template <int NT>
+__global__ __launch_bounds__(64) void dense_exact_kernel(DenseArgs a, int type)
+{
+    extern __shared__ __align__(16) uint8_t smem[];
+    float *xr = (float *)smem;                        /* [NT][C] */
+    int mi = 0;
+#pragma unroll
+    for (int i = 1; i < kDenseMats; i++)
+        if (i < a.nm && (int)blockIdx.x >= a.m[i].first_block) mi = i;
+    const DenseMat M = a.m[mi];
+    const int lane = threadIdx.x, C = a.C;
+    const int row = ((int)blockIdx.x - M.first_block) * 64 + lane;
+    const uint8_t *wr = M.w + (size_t)min(row, M.rows - 1) * a.rb;
+    for (int t0 = 0; t0 < a.T; t0 += NT) {
+        const int nt = min(NT, a.T - t0);
+        __syncthreads();
+        for (int i = lane; i < nt * (C / 4); i += 64)
+            ((float4 *)xr)[i] = ((const float4 *)(a.x + (size_t)t0 * C))[i];
+        __syncthreads();
+        float acc[NT];
+#pragma unroll
+        for (int n = 0; n < NT; n++) acc[n] = 0.0f;
+        for (int b = 0; b < C / 32; b++) {
+            float w[32];
+            dequant_block(type, wr, b, w);
+#pragma unroll
+            for (int n = 0; n < NT; n++)
+                if (n < nt)
+#pragma unroll
+                    for (int j = 0; j < 32; j++) acc[n] = __builtin_fmaf(w[j], xr[n * C + 32 * b + j], acc[n]);
+        }
+        if (row < M.rows)
+            for (int n = 0; n < nt; n++) M.y[(size_t)(t0 + n) * M.rows + row] = acc[n];
+    }
+}
+
+hipError_t launch_dense_exact(const DenseArgs &args, int type, hipStream_t st)
+{
+    DenseArgs a = args;
+    const size_t row_lds = (size_t)a.C * 4;
+    const int NT = 4 * row_lds <= 160 * 1024 ? 4 : (2 * row_lds <= 160 * 1024 ? 2 : 1);
+    if (row_lds > 160 * 1024) return hipErrorInvalidValue;
+    int nblk = 0;
+    for (int i = 0; i < a.nm; i++) {
+        a.m[i].first_block = nblk;
+        nblk += (a.m[i].rows + 63) / 64;
+    }
+    const size_t lds = NT * row_lds;
+    if (NT == 4) QLAUNCH("dense", dense_exact_kernel<4>, dim3(nblk), dim3(64), lds, st, a, type);
+    else if (NT == 2) QLAUNCH("dense", dense_exact_kernel<2>, dim3(nblk), dim3(64), lds, st, a, type);
+    else QLAUNCH("dense", dense_exact_kernel<1>, dim3(nblk), dim3(64), lds, st, a, type);
+    return hipGetLastError();
+}
+
 /* ------------------------------------------------------------------ block dots (checks) ---- */
 
 /* Exact signed int32 dot of one 32-block of a weight row with one Q8 block, formed with the

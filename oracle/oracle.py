@@ -134,6 +134,29 @@ def block_dots_at(t: int, w: np.ndarray, rb: int, eb: int, ex, row, blk, xq: np.
     return out
 
 
+def matmul_exact(t: int, w: np.ndarray, rows: int, cols: int, x: np.ndarray) -> np.ndarray:
+    """qms_matmul's matmul_exact (src/quant.c:97-115): dequantised fp32 rows, sequential FMA
+    chains. y [T][rows]."""
+    x = np.ascontiguousarray(x, np.float32).reshape(-1, cols)
+    y = np.empty((x.shape[0], rows), np.float32)
+    wb = np.ascontiguousarray(w).reshape(-1).view(np.uint8)
+    assert wb.size == rows * row_bytes(t, cols)
+    assert lib.orc_matmul_exact(t, _ptr(wb), rows, cols, row_bytes(t, cols), _ptr(x), x.shape[0], _ptr(y)) == 0
+    return y
+
+
+FAST_TYPES = (T_F32, T_Q4_0, T_Q4_1, T_Q6_K)       # qms_fast_supported, src/kernels.c:197-200
+
+
+def matmul_n(mats, x: np.ndarray, exact: bool = False) -> list:
+    """qms_matmul_n (src/quant.c:128-170) on matrices [(type, bytes, rows, cols)] of equal cols:
+    the int8 / dot_f32 loop for all of them, unless --exact is set or any one of them is
+    outside the fast path (type or cols), which sends every one to matmul_exact (131-141)."""
+    fast = not exact and all(t in FAST_TYPES and c % (256 if t == T_Q6_K else 32) == 0 for t, _, _, c in mats)
+    fn = matmul_q8 if fast else matmul_exact
+    return [fn(t, w, r, c, x) for t, w, r, c in mats]
+
+
 def dequant_row(t: int, w: np.ndarray, n: int) -> np.ndarray:
     out = np.empty(n, np.float32)
     assert lib.orc_dequant_row(t, _ptr(np.ascontiguousarray(w, np.uint8)), _ptr(out), n) == 0

@@ -92,12 +92,14 @@ def test_dense_from_gguf_and_errors(q, tmp_path):
     E, R = 1024, 256
     wq = dense_mat(orc.T_Q4_0, R, E, 11)
     wk = orc.make_input(E, 64, 13)
+    import expert_types as et
+    wv = et.expert_bytes(orc.T_Q8_0, 8, E, 1, 14)
     path = str(tmp_path / "trunk.gguf")
     gf.write_gguf(path, [("general.architecture", gf.STR, "qwen3moe")],
                   [("blk.0.attn_q.weight", orc.T_Q4_0, [E, R], wq.tobytes()),
                    ("blk.0.attn_norm.weight", orc.T_F32, [E], np.ones(E, np.float32).tobytes()),
                    ("blk.0.attn_k.weight", orc.T_F32, [E, 64], wk.tobytes()),
-                   ("blk.0.attn_v.weight", orc.T_Q8_0, [E, 8], np.zeros(8 * 34 * E // 32, np.uint8).tobytes())])
+                   ("blk.0.attn_v.weight", orc.T_Q8_0, [E, 8], wv.tobytes())])
     x = orc.make_input(E, 2, 12)
     with q.Gguf(path) as g, q.Context(256, 16, 4, 128, max_tokens=1) as ctx:
         mid = ctx.gguf_upload_mat(g, "blk.0.attn_q.weight")
@@ -108,8 +110,12 @@ def test_dense_from_gguf_and_errors(q, tmp_path):
         yk, yq = ctx.matmul_n([kid, qid], x)                       # F32 and Q4_0 in one call
         assert np.array_equal(bits(yk), bits(orc.matmul_q8(orc.T_F32, wk, 64, E, x)))
         assert np.array_equal(bits(yq), bits(y))
+        vid = ctx.gguf_upload_mat(g, "blk.0.attn_v.weight")       # Q8_0: matmul_exact, for the whole call
+        yv, yq2 = ctx.matmul_n([vid, qid], x)
+        assert np.array_equal(bits(yv), bits(orc.matmul_exact(orc.T_Q8_0, wv, 8, E, x)))
+        assert np.array_equal(bits(yq2), bits(orc.matmul_exact(orc.T_Q4_0, wq, R, E, x)))
         with pytest.raises(q.QmsgError) as ei:
-            ctx.gguf_upload_mat(g, "blk.0.attn_v.weight")         # Q8_0: not a dense kernel type
+            ctx.mat_upload(13, np.zeros(176 * 4, np.uint8), 1, 1024)     # Q5_K: no dense kernel
         assert ei.value.status == -2
         with pytest.raises(q.QmsgError):
             ctx.gguf_upload_mat(g, "blk.0.attn_norm.weight")      # 1-D
@@ -234,3 +240,34 @@ def test_dense_random_calls(q, seed):
         ys = ctx.matmul_n(ids, x)
     for (t, r), w, y in zip(specs, ws, ys):
         assert np.array_equal(bits(y), bits(orc.matmul_q8(t, w, r, C, x))), (t, r)
+
+
+EXACT_CALLS = [   # (type, rows) per matrix, cols, T, the context on QMSG_PATH_FP32
+    ([(orc.T_Q8_0, 100)], 2048, 1, False),
+    ([(orc.T_F16, 77)], 4096, 3, False),
+    ([(orc.T_Q4_0, 300), (orc.T_Q8_0, 64), (orc.T_F32, 40), (orc.T_Q6_K, 33)], 2048, 5, False),
+    ([(orc.T_Q4_0, 130), (orc.T_Q6_K, 20), (orc.T_F32, 9)], 4096, 2, True),
+    ([(orc.T_Q8_0, 50), (orc.T_F16, 3)], 96, 9, False),
+    ([(orc.T_Q4_1, 64)], 8192, 1, True),
+]
+
+
+@pytest.mark.parametrize("specs,cols,T,fp32", EXACT_CALLS,
+                         ids=[f"c{c[1]}_t{c[2]}_{'_'.join(str(t) for t, _ in c[0])}{'_fp32' if c[3] else ''}"
+                              for c in EXACT_CALLS])
+def test_dense_exact_calls(q, specs, cols, T, fp32):
+    """qms_matmul_n's matmul_exact (src/quant.c:97-115, 131-141): F16 and Q8_0 matrices, every
+    matrix of a call holding one of them, and every call of a context on the --exact path, in
+    fp32 chains on dequantised rows; bit for bit against the oracle's matmul_n."""
+    import expert_types as et
+    print(f"[case] dense exact {specs} C={cols} T={T} fp32={fp32}", flush=True)
+    ws = [et.expert_bytes(t, r, cols, 1, 600 + i) for i, (t, r) in enumerate(specs)]
+    x = orc.make_input(cols, T, 601) * np.float32(2.0)
+    with q.Context(256, 16, 4, 128, max_tokens=1) as ctx:
+        if fp32:
+            ctx.set_path(q.PATH_FP32)
+        ids = [ctx.mat_upload(t, w, r, cols) for (t, r), w in zip(specs, ws)]
+        ys = ctx.matmul_n(ids, x)
+    ref = orc.matmul_n([(t, w, r, cols) for (t, r), w in zip(specs, ws)], x, exact=fp32)
+    for y, r in zip(ys, ref):
+        assert np.array_equal(bits(y), bits(r))
