@@ -360,11 +360,13 @@ __global__ __launch_bounds__(256) void route_small_kernel(RouteArgs a)
  * chain), so each chain still walks its elements c, c+16, ... in order. The next P chunks are
  * in flight in registers while one is consumed. Small blocks (J = KT = 1: 4 experts x 4
  * tokens) spread batches of up to 64 tokens over many CUs; larger batches take J = KT = 4
- * (16 x 16), which reads each router and input row fewer times. */
+ * (16 x 16), which reads each router and input row fewer times. TAIL takes rows of any
+ * multiple of 32 floats: a last partial chunk of E % 256 elements gives every chain
+ * (E % 256) / 16 more steps, in order (dot_f32 has no scalar tail at these widths). */
 constexpr int kRouteBigCSC = 20;                  /* floats per chain and chunk in LDS (16 + pad) */
 /* LDS bytes of route_big_kernel<J, J, P>: 4J expert rows and 4J token rows of 16 chains. */
 constexpr size_t route_big_lds(int J) { return (size_t)(8 * J) * 16 * kRouteBigCSC * 4; }
-template <int J, int KT, int P>
+template <int J, int KT, int P, bool TAIL = false>
 __global__ __launch_bounds__(256) void route_big_kernel(RouteArgs a)
 {
     extern __shared__ __align__(16) uint8_t smem[];
@@ -380,17 +382,21 @@ __global__ __launch_bounds__(256) void route_big_kernel(RouteArgs a)
     float acc[J][KT];
     for (int j = 0; j < J; j++) for (int k = 0; k < KT; k++) acc[j][k] = 0.0f;
     u32x4 pw[P][J], px[P][KT];
-    const int nch = E / CH;
+    /* TAIL: rows of any multiple of 32 floats; the last chunk holds E % 256 of them (pieces
+     * past the row are not loaded, and the chains take only its steps) */
+    const int nch = TAIL ? (E + CH - 1) / CH : E / CH;
     auto load = [&](int ch, u32x4 *w, u32x4 *x) {
 #pragma unroll
         for (int m = 0; m < J; m++) {
-            const int q = tid + 256 * m;
-            w[m] = *(const u32x4 *)(a.router + (size_t)min(e0 + (q >> 6), X - 1) * E + (size_t)ch * CH + (q & 63) * 4);
+            const int q = tid + 256 * m, col = ch * CH + (q & 63) * 4;
+            if (TAIL && col >= E) w[m] = u32x4{ 0u, 0u, 0u, 0u };
+            else w[m] = *(const u32x4 *)(a.router + (size_t)min(e0 + (q >> 6), X - 1) * E + col);
         }
 #pragma unroll
         for (int m = 0; m < KT; m++) {
-            const int q = tid + 256 * m;
-            x[m] = *(const u32x4 *)(a.xn + (size_t)min(t0 + (q >> 6), T - 1) * E + (size_t)ch * CH + (q & 63) * 4);
+            const int q = tid + 256 * m, col = ch * CH + (q & 63) * 4;
+            if (TAIL && col >= E) x[m] = u32x4{ 0u, 0u, 0u, 0u };
+            else x[m] = *(const u32x4 *)(a.xn + (size_t)min(t0 + (q >> 6), T - 1) * E + col);
         }
     };
     /* the 16-byte slot q4 of a row's chunk holds elements 4 q4 .. 4 q4 + 3: step q4 / 4 of chains
@@ -423,17 +429,24 @@ __global__ __launch_bounds__(256) void route_big_kernel(RouteArgs a)
                 }
                 __syncthreads();
                 if (ch + P < nch) load(ch + P, pw[d], px[d]);
+                /* steps of each chain in this chunk: 16, or (E % 256) / 16 (even) in a last
+                 * partial one */
+                const int steps = TAIL ? min(16, (E - ch * CH) / 16) : 16;
 #pragma unroll
                 for (int s0 = 0; s0 < 16; s0 += 4) {
+                    if (TAIL && s0 >= steps) break;
                     float4 wv[J], xv[KT];
                     for (int j = 0; j < J; j++) wv[j] = *(const float4 *)(W + (J * ea + j) * RSC + c * CSC + s0);
                     for (int k = 0; k < KT; k++) xv[k] = *(const float4 *)(Xt + (KT * tb + k) * RSC + c * CSC + s0);
+                    const bool four = !TAIL || s0 + 4 <= steps;
                     for (int j = 0; j < J; j++)
                         for (int k = 0; k < KT; k++) {
                             acc[j][k] = __builtin_fmaf(wv[j].x, xv[k].x, acc[j][k]);
                             acc[j][k] = __builtin_fmaf(wv[j].y, xv[k].y, acc[j][k]);
-                            acc[j][k] = __builtin_fmaf(wv[j].z, xv[k].z, acc[j][k]);
-                            acc[j][k] = __builtin_fmaf(wv[j].w, xv[k].w, acc[j][k]);
+                            if (four) {
+                                acc[j][k] = __builtin_fmaf(wv[j].z, xv[k].z, acc[j][k]);
+                                acc[j][k] = __builtin_fmaf(wv[j].w, xv[k].w, acc[j][k]);
+                            }
                         }
                 }
             }
@@ -4049,15 +4062,17 @@ __global__ __launch_bounds__(64 * W) void dense_tok_kernel(DenseArgs a)
 }
 
 /* qms_matmul_n's fast loop (src/quant.c:134-169) for the row widths the chunked kernels above
- * do not take: F32, Q4_0 and Q4_1 rows with cols % 256 != 0 and Q6_K rows with
- * cols % 2048 != 0, which the reference's fast path still admits (cols % 32; Q6_K cols % 256).
- * A lane group per row reads the row's words straight from memory: eight lanes per quantised
- * row, lane k keeping the reference's FMA chain k (elements 4k..4k+3 of every 32-block) and
- * the offset chain; sixteen lanes per F32 row, lane c keeping chain c of dot_f32 (elements
- * c, c+16, ...; src/kernels.c:202-213). Up to NT tokens share a pass: their int8 blocks
- * (qms_quantize_q8) sit in LDS as 48-byte records {q[32], d, ds, s16[2], pad}; F32 passes
- * read the inputs from memory. Rows past a matrix's end read its last row and store nothing.
- * No Qwen3-MoE trunk matrix has such a width; this path is for completeness, not speed. */
+ * do not take: Q4_0 and Q4_1 rows with cols % 256 != 0 and Q6_K rows with cols % 2048 != 0,
+ * which the reference's fast path still admits (cols % 32; Q6_K cols % 256); F32 rows of such
+ * widths take the router kernels' tail form (launch_f32_rows). A lane group per row reads the
+ * row's words straight from memory: eight lanes per quantised row, lane k keeping the
+ * reference's FMA chain k (elements 4k..4k+3 of every 32-block) and the offset chain; the
+ * per-slot expert form (slot_any_kernel) also takes F32 expert rows, sixteen lanes each, lane
+ * c keeping chain c of dot_f32 (elements c, c+16, ...; src/kernels.c:202-213). Up to NT
+ * tokens share a pass: their int8 blocks (qms_quantize_q8) sit in LDS as 48-byte records
+ * {q[32], d, ds, s16[2], pad}; F32 passes read the inputs from memory. Rows past a matrix's
+ * end read its last row and store nothing. No Qwen3-MoE trunk matrix has such a width; this
+ * path is for completeness, not speed. */
 constexpr int kDenseAnyRec = 48;
 
 __device__ __forceinline__ uint32_t ld_u32_a2(const uint8_t *p)   /* p a multiple of 2 */
@@ -4290,21 +4305,57 @@ static void launch_dense_t(const DenseArgs &a, int CB, dim3 grid, size_t lds, hi
     else QLAUNCH("dense", (dense_kernel<TYPE, 1, NT, 8, 2>), grid, dim3(64), lds, st, a);
 }
 
+/* y[t][r] (row stride ystride) = dot_f32 of F32 row r of w [rows][C] with x[t] for T tokens
+ * (src/kernels.c:202-221, sixteen chains), for rows of any multiple of 32 floats: one token
+ * takes a block per row (rows of a multiple of 256 floats up to 4096) or 4 rows per block;
+ * more tokens 16 rows x 16 tokens per block, so each row is read once per 16 tokens (a block
+ * per row and token group re-read the rows, measured 5x slower at 4). Rows off the 256-float
+ * grid take the chunked kernel's tail form. */
+hipError_t launch_f32_rows(const float *w, int rows, int C, const float *x, int T, float *y, int ystride,
+                           const char *name, hipStream_t st)
+{
+    RouteArgs r;
+    r.router = w;
+    r.xn = x;
+    r.E = C;
+    r.X = rows;
+    r.K = 0;
+    r.T = T;
+    r.y = y;
+    r.ystride = ystride;
+    r.S = Scratch{};
+    const bool tail = C % 256 != 0;
+    if (T == 1 && C <= 4096 && !tail) {
+        r.n_route_wg = rows;
+        const size_t lds = (size_t)2 * 16 * (C / 16 + 4) * 4;
+        QLAUNCH(name, route_small_kernel<1>, dim3(rows), dim3(256), lds, st, r);
+    } else if (T == 1) {
+        r.n_route_wg = (rows + 3) / 4;
+        if (tail) QLAUNCH(name, (route_big_kernel<1, 1, kRouteBigP, true>), dim3(r.n_route_wg), dim3(256), route_big_lds(1), st, r);
+        else QLAUNCH(name, (route_big_kernel<1, 1, kRouteBigP>), dim3(r.n_route_wg), dim3(256), route_big_lds(1), st, r);
+    } else {
+        r.n_route_wg = ((T + 15) / 16) * ((rows + 15) / 16);
+        if (tail) QLAUNCH(name, (route_big_kernel<4, 4, kRouteBigP, true>), dim3(r.n_route_wg), dim3(256), route_big_lds(4), st, r);
+        else QLAUNCH(name, (route_big_kernel<4, 4, kRouteBigP>), dim3(r.n_route_wg), dim3(256), route_big_lds(4), st, r);
+    }
+    return hipGetLastError();
+}
+
 hipError_t launch_dense(const DenseArgs &args, int type, uint8_t *xqk, hipStream_t st)
 {
     DenseArgs a = args;
     const int nb = a.C / 32;
-    if (type == 14 ? nb % 64 != 0 : nb % 8 != 0) {
+    if (type != 0 && (type == 14 ? nb % 64 != 0 : nb % 8 != 0)) {
         /* widths the chunked kernels do not take: one direct-read pass per NT tokens */
         const int NT = dense_any_nt(type, a.T, nb);
         if (!NT) return hipErrorInvalidValue;
-        const int rpb = type == 0 ? 16 : 32;
+        const int rpb = 32;
         int nblk = 0;
         for (int i = 0; i < a.nm; i++) {
             a.m[i].first_block = nblk;
             nblk += (a.m[i].rows + rpb - 1) / rpb;
         }
-        const size_t lds = type == 0 ? 0 : (size_t)NT * nb * kDenseAnyRec;
+        const size_t lds = (size_t)NT * nb * kDenseAnyRec;
         auto go = [&](auto ty) {
             constexpr int TY = decltype(ty)::value;
             if (NT == 8) QLAUNCH("dense", (dense_any_kernel<TY, 8>), dim3(nblk), dim3(256), lds, st, a);
@@ -4312,8 +4363,7 @@ hipError_t launch_dense(const DenseArgs &args, int type, uint8_t *xqk, hipStream
             else if (NT == 2) QLAUNCH("dense", (dense_any_kernel<TY, 2>), dim3(nblk), dim3(256), lds, st, a);
             else QLAUNCH("dense", (dense_any_kernel<TY, 1>), dim3(nblk), dim3(256), lds, st, a);
         };
-        if (type == 0) go(std::integral_constant<int, 0>());
-        else if (type == 14) go(std::integral_constant<int, 14>());
+        if (type == 14) go(std::integral_constant<int, 14>());
         else if (type == 3) go(std::integral_constant<int, 3>());
         else go(std::integral_constant<int, 2>());
         return hipGetLastError();
@@ -4322,30 +4372,9 @@ hipError_t launch_dense(const DenseArgs &args, int type, uint8_t *xqk, hipStream
         /* F32 rows: qms_vec_dot_f32 (src/quant.c:161-163, src/kernels.c:202-221), the router's
          * arithmetic; one launch per matrix */
         for (int i = 0; i < a.nm; i++) {
-            RouteArgs r;
-            r.router = (const float *)a.m[i].w;
-            r.xn = a.x;
-            r.E = a.C;
-            r.X = a.m[i].rows;
-            r.K = 0;
-            r.T = a.T;
-            r.y = a.m[i].y;
-            r.ystride = a.m[i].rows;
-            r.S = Scratch{};
-            /* one token: a block per row (rows up to 4096 wide) or 4 rows per block; more
-             * tokens: 16 rows x 16 tokens per block, so each row is read once per 16 tokens
-             * (a block per row and token group re-read the rows, measured 5x slower at 4) */
-            if (a.T == 1 && a.C <= 4096) {
-                r.n_route_wg = r.X;
-                const size_t lds = (size_t)2 * 16 * (a.C / 16 + 4) * 4;
-                QLAUNCH("dense", route_small_kernel<1>, dim3(r.X), dim3(256), lds, st, r);
-            } else if (a.T == 1) {
-                r.n_route_wg = (r.X + 3) / 4;
-                QLAUNCH("dense", (route_big_kernel<1, 1, kRouteBigP>), dim3(r.n_route_wg), dim3(256), route_big_lds(1), st, r);
-            } else {
-                r.n_route_wg = ((a.T + 15) / 16) * ((r.X + 15) / 16);
-                QLAUNCH("dense", (route_big_kernel<4, 4, kRouteBigP>), dim3(r.n_route_wg), dim3(256), route_big_lds(4), st, r);
-            }
+            const hipError_t e = launch_f32_rows((const float *)a.m[i].w, a.m[i].rows, a.C, a.x, a.T, a.m[i].y,
+                                                 a.m[i].rows, "dense", st);
+            if (e != hipSuccess) return e;
         }
         return hipGetLastError();
     }
@@ -4590,23 +4619,8 @@ hipError_t launch_layer_slots(const Shape &s, const LayerDev &L, const Scratch &
                 s.E, s.X, S.logits);
     } else {
         /* qms_matmul of the F32 router (src/model.c:1043): dot_f32's sixteen chains */
-        DenseArgs r{};
-        r.m[0].w = (const uint8_t *)L.router;
-        r.m[0].y = S.logits;
-        r.m[0].rows = s.X;
-        r.m[0].first_block = 0;
-        r.nm = 1;
-        r.rb = (uint64_t)s.E * 4;
-        r.C = s.E;
-        r.T = T;
-        r.x = xn;
-        r.xqk = nullptr;
-        const int NT = dense_any_nt(0, T, s.E / 32);
-        const dim3 grid((s.X + 15) / 16);
-        if (NT == 8) QLAUNCH("route", (dense_any_kernel<0, 8>), grid, dim3(256), 0, st, r);
-        else if (NT == 4) QLAUNCH("route", (dense_any_kernel<0, 4>), grid, dim3(256), 0, st, r);
-        else if (NT == 2) QLAUNCH("route", (dense_any_kernel<0, 2>), grid, dim3(256), 0, st, r);
-        else QLAUNCH("route", (dense_any_kernel<0, 1>), grid, dim3(256), 0, st, r);
+        const hipError_t e = launch_f32_rows(L.router, s.X, s.E, xn, T, S.logits, s.X, "route", st);
+        if (e != hipSuccess) return e;
     }
     QLAUNCH("select", select_kernel, dim3(T), dim3(256), 0, st, sa, 0);
     QLAUNCH("dispatch", dispatch_kernel, dim3(1), dim3(64), 0, st, sa);
