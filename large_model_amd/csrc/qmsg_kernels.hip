@@ -4222,6 +4222,10 @@ struct SlotAnyArgs {
     const float *x;
     float *y;
     int y_stride, y_off;
+    /* blockIdx.z == 1: a second matrix of the same type, shape and inputs (up beside gate) */
+    const uint8_t *w2;
+    uint64_t rb2, eb2;
+    int y_off2;
     Scratch S;
 };
 
@@ -4235,7 +4239,10 @@ __global__ __launch_bounds__(256) void slot_any_kernel(SlotAnyArgs a)
     const int4 wk = a.S.work[blockIdx.y];
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, k = lane % LPR;
     const int row = (int)blockIdx.x * 4 * RPW + wave * RPW + lane / LPR, C = a.cols;
-    const uint8_t *wr = a.w + (size_t)wk.x * a.eb + (size_t)min(row, a.rows - 1) * a.rb;
+    const bool second = blockIdx.z == 1;
+    const int y_off = second ? a.y_off2 : a.y_off;
+    const uint8_t *wr = second ? a.w2 + (size_t)wk.x * a.eb2 + (size_t)min(row, a.rows - 1) * a.rb2
+                               : a.w + (size_t)wk.x * a.eb + (size_t)min(row, a.rows - 1) * a.rb;
     for (int s0 = wk.y; s0 < wk.z; s0 += NT) {
         const int nt = min(NT, wk.z - s0);
         float res[NT];
@@ -4245,7 +4252,7 @@ __global__ __launch_bounds__(256) void slot_any_kernel(SlotAnyArgs a)
         }, smem, res);
 #pragma unroll
         for (int n = 0; n < NT; n++)
-            if (k == 0 && n < nt && row < a.rows) a.y[(size_t)(s0 + n) * a.y_stride + a.y_off + row] = res[n];
+            if (k == 0 && n < nt && row < a.rows) a.y[(size_t)(s0 + n) * a.y_stride + y_off + row] = res[n];
     }
 }
 
@@ -4570,6 +4577,10 @@ struct ExactArgs {
     const float *x;
     float *y;
     int y_stride, y_off;
+    /* blockIdx.z == 1: a second matrix of the same shape and inputs (up beside gate) */
+    const uint8_t *w2;
+    uint64_t rb2, eb2;
+    int type2, y_off2;
     Scratch S;
 };
 
@@ -4581,7 +4592,10 @@ __global__ __launch_bounds__(64) void exact_rows_kernel(ExactArgs a)
     const int4 wk = a.S.work[blockIdx.y];
     const int e = wk.x, lane = threadIdx.x, r = blockIdx.x * 64 + lane, C = a.cols;
     float *xr = (float *)smem;                                      /* [NT][C] */
-    const uint8_t *row = a.w + (size_t)e * a.eb + (size_t)min(r, a.rows - 1) * a.rb;
+    const bool second = blockIdx.z == 1;
+    const int type = second ? a.type2 : a.type, y_off = second ? a.y_off2 : a.y_off;
+    const uint8_t *row = (second ? a.w2 + (size_t)e * a.eb2 + (size_t)min(r, a.rows - 1) * a.rb2
+                                 : a.w + (size_t)e * a.eb + (size_t)min(r, a.rows - 1) * a.rb);
     for (int s0 = wk.y; s0 < wk.z; s0 += NT) {
         const int nt = min(NT, wk.z - s0);
         __syncthreads();
@@ -4594,7 +4608,7 @@ __global__ __launch_bounds__(64) void exact_rows_kernel(ExactArgs a)
         float acc[NT] = { 0.0f, 0.0f, 0.0f, 0.0f };
         for (int b = 0; b < C / 32; b++) {
             float w[32];
-            dequant_block(a.type, row, b, w);
+            dequant_block(type, row, b, w);
 #pragma unroll
             for (int n = 0; n < NT; n++)
                 if (n < nt)
@@ -4602,7 +4616,7 @@ __global__ __launch_bounds__(64) void exact_rows_kernel(ExactArgs a)
                     for (int j = 0; j < 32; j++) acc[n] = __builtin_fmaf(w[j], xr[n * C + 32 * b + j], acc[n]);
         }
         if (r < a.rows)
-            for (int n = 0; n < nt; n++) a.y[(size_t)(s0 + n) * a.y_stride + a.y_off + r] = acc[n];
+            for (int n = 0; n < nt; n++) a.y[(size_t)(s0 + n) * a.y_stride + y_off + r] = acc[n];
     }
 }
 
@@ -4639,7 +4653,11 @@ hipError_t launch_layer_slots(const Shape &s, const LayerDev &L, const Scratch &
         const char *name = i == 2 ? "down" : "gateup";
         /* --exact, and F16 / Q8_0 rows at any setting (outside qms_fast_supported, so the
          * reference's qms_matmul takes matmul_exact for them): the fp32 chain */
-        if (exact || m[i].type == 1 || m[i].type == 8) {
+        auto chain_rows = [&](int t) { return exact || t == 1 || t == 8; };
+        /* gate and up in one launch (grid z = 2) when they take the same kernel */
+        const bool pair = i == 0 && (chain_rows(m[0].type) ? chain_rows(m[1].type)
+                                                           : !chain_rows(m[1].type) && m[1].type == m[0].type);
+        if (chain_rows(m[i].type)) {
             ExactArgs a;
             a.S = S;
             a.w = m[i].w;
@@ -4653,9 +4671,15 @@ hipError_t launch_layer_slots(const Shape &s, const LayerDev &L, const Scratch &
             a.y = m[i].y;
             a.y_stride = m[i].stride;
             a.y_off = m[i].off;
+            a.w2 = m[1].w;
+            a.rb2 = m[1].rb;
+            a.eb2 = m[1].eb;
+            a.type2 = m[1].type;
+            a.y_off2 = m[1].off;
             const size_t lds = (size_t)4 * m[i].cols * 4;
             if (lds > 160 * 1024) return hipErrorInvalidValue;
-            QLAUNCH(name, exact_rows_kernel, dim3((m[i].rows + 63) / 64, maxact), dim3(64), lds, st, a);
+            QLAUNCH(name, exact_rows_kernel, dim3((m[i].rows + 63) / 64, maxact, pair ? 2 : 1), dim3(64), lds, st, a);
+            if (pair) i++;
             continue;
         }
         SlotAnyArgs a;
@@ -4670,11 +4694,15 @@ hipError_t launch_layer_slots(const Shape &s, const LayerDev &L, const Scratch &
         a.y = m[i].y;
         a.y_stride = m[i].stride;
         a.y_off = m[i].off;
+        a.w2 = m[1].w;
+        a.rb2 = m[1].rb;
+        a.eb2 = m[1].eb;
+        a.y_off2 = m[1].off;
         const int nb = m[i].cols / 32, NT = dense_any_nt(m[i].type, T, nb);
         if (!NT) return hipErrorInvalidValue;
         const size_t lds = m[i].type == 0 ? 0 : (size_t)NT * nb * kDenseAnyRec;
         const int rpb = m[i].type == 0 ? 16 : 32;
-        const dim3 grid((m[i].rows + rpb - 1) / rpb, maxact);
+        const dim3 grid((m[i].rows + rpb - 1) / rpb, maxact, pair ? 2 : 1);
         auto go = [&](auto ty) {
             constexpr int TY = decltype(ty)::value;
             if (NT == 8) QLAUNCH(name, (slot_any_kernel<TY, 8>), grid, dim3(256), lds, st, a);
@@ -4686,6 +4714,7 @@ hipError_t launch_layer_slots(const Shape &s, const LayerDev &L, const Scratch &
         else if (m[i].type == 3) go(std::integral_constant<int, 3>());
         else if (m[i].type == 0) go(std::integral_constant<int, 0>());
         else go(std::integral_constant<int, 2>());
+        if (pair) i++;
     }
     if (debug && !exact) {
         /* the int8 blocks the slot kernels formed in LDS, for the debug copies */
