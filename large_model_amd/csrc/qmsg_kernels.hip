@@ -4497,26 +4497,73 @@ hipError_t launch_dense(const DenseArgs &args, int type, uint8_t *xqk, hipStream
  * (src/quant.c:97-115), a row dequantised to fp32 (qms_dequant_row, src/quant.c:17-93) against
  * fp32 inputs in one FMA chain in element order; the activations stay fp32. */
 
-/* Router logits: one lane per expert, token blockIdx.y; the token's row is staged in LDS. */
-__global__ __launch_bounds__(64) void route_exact_kernel(const float *router, const float *xn, int E, int X,
-                                                         float *logits)
+/* Router logits of the --exact mode (matmul_exact, src/quant.c:97-115): one fp32 chain per
+ * (expert, token), acc = fma(w_c, x_c, acc) in element order. A block takes 8 experts of
+ * token blockIdx.y, so the router rows stream through many CUs: its 256 threads copy each
+ * chunk of kRouteExactCW columns of the 8 rows into LDS with 16-byte loads along the rows
+ * (the next chunk in registers while lanes 0-7 run the chains on this one, reading four
+ * steps per 16-byte LDS read), rows padded so the 8 chain lanes read distinct banks. n_embd
+ * a multiple of 32. */
+constexpr int kRouteExactCW = 1024;
+constexpr int kRouteExactRS = kRouteExactCW + 4;   /* 16-byte rows 4 banks apart: 8 lanes, 32 banks */
+constexpr size_t route_exact_lds(int E) { return ((size_t)E + 2 * 8 * kRouteExactRS) * 4; }
+
+__global__ __launch_bounds__(256) void route_exact_kernel(const float *router, const float *xn, int E, int X,
+                                                          float *logits)
 {
     extern __shared__ __align__(16) uint8_t smem[];
-    float *xr = (float *)smem;
-    const int t = blockIdx.y, e = blockIdx.x * 64 + threadIdx.x;
-    for (int i = threadIdx.x; i < E / 4; i += 64) ((float4 *)xr)[i] = ((const float4 *)(xn + (size_t)t * E))[i];
-    __syncthreads();
-    if (e >= X) return;
-    const float4 *w = (const float4 *)(router + (size_t)e * E);
+    constexpr int PT = 8 * kRouteExactCW / 4 / 256;   /* 16-byte loads per thread per chunk */
+    float *xr = (float *)smem;                        /* [E]                                 */
+    float *wl = xr + E;                               /* [2][8][kRouteExactRS]               */
+    const int t = blockIdx.y, e0 = blockIdx.x * 8, tid = threadIdx.x;
+    for (int i = tid; i < E / 4; i += 256) ((float4 *)xr)[i] = ((const float4 *)(xn + (size_t)t * E))[i];
+    float4 v[PT];
+    auto load = [&](int c0) {
+        const int cw = min(kRouteExactCW, E - c0);
+#pragma unroll
+        for (int m = 0; m < PT; m++) {
+            const int i = tid + 256 * m, r = i / (kRouteExactCW / 4), q = i - r * (kRouteExactCW / 4);
+            if (4 * q < cw) v[m] = *(const float4 *)(router + (size_t)min(e0 + r, X - 1) * E + c0 + 4 * q);
+        }
+    };
+    auto stage = [&](int c0, float *buf) {
+        const int cw = min(kRouteExactCW, E - c0);
+#pragma unroll
+        for (int m = 0; m < PT; m++) {
+            const int i = tid + 256 * m, r = i / (kRouteExactCW / 4), q = i - r * (kRouteExactCW / 4);
+            if (4 * q < cw) {
+                float *d = buf + r * kRouteExactRS + 4 * q;
+                d[0] = v[m].x;
+                d[1] = v[m].y;
+                d[2] = v[m].z;
+                d[3] = v[m].w;
+            }
+        }
+    };
+    load(0);
+    stage(0, wl);
     float acc = 0.0f;
-    for (int c = 0; c < E / 4; c++) {
-        const float4 v = w[c];
-        acc = __builtin_fmaf(v.x, xr[4 * c], acc);
-        acc = __builtin_fmaf(v.y, xr[4 * c + 1], acc);
-        acc = __builtin_fmaf(v.z, xr[4 * c + 2], acc);
-        acc = __builtin_fmaf(v.w, xr[4 * c + 3], acc);
+    int buf = 0;
+    for (int c0 = 0; c0 < E; c0 += kRouteExactCW) {
+        __syncthreads();                              /* chunk c0 staged (and x, the first time) */
+        if (c0 + kRouteExactCW < E) load(c0 + kRouteExactCW);
+        if (tid < 8) {
+            const float4 *wr = (const float4 *)(wl + buf * 8 * kRouteExactRS + tid * kRouteExactRS);
+            const float4 *x4 = (const float4 *)(xr + c0);
+            const int cw4 = min(kRouteExactCW, E - c0) / 4;
+#pragma unroll 8
+            for (int j = 0; j < cw4; j++) {
+                const float4 w = wr[j], x = x4[j];
+                acc = __builtin_fmaf(w.x, x.x, acc);
+                acc = __builtin_fmaf(w.y, x.y, acc);
+                acc = __builtin_fmaf(w.z, x.z, acc);
+                acc = __builtin_fmaf(w.w, x.w, acc);
+            }
+        }
+        if (c0 + kRouteExactCW < E) stage(c0 + kRouteExactCW, wl + (buf ^ 1) * 8 * kRouteExactRS);
+        buf ^= 1;
     }
-    logits[(size_t)t * X + e] = acc;
+    if (tid < 8 && e0 + tid < X) logits[(size_t)t * X + e0 + tid] = acc;
 }
 
 /* Dequantised 32-block b of a row (src/quant.c:17-93): Q4_0 (q-8)*d, Q4_1 q*d+m (fused like
@@ -4629,7 +4676,8 @@ hipError_t launch_layer_slots(const Shape &s, const LayerDev &L, const Scratch &
     sa.T = T;
     sa.S = S;
     if (exact) {
-        QLAUNCH("route", route_exact_kernel, dim3((s.X + 63) / 64, T), dim3(64), (size_t)s.E * 4, st, L.router, xn,
+        if (route_exact_lds(s.E) > 160 * 1024) return hipErrorInvalidValue;
+        QLAUNCH("route", route_exact_kernel, dim3((s.X + 7) / 8, T), dim3(256), route_exact_lds(s.E), st, L.router, xn,
                 s.E, s.X, S.logits);
     } else {
         /* qms_matmul of the F32 router (src/model.c:1043): dot_f32's sixteen chains */
