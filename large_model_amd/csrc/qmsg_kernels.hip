@@ -4570,46 +4570,82 @@ __global__ __launch_bounds__(256) void route_exact_kernel(const float *router, c
  * the reference build), Q8_0 q*d, Q6_K (d*sc)*q, F16 and F32 as they are. */
 __device__ __forceinline__ void dequant_block(int type, const uint8_t *row, int b, float *w)
 {
+    /* each lane reads its own row, so every load touches another cache line per lane: words
+     * as wide as the row's alignment allows (F32 / F16 rows of 32-multiples are 16-byte
+     * aligned, Q4_1 blocks 4-byte, the others 2-byte) */
     if (type == 0) {
-        const float *p = (const float *)(row + (size_t)b * 128);
+        const float4 *p = (const float4 *)(row + (size_t)b * 128);
 #pragma unroll
-        for (int j = 0; j < 32; j++) w[j] = p[j];
+        for (int j = 0; j < 8; j++) {
+            const float4 f = p[j];
+            w[4 * j] = f.x; w[4 * j + 1] = f.y; w[4 * j + 2] = f.z; w[4 * j + 3] = f.w;
+        }
     } else if (type == 1) {
-        const uint16_t *p = (const uint16_t *)(row + (size_t)b * 64);
+        const u32x4 *p = (const u32x4 *)(row + (size_t)b * 64);
 #pragma unroll
-        for (int j = 0; j < 32; j++) w[j] = h2f(p[j]);
+        for (int j = 0; j < 4; j++) {
+            const u32x4 v = p[j];
+            const uint32_t u[4] = { v.x, v.y, v.z, v.w };
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                w[8 * j + 2 * k] = h2f(u[k] & 0xffffu);
+                w[8 * j + 2 * k + 1] = h2f(u[k] >> 16);
+            }
+        }
     } else if (type == 8) {
-        const uint8_t *bp = row + (size_t)b * 34;
-        const float d = h2f((uint32_t)bp[0] | ((uint32_t)bp[1] << 8));
+        const uint16_t *p = (const uint16_t *)(row + (size_t)b * 34);
+        const float d = h2f(p[0]);
 #pragma unroll
-        for (int j = 0; j < 32; j++) w[j] = (float)(int8_t)bp[2 + j] * d;
+        for (int j = 0; j < 16; j++) {
+            const uint32_t h = p[1 + j];
+            w[2 * j] = (float)(int8_t)(h & 0xff) * d;
+            w[2 * j + 1] = (float)(int8_t)(h >> 8) * d;
+        }
     } else if (type == 14) {
         const uint8_t *sb = row + (size_t)(b >> 3) * 210;
         const int h = (b & 7) >> 2, g = b & 3;
-        const float d = h2f((uint32_t)sb[208] | ((uint32_t)sb[209] << 8));
-        const float d0 = d * (float)(int8_t)sb[192 + 8 * h + 2 * g];
-        const float d1 = d * (float)(int8_t)sb[192 + 8 * h + 2 * g + 1];
+        const uint16_t *ql = (const uint16_t *)(sb + 64 * h + 32 * (g & 1)), *qh = (const uint16_t *)(sb + 128 + 32 * h);
+        const uint32_t sc = *(const uint16_t *)(sb + 192 + 8 * h + 2 * g);
+        const float d = h2f(*(const uint16_t *)(sb + 208));
+        const float d0 = d * (float)(int8_t)(sc & 0xff);
+        const float d1 = d * (float)(int8_t)(sc >> 8);
 #pragma unroll
-        for (int l = 0; l < 32; l++) {
-            const int lo = sb[64 * h + 32 * (g & 1) + l];
-            const int q = ((g < 2 ? lo & 15 : lo >> 4) | (((sb[128 + 32 * h + l] >> (2 * g)) & 3) << 4)) - 32;
-            w[l] = (l < 16 ? d0 : d1) * (float)q;
+        for (int l2 = 0; l2 < 16; l2++) {
+            const uint32_t lo2 = ql[l2], hi2 = qh[l2];
+#pragma unroll
+            for (int k = 0; k < 2; k++) {
+                const int l = 2 * l2 + k;
+                const int lo = (lo2 >> (8 * k)) & 0xff, hb = (hi2 >> (8 * k)) & 0xff;
+                const int q = ((g < 2 ? lo & 15 : lo >> 4) | (((hb >> (2 * g)) & 3) << 4)) - 32;
+                w[l] = (l < 16 ? d0 : d1) * (float)q;
+            }
         }
     } else if (type == 3) {
-        const uint8_t *bp = row + (size_t)b * 20;
-        const float d = h2f((uint32_t)bp[0] | ((uint32_t)bp[1] << 8)), m = h2f((uint32_t)bp[2] | ((uint32_t)bp[3] << 8));
+        const uint32_t *p = (const uint32_t *)(row + (size_t)b * 20);
+        const uint32_t dm = p[0];
+        const float d = h2f(dm & 0xffffu), m = h2f(dm >> 16);
 #pragma unroll
-        for (int j = 0; j < 16; j++) {
-            w[j] = __builtin_fmaf((float)(bp[4 + j] & 15), d, m);
-            w[j + 16] = __builtin_fmaf((float)(bp[4 + j] >> 4), d, m);
+        for (int j4 = 0; j4 < 4; j4++) {
+            const uint32_t c = p[1 + j4];
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                const uint32_t q = (c >> (8 * k)) & 0xff;
+                w[4 * j4 + k] = __builtin_fmaf((float)(q & 15), d, m);
+                w[4 * j4 + k + 16] = __builtin_fmaf((float)(q >> 4), d, m);
+            }
         }
     } else {
-        const uint8_t *bp = row + (size_t)b * 18;
-        const float d = h2f((uint32_t)bp[0] | ((uint32_t)bp[1] << 8));
+        const uint16_t *p = (const uint16_t *)(row + (size_t)b * 18);
+        const float d = h2f(p[0]);
 #pragma unroll
-        for (int j = 0; j < 16; j++) {
-            w[j] = (float)((int)(bp[2 + j] & 15) - 8) * d;
-            w[j + 16] = (float)((int)(bp[2 + j] >> 4) - 8) * d;
+        for (int j2 = 0; j2 < 8; j2++) {
+            const uint32_t c = p[1 + j2];
+#pragma unroll
+            for (int k = 0; k < 2; k++) {
+                const int q = (int)((c >> (8 * k)) & 0xff);
+                w[2 * j2 + k] = (float)((q & 15) - 8) * d;
+                w[2 * j2 + k + 16] = (float)((q >> 4) - 8) * d;
+            }
         }
     }
 }
@@ -4724,7 +4760,9 @@ hipError_t launch_layer_slots(const Shape &s, const LayerDev &L, const Scratch &
             a.eb2 = m[1].eb;
             a.type2 = m[1].type;
             a.y_off2 = m[1].off;
-            const size_t lds = (size_t)4 * m[i].cols * 4;
+            /* input rows for the slots of one pass: at most min(4, T), an expert's slots
+             * being distinct tokens */
+            const size_t lds = (size_t)min(4, T) * m[i].cols * 4;
             if (lds > 160 * 1024) return hipErrorInvalidValue;
             QLAUNCH(name, exact_rows_kernel, dim3((m[i].rows + 63) / 64, maxact, pair ? 2 : 1), dim3(64), lds, st, a);
             if (pair) i++;
