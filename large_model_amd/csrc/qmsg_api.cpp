@@ -839,9 +839,21 @@ static int run_layer_s(qmsg_ctx *c, const Scratch &S0, int layer, const float *d
         return fail(c, QMSG_E_INVALID, "device buffers must be 16-byte aligned (xn) and 4-byte aligned (out)");
     const Shape s{ c->cfg.n_embd, c->cfg.n_expert, c->cfg.n_used, c->cfg.n_ff_exp };
     const LayerDev d = layer_dev(c, L);
-    const bool integer = integer_grid_shape(s.E, s.F) && integer_expert_types(d.gate_type, d.up_type, d.down_type);
+    const bool types = integer_expert_types(d.gate_type, d.up_type, d.down_type);
+    const bool integer = integer_grid_shape(s.E, s.F) && types;
+    /* n_ff_exp an odd multiple of 32 at an n_embd on the grid: the streaming gate/up kernel
+     * (rows n_embd wide) and the slot kernels for the down rows */
+    const bool odd_f = !integer && types && s.E % 256 == 0 && s.F % 64 == 32 && gateup_streams(d) &&
+                       c->path != QMSG_PATH_FP32;
     if (ni && (T != 1 || c->path == QMSG_PATH_FP32 || !route_norm_fits(s.E) || !integer || ni->xn_out != d_xn))
         return fail(c, QMSG_E_INVALID, "run_layer_s: the fused rmsnorm takes one token on the integer paths");
+    if (odd_f) {
+        LAUNCH(c, "route", launch_route(s, d, S, d_xn, T, c->stream));
+        LAUNCH(c, "select", launch_select(s, S, T, 1, c->stream));
+        LAUNCH(c, "gateup", launch_gateup_exact(s, d, S, T, debug, c->n_cu, 0, c->stream));
+        LAUNCH(c, "down", launch_layer_slots(s, d, S, d_xn, d_out, T, 0, debug, c->stream, 1));
+        return QMSG_OK;
+    }
     if (c->path == QMSG_PATH_FP32 || !integer) {
         LAUNCH(c, "layer", launch_layer_slots(s, d, S, d_xn, d_out, T, c->path == QMSG_PATH_FP32 ? 1 : 0, debug,
                                               c->stream));

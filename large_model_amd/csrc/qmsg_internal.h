@@ -173,10 +173,13 @@ hipError_t launch_down_exact(const Shape &s, const LayerDev &L, const Scratch &S
  * int8 path, for shapes off the integer kernels' grid (integer_grid_shape). debug also stores
  * the int8 blocks of the inputs and activations (xq, aq) that the slot kernels keep in LDS. */
 hipError_t launch_layer_slots(const Shape &s, const LayerDev &L, const Scratch &S, const float *xn, float *out, int T,
-                              int exact, int debug, hipStream_t st);
+                              int exact, int debug, hipStream_t st, int down_only = 0);
 /* The shapes the integer kernels take: n_embd % 256 == 0 (the reference's fast gate,
  * src/model.c:1090-1093) and n_ff_exp % 64 == 0 (they pair 32-blocks). */
 inline bool integer_grid_shape(int E, int F) { return E % 256 == 0 && F % 64 == 0; }
+/* down_only: the down rows, the debug copies and the combine alone, after the integer kernels'
+ * routing and gate/up (with SwiGLU) have run: n_ff_exp an odd multiple of 32, whose down rows
+ * the integer kernels do not pair. */
 /* Expert types the integer kernels take (the quantised types of qms_fast_supported); layers
  * with F32, F16 or Q8_0 expert tensors run slot by slot. */
 inline bool integer_expert_types(int gt, int ut, int dt)

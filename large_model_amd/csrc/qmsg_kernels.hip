@@ -4704,14 +4704,16 @@ __global__ __launch_bounds__(64) void exact_rows_kernel(ExactArgs a)
 }
 
 hipError_t launch_layer_slots(const Shape &s, const LayerDev &L, const Scratch &S, const float *xn, float *out, int T,
-                              int exact, int debug, hipStream_t st)
+                              int exact, int debug, hipStream_t st, int down_only)
 {
     SelectArgs sa;
     sa.X = s.X;
     sa.K = s.K;
     sa.T = T;
     sa.S = S;
-    if (exact) {
+    if (down_only) {
+        /* routing, gate/up and SwiGLU done by the integer kernels */
+    } else if (exact) {
         if (route_exact_lds(s.E) > 160 * 1024) return hipErrorInvalidValue;
         QLAUNCH("route", route_exact_kernel, dim3((s.X + 7) / 8, T), dim3(256), route_exact_lds(s.E), st, L.router, xn,
                 s.E, s.X, S.logits);
@@ -4720,8 +4722,10 @@ hipError_t launch_layer_slots(const Shape &s, const LayerDev &L, const Scratch &
         const hipError_t e = launch_f32_rows(L.router, s.X, s.E, xn, T, S.logits, s.X, "route", st);
         if (e != hipSuccess) return e;
     }
-    QLAUNCH("select", select_kernel, dim3(T), dim3(256), 0, st, sa, 0);
-    QLAUNCH("dispatch", dispatch_kernel, dim3(1), dim3(64), 0, st, sa);
+    if (!down_only) {
+        QLAUNCH("select", select_kernel, dim3(T), dim3(256), 0, st, sa, 0);
+        QLAUNCH("dispatch", dispatch_kernel, dim3(1), dim3(64), 0, st, sa);
+    }
     const int maxact = s.X < T * s.K ? s.X : T * s.K;
     const struct { const uint8_t *w; uint64_t rb, eb; int type, rows, cols, by_token; const float *x; float *y;
                    int stride, off; } m[3] = {
@@ -4729,8 +4733,8 @@ hipError_t launch_layer_slots(const Shape &s, const LayerDev &L, const Scratch &
         { L.up, L.up_rb, L.up_eb, L.up_type, s.F, s.E, 1, xn, S.gu, 2 * s.F, s.F },
         { L.down, L.down_rb, L.down_eb, L.down_type, s.E, s.F, 0, S.act, S.dn, s.E, 0 },
     };
-    for (int i = 0; i < 3; i++) {
-        if (i == 2) {
+    for (int i = down_only ? 2 : 0; i < 3; i++) {
+        if (i == 2 && !down_only) {
             const int n = T * s.K * s.F;
             QLAUNCH("swiglu", swiglu_kernel, dim3((n + 255) / 256), dim3(256), 0, st, S, s.F, T * s.K);
         }
@@ -4805,7 +4809,8 @@ hipError_t launch_layer_slots(const Shape &s, const LayerDev &L, const Scratch &
     if (debug && !exact) {
         /* the int8 blocks the slot kernels formed in LDS, for the debug copies */
         const int nx = T * (s.E / 32), na = T * s.K * (s.F / 32);
-        QLAUNCH("debug", quant_rows_kernel, dim3((nx + 255) / 256), dim3(256), 0, st, xn, s.E, T, S.xq);
+        if (!down_only)
+            QLAUNCH("debug", quant_rows_kernel, dim3((nx + 255) / 256), dim3(256), 0, st, xn, s.E, T, S.xq);
         QLAUNCH("debug", quant_rows_kernel, dim3((na + 255) / 256), dim3(256), 0, st, S.act, s.F, T * s.K, S.aq);
     }
     const int n = T * s.E;

@@ -4,7 +4,9 @@ reference's moe() runs moe_group_exact with the int8 qms_matmul of every slot
 the same numbers. Both take the slot kernels (slot_any_kernel) on every path setting but the
 fp32 one, which runs the --exact restatement. Every intermediate bit for bit against the oracle,
 whose integer branch is held to the reference build's moe() at such shapes on the CPU
-(test_oracle.py::test_off_grid_shapes)."""
+(test_oracle.py::test_off_grid_shapes). With n_embd on the grid and an odd multiple of 32 as
+n_ff_exp, gate and up of one streaming type take the integer kernels and only the down rows
+the slot kernel."""
 import numpy as np
 import pytest
 
@@ -25,6 +27,11 @@ CASES = [
     ("e4096_f1568_t1", 4096, 32, 8, 1568, 1, Q40, Q40, Q40),
     ("e4096_f1568_t20", 4096, 32, 8, 1568, 20, Q40, Q40, Q41),
     ("e1056_f64_t40", 1056, 32, 4, 64, 40, Q41, Q41, Q41),
+    # n_embd on the grid, n_ff_exp an odd multiple of 32, gate and up of one streaming type:
+    # the integer routing and gate/up kernels, the slot kernel for the down rows
+    ("e2048_f352_t1_hybrid", 2048, 64, 8, 352, 1, Q40, Q40, Q40),
+    ("e2048_f352_t5_hybrid", 2048, 64, 8, 352, 5, Q41, Q41, Q40),
+    ("e4096_f1568_t24_hybrid", 4096, 32, 8, 1568, 24, Q40, Q40, Q41),
 ]
 
 
